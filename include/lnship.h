@@ -1,0 +1,131 @@
+/*
+ * lnship.h - C ABI of the MI355X (gfx950) LNS kernels.
+ *
+ * This is the host->device boundary below the ggml backend, the same facts
+ * the reference's abstract kernel interface carries
+ * (lns-backend/cuda/lns-cuda-kernels.h:12-26, class kernel_set :85-139), as
+ * plain extern "C" functions: F32 at op boundaries, contiguous ne[0]-fastest
+ * arrays, weights cached in HBM in a k8-interleaved layout, asynchronous
+ * on a caller-given HIP stream
+ * (passed as void *), a per-op Monte LFSR start state.
+ *
+ * Every pointer argument is a device pointer unless stated otherwise.
+ * Functions return 0 on success and a negative LNSHIP_E* code on error;
+ * lnship_last_error() describes the last error of the calling thread.
+ *
+ * Summation modes (GGML_LNS16_SUM of the reference, lns-common.cmake:24-46):
+ *   LNSHIP_BASE  sequential xlns16_add
+ *   LNSHIP_MONTE xlns16 add with one LFSR draw per addition
+ *   LNSHIP_LPVIP 32-bit LPVIP accumulator, truncated once
+ *   LNSHIP_SUM32 xlns32 accumulator, rounded to nearest once
+ * The reference fixes the mode at build time; here it is an argument.
+ */
+#ifndef LNSHIP_H
+#define LNSHIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum lnship_mode { LNSHIP_BASE = 0, LNSHIP_MONTE = 1, LNSHIP_LPVIP = 2, LNSHIP_SUM32 = 3 };
+
+enum lnship_error {
+    LNSHIP_OK = 0,
+    LNSHIP_EINVAL = -1,    /* bad argument or shape                 */
+    LNSHIP_EDEVICE = -2,   /* HIP runtime error                     */
+    LNSHIP_ENOINIT = -3,   /* lnship_init was not called for device */
+    LNSHIP_ERANGE = -4     /* shape beyond a kernel's limits        */
+};
+
+/* Builds the arithmetic tables on the host and uploads them to the current
+ * device.  Replaces kernel_set::upload_tables (lns-cuda-kernels.h:104).
+ * Idempotent per device. */
+int lnship_init(void);
+const char *lnship_last_error(void);
+/* the build's identity string */
+const char *lnship_version(void);
+/* Host copy of one arithmetic table ("cvt16", "rev16", "gauss16",
+ * "gauss16m", "exp16", "tab32", "lfsr_seq"); builds the tables on first use,
+ * needs no GPU.  No counterpart in the reference: it lets tests compare the
+ * tables with an independent restatement. */
+const void *lnship_host_table(const char *name, size_t *bytes);
+
+/* ---- conversions (kernel_set::to_lns, :107) ------------------------------ */
+int lnship16_from_f32(const float *src, uint16_t *dst, int64_t n, void *stream);
+int lnship16_to_f32(const uint16_t *src, float *dst, int64_t n, void *stream);
+int lnship32_from_f32(const float *src, uint32_t *dst, int64_t n, void *stream);
+int lnship32_to_f32(const uint32_t *src, float *dst, int64_t n, void *stream);
+/* Weight-cache fill (replaces kernel_set::to_lns_transposed, :111-112).
+ * nslices slices, each M rows of K values (F32, or IEEE half when
+ * src_is_f16), row stride src_ld and slice stride src_slice (elements), into
+ * the k8-interleaved cache layout: Kp = K rounded up to a multiple of 8;
+ * element (k, m) of a slice at ((k / 8) * M + m) * 8 + k % 8; slices Kp * M
+ * codes apart; padding codes are 0. */
+int lnship16_pack(const void *src, int src_is_f16, int64_t src_ld, int64_t src_slice, uint16_t *dst,
+                  int64_t K, int64_t M, int64_t nslices, void *stream);
+int lnship32_pack(const void *src, int src_is_f16, int64_t src_ld, int64_t src_slice, uint32_t *dst,
+                  int64_t K, int64_t M, int64_t nslices, void *stream);
+
+/* ---- MUL_MAT (kernel_set::mul_mat, :114; mul_mat_args :51-58) ----------
+ * dst = W^T x for every activation slice, each output a sequential
+ * accumulation over k = 0..K-1 (lns_mul_mat, src/lns-ops.cpp:293-384).
+ *   w:   LNS codes in the cache layout of lnship16_pack / lnship32_pack,
+ *        ne02 * ne03 slices
+ *   x:   F32, N x K per activation slice (row n at n * x_ld), ne12 * ne13
+ *        slices at x_slice apart
+ *   dst: F32, N x M per activation slice (row n at n * M), contiguous
+ * Activation slice (i12, i13) uses weight slice (i12 / (ne12/ne02),
+ * i13 / (ne13/ne03)).  monte_seed is the LFSR state where the first output
+ * (CPU loop order i13, i12, m, n) starts. */
+typedef struct lnship_mul_mat_args {
+    const void *w;
+    const float *x;
+    float *dst;
+    int64_t K, M, N;
+    int64_t ne02, ne03, ne12, ne13;
+    int64_t x_ld, x_slice;   /* 0 = contiguous (K and N*K) */
+    uint16_t monte_seed;
+} lnship_mul_mat_args;
+
+int lnship16_mul_mat(int mode, const lnship_mul_mat_args *args, void *stream);
+int lnship32_mul_mat(const lnship_mul_mat_args *args, void *stream);
+
+/* ---- RMS_NORM (kernel_set::rms_norm, :133-134) --------------------------
+ * dst = src / sqrt(mean(src^2) + eps) per row of ncols (lns_rms_norm,
+ * src/lns-ops.cpp:701-736; sum of squares from zero, in element order). */
+int lnship16_rms_norm(int mode, const float *src, float *dst, int64_t ncols, int64_t nrows, float eps,
+                      uint16_t monte_seed, void *stream);
+int lnship32_rms_norm(const float *src, float *dst, int64_t ncols, int64_t nrows, float eps, void *stream);
+
+/* ---- SOFT_MAX (kernel_set::soft_max, :136; soft_max_args :62-71) --------
+ * dst = softmax(src * scale + mask) over rows of src_ne[0] (lns_soft_max,
+ * src/lns-ops.cpp:643-695).  mask (optional, F32) row i1 of plane
+ * (i2 % mask_ne[2], i3 % mask_ne[3]); mask_ne[1] >= src_ne[1]. */
+typedef struct lnship_soft_max_args {
+    const float *src;
+    int64_t src_ne[4];
+    const float *mask;
+    int64_t mask_ne[4];
+    float scale;
+    float *dst;
+    uint16_t monte_seed;
+} lnship_soft_max_args;
+
+int lnship16_soft_max(int mode, const lnship_soft_max_args *args, void *stream);
+int lnship32_soft_max(const lnship_soft_max_args *args, void *stream);
+
+/* ---- Monte draw accounting (kernel_set::*_draws, :97-100) --------------- */
+uint64_t lnship16_mul_mat_draws(int mode, int64_t K, int64_t M, int64_t N, int64_t ne12, int64_t ne13);
+uint64_t lnship16_soft_max_draws(int mode, int64_t ncols, int64_t nrows);
+uint64_t lnship16_rms_norm_draws(int mode, int64_t ncols, int64_t nrows);
+/* the LFSR step of xlns16monte (src/lns-ops.cpp:182-188) jumped n times */
+uint16_t lnship_lfsr_jump(uint16_t state, uint64_t n);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

@@ -298,6 +298,19 @@ uint32_t lno32_add(uint32_t x, uint32_t y) {
 
 uint32_t lno32_sub(uint32_t x, uint32_t y) { return lno32_add(x, y ^ X32_SIGN); }
 
+/* the interpolation / cotransformation tables, for tests */
+const int32_t *lno32_table(const char *name, size_t *n) {
+    struct { const char *k; const int32_t *p; size_t n; } t[] = {
+        {"sb", g_sb32a, X32_SB_N + 1}, {"sbf", g_sb32b, X32_SB_FN + 1},
+        {"db", g_db32a, X32_DB_N + 1}, {"dbf", g_db32b, X32_DB_FN + 1},
+        {"dlo", g_db32lo, 1 << X32_CO_SH}, {"dhi", g_db32hi, X32_CO_END >> X32_CO_SH},
+    };
+    for (size_t i = 0; i < sizeof t / sizeof t[0]; i++)
+        if (strcmp(t[i].k, name) == 0) { *n = t[i].n; return t[i].p; }
+    *n = 0;
+    return NULL;
+}
+
 uint32_t lno32_sqrt(uint32_t x) {
     int32_t sh = (int32_t)(x << 1);
     int32_t q = sh / 4;

@@ -82,6 +82,7 @@ def lib():
         "lno32_recip": (u32, [u32]),
         "lno32_exp": (u32, [u32]),
         "lno32_gt": (ctypes.c_int, [u32, u32]),
+        "lno32_table": (P, [ctypes.c_char_p, ctypes.POINTER(SZ)]),
         "lno32_vec_dot": (u32, [P, P, SZ]),
         "lno32_rms_norm_row": (None, [P, P, SZ, u32]),
         "lno32_softmax_row": (None, [P, P, P, SZ, u32]),
@@ -137,6 +138,13 @@ def table(name, n, dtype):
     p = getattr(lib(), name)()
     buf = (ctypes.c_char * (n * np.dtype(dtype).itemsize)).from_address(p)
     return np.frombuffer(buf, dtype=dtype).copy()
+
+
+def table32(name):
+    n = SZ(0)
+    p = lib().lno32_table(name.encode(), ctypes.byref(n))
+    buf = (ctypes.c_char * (n.value * 4)).from_address(p)
+    return np.frombuffer(buf, dtype=np.int32).copy()
 
 
 def sum16(mode, a, lfsr=None):

@@ -1,0 +1,94 @@
+"""CPU checks of the product library: it loads without a GPU, exports every
+function include/*.h declares, and its arithmetic tables equal the oracle's
+independent restatement (no compute call needs a GPU here)."""
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+
+import oracle_lib as O
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+@pytest.fixture(scope="module")
+def lnship():
+    import lnship as m
+    if not os.path.exists(m.LIB_PATH):
+        pytest.fail("liblnship.so is not built (run __graft_entry__.build())")
+    return m
+
+
+def _declared(header):
+    text = open(os.path.join(ROOT, "include", header)).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b((?:lnship|ggml_backend)\w*)\s*\(", text)))
+
+
+@pytest.mark.parametrize("header", sorted(h for h in os.listdir(os.path.join(ROOT, "include")) if h.endswith(".h")))
+def test_library_exports_every_declared_symbol(lnship, header):
+    L = ctypes.CDLL(lnship.LIB_PATH)
+    names = _declared(header)
+    assert names
+    missing = [n for n in names if not hasattr(L, n)]
+    assert not missing, missing
+
+
+def test_cvt16_table_equals_oracle(lnship):
+    assert np.array_equal(lnship.host_table("cvt16", np.uint16), O.table("lno16_cvt_table", 1 << 17, np.uint16))
+
+
+def test_rev16_table_equals_oracle(lnship):
+    got = lnship.host_table("rev16", np.float32)
+    want = O.x2f16(np.arange(65536, dtype=np.uint16))
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_gauss16_tables_equal_oracle(lnship):
+    g = lnship.host_table("gauss16", np.int16)
+    n = g.size // 2
+    sb, db = O.table("lno16_sb_table", 1281, np.int16), O.table("lno16_db_table", 1281, np.int16)
+    assert np.array_equal(g[:1281], sb) and np.array_equal(g[n:n + 1281], db)
+    assert np.all(g[1281:n] == 0) and np.all(g[n + 1281:] == 0)
+
+
+def test_exp16_table_equals_oracle(lnship):
+    assert np.array_equal(lnship.host_table("exp16", np.uint16), O.table("lno16_exp_table", 1 << 16, np.uint16))
+
+
+def test_tab32_equals_oracle(lnship):
+    t = lnship.host_table("tab32", np.int32)
+    sb, sbf, db, dbf, dlo, dhi = (O.table32(k) for k in ("sb", "sbf", "db", "dbf", "dlo", "dhi"))
+    parts = [sb, sbf, db[2048:], dbf, dlo, dhi]
+    assert t.size == sum(p.size for p in parts)
+    assert np.array_equal(t, np.concatenate(parts))
+
+
+def test_lfsr_sequence_equals_oracle(lnship):
+    seq = lnship.host_table("lfsr_seq", np.uint16)
+    L = O.lib()
+    s = 1
+    for i in range(0, 65535, 997):
+        assert seq[i] == L.lno_lfsr_jump(1, i)
+    for st in (7, 1, 0xB403, 12345):
+        for n in (0, 1, 65534, 65535, 10 ** 9 + 7):
+            assert lnship.lfsr_jump(st, n) == L.lno_lfsr_jump(st, n)
+
+
+def test_draw_accounting_matches_reference_formula(lnship):
+    # test-lns-cuda-parity.cpp:77-105: K-1 per dot, n-1 per softmax row, n per rms row
+    L = lnship.lib()
+    assert L.lnship16_mul_mat_draws(lnship.MONTE, 576, 1536, 5, 2, 3) == 1536 * 5 * 6 * 575
+    assert L.lnship16_mul_mat_draws(lnship.MONTE, 0, 1536, 5, 1, 1) == 0
+    assert L.lnship16_mul_mat_draws(lnship.SUM32, 576, 1536, 5, 1, 1) == 0
+    assert L.lnship16_soft_max_draws(lnship.MONTE, 128, 9) == 9 * 127
+    assert L.lnship16_rms_norm_draws(lnship.MONTE, 576, 3) == 3 * 576
+
+
+def test_calls_without_init_fail_loudly(lnship):
+    # no device here: every compute entry point must refuse, never fall back
+    L = lnship.lib()
+    rc = L.lnship16_from_f32(None, None, 16, None)
+    assert rc != 0

@@ -1,0 +1,213 @@
+"""GPU parity: the gfx950 kernels against the CPU oracle, bit for bit.
+
+Follows the reference's parity harness (lns-backend/tests/
+test-lns-cuda-parity.cpp:158-171 memcmp, cases :255-366): mul_mat with N not
+a multiple of the column tile, K=1536 / 4096 / 1, N=1, GQA and 4-D broadcast,
+rms_norm and soft_max with singleton rows and padded masks, Monte from equal
+LFSR states.  Inputs are seeded; every case prints its name before it runs.
+"""
+import numpy as np
+import pytest
+
+import oracle_lib as O
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+MODES = ["base", "monte", "lpvip", "sum32"]
+
+
+@pytest.fixture(scope="module")
+def ln():
+    import lnship
+    assert torch.cuda.is_available(), "GPU tests need a visible GPU"
+    lnship.init()
+    return lnship
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def host(t):
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def same_bits(got, want, what):
+    g, w = np.ascontiguousarray(got), np.ascontiguousarray(want)
+    assert g.shape == w.shape, (what, g.shape, w.shape)
+    gb, wb = g.view(np.uint32), w.view(np.uint32)
+    bad = np.nonzero(gb.ravel() != wb.ravel())[0]
+    assert bad.size == 0, f"{what}: {bad.size}/{g.size} differ; first at {bad[0]}: got {g.ravel()[bad[0]]!r} want {w.ravel()[bad[0]]!r}"
+
+
+# ---------------------------------------------------------------- conversion --
+
+def test_from_f32_16_every_bucket(ln):
+    # every 2^15-wide bucket of float bit patterns: lowest, highest, middle
+    b = np.arange(1 << 17, dtype=np.uint64) << 15
+    bits = np.concatenate([b, b + 0x7FFF, b + 0x4321]).astype(np.uint32)
+    x = bits.view(np.float32)
+    got = host(ln.from_f32_16(dev(x))).view(np.uint16)
+    assert np.array_equal(got, O.f2x16(x))
+
+
+def test_to_f32_16_every_code(ln):
+    codes = np.arange(65536, dtype=np.uint16)
+    got = host(ln.to_f32_16(dev(codes.view(np.int16))))
+    same_bits(got, O.x2f16(codes), "xlns16 -> f32")
+
+
+def test_xlns32_conversion_sampled(ln):
+    rng = np.random.default_rng(11)
+    bits = rng.integers(0, 1 << 32, 1 << 20, dtype=np.uint64).astype(np.uint32)
+    special = np.array([0, 0x80000000, 0x3F800000, 0x7F800000, 0xFF800000, 0x7FC00000, 1, 0x807FFFFF,
+                        0x00800000, 0x7F7FFFFF], dtype=np.uint32)
+    x = np.concatenate([bits, special]).view(np.float32)
+    got = host(ln.from_f32_32(dev(x))).view(np.uint32)
+    want = O.f2x32(x)
+    assert np.array_equal(got, want), int(np.sum(got != want))
+    codes = rng.integers(0, 1 << 32, 1 << 20, dtype=np.uint64).astype(np.uint32)
+    back = host(ln.to_f32_32(dev(codes.view(np.int32))))
+    same_bits(back, O.x2f32(codes), "xlns32 -> f32")
+
+
+# ------------------------------------------------------------------- mul_mat --
+
+def _mm_case(ln, mode, K, M, N, ne02=1, ne03=1, ne12=1, ne13=1, seed=0, wscale=0.02, lfsr=7):
+    print(f"\n[mul_mat] mode={mode} K={K} M={M} N={N} w=({ne03},{ne02}) x=({ne13},{ne12})", flush=True)
+    rng = np.random.default_rng(seed)
+    w = (rng.standard_normal((ne03, ne02, M, K)) * wscale).astype(np.float32)
+    x = rng.standard_normal((ne13, ne12, N, K)).astype(np.float32)
+    m = O.MODES[mode]
+    O.monte_set(lfsr)
+    want = O.mul_mat16_f32w(m, w, x, ne02, ne03)
+    wp = ln.pack16(dev(w))
+    got = host(ln.mul_mat16(m, wp, dev(x), K, M, ne02, ne03, seed=lfsr))
+    same_bits(got, want, f"mul_mat {mode} K={K} M={M} N={N}")
+    if m == O.MONTE:
+        # the oracle's LFSR advanced by exactly the draws the kernel reserves
+        assert O.monte_get() == O.lib().lno_lfsr_jump(lfsr, ln.mul_mat_draws(m, K, M, N, ne12, ne13))
+
+
+@pytest.mark.parametrize("mode", MODES)
+def test_mul_mat_c1_gemv(ln, mode):
+    # 1536x576 weight times 576x1, and K=1536 with 576 rows
+    _mm_case(ln, mode, 576, 1536, 1, seed=1)
+    _mm_case(ln, mode, 1536, 576, 1, seed=2)
+
+
+@pytest.mark.parametrize("mode", MODES)
+def test_mul_mat_ragged_shapes(ln, mode):
+    _mm_case(ln, mode, 256, 67, 5, seed=3)          # N=5: not a multiple of the column tile
+    _mm_case(ln, mode, 4096, 70, 7, seed=4)         # long K, N=7
+    _mm_case(ln, mode, 1, 33, 3, seed=5)            # K=1
+    _mm_case(ln, mode, 13, 300, 9, seed=6)          # K not a multiple of 8
+    _mm_case(ln, mode, 64, 513, 130, seed=7)        # several column tiles and row blocks
+
+
+@pytest.mark.parametrize("mode", MODES)
+def test_mul_mat_broadcast(ln, mode):
+    _mm_case(ln, mode, 64, 40, 3, ne02=3, ne12=9, seed=8)                # GQA: 9 query heads over 3 kv heads
+    _mm_case(ln, mode, 32, 24, 2, ne02=2, ne03=2, ne12=4, ne13=6, seed=9)  # 4-D broadcast
+
+
+def test_mul_mat_same_sign_long(ln):
+    # same-sign K=2048: the stagnation regime of base sums
+    for mode in MODES:
+        print(f"\n[mul_mat same sign] {mode}", flush=True)
+        rng = np.random.default_rng(10)
+        w = np.abs(rng.standard_normal((1, 1, 96, 2048))).astype(np.float32)
+        x = np.abs(rng.standard_normal((1, 1, 4, 2048))).astype(np.float32)
+        O.monte_set(7)
+        want = O.mul_mat16_f32w(O.MODES[mode], w, x)
+        got = host(ln.mul_mat16(O.MODES[mode], ln.pack16(dev(w)), dev(x), 2048, 96))
+        same_bits(got, want, f"same-sign {mode}")
+
+
+def test_mul_mat_monte_seeds(ln):
+    # equal LFSR states give equal results; a different state gives another
+    for lfsr in (7, 1, 0xB403, 65535):
+        _mm_case(ln, "monte", 128, 64, 3, seed=12, lfsr=lfsr)
+
+
+def test_mul_mat_f16_weights(ln):
+    # F16 sources (the KV-cache operand of kq / kqv): converted as F32 values
+    rng = np.random.default_rng(13)
+    K, M, N = 64, 256, 4
+    w16 = (rng.standard_normal((M, K)) * 0.5).astype(np.float16)
+    x = rng.standard_normal((N, K)).astype(np.float32)
+    want = O.mul_mat16_f32w(O.SUM32, w16.astype(np.float32), x)
+    got = host(ln.mul_mat16(O.SUM32, ln.pack16(dev(w16)), dev(x), K, M))
+    same_bits(got, want, "f16 weights")
+
+
+def test_mul_mat_lns32(ln):
+    for (K, M, N, seed) in ((576, 300, 1, 20), (1536, 64, 5, 21), (9, 40, 3, 22)):
+        print(f"\n[mul_mat lns32] K={K} M={M} N={N}", flush=True)
+        rng = np.random.default_rng(seed)
+        w = (rng.standard_normal((M, K)) * 0.02).astype(np.float32)
+        x = rng.standard_normal((N, K)).astype(np.float32)
+        want = O.mul_mat32(w, x)
+        got = host(ln.mul_mat32(ln.pack32(dev(w)), dev(x), K, M))
+        same_bits(got, want, f"lns32 mul_mat K={K}")
+
+
+# ------------------------------------------------------------------ rms_norm --
+
+@pytest.mark.parametrize("mode", MODES)
+def test_rms_norm(ln, mode):
+    rng = np.random.default_rng(30)
+    for shape in ((1, 576), (128, 576), (3, 2, 2048), (5, 1), (70, 16)):
+        print(f"\n[rms_norm] {mode} {shape}", flush=True)
+        x = rng.standard_normal(shape).astype(np.float32)
+        O.monte_set(7)
+        want = O.rms_norm16(O.MODES[mode], x, 1e-5)
+        got = host(ln.rms_norm16(O.MODES[mode], dev(x), 1e-5, seed=7))
+        same_bits(got, want, f"rms_norm {mode} {shape}")
+
+
+def test_rms_norm_lns32(ln):
+    rng = np.random.default_rng(31)
+    for shape in ((1, 576), (9, 2048), (4, 1)):
+        x = rng.standard_normal(shape).astype(np.float32)
+        same_bits(host(ln.rms_norm32(dev(x), 1e-5)), O.rms_norm32(x, 1e-5), f"rms_norm lns32 {shape}")
+
+
+# ------------------------------------------------------------------- softmax --
+
+def _causal(nq, nkv):
+    m = np.zeros((nq, nkv), np.float32)
+    for i in range(nq):
+        m[i, nkv - nq + i + 1:] = -np.inf
+    return m
+
+
+@pytest.mark.parametrize("mode", MODES)
+def test_soft_max(ln, mode):
+    rng = np.random.default_rng(40)
+    m = O.MODES[mode]
+    cases = [
+        ("c1 9x128x128", (rng.standard_normal((9, 128, 128)) * 3).astype(np.float32), None, 0.125),
+        ("c1 causal", (rng.standard_normal((9, 128, 128)) * 3).astype(np.float32), _causal(128, 128), 0.125),
+        ("300x3x2", rng.standard_normal((2, 3, 300)).astype(np.float32), None, 1.0),
+        ("padded mask", rng.standard_normal((4, 5, 64)).astype(np.float32),
+         np.where(rng.random((8, 64)) < 0.2, -np.inf, rng.standard_normal((8, 64))).astype(np.float32), 0.5),
+        ("1100 wide", rng.standard_normal((3, 1100)).astype(np.float32), _causal(3, 1100), 1.0),
+        ("singleton", rng.standard_normal((7, 1)).astype(np.float32), None, 1.0),
+    ]
+    for name, x, mask, scale in cases:
+        print(f"\n[soft_max] {mode} {name}", flush=True)
+        O.monte_set(7)
+        want = O.soft_max16(m, x, mask, scale)
+        got = host(ln.soft_max16(m, dev(x), dev(mask) if mask is not None else None, scale, seed=7))
+        same_bits(got, want, f"soft_max {mode} {name}")
+
+
+def test_soft_max_lns32(ln):
+    rng = np.random.default_rng(41)
+    x = (rng.standard_normal((3, 16, 128)) * 3).astype(np.float32)
+    mask = _causal(16, 128)
+    same_bits(host(ln.soft_max32(dev(x), dev(mask), 0.125)), O.soft_max32(x, mask, 0.125), "soft_max lns32")
+    same_bits(host(ln.soft_max32(dev(x), None, 1.0)), O.soft_max32(x, None, 1.0), "soft_max lns32 unmasked")

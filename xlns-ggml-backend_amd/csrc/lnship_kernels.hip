@@ -1,0 +1,1007 @@
+// gfx950 kernels of the LNS backend and their C ABI (include/lnship.h).
+//
+// Parallelism only ever spans independent outputs; every reduction (dot
+// product, softmax normalizer, rms_norm sum of squares) runs in the
+// reference's element order inside one lane (lns-backend/cuda/
+// lns-cuda-kernels.h:16-21).  Weights are cached "k8-interleaved": element
+// (k, m) of a K x M slice sits at ((k / 8) * M + m) * 8 + k % 8 with K padded
+// to a multiple of 8, so one lane fetches eight consecutive k steps of its row
+// in a single 16-byte load and a wave reads one contiguous 1 KiB block.
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <string>
+
+#include "lnship.h"
+#include "lnship_device.h"
+#include "lnship_tables.h"
+
+namespace lnship {
+
+constexpr int k_block = 256;
+constexpr int k_max_devices = 64;
+// LDS budget of a workgroup on gfx950 (160 KiB per CU)
+constexpr int k_lds_bytes = 160 * 1024;
+constexpr int k_lds_tab32 = k32_tab_n * 4;   // 108304 bytes
+
+static thread_local std::string t_err;
+
+static int fail(int code, const char *fmt, const char *what = "") {
+    char buf[256];
+    std::snprintf(buf, sizeof buf, fmt, what);
+    t_err = buf;
+    return code;
+}
+
+static int hip_fail(hipError_t e, const char *where) {
+    char buf[256];
+    std::snprintf(buf, sizeof buf, "%s: %s", where, hipGetErrorString(e));
+    t_err = buf;
+    return LNSHIP_EDEVICE;
+}
+
+#define LNSHIP_HIP(call)                                          \
+    do {                                                          \
+        hipError_t e_ = (call);                                   \
+        if (e_ != hipSuccess) return hip_fail(e_, #call);         \
+    } while (0)
+
+// ---- per-device state -----------------------------------------------------
+
+struct device_state {
+    bool ready = false;
+    dev_tables T{};
+    void *scratch = nullptr;   // grow-only
+    size_t scratch_size = 0;
+};
+
+static device_state g_devices[k_max_devices];
+static std::mutex g_mutex;
+static host_tables *g_host = nullptr;
+
+static int current_device(int *dev) {
+    LNSHIP_HIP(hipGetDevice(dev));
+    if (*dev < 0 || *dev >= k_max_devices) return fail(LNSHIP_EDEVICE, "device index out of range%s");
+    return 0;
+}
+
+template <class T>
+static int upload(const T *src, size_t n, const T **dst) {
+    void *p = nullptr;
+    LNSHIP_HIP(hipMalloc(&p, n * sizeof(T)));
+    LNSHIP_HIP(hipMemcpy(p, src, n * sizeof(T), hipMemcpyHostToDevice));
+    *dst = static_cast<const T *>(p);
+    return 0;
+}
+
+static device_state *state() {
+    int dev = 0;
+    if (current_device(&dev) != 0) return nullptr;
+    device_state *s = &g_devices[dev];
+    if (!s->ready) {
+        fail(LNSHIP_ENOINIT, "lnship_init was not called for this device%s");
+        return nullptr;
+    }
+    return s;
+}
+
+// Grow-only device scratch of the current device; callers on one device are
+// serialized by the stream order of their launches.
+static int scratch(device_state *s, size_t bytes, void **p) {
+    std::lock_guard<std::mutex> lock(g_mutex);
+    if (bytes > s->scratch_size) {
+        if (s->scratch) {
+            LNSHIP_HIP(hipDeviceSynchronize());
+            LNSHIP_HIP(hipFree(s->scratch));
+            s->scratch = nullptr;
+            s->scratch_size = 0;
+        }
+        size_t sz = std::max(bytes, (size_t)1 << 20);
+        LNSHIP_HIP(hipMalloc(&s->scratch, sz));
+        s->scratch_size = sz;
+    }
+    *p = s->scratch;
+    return 0;
+}
+
+static unsigned grid_for(int64_t n, int per_thread = 1) {
+    int64_t b = (n + (int64_t)k_block * per_thread - 1) / ((int64_t)k_block * per_thread);
+    return (unsigned)std::max<int64_t>(1, std::min<int64_t>(b, 65535));
+}
+
+// ---- LFSR jump-ahead --------------------------------------------------------
+
+__device__ __forceinline__ uint32_t lfsr_jump(const dev_tables &T, uint32_t s, uint64_t n) {
+    if (s == 0) return 0;
+    uint32_t i = T.lfsr_log[s];
+    return T.lfsr_seq[(uint32_t)(((uint64_t)i + n % 65535u) % 65535u)];
+}
+
+// ---- conversions ------------------------------------------------------------
+
+__global__ void k_from_f32_16(const float *__restrict__ src, uint16_t *__restrict__ dst, int64_t n,
+                              const uint16_t *__restrict__ cvt) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)blockDim.x * gridDim.x)
+        dst[i] = (uint16_t)x16_from_f32(cvt, src[i]);
+}
+
+__global__ void k_to_f32_16(const uint16_t *__restrict__ src, float *__restrict__ dst, int64_t n,
+                            const float *__restrict__ rev) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)blockDim.x * gridDim.x)
+        dst[i] = rev[src[i]];
+}
+
+__global__ void k_from_f32_32(const float *__restrict__ src, uint32_t *__restrict__ dst, int64_t n) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)blockDim.x * gridDim.x)
+        dst[i] = x32_from_f32(src[i]);
+}
+
+__global__ void k_to_f32_32(const uint32_t *__restrict__ src, float *__restrict__ dst, int64_t n) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)blockDim.x * gridDim.x)
+        dst[i] = x32_to_f32(src[i]);
+}
+
+__device__ __forceinline__ float load_elem(const void *src, int is_f16, int64_t i) {
+    if (is_f16) return __half2float(reinterpret_cast<const __half *>(src)[i]);
+    return reinterpret_cast<const float *>(src)[i];
+}
+
+// rows x cols row-major -> k8-interleaved (k = col, m = row), one slice per
+// blockIdx.y; padding columns (cols..Kp) get code 0.
+template <int W32>
+__global__ void k_pack(const void *__restrict__ src, int is_f16, int64_t src_ld, int64_t src_slice,
+                       void *__restrict__ dst, int64_t rows, int64_t cols, int64_t kp,
+                       const uint16_t *__restrict__ cvt) {
+    const int64_t n = rows * kp;
+    const int64_t z = blockIdx.y;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)blockDim.x * gridDim.x) {
+        const int64_t r = i / kp, c = i - r * kp;
+        const int64_t o = z * rows * kp + ((c >> 3) * rows + r) * 8 + (c & 7);
+        float v = 0.0f;
+        bool pad = c >= cols;
+        if (!pad) v = load_elem(src, is_f16, z * src_slice + r * src_ld + c);
+        if (W32) reinterpret_cast<uint32_t *>(dst)[o] = pad ? 0u : x32_from_f32(v);
+        else reinterpret_cast<uint16_t *>(dst)[o] = pad ? (uint16_t)0 : (uint16_t)x16_from_f32(cvt, v);
+    }
+}
+
+// activation rows (N per slice, row stride x_ld, slice stride x_slice) into
+// contiguous padded LNS rows [slice][N][Kp]
+template <int W32>
+__global__ void k_act(const float *__restrict__ x, int64_t x_ld, int64_t x_slice, void *__restrict__ dst,
+                      int64_t N, int64_t K, int64_t kp, const uint16_t *__restrict__ cvt) {
+    const int64_t n_all = N * kp;
+    const int64_t z = blockIdx.y;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n_all; i += (int64_t)blockDim.x * gridDim.x) {
+        const int64_t r = i / kp, c = i - r * kp;
+        const int64_t o = z * n_all + i;
+        if (c >= K) {
+            if (W32) reinterpret_cast<uint32_t *>(dst)[o] = 0u;
+            else reinterpret_cast<uint16_t *>(dst)[o] = 0;
+            continue;
+        }
+        const float v = x[z * x_slice + r * x_ld + c];
+        if (W32) reinterpret_cast<uint32_t *>(dst)[o] = x32_from_f32(v);
+        else reinterpret_cast<uint16_t *>(dst)[o] = (uint16_t)x16_from_f32(cvt, v);
+    }
+}
+
+// ---- reductions -------------------------------------------------------------
+// One accumulator per (row, column) per lane; start/add/finish as in the
+// reference's reduction policies (cuda/lns-cuda-xlns16.cu:67-130).
+
+template <int MODE>
+struct red16;
+
+template <>
+struct red16<LNSHIP_BASE> {
+    const int16_t *g;
+    __device__ __forceinline__ uint32_t start(uint32_t v, uint32_t &) const { return v; }
+    __device__ __forceinline__ uint32_t add(uint32_t a, uint32_t t, uint32_t &) const { return x16_add_g(g, a, t); }
+    __device__ __forceinline__ uint32_t finish(uint32_t a) const { return a; }
+};
+
+template <>
+struct red16<LNSHIP_MONTE> {
+    const int32_t *gm;
+    __device__ __forceinline__ uint32_t start(uint32_t v, uint32_t &) const { return v; }
+    __device__ __forceinline__ uint32_t add(uint32_t a, uint32_t t, uint32_t &st) const {
+        st = lfsr_step(st);
+        return x16_add_monte(gm, a, t, st);
+    }
+    __device__ __forceinline__ uint32_t finish(uint32_t a) const { return a; }
+};
+
+template <>
+struct red16<LNSHIP_SUM32> {
+    const int32_t *T;
+    __device__ __forceinline__ uint32_t start(uint32_t v, uint32_t &) const { return v << 16; }
+    __device__ __forceinline__ uint32_t add(uint32_t a, uint32_t t, uint32_t &) const { return x32_add(T, a, t << 16); }
+    __device__ __forceinline__ uint32_t finish(uint32_t s) const {
+        if ((s & k32_logmask) >= 0x7fff8000u) return (s >> 16) | k16_logmask;
+        return (s + 0x8000u) >> 16;
+    }
+};
+
+// LPVIP: ROM-less xlns32 adder (Mitchell antilog + corrected Mitchell log;
+// the exact Gaussian log within one binade of the db singularity).
+__device__ __forceinline__ uint32_t mitchell_exp2_neg(uint32_t d) {
+    uint32_t q = d >> 23, r = d & 0x7fffffu;
+    if (q >= 31) return 0;
+    return ((0x1000000u - r) >> 1) >> q;
+}
+__device__ __forceinline__ int32_t lpvip_sb(uint32_t d) {
+    uint32_t u = mitchell_exp2_neg(d);
+    uint64_t corr = ((uint64_t)u * (uint64_t)(0x800000u - u)) >> 23;
+    return (int32_t)(u + (uint32_t)((corr * 0x2B8u) >> 11));
+}
+__device__ __forceinline__ int32_t lpvip_db(uint32_t d) {
+    if (d < 0x800000u) {
+        double v = log(1.0 - pow(2.0, -(double)d / 8388608.0)) / log(2.0) * 8388608.0;
+        return (int32_t)floor(v + 0.5);
+    }
+    uint32_t u = mitchell_exp2_neg(d);
+    uint64_t sq = ((uint64_t)u * u) >> 23;
+    return -(int32_t)(u + (uint32_t)((sq * 0xB8Au) >> 12));
+}
+
+template <>
+struct red16<LNSHIP_LPVIP> {
+    __device__ __forceinline__ uint32_t start(uint32_t v, uint32_t &) const { return v << 16; }
+    __device__ __forceinline__ uint32_t add(uint32_t a, uint32_t t16, uint32_t &) const {
+        uint32_t t = t16 << 16;
+        uint32_t al = a & k32_logmask, tl = t & k32_logmask;
+        uint32_t maxl = max(al, tl), d = maxl - min(al, tl);
+        uint32_t sgn = (al > tl ? a : t) & k32_sign;
+        uint32_t usedb = (a ^ t) & k32_sign;
+        if (d == 0 && usedb) return 0u;
+        int32_t adj = 0;
+        if (d < k32_esszer) adj = usedb ? lpvip_db(d) : lpvip_sb(d);
+        uint32_t s = maxl + (uint32_t)adj;
+        uint32_t l = (s & k32_sign) ? ((s & k32_one) ? 0u : k32_logmask) : s;
+        return sgn | l;
+    }
+    __device__ __forceinline__ uint32_t finish(uint32_t s) const { return s >> 16; }
+};
+
+// Stages the tables a reduction needs into LDS; returns the policy.
+template <int MODE>
+__device__ __forceinline__ red16<MODE> stage_tables(const dev_tables &T, char *lds);
+
+template <>
+__device__ __forceinline__ red16<LNSHIP_BASE> stage_tables<LNSHIP_BASE>(const dev_tables &T, char *lds) {
+    int16_t *g = reinterpret_cast<int16_t *>(lds);
+    for (int i = threadIdx.x; i < 2 * k16_gauss_n; i += blockDim.x) g[i] = T.gauss16[i];
+    return red16<LNSHIP_BASE>{g};
+}
+template <>
+__device__ __forceinline__ red16<LNSHIP_MONTE> stage_tables<LNSHIP_MONTE>(const dev_tables &T, char *lds) {
+    int32_t *g = reinterpret_cast<int32_t *>(lds);
+    for (int i = threadIdx.x; i < 2 * k16_gauss_n; i += blockDim.x) g[i] = T.gauss16m[i];
+    return red16<LNSHIP_MONTE>{g};
+}
+template <>
+__device__ __forceinline__ red16<LNSHIP_SUM32> stage_tables<LNSHIP_SUM32>(const dev_tables &T, char *lds) {
+    int32_t *t = reinterpret_cast<int32_t *>(lds);
+    const int4 *src = reinterpret_cast<const int4 *>(T.tab32);
+    int4 *d4 = reinterpret_cast<int4 *>(t);
+    for (int i = threadIdx.x; i < k32_tab_n / 4; i += blockDim.x) d4[i] = src[i];
+    for (int i = (k32_tab_n / 4) * 4 + threadIdx.x; i < k32_tab_n; i += blockDim.x) t[i] = T.tab32[i];
+    return red16<LNSHIP_SUM32>{t};
+}
+template <>
+__device__ __forceinline__ red16<LNSHIP_LPVIP> stage_tables<LNSHIP_LPVIP>(const dev_tables &, char *) {
+    return red16<LNSHIP_LPVIP>{};
+}
+
+template <int MODE>
+constexpr int lds_tables_bytes() {
+    return MODE == LNSHIP_BASE ? 2 * k16_gauss_n * 2 :
+           MODE == LNSHIP_MONTE ? 2 * k16_gauss_n * 4 :
+           MODE == LNSHIP_SUM32 ? k_lds_tab32 : 0;
+}
+
+// ---- MUL_MAT ------------------------------------------------------------------
+// One lane per weight row m and NC activation columns n (NC independent
+// accumulations interleaved for latency hiding).  xs holds the converted
+// activations [slice][N][Kp]; their index is uniform across the wave, so the
+// compiler fetches them through the scalar cache.
+
+struct mm_args16 {
+    const uint16_t *w;
+    const uint16_t *x;
+    float *dst;
+    int64_t K, kp, M, N;
+    int64_t ne02, ne12, r2, r3;
+    uint32_t seed;
+};
+
+template <int MODE, int NC>
+__global__ __launch_bounds__(k_block) void k_mm16(mm_args16 a, dev_tables T) {
+    extern __shared__ __align__(16) char lds[];
+    const red16<MODE> R = stage_tables<MODE>(T, lds);
+    __syncthreads();
+
+    const int64_t m = (int64_t)blockIdx.x * k_block + threadIdx.x;
+    if (m >= a.M) return;
+    const int64_t n0 = (int64_t)blockIdx.y * NC;
+    const int64_t z = blockIdx.z;
+    const int64_t i12 = z % a.ne12, i13 = z / a.ne12;
+    const int nc = (int)min<int64_t>(NC, a.N - n0);
+
+    const uint16_t *ws = a.w + ((i13 / a.r3) * a.ne02 + i12 / a.r2) * a.kp * a.M + m * 8;
+    const uint16_t *xs = a.x + (z * a.N + n0) * a.kp;
+    const int64_t wstride = a.M * 8;   // between consecutive groups of 8 k
+
+    uint32_t acc[NC], st[NC];
+#pragma unroll
+    for (int j = 0; j < NC; j++) {
+        acc[j] = 0;
+        st[j] = 0;
+        if (MODE == LNSHIP_MONTE && j < nc) {
+            const uint64_t out = ((uint64_t)z * (uint64_t)a.M + (uint64_t)m) * (uint64_t)a.N + (uint64_t)(n0 + j);
+            st[j] = lfsr_jump(T, a.seed, out * (uint64_t)(a.K - 1));
+        }
+    }
+    // group g holds steps 8g .. 8g+7; with first, step 0 starts the
+    // accumulation; steps [u0, u1) are added
+    auto group = [&](int64_t g, bool first, int u0, int u1) {
+        const uint4 wq = *reinterpret_cast<const uint4 *>(ws + g * wstride);
+        const uint32_t wv[8] = {wq.x & 0xffffu, wq.x >> 16, wq.y & 0xffffu, wq.y >> 16,
+                                wq.z & 0xffffu, wq.z >> 16, wq.w & 0xffffu, wq.w >> 16};
+        uint32_t xv[NC][8];
+#pragma unroll
+        for (int j = 0; j < NC; j++) {
+            const int jj = j < nc ? j : 0;
+            const uint4 xq = *reinterpret_cast<const uint4 *>(xs + jj * a.kp + g * 8);
+            xv[j][0] = xq.x & 0xffffu; xv[j][1] = xq.x >> 16; xv[j][2] = xq.y & 0xffffu; xv[j][3] = xq.y >> 16;
+            xv[j][4] = xq.z & 0xffffu; xv[j][5] = xq.z >> 16; xv[j][6] = xq.w & 0xffffu; xv[j][7] = xq.w >> 16;
+        }
+        if (first) {
+#pragma unroll
+            for (int j = 0; j < NC; j++) acc[j] = R.start(x16_mul(wv[0], xv[j][0]), st[j]);
+        }
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            if (u >= u0 && u < u1) {
+#pragma unroll
+                for (int j = 0; j < NC; j++) acc[j] = R.add(acc[j], x16_mul(wv[u], xv[j][u]), st[j]);
+            }
+        }
+    };
+    const int64_t full = a.K >> 3;
+    const int tail = (int)(a.K & 7);
+    if (a.K > 0) {
+        group(0, true, 1, full > 0 ? 8 : tail);
+        for (int64_t g = 1; g < full; g++) group(g, false, 0, 8);
+        if (full > 0 && tail > 0) group(full, false, 0, tail);
+    }
+    float *ds = a.dst + (z * a.N + n0) * a.M + m;
+#pragma unroll
+    for (int j = 0; j < NC; j++) {
+        if (j < nc) ds[(int64_t)j * a.M] = a.K == 0 ? T.rev16[0] : T.rev16[R.finish(acc[j]) & 0xffffu];
+    }
+}
+
+// xlns32 (the LNS32 backend): plain sequential xlns32_add
+struct mm_args32 {
+    const uint32_t *w;
+    const uint32_t *x;
+    float *dst;
+    int64_t K, kp, M, N;
+    int64_t ne02, ne12, r2, r3;
+};
+
+template <int NC>
+__global__ __launch_bounds__(k_block) void k_mm32(mm_args32 a, dev_tables T) {
+    extern __shared__ __align__(16) char lds[];
+    const red16<LNSHIP_SUM32> R = stage_tables<LNSHIP_SUM32>(T, lds);
+    __syncthreads();
+    const int64_t m = (int64_t)blockIdx.x * k_block + threadIdx.x;
+    if (m >= a.M) return;
+    const int64_t n0 = (int64_t)blockIdx.y * NC;
+    const int64_t z = blockIdx.z;
+    const int64_t i12 = z % a.ne12, i13 = z / a.ne12;
+    const int nc = (int)min<int64_t>(NC, a.N - n0);
+    const uint32_t *ws = a.w + ((i13 / a.r3) * a.ne02 + i12 / a.r2) * a.kp * a.M + m * 8;
+    const uint32_t *xs = a.x + (z * a.N + n0) * a.kp;
+    const int64_t wstride = a.M * 8;
+    uint32_t acc[NC];
+#pragma unroll
+    for (int j = 0; j < NC; j++) acc[j] = 0;
+    const int64_t kgroups = a.kp >> 3;
+    for (int64_t g = 0; g < kgroups; g++) {
+        const uint4 w0 = *reinterpret_cast<const uint4 *>(ws + g * wstride);
+        const uint4 w1 = *reinterpret_cast<const uint4 *>(ws + g * wstride + 4);
+        const uint32_t wv[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+        uint32_t xv[NC][8];
+#pragma unroll
+        for (int j = 0; j < NC; j++) {
+            const int jj = j < nc ? j : 0;
+            const uint4 x0 = *reinterpret_cast<const uint4 *>(xs + jj * a.kp + g * 8);
+            const uint4 x1 = *reinterpret_cast<const uint4 *>(xs + jj * a.kp + g * 8 + 4);
+            xv[j][0] = x0.x; xv[j][1] = x0.y; xv[j][2] = x0.z; xv[j][3] = x0.w;
+            xv[j][4] = x1.x; xv[j][5] = x1.y; xv[j][6] = x1.z; xv[j][7] = x1.w;
+        }
+        const int64_t kb = g * 8;
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            if (kb + u >= a.K) break;
+#pragma unroll
+            for (int j = 0; j < NC; j++) {
+                const uint32_t t = x32_mul(wv[u], xv[j][u]);
+                acc[j] = (kb + u == 0) ? t : x32_add(R.T, acc[j], t);
+            }
+        }
+    }
+    float *ds = a.dst + (z * a.N + n0) * a.M + m;
+#pragma unroll
+    for (int j = 0; j < NC; j++)
+        if (j < nc) ds[(int64_t)j * a.M] = a.K == 0 ? 0.0f : x32_to_f32(acc[j]);
+}
+
+// ---- RMS_NORM -------------------------------------------------------------------
+// A workgroup takes rb rows: all threads convert and square into LDS, one lane
+// per row runs the sequential sum, all threads scale.
+
+template <int MODE>
+__global__ __launch_bounds__(k_block) void k_rms16(const float *__restrict__ src, float *__restrict__ dst,
+                                                   int64_t ncols, int64_t nrows, int rb, float eps,
+                                                   uint32_t seed, dev_tables T) {
+    extern __shared__ __align__(16) char lds[];
+    const red16<MODE> R = stage_tables<MODE>(T, lds);
+    uint16_t *sq = reinterpret_cast<uint16_t *>(lds + ((lds_tables_bytes<MODE>() + 15) & ~15));
+    __shared__ uint32_t s_inv[64];
+    const int64_t r0 = (int64_t)blockIdx.x * rb;
+    const int nr = (int)min<int64_t>(rb, nrows - r0);
+    const int64_t ne = (int64_t)nr * ncols;
+    for (int64_t e = threadIdx.x; e < ne; e += blockDim.x) {
+        const uint32_t c = x16_from_f32(T.cvt16, src[r0 * ncols + e]);
+        sq[e] = (uint16_t)x16_mul(c, c);
+    }
+    __syncthreads();
+    if ((int)threadIdx.x < nr) {
+        const int r = threadIdx.x;
+        uint32_t s = 0;
+        if (MODE == LNSHIP_MONTE) s = lfsr_jump(T, seed, (uint64_t)(r0 + r) * (uint64_t)ncols);
+        const uint16_t *row = sq + (int64_t)r * ncols;
+        uint32_t acc = R.start(0u, s);
+        for (int64_t i = 0; i < ncols; i++) acc = R.add(acc, row[i], s);
+        const uint32_t sum = R.finish(acc) & 0xffffu;
+        const uint32_t mean = x16_mul(sum, x16_from_f32(T.cvt16, 1.0f / (float)ncols));
+        const uint32_t e16 = x16_from_f32(T.cvt16, eps);
+        // the epsilon add is a plain xlns16_add in every mode
+        const uint32_t me = x16_add_g(T.gauss16, mean, e16);
+        s_inv[r] = x16_recip(x16_sqrt(me));
+    }
+    __syncthreads();
+    for (int64_t e = threadIdx.x; e < ne; e += blockDim.x) {
+        const int r = (int)(e / ncols);
+        const uint32_t c = x16_from_f32(T.cvt16, src[r0 * ncols + e]);
+        dst[r0 * ncols + e] = T.rev16[x16_mul(c, s_inv[r])];
+    }
+}
+
+__global__ __launch_bounds__(k_block) void k_rms32(const float *__restrict__ src, float *__restrict__ dst,
+                                                   int64_t ncols, int64_t nrows, int rb, float eps, dev_tables T) {
+    extern __shared__ __align__(16) char lds[];
+    const red16<LNSHIP_SUM32> R = stage_tables<LNSHIP_SUM32>(T, lds);
+    uint32_t *sq = reinterpret_cast<uint32_t *>(lds + k_lds_tab32);
+    __shared__ uint32_t s_inv[64];
+    const int64_t r0 = (int64_t)blockIdx.x * rb;
+    const int nr = (int)min<int64_t>(rb, nrows - r0);
+    const int64_t ne = (int64_t)nr * ncols;
+    for (int64_t e = threadIdx.x; e < ne; e += blockDim.x) {
+        const uint32_t c = x32_from_f32(src[r0 * ncols + e]);
+        sq[e] = x32_mul(c, c);
+    }
+    __syncthreads();
+    if ((int)threadIdx.x < nr) {
+        const int r = threadIdx.x;
+        const uint32_t *row = sq + (int64_t)r * ncols;
+        uint32_t acc = 0;
+        for (int64_t i = 0; i < ncols; i++) acc = x32_add(R.T, acc, row[i]);
+        const uint32_t mean = x32_mul(acc, x32_from_f32(1.0f / (float)ncols));
+        s_inv[r] = x32_recip(x32_sqrt(x32_add(R.T, mean, x32_from_f32(eps))));
+    }
+    __syncthreads();
+    for (int64_t e = threadIdx.x; e < ne; e += blockDim.x) {
+        const int r = (int)(e / ncols);
+        dst[r0 * ncols + e] = x32_to_f32(x32_mul(x32_from_f32(src[r0 * ncols + e]), s_inv[r]));
+    }
+}
+
+// ---- SOFT_MAX -------------------------------------------------------------------
+// A workgroup takes rb rows: scale / mask / row maximum (order-free: canonical
+// order is total) and exp in parallel, one lane per row sums in element order,
+// then the division in parallel.
+
+struct sm_args {
+    const float *src;
+    const float *mask;
+    float *dst;
+    int64_t n, ne1, ne2, ne3;
+    int64_t mne0, mne1, mne2, mne3;
+    float scale;
+    uint32_t seed;
+    int rb;
+};
+
+__device__ __forceinline__ const float *mask_row(const sm_args &a, int64_t row) {
+    const int64_t i1 = row % a.ne1, i2 = (row / a.ne1) % a.ne2, i3 = row / (a.ne1 * a.ne2);
+    return a.mask + (((i3 % a.mne3) * a.mne2 + (i2 % a.mne2)) * a.mne1 + i1) * a.mne0;
+}
+
+template <int MODE>
+__global__ __launch_bounds__(k_block) void k_softmax16(sm_args a, dev_tables T) {
+    extern __shared__ __align__(16) char lds[];
+    const red16<MODE> R = stage_tables<MODE>(T, lds);
+    // the plain xlns16 adder (scale, mask bias, max subtraction) reads the
+    // global copy of the Gaussian-log table
+    uint16_t *c = reinterpret_cast<uint16_t *>(lds + ((lds_tables_bytes<MODE>() + 15) & ~15));
+    __shared__ int32_t s_max[64];
+    __shared__ uint32_t s_tot[64];
+    const int64_t r0 = (int64_t)blockIdx.x * a.rb;
+    const int nr = (int)min<int64_t>(a.rb, a.ne1 * a.ne2 * a.ne3 - r0);
+    const int64_t ne = (int64_t)nr * a.n;
+    if ((int)threadIdx.x < nr) s_max[threadIdx.x] = x16_canon(0xffffu);
+    __syncthreads();
+    const uint32_t sc = x16_from_f32(T.cvt16, a.scale);
+    for (int64_t e = threadIdx.x; e < ne; e += blockDim.x) {
+        const int r = (int)(e / a.n);
+        const int64_t i = e - (int64_t)r * a.n;
+        uint32_t v = x16_from_f32(T.cvt16, a.src[(r0 + r) * a.n + i]);
+        if (v != 0xffffu) {
+            v = x16_mul(v, sc);
+            if (a.mask) {
+                const float mf = mask_row(a, r0 + r)[i];
+                const uint32_t mk = mf <= -3.0e38f ? 0xffffu : x16_from_f32(T.cvt16, mf);
+                if (mk == 0xffffu) v = 0xffffu;
+                else if (mk & k16_logmask) v = x16_add_g(T.gauss16, v, mk);
+            }
+        }
+        c[e] = (uint16_t)v;
+        atomicMax(&s_max[r], x16_canon(v));
+    }
+    __syncthreads();
+    for (int64_t e = threadIdx.x; e < ne; e += blockDim.x) {
+        const int r = (int)(e / a.n);
+        const int32_t cm = s_max[r];
+        const uint32_t mx = (uint32_t)(uint16_t)(cm < 0 ? (cm ^ 0x7fff) : cm);
+        c[e] = T.exp16[x16_add_g(T.gauss16, c[e], mx ^ k16_sign)];
+    }
+    __syncthreads();
+    if ((int)threadIdx.x < nr) {
+        const int r = threadIdx.x;
+        uint32_t s = 0;
+        if (MODE == LNSHIP_MONTE) s = lfsr_jump(T, a.seed, (uint64_t)(r0 + r) * (uint64_t)(a.n - 1));
+        const uint16_t *row = c + (int64_t)r * a.n;
+        uint32_t acc = R.start(row[0], s);
+        for (int64_t i = 1; i < a.n; i++) acc = R.add(acc, row[i], s);
+        s_tot[r] = R.finish(acc) & 0xffffu;
+    }
+    __syncthreads();
+    for (int64_t e = threadIdx.x; e < ne; e += blockDim.x) {
+        const int r = (int)(e / a.n);
+        a.dst[r0 * a.n + e] = T.rev16[x16_div(c[e], s_tot[r])];
+    }
+}
+
+__global__ __launch_bounds__(k_block) void k_softmax32(sm_args a, dev_tables T) {
+    extern __shared__ __align__(16) char lds[];
+    const red16<LNSHIP_SUM32> R = stage_tables<LNSHIP_SUM32>(T, lds);
+    uint32_t *c = reinterpret_cast<uint32_t *>(lds + k_lds_tab32);
+    __shared__ int32_t s_max[64];
+    __shared__ uint32_t s_tot[64];
+    const int64_t r0 = (int64_t)blockIdx.x * a.rb;
+    const int nr = (int)min<int64_t>(a.rb, a.ne1 * a.ne2 * a.ne3 - r0);
+    const int64_t ne = (int64_t)nr * a.n;
+    if ((int)threadIdx.x < nr) s_max[threadIdx.x] = x32_canon(0xffffffffu);
+    __syncthreads();
+    const uint32_t sc = x32_from_f32(a.scale);
+    for (int64_t e = threadIdx.x; e < ne; e += blockDim.x) {
+        const int r = (int)(e / a.n);
+        const int64_t i = e - (int64_t)r * a.n;
+        uint32_t v = x32_from_f32(a.src[(r0 + r) * a.n + i]);
+        if (v != 0xffffffffu) {
+            v = x32_mul(v, sc);
+            if (a.mask) {
+                const float mf = mask_row(a, r0 + r)[i];
+                const uint32_t mk = mf <= -3.0e38f ? 0xffffffffu : x32_from_f32(mf);
+                if (mk == 0xffffffffu) v = 0xffffffffu;
+                else if (mk & k32_logmask) v = x32_add(R.T, v, mk);
+            }
+        }
+        c[e] = v;
+        atomicMax(&s_max[r], x32_canon(v));
+    }
+    __syncthreads();
+    for (int64_t e = threadIdx.x; e < ne; e += blockDim.x) {
+        const int r = (int)(e / a.n);
+        const int32_t cm = s_max[r];
+        const uint32_t mx = (uint32_t)(cm < 0 ? (cm ^ 0x7fffffff) : cm);
+        const float fv = x32_to_f32(x32_add(R.T, c[e], mx ^ k32_sign));
+        c[e] = x32_from_f32((float)exp((double)fv));
+    }
+    __syncthreads();
+    if ((int)threadIdx.x < nr) {
+        const int r = threadIdx.x;
+        const uint32_t *row = c + (int64_t)r * a.n;
+        uint32_t acc = row[0];
+        for (int64_t i = 1; i < a.n; i++) acc = x32_add(R.T, acc, row[i]);
+        s_tot[r] = acc;
+    }
+    __syncthreads();
+    for (int64_t e = threadIdx.x; e < ne; e += blockDim.x) {
+        const int r = (int)(e / a.n);
+        a.dst[r0 * a.n + e] = x32_to_f32(x32_div(c[e], s_tot[r]));
+    }
+}
+
+// ---- host helpers -------------------------------------------------------------
+
+template <int MODE>
+static int rows_per_block(int64_t ncols, int elem_bytes) {
+    const int64_t avail = k_lds_bytes - ((lds_tables_bytes<MODE>() + 15) & ~15) - 1024;
+    int64_t rb = avail / std::max<int64_t>(1, ncols * elem_bytes);
+    return (int)std::min<int64_t>(64, rb);
+}
+
+template <class K>
+static int set_lds(K kernel, int bytes) {
+    LNSHIP_HIP(hipFuncSetAttribute((const void *)kernel, hipFuncAttributeMaxDynamicSharedMemorySize, bytes));
+    return 0;
+}
+
+static int pack_common(int w32, const void *src, int src_is_f16, int64_t src_ld, int64_t src_slice, void *dst,
+                       int64_t K, int64_t M, int64_t nslices, void *stream) {
+    device_state *s = state();
+    if (!s) return LNSHIP_ENOINIT;
+    if (K < 0 || M < 0 || nslices < 0 || src_ld < K || nslices > 65535)
+        return fail(LNSHIP_EINVAL, "pack: bad shape%s");
+    if (K == 0 || M == 0 || nslices == 0) return 0;
+    const int64_t kp = (K + 7) & ~(int64_t)7;
+    dim3 grid(grid_for(M * kp, 2), (unsigned)nslices);
+    if (w32)
+        hipLaunchKernelGGL(k_pack<1>, grid, dim3(k_block), 0, (hipStream_t)stream, src, src_is_f16, src_ld, src_slice,
+                           dst, M, K, kp, s->T.cvt16);
+    else
+        hipLaunchKernelGGL(k_pack<0>, grid, dim3(k_block), 0, (hipStream_t)stream, src, src_is_f16, src_ld, src_slice,
+                           dst, M, K, kp, s->T.cvt16);
+    LNSHIP_HIP(hipGetLastError());
+    return 0;
+}
+
+static int check_mm(const lnship_mul_mat_args *a) {
+    if (!a || a->K < 0 || a->M < 0 || a->N < 0 || a->ne02 <= 0 || a->ne03 <= 0 || a->ne12 <= 0 || a->ne13 <= 0)
+        return fail(LNSHIP_EINVAL, "mul_mat: bad shape%s");
+    if (a->ne12 % a->ne02 || a->ne13 % a->ne03) return fail(LNSHIP_EINVAL, "mul_mat: slices do not broadcast%s");
+    if (a->ne12 * a->ne13 > 65535) return fail(LNSHIP_ERANGE, "mul_mat: more than 65535 activation slices%s");
+    const int64_t xld = a->x_ld ? a->x_ld : a->K;
+    if (xld < a->K) return fail(LNSHIP_EINVAL, "mul_mat: x_ld < K%s");
+    return 0;
+}
+
+template <int MODE, int NC>
+static int launch_mm16(const mm_args16 &m, const dev_tables &T, int64_t nslices, hipStream_t st) {
+    constexpr int lds = lds_tables_bytes<MODE>();
+    if (lds > 64 * 1024)
+        if (int rc = set_lds(k_mm16<MODE, NC>, lds)) return rc;
+    dim3 grid((unsigned)((m.M + k_block - 1) / k_block), (unsigned)((m.N + NC - 1) / NC), (unsigned)nslices);
+    if (grid.x > 2147483647u || grid.y > 65535u) return fail(LNSHIP_ERANGE, "mul_mat: grid too large%s");
+    hipLaunchKernelGGL((k_mm16<MODE, NC>), grid, dim3(k_block), lds, st, m, T);
+    LNSHIP_HIP(hipGetLastError());
+    return 0;
+}
+
+template <int MODE>
+static int dispatch_mm16(const mm_args16 &m, const dev_tables &T, int64_t nslices, hipStream_t st) {
+    if (m.N >= 8) return launch_mm16<MODE, 8>(m, T, nslices, st);
+    if (m.N >= 4) return launch_mm16<MODE, 4>(m, T, nslices, st);
+    return launch_mm16<MODE, 1>(m, T, nslices, st);
+}
+
+template <int NC>
+static int launch_mm32(const mm_args32 &m, const dev_tables &T, int64_t nslices, hipStream_t st) {
+    if (int rc = set_lds(k_mm32<NC>, k_lds_tab32)) return rc;
+    dim3 grid((unsigned)((m.M + k_block - 1) / k_block), (unsigned)((m.N + NC - 1) / NC), (unsigned)nslices);
+    if (grid.y > 65535u) return fail(LNSHIP_ERANGE, "mul_mat: grid too large%s");
+    hipLaunchKernelGGL((k_mm32<NC>), grid, dim3(k_block), k_lds_tab32, st, m, T);
+    LNSHIP_HIP(hipGetLastError());
+    return 0;
+}
+
+template <int MODE>
+static int launch_rms16(const float *src, float *dst, int64_t ncols, int64_t nrows, float eps, uint16_t seed,
+                        const dev_tables &T, hipStream_t st) {
+    const int rb = rows_per_block<MODE>(ncols, 2);
+    if (rb < 1) return fail(LNSHIP_ERANGE, "rms_norm: row too long for LDS%s");
+    const int lds = ((lds_tables_bytes<MODE>() + 15) & ~15) + (int)(rb * ncols * 2);
+    if (int rc = set_lds(k_rms16<MODE>, lds)) return rc;
+    hipLaunchKernelGGL(k_rms16<MODE>, dim3((unsigned)((nrows + rb - 1) / rb)), dim3(k_block), lds, st, src, dst, ncols,
+                       nrows, rb, eps, (uint32_t)seed, T);
+    LNSHIP_HIP(hipGetLastError());
+    return 0;
+}
+
+static int check_sm(const lnship_soft_max_args *a) {
+    if (!a) return fail(LNSHIP_EINVAL, "soft_max: null args%s");
+    for (int i = 0; i < 4; i++)
+        if (a->src_ne[i] < 0) return fail(LNSHIP_EINVAL, "soft_max: bad shape%s");
+    if (a->mask) {
+        for (int i = 0; i < 4; i++)
+            if (a->mask_ne[i] <= 0) return fail(LNSHIP_EINVAL, "soft_max: bad mask shape%s");
+        if (a->mask_ne[0] != a->src_ne[0] || a->mask_ne[1] < a->src_ne[1])
+            return fail(LNSHIP_EINVAL, "soft_max: mask does not cover the rows%s");
+    }
+    return 0;
+}
+
+template <int MODE>
+static int launch_sm16(sm_args &m, int64_t nrows, const dev_tables &T, hipStream_t st) {
+    m.rb = rows_per_block<MODE>(m.n, 2);
+    if (m.rb < 1) return fail(LNSHIP_ERANGE, "soft_max: row too long for LDS%s");
+    const int lds = ((lds_tables_bytes<MODE>() + 15) & ~15) + (int)(m.rb * m.n * 2);
+    if (int rc = set_lds(k_softmax16<MODE>, lds)) return rc;
+    hipLaunchKernelGGL(k_softmax16<MODE>, dim3((unsigned)((nrows + m.rb - 1) / m.rb)), dim3(k_block), lds, st, m, T);
+    LNSHIP_HIP(hipGetLastError());
+    return 0;
+}
+
+}  // namespace lnship
+
+using namespace lnship;
+
+// ===================================================================== C ABI ==
+
+extern "C" {
+
+const char *lnship_last_error(void) { return t_err.c_str(); }
+
+const char *lnship_version(void) { return "lnship 0.1: xlns16 (table, alt) + xlns32 (alt) for gfx950"; }
+
+const void *lnship_host_table(const char *name, size_t *bytes) {
+    {
+        std::lock_guard<std::mutex> lock(g_mutex);
+        if (!g_host) {
+            g_host = new host_tables;
+            build_host_tables(*g_host);
+        }
+    }
+    struct { const char *n; const void *p; size_t b; } t[] = {
+        {"cvt16", g_host->cvt16, sizeof g_host->cvt16},
+        {"rev16", g_host->rev16, sizeof g_host->rev16},
+        {"gauss16", g_host->gauss16, sizeof g_host->gauss16},
+        {"gauss16m", g_host->gauss16m, sizeof g_host->gauss16m},
+        {"exp16", g_host->exp16, sizeof g_host->exp16},
+        {"tab32", g_host->tab32, sizeof g_host->tab32},
+        {"lfsr_seq", g_host->lfsr_seq, sizeof g_host->lfsr_seq},
+    };
+    for (auto &e : t)
+        if (std::strcmp(e.n, name) == 0) {
+            if (bytes) *bytes = e.b;
+            return e.p;
+        }
+    fail(LNSHIP_EINVAL, "unknown table %s", name);
+    return nullptr;
+}
+
+int lnship_init(void) {
+    int dev = 0;
+    if (int rc = current_device(&dev)) return rc;
+    if (!lnship_host_table("cvt16", nullptr)) return LNSHIP_EINVAL;
+    std::lock_guard<std::mutex> lock(g_mutex);
+    device_state &s = g_devices[dev];
+    if (s.ready) return 0;
+    dev_tables T{};
+    if (int rc = upload(g_host->cvt16, 1u << 17, &T.cvt16)) return rc;
+    if (int rc = upload(g_host->rev16, 1u << 16, &T.rev16)) return rc;
+    if (int rc = upload(g_host->gauss16, 2 * k16_gauss_n, &T.gauss16)) return rc;
+    if (int rc = upload(g_host->gauss16m, 2 * k16_gauss_n, &T.gauss16m)) return rc;
+    if (int rc = upload(g_host->exp16, 1u << 16, &T.exp16)) return rc;
+    if (int rc = upload(g_host->tab32, (size_t)k32_tab_n, &T.tab32)) return rc;
+    if (int rc = upload(g_host->lfsr_seq, 65536, &T.lfsr_seq)) return rc;
+    if (int rc = upload(g_host->lfsr_log, 65536, &T.lfsr_log)) return rc;
+    s.T = T;
+    s.ready = true;
+    return 0;
+}
+
+uint16_t lnship_lfsr_jump(uint16_t st, uint64_t n) {
+    for (uint64_t i = n % 65535u; i > 0; i--) st = (uint16_t)((st >> 1) ^ ((st & 1u) ? 0xB400u : 0u));
+    return st;
+}
+
+uint64_t lnship16_mul_mat_draws(int mode, int64_t K, int64_t M, int64_t N, int64_t ne12, int64_t ne13) {
+    if (mode != LNSHIP_MONTE || K <= 0) return 0;
+    return (uint64_t)ne12 * (uint64_t)ne13 * (uint64_t)M * (uint64_t)N * (uint64_t)(K - 1);
+}
+uint64_t lnship16_soft_max_draws(int mode, int64_t ncols, int64_t nrows) {
+    return mode == LNSHIP_MONTE && ncols > 0 ? (uint64_t)nrows * (uint64_t)(ncols - 1) : 0;
+}
+uint64_t lnship16_rms_norm_draws(int mode, int64_t ncols, int64_t nrows) {
+    return mode == LNSHIP_MONTE ? (uint64_t)nrows * (uint64_t)ncols : 0;
+}
+
+int lnship16_from_f32(const float *src, uint16_t *dst, int64_t n, void *stream) {
+    device_state *s = state();
+    if (!s) return LNSHIP_ENOINIT;
+    if (n < 0) return fail(LNSHIP_EINVAL, "negative length%s");
+    if (n == 0) return 0;
+    hipLaunchKernelGGL(k_from_f32_16, dim3(grid_for(n, 4)), dim3(k_block), 0, (hipStream_t)stream, src, dst, n,
+                       s->T.cvt16);
+    LNSHIP_HIP(hipGetLastError());
+    return 0;
+}
+
+int lnship16_to_f32(const uint16_t *src, float *dst, int64_t n, void *stream) {
+    device_state *s = state();
+    if (!s) return LNSHIP_ENOINIT;
+    if (n < 0) return fail(LNSHIP_EINVAL, "negative length%s");
+    if (n == 0) return 0;
+    hipLaunchKernelGGL(k_to_f32_16, dim3(grid_for(n, 4)), dim3(k_block), 0, (hipStream_t)stream, src, dst, n,
+                       s->T.rev16);
+    LNSHIP_HIP(hipGetLastError());
+    return 0;
+}
+
+int lnship32_from_f32(const float *src, uint32_t *dst, int64_t n, void *stream) {
+    device_state *s = state();
+    if (!s) return LNSHIP_ENOINIT;
+    if (n < 0) return fail(LNSHIP_EINVAL, "negative length%s");
+    if (n == 0) return 0;
+    hipLaunchKernelGGL(k_from_f32_32, dim3(grid_for(n, 4)), dim3(k_block), 0, (hipStream_t)stream, src, dst, n);
+    LNSHIP_HIP(hipGetLastError());
+    return 0;
+}
+
+int lnship32_to_f32(const uint32_t *src, float *dst, int64_t n, void *stream) {
+    device_state *s = state();
+    if (!s) return LNSHIP_ENOINIT;
+    if (n < 0) return fail(LNSHIP_EINVAL, "negative length%s");
+    if (n == 0) return 0;
+    hipLaunchKernelGGL(k_to_f32_32, dim3(grid_for(n, 4)), dim3(k_block), 0, (hipStream_t)stream, src, dst, n);
+    LNSHIP_HIP(hipGetLastError());
+    return 0;
+}
+
+
+// Packs nslices weight slices, each M rows of K (row stride src_ld, slice
+// stride src_slice), into the k8-interleaved cache layout (Kp * M codes per
+// slice, Kp = K rounded up to 8).
+int lnship16_pack(const void *src, int src_is_f16, int64_t src_ld, int64_t src_slice, uint16_t *dst, int64_t K,
+                  int64_t M, int64_t nslices, void *stream) {
+    return pack_common(0, src, src_is_f16, src_ld, src_slice, dst, K, M, nslices, stream);
+}
+int lnship32_pack(const void *src, int src_is_f16, int64_t src_ld, int64_t src_slice, uint32_t *dst, int64_t K,
+                  int64_t M, int64_t nslices, void *stream) {
+    return pack_common(1, src, src_is_f16, src_ld, src_slice, dst, K, M, nslices, stream);
+}
+
+int lnship16_mul_mat(int mode, const lnship_mul_mat_args *a, void *stream) {
+    device_state *s = state();
+    if (!s) return LNSHIP_ENOINIT;
+    if (mode < 0 || mode > 3) return fail(LNSHIP_EINVAL, "unknown summation mode%s");
+    if (int rc = check_mm(a)) return rc;
+    if (a->M == 0 || a->N == 0) return 0;
+    const int64_t nslices = a->ne12 * a->ne13;
+    const int64_t kp = (a->K + 7) & ~(int64_t)7;
+    void *xs = nullptr;
+    if (int rc = scratch(s, (size_t)std::max<int64_t>(1, nslices * a->N * kp) * 2, &xs)) return rc;
+    hipStream_t st = (hipStream_t)stream;
+    if (kp > 0) {
+        dim3 g(grid_for(a->N * kp, 2), (unsigned)nslices);
+        hipLaunchKernelGGL(k_act<0>, g, dim3(k_block), 0, st, a->x, a->x_ld ? a->x_ld : a->K,
+                           a->x_slice ? a->x_slice : a->N * (a->x_ld ? a->x_ld : a->K), xs, a->N, a->K, kp,
+                           s->T.cvt16);
+        LNSHIP_HIP(hipGetLastError());
+    }
+    mm_args16 m{(const uint16_t *)a->w, (const uint16_t *)xs, a->dst, a->K, kp, a->M, a->N,
+                a->ne02, a->ne12, a->ne12 / a->ne02, a->ne13 / a->ne03, a->monte_seed};
+    switch (mode) {
+        case LNSHIP_BASE: return dispatch_mm16<LNSHIP_BASE>(m, s->T, nslices, st);
+        case LNSHIP_MONTE: return dispatch_mm16<LNSHIP_MONTE>(m, s->T, nslices, st);
+        case LNSHIP_LPVIP: return dispatch_mm16<LNSHIP_LPVIP>(m, s->T, nslices, st);
+        default: return dispatch_mm16<LNSHIP_SUM32>(m, s->T, nslices, st);
+    }
+}
+
+
+int lnship32_mul_mat(const lnship_mul_mat_args *a, void *stream) {
+    device_state *s = state();
+    if (!s) return LNSHIP_ENOINIT;
+    if (int rc = check_mm(a)) return rc;
+    if (a->M == 0 || a->N == 0) return 0;
+    const int64_t nslices = a->ne12 * a->ne13;
+    const int64_t kp = (a->K + 7) & ~(int64_t)7;
+    void *xs = nullptr;
+    if (int rc = scratch(s, (size_t)std::max<int64_t>(1, nslices * a->N * kp) * 4, &xs)) return rc;
+    hipStream_t st = (hipStream_t)stream;
+    if (kp > 0) {
+        dim3 g(grid_for(a->N * kp, 2), (unsigned)nslices);
+        hipLaunchKernelGGL(k_act<1>, g, dim3(k_block), 0, st, a->x, a->x_ld ? a->x_ld : a->K,
+                           a->x_slice ? a->x_slice : a->N * (a->x_ld ? a->x_ld : a->K), xs, a->N, a->K, kp,
+                           s->T.cvt16);
+        LNSHIP_HIP(hipGetLastError());
+    }
+    mm_args32 m{(const uint32_t *)a->w, (const uint32_t *)xs, a->dst, a->K, kp, a->M, a->N,
+                a->ne02, a->ne12, a->ne12 / a->ne02, a->ne13 / a->ne03};
+    if (m.N >= 4) return launch_mm32<4>(m, s->T, nslices, st);
+    return launch_mm32<1>(m, s->T, nslices, st);
+}
+
+
+int lnship16_rms_norm(int mode, const float *src, float *dst, int64_t ncols, int64_t nrows, float eps,
+                      uint16_t monte_seed, void *stream) {
+    device_state *s = state();
+    if (!s) return LNSHIP_ENOINIT;
+    if (mode < 0 || mode > 3 || ncols < 0 || nrows < 0) return fail(LNSHIP_EINVAL, "rms_norm: bad argument%s");
+    if (ncols == 0 || nrows == 0) return 0;
+    if ((nrows + 63) / 64 > 2147483647) return fail(LNSHIP_ERANGE, "rms_norm: too many rows%s");
+    hipStream_t st = (hipStream_t)stream;
+    switch (mode) {
+        case LNSHIP_BASE: return launch_rms16<LNSHIP_BASE>(src, dst, ncols, nrows, eps, monte_seed, s->T, st);
+        case LNSHIP_MONTE: return launch_rms16<LNSHIP_MONTE>(src, dst, ncols, nrows, eps, monte_seed, s->T, st);
+        case LNSHIP_LPVIP: return launch_rms16<LNSHIP_LPVIP>(src, dst, ncols, nrows, eps, monte_seed, s->T, st);
+        default: return launch_rms16<LNSHIP_SUM32>(src, dst, ncols, nrows, eps, monte_seed, s->T, st);
+    }
+}
+
+int lnship32_rms_norm(const float *src, float *dst, int64_t ncols, int64_t nrows, float eps, void *stream) {
+    device_state *s = state();
+    if (!s) return LNSHIP_ENOINIT;
+    if (ncols < 0 || nrows < 0) return fail(LNSHIP_EINVAL, "rms_norm: bad argument%s");
+    if (ncols == 0 || nrows == 0) return 0;
+    const int rb = rows_per_block<LNSHIP_SUM32>(ncols, 4);
+    if (rb < 1) return fail(LNSHIP_ERANGE, "rms_norm: row too long for LDS%s");
+    const int lds = k_lds_tab32 + (int)(rb * ncols * 4);
+    if (int rc = set_lds(k_rms32, lds)) return rc;
+    hipLaunchKernelGGL(k_rms32, dim3((unsigned)((nrows + rb - 1) / rb)), dim3(k_block), lds, (hipStream_t)stream, src,
+                       dst, ncols, nrows, rb, eps, s->T);
+    LNSHIP_HIP(hipGetLastError());
+    return 0;
+}
+
+
+
+int lnship16_soft_max(int mode, const lnship_soft_max_args *a, void *stream) {
+    device_state *s = state();
+    if (!s) return LNSHIP_ENOINIT;
+    if (mode < 0 || mode > 3) return fail(LNSHIP_EINVAL, "unknown summation mode%s");
+    if (int rc = check_sm(a)) return rc;
+    const int64_t nrows = a->src_ne[1] * a->src_ne[2] * a->src_ne[3];
+    if (a->src_ne[0] == 0 || nrows == 0) return 0;
+    sm_args m{a->src, a->mask, a->dst, a->src_ne[0], a->src_ne[1], a->src_ne[2], a->src_ne[3],
+              a->mask_ne[0], a->mask_ne[1], a->mask_ne[2], a->mask_ne[3], a->scale, a->monte_seed, 0};
+    hipStream_t st = (hipStream_t)stream;
+    switch (mode) {
+        case LNSHIP_BASE: return launch_sm16<LNSHIP_BASE>(m, nrows, s->T, st);
+        case LNSHIP_MONTE: return launch_sm16<LNSHIP_MONTE>(m, nrows, s->T, st);
+        case LNSHIP_LPVIP: return launch_sm16<LNSHIP_LPVIP>(m, nrows, s->T, st);
+        default: return launch_sm16<LNSHIP_SUM32>(m, nrows, s->T, st);
+    }
+}
+
+int lnship32_soft_max(const lnship_soft_max_args *a, void *stream) {
+    device_state *s = state();
+    if (!s) return LNSHIP_ENOINIT;
+    if (int rc = check_sm(a)) return rc;
+    const int64_t nrows = a->src_ne[1] * a->src_ne[2] * a->src_ne[3];
+    if (a->src_ne[0] == 0 || nrows == 0) return 0;
+    sm_args m{a->src, a->mask, a->dst, a->src_ne[0], a->src_ne[1], a->src_ne[2], a->src_ne[3],
+              a->mask_ne[0], a->mask_ne[1], a->mask_ne[2], a->mask_ne[3], a->scale, 0, 0};
+    m.rb = rows_per_block<LNSHIP_SUM32>(m.n, 4);
+    if (m.rb < 1) return fail(LNSHIP_ERANGE, "soft_max: row too long for LDS%s");
+    const int lds = k_lds_tab32 + (int)(m.rb * m.n * 4);
+    if (int rc = set_lds(k_softmax32, lds)) return rc;
+    hipLaunchKernelGGL(k_softmax32, dim3((unsigned)((nrows + m.rb - 1) / m.rb)), dim3(k_block), lds,
+                       (hipStream_t)stream, m, s->T);
+    LNSHIP_HIP(hipGetLastError());
+    return 0;
+}
+
+}  // extern "C"

@@ -1,0 +1,278 @@
+"""Python binding of the gfx950 LNS kernels (liblnship.so, include/lnship.h).
+
+Device memory and streams come from torch (torch.cuda tensors on ROCm); every
+call goes through the C ABI.  There is no CPU fallback: if liblnship.so is
+missing or no GPU is visible, the calls raise.
+"""
+import ctypes
+import os
+
+PKG_DIR = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+LIB_PATH = os.path.join(PKG_DIR, "liblnship.so")
+
+BASE, MONTE, LPVIP, SUM32 = 0, 1, 2, 3
+MODES = {"base": BASE, "monte": MONTE, "lpvip": LPVIP, "sum32": SUM32}
+
+_lib = None
+_ready = set()
+
+c_i64 = ctypes.c_int64
+c_p = ctypes.c_void_p
+
+
+class LnshipError(RuntimeError):
+    pass
+
+
+class MulMatArgs(ctypes.Structure):
+    _fields_ = [("w", c_p), ("x", c_p), ("dst", c_p), ("K", c_i64), ("M", c_i64), ("N", c_i64),
+                ("ne02", c_i64), ("ne03", c_i64), ("ne12", c_i64), ("ne13", c_i64),
+                ("x_ld", c_i64), ("x_slice", c_i64), ("monte_seed", ctypes.c_uint16)]
+
+
+class SoftMaxArgs(ctypes.Structure):
+    _fields_ = [("src", c_p), ("src_ne", c_i64 * 4), ("mask", c_p), ("mask_ne", c_i64 * 4),
+                ("scale", ctypes.c_float), ("dst", c_p), ("monte_seed", ctypes.c_uint16)]
+
+
+def build():
+    import subprocess
+    subprocess.check_call(["make", "-s", "-C", PKG_DIR])
+
+
+def lib():
+    """Loads liblnship.so (raises if it has not been built)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise LnshipError(f"{LIB_PATH} is missing: build it with __graft_entry__.build()")
+    L = ctypes.CDLL(LIB_PATH)
+    sigs = {
+        "lnship_init": (ctypes.c_int, []),
+        "lnship_last_error": (ctypes.c_char_p, []),
+        "lnship_version": (ctypes.c_char_p, []),
+        "lnship_host_table": (c_p, [ctypes.c_char_p, ctypes.POINTER(ctypes.c_size_t)]),
+        "lnship16_from_f32": (ctypes.c_int, [c_p, c_p, c_i64, c_p]),
+        "lnship16_to_f32": (ctypes.c_int, [c_p, c_p, c_i64, c_p]),
+        "lnship32_from_f32": (ctypes.c_int, [c_p, c_p, c_i64, c_p]),
+        "lnship32_to_f32": (ctypes.c_int, [c_p, c_p, c_i64, c_p]),
+        "lnship16_pack": (ctypes.c_int, [c_p, ctypes.c_int, c_i64, c_i64, c_p, c_i64, c_i64, c_i64, c_p]),
+        "lnship32_pack": (ctypes.c_int, [c_p, ctypes.c_int, c_i64, c_i64, c_p, c_i64, c_i64, c_i64, c_p]),
+        "lnship16_mul_mat": (ctypes.c_int, [ctypes.c_int, ctypes.POINTER(MulMatArgs), c_p]),
+        "lnship32_mul_mat": (ctypes.c_int, [ctypes.POINTER(MulMatArgs), c_p]),
+        "lnship16_rms_norm": (ctypes.c_int, [ctypes.c_int, c_p, c_p, c_i64, c_i64, ctypes.c_float,
+                                             ctypes.c_uint16, c_p]),
+        "lnship32_rms_norm": (ctypes.c_int, [c_p, c_p, c_i64, c_i64, ctypes.c_float, c_p]),
+        "lnship16_soft_max": (ctypes.c_int, [ctypes.c_int, ctypes.POINTER(SoftMaxArgs), c_p]),
+        "lnship32_soft_max": (ctypes.c_int, [ctypes.POINTER(SoftMaxArgs), c_p]),
+        "lnship16_mul_mat_draws": (ctypes.c_uint64, [ctypes.c_int, c_i64, c_i64, c_i64, c_i64, c_i64]),
+        "lnship16_soft_max_draws": (ctypes.c_uint64, [ctypes.c_int, c_i64, c_i64]),
+        "lnship16_rms_norm_draws": (ctypes.c_uint64, [ctypes.c_int, c_i64, c_i64]),
+        "lnship_lfsr_jump": (ctypes.c_uint16, [ctypes.c_uint16, ctypes.c_uint64]),
+    }
+    for name, (res, args) in sigs.items():
+        fn = getattr(L, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = L
+    return L
+
+
+def host_table(name, dtype):
+    """Host copy of one of the library's arithmetic tables (numpy; no GPU)."""
+    import numpy as np
+    n = ctypes.c_size_t(0)
+    p = lib().lnship_host_table(name.encode(), ctypes.byref(n))
+    if not p:
+        raise LnshipError(lib().lnship_last_error().decode())
+    buf = (ctypes.c_char * n.value).from_address(p)
+    return np.frombuffer(buf, dtype=dtype).copy()
+
+
+def check(rc):
+    if rc != 0:
+        raise LnshipError(f"lnship error {rc}: {lib().lnship_last_error().decode()}")
+
+
+def init(device=None):
+    """Uploads the tables to the current (or given) torch device."""
+    import torch
+    if not torch.cuda.is_available():
+        raise LnshipError("no GPU visible: the LNS kernels have no CPU fallback")
+    dev = torch.cuda.current_device() if device is None else device
+    with torch.cuda.device(dev):
+        if dev not in _ready:
+            check(lib().lnship_init())
+            _ready.add(dev)
+
+
+def _stream():
+    import torch
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def _p(t):
+    return ctypes.c_void_p(t.data_ptr()) if t is not None else None
+
+
+def kp(K):
+    return (K + 7) & ~7
+
+
+# ---- conversions -------------------------------------------------------------
+
+def from_f32_16(x):
+    import torch
+    init()
+    x = x.contiguous()
+    out = torch.empty(x.shape, dtype=torch.int16, device=x.device)
+    check(lib().lnship16_from_f32(_p(x), _p(out), x.numel(), _stream()))
+    return out
+
+
+def to_f32_16(v):
+    import torch
+    init()
+    v = v.contiguous()
+    out = torch.empty(v.shape, dtype=torch.float32, device=v.device)
+    check(lib().lnship16_to_f32(_p(v), _p(out), v.numel(), _stream()))
+    return out
+
+
+def from_f32_32(x):
+    import torch
+    init()
+    x = x.contiguous()
+    out = torch.empty(x.shape, dtype=torch.int32, device=x.device)
+    check(lib().lnship32_from_f32(_p(x), _p(out), x.numel(), _stream()))
+    return out
+
+
+def to_f32_32(v):
+    import torch
+    init()
+    v = v.contiguous()
+    out = torch.empty(v.shape, dtype=torch.float32, device=v.device)
+    check(lib().lnship32_to_f32(_p(v), _p(out), v.numel(), _stream()))
+    return out
+
+
+def pack16(w, dtype=None):
+    """w [..., M, K] (float32 or float16) -> k8-interleaved xlns16 cache [slices, Kp*M] (int16)."""
+    import torch
+    init()
+    w = w.contiguous()
+    K, M = w.shape[-1], w.shape[-2]
+    ns = w.numel() // max(1, K * M)
+    out = torch.empty((ns, kp(K) * M), dtype=torch.int16, device=w.device)
+    check(lib().lnship16_pack(_p(w), int(w.dtype == torch.float16), K, K * M, _p(out), K, M, ns, _stream()))
+    return out
+
+
+def pack32(w):
+    import torch
+    init()
+    w = w.contiguous()
+    K, M = w.shape[-1], w.shape[-2]
+    ns = w.numel() // max(1, K * M)
+    out = torch.empty((ns, kp(K) * M), dtype=torch.int32, device=w.device)
+    check(lib().lnship32_pack(_p(w), int(w.dtype == torch.float16), K, K * M, _p(out), K, M, ns, _stream()))
+    return out
+
+
+# ---- ops ---------------------------------------------------------------------
+
+def _mm_args(wp, x, out, K, M, ne02, ne03, seed):
+    N = x.shape[-2]
+    ne12 = x.shape[-3] if x.dim() >= 3 else 1
+    ne13 = x.shape[-4] if x.dim() >= 4 else 1
+    return MulMatArgs(_p(wp), _p(x), _p(out), K, M, N, ne02, ne03, ne12, ne13, 0, 0, seed)
+
+
+def mul_mat16(mode, wp, x, K, M, ne02=1, ne03=1, seed=7, out=None):
+    """wp: packed weights (pack16), x: [ne13, ne12, N, K] float32 -> [..., N, M] float32."""
+    import torch
+    init()
+    x = x.contiguous()
+    if out is None:
+        out = torch.empty(x.shape[:-1] + (M,), dtype=torch.float32, device=x.device)
+    a = _mm_args(wp, x, out, K, M, ne02, ne03, seed)
+    check(lib().lnship16_mul_mat(mode, ctypes.byref(a), _stream()))
+    return out
+
+
+def mul_mat32(wp, x, K, M, ne02=1, ne03=1, out=None):
+    import torch
+    init()
+    x = x.contiguous()
+    if out is None:
+        out = torch.empty(x.shape[:-1] + (M,), dtype=torch.float32, device=x.device)
+    a = _mm_args(wp, x, out, K, M, ne02, ne03, 0)
+    check(lib().lnship32_mul_mat(ctypes.byref(a), _stream()))
+    return out
+
+
+def rms_norm16(mode, x, eps, seed=7, out=None):
+    import torch
+    init()
+    x = x.contiguous()
+    if out is None:
+        out = torch.empty_like(x)
+    ncols = x.shape[-1]
+    check(lib().lnship16_rms_norm(mode, _p(x), _p(out), ncols, x.numel() // max(1, ncols), eps, seed, _stream()))
+    return out
+
+
+def rms_norm32(x, eps, out=None):
+    import torch
+    init()
+    x = x.contiguous()
+    if out is None:
+        out = torch.empty_like(x)
+    ncols = x.shape[-1]
+    check(lib().lnship32_rms_norm(_p(x), _p(out), ncols, x.numel() // max(1, ncols), eps, _stream()))
+    return out
+
+
+def _ne4(shape):
+    s = list(shape)[::-1]
+    return (c_i64 * 4)(*(s + [1] * (4 - len(s))))
+
+
+def _sm_args(x, mask, scale, out, seed):
+    ne = _ne4(x.shape)
+    mne = _ne4(mask.shape) if mask is not None else (c_i64 * 4)(*ne)
+    return SoftMaxArgs(_p(x), ne, _p(mask), mne, scale, _p(out), seed)
+
+
+def soft_max16(mode, x, mask=None, scale=1.0, seed=7, out=None):
+    import torch
+    init()
+    x = x.contiguous()
+    mask = mask.contiguous() if mask is not None else None
+    if out is None:
+        out = torch.empty_like(x)
+    a = _sm_args(x, mask, scale, out, seed)
+    check(lib().lnship16_soft_max(mode, ctypes.byref(a), _stream()))
+    return out
+
+
+def soft_max32(x, mask=None, scale=1.0, out=None):
+    import torch
+    init()
+    x = x.contiguous()
+    mask = mask.contiguous() if mask is not None else None
+    if out is None:
+        out = torch.empty_like(x)
+    a = _sm_args(x, mask, scale, out, 0)
+    check(lib().lnship32_soft_max(ctypes.byref(a), _stream()))
+    return out
+
+
+def mul_mat_draws(mode, K, M, N, ne12=1, ne13=1):
+    return lib().lnship16_mul_mat_draws(mode, K, M, N, ne12, ne13)
+
+
+def lfsr_jump(state, n):
+    return lib().lnship_lfsr_jump(state, n)
