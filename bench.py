@@ -1,0 +1,213 @@
+"""Benchmark: SmolLM2-135M-shape LNS16 decoder on one MI355X.
+
+Workload: 30 layers, d_model 576, 9 / 3 heads of 64, SwiGLU 1536, vocab 49152,
+random-init N(0, 0.02) weights stored as xlns16, LNS16 sum32 mode; a
+128-token uniform-random prompt, then greedy decode.  A step is one decoded
+token (the whole graph: 271 mul_mats, 61 rms_norms, 30 soft_maxes and the
+elementwise ops), replayed from a captured HIP graph; the next token is the
+device-side argmax, so the timed loop never waits for the host.
+
+Prints one JSON line with decode tok/s (value), prefill tok/s, weight
+mul_mat GMAC/s, the roofline of the dominant kernel (the decode GEMV) and the
+single-threaded CPU oracle timed on this host on a bounded sample.
+"""
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "xlns-ggml-backend_amd"))
+
+METRIC = "LNS16 mul_mat GMAC/s (sum32) + tok/s prefill/decode, SmolLM2-135M shape"
+HBM_PEAK_GBS = 8000.0
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=120)
+    ap.add_argument("--warmup", type=int, default=8)
+    ap.add_argument("--mode", default="sum32", choices=["base", "monte", "lpvip", "sum32"])
+    ap.add_argument("--prompt", type=int, default=128)
+    ap.add_argument("--cpu-tokens", type=int, default=3, help="decode tokens of the CPU baseline sample")
+    ap.add_argument("--no-cpu", action="store_true")
+    return ap.parse_args()
+
+
+def gemv_roofline(model, ln, torch):
+    """Times every mul_mat launch of one eager decode step with HIP events on
+    the launch stream; returns (bytes per launch, avg launch us, launches)."""
+    c = model.cfg
+    events = []
+    orig = model._mm
+
+    def timed_mm(w, x_ptr, dst_ptr, K, M, N, **kw):
+        s = torch.cuda.Event(enable_timing=True)
+        e = torch.cuda.Event(enable_timing=True)
+        s.record()
+        orig(w, x_ptr, dst_ptr, K, M, N, **kw)
+        e.record()
+        ne12 = kw.get("ne12", 1)
+        # algorithmic bytes: xlns16 weights once per weight slice, F32 in / out
+        ne02 = kw.get("ne02", 1)
+        events.append((s, e, 2 * K * M * ne02 + 4 * K * N * ne12 + 4 * M * N * ne12))
+
+    model._mm = timed_mm
+    try:
+        tok = model._buf("rtok", 1, torch.int32)
+        pos = model._buf("rpos", 1, torch.int32)
+        tok.fill_(1)
+        pos.fill_(model.n_past)
+        from lnship.llama import n_kv_for
+        model.forward(1, tok, pos, n_kv_for(model.n_past + 1, c.n_ctx))
+        torch.cuda.synchronize()
+    finally:
+        model._mm = orig
+    total_us = sum(s.elapsed_time(e) * 1e3 for s, e, _ in events)
+    total_b = sum(b for _, _, b in events)
+    n = len(events)
+    return total_b / n, total_us / n, n
+
+
+def cpu_baseline(cfg, weights, mode, n_tokens):
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import oracle_lib as O
+    from llama_oracle import LlamaOracle16
+    m = O.MODES[mode]
+    cpu = LlamaOracle16(cfg, weights, m)
+    cpu.eval([1, 2])
+    t0 = time.perf_counter()
+    tok = 3
+    for _ in range(n_tokens):
+        logits = cpu.eval([tok])
+        tok = int(logits.argmax())
+    dt = time.perf_counter() - t0
+    return {"value": round(n_tokens / dt, 4), "unit": "tok/s", "cores": 1, "kind": "port",
+            "sample": f"{n_tokens} decode tokens after a 2-token prompt, full SmolLM2-135M shape, "
+                      f"{mode}, single-threaded C oracle ({dt:.1f} s)",
+            "cpu": _cpu_name()}
+
+
+def _cpu_name():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
+              f"(multi-GPU sharding is a design note, not part of this build)", file=sys.stderr)
+        sys.exit(2)
+    import numpy as np
+    import torch
+    import lnship
+    from lnship import llama
+
+    torch.cuda.set_device(0)
+    lnship.init()
+    cfg = llama.SMOLLM2_135M
+    mode = lnship.MODES[args.mode]
+    t0 = time.perf_counter()
+    weights = llama.synthetic_weights(cfg, seed=1234, std=0.02)
+    model = llama.LlamaLNS16(cfg, weights, mode=mode)
+    torch.cuda.synchronize()
+    t_setup = time.perf_counter() - t0
+
+    rng = np.random.default_rng(2024)
+    prompt = [int(t) for t in rng.integers(0, cfg.n_vocab, args.prompt)]
+    # prefill (timed once; the first call pays the one-time kernel setup, so
+    # run it on a scratch model state first)
+    model.eval(prompt[:8])
+    model.n_past = 0
+    torch.cuda.synchronize()
+    tp = time.perf_counter()
+    logits = model.eval(prompt)
+    torch.cuda.synchronize()
+    t_prefill = time.perf_counter() - tp
+
+    tok_dev = torch.argmax(logits).to(torch.int32).reshape(1)
+    use_graph = mode != lnship.MONTE
+
+    def step():
+        nonlocal tok_dev
+        if use_graph:
+            out = _graph_step(model, tok_dev)
+        else:
+            out = model.eval([int(tok_dev.item())])
+        tok_dev = torch.argmax(out).to(torch.int32).reshape(1)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    ts = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    t_decode = time.perf_counter() - ts
+
+    decode_tok_s = args.steps / t_decode
+    macs_per_token = cfg.n_layer * (
+        (cfg.n_head + 2 * cfg.n_head_kv) * cfg.head_dim * cfg.n_embd + cfg.n_embd * cfg.n_head * cfg.head_dim +
+        3 * cfg.n_ff * cfg.n_embd) + cfg.n_vocab * cfg.n_embd
+    b_launch, us_launch, n_launch = gemv_roofline(model, lnship, torch)
+    achieved = b_launch / (us_launch * 1e-6) / 1e9
+    out = {
+        "metric": METRIC,
+        "value": round(decode_tok_s, 3),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(t_decode / args.steps * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "xlns16",
+        "data": "synthetic: splitmix64/Box-Muller N(0,0.02) weights stored as xlns16, uniform token ids",
+        "config": {"workload": "SmolLM2-135M-shape decoder, LNS16 %s, %d-token prompt then greedy decode "
+                               "(one decoded token per step)" % (args.mode, args.prompt),
+                   "mode": args.mode, "prompt_tokens": args.prompt, "n_kv": llama.n_kv_for(model.n_past, cfg.n_ctx),
+                   "graph": "hipGraph per decode step" if use_graph else "eager"},
+        "prefill_tok_s": round(args.prompt / t_prefill, 3),
+        "mul_mat_gmacs": round(macs_per_token * decode_tok_s / 1e9, 4),
+        "weight_macs_per_token": macs_per_token,
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 3), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 6), "traffic": None,
+                     "kernel": "k_mm16 (decode mul_mat, %s)" % args.mode,
+                     "launches_per_token": n_launch, "avg_launch_us": round(us_launch, 3),
+                     "bytes_per_launch": int(b_launch)},
+        "reference_published": {"rtx2050_sum32_decode_tok_s": 7.31,
+                                "source": "experiments/layer-by-layer/CPU-vs-GPU.md:21 (Q4_K_M, 5-token prompt)"},
+        "setup_s": round(t_setup, 2),
+    }
+    if not args.no_cpu:
+        out["cpu_baseline"] = cpu_baseline(cfg, weights, args.mode, args.cpu_tokens)
+    print(json.dumps(out), flush=True)
+
+
+def _graph_step(model, tok_dev):
+    """decode_graph with the token already on the device."""
+    import torch
+    from lnship.llama import n_kv_for
+    n_kv = n_kv_for(model.n_past + 1, model.cfg.n_ctx)
+    if n_kv not in model._graphs:
+        return model.decode_graph(int(tok_dev.item()), n_kv)
+    model._buf("gtok", 1, torch.int32).copy_(tok_dev)
+    model._buf("gpos", 1, torch.int32).fill_(model.n_past)
+    g, out = model._graphs[n_kv]
+    g.replay()
+    model.n_past += 1
+    return out
+
+
+if __name__ == "__main__":
+    main()

@@ -86,8 +86,13 @@ typedef struct lnship_mul_mat_args {
     float *dst;
     int64_t K, M, N;
     int64_t ne02, ne03, ne12, ne13;
-    int64_t x_ld, x_slice;   /* 0 = contiguous (K and N*K) */
+    int64_t x_ld, x_slice;     /* 0 = contiguous (K and N*K) */
     uint16_t monte_seed;
+    /* optional strides, 0 = contiguous: w_mstride is the M the weight slice
+     * was packed with (>= M, so a cache can grow in M), w_slice the codes
+     * between weight slices, dst_ld / dst_slice the floats between output
+     * rows n / activation slices */
+    int64_t w_mstride, w_slice, dst_ld, dst_slice;
 } lnship_mul_mat_args;
 
 int lnship16_mul_mat(int mode, const lnship_mul_mat_args *args, void *stream);
@@ -116,6 +121,38 @@ typedef struct lnship_soft_max_args {
 
 int lnship16_soft_max(int mode, const lnship_soft_max_args *args, void *stream);
 int lnship32_soft_max(const lnship_soft_max_args *args, void *stream);
+
+/* ---- elementwise ops of the Llama graph (F32 in / out, xlns16 inside) ----
+ * lns_add / lns_mul (src/lns-ops.cpp:468-530) with b repeated every nb
+ * elements, lns_swiglu (:812-868), lns_get_rows (:1003-1050) from a packed
+ * xlns16 table (row m of a lnship16_pack'ed K x M matrix, decoded to F32). */
+int lnship16_add(const float *a, const float *b, int64_t n, int64_t nb, float *dst, void *stream);
+int lnship16_mul(const float *a, const float *b, int64_t n, int64_t nb, float *dst, void *stream);
+int lnship16_swiglu(const float *gate, int64_t gate_ld, const float *up, int64_t up_ld, float *dst,
+                    int64_t ncols, int64_t nrows, void *stream);
+int lnship16_get_rows_packed(const uint16_t *w, int64_t K, int64_t M, const int32_t *rows, int64_t nrows,
+                             float *dst, void *stream);
+/* lns_rope (src/lns-ops.cpp:1199-1281): x rows [ntok][nhead][ne0] (token
+ * stride x_ld); cos_sin holds per position p and pair j the floats
+ * (cos, sin) at cos_sin[(p * (n_dims/2) + j) * 2]; pos[ntok] on the device.
+ * When cache is non-null the rotated rows are also rounded to IEEE half,
+ * converted to xlns16 and stored (no F32 dst) into a packed cache: head h,
+ * position p, dim d at h * cache_slice + ((d/8) * cache_m + p) * 8 + d % 8
+ * (K cache: kq's weight operand) or, with cache_transposed, at
+ * h * cache_slice + ((p/8) * ne0 + d) * 8 + p % 8 (V cache, kqv's). */
+int lnship16_rope(const float *x, int64_t x_ld, const int32_t *pos, int64_t ntok, int64_t nhead, int64_t ne0,
+                  int n_dims, int neox, const float *cos_sin, float *dst, void *stream);
+int lnship16_store_kv(const float *x, int64_t x_ld, const int32_t *pos, int64_t ntok, int64_t nhead, int64_t ne0,
+                      int rope_n_dims, const float *cos_sin, uint16_t *cache, int64_t cache_m,
+                      int64_t cache_slice, int cache_transposed, void *stream);
+/* Host: the (cos, sin) floats lns_rope uses for positions 0..n_pos-1 (the
+ * float recurrence t *= powf(freq_base, -2/n_dims) per pair, cosf / sinf;
+ * src/lns-ops.cpp:1225-1247, cuda/lns-cuda-ops.cpp:223-240), laid out as
+ * out[(p * (n_dims/2) + j) * 2 + {0, 1}].  No GPU needed. */
+int lnship_rope_table(float freq_base, int n_dims, int64_t n_pos, float *out);
+/* mask[t][j] = 0 if j <= pos0 + t else -inf (llama's causal KQ mask),
+ * t < ntok, j < n_kv; pos0 read from the device */
+int lnship_causal_mask(const int32_t *pos0, int64_t ntok, int64_t n_kv, float *mask, void *stream);
 
 /* ---- Monte draw accounting (kernel_set::*_draws, :97-100) --------------- */
 uint64_t lnship16_mul_mat_draws(int mode, int64_t K, int64_t M, int64_t N, int64_t ne12, int64_t ne13);

@@ -52,6 +52,7 @@ static float    g_rev16[1u << 16];   /* xlns16 -> float */
 static int16_t  g_sb16[X16_ESSZER + 1];
 static int16_t  g_db16[X16_ESSZER + 1];
 static uint16_t g_exp16[1u << 16];
+static uint16_t g_sig16[1u << 16];
 static int      g_ready = 0;
 
 static inline float f32_from_bits(uint32_t b) { float f; memcpy(&f, &b, 4); return f; }
@@ -162,6 +163,11 @@ uint16_t lno16_add(uint16_t x, uint16_t y) {
 uint16_t lno16_sub(uint16_t x, uint16_t y) { return lno16_add(x, (uint16_t)(y ^ X16_SIGN)); }
 
 uint16_t lno16_exp(uint16_t x) { return g_exp16[x]; }
+
+/* xlns16_silu: x * sigmoid(x), the sigmoid through the bucketed conversion
+ * table.  Pinned by the eight swiglu values of unit-tests-lns16-base.txt
+ * (test-lns-backend.cpp:554-580 inputs); the alternatives miss one to four. */
+uint16_t lno16_silu(uint16_t x) { return lno16_mul(x, g_sig16[x]); }
 
 uint16_t lno16_from_f32(float x) { return g_cvt16[bits_from_f32(x) >> 15]; }
 float    lno16_to_f32(uint16_t v) { return g_rev16[v]; }
@@ -721,6 +727,50 @@ void lno32_rms_norm(const float *src, int64_t ncols, int64_t nrows, float eps, f
 }
 
 /* ======================================================================
+ * Elementwise ops of the Llama graph (F32 in, F32 out, LNS inside).
+ * ==================================================================== */
+
+/* lns_add / lns_mul (src/lns-ops.cpp:468-530): b broadcast along rows
+ * (b has nb elements, index i % nb) */
+void lno16_add_f32(const float *a, const float *b, int64_t n, int64_t nb, float *dst) {
+    for (int64_t i = 0; i < n; i++)
+        dst[i] = lno16_to_f32(lno16_add(lno16_from_f32(a[i]), lno16_from_f32(b[i % nb])));
+}
+void lno16_mul_f32(const float *a, const float *b, int64_t n, int64_t nb, float *dst) {
+    for (int64_t i = 0; i < n; i++)
+        dst[i] = lno16_to_f32(lno16_mul(lno16_from_f32(a[i]), lno16_from_f32(b[i % nb])));
+}
+
+/* lns_swiglu (src/lns-ops.cpp:812-868): silu(gate) * up */
+void lno16_swiglu_f32(const float *gate, const float *up, int64_t n, float *dst) {
+    for (int64_t i = 0; i < n; i++)
+        dst[i] = lno16_to_f32(lno16_mul(lno16_silu(lno16_from_f32(gate[i])), lno16_from_f32(up[i])));
+}
+
+/* lns_rope (src/lns-ops.cpp:1199-1281), normal or NEOX pairs; x is
+ * [ntok][nhead][ne0], pos[ntok]; cos/sin from the float recurrence
+ * t *= theta_scale of the reference, theta_scale = powf(base, -2/n_dims) */
+void lno16_rope_f32(const float *x, const int32_t *pos, int64_t ntok, int64_t nhead, int64_t ne0,
+                    int n_dims, int neox, float freq_base, float *dst) {
+    const float theta_scale = powf(freq_base, -2.0f / (float)n_dims);
+    for (int64_t t = 0; t < ntok; t++)
+    for (int64_t h = 0; h < nhead; h++) {
+        const float *xr = x + (t * nhead + h) * ne0;
+        float *yr = dst + (t * nhead + h) * ne0;
+        float th = (float)pos[t];
+        for (int64_t j = 0; j < n_dims; j += 2) {
+            const uint16_t c = lno16_from_f32(cosf(th)), sn = lno16_from_f32(sinf(th));
+            const int64_t i0 = neox ? j / 2 : j, i1 = neox ? j / 2 + n_dims / 2 : j + 1;
+            const uint16_t x0 = lno16_from_f32(xr[i0]), x1 = lno16_from_f32(xr[i1]);
+            yr[i0] = lno16_to_f32(lno16_sub(lno16_mul(x0, c), lno16_mul(x1, sn)));
+            yr[i1] = lno16_to_f32(lno16_add(lno16_mul(x0, sn), lno16_mul(x1, c)));
+            th *= theta_scale;
+        }
+        for (int64_t j = n_dims; j < ne0; j++) yr[j] = lno16_to_f32(lno16_from_f32(xr[j]));
+    }
+}
+
+/* ======================================================================
  * Table construction.
  * ==================================================================== */
 /* xlns16_exp table: the direct (untabled) conversion of expf of the decoded
@@ -746,6 +796,10 @@ int lno_init(void) {
         g_db16m[d] = (int32_t)floorl(dbx);
     }
     for (uint32_t i = 0; i < (1u << 16); i++) g_exp16[i] = exp16_entry((uint16_t)i);
+    for (uint32_t i = 0; i < (1u << 16); i++) {
+        float v = g_rev16[i];
+        g_sig16[i] = g_cvt16[bits_from_f32(1.0f / (1.0f + expf(-v))) >> 15];
+    }
 
     for (int i = 0; i <= X32_SB_N; i++) g_sb32a[i] = (int32_t)truncl(sb32_exact((long double)i * (1 << X32_SB_SH)));
     for (int i = 0; i <= X32_SB_FN; i++)

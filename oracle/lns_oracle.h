@@ -55,6 +55,7 @@ uint16_t lno16_sub(uint16_t a, uint16_t b);
 uint16_t lno16_sqrt(uint16_t a);
 uint16_t lno16_recip(uint16_t a);
 uint16_t lno16_exp(uint16_t a);
+uint16_t lno16_silu(uint16_t a);
 int      lno16_gt(uint16_t a, uint16_t b);
 /* exported tables (for tests): cvt[1<<17], sb/db[1281], exp[1<<16] */
 const uint16_t *lno16_cvt_table(void);
@@ -114,6 +115,12 @@ void lno16_mul_mat_f32w(int mode, const float *w, const float *x, float *dst,
 void lno16_soft_max(int mode, const float *src, const int64_t ne[4], const float *mask,
                     const int64_t mne[4], float scale, float *dst);
 void lno16_rms_norm(int mode, const float *src, int64_t ncols, int64_t nrows, float eps, float *dst);
+
+void lno16_add_f32(const float *a, const float *b, int64_t n, int64_t nb, float *dst);
+void lno16_mul_f32(const float *a, const float *b, int64_t n, int64_t nb, float *dst);
+void lno16_swiglu_f32(const float *gate, const float *up, int64_t n, float *dst);
+void lno16_rope_f32(const float *x, const int32_t *pos, int64_t ntok, int64_t nhead, int64_t ne0,
+                    int n_dims, int neox, float freq_base, float *dst);
 
 void lno32_mul_mat(const float *w, const float *x, float *dst,
                    int64_t K, int64_t M, int64_t N,

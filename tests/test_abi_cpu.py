@@ -92,3 +92,22 @@ def test_calls_without_init_fail_loudly(lnship):
     L = lnship.lib()
     rc = L.lnship16_from_f32(None, None, 16, None)
     assert rc != 0
+
+
+def test_rope_table_uses_the_float_recurrence(lnship):
+    # lns_rope (src/lns-ops.cpp:1225-1247): t *= powf(base, -2/n_dims), cosf / sinf
+    libm = ctypes.CDLL("libm.so.6")
+    for fn in ("cosf", "sinf", "powf"):
+        getattr(libm, fn).restype = ctypes.c_float
+    libm.cosf.argtypes = libm.sinf.argtypes = [ctypes.c_float]
+    libm.powf.argtypes = [ctypes.c_float, ctypes.c_float]
+    n_dims, n_pos = 64, 40
+    got = np.empty(n_pos * n_dims, np.float32)
+    assert lnship.lib().lnship_rope_table(10000.0, n_dims, n_pos, ctypes.c_void_p(got.ctypes.data)) == 0
+    ts = np.float32(libm.powf(10000.0, np.float32(-2.0) / np.float32(n_dims)))
+    for p in range(n_pos):
+        t = np.float32(p)
+        for j in range(n_dims // 2):
+            assert got[(p * 32 + j) * 2] == np.float32(libm.cosf(t))
+            assert got[(p * 32 + j) * 2 + 1] == np.float32(libm.sinf(t))
+            t = np.float32(t * ts)

@@ -1,0 +1,63 @@
+"""GPU parity of the whole decoder: lnship.llama against the CPU oracle of the
+same graph (tests/llama_oracle.py), bit-exact logits after prefill and after
+each decode step, for every summation mode (BASELINE configs 2 and 3 at a
+small size; the full SmolLM2 shape is exercised by bench.py)."""
+import numpy as np
+import pytest
+
+import oracle_lib as O
+from llama_oracle import LlamaOracle16
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+
+def tiny(n_ctx=512):
+    from lnship.llama import LlamaConfig
+    return LlamaConfig(n_layer=2, n_embd=64, n_head=4, n_head_kv=2, head_dim=16, n_ff=96, n_vocab=300, n_ctx=n_ctx)
+
+
+def same(got, want, what):
+    g = np.ascontiguousarray(got, np.float32).view(np.uint32)
+    w = np.ascontiguousarray(want, np.float32).view(np.uint32)
+    bad = np.nonzero(g != w)[0]
+    assert bad.size == 0, f"{what}: {bad.size}/{g.size} logits differ, first at {bad[0]}"
+
+
+@pytest.mark.parametrize("mode", ["base", "monte", "lpvip", "sum32"])
+def test_prefill_and_decode(mode):
+    from lnship import llama
+    cfg = tiny()
+    w = llama.synthetic_weights(cfg, seed=99, std=0.2)
+    m = O.MODES[mode]
+    rng = np.random.default_rng(5)
+    prompt = [int(t) for t in rng.integers(0, cfg.n_vocab, 9)]
+    print(f"\n[llama] {mode} prefill 9", flush=True)
+    gpu = llama.LlamaLNS16(cfg, w, mode=m)
+    cpu = LlamaOracle16(cfg, w, m)
+    same(gpu.eval(prompt).cpu().numpy(), cpu.eval(prompt), f"{mode} prefill")
+    tok = int(rng.integers(0, cfg.n_vocab))
+    for step in range(3):
+        print(f"[llama] {mode} decode {step}", flush=True)
+        same(gpu.eval([tok]).cpu().numpy(), cpu.eval([tok]), f"{mode} decode {step}")
+        tok = (tok * 7 + 3) % cfg.n_vocab
+    if m != O.MONTE:
+        for step in range(3):
+            print(f"[llama] {mode} graph decode {step}", flush=True)
+            out = gpu.decode_graph(tok).cpu().numpy()
+            same(out, cpu.eval([tok]), f"{mode} graph decode {step}")
+            tok = (tok * 5 + 1) % cfg.n_vocab
+    assert O.monte_get() == gpu.lfsr or m != O.MONTE
+
+
+def test_kv_view_grows_past_256():
+    from lnship import llama
+    cfg = tiny()
+    w = llama.synthetic_weights(cfg, seed=7, std=0.2)
+    prompt = [i % cfg.n_vocab for i in range(254)]
+    print("\n[llama] sum32 prompt 254 then decode across n_kv 256 -> 512", flush=True)
+    gpu = llama.LlamaLNS16(cfg, w, mode=O.SUM32)
+    cpu = LlamaOracle16(cfg, w, O.SUM32)
+    same(gpu.eval(prompt).cpu().numpy(), cpu.eval(prompt), "prefill 254")
+    for step, tok in enumerate((3, 11, 17)):
+        same(gpu.decode_graph(tok).cpu().numpy(), cpu.eval([tok]), f"decode {254 + step}")

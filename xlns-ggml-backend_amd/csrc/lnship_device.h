@@ -21,6 +21,7 @@ struct dev_tables {
     const int16_t *gauss16;
     const int32_t *gauss16m;
     const uint16_t *exp16;
+    const uint16_t *sig16;
     const int32_t *tab32;
     const uint16_t *lfsr_seq;
     const uint16_t *lfsr_log;

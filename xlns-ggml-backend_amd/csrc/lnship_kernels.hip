@@ -317,6 +317,7 @@ struct mm_args16 {
     float *dst;
     int64_t K, kp, M, N;
     int64_t ne02, ne12, r2, r3;
+    int64_t w_mstride, w_slice, dst_ld, dst_slice;
     uint32_t seed;
 };
 
@@ -333,9 +334,9 @@ __global__ __launch_bounds__(k_block) void k_mm16(mm_args16 a, dev_tables T) {
     const int64_t i12 = z % a.ne12, i13 = z / a.ne12;
     const int nc = (int)min<int64_t>(NC, a.N - n0);
 
-    const uint16_t *ws = a.w + ((i13 / a.r3) * a.ne02 + i12 / a.r2) * a.kp * a.M + m * 8;
+    const uint16_t *ws = a.w + ((i13 / a.r3) * a.ne02 + i12 / a.r2) * a.w_slice + m * 8;
     const uint16_t *xs = a.x + (z * a.N + n0) * a.kp;
-    const int64_t wstride = a.M * 8;   // between consecutive groups of 8 k
+    const int64_t wstride = a.w_mstride * 8;   // between consecutive groups of 8 k
 
     uint32_t acc[NC], st[NC];
 #pragma unroll
@@ -380,10 +381,10 @@ __global__ __launch_bounds__(k_block) void k_mm16(mm_args16 a, dev_tables T) {
         for (int64_t g = 1; g < full; g++) group(g, false, 0, 8);
         if (full > 0 && tail > 0) group(full, false, 0, tail);
     }
-    float *ds = a.dst + (z * a.N + n0) * a.M + m;
+    float *ds = a.dst + z * a.dst_slice + n0 * a.dst_ld + m;
 #pragma unroll
     for (int j = 0; j < NC; j++) {
-        if (j < nc) ds[(int64_t)j * a.M] = a.K == 0 ? T.rev16[0] : T.rev16[R.finish(acc[j]) & 0xffffu];
+        if (j < nc) ds[(int64_t)j * a.dst_ld] = a.K == 0 ? T.rev16[0] : T.rev16[R.finish(acc[j]) & 0xffffu];
     }
 }
 
@@ -394,6 +395,7 @@ struct mm_args32 {
     float *dst;
     int64_t K, kp, M, N;
     int64_t ne02, ne12, r2, r3;
+    int64_t w_mstride, w_slice, dst_ld, dst_slice;
 };
 
 template <int NC>
@@ -407,9 +409,9 @@ __global__ __launch_bounds__(k_block) void k_mm32(mm_args32 a, dev_tables T) {
     const int64_t z = blockIdx.z;
     const int64_t i12 = z % a.ne12, i13 = z / a.ne12;
     const int nc = (int)min<int64_t>(NC, a.N - n0);
-    const uint32_t *ws = a.w + ((i13 / a.r3) * a.ne02 + i12 / a.r2) * a.kp * a.M + m * 8;
+    const uint32_t *ws = a.w + ((i13 / a.r3) * a.ne02 + i12 / a.r2) * a.w_slice + m * 8;
     const uint32_t *xs = a.x + (z * a.N + n0) * a.kp;
-    const int64_t wstride = a.M * 8;
+    const int64_t wstride = a.w_mstride * 8;
     uint32_t acc[NC];
 #pragma unroll
     for (int j = 0; j < NC; j++) acc[j] = 0;
@@ -438,10 +440,10 @@ __global__ __launch_bounds__(k_block) void k_mm32(mm_args32 a, dev_tables T) {
             }
         }
     }
-    float *ds = a.dst + (z * a.N + n0) * a.M + m;
+    float *ds = a.dst + z * a.dst_slice + n0 * a.dst_ld + m;
 #pragma unroll
     for (int j = 0; j < NC; j++)
-        if (j < nc) ds[(int64_t)j * a.M] = a.K == 0 ? 0.0f : x32_to_f32(acc[j]);
+        if (j < nc) ds[(int64_t)j * a.dst_ld] = a.K == 0 ? 0.0f : x32_to_f32(acc[j]);
 }
 
 // ---- RMS_NORM -------------------------------------------------------------------
@@ -642,6 +644,116 @@ __global__ __launch_bounds__(k_block) void k_softmax32(sm_args a, dev_tables T) 
     }
 }
 
+// ---- elementwise ops of the Llama graph ---------------------------------------
+
+template <int OP>   // 0 add, 1 mul
+__global__ void k_binary16(const float *__restrict__ a, const float *__restrict__ b, int64_t n, int64_t nb,
+                           float *__restrict__ dst, dev_tables T) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)blockDim.x * gridDim.x) {
+        const uint32_t x = x16_from_f32(T.cvt16, a[i]), y = x16_from_f32(T.cvt16, b[i % nb]);
+        dst[i] = T.rev16[OP == 0 ? x16_add_g(T.gauss16, x, y) : x16_mul(x, y)];
+    }
+}
+
+__global__ void k_swiglu16(const float *__restrict__ g, int64_t g_ld, const float *__restrict__ u, int64_t u_ld,
+                           float *__restrict__ dst, int64_t ncols, int64_t nrows, dev_tables T) {
+    const int64_t n = ncols * nrows;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)blockDim.x * gridDim.x) {
+        const int64_t r = i / ncols, c = i - r * ncols;
+        const uint32_t gv = x16_from_f32(T.cvt16, g[r * g_ld + c]);
+        const uint32_t uv = x16_from_f32(T.cvt16, u[r * u_ld + c]);
+        dst[i] = T.rev16[x16_mul(x16_mul(gv, T.sig16[gv]), uv)];
+    }
+}
+
+__global__ void k_get_rows_packed(const uint16_t *__restrict__ w, int64_t K, int64_t M, const int32_t *__restrict__ rows,
+                                  int64_t nrows, float *__restrict__ dst, const float *__restrict__ rev) {
+    const int64_t n = nrows * K;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)blockDim.x * gridDim.x) {
+        const int64_t r = i / K, k = i - r * K;
+        const int64_t m = rows[r];
+        dst[i] = rev[w[((k >> 3) * M + m) * 8 + (k & 7)]];
+    }
+}
+
+// one thread per rotated pair (or passthrough element)
+__device__ __forceinline__ void rope_pair(const float *xr, int64_t j, int n_dims, int neox, const float *cs,
+                                          const dev_tables &T, int64_t &i0, int64_t &i1, uint32_t &r0, uint32_t &r1) {
+    const uint32_t c = x16_from_f32(T.cvt16, cs[j * 2]), sn = x16_from_f32(T.cvt16, cs[j * 2 + 1]);
+    i0 = neox ? j : 2 * j;
+    i1 = neox ? j + n_dims / 2 : 2 * j + 1;
+    const uint32_t x0 = x16_from_f32(T.cvt16, xr[i0]), x1 = x16_from_f32(T.cvt16, xr[i1]);
+    r0 = x16_add_g(T.gauss16, x16_mul(x0, c), x16_mul(x1, sn) ^ k16_sign);
+    r1 = x16_add_g(T.gauss16, x16_mul(x0, sn), x16_mul(x1, c));
+}
+
+__global__ void k_rope16(const float *__restrict__ x, int64_t x_ld, const int32_t *__restrict__ pos, int64_t ntok,
+                         int64_t nhead, int64_t ne0, int n_dims, int neox, const float *__restrict__ cos_sin,
+                         float *__restrict__ dst, dev_tables T) {
+    const int64_t half = n_dims / 2, per = half + (ne0 - n_dims);
+    const int64_t n = ntok * nhead * per;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)blockDim.x * gridDim.x) {
+        const int64_t row = i / per, j = i - row * per;
+        const int64_t t = row / nhead, h = row - t * nhead;
+        const float *xr = x + t * x_ld + h * ne0;
+        float *yr = dst + (t * nhead + h) * ne0;
+        if (j < half) {
+            int64_t i0, i1;
+            uint32_t r0, r1;
+            rope_pair(xr, j, n_dims, neox, cos_sin + (int64_t)pos[t] * half * 2, T, i0, i1, r0, r1);
+            yr[i0] = T.rev16[r0];
+            yr[i1] = T.rev16[r1];
+        } else {
+            const int64_t i0 = n_dims + (j - half);
+            yr[i0] = T.rev16[x16_from_f32(T.cvt16, xr[i0])];
+        }
+    }
+}
+
+// F32 value -> IEEE half (round to nearest even) -> F32 -> xlns16, as the
+// KV cache stores and reads it
+__device__ __forceinline__ uint16_t kv_code(const dev_tables &T, float v) {
+    return (uint16_t)x16_from_f32(T.cvt16, __half2float(__float2half_rn(v)));
+}
+
+__global__ void k_store_kv16(const float *__restrict__ x, int64_t x_ld, const int32_t *__restrict__ pos, int64_t ntok,
+                             int64_t nhead, int64_t ne0, int rope_n_dims, const float *__restrict__ cos_sin,
+                             uint16_t *__restrict__ cache, int64_t cache_m, int64_t cache_slice, int transposed,
+                             dev_tables T) {
+    const int64_t n = ntok * nhead * ne0;
+    const int64_t half = rope_n_dims / 2;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)blockDim.x * gridDim.x) {
+        const int64_t row = i / ne0, d = i - row * ne0;
+        const int64_t t = row / nhead, h = row - t * nhead;
+        const float *xr = x + t * x_ld + h * ne0;
+        const int64_t p = pos[t];
+        float v;
+        if (rope_n_dims > 0 && d < rope_n_dims) {
+            // normal rope: element d belongs to pair d / 2
+            int64_t i0, i1;
+            uint32_t r0, r1;
+            rope_pair(xr, d / 2, rope_n_dims, 0, cos_sin + p * half * 2, T, i0, i1, r0, r1);
+            v = T.rev16[(d & 1) ? r1 : r0];
+        } else if (rope_n_dims > 0) {
+            v = T.rev16[x16_from_f32(T.cvt16, xr[d])];
+        } else {
+            v = xr[d];
+        }
+        const int64_t o = transposed ? h * cache_slice + ((p >> 3) * ne0 + d) * 8 + (p & 7)
+                                     : h * cache_slice + ((d >> 3) * cache_m + p) * 8 + (d & 7);
+        cache[o] = kv_code(T, v);
+    }
+}
+
+__global__ void k_causal_mask(const int32_t *__restrict__ pos0, int64_t ntok, int64_t n_kv, float *__restrict__ mask) {
+    const int64_t n = ntok * n_kv;
+    const int64_t p0 = pos0[0];
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)blockDim.x * gridDim.x) {
+        const int64_t t = i / n_kv, j = i - t * n_kv;
+        mask[i] = j <= p0 + t ? 0.0f : -INFINITY;
+    }
+}
+
 // ---- host helpers -------------------------------------------------------------
 
 template <int MODE>
@@ -683,6 +795,8 @@ static int check_mm(const lnship_mul_mat_args *a) {
     if (a->ne12 * a->ne13 > 65535) return fail(LNSHIP_ERANGE, "mul_mat: more than 65535 activation slices%s");
     const int64_t xld = a->x_ld ? a->x_ld : a->K;
     if (xld < a->K) return fail(LNSHIP_EINVAL, "mul_mat: x_ld < K%s");
+    if (a->w_mstride && a->w_mstride < a->M) return fail(LNSHIP_EINVAL, "mul_mat: w_mstride < M%s");
+    if (a->dst_ld && a->dst_ld < a->M) return fail(LNSHIP_EINVAL, "mul_mat: dst_ld < M%s");
     return 0;
 }
 
@@ -778,6 +892,7 @@ const void *lnship_host_table(const char *name, size_t *bytes) {
         {"gauss16", g_host->gauss16, sizeof g_host->gauss16},
         {"gauss16m", g_host->gauss16m, sizeof g_host->gauss16m},
         {"exp16", g_host->exp16, sizeof g_host->exp16},
+        {"sig16", g_host->sig16, sizeof g_host->sig16},
         {"tab32", g_host->tab32, sizeof g_host->tab32},
         {"lfsr_seq", g_host->lfsr_seq, sizeof g_host->lfsr_seq},
     };
@@ -803,6 +918,7 @@ int lnship_init(void) {
     if (int rc = upload(g_host->gauss16, 2 * k16_gauss_n, &T.gauss16)) return rc;
     if (int rc = upload(g_host->gauss16m, 2 * k16_gauss_n, &T.gauss16m)) return rc;
     if (int rc = upload(g_host->exp16, 1u << 16, &T.exp16)) return rc;
+    if (int rc = upload(g_host->sig16, 1u << 16, &T.sig16)) return rc;
     if (int rc = upload(g_host->tab32, (size_t)k32_tab_n, &T.tab32)) return rc;
     if (int rc = upload(g_host->lfsr_seq, 65536, &T.lfsr_seq)) return rc;
     if (int rc = upload(g_host->lfsr_log, 65536, &T.lfsr_log)) return rc;
@@ -900,8 +1016,12 @@ int lnship16_mul_mat(int mode, const lnship_mul_mat_args *a, void *stream) {
                            s->T.cvt16);
         LNSHIP_HIP(hipGetLastError());
     }
+    const int64_t wms = a->w_mstride ? a->w_mstride : a->M;
+    const int64_t dld = a->dst_ld ? a->dst_ld : a->M;
     mm_args16 m{(const uint16_t *)a->w, (const uint16_t *)xs, a->dst, a->K, kp, a->M, a->N,
-                a->ne02, a->ne12, a->ne12 / a->ne02, a->ne13 / a->ne03, a->monte_seed};
+                a->ne02, a->ne12, a->ne12 / a->ne02, a->ne13 / a->ne03,
+                wms, a->w_slice ? a->w_slice : kp * wms, dld, a->dst_slice ? a->dst_slice : a->N * dld,
+                a->monte_seed};
     switch (mode) {
         case LNSHIP_BASE: return dispatch_mm16<LNSHIP_BASE>(m, s->T, nslices, st);
         case LNSHIP_MONTE: return dispatch_mm16<LNSHIP_MONTE>(m, s->T, nslices, st);
@@ -928,8 +1048,11 @@ int lnship32_mul_mat(const lnship_mul_mat_args *a, void *stream) {
                            s->T.cvt16);
         LNSHIP_HIP(hipGetLastError());
     }
+    const int64_t wms = a->w_mstride ? a->w_mstride : a->M;
+    const int64_t dld = a->dst_ld ? a->dst_ld : a->M;
     mm_args32 m{(const uint32_t *)a->w, (const uint32_t *)xs, a->dst, a->K, kp, a->M, a->N,
-                a->ne02, a->ne12, a->ne12 / a->ne02, a->ne13 / a->ne03};
+                a->ne02, a->ne12, a->ne12 / a->ne02, a->ne13 / a->ne03,
+                wms, a->w_slice ? a->w_slice : kp * wms, dld, a->dst_slice ? a->dst_slice : a->N * dld};
     if (m.N >= 4) return launch_mm32<4>(m, s->T, nslices, st);
     return launch_mm32<1>(m, s->T, nslices, st);
 }
@@ -1000,6 +1123,104 @@ int lnship32_soft_max(const lnship_soft_max_args *a, void *stream) {
     if (int rc = set_lds(k_softmax32, lds)) return rc;
     hipLaunchKernelGGL(k_softmax32, dim3((unsigned)((nrows + m.rb - 1) / m.rb)), dim3(k_block), lds,
                        (hipStream_t)stream, m, s->T);
+    LNSHIP_HIP(hipGetLastError());
+    return 0;
+}
+
+int lnship16_add(const float *a, const float *b, int64_t n, int64_t nb, float *dst, void *stream) {
+    device_state *s = state();
+    if (!s) return LNSHIP_ENOINIT;
+    if (n < 0 || nb <= 0) return fail(LNSHIP_EINVAL, "add: bad length%s");
+    if (n == 0) return 0;
+    hipLaunchKernelGGL(k_binary16<0>, dim3(grid_for(n, 4)), dim3(k_block), 0, (hipStream_t)stream, a, b, n, nb, dst, s->T);
+    LNSHIP_HIP(hipGetLastError());
+    return 0;
+}
+
+int lnship16_mul(const float *a, const float *b, int64_t n, int64_t nb, float *dst, void *stream) {
+    device_state *s = state();
+    if (!s) return LNSHIP_ENOINIT;
+    if (n < 0 || nb <= 0) return fail(LNSHIP_EINVAL, "mul: bad length%s");
+    if (n == 0) return 0;
+    hipLaunchKernelGGL(k_binary16<1>, dim3(grid_for(n, 4)), dim3(k_block), 0, (hipStream_t)stream, a, b, n, nb, dst, s->T);
+    LNSHIP_HIP(hipGetLastError());
+    return 0;
+}
+
+int lnship16_swiglu(const float *gate, int64_t gate_ld, const float *up, int64_t up_ld, float *dst, int64_t ncols,
+                    int64_t nrows, void *stream) {
+    device_state *s = state();
+    if (!s) return LNSHIP_ENOINIT;
+    if (ncols < 0 || nrows < 0 || gate_ld < ncols || up_ld < ncols) return fail(LNSHIP_EINVAL, "swiglu: bad shape%s");
+    if (ncols == 0 || nrows == 0) return 0;
+    hipLaunchKernelGGL(k_swiglu16, dim3(grid_for(ncols * nrows, 4)), dim3(k_block), 0, (hipStream_t)stream, gate,
+                       gate_ld, up, up_ld, dst, ncols, nrows, s->T);
+    LNSHIP_HIP(hipGetLastError());
+    return 0;
+}
+
+int lnship16_get_rows_packed(const uint16_t *w, int64_t K, int64_t M, const int32_t *rows, int64_t nrows, float *dst,
+                             void *stream) {
+    device_state *s = state();
+    if (!s) return LNSHIP_ENOINIT;
+    if (K < 0 || M <= 0 || nrows < 0) return fail(LNSHIP_EINVAL, "get_rows: bad shape%s");
+    if (K == 0 || nrows == 0) return 0;
+    hipLaunchKernelGGL(k_get_rows_packed, dim3(grid_for(nrows * K, 4)), dim3(k_block), 0, (hipStream_t)stream, w, K, M,
+                       rows, nrows, dst, s->T.rev16);
+    LNSHIP_HIP(hipGetLastError());
+    return 0;
+}
+
+int lnship16_rope(const float *x, int64_t x_ld, const int32_t *pos, int64_t ntok, int64_t nhead, int64_t ne0,
+                  int n_dims, int neox, const float *cos_sin, float *dst, void *stream) {
+    device_state *s = state();
+    if (!s) return LNSHIP_ENOINIT;
+    if (n_dims <= 0 || n_dims % 2 || n_dims > ne0 || x_ld < nhead * ne0 || ntok < 0 || nhead < 0)
+        return fail(LNSHIP_EINVAL, "rope: bad shape%s");
+    const int64_t n = ntok * nhead * (n_dims / 2 + ne0 - n_dims);
+    if (n == 0) return 0;
+    hipLaunchKernelGGL(k_rope16, dim3(grid_for(n, 4)), dim3(k_block), 0, (hipStream_t)stream, x, x_ld, pos, ntok, nhead,
+                       ne0, n_dims, neox, cos_sin, dst, s->T);
+    LNSHIP_HIP(hipGetLastError());
+    return 0;
+}
+
+int lnship16_store_kv(const float *x, int64_t x_ld, const int32_t *pos, int64_t ntok, int64_t nhead, int64_t ne0,
+                      int rope_n_dims, const float *cos_sin, uint16_t *cache, int64_t cache_m, int64_t cache_slice,
+                      int cache_transposed, void *stream) {
+    device_state *s = state();
+    if (!s) return LNSHIP_ENOINIT;
+    if (rope_n_dims < 0 || rope_n_dims % 2 || rope_n_dims > ne0 || x_ld < nhead * ne0 || ntok < 0 || nhead < 0)
+        return fail(LNSHIP_EINVAL, "store_kv: bad shape%s");
+    if (!cache_transposed && ne0 % 8) return fail(LNSHIP_EINVAL, "store_kv: head size not a multiple of 8%s");
+    const int64_t n = ntok * nhead * ne0;
+    if (n == 0) return 0;
+    hipLaunchKernelGGL(k_store_kv16, dim3(grid_for(n, 4)), dim3(k_block), 0, (hipStream_t)stream, x, x_ld, pos, ntok,
+                       nhead, ne0, rope_n_dims, cos_sin, cache, cache_m, cache_slice, cache_transposed, s->T);
+    LNSHIP_HIP(hipGetLastError());
+    return 0;
+}
+
+int lnship_rope_table(float freq_base, int n_dims, int64_t n_pos, float *out) {
+    if (n_dims <= 0 || n_dims % 2 || n_pos < 0 || !out) return fail(LNSHIP_EINVAL, "rope_table: bad argument%s");
+    const float theta_scale = powf(freq_base, -2.0f / (float)n_dims);
+    const int half = n_dims / 2;
+    for (int64_t p = 0; p < n_pos; p++) {
+        float t = (float)p;
+        for (int j = 0; j < half; j++) {
+            out[(p * half + j) * 2 + 0] = cosf(t);
+            out[(p * half + j) * 2 + 1] = sinf(t);
+            t *= theta_scale;
+        }
+    }
+    return 0;
+}
+
+int lnship_causal_mask(const int32_t *pos0, int64_t ntok, int64_t n_kv, float *mask, void *stream) {
+    if (ntok < 0 || n_kv < 0) return fail(LNSHIP_EINVAL, "causal_mask: bad shape%s");
+    if (ntok == 0 || n_kv == 0) return 0;
+    hipLaunchKernelGGL(k_causal_mask, dim3(grid_for(ntok * n_kv, 4)), dim3(k_block), 0, (hipStream_t)stream, pos0, ntok,
+                       n_kv, mask);
     LNSHIP_HIP(hipGetLastError());
     return 0;
 }

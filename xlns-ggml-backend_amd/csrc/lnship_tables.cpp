@@ -87,6 +87,13 @@ void build_host_tables(host_tables &t) {
     }
 
     for (uint32_t i = 0; i < (1u << 16); i++) t.exp16[i] = encode16(std::exp(t.rev16[i]));
+    // the sigmoid goes through the bucketed conversion table
+    for (uint32_t i = 0; i < (1u << 16); i++) {
+        float sg = 1.0f / (1.0f + std::exp(-t.rev16[i]));
+        uint32_t b;
+        std::memcpy(&b, &sg, sizeof b);
+        t.sig16[i] = t.cvt16[b >> 15];
+    }
 
     int32_t *p = t.tab32;
     for (int i = 0; i < k32_sb_n; i++)

@@ -45,6 +45,7 @@ struct host_tables {
     int16_t  gauss16[2 * k16_gauss_n];   // [0]: sb, [1]: db at distance d; d = esszer + 1 -> 0
     int32_t  gauss16m[2 * k16_gauss_n];  // the same, 256x, floored (Monte)
     uint16_t exp16[1u << 16];   // xlns16 -> xlns16 exp
+    uint16_t sig16[1u << 16];   // xlns16 -> xlns16 sigmoid (silu = x * sigmoid)
     int32_t  tab32[k32_tab_n];  // xlns32 adder tables, layout above
     uint16_t lfsr_seq[65536];   // LFSR state after i steps from state 1 (i < 65535)
     uint16_t lfsr_log[65536];   // inverse of lfsr_seq

@@ -27,7 +27,8 @@ class LnshipError(RuntimeError):
 class MulMatArgs(ctypes.Structure):
     _fields_ = [("w", c_p), ("x", c_p), ("dst", c_p), ("K", c_i64), ("M", c_i64), ("N", c_i64),
                 ("ne02", c_i64), ("ne03", c_i64), ("ne12", c_i64), ("ne13", c_i64),
-                ("x_ld", c_i64), ("x_slice", c_i64), ("monte_seed", ctypes.c_uint16)]
+                ("x_ld", c_i64), ("x_slice", c_i64), ("monte_seed", ctypes.c_uint16),
+                ("w_mstride", c_i64), ("w_slice", c_i64), ("dst_ld", c_i64), ("dst_slice", c_i64)]
 
 
 class SoftMaxArgs(ctypes.Structure):
@@ -70,6 +71,16 @@ def lib():
         "lnship16_soft_max_draws": (ctypes.c_uint64, [ctypes.c_int, c_i64, c_i64]),
         "lnship16_rms_norm_draws": (ctypes.c_uint64, [ctypes.c_int, c_i64, c_i64]),
         "lnship_lfsr_jump": (ctypes.c_uint16, [ctypes.c_uint16, ctypes.c_uint64]),
+        "lnship16_add": (ctypes.c_int, [c_p, c_p, c_i64, c_i64, c_p, c_p]),
+        "lnship16_mul": (ctypes.c_int, [c_p, c_p, c_i64, c_i64, c_p, c_p]),
+        "lnship16_swiglu": (ctypes.c_int, [c_p, c_i64, c_p, c_i64, c_p, c_i64, c_i64, c_p]),
+        "lnship16_get_rows_packed": (ctypes.c_int, [c_p, c_i64, c_i64, c_p, c_i64, c_p, c_p]),
+        "lnship16_rope": (ctypes.c_int, [c_p, c_i64, c_p, c_i64, c_i64, c_i64, ctypes.c_int, ctypes.c_int, c_p, c_p,
+                                         c_p]),
+        "lnship16_store_kv": (ctypes.c_int, [c_p, c_i64, c_p, c_i64, c_i64, c_i64, ctypes.c_int, c_p, c_p, c_i64,
+                                             c_i64, ctypes.c_int, c_p]),
+        "lnship_causal_mask": (ctypes.c_int, [c_p, c_i64, c_i64, c_p, c_p]),
+        "lnship_rope_table": (ctypes.c_int, [ctypes.c_float, ctypes.c_int, c_i64, c_p]),
     }
     for name, (res, args) in sigs.items():
         fn = getattr(L, name)
@@ -187,7 +198,15 @@ def _mm_args(wp, x, out, K, M, ne02, ne03, seed):
     N = x.shape[-2]
     ne12 = x.shape[-3] if x.dim() >= 3 else 1
     ne13 = x.shape[-4] if x.dim() >= 4 else 1
-    return MulMatArgs(_p(wp), _p(x), _p(out), K, M, N, ne02, ne03, ne12, ne13, 0, 0, seed)
+    return MulMatArgs(_p(wp), _p(x), _p(out), K, M, N, ne02, ne03, ne12, ne13, 0, 0, seed, 0, 0, 0, 0)
+
+
+def mul_mat16_raw(mode, w_ptr, x_ptr, dst_ptr, K, M, N, ne02=1, ne03=1, ne12=1, ne13=1, x_ld=0, x_slice=0,
+                  seed=7, w_mstride=0, w_slice=0, dst_ld=0, dst_slice=0, stream=None):
+    """mul_mat on raw device pointers (ints), with every stride of the C ABI."""
+    a = MulMatArgs(w_ptr, x_ptr, dst_ptr, K, M, N, ne02, ne03, ne12, ne13, x_ld, x_slice, seed,
+                   w_mstride, w_slice, dst_ld, dst_slice)
+    check(lib().lnship16_mul_mat(mode, ctypes.byref(a), stream if stream is not None else _stream()))
 
 
 def mul_mat16(mode, wp, x, K, M, ne02=1, ne03=1, seed=7, out=None):

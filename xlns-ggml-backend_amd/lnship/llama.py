@@ -1,0 +1,266 @@
+"""A Llama-architecture decoder running every op on the gfx950 LNS kernels.
+
+The graph is llama.cpp's llama graph (non-flash attention) as the reference's
+LNS16 backend computes it, op by op, with F32 at op boundaries:
+
+  x = get_rows(tok_embd, tokens)                         (LNS16 weights decoded)
+  per layer:  h = rms_norm(x) * attn_norm
+              q, k, v = Wq h, Wk h, Wv h                  (one fused launch)
+              q, k = rope(q), rope(k)                      (normal pairs)
+              K/V cache <- f16(k), f16(v)                  (kept as packed LNS16)
+              p = soft_max(K^T q * 1/sqrt(d) + causal mask) over n_kv = pad(n, 256)
+              x = Wo (V p) + x                             (last layer: then last token only)
+              h = rms_norm(x) * ffn_norm
+              x = Wdown swiglu(Wgate h, Wup h) + x         (up | gate fused)
+  logits = tok_embd^T (rms_norm(x_last) * out_norm)        (tied output)
+
+Fusing Q|K|V and up|gate into one matrix keeps the Monte draw order of the
+separate ops: outputs of a mul_mat take draws in (row, column) order, so the
+fused rows enumerate Q's outputs, then K's, then V's.
+
+Activations, weights and the KV cache live in HBM; nothing is copied back to
+the host except the logits the caller asks for.
+"""
+import ctypes
+import math
+from dataclasses import dataclass
+
+import numpy as np
+
+from . import BASE, MONTE, LPVIP, SUM32, check, init, kp, lib, mul_mat16_raw
+
+KV_PAD = 256   # llama.cpp pads the KV view to 256 cells without flash attention
+
+
+@dataclass
+class LlamaConfig:
+    n_layer: int = 30
+    n_embd: int = 576
+    n_head: int = 9
+    n_head_kv: int = 3
+    head_dim: int = 64
+    n_ff: int = 1536
+    n_vocab: int = 49152
+    n_ctx: int = 512
+    rope_theta: float = 10000.0
+    eps: float = 1e-5
+
+
+SMOLLM2_135M = LlamaConfig()
+
+
+def splitmix_normal(seed, n, std):
+    """n samples of N(0, std^2): splitmix64 uniforms, Box-Muller in double, cast to float32."""
+    n2 = (n + 1) // 2
+    i = np.arange(2 * n2, dtype=np.uint64)
+    with np.errstate(over="ignore"):
+        z = (np.uint64(seed) * np.uint64(0x9E3779B97F4A7C15) + (i + np.uint64(1)) * np.uint64(0x9E3779B97F4A7C15))
+        z = (z ^ (z >> np.uint64(30))) * np.uint64(0xBF58476D1CE4E5B9)
+        z = (z ^ (z >> np.uint64(27))) * np.uint64(0x94D049BB133111EB)
+        z = z ^ (z >> np.uint64(31))
+    u = ((z >> np.uint64(11)).astype(np.float64) + 0.5) * (1.0 / 9007199254740992.0)
+    u1, u2 = u[0::2], u[1::2]
+    r = np.sqrt(-2.0 * np.log(u1))
+    out = np.empty(2 * n2, dtype=np.float64)
+    out[0::2] = r * np.cos(2.0 * np.pi * u2)
+    out[1::2] = r * np.sin(2.0 * np.pi * u2)
+    return (out[:n] * std).astype(np.float32)
+
+
+def synthetic_weights(cfg, seed=1234, std=0.02):
+    """Random-init weights of the architecture (F32, host).  Norm weights are
+    ones, as a freshly initialised RMSNorm; matrices are N(0, std^2)."""
+    e, f, d = cfg.n_embd, cfg.n_ff, cfg.head_dim
+    nq, nkv = cfg.n_head * d, cfg.n_head_kv * d
+    w = {"tok_embd": splitmix_normal(seed, cfg.n_vocab * e, std).reshape(cfg.n_vocab, e),
+         "out_norm": np.ones(e, np.float32), "layers": []}
+    for il in range(cfg.n_layer):
+        s = seed + 1000 * (il + 1)
+        w["layers"].append({
+            "attn_norm": np.ones(e, np.float32),
+            "wq": splitmix_normal(s + 1, nq * e, std).reshape(nq, e),
+            "wk": splitmix_normal(s + 2, nkv * e, std).reshape(nkv, e),
+            "wv": splitmix_normal(s + 3, nkv * e, std).reshape(nkv, e),
+            "wo": splitmix_normal(s + 4, e * nq, std).reshape(e, nq),
+            "ffn_norm": np.ones(e, np.float32),
+            "w_gate": splitmix_normal(s + 5, f * e, std).reshape(f, e),
+            "w_up": splitmix_normal(s + 6, f * e, std).reshape(f, e),
+            "w_down": splitmix_normal(s + 7, e * f, std).reshape(e, f),
+        })
+    return w
+
+
+def n_kv_for(n_used, n_ctx):
+    return min(n_ctx, max(KV_PAD, ((n_used + KV_PAD - 1) // KV_PAD) * KV_PAD))
+
+
+class LlamaLNS16:
+    """The decoder on one GPU; mode is the xlns16 summation mode."""
+
+    def __init__(self, cfg, weights, mode=SUM32, lfsr=7):
+        import torch
+        init()
+        self.cfg, self.mode, self.lfsr = cfg, mode, lfsr
+        self.torch = torch
+        dev = torch.device("cuda", torch.cuda.current_device())
+        self.dev = dev
+        c = cfg
+        from . import pack16
+        t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+        self.tok_embd = pack16(t(weights["tok_embd"]))           # K = n_embd, M = n_vocab
+        self.out_norm = t(weights["out_norm"])
+        self.layers = []
+        for L in weights["layers"]:
+            self.layers.append({
+                "attn_norm": t(L["attn_norm"]),
+                "wqkv": pack16(t(np.concatenate([L["wq"], L["wk"], L["wv"]]))),
+                "wo": pack16(t(L["wo"])),
+                "ffn_norm": t(L["ffn_norm"]),
+                "wug": pack16(t(np.concatenate([L["w_up"], L["w_gate"]]))),
+                "wdown": pack16(t(L["w_down"])),
+            })
+        hd, nkv = c.head_dim, c.n_head_kv
+        # packed LNS16 caches, per layer: K [nkv][hd/8][n_ctx][8], V [nkv][n_ctx/8][hd][8]
+        self.kslice = kp(hd) * c.n_ctx
+        self.vslice = kp(c.n_ctx) * hd
+        self.kcache = [torch.zeros(nkv * self.kslice, dtype=torch.int16, device=dev) for _ in range(c.n_layer)]
+        self.vcache = [torch.zeros(nkv * self.vslice, dtype=torch.int16, device=dev) for _ in range(c.n_layer)]
+        rt = np.empty(c.n_ctx * hd, np.float32)
+        check(lib().lnship_rope_table(c.rope_theta, hd, c.n_ctx, ctypes.c_void_p(rt.ctypes.data)))
+        self.cos_sin = t(rt)
+        self.n_past = 0
+        self._bufs = {}
+        self._graphs = {}
+
+    # -- buffers --------------------------------------------------------------
+    def _buf(self, name, n, dtype=None):
+        torch = self.torch
+        dtype = dtype or torch.float32
+        b = self._bufs.get(name)
+        if b is None or b.numel() < n:
+            b = torch.empty(max(n, 1), dtype=dtype, device=self.dev)
+            self._bufs[name] = b
+        return b
+
+    def _seed(self, draws):
+        """Monte: the LFSR state an op starts from, then advance (graph order)."""
+        s = self.lfsr
+        if self.mode == MONTE:
+            self.lfsr = lib().lnship_lfsr_jump(s, draws)
+        return s
+
+    # -- ops --------------------------------------------------------------------
+    def _mm(self, w, x_ptr, dst_ptr, K, M, N, **kw):
+        ne12 = kw.get("ne12", 1)
+        draws = lib().lnship16_mul_mat_draws(self.mode, K, M, N, ne12, 1)
+        mul_mat16_raw(self.mode, w, x_ptr, dst_ptr, K, M, N, seed=self._seed(draws), stream=self._stream, **kw)
+
+    def _rms(self, x_ptr, dst_ptr, ncols, nrows):
+        seed = self._seed(lib().lnship16_rms_norm_draws(self.mode, ncols, nrows))
+        check(lib().lnship16_rms_norm(self.mode, x_ptr, dst_ptr, ncols, nrows, self.cfg.eps, seed, self._stream))
+
+    def _softmax(self, x_ptr, ne, mask_ptr, mne, scale, dst_ptr):
+        from . import SoftMaxArgs
+        nrows = ne[1] * ne[2] * ne[3]
+        seed = self._seed(lib().lnship16_soft_max_draws(self.mode, ne[0], nrows))
+        a = SoftMaxArgs(x_ptr, (ctypes.c_int64 * 4)(*ne), mask_ptr, (ctypes.c_int64 * 4)(*mne), scale, dst_ptr, seed)
+        check(lib().lnship16_soft_max(self.mode, ctypes.byref(a), self._stream))
+
+    # -- forward -------------------------------------------------------------------
+    def forward(self, T, tokens_dev, pos_dev, n_kv):
+        """Runs T tokens at positions pos_dev[0..T) (device int32) against a
+        KV view of n_kv cells; returns the device logits of the last token."""
+        torch, c, L = self.torch, self.cfg, lib()
+        self._stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        st = self._stream
+        e, hd, nh, nkv, f = c.n_embd, c.head_dim, c.n_head, c.n_head_kv, c.n_ff
+        nq, nqkv = nh * hd, (nh + 2 * nkv) * hd
+        P = lambda b, off=0: ctypes.c_void_p(b.data_ptr() + off * b.element_size())
+        x = self._buf("x", T * e)
+        h = self._buf("h", T * e)
+        qkv = self._buf("qkv", T * nqkv)
+        q = self._buf("q", T * nq)
+        kq = self._buf("kq", nh * T * n_kv)
+        att = self._buf("att", T * nq)
+        o = self._buf("o", T * e)
+        ug = self._buf("ug", T * 2 * f)
+        sw = self._buf("sw", T * f)
+        mask = self._buf("mask", T * n_kv)
+        logits = self._buf("logits", c.n_vocab)
+        check(L.lnship16_get_rows_packed(P(self.tok_embd), e, c.n_vocab, P(tokens_dev), T, P(x), st))
+        check(L.lnship_causal_mask(P(pos_dev), T, n_kv, P(mask), st))
+        for il, W in enumerate(self.layers):
+            last = il == c.n_layer - 1
+            self._rms(P(x), P(h), e, T)
+            check(L.lnship16_mul(P(h), P(W["attn_norm"]), T * e, e, P(h), st))
+            self._mm(W["wqkv"].data_ptr(), P(h), P(qkv), e, nqkv, T)
+            check(L.lnship16_rope(P(qkv), nqkv, P(pos_dev), T, nh, hd, hd, 0, P(self.cos_sin), P(q), st))
+            check(L.lnship16_store_kv(P(qkv, nq), nqkv, P(pos_dev), T, nkv, hd, hd, P(self.cos_sin),
+                                      P(self.kcache[il]), c.n_ctx, self.kslice, 0, st))
+            check(L.lnship16_store_kv(P(qkv, nq + nkv * hd), nqkv, P(pos_dev), T, nkv, hd, 0, P(self.cos_sin),
+                                      P(self.vcache[il]), c.n_ctx, self.vslice, 1, st))
+            # kq[h][t][j] = K_j . q_t (GQA: query head h reads kv head h / (nh / nkv))
+            self._mm(self.kcache[il].data_ptr(), P(q), P(kq), hd, n_kv, T, ne02=nkv, ne12=nh,
+                     x_ld=nq, x_slice=hd, w_mstride=c.n_ctx, w_slice=self.kslice)
+            self._softmax(P(kq), (n_kv, T, nh, 1), P(mask), (n_kv, T, 1, 1), 1.0 / math.sqrt(hd), P(kq))
+            # att[t][h*hd + d] = sum_j V[j][d] p[h][t][j]
+            self._mm(self.vcache[il].data_ptr(), P(kq), P(att), n_kv, hd, T, ne02=nkv, ne12=nh,
+                     x_ld=n_kv, x_slice=T * n_kv, w_slice=self.vslice, dst_ld=nq, dst_slice=hd)
+            self._mm(W["wo"].data_ptr(), P(att), P(o), nq, e, T)
+            # after the last layer's attention only the output row goes on
+            rows = 1 if last else T
+            r0 = (T - rows) * e
+            check(L.lnship16_add(P(o, r0), P(x, r0), rows * e, rows * e, P(x), st))
+            self._rms(P(x), P(h), e, rows)
+            check(L.lnship16_mul(P(h), P(W["ffn_norm"]), rows * e, e, P(h), st))
+            self._mm(W["wug"].data_ptr(), P(h), P(ug), e, 2 * f, rows)
+            check(L.lnship16_swiglu(P(ug, f), 2 * f, P(ug), 2 * f, P(sw), f, rows, st))
+            self._mm(W["wdown"].data_ptr(), P(sw), P(o), f, e, rows)
+            check(L.lnship16_add(P(o), P(x), rows * e, rows * e, P(x), st))
+        self._rms(P(x), P(h), e, 1)
+        check(L.lnship16_mul(P(h), P(self.out_norm), e, e, P(h), st))
+        self._mm(self.tok_embd.data_ptr(), P(h), P(logits), e, c.n_vocab, 1)
+        return logits[: c.n_vocab]
+
+    def eval(self, tokens):
+        """Appends tokens (host list) at the current position; returns the
+        device logits of the last one."""
+        torch = self.torch
+        T = len(tokens)
+        assert self.n_past + T <= self.cfg.n_ctx, "context full"
+        tok = self._buf("tok", T, torch.int32)
+        pos = self._buf("pos", T, torch.int32)
+        tok[:T].copy_(torch.tensor(tokens, dtype=torch.int32))
+        pos[:T].copy_(torch.arange(self.n_past, self.n_past + T, dtype=torch.int32))
+        n_kv = n_kv_for(self.n_past + T, self.cfg.n_ctx)
+        out = self.forward(T, tok, pos, n_kv)
+        self.n_past += T
+        return out
+
+    def decode_graph(self, token, n_kv=None):
+        """One decode step through a captured HIP graph (non-Monte modes: the
+        graph bakes the op seeds).  Returns the device logits."""
+        torch = self.torch
+        assert self.mode != MONTE, "Monte seeds change every step; use eval()"
+        n_kv = n_kv or n_kv_for(self.n_past + 1, self.cfg.n_ctx)
+        tok = self._buf("gtok", 1, torch.int32)
+        pos = self._buf("gpos", 1, torch.int32)
+        tok.fill_(int(token))
+        pos.fill_(self.n_past)
+        g = self._graphs.get(n_kv)
+        if g is None:
+            # warm the library's scratch and the buffers, then capture
+            self.forward(1, tok, pos, n_kv)
+            torch.cuda.synchronize()
+            g = torch.cuda.CUDAGraph()
+            s = torch.cuda.Stream()
+            s.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(s):
+                with torch.cuda.graph(g, stream=s):
+                    out = self.forward(1, tok, pos, n_kv)
+            torch.cuda.current_stream().wait_stream(s)
+            self._graphs[n_kv] = (g, out)
+        g, out = self._graphs[n_kv]
+        g.replay()
+        self.n_past += 1
+        return out
