@@ -61,7 +61,7 @@ def test_exp16_table_equals_oracle(lnship):
 def test_tab32_equals_oracle(lnship):
     t = lnship.host_table("tab32", np.int32)
     sb, sbf, db, dbf, dlo, dhi = (O.table32(k) for k in ("sb", "sbf", "db", "dbf", "dlo", "dhi"))
-    parts = [sb, sbf, db[2048:], dbf, dlo, dhi]
+    parts = [dlo, dhi, sb, sbf, db[2048:], dbf]
     assert t.size == sum(p.size for p in parts)
     assert np.array_equal(t, np.concatenate(parts))
 

@@ -191,38 +191,118 @@ __global__ void k_act(const float *__restrict__ x, int64_t x_ld, int64_t x_slice
 }
 
 // ---- reductions -------------------------------------------------------------
-// One accumulator per (row, column) per lane; start/add/finish as in the
-// reference's reduction policies (cuda/lns-cuda-xlns16.cu:67-130).
+// One accumulator per (row, column) per lane; start / add / finish as in the
+// reference's reduction policies (cuda/lns-cuda-xlns16.cu:67-130).  The
+// accumulator keeps its log field and its sign in separate registers, so the
+// dependent chain of one addition is |dlog| -> table index -> LDS read ->
+// add -> clamp; the sign and the exact-cancellation case run beside it.
+// Exact cancellation (equal logs, opposite signs) reads a sentinel table
+// entry that clamps the log to 0 and forces the sign to +.
+
+__device__ __forceinline__ uint32_t absdiff(uint32_t a, uint32_t b) {
+    uint32_t r;
+    asm("v_sad_u32 %0, %1, %2, 0" : "=v"(r) : "v"(a), "v"(b));
+    return r;
+}
+
+__device__ __forceinline__ int32_t mul_i24(int32_t a, int32_t b) {
+    int32_t r;
+    asm("v_mul_i32_i24 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+    return r;
+}
+
+struct acc_ls {
+    uint32_t l, s;   // log field, sign bit in place
+};
 
 template <int MODE>
 struct red16;
 
 template <>
 struct red16<LNSHIP_BASE> {
-    const int16_t *g;
-    __device__ __forceinline__ uint32_t start(uint32_t v, uint32_t &) const { return v; }
-    __device__ __forceinline__ uint32_t add(uint32_t a, uint32_t t, uint32_t &) const { return x16_add_g(g, a, t); }
-    __device__ __forceinline__ uint32_t finish(uint32_t a) const { return a; }
+    const char *g;   // LDS: (sb, db) int16 pairs per distance d <= esszer + 1
+    using acc_t = acc_ls;
+    __device__ __forceinline__ acc_t start(uint32_t v, uint32_t &) const { return {v & k16_logmask, v & k16_sign}; }
+    __device__ __forceinline__ void add_ls(acc_t &a, uint32_t tl, uint32_t ts, uint32_t &) const {
+        const uint32_t d = absdiff(a.l, tl), mx = max(a.l, tl);
+        const uint32_t usedb = a.s ^ ts;
+        const int32_t adj = *reinterpret_cast<const int16_t *>(g + ((min(d, (uint32_t)k16_esszer + 1) << 2) | (usedb >> 14)));
+        const uint32_t ns = a.l > tl ? a.s : ts;
+        a.l = (uint32_t)min(max((int32_t)mx + adj, 0), (int32_t)k16_logmask);
+        a.s = (d == 0 && usedb) ? 0u : ns;
+    }
+    __device__ __forceinline__ void add(acc_t &a, uint32_t v, uint32_t &st) const { add_ls(a, v & k16_logmask, v & k16_sign, st); }
+    __device__ __forceinline__ uint32_t finish(const acc_t &a) const { return a.s | a.l; }
 };
 
 template <>
 struct red16<LNSHIP_MONTE> {
-    const int32_t *gm;
-    __device__ __forceinline__ uint32_t start(uint32_t v, uint32_t &) const { return v; }
-    __device__ __forceinline__ uint32_t add(uint32_t a, uint32_t t, uint32_t &st) const {
+    const int32_t *gm;   // LDS: (sb, db) 256x int32 pairs per distance
+    using acc_t = acc_ls;
+    __device__ __forceinline__ acc_t start(uint32_t v, uint32_t &) const { return {v & k16_logmask, v & k16_sign}; }
+    __device__ __forceinline__ void add_ls(acc_t &a, uint32_t tl, uint32_t ts, uint32_t &st) const {
         st = lfsr_step(st);
-        return x16_add_monte(gm, a, t, st);
+        const uint32_t d = absdiff(a.l, tl), mx = max(a.l, tl);
+        const uint32_t usedb = a.s ^ ts;
+        const int32_t f = gm[(min(d, (uint32_t)k16_esszer + 1) << 1) | (usedb >> 15)];
+        const int32_t adj = (f + (int32_t)(st & 0xffu)) >> 8;
+        const uint32_t ns = a.l > tl ? a.s : ts;
+        a.l = (uint32_t)min(max((int32_t)mx + adj, 0), (int32_t)k16_logmask);
+        a.s = (d == 0 && usedb) ? 0u : ns;
     }
-    __device__ __forceinline__ uint32_t finish(uint32_t a) const { return a; }
+    __device__ __forceinline__ void add(acc_t &a, uint32_t v, uint32_t &st) const { add_ls(a, v & k16_logmask, v & k16_sign, st); }
+    __device__ __forceinline__ uint32_t finish(const acc_t &a) const { return a.s | a.l; }
 };
+
+// xlns32 addition, branch-free: the interpolated sb / db and the
+// cotransformation are both evaluated and selected (T is the LDS copy of the
+// tables with the db-at-zero entry set to a sentinel).
+__device__ __forceinline__ int32_t interp_sel(const int32_t *T, uint32_t dc, bool hi, int base_lo, int base_hi) {
+    const int sh = hi ? k32_sb_fsh : k32_sb_sh;   // both grids: 2^13 / 2^19
+    const int i = (int)(dc >> sh) + (hi ? base_hi : base_lo);
+    const int32_t f = (int32_t)(dc & ((1u << sh) - 1u) & 0x7ffffu);
+    const int32_t t0 = T[i], t1 = T[i + 1];
+    // |t1 - t0| < 2^23 and f < 2^19: a full-rate 24-bit multiply
+    return t0 + (mul_i24(t1 - t0, f) >> sh);
+}
+
+__device__ __forceinline__ void x32_add_ls(const int32_t *T, acc_ls &a, uint32_t tl, uint32_t ts) {
+    const uint32_t d = absdiff(a.l, tl), mx = max(a.l, tl);
+    const bool usedb = (a.s ^ ts) != 0;
+    // direct: sb below / above 12 binades, db (>= 2 binades) below / above 8
+    const uint32_t dc = min(d, k32_esszer - 1);
+    const bool hi = dc >= (usedb ? k32_db_end : k32_sb_end);
+    const int32_t adj_d = usedb ? interp_sel(T, dc, hi, k32_off_db - k32_db_first, k32_off_dbf - (int)(k32_db_end >> k32_db_fsh))
+                                : interp_sel(T, dc, hi, k32_off_sb, k32_off_sbf - (int)(k32_sb_end >> k32_sb_fsh));
+    // cotransformation below 2 binades: 1 - 2^-d = (1 - 2^-dh) + 2^-dh (1 - 2^-dl)
+    const uint32_t dl = d & ((1u << k32_co_sh) - 1u), dh = (d >> k32_co_sh) & ((1u << k32_co_sh) - 1u);
+    const int32_t lo = T[k32_off_dlo + dl], th = T[k32_off_dhi + dh];
+    const uint32_t e = (dh << k32_co_sh) - (uint32_t)lo + (uint32_t)th;
+    const uint32_t ec = min(e, k32_esszer - 1);
+    int32_t sbe = interp_sel(T, ec, ec >= k32_sb_end, k32_off_sb, k32_off_sbf - (int)(k32_sb_end >> k32_sb_fsh));
+    sbe = e < k32_esszer ? sbe : 0;
+    const int32_t cot = dh == 0 ? lo : (dl == 0 ? th : th + sbe);
+    int32_t adj = (usedb && d < k32_co_end) ? cot : (d < k32_esszer ? adj_d : 0);
+    const int32_t r = max(__builtin_elementwise_add_sat((int32_t)mx, adj), 0);
+    const uint32_t ns = a.l > tl ? a.s : ts;
+    a.l = (uint32_t)r;
+    a.s = (d == 0 && usedb) ? 0u : ns;
+}
 
 template <>
 struct red16<LNSHIP_SUM32> {
     const int32_t *T;
-    __device__ __forceinline__ uint32_t start(uint32_t v, uint32_t &) const { return v << 16; }
-    __device__ __forceinline__ uint32_t add(uint32_t a, uint32_t t, uint32_t &) const { return x32_add(T, a, t << 16); }
-    __device__ __forceinline__ uint32_t finish(uint32_t s) const {
-        if ((s & k32_logmask) >= 0x7fff8000u) return (s >> 16) | k16_logmask;
+    using acc_t = acc_ls;   // xlns32: 31-bit log, sign in bit 31
+    __device__ __forceinline__ acc_t start(uint32_t v, uint32_t &) const {
+        return {(v & k16_logmask) << 16, (v & k16_sign) << 16};
+    }
+    __device__ __forceinline__ void add_ls(acc_t &a, uint32_t tl, uint32_t ts, uint32_t &) const {
+        x32_add_ls(T, a, tl << 16, ts << 16);
+    }
+    __device__ __forceinline__ void add(acc_t &a, uint32_t v, uint32_t &st) const { add_ls(a, v & k16_logmask, v & k16_sign, st); }
+    __device__ __forceinline__ uint32_t finish(const acc_t &a) const {
+        const uint32_t s = a.s | a.l;
+        if (a.l >= 0x7fff8000u) return (s >> 16) | k16_logmask;
         return (s + 0x8000u) >> 16;
     }
 };
@@ -251,37 +331,51 @@ __device__ __forceinline__ int32_t lpvip_db(uint32_t d) {
 
 template <>
 struct red16<LNSHIP_LPVIP> {
-    __device__ __forceinline__ uint32_t start(uint32_t v, uint32_t &) const { return v << 16; }
-    __device__ __forceinline__ uint32_t add(uint32_t a, uint32_t t16, uint32_t &) const {
-        uint32_t t = t16 << 16;
-        uint32_t al = a & k32_logmask, tl = t & k32_logmask;
-        uint32_t maxl = max(al, tl), d = maxl - min(al, tl);
-        uint32_t sgn = (al > tl ? a : t) & k32_sign;
-        uint32_t usedb = (a ^ t) & k32_sign;
-        if (d == 0 && usedb) return 0u;
+    using acc_t = acc_ls;
+    __device__ __forceinline__ acc_t start(uint32_t v, uint32_t &) const {
+        return {(v & k16_logmask) << 16, (v & k16_sign) << 16};
+    }
+    __device__ __forceinline__ void add_ls(acc_t &a, uint32_t tl16, uint32_t ts16, uint32_t &) const {
+        const uint32_t tl = tl16 << 16, ts = ts16 << 16;
+        const uint32_t mx = max(a.l, tl), d = mx - min(a.l, tl);
+        const uint32_t sgn = a.l > tl ? a.s : ts;
+        const uint32_t usedb = a.s ^ ts;
+        if (d == 0 && usedb) {
+            a.l = 0;
+            a.s = 0;
+            return;
+        }
         int32_t adj = 0;
         if (d < k32_esszer) adj = usedb ? lpvip_db(d) : lpvip_sb(d);
-        uint32_t s = maxl + (uint32_t)adj;
-        uint32_t l = (s & k32_sign) ? ((s & k32_one) ? 0u : k32_logmask) : s;
-        return sgn | l;
+        const uint32_t s = mx + (uint32_t)adj;
+        a.l = (s & k32_sign) ? ((s & k32_one) ? 0u : k32_logmask) : s;
+        a.s = sgn;
     }
-    __device__ __forceinline__ uint32_t finish(uint32_t s) const { return s >> 16; }
+    __device__ __forceinline__ void add(acc_t &a, uint32_t v, uint32_t &st) const { add_ls(a, v & k16_logmask, v & k16_sign, st); }
+    __device__ __forceinline__ uint32_t finish(const acc_t &a) const { return (a.s | a.l) >> 16; }
 };
 
-// Stages the tables a reduction needs into LDS; returns the policy.
+// Stages the tables a reduction needs into LDS (with the sentinels); returns
+// the policy.
 template <int MODE>
 __device__ __forceinline__ red16<MODE> stage_tables(const dev_tables &T, char *lds);
 
 template <>
 __device__ __forceinline__ red16<LNSHIP_BASE> stage_tables<LNSHIP_BASE>(const dev_tables &T, char *lds) {
     int16_t *g = reinterpret_cast<int16_t *>(lds);
-    for (int i = threadIdx.x; i < 2 * k16_gauss_n; i += blockDim.x) g[i] = T.gauss16[i];
-    return red16<LNSHIP_BASE>{g};
+    for (int i = threadIdx.x; i < k16_gauss_n; i += blockDim.x) {
+        g[2 * i] = T.gauss16[i];
+        g[2 * i + 1] = i == 0 ? (int16_t)-32768 : T.gauss16[k16_gauss_n + i];
+    }
+    return red16<LNSHIP_BASE>{lds};
 }
 template <>
 __device__ __forceinline__ red16<LNSHIP_MONTE> stage_tables<LNSHIP_MONTE>(const dev_tables &T, char *lds) {
     int32_t *g = reinterpret_cast<int32_t *>(lds);
-    for (int i = threadIdx.x; i < 2 * k16_gauss_n; i += blockDim.x) g[i] = T.gauss16m[i];
+    for (int i = threadIdx.x; i < k16_gauss_n; i += blockDim.x) {
+        g[2 * i] = T.gauss16m[i];
+        g[2 * i + 1] = i == 0 ? -(1 << 24) : T.gauss16m[k16_gauss_n + i];
+    }
     return red16<LNSHIP_MONTE>{g};
 }
 template <>
@@ -291,6 +385,8 @@ __device__ __forceinline__ red16<LNSHIP_SUM32> stage_tables<LNSHIP_SUM32>(const 
     int4 *d4 = reinterpret_cast<int4 *>(t);
     for (int i = threadIdx.x; i < k32_tab_n / 4; i += blockDim.x) d4[i] = src[i];
     for (int i = (k32_tab_n / 4) * 4 + threadIdx.x; i < k32_tab_n; i += blockDim.x) t[i] = T.tab32[i];
+    __syncthreads();
+    if (threadIdx.x == 0) t[k32_off_dlo] = -0x7fffffff;   // db at d = 0: exact cancellation
     return red16<LNSHIP_SUM32>{t};
 }
 template <>
@@ -309,7 +405,8 @@ constexpr int lds_tables_bytes() {
 // One lane per weight row m and NC activation columns n (NC independent
 // accumulations interleaved for latency hiding).  xs holds the converted
 // activations [slice][N][Kp]; their index is uniform across the wave, so the
-// compiler fetches them through the scalar cache.
+// compiler fetches them through the scalar cache.  The weights of the next PF
+// groups of eight k are in flight while a group is accumulated.
 
 struct mm_args16 {
     const uint16_t *w;
@@ -321,7 +418,9 @@ struct mm_args16 {
     uint32_t seed;
 };
 
-template <int MODE, int NC>
+__device__ __forceinline__ uint32_t half16(uint32_t w, int hi) { return hi ? (w >> 16) : (w & 0xffffu); }
+
+template <int MODE, int NC, int PF>
 __global__ __launch_bounds__(k_block) void k_mm16(mm_args16 a, dev_tables T) {
     extern __shared__ __align__(16) char lds[];
     const red16<MODE> R = stage_tables<MODE>(T, lds);
@@ -337,55 +436,95 @@ __global__ __launch_bounds__(k_block) void k_mm16(mm_args16 a, dev_tables T) {
     const uint16_t *ws = a.w + ((i13 / a.r3) * a.ne02 + i12 / a.r2) * a.w_slice + m * 8;
     const uint16_t *xs = a.x + (z * a.N + n0) * a.kp;
     const int64_t wstride = a.w_mstride * 8;   // between consecutive groups of 8 k
+    float *ds = a.dst + z * a.dst_slice + n0 * a.dst_ld + m;
+    if (a.K == 0) {
+        for (int j = 0; j < nc; j++) ds[(int64_t)j * a.dst_ld] = T.rev16[0];
+        return;
+    }
 
-    uint32_t acc[NC], st[NC];
+    typename red16<MODE>::acc_t acc[NC];
+    uint32_t st[NC];
 #pragma unroll
     for (int j = 0; j < NC; j++) {
-        acc[j] = 0;
         st[j] = 0;
         if (MODE == LNSHIP_MONTE && j < nc) {
             const uint64_t out = ((uint64_t)z * (uint64_t)a.M + (uint64_t)m) * (uint64_t)a.N + (uint64_t)(n0 + j);
             st[j] = lfsr_jump(T, a.seed, out * (uint64_t)(a.K - 1));
         }
     }
-    // group g holds steps 8g .. 8g+7; with first, step 0 starts the
-    // accumulation; steps [u0, u1) are added
-    auto group = [&](int64_t g, bool first, int u0, int u1) {
-        const uint4 wq = *reinterpret_cast<const uint4 *>(ws + g * wstride);
-        const uint32_t wv[8] = {wq.x & 0xffffu, wq.x >> 16, wq.y & 0xffffu, wq.y >> 16,
-                                wq.z & 0xffffu, wq.z >> 16, wq.w & 0xffffu, wq.w >> 16};
-        uint32_t xv[NC][8];
-#pragma unroll
-        for (int j = 0; j < NC; j++) {
-            const int jj = j < nc ? j : 0;
-            const uint4 xq = *reinterpret_cast<const uint4 *>(xs + jj * a.kp + g * 8);
-            xv[j][0] = xq.x & 0xffffu; xv[j][1] = xq.x >> 16; xv[j][2] = xq.y & 0xffffu; xv[j][3] = xq.y >> 16;
-            xv[j][4] = xq.z & 0xffffu; xv[j][5] = xq.z >> 16; xv[j][6] = xq.w & 0xffffu; xv[j][7] = xq.w >> 16;
-        }
-        if (first) {
-#pragma unroll
-            for (int j = 0; j < NC; j++) acc[j] = R.start(x16_mul(wv[0], xv[j][0]), st[j]);
-        }
+    const int K = (int)a.K;
+    const int full = K >> 3, tail = K & 7;
+    const int kp = (int)a.kp;
+    auto load_w = [&](int g) { return *reinterpret_cast<const uint4 *>(ws + (int64_t)g * wstride); };
+    auto load_x = [&](int j, int g) {
+        return *reinterpret_cast<const uint4 *>(xs + (j < nc ? j : 0) * kp + g * 8);
+    };
+    // steps [u0, u1) of a group: the product (xlns16_mul: log fields added
+    // and clamped, signs xor'ed), then one reduction step per column
+    auto steps = [&](const uint4 &wq, const uint4 (&xq)[NC], int u0, int u1) {
+        const uint32_t ww[4] = {wq.x, wq.y, wq.z, wq.w};
 #pragma unroll
         for (int u = 0; u < 8; u++) {
             if (u >= u0 && u < u1) {
+                const uint32_t wv = half16(ww[u >> 1], u & 1);
+                const uint32_t wl = wv & k16_logmask;
 #pragma unroll
-                for (int j = 0; j < NC; j++) acc[j] = R.add(acc[j], x16_mul(wv[u], xv[j][u]), st[j]);
+                for (int j = 0; j < NC; j++) {
+                    const uint32_t xv = half16(u < 2 ? xq[j].x : u < 4 ? xq[j].y : u < 6 ? xq[j].z : xq[j].w, u & 1);
+                    const int32_t l = (int32_t)wl + (int32_t)(xv & k16_logmask) - (int32_t)k16_one;
+                    const uint32_t tl = (uint32_t)min(max(l, 0), (int32_t)k16_logmask);
+                    const uint32_t ts = (wv ^ xv) & k16_sign;
+                    if (u == 0 && u0 < 0) acc[j] = R.start(ts | tl, st[j]);
+                    else R.add_ls(acc[j], tl, ts, st[j]);
+                }
             }
         }
     };
-    const int64_t full = a.K >> 3;
-    const int tail = (int)(a.K & 7);
-    if (a.K > 0) {
-        group(0, true, 1, full > 0 ? 8 : tail);
-        for (int64_t g = 1; g < full; g++) group(g, false, 0, 8);
-        if (full > 0 && tail > 0) group(full, false, 0, tail);
-    }
-    float *ds = a.dst + z * a.dst_slice + n0 * a.dst_ld + m;
+    {
+        // group 0 starts the accumulation (u0 = -1 marks the start step)
+        uint4 xq[NC];
 #pragma unroll
-    for (int j = 0; j < NC; j++) {
-        if (j < nc) ds[(int64_t)j * a.dst_ld] = a.K == 0 ? T.rev16[0] : T.rev16[R.finish(acc[j]) & 0xffffu];
+        for (int j = 0; j < NC; j++) xq[j] = load_x(j, 0);
+        const uint4 wq = load_w(0);
+        uint4 ring[PF], xring[PF][NC];
+#pragma unroll
+        for (int p = 0; p < PF; p++)
+            if (1 + p < full) {
+                ring[p] = load_w(1 + p);
+#pragma unroll
+                for (int j = 0; j < NC; j++) xring[p][j] = load_x(j, 1 + p);
+            }
+        steps(wq, xq, -1, full > 0 ? 8 : tail);
+        // groups 1 .. full-1, PF of them in flight
+        int g = 1;
+        for (; g + PF <= full; g += PF) {
+#pragma unroll
+            for (int p = 0; p < PF; p++) {
+                const uint4 cw = ring[p];
+                uint4 cx[NC];
+#pragma unroll
+                for (int j = 0; j < NC; j++) cx[j] = xring[p][j];
+                if (g + p + PF < full) {
+                    ring[p] = load_w(g + p + PF);
+#pragma unroll
+                    for (int j = 0; j < NC; j++) xring[p][j] = load_x(j, g + p + PF);
+                }
+                steps(cw, cx, 0, 8);
+            }
+        }
+#pragma unroll
+        for (int p = 0; p < PF; p++)
+            if (g + p < full) steps(ring[p], xring[p], 0, 8);
+        if (full > 0 && tail > 0) {
+            uint4 tx[NC];
+#pragma unroll
+            for (int j = 0; j < NC; j++) tx[j] = load_x(j, full);
+            steps(load_w(full), tx, 0, tail);
+        }
     }
+#pragma unroll
+    for (int j = 0; j < NC; j++)
+        if (j < nc) ds[(int64_t)j * a.dst_ld] = T.rev16[R.finish(acc[j]) & 0xffffu];
 }
 
 // xlns32 (the LNS32 backend): plain sequential xlns32_add
@@ -412,9 +551,7 @@ __global__ __launch_bounds__(k_block) void k_mm32(mm_args32 a, dev_tables T) {
     const uint32_t *ws = a.w + ((i13 / a.r3) * a.ne02 + i12 / a.r2) * a.w_slice + m * 8;
     const uint32_t *xs = a.x + (z * a.N + n0) * a.kp;
     const int64_t wstride = a.w_mstride * 8;
-    uint32_t acc[NC];
-#pragma unroll
-    for (int j = 0; j < NC; j++) acc[j] = 0;
+    acc_ls acc[NC];
     const int64_t kgroups = a.kp >> 3;
     for (int64_t g = 0; g < kgroups; g++) {
         const uint4 w0 = *reinterpret_cast<const uint4 *>(ws + g * wstride);
@@ -436,14 +573,15 @@ __global__ __launch_bounds__(k_block) void k_mm32(mm_args32 a, dev_tables T) {
 #pragma unroll
             for (int j = 0; j < NC; j++) {
                 const uint32_t t = x32_mul(wv[u], xv[j][u]);
-                acc[j] = (kb + u == 0) ? t : x32_add(R.T, acc[j], t);
+                if (kb + u == 0) acc[j] = {t & k32_logmask, t & k32_sign};
+                else x32_add_ls(R.T, acc[j], t & k32_logmask, t & k32_sign);
             }
         }
     }
     float *ds = a.dst + z * a.dst_slice + n0 * a.dst_ld + m;
 #pragma unroll
     for (int j = 0; j < NC; j++)
-        if (j < nc) ds[(int64_t)j * a.dst_ld] = a.K == 0 ? 0.0f : x32_to_f32(acc[j]);
+        if (j < nc) ds[(int64_t)j * a.dst_ld] = a.K == 0 ? 0.0f : x32_to_f32(acc[j].s | acc[j].l);
 }
 
 // ---- RMS_NORM -------------------------------------------------------------------
@@ -471,8 +609,8 @@ __global__ __launch_bounds__(k_block) void k_rms16(const float *__restrict__ src
         uint32_t s = 0;
         if (MODE == LNSHIP_MONTE) s = lfsr_jump(T, seed, (uint64_t)(r0 + r) * (uint64_t)ncols);
         const uint16_t *row = sq + (int64_t)r * ncols;
-        uint32_t acc = R.start(0u, s);
-        for (int64_t i = 0; i < ncols; i++) acc = R.add(acc, row[i], s);
+        typename red16<MODE>::acc_t acc = R.start(0u, s);
+        for (int64_t i = 0; i < ncols; i++) R.add(acc, row[i], s);
         const uint32_t sum = R.finish(acc) & 0xffffu;
         const uint32_t mean = x16_mul(sum, x16_from_f32(T.cvt16, 1.0f / (float)ncols));
         const uint32_t e16 = x16_from_f32(T.cvt16, eps);
@@ -582,8 +720,8 @@ __global__ __launch_bounds__(k_block) void k_softmax16(sm_args a, dev_tables T) 
         uint32_t s = 0;
         if (MODE == LNSHIP_MONTE) s = lfsr_jump(T, a.seed, (uint64_t)(r0 + r) * (uint64_t)(a.n - 1));
         const uint16_t *row = c + (int64_t)r * a.n;
-        uint32_t acc = R.start(row[0], s);
-        for (int64_t i = 1; i < a.n; i++) acc = R.add(acc, row[i], s);
+        typename red16<MODE>::acc_t acc = R.start(row[0], s);
+        for (int64_t i = 1; i < a.n; i++) R.add(acc, row[i], s);
         s_tot[r] = R.finish(acc) & 0xffffu;
     }
     __syncthreads();
@@ -802,12 +940,13 @@ static int check_mm(const lnship_mul_mat_args *a) {
 
 template <int MODE, int NC>
 static int launch_mm16(const mm_args16 &m, const dev_tables &T, int64_t nslices, hipStream_t st) {
+    constexpr int PF = NC == 1 ? 4 : (NC <= 4 ? 2 : 1);
     constexpr int lds = lds_tables_bytes<MODE>();
     if (lds > 64 * 1024)
-        if (int rc = set_lds(k_mm16<MODE, NC>, lds)) return rc;
+        if (int rc = set_lds(k_mm16<MODE, NC, PF>, lds)) return rc;
     dim3 grid((unsigned)((m.M + k_block - 1) / k_block), (unsigned)((m.N + NC - 1) / NC), (unsigned)nslices);
     if (grid.x > 2147483647u || grid.y > 65535u) return fail(LNSHIP_ERANGE, "mul_mat: grid too large%s");
-    hipLaunchKernelGGL((k_mm16<MODE, NC>), grid, dim3(k_block), lds, st, m, T);
+    hipLaunchKernelGGL((k_mm16<MODE, NC, PF>), grid, dim3(k_block), lds, st, m, T);
     LNSHIP_HIP(hipGetLastError());
     return 0;
 }
@@ -1004,6 +1143,7 @@ int lnship16_mul_mat(int mode, const lnship_mul_mat_args *a, void *stream) {
     if (mode < 0 || mode > 3) return fail(LNSHIP_EINVAL, "unknown summation mode%s");
     if (int rc = check_mm(a)) return rc;
     if (a->M == 0 || a->N == 0) return 0;
+    if (a->K > (int64_t)1 << 30) return fail(LNSHIP_ERANGE, "mul_mat: K beyond 2^30%s");
     const int64_t nslices = a->ne12 * a->ne13;
     const int64_t kp = (a->K + 7) & ~(int64_t)7;
     void *xs = nullptr;

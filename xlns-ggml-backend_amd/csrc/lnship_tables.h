@@ -30,14 +30,16 @@ constexpr int k32_db_first = (int)(k32_co_end >> k32_db_sh);                   /
 constexpr int k32_db_n = (int)(k32_db_end >> k32_db_sh) + 1 - k32_db_first;    // 6145
 constexpr int k32_db_fn = (int)((k32_esszer - k32_db_end) >> k32_db_fsh) + 1;  // 257
 
-// One contiguous int32 block for the xlns32 adder, in this order.
-constexpr int k32_off_sb = 0;
+// One contiguous int32 block for the xlns32 adder, in this order (the
+// cotransformation tables first: their LDS byte offsets fit in the 16-bit
+// immediate of an LDS read).
+constexpr int k32_off_dlo = 0;
+constexpr int k32_off_dhi = k32_off_dlo + k32_co_n;
+constexpr int k32_off_sb = k32_off_dhi + k32_co_n;
 constexpr int k32_off_sbf = k32_off_sb + k32_sb_n;
 constexpr int k32_off_db = k32_off_sbf + k32_sb_fn;
 constexpr int k32_off_dbf = k32_off_db + k32_db_n;
-constexpr int k32_off_dlo = k32_off_dbf + k32_db_fn;
-constexpr int k32_off_dhi = k32_off_dlo + k32_co_n;
-constexpr int k32_tab_n = k32_off_dhi + k32_co_n;                              // 27076
+constexpr int k32_tab_n = k32_off_dbf + k32_db_fn;                             // 27076
 
 struct host_tables {
     uint16_t cvt16[1u << 17];   // float bits >> 15 -> xlns16
