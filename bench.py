@@ -34,28 +34,41 @@ def parse():
     ap.add_argument("--prompt", type=int, default=128)
     ap.add_argument("--cpu-tokens", type=int, default=3, help="decode tokens of the CPU baseline sample")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-graph", action="store_true", help="decode eagerly instead of replaying a HIP graph")
+    ap.add_argument("--calib-copy", type=int, default=0, metavar="MIB",
+                    help="only run a plain device copy of MIB MiB three times (HBM counter calibration)")
     return ap.parse_args()
 
 
-def gemv_roofline(model, ln, torch):
-    """Times every mul_mat launch of one eager decode step with HIP events on
-    the launch stream; returns (bytes per launch, avg launch us, launches)."""
+def calib_copy(mib):
+    """A plain device-to-device copy of known size: what FETCH_SIZE / WRITE_SIZE
+    read for it scales the same counters read for the LNS kernels."""
+    import torch
+    n = mib * (1 << 20) // 4
+    src = torch.ones(n, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"calib": "copy", "bytes_read": n * 4, "bytes_written": n * 4}), flush=True)
+
+
+def gemv_roofline(model, ln, torch, reps=4):
+    """Records the mul_mat launches of one eager decode step, captures them
+    `reps` times over into one HIP graph and times a replay between two HIP
+    events on the replay stream.  Returns (algorithmic bytes per launch,
+    average launch us, launches per token); a launch is one lnship16_mul_mat
+    call, i.e. the activation conversion kernel plus the GEMV kernel."""
     c = model.cfg
-    events = []
+    calls = []
     orig = model._mm
 
-    def timed_mm(w, x_ptr, dst_ptr, K, M, N, **kw):
-        s = torch.cuda.Event(enable_timing=True)
-        e = torch.cuda.Event(enable_timing=True)
-        s.record()
+    def record_mm(w, x_ptr, dst_ptr, K, M, N, **kw):
         orig(w, x_ptr, dst_ptr, K, M, N, **kw)
-        e.record()
-        ne12 = kw.get("ne12", 1)
-        # algorithmic bytes: xlns16 weights once per weight slice, F32 in / out
-        ne02 = kw.get("ne02", 1)
-        events.append((s, e, 2 * K * M * ne02 + 4 * K * N * ne12 + 4 * M * N * ne12))
+        calls.append((w, x_ptr, dst_ptr, K, M, N, kw))
 
-    model._mm = timed_mm
+    model._mm = record_mm
     try:
         tok = model._buf("rtok", 1, torch.int32)
         pos = model._buf("rpos", 1, torch.int32)
@@ -66,10 +79,40 @@ def gemv_roofline(model, ln, torch):
         torch.cuda.synchronize()
     finally:
         model._mm = orig
-    total_us = sum(s.elapsed_time(e) * 1e3 for s, e, _ in events)
-    total_b = sum(b for _, _, b in events)
-    n = len(events)
+    # the launches go into one HIP graph so host-side launch cost stays out
+    # of the device time between the events
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for _ in range(reps):
+            for w, x_ptr, dst_ptr, K, M, N, kw in calls:
+                ln.mul_mat16_raw(model.mode, w, x_ptr, dst_ptr, K, M, N, seed=7,
+                                 stream=ctypes.c_void_p(torch.cuda.current_stream().cuda_stream), **kw)
+    g.replay()
+    s = torch.cuda.Event(enable_timing=True)
+    e = torch.cuda.Event(enable_timing=True)
+    s.record()
+    g.replay()
+    e.record()
+    e.synchronize()
+    n = len(calls)
+    total_us = s.elapsed_time(e) * 1e3 / reps
+    # algorithmic bytes: xlns16 weights once per weight slice, F32 in / out
+    total_b = sum(2 * K * M * kw.get("ne02", 1) + 4 * K * N * kw.get("ne12", 1) + 4 * M * N * kw.get("ne12", 1)
+                  for _, _, _, K, M, N, kw in calls)
     return total_b / n, total_us / n, n
+
+
+def measured_traffic(mode):
+    """HBM bytes per decode mul_mat launch from the committed rocprofv3 PMC
+    summary (FETCH_SIZE and WRITE_SIZE passes scaled by a plain copy), or None
+    when no summary exists for this mode."""
+    p = os.path.join(ROOT, "profiles", "k_mm16_decode_%s_traffic.json" % mode)
+    try:
+        with open(p) as f:
+            d = json.load(f)
+        return d["bytes_per_mul_mat"], os.path.relpath(p, ROOT)
+    except (OSError, KeyError, ValueError):
+        return None, None
 
 
 def cpu_baseline(cfg, weights, mode, n_tokens):
@@ -107,6 +150,9 @@ def main():
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
               f"(multi-GPU sharding is a design note, not part of this build)", file=sys.stderr)
         sys.exit(2)
+    if args.calib_copy:
+        calib_copy(args.calib_copy)
+        return
     import numpy as np
     import torch
     import lnship
@@ -135,7 +181,7 @@ def main():
     t_prefill = time.perf_counter() - tp
 
     tok_dev = torch.argmax(logits).to(torch.int32).reshape(1)
-    use_graph = mode != lnship.MONTE
+    use_graph = mode != lnship.MONTE and not args.no_graph
 
     def step():
         nonlocal tok_dev
@@ -160,6 +206,7 @@ def main():
         3 * cfg.n_ff * cfg.n_embd) + cfg.n_vocab * cfg.n_embd
     b_launch, us_launch, n_launch = gemv_roofline(model, lnship, torch)
     achieved = b_launch / (us_launch * 1e-6) / 1e9
+    traffic, traffic_src = measured_traffic(args.mode)
     out = {
         "metric": METRIC,
         "value": round(decode_tok_s, 3),
@@ -181,8 +228,9 @@ def main():
         "mul_mat_gmacs": round(macs_per_token * decode_tok_s / 1e9, 4),
         "weight_macs_per_token": macs_per_token,
         "roofline": {"bound": "hbm", "achieved": round(achieved, 3), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 6), "traffic": None,
-                     "kernel": "k_mm16 (decode mul_mat, %s)" % args.mode,
+                     "frac": round(achieved / HBM_PEAK_GBS, 6), "traffic": traffic,
+                     "traffic_source": traffic_src,
+                     "kernel": "lnship16_mul_mat decode launches (k_act + k_mm16<%s, NC=1>)" % args.mode,
                      "launches_per_token": n_launch, "avg_launch_us": round(us_launch, 3),
                      "bytes_per_launch": int(b_launch)},
         "reference_published": {"rtx2050_sum32_decode_tok_s": 7.31,
