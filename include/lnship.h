@@ -154,6 +154,13 @@ int lnship_rope_table(float freq_base, int n_dims, int64_t n_pos, float *out);
  * t < ntok, j < n_kv; pos0 read from the device */
 int lnship_causal_mask(const int32_t *pos0, int64_t ntok, int64_t n_kv, float *mask, void *stream);
 
+/* Longest row (ncols) the row kernels stage in LDS: which = 0 xlns16
+ * rms_norm, 1 xlns16 soft_max, 2 xlns32 rms_norm, 3 xlns32 soft_max; mode is
+ * the xlns16 summation mode (ignored for xlns32).  No GPU needed.  Plays the
+ * role of the reference's grid / shape predicates (cuda/lns-cuda-ops.cpp:
+ * 45-54, 184-189): a ggml backend declines longer rows in supports_op. */
+int64_t lnship_max_row(int which, int mode);
+
 /* ---- Monte draw accounting (kernel_set::*_draws, :97-100) --------------- */
 uint64_t lnship16_mul_mat_draws(int mode, int64_t K, int64_t M, int64_t N, int64_t ne12, int64_t ne13);
 uint64_t lnship16_soft_max_draws(int mode, int64_t ncols, int64_t nrows);

@@ -1,0 +1,221 @@
+"""Runs a small ggml graph through the LNSHIP16 (or LNSHIP32) backend on the
+GPU and checks every node against the oracle, bit for bit (TEST
+INFRASTRUCTURE; run by tests/test_gpu_ggml.py, one process per summation
+mode because the backend reads GGML_LNS16_SUM once).
+
+The graph has the shapes and layouts llama.cpp hands the reference's
+LNSCUDA16 backend (cuda/lns-cuda-ops.cpp): an rms_norm and norm-weight MUL,
+a fused QKV MUL_MAT on F32 weights, RoPE on a strided view of it, the GQA kq
+MUL_MAT on an F16 KV-cache tensor against a permuted view, a masked
+SOFT_MAX, a Q8_0-weight MUL_MAT, SWIGLU fused and split, ADD with flat and
+general broadcasts, an F16-weight MUL_MAT, a repeated MUL_MAT that hits the
+weight cache, and an unmasked SOFT_MAX.  The oracle runs the same ops in
+graph order, so Monte draws are reserved in the same sequence.
+
+Usage: python ggml_graph_check.py --mode base|monte|lpvip|sum32 [--w32]
+Exit status 0 when every node matches.
+"""
+import argparse
+import ctypes
+import json
+import os
+import sys
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, HERE)
+
+import ggml_host as G  # noqa: E402
+import oracle_lib as O  # noqa: E402
+
+
+def q8_0(w, rng):
+    """w [M, K] -> (block bytes, the F32 values the blocks decode to)."""
+    M, K = w.shape
+    blocks = w.reshape(M, K // 32, 32)
+    d = (np.abs(blocks).max(axis=2) / 127.0).astype(np.float16)
+    d[d == 0] = np.float16(1.0)
+    q = np.clip(np.rint(blocks / d.astype(np.float32)[..., None]), -127, 127).astype(np.int8)
+    raw = np.zeros((M, K // 32, 34), np.uint8)
+    raw[..., :2] = d.view(np.uint8).reshape(M, K // 32, 2)
+    raw[..., 2:] = q.view(np.uint8)
+    deq = q.astype(np.float32) * d.astype(np.float32)[..., None]
+    return raw.reshape(-1), deq.reshape(M, K)
+
+
+def oracle_fns():
+    L = O.lib()
+    for name, args in (("lno16_add_f32", [ctypes.c_void_p] * 2 + [ctypes.c_int64] * 2 + [ctypes.c_void_p]),
+                       ("lno16_mul_f32", [ctypes.c_void_p] * 2 + [ctypes.c_int64] * 2 + [ctypes.c_void_p]),
+                       ("lno16_swiglu_f32", [ctypes.c_void_p] * 2 + [ctypes.c_int64, ctypes.c_void_p]),
+                       ("lno16_rope_f32", [ctypes.c_void_p] * 2 + [ctypes.c_int64] * 3 +
+                        [ctypes.c_int, ctypes.c_int, ctypes.c_float, ctypes.c_void_p])):
+        fn = getattr(L, name)
+        fn.restype = None
+        fn.argtypes = args
+    return L
+
+
+def P(a):
+    return ctypes.c_void_p(a.ctypes.data)
+
+
+def binop(fn, a, b):
+    a = np.ascontiguousarray(a, np.float32)
+    b = np.ascontiguousarray(b, np.float32)
+    out = np.empty_like(a)
+    fn(P(a), P(b), a.size, b.size, P(out))
+    return out
+
+
+def run16(mode_name):
+    m = O.MODES[mode_name]
+    L = oracle_fns()
+    h = G.Host()
+    rng = np.random.default_rng(1234)
+    f32 = lambda *s, scale=1.0, loc=0.0: (rng.standard_normal(s) * scale + loc).astype(np.float32)
+    T, E, H, HKV, D, NKV = 3, 576, 9, 3, 64, 256
+    x0 = f32(T, E)
+    g = f32(E, scale=0.1, loc=1.0)
+    wqkv = f32(E + 2 * HKV * D, E, scale=0.02)
+    kc = (rng.standard_normal((HKV, NKV, D)) * 0.5).astype(np.float16)
+    pos = np.array([100, 101, 102], np.int32)
+    mask = np.zeros((4, NKV), np.float32)
+    for t in range(4):
+        mask[t, 101 + t:] = -np.inf
+    wq8_raw, wq8 = q8_0(f32(256, E, scale=0.02), rng)
+    bias = f32(T, 1)
+    x1 = f32(T, 1536)
+    w2 = (rng.standard_normal((E, 1536)) * 0.02).astype(np.float16)
+    z = f32(2, 5, 100, scale=3.0)
+
+    t = h.tensor
+    X0 = t([E, T], data=x0, name="inp")
+    Gw = t([E], data=g, weights=True, name="blk.0.attn_norm.weight")
+    WQKV = t([E, E + 2 * HKV * D], data=wqkv, weights=True, name="blk.0.attn_qkv.weight")
+    KC = t([D, NKV, HKV], "f16", data=kc, name="cache_k_l0")
+    POS = t([T], "i32", data=pos, name="inp_pos")
+    MASK = t([NKV, 4], data=mask, name="kq_mask")
+    WQ8 = t([E, 256], "q8_0", data=wq8_raw, weights=True, name="blk.0.ffn_up.weight")
+    BIAS = t([1, T], data=bias, name="bias")
+    X1 = t([1536, T], data=x1, name="ffn_inp")
+    W2 = t([1536, E], "f16", data=w2, weights=True, name="blk.0.ffn_down.weight")
+    Z = t([100, 5, 2], data=z, name="scores")
+    swi = h.stub.ggml_host_glu(b"SWIGLU")
+
+    nodes = {}
+    nodes["rms"] = t([E, T], op="RMS_NORM", src=(X0,), fparams={0: 1e-5}, name="norm-0")
+    nodes["mul"] = t([E, T], op="MUL", src=(nodes["rms"], Gw), name="attn_norm-0")
+    nodes["qkv"] = t([E + 2 * HKV * D, T], op="MUL_MAT", src=(WQKV, nodes["mul"]), name="qkv-0")
+    qv = t([D, H, T], op="VIEW", src=(nodes["qkv"],), data=nodes["qkv"].data,
+           nb=[4, D * 4, (E + 2 * HKV * D) * 4, (E + 2 * HKV * D) * 4 * T], name="q-0")
+    nodes["rope"] = t([D, H, T], op="ROPE", src=(qv, POS), params=(0, D, 0),
+                      fparams={5: 10000.0, 6: 1.0, 7: 0.0, 8: 1.0}, name="Qcur-0")
+    qp = t([D, T, H], op="PERMUTE", src=(nodes["rope"],), data=nodes["rope"].data,
+           nb=[4, D * H * 4, D * 4, D * H * T * 4], name="q-perm-0")
+    nodes["kq"] = t([NKV, T, H], op="MUL_MAT", src=(KC, qp), name="kq-0")
+    nodes["softmax"] = t([NKV, T, H], op="SOFT_MAX", src=(nodes["kq"], MASK), fparams={0: 0.125, 1: 0.0},
+                         name="kq_soft_max-0")
+    nodes["ug"] = t([256, T], op="MUL_MAT", src=(WQ8, nodes["mul"]), name="ffn_up-0")
+    nodes["swiglu"] = t([128, T], op="GLU", src=(nodes["ug"],), params=(swi, 0), name="ffn_swiglu-0")
+    ga = t([128, T], op="VIEW", src=(nodes["ug"],), data=nodes["ug"].data, nb=[4, 1024, 1024 * T, 1024 * T],
+           name="gate-0")
+    ua = t([128, T], op="VIEW", src=(nodes["ug"],), data=nodes["ug"].data + 512, nb=[4, 1024, 1024 * T, 1024 * T],
+           name="up-0")
+    nodes["swiglu_split"] = t([128, T], op="GLU", src=(ga, ua), params=(swi, 0), name="ffn_swiglu_split-0")
+    nodes["add"] = t([E, T], op="ADD", src=(X0, nodes["mul"]), name="ffn_inp-0")
+    nodes["add_bcast"] = t([E, T], op="ADD", src=(X0, BIAS), name="bias_add-0")
+    nodes["down"] = t([E, T], op="MUL_MAT", src=(W2, X1), name="ffn_out-0")
+    nodes["qkv_again"] = t([E + 2 * HKV * D, T], op="MUL_MAT", src=(WQKV, nodes["mul"]), name="qkv-1")
+    nodes["softmax_nomask"] = t([100, 5, 2], op="SOFT_MAX", src=(Z,), fparams={0: 1.0, 1: 0.0}, name="sm-1")
+    order = ["rms", "mul", "qkv", "view_q", "rope", "perm_q", "kq", "softmax", "ug", "swiglu", "view_g", "view_u",
+             "swiglu_split", "add", "add_bcast", "down", "qkv_again", "softmax_nomask"]
+    views = {"view_q": qv, "perm_q": qp, "view_g": ga, "view_u": ua}
+    graph = [views[k] if k in views else nodes[k] for k in order]
+
+    be = h.init()
+    if be is None:
+        print(json.dumps({"error": "no GPU: LNSHIP16 init returned NULL"}))
+        return 1
+    rc = h.compute(be, graph)
+    assert rc == 0, rc
+
+    # oracle, same op order (Monte draws in graph order)
+    O.monte_set(7)
+    want = {}
+    want["rms"] = O.rms_norm16(m, x0, 1e-5)
+    want["mul"] = binop(L.lno16_mul_f32, want["rms"], g)
+    want["qkv"] = O.mul_mat16(m, O.f2x16(wqkv), want["mul"])
+    q = np.ascontiguousarray(want["qkv"][:, :E].reshape(T, H, D))
+    want["rope"] = np.empty_like(q)
+    L.lno16_rope_f32(P(q), P(pos), T, H, D, D, 0, 10000.0, P(want["rope"]))
+    qperm = np.ascontiguousarray(want["rope"].transpose(1, 0, 2))
+    want["kq"] = O.mul_mat16_f32w(m, kc.astype(np.float32)[None], qperm[None], ne02=HKV)[0]
+    want["softmax"] = O.soft_max16(m, want["kq"], mask, 0.125)
+    want["ug"] = O.mul_mat16_f32w(m, wq8, want["mul"])
+    sw = np.empty((T, 128), np.float32)
+    gate, up = np.ascontiguousarray(want["ug"][:, :128]), np.ascontiguousarray(want["ug"][:, 128:])
+    L.lno16_swiglu_f32(P(gate), P(up), gate.size, P(sw))
+    want["swiglu"] = sw
+    want["swiglu_split"] = sw
+    want["add"] = binop(L.lno16_add_f32, x0, want["mul"])
+    want["add_bcast"] = binop(L.lno16_add_f32, x0, np.repeat(bias, E, axis=1))
+    want["down"] = O.mul_mat16_f32w(m, w2.astype(np.float32), x1)
+    want["qkv_again"] = O.mul_mat16(m, O.f2x16(wqkv), want["mul"])
+    want["softmax_nomask"] = O.soft_max16(m, z, None, 1.0)
+
+    report = {}
+    for k, tn in nodes.items():
+        got = h.f32_of(tn).reshape(want[k].shape)
+        bad = int(np.count_nonzero(got.view(np.uint32) != want[k].view(np.uint32)))
+        report[k] = bad
+    if O.MODES[mode_name] == O.MODES["monte"]:
+        s = ctypes.c_uint16()
+        h.lib.ggml_backend_lnship16_monte_get_state(ctypes.byref(s))
+        report["monte_state_matches"] = int(s.value == O.monte_get())
+    h.free(be)
+    print(json.dumps({"mode": mode_name, "mismatches": report}), flush=True)
+    ok = all(v == 0 for k, v in report.items() if k != "monte_state_matches")
+    return 0 if ok and report.get("monte_state_matches", 1) == 1 else 1
+
+
+def run32():
+    h = G.Host()
+    rng = np.random.default_rng(99)
+    f32 = lambda *s, scale=1.0: (rng.standard_normal(s) * scale).astype(np.float32)
+    T, K, M = 2, 2048, 512
+    x = f32(T, K)
+    w = f32(M, K, scale=0.02)
+    kq = f32(4, T, 200, scale=3.0)
+    mask = np.zeros((T, 200), np.float32)
+    mask[0, 150:] = -np.inf
+    t = h.tensor
+    X = t([K, T], data=x, name="inp")
+    W = t([K, M], data=w, weights=True, name="blk.0.ffn_up.weight")
+    KQ = t([200, T, 4], data=kq, name="kq")
+    MASK = t([200, T], data=mask, name="kq_mask")
+    nodes = {"rms": t([K, T], op="RMS_NORM", src=(X,), fparams={0: 1e-6}, name="norm-0"),
+             "mm": t([M, T], op="MUL_MAT", src=(W, X), name="ffn_up-0"),
+             "softmax": t([200, T, 4], op="SOFT_MAX", src=(KQ, MASK), fparams={0: 0.125, 1: 0.0}, name="sm-0")}
+    be = h.init(w32=True)
+    if be is None:
+        print(json.dumps({"error": "no GPU: LNSHIP32 init returned NULL"}))
+        return 1
+    assert h.compute(be, list(nodes.values())) == 0
+    want = {"rms": O.rms_norm32(x, 1e-6), "mm": O.mul_mat32(w, x), "softmax": O.soft_max32(kq, mask, 0.125)}
+    report = {}
+    for k, tn in nodes.items():
+        got = h.f32_of(tn).reshape(want[k].shape)
+        report[k] = int(np.count_nonzero(got.view(np.uint32) != want[k].view(np.uint32)))
+    h.free(be)
+    print(json.dumps({"mode": "lns32", "mismatches": report}), flush=True)
+    return 0 if all(v == 0 for v in report.values()) else 1
+
+
+if __name__ == "__main__":
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--mode", default="base")
+    ap.add_argument("--w32", action="store_true")
+    a = ap.parse_args()
+    sys.exit(run32() if a.w32 else run16(a.mode))

@@ -1,0 +1,146 @@
+/*
+ * ggml_host.c - TEST INFRASTRUCTURE: a stand-in for the ggml-base functions
+ * the LNSHIP ggml backends import (the list in
+ * xlns-ggml-backend_amd/csrc/ggml_abi.h), so tests can load
+ * libggml-lnship.so and drive it through its registry / device / backend
+ * vtables without a ggml build.  Its op and type numbering is its own: the
+ * backend matches ops and types by name only.
+ */
+#include "ggml_abi.h"
+
+#include <stdlib.h>
+#include <string.h>
+
+/* ---- ops -------------------------------------------------------------- */
+static const char *const k_ops[] = {"NONE", "DUP", "ADD", "MUL", "DIV", "SCALE", "RMS_NORM", "MUL_MAT", "SOFT_MAX",
+                                    "ROPE", "GLU", "UNARY", "RESHAPE", "VIEW", "PERMUTE", "TRANSPOSE", "GET_ROWS",
+                                    "CPY", "CONT", "SET_ROWS"};
+static const char *const k_glu[] = {"REGLU", "GEGLU", "SWIGLU"};
+static const char *const k_unary[] = {"ABS", "NEG", "TANH", "RELU", "GELU", "SILU"};
+#define N_OPS ((int)(sizeof k_ops / sizeof k_ops[0]))
+
+int ggml_host_op(const char *name) {
+    for (int i = 0; i < N_OPS; i++)
+        if (!strcmp(k_ops[i], name)) return i;
+    return -1;
+}
+int ggml_host_glu(const char *name) {
+    for (int i = 0; i < 3; i++)
+        if (!strcmp(k_glu[i], name)) return i;
+    return -1;
+}
+int ggml_host_unary(const char *name) {
+    for (int i = 0; i < 6; i++)
+        if (!strcmp(k_unary[i], name)) return i;
+    return -1;
+}
+
+const char *ggml_op_name(enum ggml_op op) { return (int)op >= 0 && (int)op < N_OPS ? k_ops[op] : "UNKNOWN"; }
+
+const char *ggml_op_desc(const struct ggml_tensor *t) {
+    const int op = (int)t->op;
+    if (op == ggml_host_op("GLU") && t->op_params[0] >= 0 && t->op_params[0] < 3) return k_glu[t->op_params[0]];
+    if (op == ggml_host_op("UNARY") && t->op_params[0] >= 0 && t->op_params[0] < 6) return k_unary[t->op_params[0]];
+    return ggml_op_name(t->op);
+}
+
+/* ---- types: f32, f16, q8_0 (block of 32 int8 + half scale), i32, lns16 --- */
+static float half_to_float(uint16_t h) {
+    const uint32_t s = (uint32_t)(h >> 15) << 31, e = (h >> 10) & 0x1f, m = h & 0x3ff;
+    uint32_t bits;
+    if (e == 0) {
+        if (m == 0) {
+            bits = s;
+        } else { /* subnormal: renormalise */
+            uint32_t mm = m, ee = 113;
+            while (!(mm & 0x400)) {
+                mm <<= 1;
+                ee--;
+            }
+            bits = s | (ee << 23) | ((mm & 0x3ff) << 13);
+        }
+    } else if (e == 31) {
+        bits = s | 0x7f800000u | (m << 13);
+    } else {
+        bits = s | ((e + 112) << 23) | (m << 13);
+    }
+    float f;
+    memcpy(&f, &bits, 4);
+    return f;
+}
+
+static void f16_to_float(const void *x, float *y, int64_t k) {
+    const uint16_t *h = (const uint16_t *)x;
+    for (int64_t i = 0; i < k; i++) y[i] = half_to_float(h[i]);
+}
+
+static void q8_0_to_float(const void *x, float *y, int64_t k) {
+    const uint8_t *b = (const uint8_t *)x;
+    for (int64_t i = 0; i < k / 32; i++, b += 34) {
+        uint16_t dh;
+        memcpy(&dh, b, 2);
+        const float d = half_to_float(dh);
+        for (int j = 0; j < 32; j++) y[i * 32 + j] = (float)(int8_t)b[2 + j] * d;
+    }
+}
+
+enum { T_F32 = 0, T_F16 = 1, T_Q8_0 = 8, T_I32 = 26, T_LNS16 = 43, T_COUNT = 44 };
+
+static struct ggml_type_traits k_traits[T_COUNT];
+
+static void init_traits(void) {
+    static int done = 0;
+    if (done) return;
+    done = 1;
+    for (int i = 0; i < T_COUNT; i++) k_traits[i].type_name = "unused";
+    k_traits[T_F32] = (struct ggml_type_traits){"f32", 1, 0, 4, false, NULL, NULL};
+    k_traits[T_F16] = (struct ggml_type_traits){"f16", 1, 0, 2, false, f16_to_float, NULL};
+    k_traits[T_Q8_0] = (struct ggml_type_traits){"q8_0", 32, 0, 34, true, q8_0_to_float, NULL};
+    k_traits[T_I32] = (struct ggml_type_traits){"i32", 1, 0, 4, false, NULL, NULL};
+    k_traits[T_LNS16] = (struct ggml_type_traits){"lns16", 1, 0, 2, false, NULL, NULL};
+}
+
+const struct ggml_type_traits *ggml_get_type_traits(enum ggml_type t) {
+    init_traits();
+    return &k_traits[(int)t];
+}
+const char *ggml_type_name(enum ggml_type t) { return ggml_get_type_traits(t)->type_name; }
+size_t ggml_type_size(enum ggml_type t) { return ggml_get_type_traits(t)->type_size; }
+int64_t ggml_blck_size(enum ggml_type t) { return ggml_get_type_traits(t)->blck_size; }
+
+/* ---- host buffers ------------------------------------------------------ */
+struct ggml_backend_buffer {
+    int usage;
+    void *base;
+    size_t size;
+};
+struct ggml_backend_buffer_type {
+    int tag;
+};
+static struct ggml_backend_buffer_type k_cpu_buft = {1};
+
+ggml_backend_buffer_type_t ggml_backend_cpu_buffer_type(void) { return &k_cpu_buft; }
+bool ggml_backend_buft_is_host(ggml_backend_buffer_type_t b) { return b == &k_cpu_buft; }
+
+ggml_backend_buffer_t ggml_backend_cpu_buffer_from_ptr(void *ptr, size_t size) {
+    struct ggml_backend_buffer *b = (struct ggml_backend_buffer *)calloc(1, sizeof *b);
+    b->base = ptr;
+    b->size = size;
+    return b;
+}
+
+enum ggml_backend_buffer_usage ggml_backend_buffer_get_usage(ggml_backend_buffer_t b) {
+    return (enum ggml_backend_buffer_usage)b->usage;
+}
+
+/* a buffer handle with the given usage (0 any, 1 weights, 2 compute) */
+ggml_backend_buffer_t ggml_host_buffer(int usage) {
+    struct ggml_backend_buffer *b = (struct ggml_backend_buffer *)calloc(1, sizeof *b);
+    b->usage = usage;
+    return b;
+}
+
+size_t ggml_host_sizeof_tensor(void) { return sizeof(struct ggml_tensor); }
+size_t ggml_host_offsetof_data(void) { return offsetof(struct ggml_tensor, data); }
+size_t ggml_host_offsetof_name(void) { return offsetof(struct ggml_tensor, name); }
+size_t ggml_host_offsetof_src(void) { return offsetof(struct ggml_tensor, src); }

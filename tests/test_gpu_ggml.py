@@ -1,0 +1,31 @@
+"""GPU parity of the ggml boundary: a graph run through libggml-lnship.so's
+graph_compute equals the oracle bit for bit on every node, in each xlns16
+summation mode and for LNSHIP32 (tests/ggml_graph_check.py; one process per
+mode because the backend reads GGML_LNS16_SUM once, as the reference builds
+one library per mode)."""
+import os
+import subprocess
+import sys
+
+import pytest
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+CHECK = os.path.join(HERE, "ggml_graph_check.py")
+
+
+def _run(args, env):
+    print("ggml_graph_check", *args, flush=True)
+    r = subprocess.run([sys.executable, "-u", CHECK] + args, env=env, capture_output=True, text=True, timeout=240)
+    print(r.stdout, r.stderr[-3000:], flush=True)
+    assert r.returncode == 0, r.stdout + r.stderr[-3000:]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("mode", ["base", "monte", "lpvip", "sum32"])
+def test_ggml_graph_lnship16(mode):
+    _run(["--mode", mode], dict(os.environ, GGML_LNS16_SUM=mode))
+
+
+@pytest.mark.gpu
+def test_ggml_graph_lnship32():
+    _run(["--w32"], dict(os.environ))

@@ -895,6 +895,11 @@ __global__ void k_causal_mask(const int32_t *__restrict__ pos0, int64_t ntok, in
 // ---- host helpers -------------------------------------------------------------
 
 template <int MODE>
+static int64_t max_row(int elem_bytes) {
+    return (k_lds_bytes - ((lds_tables_bytes<MODE>() + 15) & ~15) - 1024) / elem_bytes;
+}
+
+template <int MODE>
 static int rows_per_block(int64_t ncols, int elem_bytes) {
     const int64_t avail = k_lds_bytes - ((lds_tables_bytes<MODE>() + 15) & ~15) - 1024;
     int64_t rb = avail / std::max<int64_t>(1, ncols * elem_bytes);
@@ -1265,6 +1270,18 @@ int lnship32_soft_max(const lnship_soft_max_args *a, void *stream) {
                        (hipStream_t)stream, m, s->T);
     LNSHIP_HIP(hipGetLastError());
     return 0;
+}
+
+int64_t lnship_max_row(int which, int mode) {
+    if (which == 2 || which == 3) return max_row<LNSHIP_SUM32>(4);
+    if (which != 0 && which != 1) return 0;
+    switch (mode) {
+        case LNSHIP_BASE: return max_row<LNSHIP_BASE>(2);
+        case LNSHIP_MONTE: return max_row<LNSHIP_MONTE>(2);
+        case LNSHIP_LPVIP: return max_row<LNSHIP_LPVIP>(2);
+        case LNSHIP_SUM32: return max_row<LNSHIP_SUM32>(2);
+        default: return 0;
+    }
 }
 
 int lnship16_add(const float *a, const float *b, int64_t n, int64_t nb, float *dst, void *stream) {
