@@ -30,14 +30,79 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=120)
     ap.add_argument("--warmup", type=int, default=8)
-    ap.add_argument("--mode", default="sum32", choices=["base", "monte", "lpvip", "sum32"])
+    ap.add_argument("--mode", default="sum32", choices=["base", "monte", "lpvip", "sum32", "all"])
     ap.add_argument("--prompt", type=int, default=128)
     ap.add_argument("--cpu-tokens", type=int, default=3, help="decode tokens of the CPU baseline sample")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-graph", action="store_true", help="decode eagerly instead of replaying a HIP graph")
     ap.add_argument("--calib-copy", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB three times (HBM counter calibration)")
-    return ap.parse_args()
+    ap.add_argument("--ops", choices=["decode", "prefill", "all"],
+                    help="only time single ops (decode GEMVs, C5 prefill GEMM / rms_norm / soft_max), one JSON "
+                         "line each, in --mode (or every mode with --mode all)")
+    ap.add_argument("--reps", type=int, default=5, help="launches timed per op with --ops")
+    args, rest = ap.parse_known_args()
+    if rest:
+        ap.error("unrecognized arguments: %s" % " ".join(rest))
+    return args
+
+
+def _ops_modes(mode):
+    return ["base", "sum32", "monte", "lpvip"] if mode == "all" else [mode]
+
+
+def run_ops(args):
+    """Per-op timings on synthetic data (HIP events around back-to-back
+    launches on the current stream).  GEMVs report ns per dependent step,
+    K steps per output chain; C5 reports GMAC/s."""
+    import torch
+    import lnship
+    torch.cuda.set_device(0)
+    lnship.init()
+    gen = torch.Generator(device="cuda").manual_seed(0)
+    randn = lambda *s: torch.randn(*s, device="cuda", generator=gen)
+
+    def timed(fn, reps):
+        fn()
+        torch.cuda.synchronize()
+        s = torch.cuda.Event(enable_timing=True)
+        e = torch.cuda.Event(enable_timing=True)
+        s.record()
+        for _ in range(reps):
+            fn()
+        e.record()
+        e.synchronize()
+        return s.elapsed_time(e) * 1e3 / reps
+
+    def line(**kw):
+        print(json.dumps(kw), flush=True)
+
+    for mname in _ops_modes(args.mode):
+        m = lnship.MODES[mname]
+        if args.ops in ("decode", "all"):
+            # SmolLM2 decode shapes: qkv, o, up|gate, down, lm_head
+            for K, M in ((576, 960), (576, 576), (576, 3072), (1536, 576), (576, 49152)):
+                wp = lnship.pack16(randn(M, K) * 0.02)
+                x = randn(1, K)
+                us = timed(lambda: lnship.mul_mat16(m, wp, x, K, M), args.reps)
+                line(op="mul_mat", mode=mname, K=K, M=M, N=1, us=round(us, 2), ns_per_step=round(us * 1e3 / K, 2),
+                     gbs=round((2 * K * M + 4 * K + 4 * M) / us / 1e3, 3))
+            x = randn(1, 576)
+            us = timed(lambda: lnship.rms_norm16(m, x, 1e-5), args.reps)
+            line(op="rms_norm", mode=mname, rows=1, n=576, us=round(us, 2), ns_per_step=round(us * 1e3 / 576, 2))
+        if args.ops in ("prefill", "all"):
+            K, M, T = 2048, 8192, 512
+            wp = lnship.pack16(randn(M, K) * 0.02)
+            x = randn(T, K)
+            us = timed(lambda: lnship.mul_mat16(m, wp, x, K, M), max(1, args.reps // 2))
+            line(op="mul_mat", mode=mname, K=K, M=M, N=T, us=round(us, 2), gmacs=round(K * M * T / us / 1e3, 2))
+            x = randn(512, 2048)
+            us = timed(lambda: lnship.rms_norm16(m, x, 1e-5), args.reps)
+            line(op="rms_norm", mode=mname, rows=512, n=2048, us=round(us, 2))
+            s = randn(32, 512, 512) * 3
+            mask = torch.triu(torch.full((512, 512), float("-inf"), device="cuda"), 1)
+            us = timed(lambda: lnship.soft_max16(m, s, mask, 0.125), args.reps)
+            line(op="soft_max", mode=mname, heads=32, rows=512, n=512, us=round(us, 2))
 
 
 def calib_copy(mib):
@@ -59,7 +124,9 @@ def gemv_roofline(model, ln, torch, reps=4):
     `reps` times over into one HIP graph and times a replay between two HIP
     events on the replay stream.  Returns (algorithmic bytes per launch,
     average launch us, launches per token); a launch is one lnship16_mul_mat
-    call, i.e. the activation conversion kernel plus the GEMV kernel."""
+    call: one GEMV kernel when NC activation rows fit in LDS next to the
+    tables (every decode shape), else the activation conversion kernel plus
+    the GEMV kernel."""
     c = model.cfg
     calls = []
     orig = model._mm
@@ -153,6 +220,11 @@ def main():
     if args.calib_copy:
         calib_copy(args.calib_copy)
         return
+    if args.ops:
+        run_ops(args)
+        return
+    if args.mode == "all":
+        sys.exit("bench.py: --mode all is for --ops only")
     import numpy as np
     import torch
     import lnship
@@ -230,7 +302,8 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(achieved, 3), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 6), "traffic": traffic,
                      "traffic_source": traffic_src,
-                     "kernel": "lnship16_mul_mat decode launches (k_act + k_mm16<%s, NC=1>)" % args.mode,
+                     "kernel": "lnship16_mul_mat decode launches (k_mm16<%s, NC=1>, activations converted in-kernel)"
+                               % args.mode,
                      "launches_per_token": n_launch, "avg_launch_us": round(us_launch, 3),
                      "bytes_per_launch": int(b_launch)},
         "reference_published": {"rtx2050_sum32_decode_tok_s": 7.31,

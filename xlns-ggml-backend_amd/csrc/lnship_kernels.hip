@@ -226,7 +226,10 @@ struct red16<LNSHIP_BASE> {
     __device__ __forceinline__ void add_ls(acc_t &a, uint32_t tl, uint32_t ts, uint32_t &) const {
         const uint32_t d = absdiff(a.l, tl), mx = max(a.l, tl);
         const uint32_t usedb = a.s ^ ts;
-        const int32_t adj = *reinterpret_cast<const int16_t *>(g + ((min(d, (uint32_t)k16_esszer + 1) << 2) | (usedb >> 14)));
+        // the sign picks the pair half off the critical path: the address is
+        // then one shift-add of the clamped distance
+        const char *gs = g + (usedb >> 14);
+        const int32_t adj = *reinterpret_cast<const int16_t *>(gs + (min(d, (uint32_t)k16_esszer + 1) << 2));
         const uint32_t ns = a.l > tl ? a.s : ts;
         a.l = (uint32_t)min(max((int32_t)mx + adj, 0), (int32_t)k16_logmask);
         a.s = (d == 0 && usedb) ? 0u : ns;
@@ -244,7 +247,8 @@ struct red16<LNSHIP_MONTE> {
         st = lfsr_step(st);
         const uint32_t d = absdiff(a.l, tl), mx = max(a.l, tl);
         const uint32_t usedb = a.s ^ ts;
-        const int32_t f = gm[(min(d, (uint32_t)k16_esszer + 1) << 1) | (usedb >> 15)];
+        const int32_t *gms = gm + (usedb >> 15);
+        const int32_t f = gms[min(d, (uint32_t)k16_esszer + 1) << 1];
         const int32_t adj = (f + (int32_t)(st & 0xffu)) >> 8;
         const uint32_t ns = a.l > tl ? a.s : ts;
         a.l = (uint32_t)min(max((int32_t)mx + adj, 0), (int32_t)k16_logmask);
@@ -254,13 +258,15 @@ struct red16<LNSHIP_MONTE> {
     __device__ __forceinline__ uint32_t finish(const acc_t &a) const { return a.s | a.l; }
 };
 
-// xlns32 addition, branch-free: the interpolated sb / db and the
-// cotransformation are both evaluated and selected (T is the LDS copy of the
-// tables with the db-at-zero entry set to a sentinel).
-__device__ __forceinline__ int32_t interp_sel(const int32_t *T, uint32_t dc, bool hi, int base_lo, int base_hi) {
-    const int sh = hi ? k32_sb_fsh : k32_sb_sh;   // both grids: 2^13 / 2^19
-    const int i = (int)(dc >> sh) + (hi ? base_hi : base_lo);
-    const int32_t f = (int32_t)(dc & ((1u << sh) - 1u) & 0x7ffffu);
+// xlns32 addition, branch-free.  T is the LDS copy of the adder tables with
+// two changes made at staging: the db-at-zero entry holds a sentinel (exact
+// cancellation clamps the log to 0), and each dhi[dh] holds
+// (dh << 12) + dhi[dh].  The direct sb / db interpolation and the first
+// cotransformation lookups are independent reads issued together; only the
+// cotransformation's sb(e) needs a second round trip to LDS.  Every select
+// is arithmetic: a ternary around two table reads would compile to a
+// divergent branch that serialises both reads.
+__device__ __forceinline__ int32_t interp_at(const int32_t *T, int i, int32_t f, int sh) {
     const int32_t t0 = T[i], t1 = T[i + 1];
     // |t1 - t0| < 2^23 and f < 2^19: a full-rate 24-bit multiply
     return t0 + (mul_i24(t1 - t0, f) >> sh);
@@ -269,24 +275,47 @@ __device__ __forceinline__ int32_t interp_sel(const int32_t *T, uint32_t dc, boo
 __device__ __forceinline__ void x32_add_ls(const int32_t *T, acc_ls &a, uint32_t tl, uint32_t ts) {
     const uint32_t d = absdiff(a.l, tl), mx = max(a.l, tl);
     const bool usedb = (a.s ^ ts) != 0;
-    // direct: sb below / above 12 binades, db (>= 2 binades) below / above 8
+    // direct: sb below / above 12 binades, db (>= 2 binades) below / above 8;
+    // both tables use 2^13 / 2^19 grids
+    const uint32_t lim = usedb ? k32_db_end : k32_sb_end;
+    const int base_lo = usedb ? k32_off_db - k32_db_first : k32_off_sb;
+    const int base_hi = usedb ? k32_off_dbf - (int)(k32_db_end >> k32_db_fsh) : k32_off_sbf - (int)(k32_sb_end >> k32_sb_fsh);
     const uint32_t dc = min(d, k32_esszer - 1);
-    const bool hi = dc >= (usedb ? k32_db_end : k32_sb_end);
-    const int32_t adj_d = usedb ? interp_sel(T, dc, hi, k32_off_db - k32_db_first, k32_off_dbf - (int)(k32_db_end >> k32_db_fsh))
-                                : interp_sel(T, dc, hi, k32_off_sb, k32_off_sbf - (int)(k32_sb_end >> k32_sb_fsh));
+    const bool hi = dc >= lim;
+    const int sh = hi ? k32_sb_fsh : k32_sb_sh;
+    const int i = (int)(dc >> sh) + (hi ? base_hi : base_lo);
+    const int32_t f = (int32_t)(dc & ((1u << sh) - 1u));
     // cotransformation below 2 binades: 1 - 2^-d = (1 - 2^-dh) + 2^-dh (1 - 2^-dl)
     const uint32_t dl = d & ((1u << k32_co_sh) - 1u), dh = (d >> k32_co_sh) & ((1u << k32_co_sh) - 1u);
-    const int32_t lo = T[k32_off_dlo + dl], th = T[k32_off_dhi + dh];
-    const uint32_t e = (dh << k32_co_sh) - (uint32_t)lo + (uint32_t)th;
-    const uint32_t ec = min(e, k32_esszer - 1);
-    int32_t sbe = interp_sel(T, ec, ec >= k32_sb_end, k32_off_sb, k32_off_sbf - (int)(k32_sb_end >> k32_sb_fsh));
-    sbe = e < k32_esszer ? sbe : 0;
-    const int32_t cot = dh == 0 ? lo : (dl == 0 ? th : th + sbe);
-    int32_t adj = (usedb && d < k32_co_end) ? cot : (d < k32_esszer ? adj_d : 0);
-    const int32_t r = max(__builtin_elementwise_add_sat((int32_t)mx, adj), 0);
+    const int32_t lo = T[k32_off_dlo + dl], th2 = T[k32_off_dhi + dh];
+    const int32_t adj_d = interp_at(T, i, f, sh);
+    // second round trip: sb(e), e = (dh << 12) - lo + dhi[dh]; the far sb
+    // table's last node (e = esszer) is 0, which is sb beyond esszer
+    const uint32_t e = (uint32_t)th2 - (uint32_t)lo;   // wraps for the dl = 0 sentinel (unused then)
+    const uint32_t ec = min(e, k32_esszer);
+    const bool hi2 = ec >= k32_sb_end;
+    const int sh2 = hi2 ? k32_sb_fsh : k32_sb_sh;
+    const int i2 = (int)(ec >> sh2) + (hi2 ? k32_off_sbf - (int)(k32_sb_end >> k32_sb_fsh) : k32_off_sb);
+    const int32_t sbe = interp_at(T, i2, (int32_t)(ec & ((1u << sh2) - 1u)), sh2);
+    const int32_t th = th2 - (int32_t)(dh << k32_co_sh);
+    // everything but the sb(e) branch of the cotransformation is ready
+    // before sb(e) returns
+    const bool co = usedb && d < k32_co_end;
+    const int32_t adj_other = co ? (dh == 0 ? lo : th) : (d < k32_esszer ? adj_d : 0);
+    const bool use_sbe = co && dh != 0 && dl != 0;
+    const int32_t r_other = max(__builtin_elementwise_add_sat((int32_t)mx, adj_other), 0);
+    // db < 0 here, so mx + th + sbe cannot overflow
+    const int32_t r_sbe = max((int32_t)mx + th + sbe, 0);
     const uint32_t ns = a.l > tl ? a.s : ts;
-    a.l = (uint32_t)r;
+    a.l = (uint32_t)(use_sbe ? r_sbe : r_other);
     a.s = (d == 0 && usedb) ? 0u : ns;
+}
+
+// A whole xlns32 addition on packed values (sign bit 31) over the LDS tables.
+__device__ __forceinline__ uint32_t x32_add_lds(const int32_t *T, uint32_t x, uint32_t y) {
+    acc_ls a{x & k32_logmask, x & k32_sign};
+    x32_add_ls(T, a, y & k32_logmask, y & k32_sign);
+    return a.s | a.l;
 }
 
 template <>
@@ -387,6 +416,8 @@ __device__ __forceinline__ red16<LNSHIP_SUM32> stage_tables<LNSHIP_SUM32>(const 
     for (int i = (k32_tab_n / 4) * 4 + threadIdx.x; i < k32_tab_n; i += blockDim.x) t[i] = T.tab32[i];
     __syncthreads();
     if (threadIdx.x == 0) t[k32_off_dlo] = -0x7fffffff;   // db at d = 0: exact cancellation
+    // dhi[dh] -> (dh << 12) + dhi[dh], the first half of the cotransformation's e
+    for (int i = 1 + threadIdx.x; i < k32_co_n; i += blockDim.x) t[k32_off_dhi + i] += i << k32_co_sh;
     return red16<LNSHIP_SUM32>{t};
 }
 template <>
@@ -403,36 +434,55 @@ constexpr int lds_tables_bytes() {
 
 // ---- MUL_MAT ------------------------------------------------------------------
 // One lane per weight row m and NC activation columns n (NC independent
-// accumulations interleaved for latency hiding).  xs holds the converted
-// activations [slice][N][Kp]; their index is uniform across the wave, so the
-// compiler fetches them through the scalar cache.  The weights of the next PF
-// groups of eight k are in flight while a group is accumulated.
+// accumulations interleaved for latency hiding).  With XL the workgroup first
+// converts its NC activation rows into LDS (F32 -> xlns16 through the
+// conversion table) and lanes read them back with wave-uniform 16-byte LDS
+// reads; without XL (rows too long for LDS) k_act has converted them into xs
+// [slice][N][Kp] and they come from global memory through vector loads.  A
+// wave-uniform global load would otherwise become a scalar load, and since
+// scalar loads and LDS reads share one completion counter (and scalar loads
+// return out of order) every table read would then also wait for it.  The
+// weights (and activations) of the next PF groups of eight k are in flight
+// while a group is accumulated.
 
 struct mm_args16 {
     const uint16_t *w;
-    const uint16_t *x;
+    const uint16_t *x;    // converted activations [slice][N][Kp] (without XL)
+    const float *xf;      // F32 activations (XL): row n of slice z at z * x_slice + n * x_ld
     float *dst;
     int64_t K, kp, M, N;
+    int64_t x_ld, x_slice;
     int64_t ne02, ne12, r2, r3;
     int64_t w_mstride, w_slice, dst_ld, dst_slice;
     uint32_t seed;
 };
 
+template <int MODE>
+constexpr int mm_xl_offset() { return (lds_tables_bytes<MODE>() + 15) & ~15; }
+
 __device__ __forceinline__ uint32_t half16(uint32_t w, int hi) { return hi ? (w >> 16) : (w & 0xffffu); }
 
-template <int MODE, int NC, int PF>
+template <int MODE, int NC, int PF, bool XL>
 __global__ __launch_bounds__(k_block) void k_mm16(mm_args16 a, dev_tables T) {
     extern __shared__ __align__(16) char lds[];
     const red16<MODE> R = stage_tables<MODE>(T, lds);
-    __syncthreads();
-
-    const int64_t m = (int64_t)blockIdx.x * k_block + threadIdx.x;
-    if (m >= a.M) return;
     const int64_t n0 = (int64_t)blockIdx.y * NC;
     const int64_t z = blockIdx.z;
     const int64_t i12 = z % a.ne12, i13 = z / a.ne12;
     const int nc = (int)min<int64_t>(NC, a.N - n0);
+    const int kp = (int)a.kp;
+    uint16_t *xl = reinterpret_cast<uint16_t *>(lds + mm_xl_offset<MODE>());
+    if (XL) {
+        // columns past N and k past K hold xlns16 zero
+        const float *xf = a.xf + z * a.x_slice + n0 * a.x_ld;
+        for (int j = 0; j < NC; j++)
+            for (int k = threadIdx.x; k < kp; k += k_block)
+                xl[j * kp + k] = (j < nc && k < a.K) ? (uint16_t)x16_from_f32(T.cvt16, xf[j * a.x_ld + k]) : (uint16_t)0;
+    }
+    __syncthreads();
 
+    const int64_t m = (int64_t)blockIdx.x * k_block + threadIdx.x;
+    if (m >= a.M) return;
     const uint16_t *ws = a.w + ((i13 / a.r3) * a.ne02 + i12 / a.r2) * a.w_slice + m * 8;
     const uint16_t *xs = a.x + (z * a.N + n0) * a.kp;
     const int64_t wstride = a.w_mstride * 8;   // between consecutive groups of 8 k
@@ -454,10 +504,19 @@ __global__ __launch_bounds__(k_block) void k_mm16(mm_args16 a, dev_tables T) {
     }
     const int K = (int)a.K;
     const int full = K >> 3, tail = K & 7;
-    const int kp = (int)a.kp;
-    auto load_w = [&](int g) { return *reinterpret_cast<const uint4 *>(ws + (int64_t)g * wstride); };
+    // Prefetches past the last group reload the last group: every load is
+    // unconditional, so the compiler can count outstanding loads exactly and
+    // wait only for the one a step needs.
+    const int last = (kp >> 3) - 1;
+    auto load_w = [&](int g) { return *reinterpret_cast<const uint4 *>(ws + (int64_t)min(g, last) * wstride); };
     auto load_x = [&](int j, int g) {
-        return *reinterpret_cast<const uint4 *>(xs + (j < nc ? j : 0) * kp + g * 8);
+        // the offset goes through a vector register: the value then counts as
+        // per-lane, so a global read is a vector load (not a scalar one) and an
+        // LDS read is waited for where it is used, not copied to scalar
+        // registers as soon as it is issued
+        int64_t off = (int64_t)(XL || j < nc ? j : 0) * kp + (int64_t)min(g, last) * 8;
+        asm("" : "+v"(off));
+        return *reinterpret_cast<const uint4 *>((XL ? xl : xs) + off);
     };
     // steps [u0, u1) of a group: the product (xlns16_mul: log fields added
     // and clamped, signs xor'ed), then one reduction step per column
@@ -486,35 +545,31 @@ __global__ __launch_bounds__(k_block) void k_mm16(mm_args16 a, dev_tables T) {
 #pragma unroll
         for (int j = 0; j < NC; j++) xq[j] = load_x(j, 0);
         const uint4 wq = load_w(0);
-        uint4 ring[PF], xring[PF][NC];
-#pragma unroll
-        for (int p = 0; p < PF; p++)
-            if (1 + p < full) {
-                ring[p] = load_w(1 + p);
-#pragma unroll
-                for (int j = 0; j < NC; j++) xring[p][j] = load_x(j, 1 + p);
-            }
-        steps(wq, xq, -1, full > 0 ? 8 : tail);
-        // groups 1 .. full-1, PF of them in flight
-        int g = 1;
-        for (; g + PF <= full; g += PF) {
+        // groups 1 .. full-1 in blocks of PF, double-buffered: the loads of
+        // block b + 1 are issued together before block b is accumulated
+        uint4 wa[PF], wb[PF], xa[PF][NC], xb[PF][NC];
+        auto load_block = [&](uint4 (&w)[PF], uint4 (&x)[PF][NC], int g0) {
 #pragma unroll
             for (int p = 0; p < PF; p++) {
-                const uint4 cw = ring[p];
-                uint4 cx[NC];
+                w[p] = load_w(g0 + p);
 #pragma unroll
-                for (int j = 0; j < NC; j++) cx[j] = xring[p][j];
-                if (g + p + PF < full) {
-                    ring[p] = load_w(g + p + PF);
-#pragma unroll
-                    for (int j = 0; j < NC; j++) xring[p][j] = load_x(j, g + p + PF);
-                }
-                steps(cw, cx, 0, 8);
+                for (int j = 0; j < NC; j++) x[p][j] = load_x(j, g0 + p);
             }
-        }
+        };
+        auto run_block = [&](const uint4 (&w)[PF], const uint4 (&x)[PF][NC], int g0) {
 #pragma unroll
-        for (int p = 0; p < PF; p++)
-            if (g + p < full) steps(ring[p], xring[p], 0, 8);
+            for (int p = 0; p < PF; p++)
+                if (g0 + p < full) steps(w[p], x[p], 0, 8);
+        };
+        load_block(wa, xa, 1);
+        steps(wq, xq, -1, full > 0 ? 8 : tail);
+        for (int g = 1; g < full; g += 2 * PF) {
+            load_block(wb, xb, g + PF);
+            run_block(wa, xa, g);
+            if (g + PF >= full) break;
+            load_block(wa, xa, g + 2 * PF);
+            run_block(wb, xb, g + PF);
+        }
         if (full > 0 && tail > 0) {
             uint4 tx[NC];
 #pragma unroll
@@ -644,9 +699,9 @@ __global__ __launch_bounds__(k_block) void k_rms32(const float *__restrict__ src
         const int r = threadIdx.x;
         const uint32_t *row = sq + (int64_t)r * ncols;
         uint32_t acc = 0;
-        for (int64_t i = 0; i < ncols; i++) acc = x32_add(R.T, acc, row[i]);
+        for (int64_t i = 0; i < ncols; i++) acc = x32_add_lds(R.T, acc, row[i]);
         const uint32_t mean = x32_mul(acc, x32_from_f32(1.0f / (float)ncols));
-        s_inv[r] = x32_recip(x32_sqrt(x32_add(R.T, mean, x32_from_f32(eps))));
+        s_inv[r] = x32_recip(x32_sqrt(x32_add_lds(R.T, mean, x32_from_f32(eps))));
     }
     __syncthreads();
     for (int64_t e = threadIdx.x; e < ne; e += blockDim.x) {
@@ -753,7 +808,7 @@ __global__ __launch_bounds__(k_block) void k_softmax32(sm_args a, dev_tables T) 
                 const float mf = mask_row(a, r0 + r)[i];
                 const uint32_t mk = mf <= -3.0e38f ? 0xffffffffu : x32_from_f32(mf);
                 if (mk == 0xffffffffu) v = 0xffffffffu;
-                else if (mk & k32_logmask) v = x32_add(R.T, v, mk);
+                else if (mk & k32_logmask) v = x32_add_lds(R.T, v, mk);
             }
         }
         c[e] = v;
@@ -764,7 +819,7 @@ __global__ __launch_bounds__(k_block) void k_softmax32(sm_args a, dev_tables T) 
         const int r = (int)(e / a.n);
         const int32_t cm = s_max[r];
         const uint32_t mx = (uint32_t)(cm < 0 ? (cm ^ 0x7fffffff) : cm);
-        const float fv = x32_to_f32(x32_add(R.T, c[e], mx ^ k32_sign));
+        const float fv = x32_to_f32(x32_add_lds(R.T, c[e], mx ^ k32_sign));
         c[e] = x32_from_f32((float)exp((double)fv));
     }
     __syncthreads();
@@ -772,7 +827,7 @@ __global__ __launch_bounds__(k_block) void k_softmax32(sm_args a, dev_tables T) 
         const int r = threadIdx.x;
         const uint32_t *row = c + (int64_t)r * a.n;
         uint32_t acc = row[0];
-        for (int64_t i = 1; i < a.n; i++) acc = x32_add(R.T, acc, row[i]);
+        for (int64_t i = 1; i < a.n; i++) acc = x32_add_lds(R.T, acc, row[i]);
         s_tot[r] = acc;
     }
     __syncthreads();
@@ -943,24 +998,48 @@ static int check_mm(const lnship_mul_mat_args *a) {
     return 0;
 }
 
-template <int MODE, int NC>
+// NC columns per lane for N activation columns
+static int mm16_nc(int64_t N) { return N >= 8 ? 8 : (N >= 4 ? 4 : 1); }
+
+template <int MODE>
+static bool mm16_xl_fits(int nc, int64_t kp) {
+    return mm_xl_offset<MODE>() + (int64_t)nc * kp * 2 <= k_lds_bytes - 1024;
+}
+
+static bool mm16_xl(int mode, int nc, int64_t kp) {
+    switch (mode) {
+        case LNSHIP_BASE: return mm16_xl_fits<LNSHIP_BASE>(nc, kp);
+        case LNSHIP_MONTE: return mm16_xl_fits<LNSHIP_MONTE>(nc, kp);
+        case LNSHIP_LPVIP: return mm16_xl_fits<LNSHIP_LPVIP>(nc, kp);
+        default: return mm16_xl_fits<LNSHIP_SUM32>(nc, kp);
+    }
+}
+
+template <int MODE, int NC, bool XL>
 static int launch_mm16(const mm_args16 &m, const dev_tables &T, int64_t nslices, hipStream_t st) {
-    constexpr int PF = NC == 1 ? 4 : (NC <= 4 ? 2 : 1);
-    constexpr int lds = lds_tables_bytes<MODE>();
+    constexpr int PF = NC == 1 ? 8 : (NC <= 4 ? 2 : 1);
+    const int lds = mm_xl_offset<MODE>() + (XL ? (int)(NC * m.kp * 2) : 0);
     if (lds > 64 * 1024)
-        if (int rc = set_lds(k_mm16<MODE, NC, PF>, lds)) return rc;
+        if (int rc = set_lds(k_mm16<MODE, NC, PF, XL>, lds)) return rc;
     dim3 grid((unsigned)((m.M + k_block - 1) / k_block), (unsigned)((m.N + NC - 1) / NC), (unsigned)nslices);
     if (grid.x > 2147483647u || grid.y > 65535u) return fail(LNSHIP_ERANGE, "mul_mat: grid too large%s");
-    hipLaunchKernelGGL((k_mm16<MODE, NC, PF>), grid, dim3(k_block), lds, st, m, T);
+    hipLaunchKernelGGL((k_mm16<MODE, NC, PF, XL>), grid, dim3(k_block), lds, st, m, T);
     LNSHIP_HIP(hipGetLastError());
     return 0;
 }
 
+template <int MODE, int NC>
+static int launch_mm16_x(const mm_args16 &m, const dev_tables &T, int64_t nslices, bool xl, hipStream_t st) {
+    return xl ? launch_mm16<MODE, NC, true>(m, T, nslices, st) : launch_mm16<MODE, NC, false>(m, T, nslices, st);
+}
+
 template <int MODE>
-static int dispatch_mm16(const mm_args16 &m, const dev_tables &T, int64_t nslices, hipStream_t st) {
-    if (m.N >= 8) return launch_mm16<MODE, 8>(m, T, nslices, st);
-    if (m.N >= 4) return launch_mm16<MODE, 4>(m, T, nslices, st);
-    return launch_mm16<MODE, 1>(m, T, nslices, st);
+static int dispatch_mm16(const mm_args16 &m, const dev_tables &T, int64_t nslices, bool xl, hipStream_t st) {
+    switch (mm16_nc(m.N)) {
+        case 8: return launch_mm16_x<MODE, 8>(m, T, nslices, xl, st);
+        case 4: return launch_mm16_x<MODE, 4>(m, T, nslices, xl, st);
+        default: return launch_mm16_x<MODE, 1>(m, T, nslices, xl, st);
+    }
 }
 
 template <int NC>
@@ -1151,27 +1230,32 @@ int lnship16_mul_mat(int mode, const lnship_mul_mat_args *a, void *stream) {
     if (a->K > (int64_t)1 << 30) return fail(LNSHIP_ERANGE, "mul_mat: K beyond 2^30%s");
     const int64_t nslices = a->ne12 * a->ne13;
     const int64_t kp = (a->K + 7) & ~(int64_t)7;
-    void *xs = nullptr;
-    if (int rc = scratch(s, (size_t)std::max<int64_t>(1, nslices * a->N * kp) * 2, &xs)) return rc;
+    const int64_t xld = a->x_ld ? a->x_ld : a->K;
+    const int64_t xslice = a->x_slice ? a->x_slice : a->N * xld;
     hipStream_t st = (hipStream_t)stream;
-    if (kp > 0) {
-        dim3 g(grid_for(a->N * kp, 2), (unsigned)nslices);
-        hipLaunchKernelGGL(k_act<0>, g, dim3(k_block), 0, st, a->x, a->x_ld ? a->x_ld : a->K,
-                           a->x_slice ? a->x_slice : a->N * (a->x_ld ? a->x_ld : a->K), xs, a->N, a->K, kp,
-                           s->T.cvt16);
-        LNSHIP_HIP(hipGetLastError());
+    // activations converted inside the GEMV when NC rows fit in LDS next to
+    // the tables, else by k_act into scratch first
+    const bool xl = mm16_xl(mode, mm16_nc(a->N), kp);
+    void *xs = nullptr;
+    if (!xl) {
+        if (int rc = scratch(s, (size_t)std::max<int64_t>(1, nslices * a->N * kp) * 2, &xs)) return rc;
+        if (kp > 0) {
+            dim3 g(grid_for(a->N * kp, 2), (unsigned)nslices);
+            hipLaunchKernelGGL(k_act<0>, g, dim3(k_block), 0, st, a->x, xld, xslice, xs, a->N, a->K, kp, s->T.cvt16);
+            LNSHIP_HIP(hipGetLastError());
+        }
     }
     const int64_t wms = a->w_mstride ? a->w_mstride : a->M;
     const int64_t dld = a->dst_ld ? a->dst_ld : a->M;
-    mm_args16 m{(const uint16_t *)a->w, (const uint16_t *)xs, a->dst, a->K, kp, a->M, a->N,
+    mm_args16 m{(const uint16_t *)a->w, (const uint16_t *)xs, a->x, a->dst, a->K, kp, a->M, a->N, xld, xslice,
                 a->ne02, a->ne12, a->ne12 / a->ne02, a->ne13 / a->ne03,
                 wms, a->w_slice ? a->w_slice : kp * wms, dld, a->dst_slice ? a->dst_slice : a->N * dld,
                 a->monte_seed};
     switch (mode) {
-        case LNSHIP_BASE: return dispatch_mm16<LNSHIP_BASE>(m, s->T, nslices, st);
-        case LNSHIP_MONTE: return dispatch_mm16<LNSHIP_MONTE>(m, s->T, nslices, st);
-        case LNSHIP_LPVIP: return dispatch_mm16<LNSHIP_LPVIP>(m, s->T, nslices, st);
-        default: return dispatch_mm16<LNSHIP_SUM32>(m, s->T, nslices, st);
+        case LNSHIP_BASE: return dispatch_mm16<LNSHIP_BASE>(m, s->T, nslices, xl, st);
+        case LNSHIP_MONTE: return dispatch_mm16<LNSHIP_MONTE>(m, s->T, nslices, xl, st);
+        case LNSHIP_LPVIP: return dispatch_mm16<LNSHIP_LPVIP>(m, s->T, nslices, xl, st);
+        default: return dispatch_mm16<LNSHIP_SUM32>(m, s->T, nslices, xl, st);
     }
 }
 
