@@ -211,6 +211,20 @@ __device__ __forceinline__ int32_t mul_i24(int32_t a, int32_t b) {
     return r;
 }
 
+// (a << 2) + b in one instruction (LDS byte address of entry a from origin b)
+__device__ __forceinline__ uint32_t lshl2_add(uint32_t a, uint32_t b) {
+    uint32_t r;
+    asm("v_lshl_add_u32 %0, %1, 2, %2" : "=v"(r) : "v"(a), "v"(b));
+    return r;
+}
+
+// LDS addresses as 32-bit integers: a table lookup is then a shift-add of the
+// index onto a precomputed origin and the read itself, with no separate add
+// of the shared-memory base on the dependent chain.
+typedef const int32_t __attribute__((address_space(3))) *lds_i32_t;
+__device__ __forceinline__ uint32_t lds_addr(const void *p) { return (uint32_t)(uintptr_t)(lds_i32_t)p; }
+__device__ __forceinline__ int32_t lds_ld(uint32_t addr) { return *(lds_i32_t)(uintptr_t)addr; }
+
 struct acc_ls {
     uint32_t l, s;   // log field, sign bit in place
 };
@@ -266,67 +280,89 @@ struct red16<LNSHIP_MONTE> {
 // cotransformation's sb(e) needs a second round trip to LDS.  Every select
 // is arithmetic: a ternary around two table reads would compile to a
 // divergent branch that serialises both reads.
-__device__ __forceinline__ int32_t interp_at(const int32_t *T, int i, int32_t f, int sh) {
-    const int32_t t0 = T[i], t1 = T[i + 1];
-    // |t1 - t0| < 2^23 and f < 2^19: a full-rate 24-bit multiply
-    return t0 + (mul_i24(t1 - t0, f) >> sh);
+
+// Byte offsets of the interpolation tables in the LDS copy, each less its
+// grid origin, so that a distance x on grid shift sh reads node
+// (x >> sh) at origin + ((x >> sh) << 2).
+constexpr uint32_t kb_sb = (uint32_t)k32_off_sb * 4;
+constexpr uint32_t kb_sbf = (uint32_t)(k32_off_sbf - (int)(k32_sb_end >> k32_sb_fsh)) * 4;
+constexpr uint32_t kb_db = (uint32_t)(k32_off_db - k32_db_first) * 4;
+constexpr uint32_t kb_dbf = (uint32_t)(k32_off_dbf - (int)(k32_db_end >> k32_db_fsh)) * 4;
+
+// LDS byte addresses of the adder's tables (interpolation tables less their
+// grid origin), computed once per kernel; the empty asm keeps them opaque
+// registers, so that picking a table is one select and no base add follows.
+struct x32_tab {
+    uint32_t dlo, dhi, sb, sbf, db, dbf;
+};
+__device__ __forceinline__ x32_tab x32_origins(const int32_t *T) {
+    uint32_t tb = lds_addr(T);
+    asm("" : "+v"(tb));
+    return {tb + (uint32_t)k32_off_dlo * 4, tb + (uint32_t)k32_off_dhi * 4, tb + kb_sb, tb + kb_sbf, tb + kb_db,
+            tb + kb_dbf};
 }
 
-__device__ __forceinline__ void x32_add_ls(const int32_t *T, acc_ls &a, uint32_t tl, uint32_t ts) {
+__device__ __forceinline__ void x32_add_ls(const x32_tab &O, acc_ls &a, uint32_t tl, uint32_t ts) {
     const uint32_t d = absdiff(a.l, tl), mx = max(a.l, tl);
-    const bool usedb = (a.s ^ ts) != 0;
-    // direct: sb below / above 12 binades, db (>= 2 binades) below / above 8;
-    // both tables use 2^13 / 2^19 grids
-    const uint32_t lim = usedb ? k32_db_end : k32_sb_end;
-    const int base_lo = usedb ? k32_off_db - k32_db_first : k32_off_sb;
-    const int base_hi = usedb ? k32_off_dbf - (int)(k32_db_end >> k32_db_fsh) : k32_off_sbf - (int)(k32_sb_end >> k32_sb_fsh);
-    const uint32_t dc = min(d, k32_esszer - 1);
-    const bool hi = dc >= lim;
-    const int sh = hi ? k32_sb_fsh : k32_sb_sh;
-    const int i = (int)(dc >> sh) + (hi ? base_hi : base_lo);
-    const int32_t f = (int32_t)(dc & ((1u << sh) - 1u));
-    // cotransformation below 2 binades: 1 - 2^-d = (1 - 2^-dh) + 2^-dh (1 - 2^-dl)
+    const bool usedb = a.s != ts;
+    // Three exclusive cases: sb(d) for equal signs; db(d) from its tables at
+    // and above 2 binades; below 2 binades the cotransformation
+    //   1 - 2^-d = (1 - 2^-dh) + 2^-dh (1 - 2^-dl),  d = (dh << 12) + dl,
+    // which is dlo[dl] when dh = 0, dhi[dh] when dl = 0, and otherwise
+    // dhi[dh] + sb(e) with e = (dh << 12) - dlo[dl] + dhi[dh].  A lane needs
+    // at most one interpolation, so all lanes share one: at e on the sb
+    // tables for the last case, at d on the sb or db tables otherwise.  It
+    // follows the cotransformation's lookups, which every lane makes.
     const uint32_t dl = d & ((1u << k32_co_sh) - 1u), dh = (d >> k32_co_sh) & ((1u << k32_co_sh) - 1u);
-    const int32_t lo = T[k32_off_dlo + dl], th2 = T[k32_off_dhi + dh];
-    const int32_t adj_d = interp_at(T, i, f, sh);
-    // second round trip: sb(e), e = (dh << 12) - lo + dhi[dh]; the far sb
-    // table's last node (e = esszer) is 0, which is sb beyond esszer
-    const uint32_t e = (uint32_t)th2 - (uint32_t)lo;   // wraps for the dl = 0 sentinel (unused then)
-    const uint32_t ec = min(e, k32_esszer);
-    const bool hi2 = ec >= k32_sb_end;
-    const int sh2 = hi2 ? k32_sb_fsh : k32_sb_sh;
-    const int i2 = (int)(ec >> sh2) + (hi2 ? k32_off_sbf - (int)(k32_sb_end >> k32_sb_fsh) : k32_off_sb);
-    const int32_t sbe = interp_at(T, i2, (int32_t)(ec & ((1u << sh2) - 1u)), sh2);
-    const int32_t th = th2 - (int32_t)(dh << k32_co_sh);
-    // everything but the sb(e) branch of the cotransformation is ready
-    // before sb(e) returns
+    const int32_t lo = lds_ld(lshl2_add(dl, O.dlo));    // dlo[dl]
+    const int32_t th2 = lds_ld(lshl2_add(dh, O.dhi));   // (dh << 12) + dhi[dh]
+    // what depends on d and the signs alone, while the lookups are in flight
     const bool co = usedb && d < k32_co_end;
-    const int32_t adj_other = co ? (dh == 0 ? lo : th) : (d < k32_esszer ? adj_d : 0);
-    const bool use_sbe = co && dh != 0 && dl != 0;
-    const int32_t r_other = max(__builtin_elementwise_add_sat((int32_t)mx, adj_other), 0);
-    // db < 0 here, so mx + th + sbe cannot overflow
-    const int32_t r_sbe = max((int32_t)mx + th + sbe, 0);
+    const bool direct_db = usedb && !(d < k32_co_end);
+    const bool at_e = co && dh != 0 && dl != 0;
+    const bool cut = !(d < k32_esszer);
+    // the far sb table's last node (x = esszer) is 0, which is sb beyond
+    // esszer; db beyond esszer is cut off below
+    const uint32_t cap = direct_db ? k32_esszer - 1 : k32_esszer;
+    const uint32_t lim = direct_db ? k32_db_end : k32_sb_end;
+    const uint32_t b_fine = direct_db ? O.db : O.sb, b_far = direct_db ? O.dbf : O.sbf;
+    // the interpolation
+    const uint32_t e = (uint32_t)th2 - (uint32_t)lo;   // wraps for the dl = 0 sentinel (unused then)
+    const uint32_t xc = min(at_e ? e : d, cap);
+    const bool hi = xc >= lim;
+    const int sh = hi ? k32_sb_fsh : k32_sb_sh;   // both tables: 2^13 / 2^19 grids
+    const uint32_t node = lshl2_add(xc >> sh, hi ? b_far : b_fine);
+    const int32_t t0 = lds_ld(node), t1 = lds_ld(node + 4);
+    // |t1 - t0| < 2^23 and the fraction < 2^19: a full-rate 24-bit multiply
+    const int32_t ip = t0 + (mul_i24(t1 - t0, (int32_t)(xc & ((1u << sh) - 1u))) >> sh);
+    // adj = A + (keep ? ip : 0): A is the cotransformation's part (dlo[dl],
+    // dhi[dh], or 0 off the cotransformation), known before ip returns, and
+    // ip counts for sb(e) and for the direct sb / db below esszer.  A <= 0,
+    // so mx + A cannot overflow; the saturating add only meets direct sb.
+    const int32_t th = th2 - (int32_t)(dh << k32_co_sh);
+    const int32_t mA = (int32_t)mx + (co ? (dh == 0 ? lo : th) : 0);
+    const bool keep = at_e || (!co && !cut);
     const uint32_t ns = a.l > tl ? a.s : ts;
-    a.l = (uint32_t)(use_sbe ? r_sbe : r_other);
+    a.l = (uint32_t)max(__builtin_elementwise_add_sat(mA, keep ? ip : 0), 0);
     a.s = (d == 0 && usedb) ? 0u : ns;
 }
 
 // A whole xlns32 addition on packed values (sign bit 31) over the LDS tables.
-__device__ __forceinline__ uint32_t x32_add_lds(const int32_t *T, uint32_t x, uint32_t y) {
+__device__ __forceinline__ uint32_t x32_add_lds(const x32_tab &O, uint32_t x, uint32_t y) {
     acc_ls a{x & k32_logmask, x & k32_sign};
-    x32_add_ls(T, a, y & k32_logmask, y & k32_sign);
+    x32_add_ls(O, a, y & k32_logmask, y & k32_sign);
     return a.s | a.l;
 }
 
 template <>
 struct red16<LNSHIP_SUM32> {
-    const int32_t *T;
+    x32_tab O;
     using acc_t = acc_ls;   // xlns32: 31-bit log, sign in bit 31
     __device__ __forceinline__ acc_t start(uint32_t v, uint32_t &) const {
         return {(v & k16_logmask) << 16, (v & k16_sign) << 16};
     }
     __device__ __forceinline__ void add_ls(acc_t &a, uint32_t tl, uint32_t ts, uint32_t &) const {
-        x32_add_ls(T, a, tl << 16, ts << 16);
+        x32_add_ls(O, a, tl << 16, ts << 16);
     }
     __device__ __forceinline__ void add(acc_t &a, uint32_t v, uint32_t &st) const { add_ls(a, v & k16_logmask, v & k16_sign, st); }
     __device__ __forceinline__ uint32_t finish(const acc_t &a) const {
@@ -418,7 +454,7 @@ __device__ __forceinline__ red16<LNSHIP_SUM32> stage_tables<LNSHIP_SUM32>(const 
     if (threadIdx.x == 0) t[k32_off_dlo] = -0x7fffffff;   // db at d = 0: exact cancellation
     // dhi[dh] -> (dh << 12) + dhi[dh], the first half of the cotransformation's e
     for (int i = 1 + threadIdx.x; i < k32_co_n; i += blockDim.x) t[k32_off_dhi + i] += i << k32_co_sh;
-    return red16<LNSHIP_SUM32>{t};
+    return red16<LNSHIP_SUM32>{x32_origins(t)};
 }
 template <>
 __device__ __forceinline__ red16<LNSHIP_LPVIP> stage_tables<LNSHIP_LPVIP>(const dev_tables &, char *) {
@@ -629,7 +665,7 @@ __global__ __launch_bounds__(k_block) void k_mm32(mm_args32 a, dev_tables T) {
             for (int j = 0; j < NC; j++) {
                 const uint32_t t = x32_mul(wv[u], xv[j][u]);
                 if (kb + u == 0) acc[j] = {t & k32_logmask, t & k32_sign};
-                else x32_add_ls(R.T, acc[j], t & k32_logmask, t & k32_sign);
+                else x32_add_ls(R.O, acc[j], t & k32_logmask, t & k32_sign);
             }
         }
     }
@@ -699,9 +735,9 @@ __global__ __launch_bounds__(k_block) void k_rms32(const float *__restrict__ src
         const int r = threadIdx.x;
         const uint32_t *row = sq + (int64_t)r * ncols;
         uint32_t acc = 0;
-        for (int64_t i = 0; i < ncols; i++) acc = x32_add_lds(R.T, acc, row[i]);
+        for (int64_t i = 0; i < ncols; i++) acc = x32_add_lds(R.O, acc, row[i]);
         const uint32_t mean = x32_mul(acc, x32_from_f32(1.0f / (float)ncols));
-        s_inv[r] = x32_recip(x32_sqrt(x32_add_lds(R.T, mean, x32_from_f32(eps))));
+        s_inv[r] = x32_recip(x32_sqrt(x32_add_lds(R.O, mean, x32_from_f32(eps))));
     }
     __syncthreads();
     for (int64_t e = threadIdx.x; e < ne; e += blockDim.x) {
@@ -808,7 +844,7 @@ __global__ __launch_bounds__(k_block) void k_softmax32(sm_args a, dev_tables T) 
                 const float mf = mask_row(a, r0 + r)[i];
                 const uint32_t mk = mf <= -3.0e38f ? 0xffffffffu : x32_from_f32(mf);
                 if (mk == 0xffffffffu) v = 0xffffffffu;
-                else if (mk & k32_logmask) v = x32_add_lds(R.T, v, mk);
+                else if (mk & k32_logmask) v = x32_add_lds(R.O, v, mk);
             }
         }
         c[e] = v;
@@ -819,7 +855,7 @@ __global__ __launch_bounds__(k_block) void k_softmax32(sm_args a, dev_tables T) 
         const int r = (int)(e / a.n);
         const int32_t cm = s_max[r];
         const uint32_t mx = (uint32_t)(cm < 0 ? (cm ^ 0x7fffffff) : cm);
-        const float fv = x32_to_f32(x32_add_lds(R.T, c[e], mx ^ k32_sign));
+        const float fv = x32_to_f32(x32_add_lds(R.O, c[e], mx ^ k32_sign));
         c[e] = x32_from_f32((float)exp((double)fv));
     }
     __syncthreads();
@@ -827,7 +863,7 @@ __global__ __launch_bounds__(k_block) void k_softmax32(sm_args a, dev_tables T) 
         const int r = threadIdx.x;
         const uint32_t *row = c + (int64_t)r * a.n;
         uint32_t acc = row[0];
-        for (int64_t i = 1; i < a.n; i++) acc = x32_add_lds(R.T, acc, row[i]);
+        for (int64_t i = 1; i < a.n; i++) acc = x32_add_lds(R.O, acc, row[i]);
         s_tot[r] = acc;
     }
     __syncthreads();
