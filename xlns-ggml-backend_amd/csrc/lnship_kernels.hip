@@ -675,6 +675,51 @@ __global__ __launch_bounds__(k_block) void k_mm32(mm_args32 a, dev_tables T) {
         if (j < nc) ds[(int64_t)j * a.dst_ld] = a.K == 0 ? 0.0f : x32_to_f32(acc[j].s | acc[j].l);
 }
 
+// ---- sequential row sums over LDS --------------------------------------------
+// acc <- acc (+) row[i] for i = i0 .. n-1 in order (i0 < n).  row is in LDS,
+// 16-byte aligned, and readable up to n rounded up to a whole 16-byte group;
+// each group of codes arrives in one 16-byte read issued a group ahead.
+template <class RED>
+__device__ __forceinline__ void chain16(const RED &R, typename RED::acc_t &acc, const uint16_t *row, int i0, int n,
+                                        uint32_t &st) {
+    const int g0 = i0 >> 3, gl = (n - 1) >> 3;
+    auto ld = [&](int g) { return *reinterpret_cast<const uint4 *>(row + 8 * min(g, gl)); };
+    auto run = [&](const uint4 &q, int u0, int u1) {
+        const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+        for (int u = 0; u < 8; u++)
+            if (u >= u0 && u < u1) R.add(acc, half16(w[u >> 1], u & 1), st);
+    };
+    uint4 cur = ld(g0), nxt = ld(g0 + 1);
+    run(cur, i0 - 8 * g0, min(n - 8 * g0, 8));
+    for (int g = g0 + 1; g < gl; g++) {
+        cur = nxt;
+        nxt = ld(g + 1);
+        run(cur, 0, 8);
+    }
+    if (gl > g0) run(nxt, 0, n - 8 * gl);
+}
+
+// the same over packed xlns32 codes, four per 16-byte group
+__device__ __forceinline__ void chain32(const x32_tab &O, acc_ls &acc, const uint32_t *row, int i0, int n) {
+    const int g0 = i0 >> 2, gl = (n - 1) >> 2;
+    auto ld = [&](int g) { return *reinterpret_cast<const uint4 *>(row + 4 * min(g, gl)); };
+    auto run = [&](const uint4 &q, int u0, int u1) {
+        const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+        for (int u = 0; u < 4; u++)
+            if (u >= u0 && u < u1) x32_add_ls(O, acc, w[u] & k32_logmask, w[u] & k32_sign);
+    };
+    uint4 cur = ld(g0), nxt = ld(g0 + 1);
+    run(cur, i0 - 4 * g0, min(n - 4 * g0, 4));
+    for (int g = g0 + 1; g < gl; g++) {
+        cur = nxt;
+        nxt = ld(g + 1);
+        run(cur, 0, 4);
+    }
+    if (gl > g0) run(nxt, 0, n - 4 * gl);
+}
+
 // ---- RMS_NORM -------------------------------------------------------------------
 // A workgroup takes rb rows: all threads convert and square into LDS, one lane
 // per row runs the sequential sum, all threads scale.
@@ -690,18 +735,19 @@ __global__ __launch_bounds__(k_block) void k_rms16(const float *__restrict__ src
     const int64_t r0 = (int64_t)blockIdx.x * rb;
     const int nr = (int)min<int64_t>(rb, nrows - r0);
     const int64_t ne = (int64_t)nr * ncols;
-    for (int64_t e = threadIdx.x; e < ne; e += blockDim.x) {
+    const int nc = (int)ncols, rs = (nc + 7) & ~7;   // LDS rows 16-byte aligned
+    for (int e = threadIdx.x; e < nr * nc; e += blockDim.x) {
+        const int r = e / nc;
         const uint32_t c = x16_from_f32(T.cvt16, src[r0 * ncols + e]);
-        sq[e] = (uint16_t)x16_mul(c, c);
+        sq[e + r * (rs - nc)] = (uint16_t)x16_mul(c, c);
     }
     __syncthreads();
     if ((int)threadIdx.x < nr) {
         const int r = threadIdx.x;
         uint32_t s = 0;
         if (MODE == LNSHIP_MONTE) s = lfsr_jump(T, seed, (uint64_t)(r0 + r) * (uint64_t)ncols);
-        const uint16_t *row = sq + (int64_t)r * ncols;
         typename red16<MODE>::acc_t acc = R.start(0u, s);
-        for (int64_t i = 0; i < ncols; i++) R.add(acc, row[i], s);
+        chain16(R, acc, sq + r * rs, 0, nc, s);
         const uint32_t sum = R.finish(acc) & 0xffffu;
         const uint32_t mean = x16_mul(sum, x16_from_f32(T.cvt16, 1.0f / (float)ncols));
         const uint32_t e16 = x16_from_f32(T.cvt16, eps);
@@ -726,16 +772,18 @@ __global__ __launch_bounds__(k_block) void k_rms32(const float *__restrict__ src
     const int64_t r0 = (int64_t)blockIdx.x * rb;
     const int nr = (int)min<int64_t>(rb, nrows - r0);
     const int64_t ne = (int64_t)nr * ncols;
-    for (int64_t e = threadIdx.x; e < ne; e += blockDim.x) {
+    const int nc = (int)ncols, rs = (nc + 3) & ~3;   // LDS rows 16-byte aligned
+    for (int e = threadIdx.x; e < nr * nc; e += blockDim.x) {
+        const int r = e / nc;
         const uint32_t c = x32_from_f32(src[r0 * ncols + e]);
-        sq[e] = x32_mul(c, c);
+        sq[e + r * (rs - nc)] = x32_mul(c, c);
     }
     __syncthreads();
     if ((int)threadIdx.x < nr) {
         const int r = threadIdx.x;
-        const uint32_t *row = sq + (int64_t)r * ncols;
-        uint32_t acc = 0;
-        for (int64_t i = 0; i < ncols; i++) acc = x32_add_lds(R.O, acc, row[i]);
+        acc_ls a{0u, 0u};
+        chain32(R.O, a, sq + r * rs, 0, nc);
+        const uint32_t acc = a.s | a.l;
         const uint32_t mean = x32_mul(acc, x32_from_f32(1.0f / (float)ncols));
         s_inv[r] = x32_recip(x32_sqrt(x32_add_lds(R.O, mean, x32_from_f32(eps))));
     }
@@ -779,6 +827,7 @@ __global__ __launch_bounds__(k_block) void k_softmax16(sm_args a, dev_tables T) 
     const int64_t r0 = (int64_t)blockIdx.x * a.rb;
     const int nr = (int)min<int64_t>(a.rb, a.ne1 * a.ne2 * a.ne3 - r0);
     const int64_t ne = (int64_t)nr * a.n;
+    const int rs = ((int)a.n + 7) & ~7;   // LDS rows 16-byte aligned
     if ((int)threadIdx.x < nr) s_max[threadIdx.x] = x16_canon(0xffffu);
     __syncthreads();
     const uint32_t sc = x16_from_f32(T.cvt16, a.scale);
@@ -795,7 +844,7 @@ __global__ __launch_bounds__(k_block) void k_softmax16(sm_args a, dev_tables T) 
                 else if (mk & k16_logmask) v = x16_add_g(T.gauss16, v, mk);
             }
         }
-        c[e] = (uint16_t)v;
+        c[e + r * (rs - a.n)] = (uint16_t)v;
         atomicMax(&s_max[r], x16_canon(v));
     }
     __syncthreads();
@@ -803,22 +852,23 @@ __global__ __launch_bounds__(k_block) void k_softmax16(sm_args a, dev_tables T) 
         const int r = (int)(e / a.n);
         const int32_t cm = s_max[r];
         const uint32_t mx = (uint32_t)(uint16_t)(cm < 0 ? (cm ^ 0x7fff) : cm);
-        c[e] = T.exp16[x16_add_g(T.gauss16, c[e], mx ^ k16_sign)];
+        const int64_t o = e + r * (rs - a.n);
+        c[o] = T.exp16[x16_add_g(T.gauss16, c[o], mx ^ k16_sign)];
     }
     __syncthreads();
     if ((int)threadIdx.x < nr) {
         const int r = threadIdx.x;
         uint32_t s = 0;
         if (MODE == LNSHIP_MONTE) s = lfsr_jump(T, a.seed, (uint64_t)(r0 + r) * (uint64_t)(a.n - 1));
-        const uint16_t *row = c + (int64_t)r * a.n;
+        const uint16_t *row = c + r * rs;
         typename red16<MODE>::acc_t acc = R.start(row[0], s);
-        for (int64_t i = 1; i < a.n; i++) R.add(acc, row[i], s);
+        if (a.n > 1) chain16(R, acc, row, 1, (int)a.n, s);
         s_tot[r] = R.finish(acc) & 0xffffu;
     }
     __syncthreads();
     for (int64_t e = threadIdx.x; e < ne; e += blockDim.x) {
         const int r = (int)(e / a.n);
-        a.dst[r0 * a.n + e] = T.rev16[x16_div(c[e], s_tot[r])];
+        a.dst[r0 * a.n + e] = T.rev16[x16_div(c[e + r * (rs - a.n)], s_tot[r])];
     }
 }
 
@@ -831,6 +881,7 @@ __global__ __launch_bounds__(k_block) void k_softmax32(sm_args a, dev_tables T) 
     const int64_t r0 = (int64_t)blockIdx.x * a.rb;
     const int nr = (int)min<int64_t>(a.rb, a.ne1 * a.ne2 * a.ne3 - r0);
     const int64_t ne = (int64_t)nr * a.n;
+    const int rs = ((int)a.n + 3) & ~3;   // LDS rows 16-byte aligned
     if ((int)threadIdx.x < nr) s_max[threadIdx.x] = x32_canon(0xffffffffu);
     __syncthreads();
     const uint32_t sc = x32_from_f32(a.scale);
@@ -847,7 +898,7 @@ __global__ __launch_bounds__(k_block) void k_softmax32(sm_args a, dev_tables T) 
                 else if (mk & k32_logmask) v = x32_add_lds(R.O, v, mk);
             }
         }
-        c[e] = v;
+        c[e + r * (rs - a.n)] = v;
         atomicMax(&s_max[r], x32_canon(v));
     }
     __syncthreads();
@@ -855,21 +906,22 @@ __global__ __launch_bounds__(k_block) void k_softmax32(sm_args a, dev_tables T) 
         const int r = (int)(e / a.n);
         const int32_t cm = s_max[r];
         const uint32_t mx = (uint32_t)(cm < 0 ? (cm ^ 0x7fffffff) : cm);
-        const float fv = x32_to_f32(x32_add_lds(R.O, c[e], mx ^ k32_sign));
-        c[e] = x32_from_f32((float)exp((double)fv));
+        const int64_t o = e + r * (rs - a.n);
+        const float fv = x32_to_f32(x32_add_lds(R.O, c[o], mx ^ k32_sign));
+        c[o] = x32_from_f32((float)exp((double)fv));
     }
     __syncthreads();
     if ((int)threadIdx.x < nr) {
         const int r = threadIdx.x;
-        const uint32_t *row = c + (int64_t)r * a.n;
-        uint32_t acc = row[0];
-        for (int64_t i = 1; i < a.n; i++) acc = x32_add_lds(R.O, acc, row[i]);
-        s_tot[r] = acc;
+        const uint32_t *row = c + r * rs;
+        acc_ls acc{row[0] & k32_logmask, row[0] & k32_sign};
+        if (a.n > 1) chain32(R.O, acc, row, 1, (int)a.n);
+        s_tot[r] = acc.s | acc.l;
     }
     __syncthreads();
     for (int64_t e = threadIdx.x; e < ne; e += blockDim.x) {
         const int r = (int)(e / a.n);
-        a.dst[r0 * a.n + e] = x32_to_f32(x32_div(c[e], s_tot[r]));
+        a.dst[r0 * a.n + e] = x32_to_f32(x32_div(c[e + r * (rs - a.n)], s_tot[r]));
     }
 }
 
@@ -987,7 +1039,8 @@ __global__ void k_causal_mask(const int32_t *__restrict__ pos0, int64_t ntok, in
 
 template <int MODE>
 static int64_t max_row(int elem_bytes) {
-    return (k_lds_bytes - ((lds_tables_bytes<MODE>() + 15) & ~15) - 1024) / elem_bytes;
+    // rows are staged at a 16-byte stride
+    return ((k_lds_bytes - ((lds_tables_bytes<MODE>() + 15) & ~15) - 1024) / 16) * (16 / elem_bytes);
 }
 
 template <int MODE>
@@ -1091,9 +1144,10 @@ static int launch_mm32(const mm_args32 &m, const dev_tables &T, int64_t nslices,
 template <int MODE>
 static int launch_rms16(const float *src, float *dst, int64_t ncols, int64_t nrows, float eps, uint16_t seed,
                         const dev_tables &T, hipStream_t st) {
-    const int rb = rows_per_block<MODE>(ncols, 2);
+    const int64_t rs = (ncols + 7) & ~(int64_t)7;
+    const int rb = rows_per_block<MODE>(rs, 2);
     if (rb < 1) return fail(LNSHIP_ERANGE, "rms_norm: row too long for LDS%s");
-    const int lds = ((lds_tables_bytes<MODE>() + 15) & ~15) + (int)(rb * ncols * 2);
+    const int lds = ((lds_tables_bytes<MODE>() + 15) & ~15) + (int)(rb * rs * 2);
     if (int rc = set_lds(k_rms16<MODE>, lds)) return rc;
     hipLaunchKernelGGL(k_rms16<MODE>, dim3((unsigned)((nrows + rb - 1) / rb)), dim3(k_block), lds, st, src, dst, ncols,
                        nrows, rb, eps, (uint32_t)seed, T);
@@ -1116,9 +1170,10 @@ static int check_sm(const lnship_soft_max_args *a) {
 
 template <int MODE>
 static int launch_sm16(sm_args &m, int64_t nrows, const dev_tables &T, hipStream_t st) {
-    m.rb = rows_per_block<MODE>(m.n, 2);
+    const int64_t rs = (m.n + 7) & ~(int64_t)7;
+    m.rb = rows_per_block<MODE>(rs, 2);
     if (m.rb < 1) return fail(LNSHIP_ERANGE, "soft_max: row too long for LDS%s");
-    const int lds = ((lds_tables_bytes<MODE>() + 15) & ~15) + (int)(m.rb * m.n * 2);
+    const int lds = ((lds_tables_bytes<MODE>() + 15) & ~15) + (int)(m.rb * rs * 2);
     if (int rc = set_lds(k_softmax16<MODE>, lds)) return rc;
     hipLaunchKernelGGL(k_softmax16<MODE>, dim3((unsigned)((nrows + m.rb - 1) / m.rb)), dim3(k_block), lds, st, m, T);
     LNSHIP_HIP(hipGetLastError());
@@ -1344,9 +1399,10 @@ int lnship32_rms_norm(const float *src, float *dst, int64_t ncols, int64_t nrows
     if (!s) return LNSHIP_ENOINIT;
     if (ncols < 0 || nrows < 0) return fail(LNSHIP_EINVAL, "rms_norm: bad argument%s");
     if (ncols == 0 || nrows == 0) return 0;
-    const int rb = rows_per_block<LNSHIP_SUM32>(ncols, 4);
+    const int64_t rs = (ncols + 3) & ~(int64_t)3;
+    const int rb = rows_per_block<LNSHIP_SUM32>(rs, 4);
     if (rb < 1) return fail(LNSHIP_ERANGE, "rms_norm: row too long for LDS%s");
-    const int lds = k_lds_tab32 + (int)(rb * ncols * 4);
+    const int lds = k_lds_tab32 + (int)(rb * rs * 4);
     if (int rc = set_lds(k_rms32, lds)) return rc;
     hipLaunchKernelGGL(k_rms32, dim3((unsigned)((nrows + rb - 1) / rb)), dim3(k_block), lds, (hipStream_t)stream, src,
                        dst, ncols, nrows, rb, eps, s->T);
@@ -1382,9 +1438,10 @@ int lnship32_soft_max(const lnship_soft_max_args *a, void *stream) {
     if (a->src_ne[0] == 0 || nrows == 0) return 0;
     sm_args m{a->src, a->mask, a->dst, a->src_ne[0], a->src_ne[1], a->src_ne[2], a->src_ne[3],
               a->mask_ne[0], a->mask_ne[1], a->mask_ne[2], a->mask_ne[3], a->scale, 0, 0};
-    m.rb = rows_per_block<LNSHIP_SUM32>(m.n, 4);
+    const int64_t rs = (m.n + 3) & ~(int64_t)3;
+    m.rb = rows_per_block<LNSHIP_SUM32>(rs, 4);
     if (m.rb < 1) return fail(LNSHIP_ERANGE, "soft_max: row too long for LDS%s");
-    const int lds = k_lds_tab32 + (int)(m.rb * m.n * 4);
+    const int lds = k_lds_tab32 + (int)(m.rb * rs * 4);
     if (int rc = set_lds(k_softmax32, lds)) return rc;
     hipLaunchKernelGGL(k_softmax32, dim3((unsigned)((nrows + m.rb - 1) / m.rb)), dim3(k_block), lds,
                        (hipStream_t)stream, m, s->T);
