@@ -41,6 +41,9 @@ def parse():
                     help="only time single ops (decode GEMVs, C5 prefill GEMM / rms_norm / soft_max), one JSON "
                          "line each, in --mode (or every mode with --mode all)")
     ap.add_argument("--reps", type=int, default=5, help="launches timed per op with --ops")
+    ap.add_argument("--batch", type=int, default=1, metavar="S",
+                    help="BASELINE config 3: S independent sequences, each prompt prefilled on its own, then "
+                         "batched greedy decode (one token per sequence per step); prints its own JSON line")
     args, rest = ap.parse_known_args()
     if rest:
         ap.error("unrecognized arguments: %s" % " ".join(rest))
@@ -77,6 +80,18 @@ def run_ops(args):
     def line(**kw):
         print(json.dumps(kw), flush=True)
 
+    if args.ops in ("decode", "all"):
+        # LNS32 (xlns32 weights, 4 B each) at the Llama-1B shape of BASELINE
+        # config 4: q / o, k / v, gate|up, down, lm_head
+        for K, M in ((2048, 2048), (2048, 512), (2048, 16384), (8192, 2048), (2048, 32000)):
+            wp = lnship.pack32(randn(M, K) * 0.02)
+            x = randn(1, K)
+            us = timed(lambda: lnship.mul_mat32(wp, x, K, M), args.reps)
+            line(op="mul_mat", mode="lns32", K=K, M=M, N=1, us=round(us, 2), ns_per_step=round(us * 1e3 / K, 2),
+                 gbs=round((4 * K * M + 4 * K + 4 * M) / us / 1e3, 3))
+        x = randn(1, 2048)
+        us = timed(lambda: lnship.rms_norm32(x, 1e-5), args.reps)
+        line(op="rms_norm", mode="lns32", rows=1, n=2048, us=round(us, 2), ns_per_step=round(us * 1e3 / 2048, 2))
     for mname in _ops_modes(args.mode):
         m = lnship.MODES[mname]
         if args.ops in ("decode", "all"):
@@ -103,6 +118,56 @@ def run_ops(args):
             mask = torch.triu(torch.full((512, 512), float("-inf"), device="cuda"), 1)
             us = timed(lambda: lnship.soft_max16(m, s, mask, 0.125), args.reps)
             line(op="soft_max", mode=mname, heads=32, rows=512, n=512, us=round(us, 2))
+
+
+def run_batch(args):
+    """S sequences of the SmolLM2-shape model: each --prompt-token prompt is
+    prefilled on its own, then --warmup + --steps batched decode steps (one
+    token per sequence; weight GEMVs see S columns, attention is batched over
+    the sequences' own KV caches).  Non-Monte steps replay a HIP graph; Monte
+    steps run eagerly (the op seeds change every step)."""
+    import numpy as np
+    import torch
+    import lnship
+    from lnship import llama
+    torch.cuda.set_device(0)
+    lnship.init()
+    cfg, S = llama.SMOLLM2_135M, args.batch
+    mode = lnship.MODES[args.mode]
+    weights = llama.synthetic_weights(cfg, seed=1234, std=0.02)
+    model = llama.LlamaLNS16(cfg, weights, mode=mode, n_seq=S)
+    rng = np.random.default_rng(2024)
+    prompts = [[int(t) for t in rng.integers(0, cfg.n_vocab, args.prompt)] for _ in range(S)]
+    torch.cuda.synchronize()
+    tp = time.perf_counter()
+    first = [model.eval(prompts[s], seq=s).argmax() for s in range(S)]
+    torch.cuda.synchronize()
+    t_prefill = time.perf_counter() - tp
+    tok_dev = torch.stack(first).to(torch.int32)
+    use_graph = mode != lnship.MONTE
+
+    def step():
+        nonlocal tok_dev
+        out = model.decode_graph_batch(tok_dev) if use_graph else model.eval_batch(tok_dev.tolist())
+        tok_dev = out.argmax(dim=1).to(torch.int32)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    ts = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    t_decode = time.perf_counter() - ts
+    print(json.dumps({
+        "metric": "LNS16 batched decode tok/s, %d sequences, SmolLM2-135M shape" % S,
+        "value": round(S * args.steps / t_decode, 3), "unit": "tok/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(t_decode / args.steps * 1e3, 4), "higher_is_better": True,
+        "dtype": "xlns16", "data": "synthetic (as the default workload)",
+        "config": {"workload": "BASELINE config 3: %d x %d-token prompts, then batched greedy decode" % (S, args.prompt),
+                   "mode": args.mode, "sequences": S, "n_kv": model.batch_n_kv(),
+                   "graph": "hipGraph per decode step" if use_graph else "eager"},
+        "prefill_tok_s": round(S * args.prompt / t_prefill, 3)}), flush=True)
 
 
 def calib_copy(mib):
@@ -225,6 +290,9 @@ def main():
         return
     if args.mode == "all":
         sys.exit("bench.py: --mode all is for --ops only")
+    if args.batch > 1:
+        run_batch(args)
+        return
     import numpy as np
     import torch
     import lnship

@@ -135,24 +135,28 @@ int lnship16_get_rows_packed(const uint16_t *w, int64_t K, int64_t M, const int3
 /* lns_rope (src/lns-ops.cpp:1199-1281): x rows [ntok][nhead][ne0] (token
  * stride x_ld); cos_sin holds per position p and pair j the floats
  * (cos, sin) at cos_sin[(p * (n_dims/2) + j) * 2]; pos[ntok] on the device.
- * When cache is non-null the rotated rows are also rounded to IEEE half,
- * converted to xlns16 and stored (no F32 dst) into a packed cache: head h,
- * position p, dim d at h * cache_slice + ((d/8) * cache_m + p) * 8 + d % 8
- * (K cache: kq's weight operand) or, with cache_transposed, at
- * h * cache_slice + ((p/8) * ne0 + d) * 8 + p % 8 (V cache, kqv's). */
+ * lnship16_store_kv rotates the first rope_n_dims dims of each row (0: none),
+ * rounds the rows to IEEE half, converts them to xlns16 and stores them (no
+ * F32 dst) into a packed cache: head h, position p, dim d at
+ * h * cache_slice + ((d/8) * cache_m + p) * 8 + d % 8 (K cache: kq's weight
+ * operand) or, with cache_transposed, at h * cache_slice +
+ * ((p/8) * ne0 + d) * 8 + p % 8 (V cache, kqv's), plus seq[t] * seq_stride
+ * when seq (device, one sequence index per token) is non-null: per-sequence
+ * caches side by side, as llama.cpp's per-sequence KV streams. */
 int lnship16_rope(const float *x, int64_t x_ld, const int32_t *pos, int64_t ntok, int64_t nhead, int64_t ne0,
                   int n_dims, int neox, const float *cos_sin, float *dst, void *stream);
 int lnship16_store_kv(const float *x, int64_t x_ld, const int32_t *pos, int64_t ntok, int64_t nhead, int64_t ne0,
                       int rope_n_dims, const float *cos_sin, uint16_t *cache, int64_t cache_m,
-                      int64_t cache_slice, int cache_transposed, void *stream);
+                      int64_t cache_slice, int cache_transposed, const int32_t *seq, int64_t seq_stride,
+                      void *stream);
 /* Host: the (cos, sin) floats lns_rope uses for positions 0..n_pos-1 (the
  * float recurrence t *= powf(freq_base, -2/n_dims) per pair, cosf / sinf;
  * src/lns-ops.cpp:1225-1247, cuda/lns-cuda-ops.cpp:223-240), laid out as
  * out[(p * (n_dims/2) + j) * 2 + {0, 1}].  No GPU needed. */
 int lnship_rope_table(float freq_base, int n_dims, int64_t n_pos, float *out);
-/* mask[t][j] = 0 if j <= pos0 + t else -inf (llama's causal KQ mask),
- * t < ntok, j < n_kv; pos0 read from the device */
-int lnship_causal_mask(const int32_t *pos0, int64_t ntok, int64_t n_kv, float *mask, void *stream);
+/* mask[t][j] = 0 if j <= pos[t] else -inf (llama's causal KQ mask over one
+ * sequence's cache cells), t < ntok, j < n_kv; pos on the device */
+int lnship_causal_mask(const int32_t *pos, int64_t ntok, int64_t n_kv, float *mask, void *stream);
 
 /* Longest row (ncols) the row kernels stage in LDS: which = 0 xlns16
  * rms_norm, 1 xlns16 soft_max, 2 xlns32 rms_norm, 3 xlns32 soft_max; mode is

@@ -6,7 +6,10 @@ LNS16 backend computes it), built from the oracle's op drivers: mul_mat
 mul (:468-530), swiglu (:812-868), rope (:1199-1281), get_rows of LNS16
 weights (:1003-1050).  The KV cache holds IEEE half values, as llama.cpp's
 F16 cache does.  Monte ops draw from the oracle's process-global LFSR in
-graph order.
+graph order.  With n_seq > 1 each sequence has its own KV cache; eval(tokens,
+seq) runs one sequence's tokens and eval_batch(tokens) one decode step of
+every sequence, attention batched over sequences in the 4th dimension, as
+lnship.llama does.
 """
 import ctypes
 import math
@@ -35,7 +38,7 @@ def _binop(fn, a, b):
 
 
 class LlamaOracle16:
-    def __init__(self, cfg, weights, mode, lfsr=7):
+    def __init__(self, cfg, weights, mode, lfsr=7, n_seq=1):
         L = O.lib()
         for name, args in (("lno16_add_f32", [ctypes.c_void_p] * 2 + [ctypes.c_int64] * 2 + [ctypes.c_void_p]),
                            ("lno16_mul_f32", [ctypes.c_void_p] * 2 + [ctypes.c_int64] * 2 + [ctypes.c_void_p]),
@@ -60,9 +63,10 @@ class LlamaOracle16:
                 "wug": O.f2x16(np.concatenate([W["w_up"], W["w_gate"]])),
                 "wdown": O.f2x16(W["w_down"]),
             })
-        self.kcache = [np.zeros((c.n_ctx, c.n_head_kv, c.head_dim), np.float16) for _ in range(c.n_layer)]
-        self.vcache = [np.zeros((c.n_ctx, c.n_head_kv, c.head_dim), np.float16) for _ in range(c.n_layer)]
-        self.n_past = 0
+        self.n_seq = n_seq
+        self.kcache = [np.zeros((n_seq, c.n_ctx, c.n_head_kv, c.head_dim), np.float16) for _ in range(c.n_layer)]
+        self.vcache = [np.zeros((n_seq, c.n_ctx, c.n_head_kv, c.head_dim), np.float16) for _ in range(c.n_layer)]
+        self.past = [0] * n_seq
 
     def _rope(self, x, pos):
         c = self.cfg
@@ -73,14 +77,30 @@ class LlamaOracle16:
                               c.rope_theta, _ptr(out))
         return out
 
-    def eval(self, tokens):
+    @property
+    def n_past(self):
+        return self.past[0]
+
+    def eval(self, tokens, seq=0):
+        """Appends tokens to sequence seq; returns the logits of the last one."""
+        p0 = self.past[seq]
+        pos = np.arange(p0, p0 + len(tokens), dtype=np.int32)
+        out = self._graph(tokens, pos, [seq] * len(tokens), n_kv_for(p0 + len(tokens), self.cfg.n_ctx), False)
+        self.past[seq] += len(tokens)
+        return out
+
+    def eval_batch(self, tokens):
+        """One decode step of every sequence; returns logits [n_seq][n_vocab]."""
+        pos = np.asarray(self.past, dtype=np.int32)
+        out = self._graph(tokens, pos, list(range(self.n_seq)), n_kv_for(max(self.past) + 1, self.cfg.n_ctx), True)
+        self.past = [p + 1 for p in self.past]
+        return out
+
+    def _graph(self, tokens, pos, seqs, n_kv, batch):
         c, m = self.cfg, self.mode
         T = len(tokens)
         e, hd, nh, nkv, f = c.n_embd, c.head_dim, c.n_head, c.n_head_kv, c.n_ff
         nq = nh * hd
-        p0 = self.n_past
-        pos = np.arange(p0, p0 + T, dtype=np.int32)
-        n_kv = n_kv_for(p0 + T, c.n_ctx)
         mask = np.where(np.arange(n_kv)[None, :] <= pos[:, None], 0.0, -np.inf).astype(np.float32)
         x = O.x2f16(self.tok_embd[np.asarray(tokens)])                 # get_rows of LNS16 -> F32
         for il, W in enumerate(self.layers):
@@ -91,16 +111,27 @@ class LlamaOracle16:
             q = self._rope(qkv[:, :nq].reshape(T, nh, hd), pos)
             k = self._rope(qkv[:, nq:nq + nkv * hd].reshape(T, nkv, hd), pos)
             v = qkv[:, nq + nkv * hd:].reshape(T, nkv, hd)
-            self.kcache[il][p0:p0 + T] = k.astype(np.float16)
-            self.vcache[il][p0:p0 + T] = v.astype(np.float16)
-            kw = self.kcache[il][:n_kv].astype(np.float32).transpose(1, 0, 2)   # [nkv, n_kv, hd]
-            kq = O.mul_mat16_f32w(m, kw[None], q.transpose(1, 0, 2)[None], ne02=nkv)  # [1, nh, T, n_kv]
-            kq = O.soft_max16(m, kq[0], mask, 1.0 / math.sqrt(hd))
-            vw = self.vcache[il][:n_kv].astype(np.float32).transpose(1, 2, 0)   # [nkv, hd, n_kv]
-            att = O.mul_mat16_f32w(m, vw[None], kq[None], ne02=nkv)[0]          # [nh, T, hd]
-            att = np.ascontiguousarray(att.transpose(1, 0, 2).reshape(T, nq))
+            for t in range(T):
+                self.kcache[il][seqs[t], pos[t]] = k[t].astype(np.float16)
+                self.vcache[il][seqs[t], pos[t]] = v[t].astype(np.float16)
+            if batch:
+                # one query row per sequence, sequences in the 4th dimension
+                kw = self.kcache[il][:, :n_kv].astype(np.float32).transpose(0, 2, 1, 3)   # [S, nkv, n_kv, hd]
+                kq = O.mul_mat16_f32w(m, kw, q[:, :, None, :], ne02=nkv, ne03=T)        # [S, nh, 1, n_kv]
+                kq = O.soft_max16(m, kq, mask[:, None, None, :], 1.0 / math.sqrt(hd))
+                vw = self.vcache[il][:, :n_kv].astype(np.float32).transpose(0, 2, 3, 1)   # [S, nkv, hd, n_kv]
+                att = O.mul_mat16_f32w(m, vw, kq, ne02=nkv, ne03=T)                   # [S, nh, 1, hd]
+                att = np.ascontiguousarray(att.reshape(T, nq))
+            else:
+                s = seqs[0]
+                kw = self.kcache[il][s, :n_kv].astype(np.float32).transpose(1, 0, 2)   # [nkv, n_kv, hd]
+                kq = O.mul_mat16_f32w(m, kw[None], q.transpose(1, 0, 2)[None], ne02=nkv)  # [1, nh, T, n_kv]
+                kq = O.soft_max16(m, kq[0], mask, 1.0 / math.sqrt(hd))
+                vw = self.vcache[il][s, :n_kv].astype(np.float32).transpose(1, 2, 0)   # [nkv, hd, n_kv]
+                att = O.mul_mat16_f32w(m, vw[None], kq[None], ne02=nkv)[0]          # [nh, T, hd]
+                att = np.ascontiguousarray(att.transpose(1, 0, 2).reshape(T, nq))
             o = O.mul_mat16(m, W["wo"], att)
-            if last:
+            if last and not batch:
                 o, x = o[-1:], x[-1:]
             x = _binop(self.L.lno16_add_f32, o, x)
             h = O.rms_norm16(m, x, c.eps)
@@ -111,8 +142,7 @@ class LlamaOracle16:
             self.L.lno16_swiglu_f32(_ptr(gate), _ptr(up), up.size, _ptr(sw))
             d = O.mul_mat16(m, W["wdown"], sw)
             x = _binop(self.L.lno16_add_f32, d, x)
-        h = O.rms_norm16(m, x[-1:], c.eps)
+        h = O.rms_norm16(m, x if batch else x[-1:], c.eps)
         h = _binop(self.L.lno16_mul_f32, h, self.out_norm)
-        logits = O.mul_mat16(m, self.tok_embd, h)[0]
-        self.n_past += T
-        return logits
+        logits = O.mul_mat16(m, self.tok_embd, h)
+        return logits if batch else logits[0]

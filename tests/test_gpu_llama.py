@@ -61,3 +61,34 @@ def test_kv_view_grows_past_256():
     same(gpu.eval(prompt).cpu().numpy(), cpu.eval(prompt), "prefill 254")
     for step, tok in enumerate((3, 11, 17)):
         same(gpu.decode_graph(tok).cpu().numpy(), cpu.eval([tok]), f"decode {254 + step}")
+
+
+@pytest.mark.parametrize("mode", ["base", "monte", "lpvip", "sum32"])
+def test_batched_sequences(mode):
+    """BASELINE config 3 in small: independent sequences with their own KV
+    caches, each prompt run on its own, then decode steps that take one token
+    per sequence (attention batched over sequences)."""
+    from lnship import llama
+    cfg = tiny()
+    w = llama.synthetic_weights(cfg, seed=31, std=0.2)
+    m = O.MODES[mode]
+    rng = np.random.default_rng(17)
+    gpu = llama.LlamaLNS16(cfg, w, mode=m, n_seq=3)
+    cpu = LlamaOracle16(cfg, w, m, n_seq=3)
+    for s, n in enumerate((5, 9, 7)):
+        prompt = [int(t) for t in rng.integers(0, cfg.n_vocab, n)]
+        print(f"\n[llama] {mode} seq {s} prefill {n}", flush=True)
+        same(gpu.eval(prompt, seq=s).cpu().numpy(), cpu.eval(prompt, seq=s), f"{mode} seq {s} prefill")
+    toks = [int(t) for t in rng.integers(0, cfg.n_vocab, 3)]
+    for step in range(3):
+        print(f"[llama] {mode} batched decode {step}", flush=True)
+        same(gpu.eval_batch(toks).cpu().numpy(), cpu.eval_batch(toks), f"{mode} batched decode {step}")
+        toks = [(t * 7 + 3 + i) % cfg.n_vocab for i, t in enumerate(toks)]
+    if m != O.MONTE:
+        for step in range(2):
+            print(f"[llama] {mode} batched graph decode {step}", flush=True)
+            dev = torch.tensor(toks, dtype=torch.int32, device="cuda")
+            same(gpu.decode_graph_batch(dev).cpu().numpy(), cpu.eval_batch(toks), f"{mode} batched graph {step}")
+            toks = [(t * 5 + 1 + i) % cfg.n_vocab for i, t in enumerate(toks)]
+    assert gpu.past == cpu.past
+    assert O.monte_get() == gpu.lfsr or m != O.MONTE

@@ -1000,7 +1000,7 @@ __device__ __forceinline__ uint16_t kv_code(const dev_tables &T, float v) {
 __global__ void k_store_kv16(const float *__restrict__ x, int64_t x_ld, const int32_t *__restrict__ pos, int64_t ntok,
                              int64_t nhead, int64_t ne0, int rope_n_dims, const float *__restrict__ cos_sin,
                              uint16_t *__restrict__ cache, int64_t cache_m, int64_t cache_slice, int transposed,
-                             dev_tables T) {
+                             const int32_t *__restrict__ seq, int64_t seq_stride, dev_tables T) {
     const int64_t n = ntok * nhead * ne0;
     const int64_t half = rope_n_dims / 2;
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)blockDim.x * gridDim.x) {
@@ -1022,16 +1022,15 @@ __global__ void k_store_kv16(const float *__restrict__ x, int64_t x_ld, const in
         }
         const int64_t o = transposed ? h * cache_slice + ((p >> 3) * ne0 + d) * 8 + (p & 7)
                                      : h * cache_slice + ((d >> 3) * cache_m + p) * 8 + (d & 7);
-        cache[o] = kv_code(T, v);
+        cache[(seq ? (int64_t)seq[t] * seq_stride : 0) + o] = kv_code(T, v);
     }
 }
 
-__global__ void k_causal_mask(const int32_t *__restrict__ pos0, int64_t ntok, int64_t n_kv, float *__restrict__ mask) {
+__global__ void k_causal_mask(const int32_t *__restrict__ pos, int64_t ntok, int64_t n_kv, float *__restrict__ mask) {
     const int64_t n = ntok * n_kv;
-    const int64_t p0 = pos0[0];
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)blockDim.x * gridDim.x) {
         const int64_t t = i / n_kv, j = i - t * n_kv;
-        mask[i] = j <= p0 + t ? 0.0f : -INFINITY;
+        mask[i] = j <= pos[t] ? 0.0f : -INFINITY;
     }
 }
 
@@ -1521,16 +1520,18 @@ int lnship16_rope(const float *x, int64_t x_ld, const int32_t *pos, int64_t ntok
 
 int lnship16_store_kv(const float *x, int64_t x_ld, const int32_t *pos, int64_t ntok, int64_t nhead, int64_t ne0,
                       int rope_n_dims, const float *cos_sin, uint16_t *cache, int64_t cache_m, int64_t cache_slice,
-                      int cache_transposed, void *stream) {
+                      int cache_transposed, const int32_t *seq, int64_t seq_stride, void *stream) {
     device_state *s = state();
     if (!s) return LNSHIP_ENOINIT;
     if (rope_n_dims < 0 || rope_n_dims % 2 || rope_n_dims > ne0 || x_ld < nhead * ne0 || ntok < 0 || nhead < 0)
         return fail(LNSHIP_EINVAL, "store_kv: bad shape%s");
     if (!cache_transposed && ne0 % 8) return fail(LNSHIP_EINVAL, "store_kv: head size not a multiple of 8%s");
+    if (seq && seq_stride < 0) return fail(LNSHIP_EINVAL, "store_kv: negative sequence stride%s");
     const int64_t n = ntok * nhead * ne0;
     if (n == 0) return 0;
     hipLaunchKernelGGL(k_store_kv16, dim3(grid_for(n, 4)), dim3(k_block), 0, (hipStream_t)stream, x, x_ld, pos, ntok,
-                       nhead, ne0, rope_n_dims, cos_sin, cache, cache_m, cache_slice, cache_transposed, s->T);
+                       nhead, ne0, rope_n_dims, cos_sin, cache, cache_m, cache_slice, cache_transposed, seq, seq_stride,
+                       s->T);
     LNSHIP_HIP(hipGetLastError());
     return 0;
 }
@@ -1550,10 +1551,10 @@ int lnship_rope_table(float freq_base, int n_dims, int64_t n_pos, float *out) {
     return 0;
 }
 
-int lnship_causal_mask(const int32_t *pos0, int64_t ntok, int64_t n_kv, float *mask, void *stream) {
+int lnship_causal_mask(const int32_t *pos, int64_t ntok, int64_t n_kv, float *mask, void *stream) {
     if (ntok < 0 || n_kv < 0) return fail(LNSHIP_EINVAL, "causal_mask: bad shape%s");
     if (ntok == 0 || n_kv == 0) return 0;
-    hipLaunchKernelGGL(k_causal_mask, dim3(grid_for(ntok * n_kv, 4)), dim3(k_block), 0, (hipStream_t)stream, pos0, ntok,
+    hipLaunchKernelGGL(k_causal_mask, dim3(grid_for(ntok * n_kv, 4)), dim3(k_block), 0, (hipStream_t)stream, pos, ntok,
                        n_kv, mask);
     LNSHIP_HIP(hipGetLastError());
     return 0;

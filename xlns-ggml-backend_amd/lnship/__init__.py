@@ -78,7 +78,7 @@ def lib():
         "lnship16_rope": (ctypes.c_int, [c_p, c_i64, c_p, c_i64, c_i64, c_i64, ctypes.c_int, ctypes.c_int, c_p, c_p,
                                          c_p]),
         "lnship16_store_kv": (ctypes.c_int, [c_p, c_i64, c_p, c_i64, c_i64, c_i64, ctypes.c_int, c_p, c_p, c_i64,
-                                             c_i64, ctypes.c_int, c_p]),
+                                             c_i64, ctypes.c_int, c_p, c_i64, c_p]),
         "lnship_causal_mask": (ctypes.c_int, [c_p, c_i64, c_i64, c_p, c_p]),
         "lnship_rope_table": (ctypes.c_int, [ctypes.c_float, ctypes.c_int, c_i64, c_p]),
     }

@@ -18,6 +18,13 @@ Fusing Q|K|V and up|gate into one matrix keeps the Monte draw order of the
 separate ops: outputs of a mul_mat take draws in (row, column) order, so the
 fused rows enumerate Q's outputs, then K's, then V's.
 
+With n_seq > 1 the model holds that many independent sequences, each with
+its own KV cache, as llama.cpp's per-sequence KV streams.  A sequence's
+prompt runs on its own (eval with seq=s); a batched decode step (eval_batch)
+takes one token per sequence: the weight mul_mats see N = n_seq columns and
+attention runs over all sequences at once through the 4th dimension
+(kq = K_s^T q_s and kqv = V_s p_s for each sequence s, masked per sequence).
+
 Activations, weights and the KV cache live in HBM; nothing is copied back to
 the host except the logits the caller asks for.
 """
@@ -97,10 +104,10 @@ def n_kv_for(n_used, n_ctx):
 class LlamaLNS16:
     """The decoder on one GPU; mode is the xlns16 summation mode."""
 
-    def __init__(self, cfg, weights, mode=SUM32, lfsr=7):
+    def __init__(self, cfg, weights, mode=SUM32, lfsr=7, n_seq=1):
         import torch
         init()
-        self.cfg, self.mode, self.lfsr = cfg, mode, lfsr
+        self.cfg, self.mode, self.lfsr, self.n_seq = cfg, mode, lfsr, n_seq
         self.torch = torch
         dev = torch.device("cuda", torch.cuda.current_device())
         self.dev = dev
@@ -120,17 +127,30 @@ class LlamaLNS16:
                 "wdown": pack16(t(L["w_down"])),
             })
         hd, nkv = c.head_dim, c.n_head_kv
-        # packed LNS16 caches, per layer: K [nkv][hd/8][n_ctx][8], V [nkv][n_ctx/8][hd][8]
+        # packed LNS16 caches, per layer and sequence: K [nkv][hd/8][n_ctx][8],
+        # V [nkv][n_ctx/8][hd][8]; the sequences' caches follow each other
         self.kslice = kp(hd) * c.n_ctx
         self.vslice = kp(c.n_ctx) * hd
-        self.kcache = [torch.zeros(nkv * self.kslice, dtype=torch.int16, device=dev) for _ in range(c.n_layer)]
-        self.vcache = [torch.zeros(nkv * self.vslice, dtype=torch.int16, device=dev) for _ in range(c.n_layer)]
+        assert self.kslice == self.vslice
+        self.seq_stride = nkv * self.kslice
+        self.kcache = [torch.zeros(n_seq * self.seq_stride, dtype=torch.int16, device=dev) for _ in range(c.n_layer)]
+        self.vcache = [torch.zeros(n_seq * self.seq_stride, dtype=torch.int16, device=dev) for _ in range(c.n_layer)]
         rt = np.empty(c.n_ctx * hd, np.float32)
         check(lib().lnship_rope_table(c.rope_theta, hd, c.n_ctx, ctypes.c_void_p(rt.ctypes.data)))
         self.cos_sin = t(rt)
-        self.n_past = 0
+        self.seq_ids = torch.arange(n_seq, dtype=torch.int32, device=dev)
+        self.past = [0] * n_seq
         self._bufs = {}
         self._graphs = {}
+
+    @property
+    def n_past(self):
+        """Tokens held by sequence 0."""
+        return self.past[0]
+
+    @n_past.setter
+    def n_past(self, v):
+        self.past[0] = v
 
     # -- buffers --------------------------------------------------------------
     def _buf(self, name, n, dtype=None):
@@ -151,8 +171,8 @@ class LlamaLNS16:
 
     # -- ops --------------------------------------------------------------------
     def _mm(self, w, x_ptr, dst_ptr, K, M, N, **kw):
-        ne12 = kw.get("ne12", 1)
-        draws = lib().lnship16_mul_mat_draws(self.mode, K, M, N, ne12, 1)
+        ne12, ne13 = kw.get("ne12", 1), kw.get("ne13", 1)
+        draws = lib().lnship16_mul_mat_draws(self.mode, K, M, N, ne12, ne13)
         mul_mat16_raw(self.mode, w, x_ptr, dst_ptr, K, M, N, seed=self._seed(draws), stream=self._stream, **kw)
 
     def _rms(self, x_ptr, dst_ptr, ncols, nrows):
@@ -167,10 +187,14 @@ class LlamaLNS16:
         check(lib().lnship16_soft_max(self.mode, ctypes.byref(a), self._stream))
 
     # -- forward -------------------------------------------------------------------
-    def forward(self, T, tokens_dev, pos_dev, n_kv):
+    def forward(self, T, tokens_dev, pos_dev, n_kv, seq=0, batch=False):
         """Runs T tokens at positions pos_dev[0..T) (device int32) against a
-        KV view of n_kv cells; returns the device logits of the last token."""
+        KV view of n_kv cells.  Without batch all T tokens belong to sequence
+        seq and the device logits of the last one are returned; with batch
+        T == n_seq, token s belongs to sequence s, and the logits of every
+        token come back ([n_seq][n_vocab])."""
         torch, c, L = self.torch, self.cfg, lib()
+        assert not batch or T == self.n_seq
         self._stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
         st = self._stream
         e, hd, nh, nkv, f = c.n_embd, c.head_dim, c.n_head, c.n_head_kv, c.n_ff
@@ -186,7 +210,10 @@ class LlamaLNS16:
         ug = self._buf("ug", T * 2 * f)
         sw = self._buf("sw", T * f)
         mask = self._buf("mask", T * n_kv)
-        logits = self._buf("logits", c.n_vocab)
+        logits = self._buf("logits", (T if batch else 1) * c.n_vocab)
+        nseq = self.n_seq if batch else 1
+        cbase = 0 if batch else seq * self.seq_stride   # cache offset (codes) of the attended sequence
+        seq_ids = P(self.seq_ids) if batch else None
         check(L.lnship16_get_rows_packed(P(self.tok_embd), e, c.n_vocab, P(tokens_dev), T, P(x), st))
         check(L.lnship_causal_mask(P(pos_dev), T, n_kv, P(mask), st))
         for il, W in enumerate(self.layers):
@@ -196,19 +223,23 @@ class LlamaLNS16:
             self._mm(W["wqkv"].data_ptr(), P(h), P(qkv), e, nqkv, T)
             check(L.lnship16_rope(P(qkv), nqkv, P(pos_dev), T, nh, hd, hd, 0, P(self.cos_sin), P(q), st))
             check(L.lnship16_store_kv(P(qkv, nq), nqkv, P(pos_dev), T, nkv, hd, hd, P(self.cos_sin),
-                                      P(self.kcache[il]), c.n_ctx, self.kslice, 0, st))
+                                      P(self.kcache[il], cbase), c.n_ctx, self.kslice, 0, seq_ids, self.seq_stride,
+                                      st))
             check(L.lnship16_store_kv(P(qkv, nq + nkv * hd), nqkv, P(pos_dev), T, nkv, hd, 0, P(self.cos_sin),
-                                      P(self.vcache[il]), c.n_ctx, self.vslice, 1, st))
-            # kq[h][t][j] = K_j . q_t (GQA: query head h reads kv head h / (nh / nkv))
-            self._mm(self.kcache[il].data_ptr(), P(q), P(kq), hd, n_kv, T, ne02=nkv, ne12=nh,
-                     x_ld=nq, x_slice=hd, w_mstride=c.n_ctx, w_slice=self.kslice)
-            self._softmax(P(kq), (n_kv, T, nh, 1), P(mask), (n_kv, T, 1, 1), 1.0 / math.sqrt(hd), P(kq))
-            # att[t][h*hd + d] = sum_j V[j][d] p[h][t][j]
-            self._mm(self.vcache[il].data_ptr(), P(kq), P(att), n_kv, hd, T, ne02=nkv, ne12=nh,
-                     x_ld=n_kv, x_slice=T * n_kv, w_slice=self.vslice, dst_ld=nq, dst_slice=hd)
+                                      P(self.vcache[il], cbase), c.n_ctx, self.vslice, 1, seq_ids, self.seq_stride,
+                                      st))
+            Tq = 1 if batch else T   # query rows per sequence
+            # kq[s][h][t][j] = K_s,j . q_s,t (GQA: query head h reads kv head h / (nh / nkv))
+            self._mm(self.kcache[il].data_ptr() + 2 * cbase, P(q), P(kq), hd, n_kv, Tq, ne02=nkv, ne03=nseq,
+                     ne12=nh, ne13=nseq, x_ld=nq, x_slice=hd, w_mstride=c.n_ctx, w_slice=self.kslice)
+            self._softmax(P(kq), (n_kv, Tq, nh, nseq), P(mask), (n_kv, Tq, 1, nseq), 1.0 / math.sqrt(hd), P(kq))
+            # att[s, t][h*hd + d] = sum_j V_s[j][d] p[s][h][t][j]
+            self._mm(self.vcache[il].data_ptr() + 2 * cbase, P(kq), P(att), n_kv, hd, Tq, ne02=nkv, ne03=nseq,
+                     ne12=nh, ne13=nseq, x_ld=n_kv, x_slice=Tq * n_kv, w_slice=self.vslice, dst_ld=nq,
+                     dst_slice=hd)
             self._mm(W["wo"].data_ptr(), P(att), P(o), nq, e, T)
-            # after the last layer's attention only the output row goes on
-            rows = 1 if last else T
+            # after the last layer's attention only the output rows go on
+            rows = 1 if last and not batch else T
             r0 = (T - rows) * e
             check(L.lnship16_add(P(o, r0), P(x, r0), rows * e, rows * e, P(x), st))
             self._rms(P(x), P(h), e, rows)
@@ -217,25 +248,80 @@ class LlamaLNS16:
             check(L.lnship16_swiglu(P(ug, f), 2 * f, P(ug), 2 * f, P(sw), f, rows, st))
             self._mm(W["wdown"].data_ptr(), P(sw), P(o), f, e, rows)
             check(L.lnship16_add(P(o), P(x), rows * e, rows * e, P(x), st))
-        self._rms(P(x), P(h), e, 1)
-        check(L.lnship16_mul(P(h), P(self.out_norm), e, e, P(h), st))
-        self._mm(self.tok_embd.data_ptr(), P(h), P(logits), e, c.n_vocab, 1)
+        nout = T if batch else 1
+        self._rms(P(x), P(h), e, nout)
+        check(L.lnship16_mul(P(h), P(self.out_norm), nout * e, e, P(h), st))
+        self._mm(self.tok_embd.data_ptr(), P(h), P(logits), e, c.n_vocab, nout)
+        if batch:
+            return logits[: T * c.n_vocab].view(T, c.n_vocab)
         return logits[: c.n_vocab]
 
-    def eval(self, tokens):
-        """Appends tokens (host list) at the current position; returns the
-        device logits of the last one."""
+    def eval(self, tokens, seq=0):
+        """Appends tokens (host list) to sequence seq; returns the device
+        logits of the last one."""
         torch = self.torch
         T = len(tokens)
-        assert self.n_past + T <= self.cfg.n_ctx, "context full"
+        p0 = self.past[seq]
+        assert p0 + T <= self.cfg.n_ctx, "context full"
         tok = self._buf("tok", T, torch.int32)
         pos = self._buf("pos", T, torch.int32)
         tok[:T].copy_(torch.tensor(tokens, dtype=torch.int32))
-        pos[:T].copy_(torch.arange(self.n_past, self.n_past + T, dtype=torch.int32))
-        n_kv = n_kv_for(self.n_past + T, self.cfg.n_ctx)
-        out = self.forward(T, tok, pos, n_kv)
-        self.n_past += T
+        pos[:T].copy_(torch.arange(p0, p0 + T, dtype=torch.int32))
+        n_kv = n_kv_for(p0 + T, self.cfg.n_ctx)
+        out = self.forward(T, tok, pos, n_kv, seq=seq)
+        self.past[seq] += T
         return out
+
+    def eval_batch(self, tokens):
+        """One decode step of every sequence: tokens[s] is appended to
+        sequence s.  Returns the device logits [n_seq][n_vocab]."""
+        torch = self.torch
+        assert len(tokens) == self.n_seq
+        assert max(self.past) < self.cfg.n_ctx, "context full"
+        tok = self._buf("btok", self.n_seq, torch.int32)
+        pos = self._buf("bpos", self.n_seq, torch.int32)
+        tok[: self.n_seq].copy_(torch.tensor(tokens, dtype=torch.int32))
+        pos[: self.n_seq].copy_(torch.tensor(self.past, dtype=torch.int32))
+        out = self.forward(self.n_seq, tok, pos, self.batch_n_kv(), batch=True)
+        self.past = [p + 1 for p in self.past]
+        return out
+
+    def batch_n_kv(self):
+        """KV view of a batched step: the longest sequence's, padded."""
+        return n_kv_for(max(self.past) + 1, self.cfg.n_ctx)
+
+    def decode_graph_batch(self, tok_dev, n_kv=None):
+        """eval_batch through a captured HIP graph (non-Monte modes), with the
+        n_seq tokens already on the device.  Returns the device logits."""
+        torch = self.torch
+        assert self.mode != MONTE, "Monte seeds change every step; use eval_batch()"
+        n_kv = n_kv or self.batch_n_kv()
+        tok = self._buf("gbtok", self.n_seq, torch.int32)
+        pos = self._buf("gbpos", self.n_seq, torch.int32)
+        tok[: self.n_seq].copy_(tok_dev[: self.n_seq])
+        pos[: self.n_seq].copy_(torch.tensor(self.past, dtype=torch.int32))
+        key = ("batch", n_kv)
+        if key not in self._graphs:
+            self._graphs[key] = self._capture(lambda: self.forward(self.n_seq, tok, pos, n_kv, batch=True))
+        g, out = self._graphs[key]
+        g.replay()
+        self.past = [p + 1 for p in self.past]
+        return out
+
+    def _capture(self, run):
+        """Warms the library's scratch and the buffers with one eager run,
+        then captures run() into a HIP graph; returns (graph, output)."""
+        torch = self.torch
+        run()
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            with torch.cuda.graph(g, stream=s):
+                out = run()
+        torch.cuda.current_stream().wait_stream(s)
+        return g, out
 
     def decode_graph(self, token, n_kv=None):
         """One decode step through a captured HIP graph (non-Monte modes: the
@@ -247,19 +333,8 @@ class LlamaLNS16:
         pos = self._buf("gpos", 1, torch.int32)
         tok.fill_(int(token))
         pos.fill_(self.n_past)
-        g = self._graphs.get(n_kv)
-        if g is None:
-            # warm the library's scratch and the buffers, then capture
-            self.forward(1, tok, pos, n_kv)
-            torch.cuda.synchronize()
-            g = torch.cuda.CUDAGraph()
-            s = torch.cuda.Stream()
-            s.wait_stream(torch.cuda.current_stream())
-            with torch.cuda.stream(s):
-                with torch.cuda.graph(g, stream=s):
-                    out = self.forward(1, tok, pos, n_kv)
-            torch.cuda.current_stream().wait_stream(s)
-            self._graphs[n_kv] = (g, out)
+        if n_kv not in self._graphs:
+            self._graphs[n_kv] = self._capture(lambda: self.forward(1, tok, pos, n_kv))
         g, out = self._graphs[n_kv]
         g.replay()
         self.n_past += 1
