@@ -54,6 +54,7 @@ static int hip_fail(hipError_t e, const char *where) {
 
 struct device_state {
     bool ready = false;
+    int cus = 0;   // compute units
     dev_tables T{};
     void *scratch = nullptr;   // grow-only
     size_t scratch_size = 0;
@@ -1086,21 +1087,33 @@ static int check_mm(const lnship_mul_mat_args *a) {
     return 0;
 }
 
-// NC columns per lane for N activation columns
-static int mm16_nc(int64_t N) { return N >= 8 ? 8 : (N >= 4 ? 4 : 1); }
-
-template <int MODE>
-static bool mm16_xl_fits(int nc, int64_t kp) {
-    return mm_xl_offset<MODE>() + (int64_t)nc * kp * 2 <= k_lds_bytes - 1024;
+static int64_t mm16_tables_bytes(int mode) {
+    switch (mode) {
+        case LNSHIP_BASE: return mm_xl_offset<LNSHIP_BASE>();
+        case LNSHIP_MONTE: return mm_xl_offset<LNSHIP_MONTE>();
+        case LNSHIP_LPVIP: return mm_xl_offset<LNSHIP_LPVIP>();
+        default: return mm_xl_offset<LNSHIP_SUM32>();
+    }
 }
 
+// whether NC activation rows of kp codes fit in LDS next to the tables
 static bool mm16_xl(int mode, int nc, int64_t kp) {
-    switch (mode) {
-        case LNSHIP_BASE: return mm16_xl_fits<LNSHIP_BASE>(nc, kp);
-        case LNSHIP_MONTE: return mm16_xl_fits<LNSHIP_MONTE>(nc, kp);
-        case LNSHIP_LPVIP: return mm16_xl_fits<LNSHIP_LPVIP>(nc, kp);
-        default: return mm16_xl_fits<LNSHIP_SUM32>(nc, kp);
+    return mm16_tables_bytes(mode) + (int64_t)nc * kp * 2 <= k_lds_bytes - 1024;
+}
+
+// Columns per lane.  Every output is a K-long dependent chain, so a lane is
+// fastest with one chain; the fewest columns per lane whose workgroups all
+// fit on the GPU at once (LDS and about three waves per SIMD allowing) wins.
+// When even eight columns per lane take more than one round, throughput
+// decides: eight columns share one weight load and one decode per step.
+static int mm16_nc(int mode, int64_t M, int64_t N, int64_t nslices, int64_t kp, int cus) {
+    const int64_t wg_m = (M + k_block - 1) / k_block;
+    for (int nc : {1, 4, 8}) {
+        const int64_t lds = mm16_tables_bytes(mode) + (mm16_xl(mode, nc, kp) ? (int64_t)nc * kp * 2 : 0);
+        const int64_t per_cu = std::max<int64_t>(1, std::min<int64_t>(3, k_lds_bytes / std::max<int64_t>(lds, 1)));
+        if (wg_m * ((N + nc - 1) / nc) * nslices <= (int64_t)std::max(cus, 1) * per_cu) return nc;
     }
+    return 8;
 }
 
 template <int MODE, int NC, bool XL>
@@ -1122,8 +1135,8 @@ static int launch_mm16_x(const mm_args16 &m, const dev_tables &T, int64_t nslice
 }
 
 template <int MODE>
-static int dispatch_mm16(const mm_args16 &m, const dev_tables &T, int64_t nslices, bool xl, hipStream_t st) {
-    switch (mm16_nc(m.N)) {
+static int dispatch_mm16(const mm_args16 &m, const dev_tables &T, int64_t nslices, int nc, bool xl, hipStream_t st) {
+    switch (nc) {
         case 8: return launch_mm16_x<MODE, 8>(m, T, nslices, xl, st);
         case 4: return launch_mm16_x<MODE, 4>(m, T, nslices, xl, st);
         default: return launch_mm16_x<MODE, 1>(m, T, nslices, xl, st);
@@ -1236,6 +1249,7 @@ int lnship_init(void) {
     if (int rc = upload(g_host->lfsr_seq, 65536, &T.lfsr_seq)) return rc;
     if (int rc = upload(g_host->lfsr_log, 65536, &T.lfsr_log)) return rc;
     s.T = T;
+    LNSHIP_HIP(hipDeviceGetAttribute(&s.cus, hipDeviceAttributeMultiprocessorCount, dev));
     s.ready = true;
     return 0;
 }
@@ -1325,7 +1339,8 @@ int lnship16_mul_mat(int mode, const lnship_mul_mat_args *a, void *stream) {
     hipStream_t st = (hipStream_t)stream;
     // activations converted inside the GEMV when NC rows fit in LDS next to
     // the tables, else by k_act into scratch first
-    const bool xl = mm16_xl(mode, mm16_nc(a->N), kp);
+    const int nc = mm16_nc(mode, a->M, a->N, nslices, kp, s->cus);
+    const bool xl = mm16_xl(mode, nc, kp);
     void *xs = nullptr;
     if (!xl) {
         if (int rc = scratch(s, (size_t)std::max<int64_t>(1, nslices * a->N * kp) * 2, &xs)) return rc;
@@ -1342,10 +1357,10 @@ int lnship16_mul_mat(int mode, const lnship_mul_mat_args *a, void *stream) {
                 wms, a->w_slice ? a->w_slice : kp * wms, dld, a->dst_slice ? a->dst_slice : a->N * dld,
                 a->monte_seed};
     switch (mode) {
-        case LNSHIP_BASE: return dispatch_mm16<LNSHIP_BASE>(m, s->T, nslices, xl, st);
-        case LNSHIP_MONTE: return dispatch_mm16<LNSHIP_MONTE>(m, s->T, nslices, xl, st);
-        case LNSHIP_LPVIP: return dispatch_mm16<LNSHIP_LPVIP>(m, s->T, nslices, xl, st);
-        default: return dispatch_mm16<LNSHIP_SUM32>(m, s->T, nslices, xl, st);
+        case LNSHIP_BASE: return dispatch_mm16<LNSHIP_BASE>(m, s->T, nslices, nc, xl, st);
+        case LNSHIP_MONTE: return dispatch_mm16<LNSHIP_MONTE>(m, s->T, nslices, nc, xl, st);
+        case LNSHIP_LPVIP: return dispatch_mm16<LNSHIP_LPVIP>(m, s->T, nslices, nc, xl, st);
+        default: return dispatch_mm16<LNSHIP_SUM32>(m, s->T, nslices, nc, xl, st);
     }
 }
 
@@ -1372,7 +1387,10 @@ int lnship32_mul_mat(const lnship_mul_mat_args *a, void *stream) {
     mm_args32 m{(const uint32_t *)a->w, (const uint32_t *)xs, a->dst, a->K, kp, a->M, a->N,
                 a->ne02, a->ne12, a->ne12 / a->ne02, a->ne13 / a->ne03,
                 wms, a->w_slice ? a->w_slice : kp * wms, dld, a->dst_slice ? a->dst_slice : a->N * dld};
-    if (m.N >= 4) return launch_mm32<4>(m, s->T, nslices, st);
+    // one column per lane while every workgroup fits on the GPU at once
+    // (the tables allow one workgroup per CU), else four
+    const int64_t wg_m = (m.M + k_block - 1) / k_block;
+    if (m.N >= 4 && wg_m * m.N * nslices > std::max(s->cus, 1)) return launch_mm32<4>(m, s->T, nslices, st);
     return launch_mm32<1>(m, s->T, nslices, st);
 }
 
