@@ -205,9 +205,11 @@ def gemv_roofline(model, ln, torch, reps=4):
         tok = model._buf("rtok", 1, torch.int32)
         pos = model._buf("rpos", 1, torch.int32)
         tok.fill_(1)
-        pos.fill_(model.n_past)
+        # the last timed position again, so the launches have the timed
+        # steps' shapes (its KV row is rewritten; nothing reads it afterwards)
+        pos.fill_(model.n_past - 1)
         from lnship.llama import n_kv_for
-        model.forward(1, tok, pos, n_kv_for(model.n_past + 1, c.n_ctx))
+        model.forward(1, tok, pos, n_kv_for(model.n_past, c.n_ctx))
         torch.cuda.synchronize()
     finally:
         model._mm = orig

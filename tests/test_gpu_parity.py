@@ -143,6 +143,52 @@ def test_mul_mat_f16_weights(ln):
     same_bits(got, want, "f16 weights")
 
 
+def _sample(n, step):
+    return np.unique(np.concatenate([np.arange(0, n, step), [n - 1]]))
+
+
+# Shapes that select each workgroup shape of the xlns32-accumulating GEMVs on
+# a 256-CU MI355X: (columns per lane, column groups), and whether the
+# activations fit in LDS next to the tables.  Each output depends on its own
+# row and column only, so the big shapes are checked exactly on a sample of
+# rows x columns (every column group and wave slot is hit).
+X32_SHAPES = [
+    # K,    M,    N      lane cols x groups
+    (21, 64, 1),      # 1 x 1
+    (21, 64, 384),    # 1 x 2
+    (21, 70, 768),    # 1 x 4, ragged rows
+    (21, 64, 2000),   # 2 x 4, ragged columns
+    (21, 300, 2048),  # 4 x 4
+    (21, 1024, 2048),  # 8 x 4, activations in LDS
+    (1000, 1024, 2048),  # 8 x 4, activations from global memory
+    (1701, 300, 2040),  # 4 x 4, activations from global memory, K tail
+]
+
+
+@pytest.mark.parametrize("K,M,N", X32_SHAPES)
+def test_mul_mat_sum32_workgroup_shapes(ln, K, M, N):
+    print(f"\n[mul_mat sum32 shape] K={K} M={M} N={N}", flush=True)
+    rng = np.random.default_rng(K * 7 + M + N)
+    w = (rng.standard_normal((M, K)) * 0.02).astype(np.float32)
+    x = rng.standard_normal((N, K)).astype(np.float32)
+    got = host(ln.mul_mat16(O.SUM32, ln.pack16(dev(w)), dev(x), K, M))
+    rows, cols = (_sample(M, 13), _sample(N, 31)) if K * M * N > 5e7 else (np.arange(M), np.arange(N))
+    want = O.mul_mat16_f32w(O.SUM32, w[rows][None, None], x[cols][None, None])
+    same_bits(got[cols][:, rows], want.reshape(len(cols), len(rows)), f"sum32 K={K} M={M} N={N}")
+
+
+@pytest.mark.parametrize("K,M,N", X32_SHAPES[:5] + [(1000, 300, 2040)])
+def test_mul_mat_lns32_workgroup_shapes(ln, K, M, N):
+    print(f"\n[mul_mat lns32 shape] K={K} M={M} N={N}", flush=True)
+    rng = np.random.default_rng(K * 5 + M + N)
+    w = (rng.standard_normal((M, K)) * 0.02).astype(np.float32)
+    x = rng.standard_normal((N, K)).astype(np.float32)
+    got = host(ln.mul_mat32(ln.pack32(dev(w)), dev(x), K, M))
+    rows, cols = (_sample(M, 13), _sample(N, 31)) if K * M * N > 5e7 else (np.arange(M), np.arange(N))
+    want = O.mul_mat32(w[rows], x[cols])
+    same_bits(got[cols][:, rows], want.reshape(len(cols), len(rows)), f"lns32 K={K} M={M} N={N}")
+
+
 def test_mul_mat_lns32(ln):
     for (K, M, N, seed) in ((576, 300, 1, 20), (1536, 64, 5, 21), (9, 40, 3, 22)):
         print(f"\n[mul_mat lns32] K={K} M={M} N={N}", flush=True)

@@ -499,27 +499,33 @@ constexpr int mm_xl_offset() { return (lds_tables_bytes<MODE>() + 15) & ~15; }
 
 __device__ __forceinline__ uint32_t half16(uint32_t w, int hi) { return hi ? (w >> 16) : (w & 0xffffu); }
 
-template <int MODE, int NC, int PF, bool XL>
-__global__ __launch_bounds__(k_block) void k_mm16(mm_args16 a, dev_tables T) {
+template <int MODE, int NC, int PF, bool XL, int CG>
+__global__ __launch_bounds__(k_block * CG) void k_mm16(mm_args16 a, dev_tables T) {
     extern __shared__ __align__(16) char lds[];
     const red16<MODE> R = stage_tables<MODE>(T, lds);
-    const int64_t n0 = (int64_t)blockIdx.y * NC;
+    // CG column groups of k_block lanes each share the staged tables: group
+    // c takes columns [nw + c NC, nw + (c + 1) NC) of the same k_block rows
+    const int cg = CG == 1 ? 0 : (int)(threadIdx.x / k_block);
+    const int64_t nw = (int64_t)blockIdx.y * (NC * CG);
+    const int64_t n0 = nw + (int64_t)cg * NC;
     const int64_t z = blockIdx.z;
     const int64_t i12 = z % a.ne12, i13 = z / a.ne12;
-    const int nc = (int)min<int64_t>(NC, a.N - n0);
+    const int ncw = (int)min<int64_t>(NC * CG, a.N - nw);
+    const int nc = (int)max<int64_t>(0, min<int64_t>(NC, a.N - n0));
     const int kp = (int)a.kp;
     uint16_t *xl = reinterpret_cast<uint16_t *>(lds + mm_xl_offset<MODE>());
     if (XL) {
         // columns past N and k past K hold xlns16 zero
-        const float *xf = a.xf + z * a.x_slice + n0 * a.x_ld;
-        for (int j = 0; j < NC; j++)
-            for (int k = threadIdx.x; k < kp; k += k_block)
-                xl[j * kp + k] = (j < nc && k < a.K) ? (uint16_t)x16_from_f32(T.cvt16, xf[j * a.x_ld + k]) : (uint16_t)0;
+        const float *xf = a.xf + z * a.x_slice + nw * a.x_ld;
+        for (int j = 0; j < NC * CG; j++)
+            for (int k = threadIdx.x; k < kp; k += k_block * CG)
+                xl[j * kp + k] = (j < ncw && k < a.K) ? (uint16_t)x16_from_f32(T.cvt16, xf[j * a.x_ld + k]) : (uint16_t)0;
+        xl += cg * NC * kp;
     }
     __syncthreads();
 
-    const int64_t m = (int64_t)blockIdx.x * k_block + threadIdx.x;
-    if (m >= a.M) return;
+    const int64_t m = (int64_t)blockIdx.x * k_block + (threadIdx.x % k_block);
+    if (m >= a.M || nc == 0) return;
     const uint16_t *ws = a.w + ((i13 / a.r3) * a.ne02 + i12 / a.r2) * a.w_slice + m * 8;
     const uint16_t *xs = a.x + (z * a.N + n0) * a.kp;
     const int64_t wstride = a.w_mstride * 8;   // between consecutive groups of 8 k
@@ -629,51 +635,102 @@ struct mm_args32 {
     int64_t w_mstride, w_slice, dst_ld, dst_slice;
 };
 
-template <int NC>
-__global__ __launch_bounds__(k_block) void k_mm32(mm_args32 a, dev_tables T) {
+// One lane per weight row m and NC columns, CG column groups per workgroup
+// sharing the staged tables (as k_mm16).  A group of eight k is two 16-byte
+// loads of weights and two per column of activations; the next PF groups are
+// in flight while one is accumulated.
+template <int NC, int PF, int CG>
+__global__ __launch_bounds__(k_block * CG) void k_mm32(mm_args32 a, dev_tables T) {
     extern __shared__ __align__(16) char lds[];
     const red16<LNSHIP_SUM32> R = stage_tables<LNSHIP_SUM32>(T, lds);
     __syncthreads();
-    const int64_t m = (int64_t)blockIdx.x * k_block + threadIdx.x;
-    if (m >= a.M) return;
-    const int64_t n0 = (int64_t)blockIdx.y * NC;
+    const int cg = CG == 1 ? 0 : (int)(threadIdx.x / k_block);
+    const int64_t m = (int64_t)blockIdx.x * k_block + (threadIdx.x % k_block);
+    const int64_t n0 = ((int64_t)blockIdx.y * CG + cg) * NC;
+    if (m >= a.M || n0 >= a.N) return;
     const int64_t z = blockIdx.z;
     const int64_t i12 = z % a.ne12, i13 = z / a.ne12;
     const int nc = (int)min<int64_t>(NC, a.N - n0);
     const uint32_t *ws = a.w + ((i13 / a.r3) * a.ne02 + i12 / a.r2) * a.w_slice + m * 8;
     const uint32_t *xs = a.x + (z * a.N + n0) * a.kp;
     const int64_t wstride = a.w_mstride * 8;
+    float *ds = a.dst + z * a.dst_slice + n0 * a.dst_ld + m;
+    if (a.K == 0) {
+        for (int j = 0; j < nc; j++) ds[(int64_t)j * a.dst_ld] = 0.0f;
+        return;
+    }
+    struct grp {
+        uint4 lo, hi;
+    };
+    const int K = (int)a.K;
+    const int full = K >> 3, tail = K & 7;
+    const int last = (int)(a.kp >> 3) - 1;   // loads past the end reload the last group
+    auto load_w = [&](int g) {
+        const uint4 *p = reinterpret_cast<const uint4 *>(ws + (int64_t)min(g, last) * wstride);
+        return grp{p[0], p[1]};
+    };
+    auto load_x = [&](int j, int g) {
+        // a per-lane offset keeps the wave-uniform read a vector load
+        int64_t off = (int64_t)(j < nc ? j : 0) * a.kp + (int64_t)min(g, last) * 8;
+        asm("" : "+v"(off));
+        const uint4 *p = reinterpret_cast<const uint4 *>(xs + off);
+        return grp{p[0], p[1]};
+    };
     acc_ls acc[NC];
-    const int64_t kgroups = a.kp >> 3;
-    for (int64_t g = 0; g < kgroups; g++) {
-        const uint4 w0 = *reinterpret_cast<const uint4 *>(ws + g * wstride);
-        const uint4 w1 = *reinterpret_cast<const uint4 *>(ws + g * wstride + 4);
-        const uint32_t wv[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
-        uint32_t xv[NC][8];
-#pragma unroll
-        for (int j = 0; j < NC; j++) {
-            const int jj = j < nc ? j : 0;
-            const uint4 x0 = *reinterpret_cast<const uint4 *>(xs + jj * a.kp + g * 8);
-            const uint4 x1 = *reinterpret_cast<const uint4 *>(xs + jj * a.kp + g * 8 + 4);
-            xv[j][0] = x0.x; xv[j][1] = x0.y; xv[j][2] = x0.z; xv[j][3] = x0.w;
-            xv[j][4] = x1.x; xv[j][5] = x1.y; xv[j][6] = x1.z; xv[j][7] = x1.w;
-        }
-        const int64_t kb = g * 8;
+    auto steps = [&](const grp &wq, const grp (&xq)[NC], int u0, int u1) {
+        const uint32_t wv[8] = {wq.lo.x, wq.lo.y, wq.lo.z, wq.lo.w, wq.hi.x, wq.hi.y, wq.hi.z, wq.hi.w};
 #pragma unroll
         for (int u = 0; u < 8; u++) {
-            if (kb + u >= a.K) break;
+            if (u >= u0 && u < u1) {
 #pragma unroll
-            for (int j = 0; j < NC; j++) {
-                const uint32_t t = x32_mul(wv[u], xv[j][u]);
-                if (kb + u == 0) acc[j] = {t & k32_logmask, t & k32_sign};
-                else x32_add_ls(R.O, acc[j], t & k32_logmask, t & k32_sign);
+                for (int j = 0; j < NC; j++) {
+                    const uint4 &q = u < 4 ? xq[j].lo : xq[j].hi;
+                    const uint32_t xv = (u & 3) == 0 ? q.x : (u & 3) == 1 ? q.y : (u & 3) == 2 ? q.z : q.w;
+                    const uint32_t t = x32_mul(wv[u], xv);
+                    if (u == 0 && u0 < 0) acc[j] = {t & k32_logmask, t & k32_sign};
+                    else x32_add_ls(R.O, acc[j], t & k32_logmask, t & k32_sign);
+                }
             }
         }
+    };
+    {
+        grp xq[NC];
+#pragma unroll
+        for (int j = 0; j < NC; j++) xq[j] = load_x(j, 0);
+        const grp wq = load_w(0);
+        grp wa[PF], wb[PF], xa[PF][NC], xb[PF][NC];
+        auto load_block = [&](grp (&w)[PF], grp (&x)[PF][NC], int g0) {
+#pragma unroll
+            for (int p = 0; p < PF; p++) {
+                w[p] = load_w(g0 + p);
+#pragma unroll
+                for (int j = 0; j < NC; j++) x[p][j] = load_x(j, g0 + p);
+            }
+        };
+        auto run_block = [&](const grp (&w)[PF], const grp (&x)[PF][NC], int g0) {
+#pragma unroll
+            for (int p = 0; p < PF; p++)
+                if (g0 + p < full) steps(w[p], x[p], 0, 8);
+        };
+        load_block(wa, xa, 1);
+        steps(wq, xq, -1, full > 0 ? 8 : tail);
+        for (int g = 1; g < full; g += 2 * PF) {
+            load_block(wb, xb, g + PF);
+            run_block(wa, xa, g);
+            if (g + PF >= full) break;
+            load_block(wa, xa, g + 2 * PF);
+            run_block(wb, xb, g + PF);
+        }
+        if (full > 0 && tail > 0) {
+            grp tx[NC];
+#pragma unroll
+            for (int j = 0; j < NC; j++) tx[j] = load_x(j, full);
+            steps(load_w(full), tx, 0, tail);
+        }
     }
-    float *ds = a.dst + z * a.dst_slice + n0 * a.dst_ld + m;
 #pragma unroll
     for (int j = 0; j < NC; j++)
-        if (j < nc) ds[(int64_t)j * a.dst_ld] = a.K == 0 ? 0.0f : x32_to_f32(acc[j].s | acc[j].l);
+        if (j < nc) ds[(int64_t)j * a.dst_ld] = x32_to_f32(acc[j].s | acc[j].l);
 }
 
 // ---- sequential row sums over LDS --------------------------------------------
@@ -1096,9 +1153,9 @@ static int64_t mm16_tables_bytes(int mode) {
     }
 }
 
-// whether NC activation rows of kp codes fit in LDS next to the tables
-static bool mm16_xl(int mode, int nc, int64_t kp) {
-    return mm16_tables_bytes(mode) + (int64_t)nc * kp * 2 <= k_lds_bytes - 1024;
+// whether `cols` activation rows of kp codes fit in LDS next to the tables
+static bool mm16_xl(int mode, int cols, int64_t kp) {
+    return mm16_tables_bytes(mode) + (int64_t)cols * kp * 2 <= k_lds_bytes - 1024;
 }
 
 // Columns per lane.  Every output is a K-long dependent chain, so a lane is
@@ -1116,39 +1173,96 @@ static int mm16_nc(int mode, int64_t M, int64_t N, int64_t nslices, int64_t kp, 
     return 8;
 }
 
-template <int MODE, int NC, bool XL>
+struct mm16_shape {
+    int nc, cg;   // columns per lane, column groups per workgroup
+    bool xl;      // activations converted into LDS inside the kernel
+};
+
+// The xlns32 tables leave room for one workgroup per CU, so the sum32 and
+// xlns32 GEMVs take their waves per SIMD from column groups.  Time per k of a
+// shape is rounds x (chains per SIMD) x (time per chain step at that many
+// waves per SIMD); measured on MI355X, a chain step costs 166 ns with one
+// wave and one chain (the adder's latency), 148 ns with one wave of several
+// chains, 103 ns at two waves and 85 ns at four (the VALU issue rate of 49
+// instructions).
+static mm16_shape mm_shape_x32(int64_t M, int64_t N, int64_t nslices, int64_t kp, int cus, int max_nc) {
+    // (one wave of several chains, or two waves of two or more, never wins)
+    static const int shapes[][2] = {{1, 1}, {1, 2}, {1, 4}, {2, 4}, {4, 4}, {8, 4}};
+    const int64_t wg_m = (M + k_block - 1) / k_block;
+    mm16_shape best{1, 1, mm16_xl(LNSHIP_SUM32, 1, kp)};
+    int64_t best_cost = -1;
+    for (const auto &sh : shapes) {
+        const int nc = sh[0], cg = sh[1];
+        if ((nc * cg > 1 && nc * cg > N) || nc > max_nc) continue;
+        const int64_t wgs = wg_m * ((N + nc * cg - 1) / (nc * cg)) * nslices;
+        const int64_t rounds = (wgs + std::max(cus, 1) - 1) / std::max(cus, 1);
+        const int64_t step = cg == 1 ? (nc == 1 ? 166 : 148) : cg == 2 ? 103 : 85;
+        const int64_t cost = rounds * cg * nc * step;
+        // ties go to more columns per workgroup (one weight decode serves them)
+        if (best_cost < 0 || cost <= best_cost) {
+            best = {nc, cg, mm16_xl(LNSHIP_SUM32, nc * cg, kp)};
+            best_cost = cost;
+        }
+    }
+    return best;
+}
+
+static mm16_shape mm16_choose(int mode, int64_t M, int64_t N, int64_t nslices, int64_t kp, int cus) {
+    if (mode == LNSHIP_SUM32) return mm_shape_x32(M, N, nslices, kp, cus, 8);
+    const int nc = mm16_nc(mode, M, N, nslices, kp, cus);
+    return {nc, 1, mm16_xl(mode, nc, kp)};
+}
+
+template <int MODE, int NC, bool XL, int CG>
 static int launch_mm16(const mm_args16 &m, const dev_tables &T, int64_t nslices, hipStream_t st) {
-    constexpr int PF = NC == 1 ? 8 : (NC <= 4 ? 2 : 1);
-    const int lds = mm_xl_offset<MODE>() + (XL ? (int)(NC * m.kp * 2) : 0);
+    // prefetch depth within 128 VGPRs at four waves per SIMD
+    constexpr int PF = NC == 1 ? (CG >= 4 ? 4 : 8) : NC == 2 ? 2 : (NC == 4 && CG < 4) ? 2 : 1;
+    const int lds = mm_xl_offset<MODE>() + (XL ? (int)(NC * CG * m.kp * 2) : 0);
     if (lds > 64 * 1024)
-        if (int rc = set_lds(k_mm16<MODE, NC, PF, XL>, lds)) return rc;
-    dim3 grid((unsigned)((m.M + k_block - 1) / k_block), (unsigned)((m.N + NC - 1) / NC), (unsigned)nslices);
+        if (int rc = set_lds(k_mm16<MODE, NC, PF, XL, CG>, lds)) return rc;
+    dim3 grid((unsigned)((m.M + k_block - 1) / k_block), (unsigned)((m.N + NC * CG - 1) / (NC * CG)), (unsigned)nslices);
     if (grid.x > 2147483647u || grid.y > 65535u) return fail(LNSHIP_ERANGE, "mul_mat: grid too large%s");
-    hipLaunchKernelGGL((k_mm16<MODE, NC, PF, XL>), grid, dim3(k_block), lds, st, m, T);
+    hipLaunchKernelGGL((k_mm16<MODE, NC, PF, XL, CG>), grid, dim3(k_block * CG), lds, st, m, T);
     LNSHIP_HIP(hipGetLastError());
     return 0;
 }
 
-template <int MODE, int NC>
+template <int MODE, int NC, int CG>
 static int launch_mm16_x(const mm_args16 &m, const dev_tables &T, int64_t nslices, bool xl, hipStream_t st) {
-    return xl ? launch_mm16<MODE, NC, true>(m, T, nslices, st) : launch_mm16<MODE, NC, false>(m, T, nslices, st);
+    return xl ? launch_mm16<MODE, NC, true, CG>(m, T, nslices, st) : launch_mm16<MODE, NC, false, CG>(m, T, nslices, st);
 }
 
 template <int MODE>
-static int dispatch_mm16(const mm_args16 &m, const dev_tables &T, int64_t nslices, int nc, bool xl, hipStream_t st) {
-    switch (nc) {
-        case 8: return launch_mm16_x<MODE, 8>(m, T, nslices, xl, st);
-        case 4: return launch_mm16_x<MODE, 4>(m, T, nslices, xl, st);
-        default: return launch_mm16_x<MODE, 1>(m, T, nslices, xl, st);
+static int dispatch_mm16(const mm_args16 &m, const dev_tables &T, int64_t nslices, const mm16_shape &sh,
+                         hipStream_t st) {
+    if constexpr (MODE == LNSHIP_SUM32) {
+        // column groups: more waves per SIMD where the tables allow one
+        // workgroup per CU
+        switch (sh.nc * 10 + sh.cg) {
+            case 12: return launch_mm16_x<MODE, 1, 2>(m, T, nslices, sh.xl, st);
+            case 14: return launch_mm16_x<MODE, 1, 4>(m, T, nslices, sh.xl, st);
+            case 24: return launch_mm16_x<MODE, 2, 4>(m, T, nslices, sh.xl, st);
+            case 44: return launch_mm16_x<MODE, 4, 4>(m, T, nslices, sh.xl, st);
+            case 84: return launch_mm16_x<MODE, 8, 4>(m, T, nslices, sh.xl, st);
+            default: return launch_mm16_x<MODE, 1, 1>(m, T, nslices, sh.xl, st);
+        }
+    } else {
+        switch (sh.nc) {
+            case 8: return launch_mm16_x<MODE, 8, 1>(m, T, nslices, sh.xl, st);
+            case 4: return launch_mm16_x<MODE, 4, 1>(m, T, nslices, sh.xl, st);
+            default: return launch_mm16_x<MODE, 1, 1>(m, T, nslices, sh.xl, st);
+        }
     }
 }
 
-template <int NC>
+template <int NC, int CG>
 static int launch_mm32(const mm_args32 &m, const dev_tables &T, int64_t nslices, hipStream_t st) {
-    if (int rc = set_lds(k_mm32<NC>, k_lds_tab32)) return rc;
-    dim3 grid((unsigned)((m.M + k_block - 1) / k_block), (unsigned)((m.N + NC - 1) / NC), (unsigned)nslices);
-    if (grid.y > 65535u) return fail(LNSHIP_ERANGE, "mul_mat: grid too large%s");
-    hipLaunchKernelGGL((k_mm32<NC>), grid, dim3(k_block), k_lds_tab32, st, m, T);
+    // prefetch depth within 128 VGPRs at four waves per SIMD
+    constexpr int PF = NC == 1 ? (CG >= 4 ? 2 : 4) : 1;
+    if (int rc = set_lds(k_mm32<NC, PF, CG>, k_lds_tab32)) return rc;
+    dim3 grid((unsigned)((m.M + k_block - 1) / k_block), (unsigned)((m.N + NC * CG - 1) / (NC * CG)), (unsigned)nslices);
+    if (grid.x > 2147483647u || grid.y > 65535u) return fail(LNSHIP_ERANGE, "mul_mat: grid too large%s");
+    hipLaunchKernelGGL((k_mm32<NC, PF, CG>), grid, dim3(k_block * CG), k_lds_tab32, st, m, T);
     LNSHIP_HIP(hipGetLastError());
     return 0;
 }
@@ -1339,10 +1453,9 @@ int lnship16_mul_mat(int mode, const lnship_mul_mat_args *a, void *stream) {
     hipStream_t st = (hipStream_t)stream;
     // activations converted inside the GEMV when NC rows fit in LDS next to
     // the tables, else by k_act into scratch first
-    const int nc = mm16_nc(mode, a->M, a->N, nslices, kp, s->cus);
-    const bool xl = mm16_xl(mode, nc, kp);
+    const mm16_shape sh = mm16_choose(mode, a->M, a->N, nslices, kp, s->cus);
     void *xs = nullptr;
-    if (!xl) {
+    if (!sh.xl) {
         if (int rc = scratch(s, (size_t)std::max<int64_t>(1, nslices * a->N * kp) * 2, &xs)) return rc;
         if (kp > 0) {
             dim3 g(grid_for(a->N * kp, 2), (unsigned)nslices);
@@ -1357,10 +1470,10 @@ int lnship16_mul_mat(int mode, const lnship_mul_mat_args *a, void *stream) {
                 wms, a->w_slice ? a->w_slice : kp * wms, dld, a->dst_slice ? a->dst_slice : a->N * dld,
                 a->monte_seed};
     switch (mode) {
-        case LNSHIP_BASE: return dispatch_mm16<LNSHIP_BASE>(m, s->T, nslices, nc, xl, st);
-        case LNSHIP_MONTE: return dispatch_mm16<LNSHIP_MONTE>(m, s->T, nslices, nc, xl, st);
-        case LNSHIP_LPVIP: return dispatch_mm16<LNSHIP_LPVIP>(m, s->T, nslices, nc, xl, st);
-        default: return dispatch_mm16<LNSHIP_SUM32>(m, s->T, nslices, nc, xl, st);
+        case LNSHIP_BASE: return dispatch_mm16<LNSHIP_BASE>(m, s->T, nslices, sh, st);
+        case LNSHIP_MONTE: return dispatch_mm16<LNSHIP_MONTE>(m, s->T, nslices, sh, st);
+        case LNSHIP_LPVIP: return dispatch_mm16<LNSHIP_LPVIP>(m, s->T, nslices, sh, st);
+        default: return dispatch_mm16<LNSHIP_SUM32>(m, s->T, nslices, sh, st);
     }
 }
 
@@ -1387,11 +1500,14 @@ int lnship32_mul_mat(const lnship_mul_mat_args *a, void *stream) {
     mm_args32 m{(const uint32_t *)a->w, (const uint32_t *)xs, a->dst, a->K, kp, a->M, a->N,
                 a->ne02, a->ne12, a->ne12 / a->ne02, a->ne13 / a->ne03,
                 wms, a->w_slice ? a->w_slice : kp * wms, dld, a->dst_slice ? a->dst_slice : a->N * dld};
-    // one column per lane while every workgroup fits on the GPU at once
-    // (the tables allow one workgroup per CU), else four
-    const int64_t wg_m = (m.M + k_block - 1) / k_block;
-    if (m.N >= 4 && wg_m * m.N * nslices > std::max(s->cus, 1)) return launch_mm32<4>(m, s->T, nslices, st);
-    return launch_mm32<1>(m, s->T, nslices, st);
+    const mm16_shape sh = mm_shape_x32(m.M, m.N, nslices, kp, s->cus, 4);
+    switch (sh.nc * 10 + sh.cg) {
+        case 12: return launch_mm32<1, 2>(m, s->T, nslices, st);
+        case 14: return launch_mm32<1, 4>(m, s->T, nslices, st);
+        case 24: return launch_mm32<2, 4>(m, s->T, nslices, st);
+        case 44: return launch_mm32<4, 4>(m, s->T, nslices, st);
+        default: return launch_mm32<1, 1>(m, s->T, nslices, st);
+    }
 }
 
 
