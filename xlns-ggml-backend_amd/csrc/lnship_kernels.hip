@@ -26,7 +26,8 @@ constexpr int k_block = 256;
 constexpr int k_max_devices = 64;
 // LDS budget of a workgroup on gfx950 (160 KiB per CU)
 constexpr int k_lds_bytes = 160 * 1024;
-constexpr int k_lds_tab32 = k32_tab_n * 4;   // 108304 bytes
+// the xlns32 tables plus four zero entries (an interpolation on them gives 0)
+constexpr int k_lds_tab32 = (k32_tab_n + 4) * 4;   // 108320 bytes
 
 static thread_local std::string t_err;
 
@@ -294,13 +295,17 @@ constexpr uint32_t kb_dbf = (uint32_t)(k32_off_dbf - (int)(k32_db_end >> k32_db_
 // grid origin), computed once per kernel; the empty asm keeps them opaque
 // registers, so that picking a table is one select and no base add follows.
 struct x32_tab {
-    uint32_t dlo, dhi, sb, sbf, db, dbf;
+    uint32_t dlo, dhi, sb, sbf, db, dbf, zero;
 };
 __device__ __forceinline__ x32_tab x32_origins(const int32_t *T) {
     uint32_t tb = lds_addr(T);
     asm("" : "+v"(tb));
-    return {tb + (uint32_t)k32_off_dlo * 4, tb + (uint32_t)k32_off_dhi * 4, tb + kb_sb, tb + kb_sbf, tb + kb_db,
-            tb + kb_dbf};
+    x32_tab o{tb + (uint32_t)k32_off_dlo * 4, tb + (uint32_t)k32_off_dhi * 4, tb + kb_sb, tb + kb_sbf, tb + kb_db,
+              tb + kb_dbf, tb + (uint32_t)k32_tab_n * 4};
+    // each origin its own register: a select among them stays a select (not
+    // a lookup table of their constant offsets)
+    asm("" : "+v"(o.sb), "+v"(o.sbf), "+v"(o.db), "+v"(o.dbf), "+v"(o.zero));
+    return o;
 }
 
 __device__ __forceinline__ void x32_add_ls(const x32_tab &O, acc_ls &a, uint32_t tl, uint32_t ts) {
@@ -348,6 +353,59 @@ __device__ __forceinline__ void x32_add_ls(const x32_tab &O, acc_ls &a, uint32_t
     a.s = (d == 0 && usedb) ? 0u : ns;
 }
 
+// A select on values: a conditional on two struct fields is an lvalue, a
+// select of their addresses, and nested ones force the struct into scratch.
+__device__ __forceinline__ uint32_t sel(bool c, uint32_t a, uint32_t b) { return c ? a : b; }
+
+// The same addition ordered for one chain per lane, where every instruction
+// of the wave is on the chain's clock (a single wave issues about one
+// instruction per 2 ns, and an LDS round trip hides about ten).  The
+// direct interpolation node (at d) is complete before the first lookups
+// return; lanes that take no interpolation point it at the zero pair after
+// the tables, so no select follows the second lookup.  The cotransformation
+// point e always lies on the sb tables (clamped at esszer, whose far node is
+// 0).  What the tail needs but the second lookup's address does not, and the
+// caller's `shadow` work (the next product), fill the second round trip.
+// Scheduling barriers keep the groups in this order.
+template <class F>
+__device__ __forceinline__ void x32_add_lat(const x32_tab &O, acc_ls &a, uint32_t tl, uint32_t ts, F &&shadow) {
+    const uint32_t d = absdiff(a.l, tl);
+    const uint32_t dl = d & ((1u << k32_co_sh) - 1u), dh = (d >> k32_co_sh) & ((1u << k32_co_sh) - 1u);
+    const int32_t lo = lds_ld(lshl2_add(dl, O.dlo));    // dlo[dl]
+    const int32_t th2 = lds_ld(lshl2_add(dh, O.dhi));   // (dh << 12) + dhi[dh]
+    __builtin_amdgcn_sched_barrier(0);
+    const bool usedb = a.s != ts;
+    const bool co = usedb && d < k32_co_end;
+    const bool direct_db = usedb && !(d < k32_co_end);
+    const bool at_e = co && dh != 0 && dl != 0;
+    const bool keep_d = !co && d < k32_esszer;
+    const bool hi_d = d >= (direct_db ? k32_db_end : k32_sb_end);
+    const int sh_d = hi_d ? k32_sb_fsh : k32_sb_sh;   // sb and db share both grids
+    const uint32_t base_d = sel(hi_d, sel(direct_db, O.dbf, O.sbf), sel(direct_db, O.db, O.sb));
+    const uint32_t nd = lshl2_add(d >> sh_d, base_d);   // (an asm call in a ternary arm would become a branch)
+    const uint32_t node_d = sel(keep_d, nd, O.zero);
+    __builtin_amdgcn_sched_barrier(0);
+    const uint32_t e = (uint32_t)th2 - (uint32_t)lo;   // wraps for the dl = 0 sentinel (unused then)
+    const uint32_t xe = min(e, k32_esszer);
+    const bool hi_e = e >= k32_sb_end;
+    const int sh_e = hi_e ? k32_sb_fsh : k32_sb_sh;
+    const uint32_t ne = lshl2_add(xe >> sh_e, sel(hi_e, O.sbf, O.sb));
+    const uint32_t node = sel(at_e, ne, node_d);
+    const int32_t t0 = lds_ld(node), t1 = lds_ld(node + 4);
+    __builtin_amdgcn_sched_barrier(0);
+    const uint32_t mx = max(a.l, tl);
+    const int32_t th = th2 - (int32_t)(dh << k32_co_sh);
+    const int32_t mA = (int32_t)mx + (co ? (dh == 0 ? lo : th) : 0);
+    const int sh = at_e ? sh_e : sh_d;
+    const int32_t frac = (int32_t)((at_e ? xe : d) & ((1u << sh) - 1u));
+    const uint32_t nsign = (d == 0 && usedb) ? 0u : (a.l > tl ? a.s : ts);
+    shadow();
+    __builtin_amdgcn_sched_barrier(0);
+    const int32_t ip = t0 + (mul_i24(t1 - t0, frac) >> sh);
+    a.l = (uint32_t)max(__builtin_elementwise_add_sat(mA, ip), 0);
+    a.s = nsign;
+}
+
 // A whole xlns32 addition on packed values (sign bit 31) over the LDS tables.
 __device__ __forceinline__ uint32_t x32_add_lds(const x32_tab &O, uint32_t x, uint32_t y) {
     acc_ls a{x & k32_logmask, x & k32_sign};
@@ -364,6 +422,11 @@ struct red16<LNSHIP_SUM32> {
     }
     __device__ __forceinline__ void add_ls(acc_t &a, uint32_t tl, uint32_t ts, uint32_t &) const {
         x32_add_ls(O, a, tl << 16, ts << 16);
+    }
+    // operands already widened (log and sign moved to the xlns32 positions)
+    template <class F>
+    __device__ __forceinline__ void add_lat(acc_t &a, uint32_t tl32, uint32_t ts32, F &&shadow) const {
+        x32_add_lat(O, a, tl32, ts32, shadow);
     }
     __device__ __forceinline__ void add(acc_t &a, uint32_t v, uint32_t &st) const { add_ls(a, v & k16_logmask, v & k16_sign, st); }
     __device__ __forceinline__ uint32_t finish(const acc_t &a) const {
@@ -453,6 +516,7 @@ __device__ __forceinline__ red16<LNSHIP_SUM32> stage_tables<LNSHIP_SUM32>(const 
     for (int i = (k32_tab_n / 4) * 4 + threadIdx.x; i < k32_tab_n; i += blockDim.x) t[i] = T.tab32[i];
     __syncthreads();
     if (threadIdx.x == 0) t[k32_off_dlo] = -0x7fffffff;   // db at d = 0: exact cancellation
+    if (threadIdx.x < 4) t[k32_tab_n + threadIdx.x] = 0;   // the zero pair
     // dhi[dh] -> (dh << 12) + dhi[dh], the first half of the cotransformation's e
     for (int i = 1 + threadIdx.x; i < k32_co_n; i += blockDim.x) t[k32_off_dhi + i] += i << k32_co_sh;
     return red16<LNSHIP_SUM32>{x32_origins(t)};
@@ -565,6 +629,39 @@ __global__ __launch_bounds__(k_block * CG) void k_mm16(mm_args16 a, dev_tables T
     // and clamped, signs xor'ed), then one reduction step per column
     auto steps = [&](const uint4 &wq, const uint4 (&xq)[NC], int u0, int u1) {
         const uint32_t ww[4] = {wq.x, wq.y, wq.z, wq.w};
+        if constexpr (MODE == LNSHIP_SUM32 && NC == 1) {
+            // one chain per lane: the product of step u + 1, already in the
+            // accumulator's xlns32 positions, is formed in step u's shadow
+            const uint32_t xx[4] = {xq[0].x, xq[0].y, xq[0].z, xq[0].w};
+            auto prod = [&](int u, uint32_t &tl, uint32_t &ts) {
+                const uint32_t wv = half16(ww[u >> 1], u & 1), xv = half16(xx[u >> 1], u & 1);
+                const int32_t l = (int32_t)(wv & k16_logmask) + (int32_t)(xv & k16_logmask) - (int32_t)k16_one;
+                tl = (uint32_t)min(max(l, 0), (int32_t)k16_logmask) << 16;
+                ts = ((wv ^ xv) & k16_sign) << 16;
+            };
+            const bool first = u0 < 0;
+            const int ub = first ? 0 : u0;
+            uint32_t tl = 0, ts = 0;
+            if (ub < u1) prod(ub, tl, ts);
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                if (u >= ub && u < u1) {
+                    uint32_t ntl = 0, nts = 0;
+                    auto next = [&] {
+                        if (u + 1 < u1) prod(u + 1, ntl, nts);
+                    };
+                    if (first && u == 0) {
+                        acc[0] = {tl, ts};
+                        next();
+                    } else {
+                        R.add_lat(acc[0], tl, ts, next);
+                    }
+                    tl = ntl;
+                    ts = nts;
+                }
+            }
+            return;
+        }
 #pragma unroll
         for (int u = 0; u < 8; u++) {
             if (u >= u0 && u < u1) {
@@ -679,6 +776,32 @@ __global__ __launch_bounds__(k_block * CG) void k_mm32(mm_args32 a, dev_tables T
     acc_ls acc[NC];
     auto steps = [&](const grp &wq, const grp (&xq)[NC], int u0, int u1) {
         const uint32_t wv[8] = {wq.lo.x, wq.lo.y, wq.lo.z, wq.lo.w, wq.hi.x, wq.hi.y, wq.hi.z, wq.hi.w};
+        if constexpr (NC == 1) {
+            // one chain per lane: the product of step u + 1 is formed in step
+            // u's shadow
+            const uint32_t xv[8] = {xq[0].lo.x, xq[0].lo.y, xq[0].lo.z, xq[0].lo.w,
+                                    xq[0].hi.x, xq[0].hi.y, xq[0].hi.z, xq[0].hi.w};
+            const bool first = u0 < 0;
+            const int ub = first ? 0 : u0;
+            uint32_t t = ub < u1 ? x32_mul(wv[ub], xv[ub]) : 0u;
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                if (u >= ub && u < u1) {
+                    uint32_t tn = 0;
+                    auto next = [&] {
+                        if (u + 1 < u1) tn = x32_mul(wv[u + 1], xv[u + 1]);
+                    };
+                    if (first && u == 0) {
+                        acc[0] = {t & k32_logmask, t & k32_sign};
+                        next();
+                    } else {
+                        x32_add_lat(R.O, acc[0], t & k32_logmask, t & k32_sign, next);
+                    }
+                    t = tn;
+                }
+            }
+            return;
+        }
 #pragma unroll
         for (int u = 0; u < 8; u++) {
             if (u >= u0 && u < u1) {
