@@ -149,6 +149,27 @@ int lnship16_store_kv(const float *x, int64_t x_ld, const int32_t *pos, int64_t 
                       int rope_n_dims, const float *cos_sin, uint16_t *cache, int64_t cache_m,
                       int64_t cache_slice, int cache_transposed, const int32_t *seq, int64_t seq_stride,
                       void *stream);
+/* ---- the same elementwise ops in xlns32 (the LNS32 backend) ---------------
+ * lns32_add / lns32_mul (src32/lns32-ops.cpp:224-282): fp2xlns32 of both
+ * operands (b repeated every nb elements), xlns32_add / xlns32_mul,
+ * xlns322fp.  lns32_swiglu (:535-587): xlns32_mul(xlns32_silu(gate), up),
+ * xlns32_silu(x) = x times fp2xlns32 of the sigmoid of x's value (formed in
+ * double, rounded to float).  lns32_rope (:795-880): pairs rotated with
+ * xlns32 mul / add / sub of fp2xlns32(cos), fp2xlns32(sin) from cos_sin
+ * (lnship_rope_table), dims past n_dims round-tripped through xlns32.
+ * lnship32_store_kv: as lnship16_store_kv with 4-byte xlns32 codes (the F16
+ * KV cache rows that lns32_mul_mat converts, :64-79). */
+int lnship32_add(const float *a, const float *b, int64_t n, int64_t nb, float *dst, void *stream);
+int lnship32_mul(const float *a, const float *b, int64_t n, int64_t nb, float *dst, void *stream);
+int lnship32_swiglu(const float *gate, int64_t gate_ld, const float *up, int64_t up_ld, float *dst,
+                    int64_t ncols, int64_t nrows, void *stream);
+int lnship32_rope(const float *x, int64_t x_ld, const int32_t *pos, int64_t ntok, int64_t nhead, int64_t ne0,
+                  int n_dims, int neox, const float *cos_sin, float *dst, void *stream);
+int lnship32_store_kv(const float *x, int64_t x_ld, const int32_t *pos, int64_t ntok, int64_t nhead, int64_t ne0,
+                      int rope_n_dims, const float *cos_sin, uint32_t *cache, int64_t cache_m,
+                      int64_t cache_slice, int cache_transposed, const int32_t *seq, int64_t seq_stride,
+                      void *stream);
+
 /* Host: the (cos, sin) floats lns_rope uses for positions 0..n_pos-1 (the
  * float recurrence t *= powf(freq_base, -2/n_dims) per pair, cosf / sinf;
  * src/lns-ops.cpp:1225-1247, cuda/lns-cuda-ops.cpp:223-240), laid out as

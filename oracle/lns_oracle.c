@@ -770,6 +770,52 @@ void lno16_rope_f32(const float *x, const int32_t *pos, int64_t ntok, int64_t nh
     }
 }
 
+/* lns32_add / lns32_mul (src32/lns32-ops.cpp:224-282), b repeated every nb */
+void lno32_add_f32(const float *a, const float *b, int64_t n, int64_t nb, float *dst) {
+    for (int64_t i = 0; i < n; i++) dst[i] = lno32_to_f32(lno32_add(lno32_from_f32(a[i]), lno32_from_f32(b[i % nb])));
+}
+void lno32_mul_f32(const float *a, const float *b, int64_t n, int64_t nb, float *dst) {
+    for (int64_t i = 0; i < n; i++) dst[i] = lno32_to_f32(lno32_mul(lno32_from_f32(a[i]), lno32_from_f32(b[i % nb])));
+}
+
+/* xlns32_silu (xlnscpp, absent): x times fp2xlns32 of the sigmoid of x's
+ * value, the sigmoid formed in double and rounded to float.  Checked against
+ * the eight swiglu values printed in unit-tests-lns32.txt (six decimals);
+ * beyond those digits parity is unpinned. */
+uint32_t lno32_silu(uint32_t x) {
+    const double v = (double)lno32_to_f32(x);
+    return lno32_mul(x, lno32_from_f32((float)(1.0 / (1.0 + exp(-v)))));
+}
+
+/* lns32_swiglu (src32/lns32-ops.cpp:535-587): silu(gate) * up */
+void lno32_swiglu_f32(const float *gate, const float *up, int64_t n, float *dst) {
+    for (int64_t i = 0; i < n; i++)
+        dst[i] = lno32_to_f32(lno32_mul(lno32_silu(lno32_from_f32(gate[i])), lno32_from_f32(up[i])));
+}
+
+/* lns32_rope (src32/lns32-ops.cpp:795-880), normal or NEOX pairs; x is
+ * [ntok][nhead][ne0], pos[ntok]; cos/sin from the same float recurrence as
+ * the xlns16 rope; dims past n_dims round-trip through xlns32 */
+void lno32_rope_f32(const float *x, const int32_t *pos, int64_t ntok, int64_t nhead, int64_t ne0,
+                    int n_dims, int neox, float freq_base, float *dst) {
+    const float theta_scale = powf(freq_base, -2.0f / (float)n_dims);
+    for (int64_t t = 0; t < ntok; t++)
+    for (int64_t h = 0; h < nhead; h++) {
+        const float *xr = x + (t * nhead + h) * ne0;
+        float *yr = dst + (t * nhead + h) * ne0;
+        float th = (float)pos[t];
+        for (int64_t j = 0; j < n_dims; j += 2) {
+            const uint32_t c = lno32_from_f32(cosf(th)), sn = lno32_from_f32(sinf(th));
+            const int64_t i0 = neox ? j / 2 : j, i1 = neox ? j / 2 + n_dims / 2 : j + 1;
+            const uint32_t x0 = lno32_from_f32(xr[i0]), x1 = lno32_from_f32(xr[i1]);
+            yr[i0] = lno32_to_f32(lno32_sub(lno32_mul(x0, c), lno32_mul(x1, sn)));
+            yr[i1] = lno32_to_f32(lno32_add(lno32_mul(x0, sn), lno32_mul(x1, c)));
+            th *= theta_scale;
+        }
+        for (int64_t j = n_dims; j < ne0; j++) yr[j] = lno32_to_f32(lno32_from_f32(xr[j]));
+    }
+}
+
 /* ======================================================================
  * Table construction.
  * ==================================================================== */

@@ -131,6 +131,12 @@ void lno32_mul_mat_lnsw(const uint32_t *w, const float *x, float *dst,
 void lno32_soft_max(const float *src, const int64_t ne[4], const float *mask,
                     const int64_t mne[4], float scale, float *dst);
 void lno32_rms_norm(const float *src, int64_t ncols, int64_t nrows, float eps, float *dst);
+uint32_t lno32_silu(uint32_t x);
+void lno32_add_f32(const float *a, const float *b, int64_t n, int64_t nb, float *dst);
+void lno32_mul_f32(const float *a, const float *b, int64_t n, int64_t nb, float *dst);
+void lno32_swiglu_f32(const float *gate, const float *up, int64_t n, float *dst);
+void lno32_rope_f32(const float *x, const int32_t *pos, int64_t ntok, int64_t nhead, int64_t ne0,
+                    int n_dims, int neox, float freq_base, float *dst);
 
 #ifdef __cplusplus
 }

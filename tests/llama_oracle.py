@@ -1,4 +1,5 @@
-"""CPU oracle of the Llama-architecture decoder in LNS16 (test infrastructure).
+"""CPU oracles of the Llama-architecture decoder in LNS16 and LNS32 (test
+infrastructure).
 
 The same graph as lnship.llama (llama.cpp's llama graph as the reference's
 LNS16 backend computes it), built from the oracle's op drivers: mul_mat
@@ -146,3 +147,71 @@ class LlamaOracle16:
         h = _binop(self.L.lno16_mul_f32, h, self.out_norm)
         logits = O.mul_mat16(m, self.tok_embd, h)
         return logits if batch else logits[0]
+
+
+class LlamaOracle32:
+    """The same graph as the reference's LNS32 backend computes it
+    (src32/lns32-ops.cpp): get_rows copies the F32 embedding rows (:707-745),
+    every other op converts its F32 operands with fp2xlns32 (weights once:
+    the conversion of an F32 weight does not depend on the call), the KV
+    cache holds IEEE half values (kq / kqv convert them, :64-79), one
+    sequence."""
+
+    def __init__(self, cfg, weights):
+        self.cfg = cfg
+        c = cfg
+        self.tok_embd_f32 = np.ascontiguousarray(weights["tok_embd"], np.float32)
+        self.tok_embd = O.f2x32(self.tok_embd_f32)                     # [vocab, e] codes
+        self.out_norm = weights["out_norm"]
+        self.layers = []
+        for W in weights["layers"]:
+            self.layers.append({
+                "attn_norm": W["attn_norm"], "ffn_norm": W["ffn_norm"],
+                "wqkv": O.f2x32(np.concatenate([W["wq"], W["wk"], W["wv"]])),
+                "wo": O.f2x32(W["wo"]),
+                "wug": O.f2x32(np.concatenate([W["w_up"], W["w_gate"]])),
+                "wdown": O.f2x32(W["w_down"]),
+            })
+        self.kcache = [np.zeros((c.n_ctx, c.n_head_kv, c.head_dim), np.float16) for _ in range(c.n_layer)]
+        self.vcache = [np.zeros((c.n_ctx, c.n_head_kv, c.head_dim), np.float16) for _ in range(c.n_layer)]
+        self.n_past = 0
+
+    def eval(self, tokens, n_layers=None):
+        """Appends tokens; returns the logits of the last one.  n_layers runs
+        only the first layers (a bounded sample for timing)."""
+        c = self.cfg
+        T = len(tokens)
+        p0 = self.n_past
+        pos = np.arange(p0, p0 + T, dtype=np.int32)
+        n_kv = n_kv_for(p0 + T, c.n_ctx)
+        e, hd, nh, nkv, f = c.n_embd, c.head_dim, c.n_head, c.n_head_kv, c.n_ff
+        nq = nh * hd
+        mask = np.where(np.arange(n_kv)[None, :] <= pos[:, None], 0.0, -np.inf).astype(np.float32)
+        x = self.tok_embd_f32[np.asarray(tokens)]
+        layers = self.layers if n_layers is None else self.layers[:n_layers]
+        for il, W in enumerate(layers):
+            last = il == c.n_layer - 1
+            h = O.mul32(O.rms_norm32(x, c.eps), W["attn_norm"])
+            qkv = O.mul_mat32_codes(W["wqkv"], h)
+            q = O.rope32(qkv[:, :nq].reshape(T, nh, hd), pos, hd, 0, c.rope_theta)
+            k = O.rope32(qkv[:, nq:nq + nkv * hd].reshape(T, nkv, hd), pos, hd, 0, c.rope_theta)
+            v = qkv[:, nq + nkv * hd:].reshape(T, nkv, hd)
+            self.kcache[il][pos] = k.astype(np.float16)
+            self.vcache[il][pos] = v.astype(np.float16)
+            kw = self.kcache[il][:n_kv].astype(np.float32).transpose(1, 0, 2)       # [nkv, n_kv, hd]
+            kq = O.mul_mat32(kw[None], q.transpose(1, 0, 2)[None], ne02=nkv)       # [1, nh, T, n_kv]
+            kq = O.soft_max32(kq[0], mask, 1.0 / math.sqrt(hd))
+            vw = self.vcache[il][:n_kv].astype(np.float32).transpose(1, 2, 0)       # [nkv, hd, n_kv]
+            att = O.mul_mat32(vw[None], kq[None], ne02=nkv)[0]                      # [nh, T, hd]
+            att = np.ascontiguousarray(att.transpose(1, 0, 2).reshape(T, nq))
+            o = O.mul_mat32_codes(W["wo"], att)
+            if last:
+                o, x = o[-1:], x[-1:]
+            x = O.add32(o, x)
+            h = O.mul32(O.rms_norm32(x, c.eps), W["ffn_norm"])
+            ug = O.mul_mat32_codes(W["wug"], h)
+            sw = O.swiglu32(ug[:, f:], ug[:, :f])
+            x = O.add32(O.mul_mat32_codes(W["wdown"], sw), x)
+        self.n_past += T
+        h = O.mul32(O.rms_norm32(x[-1:], c.eps), self.out_norm)
+        return O.mul_mat32_codes(self.tok_embd, h)[0]

@@ -94,6 +94,11 @@ def lib():
         "lno32_mul_mat_lnsw": (None, [P, P, P, i64, i64, i64, i64, i64, i64, i64]),
         "lno32_soft_max": (None, [P, P, P, P, f32, P]),
         "lno32_rms_norm": (None, [P, i64, i64, f32, P]),
+        "lno32_silu": (u32, [u32]),
+        "lno32_add_f32": (None, [P, P, i64, i64, P]),
+        "lno32_mul_f32": (None, [P, P, i64, i64, P]),
+        "lno32_swiglu_f32": (None, [P, P, i64, P]),
+        "lno32_rope_f32": (None, [P, P, i64, i64, i64, ctypes.c_int, ctypes.c_int, f32, P]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -231,6 +236,56 @@ def mul_mat32(w, x, ne02=1, ne03=1):
     ne13 = x.shape[-4] if x.ndim >= 4 else 1
     out = np.zeros(x.shape[:-1] + (M,), dtype=np.float32)
     lib().lno32_mul_mat(_ptr(w), _ptr(x), _ptr(out), K, M, N, ne02, ne03, ne12, ne13)
+    return out
+
+
+def mul_mat32_codes(w_codes, x, ne02=1, ne03=1):
+    """mul_mat32 with the weights already converted to xlns32 codes."""
+    w = np.ascontiguousarray(w_codes, dtype=np.uint32)
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    K = w.shape[-1]
+    M = w.shape[-2]
+    N = x.shape[-2]
+    ne12 = x.shape[-3] if x.ndim >= 3 else 1
+    ne13 = x.shape[-4] if x.ndim >= 4 else 1
+    out = np.zeros(x.shape[:-1] + (M,), dtype=np.float32)
+    lib().lno32_mul_mat_lnsw(_ptr(w), _ptr(x), _ptr(out), K, M, N, ne02, ne03, ne12, ne13)
+    return out
+
+
+def _binop32(fn, a, b):
+    a = np.ascontiguousarray(a, np.float32)
+    b = np.ascontiguousarray(b, np.float32)
+    out = np.empty_like(a)
+    fn(_ptr(a), _ptr(b), a.size, b.size, _ptr(out))
+    return out
+
+
+def add32(a, b):
+    """lns32_add of F32 tensors, b repeated over a's rows."""
+    return _binop32(lib().lno32_add_f32, a, b)
+
+
+def mul32(a, b):
+    """lns32_mul of F32 tensors, b repeated over a's rows."""
+    return _binop32(lib().lno32_mul_f32, a, b)
+
+
+def swiglu32(gate, up):
+    gate = np.ascontiguousarray(gate, np.float32)
+    up = np.ascontiguousarray(up, np.float32)
+    out = np.empty_like(up)
+    lib().lno32_swiglu_f32(_ptr(gate), _ptr(up), up.size, _ptr(out))
+    return out
+
+
+def rope32(x, pos, n_dims, neox, freq_base):
+    """x [ntok][nhead][ne0] F32, pos [ntok] int32."""
+    x = np.ascontiguousarray(x, np.float32)
+    pos = np.ascontiguousarray(pos, np.int32)
+    out = np.empty_like(x)
+    lib().lno32_rope_f32(_ptr(x), _ptr(pos), x.shape[0], x.shape[1], x.shape[2], n_dims, neox, freq_base,
+                         _ptr(out))
     return out
 
 

@@ -6,7 +6,7 @@ import numpy as np
 import pytest
 
 import oracle_lib as O
-from llama_oracle import LlamaOracle16
+from llama_oracle import LlamaOracle16, LlamaOracle32
 
 torch = pytest.importorskip("torch")
 pytestmark = pytest.mark.gpu
@@ -92,3 +92,26 @@ def test_batched_sequences(mode):
             toks = [(t * 5 + 1 + i) % cfg.n_vocab for i, t in enumerate(toks)]
     assert gpu.past == cpu.past
     assert O.monte_get() == gpu.lfsr or m != O.MONTE
+
+
+def test_lns32_prefill_and_decode():
+    """BASELINE config 4 in small: the LNS32 decoder (F32 embedding rows,
+    xlns32 ops, 4-byte weights, xlns32 KV cache of half-rounded values)."""
+    from lnship import llama
+    cfg = tiny()
+    w = llama.synthetic_weights(cfg, seed=77, std=0.2)
+    rng = np.random.default_rng(8)
+    prompt = [int(t) for t in rng.integers(0, cfg.n_vocab, 9)]
+    print("\n[llama32] prefill 9", flush=True)
+    gpu = llama.LlamaLNS32(cfg, w)
+    cpu = LlamaOracle32(cfg, w)
+    same(gpu.eval(prompt).cpu().numpy(), cpu.eval(prompt), "lns32 prefill")
+    tok = int(rng.integers(0, cfg.n_vocab))
+    for step in range(3):
+        print(f"[llama32] decode {step}", flush=True)
+        same(gpu.eval([tok]).cpu().numpy(), cpu.eval([tok]), f"lns32 decode {step}")
+        tok = (tok * 7 + 3) % cfg.n_vocab
+    for step in range(2):
+        print(f"[llama32] graph decode {step}", flush=True)
+        same(gpu.decode_graph(tok).cpu().numpy(), cpu.eval([tok]), f"lns32 graph decode {step}")
+        tok = (tok * 5 + 1) % cfg.n_vocab

@@ -257,3 +257,40 @@ def test_soft_max_lns32(ln):
     mask = _causal(16, 128)
     same_bits(host(ln.soft_max32(dev(x), dev(mask), 0.125)), O.soft_max32(x, mask, 0.125), "soft_max lns32")
     same_bits(host(ln.soft_max32(dev(x), None, 1.0)), O.soft_max32(x, None, 1.0), "soft_max lns32 unmasked")
+
+
+# ------------------------------------------------- LNS32 elementwise ops --
+
+def test_elementwise_lns32(ln):
+    import ctypes
+    L = ln.lib()
+    st = ln._stream()
+    P = lambda t: ctypes.c_void_p(t.data_ptr())
+    rng = np.random.default_rng(41)
+    a = (rng.standard_normal((37, 24)) * 3).astype(np.float32)
+    b = rng.standard_normal(24).astype(np.float32)
+    a[0, :4] = [0.0, -0.0, 1e-30, -7.5]
+    b[:4] = [0.0, 2.0, -1e-30, 7.5]                   # zeros, tiny, exact cancellation
+    da, db = dev(a), dev(b)
+    for name, fn in (("add", O.add32), ("mul", O.mul32)):
+        print(f"\n[lns32 {name}]", flush=True)
+        out = torch.empty_like(da)
+        ln.check(getattr(L, "lnship32_" + name)(P(da), P(db), a.size, b.size, P(out), st))
+        same_bits(host(out), fn(a, b), f"lns32 {name}")
+    print("[lns32 swiglu]", flush=True)
+    g = (rng.standard_normal((5, 2 * 40)) * 4).astype(np.float32)
+    g[0, :3] = [0.0, 90.0, -90.0]
+    dg = dev(g)
+    out = torch.empty((5, 40), dtype=torch.float32, device="cuda")
+    ln.check(L.lnship32_swiglu(ctypes.c_void_p(dg.data_ptr() + 40 * 4), 80, P(dg), 80, P(out), 40, 5, st))
+    same_bits(host(out), O.swiglu32(g[:, 40:], g[:, :40]), "lns32 swiglu")
+    for neox, n_dims in ((0, 16), (1, 16), (0, 10)):
+        print(f"[lns32 rope] neox={neox} n_dims={n_dims}", flush=True)
+        x = rng.standard_normal((3, 4, 16)).astype(np.float32)
+        pos = np.array([0, 7, 300], np.int32)
+        cs = np.empty(512 * n_dims, np.float32)
+        ln.check(L.lnship_rope_table(10000.0, n_dims, 512, ctypes.c_void_p(cs.ctypes.data)))
+        dx, dpos, dcs = dev(x), dev(pos), dev(cs)
+        out = torch.empty_like(dx)
+        ln.check(L.lnship32_rope(P(dx), 64, P(dpos), 3, 4, 16, n_dims, neox, P(dcs), P(out), st))
+        same_bits(host(out), O.rope32(x, pos, n_dims, neox, 10000.0), f"lns32 rope neox={neox} n_dims={n_dims}")

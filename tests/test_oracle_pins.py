@@ -381,6 +381,37 @@ def test_unit_lns32():
     assert abs(float(got["nrmse"]) - float(f["mul_mat_long"]["nrmse"])) < 0.001
 
 
+def test_swiglu_lns32_printed():
+    # xlns32_silu is in the absent xlnscpp library: the oracle's definition
+    # (sigmoid in double, fp2xlns32) reproduces the eight values the
+    # reference printed for lns32_swiglu, to their six decimals
+    gate = np.array([-3.0, -1.0, 0.0, 2.0, 1.5, -0.5, 4.0, -2.0], np.float32)
+    up = np.array([0.5, -2.0, 3.0, 1.0, -1.0, 4.0, 0.25, 2.0], np.float32)
+    got = ["%.6f" % v for v in O.swiglu32(gate, up)]
+    assert got == FIG["unit_tests"]["lns32"]["swiglu"]
+    # and they differ from the float swiglu in the last printed digits only
+    want = gate / (1 + np.exp(-gate.astype(np.float64))) * up
+    assert np.abs(O.swiglu32(gate, up) - want).max() < 2e-6
+
+
+def test_lns32_elementwise_closed_forms():
+    # add / mul of values exactly representable in xlns32 (powers of two)
+    a = np.array([1.0, 2.0, -4.0, 0.5, 8.0], np.float32)
+    b = np.array([1.0, 2.0, 4.0, 0.5, -8.0], np.float32)
+    assert np.array_equal(O.mul32(a, b), a * b)
+    assert np.array_equal(O.add32(a, b)[[0, 1, 3]], (a + b)[[0, 1, 3]])
+    assert O.add32(a, b)[2] == 0.0 and O.add32(a, b)[4] == 0.0   # exact cancellation
+    # rope at position 0 is the identity up to the xlns32 round trip
+    x = np.random.default_rng(3).standard_normal((2, 3, 8)).astype(np.float32)
+    y = O.rope32(x, np.zeros(2, np.int32), 8, 0, 10000.0)
+    assert np.array_equal(y, O.x2f32(O.f2x32(x)))
+    # rope is a rotation: norms of pairs kept to xlns32 precision
+    y = O.rope32(x, np.array([5, 9], np.int32), 8, 0, 10000.0)
+    n0 = np.hypot(x[..., 0::2], x[..., 1::2])
+    n1 = np.hypot(y[..., 0::2], y[..., 1::2])
+    assert np.abs(n1 - n0).max() < 1e-5
+
+
 # ------------------------------------------------------------- Monte LFSR --
 
 def test_lfsr_contract(L):

@@ -15,6 +15,7 @@
 #include <cstring>
 #include <mutex>
 #include <string>
+#include <type_traits>
 
 #include "lnship.h"
 #include "lnship_device.h"
@@ -1108,23 +1109,58 @@ __global__ __launch_bounds__(k_block) void k_softmax32(sm_args a, dev_tables T) 
 
 // ---- elementwise ops of the Llama graph ---------------------------------------
 
-template <int OP>   // 0 add, 1 mul
-__global__ void k_binary16(const float *__restrict__ a, const float *__restrict__ b, int64_t n, int64_t nb,
-                           float *__restrict__ dst, dev_tables T) {
+// The elementwise ops in either format: fmt16 (xlns16 through the
+// conversion, decode, Gaussian-log and sigmoid tables) or fmt32 (xlns32,
+// converted arithmetically, adder over the global xlns32 tables).
+struct fmt16 {
+    using code_t = uint16_t;
+    const dev_tables &T;
+    __device__ __forceinline__ uint32_t from(float v) const { return x16_from_f32(T.cvt16, v); }
+    __device__ __forceinline__ float to(uint32_t c) const { return T.rev16[c]; }
+    __device__ __forceinline__ uint32_t add(uint32_t x, uint32_t y) const { return x16_add_g(T.gauss16, x, y); }
+    __device__ __forceinline__ uint32_t mul(uint32_t x, uint32_t y) const { return x16_mul(x, y); }
+    __device__ __forceinline__ uint32_t neg(uint32_t x) const { return x ^ k16_sign; }
+    // xlns16_silu: x times the table sigmoid of x
+    __device__ __forceinline__ uint32_t silu(uint32_t x) const { return x16_mul(x, T.sig16[x]); }
+};
+struct fmt32 {
+    using code_t = uint32_t;
+    const dev_tables &T;
+    __device__ __forceinline__ uint32_t from(float v) const { return x32_from_f32(v); }
+    __device__ __forceinline__ float to(uint32_t c) const { return x32_to_f32(c); }
+    __device__ __forceinline__ uint32_t add(uint32_t x, uint32_t y) const { return x32_add(T.tab32, x, y); }
+    __device__ __forceinline__ uint32_t mul(uint32_t x, uint32_t y) const { return x32_mul(x, y); }
+    __device__ __forceinline__ uint32_t neg(uint32_t x) const { return x ^ k32_sign; }
+    // xlns32_silu: x times the sigmoid of its value, the sigmoid formed in
+    // double and rounded to float (libm-independent at float precision)
+    __device__ __forceinline__ uint32_t silu(uint32_t x) const {
+        const double v = (double)x32_to_f32(x);
+        return x32_mul(x, x32_from_f32((float)(1.0 / (1.0 + exp(-v)))));
+    }
+};
+template <int W>
+using fmt_t = typename std::conditional<W == 16, fmt16, fmt32>::type;
+
+template <int W, int OP>   // OP 0 add, 1 mul
+__global__ void k_binary(const float *__restrict__ a, const float *__restrict__ b, int64_t n, int64_t nb,
+                         float *__restrict__ dst, dev_tables T) {
+    const fmt_t<W> F{T};
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)blockDim.x * gridDim.x) {
-        const uint32_t x = x16_from_f32(T.cvt16, a[i]), y = x16_from_f32(T.cvt16, b[i % nb]);
-        dst[i] = T.rev16[OP == 0 ? x16_add_g(T.gauss16, x, y) : x16_mul(x, y)];
+        const uint32_t x = F.from(a[i]), y = F.from(b[i % nb]);
+        dst[i] = F.to(OP == 0 ? F.add(x, y) : F.mul(x, y));
     }
 }
 
-__global__ void k_swiglu16(const float *__restrict__ g, int64_t g_ld, const float *__restrict__ u, int64_t u_ld,
-                           float *__restrict__ dst, int64_t ncols, int64_t nrows, dev_tables T) {
+template <int W>
+__global__ void k_swiglu(const float *__restrict__ g, int64_t g_ld, const float *__restrict__ u, int64_t u_ld,
+                         float *__restrict__ dst, int64_t ncols, int64_t nrows, dev_tables T) {
+    const fmt_t<W> F{T};
     const int64_t n = ncols * nrows;
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)blockDim.x * gridDim.x) {
         const int64_t r = i / ncols, c = i - r * ncols;
-        const uint32_t gv = x16_from_f32(T.cvt16, g[r * g_ld + c]);
-        const uint32_t uv = x16_from_f32(T.cvt16, u[r * u_ld + c]);
-        dst[i] = T.rev16[x16_mul(x16_mul(gv, T.sig16[gv]), uv)];
+        const uint32_t gv = F.from(g[r * g_ld + c]);
+        const uint32_t uv = F.from(u[r * u_ld + c]);
+        dst[i] = F.to(F.mul(F.silu(gv), uv));
     }
 }
 
@@ -1139,19 +1175,22 @@ __global__ void k_get_rows_packed(const uint16_t *__restrict__ w, int64_t K, int
 }
 
 // one thread per rotated pair (or passthrough element)
-__device__ __forceinline__ void rope_pair(const float *xr, int64_t j, int n_dims, int neox, const float *cs,
-                                          const dev_tables &T, int64_t &i0, int64_t &i1, uint32_t &r0, uint32_t &r1) {
-    const uint32_t c = x16_from_f32(T.cvt16, cs[j * 2]), sn = x16_from_f32(T.cvt16, cs[j * 2 + 1]);
+template <class F>
+__device__ __forceinline__ void rope_pair(const F &f, const float *xr, int64_t j, int n_dims, int neox, const float *cs,
+                                          int64_t &i0, int64_t &i1, uint32_t &r0, uint32_t &r1) {
+    const uint32_t c = f.from(cs[j * 2]), sn = f.from(cs[j * 2 + 1]);
     i0 = neox ? j : 2 * j;
     i1 = neox ? j + n_dims / 2 : 2 * j + 1;
-    const uint32_t x0 = x16_from_f32(T.cvt16, xr[i0]), x1 = x16_from_f32(T.cvt16, xr[i1]);
-    r0 = x16_add_g(T.gauss16, x16_mul(x0, c), x16_mul(x1, sn) ^ k16_sign);
-    r1 = x16_add_g(T.gauss16, x16_mul(x0, sn), x16_mul(x1, c));
+    const uint32_t x0 = f.from(xr[i0]), x1 = f.from(xr[i1]);
+    r0 = f.add(f.mul(x0, c), f.neg(f.mul(x1, sn)));
+    r1 = f.add(f.mul(x0, sn), f.mul(x1, c));
 }
 
-__global__ void k_rope16(const float *__restrict__ x, int64_t x_ld, const int32_t *__restrict__ pos, int64_t ntok,
-                         int64_t nhead, int64_t ne0, int n_dims, int neox, const float *__restrict__ cos_sin,
-                         float *__restrict__ dst, dev_tables T) {
+template <int W>
+__global__ void k_rope(const float *__restrict__ x, int64_t x_ld, const int32_t *__restrict__ pos, int64_t ntok,
+                       int64_t nhead, int64_t ne0, int n_dims, int neox, const float *__restrict__ cos_sin,
+                       float *__restrict__ dst, dev_tables T) {
+    const fmt_t<W> F{T};
     const int64_t half = n_dims / 2, per = half + (ne0 - n_dims);
     const int64_t n = ntok * nhead * per;
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)blockDim.x * gridDim.x) {
@@ -1162,26 +1201,24 @@ __global__ void k_rope16(const float *__restrict__ x, int64_t x_ld, const int32_
         if (j < half) {
             int64_t i0, i1;
             uint32_t r0, r1;
-            rope_pair(xr, j, n_dims, neox, cos_sin + (int64_t)pos[t] * half * 2, T, i0, i1, r0, r1);
-            yr[i0] = T.rev16[r0];
-            yr[i1] = T.rev16[r1];
+            rope_pair(F, xr, j, n_dims, neox, cos_sin + (int64_t)pos[t] * half * 2, i0, i1, r0, r1);
+            yr[i0] = F.to(r0);
+            yr[i1] = F.to(r1);
         } else {
             const int64_t i0 = n_dims + (j - half);
-            yr[i0] = T.rev16[x16_from_f32(T.cvt16, xr[i0])];
+            yr[i0] = F.to(F.from(xr[i0]));
         }
     }
 }
 
-// F32 value -> IEEE half (round to nearest even) -> F32 -> xlns16, as the
-// KV cache stores and reads it
-__device__ __forceinline__ uint16_t kv_code(const dev_tables &T, float v) {
-    return (uint16_t)x16_from_f32(T.cvt16, __half2float(__float2half_rn(v)));
-}
-
-__global__ void k_store_kv16(const float *__restrict__ x, int64_t x_ld, const int32_t *__restrict__ pos, int64_t ntok,
-                             int64_t nhead, int64_t ne0, int rope_n_dims, const float *__restrict__ cos_sin,
-                             uint16_t *__restrict__ cache, int64_t cache_m, int64_t cache_slice, int transposed,
-                             const int32_t *__restrict__ seq, int64_t seq_stride, dev_tables T) {
+// F32 value -> IEEE half (round to nearest even) -> F32 -> LNS, as the KV
+// cache stores and reads it
+template <int W>
+__global__ void k_store_kv(const float *__restrict__ x, int64_t x_ld, const int32_t *__restrict__ pos, int64_t ntok,
+                           int64_t nhead, int64_t ne0, int rope_n_dims, const float *__restrict__ cos_sin,
+                           typename fmt_t<W>::code_t *__restrict__ cache, int64_t cache_m, int64_t cache_slice,
+                           int transposed, const int32_t *__restrict__ seq, int64_t seq_stride, dev_tables T) {
+    const fmt_t<W> F{T};
     const int64_t n = ntok * nhead * ne0;
     const int64_t half = rope_n_dims / 2;
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)blockDim.x * gridDim.x) {
@@ -1194,16 +1231,17 @@ __global__ void k_store_kv16(const float *__restrict__ x, int64_t x_ld, const in
             // normal rope: element d belongs to pair d / 2
             int64_t i0, i1;
             uint32_t r0, r1;
-            rope_pair(xr, d / 2, rope_n_dims, 0, cos_sin + p * half * 2, T, i0, i1, r0, r1);
-            v = T.rev16[(d & 1) ? r1 : r0];
+            rope_pair(F, xr, d / 2, rope_n_dims, 0, cos_sin + p * half * 2, i0, i1, r0, r1);
+            v = F.to((d & 1) ? r1 : r0);
         } else if (rope_n_dims > 0) {
-            v = T.rev16[x16_from_f32(T.cvt16, xr[d])];
+            v = F.to(F.from(xr[d]));
         } else {
             v = xr[d];
         }
         const int64_t o = transposed ? h * cache_slice + ((p >> 3) * ne0 + d) * 8 + (p & 7)
                                      : h * cache_slice + ((d >> 3) * cache_m + p) * 8 + (d & 7);
-        cache[(seq ? (int64_t)seq[t] * seq_stride : 0) + o] = kv_code(T, v);
+        cache[(seq ? (int64_t)seq[t] * seq_stride : 0) + o] =
+            (typename fmt_t<W>::code_t)F.from(__half2float(__float2half_rn(v)));
     }
 }
 
@@ -1434,6 +1472,66 @@ static int launch_sm16(sm_args &m, int64_t nrows, const dev_tables &T, hipStream
 using namespace lnship;
 
 // ===================================================================== C ABI ==
+
+template <int W, int OP>
+static int binary_common(const float *a, const float *b, int64_t n, int64_t nb, float *dst, void *stream) {
+    device_state *s = state();
+    if (!s) return LNSHIP_ENOINIT;
+    if (n < 0 || nb <= 0) return fail(LNSHIP_EINVAL, OP == 0 ? "add: bad length%s" : "mul: bad length%s");
+    if (n == 0) return 0;
+    hipLaunchKernelGGL((k_binary<W, OP>), dim3(grid_for(n, 4)), dim3(k_block), 0, (hipStream_t)stream, a, b, n, nb,
+                       dst, s->T);
+    LNSHIP_HIP(hipGetLastError());
+    return 0;
+}
+
+template <int W>
+static int swiglu_common(const float *gate, int64_t gate_ld, const float *up, int64_t up_ld, float *dst,
+                         int64_t ncols, int64_t nrows, void *stream) {
+    device_state *s = state();
+    if (!s) return LNSHIP_ENOINIT;
+    if (ncols < 0 || nrows < 0 || gate_ld < ncols || up_ld < ncols) return fail(LNSHIP_EINVAL, "swiglu: bad shape%s");
+    if (ncols == 0 || nrows == 0) return 0;
+    hipLaunchKernelGGL(k_swiglu<W>, dim3(grid_for(ncols * nrows, 4)), dim3(k_block), 0, (hipStream_t)stream, gate,
+                       gate_ld, up, up_ld, dst, ncols, nrows, s->T);
+    LNSHIP_HIP(hipGetLastError());
+    return 0;
+}
+
+template <int W>
+static int rope_common(const float *x, int64_t x_ld, const int32_t *pos, int64_t ntok, int64_t nhead, int64_t ne0,
+                       int n_dims, int neox, const float *cos_sin, float *dst, void *stream) {
+    device_state *s = state();
+    if (!s) return LNSHIP_ENOINIT;
+    if (n_dims <= 0 || n_dims % 2 || n_dims > ne0 || x_ld < nhead * ne0 || ntok < 0 || nhead < 0)
+        return fail(LNSHIP_EINVAL, "rope: bad shape%s");
+    const int64_t n = ntok * nhead * (n_dims / 2 + ne0 - n_dims);
+    if (n == 0) return 0;
+    hipLaunchKernelGGL(k_rope<W>, dim3(grid_for(n, 4)), dim3(k_block), 0, (hipStream_t)stream, x, x_ld, pos, ntok,
+                       nhead, ne0, n_dims, neox, cos_sin, dst, s->T);
+    LNSHIP_HIP(hipGetLastError());
+    return 0;
+}
+
+template <int W>
+static int store_kv_common(const float *x, int64_t x_ld, const int32_t *pos, int64_t ntok, int64_t nhead, int64_t ne0,
+                           int rope_n_dims, const float *cos_sin, typename fmt_t<W>::code_t *cache, int64_t cache_m,
+                           int64_t cache_slice, int cache_transposed, const int32_t *seq, int64_t seq_stride,
+                           void *stream) {
+    device_state *s = state();
+    if (!s) return LNSHIP_ENOINIT;
+    if (rope_n_dims < 0 || rope_n_dims % 2 || rope_n_dims > ne0 || x_ld < nhead * ne0 || ntok < 0 || nhead < 0)
+        return fail(LNSHIP_EINVAL, "store_kv: bad shape%s");
+    if (!cache_transposed && ne0 % 8) return fail(LNSHIP_EINVAL, "store_kv: head size not a multiple of 8%s");
+    if (seq && seq_stride < 0) return fail(LNSHIP_EINVAL, "store_kv: negative sequence stride%s");
+    const int64_t n = ntok * nhead * ne0;
+    if (n == 0) return 0;
+    hipLaunchKernelGGL(k_store_kv<W>, dim3(grid_for(n, 4)), dim3(k_block), 0, (hipStream_t)stream, x, x_ld, pos, ntok,
+                       nhead, ne0, rope_n_dims, cos_sin, cache, cache_m, cache_slice, cache_transposed, seq, seq_stride,
+                       s->T);
+    LNSHIP_HIP(hipGetLastError());
+    return 0;
+}
 
 extern "C" {
 
@@ -1717,36 +1815,27 @@ int64_t lnship_max_row(int which, int mode) {
     }
 }
 
+
+
 int lnship16_add(const float *a, const float *b, int64_t n, int64_t nb, float *dst, void *stream) {
-    device_state *s = state();
-    if (!s) return LNSHIP_ENOINIT;
-    if (n < 0 || nb <= 0) return fail(LNSHIP_EINVAL, "add: bad length%s");
-    if (n == 0) return 0;
-    hipLaunchKernelGGL(k_binary16<0>, dim3(grid_for(n, 4)), dim3(k_block), 0, (hipStream_t)stream, a, b, n, nb, dst, s->T);
-    LNSHIP_HIP(hipGetLastError());
-    return 0;
+    return binary_common<16, 0>(a, b, n, nb, dst, stream);
 }
-
 int lnship16_mul(const float *a, const float *b, int64_t n, int64_t nb, float *dst, void *stream) {
-    device_state *s = state();
-    if (!s) return LNSHIP_ENOINIT;
-    if (n < 0 || nb <= 0) return fail(LNSHIP_EINVAL, "mul: bad length%s");
-    if (n == 0) return 0;
-    hipLaunchKernelGGL(k_binary16<1>, dim3(grid_for(n, 4)), dim3(k_block), 0, (hipStream_t)stream, a, b, n, nb, dst, s->T);
-    LNSHIP_HIP(hipGetLastError());
-    return 0;
+    return binary_common<16, 1>(a, b, n, nb, dst, stream);
 }
-
+int lnship32_add(const float *a, const float *b, int64_t n, int64_t nb, float *dst, void *stream) {
+    return binary_common<32, 0>(a, b, n, nb, dst, stream);
+}
+int lnship32_mul(const float *a, const float *b, int64_t n, int64_t nb, float *dst, void *stream) {
+    return binary_common<32, 1>(a, b, n, nb, dst, stream);
+}
 int lnship16_swiglu(const float *gate, int64_t gate_ld, const float *up, int64_t up_ld, float *dst, int64_t ncols,
                     int64_t nrows, void *stream) {
-    device_state *s = state();
-    if (!s) return LNSHIP_ENOINIT;
-    if (ncols < 0 || nrows < 0 || gate_ld < ncols || up_ld < ncols) return fail(LNSHIP_EINVAL, "swiglu: bad shape%s");
-    if (ncols == 0 || nrows == 0) return 0;
-    hipLaunchKernelGGL(k_swiglu16, dim3(grid_for(ncols * nrows, 4)), dim3(k_block), 0, (hipStream_t)stream, gate,
-                       gate_ld, up, up_ld, dst, ncols, nrows, s->T);
-    LNSHIP_HIP(hipGetLastError());
-    return 0;
+    return swiglu_common<16>(gate, gate_ld, up, up_ld, dst, ncols, nrows, stream);
+}
+int lnship32_swiglu(const float *gate, int64_t gate_ld, const float *up, int64_t up_ld, float *dst, int64_t ncols,
+                    int64_t nrows, void *stream) {
+    return swiglu_common<32>(gate, gate_ld, up, up_ld, dst, ncols, nrows, stream);
 }
 
 int lnship16_get_rows_packed(const uint16_t *w, int64_t K, int64_t M, const int32_t *rows, int64_t nrows, float *dst,
@@ -1761,36 +1850,27 @@ int lnship16_get_rows_packed(const uint16_t *w, int64_t K, int64_t M, const int3
     return 0;
 }
 
+
+
 int lnship16_rope(const float *x, int64_t x_ld, const int32_t *pos, int64_t ntok, int64_t nhead, int64_t ne0,
                   int n_dims, int neox, const float *cos_sin, float *dst, void *stream) {
-    device_state *s = state();
-    if (!s) return LNSHIP_ENOINIT;
-    if (n_dims <= 0 || n_dims % 2 || n_dims > ne0 || x_ld < nhead * ne0 || ntok < 0 || nhead < 0)
-        return fail(LNSHIP_EINVAL, "rope: bad shape%s");
-    const int64_t n = ntok * nhead * (n_dims / 2 + ne0 - n_dims);
-    if (n == 0) return 0;
-    hipLaunchKernelGGL(k_rope16, dim3(grid_for(n, 4)), dim3(k_block), 0, (hipStream_t)stream, x, x_ld, pos, ntok, nhead,
-                       ne0, n_dims, neox, cos_sin, dst, s->T);
-    LNSHIP_HIP(hipGetLastError());
-    return 0;
+    return rope_common<16>(x, x_ld, pos, ntok, nhead, ne0, n_dims, neox, cos_sin, dst, stream);
 }
-
+int lnship32_rope(const float *x, int64_t x_ld, const int32_t *pos, int64_t ntok, int64_t nhead, int64_t ne0,
+                  int n_dims, int neox, const float *cos_sin, float *dst, void *stream) {
+    return rope_common<32>(x, x_ld, pos, ntok, nhead, ne0, n_dims, neox, cos_sin, dst, stream);
+}
 int lnship16_store_kv(const float *x, int64_t x_ld, const int32_t *pos, int64_t ntok, int64_t nhead, int64_t ne0,
                       int rope_n_dims, const float *cos_sin, uint16_t *cache, int64_t cache_m, int64_t cache_slice,
                       int cache_transposed, const int32_t *seq, int64_t seq_stride, void *stream) {
-    device_state *s = state();
-    if (!s) return LNSHIP_ENOINIT;
-    if (rope_n_dims < 0 || rope_n_dims % 2 || rope_n_dims > ne0 || x_ld < nhead * ne0 || ntok < 0 || nhead < 0)
-        return fail(LNSHIP_EINVAL, "store_kv: bad shape%s");
-    if (!cache_transposed && ne0 % 8) return fail(LNSHIP_EINVAL, "store_kv: head size not a multiple of 8%s");
-    if (seq && seq_stride < 0) return fail(LNSHIP_EINVAL, "store_kv: negative sequence stride%s");
-    const int64_t n = ntok * nhead * ne0;
-    if (n == 0) return 0;
-    hipLaunchKernelGGL(k_store_kv16, dim3(grid_for(n, 4)), dim3(k_block), 0, (hipStream_t)stream, x, x_ld, pos, ntok,
-                       nhead, ne0, rope_n_dims, cos_sin, cache, cache_m, cache_slice, cache_transposed, seq, seq_stride,
-                       s->T);
-    LNSHIP_HIP(hipGetLastError());
-    return 0;
+    return store_kv_common<16>(x, x_ld, pos, ntok, nhead, ne0, rope_n_dims, cos_sin, cache, cache_m, cache_slice,
+                               cache_transposed, seq, seq_stride, stream);
+}
+int lnship32_store_kv(const float *x, int64_t x_ld, const int32_t *pos, int64_t ntok, int64_t nhead, int64_t ne0,
+                      int rope_n_dims, const float *cos_sin, uint32_t *cache, int64_t cache_m, int64_t cache_slice,
+                      int cache_transposed, const int32_t *seq, int64_t seq_stride, void *stream) {
+    return store_kv_common<32>(x, x_ld, pos, ntok, nhead, ne0, rope_n_dims, cos_sin, cache, cache_m, cache_slice,
+                               cache_transposed, seq, seq_stride, stream);
 }
 
 int lnship_rope_table(float freq_base, int n_dims, int64_t n_pos, float *out) {

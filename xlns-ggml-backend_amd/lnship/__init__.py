@@ -79,6 +79,13 @@ def lib():
                                          c_p]),
         "lnship16_store_kv": (ctypes.c_int, [c_p, c_i64, c_p, c_i64, c_i64, c_i64, ctypes.c_int, c_p, c_p, c_i64,
                                              c_i64, ctypes.c_int, c_p, c_i64, c_p]),
+        "lnship32_add": (ctypes.c_int, [c_p, c_p, c_i64, c_i64, c_p, c_p]),
+        "lnship32_mul": (ctypes.c_int, [c_p, c_p, c_i64, c_i64, c_p, c_p]),
+        "lnship32_swiglu": (ctypes.c_int, [c_p, c_i64, c_p, c_i64, c_p, c_i64, c_i64, c_p]),
+        "lnship32_rope": (ctypes.c_int, [c_p, c_i64, c_p, c_i64, c_i64, c_i64, ctypes.c_int, ctypes.c_int, c_p, c_p,
+                                         c_p]),
+        "lnship32_store_kv": (ctypes.c_int, [c_p, c_i64, c_p, c_i64, c_i64, c_i64, ctypes.c_int, c_p, c_p, c_i64,
+                                             c_i64, ctypes.c_int, c_p, c_i64, c_p]),
         "lnship_causal_mask": (ctypes.c_int, [c_p, c_i64, c_i64, c_p, c_p]),
         "lnship_rope_table": (ctypes.c_int, [ctypes.c_float, ctypes.c_int, c_i64, c_p]),
     }
@@ -219,6 +226,14 @@ def mul_mat16(mode, wp, x, K, M, ne02=1, ne03=1, seed=7, out=None):
     a = _mm_args(wp, x, out, K, M, ne02, ne03, seed)
     check(lib().lnship16_mul_mat(mode, ctypes.byref(a), _stream()))
     return out
+
+
+def mul_mat32_raw(w_ptr, x_ptr, dst_ptr, K, M, N, ne02=1, ne03=1, ne12=1, ne13=1, x_ld=0, x_slice=0,
+                  w_mstride=0, w_slice=0, dst_ld=0, dst_slice=0, stream=None):
+    """xlns32 mul_mat on raw device pointers (ints), with every stride of the C ABI."""
+    a = MulMatArgs(w_ptr, x_ptr, dst_ptr, K, M, N, ne02, ne03, ne12, ne13, x_ld, x_slice, 0,
+                   w_mstride, w_slice, dst_ld, dst_slice)
+    check(lib().lnship32_mul_mat(ctypes.byref(a), stream if stream is not None else _stream()))
 
 
 def mul_mat32(wp, x, K, M, ne02=1, ne03=1, out=None):

@@ -34,7 +34,7 @@ from dataclasses import dataclass
 
 import numpy as np
 
-from . import BASE, MONTE, LPVIP, SUM32, check, init, kp, lib, mul_mat16_raw
+from . import BASE, MONTE, LPVIP, SUM32, check, init, kp, lib, mul_mat16_raw, mul_mat32_raw
 
 KV_PAD = 256   # llama.cpp pads the KV view to 256 cells without flash attention
 
@@ -332,6 +332,161 @@ class LlamaLNS16:
         tok = self._buf("gtok", 1, torch.int32)
         pos = self._buf("gpos", 1, torch.int32)
         tok.fill_(int(token))
+        pos.fill_(self.n_past)
+        if n_kv not in self._graphs:
+            self._graphs[n_kv] = self._capture(lambda: self.forward(1, tok, pos, n_kv))
+        g, out = self._graphs[n_kv]
+        g.replay()
+        self.n_past += 1
+        return out
+
+
+LLAMA_1B = LlamaConfig(n_layer=16, n_embd=2048, n_head=32, n_head_kv=8, head_dim=64, n_ff=8192, n_vocab=32000,
+                       n_ctx=1024)
+
+
+class LlamaLNS32:
+    """The decoder as the reference's LNS32 backend computes it
+    (src32/lns32-ops.cpp), one sequence: get_rows copies the F32 embedding
+    rows (:707-745), every other op runs in xlns32 with F32 at its boundaries,
+    the weights are packed xlns32 (4 bytes each) and the KV cache holds the
+    xlns32 codes of the IEEE-half-rounded K / V values (llama.cpp's F16 cache
+    as lns32_mul_mat converts it, :64-79).  weights may hold host arrays or
+    device tensors (float32)."""
+
+    def __init__(self, cfg, weights):
+        import torch
+        init()
+        self.cfg = cfg
+        self.torch = torch
+        dev = torch.device("cuda", torch.cuda.current_device())
+        self.dev = dev
+        c = cfg
+        from . import pack32
+
+        def t(a):
+            if isinstance(a, torch.Tensor):
+                return a.to(dev, torch.float32).contiguous()
+            return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+        self.tok_embd_f32 = t(weights["tok_embd"])                  # [vocab, e]: get_rows
+        self.tok_embd = pack32(self.tok_embd_f32)                    # the tied output matrix
+        self.out_norm = t(weights["out_norm"])
+        self.layers = []
+        for L in weights["layers"]:
+            cat = lambda *a: torch.cat([t(x) for x in a]) if isinstance(a[0], torch.Tensor) else t(np.concatenate(a))
+            self.layers.append({
+                "attn_norm": t(L["attn_norm"]),
+                "wqkv": pack32(cat(L["wq"], L["wk"], L["wv"])),
+                "wo": pack32(t(L["wo"])),
+                "ffn_norm": t(L["ffn_norm"]),
+                "wug": pack32(cat(L["w_up"], L["w_gate"])),
+                "wdown": pack32(t(L["w_down"])),
+            })
+        hd, nkv = c.head_dim, c.n_head_kv
+        self.kslice = kp(hd) * c.n_ctx
+        self.vslice = kp(c.n_ctx) * hd
+        assert self.kslice == self.vslice
+        self.kcache = [torch.zeros(nkv * self.kslice, dtype=torch.int32, device=dev) for _ in range(c.n_layer)]
+        self.vcache = [torch.zeros(nkv * self.kslice, dtype=torch.int32, device=dev) for _ in range(c.n_layer)]
+        rt = np.empty(c.n_ctx * hd, np.float32)
+        check(lib().lnship_rope_table(c.rope_theta, hd, c.n_ctx, ctypes.c_void_p(rt.ctypes.data)))
+        self.cos_sin = t(rt)
+        self.n_past = 0
+        self._bufs = {}
+        self._graphs = {}
+
+    _buf = LlamaLNS16._buf
+    _capture = LlamaLNS16._capture
+
+    def weight_bytes_per_token(self):
+        """Bytes of packed weights one decode token reads (4 per weight)."""
+        c = self.cfg
+        e, f, hd = c.n_embd, c.n_ff, c.head_dim
+        per_layer = (c.n_head + 2 * c.n_head_kv) * hd * e + e * c.n_head * hd + 2 * f * e + e * f
+        return 4 * (c.n_layer * per_layer + c.n_vocab * e)
+
+    def forward(self, T, tokens_dev, pos_dev, n_kv):
+        """Runs T tokens at positions pos_dev[0..T) (device int32) against a
+        KV view of n_kv cells; returns the device logits of the last one."""
+        torch, c, L = self.torch, self.cfg, lib()
+        st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        e, hd, nh, nkv, f = c.n_embd, c.head_dim, c.n_head, c.n_head_kv, c.n_ff
+        nq, nqkv = nh * hd, (nh + 2 * nkv) * hd
+        P = lambda b, off=0: ctypes.c_void_p(b.data_ptr() + off * b.element_size())
+        mm = lambda w, x, dst, K, M, N, **kw: mul_mat32_raw(w, x, dst, K, M, N, stream=st, **kw)
+        x = self._buf("x", T * e)
+        h = self._buf("h", T * e)
+        qkv = self._buf("qkv", T * nqkv)
+        q = self._buf("q", T * nq)
+        kq = self._buf("kq", nh * T * n_kv)
+        att = self._buf("att", T * nq)
+        o = self._buf("o", T * e)
+        ug = self._buf("ug", T * 2 * f)
+        sw = self._buf("sw", T * f)
+        mask = self._buf("mask", T * n_kv)
+        logits = self._buf("logits", c.n_vocab)
+        # GET_ROWS of an F32 table is a row copy
+        torch.index_select(self.tok_embd_f32, 0, tokens_dev[:T].long(), out=x[: T * e].view(T, e))
+        check(L.lnship_causal_mask(P(pos_dev), T, n_kv, P(mask), st))
+        from . import SoftMaxArgs
+        for il, W in enumerate(self.layers):
+            last = il == c.n_layer - 1
+            check(L.lnship32_rms_norm(P(x), P(h), e, T, c.eps, st))
+            check(L.lnship32_mul(P(h), P(W["attn_norm"]), T * e, e, P(h), st))
+            mm(W["wqkv"].data_ptr(), P(h), P(qkv), e, nqkv, T)
+            check(L.lnship32_rope(P(qkv), nqkv, P(pos_dev), T, nh, hd, hd, 0, P(self.cos_sin), P(q), st))
+            check(L.lnship32_store_kv(P(qkv, nq), nqkv, P(pos_dev), T, nkv, hd, hd, P(self.cos_sin),
+                                      P(self.kcache[il]), c.n_ctx, self.kslice, 0, None, 0, st))
+            check(L.lnship32_store_kv(P(qkv, nq + nkv * hd), nqkv, P(pos_dev), T, nkv, hd, 0, P(self.cos_sin),
+                                      P(self.vcache[il]), c.n_ctx, self.vslice, 1, None, 0, st))
+            mm(self.kcache[il].data_ptr(), P(q), P(kq), hd, n_kv, T, ne02=nkv, ne12=nh, x_ld=nq, x_slice=hd,
+               w_mstride=c.n_ctx, w_slice=self.kslice)
+            a = SoftMaxArgs(P(kq), (ctypes.c_int64 * 4)(n_kv, T, nh, 1), P(mask), (ctypes.c_int64 * 4)(n_kv, T, 1, 1),
+                            1.0 / math.sqrt(hd), P(kq), 0)
+            check(L.lnship32_soft_max(ctypes.byref(a), st))
+            mm(self.vcache[il].data_ptr(), P(kq), P(att), n_kv, hd, T, ne02=nkv, ne12=nh, x_ld=n_kv,
+               x_slice=T * n_kv, w_slice=self.vslice, dst_ld=nq, dst_slice=hd)
+            mm(W["wo"].data_ptr(), P(att), P(o), nq, e, T)
+            rows = 1 if last else T
+            r0 = (T - rows) * e
+            check(L.lnship32_add(P(o, r0), P(x, r0), rows * e, rows * e, P(x), st))
+            check(L.lnship32_rms_norm(P(x), P(h), e, rows, c.eps, st))
+            check(L.lnship32_mul(P(h), P(W["ffn_norm"]), rows * e, e, P(h), st))
+            mm(W["wug"].data_ptr(), P(h), P(ug), e, 2 * f, rows)
+            check(L.lnship32_swiglu(P(ug, f), 2 * f, P(ug), 2 * f, P(sw), f, rows, st))
+            mm(W["wdown"].data_ptr(), P(sw), P(o), f, e, rows)
+            check(L.lnship32_add(P(o), P(x), rows * e, rows * e, P(x), st))
+        check(L.lnship32_rms_norm(P(x), P(h), e, 1, c.eps, st))
+        check(L.lnship32_mul(P(h), P(self.out_norm), e, e, P(h), st))
+        mm(self.tok_embd.data_ptr(), P(h), P(logits), e, c.n_vocab, 1)
+        return logits[: c.n_vocab]
+
+    def eval(self, tokens):
+        """Appends tokens (host list); returns the device logits of the last one."""
+        torch = self.torch
+        T = len(tokens)
+        p0 = self.n_past
+        assert p0 + T <= self.cfg.n_ctx, "context full"
+        tok = self._buf("tok", T, torch.int32)
+        pos = self._buf("pos", T, torch.int32)
+        tok[:T].copy_(torch.tensor(tokens, dtype=torch.int32))
+        pos[:T].copy_(torch.arange(p0, p0 + T, dtype=torch.int32))
+        out = self.forward(T, tok, pos, n_kv_for(p0 + T, self.cfg.n_ctx))
+        self.n_past += T
+        return out
+
+    def decode_graph(self, token, n_kv=None):
+        """One decode step through a captured HIP graph; token is a host int or
+        a device int32 tensor of one element.  Returns the device logits."""
+        torch = self.torch
+        n_kv = n_kv or n_kv_for(self.n_past + 1, self.cfg.n_ctx)
+        tok = self._buf("gtok", 1, torch.int32)
+        pos = self._buf("gpos", 1, torch.int32)
+        if isinstance(token, torch.Tensor):
+            tok[:1].copy_(token.reshape(-1)[:1])
+        else:
+            tok.fill_(int(token))
         pos.fill_(self.n_past)
         if n_kv not in self._graphs:
             self._graphs[n_kv] = self._capture(lambda: self.forward(1, tok, pos, n_kv))
