@@ -31,7 +31,7 @@ def parse():
     ap.add_argument("--steps", type=int, default=120)
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--mode", default="sum32", choices=["base", "monte", "lpvip", "sum32", "all"])
-    ap.add_argument("--prompt", type=int, default=128)
+    ap.add_argument("--prompt", type=int, default=None, help="prompt tokens (128; 512 with --lns32)")
     ap.add_argument("--cpu-tokens", type=int, default=3, help="decode tokens of the CPU baseline sample")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-graph", action="store_true", help="decode eagerly instead of replaying a HIP graph")
@@ -44,6 +44,9 @@ def parse():
     ap.add_argument("--batch", type=int, default=1, metavar="S",
                     help="BASELINE config 3: S independent sequences, each prompt prefilled on its own, then "
                          "batched greedy decode (one token per sequence per step); prints its own JSON line")
+    ap.add_argument("--lns32", action="store_true",
+                    help="BASELINE config 4: the LNS32 1B-shape decoder (prompt defaults to 512 tokens); prints its "
+                         "own JSON line")
     args, rest = ap.parse_known_args()
     if rest:
         ap.error("unrecognized arguments: %s" % " ".join(rest))
@@ -292,6 +295,11 @@ def main():
         return
     if args.mode == "all":
         sys.exit("bench.py: --mode all is for --ops only")
+    if args.lns32:
+        run_lns32(args)
+        return
+    if args.prompt is None:
+        args.prompt = 128
     if args.batch > 1:
         run_batch(args)
         return
@@ -383,6 +391,119 @@ def main():
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(cfg, weights, args.mode, args.cpu_tokens)
     print(json.dumps(out), flush=True)
+
+
+def lns32_weights(cfg, seed, std, torch):
+    """Random-init weights of the architecture on the device (N(0, std^2),
+    torch's seeded generator; norm weights ones)."""
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    e, f, d = cfg.n_embd, cfg.n_ff, cfg.head_dim
+    nq, nkv = cfg.n_head * d, cfg.n_head_kv * d
+    r = lambda *shape: torch.randn(*shape, generator=g, device="cuda") * std
+    w = {"tok_embd": r(cfg.n_vocab, e), "out_norm": torch.ones(e, device="cuda"), "layers": []}
+    for _ in range(cfg.n_layer):
+        w["layers"].append({"attn_norm": torch.ones(e, device="cuda"), "wq": r(nq, e), "wk": r(nkv, e),
+                            "wv": r(nkv, e), "wo": r(e, nq), "ffn_norm": torch.ones(e, device="cuda"),
+                            "w_gate": r(f, e), "w_up": r(f, e), "w_down": r(e, f)})
+    return w
+
+
+def run_lns32(args):
+    """the LNS32 backend's graph on a Llama-style 1B-shape
+    decoder (16 layers, d 2048, 32 / 8 heads x 64, SwiGLU 8192, vocab 32000),
+    random-init N(0, 0.02) weights packed as xlns32 (4 bytes per weight).
+    Prefill of the prompt, then greedy decode from a replayed HIP graph.  The
+    roofline is the decode's weight stream: every token reads each packed
+    weight once."""
+    import numpy as np
+    import torch
+    import lnship
+    from lnship import llama
+
+    torch.cuda.set_device(0)
+    lnship.init()
+    cfg = llama.LLAMA_1B
+    prompt_n = args.prompt if args.prompt is not None else 512
+    t0 = time.perf_counter()
+    weights = lns32_weights(cfg, 4321, 0.02, torch)
+    model = llama.LlamaLNS32(cfg, weights)
+    torch.cuda.synchronize()
+    t_setup = time.perf_counter() - t0
+    rng = np.random.default_rng(2024)
+    prompt = [int(t) for t in rng.integers(0, cfg.n_vocab, prompt_n)]
+    model.eval(prompt[:8])
+    model.n_past = 0
+    torch.cuda.synchronize()
+    tp = time.perf_counter()
+    logits = model.eval(prompt)
+    torch.cuda.synchronize()
+    t_prefill = time.perf_counter() - tp
+    tok_dev = torch.argmax(logits).to(torch.int32).reshape(1)
+
+    def step():
+        nonlocal tok_dev
+        out = model.decode_graph(tok_dev)
+        tok_dev = torch.argmax(out).to(torch.int32).reshape(1)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    ts = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    t_decode = time.perf_counter() - ts
+    tok_s = args.steps / t_decode
+    wbytes = model.weight_bytes_per_token()
+    achieved = wbytes * tok_s / 1e9
+    out = {
+        "metric": "LNS32 decode tok/s and weight-stream HBM GB/s, 1B-shape Llama decoder",
+        "value": round(tok_s, 3), "unit": "tok/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(t_decode / args.steps * 1e3, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "xlns32",
+        "data": "synthetic: torch-seeded N(0,0.02) weights packed as xlns32, uniform token ids",
+        "config": {"workload": "BASELINE config 4: LNS32 Llama-style 1B-shape decoder, %d-token prompt then "
+                               "greedy decode (one decoded token per step)" % prompt_n,
+                   "prompt_tokens": prompt_n, "n_kv": llama.n_kv_for(model.n_past, cfg.n_ctx),
+                   "graph": "hipGraph per decode step"},
+        "prefill_tok_s": round(prompt_n / t_prefill, 3),
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 3), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 6), "traffic": None,
+                     "kernel": "whole decode token: xlns32 weights read once per token",
+                     "weight_bytes_per_token": wbytes},
+        "setup_s": round(t_setup, 2),
+    }
+    if not args.no_cpu:
+        out["cpu_baseline"] = cpu_baseline_lns32(cfg, weights, torch)
+    print(json.dumps(out), flush=True)
+
+
+def cpu_baseline_lns32(cfg, weights, torch):
+    """The oracle's LNS32 graph at the 1B width on the host: one decode token
+    after a 2-token prompt through the embedding, norm and output alone (t0)
+    and through layer 0 as well (t1); a 16-layer token is t0 + 16 (t1 - t0)."""
+    import dataclasses
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    from llama_oracle import LlamaOracle32
+    h = lambda t: t.detach().float().cpu().numpy()
+    w1 = {"tok_embd": h(weights["tok_embd"]), "out_norm": h(weights["out_norm"]),
+          "layers": [{k: h(v) for k, v in weights["layers"][0].items()}]}
+    cfg1 = dataclasses.replace(cfg, n_layer=1)
+    cpu = LlamaOracle32(cfg1, w1)
+    times = []
+    for n_layers in (0, 1):
+        cpu.n_past = 0
+        cpu.eval([1, 2], n_layers=n_layers)
+        t0 = time.perf_counter()
+        cpu.eval([3], n_layers=n_layers)
+        times.append(time.perf_counter() - t0)
+    per_tok = times[0] + cfg.n_layer * (times[1] - times[0])
+    return {"value": round(1.0 / per_tok, 5), "unit": "tok/s", "cores": 1, "kind": "port",
+            "sample": "one decode token after a 2-token prompt at the 1B width, single-threaded C oracle: "
+                      "embedding + output %.2f s, plus layer 0 %.2f s; scaled to 16 layers" %
+                      (times[0], times[1] - times[0]),
+            "cpu": _cpu_name()}
 
 
 def _graph_step(model, tok_dev):
