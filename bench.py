@@ -44,6 +44,9 @@ def parse():
     ap.add_argument("--batch", type=int, default=1, metavar="S",
                     help="BASELINE config 3: S independent sequences, each prompt prefilled on its own, then "
                          "batched greedy decode (one token per sequence per step); prints its own JSON line")
+    ap.add_argument("--ggml", action="store_true",
+                    help="the PCIe-inclusive rate of the ggml boundary: BASELINE config 1 ops through graph_compute "
+                         "on host buffers next to the same ops on HBM-resident data; prints its own JSON line")
     ap.add_argument("--lns32", action="store_true",
                     help="BASELINE config 4: the LNS32 1B-shape decoder (prompt defaults to 512 tokens); prints its "
                          "own JSON line")
@@ -295,6 +298,9 @@ def main():
         return
     if args.mode == "all":
         sys.exit("bench.py: --mode all is for --ops only")
+    if args.ggml:
+        run_ggml(args)
+        return
     if args.lns32:
         run_lns32(args)
         return
@@ -391,6 +397,71 @@ def main():
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(cfg, weights, args.mode, args.cpu_tokens)
     print(json.dumps(out), flush=True)
+
+
+def run_ggml(args):
+    """BASELINE config 1's ops through libggml-lnship.so's graph_compute, as
+    llama.cpp drives the backend: host (CPU-buffer) tensors, so each call
+    uploads its activations, runs the kernels and downloads the output (the
+    weights are cached on the device after the first call, as the reference's
+    weight cache does).  Beside it, the same op on device-resident data
+    through the C ABI.  Wall-clock per call, averaged over --reps calls."""
+    import numpy as np
+    import torch
+    os.environ.setdefault("GGML_LNS16_SUM", args.mode if args.mode != "all" else "sum32")
+    mode_name = os.environ["GGML_LNS16_SUM"]
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import ggml_host as G
+    import lnship
+    torch.cuda.set_device(0)
+    lnship.init()
+    h = G.Host()
+    be = h.init()
+    rng = np.random.default_rng(7)
+    reps = max(args.reps, 20)
+    f32 = lambda *s_, scale=1.0: (rng.standard_normal(s_) * scale).astype(np.float32)
+    res = []
+
+    def wall(fn):
+        fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            fn()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) / reps * 1e6
+
+    mode = lnship.MODES[mode_name]
+    for (K, M) in ((576, 1536), (1536, 576)):
+        w, x = f32(M, K, scale=0.02), f32(1, K)
+        W = h.tensor([K, M], data=w, weights=True, name="w")
+        X = h.tensor([K, 1], data=x, name="x")
+        D = h.tensor([M, 1], op="MUL_MAT", src=(W, X), name="y")
+        us_b = wall(lambda: h.compute(be, [D]))
+        wp, xd = lnship.pack16(torch.from_numpy(w).cuda()), torch.from_numpy(x).cuda()
+        us_d = wall(lambda: lnship.mul_mat16(mode, wp, xd, K, M))
+        res.append({"op": "mul_mat", "K": K, "M": M, "N": 1, "boundary_us": round(us_b, 2),
+                    "device_us": round(us_d, 2), "pcie_bytes": 4 * (K + M),
+                    "boundary_weight_gbs": round(2 * K * M / us_b / 1e3, 3)})
+    x = f32(1, 576)
+    X = h.tensor([576, 1], data=x, name="x")
+    D = h.tensor([576, 1], op="RMS_NORM", src=(X,), fparams={0: 1e-5}, name="n")
+    xd = torch.from_numpy(x).cuda()
+    res.append({"op": "rms_norm", "n": 576, "rows": 1, "boundary_us": round(wall(lambda: h.compute(be, [D])), 2),
+                "device_us": round(wall(lambda: lnship.rms_norm16(mode, xd, 1e-5)), 2), "pcie_bytes": 8 * 576})
+    z = f32(9, 128, 128, scale=3.0)
+    Z = h.tensor([128, 128, 9], data=z, name="kq")
+    D = h.tensor([128, 128, 9], op="SOFT_MAX", src=(Z,), fparams={0: 0.125, 1: 0.0}, name="p")
+    zd = torch.from_numpy(z).cuda()
+    res.append({"op": "soft_max", "ne": [128, 128, 9], "boundary_us": round(wall(lambda: h.compute(be, [D])), 2),
+                "device_us": round(wall(lambda: lnship.soft_max16(mode, zd, None, 0.125)), 2),
+                "pcie_bytes": 8 * z.size})
+    h.free(be)
+    print(json.dumps({"metric": "ggml boundary PCIe-inclusive latency per op (BASELINE config 1 shapes)",
+                      "mode": mode_name, "reps": reps, "ops": res,
+                      "note": "boundary_us: graph_compute wall time with host tensors (upload, kernels, download, "
+                              "sync); device_us: the same op on HBM-resident tensors through the C ABI, wall time "
+                              "with launch"}), flush=True)
 
 
 def lns32_weights(cfg, seed, std, torch):
