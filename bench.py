@@ -514,7 +514,7 @@ def run_lns32(args):
 
     def step():
         nonlocal tok_dev
-        out = model.decode_graph(tok_dev)
+        out = model.eval([int(tok_dev.item())]) if args.no_graph else model.decode_graph(tok_dev)
         tok_dev = torch.argmax(out).to(torch.int32).reshape(1)
 
     for _ in range(args.warmup):
@@ -537,7 +537,7 @@ def run_lns32(args):
         "config": {"workload": "BASELINE config 4: LNS32 Llama-style 1B-shape decoder, %d-token prompt then "
                                "greedy decode (one decoded token per step)" % prompt_n,
                    "prompt_tokens": prompt_n, "n_kv": llama.n_kv_for(model.n_past, cfg.n_ctx),
-                   "graph": "hipGraph per decode step"},
+                   "graph": "eager" if args.no_graph else "hipGraph per decode step"},
         "prefill_tok_s": round(prompt_n / t_prefill, 3),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 3), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 6), "traffic": None,

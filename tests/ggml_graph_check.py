@@ -12,11 +12,16 @@ general broadcasts, an F16-weight MUL_MAT, a repeated MUL_MAT that hits the
 weight cache, and an unmasked SOFT_MAX.  The oracle runs the same ops in
 graph order, so Monte draws are reserved in the same sequence.
 
-Usage: python ggml_graph_check.py --mode base|monte|lpvip|sum32 [--w32]
+With --policy the backend runs under LNS16_SUM_POLICY and the oracle takes
+each node's summation mode from the same rules (op names, "OP:glob" on the
+node name, or a glob).
+
+Usage: python ggml_graph_check.py --mode base|monte|lpvip|sum32 [--policy RULES] [--w32]
 Exit status 0 when every node matches.
 """
 import argparse
 import ctypes
+import fnmatch
 import json
 import os
 import sys
@@ -69,8 +74,30 @@ def binop(fn, a, b):
     return out
 
 
-def run16(mode_name):
+def policy_modes(policy, default):
+    """mode_of(op, name) under LNS16_SUM_POLICY rules (the forms this check uses)."""
+    rules = []
+    for rule in filter(None, (r.strip() for r in (policy or "").split(","))):
+        sel, mode = rule.rsplit("=", 1)
+        rules.append((sel, O.MODES[mode]))
+
+    def mode_of(op, name):
+        for sel, mode in rules:
+            if sel.upper() == op:
+                return mode
+            if ":" in sel:
+                o, pat = sel.split(":", 1)
+                if o.upper() == op and fnmatch.fnmatch(name, pat):
+                    return mode
+            elif fnmatch.fnmatch(name, sel):
+                return mode
+        return default
+    return mode_of
+
+
+def run16(mode_name, policy=None):
     m = O.MODES[mode_name]
+    mode_of = policy_modes(policy, m)
     L = oracle_fns()
     h = G.Host()
     rng = np.random.default_rng(1234)
@@ -144,16 +171,16 @@ def run16(mode_name):
     # oracle, same op order (Monte draws in graph order)
     O.monte_set(7)
     want = {}
-    want["rms"] = O.rms_norm16(m, x0, 1e-5)
+    want["rms"] = O.rms_norm16(mode_of("RMS_NORM", "norm-0"), x0, 1e-5)
     want["mul"] = binop(L.lno16_mul_f32, want["rms"], g)
-    want["qkv"] = O.mul_mat16(m, O.f2x16(wqkv), want["mul"])
+    want["qkv"] = O.mul_mat16(mode_of("MUL_MAT", "qkv-0"), O.f2x16(wqkv), want["mul"])
     q = np.ascontiguousarray(want["qkv"][:, :E].reshape(T, H, D))
     want["rope"] = np.empty_like(q)
     L.lno16_rope_f32(P(q), P(pos), T, H, D, D, 0, 10000.0, P(want["rope"]))
     qperm = np.ascontiguousarray(want["rope"].transpose(1, 0, 2))
-    want["kq"] = O.mul_mat16_f32w(m, kc.astype(np.float32)[None], qperm[None], ne02=HKV)[0]
-    want["softmax"] = O.soft_max16(m, want["kq"], mask, 0.125)
-    want["ug"] = O.mul_mat16_f32w(m, wq8, want["mul"])
+    want["kq"] = O.mul_mat16_f32w(mode_of("MUL_MAT", "kq-0"), kc.astype(np.float32)[None], qperm[None], ne02=HKV)[0]
+    want["softmax"] = O.soft_max16(mode_of("SOFT_MAX", "kq_soft_max-0"), want["kq"], mask, 0.125)
+    want["ug"] = O.mul_mat16_f32w(mode_of("MUL_MAT", "ffn_up-0"), wq8, want["mul"])
     sw = np.empty((T, 128), np.float32)
     gate, up = np.ascontiguousarray(want["ug"][:, :128]), np.ascontiguousarray(want["ug"][:, 128:])
     L.lno16_swiglu_f32(P(gate), P(up), gate.size, P(sw))
@@ -161,9 +188,9 @@ def run16(mode_name):
     want["swiglu_split"] = sw
     want["add"] = binop(L.lno16_add_f32, x0, want["mul"])
     want["add_bcast"] = binop(L.lno16_add_f32, x0, np.repeat(bias, E, axis=1))
-    want["down"] = O.mul_mat16_f32w(m, w2.astype(np.float32), x1)
-    want["qkv_again"] = O.mul_mat16(m, O.f2x16(wqkv), want["mul"])
-    want["softmax_nomask"] = O.soft_max16(m, z, None, 1.0)
+    want["down"] = O.mul_mat16_f32w(mode_of("MUL_MAT", "ffn_out-0"), w2.astype(np.float32), x1)
+    want["qkv_again"] = O.mul_mat16(mode_of("MUL_MAT", "qkv-1"), O.f2x16(wqkv), want["mul"])
+    want["softmax_nomask"] = O.soft_max16(mode_of("SOFT_MAX", "sm-1"), z, None, 1.0)
 
     report = {}
     for k, tn in nodes.items():
@@ -217,5 +244,8 @@ if __name__ == "__main__":
     ap = argparse.ArgumentParser()
     ap.add_argument("--mode", default="base")
     ap.add_argument("--w32", action="store_true")
+    ap.add_argument("--policy", default=None)
     a = ap.parse_args()
-    sys.exit(run32() if a.w32 else run16(a.mode))
+    if a.policy is not None:
+        os.environ["LNS16_SUM_POLICY"] = a.policy
+    sys.exit(run32() if a.w32 else run16(a.mode, a.policy))

@@ -289,6 +289,19 @@ def test_bad_sum_mode_aborts():
     assert r.returncode != 0 and "GGML_LNS16_SUM must be one of" in r.stderr
 
 
+def test_bad_sum_policy_aborts():
+    for policy, msg in (("MUL_MAT", "is not selector=mode"), ("MUL_MAT=fast", "is not available"),
+                        ("SOFT_MAX=monte", "monte only as GGML_LNS16_SUM")):
+        e = dict(os.environ, GGML_LNS16_SUM="sum32", LNS16_SUM_POLICY=policy)
+        r = subprocess.run([sys.executable, "-c", PRELUDE + "h.reg()"], env=e, capture_output=True, text=True,
+                           timeout=120)
+        assert r.returncode != 0 and msg in r.stderr, (policy, r.stderr[-500:])
+    e = dict(os.environ, GGML_LNS16_SUM="base", LNS16_SUM_POLICY="MUL_MAT=sum32, SOFT_MAX:kq*=lpvip")
+    r = subprocess.run([sys.executable, "-c", PRELUDE + "h.reg()"], env=e, capture_output=True, text=True,
+                       timeout=120)
+    assert r.returncode == 0 and "LNS16_SUM_POLICY with 2 rules (default sum=base)" in r.stderr, r.stderr[-500:]
+
+
 def test_monte_state_api():
     out, _ = _run("""
         L = h.lib

@@ -29,3 +29,10 @@ def test_ggml_graph_lnship16(mode):
 @pytest.mark.gpu
 def test_ggml_graph_lnship32():
     _run(["--w32"], dict(os.environ))
+
+
+@pytest.mark.gpu
+def test_ggml_graph_sum_policy():
+    # LNS16_SUM_POLICY: mixed summation modes per node (cuda/lns-cuda-context.cpp:221-269)
+    _run(["--mode", "monte", "--policy", "MUL_MAT:ffn*=lpvip,SOFT_MAX=sum32,kq-0=base,qkv-1=monte"],
+         dict(os.environ, GGML_LNS16_SUM="monte"))

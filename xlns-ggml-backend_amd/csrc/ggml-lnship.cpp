@@ -217,6 +217,48 @@ static int sum_mode() {
     return mode;
 }
 
+// LNS16_SUM_POLICY (cuda/lns-cuda-context.cpp:221-269): comma-separated
+// "selector=mode" rules, selectors as LNS_DISABLE_OPS's; the first rule that
+// matches a node sets its summation mode.  base, lpvip and sum32 are always
+// available (every mode is in this library, as the reference's
+// GGML_LNSCUDA16_MIXED build); monte only as GGML_LNS16_SUM itself, since the
+// Monte state belongs to that mode.  A malformed rule aborts.
+static const std::vector<std::pair<std::string, int>> &sum_policy() {
+    static const std::vector<std::pair<std::string, int>> rules = []() {
+        std::vector<std::pair<std::string, int>> r;
+        const char *env = std::getenv("LNS16_SUM_POLICY");
+        if (!env) return r;
+        for (const std::string &rule : split_list(env)) {
+            const size_t eq = rule.rfind('=');
+            if (eq == std::string::npos) die("LNS16_SUM_POLICY rule '%s' is not selector=mode", rule.c_str());
+            const std::string m = rule.substr(eq + 1);
+            int mode = -1;
+            if (m == "base") mode = LNSHIP_BASE;
+            else if (m == "lpvip") mode = LNSHIP_LPVIP;
+            else if (m == "sum32") mode = LNSHIP_SUM32;
+            else if (m == "monte" && sum_mode() == LNSHIP_MONTE) mode = LNSHIP_MONTE;
+            if (mode < 0)
+                die("LNS16_SUM_POLICY mode '%s' is not available (base|lpvip|sum32; monte only as GGML_LNS16_SUM)",
+                    m.c_str());
+            r.emplace_back(rule.substr(0, eq), mode);
+        }
+        std::fprintf(stderr, "ggml-lnship: LNSHIP16 LNS16_SUM_POLICY with %zu rules (default sum=%s)\n", r.size(),
+                     sum_mode() == LNSHIP_MONTE ? "monte"
+                     : sum_mode() == LNSHIP_LPVIP ? "lpvip"
+                     : sum_mode() == LNSHIP_SUM32 ? "sum32"
+                                                  : "base");
+        return r;
+    }();
+    return rules;
+}
+
+// the summation mode of one xlns16 node
+static int node_mode(const ggml_tensor *node) {
+    for (const auto &rule : sum_policy())
+        if (op_matches(node, rule.first)) return rule.second;
+    return sum_mode();
+}
+
 static const char *mode_name(int m) {
     switch (m) {
         case LNSHIP_MONTE: return "monte";
@@ -385,7 +427,7 @@ static verdict check_mul_mat(const ggml_tensor *op) {
 
 static verdict check_rms_norm(const ggml_tensor *op, bool w32) {
     verdict v = f32_result(op, {is_f32(op->src[0]), "unary_like_requires_src0_f32"});
-    if (v.ok && op->src[0]->ne[0] > lnship_max_row(w32 ? 2 : 0, sum_mode())) return {false, "lnship_row_too_long"};
+    if (v.ok && op->src[0]->ne[0] > lnship_max_row(w32 ? 2 : 0, w32 ? 0 : node_mode(op))) return {false, "lnship_row_too_long"};
     return v;
 }
 
@@ -399,7 +441,7 @@ static verdict check_soft_max(const ggml_tensor *op, bool w32) {
     if (!v.ok) return v;
     if (mask && (mask->ne[0] < op->ne[0] || mask->ne[1] < op->ne[1]))
         return {false, "lnship_soft_max_mask_smaller_than_src0"};
-    if (op->ne[0] > lnship_max_row(w32 ? 3 : 1, sum_mode())) return {false, "lnship_row_too_long"};
+    if (op->ne[0] > lnship_max_row(w32 ? 3 : 1, w32 ? 0 : node_mode(op))) return {false, "lnship_row_too_long"};
     return v;
 }
 
@@ -772,6 +814,7 @@ static format &fmt16() {
     static std::once_flag once;
     std::call_once(once, []() {
         (void)sum_mode();   // a bad GGML_LNS16_SUM fails at registration
+        (void)sum_policy();   // and so does a bad LNS16_SUM_POLICY
         make_format(f, "LNSHIP16", false, "LNSHIP16-bkend--");
     });
     return f;
@@ -898,8 +941,8 @@ const void *context::lns_matrix(const ggml_tensor *t) {
 
 // ============================================================ ops
 
-static uint16_t reserve_monte(uint64_t draws) {
-    if (sum_mode() != LNSHIP_MONTE) return 0;
+static uint16_t reserve_monte(int mode, uint64_t draws) {
+    if (mode != LNSHIP_MONTE) return 0;
     uint16_t start = 0;
     if (!ggml_backend_lnship16_monte_reserve(draws, &start)) die("Monte state unavailable");
     return start;
@@ -908,7 +951,7 @@ static uint16_t reserve_monte(uint64_t draws) {
 static void op_mul_mat(context &ctx, ggml_tensor *dst) {
     const ggml_tensor *a = dst->src[0], *b = dst->src[1];
     const bool w32 = ctx.fmt->w32;
-    const int mode = sum_mode();
+    const int mode = node_mode(dst);
     lnship_mul_mat_args args;
     std::memset(&args, 0, sizeof args);
     args.w = ctx.lns_matrix(a);
@@ -924,7 +967,8 @@ static void op_mul_mat(context &ctx, ggml_tensor *dst) {
     if (w32) {
         lib_ok(lnship32_mul_mat(&args, ctx.get_stream()), "lnship32_mul_mat");
     } else {
-        args.monte_seed = reserve_monte(lnship16_mul_mat_draws(mode, args.K, args.M, args.N, args.ne12, args.ne13));
+        args.monte_seed =
+            reserve_monte(mode, lnship16_mul_mat_draws(mode, args.K, args.M, args.N, args.ne12, args.ne13));
         lib_ok(lnship16_mul_mat(mode, &args, ctx.get_stream()), "lnship16_mul_mat");
     }
     ctx.download(args.dst, dst);
@@ -939,8 +983,8 @@ static void op_rms_norm(context &ctx, ggml_tensor *dst) {
     if (ctx.fmt->w32) {
         lib_ok(lnship32_rms_norm(x, y, nc, nr, eps, ctx.get_stream()), "lnship32_rms_norm");
     } else {
-        const int mode = sum_mode();
-        const uint16_t seed = reserve_monte(lnship16_rms_norm_draws(mode, nc, nr));
+        const int mode = node_mode(dst);
+        const uint16_t seed = reserve_monte(mode, lnship16_rms_norm_draws(mode, nc, nr));
         lib_ok(lnship16_rms_norm(mode, x, y, nc, nr, eps, seed, ctx.get_stream()), "lnship16_rms_norm");
     }
     ctx.download(y, dst);
@@ -970,8 +1014,8 @@ static void op_soft_max(context &ctx, ggml_tensor *dst) {
     if (ctx.fmt->w32) {
         lib_ok(lnship32_soft_max(&args, ctx.get_stream()), "lnship32_soft_max");
     } else {
-        const int mode = sum_mode();
-        args.monte_seed = reserve_monte(lnship16_soft_max_draws(mode, a->ne[0], nrows(a)));
+        const int mode = node_mode(dst);
+        args.monte_seed = reserve_monte(mode, lnship16_soft_max_draws(mode, a->ne[0], nrows(a)));
         lib_ok(lnship16_soft_max(mode, &args, ctx.get_stream()), "lnship16_soft_max");
     }
     // the mask staging buffers are reused by the next op only after download
