@@ -404,11 +404,13 @@ def run_ggml(args):
     llama.cpp drives the backend: host (CPU-buffer) tensors, so each call
     uploads its activations, runs the kernels and downloads the output (the
     weights are cached on the device after the first call, as the reference's
-    weight cache does).  Beside it, the same op on device-resident data
-    through the C ABI.  Wall-clock per call, averaged over --reps calls."""
+    weight cache does); then with the tensors in the backend's device buffer
+    type; beside them, the same op on device-resident data through the C ABI.
+    Median wall time of one synchronised call over --reps calls."""
     import numpy as np
     import torch
     os.environ.setdefault("GGML_LNS16_SUM", args.mode if args.mode != "all" else "sum32")
+    os.environ["GGML_LNS_HIP_BUFFERS"] = "device"   # host tensors stay host; the device leg uses the HBM type
     mode_name = os.environ["GGML_LNS16_SUM"]
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     import ggml_host as G
@@ -423,45 +425,60 @@ def run_ggml(args):
     res = []
 
     def wall(fn):
+        # median wall time of one synchronised call (a stall in one call
+        # does not move it)
         fn()
         torch.cuda.synchronize()
-        t0 = time.perf_counter()
+        ts = []
         for _ in range(reps):
+            t0 = time.perf_counter()
             fn()
-        torch.cuda.synchronize()
-        return (time.perf_counter() - t0) / reps * 1e6
+            torch.cuda.synchronize()
+            ts.append(time.perf_counter() - t0)
+        return float(np.median(ts)) * 1e6
 
     mode = lnship.MODES[mode_name]
+    hbm = h.device_buffer(64 << 20)
     for (K, M) in ((576, 1536), (1536, 576)):
         w, x = f32(M, K, scale=0.02), f32(1, K)
         W = h.tensor([K, M], data=w, weights=True, name="w")
         X = h.tensor([K, 1], data=x, name="x")
         D = h.tensor([M, 1], op="MUL_MAT", src=(W, X), name="y")
         us_b = wall(lambda: h.compute(be, [D]))
+        Xh = h.tensor([K, 1], data=x, name="x", device=hbm)
+        Dh = h.tensor([M, 1], op="MUL_MAT", src=(W, Xh), name="y", device=hbm)
+        us_h = wall(lambda: h.compute(be, [Dh]))
         wp, xd = lnship.pack16(torch.from_numpy(w).cuda()), torch.from_numpy(x).cuda()
         us_d = wall(lambda: lnship.mul_mat16(mode, wp, xd, K, M))
         res.append({"op": "mul_mat", "K": K, "M": M, "N": 1, "boundary_us": round(us_b, 2),
-                    "device_us": round(us_d, 2), "pcie_bytes": 4 * (K + M),
+                    "boundary_hbm_us": round(us_h, 2), "device_us": round(us_d, 2), "pcie_bytes": 4 * (K + M),
                     "boundary_weight_gbs": round(2 * K * M / us_b / 1e3, 3)})
     x = f32(1, 576)
     X = h.tensor([576, 1], data=x, name="x")
     D = h.tensor([576, 1], op="RMS_NORM", src=(X,), fparams={0: 1e-5}, name="n")
+    Xh = h.tensor([576, 1], data=x, name="x", device=hbm)
+    Dh = h.tensor([576, 1], op="RMS_NORM", src=(Xh,), fparams={0: 1e-5}, name="n", device=hbm)
     xd = torch.from_numpy(x).cuda()
     res.append({"op": "rms_norm", "n": 576, "rows": 1, "boundary_us": round(wall(lambda: h.compute(be, [D])), 2),
+                "boundary_hbm_us": round(wall(lambda: h.compute(be, [Dh])), 2),
                 "device_us": round(wall(lambda: lnship.rms_norm16(mode, xd, 1e-5)), 2), "pcie_bytes": 8 * 576})
     z = f32(9, 128, 128, scale=3.0)
     Z = h.tensor([128, 128, 9], data=z, name="kq")
     D = h.tensor([128, 128, 9], op="SOFT_MAX", src=(Z,), fparams={0: 0.125, 1: 0.0}, name="p")
+    Zh = h.tensor([128, 128, 9], data=z, name="kq", device=hbm)
+    Dh = h.tensor([128, 128, 9], op="SOFT_MAX", src=(Zh,), fparams={0: 0.125, 1: 0.0}, name="p", device=hbm)
     zd = torch.from_numpy(z).cuda()
     res.append({"op": "soft_max", "ne": [128, 128, 9], "boundary_us": round(wall(lambda: h.compute(be, [D])), 2),
+                "boundary_hbm_us": round(wall(lambda: h.compute(be, [Dh])), 2),
                 "device_us": round(wall(lambda: lnship.soft_max16(mode, zd, None, 0.125)), 2),
                 "pcie_bytes": 8 * z.size})
     h.free(be)
     print(json.dumps({"metric": "ggml boundary PCIe-inclusive latency per op (BASELINE config 1 shapes)",
                       "mode": mode_name, "reps": reps, "ops": res,
                       "note": "boundary_us: graph_compute wall time with host tensors (upload, kernels, download, "
-                              "sync); device_us: the same op on HBM-resident tensors through the C ABI, wall time "
-                              "with launch"}), flush=True)
+                              "sync); boundary_hbm_us: graph_compute with the tensors in the backend's device buffer "
+                              "type (GGML_LNS_HIP_BUFFERS=device); device_us: the same op on HBM-resident tensors "
+                              "through the C ABI, wall time with launch"}), flush=True)
 
 
 def lns32_weights(cfg, seed, std, torch):

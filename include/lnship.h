@@ -170,6 +170,17 @@ int lnship32_store_kv(const float *x, int64_t x_ld, const int32_t *pos, int64_t 
                       int64_t cache_slice, int cache_transposed, const int32_t *seq, int64_t seq_stride,
                       void *stream);
 
+/* ggml views on the device (tensors in the ggml device buffer type): the
+ * elements of a 4-D strided view (byte strides nb, as ggml_tensor::nb)
+ * gathered into a contiguous F32 array in ggml element order, from F32
+ * (src_type 0) or IEEE half (1); and scattered back from one.  No
+ * counterpart in the reference, whose backends see host buffers only
+ * (common/lns-backend-framework.h:279-281); they replace its host-side
+ * row gathers (cuda/lns-cuda-context.cpp:156-210) for device tensors. */
+int lnship_gather_f32(const void *src, int src_type, const int64_t ne[4], const int64_t nb[4], float *dst,
+                      void *stream);
+int lnship_scatter_f32(const float *src, void *dst, const int64_t ne[4], const int64_t nb[4], void *stream);
+
 /* Host: the (cos, sin) floats lns_rope uses for positions 0..n_pos-1 (the
  * float recurrence t *= powf(freq_base, -2/n_dims) per pair, cosf / sinf;
  * src/lns-ops.cpp:1225-1247, cuda/lns-cuda-ops.cpp:223-240), laid out as

@@ -16,7 +16,11 @@ With --policy the backend runs under LNS16_SUM_POLICY and the oracle takes
 each node's summation mode from the same rules (op names, "OP:glob" on the
 node name, or a glob).
 
-Usage: python ggml_graph_check.py --mode base|monte|lpvip|sum32 [--policy RULES] [--w32]
+With --device-buffers (GGML_LNS_HIP_BUFFERS=device) the inputs, the KV
+cache, the F32 / F16 weights and every node live in the backend's device
+buffers, and results are read back through the buffer interface.
+
+Usage: python ggml_graph_check.py --mode base|monte|lpvip|sum32 [--policy RULES] [--device-buffers] [--w32]
 Exit status 0 when every node matches.
 """
 import argparse
@@ -95,11 +99,19 @@ def policy_modes(policy, default):
     return mode_of
 
 
-def run16(mode_name, policy=None):
+def run16(mode_name, policy=None, dev=False):
     m = O.MODES[mode_name]
     mode_of = policy_modes(policy, m)
     L = oracle_fns()
     h = G.Host()
+    # with dev, activations, caches and F32 / F16 weights live in the
+    # backend's device buffers (weights in one of WEIGHTS usage, so the
+    # weight cache sees them); the Q8_0 weight stays in host memory
+    act = h.device_buffer(64 << 20) if dev else None
+    wts = h.device_buffer(16 << 20) if dev else None
+    if dev:
+        h.stub.ggml_host_set_usage.argtypes = [ctypes.c_void_p, ctypes.c_int]
+        h.stub.ggml_host_set_usage(wts.addr, G.USAGE_WEIGHTS)
     rng = np.random.default_rng(1234)
     f32 = lambda *s, scale=1.0, loc=0.0: (rng.standard_normal(s) * scale + loc).astype(np.float32)
     T, E, H, HKV, D, NKV = 3, 576, 9, 3, 64, 256
@@ -117,17 +129,18 @@ def run16(mode_name, policy=None):
     w2 = (rng.standard_normal((E, 1536)) * 0.02).astype(np.float16)
     z = f32(2, 5, 100, scale=3.0)
 
-    t = h.tensor
+    t = lambda *a, **k: h.tensor(*a, device=None if k.get("weights") else act, **k)
+    tw = lambda *a, **k: h.tensor(*a, device=wts, **k)
     X0 = t([E, T], data=x0, name="inp")
-    Gw = t([E], data=g, weights=True, name="blk.0.attn_norm.weight")
-    WQKV = t([E, E + 2 * HKV * D], data=wqkv, weights=True, name="blk.0.attn_qkv.weight")
+    Gw = tw([E], data=g, weights=True, name="blk.0.attn_norm.weight")
+    WQKV = tw([E, E + 2 * HKV * D], data=wqkv, weights=True, name="blk.0.attn_qkv.weight")
     KC = t([D, NKV, HKV], "f16", data=kc, name="cache_k_l0")
     POS = t([T], "i32", data=pos, name="inp_pos")
     MASK = t([NKV, 4], data=mask, name="kq_mask")
-    WQ8 = t([E, 256], "q8_0", data=wq8_raw, weights=True, name="blk.0.ffn_up.weight")
+    WQ8 = h.tensor([E, 256], "q8_0", data=wq8_raw, weights=True, name="blk.0.ffn_up.weight")
     BIAS = t([1, T], data=bias, name="bias")
     X1 = t([1536, T], data=x1, name="ffn_inp")
-    W2 = t([1536, E], "f16", data=w2, weights=True, name="blk.0.ffn_down.weight")
+    W2 = tw([1536, E], "f16", data=w2, weights=True, name="blk.0.ffn_down.weight")
     Z = t([100, 5, 2], data=z, name="scores")
     swi = h.stub.ggml_host_glu(b"SWIGLU")
 
@@ -194,7 +207,7 @@ def run16(mode_name, policy=None):
 
     report = {}
     for k, tn in nodes.items():
-        got = h.f32_of(tn).reshape(want[k].shape)
+        got = h.f32_of(tn, act).reshape(want[k].shape)
         bad = int(np.count_nonzero(got.view(np.uint32) != want[k].view(np.uint32)))
         report[k] = bad
     if O.MODES[mode_name] == O.MODES["monte"]:
@@ -202,41 +215,62 @@ def run16(mode_name, policy=None):
         h.lib.ggml_backend_lnship16_monte_get_state(ctypes.byref(s))
         report["monte_state_matches"] = int(s.value == O.monte_get())
     h.free(be)
-    print(json.dumps({"mode": mode_name, "mismatches": report}), flush=True)
+    print(json.dumps({"mode": mode_name, "device_buffers": dev, "mismatches": report}), flush=True)
     ok = all(v == 0 for k, v in report.items() if k != "monte_state_matches")
     return 0 if ok and report.get("monte_state_matches", 1) == 1 else 1
 
 
-def run32():
+def run32(dev=False):
     h = G.Host()
     rng = np.random.default_rng(99)
     f32 = lambda *s, scale=1.0: (rng.standard_normal(s) * scale).astype(np.float32)
-    T, K, M = 2, 2048, 512
+    T, K, M, D, H = 2, 2048, 512, 64, 4
     x = f32(T, K)
+    g = f32(K, scale=0.1) + 1.0
     w = f32(M, K, scale=0.02)
     kq = f32(4, T, 200, scale=3.0)
     mask = np.zeros((T, 200), np.float32)
     mask[0, 150:] = -np.inf
-    t = h.tensor
+    res = f32(T, M)
+    qk = f32(T, H, D)
+    pos = np.array([7, 300], np.int32)
+    act = h.device_buffer(32 << 20, w32=True) if dev else None
+    t = lambda *a, **k: h.tensor(*a, device=act, **k)
     X = t([K, T], data=x, name="inp")
+    Gw = t([K], data=g, name="blk.0.attn_norm.weight")
     W = t([K, M], data=w, weights=True, name="blk.0.ffn_up.weight")
     KQ = t([200, T, 4], data=kq, name="kq")
     MASK = t([200, T], data=mask, name="kq_mask")
-    nodes = {"rms": t([K, T], op="RMS_NORM", src=(X,), fparams={0: 1e-6}, name="norm-0"),
-             "mm": t([M, T], op="MUL_MAT", src=(W, X), name="ffn_up-0"),
-             "softmax": t([200, T, 4], op="SOFT_MAX", src=(KQ, MASK), fparams={0: 0.125, 1: 0.0}, name="sm-0")}
+    RES = t([M, T], data=res, name="res")
+    QK = t([D, H, T], data=qk, name="q")
+    POS = t([T], "i32", data=pos, name="inp_pos")
+    swi = h.stub.ggml_host_glu(b"SWIGLU")
+    nodes = {"rms": t([K, T], op="RMS_NORM", src=(X,), fparams={0: 1e-6}, name="norm-0")}
+    nodes["mul"] = t([K, T], op="MUL", src=(nodes["rms"], Gw), name="attn_norm-0")
+    nodes["mm"] = t([M, T], op="MUL_MAT", src=(W, nodes["mul"]), name="ffn_up-0")
+    nodes["add"] = t([M, T], op="ADD", src=(nodes["mm"], RES), name="ffn_out-0")
+    nodes["swiglu"] = t([M // 2, T], op="GLU", src=(nodes["add"],), params=(swi, 0), name="ffn_swiglu-0")
+    nodes["rope"] = t([D, H, T], op="ROPE", src=(QK, POS), params=(0, D, 0),
+                      fparams={5: 10000.0, 6: 1.0, 7: 0.0, 8: 1.0}, name="Qcur-0")
+    nodes["softmax"] = t([200, T, 4], op="SOFT_MAX", src=(KQ, MASK), fparams={0: 0.125, 1: 0.0}, name="sm-0")
     be = h.init(w32=True)
     if be is None:
         print(json.dumps({"error": "no GPU: LNSHIP32 init returned NULL"}))
         return 1
     assert h.compute(be, list(nodes.values())) == 0
-    want = {"rms": O.rms_norm32(x, 1e-6), "mm": O.mul_mat32(w, x), "softmax": O.soft_max32(kq, mask, 0.125)}
+    want = {"rms": O.rms_norm32(x, 1e-6)}
+    want["mul"] = O.mul32(want["rms"], g)
+    want["mm"] = O.mul_mat32(w, want["mul"])
+    want["add"] = O.add32(want["mm"], res)
+    want["swiglu"] = O.swiglu32(want["add"][:, :M // 2], want["add"][:, M // 2:])
+    want["rope"] = O.rope32(qk, pos, D, 0, 10000.0)
+    want["softmax"] = O.soft_max32(kq, mask, 0.125)
     report = {}
     for k, tn in nodes.items():
-        got = h.f32_of(tn).reshape(want[k].shape)
+        got = h.f32_of(tn, act).reshape(want[k].shape)
         report[k] = int(np.count_nonzero(got.view(np.uint32) != want[k].view(np.uint32)))
     h.free(be)
-    print(json.dumps({"mode": "lns32", "mismatches": report}), flush=True)
+    print(json.dumps({"mode": "lns32", "device_buffers": dev, "mismatches": report}), flush=True)
     return 0 if all(v == 0 for v in report.values()) else 1
 
 
@@ -245,7 +279,10 @@ if __name__ == "__main__":
     ap.add_argument("--mode", default="base")
     ap.add_argument("--w32", action="store_true")
     ap.add_argument("--policy", default=None)
+    ap.add_argument("--device-buffers", action="store_true")
     a = ap.parse_args()
     if a.policy is not None:
         os.environ["LNS16_SUM_POLICY"] = a.policy
-    sys.exit(run32() if a.w32 else run16(a.mode, a.policy))
+    if a.device_buffers:
+        os.environ["GGML_LNS_HIP_BUFFERS"] = "device"
+    sys.exit(run32(a.device_buffers) if a.w32 else run16(a.mode, a.policy, a.device_buffers))

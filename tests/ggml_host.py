@@ -92,6 +92,56 @@ class DevProps(ctypes.Structure):
                 ("caps", DevCaps)]
 
 
+class BufferTypeI(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_void_p) for n in ("get_name", "alloc_buffer", "get_alignment", "get_max_size",
+                                               "get_alloc_size", "is_host")]
+
+
+class BufferType(ctypes.Structure):
+    _fields_ = [("iface", BufferTypeI), ("device", ctypes.c_void_p), ("context", ctypes.c_void_p)]
+
+
+class BufferI(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_void_p) for n in ("free_buffer", "get_base", "init_tensor", "memset_tensor",
+                                               "set_tensor", "get_tensor", "cpy_tensor", "clear", "reset")]
+
+
+class Buffer(ctypes.Structure):
+    _fields_ = [("iface", BufferI), ("buft", ctypes.c_void_p), ("context", ctypes.c_void_p),
+                ("size", ctypes.c_size_t), ("usage", ctypes.c_int)]
+
+
+class DeviceBuffer:
+    """A buffer of the backend's device buffer type, handed out by a bump
+    allocator (256-byte aligned, as the type asks)."""
+
+    def __init__(self, host, addr):
+        self.host, self.addr = host, addr
+        self.buf = ctypes.cast(addr, ctypes.POINTER(Buffer)).contents
+        self.base = call(self.buf.iface.get_base, ctypes.c_void_p, (addr, ctypes.c_void_p))
+        self.used = 0
+
+    def alloc(self, nbytes):
+        off = (self.used + 255) // 256 * 256
+        assert off + nbytes <= self.buf.size, "device buffer too small"
+        self.used = off + nbytes
+        return self.base + off
+
+    def set(self, t, arr):
+        a = np.ascontiguousarray(arr)
+        call(self.buf.iface.set_tensor, None, (self.addr, ctypes.c_void_p), (ctypes.addressof(t), ctypes.c_void_p),
+             (a.ctypes.data, ctypes.c_void_p), (0, ctypes.c_size_t), (a.nbytes, ctypes.c_size_t))
+
+    def get(self, t, nbytes):
+        out = np.empty(nbytes, np.uint8)
+        call(self.buf.iface.get_tensor, None, (self.addr, ctypes.c_void_p), (ctypes.addressof(t), ctypes.c_void_p),
+             (out.ctypes.data, ctypes.c_void_p), (0, ctypes.c_size_t), (nbytes, ctypes.c_size_t))
+        return out
+
+    def free(self):
+        call(self.buf.iface.free_buffer, None, (self.addr, ctypes.c_void_p))
+
+
 def call(addr, restype, *args_and_types):
     """Calls a vtable slot: call(addr, restype, (value, ctype), ...)."""
     fn = ctypes.CFUNCTYPE(restype, *[t for _, t in args_and_types])(addr)
@@ -133,9 +183,11 @@ class Host:
 
     # ---- tensors ----
     def tensor(self, ne, type_name="f32", data=None, nb=None, op="NONE", src=(), params=(), fparams=None,
-               name="", weights=False):
-        """A host tensor.  data: a numpy array (kept alive) or an address;
-        nb defaults to the contiguous strides of ggml."""
+               name="", weights=False, device=None):
+        """A host tensor, or with device (a DeviceBuffer) one in device
+        memory.  data: a numpy array (kept alive; copied in for a device
+        tensor) or an address (a view's); nb defaults to the contiguous
+        strides of ggml."""
         tid, tsize, blck = TYPES[type_name]
         ne = list(ne) + [1] * (4 - len(ne))
         t = Tensor()
@@ -153,6 +205,18 @@ class Host:
             t.op_params[i] = int(np.array([f], np.float32).view(np.int32)[0])
         for i, sct in enumerate(src):
             t.src[i] = ctypes.addressof(sct) if sct is not None else None
+        t.name = name.encode()
+        if device is not None:
+            t.buffer = device.addr
+            if isinstance(data, int):
+                t.data = data
+            else:
+                t.data = device.alloc(max(nb[3] * ne[3], 4))
+                if data is not None:
+                    device.set(t, data)
+            t.flags = FLAG_COMPUTE if op not in ("NONE",) else 0
+            self.keep.append(t)
+            return t
         if data is None:
             nbytes = nb[3] * ne[3]
             data = np.zeros(max(nbytes, 4) // 4 + 1, np.float32)
@@ -161,15 +225,28 @@ class Host:
             t.data = data.ctypes.data
         else:
             t.data = data
-        t.name = name.encode()
         t.buffer = self.weights_buf if weights else self.compute_buf
         t.flags = FLAG_COMPUTE if op not in ("NONE",) else 0
         self.keep.append(t)
         return t
 
-    def f32_of(self, t):
-        """Contiguous F32 view of an F32 tensor's data."""
+    def device_buffer(self, size, w32=False):
+        """A buffer of the device's default buffer type (the HBM type when
+        GGML_LNS_HIP_BUFFERS=device)."""
+        d = self.device(w32)
+        buft = call(d.iface.get_buffer_type, ctypes.c_void_p, (ctypes.addressof(d), ctypes.c_void_p))
+        bt = ctypes.cast(buft, ctypes.POINTER(BufferType)).contents
+        addr = call(bt.iface.alloc_buffer, ctypes.c_void_p, (buft, ctypes.c_void_p), (size, ctypes.c_size_t))
+        assert addr, "alloc_buffer failed"
+        db = DeviceBuffer(self, addr)
+        self.keep.append(db)
+        return db
+
+    def f32_of(self, t, device=None):
+        """Contiguous F32 copy or view of an F32 tensor's data."""
         n = t.ne[0] * t.ne[1] * t.ne[2] * t.ne[3]
+        if device is not None:
+            return device.get(t, n * 4).view(np.float32).reshape(t.ne[3], t.ne[2], t.ne[1], t.ne[0])
         return np.ctypeslib.as_array((ctypes.c_float * n).from_address(t.data)).reshape(
             t.ne[3], t.ne[2], t.ne[1], t.ne[0])
 

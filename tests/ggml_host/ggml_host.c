@@ -108,37 +108,52 @@ const char *ggml_type_name(enum ggml_type t) { return ggml_get_type_traits(t)->t
 size_t ggml_type_size(enum ggml_type t) { return ggml_get_type_traits(t)->type_size; }
 int64_t ggml_blck_size(enum ggml_type t) { return ggml_get_type_traits(t)->blck_size; }
 
-/* ---- host buffers ------------------------------------------------------ */
-struct ggml_backend_buffer {
-    int usage;
-    void *base;
-    size_t size;
-};
-struct ggml_backend_buffer_type {
-    int tag;
-};
-static struct ggml_backend_buffer_type k_cpu_buft = {1};
+/* ---- buffers (the layouts of ggml_abi.h) ------------------------------ */
+static struct ggml_backend_buffer_type k_cpu_buft; /* iface unused: is_host answers by identity */
 
 ggml_backend_buffer_type_t ggml_backend_cpu_buffer_type(void) { return &k_cpu_buft; }
 bool ggml_backend_buft_is_host(ggml_backend_buffer_type_t b) { return b == &k_cpu_buft; }
 
-ggml_backend_buffer_t ggml_backend_cpu_buffer_from_ptr(void *ptr, size_t size) {
+ggml_backend_buffer_t ggml_backend_buffer_init(ggml_backend_buffer_type_t buft, struct ggml_backend_buffer_i iface,
+                                               void *context, size_t size) {
     struct ggml_backend_buffer *b = (struct ggml_backend_buffer *)calloc(1, sizeof *b);
-    b->base = ptr;
+    b->iface = iface;
+    b->buft = buft;
+    b->context = context;
     b->size = size;
+    b->usage = GGML_BACKEND_BUFFER_USAGE_ANY;
     return b;
 }
 
-enum ggml_backend_buffer_usage ggml_backend_buffer_get_usage(ggml_backend_buffer_t b) {
-    return (enum ggml_backend_buffer_usage)b->usage;
+ggml_backend_buffer_t ggml_backend_cpu_buffer_from_ptr(void *ptr, size_t size) {
+    struct ggml_backend_buffer_i none;
+    memset(&none, 0, sizeof none);
+    (void)ptr;
+    return ggml_backend_buffer_init(&k_cpu_buft, none, NULL, size);
 }
 
-/* a buffer handle with the given usage (0 any, 1 weights, 2 compute) */
+enum ggml_backend_buffer_usage ggml_backend_buffer_get_usage(ggml_backend_buffer_t b) { return b->usage; }
+ggml_backend_buffer_type_t ggml_backend_buffer_get_type(ggml_backend_buffer_t b) { return b->buft; }
+
+/* ggml.c's ggml_nbytes */
+size_t ggml_nbytes(const struct ggml_tensor *t) {
+    for (int i = 0; i < GGML_MAX_DIMS; i++)
+        if (t->ne[i] <= 0) return 0;
+    const size_t blck = (size_t)ggml_blck_size(t->type);
+    size_t n = blck == 1 ? ggml_type_size(t->type) : (size_t)t->ne[0] * t->nb[0] / blck;
+    for (int i = blck == 1 ? 0 : 1; i < GGML_MAX_DIMS; i++) n += (size_t)(t->ne[i] - 1) * t->nb[i];
+    return n;
+}
+
+/* a host buffer handle with the given usage (0 any, 1 weights, 2 compute) */
 ggml_backend_buffer_t ggml_host_buffer(int usage) {
-    struct ggml_backend_buffer *b = (struct ggml_backend_buffer *)calloc(1, sizeof *b);
-    b->usage = usage;
+    ggml_backend_buffer_t b = ggml_backend_cpu_buffer_from_ptr(NULL, 0);
+    b->usage = (enum ggml_backend_buffer_usage)usage;
     return b;
 }
+
+/* set a buffer's usage (ggml_backend_buffer_set_usage) */
+void ggml_host_set_usage(ggml_backend_buffer_t b, int usage) { b->usage = (enum ggml_backend_buffer_usage)usage; }
 
 size_t ggml_host_sizeof_tensor(void) { return sizeof(struct ggml_tensor); }
 size_t ggml_host_offsetof_data(void) { return offsetof(struct ggml_tensor, data); }

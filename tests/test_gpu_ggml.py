@@ -36,3 +36,16 @@ def test_ggml_graph_sum_policy():
     # LNS16_SUM_POLICY: mixed summation modes per node (cuda/lns-cuda-context.cpp:221-269)
     _run(["--mode", "monte", "--policy", "MUL_MAT:ffn*=lpvip,SOFT_MAX=sum32,kq-0=base,qkv-1=monte"],
          dict(os.environ, GGML_LNS16_SUM="monte"))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("mode", ["sum32", "monte"])
+def test_ggml_graph_device_buffers(mode):
+    # GGML_LNS_HIP_BUFFERS=device: tensors in the backend's HBM buffer type,
+    # read and written in place
+    _run(["--mode", mode, "--device-buffers"], dict(os.environ, GGML_LNS16_SUM=mode))
+
+
+@pytest.mark.gpu
+def test_ggml_graph_lnship32_device_buffers():
+    _run(["--w32", "--device-buffers"], dict(os.environ))

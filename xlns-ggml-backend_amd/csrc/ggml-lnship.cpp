@@ -384,6 +384,8 @@ static void scatter_f32(const float *in, ggml_tensor *t) {
 
 // ============================================================ op predicates
 
+static bool on_device(const ggml_tensor *t);
+
 enum class kind { view, mul_mat, rms_norm, soft_max, add, mul, swiglu, rope, unary, glu, other };
 
 static kind classify(const ggml_tensor *t) {
@@ -417,6 +419,7 @@ static verdict f32_result(const ggml_tensor *op, verdict v) {
 static verdict check_mul_mat(const ggml_tensor *op) {
     const ggml_tensor *a = op->src[0], *b = op->src[1];
     if (!is_f32(b) || !to_f32_possible(a)) return {false, "mul_mat_requires_src1_f32_and_convertible_src0"};
+    if (on_device(a) && !is_f32(a) && !is_f16(a)) return {false, "lnship_device_src0_requires_f32_or_f16"};
     if (!rows_contiguous(a) || !rows_contiguous(b)) return {false, "mul_mat_requires_contiguous_rows"};
     if (!is_f32(op)) return {false, "lnship_mul_mat_requires_f32_dst"};
     if ((b->ne[1] + 3) / 4 > 65535 || b->ne[2] * b->ne[3] > 65535) return {false, "lnship_mul_mat_grid_too_large"};
@@ -496,9 +499,9 @@ static verdict check_node(const ggml_tensor *op, bool w32) {
         case kind::rms_norm: return check_rms_norm(op, w32);
         case kind::soft_max: return check_soft_max(op, w32);
         case kind::add:
-        case kind::mul: return w32 ? verdict{false, "unsupported_op"} : check_binary(op);
-        case kind::swiglu: return w32 ? verdict{false, "unsupported_glu_op"} : check_swiglu(op);
-        case kind::rope: return w32 ? verdict{false, "unsupported_op"} : check_rope(op);
+        case kind::mul: return check_binary(op);
+        case kind::swiglu: return check_swiglu(op);
+        case kind::rope: return check_rope(op);
         case kind::unary: return {false, "unsupported_unary_op"};
         case kind::glu: return {false, "unsupported_glu_op"};
         default: return {false, "unsupported_op"};
@@ -621,12 +624,22 @@ struct context {
     std::map<weight_key, dev_buffer> weights;
     size_t budget = 0, cached = 0;
     bool full_reported = false;
+    bool staging_busy = false;   // an async copy may still read the pinned staging buffers
 
     explicit context(const format *f) : fmt(f) {}
     ~context();
     hipStream_t get_stream();
     float *dev_f32(role r, int64_t n) { return (float *)dev[r].grow((size_t)std::max<int64_t>(n, 1) * 4); }
+    // pinned staging for host-side gathers, free of in-flight copies
+    void *staging(role r, size_t bytes) {
+        if (staging_busy) {
+            hip_ok(hipStreamSynchronize(get_stream()), "hipStreamSynchronize");
+            staging_busy = false;
+        }
+        return host[r].grow(bytes);
+    }
     const float *upload(const ggml_tensor *t, role r);
+    float *out_f32(ggml_tensor *t, role r);
     const void *upload_raw(const void *host, size_t bytes, role r);
     void download(const float *src, ggml_tensor *t);
     const void *lns_matrix(const ggml_tensor *t);
@@ -641,6 +654,8 @@ struct format {
     ggml_guid guid;
     ggml_backend_reg reg;
     ggml_backend_device dev;
+    ggml_backend_buffer_type buft;   // the device buffer type (HBM)
+    std::string buft_name;
 };
 
 static format &fmt16();
@@ -669,6 +684,120 @@ static const char *audit_extra(const format *f) {
     return f->w32 ? "" : e.c_str();
 }
 
+// ---- the device buffer type
+// Tensors in HBM.  GGML_LNS_HIP_BUFFERS=device makes it each device's default
+// buffer type, so ggml allocates the tensors of the nodes these backends run
+// in device memory and the ops read and write them in place; unset (or
+// "host") keeps the reference's CPU buffer type (common/lns-backend-
+// framework.h:279-281), where every op uploads its inputs and downloads its
+// output.  Transfers are synchronous; graph_compute has finished its work on
+// the GPU when it returns.
+
+struct dev_buf {
+    void *base;
+    size_t size;
+    int device;
+};
+
+static bool is_lnship_buft(ggml_backend_buffer_type_t b) { return b == &fmt16().buft || b == &fmt32().buft; }
+
+// the tensor's data lives in one of these buffers (views share their
+// source's buffer)
+static bool on_device(const ggml_tensor *t) {
+    ggml_backend_buffer_t b = t->buffer ? t->buffer : (t->view_src ? t->view_src->buffer : nullptr);
+    return b && is_lnship_buft(ggml_backend_buffer_get_type(b));
+}
+
+static dev_buf *dbuf(ggml_backend_buffer_t b) { return static_cast<dev_buf *>(b->context); }
+
+static void dbuf_free(ggml_backend_buffer_t b) {
+    dev_buf *c = dbuf(b);
+    if (c->base) {
+        (void)hipSetDevice(c->device);
+        (void)hipFree(c->base);
+    }
+    delete c;
+}
+static void *dbuf_base(ggml_backend_buffer_t b) { return dbuf(b)->base; }
+static void dbuf_memset(ggml_backend_buffer_t b, ggml_tensor *t, uint8_t v, size_t off, size_t n) {
+    hip_ok(hipSetDevice(dbuf(b)->device), "hipSetDevice");
+    hip_ok(hipMemset((char *)t->data + off, v, n), "hipMemset");
+}
+static void dbuf_set(ggml_backend_buffer_t b, ggml_tensor *t, const void *data, size_t off, size_t n) {
+    hip_ok(hipSetDevice(dbuf(b)->device), "hipSetDevice");
+    hip_ok(hipMemcpy((char *)t->data + off, data, n, hipMemcpyHostToDevice), "hipMemcpy H2D");
+}
+static void dbuf_get(ggml_backend_buffer_t b, const ggml_tensor *t, void *data, size_t off, size_t n) {
+    hip_ok(hipSetDevice(dbuf(b)->device), "hipSetDevice");
+    hip_ok(hipMemcpy(data, (const char *)t->data + off, n, hipMemcpyDeviceToHost), "hipMemcpy D2H");
+}
+// dst is in this buffer; src in another device buffer or in host memory
+static bool dbuf_cpy(ggml_backend_buffer_t b, const ggml_tensor *src, ggml_tensor *dst) {
+    if (!src->buffer) return false;
+    ggml_backend_buffer_type_t st = ggml_backend_buffer_get_type(src->buffer);
+    hipMemcpyKind kind;
+    if (is_lnship_buft(st)) kind = hipMemcpyDeviceToDevice;
+    else if (ggml_backend_buft_is_host(st)) kind = hipMemcpyHostToDevice;
+    else return false;
+    hip_ok(hipSetDevice(dbuf(b)->device), "hipSetDevice");
+    hip_ok(hipMemcpy(dst->data, src->data, ggml_nbytes(src), kind), "hipMemcpy");
+    return true;
+}
+static void dbuf_clear(ggml_backend_buffer_t b, uint8_t v) {
+    hip_ok(hipSetDevice(dbuf(b)->device), "hipSetDevice");
+    hip_ok(hipMemset(dbuf(b)->base, v, dbuf(b)->size), "hipMemset");
+}
+
+static ggml_backend_buffer_i dbuf_slots() {
+    ggml_backend_buffer_i s;
+    std::memset(&s, 0, sizeof s);
+    s.free_buffer = dbuf_free;
+    s.get_base = dbuf_base;
+    s.memset_tensor = dbuf_memset;
+    s.set_tensor = dbuf_set;
+    s.get_tensor = dbuf_get;
+    s.cpy_tensor = dbuf_cpy;
+    s.clear = dbuf_clear;
+    return s;
+}
+
+static const char *dbuft_name(ggml_backend_buffer_type_t t) {
+    return static_cast<format *>(t->context)->buft_name.c_str();
+}
+static ggml_backend_buffer_t dbuft_alloc(ggml_backend_buffer_type_t t, size_t size) {
+    const int dev = hip_device();
+    if (dev < 0) return nullptr;
+    hip_ok(hipSetDevice(dev), "hipSetDevice");
+    void *p = nullptr;
+    if (hipMalloc(&p, std::max<size_t>(size, 256)) != hipSuccess) {
+        (void)hipGetLastError();
+        return nullptr;
+    }
+    return ggml_backend_buffer_init(t, dbuf_slots(), new dev_buf{p, size, dev}, size);
+}
+static size_t dbuft_alignment(ggml_backend_buffer_type_t) { return 256; }
+static bool dbuft_is_host(ggml_backend_buffer_type_t) { return false; }
+
+static ggml_backend_buffer_type_i dbuft_slots() {
+    ggml_backend_buffer_type_i s;
+    std::memset(&s, 0, sizeof s);
+    s.get_name = dbuft_name;
+    s.alloc_buffer = dbuft_alloc;
+    s.get_alignment = dbuft_alignment;
+    s.is_host = dbuft_is_host;
+    return s;
+}
+
+static bool device_buffers() {
+    static const bool on = []() {
+        const char *v = std::getenv("GGML_LNS_HIP_BUFFERS");
+        if (!v || !v[0] || !std::strcmp(v, "host")) return false;
+        if (!std::strcmp(v, "device")) return true;
+        die("GGML_LNS_HIP_BUFFERS must be host or device (got '%s')", v);
+    }();
+    return on;
+}
+
 // ---- backend slots
 
 static const char *backend_name(ggml_backend_t b) { return static_cast<context *>(b->context)->fmt->name; }
@@ -688,6 +817,8 @@ static ggml_status backend_graph_compute(ggml_backend_t b, ggml_cgraph *g) {
         if (classify(node) == kind::view || nelements(node) == 0) continue;
         run_node(ctx, node);
     }
+    // results in device buffers are complete before ggml reads or copies them
+    if (ctx.stream) hip_ok(hipStreamSynchronize(ctx.get_stream()), "hipStreamSynchronize");
     return GGML_STATUS_SUCCESS;
 }
 
@@ -742,7 +873,9 @@ static void dev_props(ggml_backend_dev_t d, ggml_backend_dev_props *p) {
 }
 
 static ggml_backend_t dev_init(ggml_backend_dev_t d, const char *) { return init_backend(fmt_of(d)); }
-static ggml_backend_buffer_type_t dev_buft(ggml_backend_dev_t) { return ggml_backend_cpu_buffer_type(); }
+static ggml_backend_buffer_type_t dev_buft(ggml_backend_dev_t d) {
+    return device_buffers() ? &fmt_of(d)->buft : ggml_backend_cpu_buffer_type();
+}
 static ggml_backend_buffer_t dev_from_host_ptr(ggml_backend_dev_t, void *ptr, size_t size, size_t) {
     return ggml_backend_cpu_buffer_from_ptr(ptr, size);
 }
@@ -759,7 +892,7 @@ static bool dev_supports_op(ggml_backend_dev_t d, const ggml_tensor *op) {
 }
 
 static bool dev_supports_buft(ggml_backend_dev_t, ggml_backend_buffer_type_t buft) {
-    return ggml_backend_buft_is_host(buft);
+    return is_lnship_buft(buft) || ggml_backend_buft_is_host(buft);
 }
 
 static ggml_backend_device_i device_slots() {
@@ -807,6 +940,10 @@ static void make_format(format &f, const char *name, bool w32, const char guid_t
     f.dev.iface = device_slots();
     f.dev.reg = &f.reg;
     f.dev.context = &f;
+    f.buft_name = std::string(name) + "_HBM";
+    f.buft.iface = dbuft_slots();
+    f.buft.device = &f.dev;
+    f.buft.context = &f;
 }
 
 static format &fmt16() {
@@ -866,30 +1003,70 @@ const void *context::upload_raw(const void *h, size_t bytes, role r) {
     hipStream_t s = get_stream();
     void *d = dev[r].grow(bytes);
     hip_ok(hipMemcpyAsync(d, h, bytes, hipMemcpyHostToDevice, s), "hipMemcpyAsync H2D");
+    staging_busy = true;
     return d;
+}
+
+static void view_of(const ggml_tensor *t, int64_t ne[4], int64_t nb[4]) {
+    for (int d = 0; d < 4; d++) {
+        ne[d] = t->ne[d];
+        nb[d] = (int64_t)t->nb[d];
+    }
 }
 
 const float *context::upload(const ggml_tensor *t, role r) {
     const int64_t n = nelements(t);
+    if (on_device(t)) {
+        if (is_f32(t) && contiguous(t)) return (const float *)t->data;
+        if (!is_f32(t) && !is_f16(t))
+            die("%s: %s tensor '%s' in device memory cannot be read as F32", fmt->name, ggml_type_name(t->type),
+                t->name);
+        float *d = dev_f32(r, n);
+        int64_t ne[4], nb[4];
+        view_of(t, ne, nb);
+        lib_ok(lnship_gather_f32(t->data, is_f16(t) ? 1 : 0, ne, nb, d, get_stream()), "lnship_gather_f32");
+        return d;
+    }
     if (is_f32(t) && contiguous(t)) return (const float *)upload_raw(t->data, (size_t)n * 4, r);
-    float *h = (float *)host[r].grow((size_t)n * 4);
+    float *h = (float *)staging(r, (size_t)n * 4);
     gather_f32(t, h);
     return (const float *)upload_raw(h, (size_t)n * 4, r);
 }
 
-// The result is in t before this returns: the next node, on any backend,
-// may read it.
+// Where an op writes t: t's own memory when it is a contiguous F32 tensor in
+// a device buffer, else scratch that download() moves into t.
+float *context::out_f32(ggml_tensor *t, role r) {
+    if (on_device(t) && is_f32(t) && contiguous(t)) return (float *)t->data;
+    return dev_f32(r, nelements(t));
+}
+
+// A host tensor holds the result before this returns (the next node, on
+// any backend, may read it); a device tensor once the graph's stream has
+// finished, which graph_compute waits for.
 void context::download(const float *src, ggml_tensor *t) {
     hipStream_t s = get_stream();
     const int64_t n = nelements(t);
+    if (on_device(t)) {
+        if (src == t->data) return;
+        if (contiguous(t)) {
+            hip_ok(hipMemcpyAsync(t->data, src, (size_t)n * 4, hipMemcpyDeviceToDevice, s), "hipMemcpyAsync D2D");
+        } else {
+            int64_t ne[4], nb[4];
+            view_of(t, ne, nb);
+            lib_ok(lnship_scatter_f32(src, t->data, ne, nb, s), "lnship_scatter_f32");
+        }
+        return;
+    }
     if (contiguous(t)) {
         hip_ok(hipMemcpyAsync(t->data, src, (size_t)n * 4, hipMemcpyDeviceToHost, s), "hipMemcpyAsync D2H");
         hip_ok(hipStreamSynchronize(s), "hipStreamSynchronize");
+        staging_busy = false;
         return;
     }
-    float *h = (float *)host[R_DST].grow((size_t)n * 4);
+    float *h = (float *)staging(R_DST, (size_t)n * 4);
     hip_ok(hipMemcpyAsync(h, src, (size_t)n * 4, hipMemcpyDeviceToHost, s), "hipMemcpyAsync D2H");
     hip_ok(hipStreamSynchronize(s), "hipStreamSynchronize");
+    staging_busy = false;
     scatter_f32(h, t);
 }
 
@@ -902,7 +1079,7 @@ void context::pack(const ggml_tensor *t, void *dst) {
     int src_f16 = 0;
     if ((is_f32(t) || is_f16(t)) && contiguous(t)) {
         src_f16 = is_f16(t);
-        src = upload_raw(t->data, (size_t)n * ggml_type_size(t->type), R_SRC0);
+        src = on_device(t) ? t->data : upload_raw(t->data, (size_t)n * ggml_type_size(t->type), R_SRC0);
     } else {
         src = upload(t, R_SRC0);
     }
@@ -956,7 +1133,7 @@ static void op_mul_mat(context &ctx, ggml_tensor *dst) {
     std::memset(&args, 0, sizeof args);
     args.w = ctx.lns_matrix(a);
     args.x = ctx.upload(b, R_SRC1);
-    args.dst = ctx.dev_f32(R_DST, nelements(dst));
+    args.dst = ctx.out_f32(dst, R_DST);
     args.K = a->ne[0];
     args.M = a->ne[1];
     args.N = b->ne[1];
@@ -977,7 +1154,7 @@ static void op_mul_mat(context &ctx, ggml_tensor *dst) {
 static void op_rms_norm(context &ctx, ggml_tensor *dst) {
     const ggml_tensor *a = dst->src[0];
     const float *x = ctx.upload(a, R_SRC0);
-    float *y = ctx.dev_f32(R_DST, nelements(dst));
+    float *y = ctx.out_f32(dst, R_DST);
     const int64_t nc = a->ne[0], nr = nrows(a);
     const float eps = op_f32(dst, 0);
     if (ctx.fmt->w32) {
@@ -996,12 +1173,21 @@ static void op_soft_max(context &ctx, ggml_tensor *dst) {
     std::memset(&args, 0, sizeof args);
     args.src = ctx.upload(a, R_SRC0);
     for (int i = 0; i < 4; i++) args.src_ne[i] = a->ne[i];
-    if (mask) {
+    if (mask && on_device(mask)) {
+        // rows cut to the src row length, gathered on the device
+        int64_t ne[4], nb[4];
+        view_of(mask, ne, nb);
+        ne[0] = a->ne[0];
+        float *cut = ctx.dev_f32(R_SRC1, ne[0] * ne[1] * ne[2] * ne[3]);
+        lib_ok(lnship_gather_f32(mask->data, is_f16(mask) ? 1 : 0, ne, nb, cut, ctx.get_stream()), "lnship_gather_f32");
+        args.mask = cut;
+        for (int i = 0; i < 4; i++) args.mask_ne[i] = ne[i];
+    } else if (mask) {
         // rows cut to the src row length, packed contiguously
         const int64_t n0 = a->ne[0], rows = nrows(mask);
-        float *full = (float *)ctx.host[R_AUX].grow((size_t)nelements(mask) * 4);
+        float *full = (float *)ctx.staging(R_AUX, (size_t)nelements(mask) * 4);
         gather_f32(mask, full);
-        float *cut = (float *)ctx.host[R_SRC1].grow((size_t)(rows * n0) * 4);
+        float *cut = (float *)ctx.staging(R_SRC1, (size_t)(rows * n0) * 4);
         for (int64_t r = 0; r < rows; r++) std::memcpy(cut + r * n0, full + r * mask->ne[0], (size_t)n0 * 4);
         args.mask = (const float *)ctx.upload_raw(cut, (size_t)(rows * n0) * 4, R_SRC1);
         args.mask_ne[0] = n0;
@@ -1010,7 +1196,7 @@ static void op_soft_max(context &ctx, ggml_tensor *dst) {
         for (int i = 0; i < 4; i++) args.mask_ne[i] = 1;
     }
     args.scale = op_f32(dst, 0);
-    args.dst = ctx.dev_f32(R_DST, nelements(dst));
+    args.dst = ctx.out_f32(dst, R_DST);
     if (ctx.fmt->w32) {
         lib_ok(lnship32_soft_max(&args, ctx.get_stream()), "lnship32_soft_max");
     } else {
@@ -1045,9 +1231,15 @@ static void op_binary(context &ctx, ggml_tensor *dst) {
     } else {
         // ggml's general repeat, expanded on the host
         const int64_t nbe = nelements(b);
-        float *bf = (float *)ctx.host[R_AUX].grow((size_t)nbe * 4);
-        gather_f32(b, bf);
-        float *h = (float *)ctx.host[R_SRC1].grow((size_t)n * 4);
+        float *bf = (float *)ctx.staging(R_AUX, (size_t)nbe * 4);
+        if (on_device(b)) {
+            const float *bd = ctx.upload(b, R_AUX);   // contiguous on the device
+            hip_ok(hipStreamSynchronize(ctx.get_stream()), "hipStreamSynchronize");
+            hip_ok(hipMemcpy(bf, bd, (size_t)nbe * 4, hipMemcpyDeviceToHost), "hipMemcpy D2H");
+        } else {
+            gather_f32(b, bf);
+        }
+        float *h = (float *)ctx.staging(R_SRC1, (size_t)n * 4);
         int64_t i = 0;
         for (int64_t i3 = 0; i3 < a->ne[3]; i3++)
             for (int64_t i2 = 0; i2 < a->ne[2]; i2++)
@@ -1059,9 +1251,14 @@ static void op_binary(context &ctx, ggml_tensor *dst) {
         xb = (const float *)ctx.upload_raw(h, (size_t)n * 4, R_SRC1);
         nb = n;
     }
-    float *y = ctx.dev_f32(R_DST, n);
-    if (MUL) lib_ok(lnship16_mul(xa, xb, n, nb, y, ctx.get_stream()), "lnship16_mul");
-    else lib_ok(lnship16_add(xa, xb, n, nb, y, ctx.get_stream()), "lnship16_add");
+    float *y = ctx.out_f32(dst, R_DST);
+    if (ctx.fmt->w32) {
+        if (MUL) lib_ok(lnship32_mul(xa, xb, n, nb, y, ctx.get_stream()), "lnship32_mul");
+        else lib_ok(lnship32_add(xa, xb, n, nb, y, ctx.get_stream()), "lnship32_add");
+    } else {
+        if (MUL) lib_ok(lnship16_mul(xa, xb, n, nb, y, ctx.get_stream()), "lnship16_mul");
+        else lib_ok(lnship16_add(xa, xb, n, nb, y, ctx.get_stream()), "lnship16_add");
+    }
     ctx.download(y, dst);
 }
 
@@ -1080,15 +1277,29 @@ static void op_swiglu(context &ctx, ggml_tensor *dst) {
         gate = x + (swapped ? ncols : 0);
         up = x + (swapped ? 0 : ncols);
     }
-    float *y = ctx.dev_f32(R_DST, nelements(dst));
-    lib_ok(lnship16_swiglu(gate, gate_ld, up, up_ld, y, ncols, nr, ctx.get_stream()), "lnship16_swiglu");
+    float *y = ctx.out_f32(dst, R_DST);
+    if (ctx.fmt->w32) lib_ok(lnship32_swiglu(gate, gate_ld, up, up_ld, y, ncols, nr, ctx.get_stream()), "lnship32_swiglu");
+    else lib_ok(lnship16_swiglu(gate, gate_ld, up, up_ld, y, ncols, nr, ctx.get_stream()), "lnship16_swiglu");
     ctx.download(y, dst);
+}
+
+// t's first n elements on the host (a copy when t is in a device buffer)
+template <class T>
+static const T *host_elems(const ggml_tensor *t, int64_t n, std::vector<T> &keep) {
+    if (!on_device(t)) return (const T *)t->data;
+    keep.resize((size_t)n);
+    hip_ok(hipMemcpy(keep.data(), t->data, (size_t)n * sizeof(T), hipMemcpyDeviceToHost), "hipMemcpy D2H");
+    return keep.data();
 }
 
 static void op_rope(context &ctx, ggml_tensor *dst) {
     const ggml_tensor *a = dst->src[0];
-    const int32_t *pos = (const int32_t *)dst->src[1]->data;
-    const float *ff = dst->src[2] ? (const float *)dst->src[2]->data : nullptr;
+    std::vector<int32_t> pos_h;
+    std::vector<float> ff_h;
+    if (on_device(dst->src[1]) || (dst->src[2] && on_device(dst->src[2])))
+        hip_ok(hipStreamSynchronize(ctx.get_stream()), "hipStreamSynchronize");   // produced by earlier nodes
+    const int32_t *pos = host_elems<int32_t>(dst->src[1], a->ne[2], pos_h);
+    const float *ff = dst->src[2] ? host_elems<float>(dst->src[2], op_i32(dst, 1) / 2, ff_h) : nullptr;
     const int n_dims = op_i32(dst, 1), mode = op_i32(dst, 2);
     const int64_t half = n_dims / 2, ntok = a->ne[2] * a->ne[3];
     // (cos, sin) per token and pair in lns_rope's float sequence
@@ -1109,10 +1320,17 @@ static void op_rope(context &ctx, ggml_tensor *dst) {
     const float *x = ctx.upload(a, R_SRC0);
     const float *csd = (const float *)ctx.upload_raw(cs.data(), cs.size() * 4, R_AUX);
     const int32_t *idd = (const int32_t *)ctx.upload_raw(idx.data(), idx.size() * 4, R_SRC2);
-    float *y = ctx.dev_f32(R_DST, nelements(dst));
-    lib_ok(lnship16_rope(x, a->ne[0] * a->ne[1], idd, ntok, a->ne[1], a->ne[0], n_dims, mode == 2, csd, y,
-                         ctx.get_stream()),
-           "lnship16_rope");
+    float *y = ctx.out_f32(dst, R_DST);
+    if (ctx.fmt->w32)
+        lib_ok(lnship32_rope(x, a->ne[0] * a->ne[1], idd, ntok, a->ne[1], a->ne[0], n_dims, mode == 2, csd, y,
+                             ctx.get_stream()),
+               "lnship32_rope");
+    else
+        lib_ok(lnship16_rope(x, a->ne[0] * a->ne[1], idd, ntok, a->ne[1], a->ne[0], n_dims, mode == 2, csd, y,
+                             ctx.get_stream()),
+               "lnship16_rope");
+    // cs and idx are host vectors: the copies above must finish before they go
+    if (on_device(dst)) hip_ok(hipStreamSynchronize(ctx.get_stream()), "hipStreamSynchronize");
     // cs and idx are host vectors: the copies above must finish before they go
     ctx.download(y, dst);
 }
@@ -1122,18 +1340,10 @@ static void run_node(context &ctx, ggml_tensor *node) {
         case kind::mul_mat: return op_mul_mat(ctx, node);
         case kind::rms_norm: return op_rms_norm(ctx, node);
         case kind::soft_max: return op_soft_max(ctx, node);
-        case kind::add:
-            if (!ctx.fmt->w32) return op_binary<false>(ctx, node);
-            break;
-        case kind::mul:
-            if (!ctx.fmt->w32) return op_binary<true>(ctx, node);
-            break;
-        case kind::swiglu:
-            if (!ctx.fmt->w32) return op_swiglu(ctx, node);
-            break;
-        case kind::rope:
-            if (!ctx.fmt->w32) return op_rope(ctx, node);
-            break;
+        case kind::add: return op_binary<false>(ctx, node);
+        case kind::mul: return op_binary<true>(ctx, node);
+        case kind::swiglu: return op_swiglu(ctx, node);
+        case kind::rope: return op_rope(ctx, node);
         default: break;
     }
     die("%s: unsupported op %s (%s) in graph_compute", ctx.fmt->name, ggml_op_desc(node), node->name);

@@ -1245,6 +1245,42 @@ __global__ void k_store_kv(const float *__restrict__ x, int64_t x_ld, const int3
     }
 }
 
+// ggml views on the device: element (i0, i1, i2, i3) at byte offset
+// i0 nb0 + i1 nb1 + i2 nb2 + i3 nb3, gathered into (or scattered from) a
+// contiguous F32 array in ggml element order.
+struct strided4 {
+    int64_t ne[4];
+    int64_t nb[4];
+};
+
+template <int SRC_HALF>
+__global__ void k_gather_f32(const char *__restrict__ src, strided4 g, float *__restrict__ dst) {
+    const int64_t n = g.ne[0] * g.ne[1] * g.ne[2] * g.ne[3];
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)blockDim.x * gridDim.x) {
+        int64_t r = i;
+        const int64_t i0 = r % g.ne[0];
+        r /= g.ne[0];
+        const int64_t i1 = r % g.ne[1];
+        r /= g.ne[1];
+        const int64_t i2 = r % g.ne[2], i3 = r / g.ne[2];
+        const char *p = src + i0 * g.nb[0] + i1 * g.nb[1] + i2 * g.nb[2] + i3 * g.nb[3];
+        dst[i] = SRC_HALF ? __half2float(*reinterpret_cast<const __half *>(p)) : *reinterpret_cast<const float *>(p);
+    }
+}
+
+__global__ void k_scatter_f32(const float *__restrict__ src, char *__restrict__ dst, strided4 g) {
+    const int64_t n = g.ne[0] * g.ne[1] * g.ne[2] * g.ne[3];
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)blockDim.x * gridDim.x) {
+        int64_t r = i;
+        const int64_t i0 = r % g.ne[0];
+        r /= g.ne[0];
+        const int64_t i1 = r % g.ne[1];
+        r /= g.ne[1];
+        const int64_t i2 = r % g.ne[2], i3 = r / g.ne[2];
+        *reinterpret_cast<float *>(dst + i0 * g.nb[0] + i1 * g.nb[1] + i2 * g.nb[2] + i3 * g.nb[3]) = src[i];
+    }
+}
+
 __global__ void k_causal_mask(const int32_t *__restrict__ pos, int64_t ntok, int64_t n_kv, float *__restrict__ mask) {
     const int64_t n = ntok * n_kv;
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)blockDim.x * gridDim.x) {
@@ -1871,6 +1907,47 @@ int lnship32_store_kv(const float *x, int64_t x_ld, const int32_t *pos, int64_t 
                       int cache_transposed, const int32_t *seq, int64_t seq_stride, void *stream) {
     return store_kv_common<32>(x, x_ld, pos, ntok, nhead, ne0, rope_n_dims, cos_sin, cache, cache_m, cache_slice,
                                cache_transposed, seq, seq_stride, stream);
+}
+
+static bool strided_ok(const int64_t *ne, const int64_t *nb, strided4 &g) {
+    if (!ne || !nb) return false;
+    for (int d = 0; d < 4; d++) {
+        if (ne[d] < 0 || nb[d] < 0) return false;
+        g.ne[d] = ne[d];
+        g.nb[d] = nb[d];
+    }
+    return true;
+}
+
+int lnship_gather_f32(const void *src, int src_type, const int64_t ne[4], const int64_t nb[4], float *dst,
+                      void *stream) {
+    device_state *s = state();
+    if (!s) return LNSHIP_ENOINIT;
+    strided4 g;
+    if (!strided_ok(ne, nb, g) || (src_type != 0 && src_type != 1)) return fail(LNSHIP_EINVAL, "gather: bad view%s");
+    const int64_t n = ne[0] * ne[1] * ne[2] * ne[3];
+    if (n == 0) return 0;
+    if (src_type)
+        hipLaunchKernelGGL(k_gather_f32<1>, dim3(grid_for(n, 4)), dim3(k_block), 0, (hipStream_t)stream,
+                           (const char *)src, g, dst);
+    else
+        hipLaunchKernelGGL(k_gather_f32<0>, dim3(grid_for(n, 4)), dim3(k_block), 0, (hipStream_t)stream,
+                           (const char *)src, g, dst);
+    LNSHIP_HIP(hipGetLastError());
+    return 0;
+}
+
+int lnship_scatter_f32(const float *src, void *dst, const int64_t ne[4], const int64_t nb[4], void *stream) {
+    device_state *s = state();
+    if (!s) return LNSHIP_ENOINIT;
+    strided4 g;
+    if (!strided_ok(ne, nb, g)) return fail(LNSHIP_EINVAL, "scatter: bad view%s");
+    const int64_t n = ne[0] * ne[1] * ne[2] * ne[3];
+    if (n == 0) return 0;
+    hipLaunchKernelGGL(k_scatter_f32, dim3(grid_for(n, 4)), dim3(k_block), 0, (hipStream_t)stream, src, (char *)dst,
+                       g);
+    LNSHIP_HIP(hipGetLastError());
+    return 0;
 }
 
 int lnship_rope_table(float freq_base, int n_dims, int64_t n_pos, float *out) {
