@@ -130,8 +130,8 @@ def run_batch(args):
     """S sequences of the SmolLM2-shape model: each --prompt-token prompt is
     prefilled on its own, then --warmup + --steps batched decode steps (one
     token per sequence; weight GEMVs see S columns, attention is batched over
-    the sequences' own KV caches).  Non-Monte steps replay a HIP graph; Monte
-    steps run eagerly (the op seeds change every step)."""
+    the sequences' own KV caches).  Every step replays one HIP graph (Monte
+    ops read their LFSR start from a device state the graph advances)."""
     import numpy as np
     import torch
     import lnship
@@ -150,7 +150,7 @@ def run_batch(args):
     torch.cuda.synchronize()
     t_prefill = time.perf_counter() - tp
     tok_dev = torch.stack(first).to(torch.int32)
-    use_graph = mode != lnship.MONTE
+    use_graph = not args.no_graph
 
     def step():
         nonlocal tok_dev
@@ -337,12 +337,12 @@ def main():
     t_prefill = time.perf_counter() - tp
 
     tok_dev = torch.argmax(logits).to(torch.int32).reshape(1)
-    use_graph = mode != lnship.MONTE and not args.no_graph
+    use_graph = not args.no_graph
 
     def step():
         nonlocal tok_dev
         if use_graph:
-            out = _graph_step(model, tok_dev)
+            out = model.decode_graph(tok_dev)
         else:
             out = model.eval([int(tok_dev.item())])
         tok_dev = torch.argmax(out).to(torch.int32).reshape(1)
@@ -592,21 +592,6 @@ def cpu_baseline_lns32(cfg, weights, torch):
                       "embedding + output %.2f s, plus layer 0 %.2f s; scaled to 16 layers" %
                       (times[0], times[1] - times[0]),
             "cpu": _cpu_name()}
-
-
-def _graph_step(model, tok_dev):
-    """decode_graph with the token already on the device."""
-    import torch
-    from lnship.llama import n_kv_for
-    n_kv = n_kv_for(model.n_past + 1, model.cfg.n_ctx)
-    if n_kv not in model._graphs:
-        return model.decode_graph(int(tok_dev.item()), n_kv)
-    model._buf("gtok", 1, torch.int32).copy_(tok_dev)
-    model._buf("gpos", 1, torch.int32).fill_(model.n_past)
-    g, out = model._graphs[n_kv]
-    g.replay()
-    model.n_past += 1
-    return out
 
 
 if __name__ == "__main__":

@@ -93,6 +93,12 @@ typedef struct lnship_mul_mat_args {
      * between weight slices, dst_ld / dst_slice the floats between output
      * rows n / activation slices */
     int64_t w_mstride, w_slice, dst_ld, dst_slice;
+    /* optional (Monte): when monte_state is non-null, the first output starts
+     * at lfsr_jump(*monte_state, monte_offset), read on the device when the
+     * op runs (a captured graph replays with the state of its replay), and
+     * monte_seed is ignored */
+    const uint16_t *monte_state;
+    uint64_t monte_offset;
 } lnship_mul_mat_args;
 
 int lnship16_mul_mat(int mode, const lnship_mul_mat_args *args, void *stream);
@@ -103,6 +109,10 @@ int lnship32_mul_mat(const lnship_mul_mat_args *args, void *stream);
  * src/lns-ops.cpp:701-736; sum of squares from zero, in element order). */
 int lnship16_rms_norm(int mode, const float *src, float *dst, int64_t ncols, int64_t nrows, float eps,
                       uint16_t monte_seed, void *stream);
+/* The same with the Monte start read on the device: lfsr_jump(*monte_state,
+ * monte_offset) (see lnship_mul_mat_args). */
+int lnship16_rms_norm_state(int mode, const float *src, float *dst, int64_t ncols, int64_t nrows, float eps,
+                            const uint16_t *monte_state, uint64_t monte_offset, void *stream);
 int lnship32_rms_norm(const float *src, float *dst, int64_t ncols, int64_t nrows, float eps, void *stream);
 
 /* ---- SOFT_MAX (kernel_set::soft_max, :136; soft_max_args :62-71) --------
@@ -117,6 +127,8 @@ typedef struct lnship_soft_max_args {
     float scale;
     float *dst;
     uint16_t monte_seed;
+    const uint16_t *monte_state;   /* optional, as in lnship_mul_mat_args */
+    uint64_t monte_offset;
 } lnship_soft_max_args;
 
 int lnship16_soft_max(int mode, const lnship_soft_max_args *args, void *stream);
@@ -198,6 +210,10 @@ int lnship_causal_mask(const int32_t *pos, int64_t ntok, int64_t n_kv, float *ma
 int64_t lnship_max_row(int which, int mode);
 
 /* ---- Monte draw accounting (kernel_set::*_draws, :97-100) --------------- */
+/* *state = lfsr_jump(*state, draws) on the device, in stream order: the
+ * process-global LFSR advance (ggml_backend_lns16_monte_reserve,
+ * src/lns-ops.cpp:190-195) for ops that read their start from *state. */
+int lnship_lfsr_advance(uint16_t *state, uint64_t draws, void *stream);
 uint64_t lnship16_mul_mat_draws(int mode, int64_t K, int64_t M, int64_t N, int64_t ne12, int64_t ne13);
 uint64_t lnship16_soft_max_draws(int mode, int64_t ncols, int64_t nrows);
 uint64_t lnship16_rms_norm_draws(int mode, int64_t ncols, int64_t nrows);

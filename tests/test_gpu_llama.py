@@ -41,12 +41,13 @@ def test_prefill_and_decode(mode):
         print(f"[llama] {mode} decode {step}", flush=True)
         same(gpu.eval([tok]).cpu().numpy(), cpu.eval([tok]), f"{mode} decode {step}")
         tok = (tok * 7 + 3) % cfg.n_vocab
-    if m != O.MONTE:
-        for step in range(3):
-            print(f"[llama] {mode} graph decode {step}", flush=True)
-            out = gpu.decode_graph(tok).cpu().numpy()
-            same(out, cpu.eval([tok]), f"{mode} graph decode {step}")
-            tok = (tok * 5 + 1) % cfg.n_vocab
+    # graph steps, an eager step between them (Monte: the device LFSR state
+    # must be refreshed from the host's after it), then graph steps again
+    for step, kind in enumerate(("graph", "graph", "graph", "eager", "graph", "graph")):
+        print(f"[llama] {mode} {kind} decode {step}", flush=True)
+        out = gpu.decode_graph(tok) if kind == "graph" else gpu.eval([tok])
+        same(out.cpu().numpy(), cpu.eval([tok]), f"{mode} {kind} decode {step}")
+        tok = (tok * 5 + 1) % cfg.n_vocab
     assert O.monte_get() == gpu.lfsr or m != O.MONTE
 
 
@@ -84,12 +85,11 @@ def test_batched_sequences(mode):
         print(f"[llama] {mode} batched decode {step}", flush=True)
         same(gpu.eval_batch(toks).cpu().numpy(), cpu.eval_batch(toks), f"{mode} batched decode {step}")
         toks = [(t * 7 + 3 + i) % cfg.n_vocab for i, t in enumerate(toks)]
-    if m != O.MONTE:
-        for step in range(2):
-            print(f"[llama] {mode} batched graph decode {step}", flush=True)
-            dev = torch.tensor(toks, dtype=torch.int32, device="cuda")
-            same(gpu.decode_graph_batch(dev).cpu().numpy(), cpu.eval_batch(toks), f"{mode} batched graph {step}")
-            toks = [(t * 5 + 1 + i) % cfg.n_vocab for i, t in enumerate(toks)]
+    for step in range(3):
+        print(f"[llama] {mode} batched graph decode {step}", flush=True)
+        dev = torch.tensor(toks, dtype=torch.int32, device="cuda")
+        same(gpu.decode_graph_batch(dev).cpu().numpy(), cpu.eval_batch(toks), f"{mode} batched graph {step}")
+        toks = [(t * 5 + 1 + i) % cfg.n_vocab for i, t in enumerate(toks)]
     assert gpu.past == cpu.past
     assert O.monte_get() == gpu.lfsr or m != O.MONTE
 

@@ -132,6 +132,33 @@ def test_mul_mat_monte_seeds(ln):
         _mm_case(ln, "monte", 128, 64, 3, seed=12, lfsr=lfsr)
 
 
+def test_monte_start_from_device_state(ln):
+    # ops given (device state, offset) start where the 16-bit seed
+    # lfsr_jump(state, offset) would, and lnship_lfsr_advance moves the state
+    rng = np.random.default_rng(14)
+    w = (rng.standard_normal((1, 1, 64, 96)) * 0.05).astype(np.float32)
+    x = rng.standard_normal((1, 1, 3, 96)).astype(np.float32)
+    xr = rng.standard_normal((5, 200)).astype(np.float32)
+    xs = (rng.standard_normal((2, 3, 70)) * 2).astype(np.float32)
+    wp = ln.pack16(dev(w))
+    jump = O.lib().lno_lfsr_jump
+    for s0, off in ((7, 0), (0xB403, 12345), (65535, 70000), (1, 65534)):
+        print(f"\n[monte device state] state={s0:#06x} offset={off}", flush=True)
+        st = torch.tensor([s0 - 65536 if s0 >= 32768 else s0], dtype=torch.int16, device="cuda")
+        start = jump(s0, off)
+        O.monte_set(start)
+        same_bits(host(ln.mul_mat16(O.MONTE, wp, dev(x), 96, 64, seed=(st, off))), O.mul_mat16_f32w(O.MONTE, w, x),
+                  f"mul_mat from state {s0} + {off}")
+        O.monte_set(start)
+        same_bits(host(ln.rms_norm16(O.MONTE, dev(xr), 1e-5, seed=(st, off))), O.rms_norm16(O.MONTE, xr, 1e-5),
+                  f"rms_norm from state {s0} + {off}")
+        O.monte_set(start)
+        same_bits(host(ln.soft_max16(O.MONTE, dev(xs), None, 0.5, seed=(st, off))),
+                  O.soft_max16(O.MONTE, xs, None, 0.5), f"soft_max from state {s0} + {off}")
+        ln.lfsr_advance(st, off)
+        assert int(host(st)[0]) & 0xFFFF == start
+
+
 def test_mul_mat_f16_weights(ln):
     # F16 sources (the KV-cache operand of kq / kqv): converted as F32 values
     rng = np.random.default_rng(13)

@@ -557,7 +557,16 @@ struct mm_args16 {
     int64_t ne02, ne12, r2, r3;
     int64_t w_mstride, w_slice, dst_ld, dst_slice;
     uint32_t seed;
+    const uint16_t *state;   // Monte start read on the device (null: seed)
+    uint64_t offset;
 };
+
+// A Monte op's starting LFSR state: the seed, or a jump from a state read on
+// the device when the op runs.
+__device__ __forceinline__ uint32_t monte_start(const dev_tables &T, uint32_t seed, const uint16_t *state,
+                                                uint64_t offset) {
+    return state ? lfsr_jump(T, *state, offset) : seed;
+}
 
 template <int MODE>
 constexpr int mm_xl_offset() { return (lds_tables_bytes<MODE>() + 15) & ~15; }
@@ -607,7 +616,7 @@ __global__ __launch_bounds__(k_block * CG) void k_mm16(mm_args16 a, dev_tables T
         st[j] = 0;
         if (MODE == LNSHIP_MONTE && j < nc) {
             const uint64_t out = ((uint64_t)z * (uint64_t)a.M + (uint64_t)m) * (uint64_t)a.N + (uint64_t)(n0 + j);
-            st[j] = lfsr_jump(T, a.seed, out * (uint64_t)(a.K - 1));
+            st[j] = lfsr_jump(T, monte_start(T, a.seed, a.state, a.offset), out * (uint64_t)(a.K - 1));
         }
     }
     const int K = (int)a.K;
@@ -909,7 +918,8 @@ __device__ __forceinline__ void chain32(const x32_tab &O, acc_ls &acc, const uin
 template <int MODE>
 __global__ __launch_bounds__(k_block) void k_rms16(const float *__restrict__ src, float *__restrict__ dst,
                                                    int64_t ncols, int64_t nrows, int rb, float eps,
-                                                   uint32_t seed, dev_tables T) {
+                                                   uint32_t seed, const uint16_t *state, uint64_t offset,
+                                                   dev_tables T) {
     extern __shared__ __align__(16) char lds[];
     const red16<MODE> R = stage_tables<MODE>(T, lds);
     uint16_t *sq = reinterpret_cast<uint16_t *>(lds + ((lds_tables_bytes<MODE>() + 15) & ~15));
@@ -927,7 +937,8 @@ __global__ __launch_bounds__(k_block) void k_rms16(const float *__restrict__ src
     if ((int)threadIdx.x < nr) {
         const int r = threadIdx.x;
         uint32_t s = 0;
-        if (MODE == LNSHIP_MONTE) s = lfsr_jump(T, seed, (uint64_t)(r0 + r) * (uint64_t)ncols);
+        if (MODE == LNSHIP_MONTE)
+            s = lfsr_jump(T, monte_start(T, seed, state, offset), (uint64_t)(r0 + r) * (uint64_t)ncols);
         typename red16<MODE>::acc_t acc = R.start(0u, s);
         chain16(R, acc, sq + r * rs, 0, nc, s);
         const uint32_t sum = R.finish(acc) & 0xffffu;
@@ -990,6 +1001,8 @@ struct sm_args {
     float scale;
     uint32_t seed;
     int rb;
+    const uint16_t *state;   // Monte start read on the device (null: seed)
+    uint64_t offset;
 };
 
 __device__ __forceinline__ const float *mask_row(const sm_args &a, int64_t row) {
@@ -1041,7 +1054,8 @@ __global__ __launch_bounds__(k_block) void k_softmax16(sm_args a, dev_tables T) 
     if ((int)threadIdx.x < nr) {
         const int r = threadIdx.x;
         uint32_t s = 0;
-        if (MODE == LNSHIP_MONTE) s = lfsr_jump(T, a.seed, (uint64_t)(r0 + r) * (uint64_t)(a.n - 1));
+        if (MODE == LNSHIP_MONTE)
+            s = lfsr_jump(T, monte_start(T, a.seed, a.state, a.offset), (uint64_t)(r0 + r) * (uint64_t)(a.n - 1));
         const uint16_t *row = c + r * rs;
         typename red16<MODE>::acc_t acc = R.start(row[0], s);
         if (a.n > 1) chain16(R, acc, row, 1, (int)a.n, s);
@@ -1466,14 +1480,14 @@ static int launch_mm32(const mm_args32 &m, const dev_tables &T, int64_t nslices,
 
 template <int MODE>
 static int launch_rms16(const float *src, float *dst, int64_t ncols, int64_t nrows, float eps, uint16_t seed,
-                        const dev_tables &T, hipStream_t st) {
+                        const uint16_t *state, uint64_t offset, const dev_tables &T, hipStream_t st) {
     const int64_t rs = (ncols + 7) & ~(int64_t)7;
     const int rb = rows_per_block<MODE>(rs, 2);
     if (rb < 1) return fail(LNSHIP_ERANGE, "rms_norm: row too long for LDS%s");
     const int lds = ((lds_tables_bytes<MODE>() + 15) & ~15) + (int)(rb * rs * 2);
     if (int rc = set_lds(k_rms16<MODE>, lds)) return rc;
     hipLaunchKernelGGL(k_rms16<MODE>, dim3((unsigned)((nrows + rb - 1) / rb)), dim3(k_block), lds, st, src, dst, ncols,
-                       nrows, rb, eps, (uint32_t)seed, T);
+                       nrows, rb, eps, (uint32_t)seed, state, offset, T);
     LNSHIP_HIP(hipGetLastError());
     return 0;
 }
@@ -1630,6 +1644,25 @@ uint16_t lnship_lfsr_jump(uint16_t st, uint64_t n) {
     return st;
 }
 
+} // extern "C"
+
+namespace lnship {
+__global__ void k_lfsr_advance(uint16_t *state, uint64_t draws, dev_tables T) {
+    if (threadIdx.x == 0) *state = (uint16_t)lfsr_jump(T, *state, draws);
+}
+} // namespace lnship
+
+extern "C" {
+
+int lnship_lfsr_advance(uint16_t *lfsr, uint64_t draws, void *stream) {
+    device_state *s = state();
+    if (!s) return LNSHIP_ENOINIT;
+    if (!lfsr) return fail(LNSHIP_EINVAL, "lfsr_advance: null state%s");
+    hipLaunchKernelGGL(k_lfsr_advance, dim3(1), dim3(64), 0, (hipStream_t)stream, lfsr, draws, s->T);
+    LNSHIP_HIP(hipGetLastError());
+    return 0;
+}
+
 uint64_t lnship16_mul_mat_draws(int mode, int64_t K, int64_t M, int64_t N, int64_t ne12, int64_t ne13) {
     if (mode != LNSHIP_MONTE || K <= 0) return 0;
     return (uint64_t)ne12 * (uint64_t)ne13 * (uint64_t)M * (uint64_t)N * (uint64_t)(K - 1);
@@ -1725,7 +1758,7 @@ int lnship16_mul_mat(int mode, const lnship_mul_mat_args *a, void *stream) {
     mm_args16 m{(const uint16_t *)a->w, (const uint16_t *)xs, a->x, a->dst, a->K, kp, a->M, a->N, xld, xslice,
                 a->ne02, a->ne12, a->ne12 / a->ne02, a->ne13 / a->ne03,
                 wms, a->w_slice ? a->w_slice : kp * wms, dld, a->dst_slice ? a->dst_slice : a->N * dld,
-                a->monte_seed};
+                a->monte_seed, a->monte_state, a->monte_offset};
     switch (mode) {
         case LNSHIP_BASE: return dispatch_mm16<LNSHIP_BASE>(m, s->T, nslices, sh, st);
         case LNSHIP_MONTE: return dispatch_mm16<LNSHIP_MONTE>(m, s->T, nslices, sh, st);
@@ -1768,8 +1801,8 @@ int lnship32_mul_mat(const lnship_mul_mat_args *a, void *stream) {
 }
 
 
-int lnship16_rms_norm(int mode, const float *src, float *dst, int64_t ncols, int64_t nrows, float eps,
-                      uint16_t monte_seed, void *stream) {
+static int rms16_common(int mode, const float *src, float *dst, int64_t ncols, int64_t nrows, float eps,
+                        uint16_t monte_seed, const uint16_t *monte_state, uint64_t monte_offset, void *stream) {
     device_state *s = state();
     if (!s) return LNSHIP_ENOINIT;
     if (mode < 0 || mode > 3 || ncols < 0 || nrows < 0) return fail(LNSHIP_EINVAL, "rms_norm: bad argument%s");
@@ -1777,11 +1810,26 @@ int lnship16_rms_norm(int mode, const float *src, float *dst, int64_t ncols, int
     if ((nrows + 63) / 64 > 2147483647) return fail(LNSHIP_ERANGE, "rms_norm: too many rows%s");
     hipStream_t st = (hipStream_t)stream;
     switch (mode) {
-        case LNSHIP_BASE: return launch_rms16<LNSHIP_BASE>(src, dst, ncols, nrows, eps, monte_seed, s->T, st);
-        case LNSHIP_MONTE: return launch_rms16<LNSHIP_MONTE>(src, dst, ncols, nrows, eps, monte_seed, s->T, st);
-        case LNSHIP_LPVIP: return launch_rms16<LNSHIP_LPVIP>(src, dst, ncols, nrows, eps, monte_seed, s->T, st);
-        default: return launch_rms16<LNSHIP_SUM32>(src, dst, ncols, nrows, eps, monte_seed, s->T, st);
+        case LNSHIP_BASE: return launch_rms16<LNSHIP_BASE>(src, dst, ncols, nrows, eps, monte_seed, monte_state, monte_offset, s->T,
+                                                                 st);
+        case LNSHIP_MONTE: return launch_rms16<LNSHIP_MONTE>(src, dst, ncols, nrows, eps, monte_seed, monte_state, monte_offset, s->T,
+                                                                 st);
+        case LNSHIP_LPVIP: return launch_rms16<LNSHIP_LPVIP>(src, dst, ncols, nrows, eps, monte_seed, monte_state, monte_offset, s->T,
+                                                                 st);
+        default: return launch_rms16<LNSHIP_SUM32>(src, dst, ncols, nrows, eps, monte_seed, monte_state, monte_offset, s->T,
+                                                                 st);
     }
+}
+
+int lnship16_rms_norm(int mode, const float *src, float *dst, int64_t ncols, int64_t nrows, float eps,
+                      uint16_t monte_seed, void *stream) {
+    return rms16_common(mode, src, dst, ncols, nrows, eps, monte_seed, nullptr, 0, stream);
+}
+
+int lnship16_rms_norm_state(int mode, const float *src, float *dst, int64_t ncols, int64_t nrows, float eps,
+                            const uint16_t *monte_state, uint64_t monte_offset, void *stream) {
+    if (!monte_state) return fail(LNSHIP_EINVAL, "rms_norm: null monte_state%s");
+    return rms16_common(mode, src, dst, ncols, nrows, eps, 0, monte_state, monte_offset, stream);
 }
 
 int lnship32_rms_norm(const float *src, float *dst, int64_t ncols, int64_t nrows, float eps, void *stream) {
@@ -1810,7 +1858,8 @@ int lnship16_soft_max(int mode, const lnship_soft_max_args *a, void *stream) {
     const int64_t nrows = a->src_ne[1] * a->src_ne[2] * a->src_ne[3];
     if (a->src_ne[0] == 0 || nrows == 0) return 0;
     sm_args m{a->src, a->mask, a->dst, a->src_ne[0], a->src_ne[1], a->src_ne[2], a->src_ne[3],
-              a->mask_ne[0], a->mask_ne[1], a->mask_ne[2], a->mask_ne[3], a->scale, a->monte_seed, 0};
+              a->mask_ne[0], a->mask_ne[1], a->mask_ne[2], a->mask_ne[3], a->scale, a->monte_seed, 0,
+              a->monte_state, a->monte_offset};
     hipStream_t st = (hipStream_t)stream;
     switch (mode) {
         case LNSHIP_BASE: return launch_sm16<LNSHIP_BASE>(m, nrows, s->T, st);

@@ -28,12 +28,14 @@ class MulMatArgs(ctypes.Structure):
     _fields_ = [("w", c_p), ("x", c_p), ("dst", c_p), ("K", c_i64), ("M", c_i64), ("N", c_i64),
                 ("ne02", c_i64), ("ne03", c_i64), ("ne12", c_i64), ("ne13", c_i64),
                 ("x_ld", c_i64), ("x_slice", c_i64), ("monte_seed", ctypes.c_uint16),
-                ("w_mstride", c_i64), ("w_slice", c_i64), ("dst_ld", c_i64), ("dst_slice", c_i64)]
+                ("w_mstride", c_i64), ("w_slice", c_i64), ("dst_ld", c_i64), ("dst_slice", c_i64),
+                ("monte_state", c_p), ("monte_offset", ctypes.c_uint64)]
 
 
 class SoftMaxArgs(ctypes.Structure):
     _fields_ = [("src", c_p), ("src_ne", c_i64 * 4), ("mask", c_p), ("mask_ne", c_i64 * 4),
-                ("scale", ctypes.c_float), ("dst", c_p), ("monte_seed", ctypes.c_uint16)]
+                ("scale", ctypes.c_float), ("dst", c_p), ("monte_seed", ctypes.c_uint16),
+                ("monte_state", c_p), ("monte_offset", ctypes.c_uint64)]
 
 
 def build():
@@ -64,6 +66,8 @@ def lib():
         "lnship32_mul_mat": (ctypes.c_int, [ctypes.POINTER(MulMatArgs), c_p]),
         "lnship16_rms_norm": (ctypes.c_int, [ctypes.c_int, c_p, c_p, c_i64, c_i64, ctypes.c_float,
                                              ctypes.c_uint16, c_p]),
+        "lnship16_rms_norm_state": (ctypes.c_int, [ctypes.c_int, c_p, c_p, c_i64, c_i64, ctypes.c_float,
+                                                   c_p, ctypes.c_uint64, c_p]),
         "lnship32_rms_norm": (ctypes.c_int, [c_p, c_p, c_i64, c_i64, ctypes.c_float, c_p]),
         "lnship16_soft_max": (ctypes.c_int, [ctypes.c_int, ctypes.POINTER(SoftMaxArgs), c_p]),
         "lnship32_soft_max": (ctypes.c_int, [ctypes.POINTER(SoftMaxArgs), c_p]),
@@ -71,6 +75,7 @@ def lib():
         "lnship16_soft_max_draws": (ctypes.c_uint64, [ctypes.c_int, c_i64, c_i64]),
         "lnship16_rms_norm_draws": (ctypes.c_uint64, [ctypes.c_int, c_i64, c_i64]),
         "lnship_lfsr_jump": (ctypes.c_uint16, [ctypes.c_uint16, ctypes.c_uint64]),
+        "lnship_lfsr_advance": (ctypes.c_int, [c_p, ctypes.c_uint64, c_p]),
         "lnship16_add": (ctypes.c_int, [c_p, c_p, c_i64, c_i64, c_p, c_p]),
         "lnship16_mul": (ctypes.c_int, [c_p, c_p, c_i64, c_i64, c_p, c_p]),
         "lnship16_swiglu": (ctypes.c_int, [c_p, c_i64, c_p, c_i64, c_p, c_i64, c_i64, c_p]),
@@ -201,18 +206,32 @@ def pack32(w):
 
 # ---- ops ---------------------------------------------------------------------
 
+def seed_fields(seed):
+    """A Monte seed argument -> (monte_seed, monte_state, monte_offset).
+
+    seed is either the 16-bit start state itself, or a pair (state, offset):
+    a device uint16 (tensor or pointer) holding the LFSR state, read when the
+    op runs, and the jump from it to the op's first draw."""
+    if isinstance(seed, tuple):
+        st, off = seed
+        return 0, (st if isinstance(st, int) else _p(st)), off
+    return seed, None, 0
+
+
 def _mm_args(wp, x, out, K, M, ne02, ne03, seed):
     N = x.shape[-2]
     ne12 = x.shape[-3] if x.dim() >= 3 else 1
     ne13 = x.shape[-4] if x.dim() >= 4 else 1
-    return MulMatArgs(_p(wp), _p(x), _p(out), K, M, N, ne02, ne03, ne12, ne13, 0, 0, seed, 0, 0, 0, 0)
+    sd, st, off = seed_fields(seed)
+    return MulMatArgs(_p(wp), _p(x), _p(out), K, M, N, ne02, ne03, ne12, ne13, 0, 0, sd, 0, 0, 0, 0, st, off)
 
 
 def mul_mat16_raw(mode, w_ptr, x_ptr, dst_ptr, K, M, N, ne02=1, ne03=1, ne12=1, ne13=1, x_ld=0, x_slice=0,
                   seed=7, w_mstride=0, w_slice=0, dst_ld=0, dst_slice=0, stream=None):
     """mul_mat on raw device pointers (ints), with every stride of the C ABI."""
-    a = MulMatArgs(w_ptr, x_ptr, dst_ptr, K, M, N, ne02, ne03, ne12, ne13, x_ld, x_slice, seed,
-                   w_mstride, w_slice, dst_ld, dst_slice)
+    sd, st, off = seed_fields(seed)
+    a = MulMatArgs(w_ptr, x_ptr, dst_ptr, K, M, N, ne02, ne03, ne12, ne13, x_ld, x_slice, sd,
+                   w_mstride, w_slice, dst_ld, dst_slice, st, off)
     check(lib().lnship16_mul_mat(mode, ctypes.byref(a), stream if stream is not None else _stream()))
 
 
@@ -254,7 +273,13 @@ def rms_norm16(mode, x, eps, seed=7, out=None):
     if out is None:
         out = torch.empty_like(x)
     ncols = x.shape[-1]
-    check(lib().lnship16_rms_norm(mode, _p(x), _p(out), ncols, x.numel() // max(1, ncols), eps, seed, _stream()))
+    sd, st, off = seed_fields(seed)
+    if st is not None:
+        check(lib().lnship16_rms_norm_state(mode, _p(x), _p(out), ncols, x.numel() // max(1, ncols), eps, st, off,
+                                            _stream()))
+    else:
+        check(lib().lnship16_rms_norm(mode, _p(x), _p(out), ncols, x.numel() // max(1, ncols), eps, sd,
+                                      _stream()))
     return out
 
 
@@ -277,7 +302,8 @@ def _ne4(shape):
 def _sm_args(x, mask, scale, out, seed):
     ne = _ne4(x.shape)
     mne = _ne4(mask.shape) if mask is not None else (c_i64 * 4)(*ne)
-    return SoftMaxArgs(_p(x), ne, _p(mask), mne, scale, _p(out), seed)
+    sd, st, off = seed_fields(seed)
+    return SoftMaxArgs(_p(x), ne, _p(mask), mne, scale, _p(out), sd, st, off)
 
 
 def soft_max16(mode, x, mask=None, scale=1.0, seed=7, out=None):
@@ -310,3 +336,9 @@ def mul_mat_draws(mode, K, M, N, ne12=1, ne13=1):
 
 def lfsr_jump(state, n):
     return lib().lnship_lfsr_jump(state, n)
+
+
+def lfsr_advance(state, draws):
+    """state (a device uint16 tensor) <- lfsr_jump(state, draws), in stream order."""
+    init()
+    check(lib().lnship_lfsr_advance(_p(state), draws, _stream()))

@@ -34,7 +34,7 @@ from dataclasses import dataclass
 
 import numpy as np
 
-from . import BASE, MONTE, LPVIP, SUM32, check, init, kp, lib, mul_mat16_raw, mul_mat32_raw
+from . import BASE, MONTE, LPVIP, SUM32, check, init, kp, lfsr_advance, lib, mul_mat16_raw, mul_mat32_raw, seed_fields
 
 KV_PAD = 256   # llama.cpp pads the KV view to 256 cells without flash attention
 
@@ -142,6 +142,12 @@ class LlamaLNS16:
         self.past = [0] * n_seq
         self._bufs = {}
         self._graphs = {}
+        # Monte under HIP graphs: the ops of a captured step read their LFSR
+        # start from this device state (a jump of the draws before them in
+        # the step), and the step ends by advancing it past all its draws
+        self.lfsr_dev = torch.zeros(1, dtype=torch.int16, device=dev)
+        self._dev_draws = None      # draws so far of the step being built on lfsr_dev
+        self._lfsr_synced = False   # lfsr_dev holds self.lfsr
 
     @property
     def n_past(self):
@@ -163,11 +169,51 @@ class LlamaLNS16:
         return b
 
     def _seed(self, draws):
-        """Monte: the LFSR state an op starts from, then advance (graph order)."""
+        """Monte: where an op's LFSR draws start, then advance past them (graph
+        order).  Eagerly that is the 16-bit state itself; in a step built for
+        a HIP graph it is (lfsr_dev, offset): the op jumps from the state the
+        replay finds on the device."""
+        if self.mode != MONTE:
+            return self.lfsr
+        if self._dev_draws is not None:
+            off = self._dev_draws
+            self._dev_draws += draws
+            return (self.lfsr_dev, off)
         s = self.lfsr
-        if self.mode == MONTE:
-            self.lfsr = lib().lnship_lfsr_jump(s, draws)
+        self.lfsr = lib().lnship_lfsr_jump(s, draws)
+        self._lfsr_synced = False
         return s
+
+    def _device_seeded(self, run):
+        """run() with the Monte ops seeded from lfsr_dev, then lfsr_dev advanced
+        past the draws they took; returns (run's result, draws)."""
+        if self.mode != MONTE:
+            return run(), 0
+        self._dev_draws = 0
+        try:
+            out = run()
+            draws = self._dev_draws
+            lfsr_advance(self.lfsr_dev, draws)
+        finally:
+            self._dev_draws = None
+        return out, draws
+
+    def _replay(self, key, build):
+        """Replays the graph of key (capturing build() first if needed) and
+        keeps self.lfsr and lfsr_dev in step; returns the graph's output."""
+        if key not in self._graphs:
+            self._graphs[key] = self._capture(lambda: self._device_seeded(build))
+            self._lfsr_synced = False   # the warm-up run advanced lfsr_dev
+        g, (out, draws) = self._graphs[key]
+        if self.mode == MONTE:
+            if not self._lfsr_synced:
+                self.lfsr_dev.fill_(self.lfsr - 65536 if self.lfsr >= 32768 else self.lfsr)
+            g.replay()
+            self.lfsr = lib().lnship_lfsr_jump(self.lfsr, draws)
+            self._lfsr_synced = True
+        else:
+            g.replay()
+        return out
 
     # -- ops --------------------------------------------------------------------
     def _mm(self, w, x_ptr, dst_ptr, K, M, N, **kw):
@@ -176,14 +222,19 @@ class LlamaLNS16:
         mul_mat16_raw(self.mode, w, x_ptr, dst_ptr, K, M, N, seed=self._seed(draws), stream=self._stream, **kw)
 
     def _rms(self, x_ptr, dst_ptr, ncols, nrows):
-        seed = self._seed(lib().lnship16_rms_norm_draws(self.mode, ncols, nrows))
-        check(lib().lnship16_rms_norm(self.mode, x_ptr, dst_ptr, ncols, nrows, self.cfg.eps, seed, self._stream))
+        sd, st, off = seed_fields(self._seed(lib().lnship16_rms_norm_draws(self.mode, ncols, nrows)))
+        if st is not None:
+            check(lib().lnship16_rms_norm_state(self.mode, x_ptr, dst_ptr, ncols, nrows, self.cfg.eps, st, off,
+                                                self._stream))
+        else:
+            check(lib().lnship16_rms_norm(self.mode, x_ptr, dst_ptr, ncols, nrows, self.cfg.eps, sd, self._stream))
 
     def _softmax(self, x_ptr, ne, mask_ptr, mne, scale, dst_ptr):
         from . import SoftMaxArgs
         nrows = ne[1] * ne[2] * ne[3]
-        seed = self._seed(lib().lnship16_soft_max_draws(self.mode, ne[0], nrows))
-        a = SoftMaxArgs(x_ptr, (ctypes.c_int64 * 4)(*ne), mask_ptr, (ctypes.c_int64 * 4)(*mne), scale, dst_ptr, seed)
+        sd, st, off = seed_fields(self._seed(lib().lnship16_soft_max_draws(self.mode, ne[0], nrows)))
+        a = SoftMaxArgs(x_ptr, (ctypes.c_int64 * 4)(*ne), mask_ptr, (ctypes.c_int64 * 4)(*mne), scale, dst_ptr, sd,
+                        st, off)
         check(lib().lnship16_soft_max(self.mode, ctypes.byref(a), self._stream))
 
     # -- forward -------------------------------------------------------------------
@@ -291,20 +342,16 @@ class LlamaLNS16:
         return n_kv_for(max(self.past) + 1, self.cfg.n_ctx)
 
     def decode_graph_batch(self, tok_dev, n_kv=None):
-        """eval_batch through a captured HIP graph (non-Monte modes), with the
-        n_seq tokens already on the device.  Returns the device logits."""
+        """eval_batch through a captured HIP graph, with the n_seq tokens
+        already on the device.  Returns the device logits.  Monte ops read
+        their LFSR start from lfsr_dev, so one graph serves every step."""
         torch = self.torch
-        assert self.mode != MONTE, "Monte seeds change every step; use eval_batch()"
         n_kv = n_kv or self.batch_n_kv()
         tok = self._buf("gbtok", self.n_seq, torch.int32)
         pos = self._buf("gbpos", self.n_seq, torch.int32)
         tok[: self.n_seq].copy_(tok_dev[: self.n_seq])
         pos[: self.n_seq].copy_(torch.tensor(self.past, dtype=torch.int32))
-        key = ("batch", n_kv)
-        if key not in self._graphs:
-            self._graphs[key] = self._capture(lambda: self.forward(self.n_seq, tok, pos, n_kv, batch=True))
-        g, out = self._graphs[key]
-        g.replay()
+        out = self._replay(("batch", n_kv), lambda: self.forward(self.n_seq, tok, pos, n_kv, batch=True))
         self.past = [p + 1 for p in self.past]
         return out
 
@@ -324,19 +371,20 @@ class LlamaLNS16:
         return g, out
 
     def decode_graph(self, token, n_kv=None):
-        """One decode step through a captured HIP graph (non-Monte modes: the
-        graph bakes the op seeds).  Returns the device logits."""
+        """One decode step of sequence 0 through a captured HIP graph; token
+        is a host int or a one-element device int32 tensor.  Returns the
+        device logits.  Monte ops read their LFSR start from lfsr_dev, so
+        one graph serves every step."""
         torch = self.torch
-        assert self.mode != MONTE, "Monte seeds change every step; use eval()"
         n_kv = n_kv or n_kv_for(self.n_past + 1, self.cfg.n_ctx)
         tok = self._buf("gtok", 1, torch.int32)
         pos = self._buf("gpos", 1, torch.int32)
-        tok.fill_(int(token))
+        if isinstance(token, torch.Tensor):
+            tok[:1].copy_(token.reshape(-1)[:1])
+        else:
+            tok.fill_(int(token))
         pos.fill_(self.n_past)
-        if n_kv not in self._graphs:
-            self._graphs[n_kv] = self._capture(lambda: self.forward(1, tok, pos, n_kv))
-        g, out = self._graphs[n_kv]
-        g.replay()
+        out = self._replay(n_kv, lambda: self.forward(1, tok, pos, n_kv))
         self.n_past += 1
         return out
 
