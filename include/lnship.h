@@ -193,6 +193,43 @@ int lnship_gather_f32(const void *src, int src_type, const int64_t ne[4], const 
                       void *stream);
 int lnship_scatter_f32(const float *src, void *dst, const int64_t ne[4], const int64_t nb[4], void *stream);
 
+/* ---- SCALE: y = x s, then + b when b != 0, in the format's arithmetic ------
+ * cuda/lns-cuda-kernels.cuh:179-189 (k_scale), cuda/lns-cuda-ops.cpp:100-110;
+ * CPU forms src/lns-ops.cpp:562-592 and src32/lns32-ops.cpp:318-342. */
+int lnship16_scale(const float *src, float *dst, int64_t n, float s, float b, void *stream);
+int lnship32_scale(const float *src, float *dst, int64_t n, float s, float b, void *stream);
+
+/* ---- Data movement of a device-resident ggml graph ------------------------
+ * No LNS arithmetic: these keep ggml's CPY / CONT / DUP, GET_ROWS and SET_ROWS
+ * on the device when their tensors live in the HBM buffer type (the KV-cache
+ * writes and the embedding / output-row gathers).  Element types: 0 F32,
+ * 1 F16 (F32 -> F16 rounds to nearest even, as ggml_fp32_to_fp16).  Views
+ * are ggml's ne[] / nb[] (bytes). */
+/* Element i of src in its logical order (i0 fastest) -> element i of dst;
+ * equal element counts (lns_cpy, src/lns-ops.cpp:1061-1149, for the F32 /
+ * F16 pairs). */
+int lnship_copy(const void *src, int src_type, const int64_t src_ne[4], const int64_t src_nb[4], void *dst,
+                int dst_type, const int64_t dst_ne[4], const int64_t dst_nb[4], void *stream);
+/* dst (F32, ne = {src_ne[0], ids_ne[0], ids_ne[1], ids_ne[2]}) row
+ * (i10, i11, i12) = src row ids[i10, i11, i12] of src slice (i11, i12)
+ * (lns_get_rows, src/lns-ops.cpp:1003-1055).  An index outside
+ * [0, src_ne[1]) leaves its row unwritten and is reported by
+ * lnship_index_error. */
+int lnship_get_rows(const void *src, int src_type, const int64_t src_ne[4], const int64_t src_nb[4],
+                    const int32_t *ids, const int64_t ids_ne[3], const int64_t ids_nb[3], float *dst,
+                    const int64_t dst_nb[4], void *stream);
+/* ggml's SET_ROWS: dst row ids[r, i02 % ids_ne[1], i03 % ids_ne[2]] of dst
+ * slice (i02, i03) = F32 src row (r, i02, i03), converted to dst_type; ids
+ * are int64 (ids_i64 = 1) or int32.  Out-of-range indices as for get_rows. */
+int lnship_set_rows(const float *src, const int64_t src_ne[4], const int64_t src_nb[4], const void *ids,
+                    int ids_i64, const int64_t ids_ne[3], const int64_t ids_nb[3], void *dst, int dst_type,
+                    const int64_t dst_ne[4], const int64_t dst_nb[4], void *stream);
+/* Waits for stream, then returns 1 (and one offending index in *bad_index)
+ * if a get_rows / set_rows on this device met an index out of range since
+ * the last call, else 0; clears the record.  The reference asserts on such
+ * an index (src/lns-ops.cpp:1024). */
+int lnship_index_error(int64_t *bad_index, void *stream);
+
 /* Host: the (cos, sin) floats lns_rope uses for positions 0..n_pos-1 (the
  * float recurrence t *= powf(freq_base, -2/n_dims) per pair, cosf / sinf;
  * src/lns-ops.cpp:1225-1247, cuda/lns-cuda-ops.cpp:223-240), laid out as

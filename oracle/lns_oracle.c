@@ -741,6 +741,19 @@ void lno16_mul_f32(const float *a, const float *b, int64_t n, int64_t nb, float 
         dst[i] = lno16_to_f32(lno16_mul(lno16_from_f32(a[i]), lno16_from_f32(b[i % nb])));
 }
 
+/* SCALE as the GPU backend computes it (cuda/lns-cuda-kernels.cuh:179-189):
+ * y = x s, then + b when b != 0, with s and b converted once.  The CPU
+ * backend's lns_scale (src/lns-ops.cpp:562-592) has the same arithmetic but
+ * stores only into an LNS16 destination. */
+void lno16_scale_f32(const float *src, int64_t n, float s, float b, float *dst) {
+    const uint16_t sc = lno16_from_f32(s), bc = lno16_from_f32(b);
+    for (int64_t i = 0; i < n; i++) {
+        uint16_t v = lno16_mul(lno16_from_f32(src[i]), sc);
+        if (b != 0.0f) v = lno16_add(v, bc);
+        dst[i] = lno16_to_f32(v);
+    }
+}
+
 /* lns_swiglu (src/lns-ops.cpp:812-868): silu(gate) * up */
 void lno16_swiglu_f32(const float *gate, const float *up, int64_t n, float *dst) {
     for (int64_t i = 0; i < n; i++)
@@ -776,6 +789,16 @@ void lno32_add_f32(const float *a, const float *b, int64_t n, int64_t nb, float 
 }
 void lno32_mul_f32(const float *a, const float *b, int64_t n, int64_t nb, float *dst) {
     for (int64_t i = 0; i < n; i++) dst[i] = lno32_to_f32(lno32_mul(lno32_from_f32(a[i]), lno32_from_f32(b[i % nb])));
+}
+
+/* lns32_scale (src32/lns32-ops.cpp:318-342), as lno16_scale_f32 in xlns32 */
+void lno32_scale_f32(const float *src, int64_t n, float s, float b, float *dst) {
+    const uint32_t sc = lno32_from_f32(s), bc = lno32_from_f32(b);
+    for (int64_t i = 0; i < n; i++) {
+        uint32_t v = lno32_mul(lno32_from_f32(src[i]), sc);
+        if (b != 0.0f) v = lno32_add(v, bc);
+        dst[i] = lno32_to_f32(v);
+    }
 }
 
 /* xlns32_silu (xlnscpp, absent): x times fp2xlns32 of the sigmoid of x's

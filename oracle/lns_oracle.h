@@ -118,6 +118,7 @@ void lno16_rms_norm(int mode, const float *src, int64_t ncols, int64_t nrows, fl
 
 void lno16_add_f32(const float *a, const float *b, int64_t n, int64_t nb, float *dst);
 void lno16_mul_f32(const float *a, const float *b, int64_t n, int64_t nb, float *dst);
+void lno16_scale_f32(const float *src, int64_t n, float s, float b, float *dst);
 void lno16_swiglu_f32(const float *gate, const float *up, int64_t n, float *dst);
 void lno16_rope_f32(const float *x, const int32_t *pos, int64_t ntok, int64_t nhead, int64_t ne0,
                     int n_dims, int neox, float freq_base, float *dst);
@@ -134,6 +135,7 @@ void lno32_rms_norm(const float *src, int64_t ncols, int64_t nrows, float eps, f
 uint32_t lno32_silu(uint32_t x);
 void lno32_add_f32(const float *a, const float *b, int64_t n, int64_t nb, float *dst);
 void lno32_mul_f32(const float *a, const float *b, int64_t n, int64_t nb, float *dst);
+void lno32_scale_f32(const float *src, int64_t n, float s, float b, float *dst);
 void lno32_swiglu_f32(const float *gate, const float *up, int64_t n, float *dst);
 void lno32_rope_f32(const float *x, const int32_t *pos, int64_t ntok, int64_t nhead, int64_t ne0,
                     int n_dims, int neox, float freq_base, float *dst);

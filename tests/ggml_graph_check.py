@@ -20,7 +20,11 @@ With --device-buffers (GGML_LNS_HIP_BUFFERS=device) the inputs, the KV
 cache, the F32 / F16 weights and every node live in the backend's device
 buffers, and results are read back through the buffer interface.
 
+With --movement: SCALE, CPY / CONT, GET_ROWS and SET_ROWS on HBM tensors
+(the KV-cache writes and row gathers of a device-resident graph).
+
 Usage: python ggml_graph_check.py --mode base|monte|lpvip|sum32 [--policy RULES] [--device-buffers] [--w32]
+       python ggml_graph_check.py --movement [--w32]
 Exit status 0 when every node matches.
 """
 import argparse
@@ -274,15 +278,124 @@ def run32(dev=False):
     return 0 if all(v == 0 for v in report.values()) else 1
 
 
+def run_movement(w32=False):
+    """SCALE and the data movement of a device-resident graph (CPY, CONT,
+    GET_ROWS, SET_ROWS) with every tensor in the HBM buffer type except the
+    host-side tables and indices named below; expected values from numpy
+    (no LNS arithmetic) and, for SCALE, the oracle."""
+    h = G.Host()
+    rng = np.random.default_rng(5)
+    f32 = lambda *s: rng.standard_normal(s).astype(np.float32)
+    act = h.device_buffer(16 << 20, w32=w32)
+    t = lambda *a, **k: h.tensor(*a, device=act, **k)
+    x = f32(3, 64)
+    X = t([64, 3], data=x, name="x")
+    nodes, want, f16 = {}, {}, set()
+
+    # llama.cpp's KV write: set_rows(cache view [128, 32], k_cur [128, 3], k_idxs i64 [3])
+    kcur = f32(3, 128)
+    cache = np.zeros((32, 128), np.float16)
+    KCUR = t([128, 3], data=kcur, name="k_cur")
+    CACHE = t([128, 32], "f16", data=cache, name="cache_k_l0")
+    idx = np.array([5, 17, 30], np.int64)
+    IDX = t([3], "i64", data=idx, name="k_idxs")
+    nodes["set_rows"] = t([128, 32], "f16", op="SET_ROWS", src=(KCUR, IDX), data=CACHE.data, name="k_stored")
+    c = cache.copy()
+    c[idx] = kcur.astype(np.float16)
+    want["set_rows"], f16 = c, f16 | {"set_rows"}
+    # F32 destination, indices in host memory (int32), broadcast over slices
+    vs = f32(4, 3, 16)
+    VS = t([16, 3, 4], data=vs, name="v_src")
+    VD = t([16, 10, 4], data=np.zeros((4, 10, 16), np.float32), name="v_dst")
+    vid = np.array([[9, 0, 4], [1, 2, 3]], np.int32)
+    VID = h.tensor([3, 2], "i32", data=vid, name="v_idxs")
+    nodes["set_rows_bcast"] = t([16, 10, 4], op="SET_ROWS", src=(VS, VID), data=VD.data, name="v_stored")
+    d = np.zeros((4, 10, 16), np.float32)
+    for i03 in range(4):
+        for r in range(3):
+            d[i03, vid[i03 % 2, r]] = vs[i03, r]
+    want["set_rows_bcast"] = d
+
+    # the older KV write: CPY of F32 rows into an F16 cache view at row 7
+    cache2 = np.zeros((32, 64), np.float16)
+    CACHE2 = t([64, 32], "f16", data=cache2, name="cache_v_l0")
+    nodes["cpy_f16"] = t([64, 3], "f16", op="CPY", src=(X,), data=CACHE2.data + 7 * 64 * 2,
+                         nb=[2, 128, 128 * 3, 128 * 3], name="v_view")
+    want["cpy_f16"] = x.astype(np.float16)
+    f16 |= {"cpy_f16"}
+    # CONT of a permuted view; CPY from a host tensor; CPY F16 -> F32
+    XT = t([3, 64], op="PERMUTE", src=(X,), data=X.data, nb=[256, 4, 768, 768], name="x_t")
+    nodes["cont"] = t([3, 64], op="CONT", src=(XT,), name="x_t_cont")
+    want["cont"] = np.ascontiguousarray(x.T)
+    xh = f32(2, 40)
+    XH = h.tensor([40, 2], data=xh, name="host_rows")
+    nodes["cpy_host_src"] = t([40, 2], "f16", op="CPY", src=(XH,), name="host_rows_f16")
+    want["cpy_host_src"], f16 = xh.astype(np.float16), f16 | {"cpy_host_src"}
+    hv = (f32(5, 12) * 4).astype(np.float16)
+    HV = t([12, 5], "f16", data=hv, name="half_vals")
+    nodes["cpy_f16_f32"] = t([12, 5], op="CPY", src=(HV,), name="half_vals_f32")
+    want["cpy_f16_f32"] = hv.astype(np.float32)
+
+    # GET_ROWS: F16 table in HBM with device ids; host F32 and Q8_0 tables;
+    # a 3-D gather (ids [4, 3] over three table slices)
+    tab16 = (f32(50, 64) * 0.5).astype(np.float16)
+    TAB16 = t([64, 50], "f16", data=tab16, name="tab16")
+    gid = np.array([49, 0, 7, 7], np.int32)
+    GID = t([4], "i32", data=gid, name="inp_out_ids")
+    nodes["get_rows_f16"] = t([64, 4], op="GET_ROWS", src=(TAB16, GID), name="rows16")
+    want["get_rows_f16"] = tab16[gid].astype(np.float32)
+    tab = f32(50, 64)
+    TAB = h.tensor([64, 50], data=tab, weights=True, name="token_embd.weight")
+    GIDH = h.tensor([4], "i32", data=gid, name="inp_tokens")
+    nodes["get_rows_host"] = t([64, 4], op="GET_ROWS", src=(TAB, GIDH), name="inp_embd")
+    want["get_rows_host"] = tab[gid]
+    q8raw, q8 = q8_0(f32(50, 64), rng)
+    TABQ = h.tensor([64, 50], "q8_0", data=q8raw, weights=True, name="token_embd_q8.weight")
+    nodes["get_rows_q8"] = t([64, 4], op="GET_ROWS", src=(TABQ, GID), name="inp_embd_q8")
+    want["get_rows_q8"] = q8[gid]
+    tab3 = f32(3, 10, 16)
+    TAB3 = t([16, 10, 3], data=tab3, name="tab3")
+    gid3 = np.array([[0, 9, 3, 3], [1, 1, 2, 8], [5, 4, 0, 9]], np.int32)
+    GID3 = t([4, 3], "i32", data=gid3, name="ids3")
+    nodes["get_rows_3d"] = t([16, 4, 3], op="GET_ROWS", src=(TAB3, GID3), name="rows3")
+    want["get_rows_3d"] = np.stack([tab3[s][gid3[s]] for s in range(3)])
+
+    # SCALE in the backend's arithmetic
+    nodes["scale"] = t([64, 3], op="SCALE", src=(X,), fparams={0: 0.125, 1: 0.0}, name="kq_scaled")
+    want["scale"] = O.scale(w32, x, 0.125)
+    nodes["scale_bias"] = t([64, 3], op="SCALE", src=(X,), fparams={0: 1.5, 1: 0.25}, name="scaled_biased")
+    want["scale_bias"] = O.scale(w32, x, 1.5, 0.25)
+
+    be = h.init(w32=w32)
+    if be is None:
+        print(json.dumps({"error": "no GPU: init returned NULL"}))
+        return 1
+    assert h.compute(be, [XT] + list(nodes.values())) == 0
+    report = {}
+    for k, tn in nodes.items():
+        if k in f16:
+            got = act.get(tn, want[k].size * 2).view(np.float16).reshape(want[k].shape)
+            report[k] = int(np.count_nonzero(got.view(np.uint16) != want[k].view(np.uint16)))
+        else:
+            got = h.f32_of(tn, act).reshape(want[k].shape)
+            report[k] = int(np.count_nonzero(got.view(np.uint32) != want[k].view(np.uint32)))
+    h.free(be)
+    print(json.dumps({"mode": "movement32" if w32 else "movement16", "mismatches": report}), flush=True)
+    return 0 if all(v == 0 for v in report.values()) else 1
+
+
 if __name__ == "__main__":
     ap = argparse.ArgumentParser()
     ap.add_argument("--mode", default="base")
     ap.add_argument("--w32", action="store_true")
     ap.add_argument("--policy", default=None)
     ap.add_argument("--device-buffers", action="store_true")
+    ap.add_argument("--movement", action="store_true", help="SCALE and the data-movement ops (HBM buffers)")
     a = ap.parse_args()
     if a.policy is not None:
         os.environ["LNS16_SUM_POLICY"] = a.policy
-    if a.device_buffers:
+    if a.device_buffers or a.movement:
         os.environ["GGML_LNS_HIP_BUFFERS"] = "device"
+    if a.movement:
+        sys.exit(run_movement(a.w32))
     sys.exit(run32(a.device_buffers) if a.w32 else run16(a.mode, a.policy, a.device_buffers))

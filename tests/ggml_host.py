@@ -22,7 +22,7 @@ ABI_DIR = os.path.join(ROOT, "xlns-ggml-backend_amd", "csrc")
 
 FLAG_COMPUTE = 16
 USAGE_ANY, USAGE_WEIGHTS, USAGE_COMPUTE = 0, 1, 2
-TYPES = {"f32": (0, 4, 1), "f16": (1, 2, 1), "q8_0": (8, 34, 32), "i32": (26, 4, 1), "lns16": (43, 2, 1)}
+TYPES = {"f32": (0, 4, 1), "f16": (1, 2, 1), "q8_0": (8, 34, 32), "i32": (26, 4, 1), "i64": (27, 8, 1), "lns16": (43, 2, 1)}
 
 
 def build_stub():

@@ -44,7 +44,7 @@ const char *ggml_op_desc(const struct ggml_tensor *t) {
     return ggml_op_name(t->op);
 }
 
-/* ---- types: f32, f16, q8_0 (block of 32 int8 + half scale), i32, lns16 --- */
+/* ---- types: f32, f16, q8_0 (block of 32 int8 + half scale), i32, i64, lns16 --- */
 static float half_to_float(uint16_t h) {
     const uint32_t s = (uint32_t)(h >> 15) << 31, e = (h >> 10) & 0x1f, m = h & 0x3ff;
     uint32_t bits;
@@ -84,7 +84,7 @@ static void q8_0_to_float(const void *x, float *y, int64_t k) {
     }
 }
 
-enum { T_F32 = 0, T_F16 = 1, T_Q8_0 = 8, T_I32 = 26, T_LNS16 = 43, T_COUNT = 44 };
+enum { T_F32 = 0, T_F16 = 1, T_Q8_0 = 8, T_I32 = 26, T_I64 = 27, T_LNS16 = 43, T_COUNT = 44 };
 
 static struct ggml_type_traits k_traits[T_COUNT];
 
@@ -97,6 +97,7 @@ static void init_traits(void) {
     k_traits[T_F16] = (struct ggml_type_traits){"f16", 1, 0, 2, false, f16_to_float, NULL};
     k_traits[T_Q8_0] = (struct ggml_type_traits){"q8_0", 32, 0, 34, true, q8_0_to_float, NULL};
     k_traits[T_I32] = (struct ggml_type_traits){"i32", 1, 0, 4, false, NULL, NULL};
+    k_traits[T_I64] = (struct ggml_type_traits){"i64", 1, 0, 8, false, NULL, NULL};
     k_traits[T_LNS16] = (struct ggml_type_traits){"lns16", 1, 0, 2, false, NULL, NULL};
 }
 

@@ -95,6 +95,8 @@ def lib():
         "lno32_soft_max": (None, [P, P, P, P, f32, P]),
         "lno32_rms_norm": (None, [P, i64, i64, f32, P]),
         "lno32_silu": (u32, [u32]),
+        "lno16_scale_f32": (None, [P, i64, f32, f32, P]),
+        "lno32_scale_f32": (None, [P, i64, f32, f32, P]),
         "lno32_add_f32": (None, [P, P, i64, i64, P]),
         "lno32_mul_f32": (None, [P, P, i64, i64, P]),
         "lno32_swiglu_f32": (None, [P, P, i64, P]),
@@ -269,6 +271,14 @@ def add32(a, b):
 def mul32(a, b):
     """lns32_mul of F32 tensors, b repeated over a's rows."""
     return _binop32(lib().lno32_mul_f32, a, b)
+
+
+def scale(w32, x, s, b=0.0):
+    """SCALE (y = x s, + b when b != 0) in xlns16 (w32 False) or xlns32."""
+    x = np.ascontiguousarray(x, np.float32)
+    out = np.empty_like(x)
+    (lib().lno32_scale_f32 if w32 else lib().lno16_scale_f32)(_ptr(x), x.size, s, b, _ptr(out))
+    return out
 
 
 def swiglu32(gate, up):

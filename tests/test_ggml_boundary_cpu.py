@@ -149,6 +149,11 @@ def _verdicts(h, w32=False):
     cases["rope_odd_dims"] = f(ne=[64, 9, 3], op="ROPE", src=(q, pos), params=(0, 63, 0), fparams=rp)
     cases["view"] = f(ne=[576, 3], op="VIEW", src=(x,))
     cases["get_rows"] = f(ne=[576, 3], op="GET_ROWS", src=(x, pos))
+    cases["scale"] = f(ne=[576, 3], op="SCALE", src=(x,), fparams={0: 0.125, 1: 0.0})
+    xt = f(ne=[3, 576], nb=[4 * 576, 4, 4 * 576 * 3, 4 * 576 * 3])
+    cases["scale_strided"] = f(ne=[3, 576], op="SCALE", src=(xt,), fparams={0: 0.125, 1: 0.0})
+    cases["cpy"] = f(ne=[576, 3], type_name="f16", op="CPY", src=(x,))
+    cases["set_rows"] = f(ne=[576, 8], type_name="f16", op="SET_ROWS", src=(x, f(ne=[3], type_name="i64")))
     return {k: h.check(t, w32) for k, t in cases.items()}
 
 
@@ -184,7 +189,11 @@ EXPECT16 = {
     "rope_short_pos": (False, "lnship_rope_requires_i32_positions"),
     "rope_odd_dims": (False, "lnship_rope_requires_even_n_dims"),
     "view": (True, "supported_view_or_noop"),
-    "get_rows": (False, "unsupported_op"),
+    "get_rows": (False, "lnship_get_rows_requires_hbm_dst"),
+    "scale": (True, "requires_contiguous_f32_src0_and_dst"),
+    "scale_strided": (False, "requires_contiguous_f32_src0_and_dst"),
+    "cpy": (False, "lnship_copy_requires_hbm_dst"),
+    "set_rows": (False, "lnship_set_rows_requires_hbm_dst"),
 }
 
 
@@ -198,9 +207,9 @@ def test_lnship32_claims(host):
     # the xlns32 backend runs the hot ops and the Llama graph's elementwise
     # ops (cuda/lns-cuda-kernels.cuh:161-355 instantiate them for xlns32 too)
     got = _verdicts(host, w32=True)
-    for k in ("mm_f32", "mm_q8_0", "mm_gqa", "rms", "softmax", "view", "add_bcast", "swiglu_fused", "rope"):
+    for k in ("mm_f32", "mm_q8_0", "mm_gqa", "rms", "softmax", "view", "add_bcast", "swiglu_fused", "rope", "scale"):
         assert got[k][0], (k, got[k])
-    for k in ("geglu", "silu", "get_rows"):
+    for k in ("geglu", "silu", "get_rows", "cpy", "set_rows"):
         assert not got[k][0], (k, got[k])
     # xlns32 rows take 4 bytes of LDS each
     assert got["rms_long"] == (False, "lnship_row_too_long")
@@ -289,6 +298,34 @@ def test_bad_sum_mode_aborts():
     r = subprocess.run([sys.executable, "-c", PRELUDE + "h.reg()"], env=e, capture_output=True, text=True,
                        timeout=120)
     assert r.returncode != 0 and "GGML_LNS16_SUM must be one of" in r.stderr
+
+
+def test_data_movement_claimed_for_hbm_destinations():
+    # with the HBM buffer type, CPY / CONT / GET_ROWS / SET_ROWS whose
+    # destination is not allocated yet (the scheduler places it in this
+    # backend's buffer type) are claimed; a destination in host memory, a bad
+    # shape or a quantized destination are left to the CPU backend
+    out, _ = _run("""
+        def unalloc(t):
+            t.buffer = None
+            return t
+        ids = h.tensor([3], "i32")
+        ids64 = h.tensor([3], "i64")
+        cases = [
+            unalloc(h.tensor([576, 3], "f16", op="CPY", src=(x,))),
+            unalloc(h.tensor([576, 3], op="CONT", src=(x,))),
+            unalloc(h.tensor([576, 3], op="GET_ROWS", src=(h.tensor([576, 100], weights=True), ids))),
+            unalloc(h.tensor([576, 3], op="GET_ROWS", src=(h.tensor([576, 100], "q8_0", weights=True), ids))),
+            unalloc(h.tensor([576, 8], "f16", op="SET_ROWS", src=(x, ids64))),
+            unalloc(h.tensor([576, 8], "f16", op="SET_ROWS", src=(x, ids))),
+            h.tensor([576, 3], "f16", op="CPY", src=(x,)),
+            unalloc(h.tensor([576, 2], op="GET_ROWS", src=(h.tensor([576, 100]), ids))),
+            unalloc(h.tensor([576, 8], "f16", op="SET_ROWS", src=(x, h.tensor([2], "i64")))),
+            unalloc(h.tensor([576, 3], "q8_0", op="CPY", src=(x,))),
+        ]
+        print(" ".join(str(h.check(t)[0]) for t in cases))
+    """, GGML_LNS_BACKEND="hip", GGML_LNS_HIP_BUFFERS="device")
+    assert out.split() == ["True"] * 6 + ["False"] * 4
 
 
 def test_bad_sum_policy_aborts():

@@ -49,3 +49,11 @@ def test_ggml_graph_device_buffers(mode):
 @pytest.mark.gpu
 def test_ggml_graph_lnship32_device_buffers():
     _run(["--w32", "--device-buffers"], dict(os.environ))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("w32", [False, True])
+def test_ggml_graph_data_movement(w32):
+    # SCALE, and the KV-cache writes (SET_ROWS, CPY into an F16 view) and row
+    # gathers (GET_ROWS) of a graph whose tensors live in HBM
+    _run(["--movement"] + (["--w32"] if w32 else []), dict(os.environ, GGML_LNS16_SUM="sum32"))

@@ -321,3 +321,48 @@ def test_elementwise_lns32(ln):
         out = torch.empty_like(dx)
         ln.check(L.lnship32_rope(P(dx), 64, P(dpos), 3, 4, 16, n_dims, neox, P(dcs), P(out), st))
         same_bits(host(out), O.rope32(x, pos, n_dims, neox, 10000.0), f"lns32 rope neox={neox} n_dims={n_dims}")
+
+
+# ---------------------------------------- SCALE and data movement (C ABI) --
+
+def test_scale_both_formats(ln):
+    import ctypes
+    L, st = ln.lib(), ln._stream()
+    rng = np.random.default_rng(61)
+    x = (rng.standard_normal(1 << 20) * 5).astype(np.float32)
+    x[:4] = [0.0, -0.0, 1e-30, -3e38]
+    for w32, fn in ((False, L.lnship16_scale), (True, L.lnship32_scale)):
+        for s, b in ((0.125, 0.0), (-1.5, 0.25), (3.0, -7.0)):
+            print(f"\n[scale] w32={w32} s={s} b={b}", flush=True)
+            xd, yd = dev(x), torch.empty(x.size, dtype=torch.float32, device="cuda")
+            ln.check(fn(ctypes.c_void_p(xd.data_ptr()), ctypes.c_void_p(yd.data_ptr()), x.size, s, b, st))
+            same_bits(host(yd), O.scale(w32, x, s, b), f"scale w32={w32} s={s} b={b}")
+
+
+def test_row_index_out_of_range_is_reported(ln):
+    # a bad index leaves its row unwritten and is reported once; the good rows land
+    import ctypes
+    L, st = ln.lib(), ln._stream()
+    V = lambda *v: (ctypes.c_int64 * len(v))(*v)
+    P = lambda t: ctypes.c_void_p(t.data_ptr())
+    tab = dev(np.arange(40, dtype=np.float32).reshape(10, 4))
+    ids = dev(np.array([3, 10, 0], np.int32))
+    out = torch.full((3, 4), -1.0, dtype=torch.float32, device="cuda")
+    print("\n[get_rows] index 10 of 10 rows", flush=True)
+    ln.check(L.lnship_get_rows(P(tab), 0, V(4, 10, 1, 1), V(4, 16, 160, 160), P(ids), V(3, 1, 1), V(4, 12, 12),
+                               P(out), V(4, 16, 48, 48), st))
+    bad = ctypes.c_int64()
+    assert L.lnship_index_error(ctypes.byref(bad), st) == 1 and bad.value == 10
+    assert L.lnship_index_error(ctypes.byref(bad), st) == 0
+    got = host(out)
+    assert np.array_equal(got[0], np.arange(12, 16)) and np.array_equal(got[2], np.arange(4))
+    assert np.all(got[1] == -1.0)
+    print("[set_rows] index -1", flush=True)
+    src = dev(np.ones((2, 4), np.float32))
+    ids64 = dev(np.array([-1, 9], np.int64))
+    dst = torch.zeros((10, 4), dtype=torch.float16, device="cuda")
+    ln.check(L.lnship_set_rows(P(src), V(4, 2, 1, 1), V(4, 16, 32, 32), P(ids64), 1, V(2, 1, 1), V(8, 16, 16),
+                               P(dst), 1, V(4, 10, 1, 1), V(2, 8, 80, 80), st))
+    assert L.lnship_index_error(ctypes.byref(bad), st) == 1 and bad.value == -1
+    d = host(dst).astype(np.float32)
+    assert np.all(d[9] == 1.0) and np.all(d[:9] == 0.0)

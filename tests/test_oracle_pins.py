@@ -412,6 +412,25 @@ def test_lns32_elementwise_closed_forms():
     assert np.abs(n1 - n0).max() < 1e-5
 
 
+@pytest.mark.parametrize("w32", [False, True])
+def test_scale_closed_forms(w32):
+    # powers of two are exact codes in both formats, so x s is exact (zero is
+    # the smallest code, not an exact zero, under multiplication)
+    x = np.array([1.0, -2.0, 0.5, 4.0, -0.25], np.float32)
+    for s in (2.0, -0.5, 1.0):
+        assert np.array_equal(O.scale(w32, x, s), x * s)
+    # b only enters when non-zero: 0 s + b is b's round trip, x s - x s cancels,
+    # and 1 + 1 is exactly 2
+    rt = O.x2f32(O.f2x32(np.float32([0.3]))) if w32 else O.x2f16(O.f2x16(np.float32([0.3])))
+    assert O.scale(w32, np.float32([0.0]), 3.0, 0.3)[0] == rt[0]
+    assert O.scale(w32, np.float32([2.0]), 4.0, -8.0)[0] == 0.0
+    assert O.scale(w32, np.float32([1.0]), 1.0, 1.0)[0] == 2.0
+    # generic values: the product's error stays within the format's step
+    v = np.random.default_rng(9).standard_normal(256).astype(np.float32)
+    rel = np.abs(O.scale(w32, v, 0.7) / (v * np.float32(0.7)) - 1)
+    assert rel.max() < (1e-6 if w32 else 2 ** (1 / 128) - 1 + 1e-6) * 2
+
+
 # ------------------------------------------------------------- Monte LFSR --
 
 def test_lfsr_contract(L):

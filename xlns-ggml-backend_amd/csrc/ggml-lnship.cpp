@@ -385,8 +385,10 @@ static void scatter_f32(const float *in, ggml_tensor *t) {
 // ============================================================ op predicates
 
 static bool on_device(const ggml_tensor *t);
+static bool device_buffers();
 
-enum class kind { view, mul_mat, rms_norm, soft_max, add, mul, swiglu, rope, unary, glu, other };
+enum class kind { view, mul_mat, rms_norm, soft_max, add, mul, swiglu, rope, scale, copy, get_rows, set_rows, unary,
+                  glu, other };
 
 static kind classify(const ggml_tensor *t) {
     const char *n = ggml_op_name(t->op);
@@ -400,6 +402,10 @@ static kind classify(const ggml_tensor *t) {
     if (is("ROPE")) return kind::rope;
     if (is("GLU")) return std::strcmp(ggml_op_desc(t), "SWIGLU") == 0 ? kind::swiglu : kind::glu;
     if (is("UNARY")) return kind::unary;
+    if (is("SCALE")) return kind::scale;
+    if (is("CPY") || is("CONT") || is("DUP")) return kind::copy;
+    if (is("GET_ROWS")) return kind::get_rows;
+    if (is("SET_ROWS")) return kind::set_rows;
     return kind::other;
 }
 
@@ -492,6 +498,60 @@ static verdict check_rope(const ggml_tensor *op) {
     return {true, "lnship_rope"};
 }
 
+// common/lns-op-support.h:79-84 plus cuda/lns-cuda-ops.cpp:100-102
+static verdict check_scale(const ggml_tensor *op) {
+    return f32_result(op, {is_f32(op->src[0]) && contiguous(op->src[0]) && contiguous(op),
+                           "requires_contiguous_f32_src0_and_dst"});
+}
+
+// Data movement (CPY / CONT / DUP, GET_ROWS, SET_ROWS) is claimed only for a
+// destination in, or headed for, the HBM buffer type: with host buffers the
+// CPU backends run these nodes, as under the reference's GPU backend.  A
+// view into an HBM tensor (a KV-cache write) must run here, since no other
+// backend can write that memory.
+static bool dst_in_hbm(const ggml_tensor *op) {
+    if (!device_buffers()) return false;
+    const bool allocated = op->buffer || (op->view_src && op->view_src->buffer);
+    return !allocated || on_device(op);
+}
+
+// A source these ops read: F32 / F16 anywhere, any convertible type on the host.
+static bool movable_src(const ggml_tensor *t) {
+    return is_f32(t) || is_f16(t) || (!on_device(t) && to_f32_possible(t));
+}
+
+static verdict check_copy(const ggml_tensor *op) {
+    const ggml_tensor *a = op->src[0];
+    if (!dst_in_hbm(op)) return {false, "lnship_copy_requires_hbm_dst"};
+    if (!movable_src(a) || !(is_f32(op) || is_f16(op))) return {false, "lnship_copy_requires_f32_or_f16"};
+    if (nelements(a) != nelements(op)) return {false, "lnship_copy_requires_equal_sizes"};
+    return {true, "lnship_copy"};
+}
+
+// lns_get_rows (src/lns-ops.cpp:1003-1055) with an F32 destination
+static verdict check_get_rows(const ggml_tensor *op) {
+    const ggml_tensor *a = op->src[0], *ids = op->src[1];
+    if (!dst_in_hbm(op)) return {false, "lnship_get_rows_requires_hbm_dst"};
+    if (!is_f32(op) || !movable_src(a) || !ids || !type_is(ids, "i32"))
+        return {false, "get_rows_requires_f32_dst_and_convertible_src0"};
+    if (a->ne[2] != ids->ne[1] || a->ne[3] != ids->ne[2] || ids->ne[3] != 1 || op->ne[0] != a->ne[0] ||
+        op->ne[1] != ids->ne[0] || op->ne[2] != ids->ne[1] || op->ne[3] != ids->ne[2])
+        return {false, "lnship_get_rows_shape"};
+    return {true, "lnship_get_rows"};
+}
+
+// ggml's SET_ROWS: F32 rows into an F32 / F16 destination at int64 / int32 indices
+static verdict check_set_rows(const ggml_tensor *op) {
+    const ggml_tensor *b = op->src[0], *c = op->src[1];
+    if (!dst_in_hbm(op)) return {false, "lnship_set_rows_requires_hbm_dst"};
+    if (!(is_f32(op) || is_f16(op)) || !b || !is_f32(b) || !c || !(type_is(c, "i64") || type_is(c, "i32")))
+        return {false, "lnship_set_rows_requires_f32_src_and_integer_indices"};
+    if (b->ne[0] != op->ne[0] || b->ne[2] != op->ne[2] || b->ne[3] != op->ne[3] || b->ne[1] != c->ne[0] ||
+        c->ne[1] <= 0 || c->ne[2] <= 0 || b->ne[2] % c->ne[1] != 0 || b->ne[3] % c->ne[2] != 0 || c->ne[3] != 1)
+        return {false, "lnship_set_rows_shape"};
+    return {true, "lnship_set_rows"};
+}
+
 static verdict check_node(const ggml_tensor *op, bool w32) {
     switch (classify(op)) {
         case kind::view: return {true, "supported_view_or_noop"};
@@ -502,6 +562,10 @@ static verdict check_node(const ggml_tensor *op, bool w32) {
         case kind::mul: return check_binary(op);
         case kind::swiglu: return check_swiglu(op);
         case kind::rope: return check_rope(op);
+        case kind::scale: return check_scale(op);
+        case kind::copy: return check_copy(op);
+        case kind::get_rows: return check_get_rows(op);
+        case kind::set_rows: return check_set_rows(op);
         case kind::unary: return {false, "unsupported_unary_op"};
         case kind::glu: return {false, "unsupported_glu_op"};
         default: return {false, "unsupported_op"};
@@ -625,6 +689,7 @@ struct context {
     size_t budget = 0, cached = 0;
     bool full_reported = false;
     bool staging_busy = false;   // an async copy may still read the pinned staging buffers
+    bool index_kernels = false;  // a get_rows / set_rows read indices on the device this graph
 
     explicit context(const format *f) : fmt(f) {}
     ~context();
@@ -819,6 +884,12 @@ static ggml_status backend_graph_compute(ggml_backend_t b, ggml_cgraph *g) {
     }
     // results in device buffers are complete before ggml reads or copies them
     if (ctx.stream) hip_ok(hipStreamSynchronize(ctx.get_stream()), "hipStreamSynchronize");
+    if (ctx.index_kernels) {   // the reference asserts on a row index out of range (src/lns-ops.cpp:1024)
+        ctx.index_kernels = false;
+        int64_t bad = 0;
+        if (lnship_index_error(&bad, ctx.get_stream()) == 1)
+            die("%s: GET_ROWS / SET_ROWS row index %lld out of range", ctx.fmt->name, (long long)bad);
+    }
     return GGML_STATUS_SUCCESS;
 }
 
@@ -1331,8 +1402,164 @@ static void op_rope(context &ctx, ggml_tensor *dst) {
                "lnship16_rope");
     // cs and idx are host vectors: the copies above must finish before they go
     if (on_device(dst)) hip_ok(hipStreamSynchronize(ctx.get_stream()), "hipStreamSynchronize");
-    // cs and idx are host vectors: the copies above must finish before they go
     ctx.download(y, dst);
+}
+
+static void op_scale(context &ctx, ggml_tensor *dst) {
+    const ggml_tensor *a = dst->src[0];
+    const float *x = ctx.upload(a, R_SRC0);
+    float *y = ctx.out_f32(dst, R_DST);
+    const float sc = op_f32(dst, 0), b = op_f32(dst, 1);
+    if (ctx.fmt->w32) lib_ok(lnship32_scale(x, y, nelements(a), sc, b, ctx.get_stream()), "lnship32_scale");
+    else lib_ok(lnship16_scale(x, y, nelements(a), sc, b, ctx.get_stream()), "lnship16_scale");
+    ctx.download(y, dst);
+}
+
+// ---- data movement into HBM tensors
+
+static void require_hbm(const context &ctx, const ggml_tensor *t) {
+    if (!on_device(t)) die("%s: %s '%s' must be in the %s buffer type", ctx.fmt->name, ggml_op_desc(t), t->name,
+                           ctx.fmt->buft_name.c_str());
+}
+
+static int elem_type(const ggml_tensor *t) { return is_f16(t) ? 1 : 0; }
+
+// ne / nb of a contiguous F32 array of t's shape
+static void dense_f32_view(const ggml_tensor *t, int64_t ne[4], int64_t nb[4]) {
+    int64_t stride = 4;
+    for (int d = 0; d < 4; d++) {
+        ne[d] = t->ne[d];
+        nb[d] = stride;
+        stride *= t->ne[d];
+    }
+}
+
+// a's elements where the device can read them: a itself when it is an F32
+// or F16 tensor in HBM, else a contiguous F32 copy (upload)
+static const void *device_elems(context &ctx, const ggml_tensor *a, role r, int *type, int64_t ne[4],
+                                int64_t nb[4]) {
+    if (on_device(a)) {
+        *type = elem_type(a);
+        view_of(a, ne, nb);
+        return a->data;
+    }
+    *type = 0;
+    dense_f32_view(a, ne, nb);
+    return ctx.upload(a, r);
+}
+
+static void op_copy(context &ctx, ggml_tensor *dst) {
+    require_hbm(ctx, dst);
+    int st;
+    int64_t ne[4], nb[4], dne[4], dnb[4];
+    const void *x = device_elems(ctx, dst->src[0], R_SRC0, &st, ne, nb);
+    view_of(dst, dne, dnb);
+    lib_ok(lnship_copy(x, st, ne, nb, dst->data, elem_type(dst), dne, dnb, ctx.get_stream()), "lnship_copy");
+}
+
+// The indices of a GET_ROWS / SET_ROWS on the device, with their strides.
+// Host indices are range-checked here (the reference's assert) and staged
+// as a dense copy; device indices are checked by the kernel.
+template <class T>
+static const void *device_ids(context &ctx, const ggml_tensor *ids, int64_t limit, int64_t ne[3], int64_t nb[3]) {
+    if (on_device(ids)) {
+        ctx.index_kernels = true;
+        for (int d = 0; d < 3; d++) {
+            ne[d] = ids->ne[d];
+            nb[d] = (int64_t)ids->nb[d];
+        }
+        return ids->data;
+    }
+    const int64_t n = ids->ne[0] * ids->ne[1] * ids->ne[2];
+    T *h = (T *)ctx.staging(R_AUX, (size_t)std::max<int64_t>(n, 1) * sizeof(T));
+    int64_t i = 0;
+    for (int64_t i2 = 0; i2 < ids->ne[2]; i2++)
+        for (int64_t i1 = 0; i1 < ids->ne[1]; i1++)
+            for (int64_t i0 = 0; i0 < ids->ne[0]; i0++, i++) {
+                std::memcpy(&h[i], (const char *)ids->data + i0 * ids->nb[0] + i1 * ids->nb[1] + i2 * ids->nb[2],
+                            sizeof(T));
+                if ((int64_t)h[i] < 0 || (int64_t)h[i] >= limit)
+                    die("%s: row index %lld out of range [0, %lld) in '%s'", ctx.fmt->name, (long long)h[i],
+                        (long long)limit, ids->name);
+            }
+    int64_t stride = sizeof(T);
+    for (int d = 0; d < 3; d++) {
+        ne[d] = ids->ne[d];
+        nb[d] = stride;
+        stride *= ids->ne[d];
+    }
+    return ctx.upload_raw(h, (size_t)std::max<int64_t>(n, 1) * sizeof(T), R_AUX);
+}
+
+// one row of t as F32 (ggml's to_float for every non-F32 type)
+static void row_f32(const ggml_tensor *t, const char *row, float *out) {
+    const ggml_type_traits *tr = is_f32(t) ? nullptr : ggml_get_type_traits(t->type);
+    const int64_t ne0 = t->ne[0];
+    if (t->nb[0] == ggml_type_size(t->type) || (tr && tr->is_quantized)) {
+        if (!tr) std::memcpy(out, row, (size_t)ne0 * sizeof(float));
+        else tr->to_float(row, out, ne0);
+        return;
+    }
+    for (int64_t i = 0; i < ne0; i++) {
+        if (!tr) std::memcpy(out + i, row + i * t->nb[0], sizeof(float));
+        else tr->to_float(row + i * t->nb[0], out + i, 1);
+    }
+}
+
+static void op_get_rows(context &ctx, ggml_tensor *dst) {
+    require_hbm(ctx, dst);
+    const ggml_tensor *a = dst->src[0], *ids = dst->src[1];
+    int64_t dne[4], dnb[4];
+    view_of(dst, dne, dnb);
+    if (on_device(a)) {   // an F32 / F16 table in HBM
+        int64_t ane[4], anb[4], ine[3], inb[3];
+        view_of(a, ane, anb);
+        const void *id = device_ids<int32_t>(ctx, ids, a->ne[1], ine, inb);
+        lib_ok(lnship_get_rows(a->data, elem_type(a), ane, anb, (const int32_t *)id, ine, inb, (float *)dst->data, dnb,
+                               ctx.get_stream()),
+               "lnship_get_rows");
+        return;
+    }
+    // a table in host memory (any type ggml converts): the rows are gathered
+    // and converted on the host, then copied into dst
+    std::vector<char> ids_h;
+    const char *ib = (const char *)ids->data;
+    if (on_device(ids)) {   // produced by earlier nodes
+        hip_ok(hipStreamSynchronize(ctx.get_stream()), "hipStreamSynchronize");
+        ids_h.resize(ggml_nbytes(ids));
+        hip_ok(hipMemcpy(ids_h.data(), ids->data, ids_h.size(), hipMemcpyDeviceToHost), "hipMemcpy D2H");
+        ib = ids_h.data();
+    }
+    const int64_t nr = ids->ne[0] * ids->ne[1] * ids->ne[2], nc = a->ne[0];
+    float *h = (float *)ctx.staging(R_SRC0, (size_t)std::max<int64_t>(nr * nc, 1) * 4);
+    int64_t i = 0;
+    for (int64_t i12 = 0; i12 < ids->ne[2]; i12++)
+        for (int64_t i11 = 0; i11 < ids->ne[1]; i11++)
+            for (int64_t i10 = 0; i10 < ids->ne[0]; i10++, i++) {
+                int32_t r;
+                std::memcpy(&r, ib + i10 * ids->nb[0] + i11 * ids->nb[1] + i12 * ids->nb[2], 4);
+                if (r < 0 || r >= a->ne[1])
+                    die("%s: row index %d out of range [0, %lld) in '%s'", ctx.fmt->name, r, (long long)a->ne[1],
+                        ids->name);
+                row_f32(a, (const char *)a->data + r * a->nb[1] + i11 * a->nb[2] + i12 * a->nb[3], h + i * nc);
+            }
+    const float *x = (const float *)ctx.upload_raw(h, (size_t)std::max<int64_t>(nr * nc, 1) * 4, R_SRC0);
+    ctx.download(x, dst);
+}
+
+static void op_set_rows(context &ctx, ggml_tensor *dst) {
+    require_hbm(ctx, dst);
+    const ggml_tensor *b = dst->src[0], *c = dst->src[1];
+    int st;
+    int64_t bne[4], bnb[4], ine[3], inb[3], dne[4], dnb[4];
+    const void *x = device_elems(ctx, b, R_SRC0, &st, bne, bnb);   // F32 (checked)
+    const bool i64 = type_is(c, "i64");
+    const void *id = i64 ? device_ids<int64_t>(ctx, c, dst->ne[1], ine, inb)
+                         : device_ids<int32_t>(ctx, c, dst->ne[1], ine, inb);
+    view_of(dst, dne, dnb);
+    lib_ok(lnship_set_rows((const float *)x, bne, bnb, id, i64 ? 1 : 0, ine, inb, dst->data, elem_type(dst), dne, dnb,
+                           ctx.get_stream()),
+           "lnship_set_rows");
 }
 
 static void run_node(context &ctx, ggml_tensor *node) {
@@ -1344,6 +1571,10 @@ static void run_node(context &ctx, ggml_tensor *node) {
         case kind::mul: return op_binary<true>(ctx, node);
         case kind::swiglu: return op_swiglu(ctx, node);
         case kind::rope: return op_rope(ctx, node);
+        case kind::scale: return op_scale(ctx, node);
+        case kind::copy: return op_copy(ctx, node);
+        case kind::get_rows: return op_get_rows(ctx, node);
+        case kind::set_rows: return op_set_rows(ctx, node);
         default: break;
     }
     die("%s: unsupported op %s (%s) in graph_compute", ctx.fmt->name, ggml_op_desc(node), node->name);

@@ -60,6 +60,9 @@ struct device_state {
     dev_tables T{};
     void *scratch = nullptr;   // grow-only
     size_t scratch_size = 0;
+    // index check of get_rows / set_rows: [0] set to 1 by the first
+    // out-of-range index since the last lnship_index_error, [1] that index
+    unsigned long long *index_err = nullptr;
 };
 
 static device_state g_devices[k_max_devices];
@@ -1178,6 +1181,19 @@ __global__ void k_swiglu(const float *__restrict__ g, int64_t g_ld, const float 
     }
 }
 
+// y = x s (+ b when b is not zero), in the format's arithmetic
+template <int W>
+__global__ void k_scale(const float *__restrict__ src, float *__restrict__ dst, int64_t n, float s, float b,
+                        dev_tables T) {
+    const fmt_t<W> F{T};
+    const uint32_t sc = F.from(s), bc = F.from(b);
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)blockDim.x * gridDim.x) {
+        uint32_t v = F.mul(F.from(src[i]), sc);
+        if (b != 0.0f) v = F.add(v, bc);
+        dst[i] = F.to(v);
+    }
+}
+
 __global__ void k_get_rows_packed(const uint16_t *__restrict__ w, int64_t K, int64_t M, const int32_t *__restrict__ rows,
                                   int64_t nrows, float *__restrict__ dst, const float *__restrict__ rev) {
     const int64_t n = nrows * K;
@@ -1292,6 +1308,94 @@ __global__ void k_scatter_f32(const float *__restrict__ src, char *__restrict__ 
         r /= g.ne[1];
         const int64_t i2 = r % g.ne[2], i3 = r / g.ne[2];
         *reinterpret_cast<float *>(dst + i0 * g.nb[0] + i1 * g.nb[1] + i2 * g.nb[2] + i3 * g.nb[3]) = src[i];
+    }
+}
+
+// ---- data movement of a device-resident ggml graph (no LNS arithmetic) ----
+// Element types: 0 F32, 1 F16 (IEEE half; F32 -> F16 rounds to nearest even).
+
+__device__ __forceinline__ int64_t view_offset(const strided4 &g, int64_t i) {
+    const int64_t i0 = i % g.ne[0];
+    i /= g.ne[0];
+    const int64_t i1 = i % g.ne[1];
+    i /= g.ne[1];
+    const int64_t i2 = i % g.ne[2], i3 = i / g.ne[2];
+    return i0 * g.nb[0] + i1 * g.nb[1] + i2 * g.nb[2] + i3 * g.nb[3];
+}
+
+template <int TY>
+__device__ __forceinline__ float load_elem(const char *p) {
+    return TY ? __half2float(*reinterpret_cast<const __half *>(p)) : *reinterpret_cast<const float *>(p);
+}
+template <int TY>
+__device__ __forceinline__ void store_elem(char *p, float v) {
+    if (TY) *reinterpret_cast<__half *>(p) = __float2half_rn(v);
+    else *reinterpret_cast<float *>(p) = v;
+}
+
+__device__ __forceinline__ void index_fault(unsigned long long *err, int64_t idx) {
+    if (atomicCAS(&err[0], 0ull, 1ull) == 0ull) err[1] = (unsigned long long)idx;
+}
+
+// element i of src (in its logical order) -> element i of dst
+template <int ST, int DT>
+__global__ void k_copy(const char *__restrict__ src, strided4 gs, char *__restrict__ dst, strided4 gd) {
+    const int64_t n = gs.ne[0] * gs.ne[1] * gs.ne[2] * gs.ne[3];
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)blockDim.x * gridDim.x)
+        store_elem<DT>(dst + view_offset(gd, i), load_elem<ST>(src + view_offset(gs, i)));
+}
+
+// ids: ne[0..2], nb[0..2] of the index tensor
+struct ids3 {
+    int64_t ne[3];
+    int64_t nb[3];
+};
+
+__device__ __forceinline__ int64_t load_id(const char *ids, const ids3 &g, int64_t i0, int64_t i1, int64_t i2,
+                                           int i64) {
+    const char *p = ids + i0 * g.nb[0] + i1 * g.nb[1] + i2 * g.nb[2];
+    return i64 ? *reinterpret_cast<const int64_t *>(p) : (int64_t)*reinterpret_cast<const int32_t *>(p);
+}
+
+// dst row (i10, i11, i12) = src row ids[i10, i11, i12] of src slice (i11, i12)
+template <int ST>
+__global__ void k_get_rows(const char *__restrict__ src, strided4 gs, const char *__restrict__ ids, ids3 gi,
+                           float *__restrict__ dst, strided4 gd, unsigned long long *err) {
+    const int64_t nc = gs.ne[0], nr = gi.ne[0] * gi.ne[1] * gi.ne[2];
+    const int64_t n = nc * nr;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)blockDim.x * gridDim.x) {
+        const int64_t c = i % nc, r = i / nc;
+        const int64_t i10 = r % gi.ne[0], t = r / gi.ne[0];
+        const int64_t i11 = t % gi.ne[1], i12 = t / gi.ne[1];
+        const int64_t row = load_id(ids, gi, i10, i11, i12, 0);
+        if (row < 0 || row >= gs.ne[1]) {
+            index_fault(err, row);
+            continue;
+        }
+        const float v = load_elem<ST>(src + c * gs.nb[0] + row * gs.nb[1] + i11 * gs.nb[2] + i12 * gs.nb[3]);
+        *reinterpret_cast<float *>(reinterpret_cast<char *>(dst) + c * gd.nb[0] + i10 * gd.nb[1] + i11 * gd.nb[2] +
+                                   i12 * gd.nb[3]) = v;
+    }
+}
+
+// dst row ids[r, i02 % ne11, i03 % ne12] of dst slice (i02, i03) = src row
+// (r, i02, i03), converted to the destination type
+template <int DT>
+__global__ void k_set_rows(const char *__restrict__ src, strided4 gs, const char *__restrict__ ids, ids3 gi,
+                           int ids_i64, char *__restrict__ dst, strided4 gd, unsigned long long *err) {
+    const int64_t nc = gs.ne[0];
+    const int64_t n = nc * gs.ne[1] * gs.ne[2] * gs.ne[3];
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)blockDim.x * gridDim.x) {
+        const int64_t c = i % nc, t0 = i / nc;
+        const int64_t r = t0 % gs.ne[1], t1 = t0 / gs.ne[1];
+        const int64_t i02 = t1 % gs.ne[2], i03 = t1 / gs.ne[2];
+        const int64_t row = load_id(ids, gi, r, i02 % gi.ne[1], i03 % gi.ne[2], ids_i64);
+        if (row < 0 || row >= gd.ne[1]) {
+            index_fault(err, row);
+            continue;
+        }
+        const float v = load_elem<0>(src + c * gs.nb[0] + r * gs.nb[1] + i02 * gs.nb[2] + i03 * gs.nb[3]);
+        store_elem<DT>(dst + c * gd.nb[0] + row * gd.nb[1] + i02 * gd.nb[2] + i03 * gd.nb[3], v);
     }
 }
 
@@ -1536,6 +1640,18 @@ static int binary_common(const float *a, const float *b, int64_t n, int64_t nb, 
 }
 
 template <int W>
+static int scale_common(const float *src, float *dst, int64_t n, float sc, float b, void *stream) {
+    device_state *s = state();
+    if (!s) return LNSHIP_ENOINIT;
+    if (n < 0) return fail(LNSHIP_EINVAL, "scale: bad length%s");
+    if (n == 0) return 0;
+    hipLaunchKernelGGL(k_scale<W>, dim3(grid_for(n, 4)), dim3(k_block), 0, (hipStream_t)stream, src, dst, n, sc, b,
+                       s->T);
+    LNSHIP_HIP(hipGetLastError());
+    return 0;
+}
+
+template <int W>
 static int swiglu_common(const float *gate, int64_t gate_ld, const float *up, int64_t up_ld, float *dst,
                          int64_t ncols, int64_t nrows, void *stream) {
     device_state *s = state();
@@ -1635,6 +1751,8 @@ int lnship_init(void) {
     if (int rc = upload(g_host->lfsr_log, 65536, &T.lfsr_log)) return rc;
     s.T = T;
     LNSHIP_HIP(hipDeviceGetAttribute(&s.cus, hipDeviceAttributeMultiprocessorCount, dev));
+    LNSHIP_HIP(hipMalloc((void **)&s.index_err, 2 * sizeof(unsigned long long)));
+    LNSHIP_HIP(hipMemset(s.index_err, 0, 2 * sizeof(unsigned long long)));
     s.ready = true;
     return 0;
 }
@@ -1914,6 +2032,12 @@ int lnship32_add(const float *a, const float *b, int64_t n, int64_t nb, float *d
 int lnship32_mul(const float *a, const float *b, int64_t n, int64_t nb, float *dst, void *stream) {
     return binary_common<32, 1>(a, b, n, nb, dst, stream);
 }
+int lnship16_scale(const float *src, float *dst, int64_t n, float s, float b, void *stream) {
+    return scale_common<16>(src, dst, n, s, b, stream);
+}
+int lnship32_scale(const float *src, float *dst, int64_t n, float s, float b, void *stream) {
+    return scale_common<32>(src, dst, n, s, b, stream);
+}
 int lnship16_swiglu(const float *gate, int64_t gate_ld, const float *up, int64_t up_ld, float *dst, int64_t ncols,
                     int64_t nrows, void *stream) {
     return swiglu_common<16>(gate, gate_ld, up, up_ld, dst, ncols, nrows, stream);
@@ -1997,6 +2121,106 @@ int lnship_scatter_f32(const float *src, void *dst, const int64_t ne[4], const i
                        g);
     LNSHIP_HIP(hipGetLastError());
     return 0;
+}
+
+int lnship_copy(const void *src, int src_type, const int64_t src_ne[4], const int64_t src_nb[4], void *dst,
+                int dst_type, const int64_t dst_ne[4], const int64_t dst_nb[4], void *stream) {
+    device_state *s = state();
+    if (!s) return LNSHIP_ENOINIT;
+    strided4 gs, gd;
+    if (!strided_ok(src_ne, src_nb, gs) || !strided_ok(dst_ne, dst_nb, gd) || (src_type | dst_type) & ~1)
+        return fail(LNSHIP_EINVAL, "copy: bad view%s");
+    const int64_t n = gs.ne[0] * gs.ne[1] * gs.ne[2] * gs.ne[3];
+    if (n != gd.ne[0] * gd.ne[1] * gd.ne[2] * gd.ne[3]) return fail(LNSHIP_EINVAL, "copy: element counts differ%s");
+    if (n == 0) return 0;
+    const dim3 g(grid_for(n, 4));
+    hipStream_t st = (hipStream_t)stream;
+    const char *x = (const char *)src;
+    char *y = (char *)dst;
+    switch (src_type * 2 + dst_type) {
+        case 0: hipLaunchKernelGGL((k_copy<0, 0>), g, dim3(k_block), 0, st, x, gs, y, gd); break;
+        case 1: hipLaunchKernelGGL((k_copy<0, 1>), g, dim3(k_block), 0, st, x, gs, y, gd); break;
+        case 2: hipLaunchKernelGGL((k_copy<1, 0>), g, dim3(k_block), 0, st, x, gs, y, gd); break;
+        default: hipLaunchKernelGGL((k_copy<1, 1>), g, dim3(k_block), 0, st, x, gs, y, gd); break;
+    }
+    LNSHIP_HIP(hipGetLastError());
+    return 0;
+}
+
+static bool ids_ok(const int64_t *ne, const int64_t *nb, ids3 &g) {
+    if (!ne || !nb) return false;
+    for (int d = 0; d < 3; d++) {
+        if (ne[d] < 0 || nb[d] < 0) return false;
+        g.ne[d] = ne[d];
+        g.nb[d] = nb[d];
+    }
+    return true;
+}
+
+int lnship_get_rows(const void *src, int src_type, const int64_t src_ne[4], const int64_t src_nb[4],
+                    const int32_t *ids, const int64_t ids_ne[3], const int64_t ids_nb[3], float *dst,
+                    const int64_t dst_nb[4], void *stream) {
+    device_state *s = state();
+    if (!s) return LNSHIP_ENOINIT;
+    strided4 gs, gd;
+    ids3 gi;
+    if (!strided_ok(src_ne, src_nb, gs) || !ids_ok(ids_ne, ids_nb, gi) || (src_type & ~1))
+        return fail(LNSHIP_EINVAL, "get_rows: bad view%s");
+    const int64_t dne[4] = {src_ne[0], ids_ne[0], ids_ne[1], ids_ne[2]};
+    if (!strided_ok(dne, dst_nb, gd)) return fail(LNSHIP_EINVAL, "get_rows: bad destination view%s");
+    if (src_ne[2] != ids_ne[1] || src_ne[3] != ids_ne[2])
+        return fail(LNSHIP_EINVAL, "get_rows: index slices do not match the source's%s");
+    const int64_t n = dne[0] * dne[1] * dne[2] * dne[3];
+    if (n == 0) return 0;
+    const dim3 g(grid_for(n, 4));
+    if (src_type)
+        hipLaunchKernelGGL(k_get_rows<1>, g, dim3(k_block), 0, (hipStream_t)stream, (const char *)src, gs,
+                           (const char *)ids, gi, dst, gd, s->index_err);
+    else
+        hipLaunchKernelGGL(k_get_rows<0>, g, dim3(k_block), 0, (hipStream_t)stream, (const char *)src, gs,
+                           (const char *)ids, gi, dst, gd, s->index_err);
+    LNSHIP_HIP(hipGetLastError());
+    return 0;
+}
+
+int lnship_set_rows(const float *src, const int64_t src_ne[4], const int64_t src_nb[4], const void *ids,
+                    int ids_i64, const int64_t ids_ne[3], const int64_t ids_nb[3], void *dst, int dst_type,
+                    const int64_t dst_ne[4], const int64_t dst_nb[4], void *stream) {
+    device_state *s = state();
+    if (!s) return LNSHIP_ENOINIT;
+    strided4 gs, gd;
+    ids3 gi;
+    if (!strided_ok(src_ne, src_nb, gs) || !strided_ok(dst_ne, dst_nb, gd) || !ids_ok(ids_ne, ids_nb, gi) ||
+        (dst_type & ~1) || (ids_i64 & ~1))
+        return fail(LNSHIP_EINVAL, "set_rows: bad view%s");
+    if (src_ne[0] != dst_ne[0] || src_ne[2] != dst_ne[2] || src_ne[3] != dst_ne[3] || src_ne[1] != ids_ne[0])
+        return fail(LNSHIP_EINVAL, "set_rows: shapes do not match%s");
+    const int64_t n = src_ne[0] * src_ne[1] * src_ne[2] * src_ne[3];
+    if (n == 0) return 0;
+    if (ids_ne[1] <= 0 || ids_ne[2] <= 0 || src_ne[2] % ids_ne[1] || src_ne[3] % ids_ne[2])
+        return fail(LNSHIP_EINVAL, "set_rows: index slices do not broadcast%s");
+    const dim3 g(grid_for(n, 4));
+    if (dst_type)
+        hipLaunchKernelGGL(k_set_rows<1>, g, dim3(k_block), 0, (hipStream_t)stream, (const char *)src, gs,
+                           (const char *)ids, gi, ids_i64, (char *)dst, gd, s->index_err);
+    else
+        hipLaunchKernelGGL(k_set_rows<0>, g, dim3(k_block), 0, (hipStream_t)stream, (const char *)src, gs,
+                           (const char *)ids, gi, ids_i64, (char *)dst, gd, s->index_err);
+    LNSHIP_HIP(hipGetLastError());
+    return 0;
+}
+
+int lnship_index_error(int64_t *bad_index, void *stream) {
+    device_state *s = state();
+    if (!s) return LNSHIP_ENOINIT;
+    LNSHIP_HIP(hipStreamSynchronize((hipStream_t)stream));
+    unsigned long long e[2];
+    LNSHIP_HIP(hipMemcpy(e, s->index_err, sizeof e, hipMemcpyDeviceToHost));
+    if (!e[0]) return 0;
+    const unsigned long long zero[2] = {0, 0};
+    LNSHIP_HIP(hipMemcpy(s->index_err, zero, sizeof zero, hipMemcpyHostToDevice));
+    if (bad_index) *bad_index = (int64_t)e[1];
+    return 1;
 }
 
 int lnship_rope_table(float freq_base, int n_dims, int64_t n_pos, float *out) {

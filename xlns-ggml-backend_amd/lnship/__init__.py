@@ -76,6 +76,13 @@ def lib():
         "lnship16_rms_norm_draws": (ctypes.c_uint64, [ctypes.c_int, c_i64, c_i64]),
         "lnship_lfsr_jump": (ctypes.c_uint16, [ctypes.c_uint16, ctypes.c_uint64]),
         "lnship_lfsr_advance": (ctypes.c_int, [c_p, ctypes.c_uint64, c_p]),
+        "lnship16_scale": (ctypes.c_int, [c_p, c_p, c_i64, ctypes.c_float, ctypes.c_float, c_p]),
+        "lnship32_scale": (ctypes.c_int, [c_p, c_p, c_i64, ctypes.c_float, ctypes.c_float, c_p]),
+        "lnship_copy": (ctypes.c_int, [c_p, ctypes.c_int, c_p, c_p, c_p, ctypes.c_int, c_p, c_p, c_p]),
+        "lnship_get_rows": (ctypes.c_int, [c_p, ctypes.c_int, c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_p]),
+        "lnship_set_rows": (ctypes.c_int, [c_p, c_p, c_p, c_p, ctypes.c_int, c_p, c_p, c_p, ctypes.c_int, c_p, c_p,
+                                           c_p]),
+        "lnship_index_error": (ctypes.c_int, [ctypes.POINTER(c_i64), c_p]),
         "lnship16_add": (ctypes.c_int, [c_p, c_p, c_i64, c_i64, c_p, c_p]),
         "lnship16_mul": (ctypes.c_int, [c_p, c_p, c_i64, c_i64, c_p, c_p]),
         "lnship16_swiglu": (ctypes.c_int, [c_p, c_i64, c_p, c_i64, c_p, c_i64, c_i64, c_p]),
