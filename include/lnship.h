@@ -246,6 +246,33 @@ int lnship_causal_mask(const int32_t *pos, int64_t ntok, int64_t n_kv, float *ma
  * 45-54, 184-189): a ggml backend declines longer rows in supports_op. */
 int64_t lnship_max_row(int which, int mode);
 
+/* ---- MUL_MAT_ID (MoE expert FFNs) ------------------------------------------
+ * lns_mul_mat_id (src/lns-ops.cpp:394-462) and lns32_mul_mat_id
+ * (src32/lns32-ops.cpp:154-215): for token t and slot s, expert
+ * e = ids[t * ids_ld + s] and activation row i11 = s % ne11,
+ *   dst[(t * n_expert_used + s) * M + m] = dot(expert e's row m, x row (t, i11)),
+ * in the loop order t, s, m (Monte draws: K - 1 per output in that order).
+ * w holds the n_expert experts packed as lnship16_pack / lnship32_pack
+ * slices (ne = {K, M, n_expert}); x row (t, i11) starts at
+ * (t * ne11 + i11) * x_ld floats (x_ld 0: K).  ids live on the device: an
+ * expert outside [0, n_expert) leaves its slot unwritten and is reported by
+ * lnship_index_error (the reference asserts, :421).  n_expert_used a
+ * multiple of ne11; n_expert_used * n_tokens <= 65535. */
+typedef struct {
+    const void *w;
+    const float *x;
+    const int32_t *ids;
+    float *dst;
+    int64_t K, M, n_expert, n_expert_used, n_tokens, ne11;
+    int64_t x_ld, ids_ld;   /* 0: K and n_expert_used */
+    uint16_t monte_seed;    /* as lnship_mul_mat_args */
+    const uint16_t *monte_state;
+    uint64_t monte_offset;
+} lnship_mul_mat_id_args;
+int lnship16_mul_mat_id(int mode, const lnship_mul_mat_id_args *a, void *stream);
+int lnship32_mul_mat_id(const lnship_mul_mat_id_args *a, void *stream);
+uint64_t lnship16_mul_mat_id_draws(int mode, int64_t K, int64_t M, int64_t n_expert_used, int64_t n_tokens);
+
 /* ---- Monte draw accounting (kernel_set::*_draws, :97-100) --------------- */
 /* *state = lfsr_jump(*state, draws) on the device, in stream order: the
  * process-global LFSR advance (ggml_backend_lns16_monte_reserve,

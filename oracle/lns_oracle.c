@@ -624,6 +624,49 @@ void lno16_mul_mat_f32w(int mode, const float *w, const float *x, float *dst,
     free(wl);
 }
 
+/* lns_mul_mat_id (src/lns-ops.cpp:394-462): for token t, slot s, expert
+ * e = ids[t * neu + s], activation row i11 = s % ne11, each output row m in
+ * turn (Monte draws in that order).  w: n_expert experts of M rows of K
+ * xlns16 codes; x: [T][ne11][K] F32; dst: [T][neu][M] F32. */
+void lno16_mul_mat_id(int mode, const uint16_t *w, const float *x, const int32_t *ids, float *dst,
+                      int64_t K, int64_t M, int64_t n_expert, int64_t neu, int64_t T, int64_t ne11) {
+    uint16_t *xb = (uint16_t *)malloc((size_t)(ne11 * K > 0 ? ne11 * K : 1) * sizeof(uint16_t));
+    for (int64_t t = 0; t < T; t++) {
+        lno16_from_f32_n(x + t * ne11 * K, xb, (size_t)(ne11 * K));
+        for (int64_t s = 0; s < neu; s++) {
+            const int32_t e = ids[t * neu + s];
+            if (e < 0 || e >= n_expert) abort();   /* the reference's assert (:421) */
+            const uint16_t *xr = xb + (s % ne11) * K;
+            for (int64_t m = 0; m < M; m++) {
+                uint16_t d = lno16_vec_dot(mode, w + (e * M + m) * K, xr, (size_t)K, &g_lfsr);
+                dst[(t * neu + s) * M + m] = lno16_to_f32(d);
+            }
+        }
+    }
+    free(xb);
+}
+
+/* lns32_mul_mat_id (src32/lns32-ops.cpp:154-215), as lno16_mul_mat_id */
+void lno32_mul_mat_id(const float *w, const float *x, const int32_t *ids, float *dst,
+                      int64_t K, int64_t M, int64_t n_expert, int64_t neu, int64_t T, int64_t ne11) {
+    size_t nw = (size_t)(K * M * n_expert);
+    uint32_t *wl = (uint32_t *)malloc((nw ? nw : 1) * sizeof(uint32_t));
+    uint32_t *xb = (uint32_t *)malloc((size_t)(ne11 * K > 0 ? ne11 * K : 1) * sizeof(uint32_t));
+    lno32_from_f32_n(w, wl, nw);
+    for (int64_t t = 0; t < T; t++) {
+        lno32_from_f32_n(x + t * ne11 * K, xb, (size_t)(ne11 * K));
+        for (int64_t s = 0; s < neu; s++) {
+            const int32_t e = ids[t * neu + s];
+            if (e < 0 || e >= n_expert) abort();
+            const uint32_t *xr = xb + (s % ne11) * K;
+            for (int64_t m = 0; m < M; m++)
+                dst[(t * neu + s) * M + m] = lno32_to_f32(lno32_vec_dot(wl + (e * M + m) * K, xr, (size_t)K));
+        }
+    }
+    free(wl);
+    free(xb);
+}
+
 /* f32_mask_to_lns16 (src/lns-ops.cpp:634-637) */
 static inline uint16_t mask16(float m) { return m <= -3.0e38f ? X16_NEG_INF : lno16_from_f32(m); }
 static inline uint32_t mask32(float m) { return m <= -3.0e38f ? X32_NEG_INF : lno32_from_f32(m); }

@@ -108,6 +108,10 @@ void     lno32_softmax_row(const uint32_t *a, const uint32_t *mask, uint32_t *c,
 void lno16_mul_mat(int mode, const uint16_t *w, const float *x, float *dst,
                    int64_t K, int64_t M, int64_t N,
                    int64_t ne02, int64_t ne03, int64_t ne12, int64_t ne13);
+void lno16_mul_mat_id(int mode, const uint16_t *w, const float *x, const int32_t *ids, float *dst,
+                      int64_t K, int64_t M, int64_t n_expert, int64_t neu, int64_t T, int64_t ne11);
+void lno32_mul_mat_id(const float *w, const float *x, const int32_t *ids, float *dst,
+                      int64_t K, int64_t M, int64_t n_expert, int64_t neu, int64_t T, int64_t ne11);
 void lno16_mul_mat_f32w(int mode, const float *w, const float *x, float *dst,
                         int64_t K, int64_t M, int64_t N,
                         int64_t ne02, int64_t ne03, int64_t ne12, int64_t ne13);

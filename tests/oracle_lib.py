@@ -95,6 +95,8 @@ def lib():
         "lno32_soft_max": (None, [P, P, P, P, f32, P]),
         "lno32_rms_norm": (None, [P, i64, i64, f32, P]),
         "lno32_silu": (u32, [u32]),
+        "lno16_mul_mat_id": (None, [ctypes.c_int, P, P, P, P, i64, i64, i64, i64, i64, i64]),
+        "lno32_mul_mat_id": (None, [P, P, P, P, i64, i64, i64, i64, i64, i64]),
         "lno16_scale_f32": (None, [P, i64, f32, f32, P]),
         "lno32_scale_f32": (None, [P, i64, f32, f32, P]),
         "lno32_add_f32": (None, [P, P, i64, i64, P]),
@@ -271,6 +273,25 @@ def add32(a, b):
 def mul32(a, b):
     """lns32_mul of F32 tensors, b repeated over a's rows."""
     return _binop32(lib().lno32_mul_f32, a, b)
+
+
+def mul_mat_id(mode, w, x, ids):
+    """MUL_MAT_ID: w [n_expert][M][K] F32 (xlns16 via fp2xlns16, or xlns32
+    when mode is None), x [T][ne11][K] F32, ids [T][n_expert_used] int32
+    -> [T][n_expert_used][M] F32."""
+    w = np.ascontiguousarray(w, np.float32)
+    x = np.ascontiguousarray(x, np.float32)
+    ids = np.ascontiguousarray(ids, np.int32)
+    E, M, K = w.shape
+    T, ne11, _ = x.shape
+    neu = ids.shape[1]
+    out = np.zeros((T, neu, M), np.float32)
+    if mode is None:
+        lib().lno32_mul_mat_id(_ptr(w), _ptr(x), _ptr(ids), _ptr(out), K, M, E, neu, T, ne11)
+    else:
+        wc = f2x16(w)
+        lib().lno16_mul_mat_id(mode, _ptr(wc), _ptr(x), _ptr(ids), _ptr(out), K, M, E, neu, T, ne11)
+    return out
 
 
 def scale(w32, x, s, b=0.0):

@@ -366,3 +366,50 @@ def test_row_index_out_of_range_is_reported(ln):
     assert L.lnship_index_error(ctypes.byref(bad), st) == 1 and bad.value == -1
     d = host(dst).astype(np.float32)
     assert np.all(d[9] == 1.0) and np.all(d[:9] == 0.0)
+
+
+# ------------------------------------------------------------ MUL_MAT_ID --
+
+MM_ID_CASES = [
+    # (n_expert, M, K, T, n_expert_used, ne11): decode, prefill with the
+    # activation broadcast over slots, a K tail and one row per workgroup edge
+    (8, 1536, 576, 1, 2, 1),
+    (8, 256, 576, 9, 4, 1),
+    (4, 70, 13, 5, 4, 2),
+    (16, 65, 1024, 2, 8, 8),
+]
+
+
+@pytest.mark.parametrize("mode", MODES + ["lns32"])
+def test_mul_mat_id(ln, mode):
+    m = None if mode == "lns32" else O.MODES[mode]
+    for E, M, K, T, neu, ne11 in MM_ID_CASES:
+        print(f"\n[mul_mat_id] {mode} experts={E} M={M} K={K} T={T} used={neu} ne11={ne11}", flush=True)
+        rng = np.random.default_rng(E * 1000 + M + K)
+        w = (rng.standard_normal((E, M, K)) * 0.05).astype(np.float32)
+        x = rng.standard_normal((T, ne11, K)).astype(np.float32)
+        ids = rng.integers(0, E, (T, neu)).astype(np.int32)
+        O.monte_set(7)
+        want = O.mul_mat_id(m, w, x, ids)
+        wp = ln.pack32(dev(w)) if m is None else ln.pack16(dev(w))
+        got = host(ln.mul_mat_id(m, wp, dev(x), dev(ids), K, M, E, seed=7))
+        same_bits(got, want, f"mul_mat_id {mode} E={E} M={M} K={K}")
+        if m == O.MONTE:
+            assert O.monte_get() == O.lib().lno_lfsr_jump(7, ln.lib().lnship16_mul_mat_id_draws(m, K, M, neu, T))
+
+
+def test_mul_mat_id_expert_out_of_range(ln):
+    import ctypes
+    w = np.ones((3, 64, 16), np.float32)
+    x = np.ones((2, 1, 16), np.float32)
+    ids = np.array([[0, 3], [2, 1]], np.int32)
+    print("\n[mul_mat_id] expert 3 of 3", flush=True)
+    out = torch.full((2, 2, 64), -1.0, dtype=torch.float32, device="cuda")
+    ln.mul_mat_id(O.SUM32, ln.pack16(dev(w)), dev(x), dev(ids), 16, 64, 3, out=out)
+    bad = ctypes.c_int64()
+    assert ln.lib().lnship_index_error(ctypes.byref(bad), ln._stream()) == 1 and bad.value == 3
+    got = host(out)
+    want = O.mul_mat_id(O.SUM32, w, x, np.array([[0, 0], [2, 1]], np.int32))
+    assert np.all(got[0, 1] == -1.0)
+    same_bits(got[0, 0], want[0, 0], "slot before the bad expert")
+    same_bits(got[1], want[1], "token after the bad expert")

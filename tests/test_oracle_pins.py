@@ -465,3 +465,31 @@ def test_monte_is_unbiased_in_expectation(L):
     vals = [float(L.lno16_to_f32(O.sum16(O.MONTE, v, lfsr=s))) for s in range(1, 4000, 13)]
     assert abs(np.mean(vals) - 512.0) / 512.0 < 0.01
     assert abs(float(L.lno16_to_f32(O.sum16(O.BASE, v))) - 512.0) / 512.0 > 0.25
+
+
+# ------------------------------------------------------------ MUL_MAT_ID --
+
+@pytest.mark.parametrize("mode", ["base", "monte", "lpvip", "sum32", "lns32"])
+def test_mul_mat_id_is_mul_mat_per_slot_in_order(mode):
+    # each (token, slot) output is the pinned mul_mat of the slot's expert and
+    # activation row s % ne11, run in the order t, s (so Monte draws continue
+    # from one slot to the next exactly as in the reference's loop)
+    rng = np.random.default_rng(21)
+    E, M, K, T, neu, ne11 = 5, 24, 40, 3, 4, 2
+    w = (rng.standard_normal((E, M, K)) * 0.1).astype(np.float32)
+    x = rng.standard_normal((T, ne11, K)).astype(np.float32)
+    ids = rng.integers(0, E, (T, neu)).astype(np.int32)
+    m = None if mode == "lns32" else O.MODES[mode]
+    O.monte_set(7)
+    got = O.mul_mat_id(m, w, x, ids)
+    after = O.monte_get()
+    O.monte_set(7)
+    for t in range(T):
+        for s in range(neu):
+            xr = x[t, s % ne11][None]
+            e = ids[t, s]
+            want = O.mul_mat32(w[e], xr) if m is None else O.mul_mat16(m, O.f2x16(w[e]), xr)
+            assert np.array_equal(got[t, s].view(np.uint32), want[0].view(np.uint32)), (t, s)
+    assert O.monte_get() == after
+    if m == O.MONTE:
+        assert after == O.lib().lno_lfsr_jump(7, T * neu * M * (K - 1))

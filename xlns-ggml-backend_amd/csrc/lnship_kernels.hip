@@ -562,7 +562,36 @@ struct mm_args16 {
     uint32_t seed;
     const uint16_t *state;   // Monte start read on the device (null: seed)
     uint64_t offset;
+    // MUL_MAT_ID (ids non-null): slice z = (slot i12, token i13) multiplies
+    // expert ids[i12 + i13 ids_t] (of n_w) by activation slice
+    // i13 x_bcast + i12 % x_bcast; an expert out of range skips the slice
+    // and is recorded in err
+    const int32_t *ids;
+    int64_t ids_t, x_bcast, n_w;
+    unsigned long long *err;
 };
+
+// Records an index out of range: err[0] = 1, err[1] = the first such index.
+__device__ __forceinline__ void index_fault(unsigned long long *err, int64_t idx) {
+    if (atomicCAS(&err[0], 0ull, 1ull) == 0ull) err[1] = (unsigned long long)idx;
+}
+
+// The weight slice and activation slice of grid slice (i12, i13): ggml's
+// broadcast for MUL_MAT, the expert of the slot for MUL_MAT_ID.  Returns
+// false when the expert is out of range.
+template <class A>
+__device__ __forceinline__ bool mm_slices(const A &a, int64_t z, int64_t i12, int64_t i13, int64_t &zw, int64_t &zx) {
+    if (!a.ids) {
+        zw = (i13 / a.r3) * a.ne02 + i12 / a.r2;
+        zx = z;
+        return true;
+    }
+    zx = i13 * a.x_bcast + i12 % a.x_bcast;
+    zw = a.ids[i12 + i13 * a.ids_t];
+    if (zw >= 0 && zw < a.n_w) return true;
+    index_fault(a.err, zw);
+    return false;
+}
 
 // A Monte op's starting LFSR state: the seed, or a jump from a state read on
 // the device when the op runs.
@@ -590,10 +619,12 @@ __global__ __launch_bounds__(k_block * CG) void k_mm16(mm_args16 a, dev_tables T
     const int ncw = (int)min<int64_t>(NC * CG, a.N - nw);
     const int nc = (int)max<int64_t>(0, min<int64_t>(NC, a.N - n0));
     const int kp = (int)a.kp;
+    int64_t zw, zx;
+    const bool slice_ok = mm_slices(a, z, i12, i13, zw, zx);
     uint16_t *xl = reinterpret_cast<uint16_t *>(lds + mm_xl_offset<MODE>());
     if (XL) {
         // columns past N and k past K hold xlns16 zero
-        const float *xf = a.xf + z * a.x_slice + nw * a.x_ld;
+        const float *xf = a.xf + zx * a.x_slice + nw * a.x_ld;
         for (int j = 0; j < NC * CG; j++)
             for (int k = threadIdx.x; k < kp; k += k_block * CG)
                 xl[j * kp + k] = (j < ncw && k < a.K) ? (uint16_t)x16_from_f32(T.cvt16, xf[j * a.x_ld + k]) : (uint16_t)0;
@@ -602,9 +633,9 @@ __global__ __launch_bounds__(k_block * CG) void k_mm16(mm_args16 a, dev_tables T
     __syncthreads();
 
     const int64_t m = (int64_t)blockIdx.x * k_block + (threadIdx.x % k_block);
-    if (m >= a.M || nc == 0) return;
-    const uint16_t *ws = a.w + ((i13 / a.r3) * a.ne02 + i12 / a.r2) * a.w_slice + m * 8;
-    const uint16_t *xs = a.x + (z * a.N + n0) * a.kp;
+    if (m >= a.M || nc == 0 || !slice_ok) return;
+    const uint16_t *ws = a.w + zw * a.w_slice + m * 8;
+    const uint16_t *xs = a.x + (zx * a.N + n0) * a.kp;
     const int64_t wstride = a.w_mstride * 8;   // between consecutive groups of 8 k
     float *ds = a.dst + z * a.dst_slice + n0 * a.dst_ld + m;
     if (a.K == 0) {
@@ -743,6 +774,9 @@ struct mm_args32 {
     int64_t K, kp, M, N;
     int64_t ne02, ne12, r2, r3;
     int64_t w_mstride, w_slice, dst_ld, dst_slice;
+    const int32_t *ids;   // MUL_MAT_ID, as in mm_args16
+    int64_t ids_t, x_bcast, n_w;
+    unsigned long long *err;
 };
 
 // One lane per weight row m and NC columns, CG column groups per workgroup
@@ -761,8 +795,10 @@ __global__ __launch_bounds__(k_block * CG) void k_mm32(mm_args32 a, dev_tables T
     const int64_t z = blockIdx.z;
     const int64_t i12 = z % a.ne12, i13 = z / a.ne12;
     const int nc = (int)min<int64_t>(NC, a.N - n0);
-    const uint32_t *ws = a.w + ((i13 / a.r3) * a.ne02 + i12 / a.r2) * a.w_slice + m * 8;
-    const uint32_t *xs = a.x + (z * a.N + n0) * a.kp;
+    int64_t zw, zx;
+    if (!mm_slices(a, z, i12, i13, zw, zx)) return;
+    const uint32_t *ws = a.w + zw * a.w_slice + m * 8;
+    const uint32_t *xs = a.x + (zx * a.N + n0) * a.kp;
     const int64_t wstride = a.w_mstride * 8;
     float *ds = a.dst + z * a.dst_slice + n0 * a.dst_ld + m;
     if (a.K == 0) {
@@ -1331,10 +1367,6 @@ template <int TY>
 __device__ __forceinline__ void store_elem(char *p, float v) {
     if (TY) *reinterpret_cast<__half *>(p) = __float2half_rn(v);
     else *reinterpret_cast<float *>(p) = v;
-}
-
-__device__ __forceinline__ void index_fault(unsigned long long *err, int64_t idx) {
-    if (atomicCAS(&err[0], 0ull, 1ull) == 0ull) err[1] = (unsigned long long)idx;
 }
 
 // element i of src (in its logical order) -> element i of dst
@@ -1918,6 +1950,83 @@ int lnship32_mul_mat(const lnship_mul_mat_args *a, void *stream) {
     }
 }
 
+
+static int check_mm_id(const lnship_mul_mat_id_args *a) {
+    if (!a || a->K < 0 || a->M < 0 || a->n_expert <= 0 || a->n_expert_used < 0 || a->n_tokens < 0 || a->ne11 <= 0)
+        return fail(LNSHIP_EINVAL, "mul_mat_id: bad shape%s");
+    if (a->n_expert_used % a->ne11) return fail(LNSHIP_EINVAL, "mul_mat_id: slots do not broadcast over rows%s");
+    if ((a->x_ld ? a->x_ld : a->K) < a->K) return fail(LNSHIP_EINVAL, "mul_mat_id: x_ld < K%s");
+    if (a->ids_ld && a->ids_ld < a->n_expert_used) return fail(LNSHIP_EINVAL, "mul_mat_id: ids_ld < n_expert_used%s");
+    if (a->n_expert_used * a->n_tokens > 65535) return fail(LNSHIP_ERANGE, "mul_mat_id: more than 65535 slots%s");
+    if (a->K > (int64_t)1 << 30) return fail(LNSHIP_ERANGE, "mul_mat_id: K beyond 2^30%s");
+    return 0;
+}
+
+// MUL_MAT_ID as a GEMV per (slot, token): grid slice z = t n_expert_used + s
+// with one column, so the Monte draws follow the reference's (t, s, row) order
+int lnship16_mul_mat_id(int mode, const lnship_mul_mat_id_args *a, void *stream) {
+    device_state *s = state();
+    if (!s) return LNSHIP_ENOINIT;
+    if (mode < 0 || mode > 3) return fail(LNSHIP_EINVAL, "unknown summation mode%s");
+    if (int rc = check_mm_id(a)) return rc;
+    const int64_t nslices = a->n_expert_used * a->n_tokens;
+    if (a->M == 0 || nslices == 0) return 0;
+    const int64_t kp = (a->K + 7) & ~(int64_t)7, xld = a->x_ld ? a->x_ld : a->K;
+    hipStream_t st = (hipStream_t)stream;
+    const mm16_shape sh = mm16_choose(mode, a->M, 1, nslices, kp, s->cus);
+    void *xs = nullptr;
+    if (!sh.xl) {   // the distinct activation rows, converted once
+        const int64_t rows = a->ne11 * a->n_tokens;
+        if (int rc = scratch(s, (size_t)std::max<int64_t>(1, rows * kp) * 2, &xs)) return rc;
+        if (kp > 0) {
+            hipLaunchKernelGGL(k_act<0>, dim3(grid_for(kp, 2), (unsigned)rows), dim3(k_block), 0, st, a->x, xld, xld,
+                               xs, (int64_t)1, a->K, kp, s->T.cvt16);
+            LNSHIP_HIP(hipGetLastError());
+        }
+    }
+    mm_args16 m{(const uint16_t *)a->w, (const uint16_t *)xs, a->x, a->dst, a->K, kp, a->M, 1, xld, xld,
+                1, a->n_expert_used, 1, 1, a->M, kp * a->M, a->M, a->M,
+                a->monte_seed, a->monte_state, a->monte_offset,
+                a->ids, a->ids_ld ? a->ids_ld : a->n_expert_used, a->ne11, a->n_expert, s->index_err};
+    switch (mode) {
+        case LNSHIP_BASE: return dispatch_mm16<LNSHIP_BASE>(m, s->T, nslices, sh, st);
+        case LNSHIP_MONTE: return dispatch_mm16<LNSHIP_MONTE>(m, s->T, nslices, sh, st);
+        case LNSHIP_LPVIP: return dispatch_mm16<LNSHIP_LPVIP>(m, s->T, nslices, sh, st);
+        default: return dispatch_mm16<LNSHIP_SUM32>(m, s->T, nslices, sh, st);
+    }
+}
+
+int lnship32_mul_mat_id(const lnship_mul_mat_id_args *a, void *stream) {
+    device_state *s = state();
+    if (!s) return LNSHIP_ENOINIT;
+    if (int rc = check_mm_id(a)) return rc;
+    const int64_t nslices = a->n_expert_used * a->n_tokens;
+    if (a->M == 0 || nslices == 0) return 0;
+    const int64_t kp = (a->K + 7) & ~(int64_t)7, xld = a->x_ld ? a->x_ld : a->K;
+    const int64_t rows = a->ne11 * a->n_tokens;
+    void *xs = nullptr;
+    if (int rc = scratch(s, (size_t)std::max<int64_t>(1, rows * kp) * 4, &xs)) return rc;
+    hipStream_t st = (hipStream_t)stream;
+    if (kp > 0) {
+        hipLaunchKernelGGL(k_act<1>, dim3(grid_for(kp, 2), (unsigned)rows), dim3(k_block), 0, st, a->x, xld, xld, xs,
+                           (int64_t)1, a->K, kp, s->T.cvt16);
+        LNSHIP_HIP(hipGetLastError());
+    }
+    mm_args32 m{(const uint32_t *)a->w, (const uint32_t *)xs, a->dst, a->K, kp, a->M, 1,
+                1, a->n_expert_used, 1, 1, a->M, kp * a->M, a->M, a->M,
+                a->ids, a->ids_ld ? a->ids_ld : a->n_expert_used, a->ne11, a->n_expert, s->index_err};
+    const mm16_shape sh = mm_shape_x32(m.M, 1, nslices, kp, s->cus, 4);
+    switch (sh.nc * 10 + sh.cg) {
+        case 12: return launch_mm32<1, 2>(m, s->T, nslices, st);
+        case 14: return launch_mm32<1, 4>(m, s->T, nslices, st);
+        default: return launch_mm32<1, 1>(m, s->T, nslices, st);
+    }
+}
+
+uint64_t lnship16_mul_mat_id_draws(int mode, int64_t K, int64_t M, int64_t n_expert_used, int64_t n_tokens) {
+    if (mode != LNSHIP_MONTE || K <= 0) return 0;
+    return (uint64_t)n_expert_used * (uint64_t)n_tokens * (uint64_t)M * (uint64_t)(K - 1);
+}
 
 static int rms16_common(int mode, const float *src, float *dst, int64_t ncols, int64_t nrows, float eps,
                         uint16_t monte_seed, const uint16_t *monte_state, uint64_t monte_offset, void *stream) {

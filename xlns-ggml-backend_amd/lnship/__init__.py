@@ -38,6 +38,13 @@ class SoftMaxArgs(ctypes.Structure):
                 ("monte_state", c_p), ("monte_offset", ctypes.c_uint64)]
 
 
+class MulMatIdArgs(ctypes.Structure):
+    _fields_ = [("w", c_p), ("x", c_p), ("ids", c_p), ("dst", c_p), ("K", c_i64), ("M", c_i64),
+                ("n_expert", c_i64), ("n_expert_used", c_i64), ("n_tokens", c_i64), ("ne11", c_i64),
+                ("x_ld", c_i64), ("ids_ld", c_i64), ("monte_seed", ctypes.c_uint16),
+                ("monte_state", c_p), ("monte_offset", ctypes.c_uint64)]
+
+
 def build():
     import subprocess
     subprocess.check_call(["make", "-s", "-C", PKG_DIR])
@@ -76,6 +83,9 @@ def lib():
         "lnship16_rms_norm_draws": (ctypes.c_uint64, [ctypes.c_int, c_i64, c_i64]),
         "lnship_lfsr_jump": (ctypes.c_uint16, [ctypes.c_uint16, ctypes.c_uint64]),
         "lnship_lfsr_advance": (ctypes.c_int, [c_p, ctypes.c_uint64, c_p]),
+        "lnship16_mul_mat_id": (ctypes.c_int, [ctypes.c_int, ctypes.POINTER(MulMatIdArgs), c_p]),
+        "lnship32_mul_mat_id": (ctypes.c_int, [ctypes.POINTER(MulMatIdArgs), c_p]),
+        "lnship16_mul_mat_id_draws": (ctypes.c_uint64, [ctypes.c_int, c_i64, c_i64, c_i64, c_i64]),
         "lnship16_scale": (ctypes.c_int, [c_p, c_p, c_i64, ctypes.c_float, ctypes.c_float, c_p]),
         "lnship32_scale": (ctypes.c_int, [c_p, c_p, c_i64, ctypes.c_float, ctypes.c_float, c_p]),
         "lnship_copy": (ctypes.c_int, [c_p, ctypes.c_int, c_p, c_p, c_p, ctypes.c_int, c_p, c_p, c_p]),
@@ -270,6 +280,27 @@ def mul_mat32(wp, x, K, M, ne02=1, ne03=1, out=None):
         out = torch.empty(x.shape[:-1] + (M,), dtype=torch.float32, device=x.device)
     a = _mm_args(wp, x, out, K, M, ne02, ne03, 0)
     check(lib().lnship32_mul_mat(ctypes.byref(a), _stream()))
+    return out
+
+
+def mul_mat_id(mode, wp, x, ids, K, M, n_expert, seed=7, out=None):
+    """MUL_MAT_ID: wp packed experts (pack16 / pack32 of [n_expert, M, K]),
+    x [T, ne11, K] float32, ids [T, n_expert_used] int32 (device) ->
+    [T, n_expert_used, M] float32.  mode None: xlns32."""
+    import torch
+    init()
+    x = x.contiguous()
+    ids = ids.contiguous()
+    T, ne11 = x.shape[0], x.shape[1]
+    neu = ids.shape[1]
+    if out is None:
+        out = torch.empty((T, neu, M), dtype=torch.float32, device=x.device)
+    sd, st, off = seed_fields(seed)
+    a = MulMatIdArgs(_p(wp), _p(x), _p(ids), _p(out), K, M, n_expert, neu, T, ne11, 0, 0, sd, st, off)
+    if mode is None:
+        check(lib().lnship32_mul_mat_id(ctypes.byref(a), _stream()))
+    else:
+        check(lib().lnship16_mul_mat_id(mode, ctypes.byref(a), _stream()))
     return out
 
 
