@@ -9,7 +9,7 @@ a fused QKV MUL_MAT on F32 weights, RoPE on a strided view of it, the GQA kq
 MUL_MAT on an F16 KV-cache tensor against a permuted view, a masked
 SOFT_MAX, a Q8_0-weight MUL_MAT, SWIGLU fused and split, ADD with flat and
 general broadcasts, an F16-weight MUL_MAT, a repeated MUL_MAT that hits the
-weight cache, and an unmasked SOFT_MAX.  The oracle runs the same ops in
+weight cache, an unmasked SOFT_MAX and a MUL_MAT_ID over six experts.  The oracle runs the same ops in
 graph order, so Monte draws are reserved in the same sequence.
 
 With --policy the backend runs under LNS16_SUM_POLICY and the oracle takes
@@ -132,6 +132,9 @@ def run16(mode_name, policy=None, dev=False):
     x1 = f32(T, 1536)
     w2 = (rng.standard_normal((E, 1536)) * 0.02).astype(np.float16)
     z = f32(2, 5, 100, scale=3.0)
+    wmoe = f32(6, 96, 64, scale=0.05)
+    xmoe = f32(T, 1, 64)
+    ids_moe = np.array([[5, 0], [2, 2], [1, 4]], np.int32)
 
     t = lambda *a, **k: h.tensor(*a, device=None if k.get("weights") else act, **k)
     tw = lambda *a, **k: h.tensor(*a, device=wts, **k)
@@ -146,6 +149,9 @@ def run16(mode_name, policy=None, dev=False):
     X1 = t([1536, T], data=x1, name="ffn_inp")
     W2 = tw([1536, E], "f16", data=w2, weights=True, name="blk.0.ffn_down.weight")
     Z = t([100, 5, 2], data=z, name="scores")
+    WMOE = tw([64, 96, 6], data=wmoe, weights=True, name="blk.0.ffn_up_exps.weight")
+    XMOE = t([64, 1, T], data=xmoe, name="ffn_moe_inp")
+    IDS = t([2, T], "i32", data=ids_moe, name="ffn_moe_topk")
     swi = h.stub.ggml_host_glu(b"SWIGLU")
 
     nodes = {}
@@ -173,8 +179,9 @@ def run16(mode_name, policy=None, dev=False):
     nodes["down"] = t([E, T], op="MUL_MAT", src=(W2, X1), name="ffn_out-0")
     nodes["qkv_again"] = t([E + 2 * HKV * D, T], op="MUL_MAT", src=(WQKV, nodes["mul"]), name="qkv-1")
     nodes["softmax_nomask"] = t([100, 5, 2], op="SOFT_MAX", src=(Z,), fparams={0: 1.0, 1: 0.0}, name="sm-1")
+    nodes["moe"] = t([96, 2, T], op="MUL_MAT_ID", src=(WMOE, XMOE, IDS), name="ffn_moe_up-0")
     order = ["rms", "mul", "qkv", "view_q", "rope", "perm_q", "kq", "softmax", "ug", "swiglu", "view_g", "view_u",
-             "swiglu_split", "add", "add_bcast", "down", "qkv_again", "softmax_nomask"]
+             "swiglu_split", "add", "add_bcast", "down", "qkv_again", "softmax_nomask", "moe"]
     views = {"view_q": qv, "perm_q": qp, "view_g": ga, "view_u": ua}
     graph = [views[k] if k in views else nodes[k] for k in order]
 
@@ -208,6 +215,7 @@ def run16(mode_name, policy=None, dev=False):
     want["down"] = O.mul_mat16_f32w(mode_of("MUL_MAT", "ffn_out-0"), w2.astype(np.float32), x1)
     want["qkv_again"] = O.mul_mat16(mode_of("MUL_MAT", "qkv-1"), O.f2x16(wqkv), want["mul"])
     want["softmax_nomask"] = O.soft_max16(mode_of("SOFT_MAX", "sm-1"), z, None, 1.0)
+    want["moe"] = O.mul_mat_id(mode_of("MUL_MAT_ID", "ffn_moe_up-0"), wmoe, xmoe, ids_moe)
 
     report = {}
     for k, tn in nodes.items():
@@ -238,6 +246,9 @@ def run32(dev=False):
     res = f32(T, M)
     qk = f32(T, H, D)
     pos = np.array([7, 300], np.int32)
+    wmoe = f32(4, 40, 256, scale=0.05)
+    xmoe = f32(T, 2, 256)
+    ids_moe = np.array([[3, 0], [1, 1]], np.int32)
     act = h.device_buffer(32 << 20, w32=True) if dev else None
     t = lambda *a, **k: h.tensor(*a, device=act, **k)
     X = t([K, T], data=x, name="inp")
@@ -248,6 +259,9 @@ def run32(dev=False):
     RES = t([M, T], data=res, name="res")
     QK = t([D, H, T], data=qk, name="q")
     POS = t([T], "i32", data=pos, name="inp_pos")
+    WMOE = t([256, 40, 4], data=wmoe, weights=True, name="blk.0.ffn_up_exps.weight")
+    XMOE = t([256, 2, T], data=xmoe, name="ffn_moe_inp")
+    IDS = t([2, T], "i32", data=ids_moe, name="ffn_moe_topk")
     swi = h.stub.ggml_host_glu(b"SWIGLU")
     nodes = {"rms": t([K, T], op="RMS_NORM", src=(X,), fparams={0: 1e-6}, name="norm-0")}
     nodes["mul"] = t([K, T], op="MUL", src=(nodes["rms"], Gw), name="attn_norm-0")
@@ -257,6 +271,7 @@ def run32(dev=False):
     nodes["rope"] = t([D, H, T], op="ROPE", src=(QK, POS), params=(0, D, 0),
                       fparams={5: 10000.0, 6: 1.0, 7: 0.0, 8: 1.0}, name="Qcur-0")
     nodes["softmax"] = t([200, T, 4], op="SOFT_MAX", src=(KQ, MASK), fparams={0: 0.125, 1: 0.0}, name="sm-0")
+    nodes["moe"] = t([40, 2, T], op="MUL_MAT_ID", src=(WMOE, XMOE, IDS), name="ffn_moe_up-0")
     be = h.init(w32=True)
     if be is None:
         print(json.dumps({"error": "no GPU: LNSHIP32 init returned NULL"}))
@@ -269,6 +284,7 @@ def run32(dev=False):
     want["swiglu"] = O.swiglu32(want["add"][:, :M // 2], want["add"][:, M // 2:])
     want["rope"] = O.rope32(qk, pos, D, 0, 10000.0)
     want["softmax"] = O.soft_max32(kq, mask, 0.125)
+    want["moe"] = O.mul_mat_id(None, wmoe, xmoe, ids_moe)
     report = {}
     for k, tn in nodes.items():
         got = h.f32_of(tn, act).reshape(want[k].shape)

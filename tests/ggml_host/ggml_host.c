@@ -14,7 +14,7 @@
 /* ---- ops -------------------------------------------------------------- */
 static const char *const k_ops[] = {"NONE", "DUP", "ADD", "MUL", "DIV", "SCALE", "RMS_NORM", "MUL_MAT", "SOFT_MAX",
                                     "ROPE", "GLU", "UNARY", "RESHAPE", "VIEW", "PERMUTE", "TRANSPOSE", "GET_ROWS",
-                                    "CPY", "CONT", "SET_ROWS"};
+                                    "CPY", "CONT", "SET_ROWS", "MUL_MAT_ID"};
 static const char *const k_glu[] = {"REGLU", "GEGLU", "SWIGLU"};
 static const char *const k_unary[] = {"ABS", "NEG", "TANH", "RELU", "GELU", "SILU"};
 #define N_OPS ((int)(sizeof k_ops / sizeof k_ops[0]))

@@ -149,6 +149,12 @@ def _verdicts(h, w32=False):
     cases["rope_odd_dims"] = f(ne=[64, 9, 3], op="ROPE", src=(q, pos), params=(0, 63, 0), fparams=rp)
     cases["view"] = f(ne=[576, 3], op="VIEW", src=(x,))
     cases["get_rows"] = f(ne=[576, 3], op="GET_ROWS", src=(x, pos))
+    wexp = h.tensor([576, 256, 8], "q8_0", weights=True, name="blk.0.ffn_up_exps.weight")
+    xe = f(ne=[576, 1, 3])
+    cases["mm_id"] = f(ne=[256, 2, 3], op="MUL_MAT_ID", src=(wexp, xe, f(ne=[2, 3], type_name="i32")))
+    cases["mm_id_i64_ids"] = f(ne=[256, 2, 3], op="MUL_MAT_ID", src=(wexp, xe, f(ne=[2, 3], type_name="i64")))
+    cases["mm_id_bad_bcast"] = f(ne=[256, 3, 3], op="MUL_MAT_ID",
+                                 src=(wexp, f(ne=[576, 2, 3]), f(ne=[3, 3], type_name="i32")))
     cases["scale"] = f(ne=[576, 3], op="SCALE", src=(x,), fparams={0: 0.125, 1: 0.0})
     xt = f(ne=[3, 576], nb=[4 * 576, 4, 4 * 576 * 3, 4 * 576 * 3])
     cases["scale_strided"] = f(ne=[3, 576], op="SCALE", src=(xt,), fparams={0: 0.125, 1: 0.0})
@@ -190,6 +196,9 @@ EXPECT16 = {
     "rope_odd_dims": (False, "lnship_rope_requires_even_n_dims"),
     "view": (True, "supported_view_or_noop"),
     "get_rows": (False, "lnship_get_rows_requires_hbm_dst"),
+    "mm_id": (True, "lnship_mul_mat_id"),
+    "mm_id_i64_ids": (False, "mul_mat_id_requires_src1_f32_and_i32_ids_and_convertible_src0"),
+    "mm_id_bad_bcast": (False, "lnship_mul_mat_id_shape"),
     "scale": (True, "requires_contiguous_f32_src0_and_dst"),
     "scale_strided": (False, "requires_contiguous_f32_src0_and_dst"),
     "cpy": (False, "lnship_copy_requires_hbm_dst"),
@@ -207,7 +216,8 @@ def test_lnship32_claims(host):
     # the xlns32 backend runs the hot ops and the Llama graph's elementwise
     # ops (cuda/lns-cuda-kernels.cuh:161-355 instantiate them for xlns32 too)
     got = _verdicts(host, w32=True)
-    for k in ("mm_f32", "mm_q8_0", "mm_gqa", "rms", "softmax", "view", "add_bcast", "swiglu_fused", "rope", "scale"):
+    for k in ("mm_f32", "mm_q8_0", "mm_gqa", "rms", "softmax", "view", "add_bcast", "swiglu_fused", "rope", "scale",
+              "mm_id"):
         assert got[k][0], (k, got[k])
     for k in ("geglu", "silu", "get_rows", "cpy", "set_rows"):
         assert not got[k][0], (k, got[k])

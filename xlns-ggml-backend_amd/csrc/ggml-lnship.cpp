@@ -387,14 +387,15 @@ static void scatter_f32(const float *in, ggml_tensor *t) {
 static bool on_device(const ggml_tensor *t);
 static bool device_buffers();
 
-enum class kind { view, mul_mat, rms_norm, soft_max, add, mul, swiglu, rope, scale, copy, get_rows, set_rows, unary,
-                  glu, other };
+enum class kind { view, mul_mat, mul_mat_id, rms_norm, soft_max, add, mul, swiglu, rope, scale, copy, get_rows,
+                  set_rows, unary, glu, other };
 
 static kind classify(const ggml_tensor *t) {
     const char *n = ggml_op_name(t->op);
     auto is = [n](const char *s) { return std::strcmp(n, s) == 0; };
     if (is("NONE") || is("RESHAPE") || is("VIEW") || is("PERMUTE") || is("TRANSPOSE")) return kind::view;
     if (is("MUL_MAT")) return kind::mul_mat;
+    if (is("MUL_MAT_ID")) return kind::mul_mat_id;
     if (is("RMS_NORM")) return kind::rms_norm;
     if (is("SOFT_MAX")) return kind::soft_max;
     if (is("ADD")) return kind::add;
@@ -432,6 +433,26 @@ static verdict check_mul_mat(const ggml_tensor *op) {
     if (b->ne[2] % a->ne[2] != 0 || b->ne[3] % a->ne[3] != 0) return {false, "lnship_mul_mat_requires_whole_broadcast"};
     if (a->ne[0] > ((int64_t)1 << 30)) return {false, "lnship_mul_mat_k_too_large"};
     return {true, "lnship_mul_mat"};
+}
+
+// common/lns-op-support.h:43-50 plus the GEMV's limits (as check_mul_mat)
+static verdict check_mul_mat_id(const ggml_tensor *op) {
+    const ggml_tensor *a = op->src[0], *b = op->src[1], *ids = op->src[2];
+    if (!b || !is_f32(b) || !ids || !type_is(ids, "i32") || !to_f32_possible(a))
+        return {false, "mul_mat_id_requires_src1_f32_and_i32_ids_and_convertible_src0"};
+    if (on_device(a) && !is_f32(a) && !is_f16(a)) return {false, "lnship_device_src0_requires_f32_or_f16"};
+    if (!rows_contiguous(a) || !rows_contiguous(b)) return {false, "mul_mat_requires_contiguous_rows"};
+    if (!is_f32(op)) return {false, "lnship_mul_mat_requires_f32_dst"};
+    const int64_t neu = ids->ne[0], T = ids->ne[1];
+    if (a->ne[3] != 1 || b->ne[3] != 1 || ids->ne[2] != 1 || ids->ne[3] != 1 || b->ne[0] != a->ne[0] ||
+        b->ne[2] != T || b->ne[1] <= 0 || neu % b->ne[1] != 0 || op->ne[0] != a->ne[1] || op->ne[1] != neu ||
+        op->ne[2] != T)
+        return {false, "lnship_mul_mat_id_shape"};
+    if (on_device(ids) && (ids->nb[0] != 4 || ids->nb[1] % 4 != 0))
+        return {false, "lnship_mul_mat_id_requires_dense_device_ids"};
+    if (neu * T > 65535) return {false, "lnship_mul_mat_id_too_many_slots"};
+    if (a->ne[0] > ((int64_t)1 << 30)) return {false, "lnship_mul_mat_k_too_large"};
+    return {true, "lnship_mul_mat_id"};
 }
 
 static verdict check_rms_norm(const ggml_tensor *op, bool w32) {
@@ -556,6 +577,7 @@ static verdict check_node(const ggml_tensor *op, bool w32) {
     switch (classify(op)) {
         case kind::view: return {true, "supported_view_or_noop"};
         case kind::mul_mat: return check_mul_mat(op);
+        case kind::mul_mat_id: return check_mul_mat_id(op);
         case kind::rms_norm: return check_rms_norm(op, w32);
         case kind::soft_max: return check_soft_max(op, w32);
         case kind::add:
@@ -1562,9 +1584,38 @@ static void op_set_rows(context &ctx, ggml_tensor *dst) {
            "lnship_set_rows");
 }
 
+// lns_mul_mat_id (src/lns-ops.cpp:394-462), lns32_mul_mat_id (src32/lns32-ops.cpp:154-215)
+static void op_mul_mat_id(context &ctx, ggml_tensor *dst) {
+    const ggml_tensor *a = dst->src[0], *b = dst->src[1], *ids = dst->src[2];
+    lnship_mul_mat_id_args args;
+    std::memset(&args, 0, sizeof args);
+    args.w = ctx.lns_matrix(a);   // the experts, packed slice by slice
+    args.x = ctx.upload(b, R_SRC1);
+    int64_t ine[3], inb[3];
+    args.ids = (const int32_t *)device_ids<int32_t>(ctx, ids, a->ne[2], ine, inb);
+    args.dst = ctx.out_f32(dst, R_DST);
+    args.K = a->ne[0];
+    args.M = a->ne[1];
+    args.n_expert = a->ne[2];
+    args.n_expert_used = ids->ne[0];
+    args.n_tokens = ids->ne[1];
+    args.ne11 = b->ne[1];
+    args.ids_ld = inb[1] / 4;
+    if (ctx.fmt->w32) {
+        lib_ok(lnship32_mul_mat_id(&args, ctx.get_stream()), "lnship32_mul_mat_id");
+    } else {
+        const int mode = node_mode(dst);
+        args.monte_seed = reserve_monte(
+            mode, lnship16_mul_mat_id_draws(mode, args.K, args.M, args.n_expert_used, args.n_tokens));
+        lib_ok(lnship16_mul_mat_id(mode, &args, ctx.get_stream()), "lnship16_mul_mat_id");
+    }
+    ctx.download(args.dst, dst);
+}
+
 static void run_node(context &ctx, ggml_tensor *node) {
     switch (classify(node)) {
         case kind::mul_mat: return op_mul_mat(ctx, node);
+        case kind::mul_mat_id: return op_mul_mat_id(ctx, node);
         case kind::rms_norm: return op_rms_norm(ctx, node);
         case kind::soft_max: return op_soft_max(ctx, node);
         case kind::add: return op_binary<false>(ctx, node);
