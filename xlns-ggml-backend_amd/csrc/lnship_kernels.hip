@@ -28,7 +28,10 @@ constexpr int k_max_devices = 64;
 // LDS budget of a workgroup on gfx950 (160 KiB per CU)
 constexpr int k_lds_bytes = 160 * 1024;
 // the xlns32 tables plus four zero entries (an interpolation on them gives 0)
-constexpr int k_lds_tab32 = (k32_tab_n + 4) * 4;   // 108320 bytes
+// the xlns32 tables, a zero pair, and 512 (origin, shift) descriptors of the
+// direct interpolation grid, indexed by (opposite signs, binade of d)
+constexpr int k32_desc_n = 512;
+constexpr int k_lds_tab32 = (k32_tab_n + 4 + 2 * k32_desc_n) * 4;   // 112416 bytes
 
 static thread_local std::string t_err;
 
@@ -299,13 +302,13 @@ constexpr uint32_t kb_dbf = (uint32_t)(k32_off_dbf - (int)(k32_db_end >> k32_db_
 // grid origin), computed once per kernel; the empty asm keeps them opaque
 // registers, so that picking a table is one select and no base add follows.
 struct x32_tab {
-    uint32_t dlo, dhi, sb, sbf, db, dbf, zero;
+    uint32_t dlo, dhi, sb, sbf, db, dbf, zero, desc;
 };
 __device__ __forceinline__ x32_tab x32_origins(const int32_t *T) {
     uint32_t tb = lds_addr(T);
     asm("" : "+v"(tb));
     x32_tab o{tb + (uint32_t)k32_off_dlo * 4, tb + (uint32_t)k32_off_dhi * 4, tb + kb_sb, tb + kb_sbf, tb + kb_db,
-              tb + kb_dbf, tb + (uint32_t)k32_tab_n * 4};
+              tb + kb_dbf, tb + (uint32_t)k32_tab_n * 4, tb + (uint32_t)(k32_tab_n + 4) * 4};
     // each origin its own register: a select among them stays a select (not
     // a lookup table of their constant offsets)
     asm("" : "+v"(o.sb), "+v"(o.sbf), "+v"(o.db), "+v"(o.dbf), "+v"(o.zero));
@@ -363,49 +366,49 @@ __device__ __forceinline__ uint32_t sel(bool c, uint32_t a, uint32_t b) { return
 
 // The same addition ordered for one chain per lane, where every instruction
 // of the wave is on the chain's clock (a single wave issues about one
-// instruction per 2 ns, and an LDS round trip hides about ten).  The
-// direct interpolation node (at d) is complete before the first lookups
-// return; lanes that take no interpolation point it at the zero pair after
-// the tables, so no select follows the second lookup.  The cotransformation
-// point e always lies on the sb tables (clamped at esszer, whose far node is
-// 0).  What the tail needs but the second lookup's address does not, and the
-// caller's `shadow` work (the next product), fill the second round trip.
+// instruction per 2 ns).  Two rounds of LDS lookups: the cotransformation's
+// dlo[dl] and (dh << 12) + dhi[dh], and beside them a descriptor of the
+// direct interpolation at d, (origin, grid shift) of the sb / db table that
+// d uses or the zero pair where d takes none (the cotransformation region,
+// shift 30, and beyond the essential zero, shift 31); then the pair of grid
+// nodes, at e on the sb tables for the cotransformation, else at d.  The
+// dl = 0 sentinel puts e beyond the essential zero, where the sb tables read
+// 0, so every cotransformation lane with dh != 0 interpolates at e.  The
+// larger log, the result's sign and the caller's `shadow` work (the next
+// product) fill the first round trip; what the tail needs the second.
 // Scheduling barriers keep the groups in this order.
 template <class F>
-__device__ __forceinline__ void x32_add_lat(const x32_tab &O, acc_ls &a, uint32_t tl, uint32_t ts, F &&shadow) {
+__device__ __forceinline__ void x32_add_desc(const x32_tab &O, acc_ls &a, uint32_t tl, uint32_t ts, F &&shadow) {
     const uint32_t d = absdiff(a.l, tl);
+    const uint32_t u = a.s ^ ts;
     const uint32_t dl = d & ((1u << k32_co_sh) - 1u), dh = (d >> k32_co_sh) & ((1u << k32_co_sh) - 1u);
     const int32_t lo = lds_ld(lshl2_add(dl, O.dlo));    // dlo[dl]
     const int32_t th2 = lds_ld(lshl2_add(dh, O.dhi));   // (dh << 12) + dhi[dh]
+    const uint32_t dsc = (__builtin_amdgcn_ubfe(d | u, 23, 9) << 3) + O.desc;
+    const uint32_t base_d = (uint32_t)lds_ld(dsc), sh_d = (uint32_t)lds_ld(dsc + 4);
     __builtin_amdgcn_sched_barrier(0);
-    const bool usedb = a.s != ts;
-    const bool co = usedb && d < k32_co_end;
-    const bool direct_db = usedb && !(d < k32_co_end);
-    const bool at_e = co && dh != 0 && dl != 0;
-    const bool keep_d = !co && d < k32_esszer;
-    const bool hi_d = d >= (direct_db ? k32_db_end : k32_sb_end);
-    const int sh_d = hi_d ? k32_sb_fsh : k32_sb_sh;   // sb and db share both grids
-    const uint32_t base_d = sel(hi_d, sel(direct_db, O.dbf, O.sbf), sel(direct_db, O.db, O.sb));
-    const uint32_t nd = lshl2_add(d >> sh_d, base_d);   // (an asm call in a ternary arm would become a branch)
-    const uint32_t node_d = sel(keep_d, nd, O.zero);
+    uint32_t mx = max(a.l, tl);
+    uint32_t nsign = (d == 0 && u != 0) ? 0u : (a.l > tl ? a.s : ts);
+    shadow();
+    asm volatile("" : "+v"(mx), "+v"(nsign));
     __builtin_amdgcn_sched_barrier(0);
-    const uint32_t e = (uint32_t)th2 - (uint32_t)lo;   // wraps for the dl = 0 sentinel (unused then)
+    const bool co = sh_d == 30;
+    const bool at_e = co && dh != 0;
+    const uint32_t e = (uint32_t)th2 - (uint32_t)lo;
     const uint32_t xe = min(e, k32_esszer);
     const bool hi_e = e >= k32_sb_end;
     const int sh_e = hi_e ? k32_sb_fsh : k32_sb_sh;
     const uint32_t ne = lshl2_add(xe >> sh_e, sel(hi_e, O.sbf, O.sb));
-    const uint32_t node = sel(at_e, ne, node_d);
+    const uint32_t nd = lshl2_add(d >> sh_d, base_d);
+    const uint32_t node = sel(at_e, ne, nd);
     const int32_t t0 = lds_ld(node), t1 = lds_ld(node + 4);
     __builtin_amdgcn_sched_barrier(0);
-    const uint32_t mx = max(a.l, tl);
     const int32_t th = th2 - (int32_t)(dh << k32_co_sh);
     const int32_t mA = (int32_t)mx + (co ? (dh == 0 ? lo : th) : 0);
-    const int sh = at_e ? sh_e : sh_d;
-    const int32_t frac = (int32_t)((at_e ? xe : d) & ((1u << sh) - 1u));
-    const uint32_t nsign = (d == 0 && usedb) ? 0u : (a.l > tl ? a.s : ts);
-    shadow();
+    const uint32_t sh = at_e ? (uint32_t)sh_e : sh_d;
+    const int32_t frac = (int32_t)__builtin_amdgcn_ubfe(at_e ? xe : d, 0, sh);
     __builtin_amdgcn_sched_barrier(0);
-    const int32_t ip = t0 + (mul_i24(t1 - t0, frac) >> sh);
+    const int32_t ip = t0 + (__mul24(t1 - t0, frac) >> sh);
     a.l = (uint32_t)max(__builtin_elementwise_add_sat(mA, ip), 0);
     a.s = nsign;
 }
@@ -430,7 +433,7 @@ struct red16<LNSHIP_SUM32> {
     // operands already widened (log and sign moved to the xlns32 positions)
     template <class F>
     __device__ __forceinline__ void add_lat(acc_t &a, uint32_t tl32, uint32_t ts32, F &&shadow) const {
-        x32_add_lat(O, a, tl32, ts32, shadow);
+        x32_add_desc(O, a, tl32, ts32, shadow);
     }
     __device__ __forceinline__ void add(acc_t &a, uint32_t v, uint32_t &st) const { add_ls(a, v & k16_logmask, v & k16_sign, st); }
     __device__ __forceinline__ uint32_t finish(const acc_t &a) const {
@@ -523,6 +526,30 @@ __device__ __forceinline__ red16<LNSHIP_SUM32> stage_tables<LNSHIP_SUM32>(const 
     if (threadIdx.x < 4) t[k32_tab_n + threadIdx.x] = 0;   // the zero pair
     // dhi[dh] -> (dh << 12) + dhi[dh], the first half of the cotransformation's e
     for (int i = 1 + threadIdx.x; i < k32_co_n; i += blockDim.x) t[k32_off_dhi + i] += i << k32_co_sh;
+    // descriptor of key = (opposite signs) << 8 | (d >> 23): where the direct
+    // interpolation at d reads (origin, grid shift).  Keys with no direct
+    // interpolation point at the zero pair with a shift that empties d >> sh:
+    // 30 below two binades of opposite signs (the cotransformation), 31 from
+    // the essential zero on.
+    {
+        const uint32_t tb = lds_addr(t), zero = tb + (uint32_t)k32_tab_n * 4;
+        for (int k = threadIdx.x; k < k32_desc_n; k += blockDim.x) {
+            const uint32_t q = (uint32_t)k & 255u;
+            uint32_t base = zero, sh = 31;
+            if (k < 256) {
+                if (q < (k32_sb_end >> 23)) base = tb + kb_sb, sh = k32_sb_sh;
+                else if (q < (k32_esszer >> 23)) base = tb + kb_sbf, sh = k32_sb_fsh;
+            } else if (q < (k32_co_end >> 23)) {
+                sh = 30;
+            } else if (q < (k32_db_end >> 23)) {
+                base = tb + kb_db, sh = k32_db_sh;
+            } else if (q < (k32_esszer >> 23)) {
+                base = tb + kb_dbf, sh = k32_db_fsh;
+            }
+            t[k32_tab_n + 4 + 2 * k] = (int32_t)base;
+            t[k32_tab_n + 4 + 2 * k + 1] = (int32_t)sh;
+        }
+    }
     return red16<LNSHIP_SUM32>{x32_origins(t)};
 }
 template <>
@@ -844,7 +871,7 @@ __global__ __launch_bounds__(k_block * CG) void k_mm32(mm_args32 a, dev_tables T
                         acc[0] = {t & k32_logmask, t & k32_sign};
                         next();
                     } else {
-                        x32_add_lat(R.O, acc[0], t & k32_logmask, t & k32_sign, next);
+                        x32_add_desc(R.O, acc[0], t & k32_logmask, t & k32_sign, next);
                     }
                     t = tn;
                 }
@@ -918,7 +945,14 @@ __device__ __forceinline__ void chain16(const RED &R, typename RED::acc_t &acc, 
         const uint32_t w[4] = {q.x, q.y, q.z, q.w};
 #pragma unroll
         for (int u = 0; u < 8; u++)
-            if (u >= u0 && u < u1) R.add(acc, half16(w[u >> 1], u & 1), st);
+            if (u >= u0 && u < u1) {
+                if constexpr (std::is_same<RED, red16<LNSHIP_SUM32>>::value) {
+                    const uint32_t v = half16(w[u >> 1], u & 1);
+                    R.add_lat(acc, (v & k16_logmask) << 16, (v & k16_sign) << 16, [] {});
+                } else {
+                    R.add(acc, half16(w[u >> 1], u & 1), st);
+                }
+            }
     };
     uint4 cur = ld(g0), nxt = ld(g0 + 1);
     run(cur, i0 - 8 * g0, min(n - 8 * g0, 8));
@@ -938,7 +972,9 @@ __device__ __forceinline__ void chain32(const x32_tab &O, acc_ls &acc, const uin
         const uint32_t w[4] = {q.x, q.y, q.z, q.w};
 #pragma unroll
         for (int u = 0; u < 4; u++)
-            if (u >= u0 && u < u1) x32_add_ls(O, acc, w[u] & k32_logmask, w[u] & k32_sign);
+            if (u >= u0 && u < u1) {
+                x32_add_desc(O, acc, w[u] & k32_logmask, w[u] & k32_sign, [] {});
+            }
     };
     uint4 cur = ld(g0), nxt = ld(g0 + 1);
     run(cur, i0 - 4 * g0, min(n - 4 * g0, 4));
