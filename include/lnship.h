@@ -59,11 +59,14 @@ int lnship16_to_f32(const uint16_t *src, float *dst, int64_t n, void *stream);
 int lnship32_from_f32(const float *src, uint32_t *dst, int64_t n, void *stream);
 int lnship32_to_f32(const uint32_t *src, float *dst, int64_t n, void *stream);
 /* Weight-cache fill (replaces kernel_set::to_lns_transposed, :111-112).
- * nslices slices, each M rows of K values (F32, or IEEE half when
- * src_is_f16), row stride src_ld and slice stride src_slice (elements), into
- * the k8-interleaved cache layout: Kp = K rounded up to a multiple of 8;
- * element (k, m) of a slice at ((k / 8) * M + m) * 8 + k % 8; slices Kp * M
- * codes apart; padding codes are 0. */
+ * nslices slices, each M rows of K values, row stride src_ld and slice
+ * stride src_slice (elements), into the k8-interleaved cache layout:
+ * Kp = K rounded up to a multiple of 8; element (k, m) of a slice at
+ * ((k / 8) * M + m) * 8 + k % 8; slices Kp * M codes apart; padding codes
+ * are 0.  The source type (the parameter src_is_f16): 0 F32, 1 IEEE half,
+ * and for lnship16_pack 2 = xlns16 codes (ggml's GGML_TYPE_LNS16,
+ * patches/ggml-core.patch:21-27, 96-101), copied as they are, as
+ * row_to_xlns16 does (src/lns-ops.cpp:221-225). */
 int lnship16_pack(const void *src, int src_is_f16, int64_t src_ld, int64_t src_slice, uint16_t *dst,
                   int64_t K, int64_t M, int64_t nslices, void *stream);
 int lnship32_pack(const void *src, int src_is_f16, int64_t src_ld, int64_t src_slice, uint32_t *dst,

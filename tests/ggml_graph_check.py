@@ -9,7 +9,8 @@ a fused QKV MUL_MAT on F32 weights, RoPE on a strided view of it, the GQA kq
 MUL_MAT on an F16 KV-cache tensor against a permuted view, a masked
 SOFT_MAX, a Q8_0-weight MUL_MAT, SWIGLU fused and split, ADD with flat and
 general broadcasts, an F16-weight MUL_MAT, a repeated MUL_MAT that hits the
-weight cache, an unmasked SOFT_MAX and a MUL_MAT_ID over six experts.  The oracle runs the same ops in
+weight cache, an unmasked SOFT_MAX, a MUL_MAT_ID over six experts and a
+MUL_MAT on GGML_TYPE_LNS16 weights (xlns16 codes, used as they are).  The oracle runs the same ops in
 graph order, so Monte draws are reserved in the same sequence.
 
 With --policy the backend runs under LNS16_SUM_POLICY and the oracle takes
@@ -135,6 +136,7 @@ def run16(mode_name, policy=None, dev=False):
     wmoe = f32(6, 96, 64, scale=0.05)
     xmoe = f32(T, 1, 64)
     ids_moe = np.array([[5, 0], [2, 2], [1, 4]], np.int32)
+    w_codes = O.f2x16(f32(200, E, scale=0.05))   # GGML_TYPE_LNS16 weights
 
     t = lambda *a, **k: h.tensor(*a, device=None if k.get("weights") else act, **k)
     tw = lambda *a, **k: h.tensor(*a, device=wts, **k)
@@ -150,6 +152,7 @@ def run16(mode_name, policy=None, dev=False):
     W2 = tw([1536, E], "f16", data=w2, weights=True, name="blk.0.ffn_down.weight")
     Z = t([100, 5, 2], data=z, name="scores")
     WMOE = tw([64, 96, 6], data=wmoe, weights=True, name="blk.0.ffn_up_exps.weight")
+    WL16 = tw([E, 200], "lns16", data=w_codes, weights=True, name="blk.0.attn_k_lns16.weight")
     XMOE = t([64, 1, T], data=xmoe, name="ffn_moe_inp")
     IDS = t([2, T], "i32", data=ids_moe, name="ffn_moe_topk")
     swi = h.stub.ggml_host_glu(b"SWIGLU")
@@ -180,8 +183,9 @@ def run16(mode_name, policy=None, dev=False):
     nodes["qkv_again"] = t([E + 2 * HKV * D, T], op="MUL_MAT", src=(WQKV, nodes["mul"]), name="qkv-1")
     nodes["softmax_nomask"] = t([100, 5, 2], op="SOFT_MAX", src=(Z,), fparams={0: 1.0, 1: 0.0}, name="sm-1")
     nodes["moe"] = t([96, 2, T], op="MUL_MAT_ID", src=(WMOE, XMOE, IDS), name="ffn_moe_up-0")
+    nodes["mm_lns16"] = t([200, T], op="MUL_MAT", src=(WL16, nodes["mul"]), name="k_lns16-0")
     order = ["rms", "mul", "qkv", "view_q", "rope", "perm_q", "kq", "softmax", "ug", "swiglu", "view_g", "view_u",
-             "swiglu_split", "add", "add_bcast", "down", "qkv_again", "softmax_nomask", "moe"]
+             "swiglu_split", "add", "add_bcast", "down", "qkv_again", "softmax_nomask", "moe", "mm_lns16"]
     views = {"view_q": qv, "perm_q": qp, "view_g": ga, "view_u": ua}
     graph = [views[k] if k in views else nodes[k] for k in order]
 
@@ -216,6 +220,7 @@ def run16(mode_name, policy=None, dev=False):
     want["qkv_again"] = O.mul_mat16(mode_of("MUL_MAT", "qkv-1"), O.f2x16(wqkv), want["mul"])
     want["softmax_nomask"] = O.soft_max16(mode_of("SOFT_MAX", "sm-1"), z, None, 1.0)
     want["moe"] = O.mul_mat_id(mode_of("MUL_MAT_ID", "ffn_moe_up-0"), wmoe, xmoe, ids_moe)
+    want["mm_lns16"] = O.mul_mat16(mode_of("MUL_MAT", "k_lns16-0"), w_codes, want["mul"])
 
     report = {}
     for k, tn in nodes.items():

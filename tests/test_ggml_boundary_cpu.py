@@ -167,7 +167,7 @@ EXPECT16 = {
     "mm_f32": (True, "lnship_mul_mat"),
     "mm_f16": (True, "lnship_mul_mat"),
     "mm_q8_0": (True, "lnship_mul_mat"),
-    "mm_lns16_src0": (False, "mul_mat_requires_src1_f32_and_convertible_src0"),
+    "mm_lns16_src0": (True, "lnship_mul_mat"),
     "mm_src1_f16": (False, "mul_mat_requires_src1_f32_and_convertible_src0"),
     "mm_strided_rows": (False, "mul_mat_requires_contiguous_rows"),
     "mm_gqa": (True, "lnship_mul_mat"),
@@ -219,7 +219,7 @@ def test_lnship32_claims(host):
     for k in ("mm_f32", "mm_q8_0", "mm_gqa", "rms", "softmax", "view", "add_bcast", "swiglu_fused", "rope", "scale",
               "mm_id"):
         assert got[k][0], (k, got[k])
-    for k in ("geglu", "silu", "get_rows", "cpy", "set_rows"):
+    for k in ("geglu", "silu", "get_rows", "cpy", "set_rows", "mm_lns16_src0"):
         assert not got[k][0], (k, got[k])
     # xlns32 rows take 4 bytes of LDS each
     assert got["rms_long"] == (False, "lnship_row_too_long")

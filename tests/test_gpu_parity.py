@@ -170,6 +170,21 @@ def test_mul_mat_f16_weights(ln):
     same_bits(got, want, "f16 weights")
 
 
+def test_mul_mat_lns16_code_weights(ln):
+    # GGML_TYPE_LNS16 weights: xlns16 codes packed as they are (no F32 round
+    # trip, which would move about half of them)
+    rng = np.random.default_rng(15)
+    K, M, N = 200, 130, 3
+    codes = rng.integers(0, 65536, (M, K)).astype(np.uint16)
+    x = rng.standard_normal((N, K)).astype(np.float32)
+    for mode in MODES:
+        print(f"\n[mul_mat lns16 weights] {mode}", flush=True)
+        O.monte_set(7)
+        want = O.mul_mat16(O.MODES[mode], codes, x)
+        got = host(ln.mul_mat16(O.MODES[mode], ln.pack16(dev(codes.view(np.int16))), dev(x), K, M))
+        same_bits(got, want, f"lns16 weights {mode}")
+
+
 def _sample(n, step):
     return np.unique(np.concatenate([np.arange(0, n, step), [n - 1]]))
 

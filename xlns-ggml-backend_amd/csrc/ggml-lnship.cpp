@@ -423,10 +423,18 @@ static verdict f32_result(const ggml_tensor *op, verdict v) {
 }
 
 // common/lns-op-support.h:33-41 plus cuda/lns-cuda-ops.cpp:37-56
-static verdict check_mul_mat(const ggml_tensor *op) {
+// GGML_TYPE_LNS16 weights (xlns16 codes, patches/ggml-core.patch:21-27) are
+// taken as they are by the xlns16 backend, as row_to_xlns16 does
+// (src/lns-ops.cpp:221-225); the reference's own predicate declines them,
+// since the type has no to_float.
+static bool lns16_codes(const ggml_tensor *t, bool w32) { return !w32 && type_is(t, "lns16"); }
+
+static verdict check_mul_mat(const ggml_tensor *op, bool w32) {
     const ggml_tensor *a = op->src[0], *b = op->src[1];
-    if (!is_f32(b) || !to_f32_possible(a)) return {false, "mul_mat_requires_src1_f32_and_convertible_src0"};
-    if (on_device(a) && !is_f32(a) && !is_f16(a)) return {false, "lnship_device_src0_requires_f32_or_f16"};
+    const bool codes = lns16_codes(a, w32);
+    if (!is_f32(b) || !(codes || to_f32_possible(a))) return {false, "mul_mat_requires_src1_f32_and_convertible_src0"};
+    if (codes && !contiguous(a)) return {false, "lnship_lns16_weights_require_contiguous"};
+    if (on_device(a) && !is_f32(a) && !is_f16(a) && !codes) return {false, "lnship_device_src0_requires_f32_or_f16"};
     if (!rows_contiguous(a) || !rows_contiguous(b)) return {false, "mul_mat_requires_contiguous_rows"};
     if (!is_f32(op)) return {false, "lnship_mul_mat_requires_f32_dst"};
     if ((b->ne[1] + 3) / 4 > 65535 || b->ne[2] * b->ne[3] > 65535) return {false, "lnship_mul_mat_grid_too_large"};
@@ -576,7 +584,7 @@ static verdict check_set_rows(const ggml_tensor *op) {
 static verdict check_node(const ggml_tensor *op, bool w32) {
     switch (classify(op)) {
         case kind::view: return {true, "supported_view_or_noop"};
-        case kind::mul_mat: return check_mul_mat(op);
+        case kind::mul_mat: return check_mul_mat(op, w32);
         case kind::mul_mat_id: return check_mul_mat_id(op);
         case kind::rms_norm: return check_rms_norm(op, w32);
         case kind::soft_max: return check_soft_max(op, w32);
@@ -1170,8 +1178,8 @@ void context::pack(const ggml_tensor *t, void *dst) {
     const int64_t K = t->ne[0], M = t->ne[1], ns = t->ne[2] * t->ne[3], n = nelements(t);
     const void *src;
     int src_f16 = 0;
-    if ((is_f32(t) || is_f16(t)) && contiguous(t)) {
-        src_f16 = is_f16(t);
+    if ((is_f32(t) || is_f16(t) || lns16_codes(t, fmt->w32)) && contiguous(t)) {
+        src_f16 = is_f16(t) ? 1 : type_is(t, "lns16") ? 2 : 0;   // source type of lnship16_pack
         src = on_device(t) ? t->data : upload_raw(t->data, (size_t)n * ggml_type_size(t->type), R_SRC0);
     } else {
         src = upload(t, R_SRC0);

@@ -162,7 +162,7 @@ __device__ __forceinline__ float load_elem(const void *src, int is_f16, int64_t 
 // rows x cols row-major -> k8-interleaved (k = col, m = row), one slice per
 // blockIdx.y; padding columns (cols..Kp) get code 0.
 template <int W32>
-__global__ void k_pack(const void *__restrict__ src, int is_f16, int64_t src_ld, int64_t src_slice,
+__global__ void k_pack(const void *__restrict__ src, int src_type, int64_t src_ld, int64_t src_slice,
                        void *__restrict__ dst, int64_t rows, int64_t cols, int64_t kp,
                        const uint16_t *__restrict__ cvt) {
     const int64_t n = rows * kp;
@@ -170,9 +170,14 @@ __global__ void k_pack(const void *__restrict__ src, int is_f16, int64_t src_ld,
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)blockDim.x * gridDim.x) {
         const int64_t r = i / kp, c = i - r * kp;
         const int64_t o = z * rows * kp + ((c >> 3) * rows + r) * 8 + (c & 7);
+        const bool pad = c >= cols;
+        const int64_t at = z * src_slice + r * src_ld + c;
+        if (!W32 && src_type == 2) {   // xlns16 codes, taken as they are
+            reinterpret_cast<uint16_t *>(dst)[o] = pad ? (uint16_t)0 : reinterpret_cast<const uint16_t *>(src)[at];
+            continue;
+        }
         float v = 0.0f;
-        bool pad = c >= cols;
-        if (!pad) v = load_elem(src, is_f16, z * src_slice + r * src_ld + c);
+        if (!pad) v = load_elem(src, src_type, at);
         if (W32) reinterpret_cast<uint32_t *>(dst)[o] = pad ? 0u : x32_from_f32(v);
         else reinterpret_cast<uint16_t *>(dst)[o] = pad ? (uint16_t)0 : (uint16_t)x16_from_f32(cvt, v);
     }
@@ -1502,6 +1507,7 @@ static int pack_common(int w32, const void *src, int src_is_f16, int64_t src_ld,
     if (!s) return LNSHIP_ENOINIT;
     if (K < 0 || M < 0 || nslices < 0 || src_ld < K || nslices > 65535)
         return fail(LNSHIP_EINVAL, "pack: bad shape%s");
+    if (src_is_f16 < 0 || src_is_f16 > (w32 ? 1 : 2)) return fail(LNSHIP_EINVAL, "pack: bad source type%s");
     if (K == 0 || M == 0 || nslices == 0) return 0;
     const int64_t kp = (K + 7) & ~(int64_t)7;
     dim3 grid(grid_for(M * kp, 2), (unsigned)nslices);

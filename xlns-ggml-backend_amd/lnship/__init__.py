@@ -199,14 +199,15 @@ def to_f32_32(v):
 
 
 def pack16(w, dtype=None):
-    """w [..., M, K] (float32 or float16) -> k8-interleaved xlns16 cache [slices, Kp*M] (int16)."""
+    """w [..., M, K] (float32, float16, or int16 xlns16 codes) -> k8-interleaved xlns16 cache [slices, Kp*M] (int16)."""
     import torch
     init()
     w = w.contiguous()
     K, M = w.shape[-1], w.shape[-2]
     ns = w.numel() // max(1, K * M)
     out = torch.empty((ns, kp(K) * M), dtype=torch.int16, device=w.device)
-    check(lib().lnship16_pack(_p(w), int(w.dtype == torch.float16), K, K * M, _p(out), K, M, ns, _stream()))
+    src_type = 2 if w.dtype == torch.int16 else int(w.dtype == torch.float16)   # int16: xlns16 codes
+    check(lib().lnship16_pack(_p(w), src_type, K, K * M, _p(out), K, M, ns, _stream()))
     return out
 
 
