@@ -232,6 +232,13 @@ __device__ __forceinline__ uint32_t lshl2_add(uint32_t a, uint32_t b) {
     return r;
 }
 
+// (a << 3) + b in one instruction (a descriptor pair's LDS address)
+__device__ __forceinline__ uint32_t lshl3_add(uint32_t a, uint32_t b) {
+    uint32_t r;
+    asm("v_lshl_add_u32 %0, %1, 3, %2" : "=v"(r) : "v"(a), "v"(b));
+    return r;
+}
+
 // LDS addresses as 32-bit integers: a table lookup is then a shift-add of the
 // index onto a precomputed origin and the read itself, with no separate add
 // of the shared-memory base on the dependent chain.
@@ -389,11 +396,13 @@ __device__ __forceinline__ void x32_add_desc(const x32_tab &O, acc_ls &a, uint32
     const uint32_t dl = d & ((1u << k32_co_sh) - 1u), dh = (d >> k32_co_sh) & ((1u << k32_co_sh) - 1u);
     const int32_t lo = lds_ld(lshl2_add(dl, O.dlo));    // dlo[dl]
     const int32_t th2 = lds_ld(lshl2_add(dh, O.dhi));   // (dh << 12) + dhi[dh]
-    const uint32_t dsc = (__builtin_amdgcn_ubfe(d | u, 23, 9) << 3) + O.desc;
+    const uint32_t dsc = lshl3_add(__builtin_amdgcn_ubfe(d | u, 23, 9), O.desc);
     const uint32_t base_d = (uint32_t)lds_ld(dsc), sh_d = (uint32_t)lds_ld(dsc + 4);
     __builtin_amdgcn_sched_barrier(0);
     uint32_t mx = max(a.l, tl);
-    uint32_t nsign = (d == 0 && u != 0) ? 0u : (a.l > tl ? a.s : ts);
+    // sign: the larger operand's (bit 31 of tl - a.l is set when a.l > tl),
+    // and + for exact cancellation (bit 31 of d - 1 is set only for d = 0)
+    uint32_t nsign = (ts ^ ((tl - a.l) & u)) & ~((d - 1u) & u);
     shadow();
     asm volatile("" : "+v"(mx), "+v"(nsign));
     __builtin_amdgcn_sched_barrier(0);
