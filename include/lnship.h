@@ -233,6 +233,13 @@ int lnship_set_rows(const float *src, const int64_t src_ne[4], const int64_t src
  * an index (src/lns-ops.cpp:1024). */
 int lnship_index_error(int64_t *bad_index, void *stream);
 
+/* Test hook: out[i] = the lpvip accumulator's db(d0 + i) (the Gaussian log
+ * for opposite signs at distance d, xlns32 units), as the lpvip mul_mat /
+ * rms_norm / soft_max kernels compute it; xlns32_add_lpvip's exact branch
+ * below one binade follows cuda/lns-cuda-xlns16.cu:86-98 and docs/CUDA.md:176-180.
+ * No counterpart in the reference. */
+int lnship_lpvip_db_range(uint32_t d0, uint32_t n, int32_t *out, void *stream);
+
 /* Host: the (cos, sin) floats lns_rope uses for positions 0..n_pos-1 (the
  * float recurrence t *= powf(freq_base, -2/n_dims) per pair, cosf / sinf;
  * src/lns-ops.cpp:1225-1247, cuda/lns-cuda-ops.cpp:223-240), laid out as

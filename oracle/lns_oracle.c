@@ -458,6 +458,11 @@ static int32_t lpvip_db(uint32_t d) {
     return -(int32_t)(u + (uint32_t)((sq * 0xB8Au) >> 12));
 }
 
+/* lpvip db at d for d0 .. d0 + n - 1 (the checker of the GPU's db) */
+void lno32_lpvip_db_n(uint32_t d0, uint32_t n, int32_t *out) {
+    for (uint32_t i = 0; i < n; i++) out[i] = lpvip_db(d0 + i);
+}
+
 uint32_t lno16_lpvip_add(uint32_t acc, uint16_t t16) {
     uint32_t t = lno16_widen(t16);
     uint32_t al = acc & X32_LOGMASK, tl = t & X32_LOGMASK;

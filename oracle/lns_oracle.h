@@ -76,6 +76,7 @@ void     lno16_softmax_row(int mode, const uint16_t *a, const uint16_t *mask, ui
                            uint16_t scale, uint16_t *lfsr);
 uint16_t lno16_add_monte(uint16_t a, uint16_t b, uint16_t *lfsr);
 uint32_t lno16_lpvip_add(uint32_t acc, uint16_t t);
+void     lno32_lpvip_db_n(uint32_t d0, uint32_t n, int32_t *out);
 
 /* ---- Monte LFSR (process-global, seed 7) ------------------------------ */
 uint16_t lno_lfsr_step(uint16_t s);

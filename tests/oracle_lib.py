@@ -65,6 +65,7 @@ def lib():
         "lno16_softmax_row": (None, [ctypes.c_int, P, P, P, SZ, u16, P]),
         "lno16_add_monte": (u16, [u16, u16, P]),
         "lno16_lpvip_add": (u32, [u32, u16]),
+        "lno32_lpvip_db_n": (None, [u32, u32, P]),
         "lno_lfsr_step": (u16, [u16]),
         "lno_lfsr_jump": (u16, [u16, ctypes.c_uint64]),
         "lno_monte_get_state": (ctypes.c_int, [P]),

@@ -428,3 +428,19 @@ def test_mul_mat_id_expert_out_of_range(ln):
     assert np.all(got[0, 1] == -1.0)
     same_bits(got[0, 0], want[0, 0], "slot before the bad expert")
     same_bits(got[1], want[1], "token after the bad expert")
+
+
+def test_lpvip_db_every_distance_below_one_binade(ln):
+    # lpvip's exact branch (d below one binade, opposite signs) against the
+    # host's libm for every d, and the Mitchell branch just above it (d = 0
+    # is exact cancellation, handled before db)
+    import ctypes
+    n = (1 << 23) + (1 << 20)
+    print(f"\n[lpvip db] d = 1 .. {n}", flush=True)
+    out = torch.empty(n, dtype=torch.int32, device="cuda")
+    ln.check(ln.lib().lnship_lpvip_db_range(1, n, ctypes.c_void_p(out.data_ptr()), ln._stream()))
+    want = np.empty(n, np.int32)
+    O.lib().lno32_lpvip_db_n(1, n, want.ctypes.data)
+    got = host(out)
+    bad = np.nonzero(got != want)[0]
+    assert bad.size == 0, f"{bad.size} differ; first d={bad[0] + 1}: got {got[bad[0]]} want {want[bad[0]]}"

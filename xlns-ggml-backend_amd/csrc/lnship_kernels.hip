@@ -471,7 +471,10 @@ __device__ __forceinline__ int32_t lpvip_sb(uint32_t d) {
 }
 __device__ __forceinline__ int32_t lpvip_db(uint32_t d) {
     if (d < 0x800000u) {
-        double v = log(1.0 - pow(2.0, -(double)d / 8388608.0)) / log(2.0) * 8388608.0;
+        // exp2(-x) for the reference's pow(2, -x): the same integer for every
+        // d of this branch (checked against the host's pow over all of them),
+        // at two thirds of the cost
+        double v = log(1.0 - exp2(-(double)d / 8388608.0)) / log(2.0) * 8388608.0;
         return (int32_t)floor(v + 0.5);
     }
     uint32_t u = mitchell_exp2_neg(d);
@@ -1481,6 +1484,13 @@ __global__ void k_set_rows(const char *__restrict__ src, strided4 gs, const char
     }
 }
 
+// lpvip's db at d0 .. d0 + n - 1 (a test hook: the db function is checked
+// over its whole exact-branch domain against the host)
+__global__ void k_lpvip_db_range(uint32_t d0, uint32_t n, int32_t *__restrict__ out) {
+    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += blockDim.x * gridDim.x)
+        out[i] = lpvip_db(d0 + i);
+}
+
 __global__ void k_causal_mask(const int32_t *__restrict__ pos, int64_t ntok, int64_t n_kv, float *__restrict__ mask) {
     const int64_t n = ntok * n_kv;
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)blockDim.x * gridDim.x) {
@@ -2366,6 +2376,16 @@ int lnship_set_rows(const float *src, const int64_t src_ne[4], const int64_t src
     else
         hipLaunchKernelGGL(k_set_rows<0>, g, dim3(k_block), 0, (hipStream_t)stream, (const char *)src, gs,
                            (const char *)ids, gi, ids_i64, (char *)dst, gd, s->index_err);
+    LNSHIP_HIP(hipGetLastError());
+    return 0;
+}
+
+int lnship_lpvip_db_range(uint32_t d0, uint32_t n, int32_t *out, void *stream) {
+    device_state *s = state();
+    if (!s) return LNSHIP_ENOINIT;
+    if (!out) return fail(LNSHIP_EINVAL, "lpvip_db_range: null output%s");
+    if (n == 0) return 0;
+    hipLaunchKernelGGL(k_lpvip_db_range, dim3(grid_for(n, 4)), dim3(k_block), 0, (hipStream_t)stream, d0, n, out);
     LNSHIP_HIP(hipGetLastError());
     return 0;
 }

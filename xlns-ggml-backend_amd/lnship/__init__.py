@@ -93,6 +93,7 @@ def lib():
         "lnship_set_rows": (ctypes.c_int, [c_p, c_p, c_p, c_p, ctypes.c_int, c_p, c_p, c_p, ctypes.c_int, c_p, c_p,
                                            c_p]),
         "lnship_index_error": (ctypes.c_int, [ctypes.POINTER(c_i64), c_p]),
+        "lnship_lpvip_db_range": (ctypes.c_int, [ctypes.c_uint32, ctypes.c_uint32, c_p, c_p]),
         "lnship16_add": (ctypes.c_int, [c_p, c_p, c_i64, c_i64, c_p, c_p]),
         "lnship16_mul": (ctypes.c_int, [c_p, c_p, c_i64, c_i64, c_p, c_p]),
         "lnship16_swiglu": (ctypes.c_int, [c_p, c_i64, c_p, c_i64, c_p, c_i64, c_i64, c_p]),
