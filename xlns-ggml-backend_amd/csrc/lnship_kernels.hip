@@ -293,14 +293,19 @@ struct red16<LNSHIP_MONTE> {
     __device__ __forceinline__ uint32_t finish(const acc_t &a) const { return a.s | a.l; }
 };
 
-// xlns32 addition, branch-free.  T is the LDS copy of the adder tables with
-// two changes made at staging: the db-at-zero entry holds a sentinel (exact
-// cancellation clamps the log to 0), and each dhi[dh] holds
-// (dh << 12) + dhi[dh].  The direct sb / db interpolation and the first
-// cotransformation lookups are independent reads issued together; only the
-// cotransformation's sb(e) needs a second round trip to LDS.  Every select
-// is arithmetic: a ternary around two table reads would compile to a
-// divergent branch that serialises both reads.
+// xlns32 addition (xlns32_alt), branch-free.  The Gaussian log at distance
+// d has three exclusive cases: sb(d) for equal signs; db(d) from its tables
+// at and above 2 binades; below 2 binades the cotransformation
+//   1 - 2^-d = (1 - 2^-dh) + 2^-dh (1 - 2^-dl),  d = (dh << 12) + dl,
+// which is dlo[dl] when dh = 0, dhi[dh] when dl = 0, and otherwise
+// dhi[dh] + sb(e) with e = (dh << 12) - dlo[dl] + dhi[dh].  A lane needs at
+// most one interpolation (at e on the sb tables, or at d on the sb / db
+// tables), so all lanes share one.  T is the LDS copy of the adder tables
+// with changes made at staging: the db-at-zero entry holds a sentinel (exact
+// cancellation clamps the log to 0), each dhi[dh] holds (dh << 12) + dhi[dh],
+// a zero pair follows the tables, then the descriptors of the direct
+// interpolation (below).  Every select is arithmetic: a ternary around two
+// table reads would compile to a divergent branch that serialises both.
 
 // Byte offsets of the interpolation tables in the LDS copy, each less its
 // grid origin, so that a distance x on grid shift sh reads node
@@ -327,50 +332,6 @@ __device__ __forceinline__ x32_tab x32_origins(const int32_t *T) {
     return o;
 }
 
-__device__ __forceinline__ void x32_add_ls(const x32_tab &O, acc_ls &a, uint32_t tl, uint32_t ts) {
-    const uint32_t d = absdiff(a.l, tl), mx = max(a.l, tl);
-    const bool usedb = a.s != ts;
-    // Three exclusive cases: sb(d) for equal signs; db(d) from its tables at
-    // and above 2 binades; below 2 binades the cotransformation
-    //   1 - 2^-d = (1 - 2^-dh) + 2^-dh (1 - 2^-dl),  d = (dh << 12) + dl,
-    // which is dlo[dl] when dh = 0, dhi[dh] when dl = 0, and otherwise
-    // dhi[dh] + sb(e) with e = (dh << 12) - dlo[dl] + dhi[dh].  A lane needs
-    // at most one interpolation, so all lanes share one: at e on the sb
-    // tables for the last case, at d on the sb or db tables otherwise.  It
-    // follows the cotransformation's lookups, which every lane makes.
-    const uint32_t dl = d & ((1u << k32_co_sh) - 1u), dh = (d >> k32_co_sh) & ((1u << k32_co_sh) - 1u);
-    const int32_t lo = lds_ld(lshl2_add(dl, O.dlo));    // dlo[dl]
-    const int32_t th2 = lds_ld(lshl2_add(dh, O.dhi));   // (dh << 12) + dhi[dh]
-    // what depends on d and the signs alone, while the lookups are in flight
-    const bool co = usedb && d < k32_co_end;
-    const bool direct_db = usedb && !(d < k32_co_end);
-    const bool at_e = co && dh != 0 && dl != 0;
-    const bool cut = !(d < k32_esszer);
-    // the far sb table's last node (x = esszer) is 0, which is sb beyond
-    // esszer; db beyond esszer is cut off below
-    const uint32_t cap = direct_db ? k32_esszer - 1 : k32_esszer;
-    const uint32_t lim = direct_db ? k32_db_end : k32_sb_end;
-    const uint32_t b_fine = direct_db ? O.db : O.sb, b_far = direct_db ? O.dbf : O.sbf;
-    // the interpolation
-    const uint32_t e = (uint32_t)th2 - (uint32_t)lo;   // wraps for the dl = 0 sentinel (unused then)
-    const uint32_t xc = min(at_e ? e : d, cap);
-    const bool hi = xc >= lim;
-    const int sh = hi ? k32_sb_fsh : k32_sb_sh;   // both tables: 2^13 / 2^19 grids
-    const uint32_t node = lshl2_add(xc >> sh, hi ? b_far : b_fine);
-    const int32_t t0 = lds_ld(node), t1 = lds_ld(node + 4);
-    // |t1 - t0| < 2^23 and the fraction < 2^19: a full-rate 24-bit multiply
-    const int32_t ip = t0 + (mul_i24(t1 - t0, (int32_t)(xc & ((1u << sh) - 1u))) >> sh);
-    // adj = A + (keep ? ip : 0): A is the cotransformation's part (dlo[dl],
-    // dhi[dh], or 0 off the cotransformation), known before ip returns, and
-    // ip counts for sb(e) and for the direct sb / db below esszer.  A <= 0,
-    // so mx + A cannot overflow; the saturating add only meets direct sb.
-    const int32_t th = th2 - (int32_t)(dh << k32_co_sh);
-    const int32_t mA = (int32_t)mx + (co ? (dh == 0 ? lo : th) : 0);
-    const bool keep = at_e || (!co && !cut);
-    const uint32_t ns = a.l > tl ? a.s : ts;
-    a.l = (uint32_t)max(__builtin_elementwise_add_sat(mA, keep ? ip : 0), 0);
-    a.s = (d == 0 && usedb) ? 0u : ns;
-}
 
 // A select on values: a conditional on two struct fields is an lvalue, a
 // select of their addresses, and nested ones force the struct into scratch.
@@ -422,6 +383,37 @@ __device__ __forceinline__ void x32_add_desc(const x32_tab &O, acc_ls &a, uint32
     const uint32_t sh = at_e ? (uint32_t)sh_e : sh_d;
     const int32_t frac = (int32_t)__builtin_amdgcn_ubfe(at_e ? xe : d, 0, sh);
     __builtin_amdgcn_sched_barrier(0);
+    const int32_t ip = t0 + (__mul24(t1 - t0, frac) >> sh);
+    a.l = (uint32_t)max(__builtin_elementwise_add_sat(mA, ip), 0);
+    a.s = nsign;
+}
+
+// x32_add_desc without the scheduling order, for lanes that run several
+// chains (the compiler interleaves them)
+__device__ __forceinline__ void x32_add_ls(const x32_tab &O, acc_ls &a, uint32_t tl, uint32_t ts) {
+    const uint32_t d = absdiff(a.l, tl);
+    const uint32_t u = a.s ^ ts;
+    const uint32_t dl = d & ((1u << k32_co_sh) - 1u), dh = (d >> k32_co_sh) & ((1u << k32_co_sh) - 1u);
+    const int32_t lo = lds_ld(lshl2_add(dl, O.dlo));
+    const int32_t th2 = lds_ld(lshl2_add(dh, O.dhi));
+    const uint32_t dsc = lshl3_add(__builtin_amdgcn_ubfe(d | u, 23, 9), O.desc);
+    const uint32_t base_d = (uint32_t)lds_ld(dsc), sh_d = (uint32_t)lds_ld(dsc + 4);
+    const uint32_t mx = max(a.l, tl);
+    const uint32_t nsign = (ts ^ ((tl - a.l) & u)) & ~((d - 1u) & u);
+    const bool co = sh_d == 30;
+    const bool at_e = co && dh != 0;
+    const uint32_t e = (uint32_t)th2 - (uint32_t)lo;
+    const uint32_t xe = min(e, k32_esszer);
+    const bool hi_e = e >= k32_sb_end;
+    const int sh_e = hi_e ? k32_sb_fsh : k32_sb_sh;
+    const uint32_t ne = lshl2_add(xe >> sh_e, sel(hi_e, O.sbf, O.sb));
+    const uint32_t nd = lshl2_add(d >> sh_d, base_d);
+    const uint32_t node = sel(at_e, ne, nd);
+    const int32_t t0 = lds_ld(node), t1 = lds_ld(node + 4);
+    const int32_t th = th2 - (int32_t)(dh << k32_co_sh);
+    const int32_t mA = (int32_t)mx + (co ? (dh == 0 ? lo : th) : 0);
+    const uint32_t sh = at_e ? (uint32_t)sh_e : sh_d;
+    const int32_t frac = (int32_t)__builtin_amdgcn_ubfe(at_e ? xe : d, 0, sh);
     const int32_t ip = t0 + (__mul24(t1 - t0, frac) >> sh);
     a.l = (uint32_t)max(__builtin_elementwise_add_sat(mA, ip), 0);
     a.s = nsign;
