@@ -261,17 +261,33 @@ def cpu_baseline(cfg, weights, mode, n_tokens):
     from llama_oracle import LlamaOracle16
     m = O.MODES[mode]
     cpu = LlamaOracle16(cfg, weights, m)
-    cpu.eval([1, 2])
-    t0 = time.perf_counter()
-    tok = 3
-    for _ in range(n_tokens):
-        logits = cpu.eval([tok])
-        tok = int(logits.argmax())
-    dt = time.perf_counter() - t0
+    with _one_core() as core:
+        cpu.eval([1, 2])
+        t0 = time.perf_counter()
+        tok = 3
+        for _ in range(n_tokens):
+            logits = cpu.eval([tok])
+            tok = int(logits.argmax())
+        dt = time.perf_counter() - t0
     return {"value": round(n_tokens / dt, 4), "unit": "tok/s", "cores": 1, "kind": "port",
             "sample": f"{n_tokens} decode tokens after a 2-token prompt, full SmolLM2-135M shape, "
-                      f"{mode}, single-threaded C oracle ({dt:.1f} s)",
-            "cpu": _cpu_name()}
+                      f"{mode}, single-threaded C oracle pinned to core {core} ({dt:.1f} s)",
+            "cpu": _cpu_name(), "nproc": len(os.sched_getaffinity(0))}
+
+
+class _one_core:
+    """Pins the calling thread to the first core it may run on (the oracle is
+    single-threaded), and restores its affinity afterwards."""
+
+    def __enter__(self):
+        self.saved = os.sched_getaffinity(0)
+        core = min(self.saved)
+        os.sched_setaffinity(0, {core})
+        return core
+
+    def __exit__(self, *exc):
+        os.sched_setaffinity(0, self.saved)
+        return False
 
 
 def _cpu_name():
@@ -580,18 +596,19 @@ def cpu_baseline_lns32(cfg, weights, torch):
     cfg1 = dataclasses.replace(cfg, n_layer=1)
     cpu = LlamaOracle32(cfg1, w1)
     times = []
-    for n_layers in (0, 1):
-        cpu.n_past = 0
-        cpu.eval([1, 2], n_layers=n_layers)
-        t0 = time.perf_counter()
-        cpu.eval([3], n_layers=n_layers)
-        times.append(time.perf_counter() - t0)
+    with _one_core() as core:
+        for n_layers in (0, 1):
+            cpu.n_past = 0
+            cpu.eval([1, 2], n_layers=n_layers)
+            t0 = time.perf_counter()
+            cpu.eval([3], n_layers=n_layers)
+            times.append(time.perf_counter() - t0)
     per_tok = times[0] + cfg.n_layer * (times[1] - times[0])
     return {"value": round(1.0 / per_tok, 5), "unit": "tok/s", "cores": 1, "kind": "port",
-            "sample": "one decode token after a 2-token prompt at the 1B width, single-threaded C oracle: "
-                      "embedding + output %.2f s, plus layer 0 %.2f s; scaled to 16 layers" %
-                      (times[0], times[1] - times[0]),
-            "cpu": _cpu_name()}
+            "sample": "one decode token after a 2-token prompt at the 1B width, single-threaded C oracle "
+                      "pinned to core %d: embedding + output %.2f s, plus layer 0 %.2f s; scaled to 16 layers" %
+                      (core, times[0], times[1] - times[0]),
+            "cpu": _cpu_name(), "nproc": len(os.sched_getaffinity(0))}
 
 
 if __name__ == "__main__":
