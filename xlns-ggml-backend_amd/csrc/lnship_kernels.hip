@@ -502,6 +502,24 @@ struct red16<LNSHIP_LPVIP> {
 
 // Stages the tables a reduction needs into LDS (with the sentinels); returns
 // the policy.
+// Copies n > 0 int4 from global memory to LDS.  Each thread issues its loads
+// in batches of B before the first store of the batch, so a batch costs one
+// memory round trip instead of B (a launch of a chain kernel stages its
+// tables before the chain can start, and the chain waits for every byte).
+// Past the end a thread copies the last element again, to the same place and
+// with the same value: the batch has no branch for the compiler to sink a
+// load into, so the loads issue back to back.
+template <int B = 16>
+__device__ __forceinline__ void stage_copy(int4 *dst, const int4 *__restrict__ src, int n) {
+    for (int i0 = threadIdx.x; i0 < n; i0 += B * (int)blockDim.x) {
+        int4 r[B];
+#pragma unroll
+        for (int j = 0; j < B; j++) r[j] = src[min(i0 + j * (int)blockDim.x, n - 1)];
+#pragma unroll
+        for (int j = 0; j < B; j++) dst[min(i0 + j * (int)blockDim.x, n - 1)] = r[j];
+    }
+}
+
 template <int MODE>
 __device__ __forceinline__ red16<MODE> stage_tables(const dev_tables &T, char *lds);
 
@@ -528,7 +546,7 @@ __device__ __forceinline__ red16<LNSHIP_SUM32> stage_tables<LNSHIP_SUM32>(const 
     int32_t *t = reinterpret_cast<int32_t *>(lds);
     const int4 *src = reinterpret_cast<const int4 *>(T.tab32);
     int4 *d4 = reinterpret_cast<int4 *>(t);
-    for (int i = threadIdx.x; i < k32_tab_n / 4; i += blockDim.x) d4[i] = src[i];
+    stage_copy(d4, src, k32_tab_n / 4);
     for (int i = (k32_tab_n / 4) * 4 + threadIdx.x; i < k32_tab_n; i += blockDim.x) t[i] = T.tab32[i];
     __syncthreads();
     if (threadIdx.x == 0) t[k32_off_dlo] = -0x7fffffff;   // db at d = 0: exact cancellation
@@ -660,10 +678,36 @@ __global__ __launch_bounds__(k_block * CG) void k_mm16(mm_args16 a, dev_tables T
     uint16_t *xl = reinterpret_cast<uint16_t *>(lds + mm_xl_offset<MODE>());
     if (XL) {
         // columns past N and k past K hold xlns16 zero
+        // in batches of eight per thread: the loads, then the conversion
+        // table's lookups, then the stores (two memory round trips a batch)
         const float *xf = a.xf + zx * a.x_slice + nw * a.x_ld;
-        for (int j = 0; j < NC * CG; j++)
-            for (int k = threadIdx.x; k < kp; k += k_block * CG)
-                xl[j * kp + k] = (j < ncw && k < a.K) ? (uint16_t)x16_from_f32(T.cvt16, xf[j * a.x_ld + k]) : (uint16_t)0;
+        constexpr int nt = k_block * CG, B = 8;
+        const int kl = (int)a.K - 1;
+        for (int j = 0; j < NC * CG; j++) {
+            if (kl < 0) {
+                for (int k = threadIdx.x; k < kp; k += nt) xl[j * kp + k] = 0;
+                continue;
+            }
+            // loads and lookups stay in the row; only the stores are bounded
+            const float *row = xf + (int64_t)min(j, ncw - 1) * a.x_ld;
+            for (int k0 = threadIdx.x; k0 < kp; k0 += B * nt) {
+                float v[B];
+#pragma unroll
+                for (int q = 0; q < B; q++) v[q] = row[min(k0 + q * nt, kl)];
+                uint32_t c[B];
+#pragma unroll
+                for (int q = 0; q < B; q++) c[q] = x16_from_f32(T.cvt16, v[q]);
+                // every code in a register before the bounded stores: none of
+                // the batch's loads moves into a store's branch
+#pragma unroll
+                for (int q = 0; q < B; q++) asm volatile("" ::"v"(c[q]));
+#pragma unroll
+                for (int q = 0; q < B; q++) {
+                    const int k = k0 + q * nt;
+                    if (k < kp) xl[j * kp + k] = (j < ncw && k <= kl) ? (uint16_t)c[q] : (uint16_t)0;
+                }
+            }
+        }
         xl += cg * NC * kp;
     }
     __syncthreads();
