@@ -1054,12 +1054,24 @@ __global__ __launch_bounds__(k_block) void k_rms16(const float *__restrict__ src
     __shared__ uint32_t s_inv[64];
     const int64_t r0 = (int64_t)blockIdx.x * rb;
     const int nr = (int)min<int64_t>(rb, nrows - r0);
-    const int64_t ne = (int64_t)nr * ncols;
-    const int nc = (int)ncols, rs = (nc + 7) & ~7;   // LDS rows 16-byte aligned
-    for (int e = threadIdx.x; e < nr * nc; e += blockDim.x) {
-        const int r = e / nc;
-        const uint32_t c = x16_from_f32(T.cvt16, src[r0 * ncols + e]);
-        sq[e + r * (rs - nc)] = (uint16_t)x16_mul(c, c);
+    const int nc = (int)ncols, nel = nr * nc, rs = (nc + 7) & ~7;   // LDS rows 16-byte aligned
+    // element passes in batches of B per thread, loads and lookups issued
+    // before the first wait; past the end a thread redoes the last element
+    // (the same value to the same place)
+    constexpr int B = 8;
+    const int nt = (int)blockDim.x;
+    for (int e0 = threadIdx.x; e0 < nel; e0 += B * nt) {
+        float f[B];
+#pragma unroll
+        for (int q = 0; q < B; q++) f[q] = src[r0 * ncols + min(e0 + q * nt, nel - 1)];
+        uint32_t c[B];
+#pragma unroll
+        for (int q = 0; q < B; q++) c[q] = x16_from_f32(T.cvt16, f[q]);
+#pragma unroll
+        for (int q = 0; q < B; q++) {
+            const int e = min(e0 + q * nt, nel - 1);
+            sq[e + (e / nc) * (rs - nc)] = (uint16_t)x16_mul(c[q], c[q]);
+        }
     }
     __syncthreads();
     if ((int)threadIdx.x < nr) {
@@ -1077,10 +1089,19 @@ __global__ __launch_bounds__(k_block) void k_rms16(const float *__restrict__ src
         s_inv[r] = x16_recip(x16_sqrt(me));
     }
     __syncthreads();
-    for (int64_t e = threadIdx.x; e < ne; e += blockDim.x) {
-        const int r = (int)(e / ncols);
-        const uint32_t c = x16_from_f32(T.cvt16, src[r0 * ncols + e]);
-        dst[r0 * ncols + e] = T.rev16[x16_mul(c, s_inv[r])];
+    for (int e0 = threadIdx.x; e0 < nel; e0 += B * nt) {
+        float f[B];
+#pragma unroll
+        for (int q = 0; q < B; q++) f[q] = src[r0 * ncols + min(e0 + q * nt, nel - 1)];
+        uint32_t c[B];
+#pragma unroll
+        for (int q = 0; q < B; q++) c[q] = x16_from_f32(T.cvt16, f[q]);
+#pragma unroll
+        for (int q = 0; q < B; q++) f[q] = T.rev16[x16_mul(c[q], s_inv[min(e0 + q * nt, nel - 1) / nc])];
+        // only the element's own thread stores (dst may be src)
+#pragma unroll
+        for (int q = 0; q < B; q++)
+            if (e0 + q * nt < nel) dst[r0 * ncols + e0 + q * nt] = f[q];
     }
 }
 
@@ -1092,12 +1113,20 @@ __global__ __launch_bounds__(k_block) void k_rms32(const float *__restrict__ src
     __shared__ uint32_t s_inv[64];
     const int64_t r0 = (int64_t)blockIdx.x * rb;
     const int nr = (int)min<int64_t>(rb, nrows - r0);
-    const int64_t ne = (int64_t)nr * ncols;
-    const int nc = (int)ncols, rs = (nc + 3) & ~3;   // LDS rows 16-byte aligned
-    for (int e = threadIdx.x; e < nr * nc; e += blockDim.x) {
-        const int r = e / nc;
-        const uint32_t c = x32_from_f32(src[r0 * ncols + e]);
-        sq[e + r * (rs - nc)] = x32_mul(c, c);
+    const int nc = (int)ncols, nel = nr * nc, rs = (nc + 3) & ~3;   // LDS rows 16-byte aligned
+    // loads in batches of B per thread (past the end the last element again)
+    constexpr int B = 8;
+    const int nt = (int)blockDim.x;
+    for (int e0 = threadIdx.x; e0 < nel; e0 += B * nt) {
+        float f[B];
+#pragma unroll
+        for (int q = 0; q < B; q++) f[q] = src[r0 * ncols + min(e0 + q * nt, nel - 1)];
+#pragma unroll
+        for (int q = 0; q < B; q++) {
+            const int e = min(e0 + q * nt, nel - 1);
+            const uint32_t c = x32_from_f32(f[q]);
+            sq[e + (e / nc) * (rs - nc)] = x32_mul(c, c);
+        }
     }
     __syncthreads();
     if ((int)threadIdx.x < nr) {
@@ -1109,9 +1138,15 @@ __global__ __launch_bounds__(k_block) void k_rms32(const float *__restrict__ src
         s_inv[r] = x32_recip(x32_sqrt(x32_add_lds(R.O, mean, x32_from_f32(eps))));
     }
     __syncthreads();
-    for (int64_t e = threadIdx.x; e < ne; e += blockDim.x) {
-        const int r = (int)(e / ncols);
-        dst[r0 * ncols + e] = x32_to_f32(x32_mul(x32_from_f32(src[r0 * ncols + e]), s_inv[r]));
+    for (int e0 = threadIdx.x; e0 < nel; e0 += B * nt) {
+        float f[B];
+#pragma unroll
+        for (int q = 0; q < B; q++) f[q] = src[r0 * ncols + min(e0 + q * nt, nel - 1)];
+        // only the element's own thread stores (dst may be src)
+#pragma unroll
+        for (int q = 0; q < B; q++)
+            if (e0 + q * nt < nel)
+                dst[r0 * ncols + e0 + q * nt] = x32_to_f32(x32_mul(x32_from_f32(f[q]), s_inv[(e0 + q * nt) / nc]));
     }
 }
 
@@ -1147,36 +1182,79 @@ __global__ __launch_bounds__(k_block) void k_softmax16(sm_args a, dev_tables T) 
     uint16_t *c = reinterpret_cast<uint16_t *>(lds + ((lds_tables_bytes<MODE>() + 15) & ~15));
     __shared__ int32_t s_max[64];
     __shared__ uint32_t s_tot[64];
+    __shared__ const float *s_mrow[64];
     const int64_t r0 = (int64_t)blockIdx.x * a.rb;
     const int nr = (int)min<int64_t>(a.rb, a.ne1 * a.ne2 * a.ne3 - r0);
-    const int64_t ne = (int64_t)nr * a.n;
-    const int rs = ((int)a.n + 7) & ~7;   // LDS rows 16-byte aligned
-    if ((int)threadIdx.x < nr) s_max[threadIdx.x] = x16_canon(0xffffu);
-    __syncthreads();
-    const uint32_t sc = x16_from_f32(T.cvt16, a.scale);
-    for (int64_t e = threadIdx.x; e < ne; e += blockDim.x) {
-        const int r = (int)(e / a.n);
-        const int64_t i = e - (int64_t)r * a.n;
-        uint32_t v = x16_from_f32(T.cvt16, a.src[(r0 + r) * a.n + i]);
-        if (v != 0xffffu) {
-            v = x16_mul(v, sc);
-            if (a.mask) {
-                const float mf = mask_row(a, r0 + r)[i];
-                const uint32_t mk = mf <= -3.0e38f ? 0xffffu : x16_from_f32(T.cvt16, mf);
-                if (mk == 0xffffu) v = 0xffffu;
-                else if (mk & k16_logmask) v = x16_add_g(T.gauss16, v, mk);
-            }
-        }
-        c[e + r * (rs - a.n)] = (uint16_t)v;
-        atomicMax(&s_max[r], x16_canon(v));
+    const int n = (int)a.n, nel = nr * n;   // a row fits in LDS, so 32-bit counts suffice
+    const int rs = (n + 7) & ~7;            // LDS rows 16-byte aligned
+    if ((int)threadIdx.x < nr) {
+        s_max[threadIdx.x] = x16_canon(0xffffu);
+        s_mrow[threadIdx.x] = a.mask ? mask_row(a, r0 + threadIdx.x) : nullptr;
     }
     __syncthreads();
-    for (int64_t e = threadIdx.x; e < ne; e += blockDim.x) {
-        const int r = (int)(e / a.n);
-        const int32_t cm = s_max[r];
-        const uint32_t mx = (uint32_t)(uint16_t)(cm < 0 ? (cm ^ 0x7fff) : cm);
-        const int64_t o = e + r * (rs - a.n);
-        c[o] = T.exp16[x16_add_g(T.gauss16, c[o], mx ^ k16_sign)];
+    const uint32_t sc = x16_from_f32(T.cvt16, a.scale);
+    const bool has_mask = a.mask != nullptr;
+    // The element passes run in batches of B elements per thread, branch
+    // free: every load and table lookup of a batch is issued before the first
+    // one is waited for.  Past the end a thread redoes the last element (the
+    // same value to the same place).
+    constexpr int B = 8;
+    const int nt = (int)blockDim.x;
+    for (int e0 = threadIdx.x; e0 < nel; e0 += B * nt) {
+        int r[B], o[B];
+        float f[B], mf[B];
+#pragma unroll
+        for (int q = 0; q < B; q++) {
+            const int e = min(e0 + q * nt, nel - 1);
+            r[q] = e / n;
+            const int i = e - r[q] * n;
+            o[q] = e + r[q] * (rs - n);
+            f[q] = a.src[(r0 + r[q]) * a.n + i];
+            mf[q] = has_mask ? s_mrow[r[q]][i] : 0.0f;
+        }
+        uint32_t v[B], mk[B];
+#pragma unroll
+        for (int q = 0; q < B; q++) {
+            v[q] = x16_from_f32(T.cvt16, f[q]);
+            mk[q] = x16_from_f32(T.cvt16, mf[q]);
+        }
+        uint32_t vm[B], va[B];
+#pragma unroll
+        for (int q = 0; q < B; q++) {
+            vm[q] = x16_mul(v[q], sc);
+            va[q] = x16_add_g(T.gauss16, vm[q], mk[q]);
+        }
+#pragma unroll
+        for (int q = 0; q < B; q++) asm volatile("" ::"v"(va[q]));
+#pragma unroll
+        for (int q = 0; q < B; q++) {
+            const bool masked_out = has_mask && (mf[q] <= -3.0e38f || mk[q] == 0xffffu);
+            const uint32_t w = v[q] == 0xffffu || masked_out ? 0xffffu : (has_mask && (mk[q] & k16_logmask)) ? va[q] : vm[q];
+            c[o[q]] = (uint16_t)w;
+            atomicMax(&s_max[r[q]], x16_canon(w));
+        }
+    }
+    __syncthreads();
+    for (int e0 = threadIdx.x; e0 < nel; e0 += B * nt) {
+        int o[B];
+        uint32_t mx[B], cv[B], sh[B];
+#pragma unroll
+        for (int q = 0; q < B; q++) {
+            const int e = min(e0 + q * nt, nel - 1), r = e / n;
+            const int32_t cm = s_max[r];
+            mx[q] = (uint32_t)(uint16_t)(cm < 0 ? (cm ^ 0x7fff) : cm);
+            o[q] = e + r * (rs - n);
+            cv[q] = c[o[q]];
+        }
+#pragma unroll
+        for (int q = 0; q < B; q++) sh[q] = x16_add_g(T.gauss16, cv[q], mx[q] ^ k16_sign);
+#pragma unroll
+        for (int q = 0; q < B; q++) sh[q] = T.exp16[sh[q]];
+        // in place: only the element's own thread writes it (a thread that
+        // redoes the last element may read it after its owner wrote it)
+#pragma unroll
+        for (int q = 0; q < B; q++)
+            if (e0 + q * nt < nel) c[o[q]] = (uint16_t)sh[q];
     }
     __syncthreads();
     if ((int)threadIdx.x < nr) {
@@ -1190,9 +1268,18 @@ __global__ __launch_bounds__(k_block) void k_softmax16(sm_args a, dev_tables T) 
         s_tot[r] = R.finish(acc) & 0xffffu;
     }
     __syncthreads();
-    for (int64_t e = threadIdx.x; e < ne; e += blockDim.x) {
-        const int r = (int)(e / a.n);
-        a.dst[r0 * a.n + e] = T.rev16[x16_div(c[e + r * (rs - a.n)], s_tot[r])];
+    for (int e0 = threadIdx.x; e0 < nel; e0 += B * nt) {
+        uint32_t y[B];
+#pragma unroll
+        for (int q = 0; q < B; q++) {
+            const int e = min(e0 + q * nt, nel - 1), r = e / n;
+            y[q] = x16_div(c[e + r * (rs - n)], s_tot[r]);
+        }
+        float out[B];
+#pragma unroll
+        for (int q = 0; q < B; q++) out[q] = T.rev16[y[q]];
+#pragma unroll
+        for (int q = 0; q < B; q++) a.dst[r0 * a.n + min(e0 + q * nt, nel - 1)] = out[q];
     }
 }
 
@@ -1202,28 +1289,45 @@ __global__ __launch_bounds__(k_block) void k_softmax32(sm_args a, dev_tables T) 
     uint32_t *c = reinterpret_cast<uint32_t *>(lds + k_lds_tab32);
     __shared__ int32_t s_max[64];
     __shared__ uint32_t s_tot[64];
+    __shared__ const float *s_mrow[64];
     const int64_t r0 = (int64_t)blockIdx.x * a.rb;
     const int nr = (int)min<int64_t>(a.rb, a.ne1 * a.ne2 * a.ne3 - r0);
     const int64_t ne = (int64_t)nr * a.n;
+    const int n = (int)a.n, nel = nr * n;
     const int rs = ((int)a.n + 3) & ~3;   // LDS rows 16-byte aligned
-    if ((int)threadIdx.x < nr) s_max[threadIdx.x] = x32_canon(0xffffffffu);
+    if ((int)threadIdx.x < nr) {
+        s_max[threadIdx.x] = x32_canon(0xffffffffu);
+        s_mrow[threadIdx.x] = a.mask ? mask_row(a, r0 + threadIdx.x) : nullptr;
+    }
     __syncthreads();
     const uint32_t sc = x32_from_f32(a.scale);
-    for (int64_t e = threadIdx.x; e < ne; e += blockDim.x) {
-        const int r = (int)(e / a.n);
-        const int64_t i = e - (int64_t)r * a.n;
-        uint32_t v = x32_from_f32(a.src[(r0 + r) * a.n + i]);
-        if (v != 0xffffffffu) {
-            v = x32_mul(v, sc);
-            if (a.mask) {
-                const float mf = mask_row(a, r0 + r)[i];
-                const uint32_t mk = mf <= -3.0e38f ? 0xffffffffu : x32_from_f32(mf);
-                if (mk == 0xffffffffu) v = 0xffffffffu;
-                else if (mk & k32_logmask) v = x32_add_lds(R.O, v, mk);
-            }
+    // loads in batches of B per thread (past the end the last element again:
+    // the same value to the same place)
+    constexpr int B = 8;
+    const int nt = (int)blockDim.x;
+    for (int e0 = threadIdx.x; e0 < nel; e0 += B * nt) {
+        float f[B], mf[B];
+#pragma unroll
+        for (int q = 0; q < B; q++) {
+            const int e = min(e0 + q * nt, nel - 1), r = e / n, i = e - r * n;
+            f[q] = a.src[(r0 + r) * a.n + i];
+            mf[q] = a.mask ? s_mrow[r][i] : 0.0f;
         }
-        c[e + r * (rs - a.n)] = v;
-        atomicMax(&s_max[r], x32_canon(v));
+#pragma unroll
+        for (int q = 0; q < B; q++) {
+            const int e = min(e0 + q * nt, nel - 1), r = e / n;
+            uint32_t v = x32_from_f32(f[q]);
+            if (v != 0xffffffffu) {
+                v = x32_mul(v, sc);
+                if (a.mask) {
+                    const uint32_t mk = mf[q] <= -3.0e38f ? 0xffffffffu : x32_from_f32(mf[q]);
+                    if (mk == 0xffffffffu) v = 0xffffffffu;
+                    else if (mk & k32_logmask) v = x32_add_lds(R.O, v, mk);
+                }
+            }
+            c[e + r * (rs - n)] = v;
+            atomicMax(&s_max[r], x32_canon(v));
+        }
     }
     __syncthreads();
     for (int64_t e = threadIdx.x; e < ne; e += blockDim.x) {
