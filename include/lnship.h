@@ -102,6 +102,10 @@ typedef struct lnship_mul_mat_args {
      * monte_seed is ignored */
     const uint16_t *monte_state;
     uint64_t monte_offset;
+    /* optional: when non-null, dst = residual + W x: the graph's next node,
+     * ADD of the product and a residual (lns_add, src/lns-ops.cpp:468-530),
+     * in the same launch.  residual is laid out as dst and may be dst. */
+    const float *residual;
 } lnship_mul_mat_args;
 
 int lnship16_mul_mat(int mode, const lnship_mul_mat_args *args, void *stream);
@@ -117,6 +121,15 @@ int lnship16_rms_norm(int mode, const float *src, float *dst, int64_t ncols, int
 int lnship16_rms_norm_state(int mode, const float *src, float *dst, int64_t ncols, int64_t nrows, float eps,
                             const uint16_t *monte_state, uint64_t monte_offset, void *stream);
 int lnship32_rms_norm(const float *src, float *dst, int64_t ncols, int64_t nrows, float eps, void *stream);
+/* RMS_NORM and the MUL by a norm weight row w[ncols] that follows it in the
+ * graph (lns_rms_norm, then lns_mul, src/lns-ops.cpp:468-530), in one launch.
+ * The Monte start is monte_seed, or lfsr_jump(*monte_state, monte_offset)
+ * when monte_state is non-null. */
+int lnship16_rms_norm_mul(int mode, const float *src, const float *w, float *dst, int64_t ncols, int64_t nrows,
+                          float eps, uint16_t monte_seed, const uint16_t *monte_state, uint64_t monte_offset,
+                          void *stream);
+int lnship32_rms_norm_mul(const float *src, const float *w, float *dst, int64_t ncols, int64_t nrows, float eps,
+                          void *stream);
 
 /* ---- SOFT_MAX (kernel_set::soft_max, :136; soft_max_args :62-71) --------
  * dst = softmax(src * scale + mask) over rows of src_ne[0] (lns_soft_max,

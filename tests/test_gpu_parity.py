@@ -263,6 +263,75 @@ def test_rms_norm_lns32(ln):
         same_bits(host(ln.rms_norm32(dev(x), 1e-5)), O.rms_norm32(x, 1e-5), f"rms_norm lns32 {shape}")
 
 
+def _elementwise16(fn, a, b):
+    """The oracle's LNS16 elementwise op on F32 arrays (b broadcast over a):
+    both through xlns16, fn on the codes, back to F32 (lns_add / lns_mul)."""
+    ca, cb = O.f2x16(a), O.f2x16(np.broadcast_to(b, a.shape).copy())
+    f = np.vectorize(lambda x, y: fn(int(x), int(y)), otypes=[np.uint16])
+    return O.x2f16(f(ca, cb))
+
+
+@pytest.mark.parametrize("mode", MODES)
+def test_rms_norm_mul(ln, mode):
+    # RMS_NORM then MUL by the norm weight row, in one launch
+    import ctypes
+    rng = np.random.default_rng(32)
+    P = lambda t: ctypes.c_void_p(t.data_ptr())
+    for shape in ((1, 576), (70, 16), (3, 1)):
+        print(f"\n[rms_norm_mul] {mode} {shape}", flush=True)
+        x = rng.standard_normal(shape).astype(np.float32)
+        w = (rng.standard_normal(shape[1]) * 2).astype(np.float32)
+        w[0] = 0.0
+        O.monte_set(7)
+        want = _elementwise16(O.lib().lno16_mul, O.rms_norm16(O.MODES[mode], x, 1e-5), w)
+        out = torch.empty(shape, dtype=torch.float32, device="cuda")
+        dx, dw = dev(x), dev(w)
+        ln.check(ln.lib().lnship16_rms_norm_mul(O.MODES[mode], P(dx), P(dw), P(out), shape[1], shape[0],
+                                                ctypes.c_float(1e-5), 7, None, 0, ln._stream()))
+        same_bits(host(out), want, f"rms_norm_mul {mode} {shape}")
+
+
+def test_rms_norm_mul_lns32(ln):
+    import ctypes
+    rng = np.random.default_rng(33)
+    P = lambda t: ctypes.c_void_p(t.data_ptr())
+    for shape in ((1, 576), (9, 2048), (4, 1)):
+        x = rng.standard_normal(shape).astype(np.float32)
+        w = (rng.standard_normal(shape[1]) * 2).astype(np.float32)
+        want = O.mul32(O.rms_norm32(x, 1e-5), w)
+        out = torch.empty(shape, dtype=torch.float32, device="cuda")
+        dx, dw = dev(x), dev(w)
+        ln.check(ln.lib().lnship32_rms_norm_mul(P(dx), P(dw), P(out), shape[1], shape[0], ctypes.c_float(1e-5),
+                                                ln._stream()))
+        same_bits(host(out), want, f"rms_norm_mul lns32 {shape}")
+
+
+@pytest.mark.parametrize("mode", MODES + ["lns32"])
+def test_mul_mat_residual(ln, mode):
+    # the ADD after a mul_mat fused into it, in place (dst = residual), as
+    # the decoder's attention output and down projections use it
+    rng = np.random.default_rng(34)
+    for (K, M, N) in ((576, 576, 1), (1536, 70, 3), (13, 33, 2)):
+        print(f"\n[mul_mat residual] {mode} K={K} M={M} N={N}", flush=True)
+        w = (rng.standard_normal((M, K)) * 0.02).astype(np.float32)
+        x = rng.standard_normal((N, K)).astype(np.float32)
+        r = rng.standard_normal((N, M)).astype(np.float32)
+        r[0, :2] = [0.0, -1.5]
+        acc = dev(r)
+        if mode == "lns32":
+            want = O.add32(O.mul_mat32(w, x), r)
+            wp, dx = ln.pack32(dev(w)), dev(x)
+            ln.mul_mat32_raw(wp.data_ptr(), dx.data_ptr(), acc.data_ptr(), K, M, N, residual=acc.data_ptr())
+        else:
+            m = O.MODES[mode]
+            O.monte_set(7)
+            want = _elementwise16(O.lib().lno16_add, O.mul_mat16_f32w(m, w[None, None], x[None, None])[0, 0], r)
+            wp, dx = ln.pack16(dev(w)), dev(x)
+            ln.mul_mat16_raw(m, wp.data_ptr(), dx.data_ptr(), acc.data_ptr(), K, M, N, seed=7,
+                             residual=acc.data_ptr())
+        same_bits(host(acc), want, f"mul_mat residual {mode} K={K} M={M} N={N}")
+
+
 # ------------------------------------------------------------------- softmax --
 
 def _causal(nq, nkv):

@@ -623,6 +623,7 @@ struct mm_args16 {
     const int32_t *ids;
     int64_t ids_t, x_bcast, n_w;
     unsigned long long *err;
+    const float *resid;   // non-null: dst = resid + W x (the graph's ADD), resid laid out as dst
 };
 
 // Records an index out of range: err[0] = 1, err[1] = the first such index.
@@ -718,8 +719,17 @@ __global__ __launch_bounds__(k_block * CG) void k_mm16(mm_args16 a, dev_tables T
     const uint16_t *xs = a.x + (zx * a.N + n0) * a.kp;
     const int64_t wstride = a.w_mstride * 8;   // between consecutive groups of 8 k
     float *ds = a.dst + z * a.dst_slice + n0 * a.dst_ld + m;
+    // output j, with the fused ADD of the residual when there is one: the
+    // F32 result and the residual through xlns16, added, back to F32 (the
+    // ADD node's arithmetic)
+    auto put = [&](int j, float y) {
+        const int64_t o = (ds - a.dst) + (int64_t)j * a.dst_ld;
+        if (a.resid)
+            y = T.rev16[x16_add_g(T.gauss16, x16_from_f32(T.cvt16, y), x16_from_f32(T.cvt16, a.resid[o]))];
+        a.dst[o] = y;
+    };
     if (a.K == 0) {
-        for (int j = 0; j < nc; j++) ds[(int64_t)j * a.dst_ld] = T.rev16[0];
+        for (int j = 0; j < nc; j++) put(j, T.rev16[0]);
         return;
     }
 
@@ -843,7 +853,7 @@ __global__ __launch_bounds__(k_block * CG) void k_mm16(mm_args16 a, dev_tables T
     }
 #pragma unroll
     for (int j = 0; j < NC; j++)
-        if (j < nc) ds[(int64_t)j * a.dst_ld] = T.rev16[R.finish(acc[j]) & 0xffffu];
+        if (j < nc) put(j, T.rev16[R.finish(acc[j]) & 0xffffu]);
 }
 
 // xlns32 (the LNS32 backend): plain sequential xlns32_add
@@ -857,6 +867,7 @@ struct mm_args32 {
     const int32_t *ids;   // MUL_MAT_ID, as in mm_args16
     int64_t ids_t, x_bcast, n_w;
     unsigned long long *err;
+    const float *resid;   // as in mm_args16
 };
 
 // One lane per weight row m and NC columns, CG column groups per workgroup
@@ -881,8 +892,15 @@ __global__ __launch_bounds__(k_block * CG) void k_mm32(mm_args32 a, dev_tables T
     const uint32_t *xs = a.x + (zx * a.N + n0) * a.kp;
     const int64_t wstride = a.w_mstride * 8;
     float *ds = a.dst + z * a.dst_slice + n0 * a.dst_ld + m;
+    // output j, with the fused ADD of the residual (xlns32 add of the two
+    // values, as the ADD node computes it) when there is one
+    auto put = [&](int j, float y) {
+        const int64_t o = (ds - a.dst) + (int64_t)j * a.dst_ld;
+        if (a.resid) y = x32_to_f32(x32_add(T.tab32, x32_from_f32(y), x32_from_f32(a.resid[o])));
+        a.dst[o] = y;
+    };
     if (a.K == 0) {
-        for (int j = 0; j < nc; j++) ds[(int64_t)j * a.dst_ld] = 0.0f;
+        for (int j = 0; j < nc; j++) put(j, 0.0f);
         return;
     }
     struct grp {
@@ -982,7 +1000,7 @@ __global__ __launch_bounds__(k_block * CG) void k_mm32(mm_args32 a, dev_tables T
     }
 #pragma unroll
     for (int j = 0; j < NC; j++)
-        if (j < nc) ds[(int64_t)j * a.dst_ld] = x32_to_f32(acc[j].s | acc[j].l);
+        if (j < nc) put(j, x32_to_f32(acc[j].s | acc[j].l));
 }
 
 // ---- sequential row sums over LDS --------------------------------------------
@@ -1044,9 +1062,9 @@ __device__ __forceinline__ void chain32(const x32_tab &O, acc_ls &acc, const uin
 // per row runs the sequential sum, all threads scale.
 
 template <int MODE>
-__global__ __launch_bounds__(k_block) void k_rms16(const float *__restrict__ src, float *__restrict__ dst,
-                                                   int64_t ncols, int64_t nrows, int rb, float eps,
-                                                   uint32_t seed, const uint16_t *state, uint64_t offset,
+__global__ __launch_bounds__(k_block) void k_rms16(const float *__restrict__ src, const float *__restrict__ w,
+                                                   float *__restrict__ dst, int64_t ncols, int64_t nrows, int rb,
+                                                   float eps, uint32_t seed, const uint16_t *state, uint64_t offset,
                                                    dev_tables T) {
     extern __shared__ __align__(16) char lds[];
     const red16<MODE> R = stage_tables<MODE>(T, lds);
@@ -1098,6 +1116,13 @@ __global__ __launch_bounds__(k_block) void k_rms16(const float *__restrict__ src
         for (int q = 0; q < B; q++) c[q] = x16_from_f32(T.cvt16, f[q]);
 #pragma unroll
         for (int q = 0; q < B; q++) f[q] = T.rev16[x16_mul(c[q], s_inv[min(e0 + q * nt, nel - 1) / nc])];
+        if (w) {   // the fused MUL by the weight row, through xlns16 as the MUL node
+            float g[B];
+#pragma unroll
+            for (int q = 0; q < B; q++) g[q] = w[min(e0 + q * nt, nel - 1) % nc];
+#pragma unroll
+            for (int q = 0; q < B; q++) f[q] = T.rev16[x16_mul(x16_from_f32(T.cvt16, f[q]), x16_from_f32(T.cvt16, g[q]))];
+        }
         // only the element's own thread stores (dst may be src)
 #pragma unroll
         for (int q = 0; q < B; q++)
@@ -1105,8 +1130,9 @@ __global__ __launch_bounds__(k_block) void k_rms16(const float *__restrict__ src
     }
 }
 
-__global__ __launch_bounds__(k_block) void k_rms32(const float *__restrict__ src, float *__restrict__ dst,
-                                                   int64_t ncols, int64_t nrows, int rb, float eps, dev_tables T) {
+__global__ __launch_bounds__(k_block) void k_rms32(const float *__restrict__ src, const float *__restrict__ w,
+                                                   float *__restrict__ dst, int64_t ncols, int64_t nrows, int rb,
+                                                   float eps, dev_tables T) {
     extern __shared__ __align__(16) char lds[];
     const red16<LNSHIP_SUM32> R = stage_tables<LNSHIP_SUM32>(T, lds);
     uint32_t *sq = reinterpret_cast<uint32_t *>(lds + k_lds_tab32);
@@ -1139,14 +1165,21 @@ __global__ __launch_bounds__(k_block) void k_rms32(const float *__restrict__ src
     }
     __syncthreads();
     for (int e0 = threadIdx.x; e0 < nel; e0 += B * nt) {
-        float f[B];
+        float f[B], g[B];
 #pragma unroll
-        for (int q = 0; q < B; q++) f[q] = src[r0 * ncols + min(e0 + q * nt, nel - 1)];
-        // only the element's own thread stores (dst may be src)
+        for (int q = 0; q < B; q++) {
+            f[q] = src[r0 * ncols + min(e0 + q * nt, nel - 1)];
+            g[q] = w ? w[min(e0 + q * nt, nel - 1) % nc] : 0.0f;
+        }
+        // only the element's own thread stores (dst may be src); with w the
+        // fused MUL by the weight row in xlns32, as the MUL node
 #pragma unroll
         for (int q = 0; q < B; q++)
-            if (e0 + q * nt < nel)
-                dst[r0 * ncols + e0 + q * nt] = x32_to_f32(x32_mul(x32_from_f32(f[q]), s_inv[(e0 + q * nt) / nc]));
+            if (e0 + q * nt < nel) {
+                float y = x32_to_f32(x32_mul(x32_from_f32(f[q]), s_inv[(e0 + q * nt) / nc]));
+                if (w) y = x32_to_f32(x32_mul(x32_from_f32(y), x32_from_f32(g[q])));
+                dst[r0 * ncols + e0 + q * nt] = y;
+            }
     }
 }
 
@@ -1816,15 +1849,15 @@ static int launch_mm32(const mm_args32 &m, const dev_tables &T, int64_t nslices,
 }
 
 template <int MODE>
-static int launch_rms16(const float *src, float *dst, int64_t ncols, int64_t nrows, float eps, uint16_t seed,
-                        const uint16_t *state, uint64_t offset, const dev_tables &T, hipStream_t st) {
+static int launch_rms16(const float *src, const float *w, float *dst, int64_t ncols, int64_t nrows, float eps,
+                        uint16_t seed, const uint16_t *state, uint64_t offset, const dev_tables &T, hipStream_t st) {
     const int64_t rs = (ncols + 7) & ~(int64_t)7;
     const int rb = rows_per_block<MODE>(rs, 2);
     if (rb < 1) return fail(LNSHIP_ERANGE, "rms_norm: row too long for LDS%s");
     const int lds = ((lds_tables_bytes<MODE>() + 15) & ~15) + (int)(rb * rs * 2);
     if (int rc = set_lds(k_rms16<MODE>, lds)) return rc;
-    hipLaunchKernelGGL(k_rms16<MODE>, dim3((unsigned)((nrows + rb - 1) / rb)), dim3(k_block), lds, st, src, dst, ncols,
-                       nrows, rb, eps, (uint32_t)seed, state, offset, T);
+    hipLaunchKernelGGL(k_rms16<MODE>, dim3((unsigned)((nrows + rb - 1) / rb)), dim3(k_block), lds, st, src, w, dst,
+                       ncols, nrows, rb, eps, (uint32_t)seed, state, offset, T);
     LNSHIP_HIP(hipGetLastError());
     return 0;
 }
@@ -2110,6 +2143,7 @@ int lnship16_mul_mat(int mode, const lnship_mul_mat_args *a, void *stream) {
                 a->ne02, a->ne12, a->ne12 / a->ne02, a->ne13 / a->ne03,
                 wms, a->w_slice ? a->w_slice : kp * wms, dld, a->dst_slice ? a->dst_slice : a->N * dld,
                 a->monte_seed, a->monte_state, a->monte_offset};
+    m.resid = a->residual;
     switch (mode) {
         case LNSHIP_BASE: return dispatch_mm16<LNSHIP_BASE>(m, s->T, nslices, sh, st);
         case LNSHIP_MONTE: return dispatch_mm16<LNSHIP_MONTE>(m, s->T, nslices, sh, st);
@@ -2141,6 +2175,7 @@ int lnship32_mul_mat(const lnship_mul_mat_args *a, void *stream) {
     mm_args32 m{(const uint32_t *)a->w, (const uint32_t *)xs, a->dst, a->K, kp, a->M, a->N,
                 a->ne02, a->ne12, a->ne12 / a->ne02, a->ne13 / a->ne03,
                 wms, a->w_slice ? a->w_slice : kp * wms, dld, a->dst_slice ? a->dst_slice : a->N * dld};
+    m.resid = a->residual;
     const mm16_shape sh = mm_shape_x32(m.M, m.N, nslices, kp, s->cus, 4);
     switch (sh.nc * 10 + sh.cg) {
         case 12: return launch_mm32<1, 2>(m, s->T, nslices, st);
@@ -2229,8 +2264,9 @@ uint64_t lnship16_mul_mat_id_draws(int mode, int64_t K, int64_t M, int64_t n_exp
     return (uint64_t)n_expert_used * (uint64_t)n_tokens * (uint64_t)M * (uint64_t)(K - 1);
 }
 
-static int rms16_common(int mode, const float *src, float *dst, int64_t ncols, int64_t nrows, float eps,
-                        uint16_t monte_seed, const uint16_t *monte_state, uint64_t monte_offset, void *stream) {
+static int rms16_common(int mode, const float *src, const float *w, float *dst, int64_t ncols, int64_t nrows,
+                        float eps, uint16_t monte_seed, const uint16_t *monte_state, uint64_t monte_offset,
+                        void *stream) {
     device_state *s = state();
     if (!s) return LNSHIP_ENOINIT;
     if (mode < 0 || mode > 3 || ncols < 0 || nrows < 0) return fail(LNSHIP_EINVAL, "rms_norm: bad argument%s");
@@ -2238,29 +2274,37 @@ static int rms16_common(int mode, const float *src, float *dst, int64_t ncols, i
     if ((nrows + 63) / 64 > 2147483647) return fail(LNSHIP_ERANGE, "rms_norm: too many rows%s");
     hipStream_t st = (hipStream_t)stream;
     switch (mode) {
-        case LNSHIP_BASE: return launch_rms16<LNSHIP_BASE>(src, dst, ncols, nrows, eps, monte_seed, monte_state, monte_offset, s->T,
+        case LNSHIP_BASE: return launch_rms16<LNSHIP_BASE>(src, w, dst, ncols, nrows, eps, monte_seed, monte_state, monte_offset, s->T,
                                                                  st);
-        case LNSHIP_MONTE: return launch_rms16<LNSHIP_MONTE>(src, dst, ncols, nrows, eps, monte_seed, monte_state, monte_offset, s->T,
+        case LNSHIP_MONTE: return launch_rms16<LNSHIP_MONTE>(src, w, dst, ncols, nrows, eps, monte_seed, monte_state, monte_offset, s->T,
                                                                  st);
-        case LNSHIP_LPVIP: return launch_rms16<LNSHIP_LPVIP>(src, dst, ncols, nrows, eps, monte_seed, monte_state, monte_offset, s->T,
+        case LNSHIP_LPVIP: return launch_rms16<LNSHIP_LPVIP>(src, w, dst, ncols, nrows, eps, monte_seed, monte_state, monte_offset, s->T,
                                                                  st);
-        default: return launch_rms16<LNSHIP_SUM32>(src, dst, ncols, nrows, eps, monte_seed, monte_state, monte_offset, s->T,
+        default: return launch_rms16<LNSHIP_SUM32>(src, w, dst, ncols, nrows, eps, monte_seed, monte_state, monte_offset, s->T,
                                                                  st);
     }
 }
 
 int lnship16_rms_norm(int mode, const float *src, float *dst, int64_t ncols, int64_t nrows, float eps,
                       uint16_t monte_seed, void *stream) {
-    return rms16_common(mode, src, dst, ncols, nrows, eps, monte_seed, nullptr, 0, stream);
+    return rms16_common(mode, src, nullptr, dst, ncols, nrows, eps, monte_seed, nullptr, 0, stream);
 }
 
 int lnship16_rms_norm_state(int mode, const float *src, float *dst, int64_t ncols, int64_t nrows, float eps,
                             const uint16_t *monte_state, uint64_t monte_offset, void *stream) {
     if (!monte_state) return fail(LNSHIP_EINVAL, "rms_norm: null monte_state%s");
-    return rms16_common(mode, src, dst, ncols, nrows, eps, 0, monte_state, monte_offset, stream);
+    return rms16_common(mode, src, nullptr, dst, ncols, nrows, eps, 0, monte_state, monte_offset, stream);
 }
 
-int lnship32_rms_norm(const float *src, float *dst, int64_t ncols, int64_t nrows, float eps, void *stream) {
+int lnship16_rms_norm_mul(int mode, const float *src, const float *w, float *dst, int64_t ncols, int64_t nrows,
+                          float eps, uint16_t monte_seed, const uint16_t *monte_state, uint64_t monte_offset,
+                          void *stream) {
+    if (!w) return fail(LNSHIP_EINVAL, "rms_norm_mul: null weight row%s");
+    return rms16_common(mode, src, w, dst, ncols, nrows, eps, monte_seed, monte_state, monte_offset, stream);
+}
+
+static int rms32_common(const float *src, const float *w, float *dst, int64_t ncols, int64_t nrows, float eps,
+                        void *stream) {
     device_state *s = state();
     if (!s) return LNSHIP_ENOINIT;
     if (ncols < 0 || nrows < 0) return fail(LNSHIP_EINVAL, "rms_norm: bad argument%s");
@@ -2271,9 +2315,19 @@ int lnship32_rms_norm(const float *src, float *dst, int64_t ncols, int64_t nrows
     const int lds = k_lds_tab32 + (int)(rb * rs * 4);
     if (int rc = set_lds(k_rms32, lds)) return rc;
     hipLaunchKernelGGL(k_rms32, dim3((unsigned)((nrows + rb - 1) / rb)), dim3(k_block), lds, (hipStream_t)stream, src,
-                       dst, ncols, nrows, rb, eps, s->T);
+                       w, dst, ncols, nrows, rb, eps, s->T);
     LNSHIP_HIP(hipGetLastError());
     return 0;
+}
+
+int lnship32_rms_norm(const float *src, float *dst, int64_t ncols, int64_t nrows, float eps, void *stream) {
+    return rms32_common(src, nullptr, dst, ncols, nrows, eps, stream);
+}
+
+int lnship32_rms_norm_mul(const float *src, const float *w, float *dst, int64_t ncols, int64_t nrows, float eps,
+                          void *stream) {
+    if (!w) return fail(LNSHIP_EINVAL, "rms_norm_mul: null weight row%s");
+    return rms32_common(src, w, dst, ncols, nrows, eps, stream);
 }
 
 

@@ -29,7 +29,7 @@ class MulMatArgs(ctypes.Structure):
                 ("ne02", c_i64), ("ne03", c_i64), ("ne12", c_i64), ("ne13", c_i64),
                 ("x_ld", c_i64), ("x_slice", c_i64), ("monte_seed", ctypes.c_uint16),
                 ("w_mstride", c_i64), ("w_slice", c_i64), ("dst_ld", c_i64), ("dst_slice", c_i64),
-                ("monte_state", c_p), ("monte_offset", ctypes.c_uint64)]
+                ("monte_state", c_p), ("monte_offset", ctypes.c_uint64), ("residual", c_p)]
 
 
 class SoftMaxArgs(ctypes.Structure):
@@ -76,6 +76,9 @@ def lib():
         "lnship16_rms_norm_state": (ctypes.c_int, [ctypes.c_int, c_p, c_p, c_i64, c_i64, ctypes.c_float,
                                                    c_p, ctypes.c_uint64, c_p]),
         "lnship32_rms_norm": (ctypes.c_int, [c_p, c_p, c_i64, c_i64, ctypes.c_float, c_p]),
+        "lnship16_rms_norm_mul": (ctypes.c_int, [ctypes.c_int, c_p, c_p, c_p, c_i64, c_i64, ctypes.c_float,
+                                                 ctypes.c_uint16, c_p, ctypes.c_uint64, c_p]),
+        "lnship32_rms_norm_mul": (ctypes.c_int, [c_p, c_p, c_p, c_i64, c_i64, ctypes.c_float, c_p]),
         "lnship16_soft_max": (ctypes.c_int, [ctypes.c_int, ctypes.POINTER(SoftMaxArgs), c_p]),
         "lnship32_soft_max": (ctypes.c_int, [ctypes.POINTER(SoftMaxArgs), c_p]),
         "lnship16_mul_mat_draws": (ctypes.c_uint64, [ctypes.c_int, c_i64, c_i64, c_i64, c_i64, c_i64]),
@@ -246,11 +249,12 @@ def _mm_args(wp, x, out, K, M, ne02, ne03, seed):
 
 
 def mul_mat16_raw(mode, w_ptr, x_ptr, dst_ptr, K, M, N, ne02=1, ne03=1, ne12=1, ne13=1, x_ld=0, x_slice=0,
-                  seed=7, w_mstride=0, w_slice=0, dst_ld=0, dst_slice=0, stream=None):
-    """mul_mat on raw device pointers (ints), with every stride of the C ABI."""
+                  seed=7, w_mstride=0, w_slice=0, dst_ld=0, dst_slice=0, stream=None, residual=None):
+    """mul_mat on raw device pointers (ints), with every stride of the C ABI;
+    residual (a pointer laid out as dst) adds the following ADD node."""
     sd, st, off = seed_fields(seed)
     a = MulMatArgs(w_ptr, x_ptr, dst_ptr, K, M, N, ne02, ne03, ne12, ne13, x_ld, x_slice, sd,
-                   w_mstride, w_slice, dst_ld, dst_slice, st, off)
+                   w_mstride, w_slice, dst_ld, dst_slice, st, off, residual)
     check(lib().lnship16_mul_mat(mode, ctypes.byref(a), stream if stream is not None else _stream()))
 
 
@@ -267,10 +271,11 @@ def mul_mat16(mode, wp, x, K, M, ne02=1, ne03=1, seed=7, out=None):
 
 
 def mul_mat32_raw(w_ptr, x_ptr, dst_ptr, K, M, N, ne02=1, ne03=1, ne12=1, ne13=1, x_ld=0, x_slice=0,
-                  w_mstride=0, w_slice=0, dst_ld=0, dst_slice=0, stream=None):
-    """xlns32 mul_mat on raw device pointers (ints), with every stride of the C ABI."""
+                  w_mstride=0, w_slice=0, dst_ld=0, dst_slice=0, stream=None, residual=None):
+    """xlns32 mul_mat on raw device pointers (ints), with every stride of the
+    C ABI; residual as in mul_mat16_raw."""
     a = MulMatArgs(w_ptr, x_ptr, dst_ptr, K, M, N, ne02, ne03, ne12, ne13, x_ld, x_slice, 0,
-                   w_mstride, w_slice, dst_ld, dst_slice)
+                   w_mstride, w_slice, dst_ld, dst_slice, None, 0, residual)
     check(lib().lnship32_mul_mat(ctypes.byref(a), stream if stream is not None else _stream()))
 
 

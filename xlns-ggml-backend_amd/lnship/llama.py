@@ -221,13 +221,12 @@ class LlamaLNS16:
         draws = lib().lnship16_mul_mat_draws(self.mode, K, M, N, ne12, ne13)
         mul_mat16_raw(self.mode, w, x_ptr, dst_ptr, K, M, N, seed=self._seed(draws), stream=self._stream, **kw)
 
-    def _rms(self, x_ptr, dst_ptr, ncols, nrows):
+    def _rms_mul(self, x_ptr, w_ptr, dst_ptr, ncols, nrows):
+        """rms_norm of nrows rows, then the MUL by the norm weight row w, in
+        one launch (the MUL takes no draws)."""
         sd, st, off = seed_fields(self._seed(lib().lnship16_rms_norm_draws(self.mode, ncols, nrows)))
-        if st is not None:
-            check(lib().lnship16_rms_norm_state(self.mode, x_ptr, dst_ptr, ncols, nrows, self.cfg.eps, st, off,
-                                                self._stream))
-        else:
-            check(lib().lnship16_rms_norm(self.mode, x_ptr, dst_ptr, ncols, nrows, self.cfg.eps, sd, self._stream))
+        check(lib().lnship16_rms_norm_mul(self.mode, x_ptr, w_ptr, dst_ptr, ncols, nrows, self.cfg.eps, sd, st,
+                                          off or 0, self._stream))
 
     def _softmax(self, x_ptr, ne, mask_ptr, mne, scale, dst_ptr):
         from . import SoftMaxArgs
@@ -269,8 +268,7 @@ class LlamaLNS16:
         check(L.lnship_causal_mask(P(pos_dev), T, n_kv, P(mask), st))
         for il, W in enumerate(self.layers):
             last = il == c.n_layer - 1
-            self._rms(P(x), P(h), e, T)
-            check(L.lnship16_mul(P(h), P(W["attn_norm"]), T * e, e, P(h), st))
+            self._rms_mul(P(x), P(W["attn_norm"]), P(h), e, T)
             self._mm(W["wqkv"].data_ptr(), P(h), P(qkv), e, nqkv, T)
             check(L.lnship16_rope(P(qkv), nqkv, P(pos_dev), T, nh, hd, hd, 0, P(self.cos_sin), P(q), st))
             check(L.lnship16_store_kv(P(qkv, nq), nqkv, P(pos_dev), T, nkv, hd, hd, P(self.cos_sin),
@@ -288,20 +286,20 @@ class LlamaLNS16:
             self._mm(self.vcache[il].data_ptr() + 2 * cbase, P(kq), P(att), n_kv, hd, Tq, ne02=nkv, ne03=nseq,
                      ne12=nh, ne13=nseq, x_ld=n_kv, x_slice=Tq * n_kv, w_slice=self.vslice, dst_ld=nq,
                      dst_slice=hd)
-            self._mm(W["wo"].data_ptr(), P(att), P(o), nq, e, T)
             # after the last layer's attention only the output rows go on
             rows = 1 if last and not batch else T
             r0 = (T - rows) * e
-            check(L.lnship16_add(P(o, r0), P(x, r0), rows * e, rows * e, P(x), st))
-            self._rms(P(x), P(h), e, rows)
-            check(L.lnship16_mul(P(h), P(W["ffn_norm"]), rows * e, e, P(h), st))
+            if rows == T:   # x += Wo att: the residual ADD inside the mul_mat
+                self._mm(W["wo"].data_ptr(), P(att), P(x), nq, e, T, residual=P(x))
+            else:
+                self._mm(W["wo"].data_ptr(), P(att), P(o), nq, e, T)
+                check(L.lnship16_add(P(o, r0), P(x, r0), rows * e, rows * e, P(x), st))
+            self._rms_mul(P(x), P(W["ffn_norm"]), P(h), e, rows)
             self._mm(W["wug"].data_ptr(), P(h), P(ug), e, 2 * f, rows)
             check(L.lnship16_swiglu(P(ug, f), 2 * f, P(ug), 2 * f, P(sw), f, rows, st))
-            self._mm(W["wdown"].data_ptr(), P(sw), P(o), f, e, rows)
-            check(L.lnship16_add(P(o), P(x), rows * e, rows * e, P(x), st))
+            self._mm(W["wdown"].data_ptr(), P(sw), P(x), f, e, rows, residual=P(x))
         nout = T if batch else 1
-        self._rms(P(x), P(h), e, nout)
-        check(L.lnship16_mul(P(h), P(self.out_norm), nout * e, e, P(h), st))
+        self._rms_mul(P(x), P(self.out_norm), P(h), e, nout)
         self._mm(self.tok_embd.data_ptr(), P(h), P(logits), e, c.n_vocab, nout)
         if batch:
             return logits[: T * c.n_vocab].view(T, c.n_vocab)
@@ -480,8 +478,7 @@ class LlamaLNS32:
         from . import SoftMaxArgs
         for il, W in enumerate(self.layers):
             last = il == c.n_layer - 1
-            check(L.lnship32_rms_norm(P(x), P(h), e, T, c.eps, st))
-            check(L.lnship32_mul(P(h), P(W["attn_norm"]), T * e, e, P(h), st))
+            check(L.lnship32_rms_norm_mul(P(x), P(W["attn_norm"]), P(h), e, T, c.eps, st))
             mm(W["wqkv"].data_ptr(), P(h), P(qkv), e, nqkv, T)
             check(L.lnship32_rope(P(qkv), nqkv, P(pos_dev), T, nh, hd, hd, 0, P(self.cos_sin), P(q), st))
             check(L.lnship32_store_kv(P(qkv, nq), nqkv, P(pos_dev), T, nkv, hd, hd, P(self.cos_sin),
@@ -495,18 +492,18 @@ class LlamaLNS32:
             check(L.lnship32_soft_max(ctypes.byref(a), st))
             mm(self.vcache[il].data_ptr(), P(kq), P(att), n_kv, hd, T, ne02=nkv, ne12=nh, x_ld=n_kv,
                x_slice=T * n_kv, w_slice=self.vslice, dst_ld=nq, dst_slice=hd)
-            mm(W["wo"].data_ptr(), P(att), P(o), nq, e, T)
             rows = 1 if last else T
             r0 = (T - rows) * e
-            check(L.lnship32_add(P(o, r0), P(x, r0), rows * e, rows * e, P(x), st))
-            check(L.lnship32_rms_norm(P(x), P(h), e, rows, c.eps, st))
-            check(L.lnship32_mul(P(h), P(W["ffn_norm"]), rows * e, e, P(h), st))
+            if rows == T:   # x += Wo att: the residual ADD inside the mul_mat
+                mm(W["wo"].data_ptr(), P(att), P(x), nq, e, T, residual=P(x))
+            else:
+                mm(W["wo"].data_ptr(), P(att), P(o), nq, e, T)
+                check(L.lnship32_add(P(o, r0), P(x, r0), rows * e, rows * e, P(x), st))
+            check(L.lnship32_rms_norm_mul(P(x), P(W["ffn_norm"]), P(h), e, rows, c.eps, st))
             mm(W["wug"].data_ptr(), P(h), P(ug), e, 2 * f, rows)
             check(L.lnship32_swiglu(P(ug, f), 2 * f, P(ug), 2 * f, P(sw), f, rows, st))
-            mm(W["wdown"].data_ptr(), P(sw), P(o), f, e, rows)
-            check(L.lnship32_add(P(o), P(x), rows * e, rows * e, P(x), st))
-        check(L.lnship32_rms_norm(P(x), P(h), e, 1, c.eps, st))
-        check(L.lnship32_mul(P(h), P(self.out_norm), e, e, P(h), st))
+            mm(W["wdown"].data_ptr(), P(sw), P(x), f, e, rows, residual=P(x))
+        check(L.lnship32_rms_norm_mul(P(x), P(self.out_norm), P(h), e, 1, c.eps, st))
         mm(self.tok_embd.data_ptr(), P(h), P(logits), e, c.n_vocab, 1)
         return logits[: c.n_vocab]
 
