@@ -197,6 +197,27 @@ int lnship32_store_kv(const float *x, int64_t x_ld, const int32_t *pos, int64_t 
                       int rope_n_dims, const float *cos_sin, uint32_t *cache, int64_t cache_m,
                       int64_t cache_slice, int cache_transposed, const int32_t *seq, int64_t seq_stride,
                       void *stream);
+/* The three nodes that follow a fused QKV mul_mat, in one launch: ROPE of
+ * the query heads (lns_rope / lns32_rope, normal rope, as lnship16_rope) and
+ * the key and value heads stored into their caches (as lnship16_store_kv:
+ * keys rotated, row-major cache; values transposed).  qkv rows [ntok] of
+ * n_head query, n_head_kv key, then n_head_kv value heads of head_dim
+ * floats each, qkv_ld floats apart. */
+typedef struct lnship_qkv_store_args {
+    const float *qkv;
+    int64_t qkv_ld;
+    const int32_t *pos;         /* [ntok] positions, device */
+    int64_t ntok, n_head, n_head_kv, head_dim;
+    int rope_n_dims;            /* rotated dims of q and k (> 0, even) */
+    const float *cos_sin;       /* lnship_rope_table layout */
+    float *q_dst;               /* [ntok][n_head][head_dim] */
+    void *k_cache, *v_cache;    /* uint16_t (xlns16) or uint32_t (xlns32) codes */
+    int64_t cache_m, k_slice, v_slice;
+    const int32_t *seq;         /* optional, as in lnship16_store_kv */
+    int64_t seq_stride;
+} lnship_qkv_store_args;
+int lnship16_rope_store_kv(const lnship_qkv_store_args *args, void *stream);
+int lnship32_rope_store_kv(const lnship_qkv_store_args *args, void *stream);
 
 /* ggml views on the device (tensors in the ggml device buffer type): the
  * elements of a 4-D strided view (byte strides nb, as ggml_tensor::nb)

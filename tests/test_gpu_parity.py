@@ -332,6 +332,49 @@ def test_mul_mat_residual(ln, mode):
         same_bits(host(acc), want, f"mul_mat residual {mode} K={K} M={M} N={N}")
 
 
+@pytest.mark.parametrize("w32", [False, True], ids=["lns16", "lns32"])
+def test_rope_store_kv_fused(ln, w32):
+    # the fused launch writes exactly what rope + two store_kv launches write
+    # (the decoder tests pin both against the oracle's graph), caches and q
+    # included, with two sequences and positions out of order
+    import ctypes
+    rng = np.random.default_rng(35)
+    L, st = ln.lib(), ln._stream()
+    P = lambda t, off=0: ctypes.c_void_p(t.data_ptr() + off * t.element_size())
+    T, nh, nkv, hd, n_ctx = 3, 4, 2, 16, 24
+    nqkv = (nh + 2 * nkv) * hd
+    qkv = dev((rng.standard_normal((T, nqkv)) * 2).astype(np.float32))
+    pos = dev(np.array([5, 0, 17], np.int32))
+    seq = dev(np.array([1, 0, 1], np.int32))
+    rt = np.empty(n_ctx * hd, np.float32)
+    ln.check(L.lnship_rope_table(ctypes.c_float(10000.0), hd, n_ctx, ctypes.c_void_p(rt.ctypes.data)))
+    cs = dev(rt)
+    kslice = ((hd + 7) // 8 * 8) * n_ctx
+    vslice = kslice
+    seq_stride = nkv * kslice
+    dt = torch.int32 if w32 else torch.int16
+    pre = "lnship32_" if w32 else "lnship16_"
+    outs = []
+    for fused in (False, True):
+        kc = torch.full((2 * seq_stride,), 0x1234, dtype=dt, device="cuda")
+        vc = torch.full((2 * seq_stride,), 0x1234, dtype=dt, device="cuda")
+        q = torch.full((T * nh * hd,), 7.0, dtype=torch.float32, device="cuda")
+        if fused:
+            a = ln.QkvStoreArgs(P(qkv), nqkv, P(pos), T, nh, nkv, hd, hd, P(cs), P(q), P(kc), P(vc), n_ctx, kslice,
+                                vslice, P(seq), seq_stride)
+            ln.check(getattr(L, pre + "rope_store_kv")(ctypes.byref(a), st))
+        else:
+            ln.check(getattr(L, pre + "rope")(P(qkv), nqkv, P(pos), T, nh, hd, hd, 0, P(cs), P(q), st))
+            ln.check(getattr(L, pre + "store_kv")(P(qkv, nh * hd), nqkv, P(pos), T, nkv, hd, hd, P(cs), P(kc), n_ctx,
+                                                  kslice, 0, P(seq), seq_stride, st))
+            ln.check(getattr(L, pre + "store_kv")(P(qkv, (nh + nkv) * hd), nqkv, P(pos), T, nkv, hd, 0, P(cs), P(vc),
+                                                  n_ctx, vslice, 1, P(seq), seq_stride, st))
+        outs.append((host(q), host(kc), host(vc)))
+    for name, g, w in zip(("q", "k cache", "v cache"), outs[1], outs[0]):
+        assert np.array_equal(g.view(np.uint32) if g.dtype == np.float32 else g,
+                              w.view(np.uint32) if w.dtype == np.float32 else w), name
+
+
 # ------------------------------------------------------------------- softmax --
 
 def _causal(nq, nkv):

@@ -1478,33 +1478,70 @@ __device__ __forceinline__ void rope_pair(const F &f, const float *xr, int64_t j
     r1 = f.add(f.mul(x0, sn), f.mul(x1, c));
 }
 
+// item i of a rope: a rotated pair (j < n_dims / 2) or a passthrough element
+// of row (token, head); ntok * nhead * (n_dims / 2 + ne0 - n_dims) items
+template <class F>
+__device__ __forceinline__ void rope_item(const F &f, int64_t i, const float *x, int64_t x_ld, const int32_t *pos,
+                                          int64_t nhead, int64_t ne0, int n_dims, int neox, const float *cos_sin,
+                                          float *dst) {
+    const int64_t half = n_dims / 2, per = half + (ne0 - n_dims);
+    const int64_t row = i / per, j = i - row * per;
+    const int64_t t = row / nhead, h = row - t * nhead;
+    const float *xr = x + t * x_ld + h * ne0;
+    float *yr = dst + (t * nhead + h) * ne0;
+    if (j < half) {
+        int64_t i0, i1;
+        uint32_t r0, r1;
+        rope_pair(f, xr, j, n_dims, neox, cos_sin + (int64_t)pos[t] * half * 2, i0, i1, r0, r1);
+        yr[i0] = f.to(r0);
+        yr[i1] = f.to(r1);
+    } else {
+        const int64_t i0 = n_dims + (j - half);
+        yr[i0] = f.to(f.from(xr[i0]));
+    }
+}
+
 template <int W>
 __global__ void k_rope(const float *__restrict__ x, int64_t x_ld, const int32_t *__restrict__ pos, int64_t ntok,
                        int64_t nhead, int64_t ne0, int n_dims, int neox, const float *__restrict__ cos_sin,
                        float *__restrict__ dst, dev_tables T) {
     const fmt_t<W> F{T};
-    const int64_t half = n_dims / 2, per = half + (ne0 - n_dims);
-    const int64_t n = ntok * nhead * per;
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)blockDim.x * gridDim.x) {
-        const int64_t row = i / per, j = i - row * per;
-        const int64_t t = row / nhead, h = row - t * nhead;
-        const float *xr = x + t * x_ld + h * ne0;
-        float *yr = dst + (t * nhead + h) * ne0;
-        if (j < half) {
-            int64_t i0, i1;
-            uint32_t r0, r1;
-            rope_pair(F, xr, j, n_dims, neox, cos_sin + (int64_t)pos[t] * half * 2, i0, i1, r0, r1);
-            yr[i0] = F.to(r0);
-            yr[i1] = F.to(r1);
-        } else {
-            const int64_t i0 = n_dims + (j - half);
-            yr[i0] = F.to(F.from(xr[i0]));
-        }
-    }
+    const int64_t n = ntok * nhead * (n_dims / 2 + (ne0 - n_dims));
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)blockDim.x * gridDim.x)
+        rope_item(F, i, x, x_ld, pos, nhead, ne0, n_dims, neox, cos_sin, dst);
 }
 
 // F32 value -> IEEE half (round to nearest even) -> F32 -> LNS, as the KV
 // cache stores and reads it
+// item i (element (token, head, d)) of a KV-cache store;
+// ntok * nhead * ne0 items
+template <class F, class C>
+__device__ __forceinline__ void store_kv_item(const F &f, int64_t i, const float *x, int64_t x_ld, const int32_t *pos,
+                                              int64_t nhead, int64_t ne0, int rope_n_dims, const float *cos_sin,
+                                              C *cache, int64_t cache_m, int64_t cache_slice, int transposed,
+                                              const int32_t *seq, int64_t seq_stride) {
+    const int64_t half = rope_n_dims / 2;
+    const int64_t row = i / ne0, d = i - row * ne0;
+    const int64_t t = row / nhead, h = row - t * nhead;
+    const float *xr = x + t * x_ld + h * ne0;
+    const int64_t p = pos[t];
+    float v;
+    if (rope_n_dims > 0 && d < rope_n_dims) {
+        // normal rope: element d belongs to pair d / 2
+        int64_t i0, i1;
+        uint32_t r0, r1;
+        rope_pair(f, xr, d / 2, rope_n_dims, 0, cos_sin + p * half * 2, i0, i1, r0, r1);
+        v = f.to((d & 1) ? r1 : r0);
+    } else if (rope_n_dims > 0) {
+        v = f.to(f.from(xr[d]));
+    } else {
+        v = xr[d];
+    }
+    const int64_t o = transposed ? h * cache_slice + ((p >> 3) * ne0 + d) * 8 + (p & 7)
+                                 : h * cache_slice + ((d >> 3) * cache_m + p) * 8 + (d & 7);
+    cache[(seq ? (int64_t)seq[t] * seq_stride : 0) + o] = (C)f.from(__half2float(__float2half_rn(v)));
+}
+
 template <int W>
 __global__ void k_store_kv(const float *__restrict__ x, int64_t x_ld, const int32_t *__restrict__ pos, int64_t ntok,
                            int64_t nhead, int64_t ne0, int rope_n_dims, const float *__restrict__ cos_sin,
@@ -1512,28 +1549,31 @@ __global__ void k_store_kv(const float *__restrict__ x, int64_t x_ld, const int3
                            int transposed, const int32_t *__restrict__ seq, int64_t seq_stride, dev_tables T) {
     const fmt_t<W> F{T};
     const int64_t n = ntok * nhead * ne0;
-    const int64_t half = rope_n_dims / 2;
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)blockDim.x * gridDim.x) {
-        const int64_t row = i / ne0, d = i - row * ne0;
-        const int64_t t = row / nhead, h = row - t * nhead;
-        const float *xr = x + t * x_ld + h * ne0;
-        const int64_t p = pos[t];
-        float v;
-        if (rope_n_dims > 0 && d < rope_n_dims) {
-            // normal rope: element d belongs to pair d / 2
-            int64_t i0, i1;
-            uint32_t r0, r1;
-            rope_pair(F, xr, d / 2, rope_n_dims, 0, cos_sin + p * half * 2, i0, i1, r0, r1);
-            v = F.to((d & 1) ? r1 : r0);
-        } else if (rope_n_dims > 0) {
-            v = F.to(F.from(xr[d]));
-        } else {
-            v = xr[d];
-        }
-        const int64_t o = transposed ? h * cache_slice + ((p >> 3) * ne0 + d) * 8 + (p & 7)
-                                     : h * cache_slice + ((d >> 3) * cache_m + p) * 8 + (d & 7);
-        cache[(seq ? (int64_t)seq[t] * seq_stride : 0) + o] =
-            (typename fmt_t<W>::code_t)F.from(__half2float(__float2half_rn(v)));
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)blockDim.x * gridDim.x)
+        store_kv_item(F, i, x, x_ld, pos, nhead, ne0, rope_n_dims, cos_sin, cache, cache_m, cache_slice, transposed,
+                      seq, seq_stride);
+}
+
+// The query rope and the key / value cache stores after a fused QKV
+// mul_mat, as one grid: items [0, nq) rope the query heads, the next nk
+// store the (rotated) key heads, the last nk the value heads.
+template <int W>
+__global__ void k_rope_store_kv(lnship_qkv_store_args a, dev_tables T) {
+    using C = typename fmt_t<W>::code_t;
+    const fmt_t<W> F{T};
+    const int64_t hd = a.head_dim, nd = a.rope_n_dims;
+    const int64_t nq = a.ntok * a.n_head * (nd / 2 + (hd - nd)), nk = a.ntok * a.n_head_kv * hd;
+    const float *xk = a.qkv + a.n_head * hd, *xv = xk + a.n_head_kv * hd;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < nq + 2 * nk;
+         i += (int64_t)blockDim.x * gridDim.x) {
+        if (i < nq)
+            rope_item(F, i, a.qkv, a.qkv_ld, a.pos, a.n_head, hd, (int)nd, 0, a.cos_sin, a.q_dst);
+        else if (i < nq + nk)
+            store_kv_item(F, i - nq, xk, a.qkv_ld, a.pos, a.n_head_kv, hd, (int)nd, a.cos_sin, (C *)a.k_cache,
+                          a.cache_m, a.k_slice, 0, a.seq, a.seq_stride);
+        else
+            store_kv_item(F, i - nq - nk, xv, a.qkv_ld, a.pos, a.n_head_kv, hd, 0, a.cos_sin, (C *)a.v_cache,
+                          a.cache_m, a.v_slice, 1, a.seq, a.seq_stride);
     }
 }
 
@@ -1961,6 +2001,22 @@ static int store_kv_common(const float *x, int64_t x_ld, const int32_t *pos, int
     hipLaunchKernelGGL(k_store_kv<W>, dim3(grid_for(n, 4)), dim3(k_block), 0, (hipStream_t)stream, x, x_ld, pos, ntok,
                        nhead, ne0, rope_n_dims, cos_sin, cache, cache_m, cache_slice, cache_transposed, seq, seq_stride,
                        s->T);
+    LNSHIP_HIP(hipGetLastError());
+    return 0;
+}
+
+template <int W>
+static int rope_store_kv_common(const lnship_qkv_store_args *a, void *stream) {
+    device_state *s = state();
+    if (!s) return LNSHIP_ENOINIT;
+    if (!a || a->ntok < 0 || a->n_head < 0 || a->n_head_kv < 0 || a->head_dim <= 0 || a->head_dim % 8 ||
+        a->rope_n_dims <= 0 || a->rope_n_dims % 2 || a->rope_n_dims > a->head_dim ||
+        a->qkv_ld < (a->n_head + 2 * a->n_head_kv) * a->head_dim || (a->seq && a->seq_stride < 0))
+        return fail(LNSHIP_EINVAL, "rope_store_kv: bad shape%s");
+    const int64_t hd = a->head_dim, nd = a->rope_n_dims;
+    const int64_t n = a->ntok * (a->n_head * (nd / 2 + hd - nd) + 2 * a->n_head_kv * hd);
+    if (n == 0) return 0;
+    hipLaunchKernelGGL(k_rope_store_kv<W>, dim3(grid_for(n, 4)), dim3(k_block), 0, (hipStream_t)stream, *a, s->T);
     LNSHIP_HIP(hipGetLastError());
     return 0;
 }
@@ -2445,6 +2501,8 @@ int lnship32_store_kv(const float *x, int64_t x_ld, const int32_t *pos, int64_t 
     return store_kv_common<32>(x, x_ld, pos, ntok, nhead, ne0, rope_n_dims, cos_sin, cache, cache_m, cache_slice,
                                cache_transposed, seq, seq_stride, stream);
 }
+int lnship16_rope_store_kv(const lnship_qkv_store_args *a, void *stream) { return rope_store_kv_common<16>(a, stream); }
+int lnship32_rope_store_kv(const lnship_qkv_store_args *a, void *stream) { return rope_store_kv_common<32>(a, stream); }
 
 static bool strided_ok(const int64_t *ne, const int64_t *nb, strided4 &g) {
     if (!ne || !nb) return false;

@@ -45,6 +45,13 @@ class MulMatIdArgs(ctypes.Structure):
                 ("monte_state", c_p), ("monte_offset", ctypes.c_uint64)]
 
 
+class QkvStoreArgs(ctypes.Structure):
+    _fields_ = [("qkv", c_p), ("qkv_ld", c_i64), ("pos", c_p), ("ntok", c_i64), ("n_head", c_i64),
+                ("n_head_kv", c_i64), ("head_dim", c_i64), ("rope_n_dims", ctypes.c_int), ("cos_sin", c_p),
+                ("q_dst", c_p), ("k_cache", c_p), ("v_cache", c_p), ("cache_m", c_i64), ("k_slice", c_i64),
+                ("v_slice", c_i64), ("seq", c_p), ("seq_stride", c_i64)]
+
+
 def build():
     import subprocess
     subprocess.check_call(["make", "-s", "-C", PKG_DIR])
@@ -79,6 +86,8 @@ def lib():
         "lnship16_rms_norm_mul": (ctypes.c_int, [ctypes.c_int, c_p, c_p, c_p, c_i64, c_i64, ctypes.c_float,
                                                  ctypes.c_uint16, c_p, ctypes.c_uint64, c_p]),
         "lnship32_rms_norm_mul": (ctypes.c_int, [c_p, c_p, c_p, c_i64, c_i64, ctypes.c_float, c_p]),
+        "lnship16_rope_store_kv": (ctypes.c_int, [ctypes.POINTER(QkvStoreArgs), c_p]),
+        "lnship32_rope_store_kv": (ctypes.c_int, [ctypes.POINTER(QkvStoreArgs), c_p]),
         "lnship16_soft_max": (ctypes.c_int, [ctypes.c_int, ctypes.POINTER(SoftMaxArgs), c_p]),
         "lnship32_soft_max": (ctypes.c_int, [ctypes.POINTER(SoftMaxArgs), c_p]),
         "lnship16_mul_mat_draws": (ctypes.c_uint64, [ctypes.c_int, c_i64, c_i64, c_i64, c_i64, c_i64]),

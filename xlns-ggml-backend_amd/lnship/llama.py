@@ -34,7 +34,8 @@ from dataclasses import dataclass
 
 import numpy as np
 
-from . import BASE, MONTE, LPVIP, SUM32, check, init, kp, lfsr_advance, lib, mul_mat16_raw, mul_mat32_raw, seed_fields
+from . import (BASE, MONTE, LPVIP, SUM32, QkvStoreArgs, check, init, kp, lfsr_advance, lib, mul_mat16_raw,
+               mul_mat32_raw, seed_fields)
 
 KV_PAD = 256   # llama.cpp pads the KV view to 256 cells without flash attention
 
@@ -270,13 +271,11 @@ class LlamaLNS16:
             last = il == c.n_layer - 1
             self._rms_mul(P(x), P(W["attn_norm"]), P(h), e, T)
             self._mm(W["wqkv"].data_ptr(), P(h), P(qkv), e, nqkv, T)
-            check(L.lnship16_rope(P(qkv), nqkv, P(pos_dev), T, nh, hd, hd, 0, P(self.cos_sin), P(q), st))
-            check(L.lnship16_store_kv(P(qkv, nq), nqkv, P(pos_dev), T, nkv, hd, hd, P(self.cos_sin),
-                                      P(self.kcache[il], cbase), c.n_ctx, self.kslice, 0, seq_ids, self.seq_stride,
-                                      st))
-            check(L.lnship16_store_kv(P(qkv, nq + nkv * hd), nqkv, P(pos_dev), T, nkv, hd, 0, P(self.cos_sin),
-                                      P(self.vcache[il], cbase), c.n_ctx, self.vslice, 1, seq_ids, self.seq_stride,
-                                      st))
+            # rope(q) and the K / V cache stores (k rotated) in one launch
+            qs = QkvStoreArgs(P(qkv), nqkv, P(pos_dev), T, nh, nkv, hd, hd, P(self.cos_sin), P(q),
+                              P(self.kcache[il], cbase), P(self.vcache[il], cbase), c.n_ctx, self.kslice,
+                              self.vslice, seq_ids, self.seq_stride)
+            check(L.lnship16_rope_store_kv(ctypes.byref(qs), st))
             Tq = 1 if batch else T   # query rows per sequence
             # kq[s][h][t][j] = K_s,j . q_s,t (GQA: query head h reads kv head h / (nh / nkv))
             self._mm(self.kcache[il].data_ptr() + 2 * cbase, P(q), P(kq), hd, n_kv, Tq, ne02=nkv, ne03=nseq,
@@ -480,11 +479,9 @@ class LlamaLNS32:
             last = il == c.n_layer - 1
             check(L.lnship32_rms_norm_mul(P(x), P(W["attn_norm"]), P(h), e, T, c.eps, st))
             mm(W["wqkv"].data_ptr(), P(h), P(qkv), e, nqkv, T)
-            check(L.lnship32_rope(P(qkv), nqkv, P(pos_dev), T, nh, hd, hd, 0, P(self.cos_sin), P(q), st))
-            check(L.lnship32_store_kv(P(qkv, nq), nqkv, P(pos_dev), T, nkv, hd, hd, P(self.cos_sin),
-                                      P(self.kcache[il]), c.n_ctx, self.kslice, 0, None, 0, st))
-            check(L.lnship32_store_kv(P(qkv, nq + nkv * hd), nqkv, P(pos_dev), T, nkv, hd, 0, P(self.cos_sin),
-                                      P(self.vcache[il]), c.n_ctx, self.vslice, 1, None, 0, st))
+            qs = QkvStoreArgs(P(qkv), nqkv, P(pos_dev), T, nh, nkv, hd, hd, P(self.cos_sin), P(q),
+                              P(self.kcache[il]), P(self.vcache[il]), c.n_ctx, self.kslice, self.vslice, None, 0)
+            check(L.lnship32_rope_store_kv(ctypes.byref(qs), st))
             mm(self.kcache[il].data_ptr(), P(q), P(kq), hd, n_kv, T, ne02=nkv, ne12=nh, x_ld=nq, x_slice=hd,
                w_mstride=c.n_ctx, w_slice=self.kslice)
             a = SoftMaxArgs(P(kq), (ctypes.c_int64 * 4)(n_kv, T, nh, 1), P(mask), (ctypes.c_int64 * 4)(n_kv, T, 1, 1),
