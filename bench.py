@@ -236,8 +236,10 @@ def gemv_roofline(model, ln, torch, reps=4):
     e.synchronize()
     n = len(calls)
     total_us = s.elapsed_time(e) * 1e3 / reps
-    # algorithmic bytes: xlns16 weights once per weight slice, F32 in / out
-    total_b = sum(2 * K * M * kw.get("ne02", 1) + 4 * K * N * kw.get("ne12", 1) + 4 * M * N * kw.get("ne12", 1)
+    # algorithmic bytes: xlns16 weights once per weight slice, F32 in / out,
+    # and the F32 residual read by the launches that fuse the ADD after them
+    total_b = sum(2 * K * M * kw.get("ne02", 1) + 4 * K * N * kw.get("ne12", 1)
+                  + 4 * M * N * kw.get("ne12", 1) * (2 if kw.get("residual") is not None else 1)
                   for _, _, _, K, M, N, kw in calls)
     return total_b / n, total_us / n, n
 
