@@ -244,6 +244,70 @@ def gemv_roofline(model, ln, torch, reps=4):
     return total_b / n, total_us / n, n
 
 
+def chain_bound(model, ln, torch, mode):
+    """The dependent-step bound of one decode token.  steps: the sum over the
+    token's launches of their chain length (K per mul_mat, n per rms_norm row,
+    n - 1 per soft_max row); a launch's chains run side by side and the
+    launches one after another.  ns_per_step: the slope of GEMV launch time
+    against K at M = 576 (K = 576 and 1536, each a graph of 20 launches timed
+    between HIP events on the replay stream), so each launch's fixed cost
+    stays out of it.  bound_tok_s = 1 / (steps * ns_per_step)."""
+    c = model.cfg
+    steps = []
+    orig = (model._mm, model._rms_mul, model._softmax)
+
+    def mm(w, x_ptr, dst_ptr, K, M, N, **kw):
+        steps.append(K)
+        orig[0](w, x_ptr, dst_ptr, K, M, N, **kw)
+
+    def rms(x_ptr, w_ptr, dst_ptr, ncols, nrows):
+        steps.append(ncols)
+        orig[1](x_ptr, w_ptr, dst_ptr, ncols, nrows)
+
+    def sm(x_ptr, ne, mask_ptr, mne, scale, dst_ptr):
+        steps.append(ne[0] - 1)
+        orig[2](x_ptr, ne, mask_ptr, mne, scale, dst_ptr)
+
+    model._mm, model._rms_mul, model._softmax = mm, rms, sm
+    try:
+        tok = model._buf("rtok", 1, torch.int32)
+        pos = model._buf("rpos", 1, torch.int32)
+        tok.fill_(1)
+        pos.fill_(model.n_past - 1)   # the last timed position again (its KV row is rewritten)
+        from lnship.llama import n_kv_for
+        model.forward(1, tok, pos, n_kv_for(model.n_past, c.n_ctx))
+        torch.cuda.synchronize()
+    finally:
+        model._mm, model._rms_mul, model._softmax = orig
+    st = lambda: ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    us = {}
+    M = 576
+    for K in (576, 1536):
+        g0 = torch.Generator(device="cpu").manual_seed(K)
+        wp = ln.pack16((torch.randn(M, K, generator=g0) * 0.02).cuda())
+        x = torch.randn(1, K, generator=g0).cuda()
+        y = torch.empty(1, M, device="cuda")
+        launch = lambda: ln.mul_mat16_raw(ln.MODES[mode], wp.data_ptr(), x.data_ptr(), y.data_ptr(), K, M, 1,
+                                          seed=7, stream=st())
+        launch()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for _ in range(20):
+                launch()
+        g.replay()
+        s_ev, e_ev = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s_ev.record()
+        g.replay()
+        e_ev.record()
+        e_ev.synchronize()
+        us[K] = s_ev.elapsed_time(e_ev) * 1e3 / 20
+    ns_step = (us[1536] - us[576]) * 1e3 / (1536 - 576)
+    total = sum(steps)
+    return {"steps_per_token": total, "ns_per_step": round(ns_step, 2),
+            "launch_us_k576": round(us[576], 2), "launch_us_k1536": round(us[1536], 2),
+            "bound_tok_s": round(1e9 / (total * ns_step), 3), "chain_launches_per_token": len(steps)}
+
+
 def measured_traffic(mode):
     """HBM bytes per decode mul_mat launch from the committed rocprofv3 PMC
     summary (FETCH_SIZE and WRITE_SIZE passes scaled by a plain copy), or None
@@ -380,6 +444,8 @@ def main():
         3 * cfg.n_ff * cfg.n_embd) + cfg.n_vocab * cfg.n_embd
     b_launch, us_launch, n_launch = gemv_roofline(model, lnship, torch)
     achieved = b_launch / (us_launch * 1e-6) / 1e9
+    chain = chain_bound(model, lnship, torch, args.mode)
+    chain["frac"] = round(decode_tok_s / chain["bound_tok_s"], 4)
     traffic, traffic_src = measured_traffic(args.mode)
     out = {
         "metric": METRIC,
@@ -408,6 +474,7 @@ def main():
                                % args.mode,
                      "launches_per_token": n_launch, "avg_launch_us": round(us_launch, 3),
                      "bytes_per_launch": int(b_launch)},
+        "chain_bound": chain,
         "reference_published": {"rtx2050_sum32_decode_tok_s": 7.31,
                                 "source": "experiments/layer-by-layer/CPU-vs-GPU.md:21 (Q4_K_M, 5-token prompt)"},
         "setup_s": round(t_setup, 2),
