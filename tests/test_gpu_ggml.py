@@ -52,6 +52,18 @@ def test_ggml_graph_lnship32_device_buffers():
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("args", [["--mode", "sum32"], ["--mode", "monte"], ["--mode", "base", "--device-buffers"],
+                                  ["--w32"], ["--w32", "--device-buffers"]],
+                         ids=["sum32", "monte", "base-device", "lns32", "lns32-device"])
+def test_ggml_graph_fused_pairs(args):
+    # RMS_NORM -> MUL by the norm weight and MUL_MAT -> ADD of the residual
+    # whose intermediates feed only the next node run as one launch each; the
+    # outputs and (monte) the LFSR state after the graph equal the oracle's
+    mode = args[1] if args[0] == "--mode" else "sum32"
+    _run(args + ["--fused"], dict(os.environ, GGML_LNS16_SUM=mode))
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("w32", [False, True])
 def test_ggml_graph_data_movement(w32):
     # SCALE, and the KV-cache writes (SET_ROWS, CPY into an F16 view) and row

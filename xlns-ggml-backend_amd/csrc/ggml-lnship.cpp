@@ -903,6 +903,7 @@ static void backend_free(ggml_backend_t b) {
 }
 
 static void run_node(context &ctx, ggml_tensor *node);
+static bool run_fused(context &ctx, ggml_cgraph *g, int i);
 
 static ggml_status backend_graph_compute(ggml_backend_t b, ggml_cgraph *g) {
     context &ctx = *static_cast<context *>(b->context);
@@ -910,6 +911,10 @@ static ggml_status backend_graph_compute(ggml_backend_t b, ggml_cgraph *g) {
         ggml_tensor *node = g->nodes[i];
         if ((node->flags & GGML_TENSOR_FLAG_COMPUTE) == 0) continue;
         if (classify(node) == kind::view || nelements(node) == 0) continue;
+        if (run_fused(ctx, g, i)) {   // node i and node i + 1 in one launch
+            i++;
+            continue;
+        }
         run_node(ctx, node);
     }
     // results in device buffers are complete before ggml reads or copies them
@@ -1618,6 +1623,90 @@ static void op_mul_mat_id(context &ctx, ggml_tensor *dst) {
         lib_ok(lnship16_mul_mat_id(mode, &args, ctx.get_stream()), "lnship16_mul_mat_id");
     }
     ctx.download(args.dst, dst);
+}
+
+// ---- fused node pairs -----------------------------------------------------
+// llama.cpp's graphs follow RMS_NORM with the MUL by its norm weight, and a
+// MUL_MAT with the ADD of the residual.  When node i's result feeds node i + 1
+// and nothing else (no other node or view reads it, and it is not a graph
+// output), the pair runs as one launch (lnship16_rms_norm_mul, the mul_mat's
+// residual) and node i's tensor is not written.  Each fused launch keeps the
+// F32 value between the two nodes and its conversion, as the two nodes do.
+
+static bool feeds_only(const ggml_cgraph *g, int i, const ggml_tensor *next) {
+    const ggml_tensor *t = g->nodes[i];
+    if (t->flags & GGML_TENSOR_FLAG_OUTPUT) return false;
+    int uses = 0;
+    for (int s = 0; s < GGML_MAX_SRC; s++) uses += next->src[s] == t;
+    if (uses != 1) return false;
+    for (int j = i + 2; j < g->n_nodes; j++) {
+        const ggml_tensor *u = g->nodes[j];
+        if (u->view_src == t) return false;
+        for (int s = 0; s < GGML_MAX_SRC; s++)
+            if (u->src[s] == t) return false;
+    }
+    return true;
+}
+
+// an F32 tensor (upload() gathers any layout into a dense copy)
+static bool plain_f32(const ggml_tensor *t) { return t->type == GGML_TYPE_F32; }
+
+static bool run_fused(context &ctx, ggml_cgraph *g, int i) {
+    if (i + 1 >= g->n_nodes) return false;
+    ggml_tensor *t = g->nodes[i], *next = g->nodes[i + 1];
+    if ((next->flags & GGML_TENSOR_FLAG_COMPUTE) == 0 || !feeds_only(g, i, next)) return false;
+    const kind k = classify(t), kn = classify(next);
+    if (k == kind::rms_norm && kn == kind::mul && next->src[0] == t && plain_f32(t->src[0])) {
+        // MUL by one weight row of ne[0] floats
+        const ggml_tensor *w = next->src[1];
+        if (!plain_f32(w) || w->ne[0] != t->ne[0] || nelements(w) != w->ne[0] || !same_shape(next, t)) return false;
+        const int64_t nc = t->ne[0], nr = nrows(t);
+        const float *x = ctx.upload(t->src[0], R_SRC0);
+        const float *wd = ctx.upload(w, R_SRC1);
+        float *y = ctx.out_f32(next, R_DST);
+        const float eps = op_f32(t, 0);
+        if (ctx.fmt->w32) {
+            lib_ok(lnship32_rms_norm_mul(x, wd, y, nc, nr, eps, ctx.get_stream()), "lnship32_rms_norm_mul");
+        } else {
+            const int mode = node_mode(t);
+            const uint16_t seed = reserve_monte(mode, lnship16_rms_norm_draws(mode, nc, nr));
+            lib_ok(lnship16_rms_norm_mul(mode, x, wd, y, nc, nr, eps, seed, nullptr, 0, ctx.get_stream()),
+                   "lnship16_rms_norm_mul");
+        }
+        ctx.download(y, next);
+        return true;
+    }
+    if (k == kind::mul_mat && kn == kind::add) {
+        // ADD of a residual of the product's shape (either operand order:
+        // the xlns add is commutative)
+        const ggml_tensor *r = next->src[0] == t ? next->src[1] : next->src[0];
+        if (r == t || !plain_f32(r) || !same_shape(r, t) || !same_shape(next, t)) return false;
+        const ggml_tensor *a = t->src[0], *b = t->src[1];
+        lnship_mul_mat_args args;
+        std::memset(&args, 0, sizeof args);
+        args.w = ctx.lns_matrix(a);
+        args.x = ctx.upload(b, R_SRC1);
+        args.residual = ctx.upload(r, R_AUX);
+        args.dst = ctx.out_f32(next, R_DST);
+        args.K = a->ne[0];
+        args.M = a->ne[1];
+        args.N = b->ne[1];
+        args.ne02 = a->ne[2];
+        args.ne03 = a->ne[3];
+        args.ne12 = b->ne[2];
+        args.ne13 = b->ne[3];
+        if (ctx.fmt->w32) {
+            lib_ok(lnship32_mul_mat(&args, ctx.get_stream()), "lnship32_mul_mat");
+        } else {
+            const int mode = node_mode(t);
+            args.monte_seed =
+                reserve_monte(mode, lnship16_mul_mat_draws(mode, args.K, args.M, args.N, args.ne12, args.ne13));
+            lib_ok(lnship16_mul_mat(mode, &args, ctx.get_stream()), "lnship16_mul_mat");
+        }
+        ctx.download(args.dst, next);
+        return true;
+    }
+    return false;
 }
 
 static void run_node(context &ctx, ggml_tensor *node) {
