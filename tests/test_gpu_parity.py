@@ -384,6 +384,20 @@ def _causal(nq, nkv):
     return m
 
 
+def _underflowing(rng):
+    # rows whose exps are exactly zero (log 0) in the middle, at the end, or
+    # everywhere but the maximum: the chain stops after the last nonzero one
+    x = rng.standard_normal((6, 96)).astype(np.float32)
+    x[0, 40:] = -1e4
+    x[1, 10:50] = -1e4
+    x[2, :] = -1e4
+    x[2, 7] = 0.0
+    x[3, ::3] = -3e4
+    x[4, 95] = 50.0
+    x[5, 0] = 50.0
+    return x
+
+
 @pytest.mark.parametrize("mode", MODES)
 def test_soft_max(ln, mode):
     rng = np.random.default_rng(40)
@@ -396,6 +410,7 @@ def test_soft_max(ln, mode):
          np.where(rng.random((8, 64)) < 0.2, -np.inf, rng.standard_normal((8, 64))).astype(np.float32), 0.5),
         ("1100 wide", rng.standard_normal((3, 1100)).astype(np.float32), _causal(3, 1100), 1.0),
         ("singleton", rng.standard_normal((7, 1)).astype(np.float32), None, 1.0),
+        ("underflow", _underflowing(rng), None, 1.0),
     ]
     for name, x, mask, scale in cases:
         print(f"\n[soft_max] {mode} {name}", flush=True)
@@ -411,6 +426,8 @@ def test_soft_max_lns32(ln):
     mask = _causal(16, 128)
     same_bits(host(ln.soft_max32(dev(x), dev(mask), 0.125)), O.soft_max32(x, mask, 0.125), "soft_max lns32")
     same_bits(host(ln.soft_max32(dev(x), None, 1.0)), O.soft_max32(x, None, 1.0), "soft_max lns32 unmasked")
+    u = _underflowing(rng)
+    same_bits(host(ln.soft_max32(dev(u), None, 1.0)), O.soft_max32(u, None, 1.0), "soft_max lns32 underflow")
 
 
 # ------------------------------------------------- LNS32 elementwise ops --

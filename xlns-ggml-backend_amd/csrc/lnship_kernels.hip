@@ -27,6 +27,8 @@ constexpr int k_block = 256;
 constexpr int k_max_devices = 64;
 // LDS budget of a workgroup on gfx950 (160 KiB per CU)
 constexpr int k_lds_bytes = 160 * 1024;
+// what the row kernels' static shared arrays may take beside their dynamic LDS
+constexpr int k_lds_static = 2048;
 // the xlns32 tables plus four zero entries (an interpolation on them gives 0)
 // the xlns32 tables, a zero pair, and 512 (origin, shift) descriptors of the
 // direct interpolation grid, indexed by (opposite signs, binade of d)
@@ -1216,11 +1218,13 @@ __global__ __launch_bounds__(k_block) void k_softmax16(sm_args a, dev_tables T) 
     __shared__ int32_t s_max[64];
     __shared__ uint32_t s_tot[64];
     __shared__ const float *s_mrow[64];
+    __shared__ int s_last[64];   // a row's last element with a nonzero exp
     const int64_t r0 = (int64_t)blockIdx.x * a.rb;
     const int nr = (int)min<int64_t>(a.rb, a.ne1 * a.ne2 * a.ne3 - r0);
     const int n = (int)a.n, nel = nr * n;   // a row fits in LDS, so 32-bit counts suffice
     const int rs = (n + 7) & ~7;            // LDS rows 16-byte aligned
     if ((int)threadIdx.x < nr) {
+        s_last[threadIdx.x] = 0;
         s_max[threadIdx.x] = x16_canon(0xffffu);
         s_mrow[threadIdx.x] = a.mask ? mask_row(a, r0 + threadIdx.x) : nullptr;
     }
@@ -1287,7 +1291,13 @@ __global__ __launch_bounds__(k_block) void k_softmax16(sm_args a, dev_tables T) 
         // redoes the last element may read it after its owner wrote it)
 #pragma unroll
         for (int q = 0; q < B; q++)
-            if (e0 + q * nt < nel) c[o[q]] = (uint16_t)sh[q];
+            if (e0 + q * nt < nel) {
+                c[o[q]] = (uint16_t)sh[q];
+                if (sh[q] & k16_logmask) {
+                    const int e = e0 + q * nt, r = e / n;
+                    atomicMax(&s_last[r], e - r * n);
+                }
+            }
     }
     __syncthreads();
     if ((int)threadIdx.x < nr) {
@@ -1297,7 +1307,13 @@ __global__ __launch_bounds__(k_block) void k_softmax16(sm_args a, dev_tables T) 
             s = lfsr_jump(T, monte_start(T, a.seed, a.state, a.offset), (uint64_t)(r0 + r) * (uint64_t)(a.n - 1));
         const uint16_t *row = c + r * rs;
         typename red16<MODE>::acc_t acc = R.start(row[0], s);
-        if (a.n > 1) chain16(R, acc, row, 1, (int)a.n, s);
+        // The row's trailing exps of log 0 (masked or underflowed) come after
+        // its maximum, whose exp is 1; the sum is at least 1 there, every mode
+        // adds nothing at a distance of 2^14 and more, so the chain stops at
+        // the last nonzero exp (Monte: the draws after it are not taken; the
+        // next op's start does not depend on them)
+        const int n_eff = s_last[r] + 1;
+        if (n_eff > 1) chain16(R, acc, row, 1, n_eff, s);
         s_tot[r] = R.finish(acc) & 0xffffu;
     }
     __syncthreads();
@@ -1323,12 +1339,14 @@ __global__ __launch_bounds__(k_block) void k_softmax32(sm_args a, dev_tables T) 
     __shared__ int32_t s_max[64];
     __shared__ uint32_t s_tot[64];
     __shared__ const float *s_mrow[64];
+    __shared__ int s_last[64];   // a row's last element with a nonzero exp
     const int64_t r0 = (int64_t)blockIdx.x * a.rb;
     const int nr = (int)min<int64_t>(a.rb, a.ne1 * a.ne2 * a.ne3 - r0);
     const int64_t ne = (int64_t)nr * a.n;
     const int n = (int)a.n, nel = nr * n;
     const int rs = ((int)a.n + 3) & ~3;   // LDS rows 16-byte aligned
     if ((int)threadIdx.x < nr) {
+        s_last[threadIdx.x] = 0;
         s_max[threadIdx.x] = x32_canon(0xffffffffu);
         s_mrow[threadIdx.x] = a.mask ? mask_row(a, r0 + threadIdx.x) : nullptr;
     }
@@ -1370,13 +1388,17 @@ __global__ __launch_bounds__(k_block) void k_softmax32(sm_args a, dev_tables T) 
         const int64_t o = e + r * (rs - a.n);
         const float fv = x32_to_f32(x32_add_lds(R.O, c[o], mx ^ k32_sign));
         c[o] = x32_from_f32((float)exp((double)fv));
+        if (c[o] & k32_logmask) atomicMax(&s_last[r], (int)(e - (int64_t)r * a.n));
     }
     __syncthreads();
     if ((int)threadIdx.x < nr) {
         const int r = threadIdx.x;
         const uint32_t *row = c + r * rs;
         acc_ls acc{row[0] & k32_logmask, row[0] & k32_sign};
-        if (a.n > 1) chain32(R.O, acc, row, 1, (int)a.n);
+        // trailing exps of log 0 add nothing to a sum of at least 1 (as in
+        // k_softmax16): the chain stops at the last nonzero exp
+        const int n_eff = s_last[r] + 1;
+        if (n_eff > 1) chain32(R.O, acc, row, 1, n_eff);
         s_tot[r] = acc.s | acc.l;
     }
     __syncthreads();
@@ -1717,12 +1739,12 @@ __global__ void k_causal_mask(const int32_t *__restrict__ pos, int64_t ntok, int
 template <int MODE>
 static int64_t max_row(int elem_bytes) {
     // rows are staged at a 16-byte stride
-    return ((k_lds_bytes - ((lds_tables_bytes<MODE>() + 15) & ~15) - 1024) / 16) * (16 / elem_bytes);
+    return ((k_lds_bytes - ((lds_tables_bytes<MODE>() + 15) & ~15) - k_lds_static) / 16) * (16 / elem_bytes);
 }
 
 template <int MODE>
 static int rows_per_block(int64_t ncols, int elem_bytes) {
-    const int64_t avail = k_lds_bytes - ((lds_tables_bytes<MODE>() + 15) & ~15) - 1024;
+    const int64_t avail = k_lds_bytes - ((lds_tables_bytes<MODE>() + 15) & ~15) - k_lds_static;
     int64_t rb = avail / std::max<int64_t>(1, ncols * elem_bytes);
     return (int)std::min<int64_t>(64, rb);
 }
