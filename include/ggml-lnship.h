@@ -4,10 +4,17 @@
  * LNS arithmetic on an AMD Instinct GPU (gfx950) through hand-written HIP
  * kernels.  Two devices, like the reference's LNSCUDA backend
  * (lns-backend/include/ggml-lns-cuda.h:10-23):
- *   LNSHIP16 - xlns16; bit-identical to the LNS16 CPU backend built with the
- *              same GGML_LNS16_SUM (base, monte, lpvip or sum32).  Here the
- *              mode is read from GGML_LNS16_SUM at run time (default base).
- *   LNSHIP32 - xlns32; matches the LNS32 CPU backend.
+ *   LNSHIP16 - xlns16 in the summation mode GGML_LNS16_SUM names (base,
+ *              monte, lpvip or sum32), read at run time (default base).
+ *              Every mode is bit-exact against the repository's CPU
+ *              restatement of the LNS16 backend (oracle/).  Against the
+ *              reference's own printed outputs: base reproduces every one;
+ *              sum32 every one except two figures of its xlns32_alt adder;
+ *              monte and lpvip do not (their xlnscpp sources are absent and
+ *              the restated adders are contradicted by the printed figures).
+ *   LNSHIP32 - xlns32, bit-exact against the restated LNS32 backend, whose
+ *              xlns32_alt adder misses two of the reference's printed
+ *              LNS32 figures.
  * Both are ACCEL devices on host buffers: ggml keeps every tensor in host
  * memory, each op uploads its inputs and downloads its result, and weights
  * (tensors in GGML_BACKEND_BUFFER_USAGE_WEIGHTS buffers) are converted to LNS

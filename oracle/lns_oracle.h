@@ -99,6 +99,9 @@ uint32_t lno32_recip(uint32_t a);
 uint32_t lno32_exp(uint32_t a);
 int      lno32_gt(uint32_t a, uint32_t b);
 const int32_t *lno32_table(const char *name, size_t *n);
+/* 0: the restated xlns32_alt adder (default); 1: its sb replaced by the one
+ * the reference's experiments ran with (tests only); returns the old value */
+int      lno32_set_variant(int v);
 uint32_t lno32_vec_dot(const uint32_t *a, const uint32_t *b, size_t n);
 void     lno32_rms_norm_row(const uint32_t *x, uint32_t *dst, size_t n, uint32_t eps);
 void     lno32_softmax_row(const uint32_t *a, const uint32_t *mask, uint32_t *c, size_t n, uint32_t scale);

@@ -78,6 +78,7 @@ def lib():
         "lno32_mul": (u32, [u32, u32]),
         "lno32_div": (u32, [u32, u32]),
         "lno32_add": (u32, [u32, u32]),
+        "lno32_set_variant": (ctypes.c_int, [ctypes.c_int]),
         "lno32_sub": (u32, [u32, u32]),
         "lno32_sqrt": (u32, [u32]),
         "lno32_recip": (u32, [u32]),

@@ -1307,11 +1307,13 @@ __global__ __launch_bounds__(k_block) void k_softmax16(sm_args a, dev_tables T) 
             s = lfsr_jump(T, monte_start(T, a.seed, a.state, a.offset), (uint64_t)(r0 + r) * (uint64_t)(a.n - 1));
         const uint16_t *row = c + r * rs;
         typename red16<MODE>::acc_t acc = R.start(row[0], s);
-        // The row's trailing exps of log 0 (masked or underflowed) come after
-        // its maximum, whose exp is 1; the sum is at least 1 there, every mode
-        // adds nothing at a distance of 2^14 and more, so the chain stops at
-        // the last nonzero exp (Monte: the draws after it are not taken; the
-        // next op's start does not depend on them)
+        // The entries after the row's last nonzero exp lie after its maximum
+        // (whose exp, 1, is nonzero), so the running sum there is at least 1;
+        // each of them is an exp of log 0 (masked or underflowed), which every
+        // mode's adder (as restated here) adds as nothing at a distance of 2^14
+        // and more.  So the chain stops at the last nonzero exp (Monte: the
+        // draws after it are not taken; the next op's start does not depend
+        // on them)
         const int n_eff = s_last[r] + 1;
         if (n_eff > 1) chain16(R, acc, row, 1, n_eff, s);
         s_tot[r] = R.finish(acc) & 0xffffu;
