@@ -112,10 +112,14 @@ def mark_outputs(nodes, fused):
     with fused, the nodes that feed only the next node (RMS_NORM before its
     norm-weight MUL, MUL_MAT before its residual ADD) stay unflagged, so
     graph_compute fuses the pairs, and are left out of the check (a fused
-    pair does not write the intermediate tensor).  Returns the checked keys."""
+    pair does not write the intermediate tensor).  "mm_self" stays unflagged
+    too but is checked: its ADD reads the product's own activation and writes
+    over it in place, a pair graph_compute must not fuse.  Returns the
+    checked keys."""
     skip = {"rms", "mm", "down"} if fused else set()
+    noflag = {"mm_self"} if fused else set()
     for k, tn in nodes.items():
-        if k not in skip:
+        if k not in skip and k not in noflag:
             tn.flags |= FLAG_OUTPUT
     return [k for k in nodes if k not in skip]
 
@@ -153,6 +157,8 @@ def run16(mode_name, policy=None, dev=False, fused=False):
     xmoe = f32(T, 1, 64)
     ids_moe = np.array([[5, 0], [2, 2], [1, 4]], np.int32)
     w_codes = O.f2x16(f32(200, E, scale=0.05))   # GGML_TYPE_LNS16 weights
+    xs = f32(T, E)
+    wself = f32(E, E, scale=0.02)
 
     t = lambda *a, **k: h.tensor(*a, device=None if k.get("weights") else act, **k)
     tw = lambda *a, **k: h.tensor(*a, device=wts, **k)
@@ -201,8 +207,15 @@ def run16(mode_name, policy=None, dev=False, fused=False):
     nodes["softmax_nomask"] = t([100, 5, 2], op="SOFT_MAX", src=(Z,), fparams={0: 1.0, 1: 0.0}, name="sm-1")
     nodes["moe"] = t([96, 2, T], op="MUL_MAT_ID", src=(WMOE, XMOE, IDS), name="ffn_moe_up-0")
     nodes["mm_lns16"] = t([200, T], op="MUL_MAT", src=(WL16, nodes["mul"]), name="k_lns16-0")
+    # y = W x + x with y written over x (an in-place residual that is the
+    # product's own activation)
+    XS = t([E, T], data=xs.copy(), name="self_inp")   # overwritten in place
+    WS = tw([E, E], data=wself, weights=True, name="blk.0.self.weight")
+    nodes["mm_self"] = t([E, T], op="MUL_MAT", src=(WS, XS), name="self_mm-0")
+    nodes["add_self"] = t([E, T], op="ADD", src=(XS, nodes["mm_self"]), data=XS.data, name="self_out-0")
     order = ["rms", "mul", "qkv", "view_q", "rope", "perm_q", "kq", "softmax", "ug", "swiglu", "view_g", "view_u",
-             "swiglu_split", "add", "add_bcast", "down", "down_res", "qkv_again", "softmax_nomask", "moe", "mm_lns16"]
+             "swiglu_split", "add", "add_bcast", "down", "down_res", "qkv_again", "softmax_nomask", "moe", "mm_lns16",
+             "mm_self", "add_self"]
     views = {"view_q": qv, "perm_q": qp, "view_g": ga, "view_u": ua}
     graph = [views[k] if k in views else nodes[k] for k in order]
 
@@ -240,6 +253,8 @@ def run16(mode_name, policy=None, dev=False, fused=False):
     want["softmax_nomask"] = O.soft_max16(mode_of("SOFT_MAX", "sm-1"), z, None, 1.0)
     want["moe"] = O.mul_mat_id(mode_of("MUL_MAT_ID", "ffn_moe_up-0"), wmoe, xmoe, ids_moe)
     want["mm_lns16"] = O.mul_mat16(mode_of("MUL_MAT", "k_lns16-0"), w_codes, want["mul"])
+    want["mm_self"] = O.mul_mat16(mode_of("MUL_MAT", "self_mm-0"), O.f2x16(wself), xs)
+    want["add_self"] = binop(L.lno16_add_f32, xs, want["mm_self"])
 
     report = {}
     for k in checked:
@@ -443,6 +458,8 @@ if __name__ == "__main__":
     a = ap.parse_args()
     if a.policy is not None:
         os.environ["LNS16_SUM_POLICY"] = a.policy
+    if a.fused:   # node-pair fusion is opt-in
+        os.environ["GGML_LNS_HIP_FUSE"] = "1"
     if a.device_buffers or a.movement:
         os.environ["GGML_LNS_HIP_BUFFERS"] = "device"
     if a.movement:

@@ -115,3 +115,40 @@ def test_lns32_prefill_and_decode():
         print(f"[llama32] graph decode {step}", flush=True)
         same(gpu.decode_graph(tok).cpu().numpy(), cpu.eval([tok]), f"lns32 graph decode {step}")
         tok = (tok * 5 + 1) % cfg.n_vocab
+
+
+def test_lns32_graph_decode_across_kv_boundary():
+    """LNS32 decode replayed from HIP graphs while the KV view grows from 256
+    to 512 cells (a new graph is captured for the second view), after a
+    prefill that already sized every buffer and the device scratch."""
+    from lnship import llama
+    cfg = tiny()
+    w = llama.synthetic_weights(cfg, seed=13, std=0.2)
+    prompt = [(i * 7) % cfg.n_vocab for i in range(253)]
+    print("\n[llama32] prompt 253 then graph decode across n_kv 256 -> 512", flush=True)
+    gpu = llama.LlamaLNS32(cfg, w)
+    cpu = LlamaOracle32(cfg, w)
+    same(gpu.eval(prompt).cpu().numpy(), cpu.eval(prompt), "lns32 prefill 253")
+    for step, tok in enumerate((5, 9, 2, 40)):
+        print(f"[llama32] graph decode at position {253 + step}", flush=True)
+        same(gpu.decode_graph(tok).cpu().numpy(), cpu.eval([tok]), f"lns32 graph decode {253 + step}")
+    assert sorted(gpu._graphs) == [256, 512]
+
+
+def test_buffer_growth_drops_captured_graphs():
+    """A prefill longer than any before grows the activation buffers; the
+    graphs captured against the old buffers are dropped, and the next graph
+    decode is captured anew and still equals the oracle."""
+    from lnship import llama
+    cfg = tiny()
+    w = llama.synthetic_weights(cfg, seed=21, std=0.2)
+    gpu = llama.LlamaLNS16(cfg, w, mode=O.SUM32)
+    cpu = LlamaOracle16(cfg, w, O.SUM32)
+    print("\n[llama] prefill 3, graph decode, prefill 40, graph decode", flush=True)
+    same(gpu.eval([1, 2, 3]).cpu().numpy(), cpu.eval([1, 2, 3]), "prefill 3")
+    same(gpu.decode_graph(4).cpu().numpy(), cpu.eval([4]), "graph decode 3")
+    assert gpu._graphs
+    long_prompt = [(i * 3) % cfg.n_vocab for i in range(40)]
+    same(gpu.eval(long_prompt).cpu().numpy(), cpu.eval(long_prompt), "prefill 40")
+    assert not gpu._graphs
+    same(gpu.decode_graph(7).cpu().numpy(), cpu.eval([7]), "graph decode 44")

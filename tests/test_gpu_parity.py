@@ -375,6 +375,53 @@ def test_rope_store_kv_fused(ln, w32):
                               w.view(np.uint32) if w.dtype == np.float32 else w), name
 
 
+@pytest.mark.parametrize("w32", [False, True])
+def test_rope_store_kv_position_out_of_range(ln, w32):
+    # a position at or beyond the cache's n_ctx rows is reported as an index
+    # error, and nothing is written for that token (no cache cell, no query
+    # row); the other tokens are stored as usual
+    import ctypes
+    rng = np.random.default_rng(36)
+    L, st = ln.lib(), ln._stream()
+    P = lambda t, off=0: ctypes.c_void_p(t.data_ptr() + off * t.element_size())
+    T, nh, nkv, hd, n_ctx = 3, 2, 1, 16, 16
+    nqkv = (nh + 2 * nkv) * hd
+    qkv = dev((rng.standard_normal((T, nqkv)) * 2).astype(np.float32))
+    rt = np.empty(n_ctx * hd, np.float32)
+    ln.check(L.lnship_rope_table(ctypes.c_float(10000.0), hd, n_ctx, ctypes.c_void_p(rt.ctypes.data)))
+    cs = dev(rt)
+    kslice = hd * n_ctx
+    dt = torch.int32 if w32 else torch.int16
+    pre = "lnship32_" if w32 else "lnship16_"
+    bad = ctypes.c_int64(0)
+    L.lnship_index_error(ctypes.byref(bad), st)   # clear
+    outs = []
+    for p_last in (7, n_ctx):
+        pos = dev(np.array([2, 5, p_last], np.int32))
+        kc = torch.full((kslice,), 0x1234, dtype=dt, device="cuda")
+        vc = torch.full((kslice,), 0x1234, dtype=dt, device="cuda")
+        q = torch.full((T * nh * hd,), 7.0, dtype=torch.float32, device="cuda")
+        a = ln.QkvStoreArgs(P(qkv), nqkv, P(pos), T, nh, nkv, hd, hd, P(cs), P(q), P(kc), P(vc), n_ctx, kslice,
+                            kslice, None, 0)
+        ln.check(getattr(L, pre + "rope_store_kv")(ctypes.byref(a), st))
+        outs.append((host(q).reshape(T, nh * hd), host(kc), host(vc)))
+        if p_last == n_ctx:
+            assert L.lnship_index_error(ctypes.byref(bad), st) == 1 and bad.value == n_ctx
+        else:
+            assert L.lnship_index_error(ctypes.byref(bad), st) == 0
+    (q_ok, k_ok, v_ok), (q_bad, k_bad, v_bad) = outs
+    assert np.array_equal(q_bad[:2].view(np.uint32), q_ok[:2].view(np.uint32))
+    assert np.all(q_bad[2] == 7.0)                     # the refused token's query row untouched
+    fill = 0x1234
+    # the refused token wrote no cache cell: the caches equal the valid run's
+    # with position 7's cells left at the fill value
+    k_want, v_want = k_ok.copy(), v_ok.copy()
+    for d in range(hd):
+        k_want[((d >> 3) * n_ctx + 7) * 8 + (d & 7)] = fill
+        v_want[((7 >> 3) * hd + d) * 8 + (7 & 7)] = fill
+    assert np.array_equal(k_bad, k_want) and np.array_equal(v_bad, v_want)
+
+
 # ------------------------------------------------------------------- softmax --
 
 def _causal(nq, nkv):

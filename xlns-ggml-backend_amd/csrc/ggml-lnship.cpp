@@ -904,6 +904,7 @@ static void backend_free(ggml_backend_t b) {
 
 static void run_node(context &ctx, ggml_tensor *node);
 static bool run_fused(context &ctx, ggml_cgraph *g, int i);
+static bool fuse_enabled();
 
 static ggml_status backend_graph_compute(ggml_backend_t b, ggml_cgraph *g) {
     context &ctx = *static_cast<context *>(b->context);
@@ -911,7 +912,7 @@ static ggml_status backend_graph_compute(ggml_backend_t b, ggml_cgraph *g) {
         ggml_tensor *node = g->nodes[i];
         if ((node->flags & GGML_TENSOR_FLAG_COMPUTE) == 0) continue;
         if (classify(node) == kind::view || nelements(node) == 0) continue;
-        if (run_fused(ctx, g, i)) {   // node i and node i + 1 in one launch
+        if (fuse_enabled() && run_fused(ctx, g, i)) {   // node i and node i + 1 in one launch
             i++;
             continue;
         }
@@ -1633,6 +1634,35 @@ static void op_mul_mat_id(context &ctx, ggml_tensor *dst) {
 // residual) and node i's tensor is not written.  Each fused launch keeps the
 // F32 value between the two nodes and its conversion, as the two nodes do.
 
+// Opt-in (GGML_LNS_HIP_FUSE=1): graph_compute sees one split of a
+// ggml_backend_sched graph at a time, so a reader of node i's tensor in a
+// later split, on another backend, is not among the nodes scanned here.
+// Callers that hand over whole graphs (or mark such tensors as outputs, as
+// llama.cpp's scheduler does for tensors that cross splits) can enable it.
+static bool fuse_enabled() {
+    static const bool on = [] {
+        const char *v = std::getenv("GGML_LNS_HIP_FUSE");
+        return v && std::strcmp(v, "0") != 0 && v[0] != '\0';
+    }();
+    return on;
+}
+
+// the byte range a tensor's elements span
+static void byte_span(const ggml_tensor *t, uintptr_t *lo, uintptr_t *hi) {
+    size_t last = ggml_type_size(t->type);
+    for (int d = 0; d < GGML_MAX_DIMS; d++)
+        if (t->ne[d] > 1) last += (size_t)(t->ne[d] - 1) * t->nb[d];
+    *lo = (uintptr_t)t->data;
+    *hi = *lo + last;
+}
+
+static bool overlaps(const ggml_tensor *a, const ggml_tensor *b) {
+    uintptr_t a0, a1, b0, b1;
+    byte_span(a, &a0, &a1);
+    byte_span(b, &b0, &b1);
+    return a0 < b1 && b0 < a1;
+}
+
 static bool feeds_only(const ggml_cgraph *g, int i, const ggml_tensor *next) {
     const ggml_tensor *t = g->nodes[i];
     if (t->flags & GGML_TENSOR_FLAG_OUTPUT) return false;
@@ -1660,6 +1690,7 @@ static bool run_fused(context &ctx, ggml_cgraph *g, int i) {
         // MUL by one weight row of ne[0] floats
         const ggml_tensor *w = next->src[1];
         if (!plain_f32(w) || w->ne[0] != t->ne[0] || nelements(w) != w->ne[0] || !same_shape(next, t)) return false;
+        if (overlaps(next, w) || (overlaps(next, t->src[0]) && next->data != t->src[0]->data)) return false;
         const int64_t nc = t->ne[0], nr = nrows(t);
         const float *x = ctx.upload(t->src[0], R_SRC0);
         const float *wd = ctx.upload(w, R_SRC1);
@@ -1682,6 +1713,10 @@ static bool run_fused(context &ctx, ggml_cgraph *g, int i) {
         const ggml_tensor *r = next->src[0] == t ? next->src[1] : next->src[0];
         if (r == t || !plain_f32(r) || !same_shape(r, t) || !same_shape(next, t)) return false;
         const ggml_tensor *a = t->src[0], *b = t->src[1];
+        // the product reads b while the launch writes the sum: the output may
+        // only replace the residual exactly (in place), never overlap b
+        if (r == b || (b->data && overlaps(next, b))) return false;
+        if (overlaps(next, r) && (next->data != r->data || !contiguous(next) || !contiguous(r))) return false;
         lnship_mul_mat_args args;
         std::memset(&args, 0, sizeof args);
         args.w = ctx.lns_matrix(a);

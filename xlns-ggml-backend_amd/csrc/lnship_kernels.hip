@@ -16,6 +16,7 @@
 #include <mutex>
 #include <string>
 #include <type_traits>
+#include <vector>
 
 #include "lnship.h"
 #include "lnship_device.h"
@@ -65,6 +66,7 @@ struct device_state {
     dev_tables T{};
     void *scratch = nullptr;   // grow-only
     size_t scratch_size = 0;
+    std::vector<void *> retired;   // outgrown scratch blocks, kept for captured graphs
     // index check of get_rows / set_rows: [0] set to 1 by the first
     // out-of-range index since the last lnship_index_error, [1] that index
     unsigned long long *index_err = nullptr;
@@ -101,18 +103,26 @@ static device_state *state() {
 }
 
 // Grow-only device scratch of the current device; callers on one device are
-// serialized by the stream order of their launches.
-static int scratch(device_state *s, size_t bytes, void **p) {
+// serialized by the stream order of their launches.  A HIP graph captured
+// earlier keeps the address it was captured with, so a block that is
+// outgrown is retired, never freed: it stays valid for such graphs until the
+// process ends (the sizes at least double, so the retired blocks together
+// are smaller than the live one).  Growing while the stream is capturing
+// would put an allocation inside the capture, so it is refused: the caller
+// runs the op once outside the capture first.
+static int scratch(device_state *s, size_t bytes, void **p, hipStream_t st) {
     std::lock_guard<std::mutex> lock(g_mutex);
     if (bytes > s->scratch_size) {
-        if (s->scratch) {
-            LNSHIP_HIP(hipDeviceSynchronize());
-            LNSHIP_HIP(hipFree(s->scratch));
-            s->scratch = nullptr;
-            s->scratch_size = 0;
-        }
-        size_t sz = std::max(bytes, (size_t)1 << 20);
-        LNSHIP_HIP(hipMalloc(&s->scratch, sz));
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        LNSHIP_HIP(hipStreamIsCapturing(st, &cs));
+        if (cs != hipStreamCaptureStatusNone)
+            return fail(LNSHIP_ERANGE, "device scratch would grow inside a HIP graph capture (run the op once "
+                                       "before capturing it)%s");
+        size_t sz = std::max({bytes, (size_t)1 << 20, 2 * s->scratch_size});
+        void *q = nullptr;
+        LNSHIP_HIP(hipMalloc(&q, sz));
+        if (s->scratch) s->retired.push_back(s->scratch);
+        s->scratch = q;
         s->scratch_size = sz;
     }
     *p = s->scratch;
@@ -1539,16 +1549,23 @@ __global__ void k_rope(const float *__restrict__ x, int64_t x_ld, const int32_t 
 // cache stores and reads it
 // item i (element (token, head, d)) of a KV-cache store;
 // ntok * nhead * ne0 items
+// A position outside the cache's cache_m rows is recorded (err, as an index
+// out of range) and its item is skipped: nothing is read from the rope
+// table or written to the cache for it.
 template <class F, class C>
 __device__ __forceinline__ void store_kv_item(const F &f, int64_t i, const float *x, int64_t x_ld, const int32_t *pos,
                                               int64_t nhead, int64_t ne0, int rope_n_dims, const float *cos_sin,
                                               C *cache, int64_t cache_m, int64_t cache_slice, int transposed,
-                                              const int32_t *seq, int64_t seq_stride) {
+                                              const int32_t *seq, int64_t seq_stride, unsigned long long *err) {
     const int64_t half = rope_n_dims / 2;
     const int64_t row = i / ne0, d = i - row * ne0;
     const int64_t t = row / nhead, h = row - t * nhead;
     const float *xr = x + t * x_ld + h * ne0;
     const int64_t p = pos[t];
+    if (p < 0 || p >= cache_m) {
+        index_fault(err, p);
+        return;
+    }
     float v;
     if (rope_n_dims > 0 && d < rope_n_dims) {
         // normal rope: element d belongs to pair d / 2
@@ -1570,19 +1587,20 @@ template <int W>
 __global__ void k_store_kv(const float *__restrict__ x, int64_t x_ld, const int32_t *__restrict__ pos, int64_t ntok,
                            int64_t nhead, int64_t ne0, int rope_n_dims, const float *__restrict__ cos_sin,
                            typename fmt_t<W>::code_t *__restrict__ cache, int64_t cache_m, int64_t cache_slice,
-                           int transposed, const int32_t *__restrict__ seq, int64_t seq_stride, dev_tables T) {
+                           int transposed, const int32_t *__restrict__ seq, int64_t seq_stride, dev_tables T,
+                           unsigned long long *err) {
     const fmt_t<W> F{T};
     const int64_t n = ntok * nhead * ne0;
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)blockDim.x * gridDim.x)
         store_kv_item(F, i, x, x_ld, pos, nhead, ne0, rope_n_dims, cos_sin, cache, cache_m, cache_slice, transposed,
-                      seq, seq_stride);
+                      seq, seq_stride, err);
 }
 
 // The query rope and the key / value cache stores after a fused QKV
 // mul_mat, as one grid: items [0, nq) rope the query heads, the next nk
 // store the (rotated) key heads, the last nk the value heads.
 template <int W>
-__global__ void k_rope_store_kv(lnship_qkv_store_args a, dev_tables T) {
+__global__ void k_rope_store_kv(lnship_qkv_store_args a, dev_tables T, unsigned long long *err) {
     using C = typename fmt_t<W>::code_t;
     const fmt_t<W> F{T};
     const int64_t hd = a.head_dim, nd = a.rope_n_dims;
@@ -1590,14 +1608,20 @@ __global__ void k_rope_store_kv(lnship_qkv_store_args a, dev_tables T) {
     const float *xk = a.qkv + a.n_head * hd, *xv = xk + a.n_head_kv * hd;
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < nq + 2 * nk;
          i += (int64_t)blockDim.x * gridDim.x) {
-        if (i < nq)
-            rope_item(F, i, a.qkv, a.qkv_ld, a.pos, a.n_head, hd, (int)nd, 0, a.cos_sin, a.q_dst);
-        else if (i < nq + nk)
+        if (i < nq) {
+            // the rope table has cache_m rows: a query beyond them is recorded
+            // and skipped, like the cache stores
+            const int64_t t = i / (a.n_head * (nd / 2 + (hd - nd)));
+            const int64_t p = a.pos[t];
+            if (p < 0 || p >= a.cache_m) index_fault(err, p);
+            else rope_item(F, i, a.qkv, a.qkv_ld, a.pos, a.n_head, hd, (int)nd, 0, a.cos_sin, a.q_dst);
+        } else if (i < nq + nk) {
             store_kv_item(F, i - nq, xk, a.qkv_ld, a.pos, a.n_head_kv, hd, (int)nd, a.cos_sin, (C *)a.k_cache,
-                          a.cache_m, a.k_slice, 0, a.seq, a.seq_stride);
-        else
+                          a.cache_m, a.k_slice, 0, a.seq, a.seq_stride, err);
+        } else {
             store_kv_item(F, i - nq - nk, xv, a.qkv_ld, a.pos, a.n_head_kv, hd, 0, a.cos_sin, (C *)a.v_cache,
-                          a.cache_m, a.v_slice, 1, a.seq, a.seq_stride);
+                          a.cache_m, a.v_slice, 1, a.seq, a.seq_stride, err);
+        }
     }
 }
 
@@ -2024,7 +2048,7 @@ static int store_kv_common(const float *x, int64_t x_ld, const int32_t *pos, int
     if (n == 0) return 0;
     hipLaunchKernelGGL(k_store_kv<W>, dim3(grid_for(n, 4)), dim3(k_block), 0, (hipStream_t)stream, x, x_ld, pos, ntok,
                        nhead, ne0, rope_n_dims, cos_sin, cache, cache_m, cache_slice, cache_transposed, seq, seq_stride,
-                       s->T);
+                       s->T, s->index_err);
     LNSHIP_HIP(hipGetLastError());
     return 0;
 }
@@ -2040,7 +2064,8 @@ static int rope_store_kv_common(const lnship_qkv_store_args *a, void *stream) {
     const int64_t hd = a->head_dim, nd = a->rope_n_dims;
     const int64_t n = a->ntok * (a->n_head * (nd / 2 + hd - nd) + 2 * a->n_head_kv * hd);
     if (n == 0) return 0;
-    hipLaunchKernelGGL(k_rope_store_kv<W>, dim3(grid_for(n, 4)), dim3(k_block), 0, (hipStream_t)stream, *a, s->T);
+    hipLaunchKernelGGL(k_rope_store_kv<W>, dim3(grid_for(n, 4)), dim3(k_block), 0, (hipStream_t)stream, *a, s->T,
+                       s->index_err);
     LNSHIP_HIP(hipGetLastError());
     return 0;
 }
@@ -2210,7 +2235,7 @@ int lnship16_mul_mat(int mode, const lnship_mul_mat_args *a, void *stream) {
     const mm16_shape sh = mm16_choose(mode, a->M, a->N, nslices, kp, s->cus);
     void *xs = nullptr;
     if (!sh.xl) {
-        if (int rc = scratch(s, (size_t)std::max<int64_t>(1, nslices * a->N * kp) * 2, &xs)) return rc;
+        if (int rc = scratch(s, (size_t)std::max<int64_t>(1, nslices * a->N * kp) * 2, &xs, st)) return rc;
         if (kp > 0) {
             dim3 g(grid_for(a->N * kp, 2), (unsigned)nslices);
             hipLaunchKernelGGL(k_act<0>, g, dim3(k_block), 0, st, a->x, xld, xslice, xs, a->N, a->K, kp, s->T.cvt16);
@@ -2241,8 +2266,8 @@ int lnship32_mul_mat(const lnship_mul_mat_args *a, void *stream) {
     const int64_t nslices = a->ne12 * a->ne13;
     const int64_t kp = (a->K + 7) & ~(int64_t)7;
     void *xs = nullptr;
-    if (int rc = scratch(s, (size_t)std::max<int64_t>(1, nslices * a->N * kp) * 4, &xs)) return rc;
     hipStream_t st = (hipStream_t)stream;
+    if (int rc = scratch(s, (size_t)std::max<int64_t>(1, nslices * a->N * kp) * 4, &xs, st)) return rc;
     if (kp > 0) {
         dim3 g(grid_for(a->N * kp, 2), (unsigned)nslices);
         hipLaunchKernelGGL(k_act<1>, g, dim3(k_block), 0, st, a->x, a->x_ld ? a->x_ld : a->K,
@@ -2293,7 +2318,7 @@ int lnship16_mul_mat_id(int mode, const lnship_mul_mat_id_args *a, void *stream)
     void *xs = nullptr;
     if (!sh.xl) {   // the distinct activation rows, converted once
         const int64_t rows = a->ne11 * a->n_tokens;
-        if (int rc = scratch(s, (size_t)std::max<int64_t>(1, rows * kp) * 2, &xs)) return rc;
+        if (int rc = scratch(s, (size_t)std::max<int64_t>(1, rows * kp) * 2, &xs, st)) return rc;
         if (kp > 0) {
             hipLaunchKernelGGL(k_act<0>, dim3(grid_for(kp, 2), (unsigned)rows), dim3(k_block), 0, st, a->x, xld, xld,
                                xs, (int64_t)1, a->K, kp, s->T.cvt16);
@@ -2321,8 +2346,8 @@ int lnship32_mul_mat_id(const lnship_mul_mat_id_args *a, void *stream) {
     const int64_t kp = (a->K + 7) & ~(int64_t)7, xld = a->x_ld ? a->x_ld : a->K;
     const int64_t rows = a->ne11 * a->n_tokens;
     void *xs = nullptr;
-    if (int rc = scratch(s, (size_t)std::max<int64_t>(1, rows * kp) * 4, &xs)) return rc;
     hipStream_t st = (hipStream_t)stream;
+    if (int rc = scratch(s, (size_t)std::max<int64_t>(1, rows * kp) * 4, &xs, st)) return rc;
     if (kp > 0) {
         hipLaunchKernelGGL(k_act<1>, dim3(grid_for(kp, 2), (unsigned)rows), dim3(k_block), 0, st, a->x, xld, xld, xs,
                            (int64_t)1, a->K, kp, s->T.cvt16);

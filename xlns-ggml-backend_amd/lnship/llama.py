@@ -161,13 +161,29 @@ class LlamaLNS16:
 
     # -- buffers --------------------------------------------------------------
     def _buf(self, name, n, dtype=None):
+        """A grow-only device buffer.  A captured HIP graph keeps the
+        addresses it was captured with, so growing a buffer first drops every
+        captured graph (together with the tensors they reference); they are
+        captured again on their next use."""
         torch = self.torch
         dtype = dtype or torch.float32
         b = self._bufs.get(name)
         if b is None or b.numel() < n:
+            if b is not None and self._graphs:
+                torch.cuda.synchronize()
+                self._graphs.clear()
             b = torch.empty(max(n, 1), dtype=dtype, device=self.dev)
             self._bufs[name] = b
         return b
+
+    def _check_ctx(self, first, T, n_kv=None):
+        """Positions first .. first + T - 1 and a KV view of n_kv cells must
+        fit the n_ctx cells of the caches and the rope table."""
+        n_ctx = self.cfg.n_ctx
+        if first < 0 or T < 0 or first + T > n_ctx:
+            raise ValueError("context full: positions %d..%d do not fit n_ctx=%d" % (first, first + T - 1, n_ctx))
+        if n_kv is not None and not 0 < n_kv <= n_ctx:
+            raise ValueError("KV view of %d cells outside 1..n_ctx=%d" % (n_kv, n_ctx))
 
     def _seed(self, draws):
         """Monte: where an op's LFSR draws start, then advance past them (graph
@@ -245,7 +261,9 @@ class LlamaLNS16:
         T == n_seq, token s belongs to sequence s, and the logits of every
         token come back ([n_seq][n_vocab])."""
         torch, c, L = self.torch, self.cfg, lib()
-        assert not batch or T == self.n_seq
+        if batch and T != self.n_seq:
+            raise ValueError("batched forward: %d tokens for %d sequences" % (T, self.n_seq))
+        self._check_ctx(0, T, n_kv)
         self._stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
         st = self._stream
         e, hd, nh, nkv, f = c.n_embd, c.head_dim, c.n_head, c.n_head_kv, c.n_ff
@@ -310,7 +328,7 @@ class LlamaLNS16:
         torch = self.torch
         T = len(tokens)
         p0 = self.past[seq]
-        assert p0 + T <= self.cfg.n_ctx, "context full"
+        self._check_ctx(p0, T)
         tok = self._buf("tok", T, torch.int32)
         pos = self._buf("pos", T, torch.int32)
         tok[:T].copy_(torch.tensor(tokens, dtype=torch.int32))
@@ -324,8 +342,9 @@ class LlamaLNS16:
         """One decode step of every sequence: tokens[s] is appended to
         sequence s.  Returns the device logits [n_seq][n_vocab]."""
         torch = self.torch
-        assert len(tokens) == self.n_seq
-        assert max(self.past) < self.cfg.n_ctx, "context full"
+        if len(tokens) != self.n_seq:
+            raise ValueError("eval_batch: %d tokens for %d sequences" % (len(tokens), self.n_seq))
+        self._check_ctx(max(self.past), 1)
         tok = self._buf("btok", self.n_seq, torch.int32)
         pos = self._buf("bpos", self.n_seq, torch.int32)
         tok[: self.n_seq].copy_(torch.tensor(tokens, dtype=torch.int32))
@@ -343,7 +362,9 @@ class LlamaLNS16:
         already on the device.  Returns the device logits.  Monte ops read
         their LFSR start from lfsr_dev, so one graph serves every step."""
         torch = self.torch
+        self._check_ctx(max(self.past), 1)
         n_kv = n_kv or self.batch_n_kv()
+        self._check_ctx(max(self.past), 1, n_kv)
         tok = self._buf("gbtok", self.n_seq, torch.int32)
         pos = self._buf("gbpos", self.n_seq, torch.int32)
         tok[: self.n_seq].copy_(tok_dev[: self.n_seq])
@@ -373,7 +394,9 @@ class LlamaLNS16:
         device logits.  Monte ops read their LFSR start from lfsr_dev, so
         one graph serves every step."""
         torch = self.torch
+        self._check_ctx(self.n_past, 1)
         n_kv = n_kv or n_kv_for(self.n_past + 1, self.cfg.n_ctx)
+        self._check_ctx(self.n_past, 1, n_kv)
         tok = self._buf("gtok", 1, torch.int32)
         pos = self._buf("gpos", 1, torch.int32)
         if isinstance(token, torch.Tensor):
@@ -442,6 +465,7 @@ class LlamaLNS32:
         self._graphs = {}
 
     _buf = LlamaLNS16._buf
+    _check_ctx = LlamaLNS16._check_ctx
     _capture = LlamaLNS16._capture
 
     def weight_bytes_per_token(self):
@@ -455,6 +479,7 @@ class LlamaLNS32:
         """Runs T tokens at positions pos_dev[0..T) (device int32) against a
         KV view of n_kv cells; returns the device logits of the last one."""
         torch, c, L = self.torch, self.cfg, lib()
+        self._check_ctx(0, T, n_kv)
         st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
         e, hd, nh, nkv, f = c.n_embd, c.head_dim, c.n_head, c.n_head_kv, c.n_ff
         nq, nqkv = nh * hd, (nh + 2 * nkv) * hd
@@ -509,7 +534,7 @@ class LlamaLNS32:
         torch = self.torch
         T = len(tokens)
         p0 = self.n_past
-        assert p0 + T <= self.cfg.n_ctx, "context full"
+        self._check_ctx(p0, T)
         tok = self._buf("tok", T, torch.int32)
         pos = self._buf("pos", T, torch.int32)
         tok[:T].copy_(torch.tensor(tokens, dtype=torch.int32))
@@ -522,7 +547,9 @@ class LlamaLNS32:
         """One decode step through a captured HIP graph; token is a host int or
         a device int32 tensor of one element.  Returns the device logits."""
         torch = self.torch
+        self._check_ctx(self.n_past, 1)
         n_kv = n_kv or n_kv_for(self.n_past + 1, self.cfg.n_ctx)
+        self._check_ctx(self.n_past, 1, n_kv)
         tok = self._buf("gtok", 1, torch.int32)
         pos = self._buf("gpos", 1, torch.int32)
         if isinstance(token, torch.Tensor):
