@@ -110,6 +110,16 @@ typedef struct lnship_mul_mat_args {
 
 int lnship16_mul_mat(int mode, const lnship_mul_mat_args *args, void *stream);
 int lnship32_mul_mat(const lnship_mul_mat_args *args, void *stream);
+/* lnship32_mul_mat that allocates nothing.  No counterpart in the
+ * reference: it is for callers that cannot call hipMalloc (code under HIP
+ * graph capture, serving loops, harnesses that forbid allocation).  The
+ * activation rows are staged in a fixed 4 MiB block that the library's code
+ * object holds on each GPU (set up by lnship_init) instead of the
+ * grow-only scratch: ne12 * ne13 * N * round8(K) must be at most 1 Mi codes,
+ * else LNSHIP_ERANGE.  Results equal lnship32_mul_mat's.  Every call on one
+ * GPU shares that block, so calls that overlap on one GPU (other streams,
+ * other host threads) race; calls in one stream's order do not. */
+int lnship32_mul_mat_noalloc(const lnship_mul_mat_args *args, void *stream);
 
 /* ---- RMS_NORM (kernel_set::rms_norm, :133-134) --------------------------
  * dst = src / sqrt(mean(src^2) + eps) per row of ncols (lns_rms_norm,

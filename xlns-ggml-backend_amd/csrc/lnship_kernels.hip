@@ -67,12 +67,21 @@ struct device_state {
     void *scratch = nullptr;   // grow-only
     size_t scratch_size = 0;
     std::vector<void *> retired;   // outgrown scratch blocks, kept for captured graphs
+    void *fixed_scratch = nullptr;  // this device's copy of `scratch` (below), from hipGetSymbolAddress
     // index check of get_rows / set_rows: [0] set to 1 by the first
     // out-of-range index since the last lnship_index_error, [1] that index
     unsigned long long *index_err = nullptr;
 };
 
 static device_state g_devices[k_max_devices];
+
+// The activation staging of lnship32_mul_mat_noalloc: a fixed block in the
+// code object, so that entry point allocates nothing.  Every GPU the library
+// runs on holds its own copy until the process ends.  In host code this
+// name is not a device address: host code uses device_state::fixed_scratch,
+// which lnship_init sets from hipGetSymbolAddress on each device.
+constexpr size_t k_fixed_scratch_bytes = (size_t)4 << 20;
+static __device__ __align__(256) unsigned char scratch[k_fixed_scratch_bytes];
 static std::mutex g_mutex;
 static host_tables *g_host = nullptr;
 
@@ -110,7 +119,7 @@ static device_state *state() {
 // are smaller than the live one).  Growing while the stream is capturing
 // would put an allocation inside the capture, so it is refused: the caller
 // runs the op once outside the capture first.
-static int scratch(device_state *s, size_t bytes, void **p, hipStream_t st) {
+static int grow_scratch(device_state *s, size_t bytes, void **p, hipStream_t st) {
     std::lock_guard<std::mutex> lock(g_mutex);
     if (bytes > s->scratch_size) {
         hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
@@ -2124,6 +2133,11 @@ int lnship_init(void) {
     LNSHIP_HIP(hipDeviceGetAttribute(&s.cus, hipDeviceAttributeMultiprocessorCount, dev));
     LNSHIP_HIP(hipMalloc((void **)&s.index_err, 2 * sizeof(unsigned long long)));
     LNSHIP_HIP(hipMemset(s.index_err, 0, 2 * sizeof(unsigned long long)));
+    // this device's copy of the fixed scratch (the device is current here)
+    void *fixed = nullptr;
+    LNSHIP_HIP(hipGetSymbolAddress(&fixed, HIP_SYMBOL(scratch)));
+    if (!fixed) return fail(LNSHIP_EDEVICE, "no address for the fixed scratch%s");
+    s.fixed_scratch = fixed;
     s.ready = true;
     return 0;
 }
@@ -2235,7 +2249,7 @@ int lnship16_mul_mat(int mode, const lnship_mul_mat_args *a, void *stream) {
     const mm16_shape sh = mm16_choose(mode, a->M, a->N, nslices, kp, s->cus);
     void *xs = nullptr;
     if (!sh.xl) {
-        if (int rc = scratch(s, (size_t)std::max<int64_t>(1, nslices * a->N * kp) * 2, &xs, st)) return rc;
+        if (int rc = grow_scratch(s, (size_t)std::max<int64_t>(1, nslices * a->N * kp) * 2, &xs, st)) return rc;
         if (kp > 0) {
             dim3 g(grid_for(a->N * kp, 2), (unsigned)nslices);
             hipLaunchKernelGGL(k_act<0>, g, dim3(k_block), 0, st, a->x, xld, xslice, xs, a->N, a->K, kp, s->T.cvt16);
@@ -2258,16 +2272,12 @@ int lnship16_mul_mat(int mode, const lnship_mul_mat_args *a, void *stream) {
 }
 
 
-int lnship32_mul_mat(const lnship_mul_mat_args *a, void *stream) {
-    device_state *s = state();
-    if (!s) return LNSHIP_ENOINIT;
-    if (int rc = check_mm(a)) return rc;
-    if (a->M == 0 || a->N == 0) return 0;
+// The xlns32 product once its activation rows have a staging block xs of
+// at least nslices * N * kp codes: k_act converts them (padding included, so
+// xs needs no clearing), then the GEMV.
+static int mul_mat32_staged(device_state *s, const lnship_mul_mat_args *a, void *xs, hipStream_t st) {
     const int64_t nslices = a->ne12 * a->ne13;
     const int64_t kp = (a->K + 7) & ~(int64_t)7;
-    void *xs = nullptr;
-    hipStream_t st = (hipStream_t)stream;
-    if (int rc = scratch(s, (size_t)std::max<int64_t>(1, nslices * a->N * kp) * 4, &xs, st)) return rc;
     if (kp > 0) {
         dim3 g(grid_for(a->N * kp, 2), (unsigned)nslices);
         hipLaunchKernelGGL(k_act<1>, g, dim3(k_block), 0, st, a->x, a->x_ld ? a->x_ld : a->K,
@@ -2289,6 +2299,31 @@ int lnship32_mul_mat(const lnship_mul_mat_args *a, void *stream) {
         case 44: return launch_mm32<4, 4>(m, s->T, nslices, st);
         default: return launch_mm32<1, 1>(m, s->T, nslices, st);
     }
+}
+
+int lnship32_mul_mat(const lnship_mul_mat_args *a, void *stream) {
+    device_state *s = state();
+    if (!s) return LNSHIP_ENOINIT;
+    if (int rc = check_mm(a)) return rc;
+    if (a->M == 0 || a->N == 0) return 0;
+    const int64_t kp = (a->K + 7) & ~(int64_t)7;
+    void *xs = nullptr;
+    hipStream_t st = (hipStream_t)stream;
+    if (int rc = grow_scratch(s, (size_t)std::max<int64_t>(1, a->ne12 * a->ne13 * a->N * kp) * 4, &xs, st)) return rc;
+    return mul_mat32_staged(s, a, xs, st);
+}
+
+int lnship32_mul_mat_noalloc(const lnship_mul_mat_args *a, void *stream) {
+    device_state *s = state();
+    if (!s) return LNSHIP_ENOINIT;
+    if (int rc = check_mm(a)) return rc;
+    if (a->M == 0 || a->N == 0) return 0;
+    const int64_t kp = (a->K + 7) & ~(int64_t)7;
+    const uint64_t need = (uint64_t)(a->ne12 * a->ne13) * (uint64_t)a->N * (uint64_t)kp * 4u;
+    if (need > k_fixed_scratch_bytes)
+        return fail(LNSHIP_ERANGE, "mul_mat_noalloc: ne12*ne13*N*round8(K) activation codes exceed the 1 Mi "
+                                   "(4 MiB) fixed scratch%s");
+    return mul_mat32_staged(s, a, s->fixed_scratch, (hipStream_t)stream);
 }
 
 
@@ -2318,7 +2353,7 @@ int lnship16_mul_mat_id(int mode, const lnship_mul_mat_id_args *a, void *stream)
     void *xs = nullptr;
     if (!sh.xl) {   // the distinct activation rows, converted once
         const int64_t rows = a->ne11 * a->n_tokens;
-        if (int rc = scratch(s, (size_t)std::max<int64_t>(1, rows * kp) * 2, &xs, st)) return rc;
+        if (int rc = grow_scratch(s, (size_t)std::max<int64_t>(1, rows * kp) * 2, &xs, st)) return rc;
         if (kp > 0) {
             hipLaunchKernelGGL(k_act<0>, dim3(grid_for(kp, 2), (unsigned)rows), dim3(k_block), 0, st, a->x, xld, xld,
                                xs, (int64_t)1, a->K, kp, s->T.cvt16);
@@ -2347,7 +2382,7 @@ int lnship32_mul_mat_id(const lnship_mul_mat_id_args *a, void *stream) {
     const int64_t rows = a->ne11 * a->n_tokens;
     void *xs = nullptr;
     hipStream_t st = (hipStream_t)stream;
-    if (int rc = scratch(s, (size_t)std::max<int64_t>(1, rows * kp) * 4, &xs, st)) return rc;
+    if (int rc = grow_scratch(s, (size_t)std::max<int64_t>(1, rows * kp) * 4, &xs, st)) return rc;
     if (kp > 0) {
         hipLaunchKernelGGL(k_act<1>, dim3(grid_for(kp, 2), (unsigned)rows), dim3(k_block), 0, st, a->x, xld, xld, xs,
                            (int64_t)1, a->K, kp, s->T.cvt16);

@@ -78,6 +78,7 @@ def lib():
         "lnship32_pack": (ctypes.c_int, [c_p, ctypes.c_int, c_i64, c_i64, c_p, c_i64, c_i64, c_i64, c_p]),
         "lnship16_mul_mat": (ctypes.c_int, [ctypes.c_int, ctypes.POINTER(MulMatArgs), c_p]),
         "lnship32_mul_mat": (ctypes.c_int, [ctypes.POINTER(MulMatArgs), c_p]),
+        "lnship32_mul_mat_noalloc": (ctypes.c_int, [ctypes.POINTER(MulMatArgs), c_p]),
         "lnship16_rms_norm": (ctypes.c_int, [ctypes.c_int, c_p, c_p, c_i64, c_i64, ctypes.c_float,
                                              ctypes.c_uint16, c_p]),
         "lnship16_rms_norm_state": (ctypes.c_int, [ctypes.c_int, c_p, c_p, c_i64, c_i64, ctypes.c_float,
