@@ -87,6 +87,7 @@ def run_ops(args):
         print(json.dumps(kw), flush=True)
 
     if args.ops in ("decode", "all"):
+        line(op="chain_floor", **chain_floor(lnship, torch))
         # LNS32 (xlns32 weights, 4 B each) at the Llama-1B shape of BASELINE
         # config 4: q / o, k / v, gate|up, down, lm_head
         for K, M in ((2048, 2048), (2048, 512), (2048, 16384), (8192, 2048), (2048, 32000)):
@@ -303,9 +304,28 @@ def chain_bound(model, ln, torch, mode):
         us[K] = s_ev.elapsed_time(e_ev) * 1e3 / 20
     ns_step = (us[1536] - us[576]) * 1e3 / (1536 - 576)
     total = sum(steps)
+    floor = chain_floor(ln, torch)
     return {"steps_per_token": total, "ns_per_step": round(ns_step, 2),
             "launch_us_k576": round(us[576], 2), "launch_us_k1536": round(us[1536], 2),
-            "bound_tok_s": round(1e9 / (total * ns_step), 3), "chain_launches_per_token": len(steps)}
+            "bound_tok_s": round(1e9 / (total * ns_step), 3), "chain_launches_per_token": len(steps),
+            "floor_ns": floor["two_lds_round_trips_add_ns"], "floor_frac": round(floor["two_lds_round_trips_add_ns"] / ns_step, 4),
+            "floor": floor}
+
+
+def chain_floor(ln, torch, steps=200000):
+    """What gfx950 itself needs per dependent step on one wave
+    (lnship_chain_probe, HIP events on the current stream): one and two
+    dependent LDS round trips (a pointer chase), two round trips plus one
+    dependent VALU op (the least an LNS addition can be: a table read whose
+    value addresses a second one, then an add), and one dependent VALU op."""
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    out = {}
+    for key, rt, v in (("lds_round_trip_ns", 1, 0), ("two_lds_round_trips_ns", 2, 0),
+                       ("two_lds_round_trips_add_ns", 2, 1), ("dependent_valu_ns", 0, 8)):
+        ns = ctypes.c_double()
+        ln.check(ln.lib().lnship_chain_probe(rt, v, steps, st, ctypes.byref(ns)))
+        out[key] = round(ns.value / (8 if key == "dependent_valu_ns" else 1), 3)
+    return out
 
 
 def measured_traffic(mode):

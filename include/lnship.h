@@ -44,6 +44,13 @@ enum lnship_error {
  * device.  Replaces kernel_set::upload_tables (lns-cuda-kernels.h:104).
  * Idempotent per device. */
 int lnship_init(void);
+/* Measurement only, no counterpart in the reference: the latency of the
+ * floor under an LNS addition chain on this GPU.  One wave runs `steps`
+ * steps of round_trips dependent LDS reads (a pointer chase, each value the
+ * next address) then valu_ops dependent VALU operations; (round_trips,
+ * valu_ops) is one of (1,0), (2,0), (2,1), (0,1), (0,8).  Timed with HIP
+ * events on stream; writes nanoseconds per step. */
+int lnship_chain_probe(int round_trips, int valu_ops, int64_t steps, void *stream, double *ns_per_step);
 const char *lnship_last_error(void);
 /* the build's identity string */
 const char *lnship_version(void);

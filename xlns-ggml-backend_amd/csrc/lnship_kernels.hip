@@ -1984,6 +1984,31 @@ static int launch_sm16(sm_args &m, int64_t nrows, const dev_tables &T, hipStream
     return 0;
 }
 
+// ---- dependent-latency probe ------------------------------------------------
+// The floor under an LNS addition chain on one wave: RT dependent LDS reads
+// per step (each read's value is the next read's byte address: a pointer
+// chase through a permutation, no address arithmetic), then V dependent VALU
+// operations (v_xor keeps the address in the table).  One workgroup of one
+// wave, as a decode GEMV's chain lane runs.
+template <int RT, int V>
+__global__ __launch_bounds__(64) void k_chain_probe(int64_t steps, uint32_t *out) {
+    __shared__ uint32_t t[4096];
+    for (int i = threadIdx.x; i < 4096; i += 64) t[i] = ((uint32_t)(i * 97 + 13) & 4095u) << 2;
+    __syncthreads();
+    uint32_t x = (threadIdx.x * 61u & 4095u) << 2;
+    const char *base = reinterpret_cast<const char *>(t);
+    for (int64_t s = 0; s < steps; s += 8) {   // steps: a multiple of 8
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+#pragma unroll
+            for (int r = 0; r < RT; r++) x = *reinterpret_cast<const uint32_t *>(base + x);
+#pragma unroll
+            for (int v = 0; v < V; v++) asm volatile("v_xor_b32 %0, 4, %0" : "+v"(x));
+        }
+    }
+    out[threadIdx.x] = x;
+}
+
 }  // namespace lnship
 
 using namespace lnship;
@@ -2139,6 +2164,44 @@ int lnship_init(void) {
     if (!fixed) return fail(LNSHIP_EDEVICE, "no address for the fixed scratch%s");
     s.fixed_scratch = fixed;
     s.ready = true;
+    return 0;
+}
+
+int lnship_chain_probe(int round_trips, int valu_ops, int64_t steps, void *stream, double *ns_per_step) {
+    device_state *s = state();
+    if (!s) return LNSHIP_ENOINIT;
+    if (!ns_per_step || steps <= 0 || steps > ((int64_t)1 << 32)) return fail(LNSHIP_EINVAL, "chain_probe: bad steps%s");
+    steps = (steps + 7) & ~(int64_t)7;
+    auto launch = [&](hipStream_t st) -> int {
+        void *xs = nullptr;
+        if (int rc = grow_scratch(s, 256, &xs, st)) return rc;
+        uint32_t *o = static_cast<uint32_t *>(xs);
+        switch (round_trips * 10 + valu_ops) {
+            case 10: hipLaunchKernelGGL((k_chain_probe<1, 0>), dim3(1), dim3(64), 0, st, steps, o); break;
+            case 20: hipLaunchKernelGGL((k_chain_probe<2, 0>), dim3(1), dim3(64), 0, st, steps, o); break;
+            case 21: hipLaunchKernelGGL((k_chain_probe<2, 1>), dim3(1), dim3(64), 0, st, steps, o); break;
+            case 1: hipLaunchKernelGGL((k_chain_probe<0, 1>), dim3(1), dim3(64), 0, st, steps, o); break;
+            case 8: hipLaunchKernelGGL((k_chain_probe<0, 8>), dim3(1), dim3(64), 0, st, steps, o); break;
+            default: return fail(LNSHIP_EINVAL, "chain_probe: (round_trips, valu_ops) not one of (1,0) (2,0) (2,1) (0,1) (0,8)%s");
+        }
+        LNSHIP_HIP(hipGetLastError());
+        return 0;
+    };
+    hipStream_t st = (hipStream_t)stream;
+    if (int rc = launch(st)) return rc;   // warm-up
+    hipEvent_t e0, e1;
+    LNSHIP_HIP(hipEventCreate(&e0));
+    LNSHIP_HIP(hipEventCreate(&e1));
+    LNSHIP_HIP(hipEventRecord(e0, st));
+    int rc = launch(st);
+    LNSHIP_HIP(hipEventRecord(e1, st));
+    LNSHIP_HIP(hipEventSynchronize(e1));
+    float ms = 0.0f;
+    LNSHIP_HIP(hipEventElapsedTime(&ms, e0, e1));
+    LNSHIP_HIP(hipEventDestroy(e0));
+    LNSHIP_HIP(hipEventDestroy(e1));
+    if (rc) return rc;
+    *ns_per_step = (double)ms * 1e6 / (double)steps;
     return 0;
 }
 

@@ -68,6 +68,7 @@ def lib():
     sigs = {
         "lnship_init": (ctypes.c_int, []),
         "lnship_last_error": (ctypes.c_char_p, []),
+        "lnship_chain_probe": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, c_i64, c_p, ctypes.POINTER(ctypes.c_double)]),
         "lnship_version": (ctypes.c_char_p, []),
         "lnship_host_table": (c_p, [ctypes.c_char_p, ctypes.POINTER(ctypes.c_size_t)]),
         "lnship16_from_f32": (ctypes.c_int, [c_p, c_p, c_i64, c_p]),
