@@ -30,11 +30,19 @@ constexpr int k_max_devices = 64;
 constexpr int k_lds_bytes = 160 * 1024;
 // what the row kernels' static shared arrays may take beside their dynamic LDS
 constexpr int k_lds_static = 2048;
-// the xlns32 tables plus four zero entries (an interpolation on them gives 0)
-// the xlns32 tables, a zero pair, and 512 (origin, shift) descriptors of the
-// direct interpolation grid, indexed by (opposite signs, binade of d)
+// The LDS copy of the xlns32 adder tables (32-bit words): dlo, then dhi as
+// pairs (two words per dh), then the interpolation tables sb, sbf, db, dbf as
+// in the device table block, a zero pair, and 512 four-word descriptors of
+// the interpolation, indexed by (opposite signs, binade of d).
 constexpr int k32_desc_n = 512;
-constexpr int k_lds_tab32 = (k32_tab_n + 4 + 2 * k32_desc_n) * 4;   // 112416 bytes
+constexpr int kl_dlo = 0;
+constexpr int kl_dhi = kl_dlo + k32_co_n;
+constexpr int kl_sb = kl_dhi + 2 * k32_co_n;                 // the rest of the block from sb on
+constexpr int kl_zero = kl_sb + (k32_tab_n - k32_off_sb);
+constexpr int kl_desc = kl_zero + 4;
+constexpr int k_lds_tab32 = (kl_desc + 4 * k32_desc_n) * 4;   // 132896 bytes
+static_assert(k32_off_sb % 4 == 0 && kl_sb % 4 == 0 && (k32_tab_n - k32_off_sb) % 4 == 0, "16-byte staging");
+static_assert(kl_desc % 4 == 0, "descriptors are read 16 bytes at a time");
 
 static thread_local std::string t_err;
 
@@ -234,6 +242,8 @@ __global__ void k_act(const float *__restrict__ x, int64_t x_ld, int64_t x_slice
 // Exact cancellation (equal logs, opposite signs) reads a sentinel table
 // entry that clamps the log to 0 and forces the sign to +.
 
+// |a - b| as one v_sad_u32 (max - min + z, z = 0 held in a register)
+__device__ __forceinline__ uint32_t absdiff(uint32_t a, uint32_t b, uint32_t z) { return max(a, b) - min(a, b) + z; }
 __device__ __forceinline__ uint32_t absdiff(uint32_t a, uint32_t b) {
     uint32_t r;
     asm("v_sad_u32 %0, %1, %2, 0" : "=v"(r) : "v"(a), "v"(b));
@@ -246,18 +256,51 @@ __device__ __forceinline__ int32_t mul_i24(int32_t a, int32_t b) {
     return r;
 }
 
-// (a << 2) + b in one instruction (LDS byte address of entry a from origin b)
-__device__ __forceinline__ uint32_t lshl2_add(uint32_t a, uint32_t b) {
+// Packed 16-bit integer operations on both halves of a register: a - b
+// with unsigned saturation at 0, and the unsigned minimum (v_pk_sub_u16 with
+// clamp, v_pk_min_u16).
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t pk_sub_sat_u16(uint32_t a, uint32_t b) {
+    return __builtin_bit_cast(uint32_t, __builtin_elementwise_sub_sat(__builtin_bit_cast(u16x2, a), __builtin_bit_cast(u16x2, b)));
+}
+__device__ __forceinline__ uint32_t pk_min_u16(uint32_t a, uint32_t b) {
+    return __builtin_bit_cast(uint32_t, __builtin_elementwise_min(__builtin_bit_cast(u16x2, a), __builtin_bit_cast(u16x2, b)));
+}
+
+// Shift-adds in plain code select to one v_lshl_add_u32 each.  The lds_at
+// forms are the same instruction in inline asm, used where an LDS read is
+// the only reader: the compiler keeps them whole (as plain code it splits a
+// masked index into shift, mask and add), and an LDS read has no forwarding
+// hazard on an inline asm result (a vector ALU reader would get a wait state).
+__device__ __forceinline__ uint32_t lshl2_add(uint32_t a, uint32_t b) { return (a << 2) + b; }
+__device__ __forceinline__ uint32_t lshl3_add(uint32_t a, uint32_t b) { return (a << 3) + b; }
+__device__ __forceinline__ uint32_t lds_at2(uint32_t a, uint32_t b) {
     uint32_t r;
     asm("v_lshl_add_u32 %0, %1, 2, %2" : "=v"(r) : "v"(a), "v"(b));
     return r;
 }
-
-// (a << 3) + b in one instruction (a descriptor pair's LDS address)
-__device__ __forceinline__ uint32_t lshl3_add(uint32_t a, uint32_t b) {
+__device__ __forceinline__ uint32_t lds_at3(uint32_t a, uint32_t b) {
     uint32_t r;
     asm("v_lshl_add_u32 %0, %1, 3, %2" : "=v"(r) : "v"(a), "v"(b));
     return r;
+}
+__device__ __forceinline__ uint32_t lds_at4(uint32_t a, uint32_t b) {
+    uint32_t r;
+    asm("v_lshl_add_u32 %0, %1, 4, %2" : "=v"(r) : "v"(a), "v"(b));
+    return r;
+}
+
+// (a & m) | (b & ~m): a select on a lane mask held in a vector register,
+// with no compare and no condition register (whose write and read would
+// need hazard wait states on gfx950)
+__device__ __forceinline__ uint32_t bfi(uint32_t m, uint32_t a, uint32_t b) { return (a & m) | (b & ~m); }
+
+// All ones where x is negative as a signed value, else 0, as one v_bfe_i32
+// of bit 31 whose width comes from a register (one = 1 in a register the
+// compiler cannot see into).  A plain shift would be folded into a compare
+// and a select through the condition register.
+__device__ __forceinline__ uint32_t sign_mask(uint32_t x, uint32_t one) {
+    return (uint32_t)__builtin_amdgcn_sbfe((int32_t)x, 31, one);
 }
 
 // LDS addresses as 32-bit integers: a table lookup is then a shift-add of the
@@ -266,6 +309,13 @@ __device__ __forceinline__ uint32_t lshl3_add(uint32_t a, uint32_t b) {
 typedef const int32_t __attribute__((address_space(3))) *lds_i32_t;
 __device__ __forceinline__ uint32_t lds_addr(const void *p) { return (uint32_t)(uintptr_t)(lds_i32_t)p; }
 __device__ __forceinline__ int32_t lds_ld(uint32_t addr) { return *(lds_i32_t)(uintptr_t)addr; }
+// two or four consecutive words in one LDS read (ds_read_b64, ds_read_b128)
+typedef int32_t i32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef const i32x2 __attribute__((address_space(3))) *lds_i2_t;
+typedef const u32x4 __attribute__((address_space(3))) *lds_u4_t;
+__device__ __forceinline__ i32x2 lds_ld2(uint32_t addr) { return *(lds_i2_t)(uintptr_t)addr; }
+__device__ __forceinline__ u32x4 lds_ld4(uint32_t addr) { return *(lds_u4_t)(uintptr_t)addr; }
 
 struct acc_ls {
     uint32_t l, s;   // log field, sign bit in place
@@ -323,86 +373,82 @@ struct red16<LNSHIP_MONTE> {
 // most one interpolation (at e on the sb tables, or at d on the sb / db
 // tables), so all lanes share one.  T is the LDS copy of the adder tables
 // with changes made at staging: the db-at-zero entry holds a sentinel (exact
-// cancellation clamps the log to 0), each dhi[dh] holds (dh << 12) + dhi[dh],
-// a zero pair follows the tables, then the descriptors of the direct
-// interpolation (below).  Every select is arithmetic: a ternary around two
-// table reads would compile to a divergent branch that serialises both.
+// cancellation clamps the log to 0), dhi becomes pairs ((dh << 12) +
+// dhi[dh], dhi[dh]), a zero pair follows the tables, then the descriptors of
+// the interpolation (below).  Every select is arithmetic: a ternary around
+// two table reads would compile to a divergent branch that serialises both.
 
 // Byte offsets of the interpolation tables in the LDS copy, each less its
 // grid origin, so that a distance x on grid shift sh reads node
 // (x >> sh) at origin + ((x >> sh) << 2).
-constexpr uint32_t kb_sb = (uint32_t)k32_off_sb * 4;
-constexpr uint32_t kb_sbf = (uint32_t)(k32_off_sbf - (int)(k32_sb_end >> k32_sb_fsh)) * 4;
-constexpr uint32_t kb_db = (uint32_t)(k32_off_db - k32_db_first) * 4;
-constexpr uint32_t kb_dbf = (uint32_t)(k32_off_dbf - (int)(k32_db_end >> k32_db_fsh)) * 4;
+constexpr int kl_shift = kl_sb - k32_off_sb;   // LDS word offset less the device block's
+constexpr uint32_t kb_sb = (uint32_t)(k32_off_sb + kl_shift) * 4;
+constexpr uint32_t kb_sbf = (uint32_t)(k32_off_sbf + kl_shift - (int)(k32_sb_end >> k32_sb_fsh)) * 4;
+constexpr uint32_t kb_db = (uint32_t)(k32_off_db + kl_shift - k32_db_first) * 4;
+constexpr uint32_t kb_dbf = (uint32_t)(k32_off_dbf + kl_shift - (int)(k32_db_end >> k32_db_fsh)) * 4;
 
 // LDS byte addresses of the adder's tables (interpolation tables less their
 // grid origin), computed once per kernel; the empty asm keeps them opaque
 // registers, so that picking a table is one select and no base add follows.
 struct x32_tab {
     uint32_t dlo, dhi, sb, sbf, db, dbf, zero, desc;
+    uint32_t one, nil;   // 1 and 0 in registers the compiler cannot see into
 };
 __device__ __forceinline__ x32_tab x32_origins(const int32_t *T) {
     uint32_t tb = lds_addr(T);
     asm("" : "+v"(tb));
-    x32_tab o{tb + (uint32_t)k32_off_dlo * 4, tb + (uint32_t)k32_off_dhi * 4, tb + kb_sb, tb + kb_sbf, tb + kb_db,
-              tb + kb_dbf, tb + (uint32_t)k32_tab_n * 4, tb + (uint32_t)(k32_tab_n + 4) * 4};
+    x32_tab o{tb + (uint32_t)kl_dlo * 4, tb + (uint32_t)kl_dhi * 4, tb + kb_sb, tb + kb_sbf, tb + kb_db,
+              tb + kb_dbf, tb + (uint32_t)kl_zero * 4, tb + (uint32_t)kl_desc * 4, 1u, 0u};
     // each origin its own register: a select among them stays a select (not
     // a lookup table of their constant offsets)
-    asm("" : "+v"(o.sb), "+v"(o.sbf), "+v"(o.db), "+v"(o.dbf), "+v"(o.zero));
+    asm("" : "+v"(o.sb), "+v"(o.sbf), "+v"(o.db), "+v"(o.dbf), "+v"(o.zero), "+v"(o.one), "+v"(o.nil));
     return o;
 }
 
 
-// A select on values: a conditional on two struct fields is an lvalue, a
-// select of their addresses, and nested ones force the struct into scratch.
-__device__ __forceinline__ uint32_t sel(bool c, uint32_t a, uint32_t b) { return c ? a : b; }
-
 // The same addition ordered for one chain per lane, where every instruction
 // of the wave is on the chain's clock (a single wave issues about one
-// instruction per 2 ns).  Two rounds of LDS lookups: the cotransformation's
-// dlo[dl] and (dh << 12) + dhi[dh], and beside them a descriptor of the
-// direct interpolation at d, (origin, grid shift) of the sb / db table that
-// d uses or the zero pair where d takes none (the cotransformation region,
-// shift 30, and beyond the essential zero, shift 31); then the pair of grid
-// nodes, at e on the sb tables for the cotransformation, else at d.  The
-// dl = 0 sentinel puts e beyond the essential zero, where the sb tables read
-// 0, so every cotransformation lane with dh != 0 interpolates at e.  The
+// instruction per 2 ns).  Two rounds of LDS lookups.  First a descriptor
+// keyed by (opposite signs, binade of d), the cotransformation's dlo[dl] and
+// the dhi pair of dh; then the pair of grid nodes around x, where x is d on
+// the sb / db grid the descriptor names (the zero pair from the essential
+// zero on), or, on cotransformation lanes, e on sb's near or far grid.  The
+// dl = 0 sentinel and dh = 0 put e beyond the essential zero, where the sb
+// tables read 0, so every cotransformation lane interpolates at e and adds
+// dlo[dl] (dh = 0) or dhi[dh] besides.  The selects are bit-field inserts on
+// lane masks from the descriptor or from sign bits, with no compare.  The
 // larger log, the result's sign and the caller's `shadow` work (the next
 // product) fill the first round trip; what the tail needs the second.
 // Scheduling barriers keep the groups in this order.
 template <class F>
 __device__ __forceinline__ void x32_add_desc(const x32_tab &O, acc_ls &a, uint32_t tl, uint32_t ts, F &&shadow) {
-    const uint32_t d = absdiff(a.l, tl);
+    const uint32_t d = absdiff(a.l, tl, O.nil);
     const uint32_t u = a.s ^ ts;
-    const uint32_t dl = d & ((1u << k32_co_sh) - 1u), dh = (d >> k32_co_sh) & ((1u << k32_co_sh) - 1u);
-    const int32_t lo = lds_ld(lshl2_add(dl, O.dlo));    // dlo[dl]
-    const int32_t th2 = lds_ld(lshl2_add(dh, O.dhi));   // (dh << 12) + dhi[dh]
-    const uint32_t dsc = lshl3_add(__builtin_amdgcn_ubfe(d | u, 23, 9), O.desc);
-    const uint32_t base_d = (uint32_t)lds_ld(dsc), sh_d = (uint32_t)lds_ld(dsc + 4);
+    // (origin, grid shift, cap of e, cotransformation lane mask)
+    const u32x4 dsc = lds_ld4(lds_at4(__builtin_amdgcn_ubfe(d | u, 23, 9), O.desc));
+    const int32_t lo = lds_ld(lds_at2(d & ((1u << k32_co_sh) - 1u), O.dlo));   // dlo[dl]
+    // ((dh << 12) + dhi[dh], dhi[dh] or 0 for dh = 0)
+    const i32x2 hp = lds_ld2(lds_at3(__builtin_amdgcn_ubfe(d, k32_co_sh, k32_co_sh), O.dhi));
     __builtin_amdgcn_sched_barrier(0);
-    uint32_t mx = max(a.l, tl);
+    const uint32_t mx = max(a.l, tl);
     // sign: the larger operand's (bit 31 of tl - a.l is set when a.l > tl),
     // and + for exact cancellation (bit 31 of d - 1 is set only for d = 0)
-    uint32_t nsign = (ts ^ ((tl - a.l) & u)) & ~((d - 1u) & u);
+    const uint32_t nsign = (ts ^ ((tl - a.l) & u)) & ~((d - 1u) & u);
     shadow();
-    asm volatile("" : "+v"(mx), "+v"(nsign));
     __builtin_amdgcn_sched_barrier(0);
-    const bool co = sh_d == 30;
-    const bool at_e = co && dh != 0;
-    const uint32_t e = (uint32_t)th2 - (uint32_t)lo;
-    const uint32_t xe = min(e, k32_esszer);
-    const bool hi_e = e >= k32_sb_end;
-    const int sh_e = hi_e ? k32_sb_fsh : k32_sb_sh;
-    const uint32_t ne = lshl2_add(xe >> sh_e, sel(hi_e, O.sbf, O.sb));
-    const uint32_t nd = lshl2_add(d >> sh_d, base_d);
-    const uint32_t node = sel(at_e, ne, nd);
+    // x: e (capped) on cotransformation lanes, d elsewhere (cap 0 there)
+    const uint32_t xe = min((uint32_t)hp.x - (uint32_t)lo, dsc.z);
+    const uint32_t x = bfi(dsc.w, xe, d);
+    const uint32_t hi = sign_mask(k32_sb_end - 1u - xe, O.one);   // e on sb's far grid
+    const uint32_t sh = bfi(hi, (uint32_t)k32_sb_fsh, dsc.y);
+    const uint32_t node = lshl2_add(x >> sh, bfi(hi, O.sbf, dsc.x));
     const int32_t t0 = lds_ld(node), t1 = lds_ld(node + 4);
     __builtin_amdgcn_sched_barrier(0);
-    const int32_t th = th2 - (int32_t)(dh << k32_co_sh);
-    const int32_t mA = (int32_t)mx + (co ? (dh == 0 ? lo : th) : 0);
-    const uint32_t sh = at_e ? (uint32_t)sh_e : sh_d;
-    const int32_t frac = (int32_t)__builtin_amdgcn_ubfe(at_e ? xe : d, 0, sh);
+    // the addend outside the interpolation: dlo[dl] where dh = 0, else dhi[dh]
+    // (cotransformation lanes only)
+    const int32_t A = (int32_t)(dsc.w & bfi(sign_mask((uint32_t)hp.y, O.one), (uint32_t)hp.y, (uint32_t)lo));
+    const int32_t mA = (int32_t)mx + A;
+    const int32_t frac = (int32_t)__builtin_amdgcn_ubfe(x, 0, sh);
     __builtin_amdgcn_sched_barrier(0);
     const int32_t ip = t0 + (__mul24(t1 - t0, frac) >> sh);
     a.l = (uint32_t)max(__builtin_elementwise_add_sat(mA, ip), 0);
@@ -412,29 +458,22 @@ __device__ __forceinline__ void x32_add_desc(const x32_tab &O, acc_ls &a, uint32
 // x32_add_desc without the scheduling order, for lanes that run several
 // chains (the compiler interleaves them)
 __device__ __forceinline__ void x32_add_ls(const x32_tab &O, acc_ls &a, uint32_t tl, uint32_t ts) {
-    const uint32_t d = absdiff(a.l, tl);
+    const uint32_t d = absdiff(a.l, tl, O.nil);
     const uint32_t u = a.s ^ ts;
-    const uint32_t dl = d & ((1u << k32_co_sh) - 1u), dh = (d >> k32_co_sh) & ((1u << k32_co_sh) - 1u);
-    const int32_t lo = lds_ld(lshl2_add(dl, O.dlo));
-    const int32_t th2 = lds_ld(lshl2_add(dh, O.dhi));
-    const uint32_t dsc = lshl3_add(__builtin_amdgcn_ubfe(d | u, 23, 9), O.desc);
-    const uint32_t base_d = (uint32_t)lds_ld(dsc), sh_d = (uint32_t)lds_ld(dsc + 4);
+    const u32x4 dsc = lds_ld4(lds_at4(__builtin_amdgcn_ubfe(d | u, 23, 9), O.desc));
+    const int32_t lo = lds_ld(lds_at2(d & ((1u << k32_co_sh) - 1u), O.dlo));
+    const i32x2 hp = lds_ld2(lds_at3(__builtin_amdgcn_ubfe(d, k32_co_sh, k32_co_sh), O.dhi));
     const uint32_t mx = max(a.l, tl);
     const uint32_t nsign = (ts ^ ((tl - a.l) & u)) & ~((d - 1u) & u);
-    const bool co = sh_d == 30;
-    const bool at_e = co && dh != 0;
-    const uint32_t e = (uint32_t)th2 - (uint32_t)lo;
-    const uint32_t xe = min(e, k32_esszer);
-    const bool hi_e = e >= k32_sb_end;
-    const int sh_e = hi_e ? k32_sb_fsh : k32_sb_sh;
-    const uint32_t ne = lshl2_add(xe >> sh_e, sel(hi_e, O.sbf, O.sb));
-    const uint32_t nd = lshl2_add(d >> sh_d, base_d);
-    const uint32_t node = sel(at_e, ne, nd);
+    const uint32_t xe = min((uint32_t)hp.x - (uint32_t)lo, dsc.z);
+    const uint32_t x = bfi(dsc.w, xe, d);
+    const uint32_t hi = sign_mask(k32_sb_end - 1u - xe, O.one);
+    const uint32_t sh = bfi(hi, (uint32_t)k32_sb_fsh, dsc.y);
+    const uint32_t node = lshl2_add(x >> sh, bfi(hi, O.sbf, dsc.x));
     const int32_t t0 = lds_ld(node), t1 = lds_ld(node + 4);
-    const int32_t th = th2 - (int32_t)(dh << k32_co_sh);
-    const int32_t mA = (int32_t)mx + (co ? (dh == 0 ? lo : th) : 0);
-    const uint32_t sh = at_e ? (uint32_t)sh_e : sh_d;
-    const int32_t frac = (int32_t)__builtin_amdgcn_ubfe(at_e ? xe : d, 0, sh);
+    const int32_t A = (int32_t)(dsc.w & bfi(sign_mask((uint32_t)hp.y, O.one), (uint32_t)hp.y, (uint32_t)lo));
+    const int32_t mA = (int32_t)mx + A;
+    const int32_t frac = (int32_t)__builtin_amdgcn_ubfe(x, 0, sh);
     const int32_t ip = t0 + (__mul24(t1 - t0, frac) >> sh);
     a.l = (uint32_t)max(__builtin_elementwise_add_sat(mA, ip), 0);
     a.s = nsign;
@@ -567,35 +606,49 @@ __device__ __forceinline__ red16<LNSHIP_SUM32> stage_tables<LNSHIP_SUM32>(const 
     int32_t *t = reinterpret_cast<int32_t *>(lds);
     const int4 *src = reinterpret_cast<const int4 *>(T.tab32);
     int4 *d4 = reinterpret_cast<int4 *>(t);
-    stage_copy(d4, src, k32_tab_n / 4);
-    for (int i = (k32_tab_n / 4) * 4 + threadIdx.x; i < k32_tab_n; i += blockDim.x) t[i] = T.tab32[i];
+    stage_copy(d4 + kl_dlo / 4, src + k32_off_dlo / 4, k32_co_n / 4);
+    stage_copy(d4 + kl_sb / 4, src + k32_off_sb / 4, (k32_tab_n - k32_off_sb) / 4);
+    // dhi as pairs (th2, th): th2 = (dh << 12) + dhi[dh], the first half of
+    // the cotransformation's e, and th = dhi[dh] (< 0), the part the result
+    // adds.  dh = 0 gets (13 binades, 0): e = 13 binades - dlo[dl] is then
+    // beyond the essential zero for every dl (dlo[dl] <= db(4095) < -11.5
+    // binades, and the d = 0 sentinel overflows e past it), so the
+    // interpolation at e reads 0, and th = 0 (not negative) marks the lanes
+    // that add dlo[dl] instead.
+    for (int i = threadIdx.x; i < k32_co_n; i += blockDim.x) {
+        const int32_t h = T.tab32[k32_off_dhi + i];
+        t[kl_dhi + 2 * i] = i == 0 ? (int32_t)(13u << 23) : h + (i << k32_co_sh);
+        t[kl_dhi + 2 * i + 1] = i == 0 ? 0 : h;
+    }
     __syncthreads();
-    if (threadIdx.x == 0) t[k32_off_dlo] = -0x7fffffff;   // db at d = 0: exact cancellation
-    if (threadIdx.x < 4) t[k32_tab_n + threadIdx.x] = 0;   // the zero pair
-    // dhi[dh] -> (dh << 12) + dhi[dh], the first half of the cotransformation's e
-    for (int i = 1 + threadIdx.x; i < k32_co_n; i += blockDim.x) t[k32_off_dhi + i] += i << k32_co_sh;
-    // descriptor of key = (opposite signs) << 8 | (d >> 23): where the direct
-    // interpolation at d reads (origin, grid shift).  Keys with no direct
-    // interpolation point at the zero pair with a shift that empties d >> sh:
-    // 30 below two binades of opposite signs (the cotransformation), 31 from
-    // the essential zero on.
+    if (threadIdx.x == 0) t[kl_dlo] = -0x7fffffff;   // db at d = 0: exact cancellation
+    if (threadIdx.x < 4) t[kl_zero + threadIdx.x] = 0;   // the zero pair
+    // descriptor of key = (opposite signs) << 8 | (d >> 23): (origin, grid
+    // shift, cap of e, lane mask).  Direct keys read the interpolation at d:
+    // the sb / db table of d's binade, or the zero pair with a shift that
+    // empties d >> sh from the essential zero on; their cap 0 clamps e to 0.
+    // Cotransformation keys (opposite signs, d below two binades) read at e
+    // instead: sb's near grid, the far one chosen from e, e capped at the
+    // essential zero, and an all-ones mask.
     {
-        const uint32_t tb = lds_addr(t), zero = tb + (uint32_t)k32_tab_n * 4;
+        const uint32_t tb = lds_addr(t), zero = tb + (uint32_t)kl_zero * 4;
         for (int k = threadIdx.x; k < k32_desc_n; k += blockDim.x) {
             const uint32_t q = (uint32_t)k & 255u;
-            uint32_t base = zero, sh = 31;
+            uint32_t base = zero, sh = 31, cap = 0, co = 0;
             if (k < 256) {
                 if (q < (k32_sb_end >> 23)) base = tb + kb_sb, sh = k32_sb_sh;
                 else if (q < (k32_esszer >> 23)) base = tb + kb_sbf, sh = k32_sb_fsh;
             } else if (q < (k32_co_end >> 23)) {
-                sh = 30;
+                base = tb + kb_sb, sh = k32_sb_sh, cap = k32_esszer, co = ~0u;
             } else if (q < (k32_db_end >> 23)) {
                 base = tb + kb_db, sh = k32_db_sh;
             } else if (q < (k32_esszer >> 23)) {
                 base = tb + kb_dbf, sh = k32_db_fsh;
             }
-            t[k32_tab_n + 4 + 2 * k] = (int32_t)base;
-            t[k32_tab_n + 4 + 2 * k + 1] = (int32_t)sh;
+            t[kl_desc + 4 * k] = (int32_t)base;
+            t[kl_desc + 4 * k + 1] = (int32_t)sh;
+            t[kl_desc + 4 * k + 2] = (int32_t)cap;
+            t[kl_desc + 4 * k + 3] = (int32_t)co;
         }
     }
     return red16<LNSHIP_SUM32>{x32_origins(t)};
@@ -788,11 +841,25 @@ __global__ __launch_bounds__(k_block * CG) void k_mm16(mm_args16 a, dev_tables T
             // one chain per lane: the product of step u + 1, already in the
             // accumulator's xlns32 positions, is formed in step u's shadow
             const uint32_t xx[4] = {xq[0].x, xq[0].y, xq[0].z, xq[0].w};
+            // the products of steps 2i and 2i + 1 together, in the two 16-bit
+            // halves: the log fields added (no carry crosses the halves: each
+            // sum is at most 0x7fff + 0x7fff), less the offset with unsigned
+            // saturation (underflow: log 0), capped at 0x7fff (overflow)
+            uint32_t pl = 0, ps = 0;
+            auto pair = [&](int i) {
+                const uint32_t lm = (ww[i] & 0x7fff7fffu) + (xx[i] & 0x7fff7fffu);
+                pl = pk_min_u16(pk_sub_sat_u16(lm, 0x40004000u), 0x7fff7fffu);
+                ps = ww[i] ^ xx[i];
+            };
             auto prod = [&](int u, uint32_t &tl, uint32_t &ts) {
-                const uint32_t wv = half16(ww[u >> 1], u & 1), xv = half16(xx[u >> 1], u & 1);
-                const int32_t l = (int32_t)(wv & k16_logmask) + (int32_t)(xv & k16_logmask) - (int32_t)k16_one;
-                tl = (uint32_t)min(max(l, 0), (int32_t)k16_logmask) << 16;
-                ts = ((wv ^ xv) & k16_sign) << 16;
+                if ((u & 1) == 0) {
+                    pair(u >> 1);
+                    tl = pl << 16;
+                    ts = (ps & k16_sign) << 16;
+                } else {
+                    tl = pl & 0xffff0000u;
+                    ts = ps & k32_sign;
+                }
             };
             const bool first = u0 < 0;
             const int ub = first ? 0 : u0;
