@@ -479,6 +479,24 @@ __device__ __forceinline__ void x32_add_ls(const x32_tab &O, acc_ls &a, uint32_t
     a.s = nsign;
 }
 
+// An xlns32 addition of two positive values, for sums whose every addend is
+// positive (sums of squares, sums of exps): the sign stays +, the adjustment
+// is always sb(d), and one round of LDS reads suffices, the node pair around
+// d on sb's near or far grid.  d is capped at the essential zero, where the
+// far grid's last node and the interpolation read 0.  The result needs no
+// clamp at 0 (sb >= 0); it saturates on overflow as the general addition.
+__device__ __forceinline__ uint32_t x32_add_pos(const x32_tab &O, uint32_t al, uint32_t tl) {
+    const uint32_t xd = min(absdiff(al, tl, O.nil), k32_esszer);
+    const uint32_t hi = sign_mask(k32_sb_end - 1u - xd, O.one);   // d on the far grid
+    const uint32_t sh = bfi(hi, (uint32_t)k32_sb_fsh, (uint32_t)k32_sb_sh);
+    const uint32_t node = lshl2_add(xd >> sh, bfi(hi, O.sbf, O.sb));
+    const int32_t t0 = lds_ld(node), t1 = lds_ld(node + 4);
+    const int32_t mx = (int32_t)max(al, tl);
+    const int32_t frac = (int32_t)__builtin_amdgcn_ubfe(xd, 0, sh);
+    const int32_t ip = t0 + (__mul24(t1 - t0, frac) >> sh);
+    return (uint32_t)__builtin_elementwise_add_sat(mx, ip);
+}
+
 // A whole xlns32 addition on packed values (sign bit 31) over the LDS tables.
 __device__ __forceinline__ uint32_t x32_add_lds(const x32_tab &O, uint32_t x, uint32_t y) {
     acc_ls a{x & k32_logmask, x & k32_sign};
@@ -1095,7 +1113,9 @@ __global__ __launch_bounds__(k_block * CG) void k_mm32(mm_args32 a, dev_tables T
 // acc <- acc (+) row[i] for i = i0 .. n-1 in order (i0 < n).  row is in LDS,
 // 16-byte aligned, and readable up to n rounded up to a whole 16-byte group;
 // each group of codes arrives in one 16-byte read issued a group ahead.
-template <class RED>
+// POS: the accumulator and every row[i] are positive (sign bit clear), so the
+// xlns32 sum takes the one-round positive addition.
+template <class RED, bool POS = false>
 __device__ __forceinline__ void chain16(const RED &R, typename RED::acc_t &acc, const uint16_t *row, int i0, int n,
                                         uint32_t &st) {
     const int g0 = i0 >> 3, gl = (n - 1) >> 3;
@@ -1105,7 +1125,9 @@ __device__ __forceinline__ void chain16(const RED &R, typename RED::acc_t &acc, 
 #pragma unroll
         for (int u = 0; u < 8; u++)
             if (u >= u0 && u < u1) {
-                if constexpr (std::is_same<RED, red16<LNSHIP_SUM32>>::value) {
+                if constexpr (std::is_same<RED, red16<LNSHIP_SUM32>>::value && POS) {
+                    acc.l = x32_add_pos(R.O, acc.l, half16(w[u >> 1], u & 1) << 16);
+                } else if constexpr (std::is_same<RED, red16<LNSHIP_SUM32>>::value) {
                     const uint32_t v = half16(w[u >> 1], u & 1);
                     R.add_lat(acc, (v & k16_logmask) << 16, (v & k16_sign) << 16, [] {});
                 } else {
@@ -1124,6 +1146,7 @@ __device__ __forceinline__ void chain16(const RED &R, typename RED::acc_t &acc, 
 }
 
 // the same over packed xlns32 codes, four per 16-byte group
+template <bool POS = false>
 __device__ __forceinline__ void chain32(const x32_tab &O, acc_ls &acc, const uint32_t *row, int i0, int n) {
     const int g0 = i0 >> 2, gl = (n - 1) >> 2;
     auto ld = [&](int g) { return *reinterpret_cast<const uint4 *>(row + 4 * min(g, gl)); };
@@ -1132,7 +1155,8 @@ __device__ __forceinline__ void chain32(const x32_tab &O, acc_ls &acc, const uin
 #pragma unroll
         for (int u = 0; u < 4; u++)
             if (u >= u0 && u < u1) {
-                x32_add_desc(O, acc, w[u] & k32_logmask, w[u] & k32_sign, [] {});
+                if constexpr (POS) acc.l = x32_add_pos(O, acc.l, w[u]);
+                else x32_add_desc(O, acc, w[u] & k32_logmask, w[u] & k32_sign, [] {});
             }
     };
     uint4 cur = ld(g0), nxt = ld(g0 + 1);
@@ -1186,7 +1210,7 @@ __global__ __launch_bounds__(k_block) void k_rms16(const float *__restrict__ src
         if (MODE == LNSHIP_MONTE)
             s = lfsr_jump(T, monte_start(T, seed, state, offset), (uint64_t)(r0 + r) * (uint64_t)ncols);
         typename red16<MODE>::acc_t acc = R.start(0u, s);
-        chain16(R, acc, sq + r * rs, 0, nc, s);
+        chain16<red16<MODE>, true>(R, acc, sq + r * rs, 0, nc, s);   // squares: positive
         const uint32_t sum = R.finish(acc) & 0xffffu;
         const uint32_t mean = x16_mul(sum, x16_from_f32(T.cvt16, 1.0f / (float)ncols));
         const uint32_t e16 = x16_from_f32(T.cvt16, eps);
@@ -1246,7 +1270,7 @@ __global__ __launch_bounds__(k_block) void k_rms32(const float *__restrict__ src
     if ((int)threadIdx.x < nr) {
         const int r = threadIdx.x;
         acc_ls a{0u, 0u};
-        chain32(R.O, a, sq + r * rs, 0, nc);
+        chain32<true>(R.O, a, sq + r * rs, 0, nc);   // squares: positive
         const uint32_t acc = a.s | a.l;
         const uint32_t mean = x32_mul(acc, x32_from_f32(1.0f / (float)ncols));
         s_inv[r] = x32_recip(x32_sqrt(x32_add_lds(R.O, mean, x32_from_f32(eps))));
@@ -1401,7 +1425,7 @@ __global__ __launch_bounds__(k_block) void k_softmax16(sm_args a, dev_tables T) 
         // draws after it are not taken; the next op's start does not depend
         // on them)
         const int n_eff = s_last[r] + 1;
-        if (n_eff > 1) chain16(R, acc, row, 1, n_eff, s);
+        if (n_eff > 1) chain16<red16<MODE>, true>(R, acc, row, 1, n_eff, s);   // exps: positive
         s_tot[r] = R.finish(acc) & 0xffffu;
     }
     __syncthreads();
@@ -1486,7 +1510,7 @@ __global__ __launch_bounds__(k_block) void k_softmax32(sm_args a, dev_tables T) 
         // trailing exps of log 0 add nothing to a sum of at least 1 (as in
         // k_softmax16): the chain stops at the last nonzero exp
         const int n_eff = s_last[r] + 1;
-        if (n_eff > 1) chain32(R.O, acc, row, 1, n_eff);
+        if (n_eff > 1) chain32<true>(R.O, acc, row, 1, n_eff);   // exps: positive
         s_tot[r] = acc.s | acc.l;
     }
     __syncthreads();
