@@ -420,25 +420,39 @@ __device__ __forceinline__ x32_tab x32_origins(const int32_t *T) {
 // larger log, the result's sign and the caller's `shadow` work (the next
 // product) fill the first round trip; what the tail needs the second.
 // Scheduling barriers keep the groups in this order.
-template <class F>
-__device__ __forceinline__ void x32_add_desc(const x32_tab &O, acc_ls &a, uint32_t tl, uint32_t ts, F &&shadow) {
-    const uint32_t d = absdiff(a.l, tl, O.nil);
-    const uint32_t u = a.s ^ ts;
-    // (origin, grid shift, cap of e, cotransformation lane mask)
-    const u32x4 dsc = lds_ld4(lds_at4(__builtin_amdgcn_ubfe(d | u, 23, 9), O.desc));
-    const int32_t lo = lds_ld(lds_at2(d & ((1u << k32_co_sh) - 1u), O.dlo));   // dlo[dl]
-    // ((dh << 12) + dhi[dh], dhi[dh] or 0 for dh = 0)
-    const i32x2 hp = lds_ld2(lds_at3(__builtin_amdgcn_ubfe(d, k32_co_sh, k32_co_sh), O.dhi));
+template <class F, class P>
+__device__ __forceinline__ uint32_t x32_add_step(const x32_tab &O, acc_ls &a, uint32_t tl, uint32_t ts, uint32_t u,
+                                                 F &&shadow, P &&post) {
+    // du = |a.l - tl| + u: d with the opposite-signs flag in bit 31, in one
+    // v_sad_u32; its fields index the three reads, and the descriptors of
+    // opposite-sign keys carry origins less 2^31 >> shift (x = du there)
+    const uint32_t du = absdiff(a.l, tl, u);
+    // the three addresses after the three indices, in one asm block so that
+    // each shift-add waits on an index formed two instructions earlier: the
+    // reads of dlo[dl], of the dhi pair of dh ((dh << 12) + dhi[dh], dhi[dh]
+    // or 0 for dh = 0) and of the descriptor (origin, grid shift, cap of e,
+    // cotransformation lane mask) go out back to back
+    uint32_t a_lo, a_hi, a_ds;
+    asm("v_lshl_add_u32 %0, %3, 2, %6\n\tv_lshl_add_u32 %1, %4, 3, %7\n\tv_lshl_add_u32 %2, %5, 4, %8"
+        : "=&v"(a_lo), "=&v"(a_hi), "=&v"(a_ds)
+        : "v"(du & ((1u << k32_co_sh) - 1u)), "v"(__builtin_amdgcn_ubfe(du, k32_co_sh, k32_co_sh)), "v"(du >> 23),
+          "v"(O.dlo), "v"(O.dhi), "v"(O.desc));
+    const int32_t lo = lds_ld(a_lo);
+    const i32x2 hp = lds_ld2(a_hi);
+    const u32x4 dsc = lds_ld4(a_ds);
     __builtin_amdgcn_sched_barrier(0);
     const uint32_t mx = max(a.l, tl);
     // sign: the larger operand's (bit 31 of tl - a.l is set when a.l > tl),
-    // and + for exact cancellation (bit 31 of d - 1 is set only for d = 0)
-    const uint32_t nsign = (ts ^ ((tl - a.l) & u)) & ~((d - 1u) & u);
-    shadow();
+    // and + for exact cancellation (with u set, bit 31 of du - 1 is clear
+    // only for d = 0)
+    const uint32_t nsign = bfi(tl - a.l, a.s, ts) & (~u | (du - 1u));
+    const uint32_t un = nsign ^ shadow();
+    // formed here, in the first round trip
+    asm volatile("" ::"v"(mx), "v"(nsign), "v"(un));
     __builtin_amdgcn_sched_barrier(0);
-    // x: e (capped) on cotransformation lanes, d elsewhere (cap 0 there)
+    // x: e (capped) on cotransformation lanes, du elsewhere (cap 0 there)
     const uint32_t xe = min((uint32_t)hp.x - (uint32_t)lo, dsc.z);
-    const uint32_t x = bfi(dsc.w, xe, d);
+    const uint32_t x = bfi(dsc.w, xe, du);
     const uint32_t hi = sign_mask(k32_sb_end - 1u - xe, O.one);   // e on sb's far grid
     const uint32_t sh = bfi(hi, (uint32_t)k32_sb_fsh, dsc.y);
     const uint32_t node = lshl2_add(x >> sh, bfi(hi, O.sbf, dsc.x));
@@ -449,24 +463,38 @@ __device__ __forceinline__ void x32_add_desc(const x32_tab &O, acc_ls &a, uint32
     const int32_t A = (int32_t)(dsc.w & bfi(sign_mask((uint32_t)hp.y, O.one), (uint32_t)hp.y, (uint32_t)lo));
     const int32_t mA = (int32_t)mx + A;
     const int32_t frac = (int32_t)__builtin_amdgcn_ubfe(x, 0, sh);
+    post();
     __builtin_amdgcn_sched_barrier(0);
     const int32_t ip = t0 + (__mul24(t1 - t0, frac) >> sh);
     a.l = (uint32_t)max(__builtin_elementwise_add_sat(mA, ip), 0);
     a.s = nsign;
+    return un;
+}
+
+// One addition of a chain, u computed here (one dependent step more)
+template <class F>
+__device__ __forceinline__ void x32_add_desc(const x32_tab &O, acc_ls &a, uint32_t tl, uint32_t ts, F &&shadow) {
+    x32_add_step(
+        O, a, tl, ts, a.s ^ ts,
+        [&] {
+            shadow();
+            return 0u;
+        },
+        [] {});
 }
 
 // x32_add_desc without the scheduling order, for lanes that run several
 // chains (the compiler interleaves them)
 __device__ __forceinline__ void x32_add_ls(const x32_tab &O, acc_ls &a, uint32_t tl, uint32_t ts) {
-    const uint32_t d = absdiff(a.l, tl, O.nil);
     const uint32_t u = a.s ^ ts;
-    const u32x4 dsc = lds_ld4(lds_at4(__builtin_amdgcn_ubfe(d | u, 23, 9), O.desc));
-    const int32_t lo = lds_ld(lds_at2(d & ((1u << k32_co_sh) - 1u), O.dlo));
-    const i32x2 hp = lds_ld2(lds_at3(__builtin_amdgcn_ubfe(d, k32_co_sh, k32_co_sh), O.dhi));
+    const uint32_t du = absdiff(a.l, tl, u);
+    const int32_t lo = lds_ld(lds_at2(du & ((1u << k32_co_sh) - 1u), O.dlo));
+    const i32x2 hp = lds_ld2(lds_at3(__builtin_amdgcn_ubfe(du, k32_co_sh, k32_co_sh), O.dhi));
+    const u32x4 dsc = lds_ld4(lds_at4(du >> 23, O.desc));
     const uint32_t mx = max(a.l, tl);
-    const uint32_t nsign = (ts ^ ((tl - a.l) & u)) & ~((d - 1u) & u);
+    const uint32_t nsign = bfi(tl - a.l, a.s, ts) & (~u | (du - 1u));
     const uint32_t xe = min((uint32_t)hp.x - (uint32_t)lo, dsc.z);
-    const uint32_t x = bfi(dsc.w, xe, d);
+    const uint32_t x = bfi(dsc.w, xe, du);
     const uint32_t hi = sign_mask(k32_sb_end - 1u - xe, O.one);
     const uint32_t sh = bfi(hi, (uint32_t)k32_sb_fsh, dsc.y);
     const uint32_t node = lshl2_add(x >> sh, bfi(hi, O.sbf, dsc.x));
@@ -663,6 +691,8 @@ __device__ __forceinline__ red16<LNSHIP_SUM32> stage_tables<LNSHIP_SUM32>(const 
             } else if (q < (k32_esszer >> 23)) {
                 base = tb + kb_dbf, sh = k32_db_fsh;
             }
+            // opposite-sign direct keys index with du = d + 2^31
+            if (k >= 256 && co == 0) base -= (0x80000000u >> sh) << 2;
             t[kl_desc + 4 * k] = (int32_t)base;
             t[kl_desc + 4 * k + 1] = (int32_t)sh;
             t[kl_desc + 4 * k + 2] = (int32_t)cap;
@@ -825,7 +855,7 @@ __global__ __launch_bounds__(k_block * CG) void k_mm16(mm_args16 a, dev_tables T
         return;
     }
 
-    typename red16<MODE>::acc_t acc[NC];
+    typename red16<MODE>::acc_t acc[NC]{};
     uint32_t st[NC];
 #pragma unroll
     for (int j = 0; j < NC; j++) {
@@ -853,51 +883,75 @@ __global__ __launch_bounds__(k_block * CG) void k_mm16(mm_args16 a, dev_tables T
     };
     // steps [u0, u1) of a group: the product (xlns16_mul: log fields added
     // and clamped, signs xor'ed), then one reduction step per column
-    auto steps = [&](const uint4 &wq, const uint4 (&xq)[NC], int u0, int u1) {
+    // SUM32, one chain per lane: what the chain carries from group to group
+    // (the product of the next step, its opposite-signs flag, and the
+    // product pair of the next group's steps 0 and 1)
+    uint32_t c_tl = 0, c_ts = 0, c_uf = 0, c_pl = 0, c_ps = 0;
+    // steps [u0, u1) of a group; wn / xn: the next group's data.  fresh: the
+    // chain's first group, or one whose carried state was not formed from it
+    auto steps = [&](const uint4 &wq, const uint4 (&xq)[NC], const uint4 &wn, const uint4 (&xn)[NC], int u0, int u1,
+                     bool fresh) {
         const uint32_t ww[4] = {wq.x, wq.y, wq.z, wq.w};
         if constexpr (MODE == LNSHIP_SUM32 && NC == 1) {
-            // one chain per lane: the product of step u + 1, already in the
-            // accumulator's xlns32 positions, is formed in step u's shadow
             const uint32_t xx[4] = {xq[0].x, xq[0].y, xq[0].z, xq[0].w};
             // the products of steps 2i and 2i + 1 together, in the two 16-bit
             // halves: the log fields added (no carry crosses the halves: each
             // sum is at most 0x7fff + 0x7fff), less the offset with unsigned
-            // saturation (underflow: log 0), capped at 0x7fff (overflow)
-            uint32_t pl = 0, ps = 0;
-            auto pair = [&](int i) {
-                const uint32_t lm = (ww[i] & 0x7fff7fffu) + (xx[i] & 0x7fff7fffu);
-                pl = pk_min_u16(pk_sub_sat_u16(lm, 0x40004000u), 0x7fff7fffu);
-                ps = ww[i] ^ xx[i];
+            // saturation (underflow: log 0), capped at 0x7fff (overflow); and
+            // the sign bits xor'ed.  Pair i + 1 is formed in step 2i's second
+            // round trip, the next group's pair 0 in step 6's.
+            uint32_t pl[4], ps[4];
+            auto pair = [](uint32_t w, uint32_t x, uint32_t &l, uint32_t &sg) {
+                const uint32_t lm = (w & 0x7fff7fffu) + (x & 0x7fff7fffu);
+                l = pk_min_u16(pk_sub_sat_u16(lm, 0x40004000u), 0x7fff7fffu);
+                sg = w ^ x;
             };
-            auto prod = [&](int u, uint32_t &tl, uint32_t &ts) {
+            // the product of step u (xlns32 positions) from its pair
+            auto half = [](int u, uint32_t l, uint32_t sg, uint32_t &tl, uint32_t &ts) {
                 if ((u & 1) == 0) {
-                    pair(u >> 1);
-                    tl = pl << 16;
-                    ts = (ps & k16_sign) << 16;
+                    tl = l << 16;
+                    ts = (sg & k16_sign) << 16;
                 } else {
-                    tl = pl & 0xffff0000u;
-                    ts = ps & k32_sign;
+                    tl = l & 0xffff0000u;
+                    ts = sg & k32_sign;
                 }
             };
+            // u0 is 0, or -1 for the chain's first group (its step 0 starts
+            // the sum)
             const bool first = u0 < 0;
-            const int ub = first ? 0 : u0;
-            uint32_t tl = 0, ts = 0;
-            if (ub < u1) prod(ub, tl, ts);
+            const int ub = 0;
+            if (fresh) {
+                pair(ww[0], xx[0], pl[0], ps[0]);
+                half(ub, pl[0], ps[0], c_tl, c_ts);
+                c_uf = acc[0].s ^ c_ts;
+            } else {
+                pl[0] = c_pl;
+                ps[0] = c_ps;
+            }
 #pragma unroll
             for (int u = 0; u < 8; u++) {
                 if (u >= ub && u < u1) {
                     uint32_t ntl = 0, nts = 0;
+                    // the next step's product, from its pair; after step 7,
+                    // the next group's step 0 from the carried pair
                     auto next = [&] {
-                        if (u + 1 < u1) prod(u + 1, ntl, nts);
+                        if (u + 1 < u1) half(u + 1, pl[(u + 1) >> 1], ps[(u + 1) >> 1], ntl, nts);
+                        else if (u == 7) half(0, c_pl, c_ps, ntl, nts);
+                        return nts;
+                    };
+                    auto post = [&] {
+                        if ((u & 1) == 0 && u < 6) pair(ww[(u >> 1) + 1], xx[(u >> 1) + 1], pl[(u >> 1) + 1], ps[(u >> 1) + 1]);
+                        if (u == 6) pair(wn.x, xn[0].x, c_pl, c_ps);
                     };
                     if (first && u == 0) {
-                        acc[0] = {tl, ts};
-                        next();
+                        acc[0] = {c_tl, c_ts};
+                        c_uf = c_ts ^ next();
+                        post();
                     } else {
-                        R.add_lat(acc[0], tl, ts, next);
+                        c_uf = x32_add_step(R.O, acc[0], c_tl, c_ts, c_uf, next, post);
                     }
-                    tl = ntl;
-                    ts = nts;
+                    c_tl = ntl;
+                    c_ts = nts;
                 }
             }
             return;
@@ -936,25 +990,29 @@ __global__ __launch_bounds__(k_block * CG) void k_mm16(mm_args16 a, dev_tables T
                 for (int j = 0; j < NC; j++) x[p][j] = load_x(j, g0 + p);
             }
         };
-        auto run_block = [&](const uint4 (&w)[PF], const uint4 (&x)[PF][NC], int g0) {
+        // the next group of group p of a block is p + 1, or the first of the
+        // other buffer (loaded before this block runs)
+        auto run_block = [&](const uint4 (&w)[PF], const uint4 (&x)[PF][NC], const uint4 (&wo)[PF],
+                             const uint4 (&xo)[PF][NC], int g0) {
 #pragma unroll
             for (int p = 0; p < PF; p++)
-                if (g0 + p < full) steps(w[p], x[p], 0, 8);
+                if (g0 + p < full) steps(w[p], x[p], p + 1 < PF ? w[p + 1] : wo[0], p + 1 < PF ? x[p + 1] : xo[0], 0, 8, false);
         };
         load_block(wa, xa, 1);
-        steps(wq, xq, -1, full > 0 ? 8 : tail);
+        steps(wq, xq, wa[0], xa[0], -1, full > 0 ? 8 : tail, true);
         for (int g = 1; g < full; g += 2 * PF) {
             load_block(wb, xb, g + PF);
-            run_block(wa, xa, g);
+            run_block(wa, xa, wb, xb, g);
             if (g + PF >= full) break;
             load_block(wa, xa, g + 2 * PF);
-            run_block(wb, xb, g + PF);
+            run_block(wb, xb, wa, xa, g + PF);
         }
         if (full > 0 && tail > 0) {
             uint4 tx[NC];
 #pragma unroll
             for (int j = 0; j < NC; j++) tx[j] = load_x(j, full);
-            steps(load_w(full), tx, 0, tail);
+            const uint4 tw = load_w(full);
+            steps(tw, tx, tw, tx, 0, tail, true);
         }
     }
 #pragma unroll
@@ -1026,7 +1084,7 @@ __global__ __launch_bounds__(k_block * CG) void k_mm32(mm_args32 a, dev_tables T
         const uint4 *p = reinterpret_cast<const uint4 *>(xs + off);
         return grp{p[0], p[1]};
     };
-    acc_ls acc[NC];
+    acc_ls acc[NC]{};
     auto steps = [&](const grp &wq, const grp (&xq)[NC], int u0, int u1) {
         const uint32_t wv[8] = {wq.lo.x, wq.lo.y, wq.lo.z, wq.lo.w, wq.hi.x, wq.hi.y, wq.hi.z, wq.hi.w};
         if constexpr (NC == 1) {
@@ -1037,18 +1095,21 @@ __global__ __launch_bounds__(k_block * CG) void k_mm32(mm_args32 a, dev_tables T
             const bool first = u0 < 0;
             const int ub = first ? 0 : u0;
             uint32_t t = ub < u1 ? x32_mul(wv[ub], xv[ub]) : 0u;
+            // uf: the opposite-signs flag (bit 31) of the pending addition
+            uint32_t uf = (acc[0].s ^ t) & k32_sign;
 #pragma unroll
             for (int u = 0; u < 8; u++) {
                 if (u >= ub && u < u1) {
                     uint32_t tn = 0;
                     auto next = [&] {
                         if (u + 1 < u1) tn = x32_mul(wv[u + 1], xv[u + 1]);
+                        return tn & k32_sign;
                     };
                     if (first && u == 0) {
                         acc[0] = {t & k32_logmask, t & k32_sign};
-                        next();
+                        uf = (t & k32_sign) ^ next();
                     } else {
-                        x32_add_desc(R.O, acc[0], t & k32_logmask, t & k32_sign, next);
+                        uf = x32_add_step(R.O, acc[0], t & k32_logmask, t & k32_sign, uf, next, [] {});
                     }
                     t = tn;
                 }
