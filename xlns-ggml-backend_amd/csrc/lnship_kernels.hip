@@ -779,6 +779,9 @@ __device__ __forceinline__ uint32_t monte_start(const dev_tables &T, uint32_t se
 
 template <int MODE>
 constexpr int mm_xl_offset() { return (lds_tables_bytes<MODE>() + 15) & ~15; }
+// LDS padding past the activation rows (a block's prefetch reads up to that
+// far past the last column)
+constexpr int k_xl_pad = 8 * 16;
 
 __device__ __forceinline__ uint32_t half16(uint32_t w, int hi) { return hi ? (w >> 16) : (w & 0xffffu); }
 
@@ -982,12 +985,38 @@ __global__ __launch_bounds__(k_block * CG) void k_mm16(mm_args16 a, dev_tables T
         // groups 1 .. full-1 in blocks of PF, double-buffered: the loads of
         // block b + 1 are issued together before block b is accumulated
         uint4 wa[PF], wb[PF], xa[PF][NC], xb[PF][NC];
+        // A block's loads from bases that move once per block.  Weights: from
+        // the block's first group (a wave-uniform base, clamped to the slice's
+        // last group) at lane offset m * 16 plus p * (bytes between groups)
+        // for the block's group p, the offset capped at the last group's (the
+        // last block's prefetch past the slice rereads it).  Activations in
+        // LDS: at immediate offsets p * 16 from the block's base (the LDS copy
+        // has PF * 16 bytes of padding past its last column).
+        const char *wsl = reinterpret_cast<const char *>(a.w + zw * a.w_slice);
+        const uint64_t gsb = (uint64_t)wstride * 2;
+        uint32_t vo[PF];
+#pragma unroll
+        for (int p = 0; p < PF; p++) vo[p] = (uint32_t)((uint64_t)m * 16 + (uint64_t)p * gsb);
         auto load_block = [&](uint4 (&w)[PF], uint4 (&x)[PF][NC], int g0) {
+            const int gb = min(g0, last);
+            const char *wb = wsl + (uint64_t)gb * gsb;
+            const uint32_t cap = (uint32_t)((uint64_t)(last - gb) * gsb) + (uint32_t)m * 16;
 #pragma unroll
-            for (int p = 0; p < PF; p++) {
-                w[p] = load_w(g0 + p);
+            for (int p = 0; p < PF; p++) w[p] = *reinterpret_cast<const uint4 *>(wb + min(vo[p], cap));
 #pragma unroll
-                for (int j = 0; j < NC; j++) x[p][j] = load_x(j, g0 + p);
+            for (int j = 0; j < NC; j++) {
+                if constexpr (XL) {
+                    // the base through a vector register: the data then counts
+                    // as per-lane and is waited for where it is used
+                    int32_t xo = (j * kp + g0 * 8) * 2;
+                    asm("" : "+v"(xo));
+                    const char *xb = reinterpret_cast<const char *>(xl) + xo;
+#pragma unroll
+                    for (int p = 0; p < PF; p++) x[p][j] = *reinterpret_cast<const uint4 *>(xb + p * 16);
+                } else {
+#pragma unroll
+                    for (int p = 0; p < PF; p++) x[p][j] = load_x(j, g0 + p);
+                }
             }
         };
         // the next group of group p of a block is p + 1, or the first of the
@@ -1985,7 +2014,7 @@ static int64_t mm16_tables_bytes(int mode) {
 
 // whether `cols` activation rows of kp codes fit in LDS next to the tables
 static bool mm16_xl(int mode, int cols, int64_t kp) {
-    return mm16_tables_bytes(mode) + (int64_t)cols * kp * 2 <= k_lds_bytes - 1024;
+    return mm16_tables_bytes(mode) + (int64_t)cols * kp * 2 + k_xl_pad <= k_lds_bytes - 1024;
 }
 
 // Columns per lane.  Every output is a K-long dependent chain, so a lane is
@@ -2047,7 +2076,11 @@ template <int MODE, int NC, bool XL, int CG>
 static int launch_mm16(const mm_args16 &m, const dev_tables &T, int64_t nslices, hipStream_t st) {
     // prefetch depth within 128 VGPRs at four waves per SIMD
     constexpr int PF = NC == 1 ? (CG >= 4 ? 4 : 8) : NC == 2 ? 2 : (NC == 4 && CG < 4) ? 2 : 1;
-    const int lds = mm_xl_offset<MODE>() + (XL ? (int)(NC * CG * m.kp * 2) : 0);
+    const int lds = mm_xl_offset<MODE>() + (XL ? (int)(NC * CG * m.kp * 2) + k_xl_pad : 0);
+    static_assert(PF * 16 <= k_xl_pad, "prefetch past the activation rows stays in the padding");
+    // weight offsets within a block of PF groups are 32-bit
+    if ((uint64_t)m.w_mstride * 16 * PF + (uint64_t)m.M * 16 > 0xffffffffu)
+        return fail(LNSHIP_ERANGE, "mul_mat: weight rows too long for 32-bit block offsets%s");
     if (lds > 64 * 1024)
         if (int rc = set_lds(k_mm16<MODE, NC, PF, XL, CG>, lds)) return rc;
     dim3 grid((unsigned)((m.M + k_block - 1) / k_block), (unsigned)((m.N + NC * CG - 1) / (NC * CG)), (unsigned)nslices);
