@@ -650,25 +650,9 @@ __device__ __forceinline__ red16<LNSHIP_MONTE> stage_tables<LNSHIP_MONTE>(const 
 template <>
 __device__ __forceinline__ red16<LNSHIP_SUM32> stage_tables<LNSHIP_SUM32>(const dev_tables &T, char *lds) {
     int32_t *t = reinterpret_cast<int32_t *>(lds);
-    const int4 *src = reinterpret_cast<const int4 *>(T.tab32);
-    int4 *d4 = reinterpret_cast<int4 *>(t);
-    stage_copy(d4 + kl_dlo / 4, src + k32_off_dlo / 4, k32_co_n / 4);
-    stage_copy(d4 + kl_sb / 4, src + k32_off_sb / 4, (k32_tab_n - k32_off_sb) / 4);
-    // dhi as pairs (th2, th): th2 = (dh << 12) + dhi[dh], the first half of
-    // the cotransformation's e, and th = dhi[dh] (< 0), the part the result
-    // adds.  dh = 0 gets (13 binades, 0): e = 13 binades - dlo[dl] is then
-    // beyond the essential zero for every dl (dlo[dl] <= db(4095) < -11.5
-    // binades, and the d = 0 sentinel overflows e past it), so the
-    // interpolation at e reads 0, and th = 0 (not negative) marks the lanes
-    // that add dlo[dl] instead.
-    for (int i = threadIdx.x; i < k32_co_n; i += blockDim.x) {
-        const int32_t h = T.tab32[k32_off_dhi + i];
-        t[kl_dhi + 2 * i] = i == 0 ? (int32_t)(13u << 23) : h + (i << k32_co_sh);
-        t[kl_dhi + 2 * i + 1] = i == 0 ? 0 : h;
-    }
-    __syncthreads();
-    if (threadIdx.x == 0) t[kl_dlo] = -0x7fffffff;   // db at d = 0: exact cancellation
-    if (threadIdx.x < 4) t[kl_zero + threadIdx.x] = 0;   // the zero pair
+    // the image built at init (lds32_image): one copy, in one batch of loads
+    // per thread at 256 threads
+    stage_copy<32>(reinterpret_cast<int4 *>(t), reinterpret_cast<const int4 *>(T.lds32), kl_desc / 4);
     // descriptor of key = (opposite signs) << 8 | (d >> 23): (origin, grid
     // shift, cap of e, lane mask).  Direct keys read the interpolation at d:
     // the sb / db table of d's binade, or the zero pair with a shift that
@@ -2322,6 +2306,29 @@ const void *lnship_host_table(const char *name, size_t *bytes) {
     return nullptr;
 }
 
+// The LDS image of the xlns32 adder tables, up to the descriptors (which hold
+// LDS addresses, so each workgroup forms them): dlo with the db-at-zero entry
+// replaced by a sentinel (exact cancellation clamps the log to 0); dhi as
+// pairs (th2, th), th2 = (dh << 12) + dhi[dh], the first half of the
+// cotransformation's e, and th = dhi[dh] (< 0), the part the result adds.
+// dh = 0 gets (13 binades, 0): e = 13 binades - dlo[dl] is then beyond the
+// essential zero for every dl (dlo[dl] <= db(4095) < -11.5 binades, and the
+// d = 0 sentinel overflows e past it), so the interpolation at e reads 0, and
+// th = 0 (not negative) marks the lanes that add dlo[dl] instead.  Then the
+// interpolation tables sb, sbf, db, dbf as in the device block, and a zero
+// pair.
+static void lds32_image(const int32_t *tab, std::vector<int32_t> &img) {
+    img.assign(kl_desc, 0);
+    for (int i = 0; i < k32_co_n; i++) img[kl_dlo + i] = tab[k32_off_dlo + i];
+    img[kl_dlo] = -0x7fffffff;
+    for (int i = 0; i < k32_co_n; i++) {
+        const int32_t h = tab[k32_off_dhi + i];
+        img[kl_dhi + 2 * i] = i == 0 ? (int32_t)(13u << 23) : h + (i << k32_co_sh);
+        img[kl_dhi + 2 * i + 1] = i == 0 ? 0 : h;
+    }
+    for (int i = k32_off_sb; i < k32_tab_n; i++) img[i + kl_shift] = tab[i];
+}
+
 int lnship_init(void) {
     int dev = 0;
     if (int rc = current_device(&dev)) return rc;
@@ -2337,6 +2344,11 @@ int lnship_init(void) {
     if (int rc = upload(g_host->exp16, 1u << 16, &T.exp16)) return rc;
     if (int rc = upload(g_host->sig16, 1u << 16, &T.sig16)) return rc;
     if (int rc = upload(g_host->tab32, (size_t)k32_tab_n, &T.tab32)) return rc;
+    {
+        std::vector<int32_t> img;
+        lds32_image(g_host->tab32, img);
+        if (int rc = upload(img.data(), img.size(), &T.lds32)) return rc;
+    }
     if (int rc = upload(g_host->lfsr_seq, 65536, &T.lfsr_seq)) return rc;
     if (int rc = upload(g_host->lfsr_log, 65536, &T.lfsr_log)) return rc;
     s.T = T;
