@@ -30,19 +30,20 @@ constexpr int k_max_devices = 64;
 constexpr int k_lds_bytes = 160 * 1024;
 // what the row kernels' static shared arrays may take beside their dynamic LDS
 constexpr int k_lds_static = 2048;
-// The LDS copy of the xlns32 adder tables (32-bit words): dlo, then dhi as
-// pairs (two words per dh), then the interpolation tables sb, sbf, db, dbf as
-// in the device table block, a zero pair, and 512 four-word descriptors of
-// the interpolation, indexed by (opposite signs, binade of d).
+// The LDS copy of the xlns32 adder tables (32-bit words): 512 four-word
+// descriptors of the interpolation, indexed by (opposite signs, binade of d),
+// then dlo, then dhi as pairs (two words per dh), then the interpolation
+// tables sb, sbf, db, dbf as in the device table block, and a zero pair.
 constexpr int k32_desc_n = 512;
-constexpr int kl_dlo = 0;
+constexpr int kl_desc = 0;
+constexpr int kl_dlo = kl_desc + 4 * k32_desc_n;
 constexpr int kl_dhi = kl_dlo + k32_co_n;
 constexpr int kl_sb = kl_dhi + 2 * k32_co_n;                 // the rest of the block from sb on
 constexpr int kl_zero = kl_sb + (k32_tab_n - k32_off_sb);
-constexpr int kl_desc = kl_zero + 4;
-constexpr int k_lds_tab32 = (kl_desc + 4 * k32_desc_n) * 4;   // 132896 bytes
+constexpr int kl_end = kl_zero + 4;
+constexpr int k_lds_tab32 = kl_end * 4;   // 132896 bytes
 static_assert(k32_off_sb % 4 == 0 && kl_sb % 4 == 0 && (k32_tab_n - k32_off_sb) % 4 == 0, "16-byte staging");
-static_assert(kl_desc % 4 == 0, "descriptors are read 16 bytes at a time");
+static_assert(kl_dlo % 4 == 0 && (kl_end - kl_dlo) % 4 == 0, "16-byte staging");
 
 static thread_local std::string t_err;
 
@@ -393,15 +394,19 @@ constexpr uint32_t kb_dbf = (uint32_t)(k32_off_dbf + kl_shift - (int)(k32_db_end
 struct x32_tab {
     uint32_t dlo, dhi, sb, sbf, db, dbf, zero, desc;
     uint32_t one, nil;   // 1 and 0 in registers the compiler cannot see into
+    // a mask and a bound in registers: two-operand instructions take them in
+    // their short encoding (a literal operand makes an instruction 8 bytes)
+    uint32_t m0fff, ksb;
 };
 __device__ __forceinline__ x32_tab x32_origins(const int32_t *T) {
     uint32_t tb = lds_addr(T);
     asm("" : "+v"(tb));
     x32_tab o{tb + (uint32_t)kl_dlo * 4, tb + (uint32_t)kl_dhi * 4, tb + kb_sb, tb + kb_sbf, tb + kb_db,
-              tb + kb_dbf, tb + (uint32_t)kl_zero * 4, tb + (uint32_t)kl_desc * 4, 1u, 0u};
+              tb + kb_dbf, tb + (uint32_t)kl_zero * 4, tb + (uint32_t)kl_desc * 4, 1u, 0u, 0xfffu, k32_sb_end - 1u};
     // each origin its own register: a select among them stays a select (not
     // a lookup table of their constant offsets)
     asm("" : "+v"(o.sb), "+v"(o.sbf), "+v"(o.db), "+v"(o.dbf), "+v"(o.zero), "+v"(o.one), "+v"(o.nil));
+    asm("" : "+v"(o.m0fff), "+v"(o.ksb));
     return o;
 }
 
@@ -420,6 +425,10 @@ __device__ __forceinline__ x32_tab x32_origins(const int32_t *T) {
 // larger log, the result's sign and the caller's `shadow` work (the next
 // product) fill the first round trip; what the tail needs the second.
 // Scheduling barriers keep the groups in this order.
+// One addition of a single-chain step: a <- a (+) (tl, ts).  u = a.s ^ ts
+// (the opposite-signs flag, bit 31); shadow() runs in the first round trip
+// and returns the next addend's sign nts; post() runs in the second.
+// Returns the next step's flag, the new a.s ^ nts.
 template <class F, class P>
 __device__ __forceinline__ uint32_t x32_add_step(const x32_tab &O, acc_ls &a, uint32_t tl, uint32_t ts, uint32_t u,
                                                  F &&shadow, P &&post) {
@@ -435,8 +444,8 @@ __device__ __forceinline__ uint32_t x32_add_step(const x32_tab &O, acc_ls &a, ui
     uint32_t a_lo, a_hi, a_ds;
     asm("v_lshl_add_u32 %0, %3, 2, %6\n\tv_lshl_add_u32 %1, %4, 3, %7\n\tv_lshl_add_u32 %2, %5, 4, %8"
         : "=&v"(a_lo), "=&v"(a_hi), "=&v"(a_ds)
-        : "v"(du & ((1u << k32_co_sh) - 1u)), "v"(__builtin_amdgcn_ubfe(du, k32_co_sh, k32_co_sh)), "v"(du >> 23),
-          "v"(O.dlo), "v"(O.dhi), "v"(O.desc));
+        : "v"(du & O.m0fff), "v"(__builtin_amdgcn_ubfe(du, k32_co_sh, k32_co_sh)), "v"(du >> 23), "v"(O.dlo),
+          "v"(O.dhi), "v"(O.desc));
     const int32_t lo = lds_ld(a_lo);
     const i32x2 hp = lds_ld2(a_hi);
     const u32x4 dsc = lds_ld4(a_ds);
@@ -453,7 +462,7 @@ __device__ __forceinline__ uint32_t x32_add_step(const x32_tab &O, acc_ls &a, ui
     // x: e (capped) on cotransformation lanes, du elsewhere (cap 0 there)
     const uint32_t xe = min((uint32_t)hp.x - (uint32_t)lo, dsc.z);
     const uint32_t x = bfi(dsc.w, xe, du);
-    const uint32_t hi = sign_mask(k32_sb_end - 1u - xe, O.one);   // e on sb's far grid
+    const uint32_t hi = sign_mask(O.ksb - xe, O.one);   // e on sb's far grid
     const uint32_t sh = bfi(hi, (uint32_t)k32_sb_fsh, dsc.y);
     const uint32_t node = lshl2_add(x >> sh, bfi(hi, O.sbf, dsc.x));
     const int32_t t0 = lds_ld(node), t1 = lds_ld(node + 4);
@@ -652,7 +661,7 @@ __device__ __forceinline__ red16<LNSHIP_SUM32> stage_tables<LNSHIP_SUM32>(const 
     int32_t *t = reinterpret_cast<int32_t *>(lds);
     // the image built at init (lds32_image): one copy, in one batch of loads
     // per thread at 256 threads
-    stage_copy<32>(reinterpret_cast<int4 *>(t), reinterpret_cast<const int4 *>(T.lds32), kl_desc / 4);
+    stage_copy<32>(reinterpret_cast<int4 *>(t + kl_dlo), reinterpret_cast<const int4 *>(T.lds32), (kl_end - kl_dlo) / 4);
     // descriptor of key = (opposite signs) << 8 | (d >> 23): (origin, grid
     // shift, cap of e, lane mask).  Direct keys read the interpolation at d:
     // the sb / db table of d's binade, or the zero pair with a shift that
@@ -874,6 +883,9 @@ __global__ __launch_bounds__(k_block * CG) void k_mm16(mm_args16 a, dev_tables T
     // (the product of the next step, its opposite-signs flag, and the
     // product pair of the next group's steps 0 and 1)
     uint32_t c_tl = 0, c_ts = 0, c_uf = 0, c_pl = 0, c_ps = 0;
+    // masks in registers (short encodings of the instructions that take them)
+    uint32_t k_lm = 0x7fff7fffu, k_sg = k32_sign, k_hi = 0xffff0000u;
+    asm("" : "+v"(k_lm), "+v"(k_sg), "+v"(k_hi));
     // steps [u0, u1) of a group; wn / xn: the next group's data.  fresh: the
     // chain's first group, or one whose carried state was not formed from it
     auto steps = [&](const uint4 &wq, const uint4 (&xq)[NC], const uint4 &wn, const uint4 (&xn)[NC], int u0, int u1,
@@ -888,19 +900,19 @@ __global__ __launch_bounds__(k_block * CG) void k_mm16(mm_args16 a, dev_tables T
             // the sign bits xor'ed.  Pair i + 1 is formed in step 2i's second
             // round trip, the next group's pair 0 in step 6's.
             uint32_t pl[4], ps[4];
-            auto pair = [](uint32_t w, uint32_t x, uint32_t &l, uint32_t &sg) {
-                const uint32_t lm = (w & 0x7fff7fffu) + (x & 0x7fff7fffu);
+            auto pair = [&](uint32_t w, uint32_t x, uint32_t &l, uint32_t &sg) {
+                const uint32_t lm = (w & k_lm) + (x & k_lm);
                 l = pk_min_u16(pk_sub_sat_u16(lm, 0x40004000u), 0x7fff7fffu);
                 sg = w ^ x;
             };
             // the product of step u (xlns32 positions) from its pair
-            auto half = [](int u, uint32_t l, uint32_t sg, uint32_t &tl, uint32_t &ts) {
+            auto half = [&](int u, uint32_t l, uint32_t sg, uint32_t &tl, uint32_t &ts) {
                 if ((u & 1) == 0) {
                     tl = l << 16;
-                    ts = (sg & k16_sign) << 16;
+                    ts = (sg << 16) & k_sg;
                 } else {
-                    tl = l & 0xffff0000u;
-                    ts = sg & k32_sign;
+                    tl = l & k_hi;
+                    ts = sg & k_sg;
                 }
             };
             // u0 is 0, or -1 for the chain's first group (its step 0 starts
@@ -2306,7 +2318,7 @@ const void *lnship_host_table(const char *name, size_t *bytes) {
     return nullptr;
 }
 
-// The LDS image of the xlns32 adder tables, up to the descriptors (which hold
+// The LDS image of the xlns32 adder tables after the descriptors (which hold
 // LDS addresses, so each workgroup forms them): dlo with the db-at-zero entry
 // replaced by a sentinel (exact cancellation clamps the log to 0); dhi as
 // pairs (th2, th), th2 = (dh << 12) + dhi[dh], the first half of the
@@ -2318,15 +2330,17 @@ const void *lnship_host_table(const char *name, size_t *bytes) {
 // interpolation tables sb, sbf, db, dbf as in the device block, and a zero
 // pair.
 static void lds32_image(const int32_t *tab, std::vector<int32_t> &img) {
-    img.assign(kl_desc, 0);
-    for (int i = 0; i < k32_co_n; i++) img[kl_dlo + i] = tab[k32_off_dlo + i];
-    img[kl_dlo] = -0x7fffffff;
+    // (word kl_dlo of the LDS copy is word 0 of the image)
+    img.assign(kl_end - kl_dlo, 0);
+    int32_t *w = img.data() - kl_dlo;
+    for (int i = 0; i < k32_co_n; i++) w[kl_dlo + i] = tab[k32_off_dlo + i];
+    w[kl_dlo] = -0x7fffffff;
     for (int i = 0; i < k32_co_n; i++) {
         const int32_t h = tab[k32_off_dhi + i];
-        img[kl_dhi + 2 * i] = i == 0 ? (int32_t)(13u << 23) : h + (i << k32_co_sh);
-        img[kl_dhi + 2 * i + 1] = i == 0 ? 0 : h;
+        w[kl_dhi + 2 * i] = i == 0 ? (int32_t)(13u << 23) : h + (i << k32_co_sh);
+        w[kl_dhi + 2 * i + 1] = i == 0 ? 0 : h;
     }
-    for (int i = k32_off_sb; i < k32_tab_n; i++) img[i + kl_shift] = tab[i];
+    for (int i = k32_off_sb; i < k32_tab_n; i++) w[i + kl_shift] = tab[i];
 }
 
 int lnship_init(void) {
