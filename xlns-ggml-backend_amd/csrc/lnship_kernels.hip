@@ -955,6 +955,32 @@ __global__ __launch_bounds__(k_block * CG) void k_mm16(mm_args16 a, dev_tables T
             }
             return;
         }
+        if constexpr (MODE == LNSHIP_SUM32) {
+            // several chains per lane: the products of steps 2i and 2i + 1 of
+            // a chain together, in the two 16-bit halves (as in the single
+            // chain above; the weights' masked logs shared by the chains)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                if (2 * i + 1 < u0 || 2 * i >= u1) continue;
+                const uint32_t wm = ww[i] & k_lm;
+#pragma unroll
+                for (int j = 0; j < NC; j++) {
+                    const uint32_t xv = i == 0 ? xq[j].x : i == 1 ? xq[j].y : i == 2 ? xq[j].z : xq[j].w;
+                    const uint32_t pl = pk_min_u16(pk_sub_sat_u16(wm + (xv & k_lm), 0x40004000u), 0x7fff7fffu);
+                    const uint32_t ps = ww[i] ^ xv;
+#pragma unroll
+                    for (int h = 0; h < 2; h++) {
+                        const int u = 2 * i + h;
+                        if (u < u0 || u >= u1) continue;
+                        const uint32_t tl = h == 0 ? pl << 16 : pl & k_hi;
+                        const uint32_t ts = h == 0 ? (ps << 16) & k_sg : ps & k_sg;
+                        if (u == 0 && u0 < 0) acc[j] = {tl, ts};
+                        else x32_add_ls(R.O, acc[j], tl, ts);
+                    }
+                }
+            }
+            return;
+        }
 #pragma unroll
         for (int u = 0; u < 8; u++) {
             if (u >= u0 && u < u1) {
