@@ -10,8 +10,9 @@
  *              restatement of the LNS16 backend (oracle/).  Against the
  *              reference's own printed outputs: base reproduces every one;
  *              sum32 every one except two figures of its xlns32_alt adder;
- *              monte and lpvip do not (their xlnscpp sources are absent and
- *              the restated adders are contradicted by the printed figures).
+ *              monte 13 of its 15 unit-test figures (its xlnscpp source is
+ *              absent; the restated dither is fitted to the printed
+ *              figures); lpvip none (its source is absent too).
  *   LNSHIP32 - xlns32, bit-exact against the restated LNS32 backend, whose
  *              xlns32_alt adder misses two of the reference's printed
  *              LNS32 figures.

@@ -75,6 +75,8 @@ void     lno16_rms_norm_row(int mode, const uint16_t *x, uint16_t *dst, size_t n
 void     lno16_softmax_row(int mode, const uint16_t *a, const uint16_t *mask, uint16_t *c, size_t n,
                            uint16_t scale, uint16_t *lfsr);
 uint16_t lno16_add_monte(uint16_t a, uint16_t b, uint16_t *lfsr);
+/* Monte dither threshold F(d) for d0 .. d0 + n - 1 (0 outside [1091, 1732)) */
+void lno16_monte_threshold_n(int d0, int n, int32_t *out);
 uint32_t lno16_lpvip_add(uint32_t acc, uint16_t t);
 void     lno32_lpvip_db_n(uint32_t d0, uint32_t n, int32_t *out);
 

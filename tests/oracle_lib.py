@@ -64,6 +64,7 @@ def lib():
         "lno16_rms_norm_row": (None, [ctypes.c_int, P, P, SZ, u16, P]),
         "lno16_softmax_row": (None, [ctypes.c_int, P, P, P, SZ, u16, P]),
         "lno16_add_monte": (u16, [u16, u16, P]),
+        "lno16_monte_threshold_n": (None, [ctypes.c_int, ctypes.c_int, P]),
         "lno16_lpvip_add": (u32, [u32, u16]),
         "lno32_lpvip_db_n": (None, [u32, u32, P]),
         "lno_lfsr_step": (u16, [u16]),

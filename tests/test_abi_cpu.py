@@ -69,6 +69,22 @@ def test_gauss16_tables_equal_oracle(lnship):
     assert np.all(g[1281:n] == 0) and np.all(g[n + 1281:] == 0)
 
 
+def test_monte_table_encodes_the_oracle_adder(lnship):
+    # (mag << 1) | draw per distance: the base magnitude x 64 below the
+    # dither range, the oracle's threshold F(d) from it on, 0 at the end
+    g = lnship.host_table("gauss16m", np.int32)
+    n = g.size // 2
+    sb, db = O.table("lno16_sb_table", 1281, np.int16), O.table("lno16_db_table", 1281, np.int16)
+    F = np.zeros(n, np.int32)
+    O.lib().lno16_monte_threshold_n(0, n, F.ctypes.data)
+    start = int(np.argmax(F > 0))
+    assert start == 1091 and F[n - 1] == 0 and F[n - 2] > 0
+    for tab, half in ((sb, g[:n]), (db, g[n:])):
+        assert np.all(half[:start] & 1 == 0) and np.all(half[start:] & 1 == 1)
+        assert np.array_equal(half[:start] >> 1, np.abs(tab[:start].astype(np.int32)) * 64)
+        assert np.array_equal(half[start:] >> 1, F[start:])
+
+
 def test_exp16_table_equals_oracle(lnship):
     assert np.array_equal(lnship.host_table("exp16", np.uint16), O.table("lno16_exp_table", 1 << 16, np.uint16))
 

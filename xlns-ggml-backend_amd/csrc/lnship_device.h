@@ -77,22 +77,9 @@ __device__ __forceinline__ uint32_t x16_add_g(const int16_t *g, uint32_t x, uint
     return (d == 0 && usedb) ? 0u : r;
 }
 
-// Monte addition: one LFSR step; the 256x Gaussian log is rounded by the low
-// 8 bits of the new state.
+// The Monte LFSR: one step per Monte addition (Galois, taps 0xB400).
 __device__ __forceinline__ uint32_t lfsr_step(uint32_t s) {
     return (s >> 1) ^ ((s & 1u) ? 0xB400u : 0u);
-}
-
-__device__ __forceinline__ uint32_t x16_add_monte(const int32_t *gm, uint32_t x, uint32_t y, uint32_t r) {
-    uint32_t xl = x & k16_logmask, yl = y & k16_logmask;
-    uint32_t maxl = max(xl, yl), d = maxl - min(xl, yl);
-    uint32_t sgn = (xl > yl ? x : y) & k16_sign;
-    uint32_t usedb = (x ^ y) & k16_sign;
-    int32_t f = gm[min(d, (uint32_t)k16_esszer + 1) + (usedb ? k16_gauss_n : 0)];
-    int32_t adj = (f + (int32_t)(r & 0xffu)) >> 8;
-    int32_t l = min(max((int32_t)maxl + adj, 0), (int32_t)k16_logmask);
-    uint32_t res = sgn | (uint32_t)l;
-    return (d == 0 && usedb) ? 0u : res;
 }
 
 // ---- xlns32 ------------------------------------------------------------

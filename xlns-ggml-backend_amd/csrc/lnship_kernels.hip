@@ -347,16 +347,21 @@ struct red16<LNSHIP_BASE> {
 
 template <>
 struct red16<LNSHIP_MONTE> {
-    const int32_t *gm;   // LDS: (sb, db) 256x int32 pairs per distance
+    const int32_t *gm;   // LDS: (sb, db) pairs per distance, (mag << 1) | draw
     using acc_t = acc_ls;
     __device__ __forceinline__ acc_t start(uint32_t v, uint32_t &) const { return {v & k16_logmask, v & k16_sign}; }
+    // One LFSR step; below the dither range the base table's adjustment, from
+    // it on one ulp toward the smaller operand with probability F(d)/64,
+    // decided by the top 6 bits of the new state.
     __device__ __forceinline__ void add_ls(acc_t &a, uint32_t tl, uint32_t ts, uint32_t &st) const {
         st = lfsr_step(st);
         const uint32_t d = absdiff(a.l, tl), mx = max(a.l, tl);
         const uint32_t usedb = a.s ^ ts;
         const int32_t *gms = gm + (usedb >> 15);
-        const int32_t f = gms[min(d, (uint32_t)k16_esszer + 1) << 1];
-        const int32_t adj = (f + (int32_t)(st & 0xffu)) >> 8;
+        const uint32_t e = (uint32_t)gms[min(d, (uint32_t)k16_mc_end) << 1];
+        const int32_t mag = (int32_t)(((e >> 1) + ((st >> 10) & (0u - (e & 1u)))) >> 6);
+        const int32_t neg = -(int32_t)(usedb >> 15);
+        const int32_t adj = (mag ^ neg) - neg;
         const uint32_t ns = a.l > tl ? a.s : ts;
         a.l = (uint32_t)min(max((int32_t)mx + adj, 0), (int32_t)k16_logmask);
         a.s = (d == 0 && usedb) ? 0u : ns;
@@ -650,9 +655,11 @@ __device__ __forceinline__ red16<LNSHIP_BASE> stage_tables<LNSHIP_BASE>(const de
 template <>
 __device__ __forceinline__ red16<LNSHIP_MONTE> stage_tables<LNSHIP_MONTE>(const dev_tables &T, char *lds) {
     int32_t *g = reinterpret_cast<int32_t *>(lds);
-    for (int i = threadIdx.x; i < k16_gauss_n; i += blockDim.x) {
+    // db at distance 0: a magnitude that clamps the log to 0 (exact
+    // cancellation; the sign is cleared by the caller)
+    for (int i = threadIdx.x; i < k16_mc_n; i += blockDim.x) {
         g[2 * i] = T.gauss16m[i];
-        g[2 * i + 1] = i == 0 ? -(1 << 24) : T.gauss16m[k16_gauss_n + i];
+        g[2 * i + 1] = i == 0 ? (1 << 25) : T.gauss16m[k16_mc_n + i];
     }
     return red16<LNSHIP_MONTE>{g};
 }
@@ -702,7 +709,7 @@ __device__ __forceinline__ red16<LNSHIP_LPVIP> stage_tables<LNSHIP_LPVIP>(const 
 template <int MODE>
 constexpr int lds_tables_bytes() {
     return MODE == LNSHIP_BASE ? 2 * k16_gauss_n * 2 :
-           MODE == LNSHIP_MONTE ? 2 * k16_gauss_n * 4 :
+           MODE == LNSHIP_MONTE ? 2 * k16_mc_n * 4 :
            MODE == LNSHIP_SUM32 ? k_lds_tab32 : 0;
 }
 
@@ -2380,7 +2387,7 @@ int lnship_init(void) {
     if (int rc = upload(g_host->cvt16, 1u << 17, &T.cvt16)) return rc;
     if (int rc = upload(g_host->rev16, 1u << 16, &T.rev16)) return rc;
     if (int rc = upload(g_host->gauss16, 2 * k16_gauss_n, &T.gauss16)) return rc;
-    if (int rc = upload(g_host->gauss16m, 2 * k16_gauss_n, &T.gauss16m)) return rc;
+    if (int rc = upload(g_host->gauss16m, 2 * k16_mc_n, &T.gauss16m)) return rc;
     if (int rc = upload(g_host->exp16, 1u << 16, &T.exp16)) return rc;
     if (int rc = upload(g_host->sig16, 1u << 16, &T.sig16)) return rc;
     if (int rc = upload(g_host->tab32, (size_t)k32_tab_n, &T.tab32)) return rc;

@@ -69,21 +69,31 @@ void build_host_tables(host_tables &t) {
     // xlns16_alt adjust at distance d: -d + (int)(log2(+-1 + 2^(d/128))*128 + .5)
     for (int d = 0; d < k16_gauss_n; d++) {
         int16_t sb = 0, db = 0;
-        int32_t sbm = 0, dbm = 0;
         if (d <= k16_esszer) {
             double vs = std::log(1.0 + std::pow(2.0, (double)d / 128.0)) / std::log(2.0) * 128.0 + 0.5;
             sb = (int16_t)(-d + to_s32(vs));
-            sbm = (int32_t)floorl(log2l(1.0L + exp2l(-(long double)d / 128.0L)) * 128.0L * 256.0L);
             if (d > 0) {
                 double vd = std::log(-1.0 + std::pow(2.0, (double)d / 128.0)) / std::log(2.0) * 128.0 + 0.5;
                 db = (int16_t)(-d + to_s32(vd));
-                dbm = (int32_t)floorl(log2l(1.0L - exp2l(-(long double)d / 128.0L)) * 128.0L * 256.0L);
             }
         }
         t.gauss16[d] = sb;
         t.gauss16[k16_gauss_n + d] = db;
+    }
+    // Monte: the base table's magnitude x 64 below k16_mc_start, then the
+    // draw threshold F(d); db at distance 0 is left to the caller (exact
+    // cancellation)
+    for (int d = 0; d < k16_mc_n; d++) {
+        int32_t sbm, dbm;
+        if (d < k16_mc_start) {
+            sbm = (int32_t)t.gauss16[d] * 64 * 2;
+            dbm = -(int32_t)t.gauss16[k16_gauss_n + d] * 64 * 2;
+        } else {
+            const int32_t f = d < k16_mc_end ? (int32_t)std::floor(std::exp2(-(double)d / 128.0) * 185.0 * 64.0) : 0;
+            sbm = dbm = f * 2 + 1;
+        }
         t.gauss16m[d] = sbm;
-        t.gauss16m[k16_gauss_n + d] = dbm;
+        t.gauss16m[k16_mc_n + d] = dbm;
     }
 
     for (uint32_t i = 0; i < (1u << 16); i++) t.exp16[i] = encode16(std::exp(t.rev16[i]));

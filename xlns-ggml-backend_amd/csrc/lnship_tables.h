@@ -11,6 +11,11 @@ namespace lnship {
 constexpr uint32_t k16_sign = 0x8000u, k16_logmask = 0x7fffu, k16_one = 0x4000u;
 constexpr int k16_esszer = 1280;          // addends further than this are dropped
 constexpr int k16_gauss_n = k16_esszer + 2;  // entries per Gaussian-log table
+// Monte addition: the base Gaussian log below k16_mc_start; from there a draw
+// of one ulp with probability F(d)/64, F(d) = floor(2^(-d/128) * 185 * 64),
+// which is 0 from k16_mc_end on
+constexpr int k16_mc_start = 1091, k16_mc_end = 1732;
+constexpr int k16_mc_n = k16_mc_end + 1;   // entries per Monte table
 
 // xlns32: sign bit 31, log field 2^23*log2|x| + 0x40000000.
 constexpr uint32_t k32_sign = 0x80000000u, k32_logmask = 0x7fffffffu, k32_one = 0x40000000u;
@@ -45,7 +50,11 @@ struct host_tables {
     uint16_t cvt16[1u << 17];   // float bits >> 15 -> xlns16
     float    rev16[1u << 16];   // xlns16 -> float
     int16_t  gauss16[2 * k16_gauss_n];   // [0]: sb, [1]: db at distance d; d = esszer + 1 -> 0
-    int32_t  gauss16m[2 * k16_gauss_n];  // the same, 256x, floored (Monte)
+    // Monte: [0]: sb, [1]: db at distance d < k16_mc_n, as (mag << 1) | draw:
+    // draw 0: |adjust| = mag >> 6 (mag = 64 |table|); draw 1: |adjust| =
+    // (mag + top 6 bits of the LFSR state) >> 6 (mag = F(d)); the sign is
+    // the table's (db <= 0)
+    int32_t  gauss16m[2 * k16_mc_n];
     uint16_t exp16[1u << 16];   // xlns16 -> xlns16 exp
     uint16_t sig16[1u << 16];   // xlns16 -> xlns16 sigmoid (silu = x * sigmoid)
     int32_t  tab32[k32_tab_n];  // xlns32 adder tables, layout above
