@@ -348,17 +348,39 @@ def cpu_baseline(cfg, weights, mode, n_tokens):
     m = O.MODES[mode]
     cpu = LlamaOracle16(cfg, weights, m)
     with _one_core() as core:
-        cpu.eval([1, 2])
+        ref = [cpu.eval([1, 2])]
         t0 = time.perf_counter()
         tok = 3
         for _ in range(n_tokens):
             logits = cpu.eval([tok])
+            ref.append(logits)
             tok = int(logits.argmax())
         dt = time.perf_counter() - t0
     return {"value": round(n_tokens / dt, 4), "unit": "tok/s", "cores": 1, "kind": "port",
             "sample": f"{n_tokens} decode tokens after a 2-token prompt, full SmolLM2-135M shape, "
                       f"{mode}, single-threaded C oracle pinned to core {core} ({dt:.1f} s)",
-            "cpu": _cpu_name(), "nproc": len(os.sched_getaffinity(0))}
+            "cpu": _cpu_name(), "nproc": len(os.sched_getaffinity(0))}, ref
+
+
+def logits_parity(model, ref, torch, np):
+    """The GPU model replays the CPU baseline's sample from position 0 (the
+    2-token prompt, then each decode token from a HIP graph) and compares
+    every logit with the oracle's, bit for bit."""
+    model.restart()
+    # the model returns its logits buffer: copy each step's before the next
+    got = [model.eval([1, 2]).clone()]
+    tok = 3
+    for _ in ref[1:]:
+        got.append(model.decode_graph(tok).clone())
+        tok = int(torch.argmax(got[-1]))
+    torch.cuda.synchronize()
+    differ = 0
+    for g, r in zip(got, ref):
+        g = np.ascontiguousarray(g.cpu().numpy(), np.float32).view(np.uint32)
+        differ += int(np.count_nonzero(g != np.ascontiguousarray(r, np.float32).view(np.uint32)))
+    return {"bit_exact": differ == 0, "logits": sum(int(r.size) for r in ref), "differ": differ,
+            "sample": "the cpu_baseline sample: logits of the 2-token prompt and of %d graph-replayed decode "
+                      "tokens, GPU against the CPU oracle" % (len(ref) - 1)}
 
 
 class _one_core:
@@ -500,7 +522,10 @@ def main():
         "setup_s": round(t_setup, 2),
     }
     if not args.no_cpu:
-        out["cpu_baseline"] = cpu_baseline(cfg, weights, args.mode, args.cpu_tokens)
+        out["cpu_baseline"], ref = cpu_baseline(cfg, weights, args.mode, args.cpu_tokens)
+        out["parity"] = logits_parity(model, ref, torch, np)
+        if not out["parity"]["bit_exact"]:
+            print("bench.py: GPU logits differ from the CPU oracle's", file=sys.stderr)
     print(json.dumps(out), flush=True)
 
 

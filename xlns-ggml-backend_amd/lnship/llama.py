@@ -159,6 +159,13 @@ class LlamaLNS16:
     def n_past(self, v):
         self.past[0] = v
 
+    def restart(self, lfsr=7):
+        """Empties every sequence's KV cache (positions restart at 0) and puts
+        the Monte LFSR back at lfsr; captured graphs stay valid."""
+        self.past = [0] * self.n_seq
+        self.lfsr = lfsr
+        self._lfsr_synced = False
+
     # -- buffers --------------------------------------------------------------
     def _buf(self, name, n, dtype=None):
         """A grow-only device buffer.  A captured HIP graph keeps the
