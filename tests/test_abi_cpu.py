@@ -70,19 +70,25 @@ def test_gauss16_tables_equal_oracle(lnship):
 
 
 def test_monte_table_encodes_the_oracle_adder(lnship):
-    # (mag << 1) | draw per distance: the base magnitude x 64 below the
-    # dither range, the oracle's threshold F(d) from it on, 0 at the end
-    g = lnship.host_table("gauss16m", np.int32)
-    n = g.size // 2
+    # (sb e, sb m, db e, db m) per distance: the base table x 64 and no draw
+    # below the dither range, then the oracle's threshold F(d) (0 at the end)
+    g = lnship.host_table("gauss16m", np.int32).reshape(-1, 4)
+    n = g.shape[0]
     sb, db = O.table("lno16_sb_table", 1281, np.int16), O.table("lno16_db_table", 1281, np.int16)
     F = np.zeros(n, np.int32)
     O.lib().lno16_monte_threshold_n(0, n, F.ctypes.data)
     start = int(np.argmax(F > 0))
     assert start == 1091 and F[n - 1] == 0 and F[n - 2] > 0
-    for tab, half in ((sb, g[:n]), (db, g[n:])):
-        assert np.all(half[:start] & 1 == 0) and np.all(half[start:] & 1 == 1)
-        assert np.array_equal(half[:start] >> 1, np.abs(tab[:start].astype(np.int32)) * 64)
-        assert np.array_equal(half[start:] >> 1, F[start:])
+    assert np.array_equal(g[:start, 0], sb[:start].astype(np.int32) * 64) and np.all(g[:start, 1] == 0)
+    assert np.array_equal(g[:start, 2], db[:start].astype(np.int32) * 64) and np.all(g[:start, 3] == 0)
+    assert np.array_equal(g[start:, 0], F[start:]) and np.all(g[start:, 1] == 63)
+    assert np.array_equal(g[start:, 2], 64 - F[start:]) and np.all(g[start:, 3] == -1)
+    # the draw of every entry against the oracle's rule, for every draw r
+    r = np.arange(64, dtype=np.int32)[:, None]
+    for e, m, sign in ((g[:, 0], g[:, 1], 1), (g[:, 2], g[:, 3], -1)):
+        adj = (e[None, :] + ((r ^ (m[None, :] >> 31)) & m[None, :])) >> 6
+        want = np.where(np.arange(n) < start, e[None, :] >> 6, sign * ((F[None, :] + r) >> 6))
+        assert np.array_equal(adj, want)
 
 
 def test_exp16_table_equals_oracle(lnship):

@@ -347,7 +347,7 @@ struct red16<LNSHIP_BASE> {
 
 template <>
 struct red16<LNSHIP_MONTE> {
-    const int32_t *gm;   // LDS: (sb, db) pairs per distance, (mag << 1) | draw
+    const int32_t *gm;   // LDS: (sb e, sb m, db e, db m) per distance
     using acc_t = acc_ls;
     __device__ __forceinline__ acc_t start(uint32_t v, uint32_t &) const { return {v & k16_logmask, v & k16_sign}; }
     // One LFSR step; below the dither range the base table's adjustment, from
@@ -357,11 +357,11 @@ struct red16<LNSHIP_MONTE> {
         st = lfsr_step(st);
         const uint32_t d = absdiff(a.l, tl), mx = max(a.l, tl);
         const uint32_t usedb = a.s ^ ts;
-        const int32_t *gms = gm + (usedb >> 15);
-        const uint32_t e = (uint32_t)gms[min(d, (uint32_t)k16_mc_end) << 1];
-        const int32_t mag = (int32_t)(((e >> 1) + ((st >> 10) & (0u - (e & 1u)))) >> 6);
-        const int32_t neg = -(int32_t)(usedb >> 15);
-        const int32_t adj = (mag ^ neg) - neg;
+        const int32_t *gms = gm + (usedb >> 14);
+        const int2 em = *reinterpret_cast<const int2 *>(gms + (min(d, (uint32_t)k16_mc_end) << 2));
+        // the draw: r for sb, -r - 1 for db, nothing below the dither range
+        const int32_t r = (int32_t)(st >> 10);
+        const int32_t adj = (em.x + ((r ^ (em.y >> 31)) & em.y)) >> 6;
         const uint32_t ns = a.l > tl ? a.s : ts;
         a.l = (uint32_t)min(max((int32_t)mx + adj, 0), (int32_t)k16_logmask);
         a.s = (d == 0 && usedb) ? 0u : ns;
@@ -655,12 +655,11 @@ __device__ __forceinline__ red16<LNSHIP_BASE> stage_tables<LNSHIP_BASE>(const de
 template <>
 __device__ __forceinline__ red16<LNSHIP_MONTE> stage_tables<LNSHIP_MONTE>(const dev_tables &T, char *lds) {
     int32_t *g = reinterpret_cast<int32_t *>(lds);
-    // db at distance 0: a magnitude that clamps the log to 0 (exact
-    // cancellation; the sign is cleared by the caller)
-    for (int i = threadIdx.x; i < k16_mc_n; i += blockDim.x) {
-        g[2 * i] = T.gauss16m[i];
-        g[2 * i + 1] = i == 0 ? (1 << 25) : T.gauss16m[k16_mc_n + i];
-    }
+    stage_copy<8>(reinterpret_cast<int4 *>(g), reinterpret_cast<const int4 *>(T.gauss16m), k16_mc_n);
+    // db at distance 0: an adjustment that clamps the log to 0 (exact
+    // cancellation; the sign is cleared by the caller).  Thread 0 copied
+    // that entry itself, so its own later store wins.
+    if (threadIdx.x == 0) g[2] = -(1 << 30);
     return red16<LNSHIP_MONTE>{g};
 }
 template <>
@@ -709,7 +708,7 @@ __device__ __forceinline__ red16<LNSHIP_LPVIP> stage_tables<LNSHIP_LPVIP>(const 
 template <int MODE>
 constexpr int lds_tables_bytes() {
     return MODE == LNSHIP_BASE ? 2 * k16_gauss_n * 2 :
-           MODE == LNSHIP_MONTE ? 2 * k16_mc_n * 4 :
+           MODE == LNSHIP_MONTE ? 4 * k16_mc_n * 4 :
            MODE == LNSHIP_SUM32 ? k_lds_tab32 : 0;
 }
 
@@ -2387,7 +2386,7 @@ int lnship_init(void) {
     if (int rc = upload(g_host->cvt16, 1u << 17, &T.cvt16)) return rc;
     if (int rc = upload(g_host->rev16, 1u << 16, &T.rev16)) return rc;
     if (int rc = upload(g_host->gauss16, 2 * k16_gauss_n, &T.gauss16)) return rc;
-    if (int rc = upload(g_host->gauss16m, 2 * k16_mc_n, &T.gauss16m)) return rc;
+    if (int rc = upload(g_host->gauss16m, 4 * k16_mc_n, &T.gauss16m)) return rc;
     if (int rc = upload(g_host->exp16, 1u << 16, &T.exp16)) return rc;
     if (int rc = upload(g_host->sig16, 1u << 16, &T.sig16)) return rc;
     if (int rc = upload(g_host->tab32, (size_t)k32_tab_n, &T.tab32)) return rc;

@@ -80,20 +80,22 @@ void build_host_tables(host_tables &t) {
         t.gauss16[d] = sb;
         t.gauss16[k16_gauss_n + d] = db;
     }
-    // Monte: the base table's magnitude x 64 below k16_mc_start, then the
-    // draw threshold F(d); db at distance 0 is left to the caller (exact
-    // cancellation)
+    // Monte (layout in lnship_tables.h); db at distance 0 is left to the
+    // caller (exact cancellation)
     for (int d = 0; d < k16_mc_n; d++) {
-        int32_t sbm, dbm;
+        int32_t *e = t.gauss16m + 4 * d;
         if (d < k16_mc_start) {
-            sbm = (int32_t)t.gauss16[d] * 64 * 2;
-            dbm = -(int32_t)t.gauss16[k16_gauss_n + d] * 64 * 2;
+            e[0] = (int32_t)t.gauss16[d] * 64;
+            e[1] = 0;
+            e[2] = (int32_t)t.gauss16[k16_gauss_n + d] * 64;
+            e[3] = 0;
         } else {
             const int32_t f = d < k16_mc_end ? (int32_t)std::floor(std::exp2(-(double)d / 128.0) * 185.0 * 64.0) : 0;
-            sbm = dbm = f * 2 + 1;
+            e[0] = f;
+            e[1] = 63;
+            e[2] = 64 - f;
+            e[3] = -1;
         }
-        t.gauss16m[d] = sbm;
-        t.gauss16m[k16_mc_n + d] = dbm;
     }
 
     for (uint32_t i = 0; i < (1u << 16); i++) t.exp16[i] = encode16(std::exp(t.rev16[i]));

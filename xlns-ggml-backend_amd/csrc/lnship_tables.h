@@ -50,11 +50,11 @@ struct host_tables {
     uint16_t cvt16[1u << 17];   // float bits >> 15 -> xlns16
     float    rev16[1u << 16];   // xlns16 -> float
     int16_t  gauss16[2 * k16_gauss_n];   // [0]: sb, [1]: db at distance d; d = esszer + 1 -> 0
-    // Monte: [0]: sb, [1]: db at distance d < k16_mc_n, as (mag << 1) | draw:
-    // draw 0: |adjust| = mag >> 6 (mag = 64 |table|); draw 1: |adjust| =
-    // (mag + top 6 bits of the LFSR state) >> 6 (mag = F(d)); the sign is
-    // the table's (db <= 0)
-    int32_t  gauss16m[2 * k16_mc_n];
+    // Monte, per distance d < k16_mc_n: (sb e, sb m, db e, db m); the
+    // adjustment is (e + ((r ^ (m >> 31)) & m)) >> 6 with r the top 6 bits of
+    // the new LFSR state: (64 table, 0) below the dither range, then sb
+    // (F(d), 63) = +((F + r) >> 6) and db (64 - F(d), -1) = -((F + r) >> 6)
+    int32_t  gauss16m[4 * k16_mc_n];
     uint16_t exp16[1u << 16];   // xlns16 -> xlns16 exp
     uint16_t sig16[1u << 16];   // xlns16 -> xlns16 sigmoid (silu = x * sigmoid)
     int32_t  tab32[k32_tab_n];  // xlns32 adder tables, layout above
