@@ -536,6 +536,11 @@ class LlamaLNS32:
         mm(self.tok_embd.data_ptr(), P(h), P(logits), e, c.n_vocab, 1)
         return logits[: c.n_vocab]
 
+    def restart(self):
+        """Empties the KV cache (positions restart at 0); captured graphs stay
+        valid."""
+        self.n_past = 0
+
     def eval(self, tokens):
         """Appends tokens (host list); returns the device logits of the last one."""
         torch = self.torch
