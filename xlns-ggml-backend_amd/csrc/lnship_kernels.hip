@@ -380,8 +380,9 @@ struct red16<LNSHIP_MONTE> {
 // tables), so all lanes share one.  T is the LDS copy of the adder tables
 // with changes made at staging: the db-at-zero entry holds a sentinel (exact
 // cancellation clamps the log to 0), dhi becomes pairs ((dh << 12) +
-// dhi[dh], dhi[dh]), a zero pair follows the tables, then the descriptors of
-// the interpolation (below).  Every select is arithmetic: a ternary around
+// dhi[dh], dhi[dh]) with the dl = 0 sentinel in place of dhi[0] (so that the
+// addend outside the interpolation is max(dhi, dlo)), a zero pair follows
+// the tables, then the descriptors of the interpolation (below).  Every select is arithmetic: a ternary around
 // two table reads would compile to a divergent branch that serialises both.
 
 // Byte offsets of the interpolation tables in the LDS copy, each less its
@@ -443,8 +444,8 @@ __device__ __forceinline__ uint32_t x32_add_step(const x32_tab &O, acc_ls &a, ui
     const uint32_t du = absdiff(a.l, tl, u);
     // the three addresses after the three indices, in one asm block so that
     // each shift-add waits on an index formed two instructions earlier: the
-    // reads of dlo[dl], of the dhi pair of dh ((dh << 12) + dhi[dh], dhi[dh]
-    // or 0 for dh = 0) and of the descriptor (origin, grid shift, cap of e,
+    // reads of dlo[dl], of the dhi pair of dh ((dh << 12) + dhi[dh], dhi[dh],
+    // or the sentinels for dh = 0) and of the descriptor (origin, grid shift, cap of e,
     // cotransformation lane mask) go out back to back
     uint32_t a_lo, a_hi, a_ds;
     asm("v_lshl_add_u32 %0, %3, 2, %6\n\tv_lshl_add_u32 %1, %4, 3, %7\n\tv_lshl_add_u32 %2, %5, 4, %8"
@@ -473,8 +474,8 @@ __device__ __forceinline__ uint32_t x32_add_step(const x32_tab &O, acc_ls &a, ui
     const int32_t t0 = lds_ld(node), t1 = lds_ld(node + 4);
     __builtin_amdgcn_sched_barrier(0);
     // the addend outside the interpolation: dlo[dl] where dh = 0, else dhi[dh]
-    // (cotransformation lanes only)
-    const int32_t A = (int32_t)(dsc.w & bfi(sign_mask((uint32_t)hp.y, O.one), (uint32_t)hp.y, (uint32_t)lo));
+    // (cotransformation lanes only), which is the larger of the two
+    const int32_t A = (int32_t)dsc.w & max(hp.y, lo);
     const int32_t mA = (int32_t)mx + A;
     const int32_t frac = (int32_t)__builtin_amdgcn_ubfe(x, 0, sh);
     post();
@@ -513,7 +514,7 @@ __device__ __forceinline__ void x32_add_ls(const x32_tab &O, acc_ls &a, uint32_t
     const uint32_t sh = bfi(hi, (uint32_t)k32_sb_fsh, dsc.y);
     const uint32_t node = lshl2_add(x >> sh, bfi(hi, O.sbf, dsc.x));
     const int32_t t0 = lds_ld(node), t1 = lds_ld(node + 4);
-    const int32_t A = (int32_t)(dsc.w & bfi(sign_mask((uint32_t)hp.y, O.one), (uint32_t)hp.y, (uint32_t)lo));
+    const int32_t A = (int32_t)dsc.w & max(hp.y, lo);
     const int32_t mA = (int32_t)mx + A;
     const int32_t frac = (int32_t)__builtin_amdgcn_ubfe(x, 0, sh);
     const int32_t ip = t0 + (__mul24(t1 - t0, frac) >> sh);
@@ -2370,7 +2371,10 @@ static void lds32_image(const int32_t *tab, std::vector<int32_t> &img) {
     for (int i = 0; i < k32_co_n; i++) {
         const int32_t h = tab[k32_off_dhi + i];
         w[kl_dhi + 2 * i] = i == 0 ? (int32_t)(13u << 23) : h + (i << k32_co_sh);
-        w[kl_dhi + 2 * i + 1] = i == 0 ? 0 : h;
+        // dh = 0: the dl = 0 sentinel, so that max(dhi, dlo) is dlo[dl]
+        // there, and dhi[dh] elsewhere (db rises with the distance, and
+        // dh << 12 > dl)
+        w[kl_dhi + 2 * i + 1] = i == 0 ? -0x7fffffff : h;
     }
     for (int i = k32_off_sb; i < k32_tab_n; i++) w[i + kl_shift] = tab[i];
 }
