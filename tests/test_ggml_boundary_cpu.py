@@ -310,6 +310,20 @@ def test_bad_sum_mode_aborts():
     assert r.returncode != 0 and "GGML_LNS16_SUM must be one of" in r.stderr
 
 
+def test_monte_bylpvip_refused():
+    # the reference's GGML_LNS16_MONTE_BYLPVIP build is not available: asking
+    # for it in a Monte run stops with a message instead of running pure16
+    e = dict(os.environ, GGML_LNS16_SUM="monte", GGML_LNS16_MONTE_BYLPVIP="ON")
+    r = subprocess.run([sys.executable, "-c", PRELUDE + "h.reg()"], env=e, capture_output=True, text=True,
+                       timeout=120)
+    assert r.returncode != 0 and "monte=bylpvip is not available" in r.stderr
+    for off in ("OFF", "0"):
+        e = dict(os.environ, GGML_LNS16_SUM="monte", GGML_LNS16_MONTE_BYLPVIP=off)
+        r = subprocess.run([sys.executable, "-c", PRELUDE + "h.reg()"], env=e, capture_output=True, text=True,
+                           timeout=120)
+        assert r.returncode == 0, r.stderr[-500:]
+
+
 def test_data_movement_claimed_for_hbm_destinations():
     # with the HBM buffer type, CPY / CONT / GET_ROWS / SET_ROWS whose
     # destination is not allocated yet (the scheduler places it in this

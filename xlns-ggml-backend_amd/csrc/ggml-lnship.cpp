@@ -214,6 +214,17 @@ static int sum_mode() {
         if (!std::strcmp(v, "sum32")) return (int)LNSHIP_SUM32;
         die("GGML_LNS16_SUM must be one of base, monte, lpvip, sum32 (got '%s')", v);
     }();
+    // GGML_LNS16_MONTE_BYLPVIP (the reference's second Monte build,
+    // src/lns-ops.cpp:86-98): its library source, xlns16monte_bylpvip.cpp, is
+    // not available, so a Monte run that asks for it stops here rather than
+    // running the other Monte adder under its name
+    static const bool checked = []() {
+        const char *b = std::getenv("GGML_LNS16_MONTE_BYLPVIP");
+        if (mode == LNSHIP_MONTE && b && b[0] && std::strcmp(b, "0") && strcasecmp(b, "OFF") && strcasecmp(b, "false"))
+            die("GGML_LNS16_MONTE_BYLPVIP=%s: monte=bylpvip is not available in this backend (only monte=pure16)", b);
+        return true;
+    }();
+    (void)checked;
     return mode;
 }
 
