@@ -129,11 +129,13 @@ __device__ __forceinline__ uint32_t x32_add(const int32_t *T, uint32_t x, uint32
     return sgn | l;
 }
 
+// The product's log is the sum of the logs less the offset, clamped to the
+// field: an underflow gives log 0 (zero), an overflow the largest log.  The
+// sum of two 31-bit logs fits 32 bits, so one unsigned median does both
+// clamps before the offset comes off.
 __device__ __forceinline__ uint32_t x32_mul(uint32_t x, uint32_t y) {
-    uint32_t t = (x & k32_logmask) + (y & k32_logmask) - k32_one;
-    uint32_t s = (x ^ y) & k32_sign;
-    if (t & k32_sign) return (t & k32_one) ? s : (s | k32_logmask);
-    return s | t;
+    const uint32_t l = min(max((x & k32_logmask) + (y & k32_logmask), k32_one), k32_one + k32_logmask);
+    return ((x ^ y) & k32_sign) | (l - k32_one);
 }
 
 __device__ __forceinline__ uint32_t x32_div(uint32_t x, uint32_t y) {
