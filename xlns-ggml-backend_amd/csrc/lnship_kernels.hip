@@ -529,7 +529,9 @@ __device__ __forceinline__ void x32_add_ls(const x32_tab &O, acc_ls &a, uint32_t
 // far grid's last node and the interpolation read 0.  The result needs no
 // clamp at 0 (sb >= 0); it saturates on overflow as the general addition.
 __device__ __forceinline__ uint32_t x32_add_pos(const x32_tab &O, uint32_t al, uint32_t tl) {
-    const uint32_t xd = min(absdiff(al, tl, O.nil), k32_esszer);
+    // (the explicit v_sad_u32: from max - min + 0 the compiler makes four
+    // instructions here, all on the chain)
+    const uint32_t xd = min(absdiff(al, tl), k32_esszer);
     const uint32_t hi = sign_mask(k32_sb_end - 1u - xd, O.one);   // d on the far grid
     const uint32_t sh = bfi(hi, (uint32_t)k32_sb_fsh, (uint32_t)k32_sb_sh);
     const uint32_t node = lshl2_add(xd >> sh, bfi(hi, O.sbf, O.sb));
