@@ -399,7 +399,7 @@ constexpr uint32_t kb_dbf = (uint32_t)(k32_off_dbf + kl_shift - (int)(k32_db_end
 // registers, so that picking a table is one select and no base add follows.
 struct x32_tab {
     uint32_t dlo, dhi, sb, sbf, db, dbf, zero, desc;
-    uint32_t one, nil;   // 1 and 0 in registers the compiler cannot see into
+    uint32_t one;   // 1 in a register the compiler cannot see into
     // a mask and a bound in registers: two-operand instructions take them in
     // their short encoding (a literal operand makes an instruction 8 bytes)
     uint32_t m0fff, ksb;
@@ -408,10 +408,10 @@ __device__ __forceinline__ x32_tab x32_origins(const int32_t *T) {
     uint32_t tb = lds_addr(T);
     asm("" : "+v"(tb));
     x32_tab o{tb + (uint32_t)kl_dlo * 4, tb + (uint32_t)kl_dhi * 4, tb + kb_sb, tb + kb_sbf, tb + kb_db,
-              tb + kb_dbf, tb + (uint32_t)kl_zero * 4, tb + (uint32_t)kl_desc * 4, 1u, 0u, 0xfffu, k32_sb_end - 1u};
+              tb + kb_dbf, tb + (uint32_t)kl_zero * 4, tb + (uint32_t)kl_desc * 4, 1u, 0xfffu, k32_sb_end - 1u};
     // each origin its own register: a select among them stays a select (not
     // a lookup table of their constant offsets)
-    asm("" : "+v"(o.sb), "+v"(o.sbf), "+v"(o.db), "+v"(o.dbf), "+v"(o.zero), "+v"(o.one), "+v"(o.nil));
+    asm("" : "+v"(o.sb), "+v"(o.sbf), "+v"(o.db), "+v"(o.dbf), "+v"(o.zero), "+v"(o.one));
     asm("" : "+v"(o.m0fff), "+v"(o.ksb));
     return o;
 }
