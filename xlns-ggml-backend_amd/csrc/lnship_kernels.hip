@@ -748,6 +748,9 @@ struct mm_args16 {
     int64_t ids_t, x_bcast, n_w;
     unsigned long long *err;
     const float *resid;   // non-null: dst = resid + W x (the graph's ADD), resid laid out as dst
+    // set by the launcher: the grid is 2^xcd_sh times wider than the work;
+    // workgroup x works (as block x >> xcd_sh) iff x is a multiple of 2^xcd_sh
+    uint32_t xcd_sh;
 };
 
 // Records an index out of range: err[0] = 1, err[1] = the first such index.
@@ -790,6 +793,8 @@ __device__ __forceinline__ uint32_t half16(uint32_t w, int hi) { return hi ? (w 
 template <int MODE, int NC, int PF, bool XL, int CG>
 __global__ __launch_bounds__(k_block * CG) void k_mm16(mm_args16 a, dev_tables T) {
     extern __shared__ __align__(16) char lds[];
+    // a widened launch: the workgroups between the working ones leave at once
+    if (blockIdx.x & ((1u << a.xcd_sh) - 1u)) return;
     const red16<MODE> R = stage_tables<MODE>(T, lds);
     // CG column groups of k_block lanes each share the staged tables: group
     // c takes columns [nw + c NC, nw + (c + 1) NC) of the same k_block rows
@@ -840,7 +845,7 @@ __global__ __launch_bounds__(k_block * CG) void k_mm16(mm_args16 a, dev_tables T
     }
     __syncthreads();
 
-    const int64_t m = (int64_t)blockIdx.x * k_block + (threadIdx.x % k_block);
+    const int64_t m = (int64_t)(blockIdx.x >> a.xcd_sh) * k_block + (threadIdx.x % k_block);
     if (m >= a.M || nc == 0 || !slice_ok) return;
     const uint16_t *ws = a.w + zw * a.w_slice + m * 8;
     const uint16_t *xs = a.x + (zx * a.N + n0) * a.kp;
@@ -1092,6 +1097,7 @@ struct mm_args32 {
     int64_t ids_t, x_bcast, n_w;
     unsigned long long *err;
     const float *resid;   // as in mm_args16
+    uint32_t xcd_sh;      // as in mm_args16
 };
 
 // One lane per weight row m and NC columns, CG column groups per workgroup
@@ -1101,10 +1107,11 @@ struct mm_args32 {
 template <int NC, int PF, int CG>
 __global__ __launch_bounds__(k_block * CG) void k_mm32(mm_args32 a, dev_tables T) {
     extern __shared__ __align__(16) char lds[];
+    if (blockIdx.x & ((1u << a.xcd_sh) - 1u)) return;   // as in k_mm16
     const red16<LNSHIP_SUM32> R = stage_tables<LNSHIP_SUM32>(T, lds);
     __syncthreads();
     const int cg = CG == 1 ? 0 : (int)(threadIdx.x / k_block);
-    const int64_t m = (int64_t)blockIdx.x * k_block + (threadIdx.x % k_block);
+    const int64_t m = (int64_t)(blockIdx.x >> a.xcd_sh) * k_block + (threadIdx.x % k_block);
     const int64_t n0 = ((int64_t)blockIdx.y * CG + cg) * NC;
     if (m >= a.M || n0 >= a.N) return;
     const int64_t z = blockIdx.z;
@@ -2097,6 +2104,21 @@ static mm16_shape mm_shape_x32(int64_t M, int64_t N, int64_t nslices, int64_t kp
     return best;
 }
 
+// Workgroups of a launch are dealt round-robin to the XCDs (eight on MI355X,
+// each with its own L2).  A sum32 GEMV workgroup first stages the 130 KB
+// xlns32 image into LDS (one workgroup per CU at that size); in a launch of
+// few workgroups each lands on another XCD and misses the image in that
+// XCD's L2.  Launched 2^sh times wider, with only the workgroups whose index
+// is a multiple of 2^sh working, the working ones fall on 8 >> sh XCDs and
+// share those L2s' copies.  sh is the largest (at most 3) for which those
+// XCDs still hold every working workgroup at one per CU.
+static uint32_t xcd_shift(uint64_t wgs, int cus) {
+    const uint64_t per_xcd = (uint64_t)std::max(cus / 8, 1);
+    uint32_t sh = 3;
+    while (sh > 0 && wgs > (per_xcd << (3 - sh))) sh--;
+    return sh;
+}
+
 static mm16_shape mm16_choose(int mode, int64_t M, int64_t N, int64_t nslices, int64_t kp, int cus) {
     if (mode == LNSHIP_SUM32) return mm_shape_x32(M, N, nslices, kp, cus, 8);
     const int nc = mm16_nc(mode, M, N, nslices, kp, cus);
@@ -2104,7 +2126,7 @@ static mm16_shape mm16_choose(int mode, int64_t M, int64_t N, int64_t nslices, i
 }
 
 template <int MODE, int NC, bool XL, int CG>
-static int launch_mm16(const mm_args16 &m, const dev_tables &T, int64_t nslices, hipStream_t st) {
+static int launch_mm16(const mm_args16 &m, const dev_tables &T, int64_t nslices, int cus, hipStream_t st) {
     // prefetch depth within 128 VGPRs at four waves per SIMD
     constexpr int PF = NC == 1 ? (CG >= 4 ? 4 : 8) : NC == 2 ? 2 : (NC == 4 && CG < 4) ? 2 : 1;
     const int lds = mm_xl_offset<MODE>() + (XL ? (int)(NC * CG * m.kp * 2) + k_xl_pad : 0);
@@ -2116,47 +2138,53 @@ static int launch_mm16(const mm_args16 &m, const dev_tables &T, int64_t nslices,
         if (int rc = set_lds(k_mm16<MODE, NC, PF, XL, CG>, lds)) return rc;
     dim3 grid((unsigned)((m.M + k_block - 1) / k_block), (unsigned)((m.N + NC * CG - 1) / (NC * CG)), (unsigned)nslices);
     if (grid.x > 2147483647u || grid.y > 65535u) return fail(LNSHIP_ERANGE, "mul_mat: grid too large%s");
-    hipLaunchKernelGGL((k_mm16<MODE, NC, PF, XL, CG>), grid, dim3(k_block * CG), lds, st, m, T);
+    mm_args16 mx = m;
+    mx.xcd_sh = MODE == LNSHIP_SUM32 ? xcd_shift((uint64_t)grid.x * grid.y * grid.z, cus) : 0;
+    grid.x <<= mx.xcd_sh;
+    hipLaunchKernelGGL((k_mm16<MODE, NC, PF, XL, CG>), grid, dim3(k_block * CG), lds, st, mx, T);
     LNSHIP_HIP(hipGetLastError());
     return 0;
 }
 
 template <int MODE, int NC, int CG>
-static int launch_mm16_x(const mm_args16 &m, const dev_tables &T, int64_t nslices, bool xl, hipStream_t st) {
-    return xl ? launch_mm16<MODE, NC, true, CG>(m, T, nslices, st) : launch_mm16<MODE, NC, false, CG>(m, T, nslices, st);
+static int launch_mm16_x(const mm_args16 &m, const dev_tables &T, int64_t nslices, bool xl, int cus, hipStream_t st) {
+    return xl ? launch_mm16<MODE, NC, true, CG>(m, T, nslices, cus, st) : launch_mm16<MODE, NC, false, CG>(m, T, nslices, cus, st);
 }
 
 template <int MODE>
 static int dispatch_mm16(const mm_args16 &m, const dev_tables &T, int64_t nslices, const mm16_shape &sh,
-                         hipStream_t st) {
+                         int cus, hipStream_t st) {
     if constexpr (MODE == LNSHIP_SUM32) {
         // column groups: more waves per SIMD where the tables allow one
         // workgroup per CU
         switch (sh.nc * 10 + sh.cg) {
-            case 12: return launch_mm16_x<MODE, 1, 2>(m, T, nslices, sh.xl, st);
-            case 14: return launch_mm16_x<MODE, 1, 4>(m, T, nslices, sh.xl, st);
-            case 24: return launch_mm16_x<MODE, 2, 4>(m, T, nslices, sh.xl, st);
-            case 44: return launch_mm16_x<MODE, 4, 4>(m, T, nslices, sh.xl, st);
-            case 84: return launch_mm16_x<MODE, 8, 4>(m, T, nslices, sh.xl, st);
-            default: return launch_mm16_x<MODE, 1, 1>(m, T, nslices, sh.xl, st);
+            case 12: return launch_mm16_x<MODE, 1, 2>(m, T, nslices, sh.xl, cus, st);
+            case 14: return launch_mm16_x<MODE, 1, 4>(m, T, nslices, sh.xl, cus, st);
+            case 24: return launch_mm16_x<MODE, 2, 4>(m, T, nslices, sh.xl, cus, st);
+            case 44: return launch_mm16_x<MODE, 4, 4>(m, T, nslices, sh.xl, cus, st);
+            case 84: return launch_mm16_x<MODE, 8, 4>(m, T, nslices, sh.xl, cus, st);
+            default: return launch_mm16_x<MODE, 1, 1>(m, T, nslices, sh.xl, cus, st);
         }
     } else {
         switch (sh.nc) {
-            case 8: return launch_mm16_x<MODE, 8, 1>(m, T, nslices, sh.xl, st);
-            case 4: return launch_mm16_x<MODE, 4, 1>(m, T, nslices, sh.xl, st);
-            default: return launch_mm16_x<MODE, 1, 1>(m, T, nslices, sh.xl, st);
+            case 8: return launch_mm16_x<MODE, 8, 1>(m, T, nslices, sh.xl, cus, st);
+            case 4: return launch_mm16_x<MODE, 4, 1>(m, T, nslices, sh.xl, cus, st);
+            default: return launch_mm16_x<MODE, 1, 1>(m, T, nslices, sh.xl, cus, st);
         }
     }
 }
 
 template <int NC, int CG>
-static int launch_mm32(const mm_args32 &m, const dev_tables &T, int64_t nslices, hipStream_t st) {
+static int launch_mm32(const mm_args32 &m, const dev_tables &T, int64_t nslices, int cus, hipStream_t st) {
     // prefetch depth within 128 VGPRs at four waves per SIMD
     constexpr int PF = NC == 1 ? (CG >= 4 ? 2 : 4) : 1;
     if (int rc = set_lds(k_mm32<NC, PF, CG>, k_lds_tab32)) return rc;
     dim3 grid((unsigned)((m.M + k_block - 1) / k_block), (unsigned)((m.N + NC * CG - 1) / (NC * CG)), (unsigned)nslices);
     if (grid.x > 2147483647u || grid.y > 65535u) return fail(LNSHIP_ERANGE, "mul_mat: grid too large%s");
-    hipLaunchKernelGGL((k_mm32<NC, PF, CG>), grid, dim3(k_block * CG), k_lds_tab32, st, m, T);
+    mm_args32 mx = m;
+    mx.xcd_sh = xcd_shift((uint64_t)grid.x * grid.y * grid.z, cus);
+    grid.x <<= mx.xcd_sh;
+    hipLaunchKernelGGL((k_mm32<NC, PF, CG>), grid, dim3(k_block * CG), k_lds_tab32, st, mx, T);
     LNSHIP_HIP(hipGetLastError());
     return 0;
 }
@@ -2576,10 +2604,10 @@ int lnship16_mul_mat(int mode, const lnship_mul_mat_args *a, void *stream) {
                 a->monte_seed, a->monte_state, a->monte_offset};
     m.resid = a->residual;
     switch (mode) {
-        case LNSHIP_BASE: return dispatch_mm16<LNSHIP_BASE>(m, s->T, nslices, sh, st);
-        case LNSHIP_MONTE: return dispatch_mm16<LNSHIP_MONTE>(m, s->T, nslices, sh, st);
-        case LNSHIP_LPVIP: return dispatch_mm16<LNSHIP_LPVIP>(m, s->T, nslices, sh, st);
-        default: return dispatch_mm16<LNSHIP_SUM32>(m, s->T, nslices, sh, st);
+        case LNSHIP_BASE: return dispatch_mm16<LNSHIP_BASE>(m, s->T, nslices, sh, s->cus, st);
+        case LNSHIP_MONTE: return dispatch_mm16<LNSHIP_MONTE>(m, s->T, nslices, sh, s->cus, st);
+        case LNSHIP_LPVIP: return dispatch_mm16<LNSHIP_LPVIP>(m, s->T, nslices, sh, s->cus, st);
+        default: return dispatch_mm16<LNSHIP_SUM32>(m, s->T, nslices, sh, s->cus, st);
     }
 }
 
@@ -2605,11 +2633,11 @@ static int mul_mat32_staged(device_state *s, const lnship_mul_mat_args *a, void 
     m.resid = a->residual;
     const mm16_shape sh = mm_shape_x32(m.M, m.N, nslices, kp, s->cus, 4);
     switch (sh.nc * 10 + sh.cg) {
-        case 12: return launch_mm32<1, 2>(m, s->T, nslices, st);
-        case 14: return launch_mm32<1, 4>(m, s->T, nslices, st);
-        case 24: return launch_mm32<2, 4>(m, s->T, nslices, st);
-        case 44: return launch_mm32<4, 4>(m, s->T, nslices, st);
-        default: return launch_mm32<1, 1>(m, s->T, nslices, st);
+        case 12: return launch_mm32<1, 2>(m, s->T, nslices, s->cus, st);
+        case 14: return launch_mm32<1, 4>(m, s->T, nslices, s->cus, st);
+        case 24: return launch_mm32<2, 4>(m, s->T, nslices, s->cus, st);
+        case 44: return launch_mm32<4, 4>(m, s->T, nslices, s->cus, st);
+        default: return launch_mm32<1, 1>(m, s->T, nslices, s->cus, st);
     }
 }
 
@@ -2677,10 +2705,10 @@ int lnship16_mul_mat_id(int mode, const lnship_mul_mat_id_args *a, void *stream)
                 a->monte_seed, a->monte_state, a->monte_offset,
                 a->ids, a->ids_ld ? a->ids_ld : a->n_expert_used, a->ne11, a->n_expert, s->index_err};
     switch (mode) {
-        case LNSHIP_BASE: return dispatch_mm16<LNSHIP_BASE>(m, s->T, nslices, sh, st);
-        case LNSHIP_MONTE: return dispatch_mm16<LNSHIP_MONTE>(m, s->T, nslices, sh, st);
-        case LNSHIP_LPVIP: return dispatch_mm16<LNSHIP_LPVIP>(m, s->T, nslices, sh, st);
-        default: return dispatch_mm16<LNSHIP_SUM32>(m, s->T, nslices, sh, st);
+        case LNSHIP_BASE: return dispatch_mm16<LNSHIP_BASE>(m, s->T, nslices, sh, s->cus, st);
+        case LNSHIP_MONTE: return dispatch_mm16<LNSHIP_MONTE>(m, s->T, nslices, sh, s->cus, st);
+        case LNSHIP_LPVIP: return dispatch_mm16<LNSHIP_LPVIP>(m, s->T, nslices, sh, s->cus, st);
+        default: return dispatch_mm16<LNSHIP_SUM32>(m, s->T, nslices, sh, s->cus, st);
     }
 }
 
@@ -2705,9 +2733,9 @@ int lnship32_mul_mat_id(const lnship_mul_mat_id_args *a, void *stream) {
                 a->ids, a->ids_ld ? a->ids_ld : a->n_expert_used, a->ne11, a->n_expert, s->index_err};
     const mm16_shape sh = mm_shape_x32(m.M, 1, nslices, kp, s->cus, 4);
     switch (sh.nc * 10 + sh.cg) {
-        case 12: return launch_mm32<1, 2>(m, s->T, nslices, st);
-        case 14: return launch_mm32<1, 4>(m, s->T, nslices, st);
-        default: return launch_mm32<1, 1>(m, s->T, nslices, st);
+        case 12: return launch_mm32<1, 2>(m, s->T, nslices, s->cus, st);
+        case 14: return launch_mm32<1, 4>(m, s->T, nslices, s->cus, st);
+        default: return launch_mm32<1, 1>(m, s->T, nslices, s->cus, st);
     }
 }
 
