@@ -267,6 +267,16 @@ __device__ __forceinline__ uint32_t pk_sub_sat_u16(uint32_t a, uint32_t b) {
 __device__ __forceinline__ uint32_t pk_min_u16(uint32_t a, uint32_t b) {
     return __builtin_bit_cast(uint32_t, __builtin_elementwise_min(__builtin_bit_cast(u16x2, a), __builtin_bit_cast(u16x2, b)));
 }
+// Both halves: a - b wrapping (v_pk_sub_u16); and a + b with signed
+// saturation, then at least 0 (v_pk_add_i16 with clamp, v_pk_max_i16).
+typedef short i16x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t pk_sub_u16(uint32_t a, uint32_t b) {
+    return __builtin_bit_cast(uint32_t, __builtin_bit_cast(u16x2, a) - __builtin_bit_cast(u16x2, b));
+}
+__device__ __forceinline__ uint32_t pk_add_sat_nonneg_i16(uint32_t a, uint32_t b) {
+    const i16x2 s = __builtin_elementwise_add_sat(__builtin_bit_cast(i16x2, a), __builtin_bit_cast(i16x2, b));
+    return __builtin_bit_cast(uint32_t, __builtin_elementwise_max(s, i16x2{0, 0}));
+}
 
 // Shift-adds in plain code select to one v_lshl_add_u32 each.  The lds_at
 // forms are the same instruction in inline asm, used where an LDS read is
@@ -510,9 +520,9 @@ __device__ __forceinline__ void x32_add_ls(const x32_tab &O, acc_ls &a, uint32_t
     const uint32_t nsign = bfi(tl - a.l, a.s, ts) & (~u | (du - 1u));
     const uint32_t xe = min((uint32_t)hp.x - (uint32_t)lo, dsc.z);
     const uint32_t x = bfi(dsc.w, xe, du);
-    const uint32_t hi = sign_mask(k32_sb_end - 1u - xe, O.one);
-    const uint32_t sh = bfi(hi, (uint32_t)k32_sb_fsh, dsc.y);
-    const uint32_t node = lshl2_add(x >> sh, bfi(hi, O.sbf, dsc.x));
+    const bool far = xe > k32_sb_end - 1u;
+    const uint32_t sh = far ? (uint32_t)k32_sb_fsh : dsc.y;
+    const uint32_t node = lshl2_add(x >> sh, far ? O.sbf : dsc.x);
     const int32_t t0 = lds_ld(node), t1 = lds_ld(node + 4);
     const int32_t A = (int32_t)dsc.w & max(hp.y, lo);
     const int32_t mA = (int32_t)mx + A;
@@ -972,15 +982,18 @@ __global__ __launch_bounds__(k_block * CG) void k_mm16(mm_args16 a, dev_tables T
         if constexpr (MODE == LNSHIP_SUM32) {
             // several chains per lane: the products of steps 2i and 2i + 1 of
             // a chain together, in the two 16-bit halves (as in the single
-            // chain above; the weights' masked logs shared by the chains)
+            // chain above).  The weights' logs, shared by the chains, less the
+            // offset once (wl - 0x4000 in [-0x4000, 0x3fff] as int16); then
+            // per chain wl - 0x4000 + xl, saturated at 0x7fff by the signed
+            // add and at 0 by the maximum: the clamped product log
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 if (2 * i + 1 < u0 || 2 * i >= u1) continue;
-                const uint32_t wm = ww[i] & k_lm;
+                const uint32_t wb = pk_sub_u16(ww[i] & k_lm, 0x40004000u);
 #pragma unroll
                 for (int j = 0; j < NC; j++) {
                     const uint32_t xv = i == 0 ? xq[j].x : i == 1 ? xq[j].y : i == 2 ? xq[j].z : xq[j].w;
-                    const uint32_t pl = pk_min_u16(pk_sub_sat_u16(wm + (xv & k_lm), 0x40004000u), 0x7fff7fffu);
+                    const uint32_t pl = pk_add_sat_nonneg_i16(wb, xv & k_lm);
                     const uint32_t ps = ww[i] ^ xv;
 #pragma unroll
                     for (int h = 0; h < 2; h++) {
