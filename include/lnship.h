@@ -291,6 +291,15 @@ int lnship_index_error(int64_t *bad_index, void *stream);
  * No counterpart in the reference. */
 int lnship_lpvip_db_range(uint32_t d0, uint32_t n, int32_t *out, void *stream);
 
+/* Test hook: out[i] = x[i] + y[i] (xlns32 codes, sign bit 31) by the xlns32
+ * adder over its LDS tables, as the sum32 and LNS32 kernels run it: form 0
+ * the multi-chain step (prefill GEMMs, soft_max, rms_norm's epsilon), 1 the
+ * single-chain step of the decode GEMVs, 2 the positive-sum step of
+ * rms_norm / soft_max (sign bits ignored).  The arithmetic is xlns32_add as
+ * src/lns16-sum32.h:59-198 configures xlnscpp (xlns32_alt).  No counterpart
+ * in the reference. */
+int lnship32_add_lds(int form, const uint32_t *x, const uint32_t *y, uint32_t *out, int64_t n, void *stream);
+
 /* Host: the (cos, sin) floats lns_rope uses for positions 0..n_pos-1 (the
  * float recurrence t *= powf(freq_base, -2/n_dims) per pair, cosf / sinf;
  * src/lns-ops.cpp:1225-1247, cuda/lns-cuda-ops.cpp:223-240), laid out as

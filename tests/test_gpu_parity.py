@@ -59,6 +59,61 @@ def test_to_f32_16_every_code(ln):
     same_bits(got, O.x2f16(codes), "xlns16 -> f32")
 
 
+def _x32_add_cases(rng):
+    """xlns32 code pairs (x, y) over the adder's cases: every cotransformation
+    split d = (dh << 12) + dl with dl in {0, 1, 2, 4095, random} for each dh
+    and dh in {0, 1, 4095, random} for each dl, distances out to 30 binades,
+    d = 0, and logs at both ends of the field (clamp at 0, saturation)."""
+    B = 1 << 23
+    d = []
+    dh = np.arange(4096, dtype=np.int64)
+    for dl in (0, 1, 2, 4095, None):
+        d.append((dh << 12) + (rng.integers(0, 4096, 4096) if dl is None else dl))
+    dl = np.arange(4096, dtype=np.int64)
+    for h in (0, 1, 4095, None):
+        d.append(((rng.integers(0, 4096, 4096) if h is None else h) << 12) + dl)
+    d.append(rng.integers(1 << 24, 30 * B, 8192))
+    d.append(np.zeros(256, np.int64))
+    d = np.concatenate(d)
+    a = rng.integers(32 * B, (1 << 31) - 32 * B, d.size)
+    b = np.where(rng.integers(0, 2, d.size) == 1, a + d, a - d)
+    # half the pairs with opposite signs (the db and cotransformation cases)
+    sa = rng.integers(0, 2, d.size).astype(np.int64)
+    sb = np.where(np.arange(d.size) % 2 == 0, 1 - sa, rng.integers(0, 2, d.size))
+    # the ends: tiny logs that cancel below 0, large ones that overflow
+    lo = rng.integers(0, 1 << 22, 2048)
+    hi = rng.integers((1 << 31) - (1 << 22), 1 << 31, 2048)
+    a = np.concatenate([a, lo, hi, hi])
+    b = np.concatenate([b, lo + rng.integers(0, 1 << 12, 2048), hi - rng.integers(0, 1 << 23, 2048),
+                        rng.integers((1 << 31) - (1 << 24), 1 << 31, 2048)])
+    sa = np.concatenate([sa, np.zeros(2048, np.int64), np.zeros(4096, np.int64)])
+    sb = np.concatenate([sb, np.ones(2048, np.int64), np.zeros(4096, np.int64)])
+    x = (a | (sa << 31)).astype(np.uint32)
+    y = (b | (sb << 31)).astype(np.uint32)
+    return x, y
+
+
+def test_xlns32_lds_adder_every_case(ln):
+    # the adder over its LDS image (sentinels, extended far grid, descriptor
+    # caps) in the three forms the kernels run, against xlns32_add
+    import ctypes
+    x, y = _x32_add_cases(np.random.default_rng(73))
+    add = O.lib().lno32_add
+    want = np.array([add(int(p), int(q)) for p, q in zip(x, y)], np.uint32)
+    m = np.uint32(0x7FFFFFFF)
+    want_pos = np.array([add(int(p), int(q)) for p, q in zip(x & m, y & m)], np.uint32)
+    dx, dy = dev(x.view(np.int32)), dev(y.view(np.int32))
+    for form, ref in ((0, want), (1, want), (2, want_pos)):
+        print(f"\n[xlns32 LDS adder] form {form}, {x.size} pairs", flush=True)
+        out = torch.empty_like(dx)
+        ln.check(ln.lib().lnship32_add_lds(form, ctypes.c_void_p(dx.data_ptr()), ctypes.c_void_p(dy.data_ptr()),
+                                            ctypes.c_void_p(out.data_ptr()), x.size, ln._stream()))
+        got = host(out).view(np.uint32)
+        bad = np.nonzero(got != ref)[0]
+        assert bad.size == 0, (f"form {form}: {bad.size} differ; first x={x[bad[0]]:#x} y={y[bad[0]]:#x}: "
+                               f"got {got[bad[0]]:#x} want {ref[bad[0]]:#x}")
+
+
 def test_xlns32_conversion_sampled(ln):
     rng = np.random.default_rng(11)
     bits = rng.integers(0, 1 << 32, 1 << 20, dtype=np.uint64).astype(np.uint32)

@@ -32,17 +32,27 @@ constexpr int k_lds_bytes = 160 * 1024;
 constexpr int k_lds_static = 2048;
 // The LDS copy of the xlns32 adder tables (32-bit words): 512 four-word
 // descriptors of the interpolation, indexed by (opposite signs, binade of d),
-// then dlo, then dhi as pairs (two words per dh), then the interpolation
-// tables sb, sbf, db, dbf as in the device table block, and a zero pair.
+// then -dlo, then dhi as pairs (two words per dh), then the interpolation
+// tables sb, sbf (extended with zeros, and the exact-cancellation node, up
+// to k32_co_cancel), db, dbf, and a zero pair.
 constexpr int k32_desc_n = 512;
+// the cotransformation's sentinels: e = (dh << 12) + dhi[dh] - dlo[dl] of
+// the dh = 0 lanes starts at k32_co_h0, of the dl = 0 lanes at -dlo = k32_co_l0,
+// so both fall in sbf's zeros; e of exact cancellation (d = 0) is their sum,
+// the node that drives the sum below 0
+constexpr uint32_t k32_co_h0 = 13u << 23, k32_co_l0 = 36u << 23;
+constexpr uint32_t k32_co_cancel = k32_co_h0 + k32_co_l0;
+constexpr int k32_sbf_ln = (int)((k32_co_cancel - k32_sb_end) >> k32_sb_fsh) + 2;   // LDS far-grid nodes: 594
 constexpr int kl_desc = 0;
 constexpr int kl_dlo = kl_desc + 4 * k32_desc_n;
 constexpr int kl_dhi = kl_dlo + k32_co_n;
-constexpr int kl_sb = kl_dhi + 2 * k32_co_n;                 // the rest of the block from sb on
-constexpr int kl_zero = kl_sb + (k32_tab_n - k32_off_sb);
-constexpr int kl_end = kl_zero + 4;
-constexpr int k_lds_tab32 = kl_end * 4;   // 132896 bytes
-static_assert(k32_off_sb % 4 == 0 && kl_sb % 4 == 0 && (k32_tab_n - k32_off_sb) % 4 == 0, "16-byte staging");
+constexpr int kl_sb = kl_dhi + 2 * k32_co_n;
+constexpr int kl_sbf = kl_sb + k32_sb_n;
+constexpr int kl_db = kl_sbf + k32_sbf_ln;
+constexpr int kl_dbf = kl_db + k32_db_n;
+constexpr int kl_zero = kl_dbf + k32_db_fn;
+constexpr int kl_end = (kl_zero + 4 + 3) & ~3;
+constexpr int k_lds_tab32 = kl_end * 4;   // 134496 bytes
 static_assert(kl_dlo % 4 == 0 && (kl_end - kl_dlo) % 4 == 0, "16-byte staging");
 
 static thread_local std::string t_err;
@@ -388,21 +398,22 @@ struct red16<LNSHIP_MONTE> {
 // dhi[dh] + sb(e) with e = (dh << 12) - dlo[dl] + dhi[dh].  A lane needs at
 // most one interpolation (at e on the sb tables, or at d on the sb / db
 // tables), so all lanes share one.  T is the LDS copy of the adder tables
-// with changes made at staging: the db-at-zero entry holds a sentinel (exact
-// cancellation clamps the log to 0), dhi becomes pairs ((dh << 12) +
-// dhi[dh], dhi[dh]) with the dl = 0 sentinel in place of dhi[0] (so that the
-// addend outside the interpolation is max(dhi, dlo)), a zero pair follows
-// the tables, then the descriptors of the interpolation (below).  Every select is arithmetic: a ternary around
-// two table reads would compile to a divergent branch that serialises both.
+// (lds32_image): dlo negated (with a sentinel at dl = 0), dhi as pairs
+// ((dh << 12) + dhi[dh], -dhi[dh]) (with sentinels at dh = 0), so that e is
+// one add and the addend outside the interpolation, max(dhi, dlo) on
+// cotransformation lanes and 0 elsewhere, is the negated minimum of the
+// pair's second word, -dlo and the descriptor's cap; sbf runs on in zeros
+// past the essential zero to the node of exact cancellation.  Every select
+// is arithmetic: a ternary around two table reads would compile to a
+// divergent branch that serialises both.
 
 // Byte offsets of the interpolation tables in the LDS copy, each less its
 // grid origin, so that a distance x on grid shift sh reads node
 // (x >> sh) at origin + ((x >> sh) << 2).
-constexpr int kl_shift = kl_sb - k32_off_sb;   // LDS word offset less the device block's
-constexpr uint32_t kb_sb = (uint32_t)(k32_off_sb + kl_shift) * 4;
-constexpr uint32_t kb_sbf = (uint32_t)(k32_off_sbf + kl_shift - (int)(k32_sb_end >> k32_sb_fsh)) * 4;
-constexpr uint32_t kb_db = (uint32_t)(k32_off_db + kl_shift - k32_db_first) * 4;
-constexpr uint32_t kb_dbf = (uint32_t)(k32_off_dbf + kl_shift - (int)(k32_db_end >> k32_db_fsh)) * 4;
+constexpr uint32_t kb_sb = (uint32_t)kl_sb * 4;
+constexpr uint32_t kb_sbf = (uint32_t)(kl_sbf - (int)(k32_sb_end >> k32_sb_fsh)) * 4;
+constexpr uint32_t kb_db = (uint32_t)(kl_db - k32_db_first) * 4;
+constexpr uint32_t kb_dbf = (uint32_t)(kl_dbf - (int)(k32_db_end >> k32_db_fsh)) * 4;
 
 // LDS byte addresses of the adder's tables (interpolation tables less their
 // grid origin), computed once per kernel; the empty asm keeps them opaque
@@ -430,11 +441,11 @@ __device__ __forceinline__ x32_tab x32_origins(const int32_t *T) {
 // The same addition ordered for one chain per lane, where every instruction
 // of the wave is on the chain's clock (a single wave issues about one
 // instruction per 2 ns).  Two rounds of LDS lookups.  First a descriptor
-// keyed by (opposite signs, binade of d), the cotransformation's dlo[dl] and
+// keyed by (opposite signs, binade of d), the cotransformation's -dlo[dl] and
 // the dhi pair of dh; then the pair of grid nodes around x, where x is d on
 // the sb / db grid the descriptor names (the zero pair from the essential
 // zero on), or, on cotransformation lanes, e on sb's near or far grid.  The
-// dl = 0 sentinel and dh = 0 put e beyond the essential zero, where the sb
+// dl = 0 and dh = 0 sentinels put e beyond the essential zero, where the sb
 // tables read 0, so every cotransformation lane interpolates at e and adds
 // dlo[dl] (dh = 0) or dhi[dh] besides.  The selects are bit-field inserts on
 // lane masks from the descriptor or from sign bits, with no compare.  The
@@ -454,9 +465,9 @@ __device__ __forceinline__ uint32_t x32_add_step(const x32_tab &O, acc_ls &a, ui
     const uint32_t du = absdiff(a.l, tl, u);
     // the three addresses after the three indices, in one asm block so that
     // each shift-add waits on an index formed two instructions earlier: the
-    // reads of dlo[dl], of the dhi pair of dh ((dh << 12) + dhi[dh], dhi[dh],
-    // or the sentinels for dh = 0) and of the descriptor (origin, grid shift, cap of e,
-    // cotransformation lane mask) go out back to back
+    // reads of -dlo[dl], of the dhi pair of dh ((dh << 12) + dhi[dh], -dhi[dh],
+    // or the sentinels for dh = 0) and of the descriptor (origin, grid shift,
+    // cap of e, cotransformation lane mask) go out back to back
     uint32_t a_lo, a_hi, a_ds;
     asm("v_lshl_add_u32 %0, %3, 2, %6\n\tv_lshl_add_u32 %1, %4, 3, %7\n\tv_lshl_add_u32 %2, %5, 4, %8"
         : "=&v"(a_lo), "=&v"(a_hi), "=&v"(a_ds)
@@ -475,18 +486,18 @@ __device__ __forceinline__ uint32_t x32_add_step(const x32_tab &O, acc_ls &a, ui
     // formed here, in the first round trip
     asm volatile("" ::"v"(mx), "v"(nsign), "v"(un));
     __builtin_amdgcn_sched_barrier(0);
-    // x: e (capped) on cotransformation lanes, du elsewhere (cap 0 there)
-    const uint32_t xe = min((uint32_t)hp.x - (uint32_t)lo, dsc.z);
+    // x: e on cotransformation lanes, du elsewhere (cap 0 there)
+    const uint32_t xe = min((uint32_t)hp.x + (uint32_t)lo, dsc.z);
     const uint32_t x = bfi(dsc.w, xe, du);
     const uint32_t hi = sign_mask(O.ksb - xe, O.one);   // e on sb's far grid
     const uint32_t sh = bfi(hi, (uint32_t)k32_sb_fsh, dsc.y);
     const uint32_t node = lshl2_add(x >> sh, bfi(hi, O.sbf, dsc.x));
     const int32_t t0 = lds_ld(node), t1 = lds_ld(node + 4);
     __builtin_amdgcn_sched_barrier(0);
-    // the addend outside the interpolation: dlo[dl] where dh = 0, else dhi[dh]
-    // (cotransformation lanes only), which is the larger of the two
-    const int32_t A = (int32_t)dsc.w & max(hp.y, lo);
-    const int32_t mA = (int32_t)mx + A;
+    // the addend outside the interpolation, less: -dlo[dl] where dh = 0,
+    // else -dhi[dh] (the smaller of the two) on cotransformation lanes, and
+    // the cap 0 elsewhere
+    const int32_t mA = (int32_t)mx - (int32_t)min(min((uint32_t)hp.y, (uint32_t)lo), dsc.z);
     const int32_t frac = (int32_t)__builtin_amdgcn_ubfe(x, 0, sh);
     post();
     __builtin_amdgcn_sched_barrier(0);
@@ -518,14 +529,13 @@ __device__ __forceinline__ void x32_add_ls(const x32_tab &O, acc_ls &a, uint32_t
     const u32x4 dsc = lds_ld4(lds_at4(du >> 23, O.desc));
     const uint32_t mx = max(a.l, tl);
     const uint32_t nsign = bfi(tl - a.l, a.s, ts) & (~u | (du - 1u));
-    const uint32_t xe = min((uint32_t)hp.x - (uint32_t)lo, dsc.z);
+    const uint32_t xe = min((uint32_t)hp.x + (uint32_t)lo, dsc.z);
     const uint32_t x = bfi(dsc.w, xe, du);
     const bool far = xe > k32_sb_end - 1u;
     const uint32_t sh = far ? (uint32_t)k32_sb_fsh : dsc.y;
     const uint32_t node = lshl2_add(x >> sh, far ? O.sbf : dsc.x);
     const int32_t t0 = lds_ld(node), t1 = lds_ld(node + 4);
-    const int32_t A = (int32_t)dsc.w & max(hp.y, lo);
-    const int32_t mA = (int32_t)mx + A;
+    const int32_t mA = (int32_t)mx - (int32_t)min(min((uint32_t)hp.y, (uint32_t)lo), dsc.z);
     const int32_t frac = (int32_t)__builtin_amdgcn_ubfe(x, 0, sh);
     const int32_t ip = t0 + (__mul24(t1 - t0, frac) >> sh);
     a.l = (uint32_t)max(__builtin_elementwise_add_sat(mA, ip), 0);
@@ -684,10 +694,11 @@ __device__ __forceinline__ red16<LNSHIP_SUM32> stage_tables<LNSHIP_SUM32>(const 
     // descriptor of key = (opposite signs) << 8 | (d >> 23): (origin, grid
     // shift, cap of e, lane mask).  Direct keys read the interpolation at d:
     // the sb / db table of d's binade, or the zero pair with a shift that
-    // empties d >> sh from the essential zero on; their cap 0 clamps e to 0.
-    // Cotransformation keys (opposite signs, d below two binades) read at e
-    // instead: sb's near grid, the far one chosen from e, e capped at the
-    // essential zero, and an all-ones mask.
+    // empties d >> sh from the essential zero on; their cap 0 clamps e to 0
+    // (and the addend outside the interpolation to 0).  Cotransformation keys
+    // (opposite signs, d below two binades) read at e instead: sb's near
+    // grid, the far one chosen from e, a cap at the exact-cancellation node
+    // (no e reaches past it), and an all-ones mask.
     {
         const uint32_t tb = lds_addr(t), zero = tb + (uint32_t)kl_zero * 4;
         for (int k = threadIdx.x; k < k32_desc_n; k += blockDim.x) {
@@ -697,7 +708,7 @@ __device__ __forceinline__ red16<LNSHIP_SUM32> stage_tables<LNSHIP_SUM32>(const 
                 if (q < (k32_sb_end >> 23)) base = tb + kb_sb, sh = k32_sb_sh;
                 else if (q < (k32_esszer >> 23)) base = tb + kb_sbf, sh = k32_sb_fsh;
             } else if (q < (k32_co_end >> 23)) {
-                base = tb + kb_sb, sh = k32_sb_sh, cap = k32_esszer, co = ~0u;
+                base = tb + kb_sb, sh = k32_sb_sh, cap = k32_co_cancel, co = ~0u;
             } else if (q < (k32_db_end >> 23)) {
                 base = tb + kb_db, sh = k32_db_sh;
             } else if (q < (k32_esszer >> 23)) {
@@ -1993,6 +2004,32 @@ __global__ void k_lpvip_db_range(uint32_t d0, uint32_t n, int32_t *__restrict__ 
         out[i] = lpvip_db(d0 + i);
 }
 
+// The xlns32 adder over its LDS tables on code pairs, in the form the kernels
+// run it: FORM 0 the multi-chain step, 1 the single-chain step of the decode
+// GEMVs, 2 the positive-sum step (sign bits ignored).
+template <int FORM>
+__global__ __launch_bounds__(k_block) void k_x32_add_lds(const uint32_t *__restrict__ x, const uint32_t *__restrict__ y,
+                                                         uint32_t *__restrict__ out, int64_t n, dev_tables T) {
+    extern __shared__ __align__(16) char lds[];
+    const red16<LNSHIP_SUM32> R = stage_tables<LNSHIP_SUM32>(T, lds);
+    __syncthreads();
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)blockDim.x * gridDim.x) {
+        const uint32_t a = x[i], b = y[i];
+        uint32_t r;
+        if constexpr (FORM == 0) {
+            r = x32_add_lds(R.O, a, b);
+        } else if constexpr (FORM == 1) {
+            acc_ls c{a & k32_logmask, a & k32_sign};
+            const uint32_t ts = b & k32_sign;
+            x32_add_step(R.O, c, b & k32_logmask, ts, c.s ^ ts, [] { return 0u; }, [] {});
+            r = c.s | c.l;
+        } else {
+            r = x32_add_pos(R.O, a & k32_logmask, b & k32_logmask);
+        }
+        out[i] = r;
+    }
+}
+
 __global__ void k_causal_mask(const int32_t *__restrict__ pos, int64_t ntok, int64_t n_kv, float *__restrict__ mask) {
     const int64_t n = ntok * n_kv;
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)blockDim.x * gridDim.x) {
@@ -2395,31 +2432,55 @@ const void *lnship_host_table(const char *name, size_t *bytes) {
 }
 
 // The LDS image of the xlns32 adder tables after the descriptors (which hold
-// LDS addresses, so each workgroup forms them): dlo with the db-at-zero entry
-// replaced by a sentinel (exact cancellation clamps the log to 0); dhi as
-// pairs (th2, th), th2 = (dh << 12) + dhi[dh], the first half of the
-// cotransformation's e, and th = dhi[dh] (< 0), the part the result adds.
-// dh = 0 gets (13 binades, 0): e = 13 binades - dlo[dl] is then beyond the
-// essential zero for every dl (dlo[dl] <= db(4095) < -11.5 binades, and the
-// d = 0 sentinel overflows e past it), so the interpolation at e reads 0, and
-// th = 0 (not negative) marks the lanes that add dlo[dl] instead.  Then the
-// interpolation tables sb, sbf, db, dbf as in the device block, and a zero
-// pair.
-static void lds32_image(const int32_t *tab, std::vector<int32_t> &img) {
+// LDS addresses, so each workgroup forms them).  -dlo[dl] (>= 0), with 36
+// binades in place of the db-at-zero entry; dhi as pairs (th2, nth), th2 =
+// (dh << 12) + dhi[dh], the first half of the cotransformation's e, and nth =
+// -dhi[dh] (>= 0), less the part the result adds.  dh = 0 gets (13 binades,
+// 2^31 - 1).  e = th2 - dlo[dl] then lies in the essential zero's sbf
+// zeros (24 to 38 binades) on the dh = 0 lanes (-dlo[dl] in [11.5, 23.6]
+// binades for dl > 0) and on the dl = 0 lanes (th2 >= -11.6 binades for
+// dh > 0), and only at d = 0 reaches 13 + 36 = 49 binades, the node that
+// clamps the log to 0.  The addend min(nth, -dlo[dl], cap) is -dlo[dl] where
+// dh = 0, else -dhi[dh] (db rises with the distance and dh << 12 > dl, so
+// -dhi[dh] < -dlo[dl]).  Then the interpolation tables sb, sbf (extended),
+// db, dbf, and a zero pair.
+// Returns false when the tables break a bound the layout relies on.
+static bool lds32_image(const int32_t *tab, std::vector<int32_t> &img) {
     // (word kl_dlo of the LDS copy is word 0 of the image)
     img.assign(kl_end - kl_dlo, 0);
     int32_t *w = img.data() - kl_dlo;
-    for (int i = 0; i < k32_co_n; i++) w[kl_dlo + i] = tab[k32_off_dlo + i];
-    w[kl_dlo] = -0x7fffffff;
+    for (int i = 1; i < k32_co_n; i++) w[kl_dlo + i] = -tab[k32_off_dlo + i];
+    w[kl_dlo] = (int32_t)k32_co_l0;
     for (int i = 0; i < k32_co_n; i++) {
         const int32_t h = tab[k32_off_dhi + i];
-        w[kl_dhi + 2 * i] = i == 0 ? (int32_t)(13u << 23) : h + (i << k32_co_sh);
-        // dh = 0: the dl = 0 sentinel, so that max(dhi, dlo) is dlo[dl]
-        // there, and dhi[dh] elsewhere (db rises with the distance, and
-        // dh << 12 > dl)
-        w[kl_dhi + 2 * i + 1] = i == 0 ? -0x7fffffff : h;
+        w[kl_dhi + 2 * i] = i == 0 ? (int32_t)k32_co_h0 : h + (i << k32_co_sh);
+        // dh = 0: above every -dlo[dl], so the minimum takes -dlo[dl] there,
+        // and -dhi[dh] elsewhere (db rises with the distance, dh << 12 > dl)
+        w[kl_dhi + 2 * i + 1] = i == 0 ? 0x7fffffff : -h;
     }
-    for (int i = k32_off_sb; i < k32_tab_n; i++) w[i + kl_shift] = tab[i];
+    for (int i = 0; i < k32_sb_n; i++) w[kl_sb + i] = tab[k32_off_sb + i];
+    for (int i = 0; i < k32_sb_fn; i++) w[kl_sbf + i] = tab[k32_off_sbf + i];
+    // past the essential zero sbf reads 0 up to the exact-cancellation node,
+    // whose pair drives any sum below 0 (the log clamps to 0)
+    const int cancel = (int)((k32_co_cancel - k32_sb_end) >> k32_sb_fsh);
+    w[kl_sbf + cancel] = w[kl_sbf + cancel + 1] = -0x7fffffff;
+    for (int i = 0; i < k32_db_n; i++) w[kl_db + i] = tab[k32_off_db + i];
+    for (int i = 0; i < k32_db_fn; i++) w[kl_dbf + i] = tab[k32_off_dbf + i];
+    // the bounds: every e short of the segment before the cancellation node
+    // and past the essential zero on the sentinel lanes; -dhi below -dlo
+    int64_t nlo_min = INT64_MAX, nlo_max = INT64_MIN, th2_min = INT64_MAX, th2_max = INT64_MIN, nth_max = INT64_MIN;
+    for (int i = 1; i < k32_co_n; i++) {
+        nlo_min = std::min<int64_t>(nlo_min, w[kl_dlo + i]);
+        nlo_max = std::max<int64_t>(nlo_max, w[kl_dlo + i]);
+        th2_min = std::min<int64_t>(th2_min, w[kl_dhi + 2 * i]);
+        th2_max = std::max<int64_t>(th2_max, w[kl_dhi + 2 * i]);
+        nth_max = std::max<int64_t>(nth_max, w[kl_dhi + 2 * i + 1]);
+    }
+    const int64_t seg = (int64_t)k32_co_cancel - (1 << k32_sb_fsh), ess = k32_esszer;
+    return w[kl_sbf + k32_sb_fn - 1] == 0 && (int64_t)k32_co_h0 + nlo_min >= ess &&
+           (int64_t)k32_co_h0 + nlo_max < seg && th2_min + (int64_t)k32_co_l0 >= ess &&
+           th2_max + (int64_t)k32_co_l0 < seg && th2_max + nlo_max < seg && th2_min + nlo_min >= 0 &&
+           nth_max < nlo_min && nth_max < (int64_t)k32_co_l0;
 }
 
 int lnship_init(void) {
@@ -2439,7 +2500,8 @@ int lnship_init(void) {
     if (int rc = upload(g_host->tab32, (size_t)k32_tab_n, &T.tab32)) return rc;
     {
         std::vector<int32_t> img;
-        lds32_image(g_host->tab32, img);
+        if (!lds32_image(g_host->tab32, img))
+            return fail(LNSHIP_EINVAL, "init: xlns32 tables outside the bounds of their LDS layout%s");
         if (int rc = upload(img.data(), img.size(), &T.lds32)) return rc;
     }
     if (int rc = upload(g_host->lfsr_seq, 65536, &T.lfsr_seq)) return rc;
@@ -3075,6 +3137,32 @@ int lnship_lpvip_db_range(uint32_t d0, uint32_t n, int32_t *out, void *stream) {
     if (!out) return fail(LNSHIP_EINVAL, "lpvip_db_range: null output%s");
     if (n == 0) return 0;
     hipLaunchKernelGGL(k_lpvip_db_range, dim3(grid_for(n, 4)), dim3(k_block), 0, (hipStream_t)stream, d0, n, out);
+    LNSHIP_HIP(hipGetLastError());
+    return 0;
+}
+
+int lnship32_add_lds(int form, const uint32_t *x, const uint32_t *y, uint32_t *out, int64_t n, void *stream) {
+    device_state *s = state();
+    if (!s) return LNSHIP_ENOINIT;
+    if (form < 0 || form > 2 || n < 0) return fail(LNSHIP_EINVAL, "add_lds: bad argument%s");
+    if (n == 0) return 0;
+    if (!x || !y || !out) return fail(LNSHIP_EINVAL, "add_lds: null pointer%s");
+    // one staging of the tables per workgroup: a grid of one workgroup per CU
+    const dim3 g((unsigned)std::min<int64_t>((n + k_block - 1) / k_block, std::max(s->cus, 1)));
+    hipStream_t st = (hipStream_t)stream;
+    switch (form) {
+        case 0:
+            if (int rc = set_lds(k_x32_add_lds<0>, k_lds_tab32)) return rc;
+            hipLaunchKernelGGL(k_x32_add_lds<0>, g, dim3(k_block), k_lds_tab32, st, x, y, out, n, s->T);
+            break;
+        case 1:
+            if (int rc = set_lds(k_x32_add_lds<1>, k_lds_tab32)) return rc;
+            hipLaunchKernelGGL(k_x32_add_lds<1>, g, dim3(k_block), k_lds_tab32, st, x, y, out, n, s->T);
+            break;
+        default:
+            if (int rc = set_lds(k_x32_add_lds<2>, k_lds_tab32)) return rc;
+            hipLaunchKernelGGL(k_x32_add_lds<2>, g, dim3(k_block), k_lds_tab32, st, x, y, out, n, s->T);
+    }
     LNSHIP_HIP(hipGetLastError());
     return 0;
 }
