@@ -35,6 +35,10 @@ def parse():
     ap.add_argument("--cpu-tokens", type=int, default=3, help="decode tokens of the CPU baseline sample")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-graph", action="store_true", help="decode eagerly instead of replaying a HIP graph")
+    ap.add_argument("--decode-only", action="store_true",
+                    help="only the prompt and the decode steps, then one recorded eager step: prints the decode "
+                         "launches' algorithmic bytes (for HBM counter runs; with --prompt 1 every lnship16_mul_mat "
+                         "launch of the run is a decode-step launch)")
     ap.add_argument("--calib-copy", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB three times (HBM counter calibration)")
     ap.add_argument("--ops", choices=["decode", "prefill", "all"],
@@ -116,7 +120,8 @@ def run_ops(args):
             K, M, T = 2048, 8192, 512
             wp = lnship.pack16(randn(M, K) * 0.02)
             x = randn(T, K)
-            us = timed(lambda: lnship.mul_mat16(m, wp, x, K, M), max(1, args.reps // 2))
+            # a 5-25 ms launch: at least ten of them per figure
+            us = timed(lambda: lnship.mul_mat16(m, wp, x, K, M), max(10, args.reps))
             line(op="mul_mat", mode=mname, K=K, M=M, N=T, us=round(us, 2), gmacs=round(K * M * T / us / 1e3, 2))
             x = randn(512, 2048)
             us = timed(lambda: lnship.rms_norm16(m, x, 1e-5), args.reps)
@@ -199,27 +204,7 @@ def gemv_roofline(model, ln, torch, reps=4):
     call: one GEMV kernel when NC activation rows fit in LDS next to the
     tables (every decode shape), else the activation conversion kernel plus
     the GEMV kernel."""
-    c = model.cfg
-    calls = []
-    orig = model._mm
-
-    def record_mm(w, x_ptr, dst_ptr, K, M, N, **kw):
-        orig(w, x_ptr, dst_ptr, K, M, N, **kw)
-        calls.append((w, x_ptr, dst_ptr, K, M, N, kw))
-
-    model._mm = record_mm
-    try:
-        tok = model._buf("rtok", 1, torch.int32)
-        pos = model._buf("rpos", 1, torch.int32)
-        tok.fill_(1)
-        # the last timed position again, so the launches have the timed
-        # steps' shapes (its KV row is rewritten; nothing reads it afterwards)
-        pos.fill_(model.n_past - 1)
-        from lnship.llama import n_kv_for
-        model.forward(1, tok, pos, n_kv_for(model.n_past, c.n_ctx))
-        torch.cuda.synchronize()
-    finally:
-        model._mm = orig
+    calls = record_decode_step(model, torch)
     # the launches go into one HIP graph so host-side launch cost stays out
     # of the device time between the events
     g = torch.cuda.CUDAGraph()
@@ -237,12 +222,42 @@ def gemv_roofline(model, ln, torch, reps=4):
     e.synchronize()
     n = len(calls)
     total_us = s.elapsed_time(e) * 1e3 / reps
-    # algorithmic bytes: xlns16 weights once per weight slice, F32 in / out,
-    # and the F32 residual read by the launches that fuse the ADD after them
-    total_b = sum(2 * K * M * kw.get("ne02", 1) + 4 * K * N * kw.get("ne12", 1)
-                  + 4 * M * N * kw.get("ne12", 1) * (2 if kw.get("residual") is not None else 1)
-                  for _, _, _, K, M, N, kw in calls)
-    return total_b / n, total_us / n, n
+    return launch_bytes(calls) / n, total_us / n, n
+
+
+def record_decode_step(model, torch):
+    """Runs one eager decode step at the last timed position (its KV row is
+    rewritten; nothing reads it afterwards), so the launches have the timed
+    steps' shapes, and returns its lnship16_mul_mat calls."""
+    c = model.cfg
+    calls = []
+    orig = model._mm
+
+    def record_mm(w, x_ptr, dst_ptr, K, M, N, **kw):
+        orig(w, x_ptr, dst_ptr, K, M, N, **kw)
+        calls.append((w, x_ptr, dst_ptr, K, M, N, kw))
+
+    model._mm = record_mm
+    try:
+        tok = model._buf("rtok", 1, torch.int32)
+        pos = model._buf("rpos", 1, torch.int32)
+        tok.fill_(1)
+        pos.fill_(model.n_past - 1)
+        from lnship.llama import n_kv_for
+        model.forward(1, tok, pos, n_kv_for(model.n_past, c.n_ctx))
+        torch.cuda.synchronize()
+    finally:
+        model._mm = orig
+    return calls
+
+
+def launch_bytes(calls):
+    """Algorithmic bytes of mul_mat calls: xlns16 weights once per weight
+    slice, F32 in / out, and the F32 residual read by the launches that fuse
+    the ADD after them."""
+    return sum(2 * K * M * kw.get("ne02", 1) + 4 * K * N * kw.get("ne12", 1)
+               + 4 * M * N * kw.get("ne12", 1) * (2 if kw.get("residual") is not None else 1)
+               for _, _, _, K, M, N, kw in calls)
 
 
 def chain_bound(model, ln, torch, mode):
@@ -481,6 +496,13 @@ def main():
     t_decode = time.perf_counter() - ts
 
     decode_tok_s = args.steps / t_decode
+    if args.decode_only:
+        calls = record_decode_step(model, torch)
+        print(json.dumps({"decode_only": True, "mode": args.mode, "prompt_tokens": args.prompt,
+                          "decode_steps": args.warmup + args.steps + 1, "launches_per_token": len(calls),
+                          "bytes_per_launch": int(launch_bytes(calls) / len(calls)),
+                          "decode_tok_s": round(decode_tok_s, 3)}), flush=True)
+        return
     macs_per_token = cfg.n_layer * (
         (cfg.n_head + 2 * cfg.n_head_kv) * cfg.head_dim * cfg.n_embd + cfg.n_embd * cfg.n_head * cfg.head_dim +
         3 * cfg.n_ff * cfg.n_embd) + cfg.n_vocab * cfg.n_embd
