@@ -263,14 +263,15 @@ def launch_bytes(calls):
 def chain_bound(model, ln, torch, mode):
     """The dependent-step bound of one decode token.  steps: the sum over the
     token's launches of their chain length (K per mul_mat, n per rms_norm row,
-    n - 1 per soft_max row); a launch's chains run side by side and the
-    launches one after another.  ns_per_step: the slope of GEMV launch time
+    n - 1 per soft_max row; head_dim + 2 n_kv - 1 for the fused decode
+    attention, whose KQ, soft_max and KQV chains run one after another); a
+    launch's chains run side by side and the launches one after another.  ns_per_step: the slope of GEMV launch time
     against K at M = 576 (K = 576 and 1536, each a graph of 20 launches timed
     between HIP events on the replay stream), so each launch's fixed cost
     stays out of it.  bound_tok_s = 1 / (steps * ns_per_step)."""
     c = model.cfg
     steps = []
-    orig = (model._mm, model._rms_mul, model._softmax)
+    orig = (model._mm, model._rms_mul, model._softmax, model._attn)
 
     def mm(w, x_ptr, dst_ptr, K, M, N, **kw):
         steps.append(K)
@@ -284,7 +285,11 @@ def chain_bound(model, ln, torch, mode):
         steps.append(ne[0] - 1)
         orig[2](x_ptr, ne, mask_ptr, mne, scale, dst_ptr)
 
-    model._mm, model._rms_mul, model._softmax = mm, rms, sm
+    def attn(args):
+        steps.append(args.head_dim + 2 * args.n_kv - 1)
+        orig[3](args)
+
+    model._mm, model._rms_mul, model._softmax, model._attn = mm, rms, sm, attn
     try:
         tok = model._buf("rtok", 1, torch.int32)
         pos = model._buf("rpos", 1, torch.int32)
@@ -294,7 +299,7 @@ def chain_bound(model, ln, torch, mode):
         model.forward(1, tok, pos, n_kv_for(model.n_past, c.n_ctx))
         torch.cuda.synchronize()
     finally:
-        model._mm, model._rms_mul, model._softmax = orig
+        model._mm, model._rms_mul, model._softmax, model._attn = orig
     st = lambda: ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
     us = {}
     M = 576

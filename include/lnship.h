@@ -236,6 +236,30 @@ typedef struct lnship_qkv_store_args {
 int lnship16_rope_store_kv(const lnship_qkv_store_args *args, void *stream);
 int lnship32_rope_store_kv(const lnship_qkv_store_args *args, void *stream);
 
+/* Decode attention of one token in one launch: for each query head h (kv
+ * head h / (n_head / n_head_kv)) the three nodes that follow the cache
+ * stores, back to back: kq = K q (lns_mul_mat, src/lns-ops.cpp:293-384),
+ * p = softmax(kq * scale + mask) (lns_soft_max, :643-695) and dst = V p
+ * (lns_mul_mat).  Every F32 value between them is rounded as the separate
+ * nodes round it, so dst equals theirs bit for bit.  No single counterpart in
+ * the reference, which runs the three as graph nodes.  Modes 0, 2 and 3 (a
+ * Monte op's draws follow the three nodes in graph order: run them).  The
+ * caches in the layout lnship16_rope_store_kv writes: key cell j < n_kv of kv
+ * head g at k_cache + g * k_slice, its dims in groups of eight cache_m * 8
+ * codes apart; value dim d < head_dim at v_cache + g * v_slice, its cells in
+ * groups of eight head_dim * 8 codes apart.  q and dst [n_head][head_dim]
+ * F32, mask [n_kv] F32 (optional; 0 or -inf).  n_kv <= lnship_max_row(4, mode). */
+typedef struct lnship_attn_args {
+    const float *q;
+    const uint16_t *k_cache, *v_cache;
+    int64_t cache_m, k_slice, v_slice;
+    const float *mask;
+    float scale;
+    float *dst;
+    int64_t n_head, n_head_kv, head_dim, n_kv;
+} lnship_attn_args;
+int lnship16_attn_decode(int mode, const lnship_attn_args *args, void *stream);
+
 /* ggml views on the device (tensors in the ggml device buffer type): the
  * elements of a 4-D strided view (byte strides nb, as ggml_tensor::nb)
  * gathered into a contiguous F32 array in ggml element order, from F32
@@ -310,8 +334,9 @@ int lnship_rope_table(float freq_base, int n_dims, int64_t n_pos, float *out);
 int lnship_causal_mask(const int32_t *pos, int64_t ntok, int64_t n_kv, float *mask, void *stream);
 
 /* Longest row (ncols) the row kernels stage in LDS: which = 0 xlns16
- * rms_norm, 1 xlns16 soft_max, 2 xlns32 rms_norm, 3 xlns32 soft_max; mode is
- * the xlns16 summation mode (ignored for xlns32).  No GPU needed.  Plays the
+ * rms_norm, 1 xlns16 soft_max, 2 xlns32 rms_norm, 3 xlns32 soft_max, 4 the
+ * cells (n_kv) of lnship16_attn_decode with head_dim up to 256 (0 for Monte);
+ * mode is the xlns16 summation mode (ignored for xlns32).  No GPU needed.  Plays the
  * role of the reference's grid / shape predicates (cuda/lns-cuda-ops.cpp:
  * 45-54, 184-189): a ggml backend declines longer rows in supports_op. */
 int64_t lnship_max_row(int which, int mode);

@@ -661,6 +661,43 @@ def test_mul_mat_id_expert_out_of_range(ln):
     same_bits(got[1], want[1], "token after the bad expert")
 
 
+@pytest.mark.parametrize("mode,n_kv", [("base", 1), ("base", 13), ("base", 256), ("lpvip", 13), ("lpvip", 256),
+                                        ("sum32", 1), ("sum32", 13), ("sum32", 256), ("sum32", 520),
+                                        ("sum32", 2048)])
+def test_attn_decode_equals_three_nodes(ln, mode, n_kv):
+    # lnship16_attn_decode against K^T q, soft_max and V p run as three ops, on
+    # the SmolLM2 head shape (9 query heads over 3 kv heads of 64), random
+    # caches and a causal mask that hides the last cells
+    import ctypes
+    m = O.MODES[mode]
+    nh, nkv, hd, n_ctx = 9, 3, 64, max(256, (n_kv + 255) // 256 * 256)
+    rng = np.random.default_rng(n_kv)
+    print(f"\n[attn decode] {mode} n_kv={n_kv}", flush=True)
+    kc = ln.pack16(dev((rng.standard_normal((nkv, n_ctx, hd)) * 0.5).astype(np.float32)))
+    vc = ln.pack16(dev((rng.standard_normal((nkv, hd, n_ctx)) * 0.5).astype(np.float32)))
+    kslice, vslice = ln.kp(hd) * n_ctx, ln.kp(n_ctx) * hd
+    q = dev((rng.standard_normal(nh * hd) * 2).astype(np.float32))
+    pos = max(0, n_kv - 1 - n_kv // 5)
+    mask = dev(np.where(np.arange(n_kv) <= pos, 0.0, -np.inf).astype(np.float32))
+    scale = 0.125
+    P = lambda t: t.data_ptr()
+    kq = torch.empty(nh * n_kv, device="cuda")
+    ln.mul_mat16_raw(m, P(kc), P(q), P(kq), hd, n_kv, 1, ne02=nkv, ne12=nh, x_ld=nh * hd, x_slice=hd,
+                     w_mstride=n_ctx, w_slice=kslice)
+    p = ln.soft_max16(m, kq.view(1, nh, 1, n_kv), mask.view(1, 1, 1, n_kv), scale)
+    want = torch.empty(nh * hd, device="cuda")
+    ln.mul_mat16_raw(m, P(vc), P(p), P(want), n_kv, hd, 1, ne02=nkv, ne12=nh, x_ld=n_kv, x_slice=n_kv,
+                     w_slice=vslice, dst_ld=nh * hd, dst_slice=hd)
+    got = torch.full((nh * hd,), float("nan"), device="cuda")
+    a = ln.AttnArgs(P(q), P(kc), P(vc), n_ctx, kslice, vslice, P(mask), scale, P(got), nh, nkv, hd, n_kv)
+    ln.check(ln.lib().lnship16_attn_decode(m, ctypes.byref(a), ln._stream()))
+    same_bits(host(got), host(want), f"attn decode {mode} n_kv={n_kv}")
+    if mode == "sum32" and n_kv == 13:
+        # Monte is refused (its draws run across the three nodes in graph order)
+        assert ln.lib().lnship16_attn_decode(O.MONTE, ctypes.byref(a), ln._stream()) != 0
+        assert ln.lib().lnship_max_row(4, O.MONTE) == 0 and ln.lib().lnship_max_row(4, m) >= 4096
+
+
 def test_lpvip_db_every_distance_below_one_binade(ln):
     # lpvip's exact branch (d below one binade, opposite signs) against the
     # host's libm for every d, and the Mitchell branch just above it (d = 0

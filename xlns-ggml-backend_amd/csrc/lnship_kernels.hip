@@ -1596,6 +1596,130 @@ __global__ __launch_bounds__(k_block) void k_softmax16(sm_args a, dev_tables T) 
     }
 }
 
+// ---- decode attention: KQ, soft_max and KQV of one token in one launch ------
+struct attn_args {
+    const float *q;
+    const uint16_t *k, *v;
+    int64_t k_gs, k_slice, v_gs, v_slice;   // codes between groups of eight; between kv heads
+    const float *mask;
+    float scale;
+    float *dst;
+    int hd, n_kv, rep;   // head_dim, cells, query heads per kv head
+};
+
+// One output of a GEMV over weights in the packed layout: the row's groups of
+// eight codes gs codes apart from w, the activations' codes at x in LDS; the
+// K terms in k order, each an xlns16_mul product, added as k_mm16 adds them.
+// The weights of the next PF groups are in flight while a block is added.
+template <int MODE>
+__device__ __forceinline__ uint32_t row_chain(const red16<MODE> &R, const uint16_t *__restrict__ w, int64_t gs,
+                                              const uint16_t *x, int K) {
+    constexpr int PF = 4;
+    const int ng = (K + 7) >> 3;
+    uint32_t st = 0;
+    typename red16<MODE>::acc_t acc{};
+    auto load = [&](uint4 (&b)[PF], int g0) {
+#pragma unroll
+        for (int p = 0; p < PF; p++) b[p] = *reinterpret_cast<const uint4 *>(w + (int64_t)min(g0 + p, ng - 1) * gs);
+    };
+    auto run = [&](const uint4 (&b)[PF], int g0) {
+#pragma unroll
+        for (int p = 0; p < PF; p++) {
+            const int g = g0 + p;
+            if (g >= ng) break;
+            const uint4 xq = *reinterpret_cast<const uint4 *>(x + 8 * g);
+            const uint32_t ww[4] = {b[p].x, b[p].y, b[p].z, b[p].w}, xx[4] = {xq.x, xq.y, xq.z, xq.w};
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                const int k = 8 * g + u;
+                if (k >= K) break;
+                const uint32_t t = x16_mul(half16(ww[u >> 1], u & 1), half16(xx[u >> 1], u & 1));
+                if (k == 0) acc = R.start(t, st);
+                else if constexpr (MODE == LNSHIP_SUM32)
+                    R.add_lat(acc, (t & k16_logmask) << 16, (t & k16_sign) << 16, [] {});
+                else R.add(acc, t, st);
+            }
+        }
+    };
+    uint4 wa[PF], wb[PF];
+    load(wa, 0);
+    for (int g0 = 0; g0 < ng; g0 += 2 * PF) {
+        load(wb, g0 + PF);
+        run(wa, g0);
+        if (g0 + PF >= ng) break;
+        load(wa, g0 + 2 * PF);
+        run(wb, g0 + PF);
+    }
+    return R.finish(acc) & 0xffffu;
+}
+
+// One workgroup per query head h (kv head h / rep): the kq scores (one chain
+// of head_dim steps per cell), soft_max over them (k_softmax16's passes on one
+// row), then the att outputs (one chain of n_kv steps per dim).  Between the
+// nodes every value goes through F32 and back exactly as the separate nodes
+// pass it on (the GEMV writes rev16 of its code, soft_max and the KQV GEMV
+// convert their F32 inputs with cvt16), so the result is theirs bit for bit.
+template <int MODE>
+__global__ __launch_bounds__(k_block) void k_attn16(attn_args a, dev_tables T) {
+    extern __shared__ __align__(16) char lds[];
+    const red16<MODE> R = stage_tables<MODE>(T, lds);
+    const int hd = a.hd, n = a.n_kv, hp = (hd + 7) & ~7, rs = (n + 7) & ~7;
+    uint16_t *xq = reinterpret_cast<uint16_t *>(lds + mm_xl_offset<MODE>());   // the query's codes
+    uint16_t *c = xq + hp;                                                     // scores, then exps
+    uint16_t *pc = c + rs;                                                     // KQV's activation codes
+    __shared__ int32_t s_max;
+    __shared__ uint32_t s_tot;
+    __shared__ int s_last;
+    const int h = blockIdx.x, kv = h / a.rep;
+    if (threadIdx.x == 0) {
+        s_max = x16_canon(0xffffu);
+        s_last = 0;
+    }
+    for (int k = threadIdx.x; k < hp; k += blockDim.x)
+        xq[k] = k < hd ? (uint16_t)x16_from_f32(T.cvt16, a.q[(int64_t)h * hd + k]) : (uint16_t)0;
+    __syncthreads();
+    // the scores, and soft_max's first pass over them
+    const uint32_t sc = x16_from_f32(T.cvt16, a.scale);
+    const bool has_mask = a.mask != nullptr;
+    const uint16_t *kw = a.k + kv * a.k_slice;
+    for (int j = threadIdx.x; j < n; j += blockDim.x) {
+        const float f = T.rev16[row_chain<MODE>(R, kw + (int64_t)j * 8, a.k_gs, xq, hd)];
+        const float mf = has_mask ? a.mask[j] : 0.0f;
+        const uint32_t v = x16_from_f32(T.cvt16, f), mk = x16_from_f32(T.cvt16, mf);
+        const uint32_t vm = x16_mul(v, sc), va = x16_add_g(T.gauss16, vm, mk);
+        const bool masked_out = has_mask && (mf <= -3.0e38f || mk == 0xffffu);
+        const uint32_t w = v == 0xffffu || masked_out ? 0xffffu : (has_mask && (mk & k16_logmask)) ? va : vm;
+        c[j] = (uint16_t)w;
+        atomicMax(&s_max, x16_canon(w));
+    }
+    __syncthreads();
+    {
+        const int32_t cm = s_max;
+        const uint32_t mx = (uint32_t)(uint16_t)(cm < 0 ? (cm ^ 0x7fff) : cm);
+        for (int j = threadIdx.x; j < n; j += blockDim.x) {
+            const uint32_t e = T.exp16[x16_add_g(T.gauss16, c[j], mx ^ k16_sign)];
+            c[j] = (uint16_t)e;
+            if (e & k16_logmask) atomicMax(&s_last, j);
+        }
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        // the sum of exps up to the last nonzero one, as k_softmax16 runs it
+        uint32_t st = 0;
+        typename red16<MODE>::acc_t acc = R.start(c[0], st);
+        const int n_eff = s_last + 1;
+        if (n_eff > 1) chain16<red16<MODE>, true>(R, acc, c, 1, n_eff, st);
+        s_tot = R.finish(acc) & 0xffffu;
+    }
+    __syncthreads();
+    for (int j = threadIdx.x; j < rs; j += blockDim.x)
+        pc[j] = j < n ? (uint16_t)x16_from_f32(T.cvt16, T.rev16[x16_div(c[j], s_tot)]) : (uint16_t)0;
+    __syncthreads();
+    const uint16_t *vw = a.v + kv * a.v_slice;
+    for (int d = threadIdx.x; d < hd; d += blockDim.x)
+        a.dst[(int64_t)h * hd + d] = T.rev16[row_chain<MODE>(R, vw + (int64_t)d * 8, a.v_gs, pc, n)];
+}
+
 __global__ __launch_bounds__(k_block) void k_softmax32(sm_args a, dev_tables T) {
     extern __shared__ __align__(16) char lds[];
     const red16<LNSHIP_SUM32> R = stage_tables<LNSHIP_SUM32>(T, lds);
@@ -2267,6 +2391,26 @@ static int check_sm(const lnship_soft_max_args *a) {
 }
 
 template <int MODE>
+static int attn16_lds(int64_t hd, int64_t n_kv) {
+    return mm_xl_offset<MODE>() + (int)(2 * ((hd + 7) & ~(int64_t)7) + 4 * ((n_kv + 7) & ~(int64_t)7));
+}
+
+template <int MODE>
+static int launch_attn16(const attn_args &m, int64_t nh, const dev_tables &T, hipStream_t st) {
+    const int lds = attn16_lds<MODE>(m.hd, m.n_kv);
+    if (int rc = set_lds(k_attn16<MODE>, lds)) return rc;
+    hipLaunchKernelGGL(k_attn16<MODE>, dim3((unsigned)nh), dim3(k_block), lds, st, m, T);
+    LNSHIP_HIP(hipGetLastError());
+    return 0;
+}
+
+// cells of lnship16_attn_decode with head_dim up to 256
+template <int MODE>
+static int64_t max_attn_kv() {
+    return ((k_lds_bytes - k_lds_static - attn16_lds<MODE>(256, 0)) / 4) & ~(int64_t)7;
+}
+
+template <int MODE>
 static int launch_sm16(sm_args &m, int64_t nrows, const dev_tables &T, hipStream_t st) {
     const int64_t rs = (m.n + 7) & ~(int64_t)7;
     m.rb = rows_per_block<MODE>(rs, 2);
@@ -2906,6 +3050,28 @@ int lnship16_soft_max(int mode, const lnship_soft_max_args *a, void *stream) {
     }
 }
 
+int lnship16_attn_decode(int mode, const lnship_attn_args *a, void *stream) {
+    device_state *s = state();
+    if (!s) return LNSHIP_ENOINIT;
+    if (!a) return fail(LNSHIP_EINVAL, "attn_decode: null args%s");
+    if (mode == LNSHIP_MONTE)
+        return fail(LNSHIP_EINVAL, "attn_decode: Monte draws run across the three nodes in graph order; run them%s");
+    if (mode < 0 || mode > 3) return fail(LNSHIP_EINVAL, "unknown summation mode%s");
+    if (!a->q || !a->k_cache || !a->v_cache || !a->dst || a->n_head <= 0 || a->n_head_kv <= 0 ||
+        a->n_head % a->n_head_kv || a->head_dim <= 0 || a->n_kv <= 0 || a->cache_m < a->n_kv ||
+        a->head_dim > 4096 || a->n_head > 65535)
+        return fail(LNSHIP_EINVAL, "attn_decode: bad argument%s");
+    if (a->n_kv > lnship_max_row(4, mode)) return fail(LNSHIP_ERANGE, "attn_decode: n_kv too long for LDS%s");
+    const attn_args m{a->q, a->k_cache, a->v_cache, a->cache_m * 8, a->k_slice, a->head_dim * 8, a->v_slice,
+                      a->mask, a->scale, a->dst, (int)a->head_dim, (int)a->n_kv, (int)(a->n_head / a->n_head_kv)};
+    hipStream_t st = (hipStream_t)stream;
+    switch (mode) {
+        case LNSHIP_BASE: return launch_attn16<LNSHIP_BASE>(m, a->n_head, s->T, st);
+        case LNSHIP_LPVIP: return launch_attn16<LNSHIP_LPVIP>(m, a->n_head, s->T, st);
+        default: return launch_attn16<LNSHIP_SUM32>(m, a->n_head, s->T, st);
+    }
+}
+
 int lnship32_soft_max(const lnship_soft_max_args *a, void *stream) {
     device_state *s = state();
     if (!s) return LNSHIP_ENOINIT;
@@ -2927,6 +3093,14 @@ int lnship32_soft_max(const lnship_soft_max_args *a, void *stream) {
 
 int64_t lnship_max_row(int which, int mode) {
     if (which == 2 || which == 3) return max_row<LNSHIP_SUM32>(4);
+    if (which == 4) {
+        switch (mode) {
+            case LNSHIP_BASE: return max_attn_kv<LNSHIP_BASE>();
+            case LNSHIP_LPVIP: return max_attn_kv<LNSHIP_LPVIP>();
+            case LNSHIP_SUM32: return max_attn_kv<LNSHIP_SUM32>();
+            default: return 0;
+        }
+    }
     if (which != 0 && which != 1) return 0;
     switch (mode) {
         case LNSHIP_BASE: return max_row<LNSHIP_BASE>(2);

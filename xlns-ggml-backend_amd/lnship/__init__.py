@@ -52,6 +52,12 @@ class QkvStoreArgs(ctypes.Structure):
                 ("v_slice", c_i64), ("seq", c_p), ("seq_stride", c_i64)]
 
 
+class AttnArgs(ctypes.Structure):
+    _fields_ = [("q", c_p), ("k_cache", c_p), ("v_cache", c_p), ("cache_m", c_i64), ("k_slice", c_i64),
+                ("v_slice", c_i64), ("mask", c_p), ("scale", ctypes.c_float), ("dst", c_p), ("n_head", c_i64),
+                ("n_head_kv", c_i64), ("head_dim", c_i64), ("n_kv", c_i64)]
+
+
 def build():
     import subprocess
     subprocess.check_call(["make", "-s", "-C", PKG_DIR])
@@ -89,6 +95,8 @@ def lib():
                                                  ctypes.c_uint16, c_p, ctypes.c_uint64, c_p]),
         "lnship32_rms_norm_mul": (ctypes.c_int, [c_p, c_p, c_p, c_i64, c_i64, ctypes.c_float, c_p]),
         "lnship16_rope_store_kv": (ctypes.c_int, [ctypes.POINTER(QkvStoreArgs), c_p]),
+        "lnship16_attn_decode": (ctypes.c_int, [ctypes.c_int, ctypes.POINTER(AttnArgs), c_p]),
+        "lnship_max_row": (c_i64, [ctypes.c_int, ctypes.c_int]),
         "lnship32_rope_store_kv": (ctypes.c_int, [ctypes.POINTER(QkvStoreArgs), c_p]),
         "lnship16_soft_max": (ctypes.c_int, [ctypes.c_int, ctypes.POINTER(SoftMaxArgs), c_p]),
         "lnship32_soft_max": (ctypes.c_int, [ctypes.POINTER(SoftMaxArgs), c_p]),

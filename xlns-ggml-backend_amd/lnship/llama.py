@@ -16,7 +16,10 @@ LNS16 backend computes it, op by op, with F32 at op boundaries:
 
 Fusing Q|K|V and up|gate into one matrix keeps the Monte draw order of the
 separate ops: outputs of a mul_mat take draws in (row, column) order, so the
-fused rows enumerate Q's outputs, then K's, then V's.
+fused rows enumerate Q's outputs, then K's, then V's.  A single-sequence
+decode step outside Monte runs K^T q, soft_max and V p in one launch
+(lnship16_attn_decode, bit-identical to the three ops; fused_attn = False
+runs the three).
 
 With n_seq > 1 the model holds that many independent sequences, each with
 its own KV cache, as llama.cpp's per-sequence KV streams.  A sequence's
@@ -34,8 +37,8 @@ from dataclasses import dataclass
 
 import numpy as np
 
-from . import (BASE, MONTE, LPVIP, SUM32, QkvStoreArgs, check, init, kp, lfsr_advance, lib, mul_mat16_raw,
-               mul_mat32_raw, seed_fields)
+from . import (BASE, MONTE, LPVIP, SUM32, AttnArgs, QkvStoreArgs, check, init, kp, lfsr_advance, lib,
+               mul_mat16_raw, mul_mat32_raw, seed_fields)
 
 KV_PAD = 256   # llama.cpp pads the KV view to 256 cells without flash attention
 
@@ -110,6 +113,9 @@ class LlamaLNS16:
         init()
         self.cfg, self.mode, self.lfsr, self.n_seq = cfg, mode, lfsr, n_seq
         self.torch = torch
+        # decode attention in one launch where the op takes the mode and the cells
+        self.fused_attn = mode != MONTE
+        self._attn_max_kv = lib().lnship_max_row(4, mode)
         dev = torch.device("cuda", torch.cuda.current_device())
         self.dev = dev
         c = cfg
@@ -260,6 +266,9 @@ class LlamaLNS16:
                         st, off)
         check(lib().lnship16_soft_max(self.mode, ctypes.byref(a), self._stream))
 
+    def _attn(self, args):
+        check(lib().lnship16_attn_decode(self.mode, ctypes.byref(args), self._stream))
+
     # -- forward -------------------------------------------------------------------
     def forward(self, T, tokens_dev, pos_dev, n_kv, seq=0, batch=False):
         """Runs T tokens at positions pos_dev[0..T) (device int32) against a
@@ -302,14 +311,21 @@ class LlamaLNS16:
                               self.vslice, seq_ids, self.seq_stride)
             check(L.lnship16_rope_store_kv(ctypes.byref(qs), st))
             Tq = 1 if batch else T   # query rows per sequence
-            # kq[s][h][t][j] = K_s,j . q_s,t (GQA: query head h reads kv head h / (nh / nkv))
-            self._mm(self.kcache[il].data_ptr() + 2 * cbase, P(q), P(kq), hd, n_kv, Tq, ne02=nkv, ne03=nseq,
-                     ne12=nh, ne13=nseq, x_ld=nq, x_slice=hd, w_mstride=c.n_ctx, w_slice=self.kslice)
-            self._softmax(P(kq), (n_kv, Tq, nh, nseq), P(mask), (n_kv, Tq, 1, nseq), 1.0 / math.sqrt(hd), P(kq))
-            # att[s, t][h*hd + d] = sum_j V_s[j][d] p[s][h][t][j]
-            self._mm(self.vcache[il].data_ptr() + 2 * cbase, P(kq), P(att), n_kv, hd, Tq, ne02=nkv, ne03=nseq,
-                     ne12=nh, ne13=nseq, x_ld=n_kv, x_slice=Tq * n_kv, w_slice=self.vslice, dst_ld=nq,
-                     dst_slice=hd)
+            if T == 1 and not batch and self.fused_attn and n_kv <= self._attn_max_kv:
+                # the three nodes below in one launch, bit for bit
+                self._attn(AttnArgs(P(q), P(self.kcache[il], cbase), P(self.vcache[il], cbase), c.n_ctx,
+                                    self.kslice, self.vslice, P(mask), 1.0 / math.sqrt(hd), P(att), nh, nkv, hd,
+                                    n_kv))
+            else:
+                # kq[s][h][t][j] = K_s,j . q_s,t (GQA: query head h reads kv head h / (nh / nkv))
+                self._mm(self.kcache[il].data_ptr() + 2 * cbase, P(q), P(kq), hd, n_kv, Tq, ne02=nkv, ne03=nseq,
+                         ne12=nh, ne13=nseq, x_ld=nq, x_slice=hd, w_mstride=c.n_ctx, w_slice=self.kslice)
+                self._softmax(P(kq), (n_kv, Tq, nh, nseq), P(mask), (n_kv, Tq, 1, nseq), 1.0 / math.sqrt(hd),
+                              P(kq))
+                # att[s, t][h*hd + d] = sum_j V_s[j][d] p[s][h][t][j]
+                self._mm(self.vcache[il].data_ptr() + 2 * cbase, P(kq), P(att), n_kv, hd, Tq, ne02=nkv,
+                         ne03=nseq, ne12=nh, ne13=nseq, x_ld=n_kv, x_slice=Tq * n_kv, w_slice=self.vslice,
+                         dst_ld=nq, dst_slice=hd)
             # after the last layer's attention only the output rows go on
             rows = 1 if last and not batch else T
             r0 = (T - rows) * e
