@@ -1597,6 +1597,8 @@ __global__ __launch_bounds__(k_block) void k_softmax16(sm_args a, dev_tables T) 
 }
 
 // ---- decode attention: KQ, soft_max and KQV of one token in one launch ------
+// head_dim up to which the KQV chain may stop at the last nonzero exp
+constexpr int k_attn_tail_hd = 256;
 struct attn_args {
     const float *q;
     const uint16_t *k, *v;
@@ -1607,32 +1609,33 @@ struct attn_args {
     int hd, n_kv, rep;   // head_dim, cells, query heads per kv head
 };
 
-// One output of a GEMV over weights in the packed layout: the row's groups of
-// eight codes gs codes apart from w, the activations' codes at x in LDS; the
-// K terms in k order, each an xlns16_mul product, added as k_mm16 adds them.
-// The weights of the next PF groups are in flight while a block is added.
+// Terms k0 <= k < k1 of one output of a GEMV over weights in the packed
+// layout (the row's groups of eight codes gs codes apart from w, the
+// activations' codes at x in LDS), each an xlns16_mul product, added into acc
+// in k order as k_mm16 adds them (term 0 starts acc).  The weights of the next
+// PF groups are in flight while a block is added.
 template <int MODE>
-__device__ __forceinline__ uint32_t row_chain(const red16<MODE> &R, const uint16_t *__restrict__ w, int64_t gs,
-                                              const uint16_t *x, int K) {
+__device__ __forceinline__ void row_chain(const red16<MODE> &R, typename red16<MODE>::acc_t &acc, uint32_t &st,
+                                          const uint16_t *__restrict__ w, int64_t gs, const uint16_t *x, int k0,
+                                          int k1) {
     constexpr int PF = 4;
-    const int ng = (K + 7) >> 3;
-    uint32_t st = 0;
-    typename red16<MODE>::acc_t acc{};
+    const int ga = k0 >> 3, gl = (k1 - 1) >> 3;
     auto load = [&](uint4 (&b)[PF], int g0) {
 #pragma unroll
-        for (int p = 0; p < PF; p++) b[p] = *reinterpret_cast<const uint4 *>(w + (int64_t)min(g0 + p, ng - 1) * gs);
+        for (int p = 0; p < PF; p++) b[p] = *reinterpret_cast<const uint4 *>(w + (int64_t)min(g0 + p, gl) * gs);
     };
     auto run = [&](const uint4 (&b)[PF], int g0) {
 #pragma unroll
         for (int p = 0; p < PF; p++) {
             const int g = g0 + p;
-            if (g >= ng) break;
+            if (g > gl) break;
             const uint4 xq = *reinterpret_cast<const uint4 *>(x + 8 * g);
             const uint32_t ww[4] = {b[p].x, b[p].y, b[p].z, b[p].w}, xx[4] = {xq.x, xq.y, xq.z, xq.w};
 #pragma unroll
             for (int u = 0; u < 8; u++) {
                 const int k = 8 * g + u;
-                if (k >= K) break;
+                if (k < k0) continue;
+                if (k >= k1) break;
                 const uint32_t t = x16_mul(half16(ww[u >> 1], u & 1), half16(xx[u >> 1], u & 1));
                 if (k == 0) acc = R.start(t, st);
                 else if constexpr (MODE == LNSHIP_SUM32)
@@ -1641,16 +1644,16 @@ __device__ __forceinline__ uint32_t row_chain(const red16<MODE> &R, const uint16
             }
         }
     };
+    if (k1 <= k0) return;
     uint4 wa[PF], wb[PF];
-    load(wa, 0);
-    for (int g0 = 0; g0 < ng; g0 += 2 * PF) {
+    load(wa, ga);
+    for (int g0 = ga; g0 <= gl; g0 += 2 * PF) {
         load(wb, g0 + PF);
         run(wa, g0);
-        if (g0 + PF >= ng) break;
+        if (g0 + PF > gl) break;
         load(wa, g0 + 2 * PF);
         run(wb, g0 + PF);
     }
-    return R.finish(acc) & 0xffffu;
 }
 
 // One workgroup per query head h (kv head h / rep): the kq scores (one chain
@@ -1670,11 +1673,14 @@ __global__ __launch_bounds__(k_block) void k_attn16(attn_args a, dev_tables T) {
     __shared__ int32_t s_max;
     __shared__ uint32_t s_tot;
     __shared__ int s_last;
+    __shared__ uint32_t s_vmax[k_attn_tail_hd];   // per dim: the largest V log past the last nonzero exp
     const int h = blockIdx.x, kv = h / a.rep;
+    const bool tail_stop = hd <= k_attn_tail_hd;
     if (threadIdx.x == 0) {
         s_max = x16_canon(0xffffu);
         s_last = 0;
     }
+    for (int d = threadIdx.x; d < k_attn_tail_hd; d += blockDim.x) s_vmax[d] = 0;
     for (int k = threadIdx.x; k < hp; k += blockDim.x)
         xq[k] = k < hd ? (uint16_t)x16_from_f32(T.cvt16, a.q[(int64_t)h * hd + k]) : (uint16_t)0;
     __syncthreads();
@@ -1683,7 +1689,10 @@ __global__ __launch_bounds__(k_block) void k_attn16(attn_args a, dev_tables T) {
     const bool has_mask = a.mask != nullptr;
     const uint16_t *kw = a.k + kv * a.k_slice;
     for (int j = threadIdx.x; j < n; j += blockDim.x) {
-        const float f = T.rev16[row_chain<MODE>(R, kw + (int64_t)j * 8, a.k_gs, xq, hd)];
+        uint32_t st = 0;
+        typename red16<MODE>::acc_t acc{};
+        row_chain<MODE>(R, acc, st, kw + (int64_t)j * 8, a.k_gs, xq, 0, hd);
+        const float f = T.rev16[R.finish(acc) & 0xffffu];
         const float mf = has_mask ? a.mask[j] : 0.0f;
         const uint32_t v = x16_from_f32(T.cvt16, f), mk = x16_from_f32(T.cvt16, mf);
         const uint32_t vm = x16_mul(v, sc), va = x16_add_g(T.gauss16, vm, mk);
@@ -1703,21 +1712,60 @@ __global__ __launch_bounds__(k_block) void k_attn16(attn_args a, dev_tables T) {
         }
     }
     __syncthreads();
+    const uint16_t *vw = a.v + kv * a.v_slice;
+    const int n_eff = s_last + 1;
     if (threadIdx.x == 0) {
         // the sum of exps up to the last nonzero one, as k_softmax16 runs it
         uint32_t st = 0;
         typename red16<MODE>::acc_t acc = R.start(c[0], st);
-        const int n_eff = s_last + 1;
         if (n_eff > 1) chain16<red16<MODE>, true>(R, acc, c, 1, n_eff, st);
         s_tot = R.finish(acc) & 0xffffu;
+    } else if (tail_stop && threadIdx.x >= 64 && n_eff < n) {
+        // meanwhile, on the other waves: the largest V log of each dim over
+        // the cells past the last nonzero exp
+        const int g0 = n_eff >> 3, ngt = ((n - 1) >> 3) - g0 + 1, nt = (int)blockDim.x - 64;
+#pragma unroll 4
+        for (int i = (int)threadIdx.x - 64; i < hd * ngt; i += nt) {
+            const int d = i % hd, g = g0 + i / hd;
+            const uint4 q4 = *reinterpret_cast<const uint4 *>(vw + (int64_t)d * 8 + (int64_t)g * a.v_gs);
+            const uint32_t qq[4] = {q4.x, q4.y, q4.z, q4.w};
+            uint32_t m = 0;
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                const int j = 8 * g + u;
+                if (j >= n_eff && j < n) m = max(m, half16(qq[u >> 1], u & 1) & k16_logmask);
+            }
+            atomicMax(&s_vmax[d], m);
+        }
     }
     __syncthreads();
     for (int j = threadIdx.x; j < rs; j += blockDim.x)
         pc[j] = j < n ? (uint16_t)x16_from_f32(T.cvt16, T.rev16[x16_div(c[j], s_tot)]) : (uint16_t)0;
     __syncthreads();
-    const uint16_t *vw = a.v + kv * a.v_slice;
-    for (int d = threadIdx.x; d < hd; d += blockDim.x)
-        a.dst[(int64_t)h * hd + d] = T.rev16[row_chain<MODE>(R, vw + (int64_t)d * 8, a.v_gs, pc, n)];
+    // The att outputs.  Past the last nonzero exp every p has one code (all
+    // those exps are 0), so a product there has the log clamp(v + p - 0x4000)
+    // and the largest is that of the largest V log.  A lane's chain stops at
+    // the last nonzero exp when that largest product lies at or beyond the
+    // adder's essential zero below its sum: every later term would add
+    // nothing (and keep the sum's sign)
+    const uint32_t p_tail = n_eff < n ? pc[n_eff] & k16_logmask : 0u;
+    for (int d = threadIdx.x; d < hd; d += blockDim.x) {
+        const uint16_t *vr = vw + (int64_t)d * 8;
+        uint32_t st = 0;
+        typename red16<MODE>::acc_t acc{};
+        bool rest = n_eff < n;
+        if (rest && tail_stop) {
+            row_chain<MODE>(R, acc, st, vr, a.v_gs, pc, 0, n_eff);
+            const uint32_t tmax = (uint32_t)min(max((int32_t)(s_vmax[d] + p_tail) - (int32_t)k16_one, 0),
+                                                (int32_t)k16_logmask);
+            if constexpr (MODE == LNSHIP_BASE) rest = acc.l < tmax + (uint32_t)k16_esszer + 1u;
+            else rest = acc.l < (tmax << 16) + k32_esszer;   // xlns32 accumulators (sum32, lpvip)
+            if (rest) row_chain<MODE>(R, acc, st, vr, a.v_gs, pc, n_eff, n);
+        } else {
+            row_chain<MODE>(R, acc, st, vr, a.v_gs, pc, 0, n);
+        }
+        a.dst[(int64_t)h * hd + d] = T.rev16[R.finish(acc) & 0xffffu];
+    }
 }
 
 __global__ __launch_bounds__(k_block) void k_softmax32(sm_args a, dev_tables T) {
