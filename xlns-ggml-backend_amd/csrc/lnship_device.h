@@ -24,6 +24,7 @@ struct dev_tables {
     const uint16_t *sig16;
     const int32_t *tab32;
     const int32_t *lds32;   // the LDS image of the xlns32 adder tables (after the descriptors)
+    const int32_t *lds32d;  // the same as the single-chain step reads it (dhi pairs' first words as ksb - th2)
     const uint16_t *lfsr_seq;
     const uint16_t *lfsr_log;
 };

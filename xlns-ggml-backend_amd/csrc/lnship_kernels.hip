@@ -486,10 +486,12 @@ __device__ __forceinline__ uint32_t x32_add_step(const x32_tab &O, acc_ls &a, ui
     // formed here, in the first round trip
     asm volatile("" ::"v"(mx), "v"(nsign), "v"(un));
     __builtin_amdgcn_sched_barrier(0);
-    // x: e on cotransformation lanes, du elsewhere (cap 0 there)
-    const uint32_t xe = min((uint32_t)hp.x + (uint32_t)lo, dsc.z);
-    const uint32_t x = bfi(dsc.w, xe, du);
-    const uint32_t hi = sign_mask(O.ksb - xe, O.one);   // e on sb's far grid
+    // k = ksb - e (this image's dhi pairs hold ksb - th2); x: e on
+    // cotransformation lanes, du elsewhere; the far grid where k < 0 on
+    // cotransformation lanes (lane mask -1) and never elsewhere (mask 0)
+    const uint32_t k = (uint32_t)hp.x - (uint32_t)lo;
+    const uint32_t x = bfi(dsc.w, O.ksb - k, du);
+    const uint32_t hi = sign_mask((uint32_t)max((int32_t)k, (int32_t)dsc.w), O.one);
     const uint32_t sh = bfi(hi, (uint32_t)k32_sb_fsh, dsc.y);
     const uint32_t node = lshl2_add(x >> sh, bfi(hi, O.sbf, dsc.x));
     const int32_t t0 = lds_ld(node), t1 = lds_ld(node + 4);
@@ -685,12 +687,12 @@ __device__ __forceinline__ red16<LNSHIP_MONTE> stage_tables<LNSHIP_MONTE>(const 
     if (threadIdx.x == 0) g[2] = -(1 << 30);
     return red16<LNSHIP_MONTE>{g};
 }
-template <>
-__device__ __forceinline__ red16<LNSHIP_SUM32> stage_tables<LNSHIP_SUM32>(const dev_tables &T, char *lds) {
+// img: one of the two images built at init (lds32_image): the multi-chain
+// step's, or the single-chain step's
+__device__ __forceinline__ red16<LNSHIP_SUM32> stage_x32(const int32_t *img, char *lds) {
     int32_t *t = reinterpret_cast<int32_t *>(lds);
-    // the image built at init (lds32_image): one copy, in one batch of loads
-    // per thread at 256 threads
-    stage_copy<32>(reinterpret_cast<int4 *>(t + kl_dlo), reinterpret_cast<const int4 *>(T.lds32), (kl_end - kl_dlo) / 4);
+    // one copy, in one batch of loads per thread at 256 threads
+    stage_copy<32>(reinterpret_cast<int4 *>(t + kl_dlo), reinterpret_cast<const int4 *>(img), (kl_end - kl_dlo) / 4);
     // descriptor of key = (opposite signs) << 8 | (d >> 23): (origin, grid
     // shift, cap of e, lane mask).  Direct keys read the interpolation at d:
     // the sb / db table of d's binade, or the zero pair with a shift that
@@ -725,8 +727,19 @@ __device__ __forceinline__ red16<LNSHIP_SUM32> stage_tables<LNSHIP_SUM32>(const 
     return red16<LNSHIP_SUM32>{x32_origins(t)};
 }
 template <>
+__device__ __forceinline__ red16<LNSHIP_SUM32> stage_tables<LNSHIP_SUM32>(const dev_tables &T, char *lds) {
+    return stage_x32(T.lds32, lds);
+}
+template <>
 __device__ __forceinline__ red16<LNSHIP_LPVIP> stage_tables<LNSHIP_LPVIP>(const dev_tables &, char *) {
     return red16<LNSHIP_LPVIP>{};
+}
+// the tables of a kernel whose xlns32 additions are single-chain steps
+// (x32_add_step) when DEC, else multi-chain ones (x32_add_ls)
+template <int MODE, bool DEC>
+__device__ __forceinline__ red16<MODE> stage_for(const dev_tables &T, char *lds) {
+    if constexpr (MODE == LNSHIP_SUM32 && DEC) return stage_x32(T.lds32d, lds);
+    else return stage_tables<MODE>(T, lds);
 }
 
 template <int MODE>
@@ -816,7 +829,7 @@ __global__ __launch_bounds__(k_block * CG) void k_mm16(mm_args16 a, dev_tables T
     extern __shared__ __align__(16) char lds[];
     // a widened launch: the workgroups between the working ones leave at once
     if (blockIdx.x & ((1u << a.xcd_sh) - 1u)) return;
-    const red16<MODE> R = stage_tables<MODE>(T, lds);
+    const red16<MODE> R = stage_for<MODE, NC == 1>(T, lds);
     // CG column groups of k_block lanes each share the staged tables: group
     // c takes columns [nw + c NC, nw + (c + 1) NC) of the same k_block rows
     const int cg = CG == 1 ? 0 : (int)(threadIdx.x / k_block);
@@ -1132,7 +1145,7 @@ template <int NC, int PF, int CG>
 __global__ __launch_bounds__(k_block * CG) void k_mm32(mm_args32 a, dev_tables T) {
     extern __shared__ __align__(16) char lds[];
     if (blockIdx.x & ((1u << a.xcd_sh) - 1u)) return;   // as in k_mm16
-    const red16<LNSHIP_SUM32> R = stage_tables<LNSHIP_SUM32>(T, lds);
+    const red16<LNSHIP_SUM32> R = stage_for<LNSHIP_SUM32, NC == 1>(T, lds);
     __syncthreads();
     const int cg = CG == 1 ? 0 : (int)(threadIdx.x / k_block);
     const int64_t m = (int64_t)(blockIdx.x >> a.xcd_sh) * k_block + (threadIdx.x % k_block);
@@ -1665,7 +1678,7 @@ __device__ __forceinline__ void row_chain(const red16<MODE> &R, typename red16<M
 template <int MODE>
 __global__ __launch_bounds__(k_block) void k_attn16(attn_args a, dev_tables T) {
     extern __shared__ __align__(16) char lds[];
-    const red16<MODE> R = stage_tables<MODE>(T, lds);
+    const red16<MODE> R = stage_for<MODE, true>(T, lds);
     const int hd = a.hd, n = a.n_kv, hp = (hd + 7) & ~7, rs = (n + 7) & ~7;
     uint16_t *xq = reinterpret_cast<uint16_t *>(lds + mm_xl_offset<MODE>());   // the query's codes
     uint16_t *c = xq + hp;                                                     // scores, then exps
@@ -2183,7 +2196,7 @@ template <int FORM>
 __global__ __launch_bounds__(k_block) void k_x32_add_lds(const uint32_t *__restrict__ x, const uint32_t *__restrict__ y,
                                                          uint32_t *__restrict__ out, int64_t n, dev_tables T) {
     extern __shared__ __align__(16) char lds[];
-    const red16<LNSHIP_SUM32> R = stage_tables<LNSHIP_SUM32>(T, lds);
+    const red16<LNSHIP_SUM32> R = stage_for<LNSHIP_SUM32, FORM == 1>(T, lds);
     __syncthreads();
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)blockDim.x * gridDim.x) {
         const uint32_t a = x[i], b = y[i];
@@ -2636,8 +2649,9 @@ const void *lnship_host_table(const char *name, size_t *bytes) {
 // dh = 0, else -dhi[dh] (db rises with the distance and dh << 12 > dl, so
 // -dhi[dh] < -dlo[dl]).  Then the interpolation tables sb, sbf (extended),
 // db, dbf, and a zero pair.
-// Returns false when the tables break a bound the layout relies on.
-static bool lds32_image(const int32_t *tab, std::vector<int32_t> &img) {
+// Returns false when the tables break a bound the layout relies on.  dec:
+// the single-chain step's image, whose dhi pairs hold ksb - th2 in place of th2.
+static bool lds32_image(const int32_t *tab, std::vector<int32_t> &img, bool dec) {
     // (word kl_dlo of the LDS copy is word 0 of the image)
     img.assign(kl_end - kl_dlo, 0);
     int32_t *w = img.data() - kl_dlo;
@@ -2645,7 +2659,8 @@ static bool lds32_image(const int32_t *tab, std::vector<int32_t> &img) {
     w[kl_dlo] = (int32_t)k32_co_l0;
     for (int i = 0; i < k32_co_n; i++) {
         const int32_t h = tab[k32_off_dhi + i];
-        w[kl_dhi + 2 * i] = i == 0 ? (int32_t)k32_co_h0 : h + (i << k32_co_sh);
+        const int32_t th2 = i == 0 ? (int32_t)k32_co_h0 : h + (i << k32_co_sh);
+        w[kl_dhi + 2 * i] = dec ? (int32_t)(k32_sb_end - 1u) - th2 : th2;
         // dh = 0: above every -dlo[dl], so the minimum takes -dlo[dl] there,
         // and -dhi[dh] elsewhere (db rises with the distance, dh << 12 > dl)
         w[kl_dhi + 2 * i + 1] = i == 0 ? 0x7fffffff : -h;
@@ -2662,10 +2677,11 @@ static bool lds32_image(const int32_t *tab, std::vector<int32_t> &img) {
     // and past the essential zero on the sentinel lanes; -dhi below -dlo
     int64_t nlo_min = INT64_MAX, nlo_max = INT64_MIN, th2_min = INT64_MAX, th2_max = INT64_MIN, nth_max = INT64_MIN;
     for (int i = 1; i < k32_co_n; i++) {
+        const int64_t th2 = dec ? (int64_t)(k32_sb_end - 1u) - w[kl_dhi + 2 * i] : w[kl_dhi + 2 * i];
         nlo_min = std::min<int64_t>(nlo_min, w[kl_dlo + i]);
         nlo_max = std::max<int64_t>(nlo_max, w[kl_dlo + i]);
-        th2_min = std::min<int64_t>(th2_min, w[kl_dhi + 2 * i]);
-        th2_max = std::max<int64_t>(th2_max, w[kl_dhi + 2 * i]);
+        th2_min = std::min<int64_t>(th2_min, th2);
+        th2_max = std::max<int64_t>(th2_max, th2);
         nth_max = std::max<int64_t>(nth_max, w[kl_dhi + 2 * i + 1]);
     }
     const int64_t seg = (int64_t)k32_co_cancel - (1 << k32_sb_fsh), ess = k32_esszer;
@@ -2692,9 +2708,12 @@ int lnship_init(void) {
     if (int rc = upload(g_host->tab32, (size_t)k32_tab_n, &T.tab32)) return rc;
     {
         std::vector<int32_t> img;
-        if (!lds32_image(g_host->tab32, img))
+        if (!lds32_image(g_host->tab32, img, false))
             return fail(LNSHIP_EINVAL, "init: xlns32 tables outside the bounds of their LDS layout%s");
         if (int rc = upload(img.data(), img.size(), &T.lds32)) return rc;
+        if (!lds32_image(g_host->tab32, img, true))
+            return fail(LNSHIP_EINVAL, "init: xlns32 tables outside the bounds of their LDS layout%s");
+        if (int rc = upload(img.data(), img.size(), &T.lds32d)) return rc;
     }
     if (int rc = upload(g_host->lfsr_seq, 65536, &T.lfsr_seq)) return rc;
     if (int rc = upload(g_host->lfsr_log, 65536, &T.lfsr_log)) return rc;
