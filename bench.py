@@ -35,6 +35,8 @@ def parse():
     ap.add_argument("--cpu-tokens", type=int, default=3, help="decode tokens of the CPU baseline sample")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-graph", action="store_true", help="decode eagerly instead of replaying a HIP graph")
+    ap.add_argument("--split-rms", action="store_true",
+                    help="sum32 decode: rms_norm + MUL and the mul_mat after them as separate launches")
     ap.add_argument("--decode-only", action="store_true",
                     help="only the prompt and the decode steps, then one recorded eager step: prints the decode "
                          "launches' algorithmic bytes (for HBM counter runs; with --prompt 1 every lnship16_mul_mat "
@@ -465,6 +467,7 @@ def main():
     t0 = time.perf_counter()
     weights = llama.synthetic_weights(cfg, seed=1234, std=0.02)
     model = llama.LlamaLNS16(cfg, weights, mode=mode)
+    model.fused_rms = model.fused_rms and not args.split_rms
     torch.cuda.synchronize()
     t_setup = time.perf_counter() - t0
 

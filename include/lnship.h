@@ -147,6 +147,17 @@ int lnship16_rms_norm_mul(int mode, const float *src, const float *w, float *dst
                           void *stream);
 int lnship32_rms_norm_mul(const float *src, const float *w, float *dst, int64_t ncols, int64_t nrows, float eps,
                           void *stream);
+/* RMS_NORM, the MUL by its norm weight row and the MUL_MAT that reads the
+ * product, for one activation row (a decode step): dst[M] = W h with
+ * h = rms_norm(x[K]) * norm_w[K] (lns_rms_norm and lns_mul,
+ * src/lns-ops.cpp:468-530 and :701-736; then lns_mul_mat, :293-384), W
+ * packed by lnship16_pack (K x M, default layout).  Equal, bit for bit, to
+ * lnship16_rms_norm_mul followed by lnship16_mul_mat.  The mul_mat's chains
+ * start on h formed from a predicted scale while the rms sum's chain runs
+ * beside them, and run again when the predicted scale was wrong.  sum32
+ * only (LNSHIP_EINVAL otherwise). */
+int lnship16_rms_norm_mul_mat(int mode, const float *x, const float *norm_w, float eps, const void *w, float *dst,
+                              int64_t K, int64_t M, void *stream);
 
 /* ---- SOFT_MAX (kernel_set::soft_max, :136; soft_max_args :62-71) --------
  * dst = softmax(src * scale + mask) over rows of src_ne[0] (lns_soft_max,
@@ -323,6 +334,12 @@ int lnship_lpvip_db_range(uint32_t d0, uint32_t n, int32_t *out, void *stream);
  * src/lns16-sum32.h:59-198 configures xlnscpp (xlns32_alt).  No counterpart
  * in the reference. */
 int lnship32_add_lds(int form, const uint32_t *x, const uint32_t *y, uint32_t *out, int64_t n, void *stream);
+
+/* Test hook: adds skew to the scale code lnship16_rms_norm_mul_mat predicts
+ * (0 by default), so that a test can make the prediction wrong and check
+ * the rerun; returns the previous value.  Host-side only; takes effect at
+ * the next launch.  No counterpart in the reference. */
+int lnship_test_rms_predict_skew(int skew);
 
 /* Host: the (cos, sin) floats lns_rope uses for positions 0..n_pos-1 (the
  * float recurrence t *= powf(freq_base, -2/n_dims) per pair, cosf / sinf;

@@ -782,6 +782,11 @@ struct mm_args16 {
     int64_t ids_t, x_bcast, n_w;
     unsigned long long *err;
     const float *resid;   // non-null: dst = resid + W x (the graph's ADD), resid laid out as dst
+    // k_mm16_rms: x = rms_norm(xf) * norm (norm: K floats), epsilon eps; skew
+    // is added to the predicted scale code (0; a test hook sets it)
+    const float *norm;
+    float eps;
+    uint32_t skew;
     // set by the launcher: the grid is 2^xcd_sh times wider than the work;
     // workgroup x works (as block x >> xcd_sh) iff x is a multiple of 2^xcd_sh
     uint32_t xcd_sh;
@@ -824,81 +829,18 @@ constexpr int k_xl_pad = 8 * 16;
 
 __device__ __forceinline__ uint32_t half16(uint32_t w, int hi) { return hi ? (w >> 16) : (w & 0xffffu); }
 
-template <int MODE, int NC, int PF, bool XL, int CG>
-__global__ __launch_bounds__(k_block * CG) void k_mm16(mm_args16 a, dev_tables T) {
-    extern __shared__ __align__(16) char lds[];
-    // a widened launch: the workgroups between the working ones leave at once
-    if (blockIdx.x & ((1u << a.xcd_sh) - 1u)) return;
-    const red16<MODE> R = stage_for<MODE, NC == 1>(T, lds);
-    // CG column groups of k_block lanes each share the staged tables: group
-    // c takes columns [nw + c NC, nw + (c + 1) NC) of the same k_block rows
-    const int cg = CG == 1 ? 0 : (int)(threadIdx.x / k_block);
-    const int64_t nw = (int64_t)blockIdx.y * (NC * CG);
-    const int64_t n0 = nw + (int64_t)cg * NC;
-    const int64_t z = blockIdx.z;
-    const int64_t i12 = z % a.ne12, i13 = z / a.ne12;
-    const int ncw = (int)min<int64_t>(NC * CG, a.N - nw);
-    const int nc = (int)max<int64_t>(0, min<int64_t>(NC, a.N - n0));
+// The K-long chains of lane m (output row m of slice z) over columns
+// n0 .. n0 + nc: the weights from HBM, the activations from the LDS rows at
+// xl (XL) or the converted rows in scratch; each column's finished
+// accumulator (an xlns16 code) into res.
+template <int MODE, int NC, int PF, bool XL>
+__device__ __forceinline__ void mm16_chains(const mm_args16 &a, const dev_tables &T, const red16<MODE> &R,
+                                            const uint16_t *xl, int64_t m, int64_t z, int64_t zw, int64_t zx,
+                                            int64_t n0, int nc, uint32_t (&res)[NC]) {
     const int kp = (int)a.kp;
-    int64_t zw, zx;
-    const bool slice_ok = mm_slices(a, z, i12, i13, zw, zx);
-    uint16_t *xl = reinterpret_cast<uint16_t *>(lds + mm_xl_offset<MODE>());
-    if (XL) {
-        // columns past N and k past K hold xlns16 zero
-        // in batches of eight per thread: the loads, then the conversion
-        // table's lookups, then the stores (two memory round trips a batch)
-        const float *xf = a.xf + zx * a.x_slice + nw * a.x_ld;
-        constexpr int nt = k_block * CG, B = 8;
-        const int kl = (int)a.K - 1;
-        for (int j = 0; j < NC * CG; j++) {
-            if (kl < 0) {
-                for (int k = threadIdx.x; k < kp; k += nt) xl[j * kp + k] = 0;
-                continue;
-            }
-            // loads and lookups stay in the row; only the stores are bounded
-            const float *row = xf + (int64_t)min(j, ncw - 1) * a.x_ld;
-            for (int k0 = threadIdx.x; k0 < kp; k0 += B * nt) {
-                float v[B];
-#pragma unroll
-                for (int q = 0; q < B; q++) v[q] = row[min(k0 + q * nt, kl)];
-                uint32_t c[B];
-#pragma unroll
-                for (int q = 0; q < B; q++) c[q] = x16_from_f32(T.cvt16, v[q]);
-                // every code in a register before the bounded stores: none of
-                // the batch's loads moves into a store's branch
-#pragma unroll
-                for (int q = 0; q < B; q++) asm volatile("" ::"v"(c[q]));
-#pragma unroll
-                for (int q = 0; q < B; q++) {
-                    const int k = k0 + q * nt;
-                    if (k < kp) xl[j * kp + k] = (j < ncw && k <= kl) ? (uint16_t)c[q] : (uint16_t)0;
-                }
-            }
-        }
-        xl += cg * NC * kp;
-    }
-    __syncthreads();
-
-    const int64_t m = (int64_t)(blockIdx.x >> a.xcd_sh) * k_block + (threadIdx.x % k_block);
-    if (m >= a.M || nc == 0 || !slice_ok) return;
     const uint16_t *ws = a.w + zw * a.w_slice + m * 8;
     const uint16_t *xs = a.x + (zx * a.N + n0) * a.kp;
     const int64_t wstride = a.w_mstride * 8;   // between consecutive groups of 8 k
-    float *ds = a.dst + z * a.dst_slice + n0 * a.dst_ld + m;
-    // output j, with the fused ADD of the residual when there is one: the
-    // F32 result and the residual through xlns16, added, back to F32 (the
-    // ADD node's arithmetic)
-    auto put = [&](int j, float y) {
-        const int64_t o = (ds - a.dst) + (int64_t)j * a.dst_ld;
-        if (a.resid)
-            y = T.rev16[x16_add_g(T.gauss16, x16_from_f32(T.cvt16, y), x16_from_f32(T.cvt16, a.resid[o]))];
-        a.dst[o] = y;
-    };
-    if (a.K == 0) {
-        for (int j = 0; j < nc; j++) put(j, T.rev16[0]);
-        return;
-    }
-
     typename red16<MODE>::acc_t acc[NC]{};
     uint32_t st[NC];
 #pragma unroll
@@ -1118,8 +1060,86 @@ __global__ __launch_bounds__(k_block * CG) void k_mm16(mm_args16 a, dev_tables T
         }
     }
 #pragma unroll
+    for (int j = 0; j < NC; j++) res[j] = R.finish(acc[j]) & 0xffffu;
+}
+
+template <int MODE, int NC, int PF, bool XL, int CG>
+__global__ __launch_bounds__(k_block * CG) void k_mm16(mm_args16 a, dev_tables T) {
+    extern __shared__ __align__(16) char lds[];
+    // a widened launch: the workgroups between the working ones leave at once
+    if (blockIdx.x & ((1u << a.xcd_sh) - 1u)) return;
+    const red16<MODE> R = stage_for<MODE, NC == 1>(T, lds);
+    // CG column groups of k_block lanes each share the staged tables: group
+    // c takes columns [nw + c NC, nw + (c + 1) NC) of the same k_block rows
+    const int cg = CG == 1 ? 0 : (int)(threadIdx.x / k_block);
+    const int64_t nw = (int64_t)blockIdx.y * (NC * CG);
+    const int64_t n0 = nw + (int64_t)cg * NC;
+    const int64_t z = blockIdx.z;
+    const int64_t i12 = z % a.ne12, i13 = z / a.ne12;
+    const int ncw = (int)min<int64_t>(NC * CG, a.N - nw);
+    const int nc = (int)max<int64_t>(0, min<int64_t>(NC, a.N - n0));
+    const int kp = (int)a.kp;
+    int64_t zw, zx;
+    const bool slice_ok = mm_slices(a, z, i12, i13, zw, zx);
+    uint16_t *xl = reinterpret_cast<uint16_t *>(lds + mm_xl_offset<MODE>());
+    if (XL) {
+        // columns past N and k past K hold xlns16 zero
+        // in batches of eight per thread: the loads, then the conversion
+        // table's lookups, then the stores (two memory round trips a batch)
+        const float *xf = a.xf + zx * a.x_slice + nw * a.x_ld;
+        constexpr int nt = k_block * CG, B = 8;
+        const int kl = (int)a.K - 1;
+        for (int j = 0; j < NC * CG; j++) {
+            if (kl < 0) {
+                for (int k = threadIdx.x; k < kp; k += nt) xl[j * kp + k] = 0;
+                continue;
+            }
+            // loads and lookups stay in the row; only the stores are bounded
+            const float *row = xf + (int64_t)min(j, ncw - 1) * a.x_ld;
+            for (int k0 = threadIdx.x; k0 < kp; k0 += B * nt) {
+                float v[B];
+#pragma unroll
+                for (int q = 0; q < B; q++) v[q] = row[min(k0 + q * nt, kl)];
+                uint32_t c[B];
+#pragma unroll
+                for (int q = 0; q < B; q++) c[q] = x16_from_f32(T.cvt16, v[q]);
+                // every code in a register before the bounded stores: none of
+                // the batch's loads moves into a store's branch
+#pragma unroll
+                for (int q = 0; q < B; q++) asm volatile("" ::"v"(c[q]));
+#pragma unroll
+                for (int q = 0; q < B; q++) {
+                    const int k = k0 + q * nt;
+                    if (k < kp) xl[j * kp + k] = (j < ncw && k <= kl) ? (uint16_t)c[q] : (uint16_t)0;
+                }
+            }
+        }
+        xl += cg * NC * kp;
+    }
+    __syncthreads();
+
+    const int64_t m = (int64_t)(blockIdx.x >> a.xcd_sh) * k_block + (threadIdx.x % k_block);
+    if (m >= a.M || nc == 0 || !slice_ok) return;
+    float *ds = a.dst + z * a.dst_slice + n0 * a.dst_ld + m;
+    // output j, with the fused ADD of the residual when there is one: the
+    // F32 result and the residual through xlns16, added, back to F32 (the
+    // ADD node's arithmetic)
+    auto put = [&](int j, float y) {
+        const int64_t o = (ds - a.dst) + (int64_t)j * a.dst_ld;
+        if (a.resid)
+            y = T.rev16[x16_add_g(T.gauss16, x16_from_f32(T.cvt16, y), x16_from_f32(T.cvt16, a.resid[o]))];
+        a.dst[o] = y;
+    };
+    if (a.K == 0) {
+        for (int j = 0; j < nc; j++) put(j, T.rev16[0]);
+        return;
+    }
+
+    uint32_t res[NC];
+    mm16_chains<MODE, NC, PF, XL>(a, T, R, xl, m, z, zw, zx, n0, nc, res);
+#pragma unroll
     for (int j = 0; j < NC; j++)
-        if (j < nc) put(j, T.rev16[R.finish(acc[j]) & 0xffffu]);
+        if (j < nc) put(j, T.rev16[res[j]]);
 }
 
 // xlns32 (the LNS32 backend): plain sequential xlns32_add
@@ -1458,6 +1478,102 @@ __global__ __launch_bounds__(k_block) void k_rms32(const float *__restrict__ src
                 dst[r0 * ncols + e0 + q * nt] = y;
             }
     }
+}
+
+// ---- RMS_NORM -> MUL -> MUL_MAT, one activation row, sum32 ----------------------
+// The decode graph's h = rms_norm(x) * norm followed by W h, in one launch.
+// The mul_mat's chains read h, and h needs the scale, which the rms sum's
+// K-step chain gives; so the chains would wait for that chain.  Here they
+// start at once, from h formed with a predicted scale, while one lane of a
+// fourth wave runs the sum's chain.  The scale is an xlns16 code: the sum32
+// sum of the squares, narrowed to xlns16 (1/128 of a binade), then mean,
+// epsilon, square root and reciprocal.  The prediction sums the squares'
+// values in double and rounds the log to the nearest xlns16 step: that is
+// the narrowed sum unless the sum lies within the xlns32 chain's error of a
+// rounding boundary.  When the chain's scale differs from the predicted one,
+// h is formed again from it and the chains run again, so the output is that
+// of the three nodes in every case.
+constexpr int k_rms_mm_rows = 3 * 64;   // chain lanes per workgroup (waves 0-2; wave 3 sums)
+
+template <int PF>
+__global__ __launch_bounds__(k_block) void k_mm16_rms(mm_args16 a, dev_tables T) {
+    static_assert(k_block == k_rms_mm_rows + 64, "three chain waves and the sum's wave");
+    extern __shared__ __align__(16) char lds[];
+    if (blockIdx.x & ((1u << a.xcd_sh) - 1u)) return;   // as in k_mm16
+    const red16<LNSHIP_SUM32> R = stage_for<LNSHIP_SUM32, true>(T, lds);
+    const int K = (int)a.K, kp = (int)a.kp;
+    uint16_t *xl = reinterpret_cast<uint16_t *>(lds + mm_xl_offset<LNSHIP_SUM32>());   // h, as the chains read it
+    uint16_t *sq = xl + kp + k_xl_pad / 2;                                              // the squares of x
+    __shared__ double s_part[k_block / 64];
+    __shared__ uint32_t s_inv[2];   // the predicted scale, the chain's
+    // the squares of x's codes into LDS (the sum's addends), their values
+    // summed per wave
+    double part = 0.0;
+    for (int k = threadIdx.x; k < kp; k += k_block) {
+        uint32_t q = 0;
+        if (k < K) {
+            const uint32_t c = x16_from_f32(T.cvt16, a.xf[k]);
+            q = x16_mul(c, c);
+            part += exp2(((double)(int)(q & k16_logmask) - (double)k16_one) * (1.0 / 128.0));
+        }
+        sq[k] = (uint16_t)q;
+    }
+    for (int o = 32; o > 0; o >>= 1) part += __shfl_xor(part, o);
+    if ((threadIdx.x & 63) == 0) s_part[threadIdx.x >> 6] = part;
+    __syncthreads();
+    // the scale from the narrowed sum (the rms_norm node's tail, as k_rms16)
+    auto scale_of = [&](uint32_t sum) {
+        const uint32_t mean = x16_mul(sum, x16_from_f32(T.cvt16, 1.0f / (float)K));
+        return x16_recip(x16_sqrt(x16_add_g(T.gauss16, mean, x16_from_f32(T.cvt16, a.eps))));
+    };
+    if (threadIdx.x == 0) {
+        double S = 0.0;
+        for (int i = 0; i < k_block / 64; i++) S += s_part[i];
+        // the nearest xlns16 code of S, within the code range
+        const double l = S > 0.0 ? floor(log2(S) * 128.0 + 0.5) + (double)k16_one : 0.0;
+        const uint32_t sum = (uint32_t)fmin(fmax(l, 0.0), (double)k16_logmask);
+        s_inv[0] = (scale_of(sum) + a.skew) & 0xffffu;
+    }
+    __syncthreads();
+    // h = the MUL node's output from the rms_norm node's, each through F32
+    // as between graph nodes, then into xlns16 as the mul_mat converts its
+    // activations (k past K: zero)
+    auto stage_h = [&](uint32_t inv) {
+        for (int k = threadIdx.x; k < kp; k += k_block) {
+            uint32_t h = 0;
+            if (k < K) {
+                const float y = T.rev16[x16_mul(x16_from_f32(T.cvt16, a.xf[k]), inv)];
+                h = x16_from_f32(T.cvt16,
+                                 T.rev16[x16_mul(x16_from_f32(T.cvt16, y), x16_from_f32(T.cvt16, a.norm[k]))]);
+            }
+            xl[k] = (uint16_t)h;
+        }
+    };
+    uint32_t inv = s_inv[0];
+    stage_h(inv);
+    __syncthreads();
+    const int64_t m = (int64_t)(blockIdx.x >> a.xcd_sh) * k_rms_mm_rows + threadIdx.x;
+    const bool active = threadIdx.x < k_rms_mm_rows && m < a.M;
+    uint32_t res[1] = {0};
+    // pass 0 with the predicted scale; a second pass only when the chain's
+    // scale differs (every thread reads the same two words after the barrier)
+    for (int pass = 0;; pass++) {
+        if (active) {
+            mm16_chains<LNSHIP_SUM32, 1, PF, true>(a, T, R, xl, m, 0, 0, 0, 0, 1, res);
+        } else if (pass == 0 && threadIdx.x == k_rms_mm_rows) {
+            uint32_t st = 0;
+            typename red16<LNSHIP_SUM32>::acc_t acc = R.start(0u, st);
+            chain16<red16<LNSHIP_SUM32>, true>(R, acc, sq, 0, K, st);   // squares: positive
+            s_inv[1] = scale_of(R.finish(acc) & 0xffffu);
+        }
+        __syncthreads();
+        const uint32_t want = s_inv[1];
+        if (want == inv) break;
+        inv = want;
+        stage_h(inv);
+        __syncthreads();
+    }
+    if (active) a.dst[m] = T.rev16[res[0]];
 }
 
 // ---- SOFT_MAX -------------------------------------------------------------------
@@ -3067,6 +3183,44 @@ int lnship16_rms_norm_mul(int mode, const float *src, const float *w, float *dst
                           void *stream) {
     if (!w) return fail(LNSHIP_EINVAL, "rms_norm_mul: null weight row%s");
     return rms16_common(mode, src, w, dst, ncols, nrows, eps, monte_seed, monte_state, monte_offset, stream);
+}
+
+// added to k_mm16_rms's predicted scale code (lnship_test_rms_predict_skew)
+static uint32_t g_rms_skew = 0;
+
+int lnship_test_rms_predict_skew(int skew) {
+    const int prev = (int)g_rms_skew;
+    g_rms_skew = (uint32_t)skew;
+    return prev;
+}
+
+int lnship16_rms_norm_mul_mat(int mode, const float *x, const float *norm_w, float eps, const void *w, float *dst,
+                              int64_t K, int64_t M, void *stream) {
+    device_state *s = state();
+    if (!s) return LNSHIP_ENOINIT;
+    if (mode != LNSHIP_SUM32)
+        return fail(LNSHIP_EINVAL, "rms_norm_mul_mat: sum32 only (other modes: lnship16_rms_norm_mul, then "
+                                   "lnship16_mul_mat)%s");
+    if (!x || !norm_w || !w || !dst || K < 1 || M < 0) return fail(LNSHIP_EINVAL, "rms_norm_mul_mat: bad argument%s");
+    if (M == 0) return 0;
+    const int64_t kp = (K + 7) & ~(int64_t)7;
+    constexpr int PF = 8;
+    const int64_t lds = mm_xl_offset<LNSHIP_SUM32>() + 2 * (kp * 2) + k_xl_pad;
+    if (lds > k_lds_bytes - 1024) return fail(LNSHIP_ERANGE, "rms_norm_mul_mat: row too long for LDS%s");
+    if ((uint64_t)M * 16 * PF + (uint64_t)M * 16 > 0xffffffffu)
+        return fail(LNSHIP_ERANGE, "rms_norm_mul_mat: weight rows too long for 32-bit block offsets%s");
+    if (int rc = set_lds(k_mm16_rms<PF>, (int)lds)) return rc;
+    mm_args16 m{(const uint16_t *)w, nullptr, x, dst, K, kp, M, 1, K, K, 1, 1, 1, 1, M, kp * M, M, M, 0, nullptr, 0};
+    m.norm = norm_w;
+    m.eps = eps;
+    m.skew = g_rms_skew;
+    const uint64_t wgs = (uint64_t)((M + k_rms_mm_rows - 1) / k_rms_mm_rows);
+    if (wgs > 0x7fffffffu) return fail(LNSHIP_ERANGE, "rms_norm_mul_mat: grid too large%s");
+    m.xcd_sh = xcd_shift(wgs, s->cus);
+    hipLaunchKernelGGL(k_mm16_rms<PF>, dim3((unsigned)(wgs << m.xcd_sh)), dim3(k_block), (int)lds,
+                       (hipStream_t)stream, m, s->T);
+    LNSHIP_HIP(hipGetLastError());
+    return 0;
 }
 
 static int rms32_common(const float *src, const float *w, float *dst, int64_t ncols, int64_t nrows, float eps,

@@ -94,6 +94,8 @@ def lib():
         "lnship16_rms_norm_mul": (ctypes.c_int, [ctypes.c_int, c_p, c_p, c_p, c_i64, c_i64, ctypes.c_float,
                                                  ctypes.c_uint16, c_p, ctypes.c_uint64, c_p]),
         "lnship32_rms_norm_mul": (ctypes.c_int, [c_p, c_p, c_p, c_i64, c_i64, ctypes.c_float, c_p]),
+        "lnship16_rms_norm_mul_mat": (ctypes.c_int, [ctypes.c_int, c_p, c_p, ctypes.c_float, c_p, c_p, c_i64,
+                                                     c_i64, c_p]),
         "lnship16_rope_store_kv": (ctypes.c_int, [ctypes.POINTER(QkvStoreArgs), c_p]),
         "lnship16_attn_decode": (ctypes.c_int, [ctypes.c_int, ctypes.POINTER(AttnArgs), c_p]),
         "lnship_max_row": (c_i64, [ctypes.c_int, ctypes.c_int]),
@@ -117,6 +119,7 @@ def lib():
         "lnship_index_error": (ctypes.c_int, [ctypes.POINTER(c_i64), c_p]),
         "lnship_lpvip_db_range": (ctypes.c_int, [ctypes.c_uint32, ctypes.c_uint32, c_p, c_p]),
         "lnship32_add_lds": (ctypes.c_int, [ctypes.c_int, c_p, c_p, c_p, c_i64, c_p]),
+        "lnship_test_rms_predict_skew": (ctypes.c_int, [ctypes.c_int]),
         "lnship16_add": (ctypes.c_int, [c_p, c_p, c_i64, c_i64, c_p, c_p]),
         "lnship16_mul": (ctypes.c_int, [c_p, c_p, c_i64, c_i64, c_p, c_p]),
         "lnship16_swiglu": (ctypes.c_int, [c_p, c_i64, c_p, c_i64, c_p, c_i64, c_i64, c_p]),

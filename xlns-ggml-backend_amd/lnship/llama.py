@@ -19,7 +19,9 @@ separate ops: outputs of a mul_mat take draws in (row, column) order, so the
 fused rows enumerate Q's outputs, then K's, then V's.  A single-sequence
 decode step outside Monte runs K^T q, soft_max and V p in one launch
 (lnship16_attn_decode, bit-identical to the three ops; fused_attn = False
-runs the three).
+runs the three).  A single-row sum32 step runs each rms_norm, its norm MUL
+and the mul_mat that reads them in one launch (lnship16_rms_norm_mul_mat,
+bit-identical to the three; fused_rms = False runs them apart).
 
 With n_seq > 1 the model holds that many independent sequences, each with
 its own KV cache, as llama.cpp's per-sequence KV streams.  A sequence's
@@ -115,6 +117,9 @@ class LlamaLNS16:
         self.torch = torch
         # decode attention in one launch where the op takes the mode and the cells
         self.fused_attn = mode != MONTE
+        # sum32, one row: rms_norm, the norm MUL and the mul_mat after them in
+        # one launch (lnship16_rms_norm_mul_mat, bit-identical to the three)
+        self.fused_rms = mode == SUM32
         self._attn_max_kv = lib().lnship_max_row(4, mode)
         dev = torch.device("cuda", torch.cuda.current_device())
         self.dev = dev
@@ -266,6 +271,16 @@ class LlamaLNS16:
                         st, off)
         check(lib().lnship16_soft_max(self.mode, ctypes.byref(a), self._stream))
 
+    def _rms_mm(self, x_ptr, wn_ptr, w, h_ptr, dst_ptr, K, M, T):
+        """dst = W (rms_norm(x) * wn) for T rows of K: for one sum32 row in one
+        launch, else rms_norm + MUL into h, then the mul_mat."""
+        if T == 1 and self.fused_rms:
+            check(lib().lnship16_rms_norm_mul_mat(self.mode, x_ptr, wn_ptr, self.cfg.eps, ctypes.c_void_p(w), dst_ptr,
+                                                  K, M, self._stream))
+        else:
+            self._rms_mul(x_ptr, wn_ptr, h_ptr, K, T)
+            self._mm(w, h_ptr, dst_ptr, K, M, T)
+
     def _attn(self, args):
         check(lib().lnship16_attn_decode(self.mode, ctypes.byref(args), self._stream))
 
@@ -303,8 +318,7 @@ class LlamaLNS16:
         check(L.lnship_causal_mask(P(pos_dev), T, n_kv, P(mask), st))
         for il, W in enumerate(self.layers):
             last = il == c.n_layer - 1
-            self._rms_mul(P(x), P(W["attn_norm"]), P(h), e, T)
-            self._mm(W["wqkv"].data_ptr(), P(h), P(qkv), e, nqkv, T)
+            self._rms_mm(P(x), P(W["attn_norm"]), W["wqkv"].data_ptr(), P(h), P(qkv), e, nqkv, T)
             # rope(q) and the K / V cache stores (k rotated) in one launch
             qs = QkvStoreArgs(P(qkv), nqkv, P(pos_dev), T, nh, nkv, hd, hd, P(self.cos_sin), P(q),
                               P(self.kcache[il], cbase), P(self.vcache[il], cbase), c.n_ctx, self.kslice,
@@ -334,13 +348,11 @@ class LlamaLNS16:
             else:
                 self._mm(W["wo"].data_ptr(), P(att), P(o), nq, e, T)
                 check(L.lnship16_add(P(o, r0), P(x, r0), rows * e, rows * e, P(x), st))
-            self._rms_mul(P(x), P(W["ffn_norm"]), P(h), e, rows)
-            self._mm(W["wug"].data_ptr(), P(h), P(ug), e, 2 * f, rows)
+            self._rms_mm(P(x), P(W["ffn_norm"]), W["wug"].data_ptr(), P(h), P(ug), e, 2 * f, rows)
             check(L.lnship16_swiglu(P(ug, f), 2 * f, P(ug), 2 * f, P(sw), f, rows, st))
             self._mm(W["wdown"].data_ptr(), P(sw), P(x), f, e, rows, residual=P(x))
         nout = T if batch else 1
-        self._rms_mul(P(x), P(self.out_norm), P(h), e, nout)
-        self._mm(self.tok_embd.data_ptr(), P(h), P(logits), e, c.n_vocab, nout)
+        self._rms_mm(P(x), P(self.out_norm), self.tok_embd.data_ptr(), P(h), P(logits), e, c.n_vocab, nout)
         if batch:
             return logits[: T * c.n_vocab].view(T, c.n_vocab)
         return logits[: c.n_vocab]
