@@ -198,23 +198,33 @@ def calib_copy(mib):
     print(json.dumps({"calib": "copy", "bytes_read": n * 4, "bytes_written": n * 4}), flush=True)
 
 
+def replay_call(model, ln, torch, call):
+    """Launches one recorded GEMV call again on the current stream."""
+    w, x_ptr, dst_ptr, K, M, N, kw = call
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    if "norm" in kw:
+        ln.check(ln.lib().lnship16_rms_norm_mul_mat(model.mode, x_ptr, kw["norm"], model.cfg.eps, ctypes.c_void_p(w),
+                                                    dst_ptr, K, M, st))
+    else:
+        ln.mul_mat16_raw(model.mode, w, x_ptr, dst_ptr, K, M, N, seed=7, stream=st, **kw)
+
+
 def gemv_roofline(model, ln, torch, reps=4):
-    """Records the mul_mat launches of one eager decode step, captures them
+    """Records the GEMV launches of one eager decode step, captures them
     `reps` times over into one HIP graph and times a replay between two HIP
     events on the replay stream.  Returns (algorithmic bytes per launch,
     average launch us, launches per token); a launch is one lnship16_mul_mat
-    call: one GEMV kernel when NC activation rows fit in LDS next to the
-    tables (every decode shape), else the activation conversion kernel plus
-    the GEMV kernel."""
+    call (one k_mm16 kernel when its activation rows fit in LDS next to the
+    tables, as at every decode shape) or one lnship16_rms_norm_mul_mat call
+    (one k_mm16_rms kernel: the rms_norm before the GEMV runs inside it)."""
     calls = record_decode_step(model, torch)
     # the launches go into one HIP graph so host-side launch cost stays out
     # of the device time between the events
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g):
         for _ in range(reps):
-            for w, x_ptr, dst_ptr, K, M, N, kw in calls:
-                ln.mul_mat16_raw(model.mode, w, x_ptr, dst_ptr, K, M, N, seed=7,
-                                 stream=ctypes.c_void_p(torch.cuda.current_stream().cuda_stream), **kw)
+            for call in calls:
+                replay_call(model, ln, torch, call)
     g.replay()
     s = torch.cuda.Event(enable_timing=True)
     e = torch.cuda.Event(enable_timing=True)
@@ -230,16 +240,22 @@ def gemv_roofline(model, ln, torch, reps=4):
 def record_decode_step(model, torch):
     """Runs one eager decode step at the last timed position (its KV row is
     rewritten; nothing reads it afterwards), so the launches have the timed
-    steps' shapes, and returns its lnship16_mul_mat calls."""
+    steps' shapes, and returns its GEMV calls: lnship16_mul_mat's, and
+    lnship16_rms_norm_mul_mat's with the norm row as kw["norm"]."""
     c = model.cfg
     calls = []
-    orig = model._mm
+    orig, orig_rms = model._mm, model._rms_mm
 
     def record_mm(w, x_ptr, dst_ptr, K, M, N, **kw):
         orig(w, x_ptr, dst_ptr, K, M, N, **kw)
         calls.append((w, x_ptr, dst_ptr, K, M, N, kw))
 
-    model._mm = record_mm
+    def record_rms_mm(x_ptr, wn_ptr, w, h_ptr, dst_ptr, K, M, T):
+        orig_rms(x_ptr, wn_ptr, w, h_ptr, dst_ptr, K, M, T)   # split: records through record_mm
+        if T == 1 and model.fused_rms:
+            calls.append((w, x_ptr, dst_ptr, K, M, 1, {"norm": wn_ptr}))
+
+    model._mm, model._rms_mm = record_mm, record_rms_mm
     try:
         tok = model._buf("rtok", 1, torch.int32)
         pos = model._buf("rpos", 1, torch.int32)
@@ -249,16 +265,18 @@ def record_decode_step(model, torch):
         model.forward(1, tok, pos, n_kv_for(model.n_past, c.n_ctx))
         torch.cuda.synchronize()
     finally:
-        model._mm = orig
+        model._mm, model._rms_mm = orig, orig_rms
     return calls
 
 
 def launch_bytes(calls):
-    """Algorithmic bytes of mul_mat calls: xlns16 weights once per weight
-    slice, F32 in / out, and the F32 residual read by the launches that fuse
-    the ADD after them."""
+    """Algorithmic bytes of GEMV calls: xlns16 weights once per weight
+    slice, F32 in / out, the F32 residual read by the launches that fuse the
+    ADD after them, and the F32 norm row read by those that fuse the
+    rms_norm before them."""
     return sum(2 * K * M * kw.get("ne02", 1) + 4 * K * N * kw.get("ne12", 1)
                + 4 * M * N * kw.get("ne12", 1) * (2 if kw.get("residual") is not None else 1)
+               + (4 * K if "norm" in kw else 0)
                for _, _, _, K, M, N, kw in calls)
 
 
@@ -266,14 +284,15 @@ def chain_bound(model, ln, torch, mode):
     """The dependent-step bound of one decode token.  steps: the sum over the
     token's launches of their chain length (K per mul_mat, n per rms_norm row,
     n - 1 per soft_max row; head_dim + 2 n_kv - 1 for the fused decode
-    attention, whose KQ, soft_max and KQV chains run one after another); a
-    launch's chains run side by side and the launches one after another.  ns_per_step: the slope of GEMV launch time
+    attention, whose KQ, soft_max and KQV chains run one after another; K
+    for a fused rms_norm + mul_mat, whose rms chain runs beside the GEMV's);
+    a launch's chains run side by side and the launches one after another.  ns_per_step: the slope of GEMV launch time
     against K at M = 576 (K = 576 and 1536, each a graph of 20 launches timed
     between HIP events on the replay stream), so each launch's fixed cost
     stays out of it.  bound_tok_s = 1 / (steps * ns_per_step)."""
     c = model.cfg
     steps = []
-    orig = (model._mm, model._rms_mul, model._softmax, model._attn)
+    orig = (model._mm, model._rms_mul, model._softmax, model._attn, model._rms_mm)
 
     def mm(w, x_ptr, dst_ptr, K, M, N, **kw):
         steps.append(K)
@@ -291,7 +310,12 @@ def chain_bound(model, ln, torch, mode):
         steps.append(args.head_dim + 2 * args.n_kv - 1)
         orig[3](args)
 
-    model._mm, model._rms_mul, model._softmax, model._attn = mm, rms, sm, attn
+    def rms_mm(x_ptr, wn_ptr, w, h_ptr, dst_ptr, K, M, T):
+        if T == 1 and model.fused_rms:
+            steps.append(K)
+        orig[4](x_ptr, wn_ptr, w, h_ptr, dst_ptr, K, M, T)   # split: counted by rms and mm
+
+    model._mm, model._rms_mul, model._softmax, model._attn, model._rms_mm = mm, rms, sm, attn, rms_mm
     try:
         tok = model._buf("rtok", 1, torch.int32)
         pos = model._buf("rpos", 1, torch.int32)
@@ -301,7 +325,7 @@ def chain_bound(model, ln, torch, mode):
         model.forward(1, tok, pos, n_kv_for(model.n_past, c.n_ctx))
         torch.cuda.synchronize()
     finally:
-        model._mm, model._rms_mul, model._softmax, model._attn = orig
+        model._mm, model._rms_mul, model._softmax, model._attn, model._rms_mm = orig
     st = lambda: ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
     us = {}
     M = 576
@@ -542,8 +566,9 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(achieved, 3), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 6), "traffic": traffic,
                      "traffic_source": traffic_src,
-                     "kernel": "lnship16_mul_mat decode launches (k_mm16<%s, NC=1>, activations converted in-kernel)"
-                               % args.mode,
+                     "kernel": "decode GEMV launches: lnship16_mul_mat (k_mm16<%s, NC=1>, activations converted "
+                               "in-kernel)%s" % (args.mode, " and lnship16_rms_norm_mul_mat (k_mm16_rms, the rms_norm "
+                                                 "before the GEMV inside it)" if model.fused_rms else ""),
                      "launches_per_token": n_launch, "avg_launch_us": round(us_launch, 3),
                      "bytes_per_launch": int(b_launch)},
         "chain_bound": chain,
