@@ -335,11 +335,13 @@ int lnship_lpvip_db_range(uint32_t d0, uint32_t n, int32_t *out, void *stream);
  * in the reference. */
 int lnship32_add_lds(int form, const uint32_t *x, const uint32_t *y, uint32_t *out, int64_t n, void *stream);
 
-/* Test hook: adds skew to the scale code lnship16_rms_norm_mul_mat predicts
- * (0 by default), so that a test can make the prediction wrong and check
- * the rerun; returns the previous value.  Host-side only; takes effect at
- * the next launch.  No counterpart in the reference. */
-int lnship_test_rms_predict_skew(int skew);
+/* Test hook: adds skew to the codes the sum32 kernels predict before their
+ * sum chains end (lnship16_rms_norm_mul_mat's rms scale,
+ * lnship16_attn_decode's soft_max total; 0 by default), so that a test can
+ * make every prediction wrong and check the rerun; returns the previous
+ * value.  Host-side only; takes effect at the next launch.  No counterpart
+ * in the reference. */
+int lnship_test_predict_skew(int skew);
 
 /* Host: the (cos, sin) floats lns_rope uses for positions 0..n_pos-1 (the
  * float recurrence t *= powf(freq_base, -2/n_dims) per pair, cosf / sinf;

@@ -661,17 +661,21 @@ def test_mul_mat_id_expert_out_of_range(ln):
     same_bits(got[1], want[1], "token after the bad expert")
 
 
-@pytest.mark.parametrize("mode,n_kv,big_tail", [
-    ("base", 1, False), ("base", 13, False), ("base", 256, False), ("base", 256, True), ("lpvip", 13, False),
-    ("lpvip", 256, False), ("lpvip", 256, True), ("sum32", 1, False), ("sum32", 13, False), ("sum32", 256, False),
-    ("sum32", 256, True), ("sum32", 520, False), ("sum32", 2048, False)])
-def test_attn_decode_equals_three_nodes(ln, mode, n_kv, big_tail):
+@pytest.mark.parametrize("mode,n_kv,big_tail,skew", [
+    ("base", 1, False, 0), ("base", 13, False, 0), ("base", 256, False, 0), ("base", 256, True, 0),
+    ("lpvip", 13, False, 0), ("lpvip", 256, False, 0), ("lpvip", 256, True, 0), ("sum32", 1, False, 0),
+    ("sum32", 13, False, 0), ("sum32", 256, False, 0), ("sum32", 256, True, 0), ("sum32", 520, False, 0),
+    ("sum32", 2048, False, 0), ("sum32", 1, False, 1), ("sum32", 13, False, -1), ("sum32", 256, True, 3),
+    ("sum32", 520, False, -7)])
+def test_attn_decode_equals_three_nodes(ln, mode, n_kv, big_tail, skew):
     # lnship16_attn_decode against K^T q, soft_max and V p run as three ops, on
     # the SmolLM2 head shape (9 query heads over 3 kv heads of 64), random
     # caches and a causal mask that hides the last cells.  Past the last
     # nonzero exp the KQV chain stops only where the remaining products add
     # nothing; big_tail puts values of 1e35 in the masked cells of V, so that
-    # they would not and the chain runs on
+    # they would not and the chain runs on.  sum32 starts the KQV chains from
+    # a predicted soft_max total; skew makes that prediction wrong, so the
+    # result comes from the rerun
     import ctypes
     m = O.MODES[mode]
     nh, nkv, hd, n_ctx = 9, 3, 64, max(256, (n_kv + 255) // 256 * 256)
@@ -697,8 +701,12 @@ def test_attn_decode_equals_three_nodes(ln, mode, n_kv, big_tail):
                      w_slice=vslice, dst_ld=nh * hd, dst_slice=hd)
     got = torch.full((nh * hd,), float("nan"), device="cuda")
     a = ln.AttnArgs(P(q), P(kc), P(vc), n_ctx, kslice, vslice, P(mask), scale, P(got), nh, nkv, hd, n_kv)
-    ln.check(ln.lib().lnship16_attn_decode(m, ctypes.byref(a), ln._stream()))
-    same_bits(host(got), host(want), f"attn decode {mode} n_kv={n_kv}")
+    prev = ln.lib().lnship_test_predict_skew(skew)
+    try:
+        ln.check(ln.lib().lnship16_attn_decode(m, ctypes.byref(a), ln._stream()))
+    finally:
+        ln.lib().lnship_test_predict_skew(prev)
+    same_bits(host(got), host(want), f"attn decode {mode} n_kv={n_kv} skew={skew}")
     if mode == "sum32" and n_kv == 13 and not big_tail:
         # Monte is refused (its draws run across the three nodes in graph order)
         assert ln.lib().lnship16_attn_decode(O.MONTE, ctypes.byref(a), ln._stream()) != 0

@@ -104,14 +104,14 @@ def test_rms_norm_mul_mat_mispredicted_scale(ln, skew):
     # every prediction off by skew codes: the result comes from the second pass
     print(f"\n[rms_norm_mul_mat] skew={skew}", flush=True)
     rng = np.random.default_rng(100 + skew)
-    prev = ln.lib().lnship_test_rms_predict_skew(skew)
+    prev = ln.lib().lnship_test_predict_skew(skew)
     try:
         for K, M, xscale in [(576, 960, 1.0), (577, 193, 3.0), (13, 5, 30.0)]:
             x, wn, w = case(rng, K, M, xscale)
             wp = ln.pack16(dev(w))
             same_bits(fused(ln, x, wn, wp, K, M), oracle(x, wn, w), f"skew {skew} K={K} M={M}")
     finally:
-        ln.lib().lnship_test_rms_predict_skew(prev)
+        ln.lib().lnship_test_predict_skew(prev)
 
 
 def test_rms_norm_mul_mat_logits_shape(ln):

@@ -1736,6 +1736,7 @@ struct attn_args {
     float scale;
     float *dst;
     int hd, n_kv, rep;   // head_dim, cells, query heads per kv head
+    uint32_t skew;       // added to the predicted soft_max total (0; a test hook sets it)
 };
 
 // Terms k0 <= k < k1 of one output of a GEMV over weights in the packed
@@ -1800,7 +1801,8 @@ __global__ __launch_bounds__(k_block) void k_attn16(attn_args a, dev_tables T) {
     uint16_t *c = xq + hp;                                                     // scores, then exps
     uint16_t *pc = c + rs;                                                     // KQV's activation codes
     __shared__ int32_t s_max;
-    __shared__ uint32_t s_tot;
+    __shared__ uint32_t s_tot, s_tot2;   // the total (sum32: predicted, then the chain's)
+    __shared__ double s_part[k_block / 64];
     __shared__ int s_last;
     __shared__ uint32_t s_vmax[k_attn_tail_hd];   // per dim: the largest V log past the last nonzero exp
     const int h = blockIdx.x, kv = h / a.rep;
@@ -1843,18 +1845,19 @@ __global__ __launch_bounds__(k_block) void k_attn16(attn_args a, dev_tables T) {
     __syncthreads();
     const uint16_t *vw = a.v + kv * a.v_slice;
     const int n_eff = s_last + 1;
-    if (threadIdx.x == 0) {
-        // the sum of exps up to the last nonzero one, as k_softmax16 runs it
+    // the sum of exps up to the last nonzero one, as k_softmax16 runs it
+    auto sum_chain = [&]() __attribute__((always_inline)) {
         uint32_t st = 0;
         typename red16<MODE>::acc_t acc = R.start(c[0], st);
         if (n_eff > 1) chain16<red16<MODE>, true>(R, acc, c, 1, n_eff, st);
-        s_tot = R.finish(acc) & 0xffffu;
-    } else if (tail_stop && threadIdx.x >= 64 && n_eff < n) {
-        // meanwhile, on the other waves: the largest V log of each dim over
-        // the cells past the last nonzero exp
-        const int g0 = n_eff >> 3, ngt = ((n - 1) >> 3) - g0 + 1, nt = (int)blockDim.x - 64;
+        return R.finish(acc) & 0xffffu;
+    };
+    // threads t0, t0 + nt, ...: the largest V log of each dim over the cells
+    // past the last nonzero exp
+    auto tail_vmax = [&](int t0, int nt) __attribute__((always_inline)) {
+        const int g0 = n_eff >> 3, ngt = ((n - 1) >> 3) - g0 + 1;
 #pragma unroll 4
-        for (int i = (int)threadIdx.x - 64; i < hd * ngt; i += nt) {
+        for (int i = (int)threadIdx.x - t0; i < hd * ngt; i += nt) {
             const int d = i % hd, g = g0 + i / hd;
             const uint4 q4 = *reinterpret_cast<const uint4 *>(vw + (int64_t)d * 8 + (int64_t)g * a.v_gs);
             const uint32_t qq[4] = {q4.x, q4.y, q4.z, q4.w};
@@ -1866,19 +1869,21 @@ __global__ __launch_bounds__(k_block) void k_attn16(attn_args a, dev_tables T) {
             }
             atomicMax(&s_vmax[d], m);
         }
-    }
-    __syncthreads();
-    for (int j = threadIdx.x; j < rs; j += blockDim.x)
-        pc[j] = j < n ? (uint16_t)x16_from_f32(T.cvt16, T.rev16[x16_div(c[j], s_tot)]) : (uint16_t)0;
-    __syncthreads();
-    // The att outputs.  Past the last nonzero exp every p has one code (all
-    // those exps are 0), so a product there has the log clamp(v + p - 0x4000)
-    // and the largest is that of the largest V log.  A lane's chain stops at
-    // the last nonzero exp when that largest product lies at or beyond the
-    // adder's essential zero below its sum: every later term would add
-    // nothing (and keep the sum's sign)
-    const uint32_t p_tail = n_eff < n ? pc[n_eff] & k16_logmask : 0u;
-    for (int d = threadIdx.x; d < hd; d += blockDim.x) {
+    };
+    // soft_max's output as KQV's mul_mat reads it: each probability through
+    // F32 into xlns16
+    auto stage_p = [&](uint32_t tot) __attribute__((always_inline)) {
+        for (int j = threadIdx.x; j < rs; j += blockDim.x)
+            pc[j] = j < n ? (uint16_t)x16_from_f32(T.cvt16, T.rev16[x16_div(c[j], tot)]) : (uint16_t)0;
+    };
+    // The att output of dim d.  Past the last nonzero exp every p has one
+    // code (all those exps are 0), so a product there has the log
+    // clamp(v + p - 0x4000) and the largest is that of the largest V log.  A
+    // lane's chain stops at the last nonzero exp when that largest product
+    // lies at or beyond the adder's essential zero below its sum: every
+    // later term would add nothing (and keep the sum's sign)
+    auto out_chain = [&](int d) __attribute__((always_inline)) {
+        const uint32_t p_tail = n_eff < n ? pc[n_eff] & k16_logmask : 0u;
         const uint16_t *vr = vw + (int64_t)d * 8;
         uint32_t st = 0;
         typename red16<MODE>::acc_t acc{};
@@ -1893,8 +1898,56 @@ __global__ __launch_bounds__(k_block) void k_attn16(attn_args a, dev_tables T) {
         } else {
             row_chain<MODE>(R, acc, st, vr, a.v_gs, pc, 0, n);
         }
-        a.dst[(int64_t)h * hd + d] = T.rev16[R.finish(acc) & 0xffffu];
+        return R.finish(acc) & 0xffffu;
+    };
+    // sum32, with a wave beside the output chains' (head_dim <= 192): the
+    // output chains start at once from a predicted total while that wave's
+    // first lane runs the sum's chain, and run again when the total differs.
+    // The prediction sums the exps' values in double and rounds the log to
+    // the nearest xlns16 step, which is the chain's narrowed xlns32 sum
+    // unless that sum lies within the chain's error of a rounding boundary.
+    const int sum_lane = (hd + 63) & ~63;
+    if (MODE == LNSHIP_SUM32 && sum_lane < (int)blockDim.x) {
+        double part = 0.0;
+        for (int j = threadIdx.x; j < n_eff; j += blockDim.x)
+            part += exp2(((double)(int)(c[j] & k16_logmask) - (double)k16_one) * (1.0 / 128.0));
+        for (int o = 32; o > 0; o >>= 1) part += __shfl_xor(part, o);
+        if ((threadIdx.x & 63) == 0) s_part[threadIdx.x >> 6] = part;
+        if (tail_stop && n_eff < n) tail_vmax(0, (int)blockDim.x);
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            double S = 0.0;
+            for (int i = 0; i < k_block / 64; i++) S += s_part[i];
+            const double l = S > 0.0 ? floor(log2(S) * 128.0 + 0.5) + (double)k16_one : 0.0;
+            s_tot = ((uint32_t)fmin(fmax(l, 0.0), (double)k16_logmask) + a.skew) & 0xffffu;
+        }
+        __syncthreads();
+        const uint32_t tot = s_tot;
+        stage_p(tot);
+        __syncthreads();
+        uint32_t res = 0;
+        if ((int)threadIdx.x < hd) res = out_chain((int)threadIdx.x);
+        else if ((int)threadIdx.x == sum_lane) s_tot2 = sum_chain();
+        __syncthreads();
+        // (every thread reads the same word after the barrier)
+        if (s_tot2 != tot) {
+            stage_p(s_tot2);
+            __syncthreads();
+            if ((int)threadIdx.x < hd) res = out_chain((int)threadIdx.x);
+        }
+        if ((int)threadIdx.x < hd) a.dst[(int64_t)h * hd + threadIdx.x] = T.rev16[res];
+        return;
     }
+    if (threadIdx.x == 0) {
+        s_tot = sum_chain();
+    } else if (tail_stop && threadIdx.x >= 64 && n_eff < n) {
+        // meanwhile, on the other waves: the tail's V maxima
+        tail_vmax(64, (int)blockDim.x - 64);
+    }
+    __syncthreads();
+    stage_p(s_tot);
+    __syncthreads();
+    for (int d = threadIdx.x; d < hd; d += blockDim.x) a.dst[(int64_t)h * hd + d] = T.rev16[out_chain(d)];
 }
 
 __global__ __launch_bounds__(k_block) void k_softmax32(sm_args a, dev_tables T) {
@@ -3185,12 +3238,13 @@ int lnship16_rms_norm_mul(int mode, const float *src, const float *w, float *dst
     return rms16_common(mode, src, w, dst, ncols, nrows, eps, monte_seed, monte_state, monte_offset, stream);
 }
 
-// added to k_mm16_rms's predicted scale code (lnship_test_rms_predict_skew)
-static uint32_t g_rms_skew = 0;
+// added to the sums the sum32 kernels predict (k_mm16_rms's rms sum,
+// k_attn16's soft_max total): lnship_test_predict_skew
+static uint32_t g_predict_skew = 0;
 
-int lnship_test_rms_predict_skew(int skew) {
-    const int prev = (int)g_rms_skew;
-    g_rms_skew = (uint32_t)skew;
+int lnship_test_predict_skew(int skew) {
+    const int prev = (int)g_predict_skew;
+    g_predict_skew = (uint32_t)skew;
     return prev;
 }
 
@@ -3213,7 +3267,7 @@ int lnship16_rms_norm_mul_mat(int mode, const float *x, const float *norm_w, flo
     mm_args16 m{(const uint16_t *)w, nullptr, x, dst, K, kp, M, 1, K, K, 1, 1, 1, 1, M, kp * M, M, M, 0, nullptr, 0};
     m.norm = norm_w;
     m.eps = eps;
-    m.skew = g_rms_skew;
+    m.skew = g_predict_skew;
     const uint64_t wgs = (uint64_t)((M + k_rms_mm_rows - 1) / k_rms_mm_rows);
     if (wgs > 0x7fffffffu) return fail(LNSHIP_ERANGE, "rms_norm_mul_mat: grid too large%s");
     m.xcd_sh = xcd_shift(wgs, s->cus);
@@ -3284,7 +3338,8 @@ int lnship16_attn_decode(int mode, const lnship_attn_args *a, void *stream) {
         return fail(LNSHIP_EINVAL, "attn_decode: bad argument%s");
     if (a->n_kv > lnship_max_row(4, mode)) return fail(LNSHIP_ERANGE, "attn_decode: n_kv too long for LDS%s");
     const attn_args m{a->q, a->k_cache, a->v_cache, a->cache_m * 8, a->k_slice, a->head_dim * 8, a->v_slice,
-                      a->mask, a->scale, a->dst, (int)a->head_dim, (int)a->n_kv, (int)(a->n_head / a->n_head_kv)};
+                      a->mask, a->scale, a->dst, (int)a->head_dim, (int)a->n_kv, (int)(a->n_head / a->n_head_kv),
+                      g_predict_skew};
     hipStream_t st = (hipStream_t)stream;
     switch (mode) {
         case LNSHIP_BASE: return launch_attn16<LNSHIP_BASE>(m, a->n_head, s->T, st);
