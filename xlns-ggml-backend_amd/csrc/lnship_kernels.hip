@@ -1744,10 +1744,89 @@ struct attn_args {
 // activations' codes at x in LDS), each an xlns16_mul product, added into acc
 // in k order as k_mm16 adds them (term 0 starts acc).  The weights of the next
 // PF groups are in flight while a block is added.
+// row_chain for sum32, in the order of k_mm16's single-chain loop: each
+// product is formed in the first round trip of the step before it, which
+// also passes on the opposite-signs flag of the next step.
+__device__ __forceinline__ void row_chain_x32(const red16<LNSHIP_SUM32> &R, acc_ls &acc,
+                                              const uint16_t *__restrict__ w, int64_t gs, const uint16_t *x, int k0,
+                                              int k1) {
+    if (k1 <= k0) return;
+    constexpr int PF = 4;
+    const int gl = (k1 - 1) >> 3;
+    // term k: the xlns16 product, its log and sign at the xlns32 positions
+    auto term = [&](uint32_t wv, uint32_t xv, uint32_t &tl, uint32_t &ts) {
+        const uint32_t t = x16_mul(wv, xv);
+        tl = (t & k16_logmask) << 16;
+        ts = (t & k16_sign) << 16;
+    };
+    auto term_at = [&](int k, uint32_t &tl, uint32_t &ts) { term(w[(int64_t)(k >> 3) * gs + (k & 7)], x[k], tl, ts); };
+    // term 0 starts the sum; the steps add terms ks .. k1 - 1
+    const int ks = k0 == 0 ? 1 : k0;
+    uint32_t c_tl, c_ts, c_uf;
+    if (k0 == 0) {
+        term_at(0, c_tl, c_ts);
+        acc = {c_tl, c_ts};
+        if (k1 == 1) return;
+    }
+    term_at(ks, c_tl, c_ts);
+    c_uf = acc.s ^ c_ts;
+    // the steps of group g (wq, xq) at k in [ks, k1); wn, xn: the next group
+    auto group = [&](const uint4 &wq, const uint4 &xq, const uint4 &wn, const uint4 &xn, int g) {
+        const uint32_t ww[4] = {wq.x, wq.y, wq.z, wq.w}, xx[4] = {xq.x, xq.y, xq.z, xq.w};
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const int k = 8 * g + u;
+            if (k < ks || k >= k1) continue;
+            uint32_t ntl = 0, nts = 0;
+            auto next = [&] {
+                if (u < 7) term(half16(ww[(u + 1) >> 1], (u + 1) & 1), half16(xx[(u + 1) >> 1], (u + 1) & 1), ntl, nts);
+                else term(wn.x & 0xffffu, xn.x & 0xffffu, ntl, nts);
+                return nts;
+            };
+            c_uf = x32_add_step(R.O, acc, c_tl, c_ts, c_uf, next, [] {});
+            c_tl = ntl;
+            c_ts = nts;
+        }
+    };
+    // blocks of PF groups, double-buffered as in row_chain; loads past the
+    // last group reload it
+    uint4 wa[PF], xa[PF], wb[PF], xb[PF];
+    auto load = [&](uint4 (&w4)[PF], uint4 (&x4)[PF], int g0) {
+#pragma unroll
+        for (int p = 0; p < PF; p++) {
+            const int g = min(g0 + p, gl);
+            w4[p] = *reinterpret_cast<const uint4 *>(w + (int64_t)g * gs);
+            x4[p] = *reinterpret_cast<const uint4 *>(x + 8 * g);
+        }
+    };
+    auto run = [&](const uint4 (&w4)[PF], const uint4 (&x4)[PF], const uint4 (&wo)[PF], const uint4 (&xo)[PF],
+                   int g0) {
+#pragma unroll
+        for (int p = 0; p < PF; p++) {
+            if (g0 + p > gl) break;
+            group(w4[p], x4[p], p + 1 < PF ? w4[p + 1] : wo[0], p + 1 < PF ? x4[p + 1] : xo[0], g0 + p);
+        }
+    };
+    const int g1 = ks >> 3;
+    load(wa, xa, g1);
+    load(wb, xb, g1 + PF);
+    for (int g0 = g1; g0 <= gl; g0 += 2 * PF) {
+        run(wa, xa, wb, xb, g0);
+        if (g0 + PF > gl) break;
+        load(wa, xa, g0 + 2 * PF);
+        run(wb, xb, wa, xa, g0 + PF);
+        load(wb, xb, g0 + 3 * PF);
+    }
+}
+
 template <int MODE>
 __device__ __forceinline__ void row_chain(const red16<MODE> &R, typename red16<MODE>::acc_t &acc, uint32_t &st,
                                           const uint16_t *__restrict__ w, int64_t gs, const uint16_t *x, int k0,
                                           int k1) {
+    if constexpr (MODE == LNSHIP_SUM32) {
+        row_chain_x32(R, acc, w, gs, x, k0, k1);
+        return;
+    }
     constexpr int PF = 4;
     const int ga = k0 >> 3, gl = (k1 - 1) >> 3;
     auto load = [&](uint4 (&b)[PF], int g0) {
