@@ -115,8 +115,10 @@ def mark_outputs(nodes, fused):
     pair does not write the intermediate tensor).  "mm_self" stays unflagged
     too but is checked: its ADD reads the product's own activation and writes
     over it in place, a pair graph_compute must not fuse.  Returns the
-    checked keys."""
-    skip = {"rms", "mm", "down"} if fused else set()
+    checked keys.  "rms1" -> "mul1" -> "qkv1" is a decode step's norm and
+    q|k|v product (one row): in sum32 graph_compute runs the three as one
+    launch, in the other modes the first two."""
+    skip = {"rms", "mm", "down", "rms1", "mul1"} if fused else set()
     noflag = {"mm_self"} if fused else set()
     for k, tn in nodes.items():
         if k not in skip and k not in noflag:
@@ -159,6 +161,7 @@ def run16(mode_name, policy=None, dev=False, fused=False):
     w_codes = O.f2x16(f32(200, E, scale=0.05))   # GGML_TYPE_LNS16 weights
     xs = f32(T, E)
     wself = f32(E, E, scale=0.02)
+    xdec = f32(1, E)
 
     t = lambda *a, **k: h.tensor(*a, device=None if k.get("weights") else act, **k)
     tw = lambda *a, **k: h.tensor(*a, device=wts, **k)
@@ -213,9 +216,14 @@ def run16(mode_name, policy=None, dev=False, fused=False):
     WS = tw([E, E], data=wself, weights=True, name="blk.0.self.weight")
     nodes["mm_self"] = t([E, T], op="MUL_MAT", src=(WS, XS), name="self_mm-0")
     nodes["add_self"] = t([E, T], op="ADD", src=(XS, nodes["mm_self"]), data=XS.data, name="self_out-0")
+    # one decode row: its norm, the norm MUL and the q|k|v product
+    XD = t([E, 1], data=xdec, name="inp_dec")
+    nodes["rms1"] = t([E, 1], op="RMS_NORM", src=(XD,), fparams={0: 1e-5}, name="norm-1")
+    nodes["mul1"] = t([E, 1], op="MUL", src=(nodes["rms1"], Gw), name="attn_norm-1")
+    nodes["qkv1"] = t([E + 2 * HKV * D, 1], op="MUL_MAT", src=(WQKV, nodes["mul1"]), name="qkv-2")
     order = ["rms", "mul", "qkv", "view_q", "rope", "perm_q", "kq", "softmax", "ug", "swiglu", "view_g", "view_u",
              "swiglu_split", "add", "add_bcast", "down", "down_res", "qkv_again", "softmax_nomask", "moe", "mm_lns16",
-             "mm_self", "add_self"]
+             "mm_self", "add_self", "rms1", "mul1", "qkv1"]
     views = {"view_q": qv, "perm_q": qp, "view_g": ga, "view_u": ua}
     graph = [views[k] if k in views else nodes[k] for k in order]
 
@@ -255,7 +263,15 @@ def run16(mode_name, policy=None, dev=False, fused=False):
     want["mm_lns16"] = O.mul_mat16(mode_of("MUL_MAT", "k_lns16-0"), w_codes, want["mul"])
     want["mm_self"] = O.mul_mat16(mode_of("MUL_MAT", "self_mm-0"), O.f2x16(wself), xs)
     want["add_self"] = binop(L.lno16_add_f32, xs, want["mm_self"])
+    want["rms1"] = O.rms_norm16(mode_of("RMS_NORM", "norm-1"), xdec, 1e-5)
+    want["mul1"] = binop(L.lno16_mul_f32, want["rms1"], g)
+    want["qkv1"] = O.mul_mat16(mode_of("MUL_MAT", "qkv-2"), O.f2x16(wqkv), want["mul1"])
 
+    # the decode row's three nodes run as one launch only in sum32; otherwise
+    # the norm MUL is written and checked like the other nodes
+    triple = mode_of("RMS_NORM", "norm-1") == O.SUM32 and mode_of("MUL_MAT", "qkv-2") == O.SUM32
+    if fused and not triple:
+        checked.append("mul1")
     report = {}
     for k in checked:
         got = h.f32_of(nodes[k], act).reshape(want[k].shape)

@@ -914,7 +914,7 @@ static void backend_free(ggml_backend_t b) {
 }
 
 static void run_node(context &ctx, ggml_tensor *node);
-static bool run_fused(context &ctx, ggml_cgraph *g, int i);
+static int run_fused(context &ctx, ggml_cgraph *g, int i);
 static bool fuse_enabled();
 
 static ggml_status backend_graph_compute(ggml_backend_t b, ggml_cgraph *g) {
@@ -923,9 +923,11 @@ static ggml_status backend_graph_compute(ggml_backend_t b, ggml_cgraph *g) {
         ggml_tensor *node = g->nodes[i];
         if ((node->flags & GGML_TENSOR_FLAG_COMPUTE) == 0) continue;
         if (classify(node) == kind::view || nelements(node) == 0) continue;
-        if (fuse_enabled() && run_fused(ctx, g, i)) {   // node i and node i + 1 in one launch
-            i++;
-            continue;
+        if (fuse_enabled()) {   // nodes i .. i + n - 1 in one launch
+            if (const int n = run_fused(ctx, g, i)) {
+                i += n - 1;
+                continue;
+            }
         }
         run_node(ctx, node);
     }
@@ -1644,6 +1646,9 @@ static void op_mul_mat_id(context &ctx, ggml_tensor *dst) {
 // output), the pair runs as one launch (lnship16_rms_norm_mul, the mul_mat's
 // residual) and node i's tensor is not written.  Each fused launch keeps the
 // F32 value between the two nodes and its conversion, as the two nodes do.
+// In sum32, an RMS_NORM -> MUL pair of one row whose product feeds only a
+// MUL_MAT (a decode step's norm before q|k|v, up|gate or the output) runs
+// with that MUL_MAT as one launch (lnship16_rms_norm_mul_mat).
 
 // Opt-in (GGML_LNS_HIP_FUSE=1): graph_compute sees one split of a
 // ggml_backend_sched graph at a time, so a reader of node i's tensor in a
@@ -1692,16 +1697,42 @@ static bool feeds_only(const ggml_cgraph *g, int i, const ggml_tensor *next) {
 // an F32 tensor (upload() gathers any layout into a dense copy)
 static bool plain_f32(const ggml_tensor *t) { return t->type == GGML_TYPE_F32; }
 
-static bool run_fused(context &ctx, ggml_cgraph *g, int i) {
-    if (i + 1 >= g->n_nodes) return false;
+// RMS_NORM t -> MUL next -> MUL_MAT mm of one sum32 row in one launch, when
+// next feeds only mm (as its activation) and mm's output overlaps neither
+// the row nor the norm weight (the kernel reads them until its last chain)
+static bool run_rms_mul_mat(context &ctx, ggml_cgraph *g, int i, const ggml_tensor *w) {
+    if (ctx.fmt->w32 || i + 2 >= g->n_nodes) return false;
+    ggml_tensor *t = g->nodes[i], *next = g->nodes[i + 1], *mm = g->nodes[i + 2];
+    if ((mm->flags & GGML_TENSOR_FLAG_COMPUTE) == 0 || classify(mm) != kind::mul_mat || mm->src[1] != next ||
+        !feeds_only(g, i + 1, mm))
+        return false;
+    if (node_mode(t) != LNSHIP_SUM32 || node_mode(mm) != LNSHIP_SUM32 || nrows(t) != 1) return false;
+    const ggml_tensor *a = mm->src[0];
+    if (a->ne[0] != t->ne[0] || a->ne[2] != 1 || a->ne[3] != 1 || nelements(mm) != a->ne[1] || !plain_f32(mm))
+        return false;
+    if (overlaps(mm, t->src[0]) || overlaps(mm, w)) return false;
+    // the weight first: packing a host weight stages it through R_SRC0
+    const void *wm = ctx.lns_matrix(a);
+    const float *x = ctx.upload(t->src[0], R_SRC0);
+    const float *wd = ctx.upload(w, R_SRC1);
+    float *y = ctx.out_f32(mm, R_DST);
+    lib_ok(lnship16_rms_norm_mul_mat(LNSHIP_SUM32, x, wd, op_f32(t, 0), wm, y, a->ne[0], a->ne[1], ctx.get_stream()),
+           "lnship16_rms_norm_mul_mat");
+    ctx.download(y, mm);
+    return true;
+}
+
+static int run_fused(context &ctx, ggml_cgraph *g, int i) {
+    if (i + 1 >= g->n_nodes) return 0;
     ggml_tensor *t = g->nodes[i], *next = g->nodes[i + 1];
-    if ((next->flags & GGML_TENSOR_FLAG_COMPUTE) == 0 || !feeds_only(g, i, next)) return false;
+    if ((next->flags & GGML_TENSOR_FLAG_COMPUTE) == 0 || !feeds_only(g, i, next)) return 0;
     const kind k = classify(t), kn = classify(next);
     if (k == kind::rms_norm && kn == kind::mul && next->src[0] == t && plain_f32(t->src[0])) {
         // MUL by one weight row of ne[0] floats
         const ggml_tensor *w = next->src[1];
-        if (!plain_f32(w) || w->ne[0] != t->ne[0] || nelements(w) != w->ne[0] || !same_shape(next, t)) return false;
-        if (overlaps(next, w) || (overlaps(next, t->src[0]) && next->data != t->src[0]->data)) return false;
+        if (!plain_f32(w) || w->ne[0] != t->ne[0] || nelements(w) != w->ne[0] || !same_shape(next, t)) return 0;
+        if (overlaps(next, w) || (overlaps(next, t->src[0]) && next->data != t->src[0]->data)) return 0;
+        if (run_rms_mul_mat(ctx, g, i, w)) return 3;
         const int64_t nc = t->ne[0], nr = nrows(t);
         const float *x = ctx.upload(t->src[0], R_SRC0);
         const float *wd = ctx.upload(w, R_SRC1);
@@ -1716,18 +1747,18 @@ static bool run_fused(context &ctx, ggml_cgraph *g, int i) {
                    "lnship16_rms_norm_mul");
         }
         ctx.download(y, next);
-        return true;
+        return 2;
     }
     if (k == kind::mul_mat && kn == kind::add) {
         // ADD of a residual of the product's shape (either operand order:
         // the xlns add is commutative)
         const ggml_tensor *r = next->src[0] == t ? next->src[1] : next->src[0];
-        if (r == t || !plain_f32(r) || !same_shape(r, t) || !same_shape(next, t)) return false;
+        if (r == t || !plain_f32(r) || !same_shape(r, t) || !same_shape(next, t)) return 0;
         const ggml_tensor *a = t->src[0], *b = t->src[1];
         // the product reads b while the launch writes the sum: the output may
         // only replace the residual exactly (in place), never overlap b
-        if (r == b || (b->data && overlaps(next, b))) return false;
-        if (overlaps(next, r) && (next->data != r->data || !contiguous(next) || !contiguous(r))) return false;
+        if (r == b || (b->data && overlaps(next, b))) return 0;
+        if (overlaps(next, r) && (next->data != r->data || !contiguous(next) || !contiguous(r))) return 0;
         lnship_mul_mat_args args;
         std::memset(&args, 0, sizeof args);
         args.w = ctx.lns_matrix(a);
@@ -1750,9 +1781,9 @@ static bool run_fused(context &ctx, ggml_cgraph *g, int i) {
             lib_ok(lnship16_mul_mat(mode, &args, ctx.get_stream()), "lnship16_mul_mat");
         }
         ctx.download(args.dst, next);
-        return true;
+        return 2;
     }
-    return false;
+    return 0;
 }
 
 static void run_node(context &ctx, ggml_tensor *node) {
