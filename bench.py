@@ -36,7 +36,8 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-graph", action="store_true", help="decode eagerly instead of replaying a HIP graph")
     ap.add_argument("--split-rms", action="store_true",
-                    help="sum32 decode: rms_norm + MUL and the mul_mat after them as separate launches")
+                    help="decode: rms_norm + MUL (sum32) and swiglu as launches of their own, apart from the "
+                         "mul_mat after them")
     ap.add_argument("--decode-only", action="store_true",
                     help="only the prompt and the decode steps, then one recorded eager step: prints the decode "
                          "launches' algorithmic bytes (for HBM counter runs; with --prompt 1 every lnship16_mul_mat "
@@ -205,6 +206,9 @@ def replay_call(model, ln, torch, call):
     if "norm" in kw:
         ln.check(ln.lib().lnship16_rms_norm_mul_mat(model.mode, x_ptr, kw["norm"], model.cfg.eps, ctypes.c_void_p(w),
                                                     dst_ptr, K, M, st))
+    elif "glu_up" in kw:
+        ln.check(ln.lib().lnship16_swiglu_mul_mat(model.mode, x_ptr, kw["glu_up"], ctypes.c_void_p(w),
+                                                  kw["residual"], dst_ptr, K, M, st))
     else:
         ln.mul_mat16_raw(model.mode, w, x_ptr, dst_ptr, K, M, N, seed=7, stream=st, **kw)
 
@@ -244,7 +248,7 @@ def record_decode_step(model, torch):
     lnship16_rms_norm_mul_mat's with the norm row as kw["norm"]."""
     c = model.cfg
     calls = []
-    orig, orig_rms = model._mm, model._rms_mm
+    orig, orig_rms, orig_glu = model._mm, model._rms_mm, model._glu_mm
 
     def record_mm(w, x_ptr, dst_ptr, K, M, N, **kw):
         orig(w, x_ptr, dst_ptr, K, M, N, **kw)
@@ -255,7 +259,11 @@ def record_decode_step(model, torch):
         if T == 1 and model.fused_rms:
             calls.append((w, x_ptr, dst_ptr, K, M, 1, {"norm": wn_ptr}))
 
-    model._mm, model._rms_mm = record_mm, record_rms_mm
+    def record_glu_mm(gate_ptr, up_ptr, w, resid_ptr, dst_ptr, K, M):
+        orig_glu(gate_ptr, up_ptr, w, resid_ptr, dst_ptr, K, M)
+        calls.append((w, gate_ptr, dst_ptr, K, M, 1, {"glu_up": up_ptr, "residual": resid_ptr}))
+
+    model._mm, model._rms_mm, model._glu_mm = record_mm, record_rms_mm, record_glu_mm
     try:
         tok = model._buf("rtok", 1, torch.int32)
         pos = model._buf("rpos", 1, torch.int32)
@@ -265,18 +273,19 @@ def record_decode_step(model, torch):
         model.forward(1, tok, pos, n_kv_for(model.n_past, c.n_ctx))
         torch.cuda.synchronize()
     finally:
-        model._mm, model._rms_mm = orig, orig_rms
+        model._mm, model._rms_mm, model._glu_mm = orig, orig_rms, orig_glu
     return calls
 
 
 def launch_bytes(calls):
     """Algorithmic bytes of GEMV calls: xlns16 weights once per weight
     slice, F32 in / out, the F32 residual read by the launches that fuse the
-    ADD after them, and the F32 norm row read by those that fuse the
-    rms_norm before them."""
+    ADD after them, the F32 norm row read by those that fuse the rms_norm
+    before them, and the F32 up row read by those that fuse the swiglu
+    before them."""
     return sum(2 * K * M * kw.get("ne02", 1) + 4 * K * N * kw.get("ne12", 1)
                + 4 * M * N * kw.get("ne12", 1) * (2 if kw.get("residual") is not None else 1)
-               + (4 * K if "norm" in kw else 0)
+               + (4 * K if "norm" in kw or "glu_up" in kw else 0)
                for _, _, _, K, M, N, kw in calls)
 
 
@@ -292,7 +301,7 @@ def chain_bound(model, ln, torch, mode):
     stays out of it.  bound_tok_s = 1 / (steps * ns_per_step)."""
     c = model.cfg
     steps = []
-    orig = (model._mm, model._rms_mul, model._softmax, model._attn, model._rms_mm)
+    orig = (model._mm, model._rms_mul, model._softmax, model._attn, model._rms_mm, model._glu_mm)
 
     def mm(w, x_ptr, dst_ptr, K, M, N, **kw):
         steps.append(K)
@@ -315,7 +324,12 @@ def chain_bound(model, ln, torch, mode):
             steps.append(K)
         orig[4](x_ptr, wn_ptr, w, h_ptr, dst_ptr, K, M, T)   # split: counted by rms and mm
 
-    model._mm, model._rms_mul, model._softmax, model._attn, model._rms_mm = mm, rms, sm, attn, rms_mm
+    def glu_mm(gate_ptr, up_ptr, w, resid_ptr, dst_ptr, K, M):
+        steps.append(K)
+        orig[5](gate_ptr, up_ptr, w, resid_ptr, dst_ptr, K, M)
+
+    model._mm, model._rms_mul, model._softmax, model._attn, model._rms_mm, model._glu_mm = (mm, rms, sm, attn, rms_mm,
+                                                                                          glu_mm)
     try:
         tok = model._buf("rtok", 1, torch.int32)
         pos = model._buf("rpos", 1, torch.int32)
@@ -325,7 +339,7 @@ def chain_bound(model, ln, torch, mode):
         model.forward(1, tok, pos, n_kv_for(model.n_past, c.n_ctx))
         torch.cuda.synchronize()
     finally:
-        model._mm, model._rms_mul, model._softmax, model._attn, model._rms_mm = orig
+        model._mm, model._rms_mul, model._softmax, model._attn, model._rms_mm, model._glu_mm = orig
     st = lambda: ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
     us = {}
     M = 576
@@ -492,6 +506,7 @@ def main():
     weights = llama.synthetic_weights(cfg, seed=1234, std=0.02)
     model = llama.LlamaLNS16(cfg, weights, mode=mode)
     model.fused_rms = model.fused_rms and not args.split_rms
+    model.fused_glu = model.fused_glu and not args.split_rms
     torch.cuda.synchronize()
     t_setup = time.perf_counter() - t0
 
@@ -567,8 +582,10 @@ def main():
                      "frac": round(achieved / HBM_PEAK_GBS, 6), "traffic": traffic,
                      "traffic_source": traffic_src,
                      "kernel": "decode GEMV launches: lnship16_mul_mat (k_mm16<%s, NC=1>, activations converted "
-                               "in-kernel)%s" % (args.mode, " and lnship16_rms_norm_mul_mat (k_mm16_rms, the rms_norm "
-                                                 "before the GEMV inside it)" if model.fused_rms else ""),
+                               "in-kernel; the down projections with the swiglu before them inside the launch "
+                               "through lnship16_swiglu_mul_mat)%s" % (
+                                   args.mode, " and lnship16_rms_norm_mul_mat (k_mm16_rms, the rms_norm before the "
+                                              "GEMV inside it)" if model.fused_rms else ""),
                      "launches_per_token": n_launch, "avg_launch_us": round(us_launch, 3),
                      "bytes_per_launch": int(b_launch)},
         "chain_bound": chain,

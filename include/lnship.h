@@ -158,6 +158,16 @@ int lnship32_rms_norm_mul(const float *src, const float *w, float *dst, int64_t 
  * only (LNSHIP_EINVAL otherwise). */
 int lnship16_rms_norm_mul_mat(int mode, const float *x, const float *norm_w, float eps, const void *w, float *dst,
                               int64_t K, int64_t M, void *stream);
+/* The GLU node's swiglu and the MUL_MAT that reads it, for one activation
+ * row (a decode step's down projection): dst[M] = W swiglu(gate, up)
+ * (+ residual, the ADD after the mul_mat, when non-null; it may be dst),
+ * with swiglu = silu(gate) * up over K elements in xlns16 and F32 between
+ * the nodes (lns_swiglu, src/lns-ops.cpp:809-862; then lns_mul_mat,
+ * :293-384).  W packed by lnship16_pack (K x M, default layout).  Equal, bit
+ * for bit, to lnship16_swiglu followed by lnship16_mul_mat.  Not for Monte
+ * (LNSHIP_EINVAL): its draws run in graph order. */
+int lnship16_swiglu_mul_mat(int mode, const float *gate, const float *up, const void *w, const float *residual,
+                            float *dst, int64_t K, int64_t M, void *stream);
 
 /* ---- SOFT_MAX (kernel_set::soft_max, :136; soft_max_args :62-71) --------
  * dst = softmax(src * scale + mask) over rows of src_ne[0] (lns_soft_max,

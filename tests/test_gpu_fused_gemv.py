@@ -1,11 +1,13 @@
-"""GPU parity of lnship16_rms_norm_mul_mat, the decode step's rms_norm, norm
-MUL and mul_mat in one launch (lns_rms_norm, lns_mul, lns_mul_mat:
-src/lns-ops.cpp:701-736, :468-530, :293-384), bit for bit against the CPU
-oracle of the three nodes and against the library's two-launch path.
-
-The kernel starts the mul_mat's chains from a predicted rms scale and runs
-them again when the rms chain's scale differs; the skew hook makes every
-prediction wrong, so the second pass is checked too."""
+"""GPU parity of the decode GEMVs that take the graph node before them into
+their launch, bit for bit against the CPU oracle of the separate nodes and
+against the library's separate launches:
+- lnship16_rms_norm_mul_mat: rms_norm, norm MUL and mul_mat (lns_rms_norm,
+  lns_mul, lns_mul_mat: src/lns-ops.cpp:701-736, :468-530, :293-384).  The
+  kernel starts the mul_mat's chains from a predicted rms scale and runs them
+  again when the rms chain's scale differs; the skew hook makes every
+  prediction wrong, so the second pass is checked too.
+- lnship16_swiglu_mul_mat: swiglu and the mul_mat with its residual ADD
+  (lns_swiglu, src/lns-ops.cpp:809-862, then lns_mul_mat and lns_add)."""
 import ctypes
 
 import numpy as np
@@ -133,3 +135,46 @@ def test_rms_norm_mul_mat_refuses_other_modes(ln):
                                                 ln._stream())
         assert rc == -1, (mode, rc)
         assert b"sum32 only" in ln.lib().lnship_last_error()
+
+
+def swiglu_oracle(gate, up):
+    L = O.lib()
+    L.lno16_swiglu_f32.argtypes = [ctypes.c_void_p] * 2 + [ctypes.c_int64, ctypes.c_void_p]
+    sw = np.empty_like(gate)
+    L.lno16_swiglu_f32(O._ptr(gate), O._ptr(up), gate.size, O._ptr(sw))
+    return sw
+
+
+@pytest.mark.parametrize("mode", ["base", "lpvip", "sum32"])
+@pytest.mark.parametrize("K,M", [(1536, 576), (13, 5), (1537, 193)])
+def test_swiglu_mul_mat_equals_two_nodes(ln, mode, K, M):
+    # the down projection's shape (up | gate rows of 2K, residual in place)
+    print(f"\n[swiglu_mul_mat] {mode} K={K} M={M}", flush=True)
+    m = O.MODES[mode]
+    rng = np.random.default_rng(K + 31 * M)
+    ug = (rng.standard_normal(2 * K) * 0.7).astype(np.float32)
+    w = (rng.standard_normal((M, K)) * 0.02).astype(np.float32)
+    resid = rng.standard_normal(M).astype(np.float32)
+    wp = ln.pack16(dev(w))
+    dug = dev(ug)
+    gate_p, up_p = ctypes.c_void_p(dug.data_ptr() + 4 * K), P(dug)
+    # without the residual: against the oracle
+    out = torch.empty(M, device="cuda")
+    ln.check(ln.lib().lnship16_swiglu_mul_mat(m, gate_p, up_p, P(wp), None, P(out), K, M, ln._stream()))
+    want = O.mul_mat16_f32w(m, w[None, None], swiglu_oracle(ug[K:].copy(), ug[:K].copy())[None, None, None])[0, 0, 0]
+    same_bits(host(out), want, f"swiglu_mul_mat {mode} K={K} M={M}")
+    # with the residual, written over it: against lnship16_swiglu, then the mul_mat with its ADD
+    x = dev(resid)
+    ln.check(ln.lib().lnship16_swiglu_mul_mat(m, gate_p, up_p, P(wp), P(x), P(x), K, M, ln._stream()))
+    sw = torch.empty(1, K, device="cuda")
+    ln.check(ln.lib().lnship16_swiglu(gate_p, 2 * K, up_p, 2 * K, P(sw), K, 1, ln._stream()))
+    ref = dev(resid)
+    ln.mul_mat16_raw(m, wp.data_ptr(), sw.data_ptr(), ref.data_ptr(), K, M, 1, residual=P(ref))
+    same_bits(host(x), host(ref), f"swiglu_mul_mat + residual {mode} K={K} M={M}")
+
+
+def test_swiglu_mul_mat_refuses_monte(ln):
+    x = torch.ones(16, device="cuda")
+    wp = ln.pack16(torch.ones(4, 8, device="cuda"))
+    out = torch.empty(4, device="cuda")
+    assert ln.lib().lnship16_swiglu_mul_mat(O.MONTE, P(x), P(x), P(wp), None, P(out), 8, 4, ln._stream()) == -1

@@ -787,6 +787,9 @@ struct mm_args16 {
     const float *norm;
     float eps;
     uint32_t skew;
+    // non-null (XL launches): the activation is swiglu(xf, glu_up), the GLU
+    // node before the mul_mat: up row n at glu_up + n * x_ld
+    const float *glu_up;
     // set by the launcher: the grid is 2^xcd_sh times wider than the work;
     // workgroup x works (as block x >> xcd_sh) iff x is a multiple of 2^xcd_sh
     uint32_t xcd_sh;
@@ -1103,6 +1106,18 @@ __global__ __launch_bounds__(k_block * CG) void k_mm16(mm_args16 a, dev_tables T
                 uint32_t c[B];
 #pragma unroll
                 for (int q = 0; q < B; q++) c[q] = x16_from_f32(T.cvt16, v[q]);
+                if (a.glu_up) {
+                    // swiglu as its node computes it (silu(gate) * up in
+                    // xlns16, F32 out), then into xlns16 as here
+                    const float *urow = a.glu_up + zx * a.x_slice + (nw + (int64_t)min(j, ncw - 1)) * a.x_ld;
+                    float u[B];
+#pragma unroll
+                    for (int q = 0; q < B; q++) u[q] = urow[min(k0 + q * nt, kl)];
+#pragma unroll
+                    for (int q = 0; q < B; q++)
+                        c[q] = x16_from_f32(T.cvt16, T.rev16[x16_mul(x16_mul(c[q], T.sig16[c[q]]),
+                                                                     x16_from_f32(T.cvt16, u[q]))]);
+                }
                 // every code in a register before the bounded stores: none of
                 // the batch's loads moves into a store's branch
 #pragma unroll
@@ -3145,6 +3160,29 @@ int lnship16_mul_mat(int mode, const lnship_mul_mat_args *a, void *stream) {
     }
 }
 
+
+int lnship16_swiglu_mul_mat(int mode, const float *gate, const float *up, const void *w, const float *residual,
+                            float *dst, int64_t K, int64_t M, void *stream) {
+    device_state *s = state();
+    if (!s) return LNSHIP_ENOINIT;
+    if (mode == LNSHIP_MONTE)
+        return fail(LNSHIP_EINVAL, "swiglu_mul_mat: Monte draws run in graph order; run the two nodes%s");
+    if (mode < 0 || mode > 3) return fail(LNSHIP_EINVAL, "unknown summation mode%s");
+    if (!gate || !up || !w || !dst || K < 1 || M < 0) return fail(LNSHIP_EINVAL, "swiglu_mul_mat: bad argument%s");
+    if (M == 0) return 0;
+    const int64_t kp = (K + 7) & ~(int64_t)7;
+    const mm16_shape sh = mm16_choose(mode, M, 1, 1, kp, s->cus);
+    if (!sh.xl) return fail(LNSHIP_ERANGE, "swiglu_mul_mat: row too long for LDS%s");
+    mm_args16 m{(const uint16_t *)w, nullptr, gate, dst, K, kp, M, 1, K, K, 1, 1, 1, 1, M, kp * M, M, M, 0, nullptr, 0};
+    m.glu_up = up;
+    m.resid = residual;
+    hipStream_t st = (hipStream_t)stream;
+    switch (mode) {
+        case LNSHIP_BASE: return dispatch_mm16<LNSHIP_BASE>(m, s->T, 1, sh, s->cus, st);
+        case LNSHIP_LPVIP: return dispatch_mm16<LNSHIP_LPVIP>(m, s->T, 1, sh, s->cus, st);
+        default: return dispatch_mm16<LNSHIP_SUM32>(m, s->T, 1, sh, s->cus, st);
+    }
+}
 
 // The xlns32 product once its activation rows have a staging block xs of
 // at least nslices * N * kp codes: k_act converts them (padding included, so

@@ -96,6 +96,7 @@ def lib():
         "lnship32_rms_norm_mul": (ctypes.c_int, [c_p, c_p, c_p, c_i64, c_i64, ctypes.c_float, c_p]),
         "lnship16_rms_norm_mul_mat": (ctypes.c_int, [ctypes.c_int, c_p, c_p, ctypes.c_float, c_p, c_p, c_i64,
                                                      c_i64, c_p]),
+        "lnship16_swiglu_mul_mat": (ctypes.c_int, [ctypes.c_int, c_p, c_p, c_p, c_p, c_p, c_i64, c_i64, c_p]),
         "lnship16_rope_store_kv": (ctypes.c_int, [ctypes.POINTER(QkvStoreArgs), c_p]),
         "lnship16_attn_decode": (ctypes.c_int, [ctypes.c_int, ctypes.POINTER(AttnArgs), c_p]),
         "lnship_max_row": (c_i64, [ctypes.c_int, ctypes.c_int]),

@@ -21,7 +21,9 @@ decode step outside Monte runs K^T q, soft_max and V p in one launch
 (lnship16_attn_decode, bit-identical to the three ops; fused_attn = False
 runs the three).  A single-row sum32 step runs each rms_norm, its norm MUL
 and the mul_mat that reads them in one launch (lnship16_rms_norm_mul_mat,
-bit-identical to the three; fused_rms = False runs them apart).
+bit-identical to the three; fused_rms = False runs them apart).  A single-row
+step outside Monte forms swiglu inside the down projection's launch
+(lnship16_swiglu_mul_mat; fused_glu = False runs the two).
 
 With n_seq > 1 the model holds that many independent sequences, each with
 its own KV cache, as llama.cpp's per-sequence KV streams.  A sequence's
@@ -120,6 +122,9 @@ class LlamaLNS16:
         # sum32, one row: rms_norm, the norm MUL and the mul_mat after them in
         # one launch (lnship16_rms_norm_mul_mat, bit-identical to the three)
         self.fused_rms = mode == SUM32
+        # one row outside Monte: swiglu inside the down projection's launch
+        # (lnship16_swiglu_mul_mat, bit-identical to the two nodes)
+        self.fused_glu = mode != MONTE
         self._attn_max_kv = lib().lnship_max_row(4, mode)
         dev = torch.device("cuda", torch.cuda.current_device())
         self.dev = dev
@@ -281,6 +286,11 @@ class LlamaLNS16:
             self._rms_mul(x_ptr, wn_ptr, h_ptr, K, T)
             self._mm(w, h_ptr, dst_ptr, K, M, T)
 
+    def _glu_mm(self, gate_ptr, up_ptr, w, resid_ptr, dst_ptr, K, M):
+        """dst = resid + W swiglu(gate, up) for one row of K, in one launch."""
+        check(lib().lnship16_swiglu_mul_mat(self.mode, gate_ptr, up_ptr, ctypes.c_void_p(w), resid_ptr, dst_ptr, K, M,
+                                            self._stream))
+
     def _attn(self, args):
         check(lib().lnship16_attn_decode(self.mode, ctypes.byref(args), self._stream))
 
@@ -349,8 +359,11 @@ class LlamaLNS16:
                 self._mm(W["wo"].data_ptr(), P(att), P(o), nq, e, T)
                 check(L.lnship16_add(P(o, r0), P(x, r0), rows * e, rows * e, P(x), st))
             self._rms_mm(P(x), P(W["ffn_norm"]), W["wug"].data_ptr(), P(h), P(ug), e, 2 * f, rows)
-            check(L.lnship16_swiglu(P(ug, f), 2 * f, P(ug), 2 * f, P(sw), f, rows, st))
-            self._mm(W["wdown"].data_ptr(), P(sw), P(x), f, e, rows, residual=P(x))
+            if rows == 1 and self.fused_glu:   # x += Wdown swiglu(gate, up), one launch
+                self._glu_mm(P(ug, f), P(ug), W["wdown"].data_ptr(), P(x), P(x), f, e)
+            else:
+                check(L.lnship16_swiglu(P(ug, f), 2 * f, P(ug), 2 * f, P(sw), f, rows, st))
+                self._mm(W["wdown"].data_ptr(), P(sw), P(x), f, e, rows, residual=P(x))
         nout = T if batch else 1
         self._rms_mm(P(x), P(self.out_norm), self.tok_embd.data_ptr(), P(h), P(logits), e, c.n_vocab, nout)
         if batch:
