@@ -27,6 +27,7 @@ struct dev_tables {
     const int32_t *lds32d;  // the same as the single-chain step reads it (dhi pairs' first words as ksb - th2)
     const uint16_t *lfsr_seq;
     const uint16_t *lfsr_log;
+    const uint16_t *rho16;  // rho16[c] = cvt16 of rev16[c]: a code through F32 and back, as between graph nodes
 };
 
 __device__ __forceinline__ uint32_t f32_bits(float f) { return __float_as_uint(f); }

@@ -1557,9 +1557,9 @@ __global__ __launch_bounds__(k_block) void k_mm16_rms(mm_args16 a, dev_tables T)
         for (int k = threadIdx.x; k < kp; k += k_block) {
             uint32_t h = 0;
             if (k < K) {
-                const float y = T.rev16[x16_mul(x16_from_f32(T.cvt16, a.xf[k]), inv)];
-                h = x16_from_f32(T.cvt16,
-                                 T.rev16[x16_mul(x16_from_f32(T.cvt16, y), x16_from_f32(T.cvt16, a.norm[k]))]);
+                // the two F32 round trips through rho16 (cvt16 of rev16)
+                const uint32_t y = T.rho16[x16_mul(x16_from_f32(T.cvt16, a.xf[k]), inv)];
+                h = T.rho16[x16_mul(y, x16_from_f32(T.cvt16, a.norm[k]))];
             }
             xl[k] = (uint16_t)h;
         }
@@ -2964,6 +2964,17 @@ int lnship_init(void) {
     dev_tables T{};
     if (int rc = upload(g_host->cvt16, 1u << 17, &T.cvt16)) return rc;
     if (int rc = upload(g_host->rev16, 1u << 16, &T.rev16)) return rc;
+    {
+        // an xlns16 code through F32 and back (the round trip between graph
+        // nodes), as x16_from_f32(cvt16, rev16[c]) forms it on the device
+        std::vector<uint16_t> rho(1u << 16);
+        for (uint32_t c = 0; c < (1u << 16); c++) {
+            uint32_t bits;
+            std::memcpy(&bits, &g_host->rev16[c], 4);
+            rho[c] = g_host->cvt16[bits >> 15];
+        }
+        if (int rc = upload(rho.data(), rho.size(), &T.rho16)) return rc;
+    }
     if (int rc = upload(g_host->gauss16, 2 * k16_gauss_n, &T.gauss16)) return rc;
     if (int rc = upload(g_host->gauss16m, 4 * k16_mc_n, &T.gauss16m)) return rc;
     if (int rc = upload(g_host->exp16, 1u << 16, &T.exp16)) return rc;
