@@ -9,7 +9,10 @@ device-side argmax, so the timed loop never waits for the host.
 
 Prints one JSON line with decode tok/s (value), prefill tok/s, weight
 mul_mat GMAC/s, the roofline of the dominant kernel (the decode GEMV) and the
-single-threaded CPU oracle timed on this host on a bounded sample.
+single-threaded CPU oracle timed on this host on a bounded sample.  The line
+also carries BASELINE config 5's prefill GEMM (prefill_gemm: GMAC/s in sum32
+and base against the VALU-issue roofline, parity and the oracle's rate on a
+slice of it).
 """
 import argparse
 import ctypes
@@ -34,6 +37,8 @@ def parse():
     ap.add_argument("--prompt", type=int, default=None, help="prompt tokens (128; 512 with --lns32)")
     ap.add_argument("--cpu-tokens", type=int, default=3, help="decode tokens of the CPU baseline sample")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-prefill-gemm", action="store_true",
+                    help="leave BASELINE config 5's GEMM (GMAC/s, sum32 and base) out of the default line")
     ap.add_argument("--no-graph", action="store_true", help="decode eagerly instead of replaying a HIP graph")
     ap.add_argument("--split-rms", action="store_true",
                     help="decode: rms_norm + MUL (sum32) and swiglu as launches of their own, apart from the "
@@ -401,6 +406,82 @@ def measured_traffic(mode):
         return None, None
 
 
+def device_clock_ghz():
+    """The device's peak engine clock (hipDeviceAttributeClockRate, kHz)."""
+    hip = ctypes.CDLL("libamdhip64.so")
+    v = ctypes.c_int()
+    if hip.hipDeviceGetAttribute(ctypes.byref(v), 5, 0) != 0:   # 5 = hipDeviceAttributeClockRate
+        return None
+    return v.value / 1e6
+
+
+def prefill_gemm(ln, torch, np, cpu=True, reps=10):
+    """BASELINE config 5's GEMM (K 2048, M 8192 outputs, N 512 tokens, xlns16
+    weights N(0, 0.02), activations N(0, 1)) in sum32 and base: mean launch
+    time of `reps` back-to-back launches between HIP events on the launch
+    stream, GMAC/s, and the VALU-issue roofline 256 CUs x peak clock x 64 lanes
+    / VALU instructions per MAC (from the committed rocprofv3 counters).
+    With cpu, the single-threaded C oracle is timed on a slice of the same
+    product (256 rows x 8 tokens) and the GPU's outputs there are compared
+    with its bit for bit."""
+    K, M, T = 2048, 8192, 512
+    gen = torch.Generator(device="cuda").manual_seed(5)
+    w = torch.randn(M, K, device="cuda", generator=gen) * 0.02
+    x = torch.randn(T, K, device="cuda", generator=gen)
+    wp = ln.pack16(w)
+    clock = device_clock_ghz()
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    try:
+        with open(os.path.join(ROOT, "profiles", "k_mm16_prefill_c5_valu.json")) as f:
+            prof = json.load(f)
+    except (OSError, ValueError):
+        prof = {}
+    out = {"workload": "mul_mat K=2048, M=8192, N=512 (BASELINE config 5), xlns16 weights N(0,0.02), "
+                       "activations N(0,1), %d launches timed with HIP events" % reps,
+           "macs_per_launch": K * M * T, "peak_clock_ghz": clock, "cus": cus}
+    sample = None
+    if cpu:
+        sys.path.insert(0, os.path.join(ROOT, "tests"))
+        import oracle_lib as O
+        ms, ns = 256, 8
+        w_codes = O.f2x16(w[:ms].cpu().numpy())
+        x_s = np.ascontiguousarray(x[:ns].cpu().numpy())
+    for mname in ("sum32", "base"):
+        m = ln.MODES[mname]
+        y = ln.mul_mat16(m, wp, x, K, M)
+        torch.cuda.synchronize()
+        s = torch.cuda.Event(enable_timing=True)
+        e = torch.cuda.Event(enable_timing=True)
+        s.record()
+        for _ in range(reps):
+            ln.mul_mat16(m, wp, x, K, M)
+        e.record()
+        e.synchronize()
+        us = s.elapsed_time(e) * 1e3 / reps
+        gmacs = K * M * T / us / 1e3
+        r = {"us_per_launch": round(us, 2), "gmacs": round(gmacs, 2)}
+        vpm = prof.get(mname, {}).get("valu_per_mac")
+        if vpm and clock:
+            peak = cus * clock * 64 / vpm
+            r["roofline"] = {"bound": "valu", "valu_per_mac": vpm, "peak_gmacs": round(peak, 1),
+                             "frac": round(gmacs / peak, 4), "lds_busy": prof[mname].get("lds_busy"),
+                             "lds_bank_conflict_rate": prof[mname].get("lds_bank_conflict_rate"),
+                             "source": "profiles/k_mm16_prefill_c5_valu.json"}
+        if cpu:
+            with _one_core():
+                t0 = time.perf_counter()
+                want = O.mul_mat16(O.MODES[mname], w_codes, x_s)
+                dt = time.perf_counter() - t0
+            got = np.ascontiguousarray(y[:ns, :ms].cpu().numpy(), np.float32)
+            r["cpu_baseline"] = {"value": round(ms * ns * K / dt / 1e9, 5), "unit": "GMAC/s", "cores": 1,
+                                 "kind": "port", "sample": "%d rows x %d tokens of the same product, single-threaded "
+                                                           "C oracle (%.2f s)" % (ms, ns, dt)}
+            r["parity"] = {"bit_exact": bool(np.array_equal(got.view(np.uint32), want.view(np.uint32))),
+                           "outputs": ms * ns}
+        out[mname] = r
+    return out
+
+
 def cpu_baseline(cfg, weights, mode, n_tokens):
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     import oracle_lib as O
@@ -598,6 +679,8 @@ def main():
         out["parity"] = logits_parity(model, ref, torch, np)
         if not out["parity"]["bit_exact"]:
             print("bench.py: GPU logits differ from the CPU oracle's", file=sys.stderr)
+    if not args.no_prefill_gemm:
+        out["prefill_gemm"] = prefill_gemm(lnship, torch, np, cpu=not args.no_cpu)
     print(json.dumps(out), flush=True)
 
 

@@ -269,7 +269,9 @@ int lnship32_rope_store_kv(const lnship_qkv_store_args *args, void *stream);
  * head g at k_cache + g * k_slice, its dims in groups of eight cache_m * 8
  * codes apart; value dim d < head_dim at v_cache + g * v_slice, its cells in
  * groups of eight head_dim * 8 codes apart.  q and dst [n_head][head_dim]
- * F32, mask [n_kv] F32 (optional; 0 or -inf).  n_kv <= lnship_max_row(4, mode). */
+ * F32, mask [n_kv] F32 (optional; 0 or -inf).  n_kv <= lnship_max_row(4, mode);
+ * a head_dim above 256 lowers that limit, and a launch that does not fit
+ * LDS returns LNSHIP_ERANGE (checked before any device call). */
 typedef struct lnship_attn_args {
     const float *q;
     const uint16_t *k_cache, *v_cache;
@@ -364,7 +366,9 @@ int lnship_causal_mask(const int32_t *pos, int64_t ntok, int64_t n_kv, float *ma
 
 /* Longest row (ncols) the row kernels stage in LDS: which = 0 xlns16
  * rms_norm, 1 xlns16 soft_max, 2 xlns32 rms_norm, 3 xlns32 soft_max, 4 the
- * cells (n_kv) of lnship16_attn_decode with head_dim up to 256 (0 for Monte);
+ * cells (n_kv) of lnship16_attn_decode with head_dim up to 256 (0 for Monte),
+ * 5 the K of lnship16_rms_norm_mul_mat (sum32; 0 for other modes), 6 the K
+ * of lnship16_swiglu_mul_mat (0 for Monte);
  * mode is the xlns16 summation mode (ignored for xlns32).  No GPU needed.  Plays the
  * role of the reference's grid / shape predicates (cuda/lns-cuda-ops.cpp:
  * 45-54, 184-189): a ggml backend declines longer rows in supports_op. */

@@ -7,7 +7,7 @@ The graph has the shapes and layouts llama.cpp hands the reference's
 LNSCUDA16 backend (cuda/lns-cuda-ops.cpp): an rms_norm and norm-weight MUL,
 a fused QKV MUL_MAT on F32 weights, RoPE on a strided view of it, the GQA kq
 MUL_MAT on an F16 KV-cache tensor against a permuted view, a masked
-SOFT_MAX, a Q8_0-weight MUL_MAT, SWIGLU fused and split, ADD with flat and
+SOFT_MAX, a Q8_0-weight and a Q4_K-weight MUL_MAT, SWIGLU fused and split, ADD with flat and
 general broadcasts, an F16-weight MUL_MAT, a repeated MUL_MAT that hits the
 weight cache, an unmasked SOFT_MAX, a MUL_MAT_ID over six experts and a
 MUL_MAT on GGML_TYPE_LNS16 weights (xlns16 codes, used as they are).  The oracle runs the same ops in
@@ -56,6 +56,35 @@ def q8_0(w, rng):
     raw[..., 2:] = q.view(np.uint8)
     deq = q.astype(np.float32) * d.astype(np.float32)[..., None]
     return raw.reshape(-1), deq.reshape(M, K)
+
+
+def q4_k(M, K, rng):
+    """Random Q4_K blocks for an [M, K] weight (K a multiple of 256) -> (block
+    bytes, the F32 values they decode to).  ggml's published layout: per 256
+    values a half d, a half dmin, 12 bytes of eight 6-bit (scale, min) pairs
+    and 128 bytes of 4-bit quants (value = d * scale * q - dmin * min)."""
+    nb = M * (K // 256)
+    raw = np.zeros((nb, 144), np.uint8)
+    d = (rng.uniform(0.5, 1.5, nb) * 0.02 / 63).astype(np.float16)
+    dmin = (rng.uniform(0.5, 1.5, nb) * 0.02 / 63).astype(np.float16)
+    raw[:, 0:2] = d.view(np.uint8).reshape(nb, 2)
+    raw[:, 2:4] = dmin.view(np.uint8).reshape(nb, 2)
+    raw[:, 4:16] = rng.integers(0, 256, (nb, 12), dtype=np.uint8)
+    raw[:, 16:] = rng.integers(0, 256, (nb, 128), dtype=np.uint8)
+    sb = raw[:, 4:16].astype(np.int32)
+    sc = np.zeros((nb, 8), np.int32)
+    mn = np.zeros((nb, 8), np.int32)
+    for j in range(4):
+        sc[:, j] = sb[:, j] & 63
+        mn[:, j] = sb[:, j + 4] & 63
+        sc[:, j + 4] = (sb[:, j + 8] & 15) | ((sb[:, j] >> 6) << 4)
+        mn[:, j + 4] = (sb[:, j + 8] >> 4) | ((sb[:, j + 4] >> 6) << 4)
+    q = raw[:, 16:].reshape(nb, 4, 32).astype(np.int32)
+    nib = np.stack([q & 15, q >> 4], axis=2).reshape(nb, 8, 32)   # sub-block 2r: low, 2r + 1: high nibbles
+    dd = d.astype(np.float32)[:, None] * sc.astype(np.float32)
+    dm = dmin.astype(np.float32)[:, None] * mn.astype(np.float32)
+    deq = dd[:, :, None] * nib.astype(np.float32) - dm[:, :, None]
+    return raw.reshape(-1), deq.astype(np.float32).reshape(M, K)
 
 
 def oracle_fns():
@@ -117,9 +146,11 @@ def mark_outputs(nodes, fused):
     over it in place, a pair graph_compute must not fuse.  Returns the
     checked keys.  "rms1" -> "mul1" -> "qkv1" is a decode step's norm and
     q|k|v product (one row): in sum32 graph_compute runs the three as one
-    launch, in the other modes the first two."""
-    skip = {"rms", "mm", "down", "rms1", "mul1"} if fused else set()
-    noflag = {"mm_self"} if fused else set()
+    launch, in the other modes the first two.  "rms2" -> "mul2" -> "mm2" is
+    such a row too long for the three-node launch: the pair runs fused and
+    "mul2" is written."""
+    skip = {"rms", "mm", "down", "rms1", "mul1", "rms2"} if fused else set()
+    noflag = {"mm_self", "mul2"} if fused else set()
     for k, tn in nodes.items():
         if k not in skip and k not in noflag:
             tn.flags |= FLAG_OUTPUT
@@ -162,6 +193,14 @@ def run16(mode_name, policy=None, dev=False, fused=False):
     xs = f32(T, E)
     wself = f32(E, E, scale=0.02)
     xdec = f32(1, E)
+    wq4_raw, wq4 = q4_k(128, 768, rng)
+    x4 = f32(T, 768)
+    # a decode row longer than lnship16_rms_norm_mul_mat holds in LDS: with
+    # fusion on, graph_compute runs its RMS_NORM -> MUL pair and the MUL_MAT
+    K2 = int(G.lnship_max_row(5, O.SUM32)) + 8
+    xdec2 = f32(1, K2)
+    g2 = f32(K2, scale=0.1, loc=1.0)
+    wlong = f32(64, K2, scale=0.02)
 
     t = lambda *a, **k: h.tensor(*a, device=None if k.get("weights") else act, **k)
     tw = lambda *a, **k: h.tensor(*a, device=wts, **k)
@@ -180,6 +219,10 @@ def run16(mode_name, policy=None, dev=False, fused=False):
     WL16 = tw([E, 200], "lns16", data=w_codes, weights=True, name="blk.0.attn_k_lns16.weight")
     XMOE = t([64, 1, T], data=xmoe, name="ffn_moe_inp")
     IDS = t([2, T], "i32", data=ids_moe, name="ffn_moe_topk")
+    WQ4 = h.tensor([768, 128], "q4_k", data=wq4_raw, weights=True, name="blk.0.ffn_gate.weight")
+    X4 = t([768, T], data=x4, name="ffn_inp_q4")
+    G2 = tw([K2], data=g2, weights=True, name="blk.1.attn_norm.weight")
+    WLONG = tw([K2, 64], data=wlong, weights=True, name="blk.1.attn_q.weight")
     swi = h.stub.ggml_host_glu(b"SWIGLU")
 
     nodes = {}
@@ -221,9 +264,15 @@ def run16(mode_name, policy=None, dev=False, fused=False):
     nodes["rms1"] = t([E, 1], op="RMS_NORM", src=(XD,), fparams={0: 1e-5}, name="norm-1")
     nodes["mul1"] = t([E, 1], op="MUL", src=(nodes["rms1"], Gw), name="attn_norm-1")
     nodes["qkv1"] = t([E + 2 * HKV * D, 1], op="MUL_MAT", src=(WQKV, nodes["mul1"]), name="qkv-2")
+    # a Q4_K weight (ggml's to_float, then converted and cached)
+    nodes["mm_q4k"] = t([128, T], op="MUL_MAT", src=(WQ4, X4), name="ffn_gate_q4-0")
+    XD2 = t([K2, 1], data=xdec2, name="inp_dec_long")
+    nodes["rms2"] = t([K2, 1], op="RMS_NORM", src=(XD2,), fparams={0: 1e-5}, name="norm-2")
+    nodes["mul2"] = t([K2, 1], op="MUL", src=(nodes["rms2"], G2), name="attn_norm-2")
+    nodes["mm2"] = t([64, 1], op="MUL_MAT", src=(WLONG, nodes["mul2"]), name="q-2")
     order = ["rms", "mul", "qkv", "view_q", "rope", "perm_q", "kq", "softmax", "ug", "swiglu", "view_g", "view_u",
              "swiglu_split", "add", "add_bcast", "down", "down_res", "qkv_again", "softmax_nomask", "moe", "mm_lns16",
-             "mm_self", "add_self", "rms1", "mul1", "qkv1"]
+             "mm_self", "add_self", "rms1", "mul1", "qkv1", "mm_q4k", "rms2", "mul2", "mm2"]
     views = {"view_q": qv, "perm_q": qp, "view_g": ga, "view_u": ua}
     graph = [views[k] if k in views else nodes[k] for k in order]
 
@@ -266,6 +315,10 @@ def run16(mode_name, policy=None, dev=False, fused=False):
     want["rms1"] = O.rms_norm16(mode_of("RMS_NORM", "norm-1"), xdec, 1e-5)
     want["mul1"] = binop(L.lno16_mul_f32, want["rms1"], g)
     want["qkv1"] = O.mul_mat16(mode_of("MUL_MAT", "qkv-2"), O.f2x16(wqkv), want["mul1"])
+    want["mm_q4k"] = O.mul_mat16_f32w(mode_of("MUL_MAT", "ffn_gate_q4-0"), wq4, x4)
+    want["rms2"] = O.rms_norm16(mode_of("RMS_NORM", "norm-2"), xdec2, 1e-5)
+    want["mul2"] = binop(L.lno16_mul_f32, want["rms2"], g2)
+    want["mm2"] = O.mul_mat16(mode_of("MUL_MAT", "q-2"), O.f2x16(wlong), want["mul2"])
 
     # the decode row's three nodes run as one launch only in sum32; otherwise
     # the norm MUL is written and checked like the other nodes

@@ -22,7 +22,18 @@ ABI_DIR = os.path.join(ROOT, "xlns-ggml-backend_amd", "csrc")
 
 FLAG_COMPUTE = 16
 USAGE_ANY, USAGE_WEIGHTS, USAGE_COMPUTE = 0, 1, 2
-TYPES = {"f32": (0, 4, 1), "f16": (1, 2, 1), "q8_0": (8, 34, 32), "i32": (26, 4, 1), "i64": (27, 8, 1), "lns16": (43, 2, 1)}
+TYPES = {"f32": (0, 4, 1), "f16": (1, 2, 1), "q8_0": (8, 34, 32), "q4_k": (12, 144, 256), "i32": (26, 4, 1), "i64": (27, 8, 1), "lns16": (43, 2, 1)}
+
+
+LNSHIP_SO = os.path.join(ROOT, "xlns-ggml-backend_amd", "liblnship.so")
+
+
+def lnship_max_row(which, mode):
+    """liblnship's row limits (no GPU needed)."""
+    lib = ctypes.CDLL(LNSHIP_SO)
+    lib.lnship_max_row.restype = ctypes.c_int64
+    lib.lnship_max_row.argtypes = [ctypes.c_int, ctypes.c_int]
+    return lib.lnship_max_row(which, mode)
 
 
 def build_stub():

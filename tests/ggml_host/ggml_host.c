@@ -44,7 +44,7 @@ const char *ggml_op_desc(const struct ggml_tensor *t) {
     return ggml_op_name(t->op);
 }
 
-/* ---- types: f32, f16, q8_0 (block of 32 int8 + half scale), i32, i64, lns16 --- */
+/* ---- types: f32, f16, q8_0 (block of 32 int8 + half scale), q4_K, i32, i64, lns16 --- */
 static float half_to_float(uint16_t h) {
     const uint32_t s = (uint32_t)(h >> 15) << 31, e = (h >> 10) & 0x1f, m = h & 0x3ff;
     uint32_t bits;
@@ -84,7 +84,44 @@ static void q8_0_to_float(const void *x, float *y, int64_t k) {
     }
 }
 
-enum { T_F32 = 0, T_F16 = 1, T_Q8_0 = 8, T_I32 = 26, T_I64 = 27, T_LNS16 = 43, T_COUNT = 44 };
+/* Q4_K, ggml's published block of 256 (144 bytes): half d, half dmin,
+ * 12 bytes of eight 6-bit (scale, min) pairs, 128 bytes of 4-bit quants.
+ * Sub-block j (32 values) has scale sc_j and min m_j: pairs 0-3 are the low
+ * 6 bits of bytes j and j + 4; pairs 4-7 take their low 4 bits from byte
+ * j + 4 (scale: low nibble, min: high nibble) and their top 2 bits from the
+ * top 2 bits of bytes j - 4 (scale) and j (min).  Quants come in 32-byte
+ * runs: the low nibbles of a run are sub-block 2i, its high nibbles 2i + 1;
+ * value = d * sc * q - dmin * m. */
+static void q4_k_pair(int j, const uint8_t *s, int *sc, int *m) {
+    if (j < 4) {
+        *sc = s[j] & 63;
+        *m = s[j + 4] & 63;
+    } else {
+        *sc = (s[j + 4] & 15) | ((s[j - 4] >> 6) << 4);
+        *m = (s[j + 4] >> 4) | ((s[j] >> 6) << 4);
+    }
+}
+
+static void q4_k_to_float(const void *x, float *y, int64_t k) {
+    const uint8_t *b = (const uint8_t *)x;
+    for (int64_t i = 0; i < k / 256; i++, b += 144) {
+        uint16_t dh, mh;
+        memcpy(&dh, b, 2);
+        memcpy(&mh, b + 2, 2);
+        const float d = half_to_float(dh), dmin = half_to_float(mh);
+        const uint8_t *sc = b + 4, *q = b + 16;
+        for (int r = 0; r < 4; r++, q += 32) {
+            int s0, m0, s1, m1;
+            q4_k_pair(2 * r, sc, &s0, &m0);
+            q4_k_pair(2 * r + 1, sc, &s1, &m1);
+            const float d0 = d * (float)s0, o0 = dmin * (float)m0, d1 = d * (float)s1, o1 = dmin * (float)m1;
+            for (int l = 0; l < 32; l++) *y++ = d0 * (float)(q[l] & 15) - o0;
+            for (int l = 0; l < 32; l++) *y++ = d1 * (float)(q[l] >> 4) - o1;
+        }
+    }
+}
+
+enum { T_F32 = 0, T_F16 = 1, T_Q8_0 = 8, T_Q4_K = 12, T_I32 = 26, T_I64 = 27, T_LNS16 = 43, T_COUNT = 44 };
 
 static struct ggml_type_traits k_traits[T_COUNT];
 
@@ -96,6 +133,7 @@ static void init_traits(void) {
     k_traits[T_F32] = (struct ggml_type_traits){"f32", 1, 0, 4, false, NULL, NULL};
     k_traits[T_F16] = (struct ggml_type_traits){"f16", 1, 0, 2, false, f16_to_float, NULL};
     k_traits[T_Q8_0] = (struct ggml_type_traits){"q8_0", 32, 0, 34, true, q8_0_to_float, NULL};
+    k_traits[T_Q4_K] = (struct ggml_type_traits){"q4_K", 256, 0, 144, true, q4_k_to_float, NULL};
     k_traits[T_I32] = (struct ggml_type_traits){"i32", 1, 0, 4, false, NULL, NULL};
     k_traits[T_I64] = (struct ggml_type_traits){"i64", 1, 0, 8, false, NULL, NULL};
     k_traits[T_LNS16] = (struct ggml_type_traits){"lns16", 1, 0, 2, false, NULL, NULL};

@@ -148,3 +148,81 @@ def test_rope_table_uses_the_float_recurrence(lnship):
             assert got[(p * 32 + j) * 2] == np.float32(libm.cosf(t))
             assert got[(p * 32 + j) * 2 + 1] == np.float32(libm.sinf(t))
             t = np.float32(t * ts)
+
+
+def test_fused_row_limits(lnship):
+    # the fused one-row kernels hold their rows in LDS beside the tables, so
+    # callers ask for their limits before fusing (lnship_max_row 5 and 6)
+    L = lnship.lib()
+    rms_mm = L.lnship_max_row(5, lnship.SUM32)
+    # the three-node launch takes SmolLM2's and Llama-1B's rows, but fewer
+    # than the rms_norm node alone: a ggml graph may hold rows in between
+    assert 2048 <= rms_mm < L.lnship_max_row(0, lnship.SUM32)
+    assert rms_mm % 8 == 0
+    for m in (lnship.BASE, lnship.MONTE, lnship.LPVIP):
+        assert L.lnship_max_row(5, m) == 0
+    assert L.lnship_max_row(6, lnship.MONTE) == 0
+    for m in (lnship.BASE, lnship.LPVIP, lnship.SUM32):
+        glu = L.lnship_max_row(6, m)
+        assert glu >= 8192 and glu % 8 == 0   # Llama-1B's FFN
+
+
+def test_attn_decode_refuses_wide_heads_before_any_device_call(lnship):
+    # lnship_max_row(4) holds for head_dim <= 256; a wider head at that n_kv
+    # does not fit LDS and must be refused as a size error, not fail at launch
+    L = lnship.lib()
+    n_kv = L.lnship_max_row(4, lnship.SUM32)
+    fake = ctypes.c_void_p(0x1000)   # never dereferenced: the size check comes first
+    a = lnship.AttnArgs()
+    a.q = a.k_cache = a.v_cache = a.dst = fake.value
+    a.cache_m, a.n_head, a.n_head_kv, a.n_kv, a.scale = n_kv, 8, 8, n_kv, 0.125
+    ERANGE, ENOINIT = -4, -3   # include/lnship.h: enum lnship_error
+    for hd, want in ((1024, ERANGE), (4096, ERANGE)):
+        a.head_dim = hd
+        assert L.lnship16_attn_decode(lnship.SUM32, ctypes.byref(a), None) == want
+        assert b"LDS" in L.lnship_last_error()
+    # a head_dim within the limit passes the checks and then needs a device
+    a.head_dim = 64
+    assert L.lnship16_attn_decode(lnship.SUM32, ctypes.byref(a), None) == ENOINIT
+
+
+def test_q4_k_host_to_float():
+    # the test ggml host's Q4_K to_float (ggml's published block layout)
+    # equals the graph check's numpy restatement, and a hand-made block
+    # decodes to the values its fields name
+    import ggml_host as G
+    import ggml_graph_check as C
+    G.build_stub()
+    stub = ctypes.CDLL(G.STUB_SO)
+    stub.ggml_get_type_traits.restype = ctypes.c_void_p
+    stub.ggml_get_type_traits.argtypes = [ctypes.c_int]
+
+    class Traits(ctypes.Structure):
+        _fields_ = [("type_name", ctypes.c_char_p), ("blck_size", ctypes.c_int64),
+                    ("blck_size_interleave", ctypes.c_int64), ("type_size", ctypes.c_size_t),
+                    ("is_quantized", ctypes.c_bool),
+                    ("to_float", ctypes.CFUNCTYPE(None, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64))]
+
+    tr = Traits.from_address(stub.ggml_get_type_traits(12))
+    assert (tr.type_name, tr.blck_size, tr.type_size, tr.is_quantized) == (b"q4_K", 256, 144, True)
+    rng = np.random.default_rng(5)
+    raw, want = C.q4_k(3, 512, rng)
+    got = np.empty(3 * 512, np.float32)
+    tr.to_float(raw.ctypes.data, got.ctypes.data, got.size)
+    assert np.array_equal(got.view(np.uint32), want.reshape(-1).view(np.uint32))
+    # d = 1, dmin = 0.5; pair j: scale j + 1, min 2j (6-bit packing of
+    # pairs 4-7 spread over three bytes); quants 0..15 repeating
+    blk = np.zeros(144, np.uint8)
+    blk[0:2] = np.array([1.0], np.float16).view(np.uint8)
+    blk[2:4] = np.array([0.5], np.float16).view(np.uint8)
+    sc, mn = list(range(1, 9)), [2 * j for j in range(8)]
+    for j in range(4):
+        blk[4 + j] = (sc[j] & 63) | ((sc[j + 4] >> 4) << 6)
+        blk[8 + j] = (mn[j] & 63) | ((mn[j + 4] >> 4) << 6)
+        blk[12 + j] = (sc[j + 4] & 15) | ((mn[j + 4] & 15) << 4)
+    blk[16:] = np.arange(128, dtype=np.uint8) % 16 * 17   # both nibbles l % 16
+    out = np.empty(256, np.float32)
+    tr.to_float(blk.ctypes.data, out.ctypes.data, 256)
+    for j in range(8):
+        q = np.arange(32) % 16
+        assert np.array_equal(out[32 * j:32 * j + 32], (sc[j] * q - 0.5 * mn[j]).astype(np.float32))

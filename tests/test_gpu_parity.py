@@ -668,7 +668,8 @@ def test_mul_mat_id_expert_out_of_range(ln):
     ("sum32", 2048, False, 0), ("sum32", 1, False, 1), ("sum32", 13, False, -1), ("sum32", 256, True, 3),
     ("sum32", 520, False, -7)])
 def test_attn_decode_equals_three_nodes(ln, mode, n_kv, big_tail, skew):
-    # lnship16_attn_decode against K^T q, soft_max and V p run as three ops, on
+    # lnship16_attn_decode against K^T q, soft_max and V p run as three ops
+    # (the library's own launches, and the oracle's), on
     # the SmolLM2 head shape (9 query heads over 3 kv heads of 64), random
     # caches and a causal mask that hides the last cells.  Past the last
     # nonzero exp the KQV chain stops only where the remaining products add
@@ -685,11 +686,14 @@ def test_attn_decode_equals_three_nodes(ln, mode, n_kv, big_tail, skew):
     v = (rng.standard_normal((nkv, hd, n_ctx)) * 0.5).astype(np.float32)
     if big_tail:
         v[:, :, pos + 1:n_kv] *= np.float32(1e35)
-    kc = ln.pack16(dev((rng.standard_normal((nkv, n_ctx, hd)) * 0.5).astype(np.float32)))
+    kf = (rng.standard_normal((nkv, n_ctx, hd)) * 0.5).astype(np.float32)
+    kc = ln.pack16(dev(kf))
     vc = ln.pack16(dev(v))
     kslice, vslice = ln.kp(hd) * n_ctx, ln.kp(n_ctx) * hd
-    q = dev((rng.standard_normal(nh * hd) * 2).astype(np.float32))
-    mask = dev(np.where(np.arange(n_kv) <= pos, 0.0, -np.inf).astype(np.float32))
+    qf = (rng.standard_normal(nh * hd) * 2).astype(np.float32)
+    maskf = np.where(np.arange(n_kv) <= pos, 0.0, -np.inf).astype(np.float32)
+    q = dev(qf)
+    mask = dev(maskf)
     scale = 0.125
     P = lambda t: t.data_ptr()
     kq = torch.empty(nh * n_kv, device="cuda")
@@ -707,6 +711,12 @@ def test_attn_decode_equals_three_nodes(ln, mode, n_kv, big_tail, skew):
     finally:
         ln.lib().lnship_test_predict_skew(prev)
     same_bits(host(got), host(want), f"attn decode {mode} n_kv={n_kv} skew={skew}")
+    # and against the oracle's three ops: the GQA kq product (query head h on
+    # kv head h / 3), the masked soft_max, then the kqv product
+    kq_o = O.mul_mat16_f32w(m, kf[None, :, :n_kv], qf.reshape(1, nh, 1, hd), ne02=nkv)[0]
+    p_o = O.soft_max16(m, kq_o, maskf[None], scale)
+    want_o = O.mul_mat16_f32w(m, v[None, :, :, :n_kv], p_o[None], ne02=nkv)[0]
+    same_bits(host(got), want_o.reshape(-1), f"attn decode {mode} n_kv={n_kv} skew={skew} vs oracle")
     if mode == "sum32" and n_kv == 13 and not big_tail:
         # Monte is refused (its draws run across the three nodes in graph order)
         assert ln.lib().lnship16_attn_decode(O.MONTE, ctypes.byref(a), ln._stream()) != 0

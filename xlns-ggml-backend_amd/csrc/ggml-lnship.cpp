@@ -1697,6 +1697,9 @@ static bool feeds_only(const ggml_cgraph *g, int i, const ggml_tensor *next) {
 // an F32 tensor (upload() gathers any layout into a dense copy)
 static bool plain_f32(const ggml_tensor *t) { return t->type == GGML_TYPE_F32; }
 
+// whether lnship16_rms_norm_mul_mat takes a row of K (sum32)
+static bool rms_mul_mat_fits(int64_t K) { return K >= 1 && K <= lnship_max_row(5, LNSHIP_SUM32); }
+
 // RMS_NORM t -> MUL next -> MUL_MAT mm of one sum32 row in one launch, when
 // next feeds only mm (as its activation) and mm's output overlaps neither
 // the row nor the norm weight (the kernel reads them until its last chain)
@@ -1710,6 +1713,9 @@ static bool run_rms_mul_mat(context &ctx, ggml_cgraph *g, int i, const ggml_tens
     const ggml_tensor *a = mm->src[0];
     if (a->ne[0] != t->ne[0] || a->ne[2] != 1 || a->ne[3] != 1 || nelements(mm) != a->ne[1] || !plain_f32(mm))
         return false;
+    // the fused kernel holds the row and h in LDS beside the tables: longer
+    // rows run as the separate nodes
+    if (!rms_mul_mat_fits(a->ne[0])) return false;
     if (overlaps(mm, t->src[0]) || overlaps(mm, w)) return false;
     // the weight first: packing a host weight stages it through R_SRC0
     const void *wm = ctx.lns_matrix(a);

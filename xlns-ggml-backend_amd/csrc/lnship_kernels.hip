@@ -2734,6 +2734,14 @@ static int64_t max_attn_kv() {
     return ((k_lds_bytes - k_lds_static - attn16_lds<MODE>(256, 0)) / 4) & ~(int64_t)7;
 }
 
+// the dynamic LDS of a k_attn16 launch (64-bit: head_dim may be up to 4096)
+static int64_t attn16_lds_mode(int mode, int64_t hd, int64_t n_kv) {
+    const int64_t off = mode == LNSHIP_BASE ? mm_xl_offset<LNSHIP_BASE>()
+                        : mode == LNSHIP_LPVIP ? mm_xl_offset<LNSHIP_LPVIP>()
+                                               : mm_xl_offset<LNSHIP_SUM32>();
+    return off + 2 * ((hd + 7) & ~(int64_t)7) + 4 * ((n_kv + 7) & ~(int64_t)7);
+}
+
 template <int MODE>
 static int launch_sm16(sm_args &m, int64_t nrows, const dev_tables &T, hipStream_t st) {
     const int64_t rs = (m.n + 7) & ~(int64_t)7;
@@ -3454,8 +3462,7 @@ int lnship16_soft_max(int mode, const lnship_soft_max_args *a, void *stream) {
 }
 
 int lnship16_attn_decode(int mode, const lnship_attn_args *a, void *stream) {
-    device_state *s = state();
-    if (!s) return LNSHIP_ENOINIT;
+    // arguments and sizes first: they need no device
     if (!a) return fail(LNSHIP_EINVAL, "attn_decode: null args%s");
     if (mode == LNSHIP_MONTE)
         return fail(LNSHIP_EINVAL, "attn_decode: Monte draws run across the three nodes in graph order; run them%s");
@@ -3465,6 +3472,11 @@ int lnship16_attn_decode(int mode, const lnship_attn_args *a, void *stream) {
         a->head_dim > 4096 || a->n_head > 65535)
         return fail(LNSHIP_EINVAL, "attn_decode: bad argument%s");
     if (a->n_kv > lnship_max_row(4, mode)) return fail(LNSHIP_ERANGE, "attn_decode: n_kv too long for LDS%s");
+    // the limit above holds for head_dim <= 256; wider heads need more LDS
+    if ((int64_t)attn16_lds_mode(mode, a->head_dim, a->n_kv) > k_lds_bytes - k_lds_static)
+        return fail(LNSHIP_ERANGE, "attn_decode: head_dim x n_kv too large for LDS%s");
+    device_state *s = state();
+    if (!s) return LNSHIP_ENOINIT;
     const attn_args m{a->q, a->k_cache, a->v_cache, a->cache_m * 8, a->k_slice, a->head_dim * 8, a->v_slice,
                       a->mask, a->scale, a->dst, (int)a->head_dim, (int)a->n_kv, (int)(a->n_head / a->n_head_kv),
                       g_predict_skew};
@@ -3497,6 +3509,16 @@ int lnship32_soft_max(const lnship_soft_max_args *a, void *stream) {
 
 int64_t lnship_max_row(int which, int mode) {
     if (which == 2 || which == 3) return max_row<LNSHIP_SUM32>(4);
+    if (which == 5) {
+        // lnship16_rms_norm_mul_mat: the tables, the x row and h (4 B per k)
+        if (mode != LNSHIP_SUM32) return 0;
+        return ((k_lds_bytes - 1024 - mm_xl_offset<LNSHIP_SUM32>() - k_xl_pad) / 4) & ~(int64_t)7;
+    }
+    if (which == 6) {
+        // lnship16_swiglu_mul_mat: one activation row in LDS beside the tables
+        if (mode < 0 || mode > 3 || mode == LNSHIP_MONTE) return 0;
+        return ((k_lds_bytes - 1024 - mm16_tables_bytes(mode) - k_xl_pad) / 2) & ~(int64_t)7;
+    }
     if (which == 4) {
         switch (mode) {
             case LNSHIP_BASE: return max_attn_kv<LNSHIP_BASE>();

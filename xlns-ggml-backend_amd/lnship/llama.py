@@ -120,11 +120,13 @@ class LlamaLNS16:
         # decode attention in one launch where the op takes the mode and the cells
         self.fused_attn = mode != MONTE
         # sum32, one row: rms_norm, the norm MUL and the mul_mat after them in
-        # one launch (lnship16_rms_norm_mul_mat, bit-identical to the three)
-        self.fused_rms = mode == SUM32
+        # one launch (lnship16_rms_norm_mul_mat, bit-identical to the three),
+        # where the row fits the kernel's LDS
+        self.fused_rms = mode == SUM32 and cfg.n_embd <= lib().lnship_max_row(5, mode)
         # one row outside Monte: swiglu inside the down projection's launch
-        # (lnship16_swiglu_mul_mat, bit-identical to the two nodes)
-        self.fused_glu = mode != MONTE
+        # (lnship16_swiglu_mul_mat, bit-identical to the two nodes), where the
+        # activation row fits LDS
+        self.fused_glu = mode != MONTE and cfg.n_ff <= lib().lnship_max_row(6, mode)
         self._attn_max_kv = lib().lnship_max_row(4, mode)
         dev = torch.device("cuda", torch.cuda.current_device())
         self.dev = dev
