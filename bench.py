@@ -443,7 +443,7 @@ def prefill_gemm(ln, torch, np, cpu=True, reps=10):
     if cpu:
         sys.path.insert(0, os.path.join(ROOT, "tests"))
         import oracle_lib as O
-        ms, ns = 256, 8
+        ms, ns = 512, 64
         w_codes = O.f2x16(w[:ms].cpu().numpy())
         x_s = np.ascontiguousarray(x[:ns].cpu().numpy())
     for mname in ("sum32", "base"):

@@ -472,12 +472,15 @@ class LlamaLNS32:
     as lns32_mul_mat converts it, :64-79).  weights may hold host arrays or
     device tensors (float32)."""
 
-    def __init__(self, cfg, weights):
+    def __init__(self, cfg, weights, device=None):
         import torch
         init()
         self.cfg = cfg
         self.torch = torch
-        dev = torch.device("cuda", torch.cuda.current_device())
+        # device: where the weights, caches and buffers live (default the
+        # current GPU; a CPU device lets a test audit the launch arguments
+        # against the allocations with a recording stand-in for the library)
+        dev = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
         self.dev = dev
         c = cfg
         from . import pack32
