@@ -55,7 +55,8 @@ const char *lnship_last_error(void);
 /* the build's identity string */
 const char *lnship_version(void);
 /* Host copy of one arithmetic table ("cvt16", "rev16", "gauss16",
- * "gauss16m", "exp16", "tab32", "lfsr_seq"); builds the tables on first use,
+ * "gauss16m", "exp16", "tab32", "lfsr_seq", and "pos32": the positive-sum
+ * adder's (node, scaled slope) pairs of sb); builds the tables on first use,
  * needs no GPU.  No counterpart in the reference: it lets tests compare the
  * tables with an independent restatement. */
 const void *lnship_host_table(const char *name, size_t *bytes);
@@ -341,8 +342,10 @@ int lnship_lpvip_db_range(uint32_t d0, uint32_t n, int32_t *out, void *stream);
 /* Test hook: out[i] = x[i] + y[i] (xlns32 codes, sign bit 31) by the xlns32
  * adder over its LDS tables, as the sum32 and LNS32 kernels run it: form 0
  * the multi-chain step (prefill GEMMs, soft_max, rms_norm's epsilon), 1 the
- * single-chain step of the decode GEMVs, 2 the positive-sum step of
- * rms_norm / soft_max (sign bits ignored).  The arithmetic is xlns32_add as
+ * single-chain step of the decode GEMVs, 2 the positive-sum step of the
+ * fused decode kernels' rms_norm / soft_max sums, 3 the positive-sum step of
+ * the rms_norm and soft_max row kernels over the pair image (2 and 3: sign
+ * bits ignored).  The arithmetic is xlns32_add as
  * src/lns16-sum32.h:59-198 configures xlnscpp (xlns32_alt).  No counterpart
  * in the reference. */
 int lnship32_add_lds(int form, const uint32_t *x, const uint32_t *y, uint32_t *out, int64_t n, void *stream);

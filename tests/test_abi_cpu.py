@@ -226,3 +226,32 @@ def test_q4_k_host_to_float():
     for j in range(8):
         q = np.arange(32) % 16
         assert np.array_equal(out[32 * j:32 * j + 32], (sc[j] * q - 0.5 * mn[j]).astype(np.float32))
+
+
+def test_positive_sum_pair_image(lnship):
+    # the row kernels' positive-sum adder: per sb interval the node and the
+    # slope scaled by 2^10 (near grid, fraction scaled by 2^9) or 2^9 (far
+    # grid, fraction by 2^4), both 24-bit signed operands of
+    # v_mul_hi_i32_i24; the high word of their product is then exactly
+    # floor((t1 - t0) * f / 2^sh), the oracle's interpolation term
+    img = lnship.host_table("pos32", np.int32).reshape(-1, 2)
+    L = O.lib()
+    sb = O.table32("sb")
+    sbf = O.table32("sbf")
+    nn = sb.size - 1
+    assert np.array_equal(img[:nn, 0], sb[:-1])
+    assert np.array_equal(img[:nn, 1].astype(np.int64), (sb[1:].astype(np.int64) - sb[:-1]) << 10)
+    # the far grid, extended with zeros out to every distance below 2^31
+    nf = ((1 << 31) - 12 * (1 << 23)) >> 19
+    far = np.zeros(nf + 1, np.int64)
+    far[:sbf.size] = sbf
+    assert img.shape[0] >= nn + nf
+    assert np.array_equal(img[nn:nn + nf, 0], far[:-1])
+    assert np.array_equal(img[nn:nn + nf, 1].astype(np.int64), (far[1:] - far[:-1]) << 9)
+    assert sbf[-1] == 0 and np.all(np.abs(img[:, 1].astype(np.int64)) <= 1 << 23)
+    # the product identity on every fraction of the steepest intervals
+    for t, sc, fs, sh in ((img[:nn], 10, 9, 13), (img[nn:nn + nf], 9, 4, 19)):
+        i = int(np.argmin(t[:, 1]))
+        f = np.arange(1 << sh, dtype=np.int64)
+        slope = int(t[i, 1]) >> sc
+        assert np.array_equal((int(t[i, 1]) * (f << fs)) >> 32, (slope * f) >> sh)

@@ -114,6 +114,38 @@ def test_xlns32_lds_adder_every_case(ln):
                                f"got {got[bad[0]]:#x} want {ref[bad[0]]:#x}")
 
 
+def test_xlns32_positive_adders_every_grid_node(ln):
+    # the two positive-sum forms (2: over the adder's image, 3: over the
+    # pair image of the row kernels) at every sb grid node and its
+    # neighbours, random distances to 30 binades and the saturating end,
+    # against xlns32_add
+    import ctypes
+    rng = np.random.default_rng(29)
+    B = 1 << 23
+    near = np.arange(0, 12 * B + 1, 1 << 13, dtype=np.int64)
+    far = np.arange(12 * B, 24 * B + 1, 1 << 19, dtype=np.int64)
+    d = np.concatenate([near, near + 1, near + (1 << 13) - 1, far, far + 1, far + (1 << 19) - 1, far - 1,
+                        rng.integers(0, 30 * B, 1 << 16), np.array([0, 24 * B - 1, 24 * B, 24 * B + 1])])
+    d = d[d >= 0]
+    a = rng.integers(32 * B, (1 << 31) - 32 * B, d.size)
+    b = np.where(rng.integers(0, 2, d.size) == 1, a + d, a - d)
+    hi = rng.integers((1 << 31) - (1 << 22), 1 << 31, 2048)
+    x = np.concatenate([a, hi]).astype(np.uint32)
+    y = np.concatenate([b, rng.integers((1 << 31) - (1 << 24), 1 << 31, 2048)]).astype(np.uint32)
+    add = O.lib().lno32_add
+    want = np.array([add(int(p), int(q)) for p, q in zip(x, y)], np.uint32)
+    dx, dy = dev(x.view(np.int32)), dev(y.view(np.int32))
+    for form in (2, 3):
+        print(f"\n[xlns32 positive adder] form {form}, {x.size} pairs", flush=True)
+        out = torch.empty_like(dx)
+        ln.check(ln.lib().lnship32_add_lds(form, ctypes.c_void_p(dx.data_ptr()), ctypes.c_void_p(dy.data_ptr()),
+                                            ctypes.c_void_p(out.data_ptr()), x.size, ln._stream()))
+        got = host(out).view(np.uint32)
+        bad = np.nonzero(got != want)[0]
+        assert bad.size == 0, (f"form {form}: {bad.size} differ; first x={x[bad[0]]:#x} y={y[bad[0]]:#x}: "
+                               f"got {got[bad[0]]:#x} want {want[bad[0]]:#x}")
+
+
 def test_xlns32_conversion_sampled(ln):
     rng = np.random.default_rng(11)
     bits = rng.integers(0, 1 << 32, 1 << 20, dtype=np.uint64).astype(np.uint32)

@@ -25,6 +25,7 @@ struct dev_tables {
     const int32_t *tab32;
     const int32_t *lds32;   // the LDS image of the xlns32 adder tables (after the descriptors)
     const int32_t *lds32d;  // the same as the single-chain step reads it (dhi pairs' first words as ksb - th2)
+    const int32_t *pos32;   // the LDS image of the positive-sum adder (sb's (node, scaled slope) pairs)
     const uint16_t *lfsr_seq;
     const uint16_t *lfsr_log;
     const uint16_t *rho16;  // rho16[c] = cvt16 of rev16[c]: a code through F32 and back, as between graph nodes

@@ -54,6 +54,24 @@ constexpr int kl_zero = kl_dbf + k32_db_fn;
 constexpr int kl_end = (kl_zero + 4 + 3) & ~3;
 constexpr int k_lds_tab32 = kl_end * 4;   // 134496 bytes
 static_assert(kl_dlo % 4 == 0 && (kl_end - kl_dlo) % 4 == 0, "16-byte staging");
+// The LDS image of the positive-sum adder (kernels whose only xlns32
+// additions add positive values: rms_norm's sum of squares, soft_max's sum
+// of exps): one (node, scaled slope) pair per grid interval of sb, the near
+// grid's k32_sb_n - 1 intervals then the far grid's, extended with (0, 0)
+// pairs from the essential zero to every distance below 2^31, so that no
+// distance needs a cap.  A slope is
+// t[i + 1] - t[i] scaled by 2^10 (near) or 2^9 (far): a 24-bit signed
+// operand of v_mul_hi_i32_i24 whose product with the interval's fraction
+// scaled by 2^9 (near) or 2^4 (far) has the floored interpolation term in
+// its high word.
+constexpr int kp32_near = k32_sb_n - 1;
+constexpr int kp32_far = (int)((0x80000000u - k32_sb_end) >> k32_sb_fsh);
+constexpr int kp32_pairs = (kp32_near + kp32_far + 1) & ~1;
+constexpr int k_lds_pos32 = 8 * kp32_pairs;   // 129536 bytes
+constexpr int kp32_near_slope = 10, kp32_near_frac = 9, kp32_far_slope = 9, kp32_far_frac = 4;
+static_assert(kp32_near_slope + kp32_near_frac == 32 - k32_sb_sh, "near interpolation scale");
+static_assert(kp32_far_slope + kp32_far_frac == 32 - k32_sb_fsh, "far interpolation scale");
+static_assert((k32_sb_end & ((1u << k32_sb_fsh) - 1)) == 0, "the far grid starts on a far node");
 
 static thread_local std::string t_err;
 
@@ -564,6 +582,38 @@ __device__ __forceinline__ uint32_t x32_add_pos(const x32_tab &O, uint32_t al, u
     return (uint32_t)__builtin_elementwise_add_sat(mx, ip);
 }
 
+// The positive-sum addition over the pair image (k_lds_pos32): the same
+// result as x32_add_pos in fewer dependent operations.  The addresses of
+// both grids' pairs are formed side by side and one is picked by the far
+// mask; the interpolation term is the high word of one 24-bit multiply of
+// the stored scaled slope and the scaled fraction (formed while the read is
+// in flight), so after the read only that multiply and two adds remain.
+struct pos_tab {
+    uint32_t near, far;   // LDS byte addresses: near pairs, far pairs less the far grid's origin
+    uint32_t one, zero;   // 1 and 0 in registers the compiler cannot see into
+};
+__device__ __forceinline__ int32_t sext24(uint32_t x) { return (int32_t)(x << 8) >> 8; }
+// On one wave every instruction is on the chain's clock, so the read is
+// issued after the seven instructions that form its address (the distance,
+// the far mask, the grid's shift and origin, the shift-add), and the
+// fraction and the larger log are formed in its shadow (scheduling barriers
+// keep that order: left alone the compiler forms the fraction first).
+__device__ __forceinline__ uint32_t x32_add_pos2(const pos_tab &P, uint32_t al, uint32_t tl) {
+    const uint32_t d = absdiff(al, tl, P.zero);   // one v_sad_u32; < 2^31: the far pairs reach every distance
+    const uint32_t far = sign_mask(k32_sb_end - 1u - d, P.one);   // d on the far grid
+    const uint32_t sh = bfi(far, (uint32_t)k32_sb_fsh, (uint32_t)k32_sb_sh);
+    const i32x2 tp = lds_ld2(lds_at3(d >> sh, bfi(far, P.far, P.near)));
+    __builtin_amdgcn_sched_barrier(0);
+    const uint32_t fr = __builtin_amdgcn_ubfe(d, 0, sh) << bfi(far, (uint32_t)kp32_far_frac, (uint32_t)kp32_near_frac);
+    const int32_t mx = (int32_t)max(al, tl);
+    asm volatile("" ::"v"(fr), "v"(mx));
+    __builtin_amdgcn_sched_barrier(0);
+    // the high word of the product of two 24-bit signed operands (one
+    // v_mul_hi_i32_i24): both fit, so the sign extensions are free
+    const int32_t q = (int32_t)(((int64_t)sext24((uint32_t)tp.y) * (int64_t)sext24(fr)) >> 32);
+    return (uint32_t)__builtin_elementwise_add_sat(mx, tp.x + q);
+}
+
 // A whole xlns32 addition on packed values (sign bit 31) over the LDS tables.
 __device__ __forceinline__ uint32_t x32_add_lds(const x32_tab &O, uint32_t x, uint32_t y) {
     acc_ls a{x & k32_logmask, x & k32_sign};
@@ -734,6 +784,15 @@ template <>
 __device__ __forceinline__ red16<LNSHIP_LPVIP> stage_tables<LNSHIP_LPVIP>(const dev_tables &, char *) {
     return red16<LNSHIP_LPVIP>{};
 }
+// the pair image of the positive-sum adder
+__device__ __forceinline__ pos_tab stage_pos32(const dev_tables &T, char *lds) {
+    stage_copy<32>(reinterpret_cast<int4 *>(lds), reinterpret_cast<const int4 *>(T.pos32), k_lds_pos32 / 16);
+    uint32_t tb = lds_addr(lds);
+    asm("" : "+v"(tb));
+    pos_tab P{tb, tb + (uint32_t)(kp32_near - (int)(k32_sb_end >> k32_sb_fsh)) * 8u, 1u, 0u};
+    asm("" : "+v"(P.near), "+v"(P.far), "+v"(P.one), "+v"(P.zero));
+    return P;
+}
 // the tables of a kernel whose xlns32 additions are single-chain steps
 // (x32_add_step) when DEC, else multi-chain ones (x32_add_ls)
 template <int MODE, bool DEC>
@@ -747,6 +806,22 @@ constexpr int lds_tables_bytes() {
     return MODE == LNSHIP_BASE ? 2 * k16_gauss_n * 2 :
            MODE == LNSHIP_MONTE ? 4 * k16_mc_n * 4 :
            MODE == LNSHIP_SUM32 ? k_lds_tab32 : 0;
+}
+// The LDS tables of the xlns16 row kernels (rms_norm, soft_max): their sum32
+// chains add only positive values (squares, exps), over the positive-sum
+// adder's pair image; the other modes stage their adder's tables.
+template <int MODE>
+constexpr int row_tables_bytes() {
+    return MODE == LNSHIP_SUM32 ? k_lds_pos32 : lds_tables_bytes<MODE>();
+}
+template <int MODE>
+__device__ __forceinline__ red16<MODE> stage_rows(const dev_tables &T, char *lds, pos_tab &P) {
+    if constexpr (MODE == LNSHIP_SUM32) {
+        P = stage_pos32(T, lds);
+        return red16<MODE>{};
+    } else {
+        return stage_tables<MODE>(T, lds);
+    }
 }
 
 // ---- MUL_MAT ------------------------------------------------------------------
@@ -1369,6 +1444,46 @@ __device__ __forceinline__ void chain32(const x32_tab &O, acc_ls &acc, const uin
     if (gl > g0) run(nxt, 0, n - 4 * gl);
 }
 
+// Sums of positive values over the pair image: l <- l (+) row[i] for
+// i = i0 .. n-1 in order, as chain32<true> / chain16<..., true> (xlns16 codes
+// widened; a sum32 accumulator) compute them.
+__device__ __forceinline__ void chain_pos32(const pos_tab &P, uint32_t &l, const uint32_t *row, int i0, int n) {
+    const int g0 = i0 >> 2, gl = (n - 1) >> 2;
+    auto ld = [&](int g) { return *reinterpret_cast<const uint4 *>(row + 4 * min(g, gl)); };
+    auto run = [&](const uint4 &q, int u0, int u1) {
+        const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+        for (int u = 0; u < 4; u++)
+            if (u >= u0 && u < u1) l = x32_add_pos2(P, l, w[u]);
+    };
+    uint4 cur = ld(g0), nxt = ld(g0 + 1);
+    run(cur, i0 - 4 * g0, min(n - 4 * g0, 4));
+    for (int g = g0 + 1; g < gl; g++) {
+        cur = nxt;
+        nxt = ld(g + 1);
+        run(cur, 0, 4);
+    }
+    if (gl > g0) run(nxt, 0, n - 4 * gl);
+}
+__device__ __forceinline__ void chain_pos16(const pos_tab &P, uint32_t &l, const uint16_t *row, int i0, int n) {
+    const int g0 = i0 >> 3, gl = (n - 1) >> 3;
+    auto ld = [&](int g) { return *reinterpret_cast<const uint4 *>(row + 8 * min(g, gl)); };
+    auto run = [&](const uint4 &q, int u0, int u1) {
+        const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+        for (int u = 0; u < 8; u++)
+            if (u >= u0 && u < u1) l = x32_add_pos2(P, l, half16(w[u >> 1], u & 1) << 16);
+    };
+    uint4 cur = ld(g0), nxt = ld(g0 + 1);
+    run(cur, i0 - 8 * g0, min(n - 8 * g0, 8));
+    for (int g = g0 + 1; g < gl; g++) {
+        cur = nxt;
+        nxt = ld(g + 1);
+        run(cur, 0, 8);
+    }
+    if (gl > g0) run(nxt, 0, n - 8 * gl);
+}
+
 // ---- RMS_NORM -------------------------------------------------------------------
 // A workgroup takes rb rows: all threads convert and square into LDS, one lane
 // per row runs the sequential sum, all threads scale.
@@ -1379,8 +1494,9 @@ __global__ __launch_bounds__(k_block) void k_rms16(const float *__restrict__ src
                                                    float eps, uint32_t seed, const uint16_t *state, uint64_t offset,
                                                    dev_tables T) {
     extern __shared__ __align__(16) char lds[];
-    const red16<MODE> R = stage_tables<MODE>(T, lds);
-    uint16_t *sq = reinterpret_cast<uint16_t *>(lds + ((lds_tables_bytes<MODE>() + 15) & ~15));
+    pos_tab P{};
+    const red16<MODE> R = stage_rows<MODE>(T, lds, P);
+    uint16_t *sq = reinterpret_cast<uint16_t *>(lds + ((row_tables_bytes<MODE>() + 15) & ~15));
     __shared__ uint32_t s_inv[64];
     const int64_t r0 = (int64_t)blockIdx.x * rb;
     const int nr = (int)min<int64_t>(rb, nrows - r0);
@@ -1410,7 +1526,9 @@ __global__ __launch_bounds__(k_block) void k_rms16(const float *__restrict__ src
         if (MODE == LNSHIP_MONTE)
             s = lfsr_jump(T, monte_start(T, seed, state, offset), (uint64_t)(r0 + r) * (uint64_t)ncols);
         typename red16<MODE>::acc_t acc = R.start(0u, s);
-        chain16<red16<MODE>, true>(R, acc, sq + r * rs, 0, nc, s);   // squares: positive
+        // squares: positive
+        if constexpr (MODE == LNSHIP_SUM32) chain_pos16(P, acc.l, sq + r * rs, 0, nc);
+        else chain16<red16<MODE>, true>(R, acc, sq + r * rs, 0, nc, s);
         const uint32_t sum = R.finish(acc) & 0xffffu;
         const uint32_t mean = x16_mul(sum, x16_from_f32(T.cvt16, 1.0f / (float)ncols));
         const uint32_t e16 = x16_from_f32(T.cvt16, eps);
@@ -1446,8 +1564,8 @@ __global__ __launch_bounds__(k_block) void k_rms32(const float *__restrict__ src
                                                    float *__restrict__ dst, int64_t ncols, int64_t nrows, int rb,
                                                    float eps, dev_tables T) {
     extern __shared__ __align__(16) char lds[];
-    const red16<LNSHIP_SUM32> R = stage_tables<LNSHIP_SUM32>(T, lds);
-    uint32_t *sq = reinterpret_cast<uint32_t *>(lds + k_lds_tab32);
+    const pos_tab P = stage_pos32(T, lds);   // every xlns32 addition here adds positive values
+    uint32_t *sq = reinterpret_cast<uint32_t *>(lds + k_lds_pos32);
     __shared__ uint32_t s_inv[64];
     const int64_t r0 = (int64_t)blockIdx.x * rb;
     const int nr = (int)min<int64_t>(rb, nrows - r0);
@@ -1469,11 +1587,13 @@ __global__ __launch_bounds__(k_block) void k_rms32(const float *__restrict__ src
     __syncthreads();
     if ((int)threadIdx.x < nr) {
         const int r = threadIdx.x;
-        acc_ls a{0u, 0u};
-        chain32<true>(R.O, a, sq + r * rs, 0, nc);   // squares: positive
-        const uint32_t acc = a.s | a.l;
+        uint32_t acc = 0u;
+        chain_pos32(P, acc, sq + r * rs, 0, nc);   // squares: positive
         const uint32_t mean = x32_mul(acc, x32_from_f32(1.0f / (float)ncols));
-        s_inv[r] = x32_recip(x32_sqrt(x32_add_lds(R.O, mean, x32_from_f32(eps))));
+        // mean >= 0: the epsilon add is a positive one unless eps < 0
+        const uint32_t e = x32_from_f32(eps);
+        const uint32_t me = (e & k32_sign) ? x32_add(T.tab32, mean, e) : x32_add_pos2(P, mean, e);
+        s_inv[r] = x32_recip(x32_sqrt(me));
     }
     __syncthreads();
     for (int e0 = threadIdx.x; e0 < nel; e0 += B * nt) {
@@ -1617,10 +1737,11 @@ __device__ __forceinline__ const float *mask_row(const sm_args &a, int64_t row) 
 template <int MODE>
 __global__ __launch_bounds__(k_block) void k_softmax16(sm_args a, dev_tables T) {
     extern __shared__ __align__(16) char lds[];
-    const red16<MODE> R = stage_tables<MODE>(T, lds);
+    pos_tab P{};
+    const red16<MODE> R = stage_rows<MODE>(T, lds, P);
     // the plain xlns16 adder (scale, mask bias, max subtraction) reads the
     // global copy of the Gaussian-log table
-    uint16_t *c = reinterpret_cast<uint16_t *>(lds + ((lds_tables_bytes<MODE>() + 15) & ~15));
+    uint16_t *c = reinterpret_cast<uint16_t *>(lds + ((row_tables_bytes<MODE>() + 15) & ~15));
     __shared__ int32_t s_max[64];
     __shared__ uint32_t s_tot[64];
     __shared__ const float *s_mrow[64];
@@ -1721,7 +1842,10 @@ __global__ __launch_bounds__(k_block) void k_softmax16(sm_args a, dev_tables T) 
         // draws after it are not taken; the next op's start does not depend
         // on them)
         const int n_eff = s_last[r] + 1;
-        if (n_eff > 1) chain16<red16<MODE>, true>(R, acc, row, 1, n_eff, s);   // exps: positive
+        if (n_eff > 1) {   // exps: positive
+            if constexpr (MODE == LNSHIP_SUM32) chain_pos16(P, acc.l, row, 1, n_eff);
+            else chain16<red16<MODE>, true>(R, acc, row, 1, n_eff, s);
+        }
         s_tot[r] = R.finish(acc) & 0xffffu;
     }
     __syncthreads();
@@ -2454,12 +2578,16 @@ __global__ void k_lpvip_db_range(uint32_t d0, uint32_t n, int32_t *__restrict__ 
 
 // The xlns32 adder over its LDS tables on code pairs, in the form the kernels
 // run it: FORM 0 the multi-chain step, 1 the single-chain step of the decode
-// GEMVs, 2 the positive-sum step (sign bits ignored).
+// GEMVs, 2 the positive-sum step (sign bits ignored), 3 the positive-sum step
+// over the pair image (sign bits ignored).
 template <int FORM>
 __global__ __launch_bounds__(k_block) void k_x32_add_lds(const uint32_t *__restrict__ x, const uint32_t *__restrict__ y,
                                                          uint32_t *__restrict__ out, int64_t n, dev_tables T) {
     extern __shared__ __align__(16) char lds[];
-    const red16<LNSHIP_SUM32> R = stage_for<LNSHIP_SUM32, FORM == 1>(T, lds);
+    red16<LNSHIP_SUM32> R{};
+    pos_tab P{};
+    if constexpr (FORM == 3) P = stage_pos32(T, lds);
+    else R = stage_for<LNSHIP_SUM32, FORM == 1>(T, lds);
     __syncthreads();
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)blockDim.x * gridDim.x) {
         const uint32_t a = x[i], b = y[i];
@@ -2471,8 +2599,10 @@ __global__ __launch_bounds__(k_block) void k_x32_add_lds(const uint32_t *__restr
             const uint32_t ts = b & k32_sign;
             x32_add_step(R.O, c, b & k32_logmask, ts, c.s ^ ts, [] { return 0u; }, [] {});
             r = c.s | c.l;
-        } else {
+        } else if constexpr (FORM == 2) {
             r = x32_add_pos(R.O, a & k32_logmask, b & k32_logmask);
+        } else {
+            r = x32_add_pos2(P, a & k32_logmask, b & k32_logmask);
         }
         out[i] = r;
     }
@@ -2488,17 +2618,24 @@ __global__ void k_causal_mask(const int32_t *__restrict__ pos, int64_t ntok, int
 
 // ---- host helpers -------------------------------------------------------------
 
-template <int MODE>
-static int64_t max_row(int elem_bytes) {
-    // rows are staged at a 16-byte stride
-    return ((k_lds_bytes - ((lds_tables_bytes<MODE>() + 15) & ~15) - k_lds_static) / 16) * (16 / elem_bytes);
+// rows beside tab_bytes of LDS tables, staged at a 16-byte stride
+static int64_t max_row(int tab_bytes, int elem_bytes) {
+    return ((k_lds_bytes - ((tab_bytes + 15) & ~15) - k_lds_static) / 16) * (16 / elem_bytes);
 }
 
-template <int MODE>
-static int rows_per_block(int64_t ncols, int elem_bytes) {
-    const int64_t avail = k_lds_bytes - ((lds_tables_bytes<MODE>() + 15) & ~15) - k_lds_static;
-    int64_t rb = avail / std::max<int64_t>(1, ncols * elem_bytes);
-    return (int)std::min<int64_t>(64, rb);
+// Rows per workgroup of a row kernel: one chain lane per row, so a block
+// takes as long as one chain plus its element passes over all its rows.
+// The most rows LDS holds decide how many rounds of blocks the GPU needs;
+// within that many rounds the rows are spread over every block slot, so that
+// no block carries more rows (longer element passes) than it must.
+static int rows_per_block(int tab_bytes, int64_t ncols, int elem_bytes, int64_t nrows, int cus) {
+    const int64_t tabs = (tab_bytes + 15) & ~15;
+    const int64_t row = std::max<int64_t>(1, ncols * elem_bytes);
+    const int64_t rb_max = std::min<int64_t>(64, (k_lds_bytes - tabs - k_lds_static) / row);
+    if (rb_max < 1 || nrows < 1) return (int)rb_max;
+    const int64_t slots = (int64_t)std::max(cus, 1) * std::max<int64_t>(1, k_lds_bytes / (tabs + rb_max * row));
+    const int64_t rounds = (nrows + rb_max * slots - 1) / (rb_max * slots);
+    return (int)std::min<int64_t>(rb_max, (nrows + rounds * slots - 1) / (rounds * slots));
 }
 
 template <class K>
@@ -2689,11 +2826,12 @@ static int launch_mm32(const mm_args32 &m, const dev_tables &T, int64_t nslices,
 
 template <int MODE>
 static int launch_rms16(const float *src, const float *w, float *dst, int64_t ncols, int64_t nrows, float eps,
-                        uint16_t seed, const uint16_t *state, uint64_t offset, const dev_tables &T, hipStream_t st) {
+                        uint16_t seed, const uint16_t *state, uint64_t offset, const dev_tables &T, int cus,
+                        hipStream_t st) {
     const int64_t rs = (ncols + 7) & ~(int64_t)7;
-    const int rb = rows_per_block<MODE>(rs, 2);
+    const int rb = rows_per_block(row_tables_bytes<MODE>(), rs, 2, nrows, cus);
     if (rb < 1) return fail(LNSHIP_ERANGE, "rms_norm: row too long for LDS%s");
-    const int lds = ((lds_tables_bytes<MODE>() + 15) & ~15) + (int)(rb * rs * 2);
+    const int lds = ((row_tables_bytes<MODE>() + 15) & ~15) + (int)(rb * rs * 2);
     if (int rc = set_lds(k_rms16<MODE>, lds)) return rc;
     hipLaunchKernelGGL(k_rms16<MODE>, dim3((unsigned)((nrows + rb - 1) / rb)), dim3(k_block), lds, st, src, w, dst,
                        ncols, nrows, rb, eps, (uint32_t)seed, state, offset, T);
@@ -2743,11 +2881,11 @@ static int64_t attn16_lds_mode(int mode, int64_t hd, int64_t n_kv) {
 }
 
 template <int MODE>
-static int launch_sm16(sm_args &m, int64_t nrows, const dev_tables &T, hipStream_t st) {
+static int launch_sm16(sm_args &m, int64_t nrows, const dev_tables &T, int cus, hipStream_t st) {
     const int64_t rs = (m.n + 7) & ~(int64_t)7;
-    m.rb = rows_per_block<MODE>(rs, 2);
+    m.rb = rows_per_block(row_tables_bytes<MODE>(), rs, 2, nrows, cus);
     if (m.rb < 1) return fail(LNSHIP_ERANGE, "soft_max: row too long for LDS%s");
-    const int lds = ((lds_tables_bytes<MODE>() + 15) & ~15) + (int)(m.rb * rs * 2);
+    const int lds = ((row_tables_bytes<MODE>() + 15) & ~15) + (int)(m.rb * rs * 2);
     if (int rc = set_lds(k_softmax16<MODE>, lds)) return rc;
     hipLaunchKernelGGL(k_softmax16<MODE>, dim3((unsigned)((nrows + m.rb - 1) / m.rb)), dim3(k_block), lds, st, m, T);
     LNSHIP_HIP(hipGetLastError());
@@ -2880,6 +3018,9 @@ const char *lnship_last_error(void) { return t_err.c_str(); }
 
 const char *lnship_version(void) { return "lnship 0.1: xlns16 (table, alt) + xlns32 (alt) for gfx950"; }
 
+static bool pos32_image(const int32_t *tab, std::vector<int32_t> &img);
+static std::vector<int32_t> g_pos32_host;   // the positive-sum adder's pair image, for tests
+
 const void *lnship_host_table(const char *name, size_t *bytes) {
     {
         std::lock_guard<std::mutex> lock(g_mutex);
@@ -2887,6 +3028,15 @@ const void *lnship_host_table(const char *name, size_t *bytes) {
             g_host = new host_tables;
             build_host_tables(*g_host);
         }
+        if (g_pos32_host.empty() && std::strcmp(name, "pos32") == 0 && !pos32_image(g_host->tab32, g_pos32_host)) {
+            g_pos32_host.clear();
+            fail(LNSHIP_EINVAL, "sb slopes outside the positive-sum adder's 24-bit range%s");
+            return nullptr;
+        }
+    }
+    if (std::strcmp(name, "pos32") == 0) {
+        if (bytes) *bytes = g_pos32_host.size() * sizeof(int32_t);
+        return g_pos32_host.data();
     }
     struct { const char *n; const void *p; size_t b; } t[] = {
         {"cvt16", g_host->cvt16, sizeof g_host->cvt16},
@@ -2962,6 +3112,26 @@ static bool lds32_image(const int32_t *tab, std::vector<int32_t> &img, bool dec)
            nth_max < nlo_min && nth_max < (int64_t)k32_co_l0;
 }
 
+// The positive-sum adder's pair image (k_lds_pos32): for each sb grid
+// interval its first node and its slope scaled for v_mul_hi_i32_i24.
+// Returns false when a scaled slope leaves the 24-bit signed range or the
+// far grid does not end in zeros at the essential zero.
+static bool pos32_image(const int32_t *tab, std::vector<int32_t> &img) {
+    img.assign(2 * kp32_pairs, 0);
+    bool ok = true;
+    auto put = [&](int p, int32_t t0, int32_t t1, int sc) {
+        const int64_t a = (int64_t)(t1 - t0) * ((int64_t)1 << sc);
+        ok = ok && a >= -(1 << 23) && a < (1 << 23);
+        img[2 * p] = t0;
+        img[2 * p + 1] = (int32_t)a;
+    };
+    for (int i = 0; i < kp32_near; i++) put(i, tab[k32_off_sb + i], tab[k32_off_sb + i + 1], kp32_near_slope);
+    for (int j = 0; j < kp32_far; j++)
+        put(kp32_near + j, j < k32_sb_fn ? tab[k32_off_sbf + j] : 0, j + 1 < k32_sb_fn ? tab[k32_off_sbf + j + 1] : 0,
+            kp32_far_slope);
+    return ok && tab[k32_off_sbf + k32_sb_fn - 1] == 0;
+}
+
 int lnship_init(void) {
     int dev = 0;
     if (int rc = current_device(&dev)) return rc;
@@ -2996,6 +3166,9 @@ int lnship_init(void) {
         if (!lds32_image(g_host->tab32, img, true))
             return fail(LNSHIP_EINVAL, "init: xlns32 tables outside the bounds of their LDS layout%s");
         if (int rc = upload(img.data(), img.size(), &T.lds32d)) return rc;
+        if (!pos32_image(g_host->tab32, img))
+            return fail(LNSHIP_EINVAL, "init: sb slopes outside the positive-sum adder's 24-bit range%s");
+        if (int rc = upload(img.data(), img.size(), &T.pos32)) return rc;
     }
     if (int rc = upload(g_host->lfsr_seq, 65536, &T.lfsr_seq)) return rc;
     if (int rc = upload(g_host->lfsr_log, 65536, &T.lfsr_log)) return rc;
@@ -3345,14 +3518,14 @@ static int rms16_common(int mode, const float *src, const float *w, float *dst, 
     if ((nrows + 63) / 64 > 2147483647) return fail(LNSHIP_ERANGE, "rms_norm: too many rows%s");
     hipStream_t st = (hipStream_t)stream;
     switch (mode) {
-        case LNSHIP_BASE: return launch_rms16<LNSHIP_BASE>(src, w, dst, ncols, nrows, eps, monte_seed, monte_state, monte_offset, s->T,
-                                                                 st);
-        case LNSHIP_MONTE: return launch_rms16<LNSHIP_MONTE>(src, w, dst, ncols, nrows, eps, monte_seed, monte_state, monte_offset, s->T,
-                                                                 st);
-        case LNSHIP_LPVIP: return launch_rms16<LNSHIP_LPVIP>(src, w, dst, ncols, nrows, eps, monte_seed, monte_state, monte_offset, s->T,
-                                                                 st);
-        default: return launch_rms16<LNSHIP_SUM32>(src, w, dst, ncols, nrows, eps, monte_seed, monte_state, monte_offset, s->T,
-                                                                 st);
+        case LNSHIP_BASE: return launch_rms16<LNSHIP_BASE>(src, w, dst, ncols, nrows, eps, monte_seed, monte_state,
+                                                           monte_offset, s->T, s->cus, st);
+        case LNSHIP_MONTE: return launch_rms16<LNSHIP_MONTE>(src, w, dst, ncols, nrows, eps, monte_seed, monte_state,
+                                                             monte_offset, s->T, s->cus, st);
+        case LNSHIP_LPVIP: return launch_rms16<LNSHIP_LPVIP>(src, w, dst, ncols, nrows, eps, monte_seed, monte_state,
+                                                             monte_offset, s->T, s->cus, st);
+        default: return launch_rms16<LNSHIP_SUM32>(src, w, dst, ncols, nrows, eps, monte_seed, monte_state,
+                                                   monte_offset, s->T, s->cus, st);
     }
 }
 
@@ -3420,9 +3593,9 @@ static int rms32_common(const float *src, const float *w, float *dst, int64_t nc
     if (ncols < 0 || nrows < 0) return fail(LNSHIP_EINVAL, "rms_norm: bad argument%s");
     if (ncols == 0 || nrows == 0) return 0;
     const int64_t rs = (ncols + 3) & ~(int64_t)3;
-    const int rb = rows_per_block<LNSHIP_SUM32>(rs, 4);
+    const int rb = rows_per_block(k_lds_pos32, rs, 4, nrows, s->cus);
     if (rb < 1) return fail(LNSHIP_ERANGE, "rms_norm: row too long for LDS%s");
-    const int lds = k_lds_tab32 + (int)(rb * rs * 4);
+    const int lds = k_lds_pos32 + (int)(rb * rs * 4);
     if (int rc = set_lds(k_rms32, lds)) return rc;
     hipLaunchKernelGGL(k_rms32, dim3((unsigned)((nrows + rb - 1) / rb)), dim3(k_block), lds, (hipStream_t)stream, src,
                        w, dst, ncols, nrows, rb, eps, s->T);
@@ -3454,10 +3627,10 @@ int lnship16_soft_max(int mode, const lnship_soft_max_args *a, void *stream) {
               a->monte_state, a->monte_offset};
     hipStream_t st = (hipStream_t)stream;
     switch (mode) {
-        case LNSHIP_BASE: return launch_sm16<LNSHIP_BASE>(m, nrows, s->T, st);
-        case LNSHIP_MONTE: return launch_sm16<LNSHIP_MONTE>(m, nrows, s->T, st);
-        case LNSHIP_LPVIP: return launch_sm16<LNSHIP_LPVIP>(m, nrows, s->T, st);
-        default: return launch_sm16<LNSHIP_SUM32>(m, nrows, s->T, st);
+        case LNSHIP_BASE: return launch_sm16<LNSHIP_BASE>(m, nrows, s->T, s->cus, st);
+        case LNSHIP_MONTE: return launch_sm16<LNSHIP_MONTE>(m, nrows, s->T, s->cus, st);
+        case LNSHIP_LPVIP: return launch_sm16<LNSHIP_LPVIP>(m, nrows, s->T, s->cus, st);
+        default: return launch_sm16<LNSHIP_SUM32>(m, nrows, s->T, s->cus, st);
     }
 }
 
@@ -3497,7 +3670,7 @@ int lnship32_soft_max(const lnship_soft_max_args *a, void *stream) {
     sm_args m{a->src, a->mask, a->dst, a->src_ne[0], a->src_ne[1], a->src_ne[2], a->src_ne[3],
               a->mask_ne[0], a->mask_ne[1], a->mask_ne[2], a->mask_ne[3], a->scale, 0, 0};
     const int64_t rs = (m.n + 3) & ~(int64_t)3;
-    m.rb = rows_per_block<LNSHIP_SUM32>(rs, 4);
+    m.rb = rows_per_block(k_lds_tab32, rs, 4, nrows, s->cus);
     if (m.rb < 1) return fail(LNSHIP_ERANGE, "soft_max: row too long for LDS%s");
     const int lds = k_lds_tab32 + (int)(m.rb * rs * 4);
     if (int rc = set_lds(k_softmax32, lds)) return rc;
@@ -3508,7 +3681,8 @@ int lnship32_soft_max(const lnship_soft_max_args *a, void *stream) {
 }
 
 int64_t lnship_max_row(int which, int mode) {
-    if (which == 2 || which == 3) return max_row<LNSHIP_SUM32>(4);
+    if (which == 2) return max_row(k_lds_pos32, 4);
+    if (which == 3) return max_row(k_lds_tab32, 4);
     if (which == 5) {
         // lnship16_rms_norm_mul_mat: the tables, the x row and h (4 B per k)
         if (mode != LNSHIP_SUM32) return 0;
@@ -3529,10 +3703,10 @@ int64_t lnship_max_row(int which, int mode) {
     }
     if (which != 0 && which != 1) return 0;
     switch (mode) {
-        case LNSHIP_BASE: return max_row<LNSHIP_BASE>(2);
-        case LNSHIP_MONTE: return max_row<LNSHIP_MONTE>(2);
-        case LNSHIP_LPVIP: return max_row<LNSHIP_LPVIP>(2);
-        case LNSHIP_SUM32: return max_row<LNSHIP_SUM32>(2);
+        case LNSHIP_BASE: return max_row(row_tables_bytes<LNSHIP_BASE>(), 2);
+        case LNSHIP_MONTE: return max_row(row_tables_bytes<LNSHIP_MONTE>(), 2);
+        case LNSHIP_LPVIP: return max_row(row_tables_bytes<LNSHIP_LPVIP>(), 2);
+        case LNSHIP_SUM32: return max_row(row_tables_bytes<LNSHIP_SUM32>(), 2);
         default: return 0;
     }
 }
@@ -3744,7 +3918,7 @@ int lnship_lpvip_db_range(uint32_t d0, uint32_t n, int32_t *out, void *stream) {
 int lnship32_add_lds(int form, const uint32_t *x, const uint32_t *y, uint32_t *out, int64_t n, void *stream) {
     device_state *s = state();
     if (!s) return LNSHIP_ENOINIT;
-    if (form < 0 || form > 2 || n < 0) return fail(LNSHIP_EINVAL, "add_lds: bad argument%s");
+    if (form < 0 || form > 3 || n < 0) return fail(LNSHIP_EINVAL, "add_lds: bad argument%s");
     if (n == 0) return 0;
     if (!x || !y || !out) return fail(LNSHIP_EINVAL, "add_lds: null pointer%s");
     // one staging of the tables per workgroup: a grid of one workgroup per CU
@@ -3759,9 +3933,13 @@ int lnship32_add_lds(int form, const uint32_t *x, const uint32_t *y, uint32_t *o
             if (int rc = set_lds(k_x32_add_lds<1>, k_lds_tab32)) return rc;
             hipLaunchKernelGGL(k_x32_add_lds<1>, g, dim3(k_block), k_lds_tab32, st, x, y, out, n, s->T);
             break;
-        default:
+        case 2:
             if (int rc = set_lds(k_x32_add_lds<2>, k_lds_tab32)) return rc;
             hipLaunchKernelGGL(k_x32_add_lds<2>, g, dim3(k_block), k_lds_tab32, st, x, y, out, n, s->T);
+            break;
+        default:
+            if (int rc = set_lds(k_x32_add_lds<3>, k_lds_pos32)) return rc;
+            hipLaunchKernelGGL(k_x32_add_lds<3>, g, dim3(k_block), k_lds_pos32, st, x, y, out, n, s->T);
     }
     LNSHIP_HIP(hipGetLastError());
     return 0;
