@@ -40,6 +40,8 @@ def parse():
     ap.add_argument("--no-prefill-gemm", action="store_true",
                     help="leave BASELINE config 5's GEMM (GMAC/s, sum32 and base) out of the default line")
     ap.add_argument("--no-graph", action="store_true", help="decode eagerly instead of replaying a HIP graph")
+    ap.add_argument("--split-attn", action="store_true",
+                    help="run a decode step's kq, soft_max and kqv as three launches (not one fused attention)")
     ap.add_argument("--split-rms", action="store_true",
                     help="decode: rms_norm + MUL (sum32) and swiglu as launches of their own, apart from the "
                          "mul_mat after them")
@@ -588,6 +590,7 @@ def main():
     model = llama.LlamaLNS16(cfg, weights, mode=mode)
     model.fused_rms = model.fused_rms and not args.split_rms
     model.fused_glu = model.fused_glu and not args.split_rms
+    model.fused_attn = model.fused_attn and not args.split_attn
     torch.cuda.synchronize()
     t_setup = time.perf_counter() - t0
 
@@ -801,6 +804,7 @@ def run_lns32(args):
     t0 = time.perf_counter()
     weights = lns32_weights(cfg, 4321, 0.02, torch)
     model = llama.LlamaLNS32(cfg, weights)
+    model.fused_attn = model.fused_attn and not args.split_attn
     torch.cuda.synchronize()
     t_setup = time.perf_counter() - t0
     rng = np.random.default_rng(2024)

@@ -275,7 +275,7 @@ int lnship32_rope_store_kv(const lnship_qkv_store_args *args, void *stream);
  * LDS returns LNSHIP_ERANGE (checked before any device call). */
 typedef struct lnship_attn_args {
     const float *q;
-    const uint16_t *k_cache, *v_cache;
+    const void *k_cache, *v_cache;   /* uint16_t (xlns16) or uint32_t (xlns32) codes */
     int64_t cache_m, k_slice, v_slice;
     const float *mask;
     float scale;
@@ -283,6 +283,14 @@ typedef struct lnship_attn_args {
     int64_t n_head, n_head_kv, head_dim, n_kv;
 } lnship_attn_args;
 int lnship16_attn_decode(int mode, const lnship_attn_args *args, void *stream);
+/* The same for the LNS32 backend (xlns32 codes in the caches, in the layout
+ * lnship32_rope_store_kv writes): lns32_mul_mat for kq, lns32_soft_max, then
+ * lns32_mul_mat for kqv (src32/lns32-ops.cpp:98-144, :384-436), F32 between
+ * them as between the nodes, so dst equals the three nodes' bit for bit.
+ * No single counterpart in the reference.  n_kv <= lnship_max_row(7, 0) for
+ * head_dim <= 256; a launch that does not fit LDS returns LNSHIP_ERANGE
+ * (checked before any device call). */
+int lnship32_attn_decode(const lnship_attn_args *args, void *stream);
 
 /* ggml views on the device (tensors in the ggml device buffer type): the
  * elements of a 4-D strided view (byte strides nb, as ggml_tensor::nb)
@@ -371,7 +379,8 @@ int lnship_causal_mask(const int32_t *pos, int64_t ntok, int64_t n_kv, float *ma
  * rms_norm, 1 xlns16 soft_max, 2 xlns32 rms_norm, 3 xlns32 soft_max, 4 the
  * cells (n_kv) of lnship16_attn_decode with head_dim up to 256 (0 for Monte),
  * 5 the K of lnship16_rms_norm_mul_mat (sum32; 0 for other modes), 6 the K
- * of lnship16_swiglu_mul_mat (0 for Monte);
+ * of lnship16_swiglu_mul_mat (0 for Monte), 7 the cells of
+ * lnship32_attn_decode with head_dim up to 256;
  * mode is the xlns16 summation mode (ignored for xlns32).  No GPU needed.  Plays the
  * role of the reference's grid / shape predicates (cuda/lns-cuda-ops.cpp:
  * 45-54, 184-189): a ggml backend declines longer rows in supports_op. */

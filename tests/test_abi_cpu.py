@@ -184,6 +184,18 @@ def test_attn_decode_refuses_wide_heads_before_any_device_call(lnship):
     # a head_dim within the limit passes the checks and then needs a device
     a.head_dim = 64
     assert L.lnship16_attn_decode(lnship.SUM32, ctypes.byref(a), None) == ENOINIT
+    # the LNS32 one: its own cell limit (xlns32 codes), the same refusals
+    n32 = L.lnship_max_row(7, 0)
+    assert 2048 <= n32 < n_kv
+    a.n_kv = a.cache_m = n32
+    assert L.lnship32_attn_decode(ctypes.byref(a), None) == ENOINIT
+    a.head_dim = 256   # the limit's head_dim
+    assert L.lnship32_attn_decode(ctypes.byref(a), None) == ENOINIT
+    a.n_kv = a.cache_m = n32 + 8
+    assert L.lnship32_attn_decode(ctypes.byref(a), None) == ERANGE
+    a.n_kv = a.cache_m = n32
+    a.head_dim = 1024
+    assert L.lnship32_attn_decode(ctypes.byref(a), None) == ERANGE
 
 
 def test_q4_k_host_to_float():

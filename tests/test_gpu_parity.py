@@ -755,6 +755,50 @@ def test_attn_decode_equals_three_nodes(ln, mode, n_kv, big_tail, skew):
         assert ln.lib().lnship_max_row(4, O.MONTE) == 0 and ln.lib().lnship_max_row(4, m) >= 4096
 
 
+@pytest.mark.parametrize("n_kv,masked,big_tail,hd", [
+    (1, False, False, 64), (13, True, False, 64), (256, True, False, 64), (256, True, True, 64),
+    (520, True, False, 64), (768, True, False, 64), (1024, False, False, 64), (1024, True, False, 64),
+    (200, True, False, 128)])
+def test_attn32_decode_equals_three_nodes(ln, n_kv, masked, big_tail, hd):
+    # lnship32_attn_decode (LNS32) against kq, soft_max and kqv run as three
+    # ops, the library's launches and the oracle's, on the Llama-1B head
+    # geometry (32 query heads over 8 kv heads), random xlns32 caches and a
+    # causal mask that hides the last cells; big_tail puts values of 1e35 in
+    # the masked cells of V (their products still run through the chain)
+    import ctypes
+    nh, nkv, n_ctx = 32, 8, max(256, (n_kv + 255) // 256 * 256)
+    rng = np.random.default_rng(n_kv + hd)
+    print(f"\n[attn32 decode] n_kv={n_kv} masked={masked} big_tail={big_tail} hd={hd}", flush=True)
+    pos = max(0, n_kv - 1 - n_kv // 5) if masked else n_kv - 1
+    kf = (rng.standard_normal((nkv, n_ctx, hd)) * 0.5).astype(np.float32)
+    vf = (rng.standard_normal((nkv, hd, n_ctx)) * 0.5).astype(np.float32)
+    if big_tail:
+        vf[:, :, pos + 1:n_kv] *= np.float32(1e35)
+    kc, vc = ln.pack32(dev(kf)), ln.pack32(dev(vf))
+    kslice, vslice = ln.kp(hd) * n_ctx, ln.kp(n_ctx) * hd
+    qf = (rng.standard_normal(nh * hd) * 2).astype(np.float32)
+    maskf = np.where(np.arange(n_kv) <= pos, 0.0, -np.inf).astype(np.float32)
+    q, mask = dev(qf), dev(maskf)
+    scale = 0.125
+    P = lambda t: t.data_ptr()
+    kq = torch.empty(nh * n_kv, device="cuda")
+    ln.mul_mat32_raw(P(kc), P(q), P(kq), hd, n_kv, 1, ne02=nkv, ne12=nh, x_ld=nh * hd, x_slice=hd,
+                     w_mstride=n_ctx, w_slice=kslice)
+    p = ln.soft_max32(kq.view(1, nh, 1, n_kv), mask.view(1, 1, 1, n_kv), scale)
+    want = torch.empty(nh * hd, device="cuda")
+    ln.mul_mat32_raw(P(vc), P(p), P(want), n_kv, hd, 1, ne02=nkv, ne12=nh, x_ld=n_kv, x_slice=n_kv,
+                     w_slice=vslice, dst_ld=nh * hd, dst_slice=hd)
+    got = torch.full((nh * hd,), float("nan"), device="cuda")
+    a = ln.AttnArgs(P(q), P(kc), P(vc), n_ctx, kslice, vslice, P(mask), scale, P(got), nh, nkv, hd, n_kv)
+    ln.check(ln.lib().lnship32_attn_decode(ctypes.byref(a), ln._stream()))
+    same_bits(host(got), host(want), f"attn32 decode n_kv={n_kv}")
+    kq_o = O.mul_mat32(kf[None, :, :n_kv], qf.reshape(1, nh, 1, hd), ne02=nkv)[0]
+    p_o = O.soft_max32(kq_o, maskf[None], scale)
+    want_o = O.mul_mat32(vf[None, :, :, :n_kv], p_o[None], ne02=nkv)[0]
+    same_bits(host(got), want_o.reshape(-1), f"attn32 decode n_kv={n_kv} vs oracle")
+    assert ln.lib().lnship_max_row(7, 0) >= 2048
+
+
 def test_lpvip_db_every_distance_below_one_binade(ln):
     # lpvip's exact branch (d below one binade, opposite signs) against the
     # host's libm for every d, and the Mitchell branch just above it (d = 0

@@ -10,7 +10,9 @@ point reads and writes, as include/lnship.h states them for those arguments
 Llama-1B shape (head geometry, widths and n_ctx 1024 of BASELINE config 4,
 two of its sixteen identical layers): a 512-token prompt, and decode steps
 through decode_graph at n_past 1022 and 1023, where the KV view is the whole
-cache (n_kv = n_ctx = 1024) and the last position is n_ctx - 1.
+cache (n_kv = n_ctx = 1024) and the last position is n_ctx - 1, with a
+decode step's kq, soft_max and kqv as three launches and as one
+lnship32_attn_decode launch.
 
 The footprints are the kernels' own extents: k_mm32 / k_mm16 lanes of rows
 m >= M return before any load, and weight / activation prefetches past the
@@ -108,6 +110,17 @@ def footprints(name, a):
                  "k cache"),
                 # value (h, p, d) at h * v_slice + ((p / 8) * head_dim + d) * 8 + p % 8
                 (q.v_cache, ((nkv - 1) * q.v_slice + ((p_max // 8) * hd + hd - 1) * 8 + 8) * 4, "v cache")]
+    elif name == "lnship32_attn_decode":
+        q = a[0]
+        hd, nh, nkv, n = q.head_dim, q.n_head, q.n_head_kv, q.n_kv
+        out += [(q.q, nh * hd * F32, "attn q"), (q.dst, nh * hd * F32, "attn dst"),
+                # key cell j < n_kv, dim d: k_slice per kv head, groups of eight dims cache_m * 8 codes apart
+                (q.k_cache, ((nkv - 1) * q.k_slice + ((lnship.kp(hd) // 8 - 1) * q.cache_m + n - 1) * 8 + 8) * 4,
+                 "attn k cache"),
+                # value dim d, cell j: groups of eight cells head_dim * 8 codes apart
+                (q.v_cache, ((nkv - 1) * q.v_slice + lnship.kp(n) * hd) * 4, "attn v cache")]
+        if q.mask:
+            out.append((q.mask, n * F32, "attn mask"))
     elif name == "lnship32_soft_max":
         s = a[0]
         ne, mne = list(s.src_ne), list(s.mask_ne)
@@ -198,12 +211,24 @@ def test_lns32_decode_at_full_context_stays_inside_its_allocations(recorded):
     model.decode_graph(tok)
     model.decode_graph(tok)
     assert model.n_past == cfg.n_ctx
-    # the steps' KV views covered the whole cache
+    # the steps' KV views covered the whole cache (kq, soft_max and kqv as
+    # three ops at this n_kv)
     kq = [a[0] for n, a in recorded.calls if n == "lnship32_mul_mat" and a[0].w_mstride == cfg.n_ctx]
     assert kq and max(m.M for m in kq) == cfg.n_ctx
     kqv = [a[0] for n, a in recorded.calls if n == "lnship32_mul_mat" and a[0].w_slice == model.vslice]
     assert kqv and max(m.K for m in kqv) == cfg.n_ctx
     n = audit(recorded.calls, allocations(model))
+    # the same steps with the attention as one launch over the whole cache
+    # (the second step replays the graph the first one captured)
+    recorded.calls.clear()
+    model._graphs.clear()
+    model._attn_max_kv = cfg.n_ctx
+    model.n_past = cfg.n_ctx - 2
+    model.decode_graph(tok)
+    model.decode_graph(tok)
+    att = [a[0] for n, a in recorded.calls if n == "lnship32_attn_decode"]
+    assert len(att) == cfg.n_layer and max(q.n_kv for q in att) == cfg.n_ctx
+    n += audit(recorded.calls, allocations(model))
     assert n_init > 0 and n_prompt > 0 and n > 30 * cfg.n_layer
     # and a step past the cache is refused on the host before any launch
     recorded.calls.clear()
@@ -217,15 +242,17 @@ def test_audit_catches_a_view_past_the_cache(recorded):
     # is reported
     cfg, model = _model(recorded)
     recorded.calls.clear()
+    model._attn_max_kv = cfg.n_ctx
     model.n_past = cfg.n_ctx - 1
     model.forward(1, torch.zeros(1, dtype=torch.int32), torch.full((1,), cfg.n_ctx - 1, dtype=torch.int32),
                   cfg.n_ctx)
     calls = []
     for name, args in recorded.calls:
-        if name == "lnship32_mul_mat" and args[0].w_slice == model.vslice:
+        if name == "lnship32_attn_decode":
             m = type(args[0]).from_buffer_copy(args[0])
-            m.K = cfg.n_ctx + 8
+            m.n_kv = cfg.n_ctx + 8
             args = [m]
         calls.append((name, args))
+    assert any(n == "lnship32_attn_decode" for n, _ in calls)
     with pytest.raises(AssertionError, match="outside every allocation"):
         audit(calls, allocations(model))

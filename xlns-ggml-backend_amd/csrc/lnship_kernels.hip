@@ -2168,6 +2168,175 @@ __global__ __launch_bounds__(k_block) void k_attn16(attn_args a, dev_tables T) {
     for (int d = threadIdx.x; d < hd; d += blockDim.x) a.dst[(int64_t)h * hd + d] = T.rev16[out_chain(d)];
 }
 
+// ---- LNS32 decode attention: KQ, soft_max and KQV of one token in one launch --
+// row_chain_x32 over xlns32 codes (the LNS32 GEMV's terms: 4-byte weights and
+// activations, a group of eight 32 bytes; x32_mul products, as k_mm32's
+// single-chain loop forms them, each in the first round trip of the step
+// before it)
+__device__ __forceinline__ void row_chain32(const x32_tab &O, acc_ls &acc, const uint32_t *__restrict__ w,
+                                            int64_t gs, const uint32_t *x, int k0, int k1) {
+    if (k1 <= k0) return;
+    constexpr int PF = 2;
+    const int gl = (k1 - 1) >> 3;
+    auto term_at = [&](int k) { return x32_mul(w[(int64_t)(k >> 3) * gs + (k & 7)], x[k]); };
+    // term 0 starts the sum; the steps add terms ks .. k1 - 1
+    const int ks = k0 == 0 ? 1 : k0;
+    if (k0 == 0) {
+        const uint32_t t0 = term_at(0);
+        acc = {t0 & k32_logmask, t0 & k32_sign};
+        if (k1 == 1) return;
+    }
+    uint32_t t = term_at(ks);
+    uint32_t uf = acc.s ^ (t & k32_sign);
+    struct g8 {
+        uint4 lo, hi;
+    };
+    auto group = [&](const g8 &wq, const g8 &xq, const g8 &wn, const g8 &xn, int g) {
+        const uint32_t ww[8] = {wq.lo.x, wq.lo.y, wq.lo.z, wq.lo.w, wq.hi.x, wq.hi.y, wq.hi.z, wq.hi.w};
+        const uint32_t xx[8] = {xq.lo.x, xq.lo.y, xq.lo.z, xq.lo.w, xq.hi.x, xq.hi.y, xq.hi.z, xq.hi.w};
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const int k = 8 * g + u;
+            if (k < ks || k >= k1) continue;
+            uint32_t tn = 0;
+            auto next = [&] {
+                tn = u < 7 ? x32_mul(ww[u + 1], xx[u + 1]) : x32_mul(wn.lo.x, xn.lo.x);
+                return tn & k32_sign;
+            };
+            uf = x32_add_step(O, acc, t & k32_logmask, t & k32_sign, uf, next, [] {});
+            t = tn;
+        }
+    };
+    // blocks of PF groups, double-buffered; loads past the last group reload it
+    g8 wa[PF], xa[PF], wb[PF], xb[PF];
+    auto load = [&](g8 (&w4)[PF], g8 (&x4)[PF], int g0) {
+#pragma unroll
+        for (int p = 0; p < PF; p++) {
+            const int g = min(g0 + p, gl);
+            const uint4 *wp = reinterpret_cast<const uint4 *>(w + (int64_t)g * gs);
+            const uint4 *xp = reinterpret_cast<const uint4 *>(x + 8 * g);
+            w4[p] = {wp[0], wp[1]};
+            x4[p] = {xp[0], xp[1]};
+        }
+    };
+    auto run = [&](const g8 (&w4)[PF], const g8 (&x4)[PF], const g8 (&wo)[PF], const g8 (&xo)[PF], int g0) {
+#pragma unroll
+        for (int p = 0; p < PF; p++) {
+            if (g0 + p > gl) break;
+            group(w4[p], x4[p], p + 1 < PF ? w4[p + 1] : wo[0], p + 1 < PF ? x4[p + 1] : xo[0], g0 + p);
+        }
+    };
+    const int g1 = ks >> 3;
+    load(wa, xa, g1);
+    load(wb, xb, g1 + PF);
+    for (int g0 = g1; g0 <= gl; g0 += 2 * PF) {
+        run(wa, xa, wb, xb, g0);
+        if (g0 + PF > gl) break;
+        load(wa, xa, g0 + 2 * PF);
+        run(wb, xb, wa, xa, g0 + PF);
+        load(wb, xb, g0 + 3 * PF);
+    }
+}
+
+// one xlns32 addition as the single-chain step makes it (the tables of
+// stage_for<SUM32, true>), for the element passes of a kernel that stages
+// that image
+__device__ __forceinline__ uint32_t x32_add_dec(const x32_tab &O, uint32_t x, uint32_t y) {
+    acc_ls c{x & k32_logmask, x & k32_sign};
+    const uint32_t ys = y & k32_sign;
+    x32_add_step(O, c, y & k32_logmask, ys, c.s ^ ys, [] { return 0u; }, [] {});
+    return c.s | c.l;
+}
+
+struct attn32_args {
+    const float *q;
+    const uint32_t *k, *v;
+    int64_t k_gs, k_slice, v_gs, v_slice;   // codes between groups of eight; between kv heads
+    const float *mask;
+    float scale;
+    float *dst;
+    int hd, n_kv, rep;   // head_dim, cells, query heads per kv head
+};
+
+// The LNS32 backend's decode attention as k_attn16 runs the LNS16 one: one
+// workgroup per query head h (kv head h / rep), the kq scores (one chain of
+// head_dim steps per cell), k_softmax32's passes and sum over them, then the
+// att outputs (one chain of n_kv steps per dim).  Between the nodes every
+// value takes the F32 round trip the separate nodes pass it on (the GEMV
+// writes x32_to_f32 of its code, soft_max and the KQV GEMV convert their F32
+// inputs with x32_from_f32), so the result is theirs bit for bit.  The
+// soft_max total is an xlns32 code, far finer than its chain's error, so the
+// KQV chains wait for it (no predicted start as in sum32).
+__global__ __launch_bounds__(k_block) void k_attn32(attn32_args a, dev_tables T) {
+    extern __shared__ __align__(16) char lds[];
+    const red16<LNSHIP_SUM32> R = stage_for<LNSHIP_SUM32, true>(T, lds);
+    const int hd = a.hd, n = a.n_kv, hp = (hd + 7) & ~7, rs = (n + 7) & ~7;
+    uint32_t *xq = reinterpret_cast<uint32_t *>(lds + k_lds_tab32);   // the query's codes
+    uint32_t *c = xq + hp;                                             // scores, then exps
+    uint32_t *pc = c + rs;                                             // KQV's activation codes
+    __shared__ int32_t s_max;
+    __shared__ uint32_t s_tot;
+    __shared__ int s_last;
+    const int h = blockIdx.x, kv = h / a.rep;
+    if (threadIdx.x == 0) {
+        s_max = x32_canon(0xffffffffu);
+        s_last = 0;
+    }
+    for (int k = threadIdx.x; k < hp; k += blockDim.x) xq[k] = k < hd ? x32_from_f32(a.q[(int64_t)h * hd + k]) : 0u;
+    __syncthreads();
+    // the scores, and soft_max's first pass over them (k_softmax32's)
+    const uint32_t sc = x32_from_f32(a.scale);
+    const uint32_t *kw = a.k + kv * a.k_slice;
+    for (int j = threadIdx.x; j < n; j += blockDim.x) {
+        acc_ls acc{};
+        row_chain32(R.O, acc, kw + (int64_t)j * 8, a.k_gs, xq, 0, hd);
+        uint32_t v = x32_from_f32(x32_to_f32(acc.s | acc.l));
+        if (v != 0xffffffffu) {
+            v = x32_mul(v, sc);
+            if (a.mask) {
+                const float mf = a.mask[j];
+                const uint32_t mk = mf <= -3.0e38f ? 0xffffffffu : x32_from_f32(mf);
+                if (mk == 0xffffffffu) v = 0xffffffffu;
+                else if (mk & k32_logmask) v = x32_add_dec(R.O, v, mk);
+            }
+        }
+        c[j] = v;
+        atomicMax(&s_max, x32_canon(v));
+    }
+    __syncthreads();
+    {
+        const int32_t cm = s_max;
+        const uint32_t mx = (uint32_t)(cm < 0 ? (cm ^ 0x7fffffff) : cm);
+        for (int j = threadIdx.x; j < n; j += blockDim.x) {
+            const float fv = x32_to_f32(x32_add_dec(R.O, c[j], mx ^ k32_sign));
+            const uint32_t e = x32_from_f32((float)exp((double)fv));
+            c[j] = e;
+            if (e & k32_logmask) atomicMax(&s_last, j);
+        }
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        // the sum of exps up to the last nonzero one, as k_softmax32 runs it
+        acc_ls acc{c[0] & k32_logmask, c[0] & k32_sign};
+        const int n_eff = s_last + 1;
+        if (n_eff > 1) chain32<true>(R.O, acc, c, 1, n_eff);
+        s_tot = acc.s | acc.l;
+    }
+    __syncthreads();
+    // soft_max's output as KQV's mul_mat reads it: each probability through
+    // F32 into xlns32
+    const uint32_t tot = s_tot;
+    for (int j = threadIdx.x; j < rs; j += blockDim.x)
+        pc[j] = j < n ? x32_from_f32(x32_to_f32(x32_div(c[j], tot))) : 0u;
+    __syncthreads();
+    const uint32_t *vw = a.v + kv * a.v_slice;
+    for (int d = threadIdx.x; d < hd; d += blockDim.x) {
+        acc_ls acc{};
+        row_chain32(R.O, acc, vw + (int64_t)d * 8, a.v_gs, pc, 0, n);
+        a.dst[(int64_t)h * hd + d] = x32_to_f32(acc.s | acc.l);
+    }
+}
+
 __global__ __launch_bounds__(k_block) void k_softmax32(sm_args a, dev_tables T) {
     extern __shared__ __align__(16) char lds[];
     const red16<LNSHIP_SUM32> R = stage_tables<LNSHIP_SUM32>(T, lds);
@@ -2864,6 +3033,12 @@ static int launch_attn16(const attn_args &m, int64_t nh, const dev_tables &T, hi
     hipLaunchKernelGGL(k_attn16<MODE>, dim3((unsigned)nh), dim3(k_block), lds, st, m, T);
     LNSHIP_HIP(hipGetLastError());
     return 0;
+}
+
+// LDS of a k_attn32 launch: the single-chain image, the query, the scores
+// and the probabilities' codes (4 bytes each)
+static int64_t attn32_lds(int64_t hd, int64_t n_kv) {
+    return k_lds_tab32 + 4 * ((hd + 7) & ~(int64_t)7) + 8 * ((n_kv + 7) & ~(int64_t)7);
 }
 
 // cells of lnship16_attn_decode with head_dim up to 256
@@ -3650,7 +3825,8 @@ int lnship16_attn_decode(int mode, const lnship_attn_args *a, void *stream) {
         return fail(LNSHIP_ERANGE, "attn_decode: head_dim x n_kv too large for LDS%s");
     device_state *s = state();
     if (!s) return LNSHIP_ENOINIT;
-    const attn_args m{a->q, a->k_cache, a->v_cache, a->cache_m * 8, a->k_slice, a->head_dim * 8, a->v_slice,
+    const attn_args m{a->q, (const uint16_t *)a->k_cache, (const uint16_t *)a->v_cache, a->cache_m * 8, a->k_slice,
+                      a->head_dim * 8, a->v_slice,
                       a->mask, a->scale, a->dst, (int)a->head_dim, (int)a->n_kv, (int)(a->n_head / a->n_head_kv),
                       g_predict_skew};
     hipStream_t st = (hipStream_t)stream;
@@ -3659,6 +3835,27 @@ int lnship16_attn_decode(int mode, const lnship_attn_args *a, void *stream) {
         case LNSHIP_LPVIP: return launch_attn16<LNSHIP_LPVIP>(m, a->n_head, s->T, st);
         default: return launch_attn16<LNSHIP_SUM32>(m, a->n_head, s->T, st);
     }
+}
+
+int lnship32_attn_decode(const lnship_attn_args *a, void *stream) {
+    // arguments and sizes first: they need no device
+    if (!a) return fail(LNSHIP_EINVAL, "attn_decode: null args%s");
+    if (!a->q || !a->k_cache || !a->v_cache || !a->dst || a->n_head <= 0 || a->n_head_kv <= 0 ||
+        a->n_head % a->n_head_kv || a->head_dim <= 0 || a->n_kv <= 0 || a->cache_m < a->n_kv ||
+        a->head_dim > 4096 || a->n_head > 65535)
+        return fail(LNSHIP_EINVAL, "attn_decode: bad argument%s");
+    if (attn32_lds(a->head_dim, a->n_kv) > k_lds_bytes - k_lds_static)
+        return fail(LNSHIP_ERANGE, "attn_decode: head_dim x n_kv too large for LDS%s");
+    device_state *s = state();
+    if (!s) return LNSHIP_ENOINIT;
+    const attn32_args m{a->q, (const uint32_t *)a->k_cache, (const uint32_t *)a->v_cache, a->cache_m * 8, a->k_slice,
+                        a->head_dim * 8, a->v_slice, a->mask, a->scale, a->dst, (int)a->head_dim, (int)a->n_kv,
+                        (int)(a->n_head / a->n_head_kv)};
+    const int lds = (int)attn32_lds(a->head_dim, a->n_kv);
+    if (int rc = set_lds(k_attn32, lds)) return rc;
+    hipLaunchKernelGGL(k_attn32, dim3((unsigned)a->n_head), dim3(k_block), lds, (hipStream_t)stream, m, s->T);
+    LNSHIP_HIP(hipGetLastError());
+    return 0;
 }
 
 int lnship32_soft_max(const lnship_soft_max_args *a, void *stream) {
@@ -3683,6 +3880,7 @@ int lnship32_soft_max(const lnship_soft_max_args *a, void *stream) {
 int64_t lnship_max_row(int which, int mode) {
     if (which == 2) return max_row(k_lds_pos32, 4);
     if (which == 3) return max_row(k_lds_tab32, 4);
+    if (which == 7) return ((k_lds_bytes - k_lds_static - attn32_lds(256, 0)) / 8) & ~(int64_t)7;
     if (which == 5) {
         // lnship16_rms_norm_mul_mat: the tables, the x row and h (4 B per k)
         if (mode != LNSHIP_SUM32) return 0;

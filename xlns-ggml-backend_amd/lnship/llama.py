@@ -459,6 +459,10 @@ class LlamaLNS16:
         return out
 
 
+# the most cells for which LlamaLNS32 runs a decode step's attention as one
+# launch (one kq chain per lane of a 256-lane workgroup)
+ATTN32_FUSED_KV = 256
+
 LLAMA_1B = LlamaConfig(n_layer=16, n_embd=2048, n_head=32, n_head_kv=8, head_dim=64, n_ff=8192, n_vocab=32000,
                        n_ctx=1024)
 
@@ -510,6 +514,14 @@ class LlamaLNS32:
         assert self.kslice == self.vslice
         self.kcache = [torch.zeros(nkv * self.kslice, dtype=torch.int32, device=dev) for _ in range(c.n_layer)]
         self.vcache = [torch.zeros(nkv * self.kslice, dtype=torch.int32, device=dev) for _ in range(c.n_layer)]
+        # a single-token step's kq, soft_max and kqv in one launch
+        # (lnship32_attn_decode, bit-identical to the three ops) where one
+        # round of its workgroup's 256 lanes holds the cells' kq chains: past
+        # that the separate kq GEMV, whose chains spread over many CUs, wins
+        # (at n_kv 768 the fused step is 1 % slower); fused_attn = False runs
+        # the three ops
+        self.fused_attn = True
+        self._attn_max_kv = min(lib().lnship_max_row(7, 0), ATTN32_FUSED_KV)
         rt = np.empty(c.n_ctx * hd, np.float32)
         check(lib().lnship_rope_table(c.rope_theta, hd, c.n_ctx, ctypes.c_void_p(rt.ctypes.data)))
         self.cos_sin = t(rt)
@@ -560,13 +572,19 @@ class LlamaLNS32:
             qs = QkvStoreArgs(P(qkv), nqkv, P(pos_dev), T, nh, nkv, hd, hd, P(self.cos_sin), P(q),
                               P(self.kcache[il]), P(self.vcache[il]), c.n_ctx, self.kslice, self.vslice, None, 0)
             check(L.lnship32_rope_store_kv(ctypes.byref(qs), st))
-            mm(self.kcache[il].data_ptr(), P(q), P(kq), hd, n_kv, T, ne02=nkv, ne12=nh, x_ld=nq, x_slice=hd,
-               w_mstride=c.n_ctx, w_slice=self.kslice)
-            a = SoftMaxArgs(P(kq), (ctypes.c_int64 * 4)(n_kv, T, nh, 1), P(mask), (ctypes.c_int64 * 4)(n_kv, T, 1, 1),
-                            1.0 / math.sqrt(hd), P(kq), 0)
-            check(L.lnship32_soft_max(ctypes.byref(a), st))
-            mm(self.vcache[il].data_ptr(), P(kq), P(att), n_kv, hd, T, ne02=nkv, ne12=nh, x_ld=n_kv,
-               x_slice=T * n_kv, w_slice=self.vslice, dst_ld=nq, dst_slice=hd)
+            if T == 1 and self.fused_attn and n_kv <= self._attn_max_kv:
+                # the three nodes below in one launch, bit for bit
+                aa = AttnArgs(P(q), P(self.kcache[il]), P(self.vcache[il]), c.n_ctx, self.kslice, self.vslice,
+                              P(mask), 1.0 / math.sqrt(hd), P(att), nh, nkv, hd, n_kv)
+                check(L.lnship32_attn_decode(ctypes.byref(aa), st))
+            else:
+                mm(self.kcache[il].data_ptr(), P(q), P(kq), hd, n_kv, T, ne02=nkv, ne12=nh, x_ld=nq, x_slice=hd,
+                   w_mstride=c.n_ctx, w_slice=self.kslice)
+                a = SoftMaxArgs(P(kq), (ctypes.c_int64 * 4)(n_kv, T, nh, 1), P(mask),
+                                (ctypes.c_int64 * 4)(n_kv, T, 1, 1), 1.0 / math.sqrt(hd), P(kq), 0)
+                check(L.lnship32_soft_max(ctypes.byref(a), st))
+                mm(self.vcache[il].data_ptr(), P(kq), P(att), n_kv, hd, T, ne02=nkv, ne12=nh, x_ld=n_kv,
+                   x_slice=T * n_kv, w_slice=self.vslice, dst_ld=nq, dst_slice=hd)
             rows = 1 if last else T
             r0 = (T - rows) * e
             if rows == T:   # x += Wo att: the residual ADD inside the mul_mat
