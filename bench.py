@@ -12,7 +12,8 @@ mul_mat GMAC/s, the roofline of the dominant kernel (the decode GEMV) and the
 single-threaded CPU oracle timed on this host on a bounded sample.  The line
 also carries BASELINE config 5's prefill GEMM (prefill_gemm: GMAC/s in sum32
 and base against the VALU-issue roofline, parity and the oracle's rate on a
-slice of it).
+slice of it), config 3 (c3: 8 sequences x 256-token prompts, batched decode
+in monte and lpvip) and config 4 (c4: the LNS32 1B-shape decoder).
 """
 import argparse
 import ctypes
@@ -39,6 +40,9 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-prefill-gemm", action="store_true",
                     help="leave BASELINE config 5's GEMM (GMAC/s, sum32 and base) out of the default line")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="leave BASELINE configs 3 (monte and lpvip, 8 sequences) and 4 (LNS32 1B shape) out of the "
+                         "default line")
     ap.add_argument("--no-graph", action="store_true", help="decode eagerly instead of replaying a HIP graph")
     ap.add_argument("--split-attn", action="store_true",
                     help="run a decode step's kq, soft_max and kqv as three launches (not one fused attention)")
@@ -142,54 +146,65 @@ def run_ops(args):
             line(op="soft_max", mode=mname, heads=32, rows=512, n=512, us=round(us, 2))
 
 
-def run_batch(args):
-    """S sequences of the SmolLM2-shape model: each --prompt-token prompt is
-    prefilled on its own, then --warmup + --steps batched decode steps (one
-    token per sequence; weight GEMVs see S columns, attention is batched over
-    the sequences' own KV caches).  Every step replays one HIP graph (Monte
-    ops read their LFSR start from a device state the graph advances)."""
+def batch_measure(mode_name, S, prompt_n, warmup, steps, graph=True):
+    """S sequences of the SmolLM2-shape model in one mode: each prompt_n-token
+    prompt is prefilled on its own, then warmup + steps batched decode steps
+    (one token per sequence; weight GEMVs see S columns, attention is batched
+    over the sequences' own KV caches).  Every step replays one HIP graph
+    (Monte ops read their LFSR start from a device state the graph advances).
+    Returns decode tok/s over the timed steps, ms per step, prefill tok/s and
+    the KV view length."""
     import numpy as np
     import torch
     import lnship
     from lnship import llama
     torch.cuda.set_device(0)
     lnship.init()
-    cfg, S = llama.SMOLLM2_135M, args.batch
-    mode = lnship.MODES[args.mode]
+    cfg = llama.SMOLLM2_135M
     weights = llama.synthetic_weights(cfg, seed=1234, std=0.02)
-    model = llama.LlamaLNS16(cfg, weights, mode=mode, n_seq=S)
+    model = llama.LlamaLNS16(cfg, weights, mode=lnship.MODES[mode_name], n_seq=S)
     rng = np.random.default_rng(2024)
-    prompts = [[int(t) for t in rng.integers(0, cfg.n_vocab, args.prompt)] for _ in range(S)]
+    prompts = [[int(t) for t in rng.integers(0, cfg.n_vocab, prompt_n)] for _ in range(S)]
     torch.cuda.synchronize()
     tp = time.perf_counter()
     first = [model.eval(prompts[s], seq=s).argmax() for s in range(S)]
     torch.cuda.synchronize()
     t_prefill = time.perf_counter() - tp
     tok_dev = torch.stack(first).to(torch.int32)
-    use_graph = not args.no_graph
 
     def step():
         nonlocal tok_dev
-        out = model.decode_graph_batch(tok_dev) if use_graph else model.eval_batch(tok_dev.tolist())
+        out = model.decode_graph_batch(tok_dev) if graph else model.eval_batch(tok_dev.tolist())
         tok_dev = out.argmax(dim=1).to(torch.int32)
 
-    for _ in range(args.warmup):
+    for _ in range(warmup):
         step()
     torch.cuda.synchronize()
     ts = time.perf_counter()
-    for _ in range(args.steps):
+    for _ in range(steps):
         step()
     torch.cuda.synchronize()
     t_decode = time.perf_counter() - ts
+    res = {"decode_tok_s": round(S * steps / t_decode, 3), "ms_per_step": round(t_decode / steps * 1e3, 4),
+           "prefill_tok_s": round(S * prompt_n / t_prefill, 3), "n_kv": model.batch_n_kv()}
+    del model
+    torch.cuda.empty_cache()
+    return res
+
+
+def run_batch(args):
+    """BASELINE config 3 on its own line (--batch S): batch_measure in --mode."""
+    S = args.batch
+    r = batch_measure(args.mode, S, args.prompt, args.warmup, args.steps, graph=not args.no_graph)
     print(json.dumps({
         "metric": "LNS16 batched decode tok/s, %d sequences, SmolLM2-135M shape" % S,
-        "value": round(S * args.steps / t_decode, 3), "unit": "tok/s", "n_gpus": 1, "steps": args.steps,
-        "warmup": args.warmup, "ms_per_step": round(t_decode / args.steps * 1e3, 4), "higher_is_better": True,
+        "value": r["decode_tok_s"], "unit": "tok/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": r["ms_per_step"], "higher_is_better": True,
         "dtype": "xlns16", "data": "synthetic (as the default workload)",
         "config": {"workload": "BASELINE config 3: %d x %d-token prompts, then batched greedy decode" % (S, args.prompt),
-                   "mode": args.mode, "sequences": S, "n_kv": model.batch_n_kv(),
-                   "graph": "hipGraph per decode step" if use_graph else "eager"},
-        "prefill_tok_s": round(S * args.prompt / t_prefill, 3)}), flush=True)
+                   "mode": args.mode, "sequences": S, "n_kv": r["n_kv"],
+                   "graph": "eager" if args.no_graph else "hipGraph per decode step"},
+        "prefill_tok_s": r["prefill_tok_s"]}), flush=True)
 
 
 def calib_copy(mib):
@@ -684,7 +699,41 @@ def main():
             print("bench.py: GPU logits differ from the CPU oracle's", file=sys.stderr)
     if not args.no_prefill_gemm:
         out["prefill_gemm"] = prefill_gemm(lnship, torch, np, cpu=not args.no_cpu)
+    if not args.no_configs:
+        del model
+        torch.cuda.empty_cache()
+        out["c3"] = other_configs_c3()
+        out["c4"] = other_configs_c4()
     print(json.dumps(out), flush=True)
+
+
+# BASELINE configs 3 and 4 in the default line, each at its named shape, with
+# fewer timed decode steps than their own lines take by default
+C3_SEQS, C3_PROMPT, C3_WARMUP, C3_STEPS = 8, 256, 1, 63
+C4_PROMPT, C4_WARMUP, C4_STEPS = 512, 2, 24
+
+
+def other_configs_c3():
+    """8 independent 256-token prompts, each prefilled on
+    its own, then 64 graph-replayed batched greedy decode steps (the first
+    one untimed), in monte and lpvip."""
+    res = {"workload": "BASELINE config 3: %d x %d-token prompts, prefill each, then %d batched greedy decode "
+                       "steps (%d timed)" % (C3_SEQS, C3_PROMPT, C3_WARMUP + C3_STEPS, C3_STEPS),
+           "sequences": C3_SEQS, "timed_steps": C3_STEPS, "unit": "tok/s (all sequences)"}
+    for mode in ("monte", "lpvip"):
+        res[mode] = batch_measure(mode, C3_SEQS, C3_PROMPT, C3_WARMUP, C3_STEPS)
+    return res
+
+
+def other_configs_c4():
+    """the LNS32 1B-shape decoder, 512-token prompt, then
+    graph-replayed greedy decode (the first C4_WARMUP + C4_STEPS tokens of
+    its 256)."""
+    r, _ = lns32_measure(C4_PROMPT, C4_WARMUP, C4_STEPS)
+    r["workload"] = ("BASELINE config 4: LNS32 Llama-style 1B-shape decoder, %d-token prompt, then greedy decode "
+                     "(%d timed steps)" % (C4_PROMPT, C4_STEPS))
+    r["unit"] = "tok/s"
+    return r
 
 
 def run_ggml(args):
@@ -785,13 +834,13 @@ def lns32_weights(cfg, seed, std, torch):
     return w
 
 
-def run_lns32(args):
+def lns32_measure(prompt_n, warmup, steps, graph=True, split_attn=False):
     """the LNS32 backend's graph on a Llama-style 1B-shape
     decoder (16 layers, d 2048, 32 / 8 heads x 64, SwiGLU 8192, vocab 32000),
     random-init N(0, 0.02) weights packed as xlns32 (4 bytes per weight).
     Prefill of the prompt, then greedy decode from a replayed HIP graph.  The
     roofline is the decode's weight stream: every token reads each packed
-    weight once."""
+    weight once.  Returns the figures and the weights (for the CPU leg)."""
     import numpy as np
     import torch
     import lnship
@@ -800,11 +849,10 @@ def run_lns32(args):
     torch.cuda.set_device(0)
     lnship.init()
     cfg = llama.LLAMA_1B
-    prompt_n = args.prompt if args.prompt is not None else 512
     t0 = time.perf_counter()
     weights = lns32_weights(cfg, 4321, 0.02, torch)
     model = llama.LlamaLNS32(cfg, weights)
-    model.fused_attn = model.fused_attn and not args.split_attn
+    model.fused_attn = model.fused_attn and not split_attn
     torch.cuda.synchronize()
     t_setup = time.perf_counter() - t0
     rng = np.random.default_rng(2024)
@@ -820,39 +868,57 @@ def run_lns32(args):
 
     def step():
         nonlocal tok_dev
-        out = model.eval([int(tok_dev.item())]) if args.no_graph else model.decode_graph(tok_dev)
+        out = model.decode_graph(tok_dev) if graph else model.eval([int(tok_dev.item())])
         tok_dev = torch.argmax(out).to(torch.int32).reshape(1)
 
-    for _ in range(args.warmup):
+    for _ in range(warmup):
         step()
     torch.cuda.synchronize()
     ts = time.perf_counter()
-    for _ in range(args.steps):
+    for _ in range(steps):
         step()
     torch.cuda.synchronize()
     t_decode = time.perf_counter() - ts
-    tok_s = args.steps / t_decode
+    tok_s = steps / t_decode
     wbytes = model.weight_bytes_per_token()
     achieved = wbytes * tok_s / 1e9
+    res = {"decode_tok_s": round(tok_s, 3), "ms_per_step": round(t_decode / steps * 1e3, 4),
+           "prefill_tok_s": round(prompt_n / t_prefill, 3), "n_kv": llama.n_kv_for(model.n_past, cfg.n_ctx),
+           "weight_stream": {"achieved": round(achieved, 3), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                             "frac": round(achieved / HBM_PEAK_GBS, 6), "weight_bytes_per_token": wbytes},
+           "setup_s": round(t_setup, 2)}
+    del model
+    torch.cuda.empty_cache()
+    return res, weights
+
+
+def run_lns32(args):
+    """BASELINE config 4 on its own line (--lns32): lns32_measure, and the
+    oracle's LNS32 graph timed on the host beside it."""
+    from lnship import llama
+    prompt_n = args.prompt if args.prompt is not None else 512
+    r, weights = lns32_measure(prompt_n, args.warmup, args.steps, graph=not args.no_graph,
+                               split_attn=args.split_attn)
+    ws = r["weight_stream"]
     out = {
         "metric": "LNS32 decode tok/s and weight-stream HBM GB/s, 1B-shape Llama decoder",
-        "value": round(tok_s, 3), "unit": "tok/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
-        "ms_per_step": round(t_decode / args.steps * 1e3, 4), "higher_is_better": True, "scaling": "weak",
+        "value": r["decode_tok_s"], "unit": "tok/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": r["ms_per_step"], "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "xlns32",
         "data": "synthetic: torch-seeded N(0,0.02) weights packed as xlns32, uniform token ids",
         "config": {"workload": "BASELINE config 4: LNS32 Llama-style 1B-shape decoder, %d-token prompt then "
                                "greedy decode (one decoded token per step)" % prompt_n,
-                   "prompt_tokens": prompt_n, "n_kv": llama.n_kv_for(model.n_past, cfg.n_ctx),
+                   "prompt_tokens": prompt_n, "n_kv": r["n_kv"],
                    "graph": "eager" if args.no_graph else "hipGraph per decode step"},
-        "prefill_tok_s": round(prompt_n / t_prefill, 3),
-        "roofline": {"bound": "hbm", "achieved": round(achieved, 3), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 6), "traffic": None,
+        "prefill_tok_s": r["prefill_tok_s"],
+        "roofline": {"bound": "hbm", "achieved": ws["achieved"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": ws["frac"], "traffic": None,
                      "kernel": "whole decode token: xlns32 weights read once per token",
-                     "weight_bytes_per_token": wbytes},
-        "setup_s": round(t_setup, 2),
+                     "weight_bytes_per_token": ws["weight_bytes_per_token"]},
+        "setup_s": r["setup_s"],
     }
     if not args.no_cpu:
-        out["cpu_baseline"] = cpu_baseline_lns32(cfg, weights, torch)
+        out["cpu_baseline"] = cpu_baseline_lns32(llama.LLAMA_1B, weights, __import__("torch"))
     print(json.dumps(out), flush=True)
 
 
