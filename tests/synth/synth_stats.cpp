@@ -15,6 +15,7 @@
 //
 // usage: synth_stats synth <base|monte|lpvip|sum32|xlns32> <signed|positive|attn> <kmin> <kmax> [xlns32 variant]
 //        synth_stats convert <xlns16|xlns32>
+//        synth_stats monte <signed|positive|attn> <kmin> <kmax> <reps> <outputs>
 #include <algorithm>
 #include <cmath>
 #include <cstdio>
@@ -131,6 +132,57 @@ int synth(const std::string &cfg, const std::string &dist, int64_t kmin, int64_t
     return 0;
 }
 
+// The experiment's Monte rows (results/monte.jsonl, run.py:98-105:
+// dot-bench.cpp synth with --reps 32 --outputs 2048): M = outputs / 4, the
+// LFSR set before each rep's product from (seed, rep, K)
+// (dot-bench.cpp:149-150), rep 0's "acc" statistics, then those of the mean
+// over the first 1, 2, 4, ... reps of every output (dot-bench.cpp:166-177).
+int monte_reps(const std::string &dist, int64_t kmin, int64_t kmax, int reps, int64_t outputs) {
+    const uint64_t seed = 1;
+    const int64_t N = 4, M = std::max<int64_t>(1, outputs / N);
+    for (int64_t K = kmin; K <= kmax; K *= 2) {
+        std::mt19937_64 rng(seed + (uint64_t)K);
+        std::vector<float> a0, x0, a, x;
+        operands(dist, K, M, N, rng, a0, x0);
+        round16(a0, a);
+        round16(x0, x);
+        std::vector<long double> s((size_t)(M * N)), s1((size_t)(M * N));
+        for (int64_t n = 0; n < N; n++)
+            for (int64_t m = 0; m < M; m++) {
+                long double t = 0, t1 = 0;
+                for (int64_t k = 0; k < K; k++) {
+                    const long double p = (long double)a[(size_t)(m * K + k)] * (long double)x[(size_t)(n * K + k)];
+                    t += p;
+                    t1 += fabsl(p);
+                }
+                s[(size_t)(n * M + m)] = t;
+                s1[(size_t)(n * M + m)] = t1;
+            }
+        std::vector<std::vector<float>> outs((size_t)reps, std::vector<float>((size_t)(M * N)));
+        for (int r = 0; r < reps; r++) {
+            lno_monte_set_state((uint16_t)(1 + (seed * 7919 + (uint64_t)r * 104729 + (uint64_t)K) % 65535));
+            lno16_mul_mat_f32w(LNO_MONTE, a0.data(), x0.data(), outs[(size_t)r].data(), K, M, N, 1, 1, 1, 1);
+        }
+        Stats st;
+        for (size_t i = 0; i < s.size(); i++) st.add(outs[0][i], s[i], s1[i]);
+        st.print("monte", dist.c_str(), (long long)K);
+        for (int r = 1; r <= reps; r *= 2) {
+            Stats sa;
+            for (size_t i = 0; i < s.size(); i++) {
+                long double m = 0;
+                for (int q = 0; q < r; q++) m += outs[(size_t)q][i];
+                sa.add(m / r, s[i], s1[i]);
+            }
+            const double mean = sa.sum / sa.n;
+            std::printf("{\"avg\":{\"dist\":\"%s\",\"K\":%lld,\"reps\":%d,\"bias\":%.6g,\"sd\":%.6g,\"rms\":%.6g}}\n",
+                        dist.c_str(), (long long)K, r, mean, std::sqrt(std::max(0.0, sa.sumsq / sa.n - mean * mean)),
+                        std::sqrt(sa.sumsq / sa.n));
+        }
+        std::fflush(stdout);
+    }
+    return 0;
+}
+
 // dot-bench.cpp:186-218: 4M log-uniform values, three round trips
 int convert(const std::string &fmt) {
     const bool x32 = fmt == "xlns32";
@@ -180,6 +232,9 @@ int main(int argc, char **argv) {
         return synth(argv[2], argv[3], std::atoll(argv[4]), std::atoll(argv[5]));
     }
     if (argc >= 3 && !std::strcmp(argv[1], "convert")) return convert(argv[2]);
-    std::fprintf(stderr, "usage: %s synth CFG DIST KMIN KMAX [VARIANT] | convert FMT\n", argv[0]);
+    if (argc >= 7 && !std::strcmp(argv[1], "monte"))
+        return monte_reps(argv[2], std::atoll(argv[3]), std::atoll(argv[4]), std::atoi(argv[5]), std::atoll(argv[6]));
+    std::fprintf(stderr, "usage: %s synth CFG DIST KMIN KMAX [VARIANT] | convert FMT | monte DIST KMIN KMAX REPS OUTPUTS\n",
+                 argv[0]);
     return 2;
 }

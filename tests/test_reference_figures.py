@@ -8,11 +8,12 @@ evidence sets of the reference:
     xlnscpp);
   * results/sum32-evidence/standalone-sum32-invariants.txt:
     test-lns16-sum32.cpp;
-  * experiments/dot-product-scaling/results/{synth,convert}.jsonl:
+  * experiments/dot-product-scaling/results/{synth,convert,monte}.jsonl:
     dot-bench.cpp, whose operands tests/synth/synth_stats.cpp regenerates
     with the same libstdc++ generators, so its six-digit statistics over
-    4096 outputs per K are exact pins.  That experiment ran on the
-    post-merge libraries (experiments/README.md:28-37).
+    4096 outputs per K (monte.jsonl: 2048 outputs, 32 reps from per-rep
+    LFSR seeds, and the rep averages) are exact pins.  That experiment ran
+    on the post-merge libraries (experiments/README.md:28-37).
 
 Where the oracle's restatement disagrees with a printed figure, the test is a
 strict xfail that names the figure: the disagreement is reported, never
@@ -268,6 +269,38 @@ EXP_REASON = " (the experiment ran the post-merge libraries, experiments/README.
 def test_synth_mode_rows(synth_exe, cfg, dist, kmax):
     got, want = _synth_case(synth_exe, cfg, dist, kmax)
     assert got == want
+
+
+MONTE_ROWS = json.load(open(os.path.join(HERE, "golden", "monte_rows.json")))["rows"]
+
+
+def _monte_reps(exe, dist, kmax):
+    """The oracle's statistics in the Monte experiment's form (rep 0's acc
+    statistics and the averages over 1, 2, 4, ... 32 reps, each rep from
+    its own LFSR seed), as synth_stats monte prints them"""
+    out = subprocess.run([exe, "monte", dist, "16", str(kmax), "32", "2048"], capture_output=True, text=True,
+                         check=True).stdout
+    acc, avg = {}, {}
+    for line in out.splitlines():
+        d = json.loads(line)
+        if "avg" in d:
+            avg.setdefault(d["avg"]["K"], []).append({k: "%.6g" % d["avg"][k] for k in ("bias", "sd", "rms")})
+        else:
+            acc[d["K"]] = _fmt(d["acc"])
+    return acc, avg
+
+
+@pytest.mark.xfail(strict=True, reason=MONTE_REASON + EXP_REASON)
+@pytest.mark.parametrize("dist", ["signed", "positive", "attn"])
+def test_monte_rep_rows(synth_exe, dist):
+    # results/monte.jsonl: 2048 outputs per K, 32 reps with per-rep LFSR
+    # seeds; rep 0's five statistics and the rep-averaged bias, sd and rms,
+    # every row K = 16..1024 to all six printed digits
+    want = {r["K"]: r for r in MONTE_ROWS if r["dist"] == dist and r["K"] <= 1024}
+    acc, avg = _monte_reps(synth_exe, dist, 1024)
+    assert {K: acc[K] for K in want} == {K: _fmt(r["acc"]) for K, r in want.items()}
+    assert {K: avg[K] for K in want} == {
+        K: [{k: "%.6g" % a[k] for k in ("bias", "sd", "rms")} for a in r["avg"]] for K, r in want.items()}
 
 
 def test_xlns32_evidence_sets_disagree(synth_exe, standalone):
