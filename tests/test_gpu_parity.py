@@ -693,13 +693,16 @@ def test_mul_mat_id_expert_out_of_range(ln):
     same_bits(got[1], want[1], "token after the bad expert")
 
 
-@pytest.mark.parametrize("mode,n_kv,big_tail,skew", [
-    ("base", 1, False, 0), ("base", 13, False, 0), ("base", 256, False, 0), ("base", 256, True, 0),
-    ("lpvip", 13, False, 0), ("lpvip", 256, False, 0), ("lpvip", 256, True, 0), ("sum32", 1, False, 0),
-    ("sum32", 13, False, 0), ("sum32", 256, False, 0), ("sum32", 256, True, 0), ("sum32", 520, False, 0),
-    ("sum32", 2048, False, 0), ("sum32", 1, False, 1), ("sum32", 13, False, -1), ("sum32", 256, True, 3),
-    ("sum32", 520, False, -7)])
-def test_attn_decode_equals_three_nodes(ln, mode, n_kv, big_tail, skew):
+@pytest.mark.parametrize("mode,n_kv,big_tail,skew,hd", [
+    ("base", 1, False, 0, 64), ("base", 13, False, 0, 64), ("base", 256, False, 0, 64), ("base", 256, True, 0, 64),
+    ("lpvip", 13, False, 0, 64), ("lpvip", 256, False, 0, 64), ("lpvip", 256, True, 0, 64), ("sum32", 1, False, 0, 64),
+    ("sum32", 13, False, 0, 64), ("sum32", 256, False, 0, 64), ("sum32", 256, True, 0, 64), ("sum32", 520, False, 0, 64),
+    ("sum32", 2048, False, 0, 64), ("sum32", 1, False, 1, 64), ("sum32", 13, False, -1, 64),
+    ("sum32", 256, True, 3, 64), ("sum32", 520, False, -7, 64),
+    # head dims off the group of eight: the score chains end inside a group
+    ("sum32", 13, False, 0, 36), ("sum32", 200, False, 0, 72), ("sum32", 77, True, 2, 100),
+    ("base", 200, False, 0, 72)])
+def test_attn_decode_equals_three_nodes(ln, mode, n_kv, big_tail, skew, hd):
     # lnship16_attn_decode against K^T q, soft_max and V p run as three ops
     # (the library's own launches, and the oracle's), on
     # the SmolLM2 head shape (9 query heads over 3 kv heads of 64), random
@@ -711,9 +714,9 @@ def test_attn_decode_equals_three_nodes(ln, mode, n_kv, big_tail, skew):
     # result comes from the rerun
     import ctypes
     m = O.MODES[mode]
-    nh, nkv, hd, n_ctx = 9, 3, 64, max(256, (n_kv + 255) // 256 * 256)
+    nh, nkv, n_ctx = 9, 3, max(256, (n_kv + 255) // 256 * 256)
     rng = np.random.default_rng(n_kv)
-    print(f"\n[attn decode] {mode} n_kv={n_kv} big_tail={big_tail}", flush=True)
+    print(f"\n[attn decode] {mode} n_kv={n_kv} big_tail={big_tail} skew={skew} head_dim={hd}", flush=True)
     pos = max(0, n_kv - 1 - n_kv // 5)
     v = (rng.standard_normal((nkv, hd, n_ctx)) * 0.5).astype(np.float32)
     if big_tail:

@@ -1867,6 +1867,18 @@ __global__ __launch_bounds__(k_block) void k_softmax16(sm_args a, dev_tables T) 
 // ---- decode attention: KQ, soft_max and KQV of one token in one launch ------
 // head_dim up to which the KQV chain may stop at the last nonzero exp
 constexpr int k_attn_tail_hd = 256;
+// The decode attention's workgroups avoid XCD 0, where the co-located decode
+// GEMVs before them run (workgroups are dealt to the eight XCDs round-robin,
+// block b to XCD b mod 8): measured with cycle stamps, a head's chains on the
+// XCD of the preceding GEMVs ran about 13 % longer than on any other (moving
+// the GEMVs to XCD 1 moved the slow head there), and the launch waits for its
+// slowest head.  Block b (b mod 8 != 0) works as head b - b / 8 - 1; the
+// grid (attn_grid) ends at the block of the last head.
+__device__ __forceinline__ int attn_head(bool &idle) {
+    idle = (blockIdx.x & 7u) == 0;
+    return (int)(blockIdx.x - blockIdx.x / 8u - 1u);
+}
+
 struct attn_args {
     const float *q;
     const uint16_t *k, *v;
@@ -1883,73 +1895,124 @@ struct attn_args {
 // activations' codes at x in LDS), each an xlns16_mul product, added into acc
 // in k order as k_mm16 adds them (term 0 starts acc).  The weights of the next
 // PF groups are in flight while a block is added.
-// row_chain for sum32, in the order of k_mm16's single-chain loop: each
-// product is formed in the first round trip of the step before it, which
-// also passes on the opposite-signs flag of the next step.
+// row_chain for sum32, in the order and with the pipeline of k_mm16's
+// single-chain loop: the products of steps 2i and 2i + 1 are formed together
+// (the two 16-bit halves of one word) in the second round trip of an earlier
+// step, each step's product is unpacked from its pair in the first round
+// trip of the step before it, which also passes on the opposite-signs flag.
+// Groups strictly inside [k0, k1) run their eight steps with no bounds test;
+// only the first and the last group test each step.
 __device__ __forceinline__ void row_chain_x32(const red16<LNSHIP_SUM32> &R, acc_ls &acc,
                                               const uint16_t *__restrict__ w, int64_t gs, const uint16_t *x, int k0,
                                               int k1) {
     if (k1 <= k0) return;
     constexpr int PF = 4;
-    const int gl = (k1 - 1) >> 3;
-    // term k: the xlns16 product, its log and sign at the xlns32 positions
-    auto term = [&](uint32_t wv, uint32_t xv, uint32_t &tl, uint32_t &ts) {
-        const uint32_t t = x16_mul(wv, xv);
-        tl = (t & k16_logmask) << 16;
-        ts = (t & k16_sign) << 16;
+    const int gf = k0 >> 3, gl = (k1 - 1) >> 3;
+    const int uf = k0 & 7, ul = k1 - 8 * gl;   // the first group's first step, the last group's end
+    // masks in registers (short encodings of the instructions that take them)
+    uint32_t k_lm = 0x7fff7fffu, k_sg = k32_sign, k_hi = 0xffff0000u;
+    asm("" : "+v"(k_lm), "+v"(k_sg), "+v"(k_hi));
+    // two xlns16 products (xlns16_mul) in the halves of one word: the log
+    // fields added (no carry crosses the halves), less the offset with
+    // unsigned saturation (underflow: log 0), capped at 0x7fff; signs xor'ed
+    auto pair = [&](uint32_t wv, uint32_t xv, uint32_t &l, uint32_t &sg) {
+        const uint32_t lm = (wv & k_lm) + (xv & k_lm);
+        l = pk_min_u16(pk_sub_sat_u16(lm, 0x40004000u), 0x7fff7fffu);
+        sg = wv ^ xv;
     };
-    auto term_at = [&](int k, uint32_t &tl, uint32_t &ts) { term(w[(int64_t)(k >> 3) * gs + (k & 7)], x[k], tl, ts); };
-    // term 0 starts the sum; the steps add terms ks .. k1 - 1
-    const int ks = k0 == 0 ? 1 : k0;
-    uint32_t c_tl, c_ts, c_uf;
-    if (k0 == 0) {
-        term_at(0, c_tl, c_ts);
-        acc = {c_tl, c_ts};
-        if (k1 == 1) return;
-    }
-    term_at(ks, c_tl, c_ts);
-    c_uf = acc.s ^ c_ts;
-    // the steps of group g (wq, xq) at k in [ks, k1); wn, xn: the next group
-    auto group = [&](const uint4 &wq, const uint4 &xq, const uint4 &wn, const uint4 &xn, int g) {
-        const uint32_t ww[4] = {wq.x, wq.y, wq.z, wq.w}, xx[4] = {xq.x, xq.y, xq.z, xq.w};
-#pragma unroll
-        for (int u = 0; u < 8; u++) {
-            const int k = 8 * g + u;
-            if (k < ks || k >= k1) continue;
-            uint32_t ntl = 0, nts = 0;
-            auto next = [&] {
-                if (u < 7) term(half16(ww[(u + 1) >> 1], (u + 1) & 1), half16(xx[(u + 1) >> 1], (u + 1) & 1), ntl, nts);
-                else term(wn.x & 0xffffu, xn.x & 0xffffu, ntl, nts);
-                return nts;
-            };
-            c_uf = x32_add_step(R.O, acc, c_tl, c_ts, c_uf, next, [] {});
-            c_tl = ntl;
-            c_ts = nts;
+    // the product of step u at the xlns32 positions, from its pair
+    auto half = [&](int u, uint32_t l, uint32_t sg, uint32_t &tl, uint32_t &ts) {
+        if ((u & 1) == 0) {
+            tl = l << 16;
+            ts = (sg << 16) & k_sg;
+        } else {
+            tl = l & k_hi;
+            ts = sg & k_sg;
         }
     };
-    // blocks of PF groups, double-buffered as in row_chain; loads past the
-    // last group reload it
+    // carried between groups: the pending step's product and flag, and the
+    // next group's first pair
+    uint32_t c_tl = 0, c_ts = 0, c_uf = 0, c_pl = 0, c_ps = 0;
+    // steps [u0, u1) of a group (wq, xq); wn, xn: the next group's data.
+    // fresh: the group's pairs are formed here (the chain's first group);
+    // start: its step u0 = 0 is term 0, which starts the sum
+    auto group = [&](const uint4 &wq, const uint4 &xq, const uint4 &wn, const uint4 &xn, int u0, int u1, bool fresh,
+                     bool start) __attribute__((always_inline)) {
+        const uint32_t ww[4] = {wq.x, wq.y, wq.z, wq.w}, xx[4] = {xq.x, xq.y, xq.z, xq.w};
+        uint32_t pl[4], ps[4];
+        if (fresh) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) pair(ww[i], xx[i], pl[i], ps[i]);
+            pair(wn.x, xn.x, c_pl, c_ps);
+#pragma unroll
+            for (int u = 0; u < 8; u++)
+                if (u == u0) half(u, pl[u >> 1], ps[u >> 1], c_tl, c_ts);
+            c_uf = acc.s ^ c_ts;
+        } else {
+            pl[0] = c_pl;
+            ps[0] = c_ps;
+        }
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            if (u >= u0 && u < u1) {
+                uint32_t ntl = 0, nts = 0;
+                auto next = [&] {
+                    if (u + 1 < u1) half(u + 1, pl[(u + 1) >> 1], ps[(u + 1) >> 1], ntl, nts);
+                    else if (u == 7) half(0, c_pl, c_ps, ntl, nts);
+                    return nts;
+                };
+                // a fresh group has every pair already
+                auto post = [&] {
+                    if (fresh) return;
+                    if ((u & 1) == 0 && u < 6) pair(ww[(u >> 1) + 1], xx[(u >> 1) + 1], pl[(u >> 1) + 1], ps[(u >> 1) + 1]);
+                    if (u == 6) pair(wn.x, xn.x, c_pl, c_ps);
+                };
+                if (start && u == 0) {
+                    acc = {c_tl, c_ts};
+                    c_uf = c_ts ^ next();
+                    post();
+                } else {
+                    c_uf = x32_add_step(R.O, acc, c_tl, c_ts, c_uf, next, post);
+                }
+                c_tl = ntl;
+                c_ts = nts;
+            }
+        }
+    };
+    // a group of the block loop: the last one tests its steps, the others
+    // run all eight
+    auto body = [&](const uint4 &wq, const uint4 &xq, const uint4 &wn, const uint4 &xn, int g)
+                    __attribute__((always_inline)) {
+        if (g < gl) group(wq, xq, wn, xn, 0, 8, false, false);
+        else group(wq, xq, wn, xn, 0, ul, false, false);
+    };
+    // loads past the last group reload it
+    auto ldw = [&](int g) { return *reinterpret_cast<const uint4 *>(w + (int64_t)min(g, gl) * gs); };
+    auto ldx = [&](int g) { return *reinterpret_cast<const uint4 *>(x + 8 * min(g, gl)); };
     uint4 wa[PF], xa[PF], wb[PF], xb[PF];
     auto load = [&](uint4 (&w4)[PF], uint4 (&x4)[PF], int g0) {
 #pragma unroll
         for (int p = 0; p < PF; p++) {
-            const int g = min(g0 + p, gl);
-            w4[p] = *reinterpret_cast<const uint4 *>(w + (int64_t)g * gs);
-            x4[p] = *reinterpret_cast<const uint4 *>(x + 8 * g);
+            w4[p] = ldw(g0 + p);
+            x4[p] = ldx(g0 + p);
         }
     };
+    // the first group, then blocks of PF groups, double-buffered
+    {
+        const uint4 w0 = ldw(gf), x0 = ldx(gf);
+        load(wa, xa, gf + 1);
+        load(wb, xb, gf + 1 + PF);
+        group(w0, x0, wa[0], xa[0], uf, gf < gl ? 8 : ul, true, k0 == 0);
+    }
     auto run = [&](const uint4 (&w4)[PF], const uint4 (&x4)[PF], const uint4 (&wo)[PF], const uint4 (&xo)[PF],
-                   int g0) {
+                   int g0) __attribute__((always_inline)) {
 #pragma unroll
         for (int p = 0; p < PF; p++) {
             if (g0 + p > gl) break;
-            group(w4[p], x4[p], p + 1 < PF ? w4[p + 1] : wo[0], p + 1 < PF ? x4[p + 1] : xo[0], g0 + p);
+            body(w4[p], x4[p], p + 1 < PF ? w4[p + 1] : wo[0], p + 1 < PF ? x4[p + 1] : xo[0], g0 + p);
         }
     };
-    const int g1 = ks >> 3;
-    load(wa, xa, g1);
-    load(wb, xb, g1 + PF);
-    for (int g0 = g1; g0 <= gl; g0 += 2 * PF) {
+    for (int g0 = gf + 1; g0 <= gl; g0 += 2 * PF) {
         run(wa, xa, wb, xb, g0);
         if (g0 + PF > gl) break;
         load(wa, xa, g0 + 2 * PF);
@@ -2023,7 +2086,9 @@ __global__ __launch_bounds__(k_block) void k_attn16(attn_args a, dev_tables T) {
     __shared__ double s_part[k_block / 64];
     __shared__ int s_last;
     __shared__ uint32_t s_vmax[k_attn_tail_hd];   // per dim: the largest V log past the last nonzero exp
-    const int h = blockIdx.x, kv = h / a.rep;
+    bool idle;
+    const int h = attn_head(idle), kv = h / a.rep;
+    if (idle) return;
     const bool tail_stop = hd <= k_attn_tail_hd;
     if (threadIdx.x == 0) {
         s_max = x16_canon(0xffffu);
@@ -2277,7 +2342,9 @@ __global__ __launch_bounds__(k_block) void k_attn32(attn32_args a, dev_tables T)
     __shared__ int32_t s_max;
     __shared__ uint32_t s_tot;
     __shared__ int s_last;
-    const int h = blockIdx.x, kv = h / a.rep;
+    bool idle;
+    const int h = attn_head(idle), kv = h / a.rep;
+    if (idle) return;
     if (threadIdx.x == 0) {
         s_max = x32_canon(0xffffffffu);
         s_last = 0;
@@ -2916,6 +2983,10 @@ static mm16_shape mm_shape_x32(int64_t M, int64_t N, int64_t nslices, int64_t kp
 // is a multiple of 2^sh working, the working ones fall on 8 >> sh XCDs and
 // share those L2s' copies.  sh is the largest (at most 3) for which those
 // XCDs still hold every working workgroup at one per CU.
+// the grid of nh attention heads placed by attn_head: every block up to the
+// last head's, the multiples of 8 idle
+static unsigned attn_grid(int64_t nh) { return (unsigned)(nh + 1 + (nh - 1) / 7); }
+
 static uint32_t xcd_shift(uint64_t wgs, int cus) {
     const uint64_t per_xcd = (uint64_t)std::max(cus / 8, 1);
     uint32_t sh = 3;
@@ -3030,7 +3101,7 @@ template <int MODE>
 static int launch_attn16(const attn_args &m, int64_t nh, const dev_tables &T, hipStream_t st) {
     const int lds = attn16_lds<MODE>(m.hd, m.n_kv);
     if (int rc = set_lds(k_attn16<MODE>, lds)) return rc;
-    hipLaunchKernelGGL(k_attn16<MODE>, dim3((unsigned)nh), dim3(k_block), lds, st, m, T);
+    hipLaunchKernelGGL(k_attn16<MODE>, dim3(attn_grid(nh)), dim3(k_block), lds, st, m, T);
     LNSHIP_HIP(hipGetLastError());
     return 0;
 }
@@ -3853,7 +3924,7 @@ int lnship32_attn_decode(const lnship_attn_args *a, void *stream) {
                         (int)(a->n_head / a->n_head_kv)};
     const int lds = (int)attn32_lds(a->head_dim, a->n_kv);
     if (int rc = set_lds(k_attn32, lds)) return rc;
-    hipLaunchKernelGGL(k_attn32, dim3((unsigned)a->n_head), dim3(k_block), lds, (hipStream_t)stream, m, s->T);
+    hipLaunchKernelGGL(k_attn32, dim3(attn_grid(a->n_head)), dim3(k_block), lds, (hipStream_t)stream, m, s->T);
     LNSHIP_HIP(hipGetLastError());
     return 0;
 }
