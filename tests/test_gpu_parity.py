@@ -761,7 +761,7 @@ def test_attn_decode_equals_three_nodes(ln, mode, n_kv, big_tail, skew, hd):
 @pytest.mark.parametrize("n_kv,masked,big_tail,hd", [
     (1, False, False, 64), (13, True, False, 64), (256, True, False, 64), (256, True, True, 64),
     (520, True, False, 64), (768, True, False, 64), (1024, False, False, 64), (1024, True, False, 64),
-    (200, True, False, 128)])
+    (200, True, False, 128), (13, True, False, 36), (200, True, True, 72)])
 def test_attn32_decode_equals_three_nodes(ln, n_kv, masked, big_tail, hd):
     # lnship32_attn_decode (LNS32) against kq, soft_max and kqv run as three
     # ops, the library's launches and the oracle's, on the Llama-1B head

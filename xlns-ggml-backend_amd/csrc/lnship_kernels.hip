@@ -2256,13 +2256,15 @@ __device__ __forceinline__ void row_chain32(const x32_tab &O, acc_ls &acc, const
     struct g8 {
         uint4 lo, hi;
     };
-    auto group = [&](const g8 &wq, const g8 &xq, const g8 &wn, const g8 &xn, int g) {
+    // steps [u0, u1) of group g; the groups strictly inside the row run all
+    // eight with no bounds test
+    auto group = [&](const g8 &wq, const g8 &xq, const g8 &wn, const g8 &xn, int u0, int u1)
+                     __attribute__((always_inline)) {
         const uint32_t ww[8] = {wq.lo.x, wq.lo.y, wq.lo.z, wq.lo.w, wq.hi.x, wq.hi.y, wq.hi.z, wq.hi.w};
         const uint32_t xx[8] = {xq.lo.x, xq.lo.y, xq.lo.z, xq.lo.w, xq.hi.x, xq.hi.y, xq.hi.z, xq.hi.w};
 #pragma unroll
         for (int u = 0; u < 8; u++) {
-            const int k = 8 * g + u;
-            if (k < ks || k >= k1) continue;
+            if (u < u0 || u >= u1) continue;
             uint32_t tn = 0;
             auto next = [&] {
                 tn = u < 7 ? x32_mul(ww[u + 1], xx[u + 1]) : x32_mul(wn.lo.x, xn.lo.x);
@@ -2271,6 +2273,11 @@ __device__ __forceinline__ void row_chain32(const x32_tab &O, acc_ls &acc, const
             uf = x32_add_step(O, acc, t & k32_logmask, t & k32_sign, uf, next, [] {});
             t = tn;
         }
+    };
+    const int g1 = ks >> 3, ul = k1 - 8 * gl;
+    auto body = [&](const g8 &wq, const g8 &xq, const g8 &wn, const g8 &xn, int g) __attribute__((always_inline)) {
+        if (g > g1 && g < gl) group(wq, xq, wn, xn, 0, 8);
+        else group(wq, xq, wn, xn, g == g1 ? ks & 7 : 0, g == gl ? ul : 8);
     };
     // blocks of PF groups, double-buffered; loads past the last group reload it
     g8 wa[PF], xa[PF], wb[PF], xb[PF];
@@ -2284,14 +2291,14 @@ __device__ __forceinline__ void row_chain32(const x32_tab &O, acc_ls &acc, const
             x4[p] = {xp[0], xp[1]};
         }
     };
-    auto run = [&](const g8 (&w4)[PF], const g8 (&x4)[PF], const g8 (&wo)[PF], const g8 (&xo)[PF], int g0) {
+    auto run = [&](const g8 (&w4)[PF], const g8 (&x4)[PF], const g8 (&wo)[PF], const g8 (&xo)[PF], int g0)
+                   __attribute__((always_inline)) {
 #pragma unroll
         for (int p = 0; p < PF; p++) {
             if (g0 + p > gl) break;
-            group(w4[p], x4[p], p + 1 < PF ? w4[p + 1] : wo[0], p + 1 < PF ? x4[p + 1] : xo[0], g0 + p);
+            body(w4[p], x4[p], p + 1 < PF ? w4[p + 1] : wo[0], p + 1 < PF ? x4[p + 1] : xo[0], g0 + p);
         }
     };
-    const int g1 = ks >> 3;
     load(wa, xa, g1);
     load(wb, xb, g1 + PF);
     for (int g0 = g1; g0 <= gl; g0 += 2 * PF) {
