@@ -46,6 +46,9 @@ def parse():
     ap.add_argument("--no-graph", action="store_true", help="decode eagerly instead of replaying a HIP graph")
     ap.add_argument("--split-attn", action="store_true",
                     help="run a decode step's kq, soft_max and kqv as three launches (not one fused attention)")
+    ap.add_argument("--split-rope", action="store_true",
+                    help="LNS16 decode: the query rope and the cache stores as a launch of their own, apart from the "
+                         "fused attention")
     ap.add_argument("--split-rms", action="store_true",
                     help="decode: rms_norm + MUL (sum32) and swiglu as launches of their own, apart from the "
                          "mul_mat after them")
@@ -337,9 +340,12 @@ def chain_bound(model, ln, torch, mode):
         steps.append(ne[0] - 1)
         orig[2](x_ptr, ne, mask_ptr, mne, scale, dst_ptr)
 
-    def attn(args):
+    def attn(args, store=None):
         steps.append(args.head_dim + 2 * args.n_kv - 1)
-        orig[3](args)
+        if store is None:
+            orig[3](args)
+        else:
+            orig[3](args, store)
 
     def rms_mm(x_ptr, wn_ptr, w, h_ptr, dst_ptr, K, M, T):
         if T == 1 and model.fused_rms:
@@ -606,6 +612,7 @@ def main():
     model.fused_rms = model.fused_rms and not args.split_rms
     model.fused_glu = model.fused_glu and not args.split_rms
     model.fused_attn = model.fused_attn and not args.split_attn
+    model.fused_rope = not args.split_rope
     torch.cuda.synchronize()
     t_setup = time.perf_counter() - t0
 

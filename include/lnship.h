@@ -283,6 +283,21 @@ typedef struct lnship_attn_args {
     int64_t n_head, n_head_kv, head_dim, n_kv;
 } lnship_attn_args;
 int lnship16_attn_decode(int mode, const lnship_attn_args *args, void *stream);
+
+/* lnship16_rope_store_kv for one token and lnship16_attn_decode in one
+ * launch: each query head's workgroup rotates its query (lns_rope,
+ * src/lns-ops.cpp:1199-1281, written through F32) and stores its kv head's rotated
+ * key and value of the current cell (the codes lnship16_rope_store_kv writes;
+ * the query heads of one kv group store the same codes), then runs the
+ * attention.  dst and both caches come out bit-identical to the two calls.
+ * store->ntok must be 1 and store->seq null; its heads, head_dim (a multiple
+ * of 8), caches, cache_m and slices must equal the attention's; store->q_dst
+ * and args->q are not used.  A position outside the cache is recorded as in
+ * lnship16_rope_store_kv (lnship_index_error) and dst is not written.  No
+ * single counterpart in the reference, which runs ROPE, the cache copies and
+ * the attention nodes one by one. */
+int lnship16_rope_attn_decode(int mode, const lnship_qkv_store_args *store, const lnship_attn_args *args,
+                              void *stream);
 /* The same for the LNS32 backend (xlns32 codes in the caches, in the layout
  * lnship32_rope_store_kv writes): lns32_mul_mat for kq, lns32_soft_max, then
  * lns32_mul_mat for kqv (src32/lns32-ops.cpp:98-144, :384-436), F32 between

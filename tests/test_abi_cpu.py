@@ -267,3 +267,38 @@ def test_positive_sum_pair_image(lnship):
         f = np.arange(1 << sh, dtype=np.int64)
         slope = int(t[i, 1]) >> sc
         assert np.array_equal((int(t[i, 1]) * (f << fs)) >> 32, (slope * f) >> sh)
+
+
+def test_rope_attn_decode_checks_its_store_arguments_first(lnship):
+    # lnship16_rope_attn_decode takes the token's rope and cache stores with
+    # the attention: every store argument must describe the same heads and
+    # caches, one token of one sequence; a mismatch is refused before any
+    # device call, a matching pair then needs a device
+    L = lnship.lib()
+    fake = ctypes.c_void_p(0x1000).value   # never dereferenced: the checks come first
+    EINVAL, ENOINIT = -1, -3   # include/lnship.h: enum lnship_error
+    nh, nkv, hd, n_ctx = 9, 3, 64, 256
+
+    def pair():
+        a = lnship.AttnArgs()
+        a.k_cache, a.v_cache, a.dst, a.mask = fake, fake + 64, fake + 128, fake + 192
+        a.cache_m, a.k_slice, a.v_slice, a.scale = n_ctx, hd * n_ctx, hd * n_ctx, 0.125
+        a.n_head, a.n_head_kv, a.head_dim, a.n_kv = nh, nkv, hd, 200
+        q = lnship.QkvStoreArgs(fake, (nh + 2 * nkv) * hd, fake + 256, 1, nh, nkv, hd, hd, fake + 320, None,
+                                fake, fake + 64, n_ctx, hd * n_ctx, hd * n_ctx, None, 0)
+        return q, a
+
+    q, a = pair()
+    assert L.lnship16_rope_attn_decode(lnship.SUM32, ctypes.byref(q), ctypes.byref(a), None) == ENOINIT
+    # args.q may be null: the fused rope forms the queries
+    assert not a.q
+    for field, value in (("ntok", 2), ("n_head", nh - 1), ("n_head_kv", 1), ("head_dim", 60),
+                         ("rope_n_dims", 63), ("rope_n_dims", 72), ("qkv_ld", (nh + 2 * nkv) * hd - 1),
+                         ("k_cache", fake + 8), ("v_cache", fake + 8), ("cache_m", n_ctx + 8), ("k_slice", 8),
+                         ("v_slice", 8), ("seq", fake), ("qkv", None), ("pos", None), ("cos_sin", None)):
+        q, a = pair()
+        setattr(q, field, value)
+        assert L.lnship16_rope_attn_decode(lnship.SUM32, ctypes.byref(q), ctypes.byref(a), None) == EINVAL, field
+    q, a = pair()
+    assert L.lnship16_rope_attn_decode(lnship.MONTE, ctypes.byref(q), ctypes.byref(a), None) == EINVAL
+    assert L.lnship16_rope_attn_decode(lnship.SUM32, None, ctypes.byref(a), None) == EINVAL

@@ -758,6 +758,79 @@ def test_attn_decode_equals_three_nodes(ln, mode, n_kv, big_tail, skew, hd):
         assert ln.lib().lnship_max_row(4, O.MONTE) == 0 and ln.lib().lnship_max_row(4, m) >= 4096
 
 
+@pytest.mark.parametrize("mode,n_kv,nd,hd,pos", [
+    ("sum32", 1, 64, 64, 0), ("sum32", 13, 64, 64, 12), ("sum32", 256, 64, 64, 200), ("sum32", 520, 64, 64, 517),
+    ("sum32", 200, 32, 64, 150), ("sum32", 77, 72, 72, 60), ("base", 256, 64, 64, 200), ("lpvip", 13, 64, 64, 9),
+    ("sum32", 256, 64, 64, 300)])
+def test_rope_attn_decode_equals_two_launches(ln, mode, n_kv, nd, hd, pos):
+    # lnship16_rope_attn_decode against lnship16_rope_store_kv (one token)
+    # then lnship16_attn_decode: the attention output and both whole caches
+    # bit for bit, on the SmolLM2 head counts with random caches, a causal
+    # mask and partial rotations (nd < hd); at pos 300 with n_kv 256 the new
+    # cell lies past the attended cells (it is stored, not read)
+    import ctypes
+    rng = np.random.default_rng(1000 + n_kv + pos)
+    L, st = ln.lib(), ln._stream()
+    m = O.MODES[mode]
+    P = lambda t: ctypes.c_void_p(t.data_ptr())
+    nh, nkv, n_ctx = 9, 3, 768
+    print(f"\n[rope attn decode] {mode} n_kv={n_kv} rope dims={nd} head_dim={hd} pos={pos}", flush=True)
+    nqkv = (nh + 2 * nkv) * hd
+    qkv = dev((rng.standard_normal(nqkv) * 2).astype(np.float32))
+    rt = np.empty(n_ctx * nd, np.float32)
+    ln.check(L.lnship_rope_table(ctypes.c_float(10000.0), nd, n_ctx, ctypes.c_void_p(rt.ctypes.data)))
+    cs = dev(rt)
+    posd = dev(np.array([pos], np.int32))
+    kf = (rng.standard_normal((nkv, n_ctx, hd)) * 0.5).astype(np.float32)
+    vf = (rng.standard_normal((nkv, hd, n_ctx)) * 0.5).astype(np.float32)
+    kslice, vslice = ln.kp(hd) * n_ctx, ln.kp(n_ctx) * hd
+    maskf = np.where(np.arange(n_kv) <= pos, 0.0, -np.inf).astype(np.float32)
+    mask = dev(maskf)
+    outs = []
+    for fused in (False, True):
+        kc, vc = ln.pack16(dev(kf)), ln.pack16(dev(vf))
+        q = torch.full((nh * hd,), 7.0, dtype=torch.float32, device="cuda")
+        got = torch.full((nh * hd,), float("nan"), device="cuda")
+        qs = ln.QkvStoreArgs(P(qkv), nqkv, P(posd), 1, nh, nkv, hd, nd, P(cs), P(q), P(kc), P(vc), n_ctx, kslice,
+                             vslice, None, 0)
+        a = ln.AttnArgs(P(q), P(kc), P(vc), n_ctx, kslice, vslice, P(mask), 0.125, P(got), nh, nkv, hd, n_kv)
+        if fused:
+            ln.check(L.lnship16_rope_attn_decode(m, ctypes.byref(qs), ctypes.byref(a), st))
+        else:
+            ln.check(L.lnship16_rope_store_kv(ctypes.byref(qs), st))
+            ln.check(L.lnship16_attn_decode(m, ctypes.byref(a), st))
+        outs.append((host(got), host(kc), host(vc)))
+    (w_att, w_k, w_v), (g_att, g_k, g_v) = outs
+    assert np.array_equal(g_k, w_k) and np.array_equal(g_v, w_v), "caches"
+    same_bits(g_att, w_att, f"rope attn decode {mode} n_kv={n_kv}")
+
+
+def test_rope_attn_decode_position_out_of_range(ln):
+    # a position at or beyond the cache is recorded as an index error, and
+    # neither the caches nor dst are written
+    import ctypes
+    L, st = ln.lib(), ln._stream()
+    P = lambda t: ctypes.c_void_p(t.data_ptr())
+    nh, nkv, hd, n_ctx, n_kv = 2, 1, 16, 16, 8
+    nqkv = (nh + 2 * nkv) * hd
+    qkv = dev(np.ones(nqkv, np.float32))
+    rt = np.empty(n_ctx * hd, np.float32)
+    ln.check(L.lnship_rope_table(ctypes.c_float(10000.0), hd, n_ctx, ctypes.c_void_p(rt.ctypes.data)))
+    cs = dev(rt)
+    posd = dev(np.array([n_ctx], np.int32))
+    kc = torch.full((hd * n_ctx,), 0x1234, dtype=torch.int16, device="cuda")
+    vc = torch.full((hd * n_ctx,), 0x1234, dtype=torch.int16, device="cuda")
+    got = torch.full((nh * hd,), 7.0, device="cuda")
+    bad = ctypes.c_int64(0)
+    L.lnship_index_error(ctypes.byref(bad), st)   # clear
+    qs = ln.QkvStoreArgs(P(qkv), nqkv, P(posd), 1, nh, nkv, hd, hd, P(cs), None, P(kc), P(vc), n_ctx, hd * n_ctx,
+                         hd * n_ctx, None, 0)
+    a = ln.AttnArgs(None, P(kc), P(vc), n_ctx, hd * n_ctx, hd * n_ctx, None, 0.25, P(got), nh, nkv, hd, n_kv)
+    ln.check(L.lnship16_rope_attn_decode(O.SUM32, ctypes.byref(qs), ctypes.byref(a), st))
+    assert L.lnship_index_error(ctypes.byref(bad), st) == 1 and bad.value == n_ctx
+    assert np.all(host(kc) == 0x1234) and np.all(host(vc) == 0x1234) and np.all(host(got) == 7.0)
+
+
 @pytest.mark.parametrize("n_kv,masked,big_tail,hd", [
     (1, False, False, 64), (13, True, False, 64), (256, True, False, 64), (256, True, True, 64),
     (520, True, False, 64), (768, True, False, 64), (1024, False, False, 64), (1024, True, False, 64),

@@ -1864,6 +1864,247 @@ __global__ __launch_bounds__(k_block) void k_softmax16(sm_args a, dev_tables T) 
     }
 }
 
+// ---- elementwise ops of the Llama graph ---------------------------------------
+
+// The elementwise ops in either format: fmt16 (xlns16 through the
+// conversion, decode, Gaussian-log and sigmoid tables) or fmt32 (xlns32,
+// converted arithmetically, adder over the global xlns32 tables).
+struct fmt16 {
+    using code_t = uint16_t;
+    const dev_tables &T;
+    __device__ __forceinline__ uint32_t from(float v) const { return x16_from_f32(T.cvt16, v); }
+    __device__ __forceinline__ float to(uint32_t c) const { return T.rev16[c]; }
+    __device__ __forceinline__ uint32_t add(uint32_t x, uint32_t y) const { return x16_add_g(T.gauss16, x, y); }
+    __device__ __forceinline__ uint32_t mul(uint32_t x, uint32_t y) const { return x16_mul(x, y); }
+    __device__ __forceinline__ uint32_t neg(uint32_t x) const { return x ^ k16_sign; }
+    // xlns16_silu: x times the table sigmoid of x
+    __device__ __forceinline__ uint32_t silu(uint32_t x) const { return x16_mul(x, T.sig16[x]); }
+};
+struct fmt32 {
+    using code_t = uint32_t;
+    const dev_tables &T;
+    __device__ __forceinline__ uint32_t from(float v) const { return x32_from_f32(v); }
+    __device__ __forceinline__ float to(uint32_t c) const { return x32_to_f32(c); }
+    __device__ __forceinline__ uint32_t add(uint32_t x, uint32_t y) const { return x32_add(T.tab32, x, y); }
+    __device__ __forceinline__ uint32_t mul(uint32_t x, uint32_t y) const { return x32_mul(x, y); }
+    __device__ __forceinline__ uint32_t neg(uint32_t x) const { return x ^ k32_sign; }
+    // xlns32_silu: x times the sigmoid of its value, the sigmoid formed in
+    // double and rounded to float (libm-independent at float precision)
+    __device__ __forceinline__ uint32_t silu(uint32_t x) const {
+        const double v = (double)x32_to_f32(x);
+        return x32_mul(x, x32_from_f32((float)(1.0 / (1.0 + exp(-v)))));
+    }
+};
+template <int W>
+using fmt_t = typename std::conditional<W == 16, fmt16, fmt32>::type;
+
+template <int W, int OP>   // OP 0 add, 1 mul
+__global__ void k_binary(const float *__restrict__ a, const float *__restrict__ b, int64_t n, int64_t nb,
+                         float *__restrict__ dst, dev_tables T) {
+    const fmt_t<W> F{T};
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)blockDim.x * gridDim.x) {
+        const uint32_t x = F.from(a[i]), y = F.from(b[i % nb]);
+        dst[i] = F.to(OP == 0 ? F.add(x, y) : F.mul(x, y));
+    }
+}
+
+template <int W>
+__global__ void k_swiglu(const float *__restrict__ g, int64_t g_ld, const float *__restrict__ u, int64_t u_ld,
+                         float *__restrict__ dst, int64_t ncols, int64_t nrows, dev_tables T) {
+    const fmt_t<W> F{T};
+    const int64_t n = ncols * nrows;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)blockDim.x * gridDim.x) {
+        const int64_t r = i / ncols, c = i - r * ncols;
+        const uint32_t gv = F.from(g[r * g_ld + c]);
+        const uint32_t uv = F.from(u[r * u_ld + c]);
+        dst[i] = F.to(F.mul(F.silu(gv), uv));
+    }
+}
+
+// y = x s (+ b when b is not zero), in the format's arithmetic
+template <int W>
+__global__ void k_scale(const float *__restrict__ src, float *__restrict__ dst, int64_t n, float s, float b,
+                        dev_tables T) {
+    const fmt_t<W> F{T};
+    const uint32_t sc = F.from(s), bc = F.from(b);
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)blockDim.x * gridDim.x) {
+        uint32_t v = F.mul(F.from(src[i]), sc);
+        if (b != 0.0f) v = F.add(v, bc);
+        dst[i] = F.to(v);
+    }
+}
+
+__global__ void k_get_rows_packed(const uint16_t *__restrict__ w, int64_t K, int64_t M, const int32_t *__restrict__ rows,
+                                  int64_t nrows, float *__restrict__ dst, const float *__restrict__ rev) {
+    const int64_t n = nrows * K;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)blockDim.x * gridDim.x) {
+        const int64_t r = i / K, k = i - r * K;
+        const int64_t m = rows[r];
+        dst[i] = rev[w[((k >> 3) * M + m) * 8 + (k & 7)]];
+    }
+}
+
+// one thread per rotated pair (or passthrough element)
+template <class F>
+__device__ __forceinline__ void rope_pair(const F &f, const float *xr, int64_t j, int n_dims, int neox, const float *cs,
+                                          int64_t &i0, int64_t &i1, uint32_t &r0, uint32_t &r1) {
+    const uint32_t c = f.from(cs[j * 2]), sn = f.from(cs[j * 2 + 1]);
+    i0 = neox ? j : 2 * j;
+    i1 = neox ? j + n_dims / 2 : 2 * j + 1;
+    const uint32_t x0 = f.from(xr[i0]), x1 = f.from(xr[i1]);
+    r0 = f.add(f.mul(x0, c), f.neg(f.mul(x1, sn)));
+    r1 = f.add(f.mul(x0, sn), f.mul(x1, c));
+}
+
+// item i of a rope: a rotated pair (j < n_dims / 2) or a passthrough element
+// of row (token, head); ntok * nhead * (n_dims / 2 + ne0 - n_dims) items
+template <class F>
+__device__ __forceinline__ void rope_item(const F &f, int64_t i, const float *x, int64_t x_ld, const int32_t *pos,
+                                          int64_t nhead, int64_t ne0, int n_dims, int neox, const float *cos_sin,
+                                          float *dst) {
+    const int64_t half = n_dims / 2, per = half + (ne0 - n_dims);
+    const int64_t row = i / per, j = i - row * per;
+    const int64_t t = row / nhead, h = row - t * nhead;
+    const float *xr = x + t * x_ld + h * ne0;
+    float *yr = dst + (t * nhead + h) * ne0;
+    if (j < half) {
+        int64_t i0, i1;
+        uint32_t r0, r1;
+        rope_pair(f, xr, j, n_dims, neox, cos_sin + (int64_t)pos[t] * half * 2, i0, i1, r0, r1);
+        yr[i0] = f.to(r0);
+        yr[i1] = f.to(r1);
+    } else {
+        const int64_t i0 = n_dims + (j - half);
+        yr[i0] = f.to(f.from(xr[i0]));
+    }
+}
+
+template <int W>
+__global__ void k_rope(const float *__restrict__ x, int64_t x_ld, const int32_t *__restrict__ pos, int64_t ntok,
+                       int64_t nhead, int64_t ne0, int n_dims, int neox, const float *__restrict__ cos_sin,
+                       float *__restrict__ dst, dev_tables T) {
+    const fmt_t<W> F{T};
+    const int64_t n = ntok * nhead * (n_dims / 2 + (ne0 - n_dims));
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)blockDim.x * gridDim.x)
+        rope_item(F, i, x, x_ld, pos, nhead, ne0, n_dims, neox, cos_sin, dst);
+}
+
+// F32 value -> IEEE half (round to nearest even) -> F32 -> LNS, as the KV
+// cache stores and reads it
+// item i (element (token, head, d)) of a KV-cache store;
+// ntok * nhead * ne0 items
+// A position outside the cache's cache_m rows is recorded (err, as an index
+// out of range) and its item is skipped: nothing is read from the rope
+// table or written to the cache for it.
+template <class F, class C>
+__device__ __forceinline__ void store_kv_item(const F &f, int64_t i, const float *x, int64_t x_ld, const int32_t *pos,
+                                              int64_t nhead, int64_t ne0, int rope_n_dims, const float *cos_sin,
+                                              C *cache, int64_t cache_m, int64_t cache_slice, int transposed,
+                                              const int32_t *seq, int64_t seq_stride, unsigned long long *err) {
+    const int64_t half = rope_n_dims / 2;
+    const int64_t row = i / ne0, d = i - row * ne0;
+    const int64_t t = row / nhead, h = row - t * nhead;
+    const float *xr = x + t * x_ld + h * ne0;
+    const int64_t p = pos[t];
+    if (p < 0 || p >= cache_m) {
+        index_fault(err, p);
+        return;
+    }
+    float v;
+    if (rope_n_dims > 0 && d < rope_n_dims) {
+        // normal rope: element d belongs to pair d / 2
+        int64_t i0, i1;
+        uint32_t r0, r1;
+        rope_pair(f, xr, d / 2, rope_n_dims, 0, cos_sin + p * half * 2, i0, i1, r0, r1);
+        v = f.to((d & 1) ? r1 : r0);
+    } else if (rope_n_dims > 0) {
+        v = f.to(f.from(xr[d]));
+    } else {
+        v = xr[d];
+    }
+    const int64_t o = transposed ? h * cache_slice + ((p >> 3) * ne0 + d) * 8 + (p & 7)
+                                 : h * cache_slice + ((d >> 3) * cache_m + p) * 8 + (d & 7);
+    cache[(seq ? (int64_t)seq[t] * seq_stride : 0) + o] = (C)f.from(__half2float(__float2half_rn(v)));
+}
+
+template <int W>
+__global__ void k_store_kv(const float *__restrict__ x, int64_t x_ld, const int32_t *__restrict__ pos, int64_t ntok,
+                           int64_t nhead, int64_t ne0, int rope_n_dims, const float *__restrict__ cos_sin,
+                           typename fmt_t<W>::code_t *__restrict__ cache, int64_t cache_m, int64_t cache_slice,
+                           int transposed, const int32_t *__restrict__ seq, int64_t seq_stride, dev_tables T,
+                           unsigned long long *err) {
+    const fmt_t<W> F{T};
+    const int64_t n = ntok * nhead * ne0;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)blockDim.x * gridDim.x)
+        store_kv_item(F, i, x, x_ld, pos, nhead, ne0, rope_n_dims, cos_sin, cache, cache_m, cache_slice, transposed,
+                      seq, seq_stride, err);
+}
+
+// The query rope and the key / value cache stores after a fused QKV
+// mul_mat, as one grid: items [0, nq) rope the query heads, the next nk
+// store the (rotated) key heads, the last nk the value heads.
+template <int W>
+__global__ void k_rope_store_kv(lnship_qkv_store_args a, dev_tables T, unsigned long long *err) {
+    using C = typename fmt_t<W>::code_t;
+    const fmt_t<W> F{T};
+    const int64_t hd = a.head_dim, nd = a.rope_n_dims;
+    const int64_t nq = a.ntok * a.n_head * (nd / 2 + (hd - nd)), nk = a.ntok * a.n_head_kv * hd;
+    const float *xk = a.qkv + a.n_head * hd, *xv = xk + a.n_head_kv * hd;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < nq + 2 * nk;
+         i += (int64_t)blockDim.x * gridDim.x) {
+        if (i < nq) {
+            // the rope table has cache_m rows: a query beyond them is recorded
+            // and skipped, like the cache stores
+            const int64_t t = i / (a.n_head * (nd / 2 + (hd - nd)));
+            const int64_t p = a.pos[t];
+            if (p < 0 || p >= a.cache_m) index_fault(err, p);
+            else rope_item(F, i, a.qkv, a.qkv_ld, a.pos, a.n_head, hd, (int)nd, 0, a.cos_sin, a.q_dst);
+        } else if (i < nq + nk) {
+            store_kv_item(F, i - nq, xk, a.qkv_ld, a.pos, a.n_head_kv, hd, (int)nd, a.cos_sin, (C *)a.k_cache,
+                          a.cache_m, a.k_slice, 0, a.seq, a.seq_stride, err);
+        } else {
+            store_kv_item(F, i - nq - nk, xv, a.qkv_ld, a.pos, a.n_head_kv, hd, 0, a.cos_sin, (C *)a.v_cache,
+                          a.cache_m, a.v_slice, 1, a.seq, a.seq_stride, err);
+        }
+    }
+}
+
+// ggml views on the device: element (i0, i1, i2, i3) at byte offset
+// i0 nb0 + i1 nb1 + i2 nb2 + i3 nb3, gathered into (or scattered from) a
+// contiguous F32 array in ggml element order.
+struct strided4 {
+    int64_t ne[4];
+    int64_t nb[4];
+};
+
+template <int SRC_HALF>
+__global__ void k_gather_f32(const char *__restrict__ src, strided4 g, float *__restrict__ dst) {
+    const int64_t n = g.ne[0] * g.ne[1] * g.ne[2] * g.ne[3];
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)blockDim.x * gridDim.x) {
+        int64_t r = i;
+        const int64_t i0 = r % g.ne[0];
+        r /= g.ne[0];
+        const int64_t i1 = r % g.ne[1];
+        r /= g.ne[1];
+        const int64_t i2 = r % g.ne[2], i3 = r / g.ne[2];
+        const char *p = src + i0 * g.nb[0] + i1 * g.nb[1] + i2 * g.nb[2] + i3 * g.nb[3];
+        dst[i] = SRC_HALF ? __half2float(*reinterpret_cast<const __half *>(p)) : *reinterpret_cast<const float *>(p);
+    }
+}
+
+__global__ void k_scatter_f32(const float *__restrict__ src, char *__restrict__ dst, strided4 g) {
+    const int64_t n = g.ne[0] * g.ne[1] * g.ne[2] * g.ne[3];
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)blockDim.x * gridDim.x) {
+        int64_t r = i;
+        const int64_t i0 = r % g.ne[0];
+        r /= g.ne[0];
+        const int64_t i1 = r % g.ne[1];
+        r /= g.ne[1];
+        const int64_t i2 = r % g.ne[2], i3 = r / g.ne[2];
+        *reinterpret_cast<float *>(dst + i0 * g.nb[0] + i1 * g.nb[1] + i2 * g.nb[2] + i3 * g.nb[3]) = src[i];
+    }
+}
+
 // ---- decode attention: KQ, soft_max and KQV of one token in one launch ------
 // head_dim up to which the KQV chain may stop at the last nonzero exp
 constexpr int k_attn_tail_hd = 256;
@@ -1888,7 +2129,58 @@ struct attn_args {
     float *dst;
     int hd, n_kv, rep;   // head_dim, cells, query heads per kv head
     uint32_t skew;       // added to the predicted soft_max total (0; a test hook sets it)
+    // The query rope and the current cell's cache stores folded in
+    // (lnship16_rope_attn_decode); qkv null: q holds the rotated queries and
+    // the caches hold the cell (lnship16_attn_decode)
+    const float *qkv;              // [n_head + 2 n_head_kv][hd] F32: the fused QKV product of the token
+    const int32_t *pos;            // [1] the token's position, device
+    const float *cos_sin;          // the rope table (lnship_rope_table layout)
+    int rope_n_dims, nh, nhkv;     // rotated dims; query and kv heads
+    unsigned long long *err;       // a position outside the cache is recorded here
 };
+
+// The rope of head h's query into xq (its xlns16 codes, through F32 as the
+// ROPE node writes them and the kq mul_mat converts them) and the stores of
+// kv head kv's rotated key and value of the current cell, exactly as
+// k_rope_store_kv makes them for one token.  Every query head of a kv group
+// stores that group's cell, with the same codes, before its chains read the
+// caches.  false (nothing done, the fault recorded) for a position outside
+// the cache.
+__device__ __forceinline__ bool attn_rope_store(const attn_args &a, const dev_tables &T, int h, int kv, uint16_t *xq) {
+    const fmt16 F{T};
+    const int hd = a.hd, nd = a.rope_n_dims, half = nd / 2;
+    const int64_t cache_m = a.k_gs / 8;
+    const int64_t p = a.pos[0];
+    if (p < 0 || p >= cache_m) {
+        if (threadIdx.x == 0) index_fault(a.err, p);
+        return false;
+    }
+    const float *xk = a.qkv + (int64_t)a.nh * hd, *xv = xk + (int64_t)a.nhkv * hd;
+    const int64_t ld = (int64_t)(a.nh + 2 * a.nhkv) * hd;
+    for (int i = threadIdx.x; i < 2 * hd; i += blockDim.x) {
+        if (i < hd)
+            store_kv_item(F, (int64_t)kv * hd + i, xk, ld, a.pos, a.nhkv, hd, nd, a.cos_sin,
+                          const_cast<uint16_t *>(a.k), cache_m, a.k_slice, 0, (const int32_t *)nullptr, 0, a.err);
+        else
+            store_kv_item(F, (int64_t)kv * hd + (i - hd), xv, ld, a.pos, a.nhkv, hd, 0, a.cos_sin,
+                          const_cast<uint16_t *>(a.v), cache_m, a.v_slice, 1, (const int32_t *)nullptr, 0, a.err);
+    }
+    const float *xr = a.qkv + (int64_t)h * hd, *cs = a.cos_sin + p * half * 2;
+    for (int j = threadIdx.x; j < half + (hd - nd); j += blockDim.x) {
+        if (j < half) {
+            int64_t i0, i1;
+            uint32_t r0, r1;
+            rope_pair(F, xr, j, nd, 0, cs, i0, i1, r0, r1);
+            xq[i0] = (uint16_t)F.from(F.to(r0));
+            xq[i1] = (uint16_t)F.from(F.to(r1));
+        } else {
+            const int i0 = nd + (j - half);
+            xq[i0] = (uint16_t)F.from(F.to(F.from(xr[i0])));
+        }
+    }
+    for (int k = hd + threadIdx.x; k < ((hd + 7) & ~7); k += blockDim.x) xq[k] = 0;
+    return true;
+}
 
 // Terms k0 <= k < k1 of one output of a GEMV over weights in the packed
 // layout (the row's groups of eight codes gs codes apart from w, the
@@ -2076,6 +2368,9 @@ __device__ __forceinline__ void row_chain(const red16<MODE> &R, typename red16<M
 template <int MODE>
 __global__ __launch_bounds__(k_block) void k_attn16(attn_args a, dev_tables T) {
     extern __shared__ __align__(16) char lds[];
+    bool idle;
+    const int h = attn_head(idle), kv = h / a.rep;
+    if (idle) return;
     const red16<MODE> R = stage_for<MODE, true>(T, lds);
     const int hd = a.hd, n = a.n_kv, hp = (hd + 7) & ~7, rs = (n + 7) & ~7;
     uint16_t *xq = reinterpret_cast<uint16_t *>(lds + mm_xl_offset<MODE>());   // the query's codes
@@ -2086,17 +2381,19 @@ __global__ __launch_bounds__(k_block) void k_attn16(attn_args a, dev_tables T) {
     __shared__ double s_part[k_block / 64];
     __shared__ int s_last;
     __shared__ uint32_t s_vmax[k_attn_tail_hd];   // per dim: the largest V log past the last nonzero exp
-    bool idle;
-    const int h = attn_head(idle), kv = h / a.rep;
-    if (idle) return;
     const bool tail_stop = hd <= k_attn_tail_hd;
     if (threadIdx.x == 0) {
         s_max = x16_canon(0xffffu);
         s_last = 0;
     }
     for (int d = threadIdx.x; d < k_attn_tail_hd; d += blockDim.x) s_vmax[d] = 0;
-    for (int k = threadIdx.x; k < hp; k += blockDim.x)
-        xq[k] = k < hd ? (uint16_t)x16_from_f32(T.cvt16, a.q[(int64_t)h * hd + k]) : (uint16_t)0;
+    if (a.qkv) {
+        // (the position is one value for the whole workgroup)
+        if (!attn_rope_store(a, T, h, kv, xq)) return;
+    } else {
+        for (int k = threadIdx.x; k < hp; k += blockDim.x)
+            xq[k] = k < hd ? (uint16_t)x16_from_f32(T.cvt16, a.q[(int64_t)h * hd + k]) : (uint16_t)0;
+    }
     __syncthreads();
     // the scores, and soft_max's first pass over them
     const uint32_t sc = x16_from_f32(T.cvt16, a.scale);
@@ -2341,6 +2638,9 @@ struct attn32_args {
 // KQV chains wait for it (no predicted start as in sum32).
 __global__ __launch_bounds__(k_block) void k_attn32(attn32_args a, dev_tables T) {
     extern __shared__ __align__(16) char lds[];
+    bool idle;
+    const int h = attn_head(idle), kv = h / a.rep;
+    if (idle) return;
     const red16<LNSHIP_SUM32> R = stage_for<LNSHIP_SUM32, true>(T, lds);
     const int hd = a.hd, n = a.n_kv, hp = (hd + 7) & ~7, rs = (n + 7) & ~7;
     uint32_t *xq = reinterpret_cast<uint32_t *>(lds + k_lds_tab32);   // the query's codes
@@ -2349,9 +2649,6 @@ __global__ __launch_bounds__(k_block) void k_attn32(attn32_args a, dev_tables T)
     __shared__ int32_t s_max;
     __shared__ uint32_t s_tot;
     __shared__ int s_last;
-    bool idle;
-    const int h = attn_head(idle), kv = h / a.rep;
-    if (idle) return;
     if (threadIdx.x == 0) {
         s_max = x32_canon(0xffffffffu);
         s_last = 0;
@@ -2484,247 +2781,6 @@ __global__ __launch_bounds__(k_block) void k_softmax32(sm_args a, dev_tables T) 
     for (int64_t e = threadIdx.x; e < ne; e += blockDim.x) {
         const int r = (int)(e / a.n);
         a.dst[r0 * a.n + e] = x32_to_f32(x32_div(c[e + r * (rs - a.n)], s_tot[r]));
-    }
-}
-
-// ---- elementwise ops of the Llama graph ---------------------------------------
-
-// The elementwise ops in either format: fmt16 (xlns16 through the
-// conversion, decode, Gaussian-log and sigmoid tables) or fmt32 (xlns32,
-// converted arithmetically, adder over the global xlns32 tables).
-struct fmt16 {
-    using code_t = uint16_t;
-    const dev_tables &T;
-    __device__ __forceinline__ uint32_t from(float v) const { return x16_from_f32(T.cvt16, v); }
-    __device__ __forceinline__ float to(uint32_t c) const { return T.rev16[c]; }
-    __device__ __forceinline__ uint32_t add(uint32_t x, uint32_t y) const { return x16_add_g(T.gauss16, x, y); }
-    __device__ __forceinline__ uint32_t mul(uint32_t x, uint32_t y) const { return x16_mul(x, y); }
-    __device__ __forceinline__ uint32_t neg(uint32_t x) const { return x ^ k16_sign; }
-    // xlns16_silu: x times the table sigmoid of x
-    __device__ __forceinline__ uint32_t silu(uint32_t x) const { return x16_mul(x, T.sig16[x]); }
-};
-struct fmt32 {
-    using code_t = uint32_t;
-    const dev_tables &T;
-    __device__ __forceinline__ uint32_t from(float v) const { return x32_from_f32(v); }
-    __device__ __forceinline__ float to(uint32_t c) const { return x32_to_f32(c); }
-    __device__ __forceinline__ uint32_t add(uint32_t x, uint32_t y) const { return x32_add(T.tab32, x, y); }
-    __device__ __forceinline__ uint32_t mul(uint32_t x, uint32_t y) const { return x32_mul(x, y); }
-    __device__ __forceinline__ uint32_t neg(uint32_t x) const { return x ^ k32_sign; }
-    // xlns32_silu: x times the sigmoid of its value, the sigmoid formed in
-    // double and rounded to float (libm-independent at float precision)
-    __device__ __forceinline__ uint32_t silu(uint32_t x) const {
-        const double v = (double)x32_to_f32(x);
-        return x32_mul(x, x32_from_f32((float)(1.0 / (1.0 + exp(-v)))));
-    }
-};
-template <int W>
-using fmt_t = typename std::conditional<W == 16, fmt16, fmt32>::type;
-
-template <int W, int OP>   // OP 0 add, 1 mul
-__global__ void k_binary(const float *__restrict__ a, const float *__restrict__ b, int64_t n, int64_t nb,
-                         float *__restrict__ dst, dev_tables T) {
-    const fmt_t<W> F{T};
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)blockDim.x * gridDim.x) {
-        const uint32_t x = F.from(a[i]), y = F.from(b[i % nb]);
-        dst[i] = F.to(OP == 0 ? F.add(x, y) : F.mul(x, y));
-    }
-}
-
-template <int W>
-__global__ void k_swiglu(const float *__restrict__ g, int64_t g_ld, const float *__restrict__ u, int64_t u_ld,
-                         float *__restrict__ dst, int64_t ncols, int64_t nrows, dev_tables T) {
-    const fmt_t<W> F{T};
-    const int64_t n = ncols * nrows;
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)blockDim.x * gridDim.x) {
-        const int64_t r = i / ncols, c = i - r * ncols;
-        const uint32_t gv = F.from(g[r * g_ld + c]);
-        const uint32_t uv = F.from(u[r * u_ld + c]);
-        dst[i] = F.to(F.mul(F.silu(gv), uv));
-    }
-}
-
-// y = x s (+ b when b is not zero), in the format's arithmetic
-template <int W>
-__global__ void k_scale(const float *__restrict__ src, float *__restrict__ dst, int64_t n, float s, float b,
-                        dev_tables T) {
-    const fmt_t<W> F{T};
-    const uint32_t sc = F.from(s), bc = F.from(b);
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)blockDim.x * gridDim.x) {
-        uint32_t v = F.mul(F.from(src[i]), sc);
-        if (b != 0.0f) v = F.add(v, bc);
-        dst[i] = F.to(v);
-    }
-}
-
-__global__ void k_get_rows_packed(const uint16_t *__restrict__ w, int64_t K, int64_t M, const int32_t *__restrict__ rows,
-                                  int64_t nrows, float *__restrict__ dst, const float *__restrict__ rev) {
-    const int64_t n = nrows * K;
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)blockDim.x * gridDim.x) {
-        const int64_t r = i / K, k = i - r * K;
-        const int64_t m = rows[r];
-        dst[i] = rev[w[((k >> 3) * M + m) * 8 + (k & 7)]];
-    }
-}
-
-// one thread per rotated pair (or passthrough element)
-template <class F>
-__device__ __forceinline__ void rope_pair(const F &f, const float *xr, int64_t j, int n_dims, int neox, const float *cs,
-                                          int64_t &i0, int64_t &i1, uint32_t &r0, uint32_t &r1) {
-    const uint32_t c = f.from(cs[j * 2]), sn = f.from(cs[j * 2 + 1]);
-    i0 = neox ? j : 2 * j;
-    i1 = neox ? j + n_dims / 2 : 2 * j + 1;
-    const uint32_t x0 = f.from(xr[i0]), x1 = f.from(xr[i1]);
-    r0 = f.add(f.mul(x0, c), f.neg(f.mul(x1, sn)));
-    r1 = f.add(f.mul(x0, sn), f.mul(x1, c));
-}
-
-// item i of a rope: a rotated pair (j < n_dims / 2) or a passthrough element
-// of row (token, head); ntok * nhead * (n_dims / 2 + ne0 - n_dims) items
-template <class F>
-__device__ __forceinline__ void rope_item(const F &f, int64_t i, const float *x, int64_t x_ld, const int32_t *pos,
-                                          int64_t nhead, int64_t ne0, int n_dims, int neox, const float *cos_sin,
-                                          float *dst) {
-    const int64_t half = n_dims / 2, per = half + (ne0 - n_dims);
-    const int64_t row = i / per, j = i - row * per;
-    const int64_t t = row / nhead, h = row - t * nhead;
-    const float *xr = x + t * x_ld + h * ne0;
-    float *yr = dst + (t * nhead + h) * ne0;
-    if (j < half) {
-        int64_t i0, i1;
-        uint32_t r0, r1;
-        rope_pair(f, xr, j, n_dims, neox, cos_sin + (int64_t)pos[t] * half * 2, i0, i1, r0, r1);
-        yr[i0] = f.to(r0);
-        yr[i1] = f.to(r1);
-    } else {
-        const int64_t i0 = n_dims + (j - half);
-        yr[i0] = f.to(f.from(xr[i0]));
-    }
-}
-
-template <int W>
-__global__ void k_rope(const float *__restrict__ x, int64_t x_ld, const int32_t *__restrict__ pos, int64_t ntok,
-                       int64_t nhead, int64_t ne0, int n_dims, int neox, const float *__restrict__ cos_sin,
-                       float *__restrict__ dst, dev_tables T) {
-    const fmt_t<W> F{T};
-    const int64_t n = ntok * nhead * (n_dims / 2 + (ne0 - n_dims));
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)blockDim.x * gridDim.x)
-        rope_item(F, i, x, x_ld, pos, nhead, ne0, n_dims, neox, cos_sin, dst);
-}
-
-// F32 value -> IEEE half (round to nearest even) -> F32 -> LNS, as the KV
-// cache stores and reads it
-// item i (element (token, head, d)) of a KV-cache store;
-// ntok * nhead * ne0 items
-// A position outside the cache's cache_m rows is recorded (err, as an index
-// out of range) and its item is skipped: nothing is read from the rope
-// table or written to the cache for it.
-template <class F, class C>
-__device__ __forceinline__ void store_kv_item(const F &f, int64_t i, const float *x, int64_t x_ld, const int32_t *pos,
-                                              int64_t nhead, int64_t ne0, int rope_n_dims, const float *cos_sin,
-                                              C *cache, int64_t cache_m, int64_t cache_slice, int transposed,
-                                              const int32_t *seq, int64_t seq_stride, unsigned long long *err) {
-    const int64_t half = rope_n_dims / 2;
-    const int64_t row = i / ne0, d = i - row * ne0;
-    const int64_t t = row / nhead, h = row - t * nhead;
-    const float *xr = x + t * x_ld + h * ne0;
-    const int64_t p = pos[t];
-    if (p < 0 || p >= cache_m) {
-        index_fault(err, p);
-        return;
-    }
-    float v;
-    if (rope_n_dims > 0 && d < rope_n_dims) {
-        // normal rope: element d belongs to pair d / 2
-        int64_t i0, i1;
-        uint32_t r0, r1;
-        rope_pair(f, xr, d / 2, rope_n_dims, 0, cos_sin + p * half * 2, i0, i1, r0, r1);
-        v = f.to((d & 1) ? r1 : r0);
-    } else if (rope_n_dims > 0) {
-        v = f.to(f.from(xr[d]));
-    } else {
-        v = xr[d];
-    }
-    const int64_t o = transposed ? h * cache_slice + ((p >> 3) * ne0 + d) * 8 + (p & 7)
-                                 : h * cache_slice + ((d >> 3) * cache_m + p) * 8 + (d & 7);
-    cache[(seq ? (int64_t)seq[t] * seq_stride : 0) + o] = (C)f.from(__half2float(__float2half_rn(v)));
-}
-
-template <int W>
-__global__ void k_store_kv(const float *__restrict__ x, int64_t x_ld, const int32_t *__restrict__ pos, int64_t ntok,
-                           int64_t nhead, int64_t ne0, int rope_n_dims, const float *__restrict__ cos_sin,
-                           typename fmt_t<W>::code_t *__restrict__ cache, int64_t cache_m, int64_t cache_slice,
-                           int transposed, const int32_t *__restrict__ seq, int64_t seq_stride, dev_tables T,
-                           unsigned long long *err) {
-    const fmt_t<W> F{T};
-    const int64_t n = ntok * nhead * ne0;
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)blockDim.x * gridDim.x)
-        store_kv_item(F, i, x, x_ld, pos, nhead, ne0, rope_n_dims, cos_sin, cache, cache_m, cache_slice, transposed,
-                      seq, seq_stride, err);
-}
-
-// The query rope and the key / value cache stores after a fused QKV
-// mul_mat, as one grid: items [0, nq) rope the query heads, the next nk
-// store the (rotated) key heads, the last nk the value heads.
-template <int W>
-__global__ void k_rope_store_kv(lnship_qkv_store_args a, dev_tables T, unsigned long long *err) {
-    using C = typename fmt_t<W>::code_t;
-    const fmt_t<W> F{T};
-    const int64_t hd = a.head_dim, nd = a.rope_n_dims;
-    const int64_t nq = a.ntok * a.n_head * (nd / 2 + (hd - nd)), nk = a.ntok * a.n_head_kv * hd;
-    const float *xk = a.qkv + a.n_head * hd, *xv = xk + a.n_head_kv * hd;
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < nq + 2 * nk;
-         i += (int64_t)blockDim.x * gridDim.x) {
-        if (i < nq) {
-            // the rope table has cache_m rows: a query beyond them is recorded
-            // and skipped, like the cache stores
-            const int64_t t = i / (a.n_head * (nd / 2 + (hd - nd)));
-            const int64_t p = a.pos[t];
-            if (p < 0 || p >= a.cache_m) index_fault(err, p);
-            else rope_item(F, i, a.qkv, a.qkv_ld, a.pos, a.n_head, hd, (int)nd, 0, a.cos_sin, a.q_dst);
-        } else if (i < nq + nk) {
-            store_kv_item(F, i - nq, xk, a.qkv_ld, a.pos, a.n_head_kv, hd, (int)nd, a.cos_sin, (C *)a.k_cache,
-                          a.cache_m, a.k_slice, 0, a.seq, a.seq_stride, err);
-        } else {
-            store_kv_item(F, i - nq - nk, xv, a.qkv_ld, a.pos, a.n_head_kv, hd, 0, a.cos_sin, (C *)a.v_cache,
-                          a.cache_m, a.v_slice, 1, a.seq, a.seq_stride, err);
-        }
-    }
-}
-
-// ggml views on the device: element (i0, i1, i2, i3) at byte offset
-// i0 nb0 + i1 nb1 + i2 nb2 + i3 nb3, gathered into (or scattered from) a
-// contiguous F32 array in ggml element order.
-struct strided4 {
-    int64_t ne[4];
-    int64_t nb[4];
-};
-
-template <int SRC_HALF>
-__global__ void k_gather_f32(const char *__restrict__ src, strided4 g, float *__restrict__ dst) {
-    const int64_t n = g.ne[0] * g.ne[1] * g.ne[2] * g.ne[3];
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)blockDim.x * gridDim.x) {
-        int64_t r = i;
-        const int64_t i0 = r % g.ne[0];
-        r /= g.ne[0];
-        const int64_t i1 = r % g.ne[1];
-        r /= g.ne[1];
-        const int64_t i2 = r % g.ne[2], i3 = r / g.ne[2];
-        const char *p = src + i0 * g.nb[0] + i1 * g.nb[1] + i2 * g.nb[2] + i3 * g.nb[3];
-        dst[i] = SRC_HALF ? __half2float(*reinterpret_cast<const __half *>(p)) : *reinterpret_cast<const float *>(p);
-    }
-}
-
-__global__ void k_scatter_f32(const float *__restrict__ src, char *__restrict__ dst, strided4 g) {
-    const int64_t n = g.ne[0] * g.ne[1] * g.ne[2] * g.ne[3];
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)blockDim.x * gridDim.x) {
-        int64_t r = i;
-        const int64_t i0 = r % g.ne[0];
-        r /= g.ne[0];
-        const int64_t i1 = r % g.ne[1];
-        r /= g.ne[1];
-        const int64_t i2 = r % g.ne[2], i3 = r / g.ne[2];
-        *reinterpret_cast<float *>(dst + i0 * g.nb[0] + i1 * g.nb[1] + i2 * g.nb[2] + i3 * g.nb[3]) = src[i];
     }
 }
 
@@ -3887,13 +3943,14 @@ int lnship16_soft_max(int mode, const lnship_soft_max_args *a, void *stream) {
     }
 }
 
-int lnship16_attn_decode(int mode, const lnship_attn_args *a, void *stream) {
-    // arguments and sizes first: they need no device
+// the arguments of an LNS16 decode attention, checked before any device call
+// (need_q: q is read; the fused rope forms it instead)
+static int attn16_check(int mode, const lnship_attn_args *a, bool need_q) {
     if (!a) return fail(LNSHIP_EINVAL, "attn_decode: null args%s");
     if (mode == LNSHIP_MONTE)
         return fail(LNSHIP_EINVAL, "attn_decode: Monte draws run across the three nodes in graph order; run them%s");
     if (mode < 0 || mode > 3) return fail(LNSHIP_EINVAL, "unknown summation mode%s");
-    if (!a->q || !a->k_cache || !a->v_cache || !a->dst || a->n_head <= 0 || a->n_head_kv <= 0 ||
+    if ((need_q && !a->q) || !a->k_cache || !a->v_cache || !a->dst || a->n_head <= 0 || a->n_head_kv <= 0 ||
         a->n_head % a->n_head_kv || a->head_dim <= 0 || a->n_kv <= 0 || a->cache_m < a->n_kv ||
         a->head_dim > 4096 || a->n_head > 65535)
         return fail(LNSHIP_EINVAL, "attn_decode: bad argument%s");
@@ -3901,18 +3958,46 @@ int lnship16_attn_decode(int mode, const lnship_attn_args *a, void *stream) {
     // the limit above holds for head_dim <= 256; wider heads need more LDS
     if ((int64_t)attn16_lds_mode(mode, a->head_dim, a->n_kv) > k_lds_bytes - k_lds_static)
         return fail(LNSHIP_ERANGE, "attn_decode: head_dim x n_kv too large for LDS%s");
+    return 0;
+}
+
+static int attn16_launch(int mode, const attn_args &m, int64_t nh, const dev_tables &T, hipStream_t st) {
+    switch (mode) {
+        case LNSHIP_BASE: return launch_attn16<LNSHIP_BASE>(m, nh, T, st);
+        case LNSHIP_LPVIP: return launch_attn16<LNSHIP_LPVIP>(m, nh, T, st);
+        default: return launch_attn16<LNSHIP_SUM32>(m, nh, T, st);
+    }
+}
+
+int lnship16_attn_decode(int mode, const lnship_attn_args *a, void *stream) {
+    // arguments and sizes first: they need no device
+    if (int rc = attn16_check(mode, a, true)) return rc;
     device_state *s = state();
     if (!s) return LNSHIP_ENOINIT;
     const attn_args m{a->q, (const uint16_t *)a->k_cache, (const uint16_t *)a->v_cache, a->cache_m * 8, a->k_slice,
                       a->head_dim * 8, a->v_slice,
                       a->mask, a->scale, a->dst, (int)a->head_dim, (int)a->n_kv, (int)(a->n_head / a->n_head_kv),
                       g_predict_skew};
-    hipStream_t st = (hipStream_t)stream;
-    switch (mode) {
-        case LNSHIP_BASE: return launch_attn16<LNSHIP_BASE>(m, a->n_head, s->T, st);
-        case LNSHIP_LPVIP: return launch_attn16<LNSHIP_LPVIP>(m, a->n_head, s->T, st);
-        default: return launch_attn16<LNSHIP_SUM32>(m, a->n_head, s->T, st);
-    }
+    return attn16_launch(mode, m, a->n_head, s->T, (hipStream_t)stream);
+}
+
+int lnship16_rope_attn_decode(int mode, const lnship_qkv_store_args *q, const lnship_attn_args *a, void *stream) {
+    // arguments and sizes first: they need no device
+    if (int rc = attn16_check(mode, a, false)) return rc;
+    if (!q || !q->qkv || !q->pos || !q->cos_sin || q->ntok != 1 || q->seq || q->n_head != a->n_head ||
+        q->n_head_kv != a->n_head_kv || q->head_dim != a->head_dim || q->head_dim % 8 || q->rope_n_dims <= 0 ||
+        q->rope_n_dims % 2 || q->rope_n_dims > q->head_dim ||
+        q->qkv_ld < (q->n_head + 2 * q->n_head_kv) * q->head_dim || q->k_cache != a->k_cache ||
+        q->v_cache != a->v_cache || q->cache_m != a->cache_m || q->k_slice != a->k_slice || q->v_slice != a->v_slice)
+        return fail(LNSHIP_EINVAL, "rope_attn_decode: the store arguments do not match the attention's%s");
+    device_state *s = state();
+    if (!s) return LNSHIP_ENOINIT;
+    const attn_args m{nullptr, (const uint16_t *)a->k_cache, (const uint16_t *)a->v_cache, a->cache_m * 8,
+                      a->k_slice, a->head_dim * 8, a->v_slice,
+                      a->mask, a->scale, a->dst, (int)a->head_dim, (int)a->n_kv, (int)(a->n_head / a->n_head_kv),
+                      g_predict_skew, q->qkv, q->pos, q->cos_sin, q->rope_n_dims, (int)a->n_head,
+                      (int)a->n_head_kv, s->index_err};
+    return attn16_launch(mode, m, a->n_head, s->T, (hipStream_t)stream);
 }
 
 int lnship32_attn_decode(const lnship_attn_args *a, void *stream) {

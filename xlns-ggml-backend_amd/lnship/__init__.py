@@ -99,6 +99,8 @@ def lib():
         "lnship16_swiglu_mul_mat": (ctypes.c_int, [ctypes.c_int, c_p, c_p, c_p, c_p, c_p, c_i64, c_i64, c_p]),
         "lnship16_rope_store_kv": (ctypes.c_int, [ctypes.POINTER(QkvStoreArgs), c_p]),
         "lnship16_attn_decode": (ctypes.c_int, [ctypes.c_int, ctypes.POINTER(AttnArgs), c_p]),
+        "lnship16_rope_attn_decode": (ctypes.c_int, [ctypes.c_int, ctypes.POINTER(QkvStoreArgs),
+                                                     ctypes.POINTER(AttnArgs), c_p]),
         "lnship32_attn_decode": (ctypes.c_int, [ctypes.POINTER(AttnArgs), c_p]),
         "lnship_max_row": (c_i64, [ctypes.c_int, ctypes.c_int]),
         "lnship32_rope_store_kv": (ctypes.c_int, [ctypes.POINTER(QkvStoreArgs), c_p]),

@@ -119,6 +119,9 @@ class LlamaLNS16:
         self.torch = torch
         # decode attention in one launch where the op takes the mode and the cells
         self.fused_attn = mode != MONTE
+        # and with it, the query rope and the cache stores of the token
+        # (lnship16_rope_attn_decode, bit-identical to the two launches)
+        self.fused_rope = True
         # sum32, one row: rms_norm, the norm MUL and the mul_mat after them in
         # one launch (lnship16_rms_norm_mul_mat, bit-identical to the three),
         # where the row fits the kernel's LDS
@@ -293,8 +296,13 @@ class LlamaLNS16:
         check(lib().lnship16_swiglu_mul_mat(self.mode, gate_ptr, up_ptr, ctypes.c_void_p(w), resid_ptr, dst_ptr, K, M,
                                             self._stream))
 
-    def _attn(self, args):
-        check(lib().lnship16_attn_decode(self.mode, ctypes.byref(args), self._stream))
+    def _attn(self, args, store=None):
+        """The decode attention; with store (the token's rope and cache
+        stores), the two in one launch."""
+        if store is None:
+            check(lib().lnship16_attn_decode(self.mode, ctypes.byref(args), self._stream))
+        else:
+            check(lib().lnship16_rope_attn_decode(self.mode, ctypes.byref(store), ctypes.byref(args), self._stream))
 
     # -- forward -------------------------------------------------------------------
     def forward(self, T, tokens_dev, pos_dev, n_kv, seq=0, batch=False):
@@ -335,13 +343,16 @@ class LlamaLNS16:
             qs = QkvStoreArgs(P(qkv), nqkv, P(pos_dev), T, nh, nkv, hd, hd, P(self.cos_sin), P(q),
                               P(self.kcache[il], cbase), P(self.vcache[il], cbase), c.n_ctx, self.kslice,
                               self.vslice, seq_ids, self.seq_stride)
-            check(L.lnship16_rope_store_kv(ctypes.byref(qs), st))
             Tq = 1 if batch else T   # query rows per sequence
-            if T == 1 and not batch and self.fused_attn and n_kv <= self._attn_max_kv:
-                # the three nodes below in one launch, bit for bit
+            fused = T == 1 and not batch and self.fused_attn and n_kv <= self._attn_max_kv
+            if not (fused and self.fused_rope):
+                check(L.lnship16_rope_store_kv(ctypes.byref(qs), st))
+            if fused:
+                # the three nodes below in one launch, bit for bit (and the
+                # rope and cache stores above it, with fused_rope)
                 self._attn(AttnArgs(P(q), P(self.kcache[il], cbase), P(self.vcache[il], cbase), c.n_ctx,
                                     self.kslice, self.vslice, P(mask), 1.0 / math.sqrt(hd), P(att), nh, nkv, hd,
-                                    n_kv))
+                                    n_kv), qs if self.fused_rope else None)
             else:
                 # kq[s][h][t][j] = K_s,j . q_s,t (GQA: query head h reads kv head h / (nh / nkv))
                 self._mm(self.kcache[il].data_ptr() + 2 * cbase, P(q), P(kq), hd, n_kv, Tq, ne02=nkv, ne03=nseq,
