@@ -393,6 +393,56 @@ def test_rms_norm_mul_lns32(ln):
         same_bits(host(out), want, f"rms_norm_mul lns32 {shape}")
 
 
+def _narrow_cases(rng):
+    """(name, K, M, weights, activations) for the one-column sum32 GEMV"""
+    cases = []
+    for K, M in ((576, 576), (1536, 576), (576, 1000), (13, 37), (1, 5)):
+        cases.append((f"N(0,0.02) K={K} M={M}", K, M, (rng.standard_normal((M, K)) * 0.02).astype(np.float32),
+                      rng.standard_normal(K).astype(np.float32)))
+    K, M = 700, 96
+    # magnitudes over 2^-60 .. 2^60 (every grid: near, far, past the
+    # essential zero), zeros among them
+    w = (rng.standard_normal((M, K)) * np.exp2(rng.uniform(-60, 60, (M, K)))).astype(np.float32)
+    w[:, ::17] = 0.0
+    cases.append(("wide range", K, M, w, (rng.standard_normal(K) * np.exp2(rng.uniform(-20, 20, K))).astype(np.float32)))
+    # exact and near cancellations: pairs of equal terms of opposite signs
+    x = rng.standard_normal(K).astype(np.float32)
+    x[1::2] = -x[0::2]
+    w2 = np.repeat((rng.standard_normal((M, K // 2)) * 0.5).astype(np.float32), 2, axis=1)
+    w2[:, 1::4] *= np.float32(1.01)
+    cases.append(("cancellations", K, M, w2, x))
+    # one sign: only sb
+    cases.append(("positive", K, M, np.abs(rng.standard_normal((M, K))).astype(np.float32),
+                  np.abs(rng.standard_normal(K)).astype(np.float32)))
+    return cases
+
+
+@pytest.mark.parametrize("width", [0, 16])
+def test_sum32_gemv_narrow_waves(ln, width):
+    # the one-column sum32 GEMV with 16 rows per wave (the default) and with
+    # 64 (width 0) against the oracle, plain and with the residual ADD, on
+    # shapes and values that reach every table of the adder (the decoder
+    # tests run the default width, the swiglu prologue included)
+    L = ln.lib()
+    rng = np.random.default_rng(4242)
+    prev = L.lnship_test_decode_width(width)
+    try:
+        for name, K, M, w, x in _narrow_cases(rng):
+            print(f"\n[sum32 gemv] width={width} {name}", flush=True)
+            wp = ln.pack16(dev(w))
+            want = O.mul_mat16_f32w(O.SUM32, w[None, None], x[None, None, None])[0, 0, 0]
+            got = host(ln.mul_mat16(O.SUM32, wp, dev(x[None]), K, M))
+            same_bits(got.reshape(-1), want, f"width {width} {name}")
+            r = rng.standard_normal(M).astype(np.float32)
+            acc = dev(r)
+            ln.mul_mat16_raw(O.SUM32, wp.data_ptr(), dev(x[None]).data_ptr(), acc.data_ptr(), K, M, 1,
+                             residual=acc.data_ptr())
+            same_bits(host(acc), _elementwise16(O.lib().lno16_add, want[None], r[None])[0],
+                      f"width {width} {name} residual")
+    finally:
+        L.lnship_test_decode_width(prev)
+
+
 @pytest.mark.parametrize("mode", MODES + ["lns32"])
 def test_mul_mat_residual(ln, mode):
     # the ADD after a mul_mat fused into it, in place (dst = residual), as

@@ -1141,7 +1141,11 @@ __device__ __forceinline__ void mm16_chains(const mm_args16 &a, const dev_tables
     for (int j = 0; j < NC; j++) res[j] = R.finish(acc[j]) & 0xffffu;
 }
 
-template <int MODE, int NC, int PF, bool XL, int CG>
+// W < 64: W rows per wave, the wave's other lanes only staging the tables
+// and the activations (the one-column sum32 GEMV, whose chains are bound by
+// dependent latency: a VALU instruction with only the first 16 lanes active
+// completes sooner, and the step with it)
+template <int MODE, int NC, int PF, bool XL, int CG, int W = 64>
 __global__ __launch_bounds__(k_block * CG) void k_mm16(mm_args16 a, dev_tables T) {
     extern __shared__ __align__(16) char lds[];
     // a widened launch: the workgroups between the working ones leave at once
@@ -1208,8 +1212,10 @@ __global__ __launch_bounds__(k_block * CG) void k_mm16(mm_args16 a, dev_tables T
     }
     __syncthreads();
 
-    const int64_t m = (int64_t)(blockIdx.x >> a.xcd_sh) * k_block + (threadIdx.x % k_block);
-    if (m >= a.M || nc == 0 || !slice_ok) return;
+    const int lane = (int)(threadIdx.x & 63u);
+    const int64_t m = W < 64 ? (int64_t)(blockIdx.x >> a.xcd_sh) * (k_block / 64 * W) + (threadIdx.x >> 6) * W + lane
+                             : (int64_t)(blockIdx.x >> a.xcd_sh) * k_block + (threadIdx.x % k_block);
+    if ((W < 64 && lane >= W) || m >= a.M || nc == 0 || !slice_ok) return;
     float *ds = a.dst + z * a.dst_slice + n0 * a.dst_ld + m;
     // output j, with the fused ADD of the residual when there is one: the
     // F32 result and the residual through xlns16, added, back to F32 (the
@@ -1630,7 +1636,9 @@ __global__ __launch_bounds__(k_block) void k_rms32(const float *__restrict__ src
 // of the three nodes in every case.
 constexpr int k_rms_mm_rows = 3 * 64;   // chain lanes per workgroup (waves 0-2; wave 3 sums)
 
-template <int PF>
+// W: rows per chain wave (64, or 16 with the other lanes idle during the
+// chains, as in k_mm16)
+template <int PF, int W = 64>
 __global__ __launch_bounds__(k_block) void k_mm16_rms(mm_args16 a, dev_tables T) {
     static_assert(k_block == k_rms_mm_rows + 64, "three chain waves and the sum's wave");
     extern __shared__ __align__(16) char lds[];
@@ -1687,8 +1695,9 @@ __global__ __launch_bounds__(k_block) void k_mm16_rms(mm_args16 a, dev_tables T)
     uint32_t inv = s_inv[0];
     stage_h(inv);
     __syncthreads();
-    const int64_t m = (int64_t)(blockIdx.x >> a.xcd_sh) * k_rms_mm_rows + threadIdx.x;
-    const bool active = threadIdx.x < k_rms_mm_rows && m < a.M;
+    const int lane = (int)(threadIdx.x & 63u);
+    const int64_t m = (int64_t)(blockIdx.x >> a.xcd_sh) * (3 * W) + (threadIdx.x >> 6) * W + lane;
+    const bool active = threadIdx.x < k_rms_mm_rows && lane < W && m < a.M;
     uint32_t res[1] = {0};
     // pass 0 with the predicted scale; a second pass only when the chain's
     // scale differs (every thread reads the same two words after the barrier)
@@ -3046,6 +3055,10 @@ static mm16_shape mm_shape_x32(int64_t M, int64_t N, int64_t nslices, int64_t kp
 // is a multiple of 2^sh working, the working ones fall on 8 >> sh XCDs and
 // share those L2s' copies.  sh is the largest (at most 3) for which those
 // XCDs still hold every working workgroup at one per CU.
+// Rows per wave of the one-column sum32 GEMVs: 16, or 0 for 64-row waves;
+// lnship_test_decode_width sets it
+static int g_decode_w = 16;
+
 // the grid of nh attention heads placed by attn_head: every block up to the
 // last head's, the multiples of 8 idle
 static unsigned attn_grid(int64_t nh) { return (unsigned)(nh + 1 + (nh - 1) / 7); }
@@ -3063,7 +3076,7 @@ static mm16_shape mm16_choose(int mode, int64_t M, int64_t N, int64_t nslices, i
     return {nc, 1, mm16_xl(mode, nc, kp)};
 }
 
-template <int MODE, int NC, bool XL, int CG>
+template <int MODE, int NC, bool XL, int CG, int W = 64>
 static int launch_mm16(const mm_args16 &m, const dev_tables &T, int64_t nslices, int cus, hipStream_t st) {
     // prefetch depth within 128 VGPRs at four waves per SIMD
     constexpr int PF = NC == 1 ? (CG >= 4 ? 4 : 8) : NC == 2 ? 2 : (NC == 4 && CG < 4) ? 2 : 1;
@@ -3073,13 +3086,14 @@ static int launch_mm16(const mm_args16 &m, const dev_tables &T, int64_t nslices,
     if ((uint64_t)m.w_mstride * 16 * PF + (uint64_t)m.M * 16 > 0xffffffffu)
         return fail(LNSHIP_ERANGE, "mul_mat: weight rows too long for 32-bit block offsets%s");
     if (lds > 64 * 1024)
-        if (int rc = set_lds(k_mm16<MODE, NC, PF, XL, CG>, lds)) return rc;
-    dim3 grid((unsigned)((m.M + k_block - 1) / k_block), (unsigned)((m.N + NC * CG - 1) / (NC * CG)), (unsigned)nslices);
+        if (int rc = set_lds(k_mm16<MODE, NC, PF, XL, CG, W>, lds)) return rc;
+    constexpr int rows = W < 64 ? k_block / 64 * W : k_block;   // rows per workgroup
+    dim3 grid((unsigned)((m.M + rows - 1) / rows), (unsigned)((m.N + NC * CG - 1) / (NC * CG)), (unsigned)nslices);
     if (grid.x > 2147483647u || grid.y > 65535u) return fail(LNSHIP_ERANGE, "mul_mat: grid too large%s");
     mm_args16 mx = m;
     mx.xcd_sh = MODE == LNSHIP_SUM32 ? xcd_shift((uint64_t)grid.x * grid.y * grid.z, cus) : 0;
     grid.x <<= mx.xcd_sh;
-    hipLaunchKernelGGL((k_mm16<MODE, NC, PF, XL, CG>), grid, dim3(k_block * CG), lds, st, mx, T);
+    hipLaunchKernelGGL((k_mm16<MODE, NC, PF, XL, CG, W>), grid, dim3(k_block * CG), lds, st, mx, T);
     LNSHIP_HIP(hipGetLastError());
     return 0;
 }
@@ -3101,7 +3115,12 @@ static int dispatch_mm16(const mm_args16 &m, const dev_tables &T, int64_t nslice
             case 24: return launch_mm16_x<MODE, 2, 4>(m, T, nslices, sh.xl, cus, st);
             case 44: return launch_mm16_x<MODE, 4, 4>(m, T, nslices, sh.xl, cus, st);
             case 84: return launch_mm16_x<MODE, 8, 4>(m, T, nslices, sh.xl, cus, st);
-            default: return launch_mm16_x<MODE, 1, 1>(m, T, nslices, sh.xl, cus, st);
+            default:
+                // one column: 16-row waves while they fill at most one wave
+                // slot per SIMD
+                if (sh.xl && m.N == 1 && g_decode_w == 16 && m.M * nslices <= (int64_t)cus * 4 * 16)
+                    return launch_mm16<MODE, 1, true, 1, 16>(m, T, nslices, cus, st);
+                return launch_mm16_x<MODE, 1, 1>(m, T, nslices, sh.xl, cus, st);
         }
     } else {
         switch (sh.nc) {
@@ -3860,6 +3879,12 @@ int lnship16_rms_norm_mul(int mode, const float *src, const float *w, float *dst
 // k_attn16's soft_max total): lnship_test_predict_skew
 static uint32_t g_predict_skew = 0;
 
+int lnship_test_decode_width(int w) {
+    const int prev = g_decode_w;
+    if (w == 0 || w == 16) g_decode_w = w;
+    return prev;
+}
+
 int lnship_test_predict_skew(int skew) {
     const int prev = (int)g_predict_skew;
     g_predict_skew = (uint32_t)skew;
@@ -3881,16 +3906,23 @@ int lnship16_rms_norm_mul_mat(int mode, const float *x, const float *norm_w, flo
     if (lds > k_lds_bytes - 1024) return fail(LNSHIP_ERANGE, "rms_norm_mul_mat: row too long for LDS%s");
     if ((uint64_t)M * 16 * PF + (uint64_t)M * 16 > 0xffffffffu)
         return fail(LNSHIP_ERANGE, "rms_norm_mul_mat: weight rows too long for 32-bit block offsets%s");
-    if (int rc = set_lds(k_mm16_rms<PF>, (int)lds)) return rc;
+    // 16-row chain waves while every workgroup still gets a CU of its own
+    const bool narrow = g_decode_w == 16 && M <= (int64_t)s->cus * 3 * 16;
+    if (int rc = narrow ? set_lds(k_mm16_rms<PF, 16>, (int)lds) : set_lds(k_mm16_rms<PF>, (int)lds)) return rc;
     mm_args16 m{(const uint16_t *)w, nullptr, x, dst, K, kp, M, 1, K, K, 1, 1, 1, 1, M, kp * M, M, M, 0, nullptr, 0};
     m.norm = norm_w;
     m.eps = eps;
     m.skew = g_predict_skew;
-    const uint64_t wgs = (uint64_t)((M + k_rms_mm_rows - 1) / k_rms_mm_rows);
+    const int rows = narrow ? 3 * 16 : k_rms_mm_rows;
+    const uint64_t wgs = (uint64_t)((M + rows - 1) / rows);
     if (wgs > 0x7fffffffu) return fail(LNSHIP_ERANGE, "rms_norm_mul_mat: grid too large%s");
     m.xcd_sh = xcd_shift(wgs, s->cus);
-    hipLaunchKernelGGL(k_mm16_rms<PF>, dim3((unsigned)(wgs << m.xcd_sh)), dim3(k_block), (int)lds,
-                       (hipStream_t)stream, m, s->T);
+    if (narrow)
+        hipLaunchKernelGGL((k_mm16_rms<PF, 16>), dim3((unsigned)(wgs << m.xcd_sh)), dim3(k_block), (int)lds,
+                           (hipStream_t)stream, m, s->T);
+    else
+        hipLaunchKernelGGL(k_mm16_rms<PF>, dim3((unsigned)(wgs << m.xcd_sh)), dim3(k_block), (int)lds,
+                           (hipStream_t)stream, m, s->T);
     LNSHIP_HIP(hipGetLastError());
     return 0;
 }

@@ -124,6 +124,7 @@ def lib():
         "lnship_lpvip_db_range": (ctypes.c_int, [ctypes.c_uint32, ctypes.c_uint32, c_p, c_p]),
         "lnship32_add_lds": (ctypes.c_int, [ctypes.c_int, c_p, c_p, c_p, c_i64, c_p]),
         "lnship_test_predict_skew": (ctypes.c_int, [ctypes.c_int]),
+        "lnship_test_decode_width": (ctypes.c_int, [ctypes.c_int]),
         "lnship16_add": (ctypes.c_int, [c_p, c_p, c_i64, c_i64, c_p, c_p]),
         "lnship16_mul": (ctypes.c_int, [c_p, c_p, c_i64, c_i64, c_p, c_p]),
         "lnship16_swiglu": (ctypes.c_int, [c_p, c_i64, c_p, c_i64, c_p, c_i64, c_i64, c_p]),
