@@ -443,6 +443,29 @@ def test_sum32_gemv_narrow_waves(ln, width):
         L.lnship_test_decode_width(prev)
 
 
+@pytest.mark.parametrize("width", [0, 16])
+def test_lns32_gemv_narrow_waves(ln, width):
+    # the one-column xlns32 GEMV (the LNS32 decoder's) with 16 rows per wave
+    # and with 64, against the oracle, plain and with the residual ADD
+    L = ln.lib()
+    rng = np.random.default_rng(4343)
+    prev = L.lnship_test_decode_width(width)
+    try:
+        for name, K, M, w, x in _narrow_cases(rng):
+            print(f"\n[xlns32 gemv] width={width} {name}", flush=True)
+            wp, dx = ln.pack32(dev(w)), dev(x[None])
+            want = O.mul_mat32(w, x[None])
+            y = torch.empty(1, M, device="cuda")
+            ln.mul_mat32_raw(wp.data_ptr(), dx.data_ptr(), y.data_ptr(), K, M, 1)
+            same_bits(host(y), want, f"width {width} {name}")
+            r = rng.standard_normal((1, M)).astype(np.float32)
+            acc = dev(r)
+            ln.mul_mat32_raw(wp.data_ptr(), dx.data_ptr(), acc.data_ptr(), K, M, 1, residual=acc.data_ptr())
+            same_bits(host(acc), O.add32(want, r), f"width {width} {name} residual")
+    finally:
+        L.lnship_test_decode_width(prev)
+
+
 @pytest.mark.parametrize("mode", MODES + ["lns32"])
 def test_mul_mat_residual(ln, mode):
     # the ADD after a mul_mat fused into it, in place (dst = residual), as

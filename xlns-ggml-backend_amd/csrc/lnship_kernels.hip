@@ -1257,16 +1257,19 @@ struct mm_args32 {
 // sharing the staged tables (as k_mm16).  A group of eight k is two 16-byte
 // loads of weights and two per column of activations; the next PF groups are
 // in flight while one is accumulated.
-template <int NC, int PF, int CG>
+// W: rows per wave (64, or 16 with the other lanes only staging, as in k_mm16)
+template <int NC, int PF, int CG, int W = 64>
 __global__ __launch_bounds__(k_block * CG) void k_mm32(mm_args32 a, dev_tables T) {
     extern __shared__ __align__(16) char lds[];
     if (blockIdx.x & ((1u << a.xcd_sh) - 1u)) return;   // as in k_mm16
     const red16<LNSHIP_SUM32> R = stage_for<LNSHIP_SUM32, NC == 1>(T, lds);
     __syncthreads();
     const int cg = CG == 1 ? 0 : (int)(threadIdx.x / k_block);
-    const int64_t m = (int64_t)(blockIdx.x >> a.xcd_sh) * k_block + (threadIdx.x % k_block);
+    const int lane = (int)(threadIdx.x & 63u);
+    const int64_t m = W < 64 ? (int64_t)(blockIdx.x >> a.xcd_sh) * (k_block / 64 * W) + (threadIdx.x >> 6) * W + lane
+                             : (int64_t)(blockIdx.x >> a.xcd_sh) * k_block + (threadIdx.x % k_block);
     const int64_t n0 = ((int64_t)blockIdx.y * CG + cg) * NC;
-    if (m >= a.M || n0 >= a.N) return;
+    if ((W < 64 && lane >= W) || m >= a.M || n0 >= a.N) return;
     const int64_t z = blockIdx.z;
     const int64_t i12 = z % a.ne12, i13 = z / a.ne12;
     const int nc = (int)min<int64_t>(NC, a.N - n0);
@@ -3131,17 +3134,18 @@ static int dispatch_mm16(const mm_args16 &m, const dev_tables &T, int64_t nslice
     }
 }
 
-template <int NC, int CG>
+template <int NC, int CG, int W = 64>
 static int launch_mm32(const mm_args32 &m, const dev_tables &T, int64_t nslices, int cus, hipStream_t st) {
     // prefetch depth within 128 VGPRs at four waves per SIMD
     constexpr int PF = NC == 1 ? (CG >= 4 ? 2 : 4) : 1;
-    if (int rc = set_lds(k_mm32<NC, PF, CG>, k_lds_tab32)) return rc;
-    dim3 grid((unsigned)((m.M + k_block - 1) / k_block), (unsigned)((m.N + NC * CG - 1) / (NC * CG)), (unsigned)nslices);
+    if (int rc = set_lds(k_mm32<NC, PF, CG, W>, k_lds_tab32)) return rc;
+    constexpr int rows = W < 64 ? k_block / 64 * W : k_block;   // rows per workgroup
+    dim3 grid((unsigned)((m.M + rows - 1) / rows), (unsigned)((m.N + NC * CG - 1) / (NC * CG)), (unsigned)nslices);
     if (grid.x > 2147483647u || grid.y > 65535u) return fail(LNSHIP_ERANGE, "mul_mat: grid too large%s");
     mm_args32 mx = m;
     mx.xcd_sh = xcd_shift((uint64_t)grid.x * grid.y * grid.z, cus);
     grid.x <<= mx.xcd_sh;
-    hipLaunchKernelGGL((k_mm32<NC, PF, CG>), grid, dim3(k_block * CG), k_lds_tab32, st, mx, T);
+    hipLaunchKernelGGL((k_mm32<NC, PF, CG, W>), grid, dim3(k_block * CG), k_lds_tab32, st, mx, T);
     LNSHIP_HIP(hipGetLastError());
     return 0;
 }
@@ -3729,7 +3733,12 @@ static int mul_mat32_staged(device_state *s, const lnship_mul_mat_args *a, void 
         case 14: return launch_mm32<1, 4>(m, s->T, nslices, s->cus, st);
         case 24: return launch_mm32<2, 4>(m, s->T, nslices, s->cus, st);
         case 44: return launch_mm32<4, 4>(m, s->T, nslices, s->cus, st);
-        default: return launch_mm32<1, 1>(m, s->T, nslices, s->cus, st);
+        default:
+            // one column: 16-row waves while they fill at most one wave slot
+            // per SIMD (as the sum32 GEMV)
+            if (m.N == 1 && g_decode_w == 16 && m.M * nslices <= (int64_t)s->cus * 4 * 16)
+                return launch_mm32<1, 1, 16>(m, s->T, nslices, s->cus, st);
+            return launch_mm32<1, 1>(m, s->T, nslices, s->cus, st);
     }
 }
 
