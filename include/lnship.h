@@ -380,10 +380,10 @@ int lnship32_add_lds(int form, const uint32_t *x, const uint32_t *y, uint32_t *o
  * value.  Host-side only; takes effect at the next launch.  No counterpart
  * in the reference. */
 int lnship_test_predict_skew(int skew);
-/* Test hook: rows per wave of the one-column sum32 and xlns32 GEMVs
- * (lnship16_mul_mat and lnship16_swiglu_mul_mat with N = 1,
- * lnship16_rms_norm_mul_mat, lnship32_mul_mat with N = 1; up to 16 rows per
- * wave slot of the GPU): 16 (the default; the wave's other
+/* Test hook: rows per wave of the single-chain GEMVs (lnship16_mul_mat,
+ * lnship16_swiglu_mul_mat, lnship16_rms_norm_mul_mat and lnship32_mul_mat
+ * where each lane runs one output's chain and there are at most 16 chains
+ * per wave slot of the GPU): 16 (the default; the wave's other
  * lanes only stage tables and activations) or 0 for 64-row waves; other
  * values leave it unchanged.  The results do not depend on it.  Returns the
  * previous value; host-side only, taking effect at the next launch.  No

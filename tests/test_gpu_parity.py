@@ -418,6 +418,20 @@ def _narrow_cases(rng):
 
 
 @pytest.mark.parametrize("width", [0, 16])
+@pytest.mark.parametrize("mode", MODES)
+def test_gemv_narrow_waves_columns(ln, mode, width):
+    # the single-chain GEMV with several columns (the batched decode's) in
+    # every mode, with 16 rows per wave and with 64, against the oracle
+    L = ln.lib()
+    prev = L.lnship_test_decode_width(width)
+    try:
+        for (K, M, N) in ((576, 576, 8), (1536, 100, 3)):
+            _mm_case(ln, mode, K, M, N, seed=K + N)
+    finally:
+        L.lnship_test_decode_width(prev)
+
+
+@pytest.mark.parametrize("width", [0, 16])
 def test_sum32_gemv_narrow_waves(ln, width):
     # the one-column sum32 GEMV with 16 rows per wave (the default) and with
     # 64 (width 0) against the oracle, plain and with the residual ADD, on

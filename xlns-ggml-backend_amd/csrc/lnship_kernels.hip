@@ -3058,9 +3058,15 @@ static mm16_shape mm_shape_x32(int64_t M, int64_t N, int64_t nslices, int64_t kp
 // is a multiple of 2^sh working, the working ones fall on 8 >> sh XCDs and
 // share those L2s' copies.  sh is the largest (at most 3) for which those
 // XCDs still hold every working workgroup at one per CU.
-// Rows per wave of the one-column sum32 GEMVs: 16, or 0 for 64-row waves;
+// Rows per wave of the single-chain GEMVs: 16, or 0 for 64-row waves;
 // lnship_test_decode_width sets it
 static int g_decode_w = 16;
+
+// 16-row waves for a launch of `chains` chains (rows x columns x slices,
+// one column per workgroup column) while they fill at most one wave slot per
+// SIMD: the chains are bound by their dependent steps, and a step with only
+// the first 16 lanes of its wave active is shorter
+static bool narrow_mm(int64_t chains, int cus) { return g_decode_w == 16 && chains <= (int64_t)cus * 4 * 16; }
 
 // the grid of nh attention heads placed by attn_head: every block up to the
 // last head's, the multiples of 8 idle
@@ -3119,9 +3125,7 @@ static int dispatch_mm16(const mm_args16 &m, const dev_tables &T, int64_t nslice
             case 44: return launch_mm16_x<MODE, 4, 4>(m, T, nslices, sh.xl, cus, st);
             case 84: return launch_mm16_x<MODE, 8, 4>(m, T, nslices, sh.xl, cus, st);
             default:
-                // one column: 16-row waves while they fill at most one wave
-                // slot per SIMD
-                if (sh.xl && m.N == 1 && g_decode_w == 16 && m.M * nslices <= (int64_t)cus * 4 * 16)
+                if (sh.xl && narrow_mm(m.M * m.N * nslices, cus))
                     return launch_mm16<MODE, 1, true, 1, 16>(m, T, nslices, cus, st);
                 return launch_mm16_x<MODE, 1, 1>(m, T, nslices, sh.xl, cus, st);
         }
@@ -3129,7 +3133,10 @@ static int dispatch_mm16(const mm_args16 &m, const dev_tables &T, int64_t nslice
         switch (sh.nc) {
             case 8: return launch_mm16_x<MODE, 8, 1>(m, T, nslices, sh.xl, cus, st);
             case 4: return launch_mm16_x<MODE, 4, 1>(m, T, nslices, sh.xl, cus, st);
-            default: return launch_mm16_x<MODE, 1, 1>(m, T, nslices, sh.xl, cus, st);
+            default:
+                if (sh.xl && narrow_mm(m.M * m.N * nslices, cus))
+                    return launch_mm16<MODE, 1, true, 1, 16>(m, T, nslices, cus, st);
+                return launch_mm16_x<MODE, 1, 1>(m, T, nslices, sh.xl, cus, st);
         }
     }
 }
@@ -3736,8 +3743,7 @@ static int mul_mat32_staged(device_state *s, const lnship_mul_mat_args *a, void 
         default:
             // one column: 16-row waves while they fill at most one wave slot
             // per SIMD (as the sum32 GEMV)
-            if (m.N == 1 && g_decode_w == 16 && m.M * nslices <= (int64_t)s->cus * 4 * 16)
-                return launch_mm32<1, 1, 16>(m, s->T, nslices, s->cus, st);
+            if (narrow_mm(m.M * m.N * nslices, s->cus)) return launch_mm32<1, 1, 16>(m, s->T, nslices, s->cus, st);
             return launch_mm32<1, 1>(m, s->T, nslices, s->cus, st);
     }
 }
@@ -3916,7 +3922,7 @@ int lnship16_rms_norm_mul_mat(int mode, const float *x, const float *norm_w, flo
     if ((uint64_t)M * 16 * PF + (uint64_t)M * 16 > 0xffffffffu)
         return fail(LNSHIP_ERANGE, "rms_norm_mul_mat: weight rows too long for 32-bit block offsets%s");
     // 16-row chain waves while every workgroup still gets a CU of its own
-    const bool narrow = g_decode_w == 16 && M <= (int64_t)s->cus * 3 * 16;
+    const bool narrow = narrow_mm(M * 4 / 3, s->cus);
     if (int rc = narrow ? set_lds(k_mm16_rms<PF, 16>, (int)lds) : set_lds(k_mm16_rms<PF>, (int)lds)) return rc;
     mm_args16 m{(const uint16_t *)w, nullptr, x, dst, K, kp, M, 1, K, K, 1, 1, 1, 1, M, kp * M, M, M, 0, nullptr, 0};
     m.norm = norm_w;
