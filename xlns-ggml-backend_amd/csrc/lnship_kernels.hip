@@ -1529,8 +1529,12 @@ __global__ __launch_bounds__(k_block) void k_rms16(const float *__restrict__ src
         }
     }
     __syncthreads();
-    if ((int)threadIdx.x < nr) {
-        const int r = threadIdx.x;
+    // every lane of the first wave runs a row's chain, the lanes past the
+    // block's rows that of its last row again (only a row's own lane
+    // stores): with the wave's other lanes inactive the chain's steps take
+    // about 15 % longer
+    if (threadIdx.x < 64u) {
+        const int r = min((int)threadIdx.x, nr - 1);
         uint32_t s = 0;
         if (MODE == LNSHIP_MONTE)
             s = lfsr_jump(T, monte_start(T, seed, state, offset), (uint64_t)(r0 + r) * (uint64_t)ncols);
@@ -1543,7 +1547,7 @@ __global__ __launch_bounds__(k_block) void k_rms16(const float *__restrict__ src
         const uint32_t e16 = x16_from_f32(T.cvt16, eps);
         // the epsilon add is a plain xlns16_add in every mode
         const uint32_t me = x16_add_g(T.gauss16, mean, e16);
-        s_inv[r] = x16_recip(x16_sqrt(me));
+        if ((int)threadIdx.x < nr) s_inv[r] = x16_recip(x16_sqrt(me));
     }
     __syncthreads();
     for (int e0 = threadIdx.x; e0 < nel; e0 += B * nt) {
@@ -1594,15 +1598,16 @@ __global__ __launch_bounds__(k_block) void k_rms32(const float *__restrict__ src
         }
     }
     __syncthreads();
-    if ((int)threadIdx.x < nr) {
-        const int r = threadIdx.x;
+    // (all 64 lanes, as in k_rms16)
+    if (threadIdx.x < 64u) {
+        const int r = min((int)threadIdx.x, nr - 1);
         uint32_t acc = 0u;
         chain_pos32(P, acc, sq + r * rs, 0, nc);   // squares: positive
         const uint32_t mean = x32_mul(acc, x32_from_f32(1.0f / (float)ncols));
         // mean >= 0: the epsilon add is a positive one unless eps < 0
         const uint32_t e = x32_from_f32(eps);
         const uint32_t me = (e & k32_sign) ? x32_add(T.tab32, mean, e) : x32_add_pos2(P, mean, e);
-        s_inv[r] = x32_recip(x32_sqrt(me));
+        if ((int)threadIdx.x < nr) s_inv[r] = x32_recip(x32_sqrt(me));
     }
     __syncthreads();
     for (int e0 = threadIdx.x; e0 < nel; e0 += B * nt) {
@@ -1839,8 +1844,9 @@ __global__ __launch_bounds__(k_block) void k_softmax16(sm_args a, dev_tables T) 
             }
     }
     __syncthreads();
-    if ((int)threadIdx.x < nr) {
-        const int r = threadIdx.x;
+    // (all 64 lanes, as in k_rms16)
+    if (threadIdx.x < 64u) {
+        const int r = min((int)threadIdx.x, nr - 1);
         uint32_t s = 0;
         if (MODE == LNSHIP_MONTE)
             s = lfsr_jump(T, monte_start(T, a.seed, a.state, a.offset), (uint64_t)(r0 + r) * (uint64_t)(a.n - 1));
@@ -1858,7 +1864,7 @@ __global__ __launch_bounds__(k_block) void k_softmax16(sm_args a, dev_tables T) 
             if constexpr (MODE == LNSHIP_SUM32) chain_pos16(P, acc.l, row, 1, n_eff);
             else chain16<red16<MODE>, true>(R, acc, row, 1, n_eff, s);
         }
-        s_tot[r] = R.finish(acc) & 0xffffu;
+        if ((int)threadIdx.x < nr) s_tot[r] = R.finish(acc) & 0xffffu;
     }
     __syncthreads();
     for (int e0 = threadIdx.x; e0 < nel; e0 += B * nt) {
@@ -2779,15 +2785,16 @@ __global__ __launch_bounds__(k_block) void k_softmax32(sm_args a, dev_tables T) 
         if (c[o] & k32_logmask) atomicMax(&s_last[r], (int)(e - (int64_t)r * a.n));
     }
     __syncthreads();
-    if ((int)threadIdx.x < nr) {
-        const int r = threadIdx.x;
+    // (all 64 lanes, as in k_rms16)
+    if (threadIdx.x < 64u) {
+        const int r = min((int)threadIdx.x, nr - 1);
         const uint32_t *row = c + r * rs;
         acc_ls acc{row[0] & k32_logmask, row[0] & k32_sign};
         // trailing exps of log 0 add nothing to a sum of at least 1 (as in
         // k_softmax16): the chain stops at the last nonzero exp
         const int n_eff = s_last[r] + 1;
         if (n_eff > 1) chain32<true>(R.O, acc, row, 1, n_eff);   // exps: positive
-        s_tot[r] = acc.s | acc.l;
+        if ((int)threadIdx.x < nr) s_tot[r] = acc.s | acc.l;
     }
     __syncthreads();
     for (int64_t e = threadIdx.x; e < ne; e += blockDim.x) {
