@@ -284,6 +284,29 @@ typedef struct lnship_attn_args {
 } lnship_attn_args;
 int lnship16_attn_decode(int mode, const lnship_attn_args *args, void *stream);
 
+/* lnship16_attn_decode for the one decode token of each of n_seq sequences,
+ * in every mode: the kq mul_mat, soft_max and kqv mul_mat of a batched decode
+ * step (one query row per sequence; lns_mul_mat src/lns-ops.cpp:293-384 with
+ * ggml's 4-D broadcast, lns_soft_max :643-695).  Sequence s's query heads at
+ * q + s * n_head * head_dim, its kv head g at k_cache + (s * n_head_kv + g) *
+ * k_slice (v_cache and v_slice alike), its mask row at mask + s * n_kv and its
+ * output at dst + s * n_head * head_dim: the layout of the three nodes with
+ * ne03 = ne13 = n_seq.  Monte (mode 1): the three nodes' LFSR starts,
+ * monte_seed[i] or, with monte_state, the state there jumped by
+ * monte_offset[i] when the launch runs (i = 0 kq, 1 soft_max, 2 kqv), as the
+ * three nodes would take them; each reduction starts where its node's would.
+ * dst equals the three nodes' bit for bit.  No single counterpart in the
+ * reference.  n_kv <= lnship_max_row(8, mode) for head_dim <= 256; a launch
+ * that does not fit LDS returns LNSHIP_ERANGE (checked before any device
+ * call). */
+typedef struct lnship_attn_seqs {
+    int64_t n_seq;
+    uint16_t monte_seed[3];
+    const uint16_t *monte_state;
+    uint64_t monte_offset[3];
+} lnship_attn_seqs;
+int lnship16_attn_decode_seqs(int mode, const lnship_attn_args *args, const lnship_attn_seqs *seqs, void *stream);
+
 /* lnship16_rope_store_kv for one token and lnship16_attn_decode in one
  * launch: each query head's workgroup rotates its query (lns_rope,
  * src/lns-ops.cpp:1199-1281, written through F32) and stores its kv head's rotated
@@ -404,7 +427,8 @@ int lnship_causal_mask(const int32_t *pos, int64_t ntok, int64_t n_kv, float *ma
  * cells (n_kv) of lnship16_attn_decode with head_dim up to 256 (0 for Monte),
  * 5 the K of lnship16_rms_norm_mul_mat (sum32; 0 for other modes), 6 the K
  * of lnship16_swiglu_mul_mat (0 for Monte), 7 the cells of
- * lnship32_attn_decode with head_dim up to 256;
+ * lnship32_attn_decode with head_dim up to 256, 8 the cells of
+ * lnship16_attn_decode_seqs with head_dim up to 256 (every mode);
  * mode is the xlns16 summation mode (ignored for xlns32).  No GPU needed.  Plays the
  * role of the reference's grid / shape predicates (cuda/lns-cuda-ops.cpp:
  * 45-54, 184-189): a ggml backend declines longer rows in supports_op. */

@@ -302,3 +302,33 @@ def test_rope_attn_decode_checks_its_store_arguments_first(lnship):
     q, a = pair()
     assert L.lnship16_rope_attn_decode(lnship.MONTE, ctypes.byref(q), ctypes.byref(a), None) == EINVAL
     assert L.lnship16_rope_attn_decode(lnship.SUM32, None, ctypes.byref(a), None) == EINVAL
+
+
+def test_attn_decode_seqs_checks_arguments_first(lnship):
+    # lnship16_attn_decode_seqs runs every mode, Monte with the three nodes'
+    # starts; its arguments and the sequence count are checked before any
+    # device call (a valid call then needs the device)
+    L = lnship.lib()
+    fake = ctypes.c_void_p(0x1000).value   # never dereferenced: the checks come first
+    EINVAL, ENOINIT, ERANGE = -1, -3, -4   # include/lnship.h: enum lnship_error
+    a = lnship.AttnArgs()
+    a.q, a.k_cache, a.v_cache, a.dst, a.mask = fake, fake + 64, fake + 128, fake + 192, fake + 256
+    a.cache_m, a.k_slice, a.v_slice, a.scale = 512, 64 * 512, 64 * 512, 0.125
+    a.n_head, a.n_head_kv, a.head_dim, a.n_kv = 9, 3, 64, 320
+    for mode in (lnship.BASE, lnship.MONTE, lnship.LPVIP, lnship.SUM32):
+        sq = lnship.attn_seqs(8, (1, 2, 3))
+        assert L.lnship16_attn_decode_seqs(mode, ctypes.byref(a), ctypes.byref(sq), None) == ENOINIT, mode
+        # the limit of the cells is that of lnship16_attn_decode, Monte included
+        lim = L.lnship_max_row(8, mode)
+        assert lim >= 4096 and (mode == lnship.MONTE or lim == L.lnship_max_row(4, mode))
+    for n_seq in (0, -1, 0x7fffff):
+        sq = lnship.attn_seqs(n_seq)
+        assert L.lnship16_attn_decode_seqs(lnship.MONTE, ctypes.byref(a), ctypes.byref(sq), None) == EINVAL, n_seq
+    assert L.lnship16_attn_decode_seqs(lnship.SUM32, ctypes.byref(a), None, None) == EINVAL
+    # lnship16_attn_decode itself still refuses Monte (it has no starts)
+    assert L.lnship16_attn_decode(lnship.MONTE, ctypes.byref(a), None) == EINVAL
+    assert L.lnship_max_row(4, lnship.MONTE) == 0
+    a.n_kv = L.lnship_max_row(8, lnship.MONTE) + 8
+    a.cache_m = a.n_kv
+    sq = lnship.attn_seqs(2)
+    assert L.lnship16_attn_decode_seqs(lnship.MONTE, ctypes.byref(a), ctypes.byref(sq), None) == ERANGE

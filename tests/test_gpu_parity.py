@@ -845,6 +845,71 @@ def test_attn_decode_equals_three_nodes(ln, mode, n_kv, big_tail, skew, hd):
         assert ln.lib().lnship_max_row(4, O.MONTE) == 0 and ln.lib().lnship_max_row(4, m) >= 4096
 
 
+@pytest.mark.parametrize("mode,nseq,n_kv,hd,big_tail", [
+    ("monte", 1, 13, 64, False), ("monte", 1, 256, 64, False), ("monte", 3, 256, 64, False), ("monte", 8, 512, 64, False),
+    ("monte", 3, 200, 72, True), ("base", 3, 256, 64, False), ("base", 8, 512, 64, True), ("lpvip", 3, 256, 64, False),
+    ("lpvip", 8, 320, 64, False), ("sum32", 3, 256, 64, True), ("sum32", 8, 512, 64, False), ("sum32", 2, 77, 36, False)])
+def test_attn_decode_seqs_equals_three_nodes(ln, mode, nseq, n_kv, hd, big_tail):
+    # lnship16_attn_decode_seqs against the batched decode step's three ops:
+    # K^T q with ggml's 4-D broadcast (sequence s on its own caches), the
+    # masked soft_max and V p, the library's own launches, each with its own
+    # Monte start; sequences at different positions (each its own mask row).
+    # Monte runs twice: with the three starts as seeds, and read from a
+    # device state with offsets (as in a captured graph).  big_tail puts
+    # values of 1e35 in V past a sequence's last position, where the KQV
+    # chain may not stop
+    import ctypes
+    m = O.MODES[mode]
+    nh, nkv, n_ctx = 9, 3, max(256, (n_kv + 255) // 256 * 256)
+    rng = np.random.default_rng(7000 + 10 * nseq + n_kv + hd)
+    print(f"\n[attn decode seqs] {mode} n_seq={nseq} n_kv={n_kv} head_dim={hd} big_tail={big_tail}", flush=True)
+    L, P = ln.lib(), (lambda t: t.data_ptr())
+    pos = [int(x) for x in rng.integers(max(0, n_kv // 3), n_kv, nseq)]
+    pos[0] = n_kv - 1
+    v = (rng.standard_normal((nseq, nkv, hd, n_ctx)) * 0.5).astype(np.float32)
+    if big_tail:
+        for s in range(nseq):
+            v[s, :, :, pos[s] + 1:n_kv] *= np.float32(1e35)
+    kf = (rng.standard_normal((nseq, nkv, n_ctx, hd)) * 0.5).astype(np.float32)
+    kc = ln.pack16(dev(kf.reshape(nseq * nkv, n_ctx, hd)))
+    vc = ln.pack16(dev(v.reshape(nseq * nkv, hd, n_ctx)))
+    kslice, vslice = ln.kp(hd) * n_ctx, ln.kp(n_ctx) * hd
+    q = dev((rng.standard_normal(nseq * nh * hd) * 2).astype(np.float32))
+    maskf = np.where(np.arange(n_kv)[None, :] <= np.array(pos)[:, None], 0.0, -np.inf).astype(np.float32)
+    mask = dev(maskf)
+    scale = 0.125
+    d_kq = L.lnship16_mul_mat_draws(m, hd, n_kv, 1, nh, nseq)
+    d_sm = L.lnship16_soft_max_draws(m, n_kv, nh * nseq)
+    s0 = 4242
+    s1 = L.lnship_lfsr_jump(s0, d_kq)
+    s2 = L.lnship_lfsr_jump(s1, d_sm)
+    kq = torch.empty(nseq * nh * n_kv, device="cuda")
+    ln.mul_mat16_raw(m, P(kc), P(q), P(kq), hd, n_kv, 1, ne02=nkv, ne03=nseq, ne12=nh, ne13=nseq, x_ld=nh * hd,
+                     x_slice=hd, seed=s0, w_mstride=n_ctx, w_slice=kslice)
+    p = ln.soft_max16(m, kq.view(nseq, nh, 1, n_kv), mask.view(nseq, 1, 1, n_kv), scale, seed=s1)
+    want = torch.empty(nseq * nh * hd, device="cuda")
+    ln.mul_mat16_raw(m, P(vc), P(p), P(want), n_kv, hd, 1, ne02=nkv, ne03=nseq, ne12=nh, ne13=nseq, x_ld=n_kv,
+                     x_slice=n_kv, seed=s2, w_slice=vslice, dst_ld=nh * hd, dst_slice=hd)
+    a_args = lambda out: ln.AttnArgs(P(q), P(kc), P(vc), n_ctx, kslice, vslice, P(mask), scale, P(out), nh, nkv, hd,
+                                     n_kv)
+    got = torch.full((nseq * nh * hd,), float("nan"), device="cuda")
+    sq = ln.attn_seqs(nseq, (s0, s1, s2))
+    ln.check(L.lnship16_attn_decode_seqs(m, ctypes.byref(a_args(got)), ctypes.byref(sq), ln._stream()))
+    same_bits(host(got), host(want), f"attn decode seqs {mode} n_seq={nseq} n_kv={n_kv}")
+    if mode == "monte":
+        # the starts read on the device: state S, offsets 0, d_kq, d_kq + d_sm
+        S = 911
+        st = torch.tensor([S], dtype=torch.int16, device="cuda")
+        got2 = torch.full((nseq * nh * hd,), float("nan"), device="cuda")
+        sq2 = ln.attn_seqs(nseq, ((st, 0), (st, d_kq), (st, d_kq + d_sm)))
+        ln.check(L.lnship16_attn_decode_seqs(m, ctypes.byref(a_args(got2)), ctypes.byref(sq2), ln._stream()))
+        got3 = torch.full((nseq * nh * hd,), float("nan"), device="cuda")
+        sq3 = ln.attn_seqs(nseq, (S, L.lnship_lfsr_jump(S, d_kq), L.lnship_lfsr_jump(S, d_kq + d_sm)))
+        ln.check(L.lnship16_attn_decode_seqs(m, ctypes.byref(a_args(got3)), ctypes.byref(sq3), ln._stream()))
+        same_bits(host(got2), host(got3), f"attn decode seqs monte n_seq={nseq} n_kv={n_kv}: state vs seeds")
+        assert not np.array_equal(host(got3), host(got)), "other starts, other draws"
+
+
 @pytest.mark.parametrize("mode,n_kv,nd,hd,pos", [
     ("sum32", 1, 64, 64, 0), ("sum32", 13, 64, 64, 12), ("sum32", 256, 64, 64, 200), ("sum32", 520, 64, 64, 517),
     ("sum32", 200, 32, 64, 150), ("sum32", 77, 72, 72, 60), ("base", 256, 64, 64, 200), ("lpvip", 13, 64, 64, 9),

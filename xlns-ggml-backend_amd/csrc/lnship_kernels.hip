@@ -2155,6 +2155,13 @@ struct attn_args {
     const float *cos_sin;          // the rope table (lnship_rope_table layout)
     int rope_n_dims, nh, nhkv;     // rotated dims; query and kv heads
     unsigned long long *err;       // a position outside the cache is recorded here
+    // lnship16_attn_decode_seqs: nseq sequences, workgroup head hh = s nh + h
+    // (nh is set for every launch); Monte: the kq, soft_max and kqv nodes'
+    // starts, monte_start of (mseed[i], mstate, moff[i])
+    int nseq;
+    uint32_t mseed[3];
+    const uint16_t *mstate;
+    uint64_t moff[3];
 };
 
 // The rope of head h's query into xq (its xlns16 codes, through F32 as the
@@ -2387,7 +2394,8 @@ template <int MODE>
 __global__ __launch_bounds__(k_block) void k_attn16(attn_args a, dev_tables T) {
     extern __shared__ __align__(16) char lds[];
     bool idle;
-    const int h = attn_head(idle), kv = h / a.rep;
+    // head hh = s nh + h: query head h of sequence s
+    const int hh = attn_head(idle), sqn = hh / a.nh, h = hh - sqn * a.nh, kv = h / a.rep;
     if (idle) return;
     const red16<MODE> R = stage_for<MODE, true>(T, lds);
     const int hd = a.hd, n = a.n_kv, hp = (hd + 7) & ~7, rs = (n + 7) & ~7;
@@ -2410,19 +2418,27 @@ __global__ __launch_bounds__(k_block) void k_attn16(attn_args a, dev_tables T) {
         if (!attn_rope_store(a, T, h, kv, xq)) return;
     } else {
         for (int k = threadIdx.x; k < hp; k += blockDim.x)
-            xq[k] = k < hd ? (uint16_t)x16_from_f32(T.cvt16, a.q[(int64_t)h * hd + k]) : (uint16_t)0;
+            xq[k] = k < hd ? (uint16_t)x16_from_f32(T.cvt16, a.q[(int64_t)hh * hd + k]) : (uint16_t)0;
     }
     __syncthreads();
     // the scores, and soft_max's first pass over them
     const uint32_t sc = x16_from_f32(T.cvt16, a.scale);
     const bool has_mask = a.mask != nullptr;
-    const uint16_t *kw = a.k + kv * a.k_slice;
+    const uint16_t *kw = a.k + ((int64_t)sqn * a.nhkv + kv) * a.k_slice;
+    const float *mrow = has_mask ? a.mask + (int64_t)sqn * n : nullptr;
+    // Monte: each reduction starts where its node's would (kq: output
+    // hh n + j of hd - 1 draws; soft_max: row hh of n - 1; kqv: output
+    // hh hd + d of n - 1), from the node's own start
+    uint32_t ms[3] = {0, 0, 0};
+    if constexpr (MODE == LNSHIP_MONTE)
+        for (int i = 0; i < 3; i++) ms[i] = monte_start(T, a.mseed[i], a.mstate, a.moff[i]);
     for (int j = threadIdx.x; j < n; j += blockDim.x) {
         uint32_t st = 0;
+        if constexpr (MODE == LNSHIP_MONTE) st = lfsr_jump(T, ms[0], ((uint64_t)hh * n + j) * (uint64_t)(hd - 1));
         typename red16<MODE>::acc_t acc{};
         row_chain<MODE>(R, acc, st, kw + (int64_t)j * 8, a.k_gs, xq, 0, hd);
         const float f = T.rev16[R.finish(acc) & 0xffffu];
-        const float mf = has_mask ? a.mask[j] : 0.0f;
+        const float mf = has_mask ? mrow[j] : 0.0f;
         const uint32_t v = x16_from_f32(T.cvt16, f), mk = x16_from_f32(T.cvt16, mf);
         const uint32_t vm = x16_mul(v, sc), va = x16_add_g(T.gauss16, vm, mk);
         const bool masked_out = has_mask && (mf <= -3.0e38f || mk == 0xffffu);
@@ -2441,11 +2457,12 @@ __global__ __launch_bounds__(k_block) void k_attn16(attn_args a, dev_tables T) {
         }
     }
     __syncthreads();
-    const uint16_t *vw = a.v + kv * a.v_slice;
+    const uint16_t *vw = a.v + ((int64_t)sqn * a.nhkv + kv) * a.v_slice;
     const int n_eff = s_last + 1;
     // the sum of exps up to the last nonzero one, as k_softmax16 runs it
     auto sum_chain = [&]() __attribute__((always_inline)) {
         uint32_t st = 0;
+        if constexpr (MODE == LNSHIP_MONTE) st = lfsr_jump(T, ms[1], (uint64_t)hh * (uint64_t)(n - 1));
         typename red16<MODE>::acc_t acc = R.start(c[0], st);
         if (n_eff > 1) chain16<red16<MODE>, true>(R, acc, c, 1, n_eff, st);
         return R.finish(acc) & 0xffffu;
@@ -2484,6 +2501,7 @@ __global__ __launch_bounds__(k_block) void k_attn16(attn_args a, dev_tables T) {
         const uint32_t p_tail = n_eff < n ? pc[n_eff] & k16_logmask : 0u;
         const uint16_t *vr = vw + (int64_t)d * 8;
         uint32_t st = 0;
+        if constexpr (MODE == LNSHIP_MONTE) st = lfsr_jump(T, ms[2], ((uint64_t)hh * hd + d) * (uint64_t)(n - 1));
         typename red16<MODE>::acc_t acc{};
         bool rest = n_eff < n;
         if (rest && tail_stop) {
@@ -2491,6 +2509,8 @@ __global__ __launch_bounds__(k_block) void k_attn16(attn_args a, dev_tables T) {
             const uint32_t tmax = (uint32_t)min(max((int32_t)(s_vmax[d] + p_tail) - (int32_t)k16_one, 0),
                                                 (int32_t)k16_logmask);
             if constexpr (MODE == LNSHIP_BASE) rest = acc.l < tmax + (uint32_t)k16_esszer + 1u;
+            // Monte: no draw moves a sum at a distance of k16_mc_end or more
+            else if constexpr (MODE == LNSHIP_MONTE) rest = acc.l < tmax + (uint32_t)k16_mc_end;
             else rest = acc.l < (tmax << 16) + k32_esszer;   // xlns32 accumulators (sum32, lpvip)
             if (rest) row_chain<MODE>(R, acc, st, vr, a.v_gs, pc, n_eff, n);
         } else {
@@ -2533,19 +2553,21 @@ __global__ __launch_bounds__(k_block) void k_attn16(attn_args a, dev_tables T) {
             __syncthreads();
             if ((int)threadIdx.x < hd) res = out_chain((int)threadIdx.x);
         }
-        if ((int)threadIdx.x < hd) a.dst[(int64_t)h * hd + threadIdx.x] = T.rev16[res];
+        if ((int)threadIdx.x < hd) a.dst[(int64_t)hh * hd + threadIdx.x] = T.rev16[res];
         return;
     }
-    if (threadIdx.x == 0) {
-        s_tot = sum_chain();
-    } else if (tail_stop && threadIdx.x >= 64 && n_eff < n) {
+    if (threadIdx.x < 64u) {
+        // on every lane of the first wave (as the row sums of k_rms16)
+        const uint32_t t = sum_chain();
+        if (threadIdx.x == 0) s_tot = t;
+    } else if (tail_stop && n_eff < n) {
         // meanwhile, on the other waves: the tail's V maxima
         tail_vmax(64, (int)blockDim.x - 64);
     }
     __syncthreads();
     stage_p(s_tot);
     __syncthreads();
-    for (int d = threadIdx.x; d < hd; d += blockDim.x) a.dst[(int64_t)h * hd + d] = T.rev16[out_chain(d)];
+    for (int d = threadIdx.x; d < hd; d += blockDim.x) a.dst[(int64_t)hh * hd + d] = T.rev16[out_chain(d)];
 }
 
 // ---- LNS32 decode attention: KQ, soft_max and KQV of one token in one launch --
@@ -3221,6 +3243,7 @@ static int64_t max_attn_kv() {
 // the dynamic LDS of a k_attn16 launch (64-bit: head_dim may be up to 4096)
 static int64_t attn16_lds_mode(int mode, int64_t hd, int64_t n_kv) {
     const int64_t off = mode == LNSHIP_BASE ? mm_xl_offset<LNSHIP_BASE>()
+                        : mode == LNSHIP_MONTE ? mm_xl_offset<LNSHIP_MONTE>()
                         : mode == LNSHIP_LPVIP ? mm_xl_offset<LNSHIP_LPVIP>()
                                                : mm_xl_offset<LNSHIP_SUM32>();
     return off + 2 * ((hd + 7) & ~(int64_t)7) + 4 * ((n_kv + 7) & ~(int64_t)7);
@@ -3998,17 +4021,19 @@ int lnship16_soft_max(int mode, const lnship_soft_max_args *a, void *stream) {
 }
 
 // the arguments of an LNS16 decode attention, checked before any device call
-// (need_q: q is read; the fused rope forms it instead)
-static int attn16_check(int mode, const lnship_attn_args *a, bool need_q) {
+// (need_q: q is read; the fused rope forms it instead; monte: the caller
+// passes the three nodes' Monte starts)
+static int attn16_check(int mode, const lnship_attn_args *a, bool need_q, bool monte = false) {
     if (!a) return fail(LNSHIP_EINVAL, "attn_decode: null args%s");
-    if (mode == LNSHIP_MONTE)
-        return fail(LNSHIP_EINVAL, "attn_decode: Monte draws run across the three nodes in graph order; run them%s");
+    if (mode == LNSHIP_MONTE && !monte)
+        return fail(LNSHIP_EINVAL, "attn_decode: Monte draws run across the three nodes in graph order: run them, "
+                                   "or pass their starts to lnship16_attn_decode_seqs%s");
     if (mode < 0 || mode > 3) return fail(LNSHIP_EINVAL, "unknown summation mode%s");
     if ((need_q && !a->q) || !a->k_cache || !a->v_cache || !a->dst || a->n_head <= 0 || a->n_head_kv <= 0 ||
         a->n_head % a->n_head_kv || a->head_dim <= 0 || a->n_kv <= 0 || a->cache_m < a->n_kv ||
         a->head_dim > 4096 || a->n_head > 65535)
         return fail(LNSHIP_EINVAL, "attn_decode: bad argument%s");
-    if (a->n_kv > lnship_max_row(4, mode)) return fail(LNSHIP_ERANGE, "attn_decode: n_kv too long for LDS%s");
+    if (a->n_kv > lnship_max_row(8, mode)) return fail(LNSHIP_ERANGE, "attn_decode: n_kv too long for LDS%s");
     // the limit above holds for head_dim <= 256; wider heads need more LDS
     if ((int64_t)attn16_lds_mode(mode, a->head_dim, a->n_kv) > k_lds_bytes - k_lds_static)
         return fail(LNSHIP_ERANGE, "attn_decode: head_dim x n_kv too large for LDS%s");
@@ -4018,6 +4043,7 @@ static int attn16_check(int mode, const lnship_attn_args *a, bool need_q) {
 static int attn16_launch(int mode, const attn_args &m, int64_t nh, const dev_tables &T, hipStream_t st) {
     switch (mode) {
         case LNSHIP_BASE: return launch_attn16<LNSHIP_BASE>(m, nh, T, st);
+        case LNSHIP_MONTE: return launch_attn16<LNSHIP_MONTE>(m, nh, T, st);
         case LNSHIP_LPVIP: return launch_attn16<LNSHIP_LPVIP>(m, nh, T, st);
         default: return launch_attn16<LNSHIP_SUM32>(m, nh, T, st);
     }
@@ -4028,11 +4054,36 @@ int lnship16_attn_decode(int mode, const lnship_attn_args *a, void *stream) {
     if (int rc = attn16_check(mode, a, true)) return rc;
     device_state *s = state();
     if (!s) return LNSHIP_ENOINIT;
-    const attn_args m{a->q, (const uint16_t *)a->k_cache, (const uint16_t *)a->v_cache, a->cache_m * 8, a->k_slice,
+    attn_args m{a->q, (const uint16_t *)a->k_cache, (const uint16_t *)a->v_cache, a->cache_m * 8, a->k_slice,
                       a->head_dim * 8, a->v_slice,
                       a->mask, a->scale, a->dst, (int)a->head_dim, (int)a->n_kv, (int)(a->n_head / a->n_head_kv),
                       g_predict_skew};
+    m.nh = (int)a->n_head;
+    m.nhkv = (int)a->n_head_kv;
+    m.nseq = 1;
     return attn16_launch(mode, m, a->n_head, s->T, (hipStream_t)stream);
+}
+
+int lnship16_attn_decode_seqs(int mode, const lnship_attn_args *a, const lnship_attn_seqs *q, void *stream) {
+    // arguments and sizes first: they need no device
+    if (int rc = attn16_check(mode, a, true, true)) return rc;
+    if (!q || q->n_seq <= 0 || a->n_head * q->n_seq > 0x7fffff)
+        return fail(LNSHIP_EINVAL, "attn_decode_seqs: bad sequence count%s");
+    device_state *s = state();
+    if (!s) return LNSHIP_ENOINIT;
+    attn_args m{a->q, (const uint16_t *)a->k_cache, (const uint16_t *)a->v_cache, a->cache_m * 8, a->k_slice,
+                a->head_dim * 8, a->v_slice,
+                a->mask, a->scale, a->dst, (int)a->head_dim, (int)a->n_kv, (int)(a->n_head / a->n_head_kv),
+                g_predict_skew};
+    m.nh = (int)a->n_head;
+    m.nhkv = (int)a->n_head_kv;
+    m.nseq = (int)q->n_seq;
+    for (int i = 0; i < 3; i++) {
+        m.mseed[i] = q->monte_seed[i];
+        m.moff[i] = q->monte_offset[i];
+    }
+    m.mstate = q->monte_state;
+    return attn16_launch(mode, m, a->n_head * q->n_seq, s->T, (hipStream_t)stream);
 }
 
 int lnship16_rope_attn_decode(int mode, const lnship_qkv_store_args *q, const lnship_attn_args *a, void *stream) {
@@ -4050,7 +4101,7 @@ int lnship16_rope_attn_decode(int mode, const lnship_qkv_store_args *q, const ln
                       a->k_slice, a->head_dim * 8, a->v_slice,
                       a->mask, a->scale, a->dst, (int)a->head_dim, (int)a->n_kv, (int)(a->n_head / a->n_head_kv),
                       g_predict_skew, q->qkv, q->pos, q->cos_sin, q->rope_n_dims, (int)a->n_head,
-                      (int)a->n_head_kv, s->index_err};
+                      (int)a->n_head_kv, s->index_err, 1};
     return attn16_launch(mode, m, a->n_head, s->T, (hipStream_t)stream);
 }
 
@@ -4108,9 +4159,10 @@ int64_t lnship_max_row(int which, int mode) {
         if (mode < 0 || mode > 3 || mode == LNSHIP_MONTE) return 0;
         return ((k_lds_bytes - 1024 - mm16_tables_bytes(mode) - k_xl_pad) / 2) & ~(int64_t)7;
     }
-    if (which == 4) {
+    if (which == 4 || which == 8) {
         switch (mode) {
             case LNSHIP_BASE: return max_attn_kv<LNSHIP_BASE>();
+            case LNSHIP_MONTE: return which == 8 ? max_attn_kv<LNSHIP_MONTE>() : 0;
             case LNSHIP_LPVIP: return max_attn_kv<LNSHIP_LPVIP>();
             case LNSHIP_SUM32: return max_attn_kv<LNSHIP_SUM32>();
             default: return 0;

@@ -58,6 +58,28 @@ class AttnArgs(ctypes.Structure):
                 ("n_head_kv", c_i64), ("head_dim", c_i64), ("n_kv", c_i64)]
 
 
+class AttnSeqs(ctypes.Structure):
+    _fields_ = [("n_seq", c_i64), ("monte_seed", ctypes.c_uint16 * 3), ("monte_state", c_p),
+                ("monte_offset", ctypes.c_uint64 * 3)]
+
+
+def attn_seqs(n_seq, seeds=(0, 0, 0)):
+    """lnship_attn_seqs for n_seq sequences; seeds: the kq, soft_max and kqv
+    nodes' Monte seed arguments (seed_fields forms: all three 16-bit states,
+    or all three (state, offset) pairs on one device state)."""
+    a = AttnSeqs()
+    a.n_seq = n_seq
+    state = None
+    for i, sd in enumerate(seeds):
+        seed, st, off = seed_fields(sd)
+        a.monte_seed[i] = seed
+        a.monte_offset[i] = off or 0
+        if st is not None:
+            state = st
+    a.monte_state = state
+    return a
+
+
 def build():
     import subprocess
     subprocess.check_call(["make", "-s", "-C", PKG_DIR])
@@ -99,6 +121,8 @@ def lib():
         "lnship16_swiglu_mul_mat": (ctypes.c_int, [ctypes.c_int, c_p, c_p, c_p, c_p, c_p, c_i64, c_i64, c_p]),
         "lnship16_rope_store_kv": (ctypes.c_int, [ctypes.POINTER(QkvStoreArgs), c_p]),
         "lnship16_attn_decode": (ctypes.c_int, [ctypes.c_int, ctypes.POINTER(AttnArgs), c_p]),
+        "lnship16_attn_decode_seqs": (ctypes.c_int, [ctypes.c_int, ctypes.POINTER(AttnArgs), ctypes.POINTER(AttnSeqs),
+                                                     c_p]),
         "lnship16_rope_attn_decode": (ctypes.c_int, [ctypes.c_int, ctypes.POINTER(QkvStoreArgs),
                                                      ctypes.POINTER(AttnArgs), c_p]),
         "lnship32_attn_decode": (ctypes.c_int, [ctypes.POINTER(AttnArgs), c_p]),

@@ -17,9 +17,10 @@ LNS16 backend computes it, op by op, with F32 at op boundaries:
 Fusing Q|K|V and up|gate into one matrix keeps the Monte draw order of the
 separate ops: outputs of a mul_mat take draws in (row, column) order, so the
 fused rows enumerate Q's outputs, then K's, then V's.  A single-sequence
-decode step outside Monte runs K^T q, soft_max and V p in one launch
-(lnship16_attn_decode, bit-identical to the three ops; fused_attn = False
-runs the three).  A single-row sum32 step runs each rms_norm, its norm MUL
+decode step runs K^T q, soft_max and V p in one launch (lnship16_attn_decode,
+and in Monte and for a batched step of several sequences
+lnship16_attn_decode_seqs, which takes the three ops' Monte starts;
+bit-identical to the three ops; fused_attn = False runs the three).  A single-row sum32 step runs each rms_norm, its norm MUL
 and the mul_mat that reads them in one launch (lnship16_rms_norm_mul_mat,
 bit-identical to the three; fused_rms = False runs them apart).  A single-row
 step outside Monte forms swiglu inside the down projection's launch
@@ -41,7 +42,7 @@ from dataclasses import dataclass
 
 import numpy as np
 
-from . import (BASE, MONTE, LPVIP, SUM32, AttnArgs, QkvStoreArgs, check, init, kp, lfsr_advance, lib,
+from . import (BASE, MONTE, LPVIP, SUM32, AttnArgs, QkvStoreArgs, attn_seqs, check, init, kp, lfsr_advance, lib,
                mul_mat16_raw, mul_mat32_raw, seed_fields)
 
 KV_PAD = 256   # llama.cpp pads the KV view to 256 cells without flash attention
@@ -117,8 +118,8 @@ class LlamaLNS16:
         init()
         self.cfg, self.mode, self.lfsr, self.n_seq = cfg, mode, lfsr, n_seq
         self.torch = torch
-        # decode attention in one launch where the op takes the mode and the cells
-        self.fused_attn = mode != MONTE
+        # decode attention in one launch where the op takes the cells
+        self.fused_attn = True
         # and with it, the query rope and the cache stores of the token
         # (lnship16_rope_attn_decode, bit-identical to the two launches)
         self.fused_rope = True
@@ -130,7 +131,7 @@ class LlamaLNS16:
         # (lnship16_swiglu_mul_mat, bit-identical to the two nodes), where the
         # activation row fits LDS
         self.fused_glu = mode != MONTE and cfg.n_ff <= lib().lnship_max_row(6, mode)
-        self._attn_max_kv = lib().lnship_max_row(4, mode)
+        self._attn_max_kv = lib().lnship_max_row(8, mode)
         dev = torch.device("cuda", torch.cuda.current_device())
         self.dev = dev
         c = cfg
@@ -296,6 +297,16 @@ class LlamaLNS16:
         check(lib().lnship16_swiglu_mul_mat(self.mode, gate_ptr, up_ptr, ctypes.c_void_p(w), resid_ptr, dst_ptr, K, M,
                                             self._stream))
 
+    def _attn_seqs(self, args, nseq):
+        """The decode attention of one token in each of nseq sequences, with
+        the Monte starts of the three nodes it replaces, taken in their order."""
+        L, nh, hd, n_kv = lib(), args.n_head, args.head_dim, args.n_kv
+        seeds = (self._seed(L.lnship16_mul_mat_draws(self.mode, hd, n_kv, 1, nh, nseq)),
+                 self._seed(L.lnship16_soft_max_draws(self.mode, n_kv, nh * nseq)),
+                 self._seed(L.lnship16_mul_mat_draws(self.mode, n_kv, hd, 1, nh, nseq)))
+        sq = attn_seqs(nseq, seeds)
+        check(L.lnship16_attn_decode_seqs(self.mode, ctypes.byref(args), ctypes.byref(sq), self._stream))
+
     def _attn(self, args, store=None):
         """The decode attention; with store (the token's rope and cache
         stores), the two in one launch."""
@@ -344,10 +355,16 @@ class LlamaLNS16:
                               P(self.kcache[il], cbase), P(self.vcache[il], cbase), c.n_ctx, self.kslice,
                               self.vslice, seq_ids, self.seq_stride)
             Tq = 1 if batch else T   # query rows per sequence
-            fused = T == 1 and not batch and self.fused_attn and n_kv <= self._attn_max_kv
-            if not (fused and self.fused_rope):
+            fused = (T == 1 or batch) and self.fused_attn and n_kv <= self._attn_max_kv
+            # Monte and batched steps: lnship16_attn_decode_seqs (no rope inside)
+            seqs = fused and (batch or self.mode == MONTE)
+            if not (fused and self.fused_rope) or seqs:
                 check(L.lnship16_rope_store_kv(ctypes.byref(qs), st))
-            if fused:
+            if seqs:
+                self._attn_seqs(AttnArgs(P(q), P(self.kcache[il], cbase), P(self.vcache[il], cbase), c.n_ctx,
+                                         self.kslice, self.vslice, P(mask), 1.0 / math.sqrt(hd), P(att), nh, nkv, hd,
+                                         n_kv), nseq)
+            elif fused:
                 # the three nodes below in one launch, bit for bit (and the
                 # rope and cache stores above it, with fused_rope)
                 self._attn(AttnArgs(P(q), P(self.kcache[il], cbase), P(self.vcache[il], cbase), c.n_ctx,
