@@ -1141,10 +1141,14 @@ __device__ __forceinline__ void mm16_chains(const mm_args16 &a, const dev_tables
     for (int j = 0; j < NC; j++) res[j] = R.finish(acc[j]) & 0xffffu;
 }
 
-// W < 64: W rows per wave, the wave's other lanes only staging the tables
-// and the activations (the one-column sum32 GEMV, whose chains are bound by
-// dependent latency: a VALU instruction with only the first 16 lanes active
-// completes sooner, and the step with it)
+// W < 64: W rows per wave (single-chain GEMVs, bound by the dependent
+// latency of their chains).  sum32: the wave's other lanes only stage the
+// tables and the activations (a VALU instruction with only the first 16
+// lanes active completes sooner, and the step with it).  The other modes run
+// each row's chain on 64 / W lanes, so that every lane stays active: their
+// steps branch (lpvip's FP64 Gaussian log, the sign cases) and, measured,
+// run slower with part of the wave inactive (lpvip K 1536: 420 us with 16
+// lanes, 334 us with the same 16 chains on all 64, 313 us with 4 chains)
 template <int MODE, int NC, int PF, bool XL, int CG, int W = 64>
 __global__ __launch_bounds__(k_block * CG) void k_mm16(mm_args16 a, dev_tables T) {
     extern __shared__ __align__(16) char lds[];
@@ -1213,9 +1217,11 @@ __global__ __launch_bounds__(k_block * CG) void k_mm16(mm_args16 a, dev_tables T
     __syncthreads();
 
     const int lane = (int)(threadIdx.x & 63u);
-    const int64_t m = W < 64 ? (int64_t)(blockIdx.x >> a.xcd_sh) * (k_block / 64 * W) + (threadIdx.x >> 6) * W + lane
+    constexpr bool dup = W < 64 && MODE != LNSHIP_SUM32;   // a chain on 64 / W lanes
+    const int wr = dup ? lane / (64 / W) : lane;              // the lane's row in the wave
+    const int64_t m = W < 64 ? (int64_t)(blockIdx.x >> a.xcd_sh) * (k_block / 64 * W) + (threadIdx.x >> 6) * W + wr
                              : (int64_t)(blockIdx.x >> a.xcd_sh) * k_block + (threadIdx.x % k_block);
-    if ((W < 64 && lane >= W) || m >= a.M || nc == 0 || !slice_ok) return;
+    if ((W < 64 && !dup && lane >= W) || m >= a.M || nc == 0 || !slice_ok) return;
     float *ds = a.dst + z * a.dst_slice + n0 * a.dst_ld + m;
     // output j, with the fused ADD of the residual when there is one: the
     // F32 result and the residual through xlns16, added, back to F32 (the
@@ -1227,12 +1233,14 @@ __global__ __launch_bounds__(k_block * CG) void k_mm16(mm_args16 a, dev_tables T
         a.dst[o] = y;
     };
     if (a.K == 0) {
-        for (int j = 0; j < nc; j++) put(j, T.rev16[0]);
+        if (!dup || lane % (64 / W) == 0)
+            for (int j = 0; j < nc; j++) put(j, T.rev16[0]);
         return;
     }
 
     uint32_t res[NC];
     mm16_chains<MODE, NC, PF, XL>(a, T, R, xl, m, z, zw, zx, n0, nc, res);
+    if (dup && lane % (64 / W) != 0) return;   // one lane of a chain stores
 #pragma unroll
     for (int j = 0; j < NC; j++)
         if (j < nc) put(j, T.rev16[res[j]]);
@@ -3096,6 +3104,13 @@ static int g_decode_w = 16;
 // SIMD: the chains are bound by their dependent steps, and a step with only
 // the first 16 lanes of its wave active is shorter
 static bool narrow_mm(int64_t chains, int cus) { return g_decode_w == 16 && chains <= (int64_t)cus * 4 * 16; }
+// rows per wave of a single-chain lpvip GEMV (its chains on all 64 lanes):
+// fewer chains per wave branch apart less often, while the launch still
+// fits one wave per SIMD; 0: 64-row waves
+static int lpvip_w(int64_t chains, int cus) {
+    if (!narrow_mm(chains, cus)) return 0;
+    return chains <= (int64_t)cus * 4 * 4 ? 4 : chains <= (int64_t)cus * 4 * 8 ? 8 : 16;
+}
 
 // the grid of nh attention heads placed by attn_head: every block up to the
 // last head's, the multiples of 8 idle
@@ -3163,8 +3178,17 @@ static int dispatch_mm16(const mm_args16 &m, const dev_tables &T, int64_t nslice
             case 8: return launch_mm16_x<MODE, 8, 1>(m, T, nslices, sh.xl, cus, st);
             case 4: return launch_mm16_x<MODE, 4, 1>(m, T, nslices, sh.xl, cus, st);
             default:
-                if (sh.xl && narrow_mm(m.M * m.N * nslices, cus))
-                    return launch_mm16<MODE, 1, true, 1, 16>(m, T, nslices, cus, st);
+                if constexpr (MODE == LNSHIP_LPVIP) {
+                    if (sh.xl) switch (lpvip_w(m.M * m.N * nslices, cus)) {
+                            case 4: return launch_mm16<MODE, 1, true, 1, 4>(m, T, nslices, cus, st);
+                            case 8: return launch_mm16<MODE, 1, true, 1, 8>(m, T, nslices, cus, st);
+                            case 16: return launch_mm16<MODE, 1, true, 1, 16>(m, T, nslices, cus, st);
+                            default: break;
+                        }
+                } else {
+                    if (sh.xl && narrow_mm(m.M * m.N * nslices, cus))
+                        return launch_mm16<MODE, 1, true, 1, 16>(m, T, nslices, cus, st);
+                }
                 return launch_mm16_x<MODE, 1, 1>(m, T, nslices, sh.xl, cus, st);
         }
     }
