@@ -1198,8 +1198,7 @@ __global__ __launch_bounds__(k_block * CG) void k_mm16(mm_args16 a, dev_tables T
                     for (int q = 0; q < B; q++) u[q] = urow[min(k0 + q * nt, kl)];
 #pragma unroll
                     for (int q = 0; q < B; q++)
-                        c[q] = x16_from_f32(T.cvt16, T.rev16[x16_mul(x16_mul(c[q], T.sig16[c[q]]),
-                                                                     x16_from_f32(T.cvt16, u[q]))]);
+                        c[q] = T.rho16[x16_mul(x16_mul(c[q], T.sig16[c[q]]), x16_from_f32(T.cvt16, u[q]))];
                 }
                 // every code in a register before the bounded stores: none of
                 // the batch's loads moves into a store's branch
@@ -1223,18 +1222,18 @@ __global__ __launch_bounds__(k_block * CG) void k_mm16(mm_args16 a, dev_tables T
                              : (int64_t)(blockIdx.x >> a.xcd_sh) * k_block + (threadIdx.x % k_block);
     if ((W < 64 && !dup && lane >= W) || m >= a.M || nc == 0 || !slice_ok) return;
     float *ds = a.dst + z * a.dst_slice + n0 * a.dst_ld + m;
-    // output j, with the fused ADD of the residual when there is one: the
-    // F32 result and the residual through xlns16, added, back to F32 (the
-    // ADD node's arithmetic)
-    auto put = [&](int j, float y) {
+    // output j of code c, with the fused ADD of the residual when there is
+    // one: the F32 result and the residual through xlns16 (the result's
+    // round trip in one lookup, rho16), added, back to F32 (the ADD node's
+    // arithmetic)
+    auto put = [&](int j, uint32_t c) {
         const int64_t o = (ds - a.dst) + (int64_t)j * a.dst_ld;
-        if (a.resid)
-            y = T.rev16[x16_add_g(T.gauss16, x16_from_f32(T.cvt16, y), x16_from_f32(T.cvt16, a.resid[o]))];
-        a.dst[o] = y;
+        a.dst[o] = a.resid ? T.rev16[x16_add_g(T.gauss16, T.rho16[c], x16_from_f32(T.cvt16, a.resid[o]))]
+                           : T.rev16[c];
     };
     if (a.K == 0) {
         if (!dup || lane % (64 / W) == 0)
-            for (int j = 0; j < nc; j++) put(j, T.rev16[0]);
+            for (int j = 0; j < nc; j++) put(j, 0u);
         return;
     }
 
@@ -1243,7 +1242,7 @@ __global__ __launch_bounds__(k_block * CG) void k_mm16(mm_args16 a, dev_tables T
     if (dup && lane % (64 / W) != 0) return;   // one lane of a chain stores
 #pragma unroll
     for (int j = 0; j < NC; j++)
-        if (j < nc) put(j, T.rev16[res[j]]);
+        if (j < nc) put(j, res[j]);
 }
 
 // xlns32 (the LNS32 backend): plain sequential xlns32_add
@@ -2445,9 +2444,9 @@ __global__ __launch_bounds__(k_block) void k_attn16(attn_args a, dev_tables T) {
         if constexpr (MODE == LNSHIP_MONTE) st = lfsr_jump(T, ms[0], ((uint64_t)hh * n + j) * (uint64_t)(hd - 1));
         typename red16<MODE>::acc_t acc{};
         row_chain<MODE>(R, acc, st, kw + (int64_t)j * 8, a.k_gs, xq, 0, hd);
-        const float f = T.rev16[R.finish(acc) & 0xffffu];
         const float mf = has_mask ? mrow[j] : 0.0f;
-        const uint32_t v = x16_from_f32(T.cvt16, f), mk = x16_from_f32(T.cvt16, mf);
+        // the score through F32 into xlns16 (the soft_max node reads it so)
+        const uint32_t v = T.rho16[R.finish(acc) & 0xffffu], mk = x16_from_f32(T.cvt16, mf);
         const uint32_t vm = x16_mul(v, sc), va = x16_add_g(T.gauss16, vm, mk);
         const bool masked_out = has_mask && (mf <= -3.0e38f || mk == 0xffffu);
         const uint32_t w = v == 0xffffu || masked_out ? 0xffffu : (has_mask && (mk & k16_logmask)) ? va : vm;
@@ -2497,7 +2496,7 @@ __global__ __launch_bounds__(k_block) void k_attn16(attn_args a, dev_tables T) {
     // F32 into xlns16
     auto stage_p = [&](uint32_t tot) __attribute__((always_inline)) {
         for (int j = threadIdx.x; j < rs; j += blockDim.x)
-            pc[j] = j < n ? (uint16_t)x16_from_f32(T.cvt16, T.rev16[x16_div(c[j], tot)]) : (uint16_t)0;
+            pc[j] = j < n ? (uint16_t)T.rho16[x16_div(c[j], tot)] : (uint16_t)0;
     };
     // The att output of dim d.  Past the last nonzero exp every p has one
     // code (all those exps are 0), so a product there has the log
