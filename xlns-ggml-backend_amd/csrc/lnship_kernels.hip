@@ -862,6 +862,7 @@ struct mm_args16 {
     const float *norm;
     float eps;
     uint32_t skew;
+    uint32_t rms_ik, rms_eps;   // the xlns16 codes of 1 / K and of eps (from the host's table)
     // non-null (XL launches): the activation is swiglu(xf, glu_up), the GLU
     // node before the mul_mat: up row n at glu_up + n * x_ld
     const float *glu_up;
@@ -1644,9 +1645,9 @@ __global__ __launch_bounds__(k_block) void k_rms32(const float *__restrict__ src
 // fourth wave runs the sum's chain.  The scale is an xlns16 code: the sum32
 // sum of the squares, narrowed to xlns16 (1/128 of a binade), then mean,
 // epsilon, square root and reciprocal.  The prediction sums the squares'
-// values in double and rounds the log to the nearest xlns16 step: that is
-// the narrowed sum unless the sum lies within the xlns32 chain's error of a
-// rounding boundary.  When the chain's scale differs from the predicted one,
+// values in F32 and rounds the log to the nearest xlns16 step: that is the
+// narrowed sum unless the sum lies within the xlns32 chain's error (and the
+// F32 sum's) of a rounding boundary.  When the chain's scale differs from the predicted one,
 // h is formed again from it and the chains run again, so the output is that
 // of the three nodes in every case.
 constexpr int k_rms_mm_rows = 3 * 64;   // chain lanes per workgroup (waves 0-2; wave 3 sums)
@@ -1662,45 +1663,67 @@ __global__ __launch_bounds__(k_block) void k_mm16_rms(mm_args16 a, dev_tables T)
     const int K = (int)a.K, kp = (int)a.kp;
     uint16_t *xl = reinterpret_cast<uint16_t *>(lds + mm_xl_offset<LNSHIP_SUM32>());   // h, as the chains read it
     uint16_t *sq = xl + kp + k_xl_pad / 2;                                              // the squares of x
-    __shared__ double s_part[k_block / 64];
+    __shared__ float s_part[k_block / 64];
     __shared__ uint32_t s_inv[2];   // the predicted scale, the chain's
     // the squares of x's codes into LDS (the sum's addends), their values
-    // summed per wave
-    double part = 0.0;
-    for (int k = threadIdx.x; k < kp; k += k_block) {
-        uint32_t q = 0;
-        if (k < K) {
-            const uint32_t c = x16_from_f32(T.cvt16, a.xf[k]);
-            q = x16_mul(c, c);
-            part += exp2(((double)(int)(q & k16_logmask) - (double)k16_one) * (1.0 / 128.0));
-        }
+    // summed per wave (in F32: the prediction only has to land on the
+    // chain's xlns16 step, 1/128 of a binade, and a miss costs a rerun).
+    // The codes of x and of the norm row for k < RK k_block stay in
+    // registers for forming h (past that they are formed again there).
+    constexpr int RK = 4;
+    uint32_t cxr[RK], cnr[RK];
+    float part = 0.0f;
+    auto square = [&](int k, uint32_t c) {
+        const uint32_t q = x16_mul(c, c);
+        part += exp2f((float)((int)(q & k16_logmask) - (int)k16_one) * (1.0f / 128.0f));
         sq[k] = (uint16_t)q;
+    };
+#pragma unroll
+    for (int i = 0; i < RK; i++) {
+        const int k = (int)threadIdx.x + i * k_block;
+        cxr[i] = k < K ? x16_from_f32(T.cvt16, a.xf[k]) : 0u;
+        cnr[i] = k < K ? x16_from_f32(T.cvt16, a.norm[k]) : 0u;
+    }
+#pragma unroll
+    for (int i = 0; i < RK; i++) {
+        const int k = (int)threadIdx.x + i * k_block;
+        if (k < K) square(k, cxr[i]);
+        else if (k < kp) sq[k] = 0;
+    }
+    for (int k = (int)threadIdx.x + RK * k_block; k < kp; k += k_block) {
+        if (k < K) square(k, x16_from_f32(T.cvt16, a.xf[k]));
+        else sq[k] = 0;
     }
     for (int o = 32; o > 0; o >>= 1) part += __shfl_xor(part, o);
     if ((threadIdx.x & 63) == 0) s_part[threadIdx.x >> 6] = part;
     __syncthreads();
-    // the scale from the narrowed sum (the rms_norm node's tail, as k_rms16)
+    // the scale from the narrowed sum (the rms_norm node's tail, as k_rms16;
+    // the codes of 1 / K and eps come from the host's conversion table)
     auto scale_of = [&](uint32_t sum) {
-        const uint32_t mean = x16_mul(sum, x16_from_f32(T.cvt16, 1.0f / (float)K));
-        return x16_recip(x16_sqrt(x16_add_g(T.gauss16, mean, x16_from_f32(T.cvt16, a.eps))));
+        const uint32_t mean = x16_mul(sum, a.rms_ik);
+        return x16_recip(x16_sqrt(x16_add_g(T.gauss16, mean, a.rms_eps)));
     };
     if (threadIdx.x == 0) {
-        double S = 0.0;
+        float S = 0.0f;
         for (int i = 0; i < k_block / 64; i++) S += s_part[i];
         // the nearest xlns16 code of S, within the code range
-        const double l = S > 0.0 ? floor(log2(S) * 128.0 + 0.5) + (double)k16_one : 0.0;
-        const uint32_t sum = (uint32_t)fmin(fmax(l, 0.0), (double)k16_logmask);
+        const float l = S > 0.0f ? floorf(log2f(S) * 128.0f + 0.5f) + (float)k16_one : 0.0f;
+        const uint32_t sum = (uint32_t)fminf(fmaxf(l, 0.0f), (float)k16_logmask);
         s_inv[0] = (scale_of(sum) + a.skew) & 0xffffu;
     }
     __syncthreads();
     // h = the MUL node's output from the rms_norm node's, each through F32
-    // as between graph nodes, then into xlns16 as the mul_mat converts its
-    // activations (k past K: zero)
+    // as between graph nodes (rho16: cvt16 of rev16), then into xlns16 as
+    // the mul_mat converts its activations (k past K: zero)
     auto stage_h = [&](uint32_t inv) {
-        for (int k = threadIdx.x; k < kp; k += k_block) {
+#pragma unroll
+        for (int i = 0; i < RK; i++) {
+            const int k = (int)threadIdx.x + i * k_block;
+            if (k < kp) xl[k] = k < K ? (uint16_t)T.rho16[x16_mul(T.rho16[x16_mul(cxr[i], inv)], cnr[i])] : 0;
+        }
+        for (int k = (int)threadIdx.x + RK * k_block; k < kp; k += k_block) {
             uint32_t h = 0;
             if (k < K) {
-                // the two F32 round trips through rho16 (cvt16 of rev16)
                 const uint32_t y = T.rho16[x16_mul(x16_from_f32(T.cvt16, a.xf[k]), inv)];
                 h = T.rho16[x16_mul(y, x16_from_f32(T.cvt16, a.norm[k]))];
             }
@@ -2411,7 +2434,7 @@ __global__ __launch_bounds__(k_block) void k_attn16(attn_args a, dev_tables T) {
     uint16_t *pc = c + rs;                                                     // KQV's activation codes
     __shared__ int32_t s_max;
     __shared__ uint32_t s_tot, s_tot2;   // the total (sum32: predicted, then the chain's)
-    __shared__ double s_part[k_block / 64];
+    __shared__ float s_part[k_block / 64];
     __shared__ int s_last;
     __shared__ uint32_t s_vmax[k_attn_tail_hd];   // per dim: the largest V log past the last nonzero exp
     const bool tail_stop = hd <= k_attn_tail_hd;
@@ -2528,23 +2551,24 @@ __global__ __launch_bounds__(k_block) void k_attn16(attn_args a, dev_tables T) {
     // sum32, with a wave beside the output chains' (head_dim <= 192): the
     // output chains start at once from a predicted total while that wave's
     // first lane runs the sum's chain, and run again when the total differs.
-    // The prediction sums the exps' values in double and rounds the log to
-    // the nearest xlns16 step, which is the chain's narrowed xlns32 sum
-    // unless that sum lies within the chain's error of a rounding boundary.
+    // The prediction sums the exps' values in F32 and rounds the log to the
+    // nearest xlns16 step, which is the chain's narrowed xlns32 sum unless
+    // that sum lies within the chain's error (and the F32 sum's) of a
+    // rounding boundary.
     const int sum_lane = (hd + 63) & ~63;
     if (MODE == LNSHIP_SUM32 && sum_lane < (int)blockDim.x) {
-        double part = 0.0;
+        float part = 0.0f;
         for (int j = threadIdx.x; j < n_eff; j += blockDim.x)
-            part += exp2(((double)(int)(c[j] & k16_logmask) - (double)k16_one) * (1.0 / 128.0));
+            part += exp2f((float)((int)(c[j] & k16_logmask) - (int)k16_one) * (1.0f / 128.0f));
         for (int o = 32; o > 0; o >>= 1) part += __shfl_xor(part, o);
         if ((threadIdx.x & 63) == 0) s_part[threadIdx.x >> 6] = part;
         if (tail_stop && n_eff < n) tail_vmax(0, (int)blockDim.x);
         __syncthreads();
         if (threadIdx.x == 0) {
-            double S = 0.0;
+            float S = 0.0f;
             for (int i = 0; i < k_block / 64; i++) S += s_part[i];
-            const double l = S > 0.0 ? floor(log2(S) * 128.0 + 0.5) + (double)k16_one : 0.0;
-            s_tot = ((uint32_t)fmin(fmax(l, 0.0), (double)k16_logmask) + a.skew) & 0xffffu;
+            const float l = S > 0.0f ? floorf(log2f(S) * 128.0f + 0.5f) + (float)k16_one : 0.0f;
+            s_tot = ((uint32_t)fminf(fmaxf(l, 0.0f), (float)k16_logmask) + a.skew) & 0xffffu;
         }
         __syncthreads();
         const uint32_t tot = s_tot;
@@ -3981,6 +4005,16 @@ int lnship16_rms_norm_mul_mat(int mode, const float *x, const float *norm_w, flo
     m.norm = norm_w;
     m.eps = eps;
     m.skew = g_predict_skew;
+    // the codes of 1 / K and of eps, as the device's conversion reads them
+    {
+        const uint16_t *cvt = static_cast<const uint16_t *>(lnship_host_table("cvt16", nullptr));
+        const float ik = 1.0f / (float)K;
+        uint32_t b;
+        std::memcpy(&b, &ik, 4);
+        m.rms_ik = cvt[b >> 15];
+        std::memcpy(&b, &eps, 4);
+        m.rms_eps = cvt[b >> 15];
+    }
     const int rows = narrow ? 3 * 16 : k_rms_mm_rows;
     const uint64_t wgs = (uint64_t)((M + rows - 1) / rows);
     if (wgs > 0x7fffffffu) return fail(LNSHIP_ERANGE, "rms_norm_mul_mat: grid too large%s");
