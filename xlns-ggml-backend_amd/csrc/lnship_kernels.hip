@@ -908,14 +908,48 @@ constexpr int k_xl_pad = 8 * 16;
 
 __device__ __forceinline__ uint32_t half16(uint32_t w, int hi) { return hi ? (w >> 16) : (w & 0xffffu); }
 
+// The first weights of lane m's chains (group 0, then the block of groups
+// 1 .. PF), as mm16_chains loads them.  A decode GEMV loads them before it
+// stages its tables, so that their HBM latency passes meanwhile.
+template <int PF>
+struct mm_head {
+    uint4 w0, w[PF];
+};
+// the weights of groups g0 .. g0 + PF - 1 of lane m in weight slice zw (past
+// the slice's last group: the last group again)
+template <int PF>
+__device__ __forceinline__ void mm16_wblock(const mm_args16 &a, int64_t m, int64_t zw, int g0, uint4 (&w)[PF]) {
+    // from the block's first group (a wave-uniform base, clamped to the
+    // slice's last group) at lane offset m * 16 plus p * (bytes between
+    // groups) for the block's group p, the offset capped at the last group's
+    const int last = (int)(a.kp >> 3) - 1;
+    const char *wsl = reinterpret_cast<const char *>(a.w + zw * a.w_slice);
+    const uint64_t gsb = (uint64_t)a.w_mstride * 16;
+    const int gb = min(g0, last);
+    const char *wb = wsl + (uint64_t)gb * gsb;
+    const uint32_t cap = (uint32_t)((uint64_t)(last - gb) * gsb) + (uint32_t)m * 16;
+#pragma unroll
+    for (int p = 0; p < PF; p++)
+        w[p] = *reinterpret_cast<const uint4 *>(wb + min((uint32_t)((uint64_t)m * 16 + (uint64_t)p * gsb), cap));
+}
+template <int PF>
+__device__ __forceinline__ mm_head<PF> mm16_head(const mm_args16 &a, int64_t m, int64_t zw) {
+    mm_head<PF> h;
+    h.w0 = *reinterpret_cast<const uint4 *>(a.w + zw * a.w_slice + m * 8);
+    mm16_wblock<PF>(a, m, zw, 1, h.w);
+    return h;
+}
+
 // The K-long chains of lane m (output row m of slice z) over columns
 // n0 .. n0 + nc: the weights from HBM, the activations from the LDS rows at
 // xl (XL) or the converted rows in scratch; each column's finished
-// accumulator (an xlns16 code) into res.
-template <int MODE, int NC, int PF, bool XL>
+// accumulator (an xlns16 code) into res.  HEAD: the first weights come
+// loaded in head.
+template <int MODE, int NC, int PF, bool XL, bool HEAD = false>
 __device__ __forceinline__ void mm16_chains(const mm_args16 &a, const dev_tables &T, const red16<MODE> &R,
                                             const uint16_t *xl, int64_t m, int64_t z, int64_t zw, int64_t zx,
-                                            int64_t n0, int nc, uint32_t (&res)[NC]) {
+                                            int64_t n0, int nc, uint32_t (&res)[NC],
+                                            const mm_head<PF> &head = mm_head<PF>{}) {
     const int kp = (int)a.kp;
     const uint16_t *ws = a.w + zw * a.w_slice + m * 8;
     const uint16_t *xs = a.x + (zx * a.N + n0) * a.kp;
@@ -1075,28 +1109,16 @@ __device__ __forceinline__ void mm16_chains(const mm_args16 &a, const dev_tables
         uint4 xq[NC];
 #pragma unroll
         for (int j = 0; j < NC; j++) xq[j] = load_x(j, 0);
-        const uint4 wq = load_w(0);
+        const uint4 wq = HEAD ? head.w0 : load_w(0);
         // groups 1 .. full-1 in blocks of PF, double-buffered: the loads of
         // block b + 1 are issued together before block b is accumulated
         uint4 wa[PF], wb[PF], xa[PF][NC], xb[PF][NC];
-        // A block's loads from bases that move once per block.  Weights: from
-        // the block's first group (a wave-uniform base, clamped to the slice's
-        // last group) at lane offset m * 16 plus p * (bytes between groups)
-        // for the block's group p, the offset capped at the last group's (the
-        // last block's prefetch past the slice rereads it).  Activations in
-        // LDS: at immediate offsets p * 16 from the block's base (the LDS copy
-        // has PF * 16 bytes of padding past its last column).
-        const char *wsl = reinterpret_cast<const char *>(a.w + zw * a.w_slice);
-        const uint64_t gsb = (uint64_t)wstride * 2;
-        uint32_t vo[PF];
-#pragma unroll
-        for (int p = 0; p < PF; p++) vo[p] = (uint32_t)((uint64_t)m * 16 + (uint64_t)p * gsb);
-        auto load_block = [&](uint4 (&w)[PF], uint4 (&x)[PF][NC], int g0) {
-            const int gb = min(g0, last);
-            const char *wb = wsl + (uint64_t)gb * gsb;
-            const uint32_t cap = (uint32_t)((uint64_t)(last - gb) * gsb) + (uint32_t)m * 16;
-#pragma unroll
-            for (int p = 0; p < PF; p++) w[p] = *reinterpret_cast<const uint4 *>(wb + min(vo[p], cap));
+        // A block's loads from bases that move once per block: the weights
+        // as mm16_wblock (the last block's prefetch past the slice rereads
+        // the last group); activations in LDS at immediate offsets p * 16
+        // from the block's base (the LDS copy has PF * 16 bytes of padding
+        // past its last column).
+        auto load_xblock = [&](uint4 (&x)[PF][NC], int g0) {
 #pragma unroll
             for (int j = 0; j < NC; j++) {
                 if constexpr (XL) {
@@ -1113,6 +1135,10 @@ __device__ __forceinline__ void mm16_chains(const mm_args16 &a, const dev_tables
                 }
             }
         };
+        auto load_block = [&](uint4 (&w)[PF], uint4 (&x)[PF][NC], int g0) {
+            mm16_wblock<PF>(a, m, zw, g0, w);
+            load_xblock(x, g0);
+        };
         // the next group of group p of a block is p + 1, or the first of the
         // other buffer (loaded before this block runs)
         auto run_block = [&](const uint4 (&w)[PF], const uint4 (&x)[PF][NC], const uint4 (&wo)[PF],
@@ -1121,7 +1147,13 @@ __device__ __forceinline__ void mm16_chains(const mm_args16 &a, const dev_tables
             for (int p = 0; p < PF; p++)
                 if (g0 + p < full) steps(w[p], x[p], p + 1 < PF ? w[p + 1] : wo[0], p + 1 < PF ? x[p + 1] : xo[0], 0, 8, false);
         };
-        load_block(wa, xa, 1);
+        if constexpr (HEAD) {
+#pragma unroll
+            for (int p = 0; p < PF; p++) wa[p] = head.w[p];
+            load_xblock(xa, 1);
+        } else {
+            load_block(wa, xa, 1);
+        }
         steps(wq, xq, wa[0], xa[0], -1, full > 0 ? 8 : tail, true);
         for (int g = 1; g < full; g += 2 * PF) {
             load_block(wb, xb, g + PF);
@@ -1155,7 +1187,6 @@ __global__ __launch_bounds__(k_block * CG) void k_mm16(mm_args16 a, dev_tables T
     extern __shared__ __align__(16) char lds[];
     // a widened launch: the workgroups between the working ones leave at once
     if (blockIdx.x & ((1u << a.xcd_sh) - 1u)) return;
-    const red16<MODE> R = stage_for<MODE, NC == 1>(T, lds);
     // CG column groups of k_block lanes each share the staged tables: group
     // c takes columns [nw + c NC, nw + (c + 1) NC) of the same k_block rows
     const int cg = CG == 1 ? 0 : (int)(threadIdx.x / k_block);
@@ -1168,6 +1199,18 @@ __global__ __launch_bounds__(k_block * CG) void k_mm16(mm_args16 a, dev_tables T
     const int kp = (int)a.kp;
     int64_t zw, zx;
     const bool slice_ok = mm_slices(a, z, i12, i13, zw, zx);
+    const int lane = (int)(threadIdx.x & 63u);
+    constexpr bool dup = W < 64 && MODE != LNSHIP_SUM32;   // a chain on 64 / W lanes
+    const int wr = dup ? lane / (64 / W) : lane;              // the lane's row in the wave
+    const int64_t m = W < 64 ? (int64_t)(blockIdx.x >> a.xcd_sh) * (k_block / 64 * W) + (threadIdx.x >> 6) * W + wr
+                             : (int64_t)(blockIdx.x >> a.xcd_sh) * k_block + (threadIdx.x % k_block);
+    const bool live = !(W < 64 && !dup && lane >= W) && m < a.M && nc > 0 && slice_ok;
+    // one-column launches: the chain's first weights loaded before the
+    // tables are staged (their HBM latency passes meanwhile)
+    constexpr bool head = NC == 1 && XL;
+    mm_head<PF> hw{};
+    if (head && live && a.K > 0) hw = mm16_head<PF>(a, m, zw);
+    const red16<MODE> R = stage_for<MODE, NC == 1>(T, lds);
     uint16_t *xl = reinterpret_cast<uint16_t *>(lds + mm_xl_offset<MODE>());
     if (XL) {
         // columns past N and k past K hold xlns16 zero
@@ -1216,12 +1259,7 @@ __global__ __launch_bounds__(k_block * CG) void k_mm16(mm_args16 a, dev_tables T
     }
     __syncthreads();
 
-    const int lane = (int)(threadIdx.x & 63u);
-    constexpr bool dup = W < 64 && MODE != LNSHIP_SUM32;   // a chain on 64 / W lanes
-    const int wr = dup ? lane / (64 / W) : lane;              // the lane's row in the wave
-    const int64_t m = W < 64 ? (int64_t)(blockIdx.x >> a.xcd_sh) * (k_block / 64 * W) + (threadIdx.x >> 6) * W + wr
-                             : (int64_t)(blockIdx.x >> a.xcd_sh) * k_block + (threadIdx.x % k_block);
-    if ((W < 64 && !dup && lane >= W) || m >= a.M || nc == 0 || !slice_ok) return;
+    if (!live) return;
     float *ds = a.dst + z * a.dst_slice + n0 * a.dst_ld + m;
     // output j of code c, with the fused ADD of the residual when there is
     // one: the F32 result and the residual through xlns16 (the result's
@@ -1239,7 +1277,7 @@ __global__ __launch_bounds__(k_block * CG) void k_mm16(mm_args16 a, dev_tables T
     }
 
     uint32_t res[NC];
-    mm16_chains<MODE, NC, PF, XL>(a, T, R, xl, m, z, zw, zx, n0, nc, res);
+    mm16_chains<MODE, NC, PF, XL, head>(a, T, R, xl, m, z, zw, zx, n0, nc, res, hw);
     if (dup && lane % (64 / W) != 0) return;   // one lane of a chain stores
 #pragma unroll
     for (int j = 0; j < NC; j++)
@@ -1659,6 +1697,12 @@ __global__ __launch_bounds__(k_block) void k_mm16_rms(mm_args16 a, dev_tables T)
     static_assert(k_block == k_rms_mm_rows + 64, "three chain waves and the sum's wave");
     extern __shared__ __align__(16) char lds[];
     if (blockIdx.x & ((1u << a.xcd_sh) - 1u)) return;   // as in k_mm16
+    const int lane = (int)(threadIdx.x & 63u);
+    const int64_t m = (int64_t)(blockIdx.x >> a.xcd_sh) * (3 * W) + (threadIdx.x >> 6) * W + lane;
+    const bool active = threadIdx.x < k_rms_mm_rows && lane < W && m < a.M;
+    // the chain's first weights before the tables (as in k_mm16)
+    mm_head<PF> hw{};
+    if (active) hw = mm16_head<PF>(a, m, 0);
     const red16<LNSHIP_SUM32> R = stage_for<LNSHIP_SUM32, true>(T, lds);
     const int K = (int)a.K, kp = (int)a.kp;
     uint16_t *xl = reinterpret_cast<uint16_t *>(lds + mm_xl_offset<LNSHIP_SUM32>());   // h, as the chains read it
@@ -1733,15 +1777,12 @@ __global__ __launch_bounds__(k_block) void k_mm16_rms(mm_args16 a, dev_tables T)
     uint32_t inv = s_inv[0];
     stage_h(inv);
     __syncthreads();
-    const int lane = (int)(threadIdx.x & 63u);
-    const int64_t m = (int64_t)(blockIdx.x >> a.xcd_sh) * (3 * W) + (threadIdx.x >> 6) * W + lane;
-    const bool active = threadIdx.x < k_rms_mm_rows && lane < W && m < a.M;
     uint32_t res[1] = {0};
     // pass 0 with the predicted scale; a second pass only when the chain's
     // scale differs (every thread reads the same two words after the barrier)
     for (int pass = 0;; pass++) {
         if (active) {
-            mm16_chains<LNSHIP_SUM32, 1, PF, true>(a, T, R, xl, m, 0, 0, 0, 0, 1, res);
+            mm16_chains<LNSHIP_SUM32, 1, PF, true, true>(a, T, R, xl, m, 0, 0, 0, 0, 1, res, hw);
         } else if (pass == 0 && threadIdx.x == k_rms_mm_rows) {
             uint32_t st = 0;
             typename red16<LNSHIP_SUM32>::acc_t acc = R.start(0u, st);
