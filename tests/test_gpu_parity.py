@@ -421,11 +421,12 @@ def _narrow_cases(rng):
 @pytest.mark.parametrize("mode", MODES)
 def test_gemv_narrow_waves_columns(ln, mode, width):
     # the single-chain GEMV with several columns (the batched decode's) in
-    # every mode, with 16 rows per wave and with 64, against the oracle
+    # every mode, on the narrow waves the launch picks (4 to 32 rows; 300,
+    # 4608 and 24576 chains) and with 64 rows (width 0), against the oracle
     L = ln.lib()
     prev = L.lnship_test_decode_width(width)
     try:
-        for (K, M, N) in ((576, 576, 8), (1536, 100, 3)):
+        for (K, M, N) in ((576, 576, 8), (1536, 100, 3), (64, 3072, 8)):
             _mm_case(ln, mode, K, M, N, seed=K + N)
     finally:
         L.lnship_test_decode_width(prev)

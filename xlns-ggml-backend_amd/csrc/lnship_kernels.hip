@@ -3168,12 +3168,17 @@ static int g_decode_w = 16;
 // SIMD: the chains are bound by their dependent steps, and a step with only
 // the first 16 lanes of its wave active is shorter
 static bool narrow_mm(int64_t chains, int cus) { return g_decode_w == 16 && chains <= (int64_t)cus * 4 * 16; }
-// rows per wave of a single-chain lpvip GEMV (its chains on all 64 lanes):
-// fewer chains per wave branch apart less often, while the launch still
-// fits one wave per SIMD; 0: 64-row waves
-static int lpvip_w(int64_t chains, int cus) {
-    if (!narrow_mm(chains, cus)) return 0;
-    return chains <= (int64_t)cus * 4 * 4 ? 4 : chains <= (int64_t)cus * 4 * 8 ? 8 : 16;
+// rows per wave of a single-chain GEMV outside sum32 (its chains on all 64
+// lanes): fewer chains per wave branch apart less often, while the launch
+// still fits one wave per SIMD (two waves on a SIMD cost more: lpvip up|gate
+// of 8 columns, 24576 chains: 170.6 us on 64-row waves, 161.9 on 32, 190.1
+// on 16 at two per SIMD); lpvip narrows further than 16; 0: 64-row waves
+static int narrow_w(int mode, int64_t chains, int cus) {
+    if (g_decode_w != 16) return 0;
+    const int64_t slots = (int64_t)cus * 4;
+    if (mode == LNSHIP_LPVIP && chains <= slots * 4) return 4;
+    if (mode == LNSHIP_LPVIP && chains <= slots * 8) return 8;
+    return chains <= slots * 16 ? 16 : chains <= slots * 32 ? 32 : 0;
 }
 
 // the grid of nh attention heads placed by attn_head: every block up to the
@@ -3242,17 +3247,17 @@ static int dispatch_mm16(const mm_args16 &m, const dev_tables &T, int64_t nslice
             case 8: return launch_mm16_x<MODE, 8, 1>(m, T, nslices, sh.xl, cus, st);
             case 4: return launch_mm16_x<MODE, 4, 1>(m, T, nslices, sh.xl, cus, st);
             default:
-                if constexpr (MODE == LNSHIP_LPVIP) {
-                    if (sh.xl) switch (lpvip_w(m.M * m.N * nslices, cus)) {
-                            case 4: return launch_mm16<MODE, 1, true, 1, 4>(m, T, nslices, cus, st);
-                            case 8: return launch_mm16<MODE, 1, true, 1, 8>(m, T, nslices, cus, st);
-                            case 16: return launch_mm16<MODE, 1, true, 1, 16>(m, T, nslices, cus, st);
-                            default: break;
-                        }
-                } else {
-                    if (sh.xl && narrow_mm(m.M * m.N * nslices, cus))
-                        return launch_mm16<MODE, 1, true, 1, 16>(m, T, nslices, cus, st);
-                }
+                if (sh.xl) switch (narrow_w(MODE, m.M * m.N * nslices, cus)) {
+                        case 4:
+                            if constexpr (MODE == LNSHIP_LPVIP) return launch_mm16<MODE, 1, true, 1, 4>(m, T, nslices, cus, st);
+                            break;
+                        case 8:
+                            if constexpr (MODE == LNSHIP_LPVIP) return launch_mm16<MODE, 1, true, 1, 8>(m, T, nslices, cus, st);
+                            break;
+                        case 16: return launch_mm16<MODE, 1, true, 1, 16>(m, T, nslices, cus, st);
+                        case 32: return launch_mm16<MODE, 1, true, 1, 32>(m, T, nslices, cus, st);
+                        default: break;
+                    }
                 return launch_mm16_x<MODE, 1, 1>(m, T, nslices, sh.xl, cus, st);
         }
     }
