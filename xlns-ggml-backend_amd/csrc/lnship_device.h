@@ -29,6 +29,7 @@ struct dev_tables {
     const uint16_t *lfsr_seq;
     const uint16_t *lfsr_log;
     const uint16_t *rho16;  // rho16[c] = cvt16 of rev16[c]: a code through F32 and back, as between graph nodes
+    const double *lpdb;     // lpvip's db tables (host_tables::lpdb)
 };
 
 __device__ __forceinline__ uint32_t f32_bits(float f) { return __float_as_uint(f); }

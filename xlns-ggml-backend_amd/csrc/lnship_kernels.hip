@@ -656,14 +656,36 @@ __device__ __forceinline__ int32_t lpvip_sb(uint32_t d) {
     uint64_t corr = ((uint64_t)u * (uint64_t)(0x800000u - u)) >> 23;
     return (int32_t)(u + (uint32_t)((corr * 0x2B8u) >> 11));
 }
-__device__ __forceinline__ int32_t lpvip_db(uint32_t d) {
-    if (d < 0x800000u) {
-        // log2(1 - exp2(-x)) for the reference's log(1 - pow(2, -x)) / log(2):
-        // the same integer for every d of this branch (checked against the
-        // host's libm over all of them), at 60 % of the cost
-        double v = log2(1.0 - exp2(-(double)d / 8388608.0)) * 8388608.0;
-        return (int32_t)floor(v + 0.5);
-    }
+// The reference's round(2^23 log(1 - pow(2, -x)) / log(2)), x = d / 2^23,
+// for 0 < d < 2^23, from tables (lp: host_tables::lpdb): 2^-x as
+// 2^(-k/256) e^(-r ln 2) (r < 1/256, Taylor to degree 5), y = 1 - 2^-x with
+// one rounding, then log2 y as e + log2(1 + j/256) + log2(1 + s) with
+// s = m / (1 + j/256) - 1 < 2^-8 (degree 6); the polynomials by Estrin's
+// scheme.  About half the dependent FP64 latency of log2(1 - exp2(-x)) with
+// the library's functions, and the same integer for every d (every one of
+// the 2^23 - 1 checked on the GPU against the oracle); contraction is off, so
+// every caller compiles the same operations.
+__device__ __forceinline__ int32_t lpvip_db_near(const double *lp, uint32_t d) {
+#pragma clang fp contract(off)
+    const double *E = lp, *IV = lp + k_lp_n, *LG = lp + 2 * k_lp_n;
+    const double z = (double)(d & 0x7fffu) * (-0.69314718055994530942 / 8388608.0);   // -r ln 2
+    const double z2 = z * z;
+    const double pa = fma(z, 1.0 / 6.0, 0.5), pb = fma(z, 1.0 / 120.0, 1.0 / 24.0);
+    const double p = fma(z2, fma(z2, pb, pa), 1.0 + z);
+    const double y = fma(-E[d >> 15], p, 1.0);
+    const int e = __builtin_amdgcn_frexp_exp(y);                    // y = m 2^e, m in [0.5, 1)
+    const double m2 = __builtin_amdgcn_frexp_mant(y) * 2.0;         // [1, 2)
+    const uint32_t j = (uint32_t)(__double2hiint(m2) >> 12) & 255u; // its top 8 mantissa bits
+    const double sv = fma(m2, IV[j], -1.0);                          // [0, 2^-8)
+    constexpr double c = 1.4426950408889634074;                      // 1 / ln 2
+    const double s2 = sv * sv;
+    const double u0 = fma(sv, -c / 2.0, c), u1 = fma(sv, -c / 4.0, c / 3.0), u2 = fma(sv, -c / 6.0, c / 5.0);
+    const double h = fma(s2, fma(s2, u2, u1), u0);
+    const double lg = (double)(e - 1) + fma(sv, h, LG[j]);
+    return (int32_t)floor(lg * 8388608.0 + 0.5);
+}
+__device__ __forceinline__ int32_t lpvip_db(const double *lp, uint32_t d) {
+    if (d < 0x800000u) return lpvip_db_near(lp, d);
     uint32_t u = mitchell_exp2_neg(d);
     uint64_t sq = ((uint64_t)u * u) >> 23;
     return -(int32_t)(u + (uint32_t)((sq * 0xB8Au) >> 12));
@@ -671,6 +693,7 @@ __device__ __forceinline__ int32_t lpvip_db(uint32_t d) {
 
 template <>
 struct red16<LNSHIP_LPVIP> {
+    const double *lp;   // LDS: the db tables (host_tables::lpdb)
     using acc_t = acc_ls;
     __device__ __forceinline__ acc_t start(uint32_t v, uint32_t &) const {
         return {(v & k16_logmask) << 16, (v & k16_sign) << 16};
@@ -686,7 +709,7 @@ struct red16<LNSHIP_LPVIP> {
             return;
         }
         int32_t adj = 0;
-        if (d < k32_esszer) adj = usedb ? lpvip_db(d) : lpvip_sb(d);
+        if (d < k32_esszer) adj = usedb ? lpvip_db(lp, d) : lpvip_sb(d);
         const uint32_t s = mx + (uint32_t)adj;
         a.l = (s & k32_sign) ? ((s & k32_one) ? 0u : k32_logmask) : s;
         a.s = sgn;
@@ -781,8 +804,9 @@ __device__ __forceinline__ red16<LNSHIP_SUM32> stage_tables<LNSHIP_SUM32>(const 
     return stage_x32(T.lds32, lds);
 }
 template <>
-__device__ __forceinline__ red16<LNSHIP_LPVIP> stage_tables<LNSHIP_LPVIP>(const dev_tables &, char *) {
-    return red16<LNSHIP_LPVIP>{};
+__device__ __forceinline__ red16<LNSHIP_LPVIP> stage_tables<LNSHIP_LPVIP>(const dev_tables &T, char *lds) {
+    stage_copy<4>(reinterpret_cast<int4 *>(lds), reinterpret_cast<const int4 *>(T.lpdb), 3 * k_lp_n * 8 / 16);
+    return red16<LNSHIP_LPVIP>{reinterpret_cast<const double *>(lds)};
 }
 // the pair image of the positive-sum adder
 __device__ __forceinline__ pos_tab stage_pos32(const dev_tables &T, char *lds) {
@@ -805,7 +829,7 @@ template <int MODE>
 constexpr int lds_tables_bytes() {
     return MODE == LNSHIP_BASE ? 2 * k16_gauss_n * 2 :
            MODE == LNSHIP_MONTE ? 4 * k16_mc_n * 4 :
-           MODE == LNSHIP_SUM32 ? k_lds_tab32 : 0;
+           MODE == LNSHIP_SUM32 ? k_lds_tab32 : 3 * k_lp_n * 8;
 }
 // The LDS tables of the xlns16 row kernels (rms_norm, soft_max): their sum32
 // chains add only positive values (squares, exps), over the positive-sum
@@ -2983,9 +3007,9 @@ __global__ void k_set_rows(const char *__restrict__ src, strided4 gs, const char
 
 // lpvip's db at d0 .. d0 + n - 1 (a test hook: the db function is checked
 // over its whole exact-branch domain against the host)
-__global__ void k_lpvip_db_range(uint32_t d0, uint32_t n, int32_t *__restrict__ out) {
+__global__ void k_lpvip_db_range(uint32_t d0, uint32_t n, int32_t *__restrict__ out, const double *lp) {
     for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += blockDim.x * gridDim.x)
-        out[i] = lpvip_db(d0 + i);
+        out[i] = lpvip_db(lp, d0 + i);
 }
 
 // The xlns32 adder over its LDS tables on code pairs, in the form the kernels
@@ -3618,6 +3642,7 @@ int lnship_init(void) {
     if (int rc = upload(g_host->gauss16, 2 * k16_gauss_n, &T.gauss16)) return rc;
     if (int rc = upload(g_host->gauss16m, 4 * k16_mc_n, &T.gauss16m)) return rc;
     if (int rc = upload(g_host->exp16, 1u << 16, &T.exp16)) return rc;
+    if (int rc = upload(g_host->lpdb, 3 * k_lp_n, &T.lpdb)) return rc;
     if (int rc = upload(g_host->sig16, 1u << 16, &T.sig16)) return rc;
     if (int rc = upload(g_host->tab32, (size_t)k32_tab_n, &T.tab32)) return rc;
     {
@@ -4480,7 +4505,8 @@ int lnship_lpvip_db_range(uint32_t d0, uint32_t n, int32_t *out, void *stream) {
     if (!s) return LNSHIP_ENOINIT;
     if (!out) return fail(LNSHIP_EINVAL, "lpvip_db_range: null output%s");
     if (n == 0) return 0;
-    hipLaunchKernelGGL(k_lpvip_db_range, dim3(grid_for(n, 4)), dim3(k_block), 0, (hipStream_t)stream, d0, n, out);
+    hipLaunchKernelGGL(k_lpvip_db_range, dim3(grid_for(n, 4)), dim3(k_block), 0, (hipStream_t)stream, d0, n, out,
+                       s->T.lpdb);
     LNSHIP_HIP(hipGetLastError());
     return 0;
 }

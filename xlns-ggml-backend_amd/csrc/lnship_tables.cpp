@@ -132,6 +132,11 @@ void build_host_tables(host_tables &t) {
     }
     t.lfsr_seq[65535] = t.lfsr_seq[0];
     t.lfsr_log[0] = 0;
+    for (int k = 0; k < k_lp_n; k++) {
+        t.lpdb[k] = std::exp2(-(double)k / 256.0);
+        t.lpdb[k_lp_n + k] = 1.0 / (1.0 + (double)k / 256.0);
+        t.lpdb[2 * k_lp_n + k] = std::log2(1.0 + (double)k / 256.0);
+    }
 }
 
 }  // namespace lnship

@@ -46,6 +46,8 @@ constexpr int k32_off_db = k32_off_sbf + k32_sb_fn;
 constexpr int k32_off_dbf = k32_off_db + k32_db_n;
 constexpr int k32_tab_n = k32_off_dbf + k32_db_fn;                             // 27076
 
+constexpr int k_lp_n = 256;   // entries of each lpvip db table
+
 struct host_tables {
     uint16_t cvt16[1u << 17];   // float bits >> 15 -> xlns16
     float    rev16[1u << 16];   // xlns16 -> float
@@ -60,6 +62,9 @@ struct host_tables {
     int32_t  tab32[k32_tab_n];  // xlns32 adder tables, layout above
     uint16_t lfsr_seq[65536];   // LFSR state after i steps from state 1 (i < 65535)
     uint16_t lfsr_log[65536];   // inverse of lfsr_seq
+    // lpvip's Gaussian log for opposite signs below one binade, evaluated
+    // from tables: 2^(-k/256), 1/(1 + j/256) and log2(1 + j/256), k, j < 256
+    double lpdb[3 * k_lp_n];
 };
 
 // Fills t (a ~1.1 MB object); deterministic.
