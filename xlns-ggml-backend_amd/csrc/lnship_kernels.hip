@@ -698,21 +698,29 @@ struct red16<LNSHIP_LPVIP> {
     __device__ __forceinline__ acc_t start(uint32_t v, uint32_t &) const {
         return {(v & k16_logmask) << 16, (v & k16_sign) << 16};
     }
+    // lpvip_sb and lpvip_db formed side by side, without branches, but for
+    // the FP64 Gaussian log (opposite signs below one binade), which only
+    // lanes that need it run; exact cancellation (d = 0, opposite signs)
+    // gives +0
     __device__ __forceinline__ void add_ls(acc_t &a, uint32_t tl16, uint32_t ts16, uint32_t &) const {
         const uint32_t tl = tl16 << 16, ts = ts16 << 16;
         const uint32_t mx = max(a.l, tl), d = mx - min(a.l, tl);
         const uint32_t sgn = a.l > tl ? a.s : ts;
-        const uint32_t usedb = a.s ^ ts;
-        if (d == 0 && usedb) {
-            a.l = 0;
-            a.s = 0;
-            return;
-        }
-        int32_t adj = 0;
-        if (d < k32_esszer) adj = usedb ? lpvip_db(lp, d) : lpvip_sb(d);
+        const bool usedb = (a.s ^ ts) != 0;
+        // Mitchell's antilog of -d (0 from 31 binades on), then sb's and db's
+        // corrections of it
+        const uint32_t u = ((0x1000000u - (d & 0x7fffffu)) >> 1) >> min(d >> 23, 31u);
+        const uint64_t pc = ((uint64_t)u * (uint64_t)(0x800000u - u)) >> 23, pq = ((uint64_t)u * u) >> 23;
+        const int32_t sb = (int32_t)(u + (uint32_t)((pc * 0x2B8u) >> 11));
+        const int32_t dbm = -(int32_t)(u + (uint32_t)((pq * 0xB8Au) >> 12));
+        int32_t adj = usedb ? dbm : sb;
+        if (usedb && d - 1u < 0x7fffffu) adj = lpvip_db_near(lp, d);
+        adj = d < k32_esszer ? adj : 0;
         const uint32_t s = mx + (uint32_t)adj;
-        a.l = (s & k32_sign) ? ((s & k32_one) ? 0u : k32_logmask) : s;
-        a.s = sgn;
+        const uint32_t l = (s & k32_sign) ? ((s & k32_one) ? 0u : k32_logmask) : s;
+        const bool cancel = d == 0 && usedb;
+        a.l = cancel ? 0u : l;
+        a.s = cancel ? 0u : sgn;
     }
     __device__ __forceinline__ void add(acc_t &a, uint32_t v, uint32_t &st) const { add_ls(a, v & k16_logmask, v & k16_sign, st); }
     __device__ __forceinline__ uint32_t finish(const acc_t &a) const { return (a.s | a.l) >> 16; }
