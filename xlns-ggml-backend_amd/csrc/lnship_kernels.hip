@@ -1386,6 +1386,8 @@ __global__ __launch_bounds__(k_block * CG) void k_mm32(mm_args32 a, dev_tables T
         return grp{p[0], p[1]};
     };
     acc_ls acc[NC]{};
+    uint32_t k_lm = k32_logmask;   // the mask in a register (short encodings)
+    asm("" : "+v"(k_lm));
     auto steps = [&](const grp &wq, const grp (&xq)[NC], int u0, int u1) {
         const uint32_t wv[8] = {wq.lo.x, wq.lo.y, wq.lo.z, wq.lo.w, wq.hi.x, wq.hi.y, wq.hi.z, wq.hi.w};
         if constexpr (NC == 1) {
@@ -1395,24 +1397,36 @@ __global__ __launch_bounds__(k_block * CG) void k_mm32(mm_args32 a, dev_tables T
                                     xq[0].hi.x, xq[0].hi.y, xq[0].hi.z, xq[0].hi.w};
             const bool first = u0 < 0;
             const int ub = first ? 0 : u0;
-            uint32_t t = ub < u1 ? x32_mul(wv[ub], xv[ub]) : 0u;
+            // the product of step u (x32_mul) as its log and its sign, formed
+            // apart: the sign in the first round trip of the step before, the
+            // log (the fields added, clamped to the field) in its second
+            auto plog = [&](int u) {
+                return min(max((wv[u] & k_lm) + (xv[u] & k_lm), k32_one), k32_one + k32_logmask) - k32_one;
+            };
+            auto psgn = [&](int u) { return (wv[u] ^ xv[u]) & k32_sign; };
+            uint32_t tl = ub < u1 ? plog(ub) : 0u, ts = ub < u1 ? psgn(ub) : 0u;
             // uf: the opposite-signs flag (bit 31) of the pending addition
-            uint32_t uf = (acc[0].s ^ t) & k32_sign;
+            uint32_t uf = acc[0].s ^ ts;
 #pragma unroll
             for (int u = 0; u < 8; u++) {
                 if (u >= ub && u < u1) {
-                    uint32_t tn = 0;
+                    uint32_t ntl = 0, nts = 0;
                     auto next = [&] {
-                        if (u + 1 < u1) tn = x32_mul(wv[u + 1], xv[u + 1]);
-                        return tn & k32_sign;
+                        if (u + 1 < u1) nts = psgn(u + 1);
+                        return nts;
+                    };
+                    auto post = [&] {
+                        if (u + 1 < u1) ntl = plog(u + 1);
                     };
                     if (first && u == 0) {
-                        acc[0] = {t & k32_logmask, t & k32_sign};
-                        uf = (t & k32_sign) ^ next();
+                        acc[0] = {tl, ts};
+                        uf = ts ^ next();
+                        post();
                     } else {
-                        uf = x32_add_step(R.O, acc[0], t & k32_logmask, t & k32_sign, uf, next, [] {});
+                        uf = x32_add_step(R.O, acc[0], tl, ts, uf, next, post);
                     }
-                    t = tn;
+                    tl = ntl;
+                    ts = nts;
                 }
             }
             return;
