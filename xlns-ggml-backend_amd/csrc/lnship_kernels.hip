@@ -1066,15 +1066,21 @@ __device__ __forceinline__ void mm16_chains(const mm_args16 &a, const dev_tables
             for (int u = 0; u < 8; u++) {
                 if (u >= ub && u < u1) {
                     uint32_t ntl = 0, nts = 0;
-                    // the next step's product, from its pair; after step 7,
-                    // the next group's step 0 from the carried pair
+                    // the next step's product, from its pair (after step 7,
+                    // the next group's step 0 from the carried pair): its
+                    // sign in this step's first round trip, its log in the
+                    // second
                     auto next = [&] {
-                        if (u + 1 < u1) half(u + 1, pl[(u + 1) >> 1], ps[(u + 1) >> 1], ntl, nts);
-                        else if (u == 7) half(0, c_pl, c_ps, ntl, nts);
+                        uint32_t l_unused;
+                        if (u + 1 < u1) half(u + 1, pl[(u + 1) >> 1], ps[(u + 1) >> 1], l_unused, nts);
+                        else if (u == 7) half(0, c_pl, c_ps, l_unused, nts);
                         return nts;
                     };
                     auto post = [&] {
+                        uint32_t s_unused;
                         if ((u & 1) == 0 && u < 6) pair(ww[(u >> 1) + 1], xx[(u >> 1) + 1], pl[(u >> 1) + 1], ps[(u >> 1) + 1]);
+                        if (u + 1 < u1) half(u + 1, pl[(u + 1) >> 1], ps[(u + 1) >> 1], ntl, s_unused);
+                        else if (u == 7) half(0, c_pl, c_ps, ntl, s_unused);
                         if (u == 6) pair(wn.x, xn[0].x, c_pl, c_ps);
                     };
                     if (first && u == 0) {
