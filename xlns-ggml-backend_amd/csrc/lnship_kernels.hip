@@ -646,6 +646,19 @@ struct red16<LNSHIP_SUM32> {
 
 // LPVIP: ROM-less xlns32 adder (Mitchell antilog + corrected Mitchell log;
 // the exact Gaussian log within one binade of the db singularity).
+// The low 32 bits and bits 32-47 of the product of two 24-bit operands
+// (v_mul_u32_u24, v_mul_hi_u32_u24: full rate, where a 64-bit product takes
+// a quarter-rate multiply-add)
+__device__ __forceinline__ uint32_t mul_u24(uint32_t a, uint32_t b) {
+    uint32_t r;
+    asm("v_mul_u32_u24 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+    return r;
+}
+__device__ __forceinline__ uint32_t mulhi_u24(uint32_t a, uint32_t b) {
+    uint32_t r;
+    asm("v_mul_hi_u32_u24 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+    return r;
+}
 __device__ __forceinline__ uint32_t mitchell_exp2_neg(uint32_t d) {
     uint32_t q = d >> 23, r = d & 0x7fffffu;
     if (q >= 31) return 0;
@@ -708,11 +721,14 @@ struct red16<LNSHIP_LPVIP> {
         const uint32_t sgn = a.l > tl ? a.s : ts;
         const bool usedb = (a.s ^ ts) != 0;
         // Mitchell's antilog of -d (0 from 31 binades on), then sb's and db's
-        // corrections of it
+        // corrections of it, all products of 24-bit operands (u <= 2^23):
+        // u (2^23 - u) >> 23 < 2^21, so its product with 0x2B8 fits 32 bits;
+        // u^2 >> 23 <= 2^23, its product with 0xB8A taken as 48 bits
         const uint32_t u = ((0x1000000u - (d & 0x7fffffu)) >> 1) >> min(d >> 23, 31u);
-        const uint64_t pc = ((uint64_t)u * (uint64_t)(0x800000u - u)) >> 23, pq = ((uint64_t)u * u) >> 23;
-        const int32_t sb = (int32_t)(u + (uint32_t)((pc * 0x2B8u) >> 11));
-        const int32_t dbm = -(int32_t)(u + (uint32_t)((pq * 0xB8Au) >> 12));
+        const uint32_t pc = (uint32_t)(((uint64_t)u * (uint64_t)(0x800000u - u)) >> 23);
+        const uint32_t pq = (uint32_t)(((uint64_t)u * u) >> 23);
+        const int32_t sb = (int32_t)(u + (mul_u24(pc, 0x2B8u) >> 11));
+        const int32_t dbm = -(int32_t)(u + __builtin_amdgcn_alignbit(mulhi_u24(pq, 0xB8Au), mul_u24(pq, 0xB8Au), 12));
         int32_t adj = usedb ? dbm : sb;
         if (usedb && d - 1u < 0x7fffffu) adj = lpvip_db_near(lp, d);
         adj = d < k32_esszer ? adj : 0;
