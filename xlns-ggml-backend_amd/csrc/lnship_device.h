@@ -19,7 +19,7 @@ struct dev_tables {
     const uint16_t *cvt16;
     const float *rev16;
     const int16_t *gauss16;
-    const int32_t *gauss16m;
+    const int32_t *gauss16m;   // the Monte adder's LDS image (host_tables::gauss16m, db's dither entries as (-F, 63))
     const uint16_t *exp16;
     const uint16_t *sig16;
     const int32_t *tab32;

@@ -390,18 +390,20 @@ struct red16<LNSHIP_MONTE> {
     __device__ __forceinline__ acc_t start(uint32_t v, uint32_t &) const { return {v & k16_logmask, v & k16_sign}; }
     // One LFSR step; below the dither range the base table's adjustment, from
     // it on one ulp toward the smaller operand with probability F(d)/64,
-    // decided by the top 6 bits of the new state.
+    // decided by the top 6 bits r of the new state: sb adds (F + r) >> 6,
+    // db (64 - F + ~r) >> 6, here (-F + (63 - r)) >> 6 from the image's
+    // (-F, 63).  The larger log is added scaled by 64 in the same add, so
+    // after the table read only a mask, an add, a shift and the clamp remain.
     __device__ __forceinline__ void add_ls(acc_t &a, uint32_t tl, uint32_t ts, uint32_t &st) const {
         st = lfsr_step(st);
         const uint32_t d = absdiff(a.l, tl), mx = max(a.l, tl);
         const uint32_t usedb = a.s ^ ts;
         const int32_t *gms = gm + (usedb >> 14);
         const int2 em = *reinterpret_cast<const int2 *>(gms + (min(d, (uint32_t)k16_mc_end) << 2));
-        // the draw: r for sb, -r - 1 for db, nothing below the dither range
-        const int32_t r = (int32_t)(st >> 10);
-        const int32_t adj = (em.x + ((r ^ (em.y >> 31)) & em.y)) >> 6;
+        const uint32_t r = (st >> 10) ^ (usedb ? 63u : 0u);
+        const int32_t sum = (int32_t)(mx << 6) + em.x + (int32_t)(r & (uint32_t)em.y);
         const uint32_t ns = a.l > tl ? a.s : ts;
-        a.l = (uint32_t)min(max((int32_t)mx + adj, 0), (int32_t)k16_logmask);
+        a.l = (uint32_t)min(max(sum >> 6, 0), (int32_t)k16_logmask);
         a.s = (d == 0 && usedb) ? 0u : ns;
     }
     __device__ __forceinline__ void add(acc_t &a, uint32_t v, uint32_t &st) const { add_ls(a, v & k16_logmask, v & k16_sign, st); }
@@ -3684,7 +3686,18 @@ int lnship_init(void) {
         if (int rc = upload(rho.data(), rho.size(), &T.rho16)) return rc;
     }
     if (int rc = upload(g_host->gauss16, 2 * k16_gauss_n, &T.gauss16)) return rc;
-    if (int rc = upload(g_host->gauss16m, 4 * k16_mc_n, &T.gauss16m)) return rc;
+    {
+        // the Monte adder's LDS image: host_tables::gauss16m with db's dither
+        // entries (64 - F, -1) as (-F, 63): the adder then draws 63 - r for
+        // db, so that every entry's second word is a plain mask (0 or 63)
+        std::vector<int32_t> mimg(g_host->gauss16m, g_host->gauss16m + 4 * k16_mc_n);
+        for (int d = 0; d < k16_mc_n; d++)
+            if (mimg[4 * d + 3] == -1) {
+                mimg[4 * d + 2] -= 64;
+                mimg[4 * d + 3] = 63;
+            }
+        if (int rc = upload(mimg.data(), mimg.size(), &T.gauss16m)) return rc;
+    }
     if (int rc = upload(g_host->exp16, 1u << 16, &T.exp16)) return rc;
     if (int rc = upload(g_host->lpdb, 3 * k_lp_n, &T.lpdb)) return rc;
     if (int rc = upload(g_host->sig16, 1u << 16, &T.sig16)) return rc;
