@@ -1143,6 +1143,29 @@ __device__ __forceinline__ void mm16_chains(const mm_args16 &a, const dev_tables
             }
             return;
         }
+        if constexpr (NC == 1) {
+            // one chain: the products of steps 2i and 2i + 1 together in the
+            // two 16-bit halves (as the sum32 chain forms them), then each
+            // step's log and sign from its half
+            const uint32_t xx[4] = {xq[0].x, xq[0].y, xq[0].z, xq[0].w};
+            uint32_t pl[4], ps[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                if (2 * i + 1 < u0 || 2 * i >= u1) continue;
+                pl[i] = pk_min_u16(pk_sub_sat_u16((ww[i] & k_lm) + (xx[i] & k_lm), 0x40004000u), 0x7fff7fffu);
+                ps[i] = ww[i] ^ xx[i];
+            }
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                if (u >= u0 && u < u1) {
+                    const uint32_t tl = (u & 1) ? pl[u >> 1] >> 16 : pl[u >> 1] & 0xffffu;
+                    const uint32_t ts = ((u & 1) ? ps[u >> 1] >> 16 : ps[u >> 1]) & k16_sign;
+                    if (u == 0 && u0 < 0) acc[0] = R.start(ts | tl, st[0]);
+                    else R.add_ls(acc[0], tl, ts, st[0]);
+                }
+            }
+            return;
+        }
 #pragma unroll
         for (int u = 0; u < 8; u++) {
             if (u >= u0 && u < u1) {
