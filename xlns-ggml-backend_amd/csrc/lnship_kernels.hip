@@ -386,6 +386,7 @@ struct red16<LNSHIP_BASE> {
 template <>
 struct red16<LNSHIP_MONTE> {
     const int32_t *gm;   // LDS: (sb e, sb m, db e, db m) per distance
+    uint32_t gb;         // gm's LDS byte address
     using acc_t = acc_ls;
     __device__ __forceinline__ acc_t start(uint32_t v, uint32_t &) const { return {v & k16_logmask, v & k16_sign}; }
     // One LFSR step; below the dither range the base table's adjustment, from
@@ -394,17 +395,19 @@ struct red16<LNSHIP_MONTE> {
     // db (64 - F + ~r) >> 6, here (-F + (63 - r)) >> 6 from the image's
     // (-F, 63).  The larger log is added scaled by 64 in the same add, so
     // after the table read only a mask, an add, a shift and the clamp remain.
+    // The sign: the larger operand's (bit 15 of tl - a.l is set iff a.l >
+    // tl), + for exact cancellation (bit 15 of d - 1 is set iff d = 0).
     __device__ __forceinline__ void add_ls(acc_t &a, uint32_t tl, uint32_t ts, uint32_t &st) const {
         st = lfsr_step(st);
         const uint32_t d = absdiff(a.l, tl), mx = max(a.l, tl);
-        const uint32_t usedb = a.s ^ ts;
-        const int32_t *gms = gm + (usedb >> 14);
-        const int2 em = *reinterpret_cast<const int2 *>(gms + (min(d, (uint32_t)k16_mc_end) << 2));
-        const uint32_t r = (st >> 10) ^ (usedb ? 63u : 0u);
-        const int32_t sum = (int32_t)(mx << 6) + em.x + (int32_t)(r & (uint32_t)em.y);
-        const uint32_t ns = a.l > tl ? a.s : ts;
+        const uint32_t usedb = a.s ^ ts;   // 0 or k16_sign
+        // row min(d, end) of 16 bytes, db's pair 8 bytes in
+        const i32x2 em = lds_ld2(lds_at4(min(d, (uint32_t)k16_mc_end), gb + (usedb >> 12)));
+        // the draw r, or 63 - r for db (r xor all ones under the mask 63)
+        const uint32_t x = ((st >> 10) ^ (uint32_t)((int32_t)(usedb << 16) >> 31)) & (uint32_t)em.y;
+        const int32_t sum = (int32_t)(mx << 6) + em.x + (int32_t)x;
+        a.s = bfi(tl - a.l, a.s, ts) & ~(usedb & (d - 1u));
         a.l = (uint32_t)min(max(sum >> 6, 0), (int32_t)k16_logmask);
-        a.s = (d == 0 && usedb) ? 0u : ns;
     }
     __device__ __forceinline__ void add(acc_t &a, uint32_t v, uint32_t &st) const { add_ls(a, v & k16_logmask, v & k16_sign, st); }
     __device__ __forceinline__ uint32_t finish(const acc_t &a) const { return a.s | a.l; }
@@ -784,7 +787,7 @@ __device__ __forceinline__ red16<LNSHIP_MONTE> stage_tables<LNSHIP_MONTE>(const 
     // cancellation; the sign is cleared by the caller).  Thread 0 copied
     // that entry itself, so its own later store wins.
     if (threadIdx.x == 0) g[2] = -(1 << 30);
-    return red16<LNSHIP_MONTE>{g};
+    return red16<LNSHIP_MONTE>{g, lds_addr(g)};
 }
 // img: one of the two images built at init (lds32_image): the multi-chain
 // step's, or the single-chain step's
