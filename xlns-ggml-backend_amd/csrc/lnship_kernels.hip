@@ -380,6 +380,14 @@ struct red16<LNSHIP_BASE> {
         a.s = (d == 0 && usedb) ? 0u : ns;
     }
     __device__ __forceinline__ void add(acc_t &a, uint32_t v, uint32_t &st) const { add_ls(a, v & k16_logmask, v & k16_sign, st); }
+    // add() of a positive v to a positive sum (sums of squares, of exps): sb
+    // only, the sign stays +
+    __device__ __forceinline__ void add_pos(acc_t &a, uint32_t v, uint32_t &) const {
+        const uint32_t tl = v & k16_logmask;
+        const uint32_t d = absdiff(a.l, tl), mx = max(a.l, tl);
+        const int32_t adj = *reinterpret_cast<const int16_t *>(g + (min(d, (uint32_t)k16_esszer + 1) << 2));
+        a.l = (uint32_t)min(max((int32_t)mx + adj, 0), (int32_t)k16_logmask);
+    }
     __device__ __forceinline__ uint32_t finish(const acc_t &a) const { return a.s | a.l; }
 };
 
@@ -410,6 +418,16 @@ struct red16<LNSHIP_MONTE> {
         a.l = (uint32_t)min(max(sum >> 6, 0), (int32_t)k16_logmask);
     }
     __device__ __forceinline__ void add(acc_t &a, uint32_t v, uint32_t &st) const { add_ls(a, v & k16_logmask, v & k16_sign, st); }
+    // add() of a positive v to a positive sum: sb's half of the row, no
+    // sign work (the same draws)
+    __device__ __forceinline__ void add_pos(acc_t &a, uint32_t v, uint32_t &st) const {
+        st = lfsr_step(st);
+        const uint32_t tl = v & k16_logmask;
+        const uint32_t d = absdiff(a.l, tl), mx = max(a.l, tl);
+        const i32x2 em = lds_ld2(lds_at4(min(d, (uint32_t)k16_mc_end), gb));
+        const int32_t sum = (int32_t)(mx << 6) + em.x + (int32_t)((st >> 10) & (uint32_t)em.y);
+        a.l = (uint32_t)min(max(sum >> 6, 0), (int32_t)k16_logmask);
+    }
     __device__ __forceinline__ uint32_t finish(const acc_t &a) const { return a.s | a.l; }
 };
 
@@ -744,6 +762,16 @@ struct red16<LNSHIP_LPVIP> {
         a.s = cancel ? 0u : sgn;
     }
     __device__ __forceinline__ void add(acc_t &a, uint32_t v, uint32_t &st) const { add_ls(a, v & k16_logmask, v & k16_sign, st); }
+    // add() of a positive v to a positive sum: sb only, the sign stays +
+    __device__ __forceinline__ void add_pos(acc_t &a, uint32_t v, uint32_t &) const {
+        const uint32_t tl = (v & k16_logmask) << 16;
+        const uint32_t mx = max(a.l, tl), d = mx - min(a.l, tl);
+        const uint32_t u = ((0x1000000u - (d & 0x7fffffu)) >> 1) >> min(d >> 23, 31u);
+        const uint32_t pc = (uint32_t)(((uint64_t)u * (uint64_t)(0x800000u - u)) >> 23);
+        const int32_t adj = d < k32_esszer ? (int32_t)(u + (mul_u24(pc, 0x2B8u) >> 11)) : 0;
+        const uint32_t s = mx + (uint32_t)adj;
+        a.l = (s & k32_sign) ? ((s & k32_one) ? 0u : k32_logmask) : s;
+    }
     __device__ __forceinline__ uint32_t finish(const acc_t &a) const { return (a.s | a.l) >> 16; }
 };
 
@@ -1556,6 +1584,8 @@ __device__ __forceinline__ void chain16(const RED &R, typename RED::acc_t &acc, 
                 } else if constexpr (std::is_same<RED, red16<LNSHIP_SUM32>>::value) {
                     const uint32_t v = half16(w[u >> 1], u & 1);
                     R.add_lat(acc, (v & k16_logmask) << 16, (v & k16_sign) << 16, [] {});
+                } else if constexpr (POS) {
+                    R.add_pos(acc, half16(w[u >> 1], u & 1), st);
                 } else {
                     R.add(acc, half16(w[u >> 1], u & 1), st);
                 }
