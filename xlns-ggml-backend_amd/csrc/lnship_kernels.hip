@@ -2556,16 +2556,27 @@ __device__ __forceinline__ void row_chain(const red16<MODE> &R, typename red16<M
             if (g > gl) break;
             const uint4 xq = *reinterpret_cast<const uint4 *>(x + 8 * g);
             const uint32_t ww[4] = {b[p].x, b[p].y, b[p].z, b[p].w}, xx[4] = {xq.x, xq.y, xq.z, xq.w};
+            // the products two at a time in 16-bit halves (xlns16_mul: the
+            // log fields added, less the offset with unsigned saturation,
+            // capped at 0x7fff; the signs xor'ed)
+            uint32_t pl[4], ps[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                pl[i] = pk_min_u16(pk_sub_sat_u16((ww[i] & 0x7fff7fffu) + (xx[i] & 0x7fff7fffu), 0x40004000u),
+                                   0x7fff7fffu);
+                ps[i] = ww[i] ^ xx[i];
+            }
 #pragma unroll
             for (int u = 0; u < 8; u++) {
                 const int k = 8 * g + u;
                 if (k < k0) continue;
                 if (k >= k1) break;
-                const uint32_t t = x16_mul(half16(ww[u >> 1], u & 1), half16(xx[u >> 1], u & 1));
-                if (k == 0) acc = R.start(t, st);
+                const uint32_t tl = (u & 1) ? pl[u >> 1] >> 16 : pl[u >> 1] & 0xffffu;
+                const uint32_t ts = ((u & 1) ? ps[u >> 1] >> 16 : ps[u >> 1]) & k16_sign;
+                if (k == 0) acc = R.start(ts | tl, st);
                 else if constexpr (MODE == LNSHIP_SUM32)
-                    R.add_lat(acc, (t & k16_logmask) << 16, (t & k16_sign) << 16, [] {});
-                else R.add(acc, t, st);
+                    R.add_lat(acc, tl << 16, ts << 16, [] {});
+                else R.add_ls(acc, tl, ts, st);
             }
         }
     };
