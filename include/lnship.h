@@ -321,6 +321,23 @@ int lnship16_attn_decode_seqs(int mode, const lnship_attn_args *args, const lnsh
  * the attention nodes one by one. */
 int lnship16_rope_attn_decode(int mode, const lnship_qkv_store_args *store, const lnship_attn_args *args,
                               void *stream);
+/* lnship16_rope_store_kv for the one decode token of each of n_seq sequences
+ * and lnship16_attn_decode_seqs in one launch, every mode (Monte with the
+ * three nodes' starts in seqs): the workgroup of sequence s's query head h
+ * rotates that query and stores its kv head's key and value of sequence s's
+ * current cell, then runs the attention.  Token s is row s of store->qkv
+ * (store->qkv_ld floats apart) at position store->pos[s]; store->ntok must
+ * be n_seq and store->seq null, its caches, heads and slices those of args,
+ * and, for n_seq > 1, store->seq_stride = n_head_kv * k_slice = n_head_kv *
+ * v_slice (sequence s's cells where the attention reads them).  dst and both
+ * caches come out bit-identical to lnship16_rope_store_kv (seq = 0, 1, ...,
+ * n_seq - 1, the same seq_stride) followed by lnship16_attn_decode_seqs.  A
+ * position outside the cache is recorded as in lnship16_rope_store_kv and
+ * that sequence's dst rows are not written.  No single counterpart in the
+ * reference (ROPE, the cache copies and the attention nodes run one by
+ * one). */
+int lnship16_rope_attn_decode_seqs(int mode, const lnship_qkv_store_args *store, const lnship_attn_args *args,
+                                   const lnship_attn_seqs *seqs, void *stream);
 /* The same for the LNS32 backend (xlns32 codes in the caches, in the layout
  * lnship32_rope_store_kv writes): lns32_mul_mat for kq, lns32_soft_max, then
  * lns32_mul_mat for kqv (src32/lns32-ops.cpp:98-144, :384-436), F32 between

@@ -304,6 +304,47 @@ def test_rope_attn_decode_checks_its_store_arguments_first(lnship):
     assert L.lnship16_rope_attn_decode(lnship.SUM32, None, ctypes.byref(a), None) == EINVAL
 
 
+def test_rope_attn_decode_seqs_checks_its_store_arguments_first(lnship):
+    # lnship16_rope_attn_decode_seqs: one token per sequence in the store
+    # arguments, no seq map, sequence s's cells where the attention reads
+    # them (seq_stride = n_head_kv * k_slice); every mode, Monte included;
+    # mismatches are refused before any device call
+    L = lnship.lib()
+    fake = ctypes.c_void_p(0x1000).value   # never dereferenced: the checks come first
+    EINVAL, ENOINIT = -1, -3   # include/lnship.h: enum lnship_error
+    nh, nkv, hd, n_ctx, nseq = 9, 3, 64, 256, 4
+
+    def triple():
+        a = lnship.AttnArgs()
+        a.k_cache, a.v_cache, a.dst, a.mask = fake, fake + 64, fake + 128, fake + 192
+        a.cache_m, a.k_slice, a.v_slice, a.scale = n_ctx, hd * n_ctx, hd * n_ctx, 0.125
+        a.n_head, a.n_head_kv, a.head_dim, a.n_kv = nh, nkv, hd, 200
+        q = lnship.QkvStoreArgs(fake, (nh + 2 * nkv) * hd, fake + 256, nseq, nh, nkv, hd, hd, fake + 320, None,
+                                fake, fake + 64, n_ctx, hd * n_ctx, hd * n_ctx, None, nkv * hd * n_ctx)
+        return q, a, lnship.attn_seqs(nseq, (1, 2, 3))
+
+    for mode in (lnship.BASE, lnship.MONTE, lnship.LPVIP, lnship.SUM32):
+        q, a, sq = triple()
+        assert L.lnship16_rope_attn_decode_seqs(mode, ctypes.byref(q), ctypes.byref(a), ctypes.byref(sq),
+                                                None) == ENOINIT, mode
+    for field, value in (("ntok", nseq - 1), ("ntok", 1), ("seq", fake), ("seq_stride", nkv * hd * n_ctx + 8),
+                         ("n_head", nh - 1), ("head_dim", 60), ("rope_n_dims", 63),
+                         ("qkv_ld", (nh + 2 * nkv) * hd - 1), ("k_cache", fake + 8), ("cache_m", n_ctx + 8),
+                         ("v_slice", 8), ("qkv", None), ("pos", None), ("cos_sin", None)):
+        q, a, sq = triple()
+        setattr(q, field, value)
+        assert L.lnship16_rope_attn_decode_seqs(lnship.MONTE, ctypes.byref(q), ctypes.byref(a), ctypes.byref(sq),
+                                                None) == EINVAL, field
+    q, a, sq = triple()
+    assert L.lnship16_rope_attn_decode_seqs(lnship.SUM32, ctypes.byref(q), ctypes.byref(a), None, None) == EINVAL
+    assert L.lnship16_rope_attn_decode_seqs(lnship.SUM32, None, ctypes.byref(a), ctypes.byref(sq), None) == EINVAL
+    # one sequence: seq_stride is not read
+    q, a, sq = triple()
+    q.ntok, q.seq_stride, sq.n_seq = 1, 0, 1
+    assert L.lnship16_rope_attn_decode_seqs(lnship.MONTE, ctypes.byref(q), ctypes.byref(a), ctypes.byref(sq),
+                                            None) == ENOINIT
+
+
 def test_attn_decode_seqs_checks_arguments_first(lnship):
     # lnship16_attn_decode_seqs runs every mode, Monte with the three nodes'
     # starts; its arguments and the sequence count are checked before any

@@ -958,6 +958,89 @@ def test_rope_attn_decode_equals_two_launches(ln, mode, n_kv, nd, hd, pos):
     same_bits(g_att, w_att, f"rope attn decode {mode} n_kv={n_kv}")
 
 
+@pytest.mark.parametrize("mode,nseq,n_kv,nd,hd", [
+    ("monte", 1, 256, 64, 64), ("monte", 8, 512, 64, 64), ("monte", 3, 77, 32, 64), ("base", 3, 256, 64, 64),
+    ("lpvip", 8, 320, 64, 64), ("sum32", 8, 512, 64, 64), ("sum32", 2, 60, 72, 72)])
+def test_rope_attn_decode_seqs_equals_two_launches(ln, mode, nseq, n_kv, nd, hd):
+    # lnship16_rope_attn_decode_seqs against lnship16_rope_store_kv (one token
+    # per sequence, seq = 0..n_seq-1) then lnship16_attn_decode_seqs with the
+    # same Monte starts: the attention output and both whole caches bit for
+    # bit; the sequences at different positions (the first past the attended
+    # cells: stored, not read), qkv rows wider than the heads
+    import ctypes
+    rng = np.random.default_rng(2000 + 10 * nseq + n_kv + nd)
+    L, st = ln.lib(), ln._stream()
+    m = O.MODES[mode]
+    P = lambda t: ctypes.c_void_p(t.data_ptr())
+    nh, nkv, n_ctx = 9, 3, 768
+    print(f"\n[rope attn decode seqs] {mode} n_seq={nseq} n_kv={n_kv} rope dims={nd} head_dim={hd}", flush=True)
+    nqkv = (nh + 2 * nkv) * hd
+    ld = nqkv + 8
+    qkv = dev((rng.standard_normal(nseq * ld) * 2).astype(np.float32))
+    rt = np.empty(n_ctx * nd, np.float32)
+    ln.check(L.lnship_rope_table(ctypes.c_float(10000.0), nd, n_ctx, ctypes.c_void_p(rt.ctypes.data)))
+    cs = dev(rt)
+    pos = [int(x) for x in rng.integers(max(0, n_kv // 3), n_kv, nseq)]
+    pos[0] = n_kv + 5
+    posd = dev(np.array(pos, np.int32))
+    seq_ids = torch.arange(nseq, dtype=torch.int32, device="cuda")
+    kf = (rng.standard_normal((nseq * nkv, n_ctx, hd)) * 0.5).astype(np.float32)
+    vf = (rng.standard_normal((nseq * nkv, hd, n_ctx)) * 0.5).astype(np.float32)
+    kslice, vslice = ln.kp(hd) * n_ctx, ln.kp(n_ctx) * hd
+    maskf = np.where(np.arange(n_kv)[None, :] <= np.array(pos)[:, None], 0.0, -np.inf).astype(np.float32)
+    mask = dev(maskf)
+    seeds = (4242, 999, 31337)
+    outs = []
+    for fused in (False, True):
+        kc, vc = ln.pack16(dev(kf)), ln.pack16(dev(vf))
+        q = torch.full((nseq * nh * hd,), 7.0, dtype=torch.float32, device="cuda")
+        got = torch.full((nseq * nh * hd,), float("nan"), device="cuda")
+        qs = ln.QkvStoreArgs(P(qkv), ld, P(posd), nseq, nh, nkv, hd, nd, P(cs), P(q), P(kc), P(vc), n_ctx, kslice,
+                             vslice, None if fused else P(seq_ids), nkv * kslice)
+        a = ln.AttnArgs(P(q), P(kc), P(vc), n_ctx, kslice, vslice, P(mask), 0.125, P(got), nh, nkv, hd, n_kv)
+        sq = ln.attn_seqs(nseq, seeds)
+        if fused:
+            ln.check(L.lnship16_rope_attn_decode_seqs(m, ctypes.byref(qs), ctypes.byref(a), ctypes.byref(sq), st))
+        else:
+            ln.check(L.lnship16_rope_store_kv(ctypes.byref(qs), st))
+            ln.check(L.lnship16_attn_decode_seqs(m, ctypes.byref(a), ctypes.byref(sq), st))
+        outs.append((host(got), host(kc), host(vc)))
+    (w_att, w_k, w_v), (g_att, g_k, g_v) = outs
+    assert np.array_equal(g_k, w_k) and np.array_equal(g_v, w_v), "caches"
+    assert not np.array_equal(g_k, host(ln.pack16(dev(kf)))), "the cells were stored"
+    same_bits(g_att, w_att, f"rope attn decode seqs {mode} n_seq={nseq} n_kv={n_kv}")
+
+
+def test_rope_attn_decode_seqs_position_out_of_range(ln):
+    # a sequence at a position at or beyond the cache is recorded as an index
+    # error; its caches and dst rows are left alone, the other sequence runs
+    import ctypes
+    L, st = ln.lib(), ln._stream()
+    P = lambda t: ctypes.c_void_p(t.data_ptr())
+    nh, nkv, hd, n_ctx, n_kv, nseq = 2, 1, 16, 16, 8, 2
+    nqkv = (nh + 2 * nkv) * hd
+    qkv = dev(np.ones(nseq * nqkv, np.float32))
+    rt = np.empty(n_ctx * hd, np.float32)
+    ln.check(L.lnship_rope_table(ctypes.c_float(10000.0), hd, n_ctx, ctypes.c_void_p(rt.ctypes.data)))
+    cs = dev(rt)
+    posd = dev(np.array([3, n_ctx], np.int32))
+    kc = torch.full((nseq * hd * n_ctx,), 0x1234, dtype=torch.int16, device="cuda")
+    vc = torch.full((nseq * hd * n_ctx,), 0x1234, dtype=torch.int16, device="cuda")
+    got = torch.full((nseq * nh * hd,), 7.0, device="cuda")
+    mask = dev(np.zeros(nseq * n_kv, np.float32))
+    bad = ctypes.c_int64(0)
+    L.lnship_index_error(ctypes.byref(bad), st)   # clear
+    qs = ln.QkvStoreArgs(P(qkv), nqkv, P(posd), nseq, nh, nkv, hd, hd, P(cs), None, P(kc), P(vc), n_ctx, hd * n_ctx,
+                         hd * n_ctx, None, hd * n_ctx)
+    a = ln.AttnArgs(None, P(kc), P(vc), n_ctx, hd * n_ctx, hd * n_ctx, P(mask), 0.25, P(got), nh, nkv, hd, n_kv)
+    sq = ln.attn_seqs(nseq)
+    ln.check(L.lnship16_rope_attn_decode_seqs(O.SUM32, ctypes.byref(qs), ctypes.byref(a), ctypes.byref(sq), st))
+    assert L.lnship_index_error(ctypes.byref(bad), st) == 1 and bad.value == n_ctx
+    k, v, g = host(kc), host(vc), host(got)
+    assert np.all(k[hd * n_ctx:] == 0x1234) and np.all(v[hd * n_ctx:] == 0x1234) and np.all(g[nh * hd:] == 7.0)
+    assert np.any(k[:hd * n_ctx] != 0x1234) and np.all(np.isfinite(g[:nh * hd])) and np.any(g[:nh * hd] != 7.0)
+
+
 def test_rope_attn_decode_position_out_of_range(ln):
     # a position at or beyond the cache is recorded as an index error, and
     # neither the caches nor dst are written

@@ -2359,35 +2359,43 @@ struct attn_args {
     uint32_t mseed[3];
     const uint16_t *mstate;
     uint64_t moff[3];
+    // with qkv: floats between the QKV rows of consecutive sequences (row s
+    // is sequence s's token, at position pos[s], its cells in the caches at
+    // s nhkv k_slice and s nhkv v_slice, where the attention reads them)
+    int64_t qld;
 };
 
-// The rope of head h's query into xq (its xlns16 codes, through F32 as the
-// ROPE node writes them and the kq mul_mat converts them) and the stores of
-// kv head kv's rotated key and value of the current cell, exactly as
-// k_rope_store_kv makes them for one token.  Every query head of a kv group
-// stores that group's cell, with the same codes, before its chains read the
-// caches.  false (nothing done, the fault recorded) for a position outside
-// the cache.
-__device__ __forceinline__ bool attn_rope_store(const attn_args &a, const dev_tables &T, int h, int kv, uint16_t *xq) {
+// The rope of head h's query of sequence sqn into xq (its xlns16 codes,
+// through F32 as the ROPE node writes them and the kq mul_mat converts them)
+// and the stores of kv head kv's rotated key and value of that sequence's
+// current cell, exactly as k_rope_store_kv makes them for its token.  Every
+// query head of a kv group stores that group's cell, with the same codes,
+// before its chains read the caches.  false (nothing done, the fault
+// recorded) for a position outside the cache.
+__device__ __forceinline__ bool attn_rope_store(const attn_args &a, const dev_tables &T, int h, int kv, int sqn,
+                                                uint16_t *xq) {
     const fmt16 F{T};
     const int hd = a.hd, nd = a.rope_n_dims, half = nd / 2;
     const int64_t cache_m = a.k_gs / 8;
-    const int64_t p = a.pos[0];
+    const int32_t *pos = a.pos + sqn;
+    const int64_t p = pos[0];
     if (p < 0 || p >= cache_m) {
         if (threadIdx.x == 0) index_fault(a.err, p);
         return false;
     }
-    const float *xk = a.qkv + (int64_t)a.nh * hd, *xv = xk + (int64_t)a.nhkv * hd;
-    const int64_t ld = (int64_t)(a.nh + 2 * a.nhkv) * hd;
+    const float *row = a.qkv + (int64_t)sqn * a.qld;
+    const float *xk = row + (int64_t)a.nh * hd, *xv = xk + (int64_t)a.nhkv * hd;
+    uint16_t *kc = const_cast<uint16_t *>(a.k) + (int64_t)sqn * a.nhkv * a.k_slice;
+    uint16_t *vc = const_cast<uint16_t *>(a.v) + (int64_t)sqn * a.nhkv * a.v_slice;
     for (int i = threadIdx.x; i < 2 * hd; i += blockDim.x) {
         if (i < hd)
-            store_kv_item(F, (int64_t)kv * hd + i, xk, ld, a.pos, a.nhkv, hd, nd, a.cos_sin,
-                          const_cast<uint16_t *>(a.k), cache_m, a.k_slice, 0, (const int32_t *)nullptr, 0, a.err);
+            store_kv_item(F, (int64_t)kv * hd + i, xk, a.qld, pos, a.nhkv, hd, nd, a.cos_sin, kc, cache_m, a.k_slice,
+                          0, (const int32_t *)nullptr, 0, a.err);
         else
-            store_kv_item(F, (int64_t)kv * hd + (i - hd), xv, ld, a.pos, a.nhkv, hd, 0, a.cos_sin,
-                          const_cast<uint16_t *>(a.v), cache_m, a.v_slice, 1, (const int32_t *)nullptr, 0, a.err);
+            store_kv_item(F, (int64_t)kv * hd + (i - hd), xv, a.qld, pos, a.nhkv, hd, 0, a.cos_sin, vc, cache_m,
+                          a.v_slice, 1, (const int32_t *)nullptr, 0, a.err);
     }
-    const float *xr = a.qkv + (int64_t)h * hd, *cs = a.cos_sin + p * half * 2;
+    const float *xr = row + (int64_t)h * hd, *cs = a.cos_sin + p * half * 2;
     for (int j = threadIdx.x; j < half + (hd - nd); j += blockDim.x) {
         if (j < half) {
             int64_t i0, i1;
@@ -2623,7 +2631,7 @@ __global__ __launch_bounds__(k_block) void k_attn16(attn_args a, dev_tables T) {
     for (int d = threadIdx.x; d < k_attn_tail_hd; d += blockDim.x) s_vmax[d] = 0;
     if (a.qkv) {
         // (the position is one value for the whole workgroup)
-        if (!attn_rope_store(a, T, h, kv, xq)) return;
+        if (!attn_rope_store(a, T, h, kv, sqn, xq)) return;
     } else {
         for (int k = threadIdx.x; k < hp; k += blockDim.x)
             xq[k] = k < hd ? (uint16_t)x16_from_f32(T.cvt16, a.q[(int64_t)hh * hd + k]) : (uint16_t)0;
@@ -4338,23 +4346,59 @@ int lnship16_attn_decode_seqs(int mode, const lnship_attn_args *a, const lnship_
     return attn16_launch(mode, m, a->n_head * q->n_seq, s->T, (hipStream_t)stream);
 }
 
+// The store arguments of a rope-fused attention over n_seq sequences: the
+// same heads and caches as the attention's, one token per sequence (row s
+// of qkv, qkv_ld floats apart), no seq map: sequence s's cells lie at
+// s n_head_kv k_slice and s n_head_kv v_slice, where the attention reads
+// them, so seq_stride must say so when there is more than one
+static bool rope_attn_store_ok(const lnship_qkv_store_args *q, const lnship_attn_args *a, int64_t n_seq) {
+    return q && q->qkv && q->pos && q->cos_sin && q->ntok == n_seq && !q->seq && q->n_head == a->n_head &&
+           q->n_head_kv == a->n_head_kv && q->head_dim == a->head_dim && q->head_dim % 8 == 0 &&
+           q->rope_n_dims > 0 && q->rope_n_dims % 2 == 0 && q->rope_n_dims <= q->head_dim &&
+           q->qkv_ld >= (q->n_head + 2 * q->n_head_kv) * q->head_dim && q->k_cache == a->k_cache &&
+           q->v_cache == a->v_cache && q->cache_m == a->cache_m && q->k_slice == a->k_slice &&
+           q->v_slice == a->v_slice &&
+           (n_seq == 1 || (q->seq_stride == a->n_head_kv * a->k_slice && q->seq_stride == a->n_head_kv * a->v_slice));
+}
+
+static attn_args rope_attn_args(const lnship_qkv_store_args *q, const lnship_attn_args *a, const device_state *s) {
+    attn_args m{nullptr, (const uint16_t *)a->k_cache, (const uint16_t *)a->v_cache, a->cache_m * 8,
+                a->k_slice, a->head_dim * 8, a->v_slice,
+                a->mask, a->scale, a->dst, (int)a->head_dim, (int)a->n_kv, (int)(a->n_head / a->n_head_kv),
+                g_predict_skew, q->qkv, q->pos, q->cos_sin, q->rope_n_dims, (int)a->n_head,
+                (int)a->n_head_kv, s->index_err, 1};
+    m.qld = q->qkv_ld;
+    return m;
+}
+
 int lnship16_rope_attn_decode(int mode, const lnship_qkv_store_args *q, const lnship_attn_args *a, void *stream) {
     // arguments and sizes first: they need no device
     if (int rc = attn16_check(mode, a, false)) return rc;
-    if (!q || !q->qkv || !q->pos || !q->cos_sin || q->ntok != 1 || q->seq || q->n_head != a->n_head ||
-        q->n_head_kv != a->n_head_kv || q->head_dim != a->head_dim || q->head_dim % 8 || q->rope_n_dims <= 0 ||
-        q->rope_n_dims % 2 || q->rope_n_dims > q->head_dim ||
-        q->qkv_ld < (q->n_head + 2 * q->n_head_kv) * q->head_dim || q->k_cache != a->k_cache ||
-        q->v_cache != a->v_cache || q->cache_m != a->cache_m || q->k_slice != a->k_slice || q->v_slice != a->v_slice)
+    if (!rope_attn_store_ok(q, a, 1))
         return fail(LNSHIP_EINVAL, "rope_attn_decode: the store arguments do not match the attention's%s");
     device_state *s = state();
     if (!s) return LNSHIP_ENOINIT;
-    const attn_args m{nullptr, (const uint16_t *)a->k_cache, (const uint16_t *)a->v_cache, a->cache_m * 8,
-                      a->k_slice, a->head_dim * 8, a->v_slice,
-                      a->mask, a->scale, a->dst, (int)a->head_dim, (int)a->n_kv, (int)(a->n_head / a->n_head_kv),
-                      g_predict_skew, q->qkv, q->pos, q->cos_sin, q->rope_n_dims, (int)a->n_head,
-                      (int)a->n_head_kv, s->index_err, 1};
-    return attn16_launch(mode, m, a->n_head, s->T, (hipStream_t)stream);
+    return attn16_launch(mode, rope_attn_args(q, a, s), a->n_head, s->T, (hipStream_t)stream);
+}
+
+int lnship16_rope_attn_decode_seqs(int mode, const lnship_qkv_store_args *q, const lnship_attn_args *a,
+                                   const lnship_attn_seqs *sq, void *stream) {
+    // arguments and sizes first: they need no device
+    if (int rc = attn16_check(mode, a, false, true)) return rc;
+    if (!sq || sq->n_seq <= 0 || a->n_head * sq->n_seq > 0x7fffff)
+        return fail(LNSHIP_EINVAL, "rope_attn_decode_seqs: bad sequence count%s");
+    if (!rope_attn_store_ok(q, a, sq->n_seq))
+        return fail(LNSHIP_EINVAL, "rope_attn_decode_seqs: the store arguments do not match the attention's%s");
+    device_state *s = state();
+    if (!s) return LNSHIP_ENOINIT;
+    attn_args m = rope_attn_args(q, a, s);
+    m.nseq = (int)sq->n_seq;
+    for (int i = 0; i < 3; i++) {
+        m.mseed[i] = sq->monte_seed[i];
+        m.moff[i] = sq->monte_offset[i];
+    }
+    m.mstate = sq->monte_state;
+    return attn16_launch(mode, m, a->n_head * sq->n_seq, s->T, (hipStream_t)stream);
 }
 
 int lnship32_attn_decode(const lnship_attn_args *a, void *stream) {

@@ -125,6 +125,8 @@ def lib():
                                                      c_p]),
         "lnship16_rope_attn_decode": (ctypes.c_int, [ctypes.c_int, ctypes.POINTER(QkvStoreArgs),
                                                      ctypes.POINTER(AttnArgs), c_p]),
+        "lnship16_rope_attn_decode_seqs": (ctypes.c_int, [ctypes.c_int, ctypes.POINTER(QkvStoreArgs),
+                                                          ctypes.POINTER(AttnArgs), ctypes.POINTER(AttnSeqs), c_p]),
         "lnship32_attn_decode": (ctypes.c_int, [ctypes.POINTER(AttnArgs), c_p]),
         "lnship_max_row": (c_i64, [ctypes.c_int, ctypes.c_int]),
         "lnship32_rope_store_kv": (ctypes.c_int, [ctypes.POINTER(QkvStoreArgs), c_p]),

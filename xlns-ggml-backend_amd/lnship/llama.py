@@ -297,15 +297,20 @@ class LlamaLNS16:
         check(lib().lnship16_swiglu_mul_mat(self.mode, gate_ptr, up_ptr, ctypes.c_void_p(w), resid_ptr, dst_ptr, K, M,
                                             self._stream))
 
-    def _attn_seqs(self, args, nseq):
+    def _attn_seqs(self, args, nseq, store=None):
         """The decode attention of one token in each of nseq sequences, with
-        the Monte starts of the three nodes it replaces, taken in their order."""
+        the Monte starts of the three nodes it replaces, taken in their order;
+        with store (the tokens' rope and cache stores), the two in one launch."""
         L, nh, hd, n_kv = lib(), args.n_head, args.head_dim, args.n_kv
         seeds = (self._seed(L.lnship16_mul_mat_draws(self.mode, hd, n_kv, 1, nh, nseq)),
                  self._seed(L.lnship16_soft_max_draws(self.mode, n_kv, nh * nseq)),
                  self._seed(L.lnship16_mul_mat_draws(self.mode, n_kv, hd, 1, nh, nseq)))
         sq = attn_seqs(nseq, seeds)
-        check(L.lnship16_attn_decode_seqs(self.mode, ctypes.byref(args), ctypes.byref(sq), self._stream))
+        if store is None:
+            check(L.lnship16_attn_decode_seqs(self.mode, ctypes.byref(args), ctypes.byref(sq), self._stream))
+        else:
+            check(L.lnship16_rope_attn_decode_seqs(self.mode, ctypes.byref(store), ctypes.byref(args),
+                                                   ctypes.byref(sq), self._stream))
 
     def _attn(self, args, store=None):
         """The decode attention; with store (the token's rope and cache
@@ -356,14 +361,16 @@ class LlamaLNS16:
                               self.vslice, seq_ids, self.seq_stride)
             Tq = 1 if batch else T   # query rows per sequence
             fused = (T == 1 or batch) and self.fused_attn and n_kv <= self._attn_max_kv
-            # Monte and batched steps: lnship16_attn_decode_seqs (no rope inside)
+            # Monte and batched steps: lnship16_(rope_)attn_decode_seqs
             seqs = fused and (batch or self.mode == MONTE)
-            if not (fused and self.fused_rope) or seqs:
+            if not (fused and self.fused_rope):
                 check(L.lnship16_rope_store_kv(ctypes.byref(qs), st))
             if seqs:
+                # the fused rope finds sequence s's cells without the seq map
+                qs.seq = None
                 self._attn_seqs(AttnArgs(P(q), P(self.kcache[il], cbase), P(self.vcache[il], cbase), c.n_ctx,
                                          self.kslice, self.vslice, P(mask), 1.0 / math.sqrt(hd), P(att), nh, nkv, hd,
-                                         n_kv), nseq)
+                                         n_kv), nseq, qs if self.fused_rope else None)
             elif fused:
                 # the three nodes below in one launch, bit for bit (and the
                 # rope and cache stores above it, with fused_rope)
