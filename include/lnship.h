@@ -114,6 +114,22 @@ typedef struct lnship_mul_mat_args {
      * ADD of the product and a residual (lns_add, src/lns-ops.cpp:468-530),
      * in the same launch.  residual is laid out as dst and may be dst. */
     const float *residual;
+    /* optional nodes before the product, on the activations, in the same
+     * launch (lnship16_mul_mat only, one activation slice, at most one of
+     * the two; a launch whose activation rows do not fit LDS beside the
+     * tables returns LNSHIP_ERANGE, lnship32_mul_mat LNSHIP_EINVAL):
+     * rms_norm_w non-null: x becomes rms_norm(x) * rms_norm_w, the RMS_NORM
+     * node (lns_rms_norm, src/lns-ops.cpp:701-736, epsilon rms_eps, each row
+     * n of x on its own) and the MUL by the K floats of rms_norm_w, F32
+     * between the nodes; its Monte start is rms_seed or, with monte_state,
+     * monte_state jumped by rms_offset (the node's own, not the product's).
+     * glu_up non-null: x becomes swiglu(x, up), the GLU node (lns_swiglu,
+     * src/lns-ops.cpp:809-862), up row n at glu_up + n * x_ld. */
+    const float *rms_norm_w;
+    float rms_eps;
+    uint16_t rms_seed;
+    uint64_t rms_offset;
+    const float *glu_up;
 } lnship_mul_mat_args;
 
 int lnship16_mul_mat(int mode, const lnship_mul_mat_args *args, void *stream);

@@ -373,3 +373,30 @@ def test_attn_decode_seqs_checks_arguments_first(lnship):
     a.cache_m = a.n_kv
     sq = lnship.attn_seqs(2)
     assert L.lnship16_attn_decode_seqs(lnship.MONTE, ctypes.byref(a), ctypes.byref(sq), None) == ERANGE
+
+
+def test_ctypes_structs_match_the_header(lnship, tmp_path):
+    # every argument struct the Python mirror passes by pointer has the
+    # header's size and field offsets (a C program built from include/lnship.h
+    # prints them; gcc on the host, nothing launched)
+    import subprocess
+    structs = {"lnship_mul_mat_args": lnship.MulMatArgs, "lnship_soft_max_args": lnship.SoftMaxArgs,
+               "lnship_mul_mat_id_args": lnship.MulMatIdArgs, "lnship_qkv_store_args": lnship.QkvStoreArgs,
+               "lnship_attn_args": lnship.AttnArgs, "lnship_attn_seqs": lnship.AttnSeqs}
+    lines = ["#include <stdio.h>", "#include <stddef.h>", '#include "lnship.h"', "int main(void) {"]
+    for cname, py in structs.items():
+        lines.append('printf("%s size %%zu\\n", sizeof(%s));' % (cname, cname))
+        for f in py._fields_:
+            lines.append('printf("%s %s %%zu\\n", offsetof(%s, %s));' % (cname, f[0], cname, f[0]))
+    lines += ["return 0;", "}"]
+    src = tmp_path / "layout.c"
+    src.write_text("\n".join(lines) + "\n")
+    inc = os.path.join(os.path.dirname(os.path.abspath(__file__)), "..", "include")
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-std=c11", "-I", inc, str(src), "-o", str(exe)], check=True)
+    out = subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.split("\n")
+    got = {tuple(l.split()[:2]): int(l.split()[2]) for l in out if l}
+    for cname, py in structs.items():
+        assert got[(cname, "size")] == ctypes.sizeof(py), cname
+        for f in py._fields_:
+            assert got[(cname, f[0])] == getattr(py, f[0]).offset, (cname, f[0])

@@ -178,3 +178,125 @@ def test_swiglu_mul_mat_refuses_monte(ln):
     wp = ln.pack16(torch.ones(4, 8, device="cuda"))
     out = torch.empty(4, device="cuda")
     assert ln.lib().lnship16_swiglu_mul_mat(O.MONTE, P(x), P(x), P(wp), None, P(out), 8, 4, ln._stream()) == -1
+
+
+# ---- lnship16_mul_mat's prologue fields: the node before the product ---------
+# (rms_norm_w: RMS_NORM and the norm MUL; glu_up: the GLU node's swiglu) in the
+# launch of a mul_mat of N activation rows, every mode, Monte with the
+# rms_norm node's own start: against the oracle of the separate nodes (Monte:
+# one LFSR sequence through them in graph order) and against the library's
+# separate launches with the residual ADD
+
+
+def mm_args(ln, wp, x_ptr, out, K, M, N, seed, x_ld=0, residual=None):
+    sd, st, off = ln.seed_fields(seed)
+    return ln.MulMatArgs(wp.data_ptr(), x_ptr, out.data_ptr(), K, M, N, 1, 1, 1, 1, x_ld, 0, sd, 0, 0, 0, 0, st,
+                         off or 0, residual)
+
+
+def rms_mul_oracle(mode, x, wn, w, s0):
+    """rms_norm (Monte from s0), the MUL by wn, then the mul_mat (Monte: the
+    LFSR where rms_norm left it), F32 between the nodes."""
+    O.monte_set(s0)
+    h = O.rms_norm16(mode, x, EPS)
+    mul = np.vectorize(lambda a, b: O.lib().lno16_mul(int(a), int(b)), otypes=[np.uint16])
+    h = O.x2f16(mul(O.f2x16(h), O.f2x16(np.broadcast_to(wn, h.shape).copy())))
+    return O.mul_mat16_f32w(mode, w[None, None], h[None, None])[0, 0]
+
+
+@pytest.mark.parametrize("mode", ["base", "monte", "lpvip", "sum32"])
+@pytest.mark.parametrize("K,M,N", [(576, 960, 8), (577, 193, 3), (13, 5, 1), (1536, 576, 2), (576, 3072, 8)])
+def test_mul_mat_rms_prologue_equals_three_nodes(ln, mode, K, M, N):
+    print(f"\n[mul_mat rms prologue] {mode} K={K} M={M} N={N}", flush=True)
+    m = O.MODES[mode]
+    L = ln.lib()
+    rng = np.random.default_rng(K + 17 * M + 5 * N)
+    x = (rng.standard_normal((N, K)) * 1.5).astype(np.float32)
+    wn = (rng.standard_normal(K) * 0.5 + 1.0).astype(np.float32)
+    w = (rng.standard_normal((M, K)) * 0.02).astype(np.float32)
+    resid = rng.standard_normal((N, M)).astype(np.float32)
+    wp, dx, dwn = ln.pack16(dev(w)), dev(x), dev(wn)
+    s0 = 3001
+    d_rms = L.lnship16_rms_norm_draws(m, K, N)
+    s1 = L.lnship_lfsr_jump(s0, d_rms)
+
+    def fused(seeds, residual=None):
+        out = dev(resid) if residual is not None else torch.full((N, M), float("nan"), device="cuda")
+        a = mm_args(ln, wp, dx.data_ptr(), out, K, M, N, seeds[1], residual=out.data_ptr() if residual else None)
+        rsd, _, roff = ln.seed_fields(seeds[0])
+        a.rms_norm_w, a.rms_eps, a.rms_seed, a.rms_offset = dwn.data_ptr(), EPS, rsd, roff or 0
+        ln.check(L.lnship16_mul_mat(m, ctypes.byref(a), ln._stream()))
+        return host(out)
+
+    got = fused((s0, s1))
+    if M * K * N <= 8_000_000:
+        same_bits(got, rms_mul_oracle(m, x, wn, w, s0), f"rms prologue {mode} K={K} M={M} N={N} vs oracle")
+    # the residual ADD, against the library's rms_norm_mul and mul_mat launches
+    h = torch.empty(N, K, device="cuda")
+    ln.check(L.lnship16_rms_norm_mul(m, P(dx), P(dwn), P(h), K, N, ctypes.c_float(EPS), s0, None, 0, ln._stream()))
+    ref = dev(resid)
+    ln.mul_mat16_raw(m, wp.data_ptr(), h.data_ptr(), ref.data_ptr(), K, M, N, seed=s1, residual=P(ref))
+    same_bits(fused((s0, s1), residual=True), host(ref), f"rms prologue + residual {mode} K={K} M={M} N={N}")
+    if mode == "monte":
+        # both starts read from one device state, with their offsets
+        S = 777
+        st = torch.tensor([S], dtype=torch.int16, device="cuda")
+        g2 = fused(((st, 5), (st, 5 + d_rms)))
+        want = fused((L.lnship_lfsr_jump(S, 5), L.lnship_lfsr_jump(S, 5 + d_rms)))
+        same_bits(g2, want, f"rms prologue monte K={K} N={N}: state vs seeds")
+        if K >= 64:   # (a 13-term row may round alike from other draws)
+            assert not np.array_equal(want, got), "other starts, other draws"
+
+
+@pytest.mark.parametrize("mode", ["base", "monte", "lpvip", "sum32"])
+@pytest.mark.parametrize("K,M,N", [(1536, 576, 8), (13, 5, 3), (1537, 193, 1)])
+def test_mul_mat_glu_prologue_equals_two_nodes(ln, mode, K, M, N):
+    # the down projection of a decode step: gate | up rows of 2K (x_ld 2K),
+    # the residual ADD in place
+    print(f"\n[mul_mat glu prologue] {mode} K={K} M={M} N={N}", flush=True)
+    m = O.MODES[mode]
+    L = ln.lib()
+    rng = np.random.default_rng(K + 31 * M + N)
+    ug = (rng.standard_normal((N, 2 * K)) * 0.7).astype(np.float32)
+    w = (rng.standard_normal((M, K)) * 0.02).astype(np.float32)
+    resid = rng.standard_normal((N, M)).astype(np.float32)
+    wp, dug = ln.pack16(dev(w)), dev(ug)
+    gate_p, up_p = dug.data_ptr() + 4 * K, dug.data_ptr()
+    s0 = 1234
+    out = torch.full((N, M), float("nan"), device="cuda")
+    a = mm_args(ln, wp, gate_p, out, K, M, N, s0, x_ld=2 * K)
+    a.glu_up = up_p
+    ln.check(L.lnship16_mul_mat(m, ctypes.byref(a), ln._stream()))
+    sw = np.stack([swiglu_oracle(ug[n, K:].copy(), ug[n, :K].copy()) for n in range(N)])
+    O.monte_set(s0)
+    same_bits(host(out), O.mul_mat16_f32w(m, w[None, None], sw[None, None])[0, 0],
+              f"glu prologue {mode} K={K} M={M} N={N} vs oracle")
+    x = dev(resid)
+    a = mm_args(ln, wp, gate_p, x, K, M, N, s0, x_ld=2 * K, residual=x.data_ptr())
+    a.glu_up = up_p
+    ln.check(L.lnship16_mul_mat(m, ctypes.byref(a), ln._stream()))
+    swd = torch.empty(N, K, device="cuda")
+    ln.check(L.lnship16_swiglu(ctypes.c_void_p(gate_p), 2 * K, ctypes.c_void_p(up_p), 2 * K, P(swd), K, N,
+                               ln._stream()))
+    ref = dev(resid)
+    ln.mul_mat16_raw(m, wp.data_ptr(), swd.data_ptr(), ref.data_ptr(), K, M, N, seed=s0, residual=P(ref))
+    same_bits(host(x), host(ref), f"glu prologue + residual {mode} K={K} M={M} N={N}")
+
+
+def test_mul_mat_prologue_refusals(ln):
+    # both nodes at once, several activation slices, K = 0: refused, nothing
+    # launched; lnship32_mul_mat takes neither
+    L = ln.lib()
+    wp = ln.pack16(torch.ones(4, 8, device="cuda"))
+    x = torch.ones(2, 8, device="cuda")
+    out = torch.empty(2, 4, device="cuda")
+    a = mm_args(ln, wp, x.data_ptr(), out, 8, 4, 2, 7)
+    a.rms_norm_w, a.glu_up = x.data_ptr(), x.data_ptr()
+    assert L.lnship16_mul_mat(O.BASE, ctypes.byref(a), ln._stream()) == -1
+    a = mm_args(ln, wp, x.data_ptr(), out, 8, 4, 1, 7)
+    a.ne12 = a.ne02 = 2
+    a.rms_norm_w = x.data_ptr()
+    assert L.lnship16_mul_mat(O.BASE, ctypes.byref(a), ln._stream()) == -1
+    a = mm_args(ln, wp, x.data_ptr(), out, 8, 4, 2, 7)
+    a.glu_up = x.data_ptr()
+    assert L.lnship32_mul_mat(ctypes.byref(a), ln._stream()) == -1

@@ -947,6 +947,10 @@ struct mm_args16 {
     // non-null (XL launches): the activation is swiglu(xf, glu_up), the GLU
     // node before the mul_mat: up row n at glu_up + n * x_ld
     const float *glu_up;
+    // k_mm16 with norm (XL launches of one slice): the RMS_NORM node's
+    // Monte start, monte_start(rms_seed, state, rms_offset)
+    uint32_t rms_seed;
+    uint64_t rms_offset;
     // set by the launcher: the grid is 2^xcd_sh times wider than the work;
     // workgroup x works (as block x >> xcd_sh) iff x is a multiple of 2^xcd_sh
     uint32_t xcd_sh;
@@ -1322,6 +1326,34 @@ __global__ __launch_bounds__(k_block * CG) void k_mm16(mm_args16 a, dev_tables T
     if (head && live && a.K > 0) hw = mm16_head<PF>(a, m, zw);
     const red16<MODE> R = stage_for<MODE, NC == 1>(T, lds);
     uint16_t *xl = reinterpret_cast<uint16_t *>(lds + mm_xl_offset<MODE>());
+    // The RMS_NORM and MUL nodes before the product (norm): each workgroup
+    // forms the scales of its own columns' rows, as k_rms16 does: the
+    // squares into the activation rows' LDS, then one row's chain per lane
+    // of wave 0 (lane l on column l mod ncw, every lane busy); the staging
+    // below forms h from them
+    __shared__ uint32_t s_rinv[64];
+    if (XL && a.norm) {
+        const float *xf = a.xf + nw * a.x_ld;
+        const int K = (int)a.K;
+        for (int e = threadIdx.x; e < ncw * K; e += k_block * CG) {
+            const int j = e / K, k = e - j * K;
+            const uint32_t c = x16_from_f32(T.cvt16, xf[(int64_t)j * a.x_ld + k]);
+            xl[j * kp + k] = (uint16_t)x16_mul(c, c);
+        }
+        __syncthreads();
+        if (threadIdx.x < 64u) {
+            const int j = (int)threadIdx.x % ncw;
+            uint32_t s = 0;
+            if constexpr (MODE == LNSHIP_MONTE)
+                s = lfsr_jump(T, monte_start(T, a.rms_seed, a.state, a.rms_offset), (uint64_t)(nw + j) * (uint64_t)K);
+            typename red16<MODE>::acc_t acc = R.start(0u, s);
+            chain16<red16<MODE>, true>(R, acc, xl + j * kp, 0, K, s);   // squares: positive
+            const uint32_t mean = x16_mul(R.finish(acc) & 0xffffu, a.rms_ik);
+            // the epsilon add is a plain xlns16_add in every mode
+            if ((int)threadIdx.x < ncw) s_rinv[j] = x16_recip(x16_sqrt(x16_add_g(T.gauss16, mean, a.rms_eps)));
+        }
+        __syncthreads();
+    }
     if (XL) {
         // columns past N and k past K hold xlns16 zero
         // in batches of eight per thread: the loads, then the conversion
@@ -1336,6 +1368,7 @@ __global__ __launch_bounds__(k_block * CG) void k_mm16(mm_args16 a, dev_tables T
             }
             // loads and lookups stay in the row; only the stores are bounded
             const float *row = xf + (int64_t)min(j, ncw - 1) * a.x_ld;
+            const uint32_t inv = a.norm ? s_rinv[min(j, ncw - 1)] : 0u;
             for (int k0 = threadIdx.x; k0 < kp; k0 += B * nt) {
                 float v[B];
 #pragma unroll
@@ -1343,6 +1376,16 @@ __global__ __launch_bounds__(k_block * CG) void k_mm16(mm_args16 a, dev_tables T
                 uint32_t c[B];
 #pragma unroll
                 for (int q = 0; q < B; q++) c[q] = x16_from_f32(T.cvt16, v[q]);
+                if (a.norm) {
+                    // the RMS_NORM node's output, then the MUL node's by the
+                    // norm weight, each through F32 (rho16)
+                    float g[B];
+#pragma unroll
+                    for (int q = 0; q < B; q++) g[q] = a.norm[min(k0 + q * nt, kl)];
+#pragma unroll
+                    for (int q = 0; q < B; q++)
+                        c[q] = T.rho16[x16_mul(T.rho16[x16_mul(c[q], inv)], x16_from_f32(T.cvt16, g[q]))];
+                }
                 if (a.glu_up) {
                     // swiglu as its node computes it (silu(gate) * up in
                     // xlns16, F32 out), then into xlns16 as here
@@ -3932,6 +3975,14 @@ int lnship32_pack(const void *src, int src_is_f16, int64_t src_ld, int64_t src_s
     return pack_common(1, src, src_is_f16, src_ld, src_slice, dst, K, M, nslices, stream);
 }
 
+// the xlns16 code of v, as the device's conversion table gives it
+static uint32_t host_cvt16(float v) {
+    const uint16_t *cvt = static_cast<const uint16_t *>(lnship_host_table("cvt16", nullptr));
+    uint32_t b;
+    std::memcpy(&b, &v, 4);
+    return cvt[b >> 15];
+}
+
 int lnship16_mul_mat(int mode, const lnship_mul_mat_args *a, void *stream) {
     device_state *s = state();
     if (!s) return LNSHIP_ENOINIT;
@@ -3947,6 +3998,14 @@ int lnship16_mul_mat(int mode, const lnship_mul_mat_args *a, void *stream) {
     // activations converted inside the GEMV when NC rows fit in LDS next to
     // the tables, else by k_act into scratch first
     const mm16_shape sh = mm16_choose(mode, a->M, a->N, nslices, kp, s->cus);
+    if (a->rms_norm_w || a->glu_up) {
+        // the nodes before the product run in the activation staging
+        if (a->rms_norm_w && a->glu_up) return fail(LNSHIP_EINVAL, "mul_mat: rms_norm_w and glu_up together%s");
+        if (nslices != 1 || a->K < 1)
+            return fail(LNSHIP_EINVAL, "mul_mat: rms_norm_w / glu_up need one activation slice and K >= 1%s");
+        if (!sh.xl) return fail(LNSHIP_ERANGE, "mul_mat: rows too long to stage beside the tables for "
+                                               "rms_norm_w / glu_up%s");
+    }
     void *xs = nullptr;
     if (!sh.xl) {
         if (int rc = grow_scratch(s, (size_t)std::max<int64_t>(1, nslices * a->N * kp) * 2, &xs, st)) return rc;
@@ -3963,6 +4022,14 @@ int lnship16_mul_mat(int mode, const lnship_mul_mat_args *a, void *stream) {
                 wms, a->w_slice ? a->w_slice : kp * wms, dld, a->dst_slice ? a->dst_slice : a->N * dld,
                 a->monte_seed, a->monte_state, a->monte_offset};
     m.resid = a->residual;
+    m.glu_up = a->glu_up;
+    if (a->rms_norm_w) {
+        m.norm = a->rms_norm_w;
+        m.rms_ik = host_cvt16(1.0f / (float)a->K);
+        m.rms_eps = host_cvt16(a->rms_eps);
+        m.rms_seed = a->rms_seed;
+        m.rms_offset = a->rms_offset;
+    }
     switch (mode) {
         case LNSHIP_BASE: return dispatch_mm16<LNSHIP_BASE>(m, s->T, nslices, sh, s->cus, st);
         case LNSHIP_MONTE: return dispatch_mm16<LNSHIP_MONTE>(m, s->T, nslices, sh, s->cus, st);
@@ -4028,10 +4095,17 @@ static int mul_mat32_staged(device_state *s, const lnship_mul_mat_args *a, void 
     }
 }
 
+// the nodes before the product that lnship16_mul_mat takes in its launch
+static int check_mm32_plain(const lnship_mul_mat_args *a) {
+    if (a->rms_norm_w || a->glu_up) return fail(LNSHIP_EINVAL, "mul_mat (LNS32): no rms_norm_w / glu_up%s");
+    return 0;
+}
+
 int lnship32_mul_mat(const lnship_mul_mat_args *a, void *stream) {
     device_state *s = state();
     if (!s) return LNSHIP_ENOINIT;
     if (int rc = check_mm(a)) return rc;
+    if (int rc = check_mm32_plain(a)) return rc;
     if (a->M == 0 || a->N == 0) return 0;
     const int64_t kp = (a->K + 7) & ~(int64_t)7;
     void *xs = nullptr;
@@ -4044,6 +4118,7 @@ int lnship32_mul_mat_noalloc(const lnship_mul_mat_args *a, void *stream) {
     device_state *s = state();
     if (!s) return LNSHIP_ENOINIT;
     if (int rc = check_mm(a)) return rc;
+    if (int rc = check_mm32_plain(a)) return rc;
     if (a->M == 0 || a->N == 0) return 0;
     const int64_t kp = (a->K + 7) & ~(int64_t)7;
     const uint64_t need = (uint64_t)(a->ne12 * a->ne13) * (uint64_t)a->N * (uint64_t)kp * 4u;
@@ -4209,15 +4284,8 @@ int lnship16_rms_norm_mul_mat(int mode, const float *x, const float *norm_w, flo
     m.eps = eps;
     m.skew = g_predict_skew;
     // the codes of 1 / K and of eps, as the device's conversion reads them
-    {
-        const uint16_t *cvt = static_cast<const uint16_t *>(lnship_host_table("cvt16", nullptr));
-        const float ik = 1.0f / (float)K;
-        uint32_t b;
-        std::memcpy(&b, &ik, 4);
-        m.rms_ik = cvt[b >> 15];
-        std::memcpy(&b, &eps, 4);
-        m.rms_eps = cvt[b >> 15];
-    }
+    m.rms_ik = host_cvt16(1.0f / (float)K);
+    m.rms_eps = host_cvt16(eps);
     const int rows = narrow ? 3 * 16 : k_rms_mm_rows;
     const uint64_t wgs = (uint64_t)((M + rows - 1) / rows);
     if (wgs > 0x7fffffffu) return fail(LNSHIP_ERANGE, "rms_norm_mul_mat: grid too large%s");

@@ -29,7 +29,9 @@ class MulMatArgs(ctypes.Structure):
                 ("ne02", c_i64), ("ne03", c_i64), ("ne12", c_i64), ("ne13", c_i64),
                 ("x_ld", c_i64), ("x_slice", c_i64), ("monte_seed", ctypes.c_uint16),
                 ("w_mstride", c_i64), ("w_slice", c_i64), ("dst_ld", c_i64), ("dst_slice", c_i64),
-                ("monte_state", c_p), ("monte_offset", ctypes.c_uint64), ("residual", c_p)]
+                ("monte_state", c_p), ("monte_offset", ctypes.c_uint64), ("residual", c_p),
+                ("rms_norm_w", c_p), ("rms_eps", ctypes.c_float), ("rms_seed", ctypes.c_uint16),
+                ("rms_offset", ctypes.c_uint64), ("glu_up", c_p)]
 
 
 class SoftMaxArgs(ctypes.Structure):

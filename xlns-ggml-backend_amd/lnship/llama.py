@@ -20,11 +20,16 @@ fused rows enumerate Q's outputs, then K's, then V's.  A single-sequence
 decode step runs K^T q, soft_max and V p in one launch (lnship16_attn_decode,
 and in Monte and for a batched step of several sequences
 lnship16_attn_decode_seqs, which takes the three ops' Monte starts;
-bit-identical to the three ops; fused_attn = False runs the three).  A single-row sum32 step runs each rms_norm, its norm MUL
-and the mul_mat that reads them in one launch (lnship16_rms_norm_mul_mat,
-bit-identical to the three; fused_rms = False runs them apart).  A single-row
-step outside Monte forms swiglu inside the down projection's launch
-(lnship16_swiglu_mul_mat; fused_glu = False runs the two).
+bit-identical to the three ops; fused_attn = False runs the three), the
+query rope and the cache stores inside it (fused_rope).  A single-row sum32
+step runs each rms_norm, its norm MUL and the mul_mat that reads them in one
+launch (lnship16_rms_norm_mul_mat, its scale predicted, bit-identical to the
+three; fused_rms = False runs them apart).  A single-row step outside Monte
+forms swiglu inside the down projection's launch (lnship16_swiglu_mul_mat;
+fused_glu = False runs the two).  The other decode steps (a batched step, a
+Monte token) run the rms_norm and norm MUL, or the swiglu, inside the launch
+of the mul_mat that reads them through lnship16_mul_mat's prologue fields
+(fused_pre = False runs them apart).
 
 With n_seq > 1 the model holds that many independent sequences, each with
 its own KV cache, as llama.cpp's per-sequence KV streams.  A sequence's
@@ -131,6 +136,11 @@ class LlamaLNS16:
         # (lnship16_swiglu_mul_mat, bit-identical to the two nodes), where the
         # activation row fits LDS
         self.fused_glu = mode != MONTE and cfg.n_ff <= lib().lnship_max_row(6, mode)
+        # the rows of a decode step (one token, or one per sequence): the
+        # rms_norm and norm MUL, or the swiglu, inside the launch of the
+        # mul_mat that reads them (lnship16_mul_mat's prologue fields,
+        # bit-identical to the separate nodes), where the rows fit LDS
+        self.fused_pre = True
         self._attn_max_kv = lib().lnship_max_row(8, mode)
         dev = torch.device("cuda", torch.cuda.current_device())
         self.dev = dev
@@ -267,6 +277,34 @@ class LlamaLNS16:
         draws = lib().lnship16_mul_mat_draws(self.mode, K, M, N, ne12, ne13)
         mul_mat16_raw(self.mode, w, x_ptr, dst_ptr, K, M, N, seed=self._seed(draws), stream=self._stream, **kw)
 
+    def _mm_pre(self, w, x_ptr, dst_ptr, K, M, N, rms_w=None, glu_up=None, residual=None, x_ld=0):
+        """dst (+)= W pre(x) for N rows of K in one launch, pre being the
+        node(s) before the mul_mat: rms_norm and the MUL by the norm row rms_w,
+        or swiglu(x, glu_up) (lnship16_mul_mat's prologue fields; Monte: the
+        rms_norm's draws, then the product's, in graph order).  False, with
+        nothing run and no draws taken, where the launch cannot stage its
+        rows beside the tables."""
+        from . import MulMatArgs
+        L = lib()
+        saved = (self.lfsr, self._dev_draws, self._lfsr_synced)
+        rs = self._seed(L.lnship16_rms_norm_draws(self.mode, K, N)) if rms_w is not None else 0
+        sd, st, off = seed_fields(self._seed(L.lnship16_mul_mat_draws(self.mode, K, M, N, 1, 1)))
+        a = MulMatArgs(ctypes.c_void_p(w), x_ptr, dst_ptr, K, M, N, 1, 1, 1, 1, x_ld, 0, sd, 0, 0, 0, 0, st,
+                       off or 0, residual)
+        if rms_w is not None:
+            rsd, rst, roff = seed_fields(rs)
+            # (one device state, or none, for both nodes' starts)
+            assert (rst is None) == (st is None), "the two nodes' starts come from one place"
+            a.rms_norm_w, a.rms_eps, a.rms_seed, a.rms_offset = rms_w, self.cfg.eps, rsd, roff or 0
+        else:
+            a.glu_up = glu_up
+        rc = L.lnship16_mul_mat(self.mode, ctypes.byref(a), self._stream)
+        if rc == -4:   # LNSHIP_ERANGE: the rows do not fit beside the tables
+            self.lfsr, self._dev_draws, self._lfsr_synced = saved
+            return False
+        check(rc)
+        return True
+
     def _rms_mul(self, x_ptr, w_ptr, dst_ptr, ncols, nrows):
         """rms_norm of nrows rows, then the MUL by the norm weight row w, in
         one launch (the MUL takes no draws)."""
@@ -282,13 +320,14 @@ class LlamaLNS16:
                         st, off)
         check(lib().lnship16_soft_max(self.mode, ctypes.byref(a), self._stream))
 
-    def _rms_mm(self, x_ptr, wn_ptr, w, h_ptr, dst_ptr, K, M, T):
+    def _rms_mm(self, x_ptr, wn_ptr, w, h_ptr, dst_ptr, K, M, T, step=False):
         """dst = W (rms_norm(x) * wn) for T rows of K: for one sum32 row in one
-        launch, else rms_norm + MUL into h, then the mul_mat."""
+        launch (its scale predicted), for the rows of a decode step (step) in
+        one launch, else rms_norm + MUL into h, then the mul_mat."""
         if T == 1 and self.fused_rms:
             check(lib().lnship16_rms_norm_mul_mat(self.mode, x_ptr, wn_ptr, self.cfg.eps, ctypes.c_void_p(w), dst_ptr,
                                                   K, M, self._stream))
-        else:
+        elif not (step and self.fused_pre and self._mm_pre(w, x_ptr, dst_ptr, K, M, T, rms_w=wn_ptr)):
             self._rms_mul(x_ptr, wn_ptr, h_ptr, K, T)
             self._mm(w, h_ptr, dst_ptr, K, M, T)
 
@@ -354,7 +393,8 @@ class LlamaLNS16:
         check(L.lnship_causal_mask(P(pos_dev), T, n_kv, P(mask), st))
         for il, W in enumerate(self.layers):
             last = il == c.n_layer - 1
-            self._rms_mm(P(x), P(W["attn_norm"]), W["wqkv"].data_ptr(), P(h), P(qkv), e, nqkv, T)
+            self._rms_mm(P(x), P(W["attn_norm"]), W["wqkv"].data_ptr(), P(h), P(qkv), e, nqkv, T,
+                         step=T == 1 or batch)
             # rope(q) and the K / V cache stores (k rotated) in one launch
             qs = QkvStoreArgs(P(qkv), nqkv, P(pos_dev), T, nh, nkv, hd, hd, P(self.cos_sin), P(q),
                               P(self.kcache[il], cbase), P(self.vcache[il], cbase), c.n_ctx, self.kslice,
@@ -395,10 +435,12 @@ class LlamaLNS16:
             else:
                 self._mm(W["wo"].data_ptr(), P(att), P(o), nq, e, T)
                 check(L.lnship16_add(P(o, r0), P(x, r0), rows * e, rows * e, P(x), st))
-            self._rms_mm(P(x), P(W["ffn_norm"]), W["wug"].data_ptr(), P(h), P(ug), e, 2 * f, rows)
+            step = rows == 1 or batch
+            self._rms_mm(P(x), P(W["ffn_norm"]), W["wug"].data_ptr(), P(h), P(ug), e, 2 * f, rows, step=step)
             if rows == 1 and self.fused_glu:   # x += Wdown swiglu(gate, up), one launch
                 self._glu_mm(P(ug, f), P(ug), W["wdown"].data_ptr(), P(x), P(x), f, e)
-            else:
+            elif not (step and self.fused_pre and self._mm_pre(W["wdown"].data_ptr(), P(ug, f), P(x), f, e, rows,
+                                                              glu_up=P(ug), residual=P(x), x_ld=2 * f)):
                 check(L.lnship16_swiglu(P(ug, f), 2 * f, P(ug), 2 * f, P(sw), f, rows, st))
                 self._mm(W["wdown"].data_ptr(), P(sw), P(x), f, e, rows, residual=P(x))
         nout = T if batch else 1
