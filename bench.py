@@ -234,6 +234,16 @@ def replay_call(model, ln, torch, call):
     elif "glu_up" in kw:
         ln.check(ln.lib().lnship16_swiglu_mul_mat(model.mode, x_ptr, kw["glu_up"], ctypes.c_void_p(w),
                                                   kw["residual"], dst_ptr, K, M, st))
+    elif "pre" in kw:
+        # lnship16_mul_mat with the node before it in its launch
+        p = kw["pre"]
+        a = ln.MulMatArgs(w, x_ptr, dst_ptr, K, M, N, 1, 1, 1, 1, p["x_ld"], 0, 7, 0, 0, 0, 0, None, 0,
+                          kw["residual"])
+        if p["rms_w"] is not None:
+            a.rms_norm_w, a.rms_eps, a.rms_seed = p["rms_w"], model.cfg.eps, 7
+        else:
+            a.glu_up = p["glu_up"]
+        ln.check(ln.lib().lnship16_mul_mat(model.mode, ctypes.byref(a), st))
     else:
         ln.mul_mat16_raw(model.mode, w, x_ptr, dst_ptr, K, M, N, seed=7, stream=st, **kw)
 
@@ -273,14 +283,15 @@ def record_decode_step(model, torch):
     lnship16_rms_norm_mul_mat's with the norm row as kw["norm"]."""
     c = model.cfg
     calls = []
-    orig, orig_rms, orig_glu = model._mm, model._rms_mm, model._glu_mm
+    orig, orig_rms, orig_glu, orig_pre = model._mm, model._rms_mm, model._glu_mm, model._mm_pre
 
     def record_mm(w, x_ptr, dst_ptr, K, M, N, **kw):
         orig(w, x_ptr, dst_ptr, K, M, N, **kw)
         calls.append((w, x_ptr, dst_ptr, K, M, N, kw))
 
-    def record_rms_mm(x_ptr, wn_ptr, w, h_ptr, dst_ptr, K, M, T):
-        orig_rms(x_ptr, wn_ptr, w, h_ptr, dst_ptr, K, M, T)   # split: records through record_mm
+    def record_rms_mm(x_ptr, wn_ptr, w, h_ptr, dst_ptr, K, M, T, step=False):
+        # split or with the prologue: records through record_mm / record_pre
+        orig_rms(x_ptr, wn_ptr, w, h_ptr, dst_ptr, K, M, T, step=step)
         if T == 1 and model.fused_rms:
             calls.append((w, x_ptr, dst_ptr, K, M, 1, {"norm": wn_ptr}))
 
@@ -288,7 +299,14 @@ def record_decode_step(model, torch):
         orig_glu(gate_ptr, up_ptr, w, resid_ptr, dst_ptr, K, M)
         calls.append((w, gate_ptr, dst_ptr, K, M, 1, {"glu_up": up_ptr, "residual": resid_ptr}))
 
-    model._mm, model._rms_mm, model._glu_mm = record_mm, record_rms_mm, record_glu_mm
+    def record_pre(w, x_ptr, dst_ptr, K, M, N, rms_w=None, glu_up=None, residual=None, x_ld=0):
+        ok = orig_pre(w, x_ptr, dst_ptr, K, M, N, rms_w=rms_w, glu_up=glu_up, residual=residual, x_ld=x_ld)
+        if ok:
+            calls.append((w, x_ptr, dst_ptr, K, M, N,
+                          {"pre": {"rms_w": rms_w, "glu_up": glu_up, "x_ld": x_ld}, "residual": residual}))
+        return ok
+
+    model._mm, model._rms_mm, model._glu_mm, model._mm_pre = record_mm, record_rms_mm, record_glu_mm, record_pre
     try:
         tok = model._buf("rtok", 1, torch.int32)
         pos = model._buf("rpos", 1, torch.int32)
@@ -298,7 +316,7 @@ def record_decode_step(model, torch):
         model.forward(1, tok, pos, n_kv_for(model.n_past, c.n_ctx))
         torch.cuda.synchronize()
     finally:
-        model._mm, model._rms_mm, model._glu_mm = orig, orig_rms, orig_glu
+        model._mm, model._rms_mm, model._glu_mm, model._mm_pre = orig, orig_rms, orig_glu, orig_pre
     return calls
 
 
@@ -310,7 +328,7 @@ def launch_bytes(calls):
     before them."""
     return sum(2 * K * M * kw.get("ne02", 1) + 4 * K * N * kw.get("ne12", 1)
                + 4 * M * N * kw.get("ne12", 1) * (2 if kw.get("residual") is not None else 1)
-               + (4 * K if "norm" in kw or "glu_up" in kw else 0)
+               + (4 * K if "norm" in kw or "glu_up" in kw or "pre" in kw else 0)
                for _, _, _, K, M, N, kw in calls)
 
 
@@ -326,7 +344,7 @@ def chain_bound(model, ln, torch, mode):
     stays out of it.  bound_tok_s = 1 / (steps * ns_per_step)."""
     c = model.cfg
     steps = []
-    orig = (model._mm, model._rms_mul, model._softmax, model._attn, model._rms_mm, model._glu_mm)
+    orig = (model._mm, model._rms_mul, model._softmax, model._attn, model._rms_mm, model._glu_mm, model._mm_pre)
 
     def mm(w, x_ptr, dst_ptr, K, M, N, **kw):
         steps.append(K)
@@ -347,17 +365,25 @@ def chain_bound(model, ln, torch, mode):
         else:
             orig[3](args, store)
 
-    def rms_mm(x_ptr, wn_ptr, w, h_ptr, dst_ptr, K, M, T):
+    def rms_mm(x_ptr, wn_ptr, w, h_ptr, dst_ptr, K, M, T, step=False):
         if T == 1 and model.fused_rms:
             steps.append(K)
-        orig[4](x_ptr, wn_ptr, w, h_ptr, dst_ptr, K, M, T)   # split: counted by rms and mm
+        # split: counted by rms and mm; with the prologue by pre
+        orig[4](x_ptr, wn_ptr, w, h_ptr, dst_ptr, K, M, T, step=step)
+
+    def pre(w, x_ptr, dst_ptr, K, M, N, rms_w=None, glu_up=None, residual=None, x_ld=0):
+        # the rms chain, then the GEMV's (the scale is not predicted here)
+        ok = orig[6](w, x_ptr, dst_ptr, K, M, N, rms_w=rms_w, glu_up=glu_up, residual=residual, x_ld=x_ld)
+        if ok:
+            steps.append(2 * K if rms_w is not None else K)
+        return ok
 
     def glu_mm(gate_ptr, up_ptr, w, resid_ptr, dst_ptr, K, M):
         steps.append(K)
         orig[5](gate_ptr, up_ptr, w, resid_ptr, dst_ptr, K, M)
 
-    model._mm, model._rms_mul, model._softmax, model._attn, model._rms_mm, model._glu_mm = (mm, rms, sm, attn, rms_mm,
-                                                                                          glu_mm)
+    (model._mm, model._rms_mul, model._softmax, model._attn, model._rms_mm, model._glu_mm,
+     model._mm_pre) = (mm, rms, sm, attn, rms_mm, glu_mm, pre)
     try:
         tok = model._buf("rtok", 1, torch.int32)
         pos = model._buf("rpos", 1, torch.int32)
@@ -367,7 +393,8 @@ def chain_bound(model, ln, torch, mode):
         model.forward(1, tok, pos, n_kv_for(model.n_past, c.n_ctx))
         torch.cuda.synchronize()
     finally:
-        model._mm, model._rms_mul, model._softmax, model._attn, model._rms_mm, model._glu_mm = orig
+        (model._mm, model._rms_mul, model._softmax, model._attn, model._rms_mm, model._glu_mm,
+         model._mm_pre) = orig
     st = lambda: ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
     us = {}
     M = 576
