@@ -115,9 +115,11 @@ typedef struct lnship_mul_mat_args {
      * in the same launch.  residual is laid out as dst and may be dst. */
     const float *residual;
     /* optional nodes before the product, on the activations, in the same
-     * launch (lnship16_mul_mat only, one activation slice, at most one of
-     * the two; a launch whose activation rows do not fit LDS beside the
-     * tables returns LNSHIP_ERANGE, lnship32_mul_mat LNSHIP_EINVAL):
+     * launch (one activation slice, at most one of the two; a launch whose
+     * activation rows do not fit LDS beside the tables returns
+     * LNSHIP_ERANGE, lnship32_mul_mat_noalloc LNSHIP_EINVAL; in
+     * lnship32_mul_mat the nodes are lns32_rms_norm / lns32_mul and
+     * lns32_swiglu, src32/lns32-ops.cpp):
      * rms_norm_w non-null: x becomes rms_norm(x) * rms_norm_w, the RMS_NORM
      * node (lns_rms_norm, src/lns-ops.cpp:701-736, epsilon rms_eps, each row
      * n of x on its own) and the MUL by the K floats of rms_norm_w, F32

@@ -284,8 +284,8 @@ def test_mul_mat_glu_prologue_equals_two_nodes(ln, mode, K, M, N):
 
 
 def test_mul_mat_prologue_refusals(ln):
-    # both nodes at once, several activation slices, K = 0: refused, nothing
-    # launched; lnship32_mul_mat takes neither
+    # both nodes at once, several activation slices: refused, nothing
+    # launched; lnship32_mul_mat_noalloc takes neither
     L = ln.lib()
     wp = ln.pack16(torch.ones(4, 8, device="cuda"))
     x = torch.ones(2, 8, device="cuda")
@@ -299,4 +299,81 @@ def test_mul_mat_prologue_refusals(ln):
     assert L.lnship16_mul_mat(O.BASE, ctypes.byref(a), ln._stream()) == -1
     a = mm_args(ln, wp, x.data_ptr(), out, 8, 4, 2, 7)
     a.glu_up = x.data_ptr()
+    assert L.lnship32_mul_mat_noalloc(ctypes.byref(a), ln._stream()) == -1
+    a.rms_norm_w = x.data_ptr()
     assert L.lnship32_mul_mat(ctypes.byref(a), ln._stream()) == -1
+
+
+# ---- the same prologues in lnship32_mul_mat (LNS32: lns32_rms_norm,
+# lns32_mul, lns32_swiglu, then lns32_mul_mat, src32/lns32-ops.cpp), and its
+# one-column launches that convert their own activations
+
+
+@pytest.mark.parametrize("K,M,N", [(2048, 3072, 1), (2048, 300, 1), (13, 5, 1), (77, 96, 3), (4096, 256, 1)])
+def test_mul_mat32_rms_prologue_equals_three_nodes(ln, K, M, N):
+    print(f"\n[mul_mat32 rms prologue] K={K} M={M} N={N}", flush=True)
+    L = ln.lib()
+    rng = np.random.default_rng(4 * K + M + N)
+    x = (rng.standard_normal((N, K)) * 1.5).astype(np.float32)
+    wn = (rng.standard_normal(K) * 0.5 + 1.0).astype(np.float32)
+    w = (rng.standard_normal((M, K)) * 0.02).astype(np.float32)
+    resid = rng.standard_normal((N, M)).astype(np.float32)
+    wp, dx, dwn = ln.pack32(dev(w)), dev(x), dev(wn)
+    h = O.mul32(O.rms_norm32(x, EPS), wn)
+    want = O.mul_mat32(w, h)
+    for residual in (False, True):
+        out = dev(resid) if residual else torch.full((N, M), float("nan"), device="cuda")
+        a = mm_args(ln, wp, dx.data_ptr(), out, K, M, N, 0, residual=out.data_ptr() if residual else None)
+        a.rms_norm_w, a.rms_eps = dwn.data_ptr(), EPS
+        ln.check(L.lnship32_mul_mat(ctypes.byref(a), ln._stream()))
+        if not residual:
+            same_bits(host(out), want, f"mul_mat32 rms prologue K={K} M={M} N={N} vs oracle")
+        else:
+            ref = dev(resid)
+            ln.mul_mat32_raw(wp.data_ptr(), dev(h).data_ptr(), ref.data_ptr(), K, M, N, residual=P(ref))
+            same_bits(host(out), host(ref), f"mul_mat32 rms prologue + residual K={K} M={M} N={N}")
+
+
+@pytest.mark.parametrize("K,M", [(2048, 512), (13, 5), (1537, 193)])
+def test_mul_mat32_glu_prologue_equals_two_nodes(ln, K, M):
+    print(f"\n[mul_mat32 glu prologue] K={K} M={M}", flush=True)
+    L = ln.lib()
+    rng = np.random.default_rng(K + 7 * M)
+    ug = (rng.standard_normal(2 * K) * 0.7).astype(np.float32)
+    w = (rng.standard_normal((M, K)) * 0.02).astype(np.float32)
+    wp, dug = ln.pack32(dev(w)), dev(ug)
+    out = torch.full((1, M), float("nan"), device="cuda")
+    a = mm_args(ln, wp, dug.data_ptr() + 4 * K, out, K, M, 1, 0, x_ld=2 * K)
+    a.glu_up = dug.data_ptr()
+    ln.check(L.lnship32_mul_mat(ctypes.byref(a), ln._stream()))
+    want = O.mul_mat32(w, O.swiglu32(ug[K:].copy(), ug[:K].copy())[None])
+    same_bits(host(out), want, f"mul_mat32 glu prologue K={K} M={M} vs oracle")
+
+
+@pytest.mark.parametrize("K,M,N,nslices", [(2048, 3072, 1, 1), (64, 768, 1, 32), (768, 64, 1, 32), (2048, 32000, 1, 1),
+                                           (8192, 2048, 1, 1), (3, 7, 2, 1), (2048, 512, 4, 1)])
+def test_mul_mat32_own_conversion_equals_staged(ln, K, M, N, nslices):
+    # lnship32_mul_mat's one-column launches convert their activations into
+    # LDS themselves; lnship32_mul_mat_noalloc converts them first (k_act) in
+    # every case: the two agree bit for bit, GQA broadcast (32 activation
+    # slices over 8 weight slices) and the 32000-row output shape included
+    print(f"\n[mul_mat32 own conversion] K={K} M={M} N={N} slices={nslices}", flush=True)
+    L = ln.lib()
+    rng = np.random.default_rng(K + M + 13 * N + nslices)
+    ne02 = max(1, nslices // 4)
+    w = (rng.standard_normal((ne02, M, K)) * 0.05).astype(np.float32)
+    x = (rng.standard_normal((nslices, N, K))).astype(np.float32)
+    wp, dx = ln.pack32(dev(w)), dev(x)
+    outs = []
+    for fn in (L.lnship32_mul_mat, L.lnship32_mul_mat_noalloc):
+        out = torch.full((nslices, N, M), float("nan"), device="cuda")
+        a = ln.MulMatArgs(wp.data_ptr(), dx.data_ptr(), out.data_ptr(), K, M, N, ne02, 1, nslices, 1, 0, 0, 0, 0, 0, 0,
+                          0, None, 0, None)
+        rc = fn(ctypes.byref(a), ln._stream())
+        if rc == -4:   # the fixed block of noalloc holds at most 1 Mi codes
+            pytest.skip("beyond the fixed scratch")
+        ln.check(rc)
+        outs.append(host(out))
+    same_bits(outs[0], outs[1], f"own conversion K={K} M={M} N={N} slices={nslices}")
+    if M * K * N * nslices <= 4_000_000:
+        same_bits(outs[0], O.mul_mat32(w, x, ne02=ne02), f"own conversion K={K} M={M} vs oracle")

@@ -1450,18 +1450,94 @@ struct mm_args32 {
     unsigned long long *err;
     const float *resid;   // as in mm_args16
     uint32_t xcd_sh;      // as in mm_args16
+    // XL launches (one column per workgroup): the F32 activations, row n of
+    // slice z at xf + z x_slice + n x_ld, converted into LDS by the launch;
+    // with norm, x = rms_norm(xf) * norm (epsilon eps) first, with glu_up,
+    // x = swiglu(xf, glu_up) (up row n at glu_up + n x_ld)
+    const float *xf;
+    int64_t x_ld, x_slice;
+    const float *norm;
+    float eps;
+    const float *glu_up;
 };
+
+// (defined with the other sequential row sums below)
+__device__ __forceinline__ void chain_pos32(const pos_tab &P, uint32_t &l, const uint32_t *row, int i0, int n);
+
+// xlns32_silu: x times the sigmoid of its value, the sigmoid formed in
+// double and rounded to float (libm-independent at float precision)
+__device__ __forceinline__ uint32_t x32_silu(uint32_t x) {
+    const double v = (double)x32_to_f32(x);
+    return x32_mul(x, x32_from_f32((float)(1.0 / (1.0 + exp(-v)))));
+}
 
 // One lane per weight row m and NC columns, CG column groups per workgroup
 // sharing the staged tables (as k_mm16).  A group of eight k is two 16-byte
 // loads of weights and two per column of activations; the next PF groups are
 // in flight while one is accumulated.
 // W: rows per wave (64, or 16 with the other lanes only staging, as in k_mm16)
-template <int NC, int PF, int CG, int W = 64>
+// XL: the activation row converted into LDS after the tables by the launch
+// (one column per workgroup), its nodes before the product with it (the
+// rms_norm and norm MUL, or the swiglu), exactly as they run apart: F32
+// between the nodes, each converted as the next node converts it
+template <int NC, int PF, int CG, int W = 64, bool XL = false>
 __global__ __launch_bounds__(k_block * CG) void k_mm32(mm_args32 a, dev_tables T) {
+    static_assert(!XL || (NC == 1 && CG == 1), "XL launches take one column per workgroup");
     extern __shared__ __align__(16) char lds[];
     if (blockIdx.x & ((1u << a.xcd_sh) - 1u)) return;   // as in k_mm16
+    uint32_t *xl = reinterpret_cast<uint32_t *>(lds + k_lds_tab32);   // XL: the activation row's codes
+    __shared__ uint32_t s_inv;
+    int64_t zwx = 0, zxx = 0;
+    if constexpr (XL) {
+        const int64_t zz = blockIdx.z;
+        mm_slices(a, zz, zz % a.ne12, zz / a.ne12, zwx, zxx);
+        if (a.norm) {
+            // the rms_norm node's sum of squares exactly as k_rms32 forms it:
+            // the positive-sum image staged first (where the GEMV's image
+            // goes next), the squares into the row's LDS past both images,
+            // one chain (every lane of wave 0 runs it)
+            const pos_tab P = stage_pos32(T, lds);
+            const float *row = a.xf + zxx * a.x_slice + (int64_t)blockIdx.y * a.x_ld;
+            const int K = (int)a.K;
+            for (int k = threadIdx.x; k < K; k += blockDim.x) {
+                const uint32_t c = x32_from_f32(row[k]);
+                xl[k] = x32_mul(c, c);
+            }
+            __syncthreads();
+            if (threadIdx.x < 64u) {
+                uint32_t acc = 0u;
+                chain_pos32(P, acc, xl, 0, K);   // squares: positive
+                const uint32_t mean = x32_mul(acc, x32_from_f32(1.0f / (float)K));
+                // mean >= 0: the epsilon add is a positive one unless eps < 0
+                const uint32_t e = x32_from_f32(a.eps);
+                const uint32_t me = (e & k32_sign) ? x32_add(T.tab32, mean, e) : x32_add_pos2(P, mean, e);
+                if (threadIdx.x == 0) s_inv = x32_recip(x32_sqrt(me));
+            }
+            __syncthreads();
+        }
+    }
     const red16<LNSHIP_SUM32> R = stage_for<LNSHIP_SUM32, NC == 1>(T, lds);
+    if constexpr (XL) {
+        const float *row = a.xf + zxx * a.x_slice + (int64_t)blockIdx.y * a.x_ld;
+        const int K = (int)a.K, kp = (int)a.kp;
+        const uint32_t inv = a.norm ? s_inv : 0u;
+        const float *urow = a.glu_up ? a.glu_up + zxx * a.x_slice + (int64_t)blockIdx.y * a.x_ld : nullptr;
+        for (int k = threadIdx.x; k < kp; k += blockDim.x) {
+            uint32_t c = 0u;
+            if (k < K) {
+                const float f = row[k];
+                if (a.norm) {
+                    const float y = x32_to_f32(x32_mul(x32_from_f32(f), inv));
+                    c = x32_from_f32(x32_to_f32(x32_mul(x32_from_f32(y), x32_from_f32(a.norm[k]))));
+                } else if (urow) {
+                    c = x32_from_f32(x32_to_f32(x32_mul(x32_silu(x32_from_f32(f)), x32_from_f32(urow[k]))));
+                } else {
+                    c = x32_from_f32(f);
+                }
+            }
+            xl[k] = c;
+        }
+    }
     __syncthreads();
     const int cg = CG == 1 ? 0 : (int)(threadIdx.x / k_block);
     const int lane = (int)(threadIdx.x & 63u);
@@ -1475,7 +1551,7 @@ __global__ __launch_bounds__(k_block * CG) void k_mm32(mm_args32 a, dev_tables T
     int64_t zw, zx;
     if (!mm_slices(a, z, i12, i13, zw, zx)) return;
     const uint32_t *ws = a.w + zw * a.w_slice + m * 8;
-    const uint32_t *xs = a.x + (zx * a.N + n0) * a.kp;
+    const uint32_t *xs = XL ? nullptr : a.x + (zx * a.N + n0) * a.kp;
     const int64_t wstride = a.w_mstride * 8;
     float *ds = a.dst + z * a.dst_slice + n0 * a.dst_ld + m;
     // output j, with the fused ADD of the residual (xlns32 add of the two
@@ -1500,11 +1576,20 @@ __global__ __launch_bounds__(k_block * CG) void k_mm32(mm_args32 a, dev_tables T
         return grp{p[0], p[1]};
     };
     auto load_x = [&](int j, int g) {
-        // a per-lane offset keeps the wave-uniform read a vector load
-        int64_t off = (int64_t)(j < nc ? j : 0) * a.kp + (int64_t)min(g, last) * 8;
-        asm("" : "+v"(off));
-        const uint4 *p = reinterpret_cast<const uint4 *>(xs + off);
-        return grp{p[0], p[1]};
+        if constexpr (XL) {
+            // from LDS, the offset through a vector register (the data then
+            // counts as per-lane and is waited for where it is used)
+            int32_t off = min(g, last) * 32;
+            asm("" : "+v"(off));
+            const uint4 *p = reinterpret_cast<const uint4 *>(reinterpret_cast<const char *>(xl) + off);
+            return grp{p[0], p[1]};
+        } else {
+            // a per-lane offset keeps the wave-uniform read a vector load
+            int64_t off = (int64_t)(j < nc ? j : 0) * a.kp + (int64_t)min(g, last) * 8;
+            asm("" : "+v"(off));
+            const uint4 *p = reinterpret_cast<const uint4 *>(xs + off);
+            return grp{p[0], p[1]};
+        }
     };
     acc_ls acc[NC]{};
     uint32_t k_lm = k32_logmask;   // the mask in a register (short encodings)
@@ -2146,12 +2231,7 @@ struct fmt32 {
     __device__ __forceinline__ uint32_t add(uint32_t x, uint32_t y) const { return x32_add(T.tab32, x, y); }
     __device__ __forceinline__ uint32_t mul(uint32_t x, uint32_t y) const { return x32_mul(x, y); }
     __device__ __forceinline__ uint32_t neg(uint32_t x) const { return x ^ k32_sign; }
-    // xlns32_silu: x times the sigmoid of its value, the sigmoid formed in
-    // double and rounded to float (libm-independent at float precision)
-    __device__ __forceinline__ uint32_t silu(uint32_t x) const {
-        const double v = (double)x32_to_f32(x);
-        return x32_mul(x, x32_from_f32((float)(1.0 / (1.0 + exp(-v)))));
-    }
+    __device__ __forceinline__ uint32_t silu(uint32_t x) const { return x32_silu(x); }
 };
 template <int W>
 using fmt_t = typename std::conditional<W == 16, fmt16, fmt32>::type;
@@ -3451,18 +3531,25 @@ static int dispatch_mm16(const mm_args16 &m, const dev_tables &T, int64_t nslice
     }
 }
 
-template <int NC, int CG, int W = 64>
+// LDS of a k_mm32 launch: the single-chain image, and with XL the
+// activation row's codes (and the prefetch past its last group)
+static int64_t mm32_lds(bool xl, int64_t kp) { return k_lds_tab32 + (xl ? kp * 4 + 64 : 0); }
+// whether an XL launch of rows of kp codes fits LDS
+static bool mm32_xl_fits(int64_t kp) { return mm32_lds(true, kp) <= k_lds_bytes - k_lds_static; }
+
+template <int NC, int CG, int W = 64, bool XL = false>
 static int launch_mm32(const mm_args32 &m, const dev_tables &T, int64_t nslices, int cus, hipStream_t st) {
     // prefetch depth within 128 VGPRs at four waves per SIMD
     constexpr int PF = NC == 1 ? (CG >= 4 ? 2 : 4) : 1;
-    if (int rc = set_lds(k_mm32<NC, PF, CG, W>, k_lds_tab32)) return rc;
+    const int lds = (int)mm32_lds(XL, m.kp);
+    if (int rc = set_lds(k_mm32<NC, PF, CG, W, XL>, lds)) return rc;
     constexpr int rows = W < 64 ? k_block / 64 * W : k_block;   // rows per workgroup
     dim3 grid((unsigned)((m.M + rows - 1) / rows), (unsigned)((m.N + NC * CG - 1) / (NC * CG)), (unsigned)nslices);
     if (grid.x > 2147483647u || grid.y > 65535u) return fail(LNSHIP_ERANGE, "mul_mat: grid too large%s");
     mm_args32 mx = m;
     mx.xcd_sh = xcd_shift((uint64_t)grid.x * grid.y * grid.z, cus);
     grid.x <<= mx.xcd_sh;
-    hipLaunchKernelGGL((k_mm32<NC, PF, CG, W>), grid, dim3(k_block * CG), k_lds_tab32, st, mx, T);
+    hipLaunchKernelGGL((k_mm32<NC, PF, CG, W, XL>), grid, dim3(k_block * CG), lds, st, mx, T);
     LNSHIP_HIP(hipGetLastError());
     return 0;
 }
@@ -4095,9 +4182,10 @@ static int mul_mat32_staged(device_state *s, const lnship_mul_mat_args *a, void 
     }
 }
 
-// the nodes before the product that lnship16_mul_mat takes in its launch
+// the nodes before the product that only lnship32_mul_mat takes in its launch
 static int check_mm32_plain(const lnship_mul_mat_args *a) {
-    if (a->rms_norm_w || a->glu_up) return fail(LNSHIP_EINVAL, "mul_mat (LNS32): no rms_norm_w / glu_up%s");
+    if (a->rms_norm_w || a->glu_up)
+        return fail(LNSHIP_EINVAL, "mul_mat_noalloc (LNS32): no rms_norm_w / glu_up%s");
     return 0;
 }
 
@@ -4105,11 +4193,40 @@ int lnship32_mul_mat(const lnship_mul_mat_args *a, void *stream) {
     device_state *s = state();
     if (!s) return LNSHIP_ENOINIT;
     if (int rc = check_mm(a)) return rc;
-    if (int rc = check_mm32_plain(a)) return rc;
-    if (a->M == 0 || a->N == 0) return 0;
+    const int64_t nslices = a->ne12 * a->ne13;
     const int64_t kp = (a->K + 7) & ~(int64_t)7;
-    void *xs = nullptr;
+    if (a->rms_norm_w || a->glu_up) {
+        if (a->rms_norm_w && a->glu_up) return fail(LNSHIP_EINVAL, "mul_mat: rms_norm_w and glu_up together%s");
+        if (nslices != 1 || a->K < 1)
+            return fail(LNSHIP_EINVAL, "mul_mat: rms_norm_w / glu_up need one activation slice and K >= 1%s");
+    }
+    if (a->M == 0 || a->N == 0) return 0;
     hipStream_t st = (hipStream_t)stream;
+    // one column per workgroup (every decode shape) with the row beside the
+    // tables: the launch converts its activations itself (and forms the
+    // nodes before the product), no k_act launch
+    const mm16_shape sh = mm_shape_x32(a->M, a->N, nslices, kp, s->cus, 4);
+    const bool xl = sh.nc * 10 + sh.cg == 11 && kp > 0 && mm32_xl_fits(kp);
+    if ((a->rms_norm_w || a->glu_up) && !xl)
+        return fail(LNSHIP_ERANGE, "mul_mat: rows too long to stage beside the tables for rms_norm_w / glu_up%s");
+    if (xl) {
+        const int64_t wms = a->w_mstride ? a->w_mstride : a->M;
+        const int64_t dld = a->dst_ld ? a->dst_ld : a->M;
+        const int64_t xld = a->x_ld ? a->x_ld : a->K;
+        mm_args32 m{(const uint32_t *)a->w, nullptr, a->dst, a->K, kp, a->M, a->N,
+                    a->ne02, a->ne12, a->ne12 / a->ne02, a->ne13 / a->ne03,
+                    wms, a->w_slice ? a->w_slice : kp * wms, dld, a->dst_slice ? a->dst_slice : a->N * dld};
+        m.resid = a->residual;
+        m.xf = a->x;
+        m.x_ld = xld;
+        m.x_slice = a->x_slice ? a->x_slice : a->N * xld;
+        m.norm = a->rms_norm_w;
+        m.eps = a->rms_eps;
+        m.glu_up = a->glu_up;
+        if (narrow_mm(m.M * m.N * nslices, s->cus)) return launch_mm32<1, 1, 16, true>(m, s->T, nslices, s->cus, st);
+        return launch_mm32<1, 1, 64, true>(m, s->T, nslices, s->cus, st);
+    }
+    void *xs = nullptr;
     if (int rc = grow_scratch(s, (size_t)std::max<int64_t>(1, a->ne12 * a->ne13 * a->N * kp) * 4, &xs, st)) return rc;
     return mul_mat32_staged(s, a, xs, st);
 }

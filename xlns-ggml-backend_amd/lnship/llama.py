@@ -599,6 +599,10 @@ class LlamaLNS32:
         # the three ops
         self.fused_attn = True
         self._attn_max_kv = min(lib().lnship_max_row(7, 0), ATTN32_FUSED_KV)
+        # one row: the rms_norm and norm MUL inside the launch of the mul_mat
+        # that reads them (lnship32_mul_mat's rms_norm_w, bit-identical to the
+        # separate nodes) where the row fits LDS; False runs them apart
+        self.fused_pre = True
         rt = np.empty(c.n_ctx * hd, np.float32)
         check(lib().lnship_rope_table(c.rope_theta, hd, c.n_ctx, ctypes.c_void_p(rt.ctypes.data)))
         self.cos_sin = t(rt)
@@ -629,6 +633,21 @@ class LlamaLNS32:
         mm = lambda w, x, dst, K, M, N, **kw: mul_mat32_raw(w, x, dst, K, M, N, stream=st, **kw)
         x = self._buf("x", T * e)
         h = self._buf("h", T * e)
+
+        def rms_mm(x_ptr, wn_ptr, w, dst_ptr, K, M, rows):
+            """dst = W (rms_norm(x) * wn) for rows rows of K: for one row in
+            one launch (lnship32_mul_mat's rms_norm_w), else rms_norm + MUL
+            into h, then the mul_mat."""
+            if rows == 1 and self.fused_pre:
+                from . import MulMatArgs
+                a = MulMatArgs(w, x_ptr, dst_ptr, K, M, 1, 1, 1, 1, 1, 0, 0, 0, 0, 0, 0, 0, None, 0, None)
+                a.rms_norm_w, a.rms_eps = wn_ptr, c.eps
+                rc = L.lnship32_mul_mat(ctypes.byref(a), st)
+                if rc != -4:   # LNSHIP_ERANGE: the row does not fit beside the tables
+                    check(rc)
+                    return
+            check(L.lnship32_rms_norm_mul(x_ptr, wn_ptr, P(h), K, rows, c.eps, st))
+            mm(w, P(h), dst_ptr, K, M, rows)
         qkv = self._buf("qkv", T * nqkv)
         q = self._buf("q", T * nq)
         kq = self._buf("kq", nh * T * n_kv)
@@ -644,8 +663,7 @@ class LlamaLNS32:
         from . import SoftMaxArgs
         for il, W in enumerate(self.layers):
             last = il == c.n_layer - 1
-            check(L.lnship32_rms_norm_mul(P(x), P(W["attn_norm"]), P(h), e, T, c.eps, st))
-            mm(W["wqkv"].data_ptr(), P(h), P(qkv), e, nqkv, T)
+            rms_mm(P(x), P(W["attn_norm"]), W["wqkv"].data_ptr(), P(qkv), e, nqkv, T)
             qs = QkvStoreArgs(P(qkv), nqkv, P(pos_dev), T, nh, nkv, hd, hd, P(self.cos_sin), P(q),
                               P(self.kcache[il]), P(self.vcache[il]), c.n_ctx, self.kslice, self.vslice, None, 0)
             check(L.lnship32_rope_store_kv(ctypes.byref(qs), st))
@@ -669,8 +687,7 @@ class LlamaLNS32:
             else:
                 mm(W["wo"].data_ptr(), P(att), P(o), nq, e, T)
                 check(L.lnship32_add(P(o, r0), P(x, r0), rows * e, rows * e, P(x), st))
-            check(L.lnship32_rms_norm_mul(P(x), P(W["ffn_norm"]), P(h), e, rows, c.eps, st))
-            mm(W["wug"].data_ptr(), P(h), P(ug), e, 2 * f, rows)
+            rms_mm(P(x), P(W["ffn_norm"]), W["wug"].data_ptr(), P(ug), e, 2 * f, rows)
             check(L.lnship32_swiglu(P(ug, f), 2 * f, P(ug), 2 * f, P(sw), f, rows, st))
             mm(W["wdown"].data_ptr(), P(sw), P(x), f, e, rows, residual=P(x))
         check(L.lnship32_rms_norm_mul(P(x), P(self.out_norm), P(h), e, 1, c.eps, st))
