@@ -3666,7 +3666,7 @@ static int binary_common(const float *a, const float *b, int64_t n, int64_t nb, 
     if (!s) return LNSHIP_ENOINIT;
     if (n < 0 || nb <= 0) return fail(LNSHIP_EINVAL, OP == 0 ? "add: bad length%s" : "mul: bad length%s");
     if (n == 0) return 0;
-    hipLaunchKernelGGL((k_binary<W, OP>), dim3(grid_for(n, 4)), dim3(k_block), 0, (hipStream_t)stream, a, b, n, nb,
+    hipLaunchKernelGGL((k_binary<W, OP>), dim3(grid_for(n)), dim3(k_block), 0, (hipStream_t)stream, a, b, n, nb,
                        dst, s->T);
     LNSHIP_HIP(hipGetLastError());
     return 0;
@@ -3678,7 +3678,7 @@ static int scale_common(const float *src, float *dst, int64_t n, float sc, float
     if (!s) return LNSHIP_ENOINIT;
     if (n < 0) return fail(LNSHIP_EINVAL, "scale: bad length%s");
     if (n == 0) return 0;
-    hipLaunchKernelGGL(k_scale<W>, dim3(grid_for(n, 4)), dim3(k_block), 0, (hipStream_t)stream, src, dst, n, sc, b,
+    hipLaunchKernelGGL(k_scale<W>, dim3(grid_for(n)), dim3(k_block), 0, (hipStream_t)stream, src, dst, n, sc, b,
                        s->T);
     LNSHIP_HIP(hipGetLastError());
     return 0;
@@ -3691,7 +3691,7 @@ static int swiglu_common(const float *gate, int64_t gate_ld, const float *up, in
     if (!s) return LNSHIP_ENOINIT;
     if (ncols < 0 || nrows < 0 || gate_ld < ncols || up_ld < ncols) return fail(LNSHIP_EINVAL, "swiglu: bad shape%s");
     if (ncols == 0 || nrows == 0) return 0;
-    hipLaunchKernelGGL(k_swiglu<W>, dim3(grid_for(ncols * nrows, 4)), dim3(k_block), 0, (hipStream_t)stream, gate,
+    hipLaunchKernelGGL(k_swiglu<W>, dim3(grid_for(ncols * nrows)), dim3(k_block), 0, (hipStream_t)stream, gate,
                        gate_ld, up, up_ld, dst, ncols, nrows, s->T);
     LNSHIP_HIP(hipGetLastError());
     return 0;
@@ -3706,7 +3706,7 @@ static int rope_common(const float *x, int64_t x_ld, const int32_t *pos, int64_t
         return fail(LNSHIP_EINVAL, "rope: bad shape%s");
     const int64_t n = ntok * nhead * (n_dims / 2 + ne0 - n_dims);
     if (n == 0) return 0;
-    hipLaunchKernelGGL(k_rope<W>, dim3(grid_for(n, 4)), dim3(k_block), 0, (hipStream_t)stream, x, x_ld, pos, ntok,
+    hipLaunchKernelGGL(k_rope<W>, dim3(grid_for(n)), dim3(k_block), 0, (hipStream_t)stream, x, x_ld, pos, ntok,
                        nhead, ne0, n_dims, neox, cos_sin, dst, s->T);
     LNSHIP_HIP(hipGetLastError());
     return 0;
@@ -3725,7 +3725,7 @@ static int store_kv_common(const float *x, int64_t x_ld, const int32_t *pos, int
     if (seq && seq_stride < 0) return fail(LNSHIP_EINVAL, "store_kv: negative sequence stride%s");
     const int64_t n = ntok * nhead * ne0;
     if (n == 0) return 0;
-    hipLaunchKernelGGL(k_store_kv<W>, dim3(grid_for(n, 4)), dim3(k_block), 0, (hipStream_t)stream, x, x_ld, pos, ntok,
+    hipLaunchKernelGGL(k_store_kv<W>, dim3(grid_for(n)), dim3(k_block), 0, (hipStream_t)stream, x, x_ld, pos, ntok,
                        nhead, ne0, rope_n_dims, cos_sin, cache, cache_m, cache_slice, cache_transposed, seq, seq_stride,
                        s->T, s->index_err);
     LNSHIP_HIP(hipGetLastError());
@@ -3743,7 +3743,7 @@ static int rope_store_kv_common(const lnship_qkv_store_args *a, void *stream) {
     const int64_t hd = a->head_dim, nd = a->rope_n_dims;
     const int64_t n = a->ntok * (a->n_head * (nd / 2 + hd - nd) + 2 * a->n_head_kv * hd);
     if (n == 0) return 0;
-    hipLaunchKernelGGL(k_rope_store_kv<W>, dim3(grid_for(n, 4)), dim3(k_block), 0, (hipStream_t)stream, *a, s->T,
+    hipLaunchKernelGGL(k_rope_store_kv<W>, dim3(grid_for(n)), dim3(k_block), 0, (hipStream_t)stream, *a, s->T,
                        s->index_err);
     LNSHIP_HIP(hipGetLastError());
     return 0;
