@@ -97,6 +97,12 @@ def footprints(name, a):
                 (m.dst, ((ns - 1) * d_sl + (N - 1) * d_ld + M) * F32, "mul_mat dst")]
         if m.residual:
             out.append((m.residual, ((ns - 1) * d_sl + (N - 1) * d_ld + M) * F32, "mul_mat residual"))
+        # the nodes before the product: the norm row (K floats), the up rows
+        # laid out as x
+        if m.rms_norm_w:
+            out.append((m.rms_norm_w, K * F32, "mul_mat rms_norm_w"))
+        if m.glu_up:
+            out.append((m.glu_up, ((ns - 1) * x_sl + (N - 1) * x_ld + K) * F32, "mul_mat glu_up"))
     elif name == "lnship32_rope_store_kv":
         q = a[0]
         hd, nh, nkv = q.head_dim, q.n_head, q.n_head_kv
@@ -217,6 +223,9 @@ def test_lns32_decode_at_full_context_stays_inside_its_allocations(recorded):
     assert kq and max(m.M for m in kq) == cfg.n_ctx
     kqv = [a[0] for n, a in recorded.calls if n == "lnship32_mul_mat" and a[0].w_slice == model.vslice]
     assert kqv and max(m.K for m in kqv) == cfg.n_ctx
+    # q|k|v and up|gate take their rms_norm and norm MUL in their launch
+    pre = [a[0] for n, a in recorded.calls if n == "lnship32_mul_mat" and a[0].rms_norm_w]
+    assert len(pre) == 2 * cfg.n_layer   # (the second step replays the graph)
     n = audit(recorded.calls, allocations(model))
     # the same steps with the attention as one launch over the whole cache
     # (the second step replays the graph the first one captured)
