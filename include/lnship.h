@@ -417,7 +417,8 @@ int lnship_index_error(int64_t *bad_index, void *stream);
  * for opposite signs at distance d, xlns32 units), as the lpvip mul_mat /
  * rms_norm / soft_max kernels compute it; xlns32_add_lpvip's exact branch
  * below one binade follows cuda/lns-cuda-xlns16.cu:86-98 and docs/CUDA.md:176-180.
- * No counterpart in the reference. */
+ * 1 <= d0 and d0 + n <= 2^32 (d = 0 is exact cancellation, which the adder
+ * handles before db).  No counterpart in the reference. */
 int lnship_lpvip_db_range(uint32_t d0, uint32_t n, int32_t *out, void *stream);
 
 /* Test hook: out[i] = x[i] + y[i] (xlns32 codes, sign bit 31) by the xlns32

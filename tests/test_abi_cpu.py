@@ -400,3 +400,15 @@ def test_ctypes_structs_match_the_header(lnship, tmp_path):
         assert got[(cname, "size")] == ctypes.sizeof(py), cname
         for f in py._fields_:
             assert got[(cname, f[0])] == getattr(py, f[0]).offset, (cname, f[0])
+
+
+def test_lpvip_db_range_checks_its_range_first(lnship):
+    # d = 0 (exact cancellation, never a db) and ranges past 2^32 are refused
+    # before any device call; a valid range then needs the device
+    L = lnship.lib()
+    fake = ctypes.c_void_p(0x1000)
+    EINVAL, ENOINIT = -1, -3   # include/lnship.h: enum lnship_error
+    assert L.lnship_lpvip_db_range(0, 8, fake, None) == EINVAL
+    assert L.lnship_lpvip_db_range(0xffffffff, 2, fake, None) == EINVAL
+    assert L.lnship_lpvip_db_range(1, 8, None, None) == EINVAL
+    assert L.lnship_lpvip_db_range(1, 8, fake, None) == ENOINIT

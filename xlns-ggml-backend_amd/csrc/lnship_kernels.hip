@@ -4854,9 +4854,12 @@ int lnship_set_rows(const float *src, const int64_t src_ne[4], const int64_t src
 }
 
 int lnship_lpvip_db_range(uint32_t d0, uint32_t n, int32_t *out, void *stream) {
+    // arguments first: they need no device
+    if (!out) return fail(LNSHIP_EINVAL, "lpvip_db_range: null output%s");
+    // d = 0 is exact cancellation, which the adder handles before db
+    if (d0 == 0 || (uint64_t)d0 + n > 0x100000000ull) return fail(LNSHIP_EINVAL, "lpvip_db_range: d outside [1, 2^32)%s");
     device_state *s = state();
     if (!s) return LNSHIP_ENOINIT;
-    if (!out) return fail(LNSHIP_EINVAL, "lpvip_db_range: null output%s");
     if (n == 0) return 0;
     hipLaunchKernelGGL(k_lpvip_db_range, dim3(grid_for(n, 4)), dim3(k_block), 0, (hipStream_t)stream, d0, n, out,
                        s->T.lpdb);
