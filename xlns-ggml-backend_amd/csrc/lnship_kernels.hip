@@ -1333,7 +1333,7 @@ __global__ __launch_bounds__(k_block * CG) void k_mm16(mm_args16 a, dev_tables T
     // below forms h from them
     __shared__ uint32_t s_rinv[64];
     if (XL && a.norm) {
-        const float *xf = a.xf + nw * a.x_ld;
+        const float *xf = a.xf + zx * a.x_slice + nw * a.x_ld;
         const int K = (int)a.K;
         for (int e = threadIdx.x; e < ncw * K; e += k_block * CG) {
             const int j = e / K, k = e - j * K;
