@@ -205,8 +205,11 @@ def rms_mul_oracle(mode, x, wn, w, s0):
 
 
 @pytest.mark.parametrize("mode", ["base", "monte", "lpvip", "sum32"])
-@pytest.mark.parametrize("K,M,N", [(576, 960, 8), (577, 193, 3), (13, 5, 1), (1536, 576, 2), (576, 3072, 8)])
+@pytest.mark.parametrize("K,M,N", [(576, 960, 8), (577, 193, 3), (13, 5, 1), (1536, 576, 2), (576, 3072, 8),
+                                   (576, 700, 16), (200, 300, 40)])
 def test_mul_mat_rms_prologue_equals_three_nodes(ln, mode, K, M, N):
+    # (16 and 40 rows: launches of several columns per workgroup, where the
+    # rms chains of the columns share wave 0)
     print(f"\n[mul_mat rms prologue] {mode} K={K} M={M} N={N}", flush=True)
     m = O.MODES[mode]
     L = ln.lib()
@@ -281,6 +284,25 @@ def test_mul_mat_glu_prologue_equals_two_nodes(ln, mode, K, M, N):
     ref = dev(resid)
     ln.mul_mat16_raw(m, wp.data_ptr(), swd.data_ptr(), ref.data_ptr(), K, M, N, seed=s0, residual=P(ref))
     same_bits(host(x), host(ref), f"glu prologue + residual {mode} K={K} M={M} N={N}")
+
+
+def test_mul_mat_prologue_rows_too_long(ln):
+    # a row that does not fit LDS beside the tables: LNSHIP_ERANGE before
+    # any launch (the caller runs the nodes apart), dst untouched
+    L = ln.lib()
+    K, M = 100000, 8
+    wp = ln.pack16(torch.zeros(M, K, device="cuda"))
+    x = torch.ones(1, K, device="cuda")
+    out = torch.full((1, M), 7.0, device="cuda")
+    for mode in (O.BASE, O.SUM32):
+        a = mm_args(ln, wp, x.data_ptr(), out, K, M, 1, 7)
+        a.rms_norm_w, a.rms_eps = x.data_ptr(), EPS
+        assert L.lnship16_mul_mat(mode, ctypes.byref(a), ln._stream()) == -4, mode
+    wp32 = ln.pack32(torch.zeros(M, K, device="cuda"))
+    a = mm_args(ln, wp32, x.data_ptr(), out, K, M, 1, 0)
+    a.rms_norm_w, a.rms_eps = x.data_ptr(), EPS
+    assert L.lnship32_mul_mat(ctypes.byref(a), ln._stream()) == -4
+    assert np.all(host(out) == 7.0)
 
 
 def test_mul_mat_prologue_refusals(ln):
