@@ -1357,57 +1357,63 @@ __global__ __launch_bounds__(k_block * CG) void k_mm16(mm_args16 a, dev_tables T
     if (XL) {
         // columns past N and k past K hold xlns16 zero
         // in batches of eight per thread: the loads, then the conversion
-        // table's lookups, then the stores (two memory round trips a batch)
+        // table's lookups, then the stores (two memory round trips a batch).
+        // The staging with the rms_norm's scale is a loop of its own, so the
+        // plain and GLU launches keep theirs as they were.
         const float *xf = a.xf + zx * a.x_slice + nw * a.x_ld;
         constexpr int nt = k_block * CG, B = 8;
         const int kl = (int)a.K - 1;
-        for (int j = 0; j < NC * CG; j++) {
-            if (kl < 0) {
-                for (int k = threadIdx.x; k < kp; k += nt) xl[j * kp + k] = 0;
-                continue;
+        auto stage = [&](auto norm_tag) __attribute__((always_inline)) {
+            constexpr bool NORM = decltype(norm_tag)::value;
+            for (int j = 0; j < NC * CG; j++) {
+                if (kl < 0) {
+                    for (int k = threadIdx.x; k < kp; k += nt) xl[j * kp + k] = 0;
+                    continue;
+                }
+                // loads and lookups stay in the row; only the stores are bounded
+                const float *row = xf + (int64_t)min(j, ncw - 1) * a.x_ld;
+                const uint32_t inv = NORM ? s_rinv[min(j, ncw - 1)] : 0u;
+                for (int k0 = threadIdx.x; k0 < kp; k0 += B * nt) {
+                    float v[B];
+#pragma unroll
+                    for (int q = 0; q < B; q++) v[q] = row[min(k0 + q * nt, kl)];
+                    uint32_t c[B];
+#pragma unroll
+                    for (int q = 0; q < B; q++) c[q] = x16_from_f32(T.cvt16, v[q]);
+                    if constexpr (NORM) {
+                        // the RMS_NORM node's output, then the MUL node's by
+                        // the norm weight, each through F32 (rho16)
+                        float g[B];
+#pragma unroll
+                        for (int q = 0; q < B; q++) g[q] = a.norm[min(k0 + q * nt, kl)];
+#pragma unroll
+                        for (int q = 0; q < B; q++)
+                            c[q] = T.rho16[x16_mul(T.rho16[x16_mul(c[q], inv)], x16_from_f32(T.cvt16, g[q]))];
+                    } else if (a.glu_up) {
+                        // swiglu as its node computes it (silu(gate) * up in
+                        // xlns16, F32 out), then into xlns16 as here
+                        const float *urow = a.glu_up + zx * a.x_slice + (nw + (int64_t)min(j, ncw - 1)) * a.x_ld;
+                        float u[B];
+#pragma unroll
+                        for (int q = 0; q < B; q++) u[q] = urow[min(k0 + q * nt, kl)];
+#pragma unroll
+                        for (int q = 0; q < B; q++)
+                            c[q] = T.rho16[x16_mul(x16_mul(c[q], T.sig16[c[q]]), x16_from_f32(T.cvt16, u[q]))];
+                    }
+                    // every code in a register before the bounded stores: none
+                    // of the batch's loads moves into a store's branch
+#pragma unroll
+                    for (int q = 0; q < B; q++) asm volatile("" ::"v"(c[q]));
+#pragma unroll
+                    for (int q = 0; q < B; q++) {
+                        const int k = k0 + q * nt;
+                        if (k < kp) xl[j * kp + k] = (j < ncw && k <= kl) ? (uint16_t)c[q] : (uint16_t)0;
+                    }
+                }
             }
-            // loads and lookups stay in the row; only the stores are bounded
-            const float *row = xf + (int64_t)min(j, ncw - 1) * a.x_ld;
-            const uint32_t inv = a.norm ? s_rinv[min(j, ncw - 1)] : 0u;
-            for (int k0 = threadIdx.x; k0 < kp; k0 += B * nt) {
-                float v[B];
-#pragma unroll
-                for (int q = 0; q < B; q++) v[q] = row[min(k0 + q * nt, kl)];
-                uint32_t c[B];
-#pragma unroll
-                for (int q = 0; q < B; q++) c[q] = x16_from_f32(T.cvt16, v[q]);
-                if (a.norm) {
-                    // the RMS_NORM node's output, then the MUL node's by the
-                    // norm weight, each through F32 (rho16)
-                    float g[B];
-#pragma unroll
-                    for (int q = 0; q < B; q++) g[q] = a.norm[min(k0 + q * nt, kl)];
-#pragma unroll
-                    for (int q = 0; q < B; q++)
-                        c[q] = T.rho16[x16_mul(T.rho16[x16_mul(c[q], inv)], x16_from_f32(T.cvt16, g[q]))];
-                }
-                if (a.glu_up) {
-                    // swiglu as its node computes it (silu(gate) * up in
-                    // xlns16, F32 out), then into xlns16 as here
-                    const float *urow = a.glu_up + zx * a.x_slice + (nw + (int64_t)min(j, ncw - 1)) * a.x_ld;
-                    float u[B];
-#pragma unroll
-                    for (int q = 0; q < B; q++) u[q] = urow[min(k0 + q * nt, kl)];
-#pragma unroll
-                    for (int q = 0; q < B; q++)
-                        c[q] = T.rho16[x16_mul(x16_mul(c[q], T.sig16[c[q]]), x16_from_f32(T.cvt16, u[q]))];
-                }
-                // every code in a register before the bounded stores: none of
-                // the batch's loads moves into a store's branch
-#pragma unroll
-                for (int q = 0; q < B; q++) asm volatile("" ::"v"(c[q]));
-#pragma unroll
-                for (int q = 0; q < B; q++) {
-                    const int k = k0 + q * nt;
-                    if (k < kp) xl[j * kp + k] = (j < ncw && k <= kl) ? (uint16_t)c[q] : (uint16_t)0;
-                }
-            }
-        }
+        };
+        if (a.norm) stage(std::true_type{});
+        else stage(std::false_type{});
         xl += cg * NC * kp;
     }
     __syncthreads();
